@@ -1,0 +1,67 @@
+"""ctypes binding of ``libfsctep_hip.so`` (the C ABI declared in ``include/fsctep.h``).
+
+The library is required: importing an op without it raises, there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libfsctep_hip.so")
+
+_i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+_pi64 = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argtypes (all return int status)
+SIGNATURES = {
+    "fsc_sparse_conv_workspace": [_i64, _i64, _i32, _pi64, _pi64],
+    "fsc_sparse_conv_prepare_weights": [_p, _p, _i32, _p, _p, _p],
+    "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p],
+    "fsc_sparse_conv_backward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f32,
+                                 _p, _p, _p, _p, _p],
+    "fsc_sparse_conv1_pair_table": [_p, _p, _p, _i32, _i32, _p, _p, _p],
+    "fsc_sparse_conv1_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
+    "fsc_sparse_conv1_backward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} not found: build it with `python -m fsctep_amd.build` "
+                           "(the HIP kernels are the only implementation)")
+    lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+    lib.fsc_last_error.restype = ctypes.c_char_p
+    lib.fsc_last_error.argtypes = []
+    lib.fsc_abi_version.restype = ctypes.c_int
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.fsc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int:
+    """Device pointer of a tensor (None -> NULL)."""
+    return 0 if t is None else int(t.data_ptr())
+
+
+def stream_handle(device) -> int:
+    import torch
+    return int(torch.cuda.current_stream(device).cuda_stream)

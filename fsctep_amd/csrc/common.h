@@ -1,0 +1,55 @@
+// Shared helpers for the gfx950 kernels of the FSCTEP hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+namespace fsc {
+
+// v_mfma_f32_16x16x4_f32, wave64.  Operand lanes: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; the result register j of lane l is D[4*(l/16)+j][l%16].
+__device__ __forceinline__ f4 mfma16x16x4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One 16-deep K step: lane (r=l%16, q=l/16) holds A[r][k0+4q+j] in a[j] and
+// B[k0+4q+j][r] in b[j]; any fixed K order works as long as A and B agree.
+__device__ __forceinline__ f4 mfma_k16(const f4& a, const f4& b, f4 acc) {
+  acc = mfma16x16x4(a.x, b.x, acc);
+  acc = mfma16x16x4(a.y, b.y, acc);
+  acc = mfma16x16x4(a.z, b.z, acc);
+  acc = mfma16x16x4(a.w, b.w, acc);
+  return acc;
+}
+
+__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ void st4(float* p, const f4& v) { *reinterpret_cast<f4*>(p) = v; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over lanes that share lane%width groups of `width` (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+void set_error(const std::string& msg);
+int check_launch(const char* what);
+
+}  // namespace fsc
+
+#define FSC_CHECK_ARG(cond, msg)            \
+  do {                                      \
+    if (!(cond)) {                          \
+      fsc::set_error(std::string(msg));     \
+      return 1;                             \
+    }                                       \
+  } while (0)

@@ -1,0 +1,282 @@
+"""``pure-cartesian-sparse`` trunk on the HIP kernels.
+
+``PureCartesianSparseTransformerLayer`` takes the reference's constructor arguments and
+holds the reference's parameters under the same state_dict keys
+(``models/pure_cartesian_sparse_layers.py:459-855``), so reference checkpoints load
+unchanged.  Its message passing runs in ``libfsctep_hip.so``:
+
+* conv1 (``:227-330``): ``torch.ops.fsctep.sparse_conv1`` on a species-pair table;
+* conv2..n (``:382-421``): ``torch.ops.fsctep.sparse_conv``.
+
+Edge geometry, the radial basis and the first two radial-MLP layers stay in PyTorch;
+the readout (``:769-833``) runs on the same internal feature layout x[N][13][C]
+(component-major; the reference's pseudo half is identically zero and is not stored).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .graph import Graph, prepare_graph
+from .radial import radial_basis
+
+_COMPS = ((0, 1), (1, 4), (4, 13))   # component ranges of ranks 0, 1, 2
+
+
+class MainNet(nn.Module):
+    """LayerNorm -> [Linear -> LayerNorm -> SiLU]* -> Linear (reference models/mlp.py:8-66)."""
+
+    def __init__(self, input_size, hidden_sizes, output_size):
+        super().__init__()
+        self.input_norm = nn.LayerNorm(input_size)
+        self.layers = nn.ModuleList()
+        self.layer_norms = nn.ModuleList()
+        prev = input_size
+        for hsz in hidden_sizes:
+            self.layers.append(nn.Linear(prev, hsz))
+            self.layer_norms.append(nn.LayerNorm(hsz))
+            prev = hsz
+        self.output = nn.Linear(prev, output_size)
+        for m in self.modules():
+            if isinstance(m, nn.Linear):
+                if m is self.output:
+                    nn.init.normal_(m.weight, 0.0, 0.01)
+                else:
+                    nn.init.kaiming_normal_(m.weight, a=0, mode="fan_in", nonlinearity="relu")
+                nn.init.zeros_(m.bias)
+
+    def forward(self, x):
+        x = self.input_norm(x)
+        for lin, ln in zip(self.layers, self.layer_norms):
+            x = F.silu(ln(lin(x)))
+        return self.output(x)
+
+
+class RobustScalarWeightedSum(nn.Module):
+    """sum_i x_i w_i (reference models/mlp.py:117-133); zero-initialised like the reference."""
+
+    def __init__(self, num_features, init_weights="zero"):
+        super().__init__()
+        self.weights = nn.Parameter(torch.zeros(num_features) if init_weights == "zero"
+                                    else torch.randn(num_features) * 0.1)
+
+    def forward(self, x):
+        return (x * self.weights).sum(dim=-1, keepdim=True)
+
+
+def _radial_mlp(hidden_out: int, nb: int) -> nn.Sequential:
+    return nn.Sequential(nn.Linear(nb, 64), nn.SiLU(), nn.Linear(64, 64), nn.SiLU(), nn.Linear(64, hidden_out))
+
+
+def _hidden(fc: nn.Sequential, emb: torch.Tensor) -> torch.Tensor:
+    """Output of fc[:4] (the 64-wide radial hidden that feeds fc.4)."""
+    return F.silu(fc[2](F.silu(fc[0](emb))))
+
+
+class PureCartesianSparseE3Conv(nn.Module):
+    """conv1 parameters (reference :134-226): atom embedding/MLP and the radial MLP fc."""
+
+    def __init__(self, max_radius, number_of_basis, channels_out, embedding_dim=16, max_atomvalue=10,
+                 output_size=8, Lmax=2, function_type="gaussian"):
+        super().__init__()
+        self.max_radius = max_radius
+        self.number_of_basis = number_of_basis
+        self.channels_out = channels_out
+        self.output_size = output_size
+        self.Lmax = Lmax
+        self.function_type = function_type
+        self.atom_embedding = nn.Embedding(max_atomvalue, embedding_dim)
+        self.atom_mlp = nn.Sequential(nn.Linear(embedding_dim, 64), nn.SiLU(), nn.Linear(64, output_size))
+        self.fidelity_embedding = None
+        self.fc = _radial_mlp(6 * channels_out * output_size * output_size, number_of_basis)
+
+    def atom_table(self, species: torch.Tensor) -> torch.Tensor:
+        return self.atom_mlp(self.atom_embedding(species.long()))
+
+
+class PureCartesianSparseE3Conv2(nn.Module):
+    """conv2..n parameters (reference :333-380): the radial MLP fc."""
+
+    def __init__(self, max_radius, number_of_basis, channels_in, channels_out, Lmax=2,
+                 function_type="gaussian"):
+        super().__init__()
+        if channels_in != channels_out:
+            raise ValueError("the HIP sparse conv needs channels_in == channels_out")
+        self.max_radius = max_radius
+        self.number_of_basis = number_of_basis
+        self.channels_in = channels_in
+        self.channels_out = channels_out
+        self.Lmax = Lmax
+        self.function_type = function_type
+        self.fc = _radial_mlp(6 * channels_out * channels_in, number_of_basis)
+        self._prep_key = None
+        self._prep = None
+
+    def prepared_weights(self):
+        w, b = self.fc[4].weight, self.fc[4].bias
+        key = (w.data_ptr(), w._version, b.data_ptr(), b._version, w.device)
+        if self._prep_key != key:
+            with torch.no_grad():
+                self._prep = torch.ops.fsctep.sparse_prepare_weights(w.detach(), b.detach(), self.channels_out)
+            self._prep_key = key
+        return self._prep
+
+
+class PureCartesianSparseInvariantBilinear(nn.Module):
+    """product_3 parameters (reference :424-438)."""
+
+    def __init__(self, channels, out_channels, Lmax):
+        super().__init__()
+        self.channels = channels
+        self.out_channels = out_channels
+        self.Lmax = Lmax
+        self.W = nn.ParameterList([nn.Parameter(torch.randn(out_channels, channels, channels) * 0.02)
+                                   for _ in range(Lmax + 1)])
+
+    def forward(self, blocks):
+        """blocks[L]: (N, 3^L, channels) -> (N, out_channels)."""
+        total = 0
+        for L, t in enumerate(blocks):
+            N = t.shape[0]
+            scale = 1.0 / math.sqrt(3 ** L) if L > 0 else 1.0
+            gram = torch.bmm(t.transpose(1, 2).contiguous(), t) * scale
+            total = total + gram.reshape(N, -1) @ self.W[L].reshape(self.out_channels, -1).t()
+        return total
+
+
+class PureCartesianSparseTransformerLayer(nn.Module):
+    """Drop-in for the reference class of the same name (lmax 2, max_rank_other 1, k_policy k0)."""
+
+    def __init__(self, max_embed_radius, main_max_radius, main_number_of_basis, hidden_dim_conv,
+                 hidden_dim_sh=None, hidden_dim=64, channel_in2=32, embedding_dim=16, max_atomvalue=10,
+                 output_size=8, invariant_channels=32, embed_size=None, main_hidden_sizes3=None,
+                 num_layers=1, num_interaction=2, device=None, function_type_main="gaussian", lmax=2,
+                 max_rank_other=1, k_policy="k0", long_range_mode="none", external_tensor_rank=None,
+                 external_tensor_specs=None, num_fidelity_levels=0, physical_tensor_outputs=None,
+                 **unsupported):
+        super().__init__()
+        if lmax != 2 or max_rank_other != 1 or k_policy != "k0":
+            raise NotImplementedError("HIP sparse path: lmax=2, max_rank_other=1, k_policy='k0' only")
+        if long_range_mode != "none" or external_tensor_rank is not None or external_tensor_specs \
+                or num_fidelity_levels or physical_tensor_outputs:
+            raise NotImplementedError("HIP sparse path: long-range, external tensors, fidelity and "
+                                      "physical tensor heads are outside this path")
+        for k, v in unsupported.items():
+            if k.startswith(("long_range_", "feature_spectral_")) or k in ("multi_fidelity_mode",
+                                                                         "external_tensor_scale_init"):
+                continue
+            raise TypeError(f"unexpected argument {k!r}")
+        if output_size != 8:
+            raise NotImplementedError("HIP sparse conv1 needs output_size 8")
+        if hidden_dim_conv not in (32, 64):
+            raise NotImplementedError("HIP sparse path: hidden_dim_conv 32 or 64")
+        if num_interaction < 2:
+            raise ValueError(f"num_interaction must be >= 2, got {num_interaction}")
+        embed_size = [128, 128, 128] if embed_size is None else list(embed_size)
+        self.Lmax = lmax
+        self.lmax = lmax
+        self.channels = hidden_dim_conv
+        self.num_interaction = int(num_interaction)
+        self.invariant_channels = int(invariant_channels)
+        self.max_rank_other = max_rank_other
+        self.k_policy = k_policy
+        self.e3_conv_layers = nn.ModuleList()
+        self.e3_conv_layers.append(PureCartesianSparseE3Conv(
+            max_embed_radius, main_number_of_basis, self.channels, embedding_dim, max_atomvalue,
+            output_size, lmax, function_type_main))
+        self.e3_conv_emb = self.e3_conv_layers[0]
+        for _ in range(1, self.num_interaction):
+            self.e3_conv_layers.append(PureCartesianSparseE3Conv2(
+                max_embed_radius, main_number_of_basis, self.channels, self.channels, lmax, function_type_main))
+        self.combined_channels = self.channels * self.num_interaction
+        scalar_channels = (self.num_interaction - 1) * self.invariant_channels
+        self.product_3 = PureCartesianSparseInvariantBilinear(self.combined_channels, scalar_channels, lmax)
+        self.proj_total = MainNet(self.num_interaction * self.channels * (lmax + 1) + scalar_channels,
+                                  embed_size, 17)
+        self.weighted_sum = RobustScalarWeightedSum(17, init_weights="zero")
+        self.max_radius = max_embed_radius
+        self.number_of_basis = main_number_of_basis
+        self.function_type = function_type_main
+        self._graph_key = None
+        self._graph = None
+
+    # ------------------------------------------------------------------ graph handling
+    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
+        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A)
+
+    def _cached_graph(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
+        key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (edge_src, edge_dst, edge_shifts, A))
+        key = key + (num_nodes, edge_dst.device)
+        if self._graph_key != key:
+            self._graph = self.prepare(edge_src, edge_dst, edge_shifts, num_nodes, A)
+            self._graph_key = key
+        return self._graph
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
+                external_tensor=None, fidelity_ids=None, return_physical_tensors=False,
+                return_reciprocal_source=False, **_unused):
+        if external_tensor is not None or fidelity_ids is not None or return_physical_tensors:
+            raise NotImplementedError("external tensors / fidelity / physical tensors are outside the HIP path")
+        g = self._cached_graph(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+        e = self.forward_graph(pos, batch, cell, g)
+        if return_reciprocal_source:
+            return e, e.new_empty((e.shape[0], 0))
+        return e
+
+    def _check_inference(self):
+        if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            raise NotImplementedError("the HIP sparse path computes energies and forces only; parameter "
+                                      "gradients (training) are not implemented: call .eval() or "
+                                      ".requires_grad_(False)")
+
+    def forward_graph(self, pos, batch, cell, g: Graph):
+        """(N, 1) atomic energies for a prepared graph; differentiable w.r.t. ``pos``."""
+        self._check_inference()
+        if not pos.is_cuda:
+            raise RuntimeError("the HIP sparse path runs on the GPU only")
+        dtype = torch.float32
+        pos = pos.to(dtype)
+        cell = cell.to(dtype)
+        N = pos.shape[0]
+        shift_vec = torch.einsum("ni,nij->nj", g.shifts.to(dtype), cell[batch[g.src]])
+        vec = pos[g.dst] - pos[g.src] + shift_vec
+        r = vec.norm(dim=1)
+        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+        emb = radial_basis(r, self.max_radius, self.number_of_basis, self.function_type)
+
+        conv1 = self.e3_conv_layers[0]
+        atab = conv1.atom_table(g.species).to(dtype)
+        mf, mb = torch.ops.fsctep.sparse_conv1_pair_table(conv1.fc[4].weight.detach(),
+                                                          conv1.fc[4].bias.detach(), atab.detach(),
+                                                          self.channels)
+        feats = [ops.sparse_conv1_apply(_hidden(conv1.fc, emb), n, mf, mb, g, self.channels)]
+        inv_norm = 1.0 / max(g.n_edges / max(N, 1), 1e-8)
+        for conv in self.e3_conv_layers[1:]:
+            bk1, bk6 = conv.prepared_weights()
+            feats.append(ops.sparse_conv_apply(feats[-1], _hidden(conv.fc, emb), n, bk1, bk6, g, inv_norm))
+        return self.readout(feats)
+
+    def readout(self, feats):
+        """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features."""
+        blocks = [torch.cat([f[:, a:b, :] for f in feats], dim=2) for (a, b) in _COMPS]
+        f3 = self.product_3(blocks)
+        invs = []
+        for f in feats:
+            for L, (a, b) in enumerate(_COMPS):
+                invs.append((f[:, a:b, :] * f[:, a:b, :]).sum(dim=1) / math.sqrt(3 ** L))
+        f5 = torch.cat(invs + [f3 * f3], dim=-1)
+        return self.weighted_sum(self.proj_total(f5))
+
+
+def energy_and_forces(model: PureCartesianSparseTransformerLayer, pos, batch, cell, graph: Graph):
+    """Per-atom energies (N,) and forces F = -dE/dpos (N, 3)."""
+    pos = pos.detach().requires_grad_(True)
+    e = model.forward_graph(pos, batch, cell, graph)
+    (grad,) = torch.autograd.grad(e.sum(), pos)
+    return e.detach().squeeze(-1), -grad

@@ -1,0 +1,100 @@
+/*
+ * fsctep.h - C ABI of the MI355X (gfx950) kernels for the FSCTEP equivariant
+ * message-passing hot path.  Library: libfsctep_hip.so.
+ *
+ * Conventions
+ *  - Every pointer is device memory (fp32 data, int32 graph indices) unless noted.
+ *  - Outputs and workspaces are allocated by the caller; no entry point allocates.
+ *  - Work is enqueued on `stream`; no entry point synchronises the host.
+ *  - Return value: 0 ok, 1 invalid argument, 2 launch failure; the message of the
+ *    last failure on the calling thread is returned by fsc_last_error().
+ *  - Graph: edges are sorted by receiver (dst).  dst_ptr[N+1] is the receiver CSR;
+ *    src_ptr[N+1] / src_perm[E] list, for every source node, the receiver-sorted ids
+ *    of its out-edges (a stable sort of the receiver-sorted list by source).
+ *  - Node features use a component-major layout x[N][13][C] for ranks 0..2
+ *    (component 0: rank 0; 1..3: rank-1 index i; 4..12: rank-2 index 3i+j).  The
+ *    reference's flat layout (models/pure_cartesian.py:69-120) is the channel-major
+ *    [C][3^L] blocks of the true half followed by an all-zero pseudo half.
+ */
+#ifndef FSCTEP_H
+#define FSCTEP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fsc_last_error(void);
+/* ABI revision of this header (1). */
+int fsc_abi_version(void);
+
+/* ------------------------------------------------------------------ pure-cartesian-sparse
+ * conv2..n.  Replaces, per interaction layer, the chain
+ *   weights = fc(emb) ; tp(f_in[edge_src], e_flat, weights) ; scatter(., edge_dst) / (E/N)
+ * of PureCartesianSparseE3Conv2.forward (models/pure_cartesian_sparse_layers.py:382-421),
+ * i.e. the last radial-MLP Linear (fc.4), PureCartesianTensorProductO3Sparse.forward
+ * (models/pure_cartesian.py:790-863) and utils/scatter.py:63-116.
+ * Supported: lmax 2, max_rank_other 1, k_policy "k0", channels 32 or 64.
+ */
+
+/* Workspace sizes, in floats: s (node expansion, also the size of ds) and p (edge messages). */
+int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels,
+                              int64_t* s_floats, int64_t* p_floats);
+
+/* Re-layout fc.4.weight (6*C*C, 64) and fc.4.bias (6*C*C) into the two kernel operands
+ * bk1 and bk6 (each 6*65*C*C floats).  Call again whenever those parameters change. */
+int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, int32_t channels,
+                                    float* bk1, float* bk6, hipStream_t stream);
+
+/* out[N][13][C] = inv_norm * sum_{e->n} message_e.
+ * x: [N][13][C] input features; h: [E][64] radial hidden (output of fc.3, the second SiLU);
+ * n: [E][3] unit edge directions (edge_rank_powers, models/pure_cartesian.py:292-317);
+ * inv_norm: 1/max(E/N, 1e-8) as in pure_cartesian_sparse_layers.py:418-420.
+ * s_ws, p_ws: workspaces from fsc_sparse_conv_workspace; keep them for the backward. */
+int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
+                            const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
+                            const float* x, const float* h, const float* n, const float* bk1,
+                            float inv_norm, float* s_ws, float* p_ws, float* out,
+                            hipStream_t stream);
+
+/* Backward of fsc_sparse_conv_forward for forces: grad_x [N][13][C], grad_h [E][64],
+ * grad_n [E][3] from grad_out [N][13][C].  ds_ws: scratch of s_floats floats.
+ * edge_dst: [E] receiver of each receiver-sorted edge. */
+int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
+                             const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
+                             const int32_t* edge_dst, const float* grad_out, const float* h,
+                             const float* n, const float* bk6, const float* s_ws, const float* p_ws,
+                             float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
+                             float* grad_n, hipStream_t stream);
+
+/* ------------------------------------------------------------------ conv1 (sparse)
+ * Replaces the TP + scatter + in-degree normalisation of PureCartesianSparseE3Conv.forward
+ * (models/pure_cartesian_sparse_layers.py:227-330) without external tensors or fidelity
+ * embeddings, where both TP operands are functions of the species only.
+ *
+ * Pair table from fc.4 (6*C*64, 64)/(6*C*64) and the per-species atom features
+ * atom_table [n_species][8] (= atom_mlp(atom_embedding(Z)), :258-259):
+ * mf [n_species^2][3][65][C] and mb [n_species^2][3][C][65]; pair = s_src*n_species + s_dst. */
+int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const float* atom_table,
+                                int32_t n_species, int32_t channels, float* mf, float* mb,
+                                hipStream_t stream);
+
+/* out[N][13][C] = (1/max(indeg,1)) sum_{e->n} message_e; q_ws: [E][3][C] kept for backward. */
+int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
+                             const int32_t* edge_pair, const float* h, const float* n, const float* mf,
+                             float* q_ws, float* out, hipStream_t stream);
+
+/* grad_h [E][64], grad_n [E][3] from grad_out [N][13][C]. */
+int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
+                              const int32_t* edge_pair, const float* grad_out, const float* n,
+                              const float* mb, const float* q_ws, float* grad_h, float* grad_n,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FSCTEP_H */

@@ -12,6 +12,7 @@ writes are the committed fixtures.
 
 from __future__ import annotations
 
+import json
 import os
 import sys
 
@@ -88,6 +89,9 @@ def main():
             print(name, tag, "E=", float(e.sum()), "max|e|=", float(np.abs(e).max()),
                   "max|F|=", float(np.abs(f).max()), "edges=", s.num_edges)
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **out)
+        keys = [[k, list(v.shape)] for k, v in m.state_dict().items()]
+        with open(os.path.join(HERE, name + "_state_dict.json"), "w") as fh:
+            json.dump(keys, fh, indent=0)
 
 
 if __name__ == "__main__":

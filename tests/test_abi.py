@@ -1,0 +1,73 @@
+"""The C ABI library loads (no GPU needed) and exports every symbol of include/fsctep.h;
+the model mirror holds the reference's state_dict keys and shapes."""
+
+import ctypes
+import json
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import GOLDEN, ROOT
+from fsctep_amd import _lib
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "fsctep.h")).read()
+    return sorted(set(re.findall(r"\b(fsc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = header_symbols()
+    assert len(syms) >= 9
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert lib.fsc_abi_version() == 1
+    # every declared entry point has a ctypes signature (or is a metadata call)
+    for s in syms:
+        assert s in _lib.SIGNATURES or s in ("fsc_last_error", "fsc_abi_version"), s
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    lib = _lib.load()
+    s, p = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.fsc_sparse_conv_workspace(10, 20, 64, ctypes.byref(s), ctypes.byref(p)) == 0
+    assert s.value == 10 * 18 * 65 * 64 and p.value == 20 * 18 * 64
+    assert lib.fsc_sparse_conv_workspace(10, 20, 48, ctypes.byref(s), ctypes.byref(p)) == 1
+    assert b"channels" in lib.fsc_last_error()
+    with pytest.raises(RuntimeError, match="negative"):
+        _lib.call("fsc_sparse_conv_workspace", -1, 0, 64, ctypes.byref(s), ctypes.byref(p))
+
+
+@pytest.mark.parametrize("name,channels,layers", [("sparse_open32_c32_l2", 32, 2), ("sparse_pbc100_c64_l3", 64, 3)])
+def test_state_dict_keys_match_reference(name, channels, layers):
+    from sparse_helpers import seeded_hip_model
+    ref = json.load(open(os.path.join(GOLDEN, name + "_state_dict.json")))
+    m = seeded_hip_model(channels, layers, 0)
+    mine = [[k, list(v.shape)] for k, v in m.state_dict().items()]
+    assert sorted(map(tuple, map(lambda kv: (kv[0], tuple(kv[1])), mine))) == \
+        sorted(map(lambda kv: (kv[0], tuple(kv[1])), ref))
+
+
+def test_ops_refuse_cpu_tensors():
+    from fsctep_amd import ops  # noqa: F401
+    w = torch.zeros(6 * 32 * 32, 64)
+    b = torch.zeros(6 * 32 * 32)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        torch.ops.fsctep.sparse_prepare_weights(w, b, 32)
+
+
+def test_fake_kernels_trace_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from fsctep_amd import ops  # noqa: F401
+    with FakeTensorMode():
+        x = torch.empty(10, 13, 64)
+        h = torch.empty(30, 64)
+        n = torch.empty(30, 3)
+        bk = torch.empty(6 * 65 * 64 * 64)
+        i = torch.empty(11, dtype=torch.int32)
+        e = torch.empty(30, dtype=torch.int32)
+        out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, 0.5)
+        assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64,) and P.shape == (30 * 18 * 64,)

@@ -1,0 +1,158 @@
+"""GPU parity of the pure-cartesian-sparse HIP path against the oracle and the reference's
+golden vectors (fp32 on the GPU; tolerance 1e-5 relative, max-norm)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from sparse_helpers import (oracle_conv2, oracle_params, rel_inf, seeded_hip_model)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 1e-5
+
+
+def _graph_with_edge_cases(N, E_rand, seed):
+    """Random multigraph + a hub source (150 out-edges), a hub receiver (150 in-edges), an isolated node."""
+    g = torch.Generator().manual_seed(seed)
+    src = torch.randint(0, N - 1, (E_rand,), generator=g)
+    dst = torch.randint(0, N - 1, (E_rand,), generator=g)
+    hub_src = torch.zeros(150, dtype=torch.long)
+    hub_dst = torch.randint(2, N - 1, (150,), generator=g)
+    rin_src = torch.randint(2, N - 1, (150,), generator=g)
+    rin_dst = torch.ones(150, dtype=torch.long)
+    src = torch.cat([src, hub_src, rin_src])
+    dst = torch.cat([dst, hub_dst, rin_dst])
+    return src, dst
+
+
+@pytest.mark.parametrize("C", [64, 32])
+def test_conv2_op_matches_oracle(C):
+    from fsctep_amd import ops
+    from fsctep_amd.graph import prepare_graph
+    torch.manual_seed(1)
+    N = 40
+    src, dst = _graph_with_edge_cases(N, 400, 5)
+    E = src.shape[0]
+    x = torch.randn(N, 13, C, dtype=torch.float64)
+    h = torch.randn(E, 64, dtype=torch.float64)
+    v = torch.randn(E, 3, dtype=torch.float64)
+    n = v / v.norm(dim=1, keepdim=True)
+    L = torch.randn(6 * C * C, 64, dtype=torch.float64) / 8
+    b = torch.randn(6 * C * C, dtype=torch.float64) * 0.1
+    inv_norm = 1.0 / (E / N)
+    gr = prepare_graph(src.to(DEV), dst.to(DEV), torch.zeros(E, 3, device=DEV), N)
+    order = torch.argsort(dst, stable=True)
+    src_s, dst_s = src[order], dst[order]
+    h_s, n_s = h[order], n[order]
+    # oracle in float64 on the CPU, with autograd for the backward
+    xo, ho, no = (t.clone().requires_grad_(True) for t in (x, h_s, n_s))
+    ref = oracle_conv2(xo, ho, no, L, b, src_s, dst_s, N, inv_norm)
+    G = torch.randn_like(ref)
+    gx, gh, gn = torch.autograd.grad((ref * G).sum(), (xo, ho, no))
+    # HIP
+    bk1, bk6 = torch.ops.fsctep.sparse_prepare_weights(L.float().to(DEV), b.float().to(DEV), C)
+    xd = x.float().to(DEV).requires_grad_(True)
+    hd = h_s.float().to(DEV).requires_grad_(True)
+    nd = n_s.float().to(DEV).requires_grad_(True)
+    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr, inv_norm)
+    dx, dh, dn = torch.autograd.grad(out, (xd, hd, nd), G.float().to(DEV))
+    torch.cuda.synchronize()
+    assert rel_inf(out, ref) < TOL
+    assert rel_inf(dx, gx) < TOL
+    assert rel_inf(dh, gh) < TOL
+    assert rel_inf(dn, gn) < TOL
+    # isolated node N-1 has neither in- nor out-edges
+    assert float(out[N - 1].abs().max()) == 0.0 and float(dx[N - 1].abs().max()) == 0.0
+
+
+def _inputs(g, dtype=torch.float32, device=DEV):
+    n = g["pos"].shape[0]
+    return dict(pos=torch.tensor(g["pos"], dtype=dtype, device=device),
+                A=torch.tensor(g["species"], device=device),
+                batch=torch.zeros(n, dtype=torch.long, device=device),
+                src=torch.tensor(g["edge_src"], device=device), dst=torch.tensor(g["edge_dst"], device=device),
+                shifts=torch.tensor(g["edge_shifts"], dtype=dtype, device=device),
+                cell=torch.tensor(g["cell"], dtype=dtype, device=device))
+
+
+def _hip_energy_forces(model, d):
+    from fsctep_amd.sparse import energy_and_forces
+    gr = model.prepare(d["src"], d["dst"], d["shifts"], d["pos"].shape[0], d["A"])
+    return energy_and_forces(model, d["pos"], d["batch"], d["cell"], gr)
+
+
+@pytest.mark.parametrize("name", ["sparse_open32_c32_l2", "sparse_pbc100_c64_l3"])
+def test_model_matches_reference_golden(name):
+    g = load_golden(name)
+    m = seeded_hip_model(int(g["channels"]), int(g["layers"]), int(g["param_seed"])).to(DEV)
+    e, f = _hip_energy_forces(m, _inputs(g))
+    assert rel_inf(e, g["energy_f64"]) < TOL
+    assert rel_inf(f, g["forces_f64"]) < TOL
+    assert abs(float(e.sum()) - float(g["energy_f64"].sum())) < TOL * float(np.abs(g["energy_f64"]).sum())
+
+
+def test_model_forward_signature_matches_reference():
+    g = load_golden("sparse_open32_c32_l2")
+    m = seeded_hip_model(32, 2, int(g["param_seed"])).to(DEV)
+    d = _inputs(g)
+    # reference call signature, unsorted edge order
+    perm = torch.randperm(d["src"].shape[0], generator=torch.Generator().manual_seed(0)).to(DEV)
+    e = m(d["pos"], d["A"], d["batch"], d["src"][perm], d["dst"][perm], d["shifts"][perm], d["cell"])
+    assert e.shape == (d["pos"].shape[0], 1)
+    assert rel_inf(e.squeeze(-1), g["energy_f64"]) < TOL
+
+
+def test_model_matches_oracle_periodic_300():
+    from fsctep_amd.synthetic import make_system
+    from oracle import sparse_ref as R
+    s = make_system(300, density=0.1, periodic=True, seed=5)
+    g = dict(pos=s.pos, species=s.species, edge_src=s.edge_src, edge_dst=s.edge_dst,
+             edge_shifts=s.edge_shifts, cell=s.cell)
+    cfg, p = oracle_params(64, 3, 77, torch.float64)
+    d64 = _inputs(g, torch.float64, "cpu")
+    e_ref, f_ref = R.energy_forces(d64["pos"], d64["A"], d64["batch"], d64["src"], d64["dst"], d64["shifts"],
+                                   d64["cell"], p, cfg)
+    m = seeded_hip_model(64, 3, 77).to(DEV)
+    e, f = _hip_energy_forces(m, _inputs(g))
+    assert rel_inf(e, e_ref) < TOL
+    assert rel_inf(f, f_ref) < TOL
+
+
+def test_model_is_deterministic_and_o3_invariant():
+    g = load_golden("sparse_pbc100_c64_l3")
+    m = seeded_hip_model(64, 3, 9).to(DEV)
+    d = _inputs(g)
+    e1, f1 = _hip_energy_forces(m, d)
+    e2, f2 = _hip_energy_forces(m, d)
+    assert torch.equal(e1, e2) and torch.equal(f1, f2)
+    rng = np.random.default_rng(4)
+    q, r = np.linalg.qr(rng.standard_normal((3, 3)))
+    q = q * np.sign(np.diag(r))
+    if np.linalg.det(q) > 0:
+        q = -q
+    Q = torch.tensor(q, dtype=torch.float32, device=DEV)
+    d2 = dict(d)
+    d2["pos"] = d["pos"] @ Q.T
+    d2["cell"] = d["cell"] @ Q.T
+    e3, f3 = _hip_energy_forces(m, d2)
+    assert rel_inf(e3, e1) < TOL
+    assert rel_inf(f3, f1 @ Q.T) < TOL
+
+
+def test_model_without_edges():
+    from oracle import sparse_ref as R
+    g = load_golden("sparse_open32_c32_l2")
+    g = dict(g)
+    for k in ("edge_src", "edge_dst"):
+        g[k] = g[k][:0]
+    g["edge_shifts"] = g["edge_shifts"][:0]
+    cfg, p = oracle_params(32, 2, 3, torch.float64)
+    d64 = _inputs(g, torch.float64, "cpu")
+    e_ref, f_ref = R.energy_forces(d64["pos"], d64["A"], d64["batch"], d64["src"], d64["dst"], d64["shifts"],
+                                   d64["cell"], p, cfg)
+    m = seeded_hip_model(32, 2, 3).to(DEV)
+    e, f = _hip_energy_forces(m, _inputs(g))
+    assert rel_inf(e, e_ref) < TOL
+    assert float(f.abs().max()) == 0.0
