@@ -16,6 +16,8 @@ _pi64 = ctypes.POINTER(ctypes.c_int64)
 
 # name -> argtypes (all return int status)
 SIGNATURES = {
+    "fsc_timing_begin": [ctypes.c_char_p],
+    "fsc_timing_end": [ctypes.POINTER(ctypes.c_double), _pi64],
     "fsc_sparse_conv_workspace": [_i64, _i64, _i32, _pi64, _pi64],
     "fsc_sparse_conv_prepare_weights": [_p, _p, _i32, _p, _p, _p],
     "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p],
@@ -65,3 +67,23 @@ def ptr(t) -> int:
 def stream_handle(device) -> int:
     import torch
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+class KernelTimer:
+    """Context manager: summed HIP-event duration of every launch of one named kernel."""
+
+    def __init__(self, kernel: str):
+        self.kernel = kernel
+        self.total_ms = 0.0
+        self.launches = 0
+
+    def __enter__(self):
+        call("fsc_timing_begin", self.kernel.encode())
+        return self
+
+    def __exit__(self, *exc):
+        ms = ctypes.c_double()
+        n = ctypes.c_int64()
+        call("fsc_timing_end", ctypes.byref(ms), ctypes.byref(n))
+        self.total_ms, self.launches = ms.value, n.value
+        return False

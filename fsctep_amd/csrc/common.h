@@ -43,6 +43,16 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 
 void set_error(const std::string& msg);
 int check_launch(const char* what);
+int timing_mark_begin(const char* kernel, hipStream_t st);
+void timing_mark_end(int slot, hipStream_t st);
+
+// Brackets one launch with HIP events when fsc_timing_begin(name) is active.
+struct LaunchTimer {
+  int slot;
+  hipStream_t st;
+  LaunchTimer(const char* name, hipStream_t s) : slot(timing_mark_begin(name, s)), st(s) {}
+  ~LaunchTimer() { timing_mark_end(slot, st); }
+};
 
 }  // namespace fsc
 

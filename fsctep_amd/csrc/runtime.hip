@@ -2,6 +2,7 @@
 #include "common.h"
 
 #include <mutex>
+#include <vector>
 
 namespace fsc {
 
@@ -18,9 +19,79 @@ int check_launch(const char* what) {
   return 0;
 }
 
+// ---------------------------------------------------------------- launch timing
+// Opt-in measurement of one kernel's launches with HIP events recorded on the launch
+// stream (fsc_timing_begin / fsc_timing_end).  Off by default; costs nothing when off.
+namespace {
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  std::string kernel;
+  std::vector<hipEvent_t> events;   // start/stop pairs
+};
+Timing g_timing;
+}  // namespace
+
+int timing_mark_begin(const char* kernel, hipStream_t st) {
+  if (!g_timing.on) return -1;
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  if (!g_timing.on || g_timing.kernel != kernel) return -1;
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return -1;
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return -1;
+  }
+  g_timing.events.push_back(a);
+  g_timing.events.push_back(b);
+  (void)hipEventRecord(a, st);
+  return (int)g_timing.events.size() - 1;
+}
+
+void timing_mark_end(int slot, hipStream_t st) {
+  if (slot < 0) return;
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  (void)hipEventRecord(g_timing.events[slot], st);
+}
+
 }  // namespace fsc
 
 extern "C" {
+
+int fsc_timing_begin(const char* kernel_name) {
+  FSC_CHECK_ARG(kernel_name != nullptr, "fsc_timing_begin: null kernel name");
+  std::lock_guard<std::mutex> lk(fsc::g_timing.mu);
+  FSC_CHECK_ARG(!fsc::g_timing.on, "fsc_timing_begin: timing already active");
+  fsc::g_timing.on = true;
+  fsc::g_timing.kernel = kernel_name;
+  fsc::g_timing.events.clear();
+  return 0;
+}
+
+int fsc_timing_end(double* total_ms, int64_t* launches) {
+  FSC_CHECK_ARG(total_ms && launches, "fsc_timing_end: null output");
+  std::lock_guard<std::mutex> lk(fsc::g_timing.mu);
+  FSC_CHECK_ARG(fsc::g_timing.on, "fsc_timing_end: timing not active");
+  double tot = 0.0;
+  int err = 0;
+  auto& ev = fsc::g_timing.events;
+  for (size_t i = 0; i + 1 < ev.size(); i += 2) {
+    float ms = 0.f;
+    if (hipEventSynchronize(ev[i + 1]) != hipSuccess || hipEventElapsedTime(&ms, ev[i], ev[i + 1]) != hipSuccess)
+      err = 1;
+    tot += ms;
+  }
+  *total_ms = tot;
+  *launches = (int64_t)(ev.size() / 2);
+  for (auto e : ev) (void)hipEventDestroy(e);
+  ev.clear();
+  fsc::g_timing.on = false;
+  if (err) {
+    fsc::set_error("fsc_timing_end: event query failed");
+    return 2;
+  }
+  return 0;
+}
 
 const char* fsc_last_error(void) { return fsc::g_last_error.c_str(); }
 

@@ -651,12 +651,19 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
   for (int p = 0; p < 6; ++p) {
     const int64_t rows = N * kNumI[kPathL1H[p]];
     dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((65 * C + 255) / 256));
+    LaunchTimer tm("node_expand", st);
     node_expand_kernel<C><<<grid, 256, 0, st>>>(x, bk1, S, N, p);
   }
   if (check_launch("sparse node_expand")) return 2;
-  edge_message_kernel<C><<<(unsigned)N, 256, 0, st>>>(h, S, src_ptr, src_perm, P);
+  {
+    LaunchTimer tm("edge_message", st);
+    edge_message_kernel<C><<<(unsigned)N, 256, 0, st>>>(h, S, src_ptr, src_perm, P);
+  }
   if (check_launch("sparse edge_message")) return 2;
-  receiver_sum_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(P, nvec, dst_ptr, scale, out, N);
+  {
+    LaunchTimer tm("receiver_sum", st);
+    receiver_sum_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(P, nvec, dst_ptr, scale, out, N);
+  }
   return check_launch("sparse receiver_sum") ? 2 : 0;
 }
 
@@ -667,13 +674,20 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        const float* P, float scale, float* dS, float* dx, float* dh, float* dn,
                        hipStream_t st) {
   if (N == 0) return 0;
-  direction_grad_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(G, P, nvec, dst_ptr, scale, dn, N);
+  {
+    LaunchTimer tm("direction_grad", st);
+    direction_grad_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(G, P, nvec, dst_ptr, scale, dn, N);
+  }
   if (check_launch("sparse direction_grad")) return 2;
-  edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(G, nvec, h, S, src_ptr, src_perm,
-                                                           edge_dst, scale, dh, dS);
+  {
+    LaunchTimer tm("edge_message_grad", st);
+    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(G, nvec, h, S, src_ptr, src_perm,
+                                                             edge_dst, scale, dh, dS);
+  }
   if (check_launch("sparse edge_message_grad")) return 2;
   for (int g = 0; g < 3; ++g) {
     const int64_t rows = N * kNumI[g];
+    LaunchTimer tm("node_expand_grad", st);
     node_expand_grad_kernel<C><<<(unsigned)((rows + 63) / 64), 256, 0, st>>>(dS, bk6, dx, N, g);
   }
   return check_launch("sparse node_expand_grad") ? 2 : 0;
@@ -766,6 +780,7 @@ int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
   if (n_nodes == 0) return 0;
   const unsigned grid = (unsigned)((n_nodes + 3) / 4);
+  LaunchTimer tm("conv1_forward", stream);
   if (channels == 64)
     conv1_forward_kernel<64><<<grid, 256, 0, stream>>>(h, n, edge_pair, mf, dst_ptr, q_ws, out, n_nodes);
   else if (channels == 32)
@@ -788,6 +803,7 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                 "fsc_sparse_conv1_backward: null edge pointer");
   if (n_nodes == 0) return 0;
   const unsigned grid = (unsigned)((n_nodes + 3) / 4);
+  LaunchTimer tm("conv1_backward", stream);
   if (channels == 64)
     conv1_backward_kernel<64><<<grid, 256, 0, stream>>>(grad_out, n, edge_pair, mb, q_ws, dst_ptr, grad_h,
                                                         grad_n, n_nodes);

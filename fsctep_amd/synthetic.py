@@ -207,3 +207,11 @@ def seeded_value(key: str, shape, seed: int) -> np.ndarray:
 def seeded_state_dict(named_shapes, seed: int) -> dict[str, np.ndarray]:
     """``{key: float64 array}`` for an iterable of ``(key, shape)``."""
     return {k: seeded_value(k, s, seed) for k, s in named_shapes}
+
+
+def apply_seeded_parameters(module, seed: int) -> None:
+    """Overwrite every parameter of ``module`` with ``seeded_value(name, shape, seed)``."""
+    import torch
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            p.copy_(torch.from_numpy(seeded_value(name, tuple(p.shape), seed)).to(p.dtype))

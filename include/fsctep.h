@@ -31,6 +31,13 @@ const char* fsc_last_error(void);
 /* ABI revision of this header (1). */
 int fsc_abi_version(void);
 
+/* Measurement (no counterpart in the reference): while active, every launch of the named
+ * kernel ("node_expand", "edge_message", "receiver_sum", "direction_grad",
+ * "edge_message_grad", "node_expand_grad") is bracketed by HIP events on its stream.
+ * fsc_timing_end synchronises those events and returns the summed duration. */
+int fsc_timing_begin(const char* kernel_name);
+int fsc_timing_end(double* total_ms, int64_t* launches);
+
 /* ------------------------------------------------------------------ pure-cartesian-sparse
  * conv2..n.  Replaces, per interaction layer, the chain
  *   weights = fc(emb) ; tp(f_in[edge_src], e_flat, weights) ; scatter(., edge_dst) / (E/N)
