@@ -180,8 +180,9 @@ def seeded_value(key: str, shape, seed: int) -> np.ndarray:
     """Deterministic float64 value for one state_dict entry.
 
     Scale rules: LayerNorm gain 1+0.1N, LayerNorm/Linear bias 0.1N, Linear weight
-    N/sqrt(fan_in), embedding N, bilinear readout weights 0.02N, zero-initialised
-    scalars (weighted sums, external-field scales) 0.1N.
+    N/sqrt(fan_in), per-path tensor-product weight (P, out, in1, in2) N/sqrt(in1*in2),
+    embedding N, bilinear readout weights 0.02N, zero-initialised scalars (weighted
+    sums, external-field scales) 0.1N.
     """
     rng = _key_rng(seed, key)
     shape = tuple(int(s) for s in shape)
@@ -195,12 +196,12 @@ def seeded_value(key: str, shape, seed: int) -> np.ndarray:
         return 0.1 * z
     if "embedding" in key and leaf == "weight":
         return z
-    if key.startswith("product_3.W") or ".product_3.W" in key:
+    if key.startswith(("product_3.W", "W_read.")) or ".product_3.W" in key:
         return 0.02 * z
     if leaf == "weight" and len(shape) == 2:
         return z / math.sqrt(shape[1])
     if leaf == "weight" and len(shape) >= 3:
-        return z / math.sqrt(float(np.prod(shape[2:])) * max(shape[1] if len(shape) > 3 else 1, 1))
+        return z / math.sqrt(float(np.prod(shape[2:])))      # per-path (out, in1, in2): fan-in in1*in2
     return 0.1 * z
 
 
