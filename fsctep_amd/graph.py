@@ -28,6 +28,7 @@ class Graph:
     species_index: torch.Tensor | None = None   # (N,) int64 index into `species`
     species: torch.Tensor | None = None         # (S,) int64 distinct atomic numbers (sorted)
     edge_pair: torch.Tensor | None = None       # (E,) int32 species-pair index src*S+dst
+    species_index32: torch.Tensor | None = None # (N,) int32
 
 
 def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: torch.Tensor,
@@ -56,6 +57,7 @@ def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: t
         uniq, inv = torch.unique(species.long(), sorted=True, return_inverse=True)
         g.species = uniq
         g.species_index = inv
+        g.species_index32 = inv.to(torch.int32).contiguous()
         S = int(uniq.shape[0])
         g.edge_pair = (inv[src] * S + inv[dst]).to(torch.int32).contiguous()
     return g

@@ -1,0 +1,318 @@
+"""``pure-cartesian-ictd`` and ``pure-cartesian-ictd-o3`` trunks on the HIP kernels.
+
+``PureCartesianICTDTransformerLayer`` (reference models/pure_cartesian_ictd_layers_full.py:476-1078) and
+``PureCartesianICTDO3TransformerLayer`` (models/pure_cartesian_ictd_layers_o3.py:535-1074) take the
+reference's constructor arguments and hold its parameters under the same state_dict keys.  Message
+passing runs in ``libfsctep_hip.so`` (``torch.ops.fsctep.ictd_conv1`` / ``ictd_conv``); edge geometry,
+direction harmonics, radial MLPs and the readout stay in PyTorch.  Node features are x[N][M][C]
+(component-major over the active irreps); the readout rebuilds the reference's flat per-layer layout
+because the reference re-splits the layer-concatenated vector with n_layers*C channels
+(full :977-979, o3 :987-988) and its energy depends on that exact arrangement.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ictd_ops
+from .graph import Graph, prepare_graph
+from .ictd_basis import canonical, coupling, harmonic_projection, layout_full, layout_o3
+from .radial import radial_basis
+from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
+
+
+def _key_str(k) -> str:
+    return f"{k[0]}{'e' if k[1] > 0 else 'o'}"
+
+
+class _TPWeights(nn.Module):
+    """Parameter holder of HarmonicFullyConnectedTensorProduct[O3] (internal weights (P, O, I, J))."""
+
+    def __init__(self, num_paths, mul_out, mul_in1, mul_in2):
+        super().__init__()
+        self.num_paths = num_paths
+        self.weight = nn.Parameter(torch.randn(num_paths, mul_out, mul_in1, mul_in2) * 0.02)
+
+
+class _Conv1(nn.Module):
+    """conv1 parameters: ICTDIrrepsE3Conv (:211-339) / ICTDO3E3Conv (:298-422)."""
+
+    def __init__(self, o3, n_ref, n_keys, lmax, number_of_basis, channels_out, embedding_dim, max_atomvalue,
+                 output_size, external_field):
+        super().__init__()
+        self.atom_embedding = nn.Embedding(max_atomvalue, embedding_dim)
+        self.atom_mlp = nn.Sequential(nn.Linear(embedding_dim, 64), nn.SiLU(), nn.Linear(64, output_size))
+        self.fidelity_embedding = None
+        self.tp2 = _TPWeights(n_ref, channels_out, output_size, output_size)
+        self.fc = _radial_mlp(n_ref, number_of_basis)
+        if external_field:
+            if o3:
+                self.external_tensor_scale_by_irrep = nn.Parameter(torch.zeros(n_keys))
+            else:
+                self.external_tensor_scale_by_l = nn.Parameter(torch.zeros(lmax + 1))
+
+
+class _ICTDTrunk(nn.Module):
+    o3 = False
+
+    def __init__(self, max_embed_radius, main_max_radius, main_number_of_basis, hidden_dim_conv,
+                 hidden_dim_sh=None, hidden_dim=64, channel_in2=32, embedding_dim=16, max_atomvalue=10,
+                 output_size=8, embed_size=None, main_hidden_sizes3=None, num_layers=1, num_interaction=2,
+                 device=None, function_type_main="gaussian", lmax=2, ictd_tp_path_policy="full",
+                 ictd_tp_max_rank_other=None, internal_compute_dtype=None, ictd_tp_backend="auto",
+                 invariant_channels=32, physical_tensor_outputs=None, external_tensor_rank=None,
+                 external_tensor_irrep=None, external_tensor_parity=None, external_tensor_specs=None,
+                 o3_irrep_preset="auto", o3_active_irreps=None, num_fidelity_levels=0, long_range_mode="none",
+                 **unsupported):
+        super().__init__()
+        for k in unsupported:
+            if not k.startswith(("long_range_", "feature_spectral_", "external_tensor_", "multi_fidelity",
+                                 "product5_muls_by_l", "max_rank_other", "k_policy", "ictd_Lmax")):
+                raise TypeError(f"unexpected argument {k!r}")
+        if unsupported.get("product5_muls_by_l") is not None:
+            raise NotImplementedError("product5_muls_by_l adapters are outside the HIP path")
+        if ictd_tp_path_policy != "full" or long_range_mode != "none" or num_fidelity_levels or external_tensor_specs:
+            raise NotImplementedError("HIP ICTD path: path_policy 'full', no long-range, fidelity or multi-spec fields")
+        if external_tensor_rank is not None and (int(external_tensor_rank) != 1 or
+                                                 (external_tensor_irrep or "1o") != "1o"):
+            raise NotImplementedError("HIP ICTD path: external field must be a rank-1 '1o' vector")
+        embed_size = [128, 128, 128] if embed_size is None else list(embed_size)
+        self.lmax = int(lmax)
+        self.channels = int(hidden_dim_conv)
+        self.num_interaction = int(num_interaction)
+        if self.num_interaction < 2:
+            raise ValueError(f"num_interaction must be >= 2, got {self.num_interaction}")
+        if self.channels not in (32, 64, 128) or output_size != 8:
+            raise NotImplementedError("HIP ICTD path: hidden_dim_conv 32/64/128 and output_size 8")
+        self.invariant_channels = int(invariant_channels)
+        self.max_radius = float(max_embed_radius)
+        self.number_of_basis = int(main_number_of_basis)
+        self.function_type = str(function_type_main)
+        self.external_field = external_tensor_rank is not None
+        self.layout = self._make_layout(o3_irrep_preset, o3_active_irreps, physical_tensor_outputs)
+        self.keys = list(self.layout.keys)
+        self.layout_id = ictd_ops.register_layout(self.layout)
+        n_ref = self.layout.n_ref_paths()
+        self.e3_conv_emb = _Conv1(self.o3, n_ref, len(self.keys), self.lmax, main_number_of_basis, self.channels,
+                                  embedding_dim, max_atomvalue, output_size, self.external_field)
+        self.tp2_layers = nn.ModuleList([_TPWeights(n_ref, self.channels, self.channels, 1)
+                                         for _ in range(self.num_interaction - 1)])
+        self.fc2_layers = nn.ModuleList([_radial_mlp(n_ref, main_number_of_basis)
+                                         for _ in range(self.num_interaction - 1)])
+        nC = self.channels * self.num_interaction
+        S = (self.num_interaction - 1) * self.invariant_channels
+        wr = [nn.Parameter(torch.randn(S, nC, nC) * 0.02) for _ in self.keys]
+        if self.o3:
+            self.W_read = nn.ParameterDict({_key_str(k): w for k, w in zip(self.keys, wr)})
+        else:
+            self.W_read = nn.ParameterList(wr)
+        self.readout_linear = nn.Sequential(nn.Linear(S + nC * len(self.keys), embed_size[0]), nn.SiLU(),
+                                            nn.Linear(embed_size[0], 17))
+        self.weighted_sum = RobustScalarWeightedSum(17, init_weights="zero")
+        self.proj_total = MainNet(self.num_interaction * self.channels * len(self.keys) + S, embed_size, 17)
+        self.physical_tensor_heads = None
+        self._dipole = False
+        if physical_tensor_outputs:
+            if set(physical_tensor_outputs) != {"dipole"}:
+                raise NotImplementedError("HIP ICTD path: only a 'dipole' physical tensor head")
+            spec = physical_tensor_outputs["dipole"]
+            if spec.get("reduce", "sum") != "sum" or int(spec.get("channels_out", 1)) != 1:
+                raise NotImplementedError("HIP ICTD path: dipole head with reduce 'sum', channels_out 1")
+            self.physical_tensor_heads = nn.ModuleDict(
+                {"dipole": nn.ModuleDict({"1": nn.Linear(nC, 1, bias=False)})})
+            self._dipole = True
+        self._cache = {}
+
+    def _make_layout(self, preset, active, phys):
+        return layout_full(self.lmax)
+
+    # ------------------------------------------------------------------ device constants
+    def _consts(self, device):
+        key = ("consts", str(device))
+        if key not in self._cache:
+            proj = []
+            for l in range(self.lmax + 1):
+                exps, coef, P = harmonic_projection(l)
+                proj.append((torch.tensor(exps, device=device), torch.tensor(coef, dtype=torch.float32, device=device),
+                             torch.tensor(P, dtype=torch.float32, device=device)))
+            cg = torch.tensor(self.layout.cg_table(), dtype=torch.float32, device=device)
+            c1 = [p["gate"] for p in self.layout.conv1_paths()]
+            factors = [float(coupling(k[0], k[0], 0)[0, 0, 0]) for k in self.keys]
+            self._cache[key] = (proj, cg, torch.tensor(c1, device=device), factors)
+        return self._cache[key]
+
+    def _wt(self, tp):
+        w = tp.weight
+        key = ("wt", id(tp), w.data_ptr(), w._version)
+        if key not in self._cache:
+            for k in [k for k in self._cache if k[0] == "wt" and k[1] == id(tp)]:
+                del self._cache[k]
+            with torch.no_grad():
+                self._cache[key] = torch.ops.fsctep.ictd_prepare_weights(w.detach())
+        return self._cache[key]
+
+    def harmonics(self, n, proj):
+        """Y[E][(lmax+1)^2] in the ICTD basis (models/ictd_irreps.py:371-402), integer powers by products."""
+        ys = []
+        pw = [[torch.ones_like(n[:, i])] for i in range(3)]
+        for i in range(3):
+            for _ in range(self.lmax):
+                pw[i].append(pw[i][-1] * n[:, i])
+        for l in range(self.lmax + 1):
+            exps, coef, P = proj[l]
+            cols = [pw[0][int(a)] * pw[1][int(b)] * pw[2][int(c)] for a, b, c in exps.tolist()]
+            ys.append((torch.stack(cols, dim=-1) * coef) @ P)
+        return torch.cat(ys, dim=-1)
+
+    # ------------------------------------------------------------------ forward
+    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
+        g = prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A)
+        if g.species.shape[0] > 8:
+            raise NotImplementedError("HIP ICTD conv1: at most 8 distinct species per system")
+        return g
+
+    def _check_inference(self):
+        if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            raise NotImplementedError("the HIP ICTD path computes energies and forces only; call .eval() or "
+                                      ".requires_grad_(False)")
+
+    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
+                sync_after_scatter=None, external_tensor=None, external_tensor_blocks=None, fidelity_ids=None,
+                return_physical_tensors=False, return_reciprocal_source=False):
+        if sync_after_scatter is not None or external_tensor_blocks is not None or fidelity_ids is not None:
+            raise NotImplementedError("sync hooks, external blocks and fidelity ids are outside the HIP path")
+        key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (edge_src, edge_dst, edge_shifts, A))
+        if self._cache.get("graph_key") != key:
+            self._cache["graph"] = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+            self._cache["graph_key"] = key
+        e, dip = self.forward_graph(pos, batch, cell, self._cache["graph"], external_tensor=external_tensor)
+        if return_physical_tensors:
+            return e, {"dipole": {1: dip}} if dip is not None else {}
+        return e
+
+    def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None):
+        """((N,1) atomic energies, (G,1,3) dipole or None) for a prepared graph."""
+        self._check_inference()
+        if not pos.is_cuda:
+            raise RuntimeError("the HIP ICTD path runs on the GPU only")
+        f32 = torch.float32
+        pos, cell = pos.to(f32), cell.to(f32)
+        proj, cg, c1_gates, factors = self._consts(pos.device)
+        vec = pos[g.dst] - pos[g.src] + torch.einsum("ni,nij->nj", g.shifts.to(f32), cell[batch[g.src]])
+        r = vec.norm(dim=1)
+        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+        Y = self.harmonics(n, proj)
+        emb = radial_basis(r, self.max_radius, self.number_of_basis, self.function_type)
+
+        c1 = self.e3_conv_emb
+        atab = c1.atom_mlp(c1.atom_embedding(g.species)).detach()
+        W1 = c1.tp2.weight.detach()[c1_gates]                                  # (NP1, C, 8, 8)
+        NS = atab.shape[0]
+        qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
+        F_in = Y
+        if self.external_field:
+            if external_tensor is None:
+                raise ValueError("this model was built with an external field; pass external_tensor")
+            fld = external_tensor.to(f32).reshape(-1, 3)[:, [2, 1, 0]]      # rank-1 -> l=1 block order (z,y,x)
+            if self.o3:
+                s = c1.external_tensor_scale_by_irrep[self.keys.index((1, -1))]
+            else:
+                s = c1.external_tensor_scale_by_l[1]
+            add = torch.zeros_like(Y)
+            add[:, 1:4] = fld[batch[g.src]] * s.detach()
+            F_in = Y + add
+        elif external_tensor is not None:
+            raise ValueError("external_tensor given but the model has no external field")
+        feats = [ictd_ops.ictd_conv1_apply(F_in, c1.fc(emb), qtab, g, self.layout_id)]
+        for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
+            feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, fc2(emb), tp.weight.detach(), self._wt(tp), cg, g,
+                                                  self.layout_id))
+        return self.readout(feats, batch, factors)
+
+    def _to_ref_flat(self, f):
+        """x[N][M][C] -> reference flat (N, C*M): per key a channel-major (C, 2l+1) block."""
+        N = f.shape[0]
+        parts, off = [], 0
+        for k in self.keys:
+            d = 2 * k[0] + 1
+            parts.append(f[:, off:off + d, :].transpose(1, 2).reshape(N, -1))
+            off += d
+        return torch.cat(parts, dim=-1)
+
+    def _wread(self, i, k):
+        return self.W_read[_key_str(k)] if self.o3 else self.W_read[i]
+
+    def readout(self, feats, batch, factors):
+        """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included."""
+        N = feats[0].shape[0]
+        nC = self.channels * self.num_interaction
+        fc = torch.cat([self._to_ref_flat(f) for f in feats], dim=-1)
+        xb, off = {}, 0
+        for k in self.keys:
+            d = 2 * k[0] + 1
+            xb[k] = fc[:, off:off + nC * d].reshape(N, nC, d)
+            off += nC * d
+        scalars = 0
+        for i, k in enumerate(self.keys):
+            t = xb[k]
+            gram = torch.bmm(t, t.transpose(1, 2).contiguous()) / math.sqrt(2 * k[0] + 1)
+            W = self._wread(i, k)
+            scalars = scalars + gram.reshape(N, -1) @ W.reshape(W.shape[0], -1).t()
+        outs, off = [], 0
+        for i, k in enumerate(self.keys):
+            d = 2 * k[0] + 1
+            T = torch.cat([f[:, off:off + d, :] for f in feats], dim=2)        # (N, d, n*C)
+            sq = (T * T).sum(1)
+            if k == (0, 1):
+                sq = torch.cat([sq, scalars * scalars], dim=-1)
+            outs.append(sq * factors[i])
+            off += d
+        e = self.weighted_sum(self.proj_total(torch.cat(outs, dim=-1)))
+        dip = None
+        if self._dipole:
+            y = torch.einsum("ncm,oc->nom", xb[(1, -1)], self.physical_tensor_heads["dipole"]["1"].weight)
+            G = int(batch.max()) + 1 if batch.numel() else 0
+            dip = y.new_zeros(G, 1, 3).index_add(0, batch, y)
+        return e, dip
+
+
+class PureCartesianICTDTransformerLayer(_ICTDTrunk):
+    """Drop-in for the reference ``pure-cartesian-ictd`` trunk (lmax 2 or 3)."""
+
+    o3 = False
+
+    def _make_layout(self, preset, active, phys):
+        if self.lmax not in (2, 3):
+            raise NotImplementedError("HIP ICTD path: lmax 2 or 3")
+        return layout_full(self.lmax)
+
+
+class PureCartesianICTDO3TransformerLayer(_ICTDTrunk):
+    """Drop-in for the reference ``pure-cartesian-ictd-o3`` trunk with explicit active irreps."""
+
+    o3 = True
+
+    def _make_layout(self, preset, active, phys):
+        if active is None:
+            raise NotImplementedError("HIP ICTD-O3 path: pass o3_active_irreps explicitly")
+        items = active.replace(",", " ").replace("+", " ").split() if isinstance(active, str) else list(active)
+        keys = [(int(s[:-1]), 1 if s[-1] == "e" else -1) for s in items]
+        if self.external_field and (1, -1) not in keys:
+            keys.append((1, -1))
+        for l in range(self.lmax + 1):
+            if canonical(l) not in keys:
+                raise NotImplementedError("HIP ICTD-O3 path: the geometric irreps 0e,1o,2e,.. must be active")
+        return layout_o3(self.lmax, keys)
+
+
+def energy_forces(model, pos, batch, cell, graph, external_tensor=None):
+    """(per-atom energies (N,), forces (N,3), dipole or None)."""
+    pos = pos.detach().requires_grad_(True)
+    e, dip = model.forward_graph(pos, batch, cell, graph, external_tensor=external_tensor)
+    (grad,) = torch.autograd.grad(e.sum(), pos)
+    return e.detach().squeeze(-1), -grad, (dip.detach() if dip is not None else None)

@@ -100,6 +100,61 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                               const float* mb, const float* q_ws, float* grad_h, float* grad_n,
                               hipStream_t stream);
 
+/* ------------------------------------------------------------------ ICTD (pure-cartesian-ictd / -o3)
+ * Irreps are keys (l, parity) in a fixed order; node features are x[N][M][C] with M = sum(2l+1)
+ * components (component-major), edge harmonics Y[E][(lmax+1)^2] (block l at offset l^2).
+ * A layout table describes the live tensor-product paths (second operand a geometric Y_l) grouped
+ * by first-operand key; it is built on the host (fsctep_amd/ictd_basis.py) from the active irreps.
+ */
+typedef struct FscIctdLayout {
+  int32_t M, NY, KT, NP, NG, NREF, NBGP, KTT;         /* comps, Y comps, sum d3, live paths, groups,
+                                                         reference paths, padded per-edge table, kk tiles */
+  int32_t g_o1[8], g_d1[8], g_kstart[8], g_kcount[8], g_kpad[8], g_bgoff[8], g_tile0[8];
+  int32_t tile_group[16];
+  int32_t p_gate[64], p_oy[64], p_d2[64], p_d3[64], p_koff[64], p_cgoff[64], p_group[64], p_oo[64];
+  int32_t kk_path[128];                                /* live path of each output slot kk < KT */
+  int32_t NK, k_oo[16], k_d[16];                       /* output keys: component offset, 2l+1 */
+  int32_t NP1, y_path1[16], y_oo1[16], c1_gate[16];    /* conv1: per Y component, live path (-1: none) */
+} FscIctdLayout;
+
+/* conv2..n.  Replaces the chain gates = fc2(emb); tp2(x1[edge_src], Y, gates); scatter / indeg of
+ * models/pure_cartesian_ictd_layers_full.py:938-954 (O3: pure_cartesian_ictd_layers_o3.py:956-973),
+ * i.e. HarmonicFullyConnectedTensorProduct[O3].forward (models/ictd_irreps.py:971-1253, :1512-1695)
+ * and the project/mix ops of the reference extension (csrc/ictd_tp.cpp:140-494).
+ * gates [E][NREF]; W [NREF][C][C] (tp2.weight); cg: concatenated normalised C[m1][m2][m3] of the
+ * live paths; z_ws [N][KT][C] scratch; out [N][M][C]. */
+int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                          const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
+                          const float* gates, const float* cg, const float* W, float* z_ws, float* out,
+                          hipStream_t stream);
+
+/* Wt [NREF][C][C]: W with its last two axes swapped (call again when W changes). */
+int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wt, hipStream_t stream);
+
+/* Backward for forces: grad_x [N][M][C], grad_gates [E][NREF] (caller zero-fills: entries of paths
+ * without a geometric operand stay 0), grad_Y [E][NY].  dz_ws [N][KT][C], dxe_ws [E][M][C] scratch. */
+int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                           const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
+                           const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
+                           const float* gates, const float* cg, const float* Wt, float* dz_ws,
+                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, hipStream_t stream);
+
+/* conv1 (ICTDIrrepsE3Conv / ICTDO3E3Conv, pure_cartesian_ictd_layers_full.py:341-473,
+ * pure_cartesian_ictd_layers_o3.py:424-532): both operands depend only on the species, and
+ * C(l,0,l) is the identity, so out[n][comp(l)][o] = (1/indeg) sum_e gate[e][p_l] Q[pair][p_l][o] F[e][l^2+k]
+ * with Q[pair][p][o] = sum_ij W1[p][o][i][j] A_src[i] A_dst[j] (qtab [NS*NS][NP1][C]) and
+ * F = Y plus the embedded external field on the l=1 block. */
+int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                           const int32_t* dst_ptr, const int32_t* edge_pair, const float* F, const float* gates,
+                           const float* qtab, float* out, hipStream_t stream);
+
+/* grad_F [E][NY], grad_gates [E][NREF] (caller zero-fills) from grad_out [N][M][C]. */
+int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                            int32_t n_species, const int32_t* dst_ptr, const int32_t* edge_pair,
+                            const int32_t* node_species, const float* grad_out, const float* F,
+                            const float* gates, const float* qtab, float* grad_F, float* grad_gates,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
