@@ -1,6 +1,12 @@
-"""Energy + forces throughput of the pure-cartesian-sparse hot path on one MI355X.
+"""Energy + forces throughput of the equivariant message-passing hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--atoms 10000]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode sparse|ictd|ictd-o3] [--atoms N]
+
+Workloads (``--mode``): ``sparse`` (default) is pure-cartesian-sparse, 3 layers, 64 channels,
+ranks 0..2, 10,000 atoms of 4 species; ``ictd`` is pure-cartesian-ictd, 3 layers, 128 channels,
+ranks 0..3, 10,000 atoms of 8 species; ``ictd-o3`` is pure-cartesian-ictd-o3 (0e,1e,1o,2e plus a
+rank-1 external field, dipole head), 3 layers, 64 channels, 4,000 atoms.  All are periodic cubic
+boxes at 0.1 atoms/A^3, cutoff 5 A, 8 Bessel radial functions, min pair distance 0.9 A.
 
 One step = energy and forces (F = -dE/dpos) of the whole system: edge geometry, radial
 basis and MLP, conv1..conv3 message passing (HIP kernels), readout, and the backward of
@@ -12,6 +18,7 @@ between MD list rebuilds) and not timed.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
@@ -24,10 +31,20 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
-# Per-kernel algorithmic work of one launch (conv2..n layer with N nodes, E edges, C channels).
-# flops: useful multiply-adds x2 of the reassociated product; bytes: compulsory fp32 traffic of
-# the kernel's inputs/outputs at its boundary (each array once).
-def kernel_work(name: str, N: int, E: int, C: int) -> dict:
+WORKLOADS = {
+    "sparse": dict(atoms=10000, species=4, seed=22, channels=64, layers=3, lmax=2, kernel="edge_message_grad",
+                   cpu_atoms=300),
+    "ictd": dict(atoms=10000, species=8, seed=33, channels=128, layers=3, lmax=3, kernel="ictd_project_grad",
+                 cpu_atoms=200),
+    "ictd-o3": dict(atoms=4000, species=4, seed=44, channels=64, layers=3, lmax=2, kernel="ictd_project_grad",
+                    cpu_atoms=200),
+}
+
+
+# Per-kernel algorithmic work of one launch (one conv2..n layer with N nodes, E edges, C channels).
+# flops: useful multiply-adds x2; bytes: compulsory fp32 traffic at the kernel's boundary (each
+# array once, node gathers counted once per node).
+def sparse_kernel_work(name: str, N: int, E: int, C: int) -> dict:
     K = 64
     s_bytes = 4 * N * 18 * 65 * C            # node expansion S (or dS)
     p_bytes = 4 * E * 18 * C                 # edge messages P
@@ -54,6 +71,25 @@ def kernel_work(name: str, N: int, E: int, C: int) -> dict:
     raise KeyError(name)
 
 
+def ictd_kernel_work(name: str, L, N: int, E: int, C: int) -> dict:
+    """``L`` is the layout table of the model (components M, coupled rows KT, paths, groups)."""
+    M, KT, NY, NREF = L.M, L.KT, L.NY, L.NREF
+    # useful (m1, kk) pairs per edge: input component m1 of group g couples to that group's rows
+    pairs = sum(L.g_d1[g] * L.g_kcount[g] for g in range(L.NG))
+    edge_in = 4 * E * (1 + NY + NREF)        # source index, harmonics, gates
+    x_b, z_b = 4 * N * M * C, 4 * N * KT * C
+    if name == "ictd_project":
+        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * N, bound="hbm")
+    if name == "ictd_project_grad":
+        return dict(flops=2 * 2 * E * pairs * C, bytes=z_b + x_b + edge_in + 4 * E * M * C + 4 * E * (NREF + NY),
+                    bound="hbm")
+    if name == "ictd_source_sum":
+        return dict(flops=E * M * C, bytes=4 * E * M * C + x_b + 4 * (E + N), bound="hbm")
+    if name in ("ictd_mix", "ictd_mix_grad"):
+        return dict(flops=2 * N * KT * C * C, bytes=z_b + x_b + 4 * L.NP * C * C, bound="mfma")
+    raise KeyError(name)
+
+
 def gpu_info():
     import torch
     p = torch.cuda.get_device_properties(0)
@@ -61,38 +97,99 @@ def gpu_info():
             "hbm_gib": round(p.total_memory / 2 ** 30, 1)}
 
 
-def cpu_baseline(n_atoms: int, steps: int, seed: int) -> dict:
-    """The oracle (the reference's algorithm restated in PyTorch on the CPU) on host cores."""
-    import torch
-    from fsctep_amd.synthetic import make_system, seeded_value
-    from oracle import sparse_ref as R
-
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
-    s = make_system(n_atoms, density=0.1, periodic=True, seed=seed)
-    cfg = R.SparseConfig(channels=64, num_interaction=3, function_type="bessel")
-    p = {k: torch.tensor(seeded_value(k, sh, 1), dtype=torch.float32) for k, sh in R.param_shapes(cfg)}
-    args = (torch.tensor(s.pos, dtype=torch.float32), torch.tensor(s.species),
-            torch.zeros(n_atoms, dtype=torch.long), torch.tensor(s.edge_src), torch.tensor(s.edge_dst),
-            torch.tensor(s.edge_shifts, dtype=torch.float32), torch.tensor(s.cell, dtype=torch.float32))
-    R.energy_forces(*args, p, cfg)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        R.energy_forces(*args, p, cfg)
-    dt = (time.perf_counter() - t0) / steps
-    cpu_model = ""
+def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as fh:
             for ln in fh:
                 if ln.startswith("model name"):
-                    cpu_model = ln.split(":", 1)[1].strip()
-                    break
+                    return ln.split(":", 1)[1].strip()
     except OSError:
         pass
+    return ""
+
+
+def _system(mode: str, n_atoms: int, seed: int):
+    from fsctep_amd.synthetic import SPECIES_4, SPECIES_8, make_system
+    w = WORKLOADS[mode]
+    return make_system(n_atoms, density=0.1, periodic=True, species=SPECIES_8 if w["species"] == 8 else SPECIES_4,
+                       seed=seed)
+
+
+def _field(n_graphs: int, seed: int):
+    """External field per graph, N(0, 0.1) V/A, seeded."""
+    import numpy as np
+    return np.random.Generator(np.random.PCG64(seed)).normal(0.0, 0.1, size=(n_graphs, 3))
+
+
+def cpu_baseline(mode: str, n_atoms: int, steps: int, seed: int) -> dict:
+    """The oracle (the reference's algorithm restated in PyTorch on the CPU) on host cores."""
+    import torch
+    from fsctep_amd.synthetic import seeded_value
+    w = WORKLOADS[mode]
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    s = _system(mode, n_atoms, seed)
+    args = (torch.tensor(s.pos, dtype=torch.float32), torch.tensor(s.species),
+            torch.zeros(n_atoms, dtype=torch.long), torch.tensor(s.edge_src), torch.tensor(s.edge_dst),
+            torch.tensor(s.edge_shifts, dtype=torch.float32), torch.tensor(s.cell, dtype=torch.float32))
+    if mode == "sparse":
+        from oracle import sparse_ref as R
+        cfg = R.SparseConfig(channels=w["channels"], num_interaction=w["layers"], function_type="bessel")
+        run = lambda p: R.energy_forces(*args, p, cfg)
+        what = "materialised per-edge weights, per-path einsums, index_add"
+    else:
+        from oracle import ictd_ref as R
+        o3 = mode == "ictd-o3"
+        cfg = R.ICTDConfig(channels=w["channels"], lmax=w["lmax"], num_interaction=w["layers"],
+                           function_type="bessel", o3=o3,
+                           active=((0, 1), (1, 1), (1, -1), (2, 1)) if o3 else (), external_field=o3, dipole=o3)
+        field = torch.tensor(_field(1, seed), dtype=torch.float32) if o3 else None
+        run = lambda p: R.energy_forces(*args, p, cfg, field)
+        what = "per-path CG contractions with materialised per-edge weights, index_add"
+    p = {k: torch.tensor(seeded_value(k, sh, 1), dtype=torch.float32) for k, sh in R.param_shapes(cfg)}
+    run(p)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run(p)
+    dt = (time.perf_counter() - t0) / steps
     return {"value": round(n_atoms / dt, 3), "unit": "atom-steps/s", "cores": cores, "kind": "port",
-            "sample": f"oracle (materialised per-edge weights, per-path einsums, index_add), fp32, "
-                      f"{n_atoms} atoms / {s.num_edges} edges of the same recipe, {steps} timed steps "
-                      f"after 1 warm-up, {dt:.2f} s/step, {cores} threads on {cpu_model}"}
+            "sample": f"oracle ({what}), fp32, {n_atoms} atoms / {s.num_edges} edges of the same recipe, "
+                      f"{steps} timed steps after 1 warm-up, {dt:.2f} s/step, {cores} threads on {_cpu_model()}"}
+
+
+def build_model(mode: str, dev):
+    """Random-init (seeded) model of the workload, inference mode, on ``dev``."""
+    from fsctep_amd.synthetic import apply_seeded_parameters
+    w = WORKLOADS[mode]
+    C = w["channels"]
+    kw = dict(max_embed_radius=5.0, main_max_radius=5.0, main_number_of_basis=8, hidden_dim_conv=C,
+              hidden_dim_sh=C, hidden_dim=64, channel_in2=32, embedding_dim=16, max_atomvalue=10,
+              output_size=8, invariant_channels=32, embed_size=[128, 128, 128], num_interaction=w["layers"],
+              function_type_main="bessel", lmax=w["lmax"])
+    if mode == "sparse":
+        from fsctep_amd.sparse import PureCartesianSparseTransformerLayer
+        model = PureCartesianSparseTransformerLayer(**kw, max_rank_other=1, k_policy="k0")
+    elif mode == "ictd":
+        from fsctep_amd.ictd import PureCartesianICTDTransformerLayer
+        model = PureCartesianICTDTransformerLayer(**kw, ictd_tp_path_policy="full")
+    else:
+        from fsctep_amd.ictd import PureCartesianICTDO3TransformerLayer
+        model = PureCartesianICTDO3TransformerLayer(
+            **kw, ictd_tp_path_policy="full", o3_active_irreps="0e,1e,1o,2e", external_tensor_rank=1,
+            external_tensor_irrep="1o",
+            physical_tensor_outputs={"dipole": {"irreps": ["1o"], "channels_out": 1, "reduce": "sum"}})
+    apply_seeded_parameters(model, 1)
+    return model.to(dev).eval().requires_grad_(False)
+
+
+def workload_name(mode: str, N: int, E: int) -> str:
+    w = WORKLOADS[mode]
+    head = {"sparse": "pure-cartesian-sparse energy+forces",
+            "ictd": "pure-cartesian-ictd energy+forces",
+            "ictd-o3": "pure-cartesian-ictd-o3 (0e,1e,1o,2e + rank-1 external field) energy+forces+dipole"}[mode]
+    return (f"{head}, {N} atoms, {E} edges, periodic cubic box, density 0.1/A^3, {w['species']} species, "
+            f"{w['layers']} interaction layers, {w['channels']} channels, ranks 0..{w['lmax']}, "
+            f"cutoff 5.0 A, 8 Bessel radial basis")
 
 
 def main():
@@ -100,10 +197,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--atoms", type=int, default=10000)
-    ap.add_argument("--seed", type=int, default=22)
-    ap.add_argument("--roofline-kernel", default="edge_message_grad")
-    ap.add_argument("--cpu-atoms", type=int, default=300)
+    ap.add_argument("--mode", choices=sorted(WORKLOADS), default="sparse")
+    ap.add_argument("--atoms", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--roofline-kernel", default=None)
+    ap.add_argument("--cpu-atoms", type=int, default=None)
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -113,25 +211,22 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the message passing would shard by receiver domain; not built here)", file=sys.stderr)
         sys.exit(2)
+    w = WORKLOADS[args.mode]
+    n_atoms = w["atoms"] if args.atoms is None else args.atoms
+    seed = w["seed"] if args.seed is None else args.seed
+    kname = w["kernel"] if args.roofline_kernel is None else args.roofline_kernel
+    sparse = args.mode == "sparse"
 
     import torch
     from fsctep_amd import _lib
-    from fsctep_amd.sparse import PureCartesianSparseTransformerLayer, energy_and_forces
-    from fsctep_amd.synthetic import apply_seeded_parameters, make_system
 
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
-    system = make_system(args.atoms, density=0.1, periodic=True, seed=args.seed)
-    print(f"[bench] system: {system.num_atoms} atoms, {system.num_edges} edges "
+    system = _system(args.mode, n_atoms, seed)
+    print(f"[bench] {args.mode}: {system.num_atoms} atoms, {system.num_edges} edges "
           f"({time.perf_counter() - t_build:.1f} s to build)", file=sys.stderr, flush=True)
-    C, layers = 64, 3
-    model = PureCartesianSparseTransformerLayer(
-        max_embed_radius=5.0, main_max_radius=5.0, main_number_of_basis=8, hidden_dim_conv=C,
-        hidden_dim_sh=C, hidden_dim=64, channel_in2=32, embedding_dim=16, max_atomvalue=10,
-        output_size=8, invariant_channels=32, embed_size=[128, 128, 128], num_interaction=layers,
-        function_type_main="bessel", lmax=2, max_rank_other=1, k_policy="k0")
-    apply_seeded_parameters(model, 1)
-    model = model.to(dev).eval().requires_grad_(False)
+    model = build_model(args.mode, dev)
+    C = w["channels"]
 
     pos = torch.tensor(system.pos, dtype=torch.float32, device=dev)
     A = torch.tensor(system.species, device=dev)
@@ -143,33 +238,48 @@ def main():
                           system.num_atoms, A)
     torch.cuda.synchronize()
     t_graph = time.perf_counter() - t_g
+    if sparse:
+        from fsctep_amd.sparse import energy_and_forces
+
+        def step():
+            return energy_and_forces(model, pos, batch, cell, graph)
+    else:
+        from fsctep_amd.ictd import energy_forces
+        field = (torch.tensor(_field(1, seed), dtype=torch.float32, device=dev)
+                 if args.mode == "ictd-o3" else None)
+
+        def step():
+            return energy_forces(model, pos, batch, cell, graph, external_tensor=field)
 
     for i in range(args.warmup):
-        energy_and_forces(model, pos, batch, cell, graph)
+        step()
     torch.cuda.synchronize()
     print(f"[bench] warm-up done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
     # timed region: exactly `steps` steps, synchronised on both sides
-    step_ms = []
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    with _lib.KernelTimer(args.roofline_kernel) as kt:
+    with _lib.KernelTimer(kname) as kt:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev[0].record()
         for i in range(args.steps):
-            e, f = energy_and_forces(model, pos, batch, cell, graph)
+            res = step()
             ev[i + 1].record()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+    e, f = res[0], res[1]
     step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
     ms_per_step = elapsed * 1000.0 / args.steps
-    e_sum = float(e.sum())
     assert torch.isfinite(e).all() and torch.isfinite(f).all()
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (median {statistics.median(step_ms):.3f}); "
-          f"E={e_sum:.6f} max|F|={float(f.abs().max()):.4f}", file=sys.stderr, flush=True)
+          f"E={float(e.sum()):.6f} max|F|={float(f.abs().max()):.4f}", file=sys.stderr, flush=True)
 
     N, E = system.num_atoms, system.num_edges
-    work = kernel_work(args.roofline_kernel, N, E, C)
+    if sparse:
+        work = sparse_kernel_work(kname, N, E, C)
+    else:
+        from fsctep_amd import ictd_ops
+        work = ictd_kernel_work(kname, ictd_ops.layout_struct(model.layout_id), N, E, C)
     avg_ms = kt.total_ms / max(kt.launches, 1)
     if work["bound"] == "mfma":
         achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
@@ -180,15 +290,14 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4)}
     roof["traffic"] = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{args.roofline_kernel}_sparse{N}.json")
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{kname}_{args.mode}{N}.json")
     if os.path.exists(tfile):
-        import hashlib
         with open(tfile) as fh:
             tinfo = json.load(fh)
         src = os.path.join(ROOT, tinfo.get("source", ""))
         if os.path.isfile(src) and hashlib.sha256(open(src, "rb").read()).hexdigest() == tinfo.get("source_sha256"):
             roof["traffic"] = tinfo.get("hbm_bytes_per_launch")   # measured for this exact kernel source
-    roof["kernel"] = args.roofline_kernel
+    roof["kernel"] = kname
     roof["avg_launch_ms"] = round(avg_ms, 4)
     roof["launches"] = kt.launches
     roof["algorithmic_per_launch"] = {"flops": work["flops"], "bytes": work["bytes"]}
@@ -207,9 +316,7 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded random sequential addition, random-init seeded parameters)",
-        "config": {"workload": f"pure-cartesian-sparse energy+forces, {N} atoms, {E} edges, periodic cubic box, "
-                               f"density 0.1/A^3, 4 species, 3 interaction layers, 64 channels, ranks 0..2, "
-                               f"cutoff 5.0 A, 8 Bessel radial basis",
+        "config": {"workload": workload_name(args.mode, N, E), "mode": args.mode,
                    "atoms": N, "edges": E, "graph_prep_ms_untimed": round(t_graph * 1000, 2)},
         "roofline": roof,
         "gpu": gpu_info(),
@@ -223,7 +330,8 @@ def main():
         del src_buf, dst_buf
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(args.cpu_atoms, args.cpu_steps, args.seed)
+        cpu_atoms = w["cpu_atoms"] if args.cpu_atoms is None else args.cpu_atoms
+        out["cpu_baseline"] = cpu_baseline(args.mode, cpu_atoms, args.cpu_steps, seed)
         out["cpu_baseline"]["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
     else:
         out["cpu_baseline"] = None
