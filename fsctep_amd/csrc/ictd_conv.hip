@@ -22,107 +22,236 @@
 namespace fsc {
 namespace ictd {
 
-constexpr int EBF = 16;   // edges per LDS chunk, forward
-constexpr int EBB = 8;    // edges per LDS chunk, backward
+constexpr int EB = 16;    // edges per LDS chunk (power of two: K rows are ordered m1-major, row = m1*EB + e)
 
-// Per-edge gated coupling table of a chunk: BG[e][bgoff_g + m1*kpad_g + kkl] (zero padded).
-__device__ __forceinline__ void build_bg(const FscIctdLayout& L, float* __restrict__ bg, int eb, int cnt, int EB,
-                                         const float* __restrict__ Y, const float* __restrict__ gates,
-                                         const float* __restrict__ cg, bool with_gate) {
-  const int total = EB * L.NBGP;
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-    const int e = idx / L.NBGP, j = idx - e * L.NBGP;
-    float v = 0.f;
-    if (e < cnt) {
-      int g = 0;
-      while (g + 1 < L.NG && j >= L.g_bgoff[g + 1]) ++g;
-      const int rel = j - L.g_bgoff[g];
-      const int kpad = L.g_kpad[g];
-      const int m1 = rel / kpad, kkl = rel - m1 * kpad;
-      if (m1 < L.g_d1[g] && kkl < L.g_kcount[g]) {
-        const int kk = L.g_kstart[g] + kkl;
-        const int p = L.kk_path[kk];
-        const int d2 = L.p_d2[p], d3 = L.p_d3[p], k = kk - L.p_koff[p];
-        const int64_t eid = (int64_t)(eb + e);
-        const float* y = Y + eid * L.NY + L.p_oy[p];
-        const float* c = cg + L.p_cgoff[p] + (m1 * d2) * d3 + k;
-        float s = 0.f;
-        for (int m2 = 0; m2 < d2; ++m2) s += y[m2] * c[m2 * d3];
-        v = with_gate ? s * gates[eid * L.NREF + L.p_gate[p]] : s;
-      }
+// Shared-memory carve-up of the projection kernels (offsets in 4-byte words, regions 16-byte aligned).
+struct ProjSmem {
+  int cgs, desc, ys, gs, srcs, wtask, bg, T, tmap, toff, total, TT;
+};
+
+__host__ __device__ inline int up4(int v) { return (v + 3) & ~3; }
+
+__host__ __device__ inline ProjSmem proj_smem(const FscIctdLayout& L, int ncg, bool bwd) {
+  ProjSmem s;
+  int TT = 0;
+  for (int p = 0; p < L.NP; ++p) TT += L.p_d2[p];
+  s.TT = TT;
+  int o = 0;
+  s.cgs = o;   o += up4(ncg);
+  s.desc = o;  o += 2 * L.NBGP;            // int2 per coupling column
+  s.ys = o;    o += up4(EB * L.NY);
+  s.gs = o;    o += up4(EB * L.NREF);
+  s.srcs = o;  o += EB;
+  s.wtask = o; o += 32;                    // per wave: task count + up to 4 task ids
+  s.bg = o;    o += EB * L.NBGP;
+  s.T = s.tmap = s.toff = o;
+  if (bwd) {
+    s.T = o;    o += up4(EB * TT);
+    s.tmap = o; o += up4(TT);
+    s.toff = o; o += up4(L.NP + 1);
+  }
+  s.total = o;
+  return s;
+}
+
+// Per-block constant tables: the coupling tensors and, per column j of a chunk row of the gated coupling
+// table, where its coupling coefficients live: desc[j] = {cg offset or -1, oy | d2 << 8 | d3 << 12 | gate << 16}.
+__device__ __forceinline__ void stage_tables(const FscIctdLayout& L, const float* __restrict__ cg, int ncg,
+                                             float* __restrict__ cgs, int2* __restrict__ desc) {
+  for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
+  for (int j = threadIdx.x; j < L.NBGP; j += blockDim.x) {
+    int g = 0;
+    while (g + 1 < L.NG && j >= L.g_bgoff[g + 1]) ++g;
+    const int rel = j - L.g_bgoff[g], kpad = L.g_kpad[g];
+    const int m1 = rel / kpad, kkl = rel - m1 * kpad;
+    int2 d = make_int2(-1, 0);
+    if (m1 < L.g_d1[g] && kkl < L.g_kcount[g]) {
+      const int kk = L.g_kstart[g] + kkl;
+      const int p = L.kk_path[kk];
+      const int d2 = L.p_d2[p], d3 = L.p_d3[p];
+      d.x = L.p_cgoff[p] + m1 * d2 * d3 + (kk - L.p_koff[p]);
+      d.y = L.p_oy[p] | (d2 << 8) | (d3 << 12) | (L.p_gate[p] << 16);
     }
-    bg[idx] = v;
+    desc[j] = d;
+  }
+}
+
+// Chunk inputs: harmonics, gates and source ids of edges [eb, eb + cnt) (zero / node 0 beyond cnt).
+__device__ __forceinline__ void stage_chunk(const FscIctdLayout& L, int eb, int cnt, const float* __restrict__ Y,
+                                            const float* __restrict__ gates, const int32_t* __restrict__ esrc,
+                                            float* __restrict__ ys, float* __restrict__ gs,
+                                            int32_t* __restrict__ srcs) {
+  for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
+    const int e = i / L.NY;
+    ys[i] = (e < cnt) ? Y[(int64_t)eb * L.NY + i] : 0.f;
+  }
+  for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
+    const int e = i / L.NREF;
+    gs[i] = (e < cnt) ? gates[(int64_t)eb * L.NREF + i] : 0.f;
+  }
+  if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
+}
+
+// Gated coupling table of the chunk: bg[e][j] = gate_e[p] sum_m2 Y_e[oy_p + m2] C_p[m1][m2][m3] (LDS only).
+__device__ __forceinline__ void build_bg(const FscIctdLayout& L, const float* __restrict__ cgs,
+                                         const int2* __restrict__ desc, const float* __restrict__ ys,
+                                         const float* __restrict__ gs, float* __restrict__ bg) {
+  for (int j = threadIdx.x; j < L.NBGP; j += blockDim.x) {
+    const int2 d = desc[j];
+    float s[EB];
+#pragma unroll
+    for (int e = 0; e < EB; ++e) s[e] = 0.f;
+    if (d.x >= 0) {
+      const int oy = d.y & 255, d2 = (d.y >> 8) & 15, d3 = (d.y >> 12) & 15, gate = d.y >> 16;
+      for (int m2 = 0; m2 < d2; ++m2) {
+        const float c = cgs[d.x + m2 * d3];
+#pragma unroll
+        for (int e = 0; e < EB; ++e) s[e] += ys[e * L.NY + oy + m2] * c;
+      }
+#pragma unroll
+      for (int e = 0; e < EB; ++e) s[e] *= gs[e * L.NREF + gate];
+    }
+#pragma unroll
+    for (int e = 0; e < EB; ++e) bg[e * L.NBGP + j] = s[e];
+  }
+}
+
+// V consecutive floats (V = 2 or 4) as an MFMA-operand bundle.
+template <int V>
+struct VecF {
+  float v[V];
+};
+
+template <int V>
+__device__ __forceinline__ VecF<V> ldv(const float* p) {
+  VecF<V> r;
+  if constexpr (V == 4) {
+    const f4 t = *reinterpret_cast<const f4*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.v[j] = t[j];
+  } else {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+  }
+  return r;
+}
+
+template <int V>
+__device__ __forceinline__ void stv(float* p, const VecF<V>& r) {
+  if constexpr (V == 4) {
+    *reinterpret_cast<f4*>(p) = f4{r.v[0], r.v[1], r.v[2], r.v[3]};
+  } else {
+    *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
+  }
+}
+
+// Forward tasks are (channel span, 16-row kk tile) pairs of cost d1(group).  Snake order over the
+// cost-sorted list gives every wave at most 4 tasks with near-equal cost.
+__device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int nspan, int* __restrict__ wtask) {
+  if (threadIdx.x != 0) return;
+  const int T = nspan * L.KTT;
+  for (int w = 0; w < 4; ++w) wtask[w * 8] = 0;
+  for (int t = 0; t < T; ++t) {
+    const int ct = L.g_d1[L.tile_group[t % L.KTT]];
+    int rank = 0;
+    for (int u = 0; u < T; ++u) {
+      const int cu = L.g_d1[L.tile_group[u % L.KTT]];
+      rank += (cu > ct) || (cu == ct && u < t);
+    }
+    const int round = rank >> 2, pos = rank & 3;
+    const int w = (round & 1) ? 3 - pos : pos;
+    wtask[w * 8 + 1 + wtask[w * 8]++] = t;
   }
 }
 
 // ---------------------------------------------------------------- forward projection (one block per receiver)
-template <int C, int KTT>
-__global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, const float* __restrict__ x,
+// Z[n][kk][i] = (1/deg) sum_{(e,m1)} bg[e][m1][kk] x[src_e][o1 + m1][i], MFMA with K = (m1, e).
+// Column tile j of a 16*V-channel span holds channels span0 + V*r + j, so each lane gathers V
+// consecutive channels of x with one vector load and stores V consecutive channels of Z.
+template <int C>
+__global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
                                                           const float* __restrict__ Y,
                                                           const float* __restrict__ gates,
                                                           const float* __restrict__ cg,
                                                           const int32_t* __restrict__ dst_ptr,
                                                           const int32_t* __restrict__ esrc,
                                                           float* __restrict__ Z) {
-  extern __shared__ float smem[];
-  float* bg = smem;                                        // [EBF][NBGP]
-  int32_t* srcs = reinterpret_cast<int32_t*>(smem + EBF * L.NBGP);
-  constexpr int CT = C / 16;
-  constexpr int CTW = (CT + 3) / 4;
+  constexpr int SPAN = C < 64 ? C : 64;
+  constexpr int V = SPAN / 16;
+  extern __shared__ __align__(16) float smem[];
+  const ProjSmem sm = proj_smem(L, ncg, false);
+  float* cgs = smem + sm.cgs;
+  int2* desc = reinterpret_cast<int2*>(smem + sm.desc);
+  float* ys = smem + sm.ys;
+  float* gs = smem + sm.gs;
+  int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
+  int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
+  float* bg = smem + sm.bg;
+
   const int n = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
+  stage_tables(L, cg, ncg, cgs, desc);
+  assign_fwd_tasks(L, C / SPAN, wtask);
 
-  f4 acc[KTT][CTW];
+  f4 acc[4][V];
 #pragma unroll
-  for (int kt = 0; kt < KTT; ++kt)
+  for (int lt = 0; lt < 4; ++lt)
 #pragma unroll
-    for (int cw = 0; cw < CTW; ++cw) acc[kt][cw] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < V; ++j) acc[lt][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int eb = beg; eb < end; eb += EBF) {
-    const int cnt = min(EBF, end - eb);
+  for (int eb = beg; eb < end; eb += EB) {
+    const int cnt = min(EB, end - eb);
     __syncthreads();
-    build_bg(L, bg, eb, cnt, EBF, Y, gates, cg, true);
-    if (threadIdx.x < EBF) srcs[threadIdx.x] = (threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
+    stage_chunk(L, eb, cnt, Y, gates, esrc, ys, gs, srcs);
     __syncthreads();
-    for (int g = 0; g < L.NG; ++g) {
-      const int d1 = L.g_d1[g], o1 = L.g_o1[g], kpad = L.g_kpad[g], bgoff = L.g_bgoff[g], t0 = L.g_tile0[g];
-      const int nk = EBF * d1;
-      for (int s = 0; s < nk; s += 4) {
-        const int kidx = s + q;
-        const int e = kidx / d1, m1 = kidx - e * d1;
-        float b[CTW];
+    build_bg(L, cgs, desc, ys, gs, bg);
+    __syncthreads();
+    const int ntask = wtask[wave * 8];
 #pragma unroll
-        for (int cw = 0; cw < CTW; ++cw) {
-          const int ct = wave * CTW + cw;
-          b[cw] = (ct < CT && e < cnt) ? x[((int64_t)srcs[e] * L.M + o1 + m1) * C + ct * 16 + r] : 0.f;
+    for (int lt = 0; lt < 4; ++lt) {
+      if (lt >= ntask) break;
+      const int t = wtask[wave * 8 + 1 + lt];
+      const int span = t / L.KTT, kt = t - span * L.KTT;
+      const int g = L.tile_group[kt];
+      const int d1 = L.g_d1[g], o1 = L.g_o1[g], kpad = L.g_kpad[g];
+      const float* arow = bg + L.g_bgoff[g] + (kt - L.g_tile0[g]) * 16 + r;
+      const float* xcol = x + o1 * C + span * SPAN + V * r;
+      for (int m1 = 0; m1 < d1; ++m1) {        // K rows m1*EB + e, e = 4u + q
+        float a[EB / 4];
+        VecF<V> b[EB / 4];
+#pragma unroll
+        for (int u = 0; u < EB / 4; ++u) {
+          const int e = 4 * u + q;
+          a[u] = arow[e * L.NBGP + m1 * kpad];
+          b[u] = ldv<V>(xcol + ((int64_t)srcs[e] * L.M + m1) * C);
         }
-        const float* arow = bg + e * L.NBGP + bgoff + m1 * kpad + r;
 #pragma unroll
-        for (int kt = 0; kt < KTT; ++kt) {
-          if (L.tile_group[kt] != g) continue;
-          const float a = arow[(kt - t0) * 16];
+        for (int u = 0; u < EB / 4; ++u)
 #pragma unroll
-          for (int cw = 0; cw < CTW; ++cw) acc[kt][cw] = mfma16x16x4(a, b[cw], acc[kt][cw]);
-        }
+          for (int j = 0; j < V; ++j) acc[lt][j] = mfma16x16x4(a[u], b[u].v[j], acc[lt][j]);
       }
     }
   }
   const float scale = 1.f / (float)max(end - beg, 1);
+  __syncthreads();
+  const int ntask = wtask[wave * 8];
 #pragma unroll
-  for (int kt = 0; kt < KTT; ++kt) {
+  for (int lt = 0; lt < 4; ++lt) {
+    if (lt >= ntask) break;
+    const int t = wtask[wave * 8 + 1 + lt];
+    const int span = t / L.KTT, kt = t - span * L.KTT;
     const int g = L.tile_group[kt];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kkl = (kt - L.g_tile0[g]) * 16 + 4 * q + i;
       if (kkl >= L.g_kcount[g]) continue;
-      const int kk = L.g_kstart[g] + kkl;
+      VecF<V> o;
 #pragma unroll
-      for (int cw = 0; cw < CTW; ++cw) {
-        const int ct = wave * CTW + cw;
-        if (ct < CT) Z[((int64_t)n * L.KT + kk) * C + ct * 16 + r] = acc[kt][cw][i] * scale;
-      }
+      for (int j = 0; j < V; ++j) o.v[j] = acc[lt][j][i] * scale;
+      stv<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + span * SPAN + V * r, o);
     }
   }
 }
@@ -213,8 +342,13 @@ __global__ __launch_bounds__(256) void mix_bwd_kernel(FscIctdLayout L, const flo
 }
 
 // ---------------------------------------------------------------- backward projection (one block per receiver)
+// With g = dZ[n] / deg, per chunk of EB receiver edges:
+//   (a) DX[e][o1+m1][i] = sum_kk bg[e][m1][kk] g[kk][i]     MFMA, K = kk; dZ rows read as V-channel vectors
+//   (b) H[e][m1][kk]    = sum_i x[src_e][o1+m1][i] g[kk][i]  MFMA, K = channels (H overwrites bg in LDS)
+//   (c) T[e][p][m2]     = sum_{m1,m3} H[e][m1][koff_p+m3] C_p[m1][m2][m3]
+//       dgate[e][p] = sum_m2 Y_e[oy_p+m2] T[e][p][m2];   dY[e][y] = sum_{p covers y} gate_e[p] T[e][p][y-oy_p]
 template <int C>
-__global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, const float* __restrict__ dZ,
+__global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
                                                           const float* __restrict__ x,
                                                           const float* __restrict__ Y,
                                                           const float* __restrict__ gates,
@@ -223,134 +357,159 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, const
                                                           const int32_t* __restrict__ esrc,
                                                           float* __restrict__ DX, float* __restrict__ dgates,
                                                           float* __restrict__ dY) {
-  extern __shared__ float smem[];
-  float* bg = smem;                                   // [EBB][NBGP] gated coupling table
-  float* hs = smem + EBB * L.NBGP;                    // [EBB][NBGP] H = x . g
-  int32_t* srcs = reinterpret_cast<int32_t*>(hs + EBB * L.NBGP);
-  constexpr int CT = C / 16;
+  constexpr int SPAN = C < 64 ? C : 64;
+  constexpr int V = SPAN / 16;
+  constexpr int NSPAN = C / SPAN;
+  extern __shared__ __align__(16) float smem[];
+  const ProjSmem sm = proj_smem(L, ncg, true);
+  float* cgs = smem + sm.cgs;
+  int2* desc = reinterpret_cast<int2*>(smem + sm.desc);
+  float* ys = smem + sm.ys;
+  float* gs = smem + sm.gs;
+  int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
+  float* bg = smem + sm.bg;            // gated coupling table, then H
+  float* T = smem + sm.T;              // [TT][EB]
+  int* tmap = reinterpret_cast<int*>(smem + sm.tmap);
+  int* toff = reinterpret_cast<int*>(smem + sm.toff);
+
   const int n = blockIdx.x;
+  const int beg = dst_ptr[n], end = dst_ptr[n + 1];
+  if (beg == end) return;                               // uniform over the block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int beg = dst_ptr[n], end = dst_ptr[n + 1];
-  const float scale = 1.f / (float)max(end - beg, 1);
+  const int TT = sm.TT;
+  const float scale = 1.f / (float)(end - beg);
   const float* gn = dZ + (int64_t)n * L.KT * C;
+  stage_tables(L, cg, ncg, cgs, desc);
+  if (threadIdx.x == 0) {
+    int o = 0;
+    for (int p = 0; p < L.NP; ++p) {
+      toff[p] = o;
+      for (int m2 = 0; m2 < L.p_d2[p]; ++m2) tmap[o + m2] = p;
+      o += L.p_d2[p];
+    }
+    toff[L.NP] = o;
+  }
 
-  for (int eb = beg; eb < end; eb += EBB) {
-    const int cnt = min(EBB, end - eb);
+  for (int eb = beg; eb < end; eb += EB) {
+    const int cnt = min(EB, end - eb);
     __syncthreads();
-    build_bg(L, bg, eb, cnt, EBB, Y, gates, cg, true);
-    if (threadIdx.x < EBB) srcs[threadIdx.x] = (threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
+    stage_chunk(L, eb, cnt, Y, gates, esrc, ys, gs, srcs);
     __syncthreads();
-    // (a) DX rows (e, m1) x channels, K = padded kk of the group
-    int items = 0;
-    for (int g = 0; g < L.NG; ++g) items += ((EBB * L.g_d1[g] + 15) / 16) * CT;
-    for (int it = wave; it < items; it += 4) {
-      int g = 0, rem = it;
-      for (;; ++g) {
-        const int ng = ((EBB * L.g_d1[g] + 15) / 16) * CT;
-        if (rem < ng) break;
-        rem -= ng;
-      }
-      const int rt = rem / CT, ct = rem - rt * CT;
-      const int d1 = L.g_d1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g], kstart = L.g_kstart[g];
-      const int arow = rt * 16 + r;
-      const bool aok = arow < EBB * d1;
-      const int ae = aok ? arow / d1 : 0, am = aok ? arow - (arow / d1) * d1 : 0;
-      const float* ap = bg + ae * L.NBGP + L.g_bgoff[g] + am * kpad;
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
+    build_bg(L, cgs, desc, ys, gs, bg);
+    __syncthreads();
+
+    // (a) one task per (component m = o1 + m1, channel span): 16 edge rows x 16*V channels
+    for (int task = wave; task < L.M * NSPAN; task += 4) {
+      const int m = task / NSPAN, span = task - m * NSPAN;
+      int g = 0;
+      while (g + 1 < L.NG && m >= L.g_o1[g + 1]) ++g;
+      const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
+      const float* arow = bg + r * L.NBGP + L.g_bgoff[g] + m1 * kpad + 4 * q;
+      const float* bcol = gn + (int64_t)L.g_kstart[g] * C + span * SPAN + V * r;
+      f4 acc[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
       for (int t = 0; t < kpad; t += 16) {
-        const f4 a4 = aok ? *reinterpret_cast<const f4*>(ap + t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
-        f4 b4;
+        const f4 a4 = *reinterpret_cast<const f4*>(arow + t);
+        VecF<V> bf[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int kkl = t + 4 * q + j;
-          b4[j] = (kkl < kcount) ? gn[(int64_t)(kstart + kkl) * C + ct * 16 + r] : 0.f;
+        for (int s = 0; s < 4; ++s) {
+          const int kkl = t + 4 * q + s;
+          if (kkl < kcount) {
+            bf[s] = ldv<V>(bcol + (int64_t)kkl * C);
+          } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) bf[s].v[j] = 0.f;
+          }
         }
-        acc = mfma_k16(a4, b4, acc);
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          acc[j] = mfma_k16(a4, f4{bf[0].v[j], bf[1].v[j], bf[2].v[j], bf[3].v[j]}, acc[j]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = rt * 16 + 4 * q + i;
-        if (row >= EBB * d1) continue;
-        const int e = row / d1, m1 = row - e * d1;
-        if (e < cnt)
-          DX[((int64_t)(eb + e) * L.M + L.g_o1[g] + m1) * C + ct * 16 + r] = acc[i] * scale;
-      }
-    }
-    // (b) H rows (e, m1) x padded kk, K = channels
-    items = 0;
-    for (int g = 0; g < L.NG; ++g) items += ((EBB * L.g_d1[g] + 15) / 16) * (L.g_kpad[g] / 16);
-    for (int it = wave; it < items; it += 4) {
-      int g = 0, rem = it;
-      for (;; ++g) {
-        const int ng = ((EBB * L.g_d1[g] + 15) / 16) * (L.g_kpad[g] / 16);
-        if (rem < ng) break;
-        rem -= ng;
-      }
-      const int nkt = L.g_kpad[g] / 16;
-      const int rt = rem / nkt, kt = rem - rt * nkt;
-      const int d1 = L.g_d1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g], kstart = L.g_kstart[g];
-      const int arow = rt * 16 + r;
-      const bool aok = arow < EBB * d1;
-      const int ae = aok ? arow / d1 : 0, am = aok ? arow - (arow / d1) * d1 : 0;
-      const bool xok = aok && ae < cnt;
-      const float* xr = x + ((int64_t)srcs[ae] * L.M + L.g_o1[g] + am) * C;
-      const int bkk = kt * 16 + r;
-      const bool bok = bkk < kcount;
-      const float* gr = gn + (int64_t)(kstart + (bok ? bkk : 0)) * C;
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-      for (int t = 0; t < C / 16; ++t) {
-        const f4 a4 = xok ? ld4(xr + 16 * t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
-        const f4 b4 = bok ? ld4(gr + 16 * t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
-        acc = mfma_k16(a4, b4, acc);
-      }
+        const int e = 4 * q + i;
+        if (e >= cnt) continue;
+        VecF<V> o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rt * 16 + 4 * q + i;
-        if (row >= EBB * d1) continue;
-        const int e = row / d1, m1 = row - e * d1;
-        hs[e * L.NBGP + L.g_bgoff[g] + m1 * kpad + kt * 16 + r] = acc[i] * scale;
+        for (int j = 0; j < V; ++j) o.v[j] = acc[j][i] * scale;
+        stv<V>(DX + ((int64_t)(eb + e) * L.M + m) * C + span * SPAN + V * r, o);
       }
     }
     __syncthreads();
-    // (c) dgate[e][p] = sum_{m1,m3} H[m1][koff_p+m3] Bn[m1][m3];  dY[e][y] = sum_p gate_p sum H C_p
-    for (int idx = threadIdx.x; idx < EBB * L.NP; idx += blockDim.x) {
-      const int e = idx / L.NP, p = idx - e * L.NP;
-      if (e >= cnt) continue;
+
+    // (b) one task per component m: 16 edge rows x (kpad of its group), K = channels
+    for (int m = wave; m < L.M; m += 4) {
+      int g = 0;
+      while (g + 1 < L.NG && m >= L.g_o1[g + 1]) ++g;
+      const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
+      const int nkt = kpad / 16;
+      const float* xr = x + ((int64_t)srcs[r] * L.M + m) * C + 4 * q;
+      f4 acc[4];
+      const float* br[4];
+      bool bok[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        acc[kt] = f4{0.f, 0.f, 0.f, 0.f};
+        const int kkl = kt * 16 + r;
+        bok[kt] = kt < nkt && kkl < kcount;
+        br[kt] = gn + (int64_t)(L.g_kstart[g] + (bok[kt] ? kkl : 0)) * C + 4 * q;
+      }
+#pragma unroll 2
+      for (int t = 0; t < C; t += 16) {
+        const f4 a4 = ld4(xr + t);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          if (kt >= nkt) break;
+          const f4 b4 = bok[kt] ? ld4(br[kt] + t) : f4{0.f, 0.f, 0.f, 0.f};
+          acc[kt] = mfma_k16(a4, b4, acc[kt]);
+        }
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        if (kt >= nkt) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          bg[(4 * q + i) * L.NBGP + L.g_bgoff[g] + m1 * kpad + kt * 16 + r] = acc[kt][i] * scale;
+      }
+    }
+    __syncthreads();
+
+    // (c1) T[j][e], j = (path p, m2)
+    for (int idx = threadIdx.x; idx < TT * EB; idx += blockDim.x) {
+      const int j = idx / EB, e = idx & (EB - 1);
+      const int p = tmap[j], m2 = j - toff[p];
       const int g = L.p_group[p];
-      const int d1 = L.g_d1[g], d2 = L.p_d2[p], d3 = L.p_d3[p], kpad = L.g_kpad[g];
-      const int64_t eid = (int64_t)(eb + e);
-      const float* y = Y + eid * L.NY + L.p_oy[p];
-      const float* h = hs + e * L.NBGP + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
-      const float* c = cg + L.p_cgoff[p];
+      const int d1 = L.g_d1[g], kpad = L.g_kpad[g], d2 = L.p_d2[p], d3 = L.p_d3[p];
+      const float* h = bg + e * L.NBGP + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
+      const float* c = cgs + L.p_cgoff[p] + m2 * d3;
       float acc = 0.f;
       for (int m1 = 0; m1 < d1; ++m1)
-        for (int m3 = 0; m3 < d3; ++m3) {
-          float bn = 0.f;
-          for (int m2 = 0; m2 < d2; ++m2) bn += y[m2] * c[(m1 * d2 + m2) * d3 + m3];
-          acc += h[m1 * kpad + m3] * bn;
-        }
-      dgates[eid * L.NREF + L.p_gate[p]] = acc;
+        for (int m3 = 0; m3 < d3; ++m3) acc += h[m1 * kpad + m3] * c[m1 * d2 * d3 + m3];
+      T[idx] = acc;
     }
-    for (int idx = threadIdx.x; idx < EBB * L.NY; idx += blockDim.x) {
-      const int e = idx / L.NY, yc = idx - e * L.NY;
+    __syncthreads();
+
+    // (c2) gate and harmonic gradients of the chunk's edges
+    for (int idx = threadIdx.x; idx < L.NP * EB; idx += blockDim.x) {
+      const int p = idx / EB, e = idx & (EB - 1);
       if (e >= cnt) continue;
-      const int64_t eid = (int64_t)(eb + e);
+      const int oy = L.p_oy[p], d2 = L.p_d2[p], t0 = toff[p];
+      float acc = 0.f;
+      for (int m2 = 0; m2 < d2; ++m2) acc += ys[e * L.NY + oy + m2] * T[(t0 + m2) * EB + e];
+      dgates[(int64_t)(eb + e) * L.NREF + L.p_gate[p]] = acc;
+    }
+    for (int idx = threadIdx.x; idx < L.NY * EB; idx += blockDim.x) {
+      const int yc = idx / EB, e = idx & (EB - 1);
+      if (e >= cnt) continue;
       float acc = 0.f;
       for (int p = 0; p < L.NP; ++p) {
         const int m2 = yc - L.p_oy[p];
         if (m2 < 0 || m2 >= L.p_d2[p]) continue;
-        const int g = L.p_group[p];
-        const int d1 = L.g_d1[g], d2 = L.p_d2[p], d3 = L.p_d3[p], kpad = L.g_kpad[g];
-        const float* h = hs + e * L.NBGP + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
-        const float* c = cg + L.p_cgoff[p] + m2 * d3;
-        float s = 0.f;
-        for (int m1 = 0; m1 < d1; ++m1)
-          for (int m3 = 0; m3 < d3; ++m3) s += h[m1 * kpad + m3] * c[m1 * d2 * d3 + m3];
-        acc += gates[eid * L.NREF + L.p_gate[p]] * s;
+        acc += gs[e * L.NREF + L.p_gate[p]] * T[(toff[p] + m2) * EB + e];
       }
-      dY[eid * L.NY + yc] = acc;
+      dY[(int64_t)(eb + e) * L.NY + yc] = acc;
     }
   }
 }
@@ -467,6 +626,13 @@ __global__ void transpose_weights_kernel(const float* __restrict__ W, float* __r
 }
 
 // ---------------------------------------------------------------- host side
+// Coupling-table length implied by the layout.
+int cg_length(const FscIctdLayout& L) {
+  int n = 0;
+  for (int p = 0; p < L.NP; ++p) n = max(n, L.p_cgoff[p] + L.g_d1[L.p_group[p]] * L.p_d2[p] * L.p_d3[p]);
+  return n;
+}
+
 int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
   if (!L) { set_error(std::string(who) + ": null layout"); return 1; }
   if (!(C == 32 || C == 64 || C == 128)) { set_error(std::string(who) + ": channels must be 32, 64 or 128"); return 1; }
@@ -489,33 +655,58 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
     set_error(std::string(who) + ": every input irrep needs a live path");
     return 1;
   }
+  // limits of the projection kernels: <= 64 kk slots per group (4 MFMA tiles), 4-bit component
+  // counts in the coupling descriptors, tiles inside their group, LDS within 64 KiB
+  int bgoff = 0;
+  for (int g = 0; g < L->NG; ++g) {
+    if (L->g_kpad[g] < 16 || L->g_kpad[g] > 64 || L->g_d1[g] < 1 || L->g_d1[g] > 15 ||
+        L->g_bgoff[g] != bgoff || L->g_kstart[g] < 0 || L->g_kstart[g] + L->g_kcount[g] > L->KT) {
+      set_error(std::string(who) + ": path group exceeds the projection kernel limits");
+      return 1;
+    }
+    bgoff += L->g_d1[g] * L->g_kpad[g];
+  }
+  if (bgoff != L->NBGP || L->NREF > 4096) {
+    set_error(std::string(who) + ": coupling table size mismatch");
+    return 1;
+  }
+  for (int t = 0; t < L->KTT; ++t) {
+    const int g = L->tile_group[t];
+    if (g < 0 || g >= L->NG || t < L->g_tile0[g] || (t - L->g_tile0[g]) * 16 >= L->g_kpad[g]) {
+      set_error(std::string(who) + ": kk tile table inconsistent");
+      return 1;
+    }
+  }
+  for (int p = 0; p < L->NP; ++p) {
+    if (L->p_group[p] < 0 || L->p_group[p] >= L->NG || L->p_d2[p] < 1 || L->p_d2[p] > 15 || L->p_d3[p] < 1 ||
+        L->p_d3[p] > 15 || L->p_oy[p] < 0 || L->p_oy[p] + L->p_d2[p] > L->NY || L->p_gate[p] < 0 ||
+        L->p_gate[p] >= L->NREF || L->p_koff[p] < 0 || L->p_koff[p] + L->p_d3[p] > L->KT || L->p_cgoff[p] < 0) {
+      set_error(std::string(who) + ": path table out of range");
+      return 1;
+    }
+  }
+  for (int kk = 0; kk < L->KT; ++kk) {
+    if (L->kk_path[kk] < 0 || L->kk_path[kk] >= L->NP) {
+      set_error(std::string(who) + ": kk_path out of range");
+      return 1;
+    }
+  }
+  if ((size_t)proj_smem(*L, cg_length(*L), true).total * sizeof(float) > 65536) {
+    set_error(std::string(who) + ": layout needs more than 64 KiB of LDS per block");
+    return 1;
+  }
   return 0;
-}
-
-template <int C, int KTT>
-void launch_project_fwd(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc,
-                        const float* x, const float* Y, const float* gates, const float* cg, float* Z,
-                        hipStream_t st) {
-  const size_t lds = (size_t)EBF * L.NBGP * sizeof(float) + EBF * sizeof(int32_t);
-  project_fwd_kernel<C, KTT><<<(unsigned)N, 256, lds, st>>>(L, x, Y, gates, cg, dst_ptr, esrc, Z);
 }
 
 template <int C>
 int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
               const float* Y, const float* gates, const float* cg, const float* W, float* Z, float* out,
               hipStream_t st) {
+  const int ncg = cg_length(L);
   {
     LaunchTimer tm("ictd_project", st);
-    switch (L.KTT) {
-      case 1: launch_project_fwd<C, 1>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 2: launch_project_fwd<C, 2>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 3: launch_project_fwd<C, 3>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 4: launch_project_fwd<C, 4>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 5: launch_project_fwd<C, 5>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 6: launch_project_fwd<C, 6>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      case 7: launch_project_fwd<C, 7>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-      default: launch_project_fwd<C, 8>(L, N, dst_ptr, esrc, x, Y, gates, cg, Z, st); break;
-    }
+    const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
+    project_fwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z);
   }
   if (check_launch("ictd project_fwd")) return 2;
   int dmax = 1;
@@ -543,8 +734,10 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   if (check_launch("ictd mix_bwd")) return 2;
   {
     LaunchTimer tm("ictd_project_grad", st);
-    const size_t lds = 2 * (size_t)EBB * L.NBGP * sizeof(float) + EBB * sizeof(int32_t);
-    project_bwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, dZ, x, Y, gates, cg, dst_ptr, esrc, DX, dgates, dY);
+    const int ncg = cg_length(L);
+    const size_t lds = (size_t)proj_smem(L, ncg, true).total * sizeof(float);
+    project_bwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, DX, dgates,
+                                                          dY);
   }
   if (check_launch("ictd project_bwd")) return 2;
   {
