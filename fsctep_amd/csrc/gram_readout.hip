@@ -1,0 +1,298 @@
+// Invariant Gram bilinear of the readout on gfx950 (sparse and ICTD trunks).
+//
+//   out[n][o] = sum_{i,j} W[o][i][j] G_n[i][j],      G_n[i][j] = scale * sum_m t[n][m][i] t[n][m][j]
+//
+// Replaces PureCartesianSparseInvariantBilinear.forward (models/pure_cartesian_sparse_layers.py:424-456)
+// and the Gram x W_read readout of the ICTD trunks (models/pure_cartesian_ictd_layers_full.py:999-1000,
+// models/pure_cartesian_ictd_layers_o3.py:1017-1018).  The reference materialises G (N x nC x nC,
+// 5.9 GB per irrep at 10k atoms and nC = 384) and runs a GEMM over it; here G is formed tile by tile
+// in registers from t and consumed by the MFMA at once.
+//
+// Channels split into nb = nC/16 blocks.  G is symmetric, so the forward sums block pairs I <= J only:
+//   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
+// with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  The backward is
+//   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
+// computed per (64-node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
+// with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
+// the diagonal.  Layouts: t [N][D][nC], W [S][nC][nC], out/grad_out [N][S].
+
+#include "common.h"
+#include "fsctep.h"
+
+namespace fsc {
+namespace gram {
+
+constexpr int NODES = 64;    // nodes per workgroup (4 waves x 16 MFMA rows)
+constexpr int PCHUNK = 8;    // block pairs per forward workgroup
+
+__host__ __device__ inline int n_pairs(int nb) { return nb * (nb + 1) / 2; }
+__host__ __device__ inline int pair_index(int I, int J, int nb) { return I * nb - (I * (I - 1)) / 2 + (J - I); }
+
+// Workgroup w runs on XCD w % 8; give each XCD a contiguous range of logical tiles so tiles that
+// share weight blocks share an L2.  Returns -1 for the padding workgroups.
+__device__ __forceinline__ int xcd_logical(int nwg) {
+  const int per = (nwg + 7) / 8;
+  const int w = blockIdx.x;
+  const int logical = (w & 7) * per + (w >> 3);
+  return logical < nwg ? logical : -1;
+}
+
+// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).
+__global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
+                               float* __restrict__ Wb) {
+  const int I = blockIdx.y, J = blockIdx.x, nb = nC / 16;
+  if (I > J) return;
+  const int p = pair_index(I, J, nb);
+  for (int idx = threadIdx.x; idx < 256 * S; idx += blockDim.x) {
+    const int o = idx % S, ab = idx / S, a = ab / 16, b = ab % 16;
+    const float wij = W[((int64_t)o * nC + I * 16 + a) * nC + J * 16 + b];
+    const float wji = W[((int64_t)o * nC + J * 16 + b) * nC + I * 16 + a];
+    Wb[((int64_t)p * 256 + ab) * S + o] = wij + wji;
+    Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = (I == J) ? wij : wij + wji;
+  }
+}
+
+// Forward partial sums over PCHUNK block pairs: part[chunk][n][o].
+template <int D, int S>
+__global__ __launch_bounds__(256) void forward_kernel(int64_t N, int nC, float scale, const float* __restrict__ t,
+                                                      const float* __restrict__ Wf, int nchunks,
+                                                      float* __restrict__ part) {
+  constexpr int CT = S / 16;
+  const int nb = nC / 16, np = n_pairs(nb);
+  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const int logical = xcd_logical(nchunks * ntiles);
+  if (logical < 0) return;
+  const int chunk = logical / ntiles, tile = logical - chunk * ntiles;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t n = (int64_t)tile * NODES + wave * 16 + r;
+  const bool valid = n < N;
+  const float* tn = t + (valid ? n : 0) * D * nC;
+
+  const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
+  int I = 0, rowstart = 0;
+  while (rowstart + (nb - I) <= p0) {
+    rowstart += nb - I;
+    ++I;
+  }
+  int J = I + (p0 - rowstart);
+
+  f4 acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = f4{0.f, 0.f, 0.f, 0.f};
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  for (int p = p0; p < p1; ++p) {
+    f4 tj[D];
+#pragma unroll
+    for (int m = 0; m < D; ++m) tj[m] = valid ? ld4(tn + m * nC + J * 16 + 4 * q) : zero;
+    const float* wp = Wf + (int64_t)p * 16 * S * 16 + r * 16 + 4 * q;
+#pragma unroll 1
+    for (int ig = 0; ig < 4; ++ig) {
+      f4 ti[D];
+#pragma unroll
+      for (int m = 0; m < D; ++m) ti[m] = valid ? ld4(tn + m * nC + I * 16 + 4 * ig) : zero;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int il = 4 * ig + ii;
+        f4 a = zero;
+#pragma unroll
+        for (int m = 0; m < D; ++m) a += ti[m][ii] * tj[m];
+        a *= scale;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_k16(a, ld4(wp + ((int64_t)il * S + ct * 16) * 16), acc[ct]);
+      }
+    }
+    if (++J == nb) {
+      ++I;
+      J = I;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t node = (int64_t)tile * NODES + wave * 16 + 4 * q + i;
+    if (node >= N) continue;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 16 + r] = acc[ct][i];
+  }
+}
+
+// out[n][o] = sum over chunks of part[chunk][n][o] (fixed order: deterministic).
+__global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__ part, float* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < NS; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int c = 0; c < nchunks; ++c) s += part[(int64_t)c * NS + i];
+    out[i] = s;
+  }
+}
+
+// Backward: one workgroup per (64-node tile, row block I); dt[n][m][I0 + il] complete after the J loop.
+template <int D, int S>
+__global__ __launch_bounds__(256) void backward_kernel(int64_t N, int nC, float scale,
+                                                       const float* __restrict__ g, const float* __restrict__ t,
+                                                       const float* __restrict__ Wb, float* __restrict__ dt) {
+  __shared__ __align__(16) float ts[NODES * D * 16];     // t[node][m][J0 .. J0+15] of the current J
+  constexpr int KT = S / 16;
+  const int nb = nC / 16;
+  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const int logical = xcd_logical(nb * ntiles);
+  if (logical < 0) return;                                // uniform over the block
+  const int I = logical / ntiles, tile = logical - I * ntiles;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t n = (int64_t)tile * NODES + wave * 16 + r;
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+
+  f4 ga[KT];                                              // A operand: g[n_r][o], K = o
+#pragma unroll
+  for (int k = 0; k < KT; ++k) ga[k] = (n < N) ? ld4(g + n * S + 16 * k + 4 * q) : zero;
+  float acc[4][D];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int m = 0; m < D; ++m) acc[i][m] = 0.f;
+  const float* tsw = ts + (wave * 16 + 4 * q) * D * 16;   // this lane's 4 output nodes
+
+  for (int J = 0; J < nb; ++J) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < NODES * D * 4; idx += blockDim.x) {
+      const int nl = idx / (D * 4), rem = idx - nl * (D * 4);
+      const int m = rem >> 2, c4 = rem & 3;
+      const int64_t nn = (int64_t)tile * NODES + nl;
+      reinterpret_cast<f4*>(ts)[idx] = (nn < N) ? ld4(t + (nn * D + m) * nC + J * 16 + 4 * c4) : zero;
+    }
+    __syncthreads();
+    // B[k = o][col = il = r] = (W + W^T)[o][I0 + r][J0 + jl]
+    const float* bp;
+    int bstride;
+    if (I <= J) {
+      bp = Wb + ((int64_t)pair_index(I, J, nb) * 256 + r * 16) * S + 4 * q;
+      bstride = S;                                         // + jl * S
+    } else {
+      bp = Wb + ((int64_t)pair_index(J, I, nb) * 256 + r) * S + 4 * q;
+      bstride = 16 * S;                                    // + jl * 16 * S
+    }
+#pragma unroll 1
+    for (int jl4 = 0; jl4 < 4; ++jl4) {
+      f4 dd[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dd[jj] = zero;
+#pragma unroll
+      for (int k = 0; k < KT; ++k)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          dd[jj] = mfma_k16(ga[k], ld4(bp + (int64_t)(4 * jl4 + jj) * bstride + 16 * k), dd[jj]);
+      // dd[jj][i] = A[n_{4q+i}][I0 + r][J0 + 4 jl4 + jj]
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int m = 0; m < D; ++m) {
+          const f4 tv = *reinterpret_cast<const f4*>(tsw + (i * D + m) * 16 + 4 * jl4);
+          acc[i][m] += dd[0][i] * tv[0] + dd[1][i] * tv[1] + dd[2][i] * tv[2] + dd[3][i] * tv[3];
+        }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t node = (int64_t)tile * NODES + wave * 16 + 4 * q + i;
+    if (node >= N) continue;
+#pragma unroll
+    for (int m = 0; m < D; ++m) dt[(node * D + m) * nC + I * 16 + r] = acc[i][m] * scale;
+  }
+}
+
+int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
+  if (N < 0 || N >= (1LL << 31) || nC < 16 || nC % 16 != 0 || nC > 16 * 64 || !(S == 32 || S == 64) ||
+      !(D == 1 || D == 3 || D == 5 || D == 7 || D == 9)) {
+    set_error(std::string(who) + ": need D in {1,3,5,7,9}, nC a multiple of 16 (<= 1024), S 32 or 64");
+    return 1;
+  }
+  return 0;
+}
+
+template <int S>
+int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float* Wf, float* part, float* out,
+              hipStream_t st) {
+  const int nchunks = (n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK;
+  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
+  {
+    LaunchTimer tm("gram_forward", st);
+#define FSC_GF(DD) forward_kernel<DD, S><<<grid, 256, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
+    switch (D) {
+      case 1: FSC_GF(1); break;
+      case 3: FSC_GF(3); break;
+      case 5: FSC_GF(5); break;
+      case 7: FSC_GF(7); break;
+      default: FSC_GF(9); break;
+    }
+#undef FSC_GF
+  }
+  if (check_launch("gram forward")) return 2;
+  const int64_t NS = N * S;
+  reduce_kernel<<<(unsigned)std::min<int64_t>((NS + 255) / 256, 4096), 256, 0, st>>>(NS, nchunks, part, out);
+  return check_launch("gram reduce") ? 2 : 0;
+}
+
+template <int S>
+int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
+               hipStream_t st) {
+  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
+  LaunchTimer tm("gram_backward", st);
+#define FSC_GB(DD) backward_kernel<DD, S><<<grid, 256, 0, st>>>(N, nC, scale, g, t, Wb, dt)
+  switch (D) {
+    case 1: FSC_GB(1); break;
+    case 3: FSC_GB(3); break;
+    case 5: FSC_GB(5); break;
+    case 7: FSC_GB(7); break;
+    default: FSC_GB(9); break;
+  }
+#undef FSC_GB
+  return check_launch("gram backward") ? 2 : 0;
+}
+
+}  // namespace gram
+}  // namespace fsc
+
+using namespace fsc;
+using namespace fsc::gram;
+
+extern "C" {
+
+int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* weight_floats, int64_t* workspace_floats) {
+  FSC_CHECK_ARG(weight_floats && workspace_floats, "fsc_gram_sizes: null pointer");
+  FSC_CHECK_ARG(n_nodes >= 0 && nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
+                "fsc_gram_sizes: nC must be a multiple of 16 (<= 1024), S 32 or 64");
+  *weight_floats = (int64_t)n_pairs(nC / 16) * 256 * S;
+  *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S;
+  return 0;
+}
+
+int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, float* Wb, hipStream_t stream) {
+  FSC_CHECK_ARG(W && Wf && Wb, "fsc_gram_prepare_weights: null pointer");
+  FSC_CHECK_ARG(nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
+                "fsc_gram_prepare_weights: nC must be a multiple of 16 (<= 1024), S 32 or 64");
+  const int nb = nC / 16;
+  prepare_kernel<<<dim3(nb, nb), 256, 0, stream>>>(W, S, nC, Wf, Wb);
+  return check_launch("gram prepare") ? 2 : 0;
+}
+
+int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
+                     const float* Wf, float* part_ws, float* out, hipStream_t stream) {
+  if (check_dims(n_nodes, D, nC, S, "fsc_gram_forward")) return 1;
+  FSC_CHECK_ARG(Wf && (n_nodes == 0 || (t && part_ws && out)), "fsc_gram_forward: null pointer");
+  if (n_nodes == 0) return 0;
+  if (S == 64) return forward_s<64>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+  return forward_s<32>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+}
+
+int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* grad_out,
+                      const float* t, const float* Wb, float* grad_t, hipStream_t stream) {
+  if (check_dims(n_nodes, D, nC, S, "fsc_gram_backward")) return 1;
+  FSC_CHECK_ARG(Wb && (n_nodes == 0 || (grad_out && t && grad_t)), "fsc_gram_backward: null pointer");
+  if (n_nodes == 0) return 0;
+  if (S == 64) return backward_s<64>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+  return backward_s<32>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+}
+
+}  // extern "C"

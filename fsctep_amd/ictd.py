@@ -20,6 +20,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ictd_ops
+from .readout_ops import GramWeights
 from .graph import Graph, prepare_graph
 from .ictd_basis import canonical, coupling, harmonic_projection, layout_full, layout_o3
 from .radial import radial_basis
@@ -126,6 +127,7 @@ class _ICTDTrunk(nn.Module):
             self.physical_tensor_heads = nn.ModuleDict(
                 {"dipole": nn.ModuleDict({"1": nn.Linear(nC, 1, bias=False)})})
             self._dipole = True
+        self._gram_w = [GramWeights() for _ in self.keys]
         self._cache = {}
 
     def _make_layout(self, preset, active, phys):
@@ -203,7 +205,7 @@ class _ICTDTrunk(nn.Module):
         f32 = torch.float32
         pos, cell = pos.to(f32), cell.to(f32)
         proj, cg, c1_gates, factors = self._consts(pos.device)
-        vec = pos[g.dst] - pos[g.src] + torch.einsum("ni,nij->nj", g.shifts.to(f32), cell[batch[g.src]])
+        vec = pos[g.dst] - pos[g.src] + (g.shifts.to(f32).unsqueeze(-1) * cell[batch[g.src]]).sum(1)
         r = vec.norm(dim=1)
         n = vec / r.clamp(min=1e-8).unsqueeze(-1)
         Y = self.harmonics(n, proj)
@@ -259,10 +261,9 @@ class _ICTDTrunk(nn.Module):
             off += nC * d
         scalars = 0
         for i, k in enumerate(self.keys):
-            t = xb[k]
-            gram = torch.bmm(t, t.transpose(1, 2).contiguous()) / math.sqrt(2 * k[0] + 1)
-            W = self._wread(i, k)
-            scalars = scalars + gram.reshape(N, -1) @ W.reshape(W.shape[0], -1).t()
+            Wf, Wb = self._gram_w[i].get(self._wread(i, k))
+            scalars = scalars + torch.ops.fsctep.gram_bilinear(xb[k].transpose(1, 2), Wf, Wb,
+                                                               1.0 / math.sqrt(2 * k[0] + 1))
         outs, off = [], 0
         for i, k in enumerate(self.keys):
             d = 2 * k[0] + 1

@@ -123,10 +123,13 @@ def _sparse_conv_setup(ctx, inputs, output):
     ctx.save_for_backward(h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst)
     ctx.inv_norm = inv_norm
     ctx.mark_non_differentiable(S, P)
+    ctx.set_materialize_grads(False)     # S and P are saved workspaces: no zero-filled gradients for them
 
 
 def _sparse_conv_bwd(ctx, grad_out, grad_s, grad_p):
     h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst = ctx.saved_tensors
+    if grad_out is None:
+        return (None,) * 10
     if ctx.needs_input_grad[3] or ctx.needs_input_grad[4]:
         raise NotImplementedError("parameter gradients of the sparse conv are not implemented "
                                   "(energy/force inference only)")
@@ -214,10 +217,13 @@ def _sparse_conv1_setup(ctx, inputs, output):
     _, Q = output
     ctx.save_for_backward(n, mb, Q, dst_ptr, edge_pair)
     ctx.mark_non_differentiable(Q)
+    ctx.set_materialize_grads(False)
 
 
 def _sparse_conv1_bwd(ctx, grad_out, grad_q):
     n, mb, Q, dst_ptr, edge_pair = ctx.saved_tensors
+    if grad_out is None:
+        return (None,) * 8
     if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
         raise NotImplementedError("parameter gradients of the sparse conv1 are not implemented "
                                   "(energy/force inference only)")

@@ -6,10 +6,11 @@ holds the reference's parameters under the same state_dict keys
 unchanged.  Its message passing runs in ``libfsctep_hip.so``:
 
 * conv1 (``:227-330``): ``torch.ops.fsctep.sparse_conv1`` on a species-pair table;
-* conv2..n (``:382-421``): ``torch.ops.fsctep.sparse_conv``.
+* conv2..n (``:382-421``): ``torch.ops.fsctep.sparse_conv``;
+* readout Gram bilinear ``product_3`` (``:424-456``): ``torch.ops.fsctep.gram_bilinear``.
 
-Edge geometry, the radial basis and the first two radial-MLP layers stay in PyTorch;
-the readout (``:769-833``) runs on the same internal feature layout x[N][13][C]
+Edge geometry, the radial basis, the first two radial-MLP layers and the rest of the
+readout (``:769-833``) stay in PyTorch, on the same internal feature layout x[N][13][C]
 (component-major; the reference's pseudo half is identically zero and is not stored).
 """
 
@@ -22,6 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
+from .readout_ops import GramWeights
 from .graph import Graph, prepare_graph
 from .radial import radial_basis
 
@@ -137,15 +139,15 @@ class PureCartesianSparseInvariantBilinear(nn.Module):
         self.Lmax = Lmax
         self.W = nn.ParameterList([nn.Parameter(torch.randn(out_channels, channels, channels) * 0.02)
                                    for _ in range(Lmax + 1)])
+        self._prepared = [GramWeights() for _ in range(Lmax + 1)]
 
     def forward(self, blocks):
-        """blocks[L]: (N, 3^L, channels) -> (N, out_channels)."""
+        """blocks[L]: (N, 3^L, channels) -> (N, out_channels), by the fused Gram-bilinear kernel."""
         total = 0
         for L, t in enumerate(blocks):
-            N = t.shape[0]
             scale = 1.0 / math.sqrt(3 ** L) if L > 0 else 1.0
-            gram = torch.bmm(t.transpose(1, 2).contiguous(), t) * scale
-            total = total + gram.reshape(N, -1) @ self.W[L].reshape(self.out_channels, -1).t()
+            Wf, Wb = self._prepared[L].get(self.W[L])
+            total = total + torch.ops.fsctep.gram_bilinear(t, Wf, Wb, scale)
         return total
 
 
@@ -244,7 +246,7 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         pos = pos.to(dtype)
         cell = cell.to(dtype)
         N = pos.shape[0]
-        shift_vec = torch.einsum("ni,nij->nj", g.shifts.to(dtype), cell[batch[g.src]])
+        shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * cell[batch[g.src]]).sum(1)   # elementwise: no batched GEMM
         vec = pos[g.dst] - pos[g.src] + shift_vec
         r = vec.norm(dim=1)
         n = vec / r.clamp(min=1e-8).unsqueeze(-1)

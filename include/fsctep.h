@@ -155,6 +155,30 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
                             const float* gates, const float* qtab, float* grad_F, float* grad_gates,
                             hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Readout invariant Gram bilinear: out[n][o] = sum_{i,j} W[o][i][j] G_n[i][j],
+ * G_n[i][j] = scale * sum_m t[n][m][i] t[n][m][j], for t [N][D][nC] (D in {1,3,5,7,9}, nC a
+ * multiple of 16 up to 1024) and W [S][nC][nC] (S 32 or 64).  G is never materialised.
+ * Replaces PureCartesianSparseInvariantBilinear.forward (models/pure_cartesian_sparse_layers.py:424-456;
+ * one call per rank L with scale 3^{-L/2}) and the ICTD readout
+ * `einsum("ocd,ncd->no", W_read[l], gram)` (models/pure_cartesian_ictd_layers_full.py:999-1000,
+ * models/pure_cartesian_ictd_layers_o3.py:1017-1018; one call per irrep, scale (2l+1)^{-1/2}).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Floats of each prepared weight layout (Wf and Wb) and of the forward workspace. */
+int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* weight_floats, int64_t* workspace_floats);
+
+/* Block-pair layouts of W: Wf[p][16][S][16] (forward) and Wb[p][256][S] (backward, W + W^T). */
+int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, float* Wb, hipStream_t stream);
+
+/* out [N][S]; part_ws holds fsc_gram_sizes' workspace_floats (per-chunk partial sums). */
+int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
+                     const float* Wf, float* part_ws, float* out, hipStream_t stream);
+
+/* grad_t [N][D][nC] = scale * sum_j (sum_o grad_out[n][o] (W[o] + W[o]^T))[i][j] t[n][m][j]. */
+int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* grad_out,
+                      const float* t, const float* Wb, float* grad_t, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,3 +71,18 @@ def test_fake_kernels_trace_shapes():
         e = torch.empty(30, dtype=torch.int32)
         out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, 0.5)
         assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64,) and P.shape == (30 * 18 * 64,)
+
+
+def test_gram_sizes_and_fake_kernels():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from fsctep_amd import readout_ops
+    w, ws = readout_ops.gram_sizes(1000, 384, 64)
+    assert w == 300 * 256 * 64 and ws == 38 * 1000 * 64      # 24 blocks -> 300 pairs -> 38 chunks of 8
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        readout_ops.gram_sizes(10, 40, 64)
+    with FakeTensorMode():
+        W = torch.empty(64, 192, 192)
+        Wf, Wb = torch.ops.fsctep.gram_prepare_weights(W)
+        assert Wf.shape == (78, 16, 64, 16) and Wb.shape == (78, 256, 64)
+        out = torch.ops.fsctep.gram_bilinear(torch.empty(7, 9, 192), Wf, Wb, 1.0)
+        assert out.shape == (7, 64)
