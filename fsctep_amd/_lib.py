@@ -1,6 +1,7 @@
-"""ctypes binding of ``libfsctep_hip.so`` (the C ABI declared in ``include/fsctep.h``).
+"""ctypes binding of ``libfsctep_hip.so`` (the C ABI declared in ``include/fsctep.h``) and the
+loader of ``libfsctep_torch.so``, which registers ``torch.ops.fsctep.*``.
 
-The library is required: importing an op without it raises, there is no CPU path.
+Both libraries are required: importing an op module without them raises, there is no CPU path.
 """
 
 from __future__ import annotations
@@ -10,6 +11,7 @@ import os
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libfsctep_hip.so")
+TORCH_LIB_PATH = os.path.join(_PKG, "libfsctep_torch.so")
 
 _i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 _pi64 = ctypes.POINTER(ctypes.c_int64)
@@ -58,6 +60,23 @@ def load(path: str = LIB_PATH):
         fn.restype = ctypes.c_int
     _lib = lib
     return lib
+
+
+_torch_ops_loaded = False
+
+
+def load_torch_ops(path: str = TORCH_LIB_PATH) -> None:
+    """Register ``torch.ops.fsctep.*`` from ``libfsctep_torch.so`` (once); raises if it is not built."""
+    global _torch_ops_loaded
+    if _torch_ops_loaded:
+        return
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} not found: build it with `python -m fsctep_amd.build` "
+                           "(the HIP kernels are the only implementation)")
+    load()                          # the C ABI library first (same instance the op library links)
+    import torch
+    torch.ops.load_library(path)
+    _torch_ops_loaded = True
 
 
 def call(name: str, *args) -> None:

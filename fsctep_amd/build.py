@@ -1,4 +1,8 @@
-"""Compile the gfx950 HIP library ``libfsctep_hip.so`` in-tree with hipcc.
+"""Compile the in-tree libraries with hipcc.
+
+* ``libfsctep_hip.so``: the gfx950 HIP kernels behind the C ABI of ``include/fsctep.h``.
+* ``libfsctep_torch.so``: the ``torch.ops.fsctep.*`` registration (schemas, device, Meta and
+  autograd kernels) over that C ABI; loadable by LibTorch processes without Python.
 
     python -m fsctep_amd.build
 """
@@ -14,12 +18,13 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libfsctep_hip.so")
+TORCH_LIB = os.path.join(PKG, "libfsctep_torch.so")
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     # packed fp32 (v_pk_*_f32) code generation disabled for every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wno-unused-command-line-argument",
+    "-Wno-unused-command-line-argument", "-Wl,-soname,libfsctep_hip.so",
 ]
 
 
@@ -27,21 +32,48 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
+def _torch_dirs() -> tuple[str, str]:
+    import torch
+    base = os.path.dirname(torch.__file__)
+    return os.path.join(base, "include"), os.path.join(base, "lib")
+
+
+def _check(res: subprocess.CompletedProcess | None, proc, what: str) -> str:
+    out, err = proc.communicate()
+    if proc.returncode != 0:
+        sys.stderr.write(out + err)
+        raise RuntimeError(f"hipcc failed building {what}")
+    return "\n".join(ln for ln in (out + err).splitlines()
+                     if ln.strip() and "packed-fp32-ops" not in ln and "not a recognized feature" not in ln)
+
+
 def build(verbose: bool = False) -> str:
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
     tmp = LIB + ".tmp"
-    cmd = [hipcc, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *sources(), "-o", tmp]
+    hip_cmd = [hipcc, *HIP_FLAGS, *inc, *sources(), "-o", tmp]
+    tinc, tlib = _torch_dirs()
+    obj = os.path.join(PKG, "torch_ops.o.tmp")
+    torch_cc = [hipcc, "-std=c++17", "-O2", "-fPIC", "-c", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+                "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"),
+                "-I", "/opt/rocm/include", *inc, os.path.join(CSRC, "torch_ops.cpp"), "-o", obj]
     if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+        print(" ".join(hip_cmd), "\n", " ".join(torch_cc), flush=True)
+    procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+             for c in (hip_cmd, torch_cc)]
+    notes = [_check(None, procs[0], "libfsctep_hip.so"), _check(None, procs[1], "torch_ops.cpp")]
+    os.replace(tmp, LIB)
+    ttmp = TORCH_LIB + ".tmp"
+    link = [hipcc, "-shared", "-fPIC", obj, "-o", ttmp, "-L", PKG, "-lfsctep_hip", "-L", tlib, "-ltorch",
+            "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}"]
+    res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libfsctep_hip.so")
-    noise = [ln for ln in (res.stdout + res.stderr).splitlines()
-             if ln.strip() and "packed-fp32-ops" not in ln and "not a recognized feature" not in ln]
-    if verbose and noise:
-        print("\n".join(noise))
-    os.replace(tmp, LIB)
+        raise RuntimeError("linking libfsctep_torch.so failed")
+    os.remove(obj)
+    os.replace(ttmp, TORCH_LIB)
+    if verbose and any(notes):
+        print("\n".join(n for n in notes if n))
     return LIB
 
 

@@ -1,0 +1,593 @@
+// TorchScript / LibTorch registration of the fsctep ops: `torch.ops.fsctep.*`.
+//
+// This library (libfsctep_torch.so) is the op boundary for both Python and C++ callers.  It holds
+// the schemas, the device kernels (the C ABI of libfsctep_hip.so launched on the current stream),
+// Meta kernels (shapes only: make_fx / torch.export / FakeTensor) and C++ autograd kernels whose
+// backward is again a registered op.  It needs no Python: a LibTorch process (the LAMMPS engine,
+// lammps_user_mfftorch/src/USER-MFFTORCH/mff_torch_engine.cpp:226-249 loads MFF_CUSTOM_OPS_LIB with
+// RTLD_GLOBAL) gets the ops by loading it, and a TorchScript core.pt whose graph calls them runs
+// there with forces from C++ autograd (mff_torch_engine.cpp:818-820).
+//
+// Parameter gradients are not produced (the path serves energy and forces); the autograd kernels
+// raise if one is requested.  ICTD layout tables travel as a CPU int32 tensor holding the
+// FscIctdLayout struct.
+
+#include <ATen/ATen.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/autograd.h>
+#include <torch/library.h>
+
+#include "fsctep.h"
+
+namespace {
+
+using at::Tensor;
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+constexpr int64_t KH = 64;   // radial hidden width feeding the last radial Linear
+
+hipStream_t stream_of(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+
+void check(int rc, const char* name) {
+  TORCH_CHECK(rc == 0, name, " failed (", rc, "): ", fsc_last_error());
+}
+
+void require_gpu(std::initializer_list<std::reference_wrapper<const Tensor>> ts) {
+  for (const Tensor& t : ts)
+    TORCH_CHECK(!t.defined() || t.is_cuda(), "fsctep ops run on the GPU only (HIP kernels); got a ",
+                t.device(), " tensor");
+}
+
+Tensor f32c(const Tensor& t) { return t.to(at::kFloat).contiguous(); }
+
+Tensor i32c(const Tensor& t, const char* what) {
+  TORCH_CHECK(t.scalar_type() == at::kInt, what, " must be int32");
+  return t.contiguous();
+}
+
+const float* cf(const Tensor& t) { return t.numel() ? t.data_ptr<float>() : nullptr; }
+float* mf(Tensor& t) { return t.numel() ? t.data_ptr<float>() : nullptr; }
+const int32_t* ci(const Tensor& t) { return t.numel() ? t.data_ptr<int32_t>() : nullptr; }
+
+at::TensorOptions fopts(const Tensor& like) { return like.options().dtype(at::kFloat); }
+
+const FscIctdLayout* layout_of(const Tensor& layout) {
+  TORCH_CHECK(layout.device().is_cpu() && layout.scalar_type() == at::kInt && layout.is_contiguous() &&
+                  layout.numel() * 4 == (int64_t)sizeof(FscIctdLayout),
+              "layout must be a contiguous CPU int32 tensor holding an FscIctdLayout (",
+              sizeof(FscIctdLayout) / 4, " entries)");
+  return reinterpret_cast<const FscIctdLayout*>(layout.data_ptr<int32_t>());
+}
+
+// ============================================================== sparse (pure-cartesian-sparse)
+
+std::tuple<Tensor, Tensor> sparse_prepare_weights(const Tensor& w_last, const Tensor& b_last, int64_t channels) {
+  require_gpu({w_last, b_last});
+  const int64_t C = channels;
+  TORCH_CHECK(w_last.dim() == 2 && w_last.size(0) == 6 * C * C && w_last.size(1) == KH && b_last.numel() == 6 * C * C,
+              "fc.4 of a sparse conv2 layer must be (6*C*C, 64)");
+  Tensor w = f32c(w_last), b = f32c(b_last);
+  Tensor bk1 = at::empty({6 * 65 * C * C}, fopts(w)), bk6 = at::empty_like(bk1);
+  check(fsc_sparse_conv_prepare_weights(cf(w), cf(b), (int32_t)C, mf(bk1), mf(bk6), stream_of(w)),
+        "fsc_sparse_conv_prepare_weights");
+  return {bk1, bk6};
+}
+
+std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, const Tensor& b_last, int64_t C) {
+  return {at::empty({6 * 65 * C * C}, fopts(w_last)), at::empty({6 * 65 * C * C}, fopts(w_last))};
+}
+
+std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,
+                                               const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
+                                               const Tensor& src_ptr, const Tensor& src_perm,
+                                               const Tensor& edge_dst, double inv_norm) {
+  require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst});
+  TORCH_CHECK(x_.dim() == 3 && x_.size(1) == 13, "x must be (N, 13, C)");
+  const int64_t N = x_.size(0), C = x_.size(2), E = h_.size(0);
+  Tensor x = f32c(x_), h = f32c(h_), n = f32c(n_);
+  Tensor dp = i32c(dst_ptr, "dst_ptr"), sp = i32c(src_ptr, "src_ptr"), pm = i32c(src_perm, "src_perm");
+  int64_t s_f = 0, p_f = 0;
+  check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
+  Tensor S = at::empty({s_f}, fopts(x)), P = at::empty({p_f}, fopts(x)), out = at::empty({N, 13, C}, fopts(x));
+  check(fsc_sparse_conv_forward(N, E, (int32_t)C, ci(dp), ci(sp), ci(pm), cf(x), cf(h), cf(n), cf(bk1),
+                                (float)inv_norm, mf(S), mf(P), mf(out), stream_of(x)),
+        "fsc_sparse_conv_forward");
+  return {out, S, P};
+}
+
+std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tensor& h, const Tensor&, const Tensor&,
+                                                    const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                    const Tensor&, double) {
+  const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
+  return {at::empty({N, 13, C}, fopts(x)), at::empty({N * 18 * 65 * C}, fopts(x)), at::empty({E * 18 * C}, fopts(x))};
+}
+
+std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_, const Tensor& n_,
+                                                        const Tensor& bk6, const Tensor& S, const Tensor& P,
+                                                        const Tensor& dst_ptr, const Tensor& src_ptr,
+                                                        const Tensor& src_perm, const Tensor& edge_dst,
+                                                        double inv_norm) {
+  require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
+  const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
+  Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_);
+  Tensor dS = at::empty_like(S), dx = at::empty({N, 13, C}, fopts(g)), dh = at::empty({E, KH}, fopts(g)),
+         dn = at::empty({E, 3}, fopts(g));
+  check(fsc_sparse_conv_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(src_ptr, "src_ptr")),
+                                 ci(i32c(src_perm, "src_perm")), ci(i32c(edge_dst, "edge_dst")), cf(g), cf(h), cf(n),
+                                 cf(bk6), cf(S), cf(P), (float)inv_norm, mf(dS), mf(dx), mf(dh), mf(dn),
+                                 stream_of(g)),
+        "fsc_sparse_conv_backward");
+  return {dx, dh, dn};
+}
+
+std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h, const Tensor&,
+                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                             const Tensor&, const Tensor&, const Tensor&, double) {
+  const int64_t E = h.size(0);
+  return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h))};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1_pair_table(const Tensor& w_last, const Tensor& b_last,
+                                                   const Tensor& atom_table, int64_t channels) {
+  require_gpu({w_last, b_last, atom_table});
+  const int64_t C = channels, NS = atom_table.size(0);
+  TORCH_CHECK(atom_table.dim() == 2 && atom_table.size(1) == 8 && w_last.size(0) == 6 * C * 64 && w_last.size(1) == KH,
+              "conv1 pair table needs output_size 8 and fc.4 of shape (6*C*64, 64)");
+  Tensor w = f32c(w_last), b = f32c(b_last), a = f32c(atom_table);
+  Tensor mf_ = at::empty({NS * NS * 3 * 65 * C}, fopts(w)), mb = at::empty_like(mf_);
+  check(fsc_sparse_conv1_pair_table(cf(w), cf(b), cf(a), (int32_t)NS, (int32_t)C, mf(mf_), mf(mb), stream_of(w)),
+        "fsc_sparse_conv1_pair_table");
+  return {mf_, mb};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1_pair_table_meta(const Tensor& w_last, const Tensor&, const Tensor& atom_table,
+                                                        int64_t C) {
+  const int64_t NS = atom_table.size(0);
+  return {at::empty({NS * NS * 3 * 65 * C}, fopts(w_last)), at::empty({NS * NS * 3 * 65 * C}, fopts(w_last))};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1(const Tensor& h_, const Tensor& n_, const Tensor& mf_, const Tensor& mb,
+                                        const Tensor& dst_ptr, const Tensor& edge_pair, int64_t n_nodes,
+                                        int64_t channels) {
+  require_gpu({h_, n_, mf_, mb, dst_ptr, edge_pair});
+  const int64_t E = h_.size(0), C = channels;
+  Tensor h = f32c(h_), n = f32c(n_);
+  Tensor Q = at::empty({E * 3 * C}, fopts(h)), out = at::empty({n_nodes, 13, C}, fopts(h));
+  check(fsc_sparse_conv1_forward(n_nodes, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")),
+                                 ci(i32c(edge_pair, "edge_pair")), cf(h), cf(n), cf(mf_), mf(Q), mf(out), stream_of(h)),
+        "fsc_sparse_conv1_forward");
+  return {out, Q};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1_meta(const Tensor& h, const Tensor&, const Tensor&, const Tensor&,
+                                             const Tensor&, const Tensor&, int64_t n_nodes, int64_t C) {
+  return {at::empty({n_nodes, 13, C}, fopts(h)), at::empty({h.size(0) * 3 * C}, fopts(h))};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1_backward(const Tensor& grad_out, const Tensor& n_, const Tensor& mb,
+                                                 const Tensor& Q, const Tensor& dst_ptr, const Tensor& edge_pair) {
+  require_gpu({grad_out, n_, mb, Q, dst_ptr, edge_pair});
+  const int64_t N = grad_out.size(0), C = grad_out.size(2), E = n_.size(0);
+  Tensor g = f32c(grad_out), n = f32c(n_);
+  Tensor dh = at::empty({E, KH}, fopts(g)), dn = at::empty({E, 3}, fopts(g));
+  check(fsc_sparse_conv1_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_pair, "edge_pair")),
+                                  cf(g), cf(n), cf(mb), cf(Q), mf(dh), mf(dn), stream_of(g)),
+        "fsc_sparse_conv1_backward");
+  return {dh, dn};
+}
+
+std::tuple<Tensor, Tensor> sparse_conv1_backward_meta(const Tensor&, const Tensor& n, const Tensor&, const Tensor&,
+                                                      const Tensor&, const Tensor&) {
+  return {at::empty({n.size(0), KH}, fopts(n)), at::empty({n.size(0), 3}, fopts(n))};
+}
+
+// ============================================================== ICTD (pure-cartesian-ictd / -o3)
+
+Tensor ictd_prepare_weights(const Tensor& W) {
+  require_gpu({W});
+  const int64_t P = W.size(0), C = W.size(1);
+  Tensor Wc = f32c(W).reshape({P, C, C});
+  Tensor Wt = at::empty_like(Wc);
+  check(fsc_ictd_prepare_weights(cf(Wc), (int32_t)P, (int32_t)C, mf(Wt), stream_of(Wc)), "fsc_ictd_prepare_weights");
+  return Wt;
+}
+
+Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({W.size(0), W.size(1), W.size(1)}, fopts(W)); }
+
+Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
+                 const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
+                 const Tensor& src_perm, const Tensor& layout) {
+  require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+  const FscIctdLayout* L = layout_of(layout);
+  TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
+  const int64_t N = x_.size(0), C = x_.size(2), E = Y_.size(0);
+  Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_), W = f32c(W_).reshape({W_.size(0), C, C});
+  Tensor z = at::empty({N, L->KT, C}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
+  check(fsc_ictd_conv_forward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
+                              cf(x), cf(Y), cf(gates), cf(cg), cf(W), mf(z), mf(out), stream_of(x)),
+        "fsc_ictd_conv_forward");
+  return out;
+}
+
+Tensor ictd_conv_meta(const Tensor& x, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&) {
+  return at::empty(x.sizes(), fopts(x));
+}
+
+std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, const Tensor& x_, const Tensor& Y_,
+                                                      const Tensor& gates_, const Tensor& Wt, const Tensor& cg,
+                                                      const Tensor& dst_ptr, const Tensor& edge_src,
+                                                      const Tensor& src_ptr, const Tensor& src_perm,
+                                                      const Tensor& layout) {
+  require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+  const FscIctdLayout* L = layout_of(layout);
+  const int64_t N = x_.size(0), M = x_.size(1), C = x_.size(2), E = Y_.size(0);
+  Tensor g = f32c(grad_out), x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
+  Tensor dz = at::empty({N, L->KT, C}, fopts(x)), dxe = at::empty({E, M, C}, fopts(x)), dx = at::empty({N, M, C}, fopts(x));
+  Tensor dgates = at::zeros({E, L->NREF}, fopts(x)), dY = at::empty({E, L->NY}, fopts(x));
+  check(fsc_ictd_conv_backward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
+                               ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")), cf(g), cf(x), cf(Y),
+                               cf(gates), cf(cg), cf(Wt), mf(dz), mf(dxe), mf(dx), mf(dgates), mf(dY), stream_of(x)),
+        "fsc_ictd_conv_backward");
+  return {dx, dgates, dY};
+}
+
+std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward_meta(const Tensor&, const Tensor& x, const Tensor& Y,
+                                                           const Tensor& gates, const Tensor&, const Tensor&,
+                                                           const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                           const Tensor&) {
+  return {at::empty(x.sizes(), fopts(x)), at::empty(gates.sizes(), fopts(gates)), at::empty(Y.sizes(), fopts(Y))};
+}
+
+Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, const Tensor& dst_ptr,
+                  const Tensor& edge_pair, const Tensor& node_species, int64_t n_nodes, int64_t n_species,
+                  int64_t n_comps, const Tensor& layout) {
+  require_gpu({F_, gates_, qtab_, dst_ptr, edge_pair, node_species});
+  const FscIctdLayout* L = layout_of(layout);
+  TORCH_CHECK(n_comps == L->M, "n_comps does not match the layout");
+  const int64_t C = qtab_.size(-1), E = F_.size(0);
+  Tensor F = f32c(F_), gates = f32c(gates_), qtab = f32c(qtab_);
+  Tensor out = at::empty({n_nodes, L->M, C}, fopts(F));
+  check(fsc_ictd_conv1_forward(L, n_nodes, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")),
+                               ci(i32c(edge_pair, "edge_pair")), cf(F), cf(gates), cf(qtab), mf(out), stream_of(F)),
+        "fsc_ictd_conv1_forward");
+  return out;
+}
+
+Tensor ictd_conv1_meta(const Tensor& F, const Tensor&, const Tensor& qtab, const Tensor&, const Tensor&, const Tensor&,
+                       int64_t n_nodes, int64_t, int64_t n_comps, const Tensor&) {
+  return at::empty({n_nodes, n_comps, qtab.size(-1)}, fopts(F));
+}
+
+std::tuple<Tensor, Tensor> ictd_conv1_backward(const Tensor& grad_out, const Tensor& F_, const Tensor& gates_,
+                                               const Tensor& qtab_, const Tensor& dst_ptr, const Tensor& edge_pair,
+                                               const Tensor& node_species, int64_t n_species, const Tensor& layout) {
+  require_gpu({grad_out, F_, gates_, qtab_, dst_ptr, edge_pair, node_species});
+  const FscIctdLayout* L = layout_of(layout);
+  const int64_t N = grad_out.size(0), C = grad_out.size(2), E = F_.size(0);
+  Tensor g = f32c(grad_out), F = f32c(F_), gates = f32c(gates_), qtab = f32c(qtab_);
+  Tensor dF = at::empty_like(F), dgates = at::zeros_like(gates);
+  check(fsc_ictd_conv1_backward(L, N, E, (int32_t)C, (int32_t)n_species, ci(i32c(dst_ptr, "dst_ptr")),
+                                ci(i32c(edge_pair, "edge_pair")), ci(i32c(node_species, "node_species")), cf(g), cf(F),
+                                cf(gates), cf(qtab), mf(dF), mf(dgates), stream_of(F)),
+        "fsc_ictd_conv1_backward");
+  return {dF, dgates};
+}
+
+std::tuple<Tensor, Tensor> ictd_conv1_backward_meta(const Tensor&, const Tensor& F, const Tensor& gates, const Tensor&,
+                                                    const Tensor&, const Tensor&, const Tensor&, int64_t, const Tensor&) {
+  return {at::empty(F.sizes(), fopts(F)), at::empty(gates.sizes(), fopts(gates))};
+}
+
+// ============================================================== readout Gram bilinear
+
+std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
+  require_gpu({W_});
+  TORCH_CHECK(W_.dim() == 3 && W_.size(1) == W_.size(2), "W must be (S, nC, nC)");
+  const int64_t S = W_.size(0), nC = W_.size(1), nb = nC / 16, P = nb * (nb + 1) / 2;
+  Tensor W = f32c(W_);
+  Tensor Wf = at::empty({P, 16, S, 16}, fopts(W)), Wb = at::empty({P, 256, S}, fopts(W));
+  check(fsc_gram_prepare_weights(cf(W), (int32_t)S, (int32_t)nC, mf(Wf), mf(Wb), stream_of(W)),
+        "fsc_gram_prepare_weights");
+  return {Wf, Wb};
+}
+
+std::tuple<Tensor, Tensor> gram_prepare_weights_meta(const Tensor& W) {
+  const int64_t S = W.size(0), nb = W.size(1) / 16, P = nb * (nb + 1) / 2;
+  return {at::empty({P, 16, S, 16}, fopts(W)), at::empty({P, 256, S}, fopts(W))};
+}
+
+Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale) {
+  require_gpu({t_, Wf, Wb});
+  TORCH_CHECK(t_.dim() == 3 && Wb.dim() == 3, "t must be (N, D, nC) and Wb (P, 256, S)");
+  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wb.size(2);
+  Tensor t = f32c(t_);
+  int64_t wn = 0, wsn = 0;
+  check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wn, &wsn), "fsc_gram_sizes");
+  TORCH_CHECK(Wf.numel() == wn && Wb.numel() == wn, "prepared Gram weights do not match nC = ", nC);
+  Tensor ws = at::empty({std::max<int64_t>(wsn, 1)}, fopts(t)), out = at::empty({N, S}, fopts(t));
+  check(fsc_gram_forward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(t), cf(Wf), mf(ws), mf(out),
+                         stream_of(t)),
+        "fsc_gram_forward");
+  return out;
+}
+
+Tensor gram_bilinear_meta(const Tensor& t, const Tensor&, const Tensor& Wb, double) {
+  return at::empty({t.size(0), Wb.size(2)}, fopts(t));
+}
+
+Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t_, const Tensor& Wb, double scale) {
+  require_gpu({grad_out, t_, Wb});
+  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wb.size(2);
+  Tensor g = f32c(grad_out), t = f32c(t_);
+  Tensor dt = at::empty({N, D, nC}, fopts(t));
+  check(fsc_gram_backward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(g), cf(t), cf(Wb), mf(dt),
+                          stream_of(t)),
+        "fsc_gram_backward");
+  return dt;
+}
+
+Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&, double) {
+  return at::empty(t.sizes(), fopts(t));
+}
+
+// ============================================================== autograd
+
+template <typename... Args>
+c10::TypedOperatorHandle<Args...> op_handle(const char* name) {
+  return c10::Dispatcher::singleton().findSchemaOrThrow(name, "").typed<Args...>();
+}
+
+void refuse_param_grad(AutogradContext* ctx, std::initializer_list<int> idx, const char* what) {
+  for (int i : idx)
+    TORCH_CHECK(!ctx->needs_input_grad(i), "parameter gradients of ", what,
+                " are not implemented (energy/force inference only)");
+}
+
+struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
+                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, double inv_norm) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&,
+                                                                  const Tensor&, const Tensor&, const Tensor&,
+                                                                  const Tensor&, const Tensor&, const Tensor&, double)>(
+        "fsctep::sparse_conv");
+    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm);
+    ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
+    ctx->saved_data["inv_norm"] = inv_norm;
+    ctx->mark_non_differentiable({S, P});
+    ctx->set_materialize_grads(false);   // S and P are saved workspaces: no zero-filled gradients for them
+    return {out, S, P};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(10);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {3, 4}, "the sparse conv");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+        const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::sparse_conv_backward");
+    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8],
+                                ctx->saved_data["inv_norm"].toDouble());
+    res[0] = dx;
+    res[1] = dh;
+    res[2] = dn;
+    return res;
+  }
+};
+
+std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const Tensor& h, const Tensor& n,
+                                                        const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
+                                                        const Tensor& src_ptr, const Tensor& src_perm,
+                                                        const Tensor& edge_dst, double inv_norm) {
+  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm);
+  return {r[0], r[1], r[2]};
+}
+
+struct SparseConv1Fn : public torch::autograd::Function<SparseConv1Fn> {
+  static variable_list forward(AutogradContext* ctx, Tensor h, Tensor n, Tensor mf_, Tensor mb, Tensor dst_ptr,
+                               Tensor edge_pair, int64_t n_nodes, int64_t channels) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&, int64_t, int64_t)>(
+        "fsctep::sparse_conv1");
+    auto [out, Q] = op.call(h, n, mf_, mb, dst_ptr, edge_pair, n_nodes, channels);
+    ctx->save_for_backward({n, mb, Q, dst_ptr, edge_pair});
+    ctx->mark_non_differentiable({Q});
+    ctx->set_materialize_grads(false);
+    return {out, Q};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(8);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {2, 3}, "the sparse conv1");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&)>("fsctep::sparse_conv1_backward");
+    auto [dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4]);
+    res[0] = dh;
+    res[1] = dn;
+    return res;
+  }
+};
+
+std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& n, const Tensor& mf_, const Tensor& mb,
+                                                 const Tensor& dst_ptr, const Tensor& edge_pair, int64_t n_nodes,
+                                                 int64_t channels) {
+  auto r = SparseConv1Fn::apply(h, n, mf_, mb, dst_ptr, edge_pair, n_nodes, channels);
+  return {r[0], r[1]};
+}
+
+struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg,
+                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                      const Tensor&)>("fsctep::ictd_conv");
+    Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout);
+    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout});
+    return {out};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(11);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {3, 4, 5}, "the ICTD conv");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&)>("fsctep::ictd_conv_backward");
+    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9]);
+    res[0] = dx;
+    res[1] = dY;
+    res[2] = dgates;
+    return res;
+  }
+};
+
+Tensor ictd_conv_autograd(const Tensor& x, const Tensor& Y, const Tensor& gates, const Tensor& W, const Tensor& Wt,
+                          const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
+                          const Tensor& src_perm, const Tensor& layout) {
+  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout)[0];
+}
+
+struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
+  static variable_list forward(AutogradContext* ctx, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr,
+                               Tensor edge_pair, Tensor node_species, int64_t n_nodes, int64_t n_species,
+                               int64_t n_comps, Tensor layout) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                      const Tensor&, int64_t, int64_t, int64_t, const Tensor&)>("fsctep::ictd_conv1");
+    Tensor out = op.call(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout);
+    ctx->save_for_backward({F, gates, qtab, dst_ptr, edge_pair, node_species, layout});
+    ctx->saved_data["n_species"] = n_species;
+    return {out};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(10);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {2}, "the ICTD conv1");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&, const Tensor&, int64_t,
+                                                          const Tensor&)>("fsctep::ictd_conv1_backward");
+    auto [dF, dgates] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], ctx->saved_data["n_species"].toInt(), s[6]);
+    res[0] = dF;
+    res[1] = dgates;
+    return res;
+  }
+};
+
+Tensor ictd_conv1_autograd(const Tensor& F, const Tensor& gates, const Tensor& qtab, const Tensor& dst_ptr,
+                           const Tensor& edge_pair, const Tensor& node_species, int64_t n_nodes, int64_t n_species,
+                           int64_t n_comps, const Tensor& layout) {
+  return IctdConv1Fn::apply(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout)[0];
+}
+
+struct GramFn : public torch::autograd::Function<GramFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor t, Tensor Wf, Tensor Wb, double scale) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear");
+    Tensor out = op.call(t, Wf, Wb, scale);
+    ctx->save_for_backward({t, Wb});
+    ctx->saved_data["scale"] = scale;
+    return {out};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(4);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {1, 2}, "the readout Gram bilinear");
+    auto s = ctx->get_saved_variables();
+    static auto op =
+        op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear_backward");
+    res[0] = op.call(grads[0], s[0], s[1], ctx->saved_data["scale"].toDouble());
+    return res;
+  }
+};
+
+Tensor gram_bilinear_autograd(const Tensor& t, const Tensor& Wf, const Tensor& Wb, double scale) {
+  return GramFn::apply(t, Wf, Wb, scale)[0];
+}
+
+// CPU tensors: the HIP kernels are the only implementation, so say that instead of "no CPU kernel".
+void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
+  TORCH_CHECK(false, op.schema().name(), ": fsctep ops run on the GPU only (HIP kernels); got CPU tensors");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(fsctep, m) {
+  m.def("sparse_prepare_weights(Tensor w_last, Tensor b_last, int channels) -> (Tensor, Tensor)");
+  m.def("sparse_conv(Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6, Tensor dst_ptr, Tensor src_ptr, "
+        "Tensor src_perm, Tensor edge_dst, float inv_norm) -> (Tensor, Tensor, Tensor)");
+  m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
+        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, float inv_norm) -> (Tensor, Tensor, Tensor)");
+  m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
+  m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor edge_pair, int n_nodes, "
+        "int channels) -> (Tensor, Tensor)");
+  m.def("sparse_conv1_backward(Tensor grad_out, Tensor n, Tensor mb, Tensor Q, Tensor dst_ptr, Tensor edge_pair) "
+        "-> (Tensor, Tensor)");
+  m.def("ictd_prepare_weights(Tensor W) -> Tensor");
+  m.def("ictd_conv(Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg, Tensor dst_ptr, "
+        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) -> Tensor");
+  m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
+        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) -> (Tensor, Tensor, Tensor)");
+  m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
+        "int n_nodes, int n_species, int n_comps, Tensor layout) -> Tensor");
+  m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "
+        "Tensor edge_pair, Tensor node_species, int n_species, Tensor layout) -> (Tensor, Tensor)");
+  m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
+  m.def("gram_bilinear(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
+  m.def("gram_bilinear_backward(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
+  m.impl("sparse_prepare_weights", sparse_prepare_weights);
+  m.impl("sparse_conv", sparse_conv);
+  m.impl("sparse_conv_backward", sparse_conv_backward);
+  m.impl("sparse_conv1_pair_table", sparse_conv1_pair_table);
+  m.impl("sparse_conv1", sparse_conv1);
+  m.impl("sparse_conv1_backward", sparse_conv1_backward);
+  m.impl("ictd_prepare_weights", ictd_prepare_weights);
+  m.impl("ictd_conv", ictd_conv);
+  m.impl("ictd_conv_backward", ictd_conv_backward);
+  m.impl("ictd_conv1", ictd_conv1);
+  m.impl("ictd_conv1_backward", ictd_conv1_backward);
+  m.impl("gram_prepare_weights", gram_prepare_weights);
+  m.impl("gram_bilinear", gram_bilinear);
+  m.impl("gram_bilinear_backward", gram_bilinear_backward);
+}
+
+TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
+  m.impl("sparse_prepare_weights", sparse_prepare_weights_meta);
+  m.impl("sparse_conv", sparse_conv_meta);
+  m.impl("sparse_conv_backward", sparse_conv_backward_meta);
+  m.impl("sparse_conv1_pair_table", sparse_conv1_pair_table_meta);
+  m.impl("sparse_conv1", sparse_conv1_meta);
+  m.impl("sparse_conv1_backward", sparse_conv1_backward_meta);
+  m.impl("ictd_prepare_weights", ictd_prepare_weights_meta);
+  m.impl("ictd_conv", ictd_conv_meta);
+  m.impl("ictd_conv_backward", ictd_conv_backward_meta);
+  m.impl("ictd_conv1", ictd_conv1_meta);
+  m.impl("ictd_conv1_backward", ictd_conv1_backward_meta);
+  m.impl("gram_prepare_weights", gram_prepare_weights_meta);
+  m.impl("gram_bilinear", gram_bilinear_meta);
+  m.impl("gram_bilinear_backward", gram_bilinear_backward_meta);
+}
+
+TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
+  m.impl("sparse_conv", sparse_conv_autograd);
+  m.impl("sparse_conv1", sparse_conv1_autograd);
+  m.impl("ictd_conv", ictd_conv_autograd);
+  m.impl("ictd_conv1", ictd_conv1_autograd);
+  m.impl("gram_bilinear", gram_bilinear_autograd);
+}
+
+TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
+  for (const char* name : {"sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table",
+                           "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
+                           "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
+                           "gram_bilinear", "gram_bilinear_backward"})
+    m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
+}

@@ -1,7 +1,14 @@
-"""ICTD custom ops (``torch.ops.fsctep.ictd_*``) over the C ABI, and the kernel layout tables.
+"""ICTD kernel layout tables and helpers over the ``torch.ops.fsctep.ictd_*`` ops.
 
 A layout (active irreps + live paths, see ``ictd_basis.Layout``) is turned into the C struct
-``FscIctdLayout`` once and registered under an integer id that the ops carry.
+``FscIctdLayout`` once, registered under an integer id, and handed to the ops as a CPU int32
+tensor holding the struct.  The ops are registered in C++ by ``libfsctep_torch.so``:
+
+    ictd_prepare_weights(W) -> Wt
+    ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout) -> out
+    ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout)
+    ictd_conv1(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout)
+    ictd_conv1_backward(grad_out, F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, layout)
 """
 
 from __future__ import annotations
@@ -14,6 +21,8 @@ from torch import Tensor
 
 from . import _lib
 from .ictd_basis import Layout
+
+_lib.load_torch_ops()
 
 _i32 = ctypes.c_int32
 
@@ -92,172 +101,27 @@ def layout_struct(layout_id: int) -> FscIctdLayout:
     return _LAYOUTS[layout_id][2]
 
 
-def _ref(layout_id: int) -> int:
-    return ctypes.addressof(layout_struct(layout_id))
+def layout_tensor(layout_id: int) -> Tensor:
+    """The layout table as the CPU int32 tensor the ops take (one per layout, cached)."""
+    name, lay, st = _LAYOUTS[layout_id]
+    key = ("tensor", layout_id)
+    if key not in _TENSORS:
+        raw = np.frombuffer(ctypes.string_at(ctypes.addressof(st), ctypes.sizeof(st)), dtype=np.int32)
+        _TENSORS[key] = torch.from_numpy(raw.copy())
+    return _TENSORS[key]
 
 
-def _require_cuda(*ts):
-    for t in ts:
-        if t is not None and not t.is_cuda:
-            raise RuntimeError("fsctep ops run on the GPU only (HIP kernels); got a CPU tensor")
-
-
-def _c(t: Tensor) -> Tensor:
-    t = t if t.dtype == torch.float32 else t.float()
-    return t if t.is_contiguous() else t.contiguous()
-
-
-# ----------------------------------------------------------------------------- conv2..n
-
-@torch.library.custom_op("fsctep::ictd_prepare_weights", mutates_args=())
-def ictd_prepare_weights(W: Tensor) -> Tensor:
-    _require_cuda(W)
-    P, C = W.shape[0], W.shape[1]
-    Wc = _c(W.reshape(P, C, C))
-    Wt = torch.empty_like(Wc)
-    _lib.call("fsc_ictd_prepare_weights", _lib.ptr(Wc), P, C, _lib.ptr(Wt), _lib.stream_handle(W.device))
-    return Wt
-
-
-@ictd_prepare_weights.register_fake
-def _(W):
-    return W.new_empty(W.shape[0], W.shape[1], W.shape[1])
-
-
-@torch.library.custom_op("fsctep::ictd_conv", mutates_args=())
-def ictd_conv(x: Tensor, Y: Tensor, gates: Tensor, W: Tensor, Wt: Tensor, cg: Tensor, dst_ptr: Tensor,
-              edge_src: Tensor, src_ptr: Tensor, src_perm: Tensor, layout_id: int) -> Tensor:
-    """x (N,M,C), Y (E,NY), gates (E,NREF), W (NREF,C,C[,1]) -> (N,M,C).  Wt, src_ptr, src_perm: backward."""
-    _require_cuda(x, Y, gates, W, cg)
-    L = layout_struct(layout_id)
-    N, M, C = x.shape
-    E = Y.shape[0]
-    x, Y, gates = _c(x), _c(Y), _c(gates)
-    W = _c(W.reshape(W.shape[0], C, C))
-    z = torch.empty(N, L.KT, C, device=x.device, dtype=torch.float32)
-    out = torch.empty(N, M, C, device=x.device, dtype=torch.float32)
-    _lib.call("fsc_ictd_conv_forward", _ref(layout_id), N, E, C, _lib.ptr(dst_ptr), _lib.ptr(edge_src),
-              _lib.ptr(x), _lib.ptr(Y), _lib.ptr(gates), _lib.ptr(cg), _lib.ptr(W), _lib.ptr(z), _lib.ptr(out),
-              _lib.stream_handle(x.device))
-    return out
-
-
-@ictd_conv.register_fake
-def _(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout_id):
-    return torch.empty_like(x)
-
-
-@torch.library.custom_op("fsctep::ictd_conv_backward", mutates_args=())
-def ictd_conv_backward(grad_out: Tensor, x: Tensor, Y: Tensor, gates: Tensor, Wt: Tensor, cg: Tensor,
-                       dst_ptr: Tensor, edge_src: Tensor, src_ptr: Tensor, src_perm: Tensor,
-                       layout_id: int) -> tuple[Tensor, Tensor, Tensor]:
-    _require_cuda(grad_out, x, Y, gates, Wt, cg)
-    L = layout_struct(layout_id)
-    N, M, C = x.shape
-    E = Y.shape[0]
-    g, x, Y, gates = _c(grad_out), _c(x), _c(Y), _c(gates)
-    dz = torch.empty(N, L.KT, C, device=x.device, dtype=torch.float32)
-    dxe = torch.empty(E, M, C, device=x.device, dtype=torch.float32)
-    dx = torch.empty(N, M, C, device=x.device, dtype=torch.float32)
-    dgates = torch.zeros(E, L.NREF, device=x.device, dtype=torch.float32)
-    dY = torch.empty(E, L.NY, device=x.device, dtype=torch.float32)
-    _lib.call("fsc_ictd_conv_backward", _ref(layout_id), N, E, C, _lib.ptr(dst_ptr), _lib.ptr(edge_src),
-              _lib.ptr(src_ptr), _lib.ptr(src_perm), _lib.ptr(g), _lib.ptr(x), _lib.ptr(Y), _lib.ptr(gates),
-              _lib.ptr(cg), _lib.ptr(Wt), _lib.ptr(dz), _lib.ptr(dxe), _lib.ptr(dx), _lib.ptr(dgates),
-              _lib.ptr(dY), _lib.stream_handle(x.device))
-    return dx, dgates, dY
-
-
-@ictd_conv_backward.register_fake
-def _(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout_id):
-    return torch.empty_like(x), torch.empty_like(gates), torch.empty_like(Y)
-
-
-def _ictd_conv_setup(ctx, inputs, output):
-    x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout_id = inputs
-    ctx.save_for_backward(x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm)
-    ctx.layout_id = layout_id
-
-
-def _ictd_conv_bwd(ctx, grad_out):
-    x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm = ctx.saved_tensors
-    if ctx.needs_input_grad[3] or ctx.needs_input_grad[4] or ctx.needs_input_grad[5]:
-        raise NotImplementedError("parameter gradients of the ICTD conv are not implemented "
-                                  "(energy/force inference only)")
-    dx, dgates, dY = torch.ops.fsctep.ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src,
-                                                         src_ptr, src_perm, ctx.layout_id)
-    return dx, dY, dgates, None, None, None, None, None, None, None, None
-
-
-torch.library.register_autograd("fsctep::ictd_conv", _ictd_conv_bwd, setup_context=_ictd_conv_setup)
+_TENSORS: dict = {}
 
 
 def ictd_conv_apply(x, Y, gates, W, Wt, cg, graph, layout_id: int):
+    """Differentiable conv2..n: x (N,M,C), Y (E,NY), gates (E,NREF) -> (N,M,C)."""
     return torch.ops.fsctep.ictd_conv(x, Y, gates, W, Wt, cg, graph.dst_ptr, graph.src32, graph.src_ptr,
-                                      graph.src_perm, int(layout_id))
-
-
-# ----------------------------------------------------------------------------- conv1
-
-@torch.library.custom_op("fsctep::ictd_conv1", mutates_args=())
-def ictd_conv1(F: Tensor, gates: Tensor, qtab: Tensor, dst_ptr: Tensor, edge_pair: Tensor, node_species: Tensor,
-               n_nodes: int, n_species: int, layout_id: int) -> Tensor:
-    """F (E,NY) harmonics (+ field), gates (E,NREF), qtab (NS*NS,NP1,C) -> (N,M,C)."""
-    _require_cuda(F, gates, qtab)
-    L = layout_struct(layout_id)
-    C = qtab.shape[-1]
-    E = F.shape[0]
-    F, gates, qtab = _c(F), _c(gates), _c(qtab)
-    out = torch.empty(n_nodes, L.M, C, device=F.device, dtype=torch.float32)
-    _lib.call("fsc_ictd_conv1_forward", _ref(layout_id), n_nodes, E, C, _lib.ptr(dst_ptr), _lib.ptr(edge_pair),
-              _lib.ptr(F), _lib.ptr(gates), _lib.ptr(qtab), _lib.ptr(out), _lib.stream_handle(F.device))
-    return out
-
-
-@ictd_conv1.register_fake
-def _(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, layout_id):
-    return F.new_empty(n_nodes, layout_struct(layout_id).M, qtab.shape[-1])
-
-
-@torch.library.custom_op("fsctep::ictd_conv1_backward", mutates_args=())
-def ictd_conv1_backward(grad_out: Tensor, F: Tensor, gates: Tensor, qtab: Tensor, dst_ptr: Tensor,
-                        edge_pair: Tensor, node_species: Tensor, n_species: int,
-                        layout_id: int) -> tuple[Tensor, Tensor]:
-    _require_cuda(grad_out, F, gates, qtab)
-    N, M, C = grad_out.shape
-    E = F.shape[0]
-    g, F, gates, qtab = _c(grad_out), _c(F), _c(gates), _c(qtab)
-    dF = torch.empty_like(F)
-    dgates = torch.zeros_like(gates)
-    _lib.call("fsc_ictd_conv1_backward", _ref(layout_id), N, E, C, n_species, _lib.ptr(dst_ptr),
-              _lib.ptr(edge_pair), _lib.ptr(node_species), _lib.ptr(g), _lib.ptr(F), _lib.ptr(gates),
-              _lib.ptr(qtab), _lib.ptr(dF), _lib.ptr(dgates), _lib.stream_handle(F.device))
-    return dF, dgates
-
-
-@ictd_conv1_backward.register_fake
-def _(grad_out, F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, layout_id):
-    return torch.empty_like(F), torch.empty_like(gates)
-
-
-def _ictd_conv1_setup(ctx, inputs, output):
-    F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, layout_id = inputs
-    ctx.save_for_backward(F, gates, qtab, dst_ptr, edge_pair, node_species)
-    ctx.n_species, ctx.layout_id = n_species, layout_id
-
-
-def _ictd_conv1_bwd(ctx, grad_out):
-    F, gates, qtab, dst_ptr, edge_pair, node_species = ctx.saved_tensors
-    if ctx.needs_input_grad[2]:
-        raise NotImplementedError("parameter gradients of the ICTD conv1 are not implemented")
-    dF, dgates = torch.ops.fsctep.ictd_conv1_backward(grad_out, F, gates, qtab, dst_ptr, edge_pair, node_species,
-                                                      ctx.n_species, ctx.layout_id)
-    return dF, dgates, None, None, None, None, None, None, None
-
-
-torch.library.register_autograd("fsctep::ictd_conv1", _ictd_conv1_bwd, setup_context=_ictd_conv1_setup)
+                                      graph.src_perm, layout_tensor(layout_id))
 
 
 def ictd_conv1_apply(F, gates, qtab, graph, layout_id: int):
+    """Differentiable conv1: F (E,NY) harmonics (+ field), gates (E,NREF), qtab (NS*NS,NP1,C) -> (N,M,C)."""
     return torch.ops.fsctep.ictd_conv1(F, gates, qtab, graph.dst_ptr, graph.edge_pair, graph.species_index32,
-                                       graph.n_nodes, int(graph.species.shape[0]), int(layout_id))
+                                       graph.n_nodes, int(graph.species.shape[0]), layout_struct(layout_id).M,
+                                       layout_tensor(layout_id))

@@ -60,3 +60,25 @@ def test_gram_bilinear_strided_input_and_empty():
     assert torch.equal(a, b)
     e = torch.ops.fsctep.gram_bilinear(torch.zeros(0, 3, 64, device=DEV), Wf, Wb, 0.5)
     assert e.shape == (0, 32)
+
+
+class _GramProbe(torch.nn.Module):
+    def forward(self, t: torch.Tensor, Wf: torch.Tensor, Wb: torch.Tensor) -> torch.Tensor:
+        return torch.ops.fsctep.gram_bilinear(t, Wf, Wb, 0.25)
+
+
+def test_scripted_graph_matches_eager_with_cpp_autograd():
+    """TorchScript runs the same C++-registered op, forward and backward (the core.pt route)."""
+    from fsctep_amd import readout_ops  # noqa: F401
+    g = torch.Generator().manual_seed(9)
+    t = torch.randn(90, 5, 128, generator=g).to(DEV)
+    W = (torch.randn(64, 128, 128, generator=g) * 0.02).to(DEV)
+    Wf, Wb = torch.ops.fsctep.gram_prepare_weights(W)
+    m = torch.jit.script(_GramProbe())
+    t1 = t.clone().requires_grad_(True)
+    t2 = t.clone().requires_grad_(True)
+    y1 = m(t1, Wf, Wb)
+    y2 = torch.ops.fsctep.gram_bilinear(t2, Wf, Wb, 0.25)
+    (g1,) = torch.autograd.grad(y1.square().sum(), t1)
+    (g2,) = torch.autograd.grad(y2.square().sum(), t2)
+    assert torch.equal(y1, y2) and torch.equal(g1, g2)

@@ -1,0 +1,80 @@
+"""The op boundary for TorchScript / LibTorch: every ``torch.ops.fsctep.*`` op is registered in C++
+by ``libfsctep_torch.so`` with device, Meta and autograd kernels; scripted graphs call the ops by
+name; and a C++ process with no Python loads the library (as the LAMMPS engine loads
+MFF_CUSTOM_OPS_LIB, lammps_user_mfftorch/src/USER-MFFTORCH/mff_torch_engine.cpp:226-249) and runs a
+scripted module that calls them.  No GPU is needed: these run on Meta tensors."""
+
+import os
+import subprocess
+
+import pytest
+import torch
+
+from conftest import ROOT
+from fsctep_amd import _lib
+
+OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table", "sparse_conv1",
+       "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv", "ictd_conv_backward", "ictd_conv1",
+       "ictd_conv1_backward", "gram_prepare_weights", "gram_bilinear", "gram_bilinear_backward"]
+
+
+class GramProbe(torch.nn.Module):
+    def forward(self, t: torch.Tensor, Wf: torch.Tensor, Wb: torch.Tensor) -> torch.Tensor:
+        return torch.ops.fsctep.gram_bilinear(t, Wf, Wb, 0.5)
+
+
+def test_schemas_registered_in_cpp():
+    _lib.load_torch_ops()
+    for name in OPS:
+        op = getattr(torch.ops.fsctep, name)
+        schema = op.default._schema
+        assert schema.name == f"fsctep::{name}"
+        # registered by the C++ library, not by Python
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "CUDA")
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "Meta")
+    for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear"):
+        assert torch._C._dispatch_has_computed_kernel_for_dispatch_key(f"fsctep::{name}", "AutogradCUDA")
+
+
+def test_scripted_graph_calls_ops_by_name():
+    _lib.load_torch_ops()
+    m = torch.jit.script(GramProbe())
+    assert "fsctep::gram_bilinear" in str(m.graph)
+
+
+def test_ictd_layout_tensor_round_trips():
+    from fsctep_amd import ictd_basis as B, ictd_ops
+    lid = ictd_ops.register_layout(B.layout_full(3))
+    t = ictd_ops.layout_tensor(lid)
+    s = ictd_ops.layout_struct(lid)
+    assert t.dtype == torch.int32 and t.device.type == "cpu" and t.numel() * 4 == ctypes_sizeof(s)
+    assert int(t[0]) == s.M and int(t[2]) == s.KT
+    with torch._subclasses.fake_tensor.FakeTensorMode(allow_non_fake_inputs=True):   # the layout is a constant
+        x = torch.empty(10, s.M, 128)
+        out = torch.ops.fsctep.ictd_conv1(torch.empty(40, s.NY), torch.empty(40, s.NREF), torch.empty(64, s.NP1, 128),
+                                          torch.empty(11, dtype=torch.int32), torch.empty(40, dtype=torch.int32),
+                                          torch.empty(10, dtype=torch.int32), 10, 8, s.M, t)
+        assert out.shape == x.shape
+
+
+def ctypes_sizeof(s):
+    import ctypes
+    return ctypes.sizeof(s)
+
+
+def test_python_free_process_loads_ops_and_runs_scripted_module(tmp_path):
+    _lib.load_torch_ops()
+    pt = tmp_path / "gram_probe.pt"
+    torch.jit.script(GramProbe()).save(str(pt))
+    base = os.path.dirname(torch.__file__)
+    inc, lib = os.path.join(base, "include"), os.path.join(base, "lib")
+    exe = tmp_path / "load_ops"
+    cmd = ["g++", "-std=c++17", "-O1", "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", inc,
+           "-I", os.path.join(inc, "torch", "csrc", "api", "include"), os.path.join(ROOT, "tests", "cpp", "load_ops.cpp"),
+           "-o", str(exe), "-L", lib, "-ltorch", "-ltorch_cpu", "-lc10", f"-Wl,-rpath,{lib}", "-ldl"]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-3000:]
+    env = {k: v for k, v in os.environ.items() if not k.startswith("PYTHON")}
+    run = subprocess.run([str(exe), _lib.TORCH_LIB_PATH, str(pt)], capture_output=True, text=True, timeout=300, env=env)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "fsctep ops registered: 14; scripted module -> [7, 64]" in run.stdout
