@@ -199,8 +199,11 @@ def conv1(A, vec, src, dst, n_nodes, p, cfg: SparseConfig):
     return scatter_sum(msg, dst, n_nodes) / cnt.unsqueeze(-1)
 
 
-def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig):
-    """pure_cartesian_sparse_layers.py:382-421: x1 = f[src], x2 = [1, n, n(x)n] with C2=1, / (E/N)."""
+def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig, avg_degree: float | None = None):
+    """pure_cartesian_sparse_layers.py:382-421: x1 = f[src], x2 = [1, n, n(x)n] with C2=1, / (E/N).
+
+    ``avg_degree`` replaces E/N, so that a cluster cut out of a larger system is normalised like
+    its parent system (the normalisation is the only non-local term of the trunk)."""
     lmax, E = cfg.lmax, vec.shape[0]
     e = rank_powers(vec, lmax)
     eb = {(0, 0): e[0].view(E, 1), (1, 0): torch.zeros(E, 1, dtype=vec.dtype)}
@@ -213,7 +216,7 @@ def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig):
     w = radial_mlp(emb, p, f"e3_conv_layers.{layer}.fc")
     msg = sparse_tp(f[src], x2, w, cfg.channels, 1, cfg.channels, lmax)
     out = scatter_sum(msg, dst, n_nodes)
-    avg = msg.new_tensor(E / max(n_nodes, 1)).clamp_min(1e-8)
+    avg = msg.new_tensor(E / max(n_nodes, 1) if avg_degree is None else avg_degree).clamp_min(1e-8)
     return out / avg
 
 
@@ -271,7 +274,8 @@ def readout(features: list, p, cfg: SparseConfig):
 
 # ----------------------------------------------------------------------------- trunk
 
-def atom_energies(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseConfig):
+def atom_energies(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseConfig,
+                  avg_degree: float | None = None):
     """(N, 1) atomic energies of the sparse trunk (pure_cartesian_sparse_layers.py:723-855)."""
     dtype = p["weighted_sum.weights"].dtype
     pos, cell, shifts = pos.to(dtype), cell.to(dtype), shifts.to(dtype)
@@ -281,7 +285,7 @@ def atom_energies(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseCon
     N = pos.shape[0]
     feats = [conv1(A, vec, src, dst, N, p, cfg)]
     for layer in range(1, cfg.num_interaction):
-        feats.append(conv2(feats[-1], vec, src, dst, N, p, layer, cfg))
+        feats.append(conv2(feats[-1], vec, src, dst, N, p, layer, cfg, avg_degree))
     return readout(feats, p, cfg)
 
 
