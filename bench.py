@@ -49,25 +49,25 @@ def sparse_kernel_work(name: str, N: int, E: int, C: int) -> dict:
     s_bytes = 4 * N * 18 * 65 * C            # node expansion S (or dS)
     p_bytes = 4 * E * 18 * C                 # edge messages P
     if name == "edge_message_grad":
-        flops = 2 * (2 * E * 18 * C * K) + E * 18 * C
-        byts = s_bytes + s_bytes + 4 * E * K * 2 + 4 * N * 13 * C + 4 * E * 3 + 4 * E * 2
+        # dh and dS products; the fused direction gradient reads P slots 1, 2, 6, 7, 8 and writes dn
+        flops = 2 * (2 * E * 18 * C * K) + E * 18 * C + 2 * E * 30 * C
+        byts = (s_bytes + s_bytes + 4 * E * K * 2 + 4 * N * 13 * C + 4 * E * 3 * 2 + 4 * E * 5 * C
+                + 4 * E * 2)
         return dict(flops=flops, bytes=byts, bound="mfma")
     if name == "edge_message":
         flops = 2 * E * 18 * C * K
         byts = s_bytes + p_bytes + 4 * E * K + 4 * E
         return dict(flops=flops, bytes=byts, bound="hbm")
-    if name == "node_expand":   # per launch = one path; report the 6-launch average
-        flops = 2 * N * 18 * 65 * C * C / 6
-        byts = (s_bytes + 4 * N * 13 * C) / 6
+    if name == "node_expand":
+        flops = 2 * N * 18 * 65 * C * C
+        byts = s_bytes + 4 * N * 13 * C
         return dict(flops=flops, bytes=byts, bound="mfma")
-    if name == "node_expand_grad":   # 3 launches (source-rank groups)
-        flops = 2 * N * 18 * 65 * C * C / 3
-        byts = (s_bytes + 4 * N * 13 * C) / 3
+    if name == "node_expand_grad":
+        flops = 2 * N * 18 * 65 * C * C
+        byts = s_bytes + 4 * 2 * 18 * N * C
         return dict(flops=flops, bytes=byts, bound="mfma")
     if name == "receiver_sum":
         return dict(flops=2 * E * 34 * C, bytes=p_bytes + 12 * E + 4 * N * 13 * C, bound="hbm")
-    if name == "direction_grad":
-        return dict(flops=2 * E * 30 * C, bytes=4 * E * 5 * C + 24 * E + 4 * N * 13 * C, bound="hbm")
     raise KeyError(name)
 
 

@@ -63,126 +63,238 @@ __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __
 }
 
 // ---------------------------------------------------------------- K1: node expansion
-// S[m][slot_base(p)+I][col] = sum_a x[m][comp0+I][a] * bk1[p][col][a]
-// grid: (ceil(rows/64), ceil(65C/256)), block 256 (4 waves, one 16-row tile each,
-// 16 column tiles of 16 per block).
+// S[m][sbase(p)+I][col] = sum_a x[m][comp0(p)+I][a] * bk1[p][col][a].  A block takes 128 rows
+// (m, I) of one path (4 waves x 32 rows; blocks numbered path by path, `off` = first block of
+// each path) and a group of 80-column tiles.  The rows of x stay in registers; each column
+// tile of bk1 (80 x C) is staged in LDS, the next one loaded while the current one is
+// multiplied.  Transposed product: bk1 rows are the MFMA A operand and x rows the B operand,
+// and tile j's A row i is column 20*(i/4) + 4*j + i%4, so lane (r, q) ends with columns
+// [20q, 20q+20) of row r: five float4 stores per row.
+struct PathTiles {
+  int off[7];
+};
+constexpr int NE_ROWS = 128;   // rows per node_expand block
+constexpr int NE_TPB = 13;     // 80-column tiles per node_expand block
+
 template <int C>
-__global__ __launch_bounds__(256) void node_expand_kernel(const float* __restrict__ x,
-                                                          const float* __restrict__ bk1,
-                                                          float* __restrict__ S, int64_t n_nodes,
-                                                          int p) {
+__global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ bk1,
+                                                             float* __restrict__ S, int64_t n_nodes,
+                                                             PathTiles tiles) {
+  constexpr int COLS = 65 * C, NT = 5, WCOLS = 16 * NT, KT = C / 16, RW = C / 4 + 1;
+  constexpr int NTC = COLS / WCOLS;                  // column tiles (52 or 26)
+  constexpr int NCG = (NTC + NE_TPB - 1) / NE_TPB;   // column groups
+  constexpr int RT = NE_ROWS / 64;                   // 16-row tiles per wave
+  __shared__ f4 sb[2][WCOLS][RW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
+  const int bt = blockIdx.x / NCG, cg = blockIdx.x % NCG;
+  int p = 0;
+  while (p < 5 && bt >= tiles.off[p + 1]) ++p;
   const int L1 = kPathL1[p];
   const int nI = (L1 == 0) ? 1 : (L1 == 1 ? 3 : 9);
   const int comp0 = (L1 == 0) ? 0 : (L1 == 1 ? 1 : 4);
   const int sbase = kSlotBase[p];
   const int64_t rows = n_nodes * nI;
-  const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16;
-  constexpr int COLS = 65 * C;
-  constexpr int KT = C / 16;
-
-  // A fragments: row (row0 + r), K = a
-  f4 a4[KT];
-  {
-    const int64_t row = row0 + r;
-    if (row < rows) {
-      const int64_t m = row / nI;
-      const int I = (int)(row % nI);
-      const float* xr = x + (m * NCOMP + comp0 + I) * C;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) a4[t] = ld4(xr + 16 * t + 4 * q);
-    } else {
-#pragma unroll
-      for (int t = 0; t < KT; ++t) a4[t] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
+  const int64_t row0 = (int64_t)(bt - tiles.off[p]) * NE_ROWS + wave * (16 * RT);
   const float* bp = bk1 + (int64_t)p * COLS * C;
-  const int col_base = blockIdx.y * 256;
-#pragma unroll 1
-  for (int ct = 0; ct < 16; ++ct) {
-    const int colt = col_base + ct * 16;
-    if (colt >= COLS) break;
-    const int col = colt + r;
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int ct0 = cg * NE_TPB, ct1 = min(NTC, ct0 + NE_TPB);
+  f4 xb[RT][KT];
+  int64_t obase[RT];
+  bool ok[RT];
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      const f4 b4 = ld4(bp + (int64_t)col * C + 16 * t + 4 * q);
-      acc = mfma_k16(a4[t], b4, acc);
+  for (int rt = 0; rt < RT; ++rt) {
+    int64_t row = row0 + 16 * rt + r;
+    ok[rt] = row < rows;
+    if (!ok[rt]) row = 0;   // a valid row; its result is not stored
+    const int64_t m = (uint32_t)row / (uint32_t)nI;
+    const int I = (int)(row - m * nI);
+    const float* xr = x + (m * NCOMP + comp0 + I) * C + 4 * q;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) xb[rt][t] = ld4(xr + 16 * t);
+    obase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 20 * q;
+  }
+  constexpr int NSTG = (WCOLS * (C / 4) + 255) / 256;
+  f4 stg[NSTG];
+  auto gload = [&](int ct) {
+#pragma unroll
+    for (int i = 0; i < NSTG; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      if (idx < WCOLS * (C / 4))
+        stg[i] = ld4(bp + (int64_t)(ct * WCOLS + idx / (C / 4)) * C + 4 * (idx % (C / 4)));
     }
+  };
+  auto sstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + 4 * q + i;
-      if (row < rows) {
-        const int64_t m = row / nI;
-        const int I = (int)(row % nI);
-        S[m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + col] = acc[i];
+    for (int i = 0; i < NSTG; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      if (idx < WCOLS * (C / 4)) sb[buf][idx / (C / 4)][idx % (C / 4)] = stg[i];
+    }
+  };
+  gload(ct0);
+  sstore(0);
+  __syncthreads();
+  for (int ct = ct0; ct < ct1; ++ct) {
+    const int buf = (ct - ct0) & 1;
+    if (ct + 1 < ct1) gload(ct + 1);
+    f4 acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[rt][j] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const f4 a4 = sb[buf][20 * (r >> 2) + 4 * j + (r & 3)][4 * t + q];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_k16(a4, xb[rt][t], acc[rt][j]);
+      }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (ok[rt]) {
+        float* o = S + obase[rt] + ct * WCOLS;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) st4(o + 4 * j, acc[rt][j]);
       }
     }
+    if (ct + 1 < ct1) sstore(buf ^ 1);
+    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------- K6: node expansion grad
-// dx[m][comp0+I][a] = sum_{p in group} sum_col dS[m][slot_base(p)+I][col] * bk6[p][a][col]
-// grid: ceil(rows/64), block 256 (4 waves x 16 rows), C/16 column tiles per wave.
+// dxp[kh][slot][m][a] = sum_{col in half kh} dS[m][slot][col] * bk6[p][a][col] for every slot
+// row (m, I) of path p, then dx[m][comp][a] = sum over the halves and the slots of comp
+// (node_expand_grad_combine).  A wave's work unit is (path, 64-row tile, K half): all units
+// are equally long, which keeps the waves balanced although paths 0-2 share component 0.
+// Transposed product: bk6 rows (a) are the A operand, dS rows the B operand; tile at's A row
+// i is a = (C/4)*(i/4) + 4*at + i%4, so lane (r, q) ends with C/4 consecutive a of one row.
+// K runs in chunks of 32 (lane group q reads 8 consecutive floats of both operands); chunk
+// t+1 is loaded while chunk t is multiplied.
 template <int C>
-__global__ __launch_bounds__(256) void node_expand_grad_kernel(const float* __restrict__ dS,
-                                                               const float* __restrict__ bk6,
-                                                               float* __restrict__ dx,
-                                                               int64_t n_nodes, int group) {
+__global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
+                                                                  const float* __restrict__ bk6,
+                                                                  float* __restrict__ dxp,
+                                                                  int64_t n_nodes, PathTiles tiles) {
+  constexpr int COLS = 65 * C;
+  constexpr int NA = C / 16;     // output a tiles
+  constexpr int QW = C / 4;      // consecutive a per lane in the output
+  constexpr int TPP = COLS / 32; // K chunks per path
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int nI = (group == 0) ? 1 : (group == 1 ? 3 : 9);
-  const int comp0 = (group == 0) ? 0 : (group == 1 ? 1 : 4);
-  const int p_first = (group == 0) ? 0 : (group == 1 ? 3 : 5);
-  const int p_count = (group == 0) ? 3 : (group == 1 ? 2 : 1);
+  const int wu = blockIdx.x * 4 + wave;
+  if (wu >= 2 * tiles.off[6]) return;   // whole wave
+  const int kh = wu & 1, wt = wu >> 1;
+  int p = 0;
+  while (p < 5 && wt >= tiles.off[p + 1]) ++p;
+  const int L1 = kPathL1[p];
+  const int nI = (L1 == 0) ? 1 : (L1 == 1 ? 3 : 9);
+  const int sbase = kSlotBase[p];
   const int64_t rows = n_nodes * nI;
-  const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16;
-  constexpr int COLS = 65 * C;
-  constexpr int NT = C / 16;
+  const int64_t row0 = (int64_t)(wt - tiles.off[p]) * 64;
 
-  const int64_t arow = row0 + r;
-  const bool arow_ok = arow < rows;
-  const int64_t am = arow_ok ? arow / nI : 0;
-  const int aI = arow_ok ? (int)(arow % nI) : 0;
-
-  f4 acc[NT];
+  bool ok[4];
+  int64_t rbase[4], mrow[4];
+  int irow[4];
 #pragma unroll
-  for (int ct = 0; ct < NT; ++ct) acc[ct] = f4{0.f, 0.f, 0.f, 0.f};
-
-  for (int pp = 0; pp < p_count; ++pp) {
-    const int p = p_first + pp;
-    const float* ar = dS + am * s_node_stride(C) + (int64_t)(kSlotBase[p] + aI) * COLS;
-    const float* bp = bk6 + (int64_t)p * C * COLS;
-#pragma unroll 2
-    for (int t = 0; t < COLS / 16; ++t) {
-      const f4 a4 = arow_ok ? ld4(ar + 16 * t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
+  for (int rt = 0; rt < 4; ++rt) {
+    int64_t row = row0 + 16 * rt + r;
+    ok[rt] = row < rows;
+    if (!ok[rt]) row = row0;   // a valid row; its result is not stored
+    const int64_t m = (uint32_t)row / (uint32_t)nI;
+    const int I = (int)(row - m * nI);
+    mrow[rt] = m;
+    irow[rt] = I;
+    rbase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 8 * q;
+  }
+  int64_t abase[NA];
 #pragma unroll
-      for (int ct = 0; ct < NT; ++ct) {
-        const f4 b4 = ld4(bp + (int64_t)(16 * ct + r) * COLS + 16 * t + 4 * q);
-        acc[ct] = mfma_k16(a4, b4, acc[ct]);
-      }
+  for (int at = 0; at < NA; ++at)
+    abase[at] = ((int64_t)p * C + QW * (r >> 2) + 4 * at + (r & 3)) * COLS + 8 * q;
+  f4 acc[4][NA];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int at = 0; at < NA; ++at) acc[rt][at] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int tb = kh ? TPP / 2 : 0, te = kh ? TPP : TPP / 2;
+  f4 b0[4][2], a0[NA][2], b1[4][2], a1[NA][2];
+  auto load = [&](f4 (&b)[4][2], f4 (&a)[NA][2], int t) {
+    const int64_t k0 = 32 * (int64_t)t;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) b[rt][u] = ld4(dS + rbase[rt] + k0 + 4 * u);
+#pragma unroll
+    for (int at = 0; at < NA; ++at)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) a[at][u] = ld4(bk6 + abase[at] + k0 + 4 * u);
+  };
+  auto mul = [&](const f4 (&b)[4][2], const f4 (&a)[NA][2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int at = 0; at < NA; ++at) acc[rt][at] = mfma_k16(a[at][u], b[rt][u], acc[rt][at]);
+  };
+  load(b0, a0, tb);
+#pragma unroll 1
+  for (int t = tb; t < te; t += 2) {
+    if (t + 1 < te) load(b1, a1, t + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mul(b0, a0);
+    if (t + 1 < te) {
+      if (t + 2 < te) load(b0, a0, t + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mul(b1, a1);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + 4 * q + i;
-    if (row < rows) {
-      const int64_t m = row / nI;
-      const int I = (int)(row % nI);
-      float* o = dx + (m * NCOMP + comp0 + I) * C;
+  for (int rt = 0; rt < 4; ++rt) {
+    if (!ok[rt]) continue;
+    float* o = dxp + (((int64_t)kh * NSLOT + sbase + irow[rt]) * n_nodes + mrow[rt]) * C + QW * q;
 #pragma unroll
-      for (int ct = 0; ct < NT; ++ct) o[16 * ct + r] = acc[ct][i];
-    }
+    for (int at = 0; at < NA; ++at) st4(o + 4 * at, acc[rt][at]);
   }
 }
 
+// dx[m][comp][a] = sum over the two K halves and the slots of comp: comp 0 <- slots 0,1,2;
+// comp 1+i <- slots 3+i, 6+i; comp 4+ij <- slot 9+ij.
+template <int C>
+__global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, float* __restrict__ dx,
+                                                int64_t n_nodes) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // over N*13*C/4
+  if (idx >= n_nodes * NCOMP * (C / 4)) return;
+  const int a4 = (int)(idx % (C / 4));
+  const int comp = (int)((idx / (C / 4)) % NCOMP);
+  const int64_t m = idx / (NCOMP * (C / 4));
+  int sl[3];
+  int ns;
+  if (comp == 0) {
+    sl[0] = 0; sl[1] = 1; sl[2] = 2; ns = 3;
+  } else if (comp < 4) {
+    sl[0] = 2 + comp; sl[1] = 5 + comp; sl[2] = 0; ns = 2;
+  } else {
+    sl[0] = 5 + comp; sl[1] = 0; sl[2] = 0; ns = 1;
+  }
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int kh = 0; kh < 2; ++kh)
+    for (int i = 0; i < ns; ++i) s += ld4(dxp + (((int64_t)kh * NSLOT + sl[i]) * n_nodes + m) * C + 4 * a4);
+  st4(dx + (m * NCOMP + comp) * C + 4 * a4, s);
+}
+
 // ---------------------------------------------------------------- K2: edge message
-// One block per source node; P[eid][col] = sum_k h[eid][k] S[m][col][k] + Sb[m][col].
+// One block (3 waves) per source node; P[eid][col] = sum_k h[eid][k] S[m][col][k] + Sb[m][col].
+// Transposed product: S rows (columns of P) are the A operand, the node's edges (h rows,
+// staged in LDS) the B operand.  A wave takes 32-column blocks; tile jt's A row i is column
+// 8*(i/4) + 4*jt + i%4 of the block, so lane (r, q) ends with 8 consecutive columns of
+// edge r: two float4 stores.
 constexpr int EP = 64;   // edges per pass held in LDS
 
 template <int C>
-__global__ __launch_bounds__(256) void edge_message_kernel(const float* __restrict__ h,
+__global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __restrict__ h,
                                                            const float* __restrict__ S,
                                                            const int32_t* __restrict__ src_ptr,
                                                            const int32_t* __restrict__ src_perm,
@@ -194,41 +306,86 @@ __global__ __launch_bounds__(256) void edge_message_kernel(const float* __restri
   const int r = lane & 15, q = lane >> 4;
   const int beg = src_ptr[m], end = src_ptr[m + 1];
   constexpr int COLS = 65 * C;
-  constexpr int NCT = NSLOT * C / 16;   // 16-wide column tiles of P
+  constexpr int NCOL = NSLOT * C;
+  constexpr int NJ = 2;              // 16-column tiles per column block
+  constexpr int BW = 16 * NJ;        // column block width
+  constexpr int NCB = NCOL / BW;
   const float* Sm = S + (int64_t)m * s_node_stride(C);
+
+  // a[jt][0..3]: S row of A row r of tile jt (K = 64); a[jt][4]: the biases of the lane's four
+  // output columns of tile jt.  Column block cb+3 is loaded while block cb is multiplied.
+  f4 a0[NJ][5], a1[NJ][5];
+  auto load = [&](f4 (&a)[NJ][5], int cb) {
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) {
+      const int col = cb * BW + 4 * NJ * (r >> 2) + 4 * jt + (r & 3);
+      const float* srow = Sm + (int64_t)(col / C) * COLS + (col % C) * KH + 4 * q;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[jt][t] = ld4(srow + 16 * t);
+      const int colq = cb * BW + 4 * NJ * q + 4 * jt;
+      a[jt][4] = ld4(Sm + (int64_t)(colq / C) * COLS + 64 * C + (colq % C));
+    }
+  };
 
   for (int pb = beg; pb < end; pb += EP) {
     const int cnt = min(EP, end - pb);
+    if (wave < NCB) load(a0, wave);   // independent of the staging below
     __syncthreads();
-    for (int idx = threadIdx.x; idx < EP * (KH / 4); idx += 256) {
-      const int e = idx / (KH / 4), k4 = (idx % (KH / 4)) * 4;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (e < cnt) v = ld4(h + (int64_t)src_perm[pb + e] * KH + k4);
-      *reinterpret_cast<f4*>(&hs[e][k4]) = v;
+    if (threadIdx.x < EP) eids[threadIdx.x] = src_perm[pb + min((int)threadIdx.x, cnt - 1)];
+    __syncthreads();
+    {
+      // rows e >= cnt repeat edge cnt-1 (their results are not stored)
+      constexpr int NV = (EP * KH / 4 + 191) / 192;
+      f4 v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = threadIdx.x + 192 * i;
+        if (idx < EP * (KH / 4)) v[i] = ld4(h + (int64_t)eids[idx / (KH / 4)] * KH + (idx % (KH / 4)) * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = threadIdx.x + 192 * i;
+        if (idx < EP * (KH / 4)) *reinterpret_cast<f4*>(&hs[idx / (KH / 4)][(idx % (KH / 4)) * 4]) = v[i];
+      }
     }
-    if (threadIdx.x < EP) eids[threadIdx.x] = (threadIdx.x < cnt) ? src_perm[pb + threadIdx.x] : -1;
     __syncthreads();
     const int nrt = (cnt + 15) / 16;
-    for (int ct = wave; ct < NCT; ct += 4) {
-      const int col = ct * 16 + r;        // flat (slot, c)
-      const int slot = col / C, c = col % C;
-      const float* srow = Sm + (int64_t)slot * COLS + c * KH;
-      f4 b4[4];
+    auto run = [&](const f4 (&a)[NJ][5], int cb) {
+      f4 acc[4][NJ];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) b4[t] = ld4(srow + 16 * t + 4 * q);
-      const float bias = Sm[(int64_t)slot * COLS + 64 * C + c];
-      for (int rt = 0; rt < nrt; ++rt) {
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int et = 0; et < 4; ++et)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f4 a4 = *reinterpret_cast<const f4*>(&hs[rt * 16 + r][16 * t + 4 * q]);
-          acc = mfma_k16(a4, b4[t], acc);
+        for (int jt = 0; jt < NJ; ++jt) acc[et][jt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int et = 0; et < 4; ++et) {
+        if (et < nrt) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const f4 b4 = *reinterpret_cast<const f4*>(&hs[16 * et + r][16 * t + 4 * q]);
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) acc[et][jt] = mfma_k16(a[jt][t], b4, acc[et][jt]);
+          }
         }
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = rt * 16 + 4 * q + i;
-          if (e < cnt) P[(int64_t)eids[e] * (NSLOT * C) + col] = acc[i] + bias;
+      for (int et = 0; et < 4; ++et) {
+        const int e = 16 * et + r;
+        if (et < nrt && e < cnt) {
+          float* o = P + (int64_t)eids[e] * NCOL + cb * BW + 4 * NJ * q;
+#pragma unroll
+          for (int jt = 0; jt < NJ; ++jt) st4(o + 4 * jt, acc[et][jt] + a[jt][4]);
         }
+      }
+    };
+#pragma unroll 1
+    for (int cb = wave; cb < NCB; cb += 6) {
+      if (cb + 3 < NCB) load(a1, cb + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      run(a0, cb);
+      if (cb + 3 < NCB) {
+        if (cb + 6 < NCB) load(a0, cb + 6);
+        __builtin_amdgcn_sched_barrier(0);
+        run(a1, cb + 3);
       }
     }
   }
@@ -279,211 +436,228 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
   }
 }
 
-// ---------------------------------------------------------------- K4: direction gradient
-// dn[e][k] = sum_c g1[k] P1 + P2 (sum_j g2[k][j] n_j + sum_i g2[i][k] n_i) + sum_i g2[i][k] P4[i]
-template <int C>
-__global__ __launch_bounds__(256) void direction_grad_kernel(const float* __restrict__ G,
-                                                             const float* __restrict__ P,
-                                                             const float* __restrict__ nvec,
-                                                             const int32_t* __restrict__ dst_ptr,
-                                                             float scale, float* __restrict__ dn,
-                                                             int64_t n_nodes) {
-  const int lane = threadIdx.x & 63;
-  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= n_nodes) return;
-  constexpr int EPW = 64 / C;
-  const int c = lane % C, sub = lane / C;
-  float g[NCOMP];
-#pragma unroll
-  for (int i = 0; i < NCOMP; ++i) g[i] = G[(n * NCOMP + i) * C + c] * scale;
-  const int beg = dst_ptr[n], end = dst_ptr[n + 1];
-  for (int eb = beg; eb < end; eb += EPW) {
-    const int e = eb + sub;
-    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
-    if (e < end) {
-      const float* pr = P + (int64_t)e * (NSLOT * C) + c;
-      const float nn[3] = {nvec[3 * (int64_t)e], nvec[3 * (int64_t)e + 1], nvec[3 * (int64_t)e + 2]};
-      const float p1 = pr[C], p2 = pr[2 * C];
-      const float p4[3] = {pr[6 * C], pr[7 * C], pr[8 * C]};
-      float t[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        float row = 0.f, colv = 0.f, p4t = 0.f;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          row += g[4 + 3 * k + j] * nn[j];
-          colv += g[4 + 3 * j + k] * nn[j];
-          p4t += g[4 + 3 * j + k] * p4[j];
-        }
-        t[k] = g[1 + k] * p1 + p2 * (row + colv) + p4t;
-      }
-      t0 = t[0]; t1 = t[1]; t2 = t[2];
-    }
-    t0 = group_sum(t0, C);
-    t1 = group_sum(t1, C);
-    t2 = group_sum(t2, C);
-    if (c == 0 && e < end) {
-      dn[3 * (int64_t)e] = t0;
-      dn[3 * (int64_t)e + 1] = t1;
-      dn[3 * (int64_t)e + 2] = t2;
-    }
-  }
-}
-
 // ---------------------------------------------------------------- K5: edge message grad
-// One block per source node.  dP_e[(slot,c)] is rebuilt from the receiver gradient
-// g = G[dst(e)]*scale and n_e, 64 columns at a time in LDS, then
-//   dh[e][k]       += sum_col dP_e[col] S[m][col][k]     (MFMA, rows = edges)
-//   dS[m][col][k]   = sum_e h[e][k] dP_e[col]            (MFMA, rows = columns)
-//   dS[m][col][64C] = sum_e dP_e[col]                    (bias column)
+// One block per source node.  With g = G[dst(e)] * scale, the message gradient is
+//   dP_e[0] = g0, dP_e[1] = g1.n, dP_e[2] = n.g2.n, dP_e[3+i] = g1[i],
+//   dP_e[6+i] = (g2 n)[i], dP_e[9+ij] = g2[ij]
+// (per channel).  Per chunk of CC channels the block writes dP for its edges into LDS, then
+//   dh[e][k]            += sum_{slot,c} dP_e[slot][c] S[m][slot][c][k]    (MFMA, rows = edges)
+//   dS[m][slot][c][k]    = sum_e dP_e[slot][c] h[e][k]                    (MFMA, rows = k)
+//   dS[m][slot][64C + c] = sum_e dP_e[slot][c]                            (bias column)
+// and the direction gradient of the receiver assembly (m1 = P1 n + P3, m2 = P2 n n + P4 n + P5)
+//   dn_e[k] = sum_c g1[k] P1 + P2 ((g2 n)[k] + (g2^T n)[k]) + (g2^T P4)[k]
+// is summed over the chunk's channels by lane shuffles and over chunks in a fixed order.
 template <int C>
-__device__ __forceinline__ float dp_value(const float* __restrict__ g, int slot, const float* nn) {
-  // g points at G[dst][0][c]; component stride C.
-  switch (slot) {
-    case 0: return g[0];
-    case 1: return g[1 * C] * nn[0] + g[2 * C] * nn[1] + g[3 * C] * nn[2];
-    case 2: {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 3; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) s += g[(4 + 3 * i + j) * C] * nn[i] * nn[j];
-      return s;
-    }
-    case 3: case 4: case 5: return g[(1 + slot - 3) * C];
-    case 6: case 7: case 8: {
-      const int i = slot - 6;
-      return g[(4 + 3 * i) * C] * nn[0] + g[(5 + 3 * i) * C] * nn[1] + g[(6 + 3 * i) * C] * nn[2];
-    }
-    default: return g[(4 + slot - 9) * C];
-  }
-}
-
-template <int C>
-__global__ __launch_bounds__(256) void edge_message_grad_kernel(
+__global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
     const float* __restrict__ G, const float* __restrict__ nvec, const float* __restrict__ h,
-    const float* __restrict__ S, const int32_t* __restrict__ src_ptr,
+    const float* __restrict__ S, const float* __restrict__ P, const int32_t* __restrict__ src_ptr,
     const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst, float scale,
-    float* __restrict__ dh, float* __restrict__ dS) {
+    float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn) {
+  constexpr int CC = 8;              // channels per chunk
+  constexpr int NCH = C / CC;
+  constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
+  constexpr int NCT = DW / 16;       // 16-wide column tiles per chunk
+  constexpr int COLS = 65 * C;
+  constexpr int NCOL = NSLOT * C;
   __shared__ float hs[EP][KH + 4];
-  __shared__ float dps[EP][64 + 4];
-  __shared__ float ss[64][KH + 4];
+  __shared__ float dps[EP][DW + 4];
   __shared__ int32_t eids[EP];
   __shared__ int32_t dsts[EP];
   __shared__ float ns[EP][3];
+  __shared__ float dnacc[EP][3];
   const int m = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int beg = src_ptr[m], end = src_ptr[m + 1];
-  constexpr int COLS = 65 * C;
-  constexpr int NCOL = NSLOT * C;
   const float* Sm = S + (int64_t)m * s_node_stride(C);
   float* dSm = dS + (int64_t)m * s_node_stride(C);
+  const int cl = threadIdx.x & (CC - 1);   // dP builder: channel within the chunk
+  const int eb = threadIdx.x / CC;         // dP builder: edges eb, eb + 32
 
+  if (end == beg) {   // no out-edges: dS of this node is zero (block-uniform branch)
+    for (int idx = threadIdx.x; idx < NSLOT * COLS / 4; idx += 256) st4(dSm + 4 * idx, f4{0.f, 0.f, 0.f, 0.f});
+    return;
+  }
   int pb = beg;
   bool first = true;
   do {
-    const int cnt = min(EP, end - pb);   // may be 0 for a node without out-edges
+    const int cnt = min(EP, end - pb);   // >= 1
     __syncthreads();
-    for (int idx = threadIdx.x; idx < EP * (KH / 4); idx += 256) {
-      const int e = idx / (KH / 4), k4 = (idx % (KH / 4)) * 4;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (e < cnt) v = ld4(h + (int64_t)src_perm[pb + e] * KH + k4);
-      *reinterpret_cast<f4*>(&hs[e][k4]) = v;
-    }
+    // Rows e >= cnt point at edge cnt-1, so every load below stays unconditional; their
+    // direction and h rows are zero and their dP is masked to zero.
     if (threadIdx.x < EP) {
       const int e = threadIdx.x;
-      const int32_t id = (e < cnt) ? src_perm[pb + e] : -1;
+      const int32_t id = src_perm[pb + min(e, cnt - 1)];
       eids[e] = id;
-      dsts[e] = (e < cnt) ? edge_dst[id] : 0;
-      ns[e][0] = (e < cnt) ? nvec[3 * (int64_t)id] : 0.f;
-      ns[e][1] = (e < cnt) ? nvec[3 * (int64_t)id + 1] : 0.f;
-      ns[e][2] = (e < cnt) ? nvec[3 * (int64_t)id + 2] : 0.f;
+      dsts[e] = edge_dst[id];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float v = nvec[3 * (int64_t)id + k];
+        ns[e][k] = (e < cnt) ? v : 0.f;
+        dnacc[e][k] = 0.f;
+      }
+    }
+    __syncthreads();
+    {
+      constexpr int NV = EP * (KH / 4) / 256;
+      f4 v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        v[i] = ld4(h + (int64_t)eids[idx / (KH / 4)] * KH + (idx % (KH / 4)) * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        const int e = idx / (KH / 4);
+        *reinterpret_cast<f4*>(&hs[e][(idx % (KH / 4)) * 4]) = (e < cnt) ? v[i] : f4{0.f, 0.f, 0.f, 0.f};
+      }
     }
     const int nrt = (cnt + 15) / 16;
-    f4 dacc[EP / 16];
+    const int ksteps = (cnt + 3) / 4;
+    f4 dacc[4];
 #pragma unroll
-    for (int i = 0; i < EP / 16; ++i) dacc[i] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int et = 0; et < 4; ++et) dacc[et] = f4{0.f, 0.f, 0.f, 0.f};
 
-    for (int cb = 0; cb < NCOL; cb += 64) {
+    // Receiver gradients (and P) for the next chunk's dP are loaded while the current chunk is
+    // multiplied; the S values of a chunk's dh product are loaded before its dP is built.
+    float gN[2][NCOMP], pN[2][5], sv[NCT][4];
+    auto load_g = [&](int ch) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int e = eb + 32 * hh;
+        const float* gp = G + (int64_t)dsts[e] * NCOMP * C + ch * CC + cl;
+#pragma unroll
+        for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * C];
+        const float* pp = P + (int64_t)eids[e] * NCOL + ch * CC + cl;
+        pN[hh][0] = pp[C];
+        pN[hh][1] = pp[2 * C];
+        pN[hh][2] = pp[6 * C];
+        pN[hh][3] = pp[7 * C];
+        pN[hh][4] = pp[8 * C];
+      }
+    };
+    auto load_s = [&](int ch) {
+#pragma unroll
+      for (int tt = 0; tt < NCT; ++tt)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const int kk = 16 * tt + 4 * q + s4;
+          sv[tt][s4] = Sm[(int64_t)(kk / CC) * COLS + (ch * CC + kk % CC) * KH + 16 * wave + r];
+        }
+    };
+    load_g(0);
+#pragma unroll 1
+    for (int ch = 0; ch < NCH; ++ch) {
+      const int c0 = ch * CC;
+      load_s(ch);
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- dP for edges eb, eb+32 and channel c0+cl; direction-gradient partials
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int e = eb + 32 * hh;
+        float v[NSLOT];
+        float t[3];
+        float g[NCOMP];
+        const float sc = (e < cnt) ? scale : 0.f;
+#pragma unroll
+        for (int i = 0; i < NCOMP; ++i) g[i] = gN[hh][i] * sc;
+        const float nn[3] = {ns[e][0], ns[e][1], ns[e][2]};
+        const float p1 = pN[hh][0], p2 = pN[hh][1];
+        const float p4[3] = {pN[hh][2], pN[hh][3], pN[hh][4]};
+        v[0] = g[0];
+        v[1] = g[1] * nn[0] + g[2] * nn[1] + g[3] * nn[2];
+        float nqn = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          float row = 0.f, colv = 0.f, p4t = 0.f;
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            row += g[4 + 3 * i + j] * nn[j];
+            colv += g[4 + 3 * j + i] * nn[j];
+            p4t += g[4 + 3 * j + i] * p4[j];
+          }
+          v[3 + i] = g[1 + i];
+          v[6 + i] = row;
+          nqn += row * nn[i];
+          t[i] = g[1 + i] * p1 + p2 * (row + colv) + p4t;
+        }
+        v[2] = nqn;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) v[9 + i] = g[4 + i];
+        // rows e >= cnt hold zeros (g is masked)
+#pragma unroll
+        for (int s4 = 0; s4 < NSLOT; ++s4) dps[e][s4 * CC + cl] = v[s4];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) t[k] = group_sum(t[k], CC);
+        if (cl == 0 && e < cnt) {
+#pragma unroll
+          for (int k = 0; k < 3; ++k) dnacc[e][k] += t[k];
+        }
+      }
       __syncthreads();
-      // dP tile (zero rows beyond cnt) and the S chunk for these 64 columns.
-      for (int idx = threadIdx.x; idx < EP * 64; idx += 256) {
-        const int e = idx >> 6, cl = idx & 63;
-        float v = 0.f;
-        if (e < cnt) {
-          const int col = cb + cl;
-          const int slot = col / C, c = col % C;
-          const float* gp = G + (int64_t)dsts[e] * NCOMP * C + c;
-          v = dp_value<C>(gp, slot, ns[e]) * scale;
-        }
-        dps[e][cl] = v;
-      }
-      for (int idx = threadIdx.x; idx < 64 * (KH / 4); idx += 256) {
-        const int cl = idx / (KH / 4), k4 = (idx % (KH / 4)) * 4;
-        const int col = cb + cl;
-        const int slot = col / C, c = col % C;
-        *reinterpret_cast<f4*>(&ss[cl][k4]) = ld4(Sm + (int64_t)slot * COLS + c * KH + k4);
-      }
-      __syncthreads();
-      // dh: rows = edges (tile rt), cols = k in [16*wave, 16*wave+16), K = 64 columns.
-      for (int rt = 0; rt < nrt; ++rt) {
+      if (ch + 1 < NCH) load_g(ch + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- dh: rows = edges (tile et), columns = k in [16*wave, 16*wave+16), K = chunk columns
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f4 a4 = *reinterpret_cast<const f4*>(&dps[rt * 16 + r][16 * t + 4 * q]);
-          f4 b4;
-          b4.x = ss[16 * t + 4 * q + 0][16 * wave + r];
-          b4.y = ss[16 * t + 4 * q + 1][16 * wave + r];
-          b4.z = ss[16 * t + 4 * q + 2][16 * wave + r];
-          b4.w = ss[16 * t + 4 * q + 3][16 * wave + r];
-          dacc[rt] = mfma_k16(a4, b4, dacc[rt]);
+      for (int tt = 0; tt < NCT; ++tt) {
+        const f4 b4 = {sv[tt][0], sv[tt][1], sv[tt][2], sv[tt][3]};
+#pragma unroll
+        for (int et = 0; et < 4; ++et) {
+          if (et < nrt) {
+            const f4 a4 = *reinterpret_cast<const f4*>(&dps[16 * et + r][16 * tt + 4 * q]);
+            dacc[et] = mfma_k16(a4, b4, dacc[et]);
+          }
         }
       }
-      // dS: rows = columns cb+16*wave+.., output col tile ct covers k = 4*r + ct, K = edges.
-      f4 sacc[4];
+      // ---- dS^T: rows = k in [16*wave, 16*wave+16), columns = chunk columns, K = edges
+      f4 sacc[NCT];
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) sacc[ct] = f4{0.f, 0.f, 0.f, 0.f};
-      for (int t = 0; t < nrt; ++t) {
-        f4 a4;
-        a4.x = dps[16 * t + 4 * q + 0][16 * wave + r];
-        a4.y = dps[16 * t + 4 * q + 1][16 * wave + r];
-        a4.z = dps[16 * t + 4 * q + 2][16 * wave + r];
-        a4.w = dps[16 * t + 4 * q + 3][16 * wave + r];
-        f4 hv[4];
+      for (int ct = 0; ct < NCT; ++ct) sacc[ct] = f4{0.f, 0.f, 0.f, 0.f};
+      // edges are taken in pairs of K steps; rows up to 64 are zero beyond cnt
+      for (int u = 0; u < ksteps; u += 2) {
+        const float a0 = hs[4 * u + q][16 * wave + r];
+        const float a1 = hs[4 * u + 4 + q][16 * wave + r];
+        float b0[NCT], b1[NCT];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) hv[j] = *reinterpret_cast<const f4*>(&hs[16 * t + 4 * q + j][4 * r]);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const f4 b4 = {hv[0][ct], hv[1][ct], hv[2][ct], hv[3][ct]};
-          sacc[ct] = mfma_k16(a4, b4, sacc[ct]);
+        for (int ct = 0; ct < NCT; ++ct) {
+          b0[ct] = dps[4 * u + q][16 * ct + r];
+          b1[ct] = dps[4 * u + 4 + q][16 * ct + r];
         }
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(a0, b0[ct], sacc[ct]);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(a1, b1[ct], sacc[ct]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int col = cb + 16 * wave + 4 * q + i;
-        const int slot = col / C, c = col % C;
-        float* o = dSm + (int64_t)slot * COLS + c * KH + 4 * r;
-        f4 v = {sacc[0][i], sacc[1][i], sacc[2][i], sacc[3][i]};
+      for (int ct = 0; ct < NCT; ++ct) {
+        const int col = 16 * ct + r;
+        float* o = dSm + (int64_t)(col / CC) * COLS + (c0 + col % CC) * KH + 16 * wave + 4 * q;
+        f4 v = sacc[ct];
         if (!first) v += ld4(o);
         st4(o, v);
       }
-      if (threadIdx.x < 64) {
-        const int cl = threadIdx.x;
-        float s = 0.f;
-        for (int e = 0; e < cnt; ++e) s += dps[e][cl];
-        const int col = cb + cl;
-        const int slot = col / C, c = col % C;
-        float* o = dSm + (int64_t)slot * COLS + 64 * C + c;
-        *o = first ? s : (*o + s);
+      if (threadIdx.x < DW) {
+        const int col = threadIdx.x;
+        float sum = 0.f;
+        for (int e = 0; e < cnt; ++e) sum += dps[e][col];
+        float* o = dSm + (int64_t)(col / CC) * COLS + 64 * C + c0 + col % CC;
+        *o = first ? sum : (*o + sum);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int et = 0; et < 4; ++et) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 16 * et + 4 * q + j;
+        if (e < cnt) dh[(int64_t)eids[e] * KH + 16 * wave + r] = dacc[et][j];
       }
     }
-    // dh rows of this pass
-    for (int rt = 0; rt < nrt; ++rt) {
+    if (threadIdx.x < cnt) {
+      const int e = threadIdx.x;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = rt * 16 + 4 * q + i;
-        if (e < cnt) dh[(int64_t)eids[e] * KH + 16 * wave + r] = dacc[rt][i];
-      }
+      for (int k = 0; k < 3; ++k) dn[3 * (int64_t)eids[e] + k] = dnacc[e][k];
     }
     first = false;
     pb += EP;
@@ -648,16 +822,19 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
                       const float* bk1, float scale, float* S, float* P, float* out,
                       hipStream_t st) {
   if (N == 0) return 0;
-  for (int p = 0; p < 6; ++p) {
-    const int64_t rows = N * kNumI[kPathL1H[p]];
-    dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((65 * C + 255) / 256));
+  {
+    PathTiles tiles;
+    tiles.off[0] = 0;
+    for (int p = 0; p < 6; ++p)
+      tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + NE_ROWS - 1) / NE_ROWS);
+    constexpr int ncg = ((65 * C) / 80 + NE_TPB - 1) / NE_TPB;
     LaunchTimer tm("node_expand", st);
-    node_expand_kernel<C><<<grid, 256, 0, st>>>(x, bk1, S, N, p);
+    node_expand_kernel<C><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(x, bk1, S, N, tiles);
   }
   if (check_launch("sparse node_expand")) return 2;
   {
     LaunchTimer tm("edge_message", st);
-    edge_message_kernel<C><<<(unsigned)N, 256, 0, st>>>(h, S, src_ptr, src_perm, P);
+    edge_message_kernel<C><<<(unsigned)N, 192, 0, st>>>(h, S, src_ptr, src_perm, P);
   }
   if (check_launch("sparse edge_message")) return 2;
   {
@@ -675,20 +852,22 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        hipStream_t st) {
   if (N == 0) return 0;
   {
-    LaunchTimer tm("direction_grad", st);
-    direction_grad_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(G, P, nvec, dst_ptr, scale, dn, N);
-  }
-  if (check_launch("sparse direction_grad")) return 2;
-  {
     LaunchTimer tm("edge_message_grad", st);
-    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(G, nvec, h, S, src_ptr, src_perm,
-                                                             edge_dst, scale, dh, dS);
+    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(G, nvec, h, S, P, src_ptr, src_perm,
+                                                             edge_dst, scale, dh, dS, dn);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
-  for (int g = 0; g < 3; ++g) {
-    const int64_t rows = N * kNumI[g];
-    LaunchTimer tm("node_expand_grad", st);
-    node_expand_grad_kernel<C><<<(unsigned)((rows + 63) / 64), 256, 0, st>>>(dS, bk6, dx, N, g);
+  {
+    PathTiles tiles;
+    tiles.off[0] = 0;
+    for (int p = 0; p < 6; ++p) tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + 63) / 64);
+    float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums
+    {
+      LaunchTimer tm("node_expand_grad", st);
+      node_expand_grad_kernel<C><<<(unsigned)((2 * tiles.off[6] + 3) / 4), 256, 0, st>>>(dS, bk6, dxp, N, tiles);
+    }
+    if (check_launch("sparse node_expand_grad")) return 2;
+    node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N);
   }
   return check_launch("sparse node_expand_grad") ? 2 : 0;
 }
@@ -707,7 +886,8 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_workspace: negative size");
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_workspace: channels must be 32 or 64");
   FSC_CHECK_ARG(s_floats && p_floats, "fsc_sparse_conv_workspace: null output");
-  *s_floats = n_nodes * s_node_stride(channels);
+  // the tail (2 x 18 x N x C) holds the partial input gradients of the backward
+  *s_floats = n_nodes * s_node_stride(channels) + 2LL * NSLOT * n_nodes * channels;
   *p_floats = n_edges * (int64_t)NSLOT * channels;
   return 0;
 }

@@ -100,7 +100,9 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tenso
                                                     const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                                     const Tensor&, double) {
   const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
-  return {at::empty({N, 13, C}, fopts(x)), at::empty({N * 18 * 65 * C}, fopts(x)), at::empty({E * 18 * C}, fopts(x))};
+  int64_t s_f = 0, p_f = 0;
+  check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
+  return {at::empty({N, 13, C}, fopts(x)), at::empty({s_f}, fopts(x)), at::empty({p_f}, fopts(x))};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_, const Tensor& n_,
