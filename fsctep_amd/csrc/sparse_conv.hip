@@ -670,6 +670,11 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 // per species pair: M[pair][p][k'][c] = sum_{a,b} W[(p,c,a,b),k'] A_s[a] A_t[b]
 // for the three live paths p0 (0,0->0), p3 (1,0->1), p5 (2,0->2); k' = 64 is the bias.
 // Per edge Q_p[c] = sum_k' M[pair][p][k'][c] h'_e[k'];  m = [Q0, Q1 n, Q2 n n].
+// Tables: mf[pair][p][k'][c] (k' = 0..64) and mb[pair][p][c][k'] (rows padded to MB_STRIDE).
+// Q is a GEMM per species pair over the edges of that pair (16-edge tiles of the pair-sorted,
+// padded edge list `pair_tiles`); the receiver sum then reads Q in receiver order.
+constexpr int MB_STRIDE = 68;
+
 __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float* __restrict__ b,
                                         const float* __restrict__ atab, int n_species, int C,
                                         float* __restrict__ mf, float* __restrict__ mb) {
@@ -692,54 +697,81 @@ __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float
         acc += w * as * atab[t * 8 + bb];
       }
     }
-    mf[idx] = acc;                                                   // [pair][p3][k][c]
-    mb[(((int64_t)pair * 3 + p3) * C + c) * 65 + k] = acc;           // [pair][p3][c][k]
+    mf[idx] = acc;                                                       // [pair][p3][k][c]
+    mb[(((int64_t)pair * 3 + p3) * C + c) * MB_STRIDE + k] = acc;        // [pair][p3][c][k]
+    if (k == 64) {
+#pragma unroll
+      for (int z = 65; z < MB_STRIDE; ++z) mb[(((int64_t)pair * 3 + p3) * C + c) * MB_STRIDE + z] = 0.f;
+    }
   }
 }
 
+// Q[e][p*C + c] = sum_k h[e][k] mb[pair][p][c][k] + mf[pair][p][64][c] for one 16-edge tile of
+// one species pair per wave.  pair_tiles = [16*n_tiles padded edge ids (-1: none) | n_tiles
+// pair ids]; a tile's first entry is always an edge.  Transposed product: table rows (p, c)
+// are the A operand and the tile's h rows the B operand, so lane (r, q) ends with four
+// consecutive (p, c) columns of edge r.
 template <int C>
-__global__ __launch_bounds__(256) void conv1_forward_kernel(const float* __restrict__ h,
-                                                            const float* __restrict__ nvec,
-                                                            const int32_t* __restrict__ edge_pair,
-                                                            const float* __restrict__ mf,
-                                                            const int32_t* __restrict__ dst_ptr,
-                                                            float* __restrict__ Q,
-                                                            float* __restrict__ out,
-                                                            int64_t n_nodes) {
+__global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __restrict__ h,
+                                                              const float* __restrict__ mf,
+                                                              const float* __restrict__ mb,
+                                                              const int32_t* __restrict__ pair_tiles,
+                                                              int n_tiles, float* __restrict__ Q) {
+  constexpr int NRT = 3 * C / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= n_tiles) return;   // whole wave
+  const int32_t e = pair_tiles[16 * t + r];
+  const int32_t eld = (e >= 0) ? e : pair_tiles[16 * t];
+  const int pair = pair_tiles[16 * n_tiles + t];
+  f4 hb[4];
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4) hb[t4] = ld4(h + (int64_t)eld * KH + 16 * t4 + 4 * q);
+  const float* mp = mb + (int64_t)pair * 3 * C * MB_STRIDE;
+  const float* fp = mf + (int64_t)pair * 3 * 65 * C;
+#pragma unroll 3
+  for (int rt = 0; rt < NRT; ++rt) {
+    f4 a[4];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) a[t4] = ld4(mp + (int64_t)(16 * rt + r) * MB_STRIDE + 16 * t4 + 4 * q);
+    const int row = 16 * rt + 4 * q;   // first of the lane's four (p, c) outputs
+    const f4 bias = ld4(fp + (row / C) * 65 * C + 64 * C + row % C);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) acc = mfma_k16(a[t4], hb[t4], acc);
+    if (e >= 0) st4(Q + (int64_t)e * 3 * C + row, acc + bias);
+  }
+}
+
+// out[n] = (1/max(indeg,1)) sum_{e->n} [Q0, Q1 n, Q2 n n]; one wave per receiver, lane = channel.
+template <int C>
+__global__ __launch_bounds__(256) void conv1_receiver_kernel(const float* __restrict__ Q,
+                                                             const float* __restrict__ nvec,
+                                                             const int32_t* __restrict__ dst_ptr,
+                                                             float* __restrict__ out, int64_t n_nodes) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= n_nodes) return;
-  const int c = lane;
-  const bool act = lane < C;
+  const int c = lane & (C - 1);
   float o[NCOMP];
 #pragma unroll
   for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg; e < end; ++e) {
-    const float* M = mf + (int64_t)edge_pair[e] * 3 * 65 * C + (act ? c : 0);
-    const float* he = h + (int64_t)e * KH;
-    float q0 = M[64 * C], q1 = M[65 * C + 64 * C], q2 = M[2 * 65 * C + 64 * C];
-#pragma unroll 8
-    for (int k = 0; k < KH; ++k) {
-      const float hk = he[k];
-      q0 += M[k * C] * hk;
-      q1 += M[65 * C + k * C] * hk;
-      q2 += M[2 * 65 * C + k * C] * hk;
-    }
+    const float* qr = Q + (int64_t)e * 3 * C + c;
+    const float q0 = qr[0], q1 = qr[C], q2 = qr[2 * C];
     const float nn[3] = {nvec[3 * (int64_t)e], nvec[3 * (int64_t)e + 1], nvec[3 * (int64_t)e + 2]};
-    if (act) {
-      float* qr = Q + (int64_t)e * 3 * C + c;
-      qr[0] = q0; qr[C] = q1; qr[2 * C] = q2;
-      o[0] += q0;
+    o[0] += q0;
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        o[1 + i] += q1 * nn[i];
+    for (int i = 0; i < 3; ++i) {
+      o[1 + i] += q1 * nn[i];
+      const float q2n = q2 * nn[i];
 #pragma unroll
-        for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += q2 * nn[i] * nn[j];
-      }
+      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += q2n * nn[j];
     }
   }
-  if (act) {
+  if (lane < C) {
     const float scale = 1.f / (float)max(end - beg, 1);
     float* orow = out + n * NCOMP * C + c;
 #pragma unroll
@@ -747,21 +779,19 @@ __global__ __launch_bounds__(256) void conv1_forward_kernel(const float* __restr
   }
 }
 
+// Receiver side of the backward: dQ[e] = (g0, g1.n, n.g2.n) with g = G[n]/max(indeg,1), and
+// dn_e[k] = sum_c g1[k] Q1 + Q2 ((g2 n)[k] + (g2^T n)[k]).  One wave per receiver, lane = channel.
 template <int C>
-__global__ __launch_bounds__(256) void conv1_backward_kernel(const float* __restrict__ G,
-                                                             const float* __restrict__ nvec,
-                                                             const int32_t* __restrict__ edge_pair,
-                                                             const float* __restrict__ mb,
-                                                             const float* __restrict__ Q,
-                                                             const int32_t* __restrict__ dst_ptr,
-                                                             float* __restrict__ dh,
-                                                             float* __restrict__ dn,
-                                                             int64_t n_nodes) {
-  __shared__ float dq[4][3][C];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t n = (int64_t)blockIdx.x * 4 + wave;
-  if (n >= n_nodes) return;   // whole wave exits together; no block-level barrier below
-  const int c = lane;
+__global__ __launch_bounds__(256) void conv1_receiver_grad_kernel(const float* __restrict__ G,
+                                                                  const float* __restrict__ nvec,
+                                                                  const float* __restrict__ Q,
+                                                                  const int32_t* __restrict__ dst_ptr,
+                                                                  float* __restrict__ dQ,
+                                                                  float* __restrict__ dn, int64_t n_nodes) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= n_nodes) return;   // whole wave
+  const int c = lane & (C - 1);
   const bool act = lane < C;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const float scale = 1.f / (float)max(end - beg, 1);
@@ -770,30 +800,26 @@ __global__ __launch_bounds__(256) void conv1_backward_kernel(const float* __rest
   for (int i = 0; i < NCOMP; ++i) g[i] = act ? G[(n * NCOMP + i) * C + c] * scale : 0.f;
   for (int e = beg; e < end; ++e) {
     const float nn[3] = {nvec[3 * (int64_t)e], nvec[3 * (int64_t)e + 1], nvec[3 * (int64_t)e + 2]};
-    float t[3] = {0.f, 0.f, 0.f};
+    const float* qr = Q + (int64_t)e * 3 * C + c;
+    const float q1 = qr[C], q2 = qr[2 * C];
+    float d1 = 0.f, d2 = 0.f, t[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float row = 0.f, colv = 0.f;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        row += g[4 + 3 * k + j] * nn[j];
+        colv += g[4 + 3 * j + k] * nn[j];
+      }
+      d1 += g[1 + k] * nn[k];
+      d2 += row * nn[k];
+      t[k] = act ? g[1 + k] * q1 + q2 * (row + colv) : 0.f;
+    }
     if (act) {
-      const float* qr = Q + (int64_t)e * 3 * C + c;
-      const float q1 = qr[C], q2 = qr[2 * C];
-      float d1 = 0.f, d2 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        d1 += g[1 + i] * nn[i];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) d2 += g[4 + 3 * i + j] * nn[i] * nn[j];
-      }
-      dq[wave][0][c] = g[0];
-      dq[wave][1][c] = d1;
-      dq[wave][2][c] = d2;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        float row = 0.f, colv = 0.f;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          row += g[4 + 3 * k + j] * nn[j];
-          colv += g[4 + 3 * j + k] * nn[j];
-        }
-        t[k] = g[1 + k] * q1 + q2 * (row + colv);
-      }
+      float* dq = dQ + (int64_t)e * 3 * C + c;
+      dq[0] = g[0];
+      dq[C] = d1;
+      dq[2 * C] = d2;
     }
     const float t0 = wave_sum(t[0]), t1 = wave_sum(t[1]), t2 = wave_sum(t[2]);
     if (lane == 0) {
@@ -801,17 +827,40 @@ __global__ __launch_bounds__(256) void conv1_backward_kernel(const float* __rest
       dn[3 * (int64_t)e + 1] = t1;
       dn[3 * (int64_t)e + 2] = t2;
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    // dh[e][k] = sum_p sum_c dQ_p[c] M[pair][p][c][k], lane = k
-    const float* M = mb + (int64_t)edge_pair[e] * 3 * C * 65 + lane;
-    float acc = 0.f;
-    for (int p = 0; p < 3; ++p)
-#pragma unroll 8
-      for (int cc = 0; cc < C; ++cc) acc += dq[wave][p][cc] * M[(p * C + cc) * 65];
-    dh[(int64_t)e * KH + lane] = acc;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  }
+}
+
+// dh[e][k] = sum_{p,c} dQ[e][p][c] mf[pair][p][k][c] for one 16-edge tile of one pair per
+// wave; transposed product (table rows k are the A operand), lane (r, q) ends with four
+// consecutive k of edge r per k tile.
+template <int C>
+__global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* __restrict__ dQ,
+                                                                   const float* __restrict__ mf,
+                                                                   const int32_t* __restrict__ pair_tiles,
+                                                                   int n_tiles, float* __restrict__ dh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= n_tiles) return;   // whole wave
+  const int32_t e = pair_tiles[16 * t + r];
+  const int32_t eld = (e >= 0) ? e : pair_tiles[16 * t];
+  const int pair = pair_tiles[16 * n_tiles + t];
+  const float* fp = mf + (int64_t)pair * 3 * 65 * C;
+  const float* dq = dQ + (int64_t)eld * 3 * C + 4 * q;
+  f4 acc[4] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll 3
+  for (int kc = 0; kc < 3 * C / 16; ++kc) {   // K chunk: path p = kc / (C/16), channels c0..c0+15
+    const int p = kc / (C / 16), c0 = 16 * (kc % (C / 16));
+    const f4 b = ld4(dq + p * C + c0);
+    f4 a[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) a[kt] = ld4(fp + (int64_t)(p * 65 + 16 * kt + r) * C + c0 + 4 * q);
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) acc[kt] = mfma_k16(a[kt], b, acc[kt]);
+  }
+  if (e >= 0) {
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) st4(dh + (int64_t)e * KH + 16 * kt + 4 * q, acc[kt]);
   }
 }
 
@@ -952,47 +1001,49 @@ int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const 
 }
 
 int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
-                             const int32_t* edge_pair, const float* h, const float* n, const float* mf,
-                             float* q_ws, float* out, hipStream_t stream) {
+                             int64_t n_tiles, const int32_t* pair_tiles, const float* h, const float* n,
+                             const float* mf, const float* mb, float* q_ws, float* out, hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_sparse_conv1_forward: bad size");
-  FSC_CHECK_ARG(dst_ptr && mf && out, "fsc_sparse_conv1_forward: null pointer");
-  FSC_CHECK_ARG(n_edges == 0 || (edge_pair && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
+  FSC_CHECK_ARG(n_tiles >= 0 && n_tiles < (1LL << 27) && n_tiles * 16 >= n_edges,
+                "fsc_sparse_conv1_forward: pair tiles do not cover the edges");
+  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_forward: channels must be 32 or 64");
+  FSC_CHECK_ARG(dst_ptr && mf && mb && out, "fsc_sparse_conv1_forward: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
   if (n_nodes == 0) return 0;
-  const unsigned grid = (unsigned)((n_nodes + 3) / 4);
   LaunchTimer tm("conv1_forward", stream);
-  if (channels == 64)
-    conv1_forward_kernel<64><<<grid, 256, 0, stream>>>(h, n, edge_pair, mf, dst_ptr, q_ws, out, n_nodes);
-  else if (channels == 32)
-    conv1_forward_kernel<32><<<grid, 256, 0, stream>>>(h, n, edge_pair, mf, dst_ptr, q_ws, out, n_nodes);
-  else {
-    set_error("fsc_sparse_conv1_forward: channels must be 32 or 64");
-    return 1;
+  const unsigned tgrid = (unsigned)((n_tiles + 3) / 4), ngrid = (unsigned)((n_nodes + 3) / 4);
+  if (channels == 64) {
+    if (n_tiles) conv1_pair_gemm_kernel<64><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
+    conv1_receiver_kernel<64><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
+  } else {
+    if (n_tiles) conv1_pair_gemm_kernel<32><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
+    conv1_receiver_kernel<32><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
   }
   return check_launch("sparse conv1_forward") ? 2 : 0;
 }
 
 int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
-                              const int32_t* edge_pair, const float* grad_out, const float* n,
-                              const float* mb, const float* q_ws, float* grad_h, float* grad_n,
+                              int64_t n_tiles, const int32_t* pair_tiles, const float* grad_out, const float* n,
+                              const float* mf, const float* q_ws, float* dq_ws, float* grad_h, float* grad_n,
                               hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_sparse_conv1_backward: bad size");
-  FSC_CHECK_ARG(dst_ptr && grad_out && mb, "fsc_sparse_conv1_backward: null pointer");
-  FSC_CHECK_ARG(n_edges == 0 || (edge_pair && n && q_ws && grad_h && grad_n),
+  FSC_CHECK_ARG(n_tiles >= 0 && n_tiles < (1LL << 27) && n_tiles * 16 >= n_edges,
+                "fsc_sparse_conv1_backward: pair tiles do not cover the edges");
+  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_backward: channels must be 32 or 64");
+  FSC_CHECK_ARG(dst_ptr && grad_out && mf, "fsc_sparse_conv1_backward: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && n && q_ws && dq_ws && grad_h && grad_n),
                 "fsc_sparse_conv1_backward: null edge pointer");
   if (n_nodes == 0) return 0;
-  const unsigned grid = (unsigned)((n_nodes + 3) / 4);
   LaunchTimer tm("conv1_backward", stream);
-  if (channels == 64)
-    conv1_backward_kernel<64><<<grid, 256, 0, stream>>>(grad_out, n, edge_pair, mb, q_ws, dst_ptr, grad_h,
-                                                        grad_n, n_nodes);
-  else if (channels == 32)
-    conv1_backward_kernel<32><<<grid, 256, 0, stream>>>(grad_out, n, edge_pair, mb, q_ws, dst_ptr, grad_h,
-                                                        grad_n, n_nodes);
-  else {
-    set_error("fsc_sparse_conv1_backward: channels must be 32 or 64");
-    return 1;
+  const unsigned tgrid = (unsigned)((n_tiles + 3) / 4), ngrid = (unsigned)((n_nodes + 3) / 4);
+  if (channels == 64) {
+    conv1_receiver_grad_kernel<64><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
+    if (n_tiles) conv1_pair_gemm_grad_kernel<64><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
+  } else {
+    conv1_receiver_grad_kernel<32><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
+    if (n_tiles) conv1_pair_gemm_grad_kernel<32><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
   }
   return check_launch("sparse conv1_backward") ? 2 : 0;
 }

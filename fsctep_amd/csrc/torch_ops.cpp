@@ -137,7 +137,7 @@ std::tuple<Tensor, Tensor> sparse_conv1_pair_table(const Tensor& w_last, const T
   TORCH_CHECK(atom_table.dim() == 2 && atom_table.size(1) == 8 && w_last.size(0) == 6 * C * 64 && w_last.size(1) == KH,
               "conv1 pair table needs output_size 8 and fc.4 of shape (6*C*64, 64)");
   Tensor w = f32c(w_last), b = f32c(b_last), a = f32c(atom_table);
-  Tensor mf_ = at::empty({NS * NS * 3 * 65 * C}, fopts(w)), mb = at::empty_like(mf_);
+  Tensor mf_ = at::empty({NS * NS * 3 * 65 * C}, fopts(w)), mb = at::empty({NS * NS * 3 * C * 68}, fopts(w));
   check(fsc_sparse_conv1_pair_table(cf(w), cf(b), cf(a), (int32_t)NS, (int32_t)C, mf(mf_), mf(mb), stream_of(w)),
         "fsc_sparse_conv1_pair_table");
   return {mf_, mb};
@@ -146,18 +146,20 @@ std::tuple<Tensor, Tensor> sparse_conv1_pair_table(const Tensor& w_last, const T
 std::tuple<Tensor, Tensor> sparse_conv1_pair_table_meta(const Tensor& w_last, const Tensor&, const Tensor& atom_table,
                                                         int64_t C) {
   const int64_t NS = atom_table.size(0);
-  return {at::empty({NS * NS * 3 * 65 * C}, fopts(w_last)), at::empty({NS * NS * 3 * 65 * C}, fopts(w_last))};
+  return {at::empty({NS * NS * 3 * 65 * C}, fopts(w_last)), at::empty({NS * NS * 3 * C * 68}, fopts(w_last))};
 }
 
 std::tuple<Tensor, Tensor> sparse_conv1(const Tensor& h_, const Tensor& n_, const Tensor& mf_, const Tensor& mb,
-                                        const Tensor& dst_ptr, const Tensor& edge_pair, int64_t n_nodes,
+                                        const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t n_nodes,
                                         int64_t channels) {
-  require_gpu({h_, n_, mf_, mb, dst_ptr, edge_pair});
+  require_gpu({h_, n_, mf_, mb, dst_ptr, pair_tiles});
   const int64_t E = h_.size(0), C = channels;
+  TORCH_CHECK(pair_tiles.numel() % 17 == 0, "pair_tiles must hold 17 int32 per 16-edge tile");
   Tensor h = f32c(h_), n = f32c(n_);
   Tensor Q = at::empty({E * 3 * C}, fopts(h)), out = at::empty({n_nodes, 13, C}, fopts(h));
-  check(fsc_sparse_conv1_forward(n_nodes, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")),
-                                 ci(i32c(edge_pair, "edge_pair")), cf(h), cf(n), cf(mf_), mf(Q), mf(out), stream_of(h)),
+  check(fsc_sparse_conv1_forward(n_nodes, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), pair_tiles.numel() / 17,
+                                 ci(i32c(pair_tiles, "pair_tiles")), cf(h), cf(n), cf(mf_), cf(mb), mf(Q), mf(out),
+                                 stream_of(h)),
         "fsc_sparse_conv1_forward");
   return {out, Q};
 }
@@ -167,14 +169,16 @@ std::tuple<Tensor, Tensor> sparse_conv1_meta(const Tensor& h, const Tensor&, con
   return {at::empty({n_nodes, 13, C}, fopts(h)), at::empty({h.size(0) * 3 * C}, fopts(h))};
 }
 
-std::tuple<Tensor, Tensor> sparse_conv1_backward(const Tensor& grad_out, const Tensor& n_, const Tensor& mb,
-                                                 const Tensor& Q, const Tensor& dst_ptr, const Tensor& edge_pair) {
-  require_gpu({grad_out, n_, mb, Q, dst_ptr, edge_pair});
+std::tuple<Tensor, Tensor> sparse_conv1_backward(const Tensor& grad_out, const Tensor& n_, const Tensor& mf_,
+                                                 const Tensor& Q, const Tensor& dst_ptr, const Tensor& pair_tiles) {
+  require_gpu({grad_out, n_, mf_, Q, dst_ptr, pair_tiles});
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = n_.size(0);
+  TORCH_CHECK(pair_tiles.numel() % 17 == 0, "pair_tiles must hold 17 int32 per 16-edge tile");
   Tensor g = f32c(grad_out), n = f32c(n_);
-  Tensor dh = at::empty({E, KH}, fopts(g)), dn = at::empty({E, 3}, fopts(g));
-  check(fsc_sparse_conv1_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_pair, "edge_pair")),
-                                  cf(g), cf(n), cf(mb), cf(Q), mf(dh), mf(dn), stream_of(g)),
+  Tensor dh = at::empty({E, KH}, fopts(g)), dn = at::empty({E, 3}, fopts(g)), dQ = at::empty({E * 3 * C}, fopts(g));
+  check(fsc_sparse_conv1_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), pair_tiles.numel() / 17,
+                                  ci(i32c(pair_tiles, "pair_tiles")), cf(g), cf(n), cf(mf_), cf(Q), mf(dQ), mf(dh),
+                                  mf(dn), stream_of(g)),
         "fsc_sparse_conv1_backward");
   return {dh, dn};
 }
@@ -389,13 +393,13 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const T
 
 struct SparseConv1Fn : public torch::autograd::Function<SparseConv1Fn> {
   static variable_list forward(AutogradContext* ctx, Tensor h, Tensor n, Tensor mf_, Tensor mb, Tensor dst_ptr,
-                               Tensor edge_pair, int64_t n_nodes, int64_t channels) {
+                               Tensor pair_tiles, int64_t n_nodes, int64_t channels) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                                           const Tensor&, const Tensor&, int64_t, int64_t)>(
         "fsctep::sparse_conv1");
-    auto [out, Q] = op.call(h, n, mf_, mb, dst_ptr, edge_pair, n_nodes, channels);
-    ctx->save_for_backward({n, mb, Q, dst_ptr, edge_pair});
+    auto [out, Q] = op.call(h, n, mf_, mb, dst_ptr, pair_tiles, n_nodes, channels);
+    ctx->save_for_backward({n, mf_, Q, dst_ptr, pair_tiles});
     ctx->mark_non_differentiable({Q});
     ctx->set_materialize_grads(false);
     return {out, Q};
@@ -415,9 +419,9 @@ struct SparseConv1Fn : public torch::autograd::Function<SparseConv1Fn> {
 };
 
 std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& n, const Tensor& mf_, const Tensor& mb,
-                                                 const Tensor& dst_ptr, const Tensor& edge_pair, int64_t n_nodes,
+                                                 const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t n_nodes,
                                                  int64_t channels) {
-  auto r = SparseConv1Fn::apply(h, n, mf_, mb, dst_ptr, edge_pair, n_nodes, channels);
+  auto r = SparseConv1Fn::apply(h, n, mf_, mb, dst_ptr, pair_tiles, n_nodes, channels);
   return {r[0], r[1]};
 }
 
@@ -526,9 +530,9 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
         "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, float inv_norm) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
-  m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor edge_pair, int n_nodes, "
+  m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, int n_nodes, "
         "int channels) -> (Tensor, Tensor)");
-  m.def("sparse_conv1_backward(Tensor grad_out, Tensor n, Tensor mb, Tensor Q, Tensor dst_ptr, Tensor edge_pair) "
+  m.def("sparse_conv1_backward(Tensor grad_out, Tensor n, Tensor mf, Tensor Q, Tensor dst_ptr, Tensor pair_tiles) "
         "-> (Tensor, Tensor)");
   m.def("ictd_prepare_weights(Tensor W) -> Tensor");
   m.def("ictd_conv(Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg, Tensor dst_ptr, "

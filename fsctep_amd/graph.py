@@ -28,6 +28,7 @@ class Graph:
     species_index: torch.Tensor | None = None   # (N,) int64 index into `species`
     species: torch.Tensor | None = None         # (S,) int64 distinct atomic numbers (sorted)
     edge_pair: torch.Tensor | None = None       # (E,) int32 species-pair index src*S+dst
+    pair_tiles: torch.Tensor | None = None      # (17*T,) int32: edge ids by pair in 16-tiles | tile pairs
     species_index32: torch.Tensor | None = None # (N,) int32
 
 
@@ -60,4 +61,26 @@ def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: t
         g.species_index32 = inv.to(torch.int32).contiguous()
         S = int(uniq.shape[0])
         g.edge_pair = (inv[src] * S + inv[dst]).to(torch.int32).contiguous()
+        g.pair_tiles = pair_tiles(g.edge_pair, S * S)
     return g
+
+
+def pair_tiles(edge_pair: torch.Tensor, n_pairs: int) -> torch.Tensor:
+    """Edge ids grouped by species pair, each group padded with -1 to a multiple of 16, followed by
+    the pair of each 16-entry tile: [16*T ids | T pairs] (int32).  The sparse conv1 runs one small
+    GEMM per tile with that pair's table."""
+    dev = edge_pair.device
+    E = int(edge_pair.shape[0])
+    pair = edge_pair.long()
+    counts = torch.bincount(pair, minlength=n_pairs) if E else torch.zeros(n_pairs, dtype=torch.long, device=dev)
+    tiles_per = (counts + 15) // 16
+    T = int(tiles_per.sum())
+    tile_start = torch.cumsum(tiles_per, 0) - tiles_per            # first tile of each pair
+    order = torch.argsort(pair, stable=True) if E else torch.zeros(0, dtype=torch.long, device=dev)
+    sorted_pair = pair[order]
+    first = torch.cumsum(counts, 0) - counts                        # first sorted position of each pair
+    pos = tile_start[sorted_pair] * 16 + (torch.arange(E, device=dev) - first[sorted_pair])
+    ids = torch.full((16 * T,), -1, dtype=torch.int32, device=dev)
+    ids[pos] = order.to(torch.int32)
+    tpair = torch.repeat_interleave(torch.arange(n_pairs, device=dev), tiles_per).to(torch.int32)
+    return torch.cat([ids, tpair]).contiguous()

@@ -10,8 +10,8 @@ produced (the path serves energy + forces).
     sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm) -> (out, S, P)
     sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm)
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
-    sparse_conv1(h, n, mf, mb, dst_ptr, edge_pair, n_nodes, channels) -> (out, Q)
-    sparse_conv1_backward(grad_out, n, mb, Q, dst_ptr, edge_pair) -> (dh, dn)
+    sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, n_nodes, channels) -> (out, Q)
+    sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
 """
 
 from __future__ import annotations
@@ -32,6 +32,6 @@ def sparse_conv_apply(x, h, n, bk1, bk6, graph, inv_norm: float):
 
 def sparse_conv1_apply(h, n, mf, mb, graph, channels: int):
     """Differentiable conv1 message passing from the species-pair tables: -> (N,13,C)."""
-    out, _ = torch.ops.fsctep.sparse_conv1(h, n, mf, mb, graph.dst_ptr, graph.edge_pair, graph.n_nodes,
+    out, _ = torch.ops.fsctep.sparse_conv1(h, n, mf, mb, graph.dst_ptr, graph.pair_tiles, graph.n_nodes,
                                            int(channels))
     return out

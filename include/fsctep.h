@@ -84,20 +84,23 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
  *
  * Pair table from fc.4 (6*C*64, 64)/(6*C*64) and the per-species atom features
  * atom_table [n_species][8] (= atom_mlp(atom_embedding(Z)), :258-259):
- * mf [n_species^2][3][65][C] and mb [n_species^2][3][C][65]; pair = s_src*n_species + s_dst. */
+ * mf [n_species^2][3][65][C] and mb [n_species^2][3][C][68] (k' = 0..64, rows zero-padded);
+ * pair = s_src*n_species + s_dst. */
 int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const float* atom_table,
                                 int32_t n_species, int32_t channels, float* mf, float* mb,
                                 hipStream_t stream);
 
-/* out[N][13][C] = (1/max(indeg,1)) sum_{e->n} message_e; q_ws: [E][3][C] kept for backward. */
+/* out[N][13][C] = (1/max(indeg,1)) sum_{e->n} message_e; q_ws: [E][3][C] kept for backward.
+ * pair_tiles: [16*n_tiles edge ids | n_tiles pair ids], the receiver-sorted edge ids grouped by
+ * species pair, each pair's list padded with -1 to a multiple of 16 (fsctep_amd/graph.py). */
 int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
-                             const int32_t* edge_pair, const float* h, const float* n, const float* mf,
-                             float* q_ws, float* out, hipStream_t stream);
+                             int64_t n_tiles, const int32_t* pair_tiles, const float* h, const float* n,
+                             const float* mf, const float* mb, float* q_ws, float* out, hipStream_t stream);
 
-/* grad_h [E][64], grad_n [E][3] from grad_out [N][13][C]. */
+/* grad_h [E][64], grad_n [E][3] from grad_out [N][13][C]; dq_ws: scratch of E*3*C floats. */
 int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
-                              const int32_t* edge_pair, const float* grad_out, const float* n,
-                              const float* mb, const float* q_ws, float* grad_h, float* grad_n,
+                              int64_t n_tiles, const int32_t* pair_tiles, const float* grad_out, const float* n,
+                              const float* mf, const float* q_ws, float* dq_ws, float* grad_h, float* grad_n,
                               hipStream_t stream);
 
 /* ------------------------------------------------------------------ ICTD (pure-cartesian-ictd / -o3)

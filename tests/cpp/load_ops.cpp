@@ -50,7 +50,7 @@ int main(int argc, char** argv) {
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, double)>();
   auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, 0.5);
-  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 || P.numel() != 30 * 18 * 64) {
+  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 || P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;
   }
