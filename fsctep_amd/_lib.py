@@ -37,6 +37,10 @@ SIGNATURES = {
     "fsc_gram_prepare_weights": [_p, _i32, _i32, _p, _p, _p],
     "fsc_gram_forward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
     "fsc_gram_backward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
+    "fsc_edge_geometry_forward": [_i64, _p, _p, _p, _p, _p, _p, _p],
+    "fsc_edge_geometry_backward": [_i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "fsc_radial_mlp_forward": [_i64, _p, _p, _p, _p, _p, _i32, _f32, _i32, _p, _p],
+    "fsc_radial_mlp_backward": [_i64, _p, _p, _p, _p, _p, _i32, _f32, _i32, _p, _p, _p],
 }
 
 _lib = None

@@ -1,0 +1,346 @@
+// Edge geometry and the radial MLP of every interaction layer, fused, with their backward.
+//
+// Replaces, per call of the reference trunks (models/pure_cartesian_sparse_layers.py:745-756,
+// 319-321, 410-412, 204-210, 372-378; models/pure_cartesian_ictd_layers_full.py:896-909,
+// 930-937, 277-283, 693-699; models/pure_cartesian_ictd_layers_o3.py:924-936, 953-955):
+//   vec = pos[dst] - pos[src] + shift,  r = |vec|,  n = vec / max(r, 1e-8)
+//   emb = soft_one_hot_linspace(r, 0, rc, nb, basis, cutoff=True) * sqrt(nb)      (e3nn form)
+//   h   = silu(W2 silu(W0 emb + b0) + b2)                                          (fc[:4])
+// and the force backward: dr from dh (activations recomputed), dvec from (dn, dr), and
+// dpos[m] = sum_{e: dst(e)=m} dvec_e - sum_{e: src(e)=m} dvec_e as two deterministic segmented
+// sums over the receiver CSR and the source grouping (no atomics).
+#include "common.h"
+
+namespace fsc {
+namespace radial {
+
+constexpr int HID = 64;     // hidden width of the radial MLP (fixed by the reference's fc)
+constexpr int NBMAX = 16;   // radial basis functions supported
+
+// emb_k(r) and d emb_k / dr for k < nb (basis 0: Bessel, 1: Gaussian), matching the device
+// formula used by the model code (bessel: sqrt(2/rc) sin(k pi r/rc)/r on (0, rc); gaussian:
+// exp(-((r - mu_k)/step)^2)/1.12 with mu_k = k*step, step = rc/(nb+1)), times sqrt(nb).
+__device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int basis, float& f, float& df) {
+  const float snb = sqrtf((float)nb);
+  if (basis == 0) {
+    const float w = (float)(k + 1) * (3.14159265358979323846f / rc);
+    const bool inside = (r / rc < 1.f) && (r > 0.f);
+    const float a = sqrtf(2.f / rc) * snb;
+    const float rr = inside ? r : 1.f;
+    const float x = w * rr, s = sinf(x), c = cosf(x);
+    // d/dr sin(wr)/r = w^2 (x cos x - sin x)/x^2; below x = 0.3 the Taylor series avoids the
+    // cancellation (-x/3 + x^3/30 - x^5/840, truncation below 1e-8 relative)
+    const float x2 = x * x;
+    const float g = (x < 0.3f) ? x * (-1.f / 3.f + x2 * (1.f / 30.f - x2 * (1.f / 840.f))) : (x * c - s) / x2;
+    f = inside ? a * s / rr : 0.f;
+    df = inside ? a * w * w * g : 0.f;
+  } else {
+    const float step = rc / (float)(nb + 1);
+    const float d = (r - (float)(k + 1) * step) / step;
+    const float e = expf(-d * d) / 1.12f * snb;
+    f = e;
+    df = e * (-2.f * d / step);
+  }
+}
+
+__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
+
+// One wave per 16-edge tile; lane (r, q) works for edge e0 + r.  The hidden units are laid
+// out as the MFMA output: lane (r, q) holds unit j = 16*jt + 4*q + i in register (jt, i), so
+// one layer's output is directly the next product's B operand (K index q <-> 16*jt + 4*q + i).
+// Weights are staged in LDS: W0 [64][NBMAX], W2 [64][65] (row padded), b0, b2.
+struct Smem {
+  float w0[HID][NBMAX];
+  float w2[HID][HID + 1];
+  float b0[HID];
+  float b2[HID];
+};
+
+__device__ void stage_weights(Smem& sm, const float* __restrict__ W0, const float* __restrict__ b0,
+                              const float* __restrict__ W2, const float* __restrict__ b2, int nb) {
+  for (int i = threadIdx.x; i < HID * NBMAX; i += blockDim.x) {
+    const int j = i / NBMAX, k = i % NBMAX;
+    sm.w0[j][k] = (k < nb) ? W0[j * nb + k] : 0.f;
+  }
+  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) sm.w2[i / HID][i % HID] = W2[i];
+  for (int i = threadIdx.x; i < HID; i += blockDim.x) {
+    sm.b0[i] = b0[i];
+    sm.b2[i] = b2[i];
+  }
+}
+
+// u0 = W0 emb + b0 and u2 = W2 silu(u0) + b2 for the lane's edge (MFMA layout above).
+__device__ __forceinline__ void mlp_forward(const Smem& sm, const float (&emb)[NBMAX], int nks, int r, int q,
+                                            f4 (&u0)[4], f4 (&u2)[4]) {
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nks; ++ks) acc = mfma16x16x4(sm.w0[16 * jt + r][4 * ks + q], emb[4 * ks + q], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += sm.b0[16 * jt + 4 * q + i];
+    u0[jt] = acc;
+  }
+  f4 a0[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a0[jt][i] = u0[jt][i] * sigm(u0[jt][i]);
+#pragma unroll
+  for (int ot = 0; ot < 4; ++ot) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = mfma16x16x4(sm.w2[16 * ot + r][16 * jt + 4 * q + i], a0[jt][i], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += sm.b2[16 * ot + 4 * q + i];
+    u2[ot] = acc;
+  }
+}
+
+__device__ __forceinline__ void edge_basis(float rr, int nb, float rc, int basis, float (&emb)[NBMAX],
+                                           float (&demb)[NBMAX]) {
+#pragma unroll
+  for (int k = 0; k < NBMAX; ++k) {
+    float f = 0.f, df = 0.f;
+    if (k < nb) basis_eval(rr, k, nb, rc, basis, f, df);
+    emb[k] = f;
+    demb[k] = df;
+  }
+}
+
+__global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
+                                                                 const float* __restrict__ b0, const float* __restrict__ W2,
+                                                                 const float* __restrict__ b2, int nb, float rc, int basis,
+                                                                 int64_t n_edges, float* __restrict__ h) {
+  __shared__ Smem sm;
+  stage_weights(sm, W0, b0, W2, b2, nb);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int nks = (nb + 3) / 4;
+  const int64_t ntiles = (n_edges + 15) / 16;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+    const int64_t e = 16 * t + r;
+    const float rr = (e < n_edges) ? rad[e] : 1.f;
+    float emb[NBMAX], demb[NBMAX];
+    edge_basis(rr, nb, rc, basis, emb, demb);
+    f4 u0[4], u2[4];
+    mlp_forward(sm, emb, nks, r, q, u0, u2);
+    if (e < n_edges) {
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot) {
+        f4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = u2[ot][i] * sigm(u2[ot][i]);
+        st4(h + e * HID + 16 * ot + 4 * q, v);
+      }
+    }
+  }
+}
+
+// dr[e] = sum_k d emb_k/dr * (W0^T (silu'(u0) * W2^T (silu'(u2) * dh)))_k
+__global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
+                                                                  const float* __restrict__ b0, const float* __restrict__ W2,
+                                                                  const float* __restrict__ b2, int nb, float rc, int basis,
+                                                                  int64_t n_edges, const float* __restrict__ dh,
+                                                                  float* __restrict__ dr) {
+  __shared__ Smem sm;
+  stage_weights(sm, W0, b0, W2, b2, nb);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int nks = (nb + 3) / 4;
+  const int64_t ntiles = (n_edges + 15) / 16;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+    const int64_t e = 16 * t + r;
+    const bool ok = e < n_edges;
+    const float rr = ok ? rad[e] : 1.f;
+    float emb[NBMAX], demb[NBMAX];
+    edge_basis(rr, nb, rc, basis, emb, demb);
+    f4 u0[4], u2[4];
+    mlp_forward(sm, emb, nks, r, q, u0, u2);
+    f4 g2[4];
+#pragma unroll
+    for (int ot = 0; ot < 4; ++ot) {
+      const f4 d = ok ? ld4(dh + e * HID + 16 * ot + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s = sigm(u2[ot][i]);
+        g2[ot][i] = d[i] * s * (1.f + u2[ot][i] * (1.f - s));
+      }
+    }
+    f4 g0[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = mfma16x16x4(sm.w2[16 * ot + 4 * q + i][16 * jt + r], g2[ot][i], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s = sigm(u0[jt][i]);
+        g0[jt][i] = acc[i] * s * (1.f + u0[jt][i] * (1.f - s));
+      }
+    }
+    // d emb[k] for k = 4q + i (rows k of one 16-row tile; k >= nb rows are zero)
+    f4 de = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) de = mfma16x16x4(sm.w0[16 * jt + 4 * q + i][r], g0[jt][i], de);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 4 * q + i;
+      float dd = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < NBMAX; ++kk)
+        if (kk == k) dd = demb[kk];
+      part += de[i] * dd;
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if (ok && q == 0) dr[e] = part;
+  }
+}
+
+// ---------------------------------------------------------------- geometry
+__global__ void geometry_forward_kernel(const float* __restrict__ pos, const float* __restrict__ shift,
+                                        const int32_t* __restrict__ src, const int32_t* __restrict__ dst,
+                                        int64_t n_edges, float* __restrict__ nvec, float* __restrict__ rad) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  const int64_t s = src[e], d = dst[e];
+  float v[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) v[k] = pos[3 * d + k] - pos[3 * s + k] + shift[3 * e + k];
+  const float r = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float inv = 1.f / fmaxf(r, 1e-8f);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) nvec[3 * e + k] = v[k] * inv;
+  rad[e] = r;
+}
+
+// dvec_e = dr_e n_e + (dn_e - (n_e . dn_e) n_e) / r_e  (for r_e > 1e-8; below it n = vec/1e-8)
+__device__ __forceinline__ void edge_dvec(const float* __restrict__ gn, const float* __restrict__ gr,
+                                          const float* __restrict__ nvec, const float* __restrict__ rad,
+                                          int64_t e, float (&dv)[3]) {
+  const float r = rad[e];
+  const float n0 = nvec[3 * e], n1 = nvec[3 * e + 1], n2 = nvec[3 * e + 2];
+  const float d0 = gn ? gn[3 * e] : 0.f, d1 = gn ? gn[3 * e + 1] : 0.f, d2 = gn ? gn[3 * e + 2] : 0.f;
+  const float dr = gr ? gr[e] : 0.f;
+  if (r > 1e-8f) {
+    const float dot = n0 * d0 + n1 * d1 + n2 * d2;
+    const float ir = 1.f / r;
+    dv[0] = dr * n0 + (d0 - dot * n0) * ir;
+    dv[1] = dr * n1 + (d1 - dot * n1) * ir;
+    dv[2] = dr * n2 + (d2 - dot * n2) * ir;
+  } else {
+    const float rr = fmaxf(r, 1e-30f);
+    dv[0] = dr * n0 * 1e-8f / rr + d0 * 1e8f;
+    dv[1] = dr * n1 * 1e-8f / rr + d1 * 1e8f;
+    dv[2] = dr * n2 * 1e-8f / rr + d2 * 1e8f;
+  }
+}
+
+// One wave per atom: its in-edges (receiver CSR) add dvec, its out-edges (source grouping) subtract.
+__global__ __launch_bounds__(256) void geometry_backward_kernel(const float* __restrict__ gn, const float* __restrict__ gr,
+                                                                const float* __restrict__ nvec,
+                                                                const float* __restrict__ rad,
+                                                                const int32_t* __restrict__ dst_ptr,
+                                                                const int32_t* __restrict__ src_ptr,
+                                                                const int32_t* __restrict__ src_perm,
+                                                                int64_t n_nodes, float* __restrict__ gpos) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= n_nodes) return;
+  float acc[3] = {0.f, 0.f, 0.f};
+  for (int e = dst_ptr[m] + lane; e < dst_ptr[m + 1]; e += 64) {
+    float dv[3];
+    edge_dvec(gn, gr, nvec, rad, e, dv);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) acc[k] += dv[k];
+  }
+  for (int j = src_ptr[m] + lane; j < src_ptr[m + 1]; j += 64) {
+    float dv[3];
+    edge_dvec(gn, gr, nvec, rad, src_perm[j], dv);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) acc[k] -= dv[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) acc[k] = wave_sum(acc[k]);
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) gpos[3 * m + k] = acc[k];
+  }
+}
+
+}  // namespace radial
+}  // namespace fsc
+
+using namespace fsc;
+using namespace fsc::radial;
+
+extern "C" {
+
+int fsc_edge_geometry_forward(int64_t n_edges, const float* pos, const float* shift, const int32_t* edge_src,
+                              const int32_t* edge_dst, float* n_out, float* r_out, hipStream_t stream) {
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_edge_geometry_forward: bad size");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(pos && shift && edge_src && edge_dst && n_out && r_out, "fsc_edge_geometry_forward: null pointer");
+  geometry_forward_kernel<<<(unsigned)((n_edges + 255) / 256), 256, 0, stream>>>(pos, shift, edge_src, edge_dst,
+                                                                                 n_edges, n_out, r_out);
+  return check_launch("edge geometry forward") ? 2 : 0;
+}
+
+int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* grad_n, const float* grad_r,
+                               const float* n, const float* r, const int32_t* dst_ptr, const int32_t* src_ptr,
+                               const int32_t* src_perm, float* grad_pos, hipStream_t stream) {
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+                "fsc_edge_geometry_backward: bad size");
+  if (n_nodes == 0) return 0;
+  FSC_CHECK_ARG(dst_ptr && src_ptr && grad_pos, "fsc_edge_geometry_backward: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (n && r && src_perm), "fsc_edge_geometry_backward: null edge pointer");
+  geometry_backward_kernel<<<(unsigned)((n_nodes + 3) / 4), 256, 0, stream>>>(grad_n, grad_r, n, r, dst_ptr,
+                                                                              src_ptr, src_perm, n_nodes, grad_pos);
+  return check_launch("edge geometry backward") ? 2 : 0;
+}
+
+static unsigned radial_grid(int64_t n_edges) {
+  const int64_t tiles = (n_edges + 15) / 16;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + 3) / 4, 2048));
+}
+
+int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
+                           const float* b2, int32_t n_basis, float r_cut, int32_t basis, float* h,
+                           hipStream_t stream) {
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_forward: bad size");
+  FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_forward: n_basis must be 1..16");
+  FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_forward: basis must be 0 (bessel) or 1 (gaussian)");
+  FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_forward: r_cut must be positive");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && h, "fsc_radial_mlp_forward: null pointer");
+  LaunchTimer tm("radial_mlp", stream);
+  radial_mlp_forward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, n_basis, r_cut, basis,
+                                                                     n_edges, h);
+  return check_launch("radial mlp forward") ? 2 : 0;
+}
+
+int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
+                            const float* b2, int32_t n_basis, float r_cut, int32_t basis, const float* grad_h,
+                            float* grad_r, hipStream_t stream) {
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_backward: bad size");
+  FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_backward: n_basis must be 1..16");
+  FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_backward: basis must be 0 (bessel) or 1 (gaussian)");
+  FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_backward: r_cut must be positive");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && grad_h && grad_r, "fsc_radial_mlp_backward: null pointer");
+  LaunchTimer tm("radial_mlp_grad", stream);
+  radial_mlp_backward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, n_basis, r_cut, basis,
+                                                                      n_edges, grad_h, grad_r);
+  return check_launch("radial mlp backward") ? 2 : 0;
+}
+
+}  // extern "C"

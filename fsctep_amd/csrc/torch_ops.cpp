@@ -340,6 +340,92 @@ Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&
 
 // ============================================================== autograd
 
+// ============================================================== edge geometry and radial MLP
+
+std::tuple<Tensor, Tensor> edge_geometry(const Tensor& pos_, const Tensor& shift_, const Tensor& edge_src,
+                                         const Tensor& edge_dst, const Tensor& dst_ptr, const Tensor& src_ptr,
+                                         const Tensor& src_perm) {
+  require_gpu({pos_, shift_, edge_src, edge_dst, dst_ptr, src_ptr, src_perm});
+  const int64_t E = edge_src.numel();
+  TORCH_CHECK(pos_.dim() == 2 && pos_.size(1) == 3 && shift_.numel() == 3 * E, "pos (N,3), shift (E,3)");
+  Tensor pos = f32c(pos_), shift = f32c(shift_);
+  Tensor n = at::empty({E, 3}, fopts(pos)), r = at::empty({E}, fopts(pos));
+  check(fsc_edge_geometry_forward(E, cf(pos), cf(shift), ci(i32c(edge_src, "edge_src")), ci(i32c(edge_dst, "edge_dst")),
+                                  mf(n), mf(r), stream_of(pos)),
+        "fsc_edge_geometry_forward");
+  return {n, r};
+}
+
+std::tuple<Tensor, Tensor> edge_geometry_meta(const Tensor& pos, const Tensor&, const Tensor& edge_src, const Tensor&,
+                                              const Tensor&, const Tensor&, const Tensor&) {
+  const int64_t E = edge_src.numel();
+  return {at::empty({E, 3}, fopts(pos)), at::empty({E}, fopts(pos))};
+}
+
+Tensor edge_geometry_backward(const std::optional<Tensor>& grad_n, const std::optional<Tensor>& grad_r,
+                              const Tensor& n_, const Tensor& r_, const Tensor& dst_ptr, const Tensor& src_ptr,
+                              const Tensor& src_perm) {
+  const bool has_n = grad_n.has_value() && grad_n->defined(), has_r = grad_r.has_value() && grad_r->defined();
+  require_gpu({n_, r_, dst_ptr, src_ptr, src_perm});
+  if (has_n) require_gpu({*grad_n});
+  if (has_r) require_gpu({*grad_r});
+  const int64_t N = dst_ptr.numel() - 1, E = r_.numel();
+  Tensor n = f32c(n_), r = f32c(r_);
+  Tensor gn = has_n ? f32c(*grad_n) : Tensor(), gr = has_r ? f32c(*grad_r) : Tensor();
+  Tensor gpos = at::empty({N, 3}, fopts(n));
+  check(fsc_edge_geometry_backward(N, E, gn.defined() ? cf(gn) : nullptr, gr.defined() ? cf(gr) : nullptr, cf(n),
+                                   cf(r), ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(src_ptr, "src_ptr")),
+                                   ci(i32c(src_perm, "src_perm")), mf(gpos), stream_of(n)),
+        "fsc_edge_geometry_backward");
+  return gpos;
+}
+
+Tensor edge_geometry_backward_meta(const std::optional<Tensor>&, const std::optional<Tensor>&, const Tensor& n,
+                                   const Tensor&, const Tensor& dst_ptr, const Tensor&, const Tensor&) {
+  return at::empty({dst_ptr.numel() - 1, 3}, fopts(n));
+}
+
+int32_t basis_code(int64_t basis) {
+  TORCH_CHECK(basis == 0 || basis == 1, "radial basis: 0 (bessel) or 1 (gaussian)");
+  return (int32_t)basis;
+}
+
+Tensor radial_mlp(const Tensor& r_, const Tensor& w0_, const Tensor& b0_, const Tensor& w2_, const Tensor& b2_,
+                  double r_cut, int64_t basis) {
+  require_gpu({r_, w0_, b0_, w2_, b2_});
+  TORCH_CHECK(w0_.dim() == 2 && w0_.size(0) == KH && w2_.dim() == 2 && w2_.size(0) == KH && w2_.size(1) == KH &&
+                  b0_.numel() == KH && b2_.numel() == KH,
+              "radial MLP: fc.0 (64, nb) and fc.2 (64, 64)");
+  const int64_t E = r_.numel();
+  Tensor r = f32c(r_), w0 = f32c(w0_), b0 = f32c(b0_), w2 = f32c(w2_), b2 = f32c(b2_);
+  Tensor h = at::empty({E, KH}, fopts(r));
+  check(fsc_radial_mlp_forward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), (int32_t)w0.size(1), (float)r_cut,
+                               basis_code(basis), mf(h), stream_of(r)),
+        "fsc_radial_mlp_forward");
+  return h;
+}
+
+Tensor radial_mlp_meta(const Tensor& r, const Tensor&, const Tensor&, const Tensor&, const Tensor&, double, int64_t) {
+  return at::empty({r.numel(), KH}, fopts(r));
+}
+
+Tensor radial_mlp_backward(const Tensor& grad_h, const Tensor& r_, const Tensor& w0_, const Tensor& b0_,
+                           const Tensor& w2_, const Tensor& b2_, double r_cut, int64_t basis) {
+  require_gpu({grad_h, r_, w0_, b0_, w2_, b2_});
+  const int64_t E = r_.numel();
+  Tensor g = f32c(grad_h), r = f32c(r_), w0 = f32c(w0_), b0 = f32c(b0_), w2 = f32c(w2_), b2 = f32c(b2_);
+  Tensor gr = at::empty({E}, fopts(r));
+  check(fsc_radial_mlp_backward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), (int32_t)w0.size(1), (float)r_cut,
+                                basis_code(basis), cf(g), mf(gr), stream_of(r)),
+        "fsc_radial_mlp_backward");
+  return gr;
+}
+
+Tensor radial_mlp_backward_meta(const Tensor&, const Tensor& r, const Tensor&, const Tensor&, const Tensor&,
+                                const Tensor&, double, int64_t) {
+  return at::empty({r.numel()}, fopts(r));
+}
+
 template <typename... Args>
 c10::TypedOperatorHandle<Args...> op_handle(const char* name) {
   return c10::Dispatcher::singleton().findSchemaOrThrow(name, "").typed<Args...>();
@@ -516,6 +602,71 @@ Tensor gram_bilinear_autograd(const Tensor& t, const Tensor& Wf, const Tensor& W
   return GramFn::apply(t, Wf, Wb, scale)[0];
 }
 
+struct EdgeGeometryFn : public torch::autograd::Function<EdgeGeometryFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor pos, Tensor shift, Tensor edge_src, Tensor edge_dst,
+                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&, const Tensor&)>(
+        "fsctep::edge_geometry");
+    auto [n, r] = op.call(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm);
+    ctx->save_for_backward({n, r, dst_ptr, src_ptr, src_perm});
+    ctx->set_materialize_grads(false);
+    return {n, r};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(7);
+    if (!grads[0].defined() && !grads[1].defined()) return res;
+    TORCH_CHECK(!ctx->needs_input_grad(1), "gradients w.r.t. the periodic shift vectors (stress) are not implemented");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<Tensor(const std::optional<Tensor>&, const std::optional<Tensor>&, const Tensor&,
+                                      const Tensor&, const Tensor&, const Tensor&, const Tensor&)>(
+        "fsctep::edge_geometry_backward");
+    const std::optional<Tensor> gn = grads[0].defined() ? std::optional<Tensor>(grads[0]) : std::nullopt;
+    const std::optional<Tensor> gr = grads[1].defined() ? std::optional<Tensor>(grads[1]) : std::nullopt;
+    res[0] = op.call(gn, gr, s[0], s[1], s[2], s[3], s[4]);
+    return res;
+  }
+};
+
+std::tuple<Tensor, Tensor> edge_geometry_autograd(const Tensor& pos, const Tensor& shift, const Tensor& edge_src,
+                                                  const Tensor& edge_dst, const Tensor& dst_ptr, const Tensor& src_ptr,
+                                                  const Tensor& src_perm) {
+  auto r = EdgeGeometryFn::apply(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm);
+  return {r[0], r[1]};
+}
+
+struct RadialMlpFn : public torch::autograd::Function<RadialMlpFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2,
+                               double r_cut, int64_t basis) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                      double, int64_t)>("fsctep::radial_mlp");
+    Tensor h = op.call(r, w0, b0, w2, b2, r_cut, basis);
+    ctx->save_for_backward({r, w0, b0, w2, b2});
+    ctx->saved_data["r_cut"] = r_cut;
+    ctx->saved_data["basis"] = basis;
+    ctx->set_materialize_grads(false);
+    return {h};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(7);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {1, 2, 3, 4}, "the radial MLP");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                      const Tensor&, double, int64_t)>("fsctep::radial_mlp_backward");
+    res[0] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], ctx->saved_data["r_cut"].toDouble(),
+                     ctx->saved_data["basis"].toInt());
+    return res;
+  }
+};
+
+Tensor radial_mlp_autograd(const Tensor& r, const Tensor& w0, const Tensor& b0, const Tensor& w2, const Tensor& b2,
+                           double r_cut, int64_t basis) {
+  return RadialMlpFn::apply(r, w0, b0, w2, b2, r_cut, basis)[0];
+}
+
 // CPU tensors: the HIP kernels are the only implementation, so say that instead of "no CPU kernel".
 void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
   TORCH_CHECK(false, op.schema().name(), ": fsctep ops run on the GPU only (HIP kernels); got CPU tensors");
@@ -546,6 +697,13 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
   m.def("gram_bilinear(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
   m.def("gram_bilinear_backward(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
+  m.def("edge_geometry(Tensor pos, Tensor shift, Tensor edge_src, Tensor edge_dst, Tensor dst_ptr, Tensor src_ptr, "
+        "Tensor src_perm) -> (Tensor, Tensor)");
+  m.def("edge_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor dst_ptr, Tensor src_ptr, "
+        "Tensor src_perm) -> Tensor");
+  m.def("radial_mlp(Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, float r_cut, int basis) -> Tensor");
+  m.def("radial_mlp_backward(Tensor grad_h, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, float r_cut, "
+        "int basis) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -563,6 +721,10 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("gram_prepare_weights", gram_prepare_weights);
   m.impl("gram_bilinear", gram_bilinear);
   m.impl("gram_bilinear_backward", gram_bilinear_backward);
+  m.impl("edge_geometry", edge_geometry);
+  m.impl("edge_geometry_backward", edge_geometry_backward);
+  m.impl("radial_mlp", radial_mlp);
+  m.impl("radial_mlp_backward", radial_mlp_backward);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -580,6 +742,10 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("gram_prepare_weights", gram_prepare_weights_meta);
   m.impl("gram_bilinear", gram_bilinear_meta);
   m.impl("gram_bilinear_backward", gram_bilinear_backward_meta);
+  m.impl("edge_geometry", edge_geometry_meta);
+  m.impl("edge_geometry_backward", edge_geometry_backward_meta);
+  m.impl("radial_mlp", radial_mlp_meta);
+  m.impl("radial_mlp_backward", radial_mlp_backward_meta);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
@@ -588,12 +754,15 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
   m.impl("ictd_conv", ictd_conv_autograd);
   m.impl("ictd_conv1", ictd_conv1_autograd);
   m.impl("gram_bilinear", gram_bilinear_autograd);
+  m.impl("edge_geometry", edge_geometry_autograd);
+  m.impl("radial_mlp", radial_mlp_autograd);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
   for (const char* name : {"sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table",
                            "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
                            "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
-                           "gram_bilinear", "gram_bilinear_backward"})
+                           "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
+                           "radial_mlp", "radial_mlp_backward"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

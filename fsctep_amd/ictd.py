@@ -23,7 +23,6 @@ from . import ictd_ops
 from .readout_ops import GramWeights
 from .graph import Graph, prepare_graph
 from .ictd_basis import canonical, coupling, harmonic_projection, layout_full, layout_o3
-from .radial import radial_basis
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
 
 
@@ -205,11 +204,10 @@ class _ICTDTrunk(nn.Module):
         f32 = torch.float32
         pos, cell = pos.to(f32), cell.to(f32)
         proj, cg, c1_gates, factors = self._consts(pos.device)
-        vec = pos[g.dst] - pos[g.src] + (g.shifts.to(f32).unsqueeze(-1) * cell[batch[g.src]]).sum(1)
-        r = vec.norm(dim=1)
-        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+        with torch.no_grad():
+            shift_vec = (g.shifts.to(f32).unsqueeze(-1) * cell[batch[g.src]]).sum(1)
+        n, r = ictd_ops.edge_geometry(pos, shift_vec, g)
         Y = self.harmonics(n, proj)
-        emb = radial_basis(r, self.max_radius, self.number_of_basis, self.function_type)
 
         c1 = self.e3_conv_emb
         atab = c1.atom_mlp(c1.atom_embedding(g.species)).detach()
@@ -230,11 +228,16 @@ class _ICTDTrunk(nn.Module):
             F_in = Y + add
         elif external_tensor is not None:
             raise ValueError("external_tensor given but the model has no external field")
-        feats = [ictd_ops.ictd_conv1_apply(F_in, c1.fc(emb), qtab, g, self.layout_id)]
+        feats = [ictd_ops.ictd_conv1_apply(F_in, self._gates(c1.fc, r), qtab, g, self.layout_id)]
         for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
-            feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, fc2(emb), tp.weight.detach(), self._wt(tp), cg, g,
-                                                  self.layout_id))
+            feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, self._gates(fc2, r), tp.weight.detach(),
+                                                  self._wt(tp), cg, g, self.layout_id))
         return self.readout(feats, batch, factors)
+
+    def _gates(self, fc, r):
+        """Per-path gates fc(radial_basis(r)) (E, P): fc[:4] on the device, the last Linear in torch."""
+        h = ictd_ops.radial_hidden(r, fc, self.max_radius, self.function_type)
+        return F.linear(h, fc[4].weight.detach(), fc[4].bias.detach())
 
     def _to_ref_flat(self, f):
         """x[N][M][C] -> reference flat (N, C*M): per key a channel-major (C, 2l+1) block."""

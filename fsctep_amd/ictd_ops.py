@@ -21,6 +21,7 @@ from torch import Tensor
 
 from . import _lib
 from .ictd_basis import Layout
+from .ops import edge_geometry, radial_hidden  # noqa: F401  (shared edge geometry / radial MLP ops)
 
 _lib.load_torch_ops()
 

@@ -12,6 +12,8 @@ produced (the path serves energy + forces).
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
     sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, n_nodes, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
+    edge_geometry(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm) -> (n, r)
+    radial_mlp(r, w0, b0, w2, b2, r_cut, basis) -> h
 """
 
 from __future__ import annotations
@@ -35,3 +37,21 @@ def sparse_conv1_apply(h, n, mf, mb, graph, channels: int):
     out, _ = torch.ops.fsctep.sparse_conv1(h, n, mf, mb, graph.dst_ptr, graph.pair_tiles, graph.n_nodes,
                                            int(channels))
     return out
+
+
+BASIS = {"bessel": 0, "gaussian": 1}
+
+
+def edge_geometry(pos, shift_vec, graph):
+    """Differentiable (w.r.t. ``pos``) unit vectors n (E,3) and lengths r (E,) of the receiver-sorted edges;
+    ``shift_vec`` = edge_shifts @ cell (no gradient)."""
+    return torch.ops.fsctep.edge_geometry(pos, shift_vec.detach(), graph.src32, graph.dst32, graph.dst_ptr,
+                                          graph.src_ptr, graph.src_perm)
+
+
+def radial_hidden(r, fc, r_cut: float, basis: str):
+    """fc[:4](radial_basis(r)) = silu(fc[2](silu(fc[0](emb)))) on the device: (E, 64)."""
+    if basis not in BASIS:
+        raise ValueError(f"radial basis {basis!r} is not supported by the HIP path")
+    return torch.ops.fsctep.radial_mlp(r, fc[0].weight.detach(), fc[0].bias.detach(), fc[2].weight.detach(),
+                                       fc[2].bias.detach(), float(r_cut), BASIS[basis])

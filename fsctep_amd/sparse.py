@@ -9,8 +9,9 @@ unchanged.  Its message passing runs in ``libfsctep_hip.so``:
 * conv2..n (``:382-421``): ``torch.ops.fsctep.sparse_conv``;
 * readout Gram bilinear ``product_3`` (``:424-456``): ``torch.ops.fsctep.gram_bilinear``.
 
-Edge geometry, the radial basis, the first two radial-MLP layers and the rest of the
-readout (``:769-833``) stay in PyTorch, on the same internal feature layout x[N][13][C]
+Edge geometry and the radial MLP fc[:4] (``:745-756``, ``:204-210``, ``:319-321``, ``:372-378``,
+``:410-412``) run as ``torch.ops.fsctep.edge_geometry`` / ``radial_mlp``; the rest of the readout
+(``:769-833``) stays in PyTorch, on the same internal feature layout x[N][13][C]
 (component-major; the reference's pseudo half is identically zero and is not stored).
 """
 
@@ -25,7 +26,6 @@ import torch.nn.functional as F
 from . import ops
 from .readout_ops import GramWeights
 from .graph import Graph, prepare_graph
-from .radial import radial_basis
 
 _COMPS = ((0, 1), (1, 4), (4, 13))   # component ranges of ranks 0, 1, 2
 
@@ -73,11 +73,6 @@ class RobustScalarWeightedSum(nn.Module):
 
 def _radial_mlp(hidden_out: int, nb: int) -> nn.Sequential:
     return nn.Sequential(nn.Linear(nb, 64), nn.SiLU(), nn.Linear(64, 64), nn.SiLU(), nn.Linear(64, hidden_out))
-
-
-def _hidden(fc: nn.Sequential, emb: torch.Tensor) -> torch.Tensor:
-    """Output of fc[:4] (the 64-wide radial hidden that feeds fc.4)."""
-    return F.silu(fc[2](F.silu(fc[0](emb))))
 
 
 class PureCartesianSparseE3Conv(nn.Module):
@@ -246,22 +241,22 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         pos = pos.to(dtype)
         cell = cell.to(dtype)
         N = pos.shape[0]
-        shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * cell[batch[g.src]]).sum(1)   # elementwise: no batched GEMM
-        vec = pos[g.dst] - pos[g.src] + shift_vec
-        r = vec.norm(dim=1)
-        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
-        emb = radial_basis(r, self.max_radius, self.number_of_basis, self.function_type)
+        with torch.no_grad():
+            shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * cell[batch[g.src]]).sum(1)   # elementwise: no batched GEMM
+        n, r = ops.edge_geometry(pos, shift_vec, g)
 
         conv1 = self.e3_conv_layers[0]
         atab = conv1.atom_table(g.species).to(dtype)
         mf, mb = torch.ops.fsctep.sparse_conv1_pair_table(conv1.fc[4].weight.detach(),
                                                           conv1.fc[4].bias.detach(), atab.detach(),
                                                           self.channels)
-        feats = [ops.sparse_conv1_apply(_hidden(conv1.fc, emb), n, mf, mb, g, self.channels)]
+        h1 = ops.radial_hidden(r, conv1.fc, self.max_radius, self.function_type)
+        feats = [ops.sparse_conv1_apply(h1, n, mf, mb, g, self.channels)]
         inv_norm = 1.0 / max(g.n_edges / max(N, 1), 1e-8)
         for conv in self.e3_conv_layers[1:]:
             bk1, bk6 = conv.prepared_weights()
-            feats.append(ops.sparse_conv_apply(feats[-1], _hidden(conv.fc, emb), n, bk1, bk6, g, inv_norm))
+            h = ops.radial_hidden(r, conv.fc, self.max_radius, self.function_type)
+            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, inv_norm))
         return self.readout(feats)
 
     def readout(self, feats):

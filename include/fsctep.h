@@ -103,6 +103,32 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                               const float* mf, const float* q_ws, float* dq_ws, float* grad_h, float* grad_n,
                               hipStream_t stream);
 
+/* ------------------------------------------------------------------ edge geometry and radial MLP
+ * Replaces the edge geometry of the trunks (models/pure_cartesian_sparse_layers.py:745-756,
+ * models/pure_cartesian_ictd_layers_full.py:896-909, models/pure_cartesian_ictd_layers_o3.py:924-936):
+ * vec = pos[dst] - pos[src] + shift (shift = edge_shifts @ cell), r = |vec|, n = vec/max(r, 1e-8),
+ * with edges in receiver order.  The backward writes grad_pos [N][3] = dE/dpos from grad_n
+ * [E][3] and grad_r [E] (either may be null) by segmented sums over the receiver CSR and the
+ * source grouping (src_ptr, src_perm); no atomics. */
+int fsc_edge_geometry_forward(int64_t n_edges, const float* pos, const float* shift, const int32_t* edge_src,
+                              const int32_t* edge_dst, float* n_out, float* r_out, hipStream_t stream);
+int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* grad_n, const float* grad_r,
+                               const float* n, const float* r, const int32_t* dst_ptr, const int32_t* src_ptr,
+                               const int32_t* src_perm, float* grad_pos, hipStream_t stream);
+
+/* Radial basis + the first four layers of a radial MLP (fc = Linear(nb,64), SiLU, Linear(64,64), SiLU,
+ * ...; models/pure_cartesian_sparse_layers.py:204-210,319-321,372-378,410-412,
+ * models/pure_cartesian_ictd_layers_full.py:277-283,464-465,693-699,930-937):
+ * h [E][64] = silu(w2 silu(w0 emb(r) + b0) + b2), emb = soft_one_hot_linspace(r, 0, r_cut, n_basis,
+ * basis, cutoff=True) * sqrt(n_basis); basis 0 = bessel, 1 = gaussian; w0 [64][n_basis], w2 [64][64]
+ * (torch Linear layout).  The backward gives grad_r [E] from grad_h [E][64] (activations recomputed). */
+int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
+                           const float* b2, int32_t n_basis, float r_cut, int32_t basis, float* h,
+                           hipStream_t stream);
+int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
+                            const float* b2, int32_t n_basis, float r_cut, int32_t basis, const float* grad_h,
+                            float* grad_r, hipStream_t stream);
+
 /* ------------------------------------------------------------------ ICTD (pure-cartesian-ictd / -o3)
  * Irreps are keys (l, parity) in a fixed order; node features are x[N][M][C] with M = sum(2l+1)
  * components (component-major), edge harmonics Y[E][(lmax+1)^2] (block l at offset l^2).

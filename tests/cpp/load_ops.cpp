@@ -24,7 +24,8 @@ int main(int argc, char** argv) {
   const char* names[] = {"sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table",
                          "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
                          "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
-                         "gram_bilinear", "gram_bilinear_backward"};
+                         "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
+                         "radial_mlp", "radial_mlp_backward"};
   for (const char* n : names) {
     auto op = disp.findSchema({std::string("fsctep::") + n, ""});
     if (!op) {

@@ -4,7 +4,8 @@ No reference test holds values of this third-party function; these checks fix wh
 mathematics fixes: the Bessel functions sqrt(2/rc) sin(k pi r/rc) are orthonormal on
 (0, rc) after multiplying by r, vanish outside it and tend to sqrt(2/rc) k pi/rc at r->0;
 the Gaussians peak at the interior linspace points with height 1/1.12 and fall by e^-1
-one step away.  The device implementation (fsctep_amd.radial) must agree with the oracle.
+one step away.  The device kernel (radial_mlp) is checked against this oracle in
+tests/test_edge_radial_gpu.py.
 """
 
 import math
@@ -12,7 +13,6 @@ import math
 import numpy as np
 import torch
 
-from fsctep_amd.radial import radial_basis
 from oracle.radial import soft_one_hot_linspace
 
 
@@ -39,11 +39,3 @@ def test_gaussian_centres_and_width():
     np.testing.assert_allclose(torch.diagonal(b).numpy(), np.full(nb, 1 / 1.12), rtol=1e-12)
     b1 = soft_one_hot_linspace(centres + step, 0.0, rc, nb, "gaussian", True)
     np.testing.assert_allclose(torch.diagonal(b1).numpy(), np.full(nb, math.exp(-1) / 1.12), rtol=1e-12)
-
-
-def test_device_basis_matches_oracle():
-    r = torch.linspace(0.3, 5.5, 1000, dtype=torch.float64)
-    for basis in ("bessel", "gaussian"):
-        a = radial_basis(r, 5.0, 8, basis)
-        b = soft_one_hot_linspace(r, 0.0, 5.0, 8, basis, True) * math.sqrt(8)
-        np.testing.assert_allclose(a.numpy(), b.numpy(), rtol=1e-12, atol=1e-12)
