@@ -10,6 +10,7 @@
 // dpos[m] = sum_{e: dst(e)=m} dvec_e - sum_{e: src(e)=m} dvec_e as two deterministic segmented
 // sums over the receiver CSR and the source grouping (no atomics).
 #include "common.h"
+#include "fsctep.h"
 
 namespace fsc {
 namespace radial {
@@ -48,29 +49,78 @@ __device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); 
 // One wave per 16-edge tile; lane (r, q) works for edge e0 + r.  The hidden units are laid
 // out as the MFMA output: lane (r, q) holds unit j = 16*jt + 4*q + i in register (jt, i), so
 // one layer's output is directly the next product's B operand (K index q <-> 16*jt + 4*q + i).
-// Weights are staged in LDS: W0 [64][NBMAX], W2 [64][65] (row padded), b0, b2.
+// Weights are staged in LDS with rows padded to a multiple of four so that the four K values a
+// lane needs come in one 16-byte read: W0 [64][NBMAX] and W0^T [NBMAX][68], W2 [64][68] and
+// W2^T [64][68], W4 [64][68] (an optional last Linear with up to 64 outputs, zero rows beyond).
+constexpr int WS = HID + 4;
+template <bool BWD>
 struct Smem {
   float w0[HID][NBMAX];
-  float w2[HID][HID + 1];
+  float w0t[BWD ? NBMAX : 1][WS];
+  float w2[HID][WS];
+  float w2t[BWD ? HID : 1][WS];
+  float w4[BWD ? 1 : HID][WS];
+  float w4t[BWD ? HID : 1][WS];
   float b0[HID];
   float b2[HID];
+  float b4[HID];
 };
 
-__device__ void stage_weights(Smem& sm, const float* __restrict__ W0, const float* __restrict__ b0,
-                              const float* __restrict__ W2, const float* __restrict__ b2, int nb) {
+template <bool BWD>
+__device__ void stage_weights(Smem<BWD>& sm, const float* __restrict__ W0, const float* __restrict__ b0,
+                              const float* __restrict__ W2, const float* __restrict__ b2,
+                              const float* __restrict__ W4, const float* __restrict__ b4, int nb, int nout) {
   for (int i = threadIdx.x; i < HID * NBMAX; i += blockDim.x) {
     const int j = i / NBMAX, k = i % NBMAX;
-    sm.w0[j][k] = (k < nb) ? W0[j * nb + k] : 0.f;
+    const float v = (k < nb) ? W0[j * nb + k] : 0.f;
+    sm.w0[j][k] = v;
+    if (BWD) sm.w0t[k][j] = v;
   }
-  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) sm.w2[i / HID][i % HID] = W2[i];
+  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) {
+    const int a = i / HID, b = i % HID;
+    sm.w2[a][b] = W2[i];
+    if (BWD) sm.w2t[b][a] = W2[i];
+    if (W4) {
+      const float v = (a < nout) ? W4[a * HID + b] : 0.f;
+      if (BWD)
+        sm.w4t[b][a] = v;
+      else
+        sm.w4[a][b] = v;
+    }
+  }
   for (int i = threadIdx.x; i < HID; i += blockDim.x) {
     sm.b0[i] = b0[i];
     sm.b2[i] = b2[i];
+    sm.b4[i] = (W4 && i < nout && b4) ? b4[i] : 0.f;
+  }
+}
+
+__device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+// out = W x + b for a 64-wide layer: x in the MFMA layout (x[jt][i] = unit 16 jt + 4 q + i),
+// W [64][WS] row-major; A operand row r of output tile ot reads W[16 ot + r][16 jt + 4q .. +3].
+__device__ __forceinline__ void dense64(const float (*W)[WS], const float* b, const f4 (&x)[4], int r, int q,
+                                        f4 (&out)[4]) {
+#pragma unroll
+  for (int ot = 0; ot < 4; ++ot) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const f4 a = lds4(&W[16 * ot + r][16 * jt + 4 * q]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = mfma16x16x4(a[i], x[jt][i], acc);
+    }
+    if (b) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += b[16 * ot + 4 * q + i];
+    }
+    out[ot] = acc;
   }
 }
 
 // u0 = W0 emb + b0 and u2 = W2 silu(u0) + b2 for the lane's edge (MFMA layout above).
-__device__ __forceinline__ void mlp_forward(const Smem& sm, const float (&emb)[NBMAX], int nks, int r, int q,
+template <bool BWD>
+__device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&emb)[NBMAX], int nks, int r, int q,
                                             f4 (&u0)[4], f4 (&u2)[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
@@ -85,17 +135,7 @@ __device__ __forceinline__ void mlp_forward(const Smem& sm, const float (&emb)[N
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) a0[jt][i] = u0[jt][i] * sigm(u0[jt][i]);
-#pragma unroll
-  for (int ot = 0; ot < 4; ++ot) {
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc = mfma16x16x4(sm.w2[16 * ot + r][16 * jt + 4 * q + i], a0[jt][i], acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += sm.b2[16 * ot + 4 * q + i];
-    u2[ot] = acc;
-  }
+  dense64(sm.w2, sm.b2, a0, r, q, u2);
 }
 
 __device__ __forceinline__ void edge_basis(float rr, int nb, float rc, int basis, float (&emb)[NBMAX],
@@ -111,10 +151,11 @@ __device__ __forceinline__ void edge_basis(float rr, int nb, float rc, int basis
 
 __global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
                                                                  const float* __restrict__ b0, const float* __restrict__ W2,
-                                                                 const float* __restrict__ b2, int nb, float rc, int basis,
-                                                                 int64_t n_edges, float* __restrict__ h) {
-  __shared__ Smem sm;
-  stage_weights(sm, W0, b0, W2, b2, nb);
+                                                                 const float* __restrict__ b2, const float* __restrict__ W4,
+                                                                 const float* __restrict__ b4, int nout, int nb, float rc,
+                                                                 int basis, int64_t n_edges, float* __restrict__ h) {
+  __shared__ Smem<false> sm;
+  stage_weights(sm, W0, b0, W2, b2, W4, b4, nb, nout);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -125,28 +166,40 @@ __global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __
     const float rr = (e < n_edges) ? rad[e] : 1.f;
     float emb[NBMAX], demb[NBMAX];
     edge_basis(rr, nb, rc, basis, emb, demb);
-    f4 u0[4], u2[4];
+    f4 u0[4], u2[4], a2[4];
     mlp_forward(sm, emb, nks, r, q, u0, u2);
-    if (e < n_edges) {
 #pragma unroll
-      for (int ot = 0; ot < 4; ++ot) {
-        f4 v;
+    for (int ot = 0; ot < 4; ++ot)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = u2[ot][i] * sigm(u2[ot][i]);
-        st4(h + e * HID + 16 * ot + 4 * q, v);
+      for (int i = 0; i < 4; ++i) a2[ot][i] = u2[ot][i] * sigm(u2[ot][i]);
+    if (W4) {
+      f4 o[4];
+      dense64(sm.w4, sm.b4, a2, r, q, o);
+      if (e < n_edges) {
+#pragma unroll
+        for (int ot = 0; ot < 4; ++ot)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * ot + 4 * q + i;
+            if (j < nout) h[e * nout + j] = o[ot][i];
+          }
       }
+    } else if (e < n_edges) {
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot) st4(h + e * HID + 16 * ot + 4 * q, a2[ot]);
     }
   }
 }
 
-// dr[e] = sum_k d emb_k/dr * (W0^T (silu'(u0) * W2^T (silu'(u2) * dh)))_k
+// dr[e] = sum_k d emb_k/dr * (W0^T (silu'(u0) * W2^T (silu'(u2) * dh)))_k, with dh = W4^T dout when the
+// last Linear is fused.
 __global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
                                                                   const float* __restrict__ b0, const float* __restrict__ W2,
-                                                                  const float* __restrict__ b2, int nb, float rc, int basis,
-                                                                  int64_t n_edges, const float* __restrict__ dh,
-                                                                  float* __restrict__ dr) {
-  __shared__ Smem sm;
-  stage_weights(sm, W0, b0, W2, b2, nb);
+                                                                  const float* __restrict__ b2, const float* __restrict__ W4,
+                                                                  int nout, int nb, float rc, int basis, int64_t n_edges,
+                                                                  const float* __restrict__ dout, float* __restrict__ dr) {
+  __shared__ Smem<true> sm;
+  stage_weights(sm, W0, b0, W2, b2, W4, nullptr, nb, nout);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -160,36 +213,46 @@ __global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* _
     edge_basis(rr, nb, rc, basis, emb, demb);
     f4 u0[4], u2[4];
     mlp_forward(sm, emb, nks, r, q, u0, u2);
-    f4 g2[4];
-#pragma unroll
-    for (int ot = 0; ot < 4; ++ot) {
-      const f4 d = ok ? ld4(dh + e * HID + 16 * ot + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s = sigm(u2[ot][i]);
-        g2[ot][i] = d[i] * s * (1.f + u2[ot][i] * (1.f - s));
-      }
-    }
-    f4 g0[4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
+    f4 dh[4];
+    if (W4) {
+      f4 d[4];
 #pragma unroll
       for (int ot = 0; ot < 4; ++ot)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc = mfma16x16x4(sm.w2[16 * ot + 4 * q + i][16 * jt + r], g2[ot][i], acc);
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * ot + 4 * q + i;
+          d[ot][i] = (ok && j < nout) ? dout[e * nout + j] : 0.f;
+        }
+      dense64(sm.w4t, nullptr, d, r, q, dh);
+    } else {
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot) dh[ot] = ok ? ld4(dout + e * HID + 16 * ot + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    f4 g2[4];
+#pragma unroll
+    for (int ot = 0; ot < 4; ++ot)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float s = sigm(u0[jt][i]);
-        g0[jt][i] = acc[i] * s * (1.f + u0[jt][i] * (1.f - s));
+        const float s = sigm(u2[ot][i]);
+        g2[ot][i] = dh[ot][i] * s * (1.f + u2[ot][i] * (1.f - s));
       }
-    }
-    // d emb[k] for k = 4q + i (rows k of one 16-row tile; k >= nb rows are zero)
-    f4 de = {0.f, 0.f, 0.f, 0.f};
+    f4 da0[4], g0[4];
+    dense64(sm.w2t, nullptr, g2, r, q, da0);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) de = mfma16x16x4(sm.w0[16 * jt + 4 * q + i][r], g0[jt][i], de);
+      for (int i = 0; i < 4; ++i) {
+        const float s = sigm(u0[jt][i]);
+        g0[jt][i] = da0[jt][i] * s * (1.f + u0[jt][i] * (1.f - s));
+      }
+    // d emb[k] for k = 4q + i (rows k of one 16-row tile; k >= nb rows are zero)
+    f4 de = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const f4 a = lds4(&sm.w0t[r][16 * jt + 4 * q]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) de = mfma16x16x4(a[i], g0[jt][i], de);
+    }
     float part = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -277,6 +340,79 @@ __global__ __launch_bounds__(256) void geometry_backward_kernel(const float* __r
   }
 }
 
+// ---------------------------------------------------------------- direction harmonics (ICTD)
+// Y[e][l^2 + m] = sum_{k of degree l} M[k][m] n_x^a n_y^b n_z^c (M = multinomial * G_l B_l, the
+// ICTD harmonic basis); backward dn = sum_k (sum_m dY[l^2+m] M[k][m]) grad(n^abc).  One thread
+// per edge; the table travels as a kernel argument.
+__device__ __forceinline__ float ipow(const float (&p)[4], int e) {
+  return e == 0 ? p[0] : (e == 1 ? p[1] : (e == 2 ? p[2] : p[3]));
+}
+
+__global__ void harmonics_forward_kernel(FscHarmTable tab, int64_t n_edges, const float* __restrict__ nvec,
+                                         float* __restrict__ Y) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  float px[4], py[4], pz[4];
+  px[0] = py[0] = pz[0] = 1.f;
+  const float x = nvec[3 * e], y = nvec[3 * e + 1], z = nvec[3 * e + 2];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    px[i] = px[i - 1] * x;
+    py[i] = py[i - 1] * y;
+    pz[i] = pz[i - 1] * z;
+  }
+  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
+  float out[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out[i] = 0.f;
+  for (int k = 0; k < tab.nmono; ++k) {
+    const int l = tab.mono_l[k];
+    const float m = ipow(px, tab.mono_exp[k][0]) * ipow(py, tab.mono_exp[k][1]) * ipow(pz, tab.mono_exp[k][2]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int jj = j - l * l;
+      if (jj >= 0 && jj < 2 * l + 1) out[j] += m * tab.coef[k][jj];
+    }
+  }
+  for (int j = 0; j < ny; ++j) Y[e * ny + j] = out[j];
+}
+
+__global__ void harmonics_backward_kernel(FscHarmTable tab, int64_t n_edges, const float* __restrict__ nvec,
+                                          const float* __restrict__ dY, float* __restrict__ dn) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  float px[4], py[4], pz[4];
+  px[0] = py[0] = pz[0] = 1.f;
+  const float x = nvec[3 * e], y = nvec[3 * e + 1], z = nvec[3 * e + 2];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    px[i] = px[i - 1] * x;
+    py[i] = py[i - 1] * y;
+    pz[i] = pz[i - 1] * z;
+  }
+  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
+  float g[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) g[j] = (j < ny) ? dY[e * ny + j] : 0.f;
+  float d[3] = {0.f, 0.f, 0.f};
+  for (int k = 0; k < tab.nmono; ++k) {
+    const int l = tab.mono_l[k];
+    float dm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int jj = j - l * l;
+      if (jj >= 0 && jj < 2 * l + 1) dm += g[j] * tab.coef[k][jj];
+    }
+    const int a = tab.mono_exp[k][0], b = tab.mono_exp[k][1], c = tab.mono_exp[k][2];
+    const float fx = ipow(px, a), fy = ipow(py, b), fz = ipow(pz, c);
+    if (a) d[0] += dm * (float)a * ipow(px, a - 1) * fy * fz;
+    if (b) d[1] += dm * (float)b * fx * ipow(py, b - 1) * fz;
+    if (c) d[2] += dm * (float)c * fx * fy * ipow(pz, c - 1);
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) dn[3 * e + i] = d[i];
+}
+
 }  // namespace radial
 }  // namespace fsc
 
@@ -314,33 +450,59 @@ static unsigned radial_grid(int64_t n_edges) {
 }
 
 int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
-                           const float* b2, int32_t n_basis, float r_cut, int32_t basis, float* h,
-                           hipStream_t stream) {
+                           const float* b2, const float* w4, const float* b4, int32_t n_out, int32_t n_basis,
+                           float r_cut, int32_t basis, float* out, hipStream_t stream) {
   FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_forward: bad size");
   FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_forward: n_basis must be 1..16");
   FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_forward: basis must be 0 (bessel) or 1 (gaussian)");
   FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_forward: r_cut must be positive");
+  FSC_CHECK_ARG(!w4 || (b4 && n_out >= 1 && n_out <= HID), "fsc_radial_mlp_forward: last Linear needs 1..64 outputs");
   if (n_edges == 0) return 0;
-  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && h, "fsc_radial_mlp_forward: null pointer");
+  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && out, "fsc_radial_mlp_forward: null pointer");
   LaunchTimer tm("radial_mlp", stream);
-  radial_mlp_forward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, n_basis, r_cut, basis,
-                                                                     n_edges, h);
+  radial_mlp_forward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, w4, b4, w4 ? n_out : HID,
+                                                                     n_basis, r_cut, basis, n_edges, out);
   return check_launch("radial mlp forward") ? 2 : 0;
 }
 
 int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
-                            const float* b2, int32_t n_basis, float r_cut, int32_t basis, const float* grad_h,
-                            float* grad_r, hipStream_t stream) {
+                            const float* b2, const float* w4, int32_t n_out, int32_t n_basis, float r_cut,
+                            int32_t basis, const float* grad_out, float* grad_r, hipStream_t stream) {
   FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_backward: bad size");
   FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_backward: n_basis must be 1..16");
   FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_backward: basis must be 0 (bessel) or 1 (gaussian)");
   FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_backward: r_cut must be positive");
+  FSC_CHECK_ARG(!w4 || (n_out >= 1 && n_out <= HID), "fsc_radial_mlp_backward: last Linear needs 1..64 outputs");
   if (n_edges == 0) return 0;
-  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && grad_h && grad_r, "fsc_radial_mlp_backward: null pointer");
+  FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && grad_out && grad_r, "fsc_radial_mlp_backward: null pointer");
   LaunchTimer tm("radial_mlp_grad", stream);
-  radial_mlp_backward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, n_basis, r_cut, basis,
-                                                                      n_edges, grad_h, grad_r);
+  radial_mlp_backward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, w4, w4 ? n_out : HID,
+                                                                      n_basis, r_cut, basis, n_edges, grad_out, grad_r);
   return check_launch("radial mlp backward") ? 2 : 0;
+}
+
+
+int fsc_edge_harmonics_forward(const FscHarmTable* table, int64_t n_edges, const float* n, float* Y,
+                               hipStream_t stream) {
+  FSC_CHECK_ARG(table && table->lmax >= 0 && table->lmax <= 3 && table->nmono >= 1 && table->nmono <= 20,
+                "fsc_edge_harmonics_forward: table must describe lmax <= 3 with at most 20 monomials");
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_edge_harmonics_forward: bad size");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(n && Y, "fsc_edge_harmonics_forward: null pointer");
+  harmonics_forward_kernel<<<(unsigned)((n_edges + 255) / 256), 256, 0, stream>>>(*table, n_edges, n, Y);
+  return check_launch("edge harmonics forward") ? 2 : 0;
+}
+
+int fsc_edge_harmonics_backward(const FscHarmTable* table, int64_t n_edges, const float* n, const float* grad_Y,
+                                float* grad_n, hipStream_t stream) {
+  FSC_CHECK_ARG(table && table->lmax >= 0 && table->lmax <= 3 && table->nmono >= 1 && table->nmono <= 20,
+                "fsc_edge_harmonics_backward: table must describe lmax <= 3 with at most 20 monomials");
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_edge_harmonics_backward: bad size");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(n && grad_Y && grad_n, "fsc_edge_harmonics_backward: null pointer");
+  harmonics_backward_kernel<<<(unsigned)((n_edges + 255) / 256), 256, 0, stream>>>(*table, n_edges, n, grad_Y,
+                                                                                   grad_n);
+  return check_launch("edge harmonics backward") ? 2 : 0;
 }
 
 }  // extern "C"

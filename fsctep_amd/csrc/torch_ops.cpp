@@ -391,39 +391,92 @@ int32_t basis_code(int64_t basis) {
 }
 
 Tensor radial_mlp(const Tensor& r_, const Tensor& w0_, const Tensor& b0_, const Tensor& w2_, const Tensor& b2_,
-                  double r_cut, int64_t basis) {
+                  const std::optional<Tensor>& w4_, const std::optional<Tensor>& b4_, double r_cut, int64_t basis) {
   require_gpu({r_, w0_, b0_, w2_, b2_});
   TORCH_CHECK(w0_.dim() == 2 && w0_.size(0) == KH && w2_.dim() == 2 && w2_.size(0) == KH && w2_.size(1) == KH &&
                   b0_.numel() == KH && b2_.numel() == KH,
               "radial MLP: fc.0 (64, nb) and fc.2 (64, 64)");
-  const int64_t E = r_.numel();
+  const bool fused = w4_.has_value() && w4_->defined();
+  Tensor w4, b4;
+  if (fused) {
+    TORCH_CHECK(b4_.has_value() && b4_->defined() && w4_->dim() == 2 && w4_->size(1) == KH && w4_->size(0) >= 1 &&
+                    w4_->size(0) <= KH && b4_->numel() == w4_->size(0),
+                "radial MLP: the fused last Linear must be (P, 64) with P <= 64, bias (P)");
+    require_gpu({*w4_, *b4_});
+    w4 = f32c(*w4_);
+    b4 = f32c(*b4_);
+  }
+  const int64_t E = r_.numel(), P = fused ? w4.size(0) : KH;
   Tensor r = f32c(r_), w0 = f32c(w0_), b0 = f32c(b0_), w2 = f32c(w2_), b2 = f32c(b2_);
-  Tensor h = at::empty({E, KH}, fopts(r));
-  check(fsc_radial_mlp_forward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), (int32_t)w0.size(1), (float)r_cut,
+  Tensor h = at::empty({E, P}, fopts(r));
+  check(fsc_radial_mlp_forward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), fused ? cf(w4) : nullptr,
+                               fused ? cf(b4) : nullptr, (int32_t)P, (int32_t)w0.size(1), (float)r_cut,
                                basis_code(basis), mf(h), stream_of(r)),
         "fsc_radial_mlp_forward");
   return h;
 }
 
-Tensor radial_mlp_meta(const Tensor& r, const Tensor&, const Tensor&, const Tensor&, const Tensor&, double, int64_t) {
-  return at::empty({r.numel(), KH}, fopts(r));
+Tensor radial_mlp_meta(const Tensor& r, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                       const std::optional<Tensor>& w4, const std::optional<Tensor>&, double, int64_t) {
+  return at::empty({r.numel(), (w4.has_value() && w4->defined()) ? w4->size(0) : KH}, fopts(r));
 }
 
-Tensor radial_mlp_backward(const Tensor& grad_h, const Tensor& r_, const Tensor& w0_, const Tensor& b0_,
-                           const Tensor& w2_, const Tensor& b2_, double r_cut, int64_t basis) {
-  require_gpu({grad_h, r_, w0_, b0_, w2_, b2_});
-  const int64_t E = r_.numel();
-  Tensor g = f32c(grad_h), r = f32c(r_), w0 = f32c(w0_), b0 = f32c(b0_), w2 = f32c(w2_), b2 = f32c(b2_);
+Tensor radial_mlp_backward(const Tensor& grad_out, const Tensor& r_, const Tensor& w0_, const Tensor& b0_,
+                           const Tensor& w2_, const Tensor& b2_, const std::optional<Tensor>& w4_, double r_cut,
+                           int64_t basis) {
+  require_gpu({grad_out, r_, w0_, b0_, w2_, b2_});
+  const bool fused = w4_.has_value() && w4_->defined();
+  Tensor w4 = fused ? f32c(*w4_) : Tensor();
+  const int64_t E = r_.numel(), P = fused ? w4.size(0) : KH;
+  TORCH_CHECK(grad_out.numel() == E * P, "radial MLP backward: grad shape");
+  Tensor g = f32c(grad_out), r = f32c(r_), w0 = f32c(w0_), b0 = f32c(b0_), w2 = f32c(w2_), b2 = f32c(b2_);
   Tensor gr = at::empty({E}, fopts(r));
-  check(fsc_radial_mlp_backward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), (int32_t)w0.size(1), (float)r_cut,
-                                basis_code(basis), cf(g), mf(gr), stream_of(r)),
+  check(fsc_radial_mlp_backward(E, cf(r), cf(w0), cf(b0), cf(w2), cf(b2), fused ? cf(w4) : nullptr, (int32_t)P,
+                                (int32_t)w0.size(1), (float)r_cut, basis_code(basis), cf(g), mf(gr), stream_of(r)),
         "fsc_radial_mlp_backward");
   return gr;
 }
 
 Tensor radial_mlp_backward_meta(const Tensor&, const Tensor& r, const Tensor&, const Tensor&, const Tensor&,
-                                const Tensor&, double, int64_t) {
+                                const Tensor&, const std::optional<Tensor>&, double, int64_t) {
   return at::empty({r.numel()}, fopts(r));
+}
+
+const FscHarmTable* harm_table_of(const Tensor& table) {
+  TORCH_CHECK(table.device().is_cpu() && table.scalar_type() == at::kInt && table.is_contiguous() &&
+                  table.numel() * 4 == (int64_t)sizeof(FscHarmTable),
+              "harmonics table must be a contiguous CPU int32 tensor holding an FscHarmTable (",
+              sizeof(FscHarmTable) / 4, " entries)");
+  return reinterpret_cast<const FscHarmTable*>(table.data_ptr<int32_t>());
+}
+
+Tensor edge_harmonics(const Tensor& n_, const Tensor& table) {
+  require_gpu({n_});
+  const FscHarmTable* T = harm_table_of(table);
+  const int64_t E = n_.size(0), NY = (T->lmax + 1) * (T->lmax + 1);
+  Tensor n = f32c(n_);
+  Tensor Y = at::empty({E, NY}, fopts(n));
+  check(fsc_edge_harmonics_forward(T, E, cf(n), mf(Y), stream_of(n)), "fsc_edge_harmonics_forward");
+  return Y;
+}
+
+Tensor edge_harmonics_meta(const Tensor& n, const Tensor& table) {
+  const FscHarmTable* T = harm_table_of(table);
+  return at::empty({n.size(0), (T->lmax + 1) * (T->lmax + 1)}, fopts(n));
+}
+
+Tensor edge_harmonics_backward(const Tensor& grad_Y, const Tensor& n_, const Tensor& table) {
+  require_gpu({grad_Y, n_});
+  const FscHarmTable* T = harm_table_of(table);
+  const int64_t E = n_.size(0);
+  Tensor n = f32c(n_), g = f32c(grad_Y);
+  Tensor dn = at::empty({E, 3}, fopts(n));
+  check(fsc_edge_harmonics_backward(T, E, cf(n), cf(g), mf(dn), stream_of(n)), "fsc_edge_harmonics_backward");
+  return dn;
+}
+
+Tensor edge_harmonics_backward_meta(const Tensor&, const Tensor& n, const Tensor&) {
+  return at::empty({n.size(0), 3}, fopts(n));
 }
 
 template <typename... Args>
@@ -638,34 +691,63 @@ std::tuple<Tensor, Tensor> edge_geometry_autograd(const Tensor& pos, const Tenso
 
 struct RadialMlpFn : public torch::autograd::Function<RadialMlpFn> {
   static variable_list forward(AutogradContext* ctx, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2,
-                               double r_cut, int64_t basis) {
+                               std::optional<Tensor> w4, std::optional<Tensor> b4, double r_cut, int64_t basis) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      double, int64_t)>("fsctep::radial_mlp");
-    Tensor h = op.call(r, w0, b0, w2, b2, r_cut, basis);
-    ctx->save_for_backward({r, w0, b0, w2, b2});
+                                      const std::optional<Tensor>&, const std::optional<Tensor>&, double, int64_t)>(
+        "fsctep::radial_mlp");
+    const bool fused = w4.has_value() && w4->defined();
+    TORCH_CHECK(!fused || !at::GradMode::is_enabled() ||
+                    !(w4->requires_grad() || (b4.has_value() && b4->defined() && b4->requires_grad())),
+                "parameter gradients of the radial MLP are not implemented (energy/force inference only)");
+    Tensor h = op.call(r, w0, b0, w2, b2, w4, b4, r_cut, basis);
+    ctx->save_for_backward({r, w0, b0, w2, b2, fused ? *w4 : Tensor()});
     ctx->saved_data["r_cut"] = r_cut;
     ctx->saved_data["basis"] = basis;
     ctx->set_materialize_grads(false);
     return {h};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(7);
+    variable_list res(9);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {1, 2, 3, 4}, "the radial MLP");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, double, int64_t)>("fsctep::radial_mlp_backward");
-    res[0] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], ctx->saved_data["r_cut"].toDouble(),
+                                      const Tensor&, const std::optional<Tensor>&, double, int64_t)>(
+        "fsctep::radial_mlp_backward");
+    const std::optional<Tensor> w4 = s[5].defined() ? std::optional<Tensor>(s[5]) : std::nullopt;
+    res[0] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], w4, ctx->saved_data["r_cut"].toDouble(),
                      ctx->saved_data["basis"].toInt());
     return res;
   }
 };
 
 Tensor radial_mlp_autograd(const Tensor& r, const Tensor& w0, const Tensor& b0, const Tensor& w2, const Tensor& b2,
-                           double r_cut, int64_t basis) {
-  return RadialMlpFn::apply(r, w0, b0, w2, b2, r_cut, basis)[0];
+                           const std::optional<Tensor>& w4, const std::optional<Tensor>& b4, double r_cut,
+                           int64_t basis) {
+  return RadialMlpFn::apply(r, w0, b0, w2, b2, w4, b4, r_cut, basis)[0];
 }
+
+struct EdgeHarmonicsFn : public torch::autograd::Function<EdgeHarmonicsFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor n, Tensor table) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&)>("fsctep::edge_harmonics");
+    Tensor Y = op.call(n, table);
+    ctx->save_for_backward({n, table});
+    ctx->set_materialize_grads(false);
+    return {Y};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(2);
+    if (!grads[0].defined()) return res;
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&)>("fsctep::edge_harmonics_backward");
+    res[0] = op.call(grads[0], s[0], s[1]);
+    return res;
+  }
+};
+
+Tensor edge_harmonics_autograd(const Tensor& n, const Tensor& table) { return EdgeHarmonicsFn::apply(n, table)[0]; }
 
 // CPU tensors: the HIP kernels are the only implementation, so say that instead of "no CPU kernel".
 void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
@@ -701,9 +783,12 @@ TORCH_LIBRARY(fsctep, m) {
         "Tensor src_perm) -> (Tensor, Tensor)");
   m.def("edge_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor dst_ptr, Tensor src_ptr, "
         "Tensor src_perm) -> Tensor");
-  m.def("radial_mlp(Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, float r_cut, int basis) -> Tensor");
-  m.def("radial_mlp_backward(Tensor grad_h, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, float r_cut, "
+  m.def("radial_mlp(Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, Tensor? b4, float r_cut, "
         "int basis) -> Tensor");
+  m.def("edge_harmonics(Tensor n, Tensor table) -> Tensor");
+  m.def("edge_harmonics_backward(Tensor grad_Y, Tensor n, Tensor table) -> Tensor");
+  m.def("radial_mlp_backward(Tensor grad_out, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, "
+        "float r_cut, int basis) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -725,6 +810,8 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("edge_geometry_backward", edge_geometry_backward);
   m.impl("radial_mlp", radial_mlp);
   m.impl("radial_mlp_backward", radial_mlp_backward);
+  m.impl("edge_harmonics", edge_harmonics);
+  m.impl("edge_harmonics_backward", edge_harmonics_backward);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -746,6 +833,8 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("edge_geometry_backward", edge_geometry_backward_meta);
   m.impl("radial_mlp", radial_mlp_meta);
   m.impl("radial_mlp_backward", radial_mlp_backward_meta);
+  m.impl("edge_harmonics", edge_harmonics_meta);
+  m.impl("edge_harmonics_backward", edge_harmonics_backward_meta);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
@@ -756,6 +845,7 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
   m.impl("gram_bilinear", gram_bilinear_autograd);
   m.impl("edge_geometry", edge_geometry_autograd);
   m.impl("radial_mlp", radial_mlp_autograd);
+  m.impl("edge_harmonics", edge_harmonics_autograd);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
@@ -763,6 +853,6 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
                            "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
-                           "radial_mlp", "radial_mlp_backward"})
+                           "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -3,8 +3,9 @@
 ``PureCartesianICTDTransformerLayer`` (reference models/pure_cartesian_ictd_layers_full.py:476-1078) and
 ``PureCartesianICTDO3TransformerLayer`` (models/pure_cartesian_ictd_layers_o3.py:535-1074) take the
 reference's constructor arguments and hold its parameters under the same state_dict keys.  Message
-passing runs in ``libfsctep_hip.so`` (``torch.ops.fsctep.ictd_conv1`` / ``ictd_conv``); edge geometry,
-direction harmonics, radial MLPs and the readout stay in PyTorch.  Node features are x[N][M][C]
+passing runs in ``libfsctep_hip.so`` (``torch.ops.fsctep.ictd_conv1`` / ``ictd_conv``), as do the edge geometry,
+the direction harmonics and the radial MLPs (``edge_geometry``, ``edge_harmonics``, ``radial_mlp``); the readout
+outside its Gram bilinear stays in PyTorch.  Node features are x[N][M][C]
 (component-major over the active irreps); the readout rebuilds the reference's flat per-layer layout
 because the reference re-splits the layer-concatenated vector with n_layers*C channels
 (full :977-979, o3 :987-988) and its energy depends on that exact arrangement.
@@ -22,7 +23,7 @@ import torch.nn.functional as F
 from . import ictd_ops
 from .readout_ops import GramWeights
 from .graph import Graph, prepare_graph
-from .ictd_basis import canonical, coupling, harmonic_projection, layout_full, layout_o3
+from .ictd_basis import canonical, coupling, layout_full, layout_o3
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
 
 
@@ -136,15 +137,10 @@ class _ICTDTrunk(nn.Module):
     def _consts(self, device):
         key = ("consts", str(device))
         if key not in self._cache:
-            proj = []
-            for l in range(self.lmax + 1):
-                exps, coef, P = harmonic_projection(l)
-                proj.append((torch.tensor(exps, device=device), torch.tensor(coef, dtype=torch.float32, device=device),
-                             torch.tensor(P, dtype=torch.float32, device=device)))
             cg = torch.tensor(self.layout.cg_table(), dtype=torch.float32, device=device)
             c1 = [p["gate"] for p in self.layout.conv1_paths()]
             factors = [float(coupling(k[0], k[0], 0)[0, 0, 0]) for k in self.keys]
-            self._cache[key] = (proj, cg, torch.tensor(c1, device=device), factors)
+            self._cache[key] = (cg, torch.tensor(c1, device=device), factors)
         return self._cache[key]
 
     def _wt(self, tp):
@@ -156,19 +152,6 @@ class _ICTDTrunk(nn.Module):
             with torch.no_grad():
                 self._cache[key] = torch.ops.fsctep.ictd_prepare_weights(w.detach())
         return self._cache[key]
-
-    def harmonics(self, n, proj):
-        """Y[E][(lmax+1)^2] in the ICTD basis (models/ictd_irreps.py:371-402), integer powers by products."""
-        ys = []
-        pw = [[torch.ones_like(n[:, i])] for i in range(3)]
-        for i in range(3):
-            for _ in range(self.lmax):
-                pw[i].append(pw[i][-1] * n[:, i])
-        for l in range(self.lmax + 1):
-            exps, coef, P = proj[l]
-            cols = [pw[0][int(a)] * pw[1][int(b)] * pw[2][int(c)] for a, b, c in exps.tolist()]
-            ys.append((torch.stack(cols, dim=-1) * coef) @ P)
-        return torch.cat(ys, dim=-1)
 
     # ------------------------------------------------------------------ forward
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
@@ -203,11 +186,11 @@ class _ICTDTrunk(nn.Module):
             raise RuntimeError("the HIP ICTD path runs on the GPU only")
         f32 = torch.float32
         pos, cell = pos.to(f32), cell.to(f32)
-        proj, cg, c1_gates, factors = self._consts(pos.device)
+        cg, c1_gates, factors = self._consts(pos.device)
         with torch.no_grad():
             shift_vec = (g.shifts.to(f32).unsqueeze(-1) * cell[batch[g.src]]).sum(1)
         n, r = ictd_ops.edge_geometry(pos, shift_vec, g)
-        Y = self.harmonics(n, proj)
+        Y = ictd_ops.edge_harmonics(n, self.lmax)
 
         c1 = self.e3_conv_emb
         atab = c1.atom_mlp(c1.atom_embedding(g.species)).detach()
@@ -235,9 +218,11 @@ class _ICTDTrunk(nn.Module):
         return self.readout(feats, batch, factors)
 
     def _gates(self, fc, r):
-        """Per-path gates fc(radial_basis(r)) (E, P): fc[:4] on the device, the last Linear in torch."""
-        h = ictd_ops.radial_hidden(r, fc, self.max_radius, self.function_type)
-        return F.linear(h, fc[4].weight.detach(), fc[4].bias.detach())
+        """Per-path gates fc(radial_basis(r)) (E, P) by one fused kernel (P <= 64)."""
+        if fc[4].weight.shape[0] > 64:
+            h = ictd_ops.radial_hidden(r, fc, self.max_radius, self.function_type)
+            return F.linear(h, fc[4].weight.detach(), fc[4].bias.detach())
+        return ictd_ops.radial_full(r, fc, self.max_radius, self.function_type)
 
     def _to_ref_flat(self, f):
         """x[N][M][C] -> reference flat (N, C*M): per key a channel-major (C, 2l+1) block."""

@@ -21,7 +21,7 @@ from torch import Tensor
 
 from . import _lib
 from .ictd_basis import Layout
-from .ops import edge_geometry, radial_hidden  # noqa: F401  (shared edge geometry / radial MLP ops)
+from .ops import edge_geometry, radial_full, radial_hidden  # noqa: F401  (shared edge geometry / radial MLP ops)
 
 _lib.load_torch_ops()
 
@@ -113,6 +113,43 @@ def layout_tensor(layout_id: int) -> Tensor:
 
 
 _TENSORS: dict = {}
+
+
+class FscHarmTable(ctypes.Structure):
+    _fields_ = [("lmax", _i32), ("nmono", _i32), ("mono_l", _i32 * 20), ("mono_exp", (_i32 * 3) * 20),
+                ("coef", (ctypes.c_float * 7) * 20)]
+
+
+def harmonics_table(lmax: int) -> Tensor:
+    """The ICTD direction-harmonics table (degree-l monomials and multinomial * G_l B_l, lmax <= 3) as the
+    CPU int32 tensor the ``edge_harmonics`` op takes (cached)."""
+    from .ictd_basis import harmonic_projection
+    key = ("harm", lmax)
+    if key not in _TENSORS:
+        if not 0 <= lmax <= 3:
+            raise NotImplementedError("the HIP direction harmonics support lmax <= 3")
+        t = FscHarmTable()
+        t.lmax = lmax
+        k = 0
+        for l in range(lmax + 1):
+            exps, coef, P = harmonic_projection(l)
+            M = coef[:, None] * P
+            for i in range(len(exps)):
+                t.mono_l[k] = l
+                for j in range(3):
+                    t.mono_exp[k][j] = int(exps[i][j])
+                for j in range(2 * l + 1):
+                    t.coef[k][j] = float(M[i][j])
+                k += 1
+        t.nmono = k
+        raw = np.frombuffer(ctypes.string_at(ctypes.addressof(t), ctypes.sizeof(t)), dtype=np.int32)
+        _TENSORS[key] = torch.from_numpy(raw.copy())
+    return _TENSORS[key]
+
+
+def edge_harmonics(n: Tensor, lmax: int) -> Tensor:
+    """Differentiable Y (E, (lmax+1)^2) of the unit edge vectors n (E, 3) in the ICTD basis."""
+    return torch.ops.fsctep.edge_harmonics(n, harmonics_table(lmax))
 
 
 def ictd_conv_apply(x, Y, gates, W, Wt, cg, graph, layout_id: int):

@@ -13,7 +13,7 @@ produced (the path serves energy + forces).
     sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, n_nodes, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
     edge_geometry(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm) -> (n, r)
-    radial_mlp(r, w0, b0, w2, b2, r_cut, basis) -> h
+    radial_mlp(r, w0, b0, w2, b2, w4?, b4?, r_cut, basis) -> h (E,64) or the fused last Linear (E,P)
 """
 
 from __future__ import annotations
@@ -54,4 +54,13 @@ def radial_hidden(r, fc, r_cut: float, basis: str):
     if basis not in BASIS:
         raise ValueError(f"radial basis {basis!r} is not supported by the HIP path")
     return torch.ops.fsctep.radial_mlp(r, fc[0].weight.detach(), fc[0].bias.detach(), fc[2].weight.detach(),
-                                       fc[2].bias.detach(), float(r_cut), BASIS[basis])
+                                       fc[2].bias.detach(), None, None, float(r_cut), BASIS[basis])
+
+
+def radial_full(r, fc, r_cut: float, basis: str):
+    """The whole radial MLP fc(radial_basis(r)) including its last Linear (<= 64 outputs): (E, P)."""
+    if basis not in BASIS:
+        raise ValueError(f"radial basis {basis!r} is not supported by the HIP path")
+    return torch.ops.fsctep.radial_mlp(r, fc[0].weight.detach(), fc[0].bias.detach(), fc[2].weight.detach(),
+                                       fc[2].bias.detach(), fc[4].weight.detach(), fc[4].bias.detach(),
+                                       float(r_cut), BASIS[basis])

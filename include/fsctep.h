@@ -116,18 +116,35 @@ int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* gr
                                const float* n, const float* r, const int32_t* dst_ptr, const int32_t* src_ptr,
                                const int32_t* src_perm, float* grad_pos, hipStream_t stream);
 
-/* Radial basis + the first four layers of a radial MLP (fc = Linear(nb,64), SiLU, Linear(64,64), SiLU,
- * ...; models/pure_cartesian_sparse_layers.py:204-210,319-321,372-378,410-412,
+/* Radial basis + a radial MLP (fc = Linear(nb,64), SiLU, Linear(64,64), SiLU, Linear(64,P);
+ * models/pure_cartesian_sparse_layers.py:204-210,319-321,372-378,410-412,
  * models/pure_cartesian_ictd_layers_full.py:277-283,464-465,693-699,930-937):
- * h [E][64] = silu(w2 silu(w0 emb(r) + b0) + b2), emb = soft_one_hot_linspace(r, 0, r_cut, n_basis,
- * basis, cutoff=True) * sqrt(n_basis); basis 0 = bessel, 1 = gaussian; w0 [64][n_basis], w2 [64][64]
- * (torch Linear layout).  The backward gives grad_r [E] from grad_h [E][64] (activations recomputed). */
+ * h = silu(w2 silu(w0 emb(r) + b0) + b2), emb = soft_one_hot_linspace(r, 0, r_cut, n_basis, basis,
+ * cutoff=True) * sqrt(n_basis); basis 0 = bessel, 1 = gaussian; weights in torch Linear layout
+ * (w0 [64][n_basis], w2 [64][64]).  With w4 == NULL the output is h [E][64] (the sparse trunk's
+ * fc[:4]); with w4 [n_out][64], b4 [n_out] (n_out <= 64) it is w4 h + b4 [E][n_out] (the ICTD gates,
+ * the whole fc).  The backward gives grad_r [E] from grad_out (activations recomputed). */
 int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
-                           const float* b2, int32_t n_basis, float r_cut, int32_t basis, float* h,
-                           hipStream_t stream);
+                           const float* b2, const float* w4, const float* b4, int32_t n_out, int32_t n_basis,
+                           float r_cut, int32_t basis, float* out, hipStream_t stream);
 int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
-                            const float* b2, int32_t n_basis, float r_cut, int32_t basis, const float* grad_h,
-                            float* grad_r, hipStream_t stream);
+                            const float* b2, const float* w4, int32_t n_out, int32_t n_basis, float r_cut,
+                            int32_t basis, const float* grad_out, float* grad_r, hipStream_t stream);
+
+/* Direction harmonics of the ICTD trunks (direction_harmonics_fast/_all, models/ictd_irreps.py:371-402,
+ * 489-494): Y [E][(lmax+1)^2], block l at offset l^2, Y_l(n) = sum_k coef[k][.] n_x^a n_y^b n_z^c over the
+ * degree-l monomials k (coef = multinomial * G_l B_l of the harmonic basis, built on the host by
+ * fsctep_amd/ictd_basis.py).  lmax <= 3.  The backward gives grad_n [E][3] from grad_Y. */
+typedef struct FscHarmTable {
+  int32_t lmax, nmono;
+  int32_t mono_l[20];
+  int32_t mono_exp[20][3];
+  float coef[20][7];
+} FscHarmTable;
+int fsc_edge_harmonics_forward(const FscHarmTable* table, int64_t n_edges, const float* n, float* Y,
+                               hipStream_t stream);
+int fsc_edge_harmonics_backward(const FscHarmTable* table, int64_t n_edges, const float* n, const float* grad_Y,
+                                float* grad_n, hipStream_t stream);
 
 /* ------------------------------------------------------------------ ICTD (pure-cartesian-ictd / -o3)
  * Irreps are keys (l, parity) in a fixed order; node features are x[N][M][C] with M = sum(2l+1)

@@ -39,7 +39,7 @@ def test_radial_mlp_matches_torch(basis, nb):
     dh = torch.randn(E, 64, generator=g, dtype=torch.float64)
     dev = lambda t: t.float().to(DEV)
     rd = dev(r).requires_grad_(True)
-    h = torch.ops.fsctep.radial_mlp(rd, dev(w0), dev(b0), dev(w2), dev(b2), rc, ops.BASIS[basis])
+    h = torch.ops.fsctep.radial_mlp(rd, dev(w0), dev(b0), dev(w2), dev(b2), None, None, rc, ops.BASIS[basis])
     (gr,) = torch.autograd.grad(h, rd, dev(dh))
     rr = r.clone().requires_grad_(True)
     href = _hidden_ref(rr, w0, b0, w2, b2, rc, nb, basis)
@@ -47,6 +47,30 @@ def test_radial_mlp_matches_torch(basis, nb):
     assert rel(h, href) < 1e-5
     # d/dr of the basis: relative to the largest entry; near r -> 0 the Bessel slope is large
     assert rel(gr, grr) < 1e-5
+
+
+@pytest.mark.parametrize("P", [23, 17, 64, 1])
+def test_radial_mlp_with_last_linear(P):
+    from fsctep_amd import ops
+    g = torch.Generator().manual_seed(P)
+    E, rc, nb = 2049, 5.0, 8
+    r = torch.rand(E, generator=g, dtype=torch.float64) * 5.5 + 0.5
+    w0 = torch.randn(64, nb, generator=g, dtype=torch.float64) * 0.5
+    b0 = torch.randn(64, generator=g, dtype=torch.float64) * 0.1
+    w2 = torch.randn(64, 64, generator=g, dtype=torch.float64) * 0.2
+    b2 = torch.randn(64, generator=g, dtype=torch.float64) * 0.1
+    w4 = torch.randn(P, 64, generator=g, dtype=torch.float64) * 0.2
+    b4 = torch.randn(P, generator=g, dtype=torch.float64) * 0.1
+    dg = torch.randn(E, P, generator=g, dtype=torch.float64)
+    dev = lambda t: t.float().to(DEV)
+    rd = dev(r).requires_grad_(True)
+    out = torch.ops.fsctep.radial_mlp(rd, dev(w0), dev(b0), dev(w2), dev(b2), dev(w4), dev(b4), rc, 0)
+    (gr,) = torch.autograd.grad(out, rd, dev(dg))
+    rr = r.clone().requires_grad_(True)
+    ref = _hidden_ref(rr, w0, b0, w2, b2, rc, nb, "bessel") @ w4.T + b4
+    (grr,) = torch.autograd.grad(ref, rr, dg)
+    assert out.shape == (E, P)
+    assert rel(out, ref) < 1e-5 and rel(gr, grr) < 1e-5
 
 
 def _periodic_graph(N, E, seed):
@@ -103,3 +127,21 @@ def test_edge_geometry_empty_graph():
     assert n.shape == (0, 3) and r.shape == (0,)
     (gp,) = torch.autograd.grad((n.sum() + r.sum()), p, allow_unused=True)
     assert gp is None or float(gp.abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("lmax", [1, 2, 3])
+def test_edge_harmonics_match_oracle(lmax):
+    from fsctep_amd import ictd_ops
+    from oracle.ictd_ref import direction_harmonics
+    g = torch.Generator().manual_seed(lmax)
+    v = torch.randn(4097, 3, generator=g, dtype=torch.float64)
+    n = v / v.norm(dim=1, keepdim=True)
+    dY = torch.randn(4097, (lmax + 1) ** 2, generator=g, dtype=torch.float64)
+    nd = n.float().to(DEV).requires_grad_(True)
+    Y = ictd_ops.edge_harmonics(nd, lmax)
+    (gn,) = torch.autograd.grad(Y, nd, dY.float().to(DEV))
+    nr = n.clone().requires_grad_(True)
+    Yr = torch.cat([direction_harmonics(nr, l) for l in range(lmax + 1)], dim=-1)
+    (gnr,) = torch.autograd.grad(Yr, nr, dY)
+    assert Y.shape == Yr.shape
+    assert rel(Y, Yr) < 1e-6 and rel(gn, gnr) < 1e-5
