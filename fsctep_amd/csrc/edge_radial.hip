@@ -21,6 +21,7 @@ constexpr int NBMAX = 16;   // radial basis functions supported
 // emb_k(r) and d emb_k / dr for k < nb (basis 0: Bessel, 1: Gaussian), matching the device
 // formula used by the model code (bessel: sqrt(2/rc) sin(k pi r/rc)/r on (0, rc); gaussian:
 // exp(-((r - mu_k)/step)^2)/1.12 with mu_k = k*step, step = rc/(nb+1)), times sqrt(nb).
+template <bool DERIV>
 __device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int basis, float& f, float& df) {
   const float snb = sqrtf((float)nb);
   if (basis == 0) {
@@ -28,23 +29,26 @@ __device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int
     const bool inside = (r / rc < 1.f) && (r > 0.f);
     const float a = sqrtf(2.f / rc) * snb;
     const float rr = inside ? r : 1.f;
-    const float x = w * rr, s = sinf(x), c = cosf(x);
-    // d/dr sin(wr)/r = w^2 (x cos x - sin x)/x^2; below x = 0.3 the Taylor series avoids the
-    // cancellation (-x/3 + x^3/30 - x^5/840, truncation below 1e-8 relative)
-    const float x2 = x * x;
-    const float g = (x < 0.3f) ? x * (-1.f / 3.f + x2 * (1.f / 30.f - x2 * (1.f / 840.f))) : (x * c - s) / x2;
+    const float x = w * rr, s = sinf(x);
     f = inside ? a * s / rr : 0.f;
-    df = inside ? a * w * w * g : 0.f;
+    if (DERIV) {
+      // d/dr sin(wr)/r = w^2 (x cos x - sin x)/x^2; below x = 0.3 the Taylor series avoids the
+      // cancellation (-x/3 + x^3/30 - x^5/840, truncation below 1e-8 relative)
+      const float c = cosf(x), x2 = x * x;
+      const float g = (x < 0.3f) ? x * (-1.f / 3.f + x2 * (1.f / 30.f - x2 * (1.f / 840.f))) : (x * c - s) / x2;
+      df = inside ? a * w * w * g : 0.f;
+    }
   } else {
     const float step = rc / (float)(nb + 1);
     const float d = (r - (float)(k + 1) * step) / step;
     const float e = expf(-d * d) / 1.12f * snb;
     f = e;
-    df = e * (-2.f * d / step);
+    if (DERIV) df = e * (-2.f * d / step);
   }
 }
 
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
+// logistic sigmoid with the hardware exp2 and reciprocal (relative error ~1e-7)
+__device__ __forceinline__ float sigm(float x) { return __fdividef(1.f, 1.f + __expf(-x)); }
 
 // One wave per 16-edge tile; lane (r, q) works for edge e0 + r.  The hidden units are laid
 // out as the MFMA output: lane (r, q) holds unit j = 16*jt + 4*q + i in register (jt, i), so
@@ -120,12 +124,14 @@ __device__ __forceinline__ void dense64(const float (*W)[WS], const float* b, co
 
 // u0 = W0 emb + b0 and u2 = W2 silu(u0) + b2 for the lane's edge (MFMA layout above).
 template <bool BWD>
-__device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&emb)[NBMAX], int nks, int r, int q,
+__device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&emb)[NBMAX / 4], int nks, int r, int q,
                                             f4 (&u0)[4], f4 (&u2)[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < nks; ++ks) acc = mfma16x16x4(sm.w0[16 * jt + r][4 * ks + q], emb[4 * ks + q], acc);
+#pragma unroll
+    for (int ks = 0; ks < NBMAX / 4; ++ks)
+      if (ks < nks) acc = mfma16x16x4(sm.w0[16 * jt + r][4 * ks + q], emb[ks], acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] += sm.b0[16 * jt + 4 * q + i];
     u0[jt] = acc;
@@ -138,14 +144,25 @@ __device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&e
   dense64(sm.w2, sm.b2, a0, r, q, u2);
 }
 
-__device__ __forceinline__ void edge_basis(float rr, int nb, float rc, int basis, float (&emb)[NBMAX],
-                                           float (&demb)[NBMAX]) {
+// The basis values a lane feeds to the first product: emb[4*ks + q] for ks < nks (lane group q).
+__device__ __forceinline__ void lane_basis(float rr, int nb, float rc, int basis, int q, float (&emb)[NBMAX / 4]) {
 #pragma unroll
-  for (int k = 0; k < NBMAX; ++k) {
+  for (int ks = 0; ks < NBMAX / 4; ++ks) {
+    const int k = 4 * ks + q;
     float f = 0.f, df = 0.f;
-    if (k < nb) basis_eval(rr, k, nb, rc, basis, f, df);
-    emb[k] = f;
-    demb[k] = df;
+    if (k < nb) basis_eval<false>(rr, k, nb, rc, basis, f, df);
+    emb[ks] = f;
+  }
+}
+
+// d emb_k / dr for the lane's rows k = 4q + i of the d-emb tile (zero for k >= nb).
+__device__ __forceinline__ void lane_basis_deriv(float rr, int nb, float rc, int basis, int q, float (&demb)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = 4 * q + i;
+    float f = 0.f, df = 0.f;
+    if (k < nb) basis_eval<true>(rr, k, nb, rc, basis, f, df);
+    demb[i] = df;
   }
 }
 
@@ -164,8 +181,8 @@ __global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __
   for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
     const int64_t e = 16 * t + r;
     const float rr = (e < n_edges) ? rad[e] : 1.f;
-    float emb[NBMAX], demb[NBMAX];
-    edge_basis(rr, nb, rc, basis, emb, demb);
+    float emb[NBMAX / 4];
+    lane_basis(rr, nb, rc, basis, q, emb);
     f4 u0[4], u2[4], a2[4];
     mlp_forward(sm, emb, nks, r, q, u0, u2);
 #pragma unroll
@@ -209,8 +226,9 @@ __global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* _
     const int64_t e = 16 * t + r;
     const bool ok = e < n_edges;
     const float rr = ok ? rad[e] : 1.f;
-    float emb[NBMAX], demb[NBMAX];
-    edge_basis(rr, nb, rc, basis, emb, demb);
+    float emb[NBMAX / 4], demb[4];
+    lane_basis(rr, nb, rc, basis, q, emb);
+    lane_basis_deriv(rr, nb, rc, basis, q, demb);
     f4 u0[4], u2[4];
     mlp_forward(sm, emb, nks, r, q, u0, u2);
     f4 dh[4];
@@ -255,14 +273,7 @@ __global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* _
     }
     float part = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = 4 * q + i;
-      float dd = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < NBMAX; ++kk)
-        if (kk == k) dd = demb[kk];
-      part += de[i] * dd;
-    }
+    for (int i = 0; i < 4; ++i) part += de[i] * demb[i];
     part += __shfl_xor(part, 16, 64);
     part += __shfl_xor(part, 32, 64);
     if (ok && q == 0) dr[e] = part;
@@ -446,7 +457,8 @@ int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* gr
 
 static unsigned radial_grid(int64_t n_edges) {
   const int64_t tiles = (n_edges + 15) / 16;
-  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + 3) / 4, 2048));
+  // about two blocks per CU: the weights are staged in LDS once per block
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + 3) / 4, 512));
 }
 
 int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
