@@ -12,7 +12,7 @@
 //   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
 // with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  The backward is
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
-// computed per (64-node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
+// computed per (128-node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
 // the diagonal.  Layouts: t [N][D][nC], W [S][nC][nC], out/grad_out [N][S].
 
@@ -22,7 +22,7 @@
 namespace fsc {
 namespace gram {
 
-constexpr int NODES = 64;    // nodes per workgroup (4 waves x 16 MFMA rows)
+constexpr int NODES = 128;   // nodes per workgroup (8 waves x 16 MFMA rows)
 constexpr int PCHUNK = 8;    // block pairs per forward workgroup
 
 __host__ __device__ inline int n_pairs(int nb) { return nb * (nb + 1) / 2; }
@@ -52,40 +52,50 @@ __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float
   }
 }
 
-// Forward partial sums over PCHUNK block pairs: part[chunk][n][o].
+// Forward partial sums over PCHUNK block pairs: part[chunk][n][o].  A workgroup is 128 nodes (8 waves x
+// 16 MFMA rows) x one chunk; each pair's Wf block [il][o][jl] (256*S floats) is staged in LDS and shared
+// by the 8 waves, the next pair's block is loaded into registers while the current one is multiplied.
 template <int D, int S>
-__global__ __launch_bounds__(256) void forward_kernel(int64_t N, int nC, float scale, const float* __restrict__ t,
-                                                      const float* __restrict__ Wf, int nchunks,
-                                                      float* __restrict__ part) {
-  constexpr int CT = S / 16;
+__global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float scale, const float* __restrict__ t,
+                                           const float* __restrict__ Wf, int nchunks, float* __restrict__ part) {
+  constexpr int NN = NODES, CT = S / 16;
+  constexpr int WBF4 = 256 * S / 4, PW = (WBF4 + 511) / 512;
+  __shared__ f4 wl[WBF4];
   const int nb = nC / 16, np = n_pairs(nb);
-  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nchunks * ntiles);
   if (logical < 0) return;
   const int chunk = logical / ntiles, tile = logical - chunk * ntiles;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int64_t n = (int64_t)tile * NODES + wave * 16 + r;
+  const int64_t n = (int64_t)tile * NN + wave * 16 + r;
   const bool valid = n < N;
   const float* tn = t + (valid ? n : 0) * D * nC;
-
   const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
   int I = 0, rowstart = 0;
-  while (rowstart + (nb - I) <= p0) {
-    rowstart += nb - I;
-    ++I;
-  }
+  while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
   int J = I + (p0 - rowstart);
-
   f4 acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) acc[ct] = f4{0.f, 0.f, 0.f, 0.f};
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  f4 pw[PW];
+  auto fetch = [&](int p) {
+    const f4* src = reinterpret_cast<const f4*>(Wf + (int64_t)p * 256 * S);
+#pragma unroll
+    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) pw[i] = src[idx]; }
+  };
+  fetch(p0);
   for (int p = p0; p < p1; ++p) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) wl[idx] = pw[i]; }
+    __syncthreads();
+    if (p + 1 < p1) fetch(p + 1);
     f4 tj[D];
 #pragma unroll
     for (int m = 0; m < D; ++m) tj[m] = valid ? ld4(tn + m * nC + J * 16 + 4 * q) : zero;
-    const float* wp = Wf + (int64_t)p * 16 * S * 16 + r * 16 + 4 * q;
+    const float* wp = reinterpret_cast<const float*>(wl) + r * 16 + 4 * q;
 #pragma unroll 1
     for (int ig = 0; ig < 4; ++ig) {
       f4 ti[D];
@@ -99,17 +109,15 @@ __global__ __launch_bounds__(256) void forward_kernel(int64_t N, int nC, float s
         for (int m = 0; m < D; ++m) a += ti[m][ii] * tj[m];
         a *= scale;
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_k16(a, ld4(wp + ((int64_t)il * S + ct * 16) * 16), acc[ct]);
+        for (int ct = 0; ct < CT; ++ct)
+          acc[ct] = mfma_k16(a, *reinterpret_cast<const f4*>(wp + (il * S + ct * 16) * 16), acc[ct]);
       }
     }
-    if (++J == nb) {
-      ++I;
-      J = I;
-    }
+    if (++J == nb) { ++I; J = I; }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t node = (int64_t)tile * NODES + wave * 16 + 4 * q + i;
+    const int64_t node = (int64_t)tile * NN + wave * 16 + 4 * q + i;
     if (node >= N) continue;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 16 + r] = acc[ct][i];
@@ -125,24 +133,29 @@ __global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__
   }
 }
 
-// Backward: one workgroup per (64-node tile, row block I); dt[n][m][I0 + il] complete after the J loop.
+// Backward: one workgroup per (128-node tile, row block I), 8 waves x 16 nodes; dt[n][m][I0 + il] is
+// complete after the J loop.  Per J the (I,J) block of (W + W^T) [a][b][o] and t[node][m][J0..J0+15] are
+// staged in LDS (shared by the 8 waves); the next J is loaded into registers meanwhile.
 template <int D, int S>
-__global__ __launch_bounds__(256) void backward_kernel(int64_t N, int nC, float scale,
-                                                       const float* __restrict__ g, const float* __restrict__ t,
-                                                       const float* __restrict__ Wb, float* __restrict__ dt) {
-  __shared__ __align__(16) float ts[NODES * D * 16];     // t[node][m][J0 .. J0+15] of the current J
-  constexpr int KT = S / 16;
+__global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float scale, const float* __restrict__ g,
+                                           const float* __restrict__ t, const float* __restrict__ Wb,
+                                           float* __restrict__ dt) {
+  constexpr int NN = NODES, KT = S / 16;
+  constexpr int WBF4 = 256 * S / 4;            // float4 of one Wb block
+  constexpr int TSF4 = NN * D * 4;             // float4 of the t tile
+  constexpr int PW = (WBF4 + 511) / 512, PT = (TSF4 + 511) / 512;
+  __shared__ f4 wb[WBF4];
+  __shared__ f4 ts[TSF4];
   const int nb = nC / 16;
-  const int ntiles = (int)((N + NODES - 1) / NODES);
+  const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nb * ntiles);
-  if (logical < 0) return;                                // uniform over the block
+  if (logical < 0) return;
   const int I = logical / ntiles, tile = logical - I * ntiles;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int64_t n = (int64_t)tile * NODES + wave * 16 + r;
+  const int64_t n = (int64_t)tile * NN + wave * 16 + r;
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
-
-  f4 ga[KT];                                              // A operand: g[n_r][o], K = o
+  f4 ga[KT];
 #pragma unroll
   for (int k = 0; k < KT; ++k) ga[k] = (n < N) ? ld4(g + n * S + 16 * k + 4 * q) : zero;
   float acc[4][D];
@@ -150,27 +163,35 @@ __global__ __launch_bounds__(256) void backward_kernel(int64_t N, int nC, float 
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int m = 0; m < D; ++m) acc[i][m] = 0.f;
-  const float* tsw = ts + (wave * 16 + 4 * q) * D * 16;   // this lane's 4 output nodes
-
+  f4 pw[PW], pt[PT];
+  auto fetch = [&](int J) {
+    const int pr = (I <= J) ? pair_index(I, J, nb) : pair_index(J, I, nb);
+    const f4* src = reinterpret_cast<const f4*>(Wb + (int64_t)pr * 256 * S);
+#pragma unroll
+    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) pw[i] = src[idx]; }
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int idx = threadIdx.x + 512 * i;
+      if (idx < TSF4) {
+        const int nl = idx / (D * 4), rem = idx - nl * (D * 4), m = rem >> 2, c4 = rem & 3;
+        const int64_t nn = (int64_t)tile * NN + nl;
+        pt[i] = (nn < N) ? ld4(t + (nn * D + m) * nC + J * 16 + 4 * c4) : zero;
+      }
+    }
+  };
+  fetch(0);
   for (int J = 0; J < nb; ++J) {
     __syncthreads();
-    for (int idx = threadIdx.x; idx < NODES * D * 4; idx += blockDim.x) {
-      const int nl = idx / (D * 4), rem = idx - nl * (D * 4);
-      const int m = rem >> 2, c4 = rem & 3;
-      const int64_t nn = (int64_t)tile * NODES + nl;
-      reinterpret_cast<f4*>(ts)[idx] = (nn < N) ? ld4(t + (nn * D + m) * nC + J * 16 + 4 * c4) : zero;
-    }
+#pragma unroll
+    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) wb[idx] = pw[i]; }
+#pragma unroll
+    for (int i = 0; i < PT; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < TSF4) ts[idx] = pt[i]; }
     __syncthreads();
-    // B[k = o][col = il = r] = (W + W^T)[o][I0 + r][J0 + jl]
-    const float* bp;
-    int bstride;
-    if (I <= J) {
-      bp = Wb + ((int64_t)pair_index(I, J, nb) * 256 + r * 16) * S + 4 * q;
-      bstride = S;                                         // + jl * S
-    } else {
-      bp = Wb + ((int64_t)pair_index(J, I, nb) * 256 + r) * S + 4 * q;
-      bstride = 16 * S;                                    // + jl * 16 * S
-    }
+    if (J + 1 < nb) fetch(J + 1);
+    // B[k = o][col = il] = (W + W^T)[o][I0 + il][J0 + jl]; I <= J: block [a = il][b = jl][o], else [a = jl][b = il][o]
+    const float* wbf = reinterpret_cast<const float*>(wb);
+    const int st_il = (I <= J) ? 16 * S : S, st_jl = (I <= J) ? S : 16 * S;
+    const float* tsw = reinterpret_cast<const float*>(ts) + (wave * 16 + 4 * q) * D * 16;
 #pragma unroll 1
     for (int jl4 = 0; jl4 < 4; ++jl4) {
       f4 dd[4];
@@ -180,8 +201,7 @@ __global__ __launch_bounds__(256) void backward_kernel(int64_t N, int nC, float 
       for (int k = 0; k < KT; ++k)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
-          dd[jj] = mfma_k16(ga[k], ld4(bp + (int64_t)(4 * jl4 + jj) * bstride + 16 * k), dd[jj]);
-      // dd[jj][i] = A[n_{4q+i}][I0 + r][J0 + 4 jl4 + jj]
+          dd[jj] = mfma_k16(ga[k], *reinterpret_cast<const f4*>(wbf + r * st_il + (4 * jl4 + jj) * st_jl + 16 * k + 4 * q), dd[jj]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -193,7 +213,7 @@ __global__ __launch_bounds__(256) void backward_kernel(int64_t N, int nC, float 
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t node = (int64_t)tile * NODES + wave * 16 + 4 * q + i;
+    const int64_t node = (int64_t)tile * NN + wave * 16 + 4 * q + i;
     if (node >= N) continue;
 #pragma unroll
     for (int m = 0; m < D; ++m) dt[(node * D + m) * nC + I * 16 + r] = acc[i][m] * scale;
@@ -217,7 +237,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
   {
     LaunchTimer tm("gram_forward", st);
-#define FSC_GF(DD) forward_kernel<DD, S><<<grid, 256, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
+#define FSC_GF(DD) forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
     switch (D) {
       case 1: FSC_GF(1); break;
       case 3: FSC_GF(3); break;
@@ -239,7 +259,7 @@ int backward_s(int64_t N, int D, int nC, float scale, const float* g, const floa
   const int ntiles = (int)((N + NODES - 1) / NODES);
   const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
   LaunchTimer tm("gram_backward", st);
-#define FSC_GB(DD) backward_kernel<DD, S><<<grid, 256, 0, st>>>(N, nC, scale, g, t, Wb, dt)
+#define FSC_GB(DD) backward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt)
   switch (D) {
     case 1: FSC_GB(1); break;
     case 3: FSC_GB(3); break;
