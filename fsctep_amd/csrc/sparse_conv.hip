@@ -18,7 +18,8 @@
 //
 // Layouts (fp32): node features x[N][13][C] (comp-major: 0 | 1..3 = i | 4..12 = 3i+j);
 // S[N][18][65*C]: per slot a row of C*64 (c-major, k-minor) then C bias entries;
-// P[E][18*C] at the receiver-sorted edge id; h[E][64]; n[E][3] (unit vectors).
+// P[E][C/8][18][8] at the receiver-sorted edge id (channel chunks of 8, slot-major inside a chunk, so
+// that a chunk of the backward reads one contiguous block per edge); h[E][64]; n[E][3] (unit vectors).
 
 #include "common.h"
 
@@ -288,9 +289,9 @@ __global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, f
 // ---------------------------------------------------------------- K2: edge message
 // One block (3 waves) per source node; P[eid][col] = sum_k h[eid][k] S[m][col][k] + Sb[m][col].
 // Transposed product: S rows (columns of P) are the A operand, the node's edges (h rows,
-// staged in LDS) the B operand.  A wave takes 32-column blocks; tile jt's A row i is column
-// 8*(i/4) + 4*jt + i%4 of the block, so lane (r, q) ends with 8 consecutive columns of
-// edge r: two float4 stores.
+// staged in LDS) the B operand.  A wave takes 32-column blocks of P's chunk-major column order;
+// tile jt's A row i is column 8*(i/4) + 4*jt + i%4 of the block, so lane (r, q) ends with 8
+// consecutive columns of edge r: two float4 stores, 128 contiguous bytes per edge per block.
 constexpr int EP = 64;   // edges per pass held in LDS
 
 template <int C>
@@ -315,15 +316,18 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
   // a[jt][0..3]: S row of A row r of tile jt (K = 64); a[jt][4]: the biases of the lane's four
   // output columns of tile jt.  Column block cb+3 is loaded while block cb is multiplied.
   f4 a0[NJ][5], a1[NJ][5];
+  // Columns are numbered in P's chunk-major order: col = ch*144 + slot*8 + cl for channel c = 8*ch + cl.
   auto load = [&](f4 (&a)[NJ][5], int cb) {
 #pragma unroll
     for (int jt = 0; jt < NJ; ++jt) {
       const int col = cb * BW + 4 * NJ * (r >> 2) + 4 * jt + (r & 3);
-      const float* srow = Sm + (int64_t)(col / C) * COLS + (col % C) * KH + 4 * q;
+      const int rem = col % (8 * NSLOT), slot = rem / 8, c = 8 * (col / (8 * NSLOT)) + rem % 8;
+      const float* srow = Sm + (int64_t)slot * COLS + c * KH + 4 * q;
 #pragma unroll
       for (int t = 0; t < 4; ++t) a[jt][t] = ld4(srow + 16 * t);
-      const int colq = cb * BW + 4 * NJ * q + 4 * jt;
-      a[jt][4] = ld4(Sm + (int64_t)(colq / C) * COLS + 64 * C + (colq % C));
+      const int colq = cb * BW + 4 * NJ * q + 4 * jt;   // four consecutive channels of one slot
+      const int remq = colq % (8 * NSLOT);
+      a[jt][4] = ld4(Sm + (int64_t)(remq / 8) * COLS + 64 * C + 8 * (colq / (8 * NSLOT)) + remq % 8);
     }
   };
 
@@ -409,19 +413,19 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
   for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg + sub; e < end; e += EPW) {
-    const float* pr = P + (int64_t)e * (NSLOT * C) + c;
+    const float* pr = P + (int64_t)e * (NSLOT * C) + (c / 8) * (8 * NSLOT) + (c % 8);   // + 8 * slot
     const float n0 = nvec[3 * (int64_t)e], n1 = nvec[3 * (int64_t)e + 1], n2 = nvec[3 * (int64_t)e + 2];
     const float nn[3] = {n0, n1, n2};
-    const float p0 = pr[0], p1 = pr[C], p2 = pr[2 * C];
+    const float p0 = pr[0], p1 = pr[8], p2 = pr[2 * 8];
     o[0] += p0;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + pr[(3 + i) * C];
+    for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + pr[(3 + i) * 8];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      const float p4 = pr[(6 + i) * C];
+      const float p4 = pr[(6 + i) * 8];
       const float p2ni = p2 * nn[i];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + pr[(9 + 3 * i + j) * C];
+      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + pr[(9 + 3 * i + j) * 8];
     }
   }
   if (EPW > 1) {
@@ -437,7 +441,8 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------- K5: edge message grad
-// One block per source node.  With g = G[dst(e)] * scale, the message gradient is
+// One block per source node; the receiver gradient comes chunk-major (grad_chunk_major_kernel).
+// With g = G[dst(e)] * scale, the message gradient is
 //   dP_e[0] = g0, dP_e[1] = g1.n, dP_e[2] = n.g2.n, dP_e[3+i] = g1[i],
 //   dP_e[6+i] = (g2 n)[i], dP_e[9+ij] = g2[ij]
 // (per channel).  Per chunk of CC channels the block writes dP for its edges into LDS, then
@@ -447,12 +452,22 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
 // and the direction gradient of the receiver assembly (m1 = P1 n + P3, m2 = P2 n n + P4 n + P5)
 //   dn_e[k] = sum_c g1[k] P1 + P2 ((g2 n)[k] + (g2^T n)[k]) + (g2^T P4)[k]
 // is summed over the chunk's channels by lane shuffles and over chunks in a fixed order.
+// The receiver gradient in channel chunks: Gt[c/8][n][comp][c%8] = G[n][comp][c].
+template <int C>
+__global__ void grad_chunk_major_kernel(const float* __restrict__ G, float* __restrict__ Gt, int64_t n_nodes) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // float4 of G
+  if (idx >= n_nodes * NCOMP * (C / 4)) return;
+  const int c4 = (int)(idx % (C / 4));
+  const int64_t row = idx / (C / 4);                                    // n*13 + comp
+  st4(Gt + ((int64_t)(c4 / 2) * n_nodes * NCOMP + row) * 8 + 4 * (c4 % 2), ld4(G + row * C + 4 * c4));
+}
+
 template <int C>
 __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
-    const float* __restrict__ G, const float* __restrict__ nvec, const float* __restrict__ h,
+    const float* __restrict__ Gt, const float* __restrict__ nvec, const float* __restrict__ h,
     const float* __restrict__ S, const float* __restrict__ P, const int32_t* __restrict__ src_ptr,
     const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst, float scale,
-    float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn) {
+    float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, int64_t n_nodes) {
   constexpr int CC = 8;              // channels per chunk
   constexpr int NCH = C / CC;
   constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
@@ -526,15 +541,16 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int e = eb + 32 * hh;
-        const float* gp = G + (int64_t)dsts[e] * NCOMP * C + ch * CC + cl;
+        // Gt[ch][dst][13][8]: the chunk's 13 components of the receiver gradient are contiguous
+        const float* gp = Gt + ((int64_t)ch * n_nodes + dsts[e]) * (NCOMP * CC) + cl;
 #pragma unroll
-        for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * C];
-        const float* pp = P + (int64_t)eids[e] * NCOL + ch * CC + cl;
-        pN[hh][0] = pp[C];
-        pN[hh][1] = pp[2 * C];
-        pN[hh][2] = pp[6 * C];
-        pN[hh][3] = pp[7 * C];
-        pN[hh][4] = pp[8 * C];
+        for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * CC];
+        const float* pp = P + (int64_t)eids[e] * NCOL + ch * (NSLOT * CC) + cl;
+        pN[hh][0] = pp[1 * CC];
+        pN[hh][1] = pp[2 * CC];
+        pN[hh][2] = pp[6 * CC];
+        pN[hh][3] = pp[7 * CC];
+        pN[hh][4] = pp[8 * CC];
       }
     };
     auto load_s = [&](int ch) {
@@ -900,17 +916,21 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        const float* P, float scale, float* dS, float* dx, float* dh, float* dn,
                        hipStream_t st) {
   if (N == 0) return 0;
+  // workspace tail (2 x 18 x N x C floats): first the chunk-major receiver gradient (13 x N x C), later
+  // the partial input gradients of node_expand_grad
+  float* tail = dS + N * s_node_stride(C);
+  grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   {
     LaunchTimer tm("edge_message_grad", st);
-    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(G, nvec, h, S, P, src_ptr, src_perm,
-                                                             edge_dst, scale, dh, dS, dn);
+    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(tail, nvec, h, S, P, src_ptr, src_perm,
+                                                             edge_dst, scale, dh, dS, dn, N);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
   {
     PathTiles tiles;
     tiles.off[0] = 0;
     for (int p = 0; p < 6; ++p) tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + 63) / 64);
-    float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums
+    float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums (Gt is dead)
     {
       LaunchTimer tm("node_expand_grad", st);
       node_expand_grad_kernel<C><<<(unsigned)((2 * tiles.off[6] + 3) / 4), 256, 0, st>>>(dS, bk6, dxp, N, tiles);
