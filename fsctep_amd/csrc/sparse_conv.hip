@@ -167,33 +167,39 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 // ---------------------------------------------------------------- K6: node expansion grad
 // dxp[kh][slot][m][a] = sum_{col in half kh} dS[m][slot][col] * bk6[p][a][col] for every slot
 // row (m, I) of path p, then dx[m][comp][a] = sum over the halves and the slots of comp
-// (node_expand_grad_combine).  A wave's work unit is (path, 64-row tile, K half): all units
-// are equally long, which keeps the waves balanced although paths 0-2 share component 0.
+// (node_expand_grad_combine).  A block's work unit is (path, 256-row tile, K half), one 64-row
+// strip per wave: all units are equally long, which keeps the blocks balanced although paths
+// 0-2 share component 0.  The four waves share the path's weights: each 32-column chunk of bk6
+// (C x 32) is loaded once per block into LDS (double-buffered) while the waves stream their own
+// dS rows, so a wave's loads are its dS strip and a quarter of the weight chunk.
 // Transposed product: bk6 rows (a) are the A operand, dS rows the B operand; tile at's A row
 // i is a = (C/4)*(i/4) + 4*at + i%4, so lane (r, q) ends with C/4 consecutive a of one row.
-// K runs in chunks of 32 (lane group q reads 8 consecutive floats of both operands); chunk
-// t+1 is loaded while chunk t is multiplied.
+// Chunk t+1 (dS in registers, bk6 via registers into the other LDS buffer) is loaded while
+// chunk t is multiplied.
+constexpr int NEG_ROWS = 256;   // slot rows per block
+
 template <int C>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
                                                                   const float* __restrict__ bk6,
                                                                   float* __restrict__ dxp,
                                                                   int64_t n_nodes, PathTiles tiles) {
   constexpr int COLS = 65 * C;
-  constexpr int NA = C / 16;     // output a tiles
-  constexpr int QW = C / 4;      // consecutive a per lane in the output
-  constexpr int TPP = COLS / 32; // K chunks per path
+  constexpr int NA = C / 16;        // output a tiles
+  constexpr int QW = C / 4;         // consecutive a per lane in the output
+  constexpr int TPP = COLS / 32;    // K chunks per path
+  constexpr int NST = C * 8 / 256;  // float4 of a bk6 chunk per thread
+  static_assert(NST >= 1 && C * 8 % 256 == 0, "bk6 chunk staging assumes C % 32 == 0");
+  __shared__ f4 wsh[2][C][9];       // [buffer][a][4 consecutive K]; 9 avoids bank conflicts
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int wu = blockIdx.x * 4 + wave;
-  if (wu >= 2 * tiles.off[6]) return;   // whole wave
-  const int kh = wu & 1, wt = wu >> 1;
+  const int kh = blockIdx.x & 1, bt = blockIdx.x >> 1;
   int p = 0;
-  while (p < 5 && wt >= tiles.off[p + 1]) ++p;
+  while (p < 5 && bt >= tiles.off[p + 1]) ++p;
   const int L1 = kPathL1[p];
   const int nI = (L1 == 0) ? 1 : (L1 == 1 ? 3 : 9);
   const int sbase = kSlotBase[p];
   const int64_t rows = n_nodes * nI;
-  const int64_t row0 = (int64_t)(wt - tiles.off[p]) * 64;
+  const int64_t row0 = (int64_t)(bt - tiles.off[p]) * NEG_ROWS + wave * 64;
 
   bool ok[4];
   int64_t rbase[4], mrow[4];
@@ -202,17 +208,14 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   for (int rt = 0; rt < 4; ++rt) {
     int64_t row = row0 + 16 * rt + r;
     ok[rt] = row < rows;
-    if (!ok[rt]) row = row0;   // a valid row; its result is not stored
+    if (!ok[rt]) row = 0;   // a valid row; its result is not stored
     const int64_t m = (uint32_t)row / (uint32_t)nI;
     const int I = (int)(row - m * nI);
     mrow[rt] = m;
     irow[rt] = I;
     rbase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 8 * q;
   }
-  int64_t abase[NA];
-#pragma unroll
-  for (int at = 0; at < NA; ++at)
-    abase[at] = ((int64_t)p * C + QW * (r >> 2) + 4 * at + (r & 3)) * COLS + 8 * q;
+  const float* wp = bk6 + (int64_t)p * C * COLS;
   f4 acc[4][NA];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
@@ -220,37 +223,56 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
     for (int at = 0; at < NA; ++at) acc[rt][at] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int tb = kh ? TPP / 2 : 0, te = kh ? TPP : TPP / 2;
-  f4 b0[4][2], a0[NA][2], b1[4][2], a1[NA][2];
-  auto load = [&](f4 (&b)[4][2], f4 (&a)[NA][2], int t) {
-    const int64_t k0 = 32 * (int64_t)t;
+  f4 stg[NST], bc[4][2], bn[4][2];
+  auto load_w = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      stg[i] = ld4(wp + (int64_t)(idx >> 3) * COLS + 32 * t + 4 * (idx & 7));
+    }
+  };
+  auto store_w = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      wsh[buf][idx >> 3][idx & 7] = stg[i];
+    }
+  };
+  auto load_ds = [&](f4 (&b)[4][2], int t) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) b[rt][u] = ld4(dS + rbase[rt] + k0 + 4 * u);
-#pragma unroll
-    for (int at = 0; at < NA; ++at)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) a[at][u] = ld4(bk6 + abase[at] + k0 + 4 * u);
+      for (int u = 0; u < 2; ++u) b[rt][u] = ld4(dS + rbase[rt] + 32 * t + 4 * u);
   };
-  auto mul = [&](const f4 (&b)[4][2], const f4 (&a)[NA][2]) {
+  load_w(tb);
+  load_ds(bc, tb);
+  store_w(0);
+  __syncthreads();
+#pragma unroll 1
+  for (int t = tb; t < te; ++t) {
+    const int buf = (t - tb) & 1;
+    if (t + 1 < te) {
+      load_w(t + 1);
+      load_ds(bn, t + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+      for (int at = 0; at < NA; ++at) {
+        const f4 a4 = wsh[buf][QW * (r >> 2) + 4 * at + (r & 3)][2 * q + u];
 #pragma unroll
-        for (int at = 0; at < NA; ++at) acc[rt][at] = mfma_k16(a[at][u], b[rt][u], acc[rt][at]);
-  };
-  load(b0, a0, tb);
-#pragma unroll 1
-  for (int t = tb; t < te; t += 2) {
-    if (t + 1 < te) load(b1, a1, t + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mul(b0, a0);
+        for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_k16(a4, bc[rt][u], acc[rt][at]);
+      }
     if (t + 1 < te) {
-      if (t + 2 < te) load(b0, a0, t + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      mul(b1, a1);
+      store_w(buf ^ 1);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        bc[rt][0] = bn[rt][0];
+        bc[rt][1] = bn[rt][1];
+      }
     }
+    __syncthreads();
   }
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
@@ -929,11 +951,12 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
   {
     PathTiles tiles;
     tiles.off[0] = 0;
-    for (int p = 0; p < 6; ++p) tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + 63) / 64);
+    for (int p = 0; p < 6; ++p)
+      tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + NEG_ROWS - 1) / NEG_ROWS);
     float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums (Gt is dead)
     {
       LaunchTimer tm("node_expand_grad", st);
-      node_expand_grad_kernel<C><<<(unsigned)((2 * tiles.off[6] + 3) / 4), 256, 0, st>>>(dS, bk6, dxp, N, tiles);
+      node_expand_grad_kernel<C><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(dS, bk6, dxp, N, tiles);
     }
     if (check_launch("sparse node_expand_grad")) return 2;
     node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N);
