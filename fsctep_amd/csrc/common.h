@@ -29,6 +29,18 @@ __device__ __forceinline__ f4 mfma_k16(const f4& a, const f4& b, f4 acc) {
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ void st4(float* p, const f4& v) { *reinterpret_cast<f4*>(p) = v; }
 
+// Raw buffer descriptor over [base, base + bytes) (bytes < 2^32).  A vector buffer store whose
+// byte offset lies outside the range is dropped by the hardware, which lets a kernel store
+// unconditionally and send the lanes of out-of-range rows to kDropOffset instead of branching.
+constexpr uint32_t kDropOffset = 0xF0000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off, const f4& v) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rsrc, (int)byte_off, 0, 0);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

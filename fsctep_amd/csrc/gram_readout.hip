@@ -12,7 +12,7 @@
 //   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
 // with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  The backward is
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
-// computed per (128-node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
+// computed per (node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
 // the diagonal.  Layouts: t [N][D][nC], W [S][nC][nC], out/grad_out [N][S].
 
@@ -35,6 +35,18 @@ __device__ __forceinline__ int xcd_logical(int nwg) {
   const int w = blockIdx.x;
   const int logical = (w & 7) * per + (w >> 3);
   return logical < nwg ? logical : -1;
+}
+
+// Forward work order: groups of TILE_GROUP node tiles, and within a group all pair chunks of its
+// tiles with the tiles innermost.  Workgroups that run together on an XCD then share both the
+// weight chunk (read by the group's tiles) and the t rows of the group, which stay in its L2.
+constexpr int TILE_GROUP = 4;
+__device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles, int& chunk, int& tile) {
+  const int grp = logical / (TILE_GROUP * nchunks);
+  const int gsize = min(TILE_GROUP, ntiles - grp * TILE_GROUP);
+  const int rem = logical - grp * TILE_GROUP * nchunks;
+  chunk = rem / gsize;
+  tile = grp * TILE_GROUP + (rem - chunk * gsize);
 }
 
 // Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).
@@ -65,7 +77,8 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
   const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nchunks * ntiles);
   if (logical < 0) return;
-  const int chunk = logical / ntiles, tile = logical - chunk * ntiles;
+  int chunk, tile;
+  group_order(logical, nchunks, ntiles, chunk, tile);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int64_t n = (int64_t)tile * NN + wave * 16 + r;
@@ -133,19 +146,24 @@ __global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__
   }
 }
 
-// Backward: one workgroup per (128-node tile, row block I), 8 waves x 16 nodes; dt[n][m][I0 + il] is
-// complete after the J loop.  Per J the (I,J) block of (W + W^T) [a][b][o] and t[node][m][J0..J0+15] are
-// staged in LDS (shared by the 8 waves); the next J is loaded into registers meanwhile.
-template <int D, int S>
+// Backward: one workgroup per (node tile, row block I); a wave takes 16 nodes x ILW rows il of the
+// block (ILW = 16: 128 nodes per workgroup, ILW = 8: two waves per node group, 64 nodes).  Per J the
+// (I,J) block of (W + W^T) [a][b][o] is staged in LDS (rows padded so both the direct and the
+// transposed reads are free of bank conflicts) and shared by the 8 waves; the next J's block and
+// t rows are loaded into registers meanwhile.  The MFMA takes A = (W + W^T) rows jl (K = o) and
+// B = g of the wave's 16 nodes, so lane (r = node, q) ends with A_n[il][4q..4q+3] and contracts
+// it on the VALU with its own t[n][m][J0+4q..J0+4q+3]; the partial sums over q are reduced once,
+// after the J loop, with a butterfly that leaves lane q the rows il of its quarter.
+template <int D, int S, int ILW>
 __global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float scale, const float* __restrict__ g,
                                            const float* __restrict__ t, const float* __restrict__ Wb,
                                            float* __restrict__ dt) {
-  constexpr int NN = NODES, KT = S / 16;
-  constexpr int WBF4 = 256 * S / 4;            // float4 of one Wb block
-  constexpr int TSF4 = NN * D * 4;             // float4 of the t tile
-  constexpr int PW = (WBF4 + 511) / 512, PT = (TSF4 + 511) / 512;
-  __shared__ f4 wb[WBF4];
-  __shared__ f4 ts[TSF4];
+  constexpr int NGRP = 16 / ILW;                 // waves sharing a node group
+  constexpr int NN = 16 * 8 / NGRP;              // nodes per workgroup
+  constexpr int KT = S / 16;
+  constexpr int RS = S + 4, AS = 16 * RS + 4;    // padded LDS strides of b and a (floats)
+  constexpr int PW = 256 * S / 4 / 512;          // float4 of a Wb block per thread
+  __shared__ float wl[16 * AS];
   const int nb = nC / 16;
   const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nb * ntiles);
@@ -153,70 +171,88 @@ __global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float 
   const int I = logical / ntiles, tile = logical - I * ntiles;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int64_t n = (int64_t)tile * NN + wave * 16 + r;
+  const int il0 = (wave % NGRP) * ILW;
+  const int64_t n = (int64_t)tile * NN + (wave / NGRP) * 16 + r;
+  const bool valid = n < N;
+  const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
   f4 ga[KT];
 #pragma unroll
-  for (int k = 0; k < KT; ++k) ga[k] = (n < N) ? ld4(g + n * S + 16 * k + 4 * q) : zero;
-  float acc[4][D];
+  for (int k = 0; k < KT; ++k) ga[k] = valid ? ld4(g + n * S + 16 * k + 4 * q) : zero;
+  float acc[ILW][D];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < ILW; ++i)
 #pragma unroll
     for (int m = 0; m < D; ++m) acc[i][m] = 0.f;
-  f4 pw[PW], pt[PT];
+  f4 pw[PW], tq[D];
   auto fetch = [&](int J) {
     const int pr = (I <= J) ? pair_index(I, J, nb) : pair_index(J, I, nb);
     const f4* src = reinterpret_cast<const f4*>(Wb + (int64_t)pr * 256 * S);
 #pragma unroll
-    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) pw[i] = src[idx]; }
+    for (int i = 0; i < PW; ++i) pw[i] = src[threadIdx.x + 512 * i];
 #pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      const int idx = threadIdx.x + 512 * i;
-      if (idx < TSF4) {
-        const int nl = idx / (D * 4), rem = idx - nl * (D * 4), m = rem >> 2, c4 = rem & 3;
-        const int64_t nn = (int64_t)tile * NN + nl;
-        pt[i] = (nn < N) ? ld4(t + (nn * D + m) * nC + J * 16 + 4 * c4) : zero;
-      }
-    }
+    for (int m = 0; m < D; ++m) tq[m] = ld4(t + (nl * D + m) * nC + J * 16 + 4 * q);
   };
   fetch(0);
   for (int J = 0; J < nb; ++J) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < PW; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < WBF4) wb[idx] = pw[i]; }
-#pragma unroll
-    for (int i = 0; i < PT; ++i) { const int idx = threadIdx.x + 512 * i; if (idx < TSF4) ts[idx] = pt[i]; }
+    for (int i = 0; i < PW; ++i) {
+      const int idx = threadIdx.x + 512 * i;   // float4 index in [a][b][o]
+      const int o4 = idx % (S / 4), ab = idx / (S / 4);
+      *reinterpret_cast<f4*>(&wl[(ab >> 4) * AS + (ab & 15) * RS + 4 * o4]) = pw[i];
+    }
     __syncthreads();
-    if (J + 1 < nb) fetch(J + 1);
-    // B[k = o][col = il] = (W + W^T)[o][I0 + il][J0 + jl]; I <= J: block [a = il][b = jl][o], else [a = jl][b = il][o]
-    const float* wbf = reinterpret_cast<const float*>(wb);
-    const int st_il = (I <= J) ? 16 * S : S, st_jl = (I <= J) ? S : 16 * S;
-    const float* tsw = reinterpret_cast<const float*>(ts) + (wave * 16 + 4 * q) * D * 16;
-#pragma unroll 1
-    for (int jl4 = 0; jl4 < 4; ++jl4) {
-      f4 dd[4];
+    f4 tc[D];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dd[jj] = zero;
+    for (int m = 0; m < D; ++m) tc[m] = tq[m];
+    if (J + 1 < nb) fetch(J + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // A[row = jl][k = o] = (W + W^T)[o][I0 + il][J0 + jl]: block [a = il][b = jl] if I <= J, else [a = jl][b = il]
+    const bool upper = I <= J;
+    const int rbase = (upper ? r * RS : r * AS) + 4 * q;
+    const int ilstep = upper ? AS : RS;
+#pragma unroll
+    for (int i4 = 0; i4 < ILW / 4; ++i4) {
+      f4 dd[4] = {zero, zero, zero, zero};
 #pragma unroll
       for (int k = 0; k < KT; ++k)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          dd[jj] = mfma_k16(ga[k], *reinterpret_cast<const f4*>(wbf + r * st_il + (4 * jl4 + jj) * st_jl + 16 * k + 4 * q), dd[jj]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int m = 0; m < D; ++m) {
-          const f4 tv = *reinterpret_cast<const f4*>(tsw + (i * D + m) * 16 + 4 * jl4);
-          acc[i][m] += dd[0][i] * tv[0] + dd[1][i] * tv[1] + dd[2][i] * tv[2] + dd[3][i] * tv[3];
+        for (int jj = 0; jj < 4; ++jj) {
+          const f4 a4 = *reinterpret_cast<const f4*>(&wl[rbase + (il0 + 4 * i4 + jj) * ilstep + 16 * k]);
+          dd[jj] = mfma_k16(a4, ga[k], dd[jj]);
         }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int m = 0; m < D; ++m)
+          acc[4 * i4 + jj][m] += dd[jj][0] * tc[m][0] + dd[jj][1] * tc[m][1] + dd[jj][2] * tc[m][2] +
+                                 dd[jj][3] * tc[m][3];
     }
   }
+  // sum over q (lanes r + 16q): after the xor-32 step a lane keeps the half of the rows selected by
+  // q & 2, after the xor-16 step the quarter selected by q & 1, i.e. rows [q*ILW/4, (q+1)*ILW/4)
+  constexpr int H = ILW / 2, QR = ILW / 4;
+  const bool hi = (q & 2) != 0, odd = (q & 1) != 0;
+  float h1[H][D];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t node = (int64_t)tile * NN + wave * 16 + 4 * q + i;
-    if (node >= N) continue;
+  for (int i = 0; i < H; ++i)
 #pragma unroll
-    for (int m = 0; m < D; ++m) dt[(node * D + m) * nC + I * 16 + r] = acc[i][m] * scale;
+    for (int m = 0; m < D; ++m)
+      h1[i][m] = (hi ? acc[H + i][m] : acc[i][m]) + __shfl_xor(hi ? acc[i][m] : acc[H + i][m], 32, 64);
+  float h2[QR][D];
+#pragma unroll
+  for (int i = 0; i < QR; ++i)
+#pragma unroll
+    for (int m = 0; m < D; ++m)
+      h2[i][m] = (odd ? h1[QR + i][m] : h1[i][m]) + __shfl_xor(odd ? h1[i][m] : h1[QR + i][m], 16, 64);
+  if (valid) {
+#pragma unroll
+    for (int m = 0; m < D; ++m) {
+      float* o = dt + (n * D + m) * nC + I * 16 + il0 + QR * q;
+#pragma unroll
+      for (int i = 0; i < QR; ++i) o[i] = h2[i][m] * scale;
+    }
   }
 }
 
@@ -256,10 +292,12 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
 template <int S>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
-  const int ntiles = (int)((N + NODES - 1) / NODES);
+  // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8
+  const int nn = (D <= 5) ? NODES : NODES / 2;
+  const int ntiles = (int)((N + nn - 1) / nn);
   const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
   LaunchTimer tm("gram_backward", st);
-#define FSC_GB(DD) backward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt)
+#define FSC_GB(DD) backward_kernel<DD, S, (DD <= 5 ? 16 : 8)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt)
   switch (D) {
     case 1: FSC_GB(1); break;
     case 3: FSC_GB(3); break;

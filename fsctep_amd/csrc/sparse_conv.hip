@@ -68,9 +68,11 @@ __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __
 // (m, I) of one path (4 waves x 32 rows; blocks numbered path by path, `off` = first block of
 // each path) and a group of 80-column tiles.  The rows of x stay in registers; each column
 // tile of bk1 (80 x C) is staged in LDS, the next one loaded while the current one is
-// multiplied.  Transposed product: bk1 rows are the MFMA A operand and x rows the B operand,
-// and tile j's A row i is column 20*(i/4) + 4*j + i%4, so lane (r, q) ends with columns
-// [20q, 20q+20) of row r: five float4 stores per row.
+// multiplied and written to the other LDS buffer before the current results are stored.
+// Transposed product: bk1 rows are the MFMA A operand and x rows the B operand, and tile j's
+// A row i is column 16*j + i, so lane (r, q) ends with columns 16j+4q..16j+4q+3 of row r: the
+// four lanes of a row store 64 contiguous bytes per instruction.  Stores go through a buffer
+// descriptor spanning the block's nodes; rows past the end are sent out of range and dropped.
 struct PathTiles {
   int off[7];
 };
@@ -97,23 +99,28 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   const int comp0 = (L1 == 0) ? 0 : (L1 == 1 ? 1 : 4);
   const int sbase = kSlotBase[p];
   const int64_t rows = n_nodes * nI;
-  const int64_t row0 = (int64_t)(bt - tiles.off[p]) * NE_ROWS + wave * (16 * RT);
+  const int64_t brow0 = (int64_t)(bt - tiles.off[p]) * NE_ROWS;
+  const int64_t row0 = brow0 + wave * (16 * RT);
   const float* bp = bk1 + (int64_t)p * COLS * C;
   const int ct0 = cg * NE_TPB, ct1 = min(NTC, ct0 + NE_TPB);
+  // store window: the nodes of the block's rows (at most NE_ROWS nodes, well below 4 GiB)
+  const int64_t mfirst = (uint32_t)brow0 / (uint32_t)nI;
+  const int64_t mlast = min(n_nodes - 1, (int64_t)((uint32_t)(brow0 + NE_ROWS - 1) / (uint32_t)nI));
+  const __amdgpu_buffer_rsrc_t out =
+      buffer_rsrc(S + mfirst * s_node_stride(C), (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * 4));
   f4 xb[RT][KT];
-  int64_t obase[RT];
-  bool ok[RT];
+  uint32_t ooff[RT];   // byte offset of the lane's first column in the store window
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    int64_t row = row0 + 16 * rt + r;
-    ok[rt] = row < rows;
-    if (!ok[rt]) row = 0;   // a valid row; its result is not stored
-    const int64_t m = (uint32_t)row / (uint32_t)nI;
-    const int I = (int)(row - m * nI);
+    const int64_t row = row0 + 16 * rt + r;
+    const bool ok = row < rows;
+    const int64_t m = ok ? (int64_t)((uint32_t)row / (uint32_t)nI) : mfirst;
+    const int I = ok ? (int)(row - m * nI) : 0;
     const float* xr = x + (m * NCOMP + comp0 + I) * C + 4 * q;
 #pragma unroll
     for (int t = 0; t < KT; ++t) xb[rt][t] = ld4(xr + 16 * t);
-    obase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 20 * q;
+    ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * 4)
+                  : kDropOffset;
   }
   constexpr int NSTG = (WCOLS * (C / 4) + 255) / 256;
   f4 stg[NSTG];
@@ -138,6 +145,11 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   for (int ct = ct0; ct < ct1; ++ct) {
     const int buf = (ct - ct0) & 1;
     if (ct + 1 < ct1) gload(ct + 1);
+    f4 a4[NT][KT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < KT; ++t) a4[j][t] = sb[buf][16 * j + r][4 * t + q];
     f4 acc[RT][NT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -146,20 +158,17 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const f4 a4 = sb[buf][20 * (r >> 2) + 4 * j + (r & 3)][4 * t + q];
+      for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_k16(a4, xb[rt][t], acc[rt][j]);
-      }
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      if (ok[rt]) {
-        float* o = S + obase[rt] + ct * WCOLS;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) st4(o + 4 * j, acc[rt][j]);
-      }
-    }
+        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_k16(a4[j][t], xb[rt][t], acc[rt][j]);
+    // stage the next tile first: the waits for its loads then do not cover this tile's stores
+    __builtin_amdgcn_sched_barrier(0);
     if (ct + 1 < ct1) sstore(buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) buffer_st4(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 4, acc[rt][j]);
     __syncthreads();
   }
 }
