@@ -446,28 +446,31 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
       const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
       const int nkt = kpad / 16;
       const float* xr = x + ((int64_t)srcs[r] * L.M + m) * C + 4 * q;
-      f4 acc[4];
-      const float* br[4];
-      bool bok[4];
+      f4 acc[2];
+      const float* br[2];
+      bool bok[2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < 2; ++kt) {
         acc[kt] = f4{0.f, 0.f, 0.f, 0.f};
         const int kkl = kt * 16 + r;
         bok[kt] = kt < nkt && kkl < kcount;
         br[kt] = gn + (int64_t)(L.g_kstart[g] + (bok[kt] ? kkl : 0)) * C + 4 * q;
       }
-#pragma unroll 2
-      for (int t = 0; t < C; t += 16) {
-        const f4 a4 = ld4(xr + t);
+      // every K step's gathered x row and gradient rows are requested before the first product
+      f4 av[C / 16], bv[2][C / 16];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          if (kt >= nkt) break;
-          const f4 b4 = bok[kt] ? ld4(br[kt] + t) : f4{0.f, 0.f, 0.f, 0.f};
-          acc[kt] = mfma_k16(a4, b4, acc[kt]);
-        }
+      for (int s = 0; s < C / 16; ++s) {
+        av[s] = ld4(xr + 16 * s);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) bv[kt][s] = bok[kt] ? ld4(br[kt] + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int s = 0; s < C / 16; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          if (kt < nkt) acc[kt] = mfma_k16(av[s], bv[kt][s], acc[kt]);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
         if (kt >= nkt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -655,11 +658,11 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
     set_error(std::string(who) + ": every input irrep needs a live path");
     return 1;
   }
-  // limits of the projection kernels: <= 64 kk slots per group (4 MFMA tiles), 4-bit component
+  // limits of the projection kernels: <= 32 kk slots per group (2 MFMA tiles), 4-bit component
   // counts in the coupling descriptors, tiles inside their group, LDS within 64 KiB
   int bgoff = 0;
   for (int g = 0; g < L->NG; ++g) {
-    if (L->g_kpad[g] < 16 || L->g_kpad[g] > 64 || L->g_d1[g] < 1 || L->g_d1[g] > 15 ||
+    if (L->g_kpad[g] < 16 || L->g_kpad[g] > 32 || L->g_d1[g] < 1 || L->g_d1[g] > 15 ||
         L->g_bgoff[g] != bgoff || L->g_kstart[g] < 0 || L->g_kstart[g] + L->g_kcount[g] > L->KT) {
       set_error(std::string(who) + ": path group exceeds the projection kernel limits");
       return 1;

@@ -686,8 +686,17 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
       }
       if (threadIdx.x < DW) {
         const int col = threadIdx.x;
-        float sum = 0.f;
-        for (int e = 0; e < cnt; ++e) sum += dps[e][col];
+        // rows >= cnt hold zeros: run to a multiple of 8 with the reads of a group issued together
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+        const int e8 = (cnt + 7) & ~7;
+        for (int e = 0; e < e8; e += 8) {
+          float v8[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v8[u] = dps[e + u][col];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) s4[u & 3] += v8[u];
+        }
+        const float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
         float* o = dSm + (int64_t)(col / CC) * COLS + 64 * C + c0 + col % CC;
         *o = first ? sum : (*o + sum);
       }
