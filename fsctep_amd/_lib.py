@@ -41,6 +41,8 @@ SIGNATURES = {
     "fsc_edge_geometry_backward": [_i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_edge_harmonics_forward": [_p, _i64, _p, _p, _p],
     "fsc_edge_harmonics_backward": [_p, _i64, _p, _p, _p, _p],
+    "fsc_readout_gather": [_p, _i64, _p, _p, _p, _p, _p],
+    "fsc_readout_scatter": [_p, _i64, _p, _p, _p, _p, _p, _p],
     "fsc_radial_mlp_forward": [_i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p, _p],
     "fsc_radial_mlp_backward": [_i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p],
 }

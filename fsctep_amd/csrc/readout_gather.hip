@@ -1,0 +1,185 @@
+// Readout feature assembly on gfx950 (sparse and ICTD trunks).
+//
+// The readouts combine the per-layer node features X_l [N][M][C] (l < n_layers) in two ways:
+//   * Gram inputs t_k [N][d_k][nC] (nC = n_layers * C), one per key k (a run of d_k components
+//     starting at comp0_k): a fixed permutation of the (l, m, c) entries of a node over the
+//     key-major columns of all t_k, given by the host as srcmap (destination -> source) and gmap
+//     (source -> destination; an entry need not land in the Gram input of its own key);
+//   * squared norms sq[n][k][l*C + c] = sum_{m in key k} X_l[n][m][c]^2.
+// The sparse trunk builds t_k as the concatenation over layers of the rank-L component block
+// (models/pure_cartesian_sparse_layers.py:769-833); the ICTD trunks flatten each layer channel-major
+// per key, concatenate the layers and re-split the result by key
+// (models/pure_cartesian_ictd_layers_full.py:977-1001, models/pure_cartesian_ictd_layers_o3.py:987-1019),
+// which mixes keys and layers; both are permutations, so one gather builds every t_k and the
+// backward is one gather through the inverse map plus the squared-norm term:
+//   dX_l[n][m][c] = dt_{k'}[n][gmap(l,m,c) - col0_{k'}] + 2 X_l[n][m][c] dsq[n][k][l*C + c],
+// k' the key whose columns hold gmap(l,m,c), k the key of component m.
+// Layouts: t_all holds the t_k one after another (t_k at N * col0_k, col0_k = sum_{k'<k} d_k' nC).
+
+#include "common.h"
+#include "fsctep.h"
+
+namespace fsc {
+namespace readout {
+
+struct LayerPtrs {
+  const float* p[4];
+};
+struct KeyPtrs {
+  const float* p[8];
+};
+struct OutPtrs {
+  float* p[4];
+};
+
+// Key of component m.
+__device__ __forceinline__ int key_of(const FscReadoutTable& T, int m) {
+  int k = 0;
+  while (k + 1 < T.n_keys && m >= T.key_comp0[k + 1]) ++k;
+  return k;
+}
+
+// Key holding key-major column j (of n_layers*M*C) and its first column.
+__device__ __forceinline__ int key_of_column(const FscReadoutTable& T, int nC, int j, int& col0) {
+  int k = 0;
+  col0 = 0;
+  while (k + 1 < T.n_keys && j >= col0 + T.key_dim[k] * nC) {
+    col0 += T.key_dim[k] * nC;
+    ++k;
+  }
+  return k;
+}
+
+// t_all[N * col0_k + n * d_k nC + j'] = X[src], thread per (node, key-major column); columns fastest.
+__global__ void gather_kernel(FscReadoutTable T, int64_t N, LayerPtrs X, const int32_t* __restrict__ srcmap,
+                              float* __restrict__ t_all) {
+  const int MC = T.M * T.C, nC = T.n_layers * T.C, P = T.n_layers * MC;
+  const int64_t total = N * P;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = idx / P;
+    const int jg = (int)(idx - n * P);
+    int col0;
+    const int k = key_of_column(T, nC, jg, col0);
+    const int src = min(max(srcmap[jg], 0), P - 1);   // maps are host-checked permutations; stay in bounds
+    const int l = src / MC;
+    t_all[N * col0 + n * (int64_t)(T.key_dim[k] * nC) + (jg - col0)] = X.p[l][n * MC + (src - l * MC)];
+  }
+}
+
+// sq[n][k][l*C + c] = sum over the components of key k of X_l[n][m][c]^2; thread per (n, k, l, c).
+__global__ void sq_kernel(FscReadoutTable T, int64_t N, LayerPtrs X, float* __restrict__ sq) {
+  const int C = T.C, L = T.n_layers, K = T.n_keys;
+  const int64_t total = N * K * L * C;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % C);
+    const int l = (int)((idx / C) % L);
+    const int k = (int)((idx / ((int64_t)C * L)) % K);
+    const int64_t n = idx / ((int64_t)C * L * K);
+    const float* x = X.p[l] + (n * T.M + T.key_comp0[k]) * C + c;
+    float s = 0.f;
+    for (int m = 0; m < T.key_dim[k]; ++m) s += x[m * C] * x[m * C];
+    sq[idx] = s;
+  }
+}
+
+// dX_l[n][m][c] = dt_k'[n][gmap(l,m,c) - col0_k'] + 2 X_l[n][m][c] dsq[n][key(m)][l*C + c]; thread per
+// (l, n, m, c).
+__global__ void scatter_kernel(FscReadoutTable T, int64_t N, KeyPtrs dt, const float* __restrict__ dsq, LayerPtrs X,
+                               const int32_t* __restrict__ gmap, OutPtrs dX) {
+  const int C = T.C, M = T.M, MC = M * C, nC = T.n_layers * C, P = T.n_layers * MC;
+  const int64_t total = (int64_t)T.n_layers * N * MC;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(idx / (N * MC));
+    const int64_t rem = idx - (int64_t)l * N * MC;
+    const int64_t n = rem / MC;
+    const int mc = (int)(rem - n * MC);
+    const int m = mc / C, c = mc - m * C;
+    const int j = min(max(gmap[l * MC + mc], 0), P - 1);
+    int col0;
+    const int kt = key_of_column(T, nC, j, col0);
+    float v = 0.f;
+    if (dt.p[kt]) v = dt.p[kt][n * (int64_t)(T.key_dim[kt] * nC) + (j - col0)];
+    if (dsq) v += 2.f * X.p[l][rem] * dsq[(n * T.n_keys + key_of(T, m)) * nC + l * C + c];
+    dX.p[l][rem] = v;
+  }
+}
+
+int check_table(const FscReadoutTable* T, const char* who) {
+  if (!T) {
+    set_error(std::string(who) + ": null table");
+    return 1;
+  }
+  if (T->n_layers < 1 || T->n_layers > 4 || T->n_keys < 1 || T->n_keys > 8 || T->M < 1 || T->M > 64 ||
+      T->C < 1 || T->C > 1024) {
+    set_error(std::string(who) + ": table out of range (1..4 layers, 1..8 keys, M <= 64, C <= 1024)");
+    return 1;
+  }
+  int covered = 0;
+  for (int k = 0; k < T->n_keys; ++k) {
+    if (T->key_comp0[k] != covered || T->key_dim[k] < 1) {
+      set_error(std::string(who) + ": keys must tile the components in order");
+      return 1;
+    }
+    covered += T->key_dim[k];
+  }
+  if (covered != T->M) {
+    set_error(std::string(who) + ": keys must cover all M components");
+    return 1;
+  }
+  return 0;
+}
+
+unsigned grid_for(int64_t total) { return (unsigned)std::min<int64_t>((total + 255) / 256, 8192); }
+
+}  // namespace readout
+}  // namespace fsc
+
+using namespace fsc;
+using namespace fsc::readout;
+
+extern "C" {
+
+int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
+                       const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream) {
+  if (check_table(table, "fsc_readout_gather")) return 1;
+  FSC_CHECK_ARG(n_nodes >= 0 && n_nodes < (1LL << 31), "fsc_readout_gather: bad node count");
+  if (n_nodes == 0) return 0;
+  FSC_CHECK_ARG(layers && srcmap && t_all && sq, "fsc_readout_gather: null pointer");
+  LayerPtrs X{};
+  for (int l = 0; l < table->n_layers; ++l) {
+    FSC_CHECK_ARG(layers[l], "fsc_readout_gather: null layer pointer");
+    X.p[l] = layers[l];
+  }
+  const int64_t P = (int64_t)table->n_layers * table->M * table->C;
+  gather_kernel<<<grid_for(n_nodes * P), 256, 0, stream>>>(*table, n_nodes, X, srcmap, t_all);
+  if (check_launch("readout gather")) return 2;
+  const int64_t S = n_nodes * table->n_keys * table->n_layers * table->C;
+  sq_kernel<<<grid_for(S), 256, 0, stream>>>(*table, n_nodes, X, sq);
+  return check_launch("readout sq") ? 2 : 0;
+}
+
+int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const float* const* grad_t,
+                        const float* grad_sq, const float* const* layers, const int32_t* gmap,
+                        float* const* grad_layers, hipStream_t stream) {
+  if (check_table(table, "fsc_readout_scatter")) return 1;
+  FSC_CHECK_ARG(n_nodes >= 0 && n_nodes < (1LL << 31), "fsc_readout_scatter: bad node count");
+  if (n_nodes == 0) return 0;
+  FSC_CHECK_ARG(grad_t && layers && gmap && grad_layers, "fsc_readout_scatter: null pointer");
+  KeyPtrs dt{};
+  for (int k = 0; k < table->n_keys; ++k) dt.p[k] = grad_t[k];   // null: no gradient through key k
+  LayerPtrs X{};
+  OutPtrs dX{};
+  for (int l = 0; l < table->n_layers; ++l) {
+    FSC_CHECK_ARG(layers[l] && grad_layers[l], "fsc_readout_scatter: null layer pointer");
+    X.p[l] = layers[l];
+    dX.p[l] = grad_layers[l];
+  }
+  const int64_t total = (int64_t)table->n_layers * n_nodes * table->M * table->C;
+  scatter_kernel<<<grid_for(total), 256, 0, stream>>>(*table, n_nodes, dt, grad_sq, X, gmap, dX);
+  return check_launch("readout scatter") ? 2 : 0;
+}
+
+}  // extern "C"

@@ -338,6 +338,135 @@ Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&
   return at::empty(t.sizes(), fopts(t));
 }
 
+// -------------------------------------------------------------- readout feature assembly
+const FscReadoutTable* readout_table_of(const Tensor& table) {
+  TORCH_CHECK(table.device().is_cpu() && table.scalar_type() == at::kInt && table.is_contiguous() &&
+                  table.numel() * 4 == (int64_t)sizeof(FscReadoutTable),
+              "readout table must be a contiguous CPU int32 tensor holding an FscReadoutTable (",
+              sizeof(FscReadoutTable) / 4, " entries)");
+  return reinterpret_cast<const FscReadoutTable*>(table.data_ptr<int32_t>());
+}
+
+// The layers as float32 contiguous [N][M][C] tensors (kept alive by the caller).
+std::vector<Tensor> readout_layers(at::TensorList layers, const FscReadoutTable* T) {
+  TORCH_CHECK((int64_t)layers.size() == T->n_layers, "expected ", T->n_layers, " feature layers, got ",
+              layers.size());
+  std::vector<Tensor> out;
+  for (const Tensor& x : layers) {
+    require_gpu({x});
+    TORCH_CHECK(x.dim() == 3 && x.size(0) == layers[0].size(0) && x.size(1) == T->M && x.size(2) == T->C,
+                "feature layers must be (N, ", T->M, ", ", T->C, ")");
+    out.push_back(f32c(x));
+  }
+  return out;
+}
+
+Tensor readout_map(const Tensor& map, const FscReadoutTable* T, const char* what) {
+  require_gpu({map});
+  TORCH_CHECK(map.numel() == (int64_t)T->n_layers * T->M * T->C, what, " must have n_layers*M*C entries");
+  return i32c(map, what);
+}
+
+std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& srcmap, const Tensor& table) {
+  const FscReadoutTable* T = readout_table_of(table);
+  std::vector<Tensor> X = readout_layers(layers, T);
+  Tensor sm = readout_map(srcmap, T, "srcmap");
+  const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C;
+  Tensor t_all = at::empty({N * T->M * nC}, fopts(X[0]));
+  Tensor sq = at::empty({N, T->n_keys, nC}, fopts(X[0]));
+  std::vector<const float*> xp;
+  for (const Tensor& x : X) xp.push_back(cf(x));
+  check(fsc_readout_gather(T, N, xp.data(), ci(sm), mf(t_all), mf(sq), stream_of(X[0])), "fsc_readout_gather");
+  return {t_all, sq};
+}
+
+std::tuple<Tensor, Tensor> readout_gather_meta(at::TensorList layers, const Tensor&, const Tensor& table) {
+  const FscReadoutTable* T = readout_table_of(table);
+  const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
+  return {at::empty({N * T->M * nC}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
+}
+
+std::vector<Tensor> readout_scatter(const c10::List<std::optional<Tensor>>& grad_t, const std::optional<Tensor>& grad_sq,
+                                    at::TensorList layers, const Tensor& gmap, const Tensor& table) {
+  const FscReadoutTable* T = readout_table_of(table);
+  std::vector<Tensor> X = readout_layers(layers, T);
+  Tensor gm = readout_map(gmap, T, "gmap");
+  const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C;
+  TORCH_CHECK((int64_t)grad_t.size() == T->n_keys, "expected ", T->n_keys, " Gram-input gradients");
+  std::vector<Tensor> dt;
+  std::vector<const float*> dtp;
+  for (int k = 0; k < T->n_keys; ++k) {
+    const std::optional<Tensor> g = grad_t.get(k);
+    if (g.has_value() && g->defined()) {
+      require_gpu({*g});
+      TORCH_CHECK(g->numel() == N * T->key_dim[k] * nC, "gradient of Gram input ", k, " has the wrong size");
+      dt.push_back(f32c(*g));
+      dtp.push_back(cf(dt.back()));
+    } else {
+      dtp.push_back(nullptr);
+    }
+  }
+  Tensor dsq;
+  if (grad_sq.has_value() && grad_sq->defined()) {
+    require_gpu({*grad_sq});
+    TORCH_CHECK(grad_sq->numel() == N * T->n_keys * nC, "grad_sq must be (N, n_keys, n_layers*C)");
+    dsq = f32c(*grad_sq);
+  }
+  std::vector<Tensor> dX;
+  std::vector<const float*> xp;
+  std::vector<float*> dxp;
+  for (const Tensor& x : X) {
+    dX.push_back(at::empty(x.sizes(), fopts(x)));
+    xp.push_back(cf(x));
+    dxp.push_back(mf(dX.back()));
+  }
+  check(fsc_readout_scatter(T, N, dtp.data(), dsq.defined() ? cf(dsq) : nullptr, xp.data(), ci(gm), dxp.data(),
+                            stream_of(X[0])),
+        "fsc_readout_scatter");
+  return dX;
+}
+
+std::vector<Tensor> readout_scatter_meta(const c10::List<std::optional<Tensor>>&, const std::optional<Tensor>&,
+                                         at::TensorList layers, const Tensor&, const Tensor&) {
+  std::vector<Tensor> dX;
+  for (const Tensor& x : layers) dX.push_back(at::empty(x.sizes(), fopts(x)));
+  return dX;
+}
+
+// Gram input k of the gathered buffer as an (N, d_k, nC) view.
+Tensor gram_input(const Tensor& t_all, const FscReadoutTable* T, int64_t N, int k) {
+  const int64_t nC = (int64_t)T->n_layers * T->C;
+  int64_t col0 = 0;
+  for (int j = 0; j < k; ++j) col0 += T->key_dim[j] * nC;
+  return t_all.narrow(0, N * col0, N * T->key_dim[k] * nC).view({N, T->key_dim[k], nC});
+}
+
+// scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.
+std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
+                                            at::ArrayRef<double> scales, const Tensor& srcmap, const Tensor& gmap,
+                                            const Tensor& table) {
+  const FscReadoutTable* T = readout_table_of(table);
+  TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
+                  (int64_t)scales.size() == T->n_keys,
+              "one prepared Gram weight pair and scale per key");
+  auto [t_all, sq] = readout_gather(layers, srcmap, table);
+  const int64_t N = layers[0].size(0);
+  Tensor scalars;
+  for (int k = 0; k < T->n_keys; ++k) {
+    Tensor o = gram_bilinear(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
+    scalars = scalars.defined() ? scalars.add_(o) : o;
+  }
+  return {scalars, sq};
+}
+
+std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList, at::TensorList Wb,
+                                                 at::ArrayRef<double>, const Tensor&, const Tensor&,
+                                                 const Tensor& table) {
+  const FscReadoutTable* T = readout_table_of(table);
+  const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
+  return {at::empty({N, Wb[0].size(2)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
+}
+
 // ============================================================== autograd
 
 // ============================================================== edge geometry and radial MLP
@@ -655,6 +784,80 @@ Tensor gram_bilinear_autograd(const Tensor& t, const Tensor& Wf, const Tensor& W
   return GramFn::apply(t, Wf, Wb, scale)[0];
 }
 
+// Readout features: the gradient w.r.t. the layers is one scatter kernel fed by the per-key Gram
+// backward and the squared-norm gradient (no per-slice zero fills or accumulations).
+struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
+  static variable_list forward(AutogradContext* ctx, at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
+                               std::vector<double> scales, Tensor srcmap, Tensor gmap, Tensor table) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto gather =
+        op_handle<std::tuple<Tensor, Tensor>(at::TensorList, const Tensor&, const Tensor&)>("fsctep::readout_gather");
+    static auto gram = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear");
+    const FscReadoutTable* T = readout_table_of(table);
+    TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
+                    (int64_t)scales.size() == T->n_keys,
+                "one prepared Gram weight pair and scale per key");
+    auto [t_all, sq] = gather.call(layers, srcmap, table);
+    const int64_t N = layers[0].size(0);
+    Tensor scalars;
+    for (int k = 0; k < T->n_keys; ++k) {
+      Tensor o = gram.call(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
+      scalars = scalars.defined() ? scalars.add_(o) : o;
+    }
+    variable_list keep(layers.begin(), layers.end());
+    keep.push_back(t_all);
+    for (const Tensor& w : Wb) keep.push_back(w);
+    keep.push_back(gmap);
+    keep.push_back(table);
+    ctx->save_for_backward(keep);
+    ctx->saved_data["n_layers"] = (int64_t)layers.size();
+    ctx->saved_data["scales"] = c10::IValue(c10::ArrayRef<double>(scales));
+    ctx->set_materialize_grads(false);   // an unused output skips its part of the backward
+    return {scalars, sq};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    auto s = ctx->get_saved_variables();
+    const int64_t nL = ctx->saved_data["n_layers"].toInt();
+    const std::vector<double> scales = ctx->saved_data["scales"].toDoubleVector();
+    const int64_t nK = (int64_t)scales.size();
+    variable_list res(nL + 2 * nK + 4);
+    if (!grads[0].defined() && !grads[1].defined()) return res;
+    for (int64_t i = nL; i < nL + 2 * nK; ++i)
+      TORCH_CHECK(!ctx->needs_input_grad(i), "parameter gradients of the readout Gram bilinear are not implemented "
+                                             "(energy/force inference only)");
+    static auto gram_bwd =
+        op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear_backward");
+    static auto scatter = op_handle<std::vector<Tensor>(const c10::List<std::optional<Tensor>>&,
+                                                        const std::optional<Tensor>&, at::TensorList, const Tensor&,
+                                                        const Tensor&)>("fsctep::readout_scatter");
+    std::vector<Tensor> layers(s.begin(), s.begin() + nL);
+    const Tensor& t_all = s[nL];
+    const Tensor& gmap = s[nL + 1 + nK];
+    const Tensor& table = s[nL + 2 + nK];
+    const FscReadoutTable* T = readout_table_of(table);
+    const int64_t N = layers[0].size(0);
+    c10::List<std::optional<Tensor>> dt;
+    for (int k = 0; k < nK; ++k) {
+      if (grads[0].defined())
+        dt.push_back(gram_bwd.call(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k]));
+      else
+        dt.push_back(std::nullopt);
+    }
+    std::optional<Tensor> dsq;
+    if (grads[1].defined()) dsq = grads[1];
+    std::vector<Tensor> dX = scatter.call(dt, dsq, layers, gmap, table);
+    for (int64_t l = 0; l < nL; ++l) res[l] = dX[l];
+    return res;
+  }
+};
+
+std::tuple<Tensor, Tensor> readout_features_autograd(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
+                                                     at::ArrayRef<double> scales, const Tensor& srcmap,
+                                                     const Tensor& gmap, const Tensor& table) {
+  auto out = ReadoutFn::apply(layers, Wf, Wb, scales.vec(), srcmap, gmap, table);
+  return {out[0], out[1]};
+}
+
 struct EdgeGeometryFn : public torch::autograd::Function<EdgeGeometryFn> {
   static variable_list forward(AutogradContext* ctx, Tensor pos, Tensor shift, Tensor edge_src, Tensor edge_dst,
                                Tensor dst_ptr, Tensor src_ptr, Tensor src_perm) {
@@ -789,6 +992,10 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("edge_harmonics_backward(Tensor grad_Y, Tensor n, Tensor table) -> Tensor");
   m.def("radial_mlp_backward(Tensor grad_out, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, "
         "float r_cut, int basis) -> Tensor");
+  m.def("readout_gather(Tensor[] layers, Tensor srcmap, Tensor table) -> (Tensor, Tensor)");
+  m.def("readout_scatter(Tensor?[] grad_t, Tensor? grad_sq, Tensor[] layers, Tensor gmap, Tensor table) -> Tensor[]");
+  m.def("readout_features(Tensor[] layers, Tensor[] Wf, Tensor[] Wb, float[] scales, Tensor srcmap, Tensor gmap, "
+        "Tensor table) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -812,6 +1019,9 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("radial_mlp_backward", radial_mlp_backward);
   m.impl("edge_harmonics", edge_harmonics);
   m.impl("edge_harmonics_backward", edge_harmonics_backward);
+  m.impl("readout_gather", readout_gather);
+  m.impl("readout_scatter", readout_scatter);
+  m.impl("readout_features", readout_features);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -835,6 +1045,9 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("radial_mlp_backward", radial_mlp_backward_meta);
   m.impl("edge_harmonics", edge_harmonics_meta);
   m.impl("edge_harmonics_backward", edge_harmonics_backward_meta);
+  m.impl("readout_gather", readout_gather_meta);
+  m.impl("readout_scatter", readout_scatter_meta);
+  m.impl("readout_features", readout_features_meta);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
@@ -846,6 +1059,7 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
   m.impl("edge_geometry", edge_geometry_autograd);
   m.impl("radial_mlp", radial_mlp_autograd);
   m.impl("edge_harmonics", edge_harmonics_autograd);
+  m.impl("readout_features", readout_features_autograd);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
@@ -853,6 +1067,7 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
                            "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
-                           "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward"})
+                           "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
+                           "readout_gather", "readout_scatter", "readout_features"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -21,7 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ictd_ops
-from .readout_ops import GramWeights
+from .readout_ops import GramWeights, ReadoutMaps, readout_features
 from .graph import Graph, prepare_graph
 from .ictd_basis import canonical, coupling, layout_full, layout_o3
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
@@ -224,47 +224,38 @@ class _ICTDTrunk(nn.Module):
             return F.linear(h, fc[4].weight.detach(), fc[4].bias.detach())
         return ictd_ops.radial_full(r, fc, self.max_radius, self.function_type)
 
-    def _to_ref_flat(self, f):
-        """x[N][M][C] -> reference flat (N, C*M): per key a channel-major (C, 2l+1) block."""
-        N = f.shape[0]
-        parts, off = [], 0
-        for k in self.keys:
-            d = 2 * k[0] + 1
-            parts.append(f[:, off:off + d, :].transpose(1, 2).reshape(N, -1))
-            off += d
-        return torch.cat(parts, dim=-1)
-
     def _wread(self, i, k):
         return self.W_read[_key_str(k)] if self.o3 else self.W_read[i]
 
     def readout(self, feats, batch, factors):
-        """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included."""
-        N = feats[0].shape[0]
-        nC = self.channels * self.num_interaction
-        fc = torch.cat([self._to_ref_flat(f) for f in feats], dim=-1)
-        xb, off = {}, 0
-        for k in self.keys:
-            d = 2 * k[0] + 1
-            xb[k] = fc[:, off:off + nC * d].reshape(N, nC, d)
-            off += nC * d
-        scalars = 0
+        """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included: the
+        Gram inputs (the reference's channel-major flatten, layer concatenation and re-split by key)
+        and the per-key squared norms of the layer concatenation come from one fused readout op."""
+        N, nL = feats[0].shape[0], len(feats)
+        key = ("maps", nL)
+        if key not in self._cache:
+            self._cache[key] = ReadoutMaps(nL, self.channels, [2 * k[0] + 1 for k in self.keys], resplit=True)
+        maps = self._cache[key]
+        grams = [self._gram_w[i].get(self._wread(i, k)) for i, k in enumerate(self.keys)]
+        scales = [1.0 / math.sqrt(2 * k[0] + 1) for k in self.keys]
+        scalars, sq_all = readout_features(feats, grams, scales, maps)
+        outs = []
         for i, k in enumerate(self.keys):
-            Wf, Wb = self._gram_w[i].get(self._wread(i, k))
-            scalars = scalars + torch.ops.fsctep.gram_bilinear(xb[k].transpose(1, 2), Wf, Wb,
-                                                               1.0 / math.sqrt(2 * k[0] + 1))
-        outs, off = [], 0
-        for i, k in enumerate(self.keys):
-            d = 2 * k[0] + 1
-            T = torch.cat([f[:, off:off + d, :] for f in feats], dim=2)        # (N, d, n*C)
-            sq = (T * T).sum(1)
+            sq = sq_all[:, i, :]
             if k == (0, 1):
                 sq = torch.cat([sq, scalars * scalars], dim=-1)
             outs.append(sq * factors[i])
-            off += d
         e = self.weighted_sum(self.proj_total(torch.cat(outs, dim=-1)))
         dip = None
         if self._dipole:
-            y = torch.einsum("ncm,oc->nom", xb[(1, -1)], self.physical_tensor_heads["dipole"]["1"].weight)
+            # the (1, -1) Gram input, (N, d, n*C), by the same column map (differentiable gather)
+            i = self.keys.index((1, -1))
+            nC = nL * self.channels
+            col0 = sum(d * nC for d in maps.key_dims[:i])
+            idx = maps.on(feats[0].device)[0][col0:col0 + 3 * nC].long()
+            t = torch.cat([f.reshape(N, -1) for f in feats], dim=1).index_select(1, idx).view(N, 3, nC)
+            W = self.physical_tensor_heads["dipole"]["1"].weight
+            y = torch.matmul(t, W.t().contiguous()).transpose(1, 2)          # (N, o, 3) = einsum("ncm,oc->nom")
             G = int(batch.max()) + 1 if batch.numel() else 0
             dip = y.new_zeros(G, 1, 3).index_add(0, batch, y)
         return e, dip

@@ -24,7 +24,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .readout_ops import GramWeights
+from .readout_ops import GramWeights, ReadoutMaps, readout_features
 from .graph import Graph, prepare_graph
 
 _COMPS = ((0, 1), (1, 4), (4, 13))   # component ranges of ranks 0, 1, 2
@@ -198,6 +198,7 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         self.weighted_sum = RobustScalarWeightedSum(17, init_weights="zero")
         self.max_radius = max_embed_radius
         self.number_of_basis = main_number_of_basis
+        self._readout_cache = {}
         self.function_type = function_type_main
         self._graph_key = None
         self._graph = None
@@ -260,14 +261,24 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         return self.readout(feats)
 
     def readout(self, feats):
-        """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features."""
-        blocks = [torch.cat([f[:, a:b, :] for f in feats], dim=2) for (a, b) in _COMPS]
-        f3 = self.product_3(blocks)
-        invs = []
-        for f in feats:
-            for L, (a, b) in enumerate(_COMPS):
-                invs.append((f[:, a:b, :] * f[:, a:b, :]).sum(dim=1) / math.sqrt(3 ** L))
-        f5 = torch.cat(invs + [f3 * f3], dim=-1)
+        """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features: the rank-L blocks of all
+        layers (t_L = cat_l x_l[:, block L, :]) feed product_3 and their squared norms
+        sum_m x^2 / 3^{L/2} the invariants, all assembled by one fused readout op."""
+        N, nL = feats[0].shape[0], len(feats)
+        key = ("maps", nL)
+        if key not in self._readout_cache:
+            self._readout_cache[key] = ReadoutMaps(nL, self.channels, [b - a for (a, b) in _COMPS], resplit=False)
+        maps = self._readout_cache[key]
+        p3 = self.product_3
+        scales = [1.0 / math.sqrt(3 ** L) for L in range(len(_COMPS))]
+        grams = [p3._prepared[L].get(p3.W[L]) for L in range(len(_COMPS))]
+        f3, sq = readout_features(feats, grams, scales, maps)
+        skey = ("scales", str(sq.device))
+        if skey not in self._readout_cache:
+            self._readout_cache[skey] = torch.tensor(scales, dtype=sq.dtype, device=sq.device).view(1, -1, 1, 1)
+        # invariants in the reference order: layer-major, then rank L
+        invs = (sq.view(N, len(_COMPS), nL, self.channels) * self._readout_cache[skey]).transpose(1, 2)
+        f5 = torch.cat([invs.reshape(N, -1), f3 * f3], dim=-1)
         return self.weighted_sum(self.proj_total(f5))
 
 

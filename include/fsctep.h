@@ -225,6 +225,36 @@ int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float sc
 int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* grad_out,
                       const float* t, const float* Wb, float* grad_t, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Readout feature assembly.  From the per-layer node features X_l [N][M][C] (n_layers <= 4) it
+ * builds the Gram inputs t_k [N][d_k][nC] of every key k (nC = n_layers * C; key k = components
+ * [key_comp0[k], key_comp0[k] + key_dim[k]), n_keys <= 8) and the squared norms
+ * sq [N][n_keys][nC], sq[n][k][l*C + c] = sum_{m in key k} X_l[n][m][c]^2.
+ * Replaces the readout slicing, concatenation and squared sums of the sparse trunk
+ * (models/pure_cartesian_sparse_layers.py:769-833: t_k = cat_l X_l[:, block L, :], invariants
+ * sum_m x^2 / 3^{L/2}) and of the ICTD trunks (models/pure_cartesian_ictd_layers_full.py:977-1024,
+ * models/pure_cartesian_ictd_layers_o3.py:987-1030: channel-major flatten, layer concatenation and
+ * re-split by key for the Gram inputs, (T*T).sum(1) of the per-key layer concatenation T).
+ * The t_k layout is a permutation of a node's n_layers*M*C entries given by the host:
+ * srcmap[j] = l*M*C + m*C + c for key-major destination column j (t_0's d_0*nC columns, then
+ * t_1's, ...), gmap[l*M*C + m*C + c] = j (the inverse; an entry may land in another key's Gram
+ * input, as in the ICTD re-split).  t_all holds t_0, t_1, ... back to back (t_k at offset
+ * N * sum_{k'<k} key_dim[k'] * nC).  layers / grad_t / grad_layers are host arrays of
+ * device pointers (n_layers, n_keys and n_layers entries; a null grad_t[k] means no gradient
+ * through t_k, a null grad_sq none through sq).  The scatter writes
+ * dX_l[n][m][c] = grad_t_k'[n][gmap(l,m,c) - first column of k'] + 2 X_l[n][m][c] grad_sq[n][k][l*C + c]
+ * (k' the key holding column gmap(l,m,c), k the key of component m).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct FscReadoutTable {
+  int32_t n_layers, M, C, n_keys;
+  int32_t key_comp0[8], key_dim[8];
+} FscReadoutTable;
+int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
+                       const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream);
+int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const float* const* grad_t,
+                        const float* grad_sq, const float* const* layers, const int32_t* gmap,
+                        float* const* grad_layers, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

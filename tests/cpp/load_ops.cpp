@@ -25,7 +25,8 @@ int main(int argc, char** argv) {
                          "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
                          "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                          "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
-                         "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward"};
+                         "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
+                         "readout_gather", "readout_scatter", "readout_features"};
   for (const char* n : names) {
     auto op = disp.findSchema({std::string("fsctep::") + n, ""});
     if (!op) {

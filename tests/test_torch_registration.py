@@ -16,7 +16,8 @@ from fsctep_amd import _lib
 OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table", "sparse_conv1",
        "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv", "ictd_conv_backward", "ictd_conv1",
        "ictd_conv1_backward", "gram_prepare_weights", "gram_bilinear", "gram_bilinear_backward", "edge_geometry",
-       "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward"]
+       "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
+       "readout_gather", "readout_scatter", "readout_features"]
 
 
 class GramProbe(torch.nn.Module):
@@ -33,7 +34,7 @@ def test_schemas_registered_in_cpp():
         # registered by the C++ library, not by Python
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "CUDA")
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "Meta")
-    for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear"):
+    for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear", "readout_features"):
         assert torch._C._dispatch_has_computed_kernel_for_dispatch_key(f"fsctep::{name}", "AutogradCUDA")
 
 
@@ -78,4 +79,4 @@ def test_python_free_process_loads_ops_and_runs_scripted_module(tmp_path):
     env = {k: v for k, v in os.environ.items() if not k.startswith("PYTHON")}
     run = subprocess.run([str(exe), _lib.TORCH_LIB_PATH, str(pt)], capture_output=True, text=True, timeout=300, env=env)
     assert run.returncode == 0, run.stdout + run.stderr
-    assert "fsctep ops registered: 20; scripted module -> [7, 64]" in run.stdout
+    assert "fsctep ops registered: 23; scripted module -> [7, 64]" in run.stdout
