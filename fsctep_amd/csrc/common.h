@@ -40,6 +40,19 @@ __device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t rsrc, uint32_t
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rsrc, (int)byte_off, 0, 0);
 }
+// One float at byte offset voff (per lane) + soff (wave-uniform, kept in a scalar register): a load
+// loop whose offsets are compile-time multiples of a large stride needs one address VGPR, not one
+// 64-bit address per load.
+__device__ __forceinline__ float buffer_ld1(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ f4 buffer_ld4(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff, const f4& v) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rsrc, (int)voff, (int)soff, 0);
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

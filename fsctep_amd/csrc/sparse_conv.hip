@@ -483,6 +483,9 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
 // and the direction gradient of the receiver assembly (m1 = P1 n + P3, m2 = P2 n n + P4 n + P5)
 //   dn_e[k] = sum_c g1[k] P1 + P2 ((g2 n)[k] + (g2^T n)[k]) + (g2^T P4)[k]
 // is summed over the chunk's channels by lane shuffles and over chunks in a fixed order.
+// Register budget (3 waves per SIMD): the h values of the dS product stay in registers for the edge
+// block (no LDS copy, 40 KB of LDS per block), and the S loads and dS stores use buffer addressing
+// with the large constant strides in scalar offsets, so no per-load 64-bit addresses are held.
 // The receiver gradient in channel chunks: Gt[c/8][n][comp][c%8] = G[n][comp][c].
 template <int C>
 __global__ void grad_chunk_major_kernel(const float* __restrict__ G, float* __restrict__ Gt, int64_t n_nodes) {
@@ -505,7 +508,6 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   constexpr int NCT = DW / 16;       // 16-wide column tiles per chunk
   constexpr int COLS = 65 * C;
   constexpr int NCOL = NSLOT * C;
-  __shared__ float hs[EP][KH + 4];
   __shared__ float dps[EP][DW + 4];
   __shared__ int32_t eids[EP];
   __shared__ int32_t dsts[EP];
@@ -517,6 +519,10 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   const int beg = src_ptr[m], end = src_ptr[m + 1];
   const float* Sm = S + (int64_t)m * s_node_stride(C);
   float* dSm = dS + (int64_t)m * s_node_stride(C);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(const_cast<float*>(Sm), (uint32_t)(s_node_stride(C) * 4));
+  const __amdgpu_buffer_rsrc_t drs = buffer_rsrc(dSm, (uint32_t)(s_node_stride(C) * 4));
+  const uint32_t svoff = (uint32_t)(((q >> 1) * COLS + 4 * (q & 1) * KH + 16 * wave + r) * 4);
+  const uint32_t dvoff = (uint32_t)(((r >> 3) * COLS + (r & 7) * KH + 16 * wave + 4 * q) * 4);
   const int cl = threadIdx.x & (CC - 1);   // dP builder: channel within the chunk
   const int eb = threadIdx.x / CC;         // dP builder: edges eb, eb + 32
 
@@ -544,20 +550,13 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
       }
     }
     __syncthreads();
-    {
-      constexpr int NV = EP * (KH / 4) / 256;
-      f4 v[NV];
+    // A operand of the dS product, kept in registers for the whole edge block: lane (r, q) of wave w
+    // holds h[edge 4u + q][16 w + r] (zero beyond cnt)
+    float hreg[EP / 4];
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int idx = threadIdx.x + 256 * i;
-        v[i] = ld4(h + (int64_t)eids[idx / (KH / 4)] * KH + (idx % (KH / 4)) * 4);
-      }
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int idx = threadIdx.x + 256 * i;
-        const int e = idx / (KH / 4);
-        *reinterpret_cast<f4*>(&hs[e][(idx % (KH / 4)) * 4]) = (e < cnt) ? v[i] : f4{0.f, 0.f, 0.f, 0.f};
-      }
+    for (int u = 0; u < EP / 4; ++u) {
+      const int e = 4 * u + q;
+      hreg[u] = (e < cnt) ? h[(int64_t)eids[e] * KH + 16 * wave + r] : 0.f;
     }
     const int nrt = (cnt + 15) / 16;
     const int ksteps = (cnt + 3) / 4;
@@ -584,14 +583,15 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
         pN[hh][4] = pp[8 * CC];
       }
     };
+    // Chunk column kk = 16 tt + 4 q + s4 is slot kk/8 = 2 tt + q/2, channel ch*8 + 4 (q&1) + s4: the lane
+    // part of the address is one vector offset, the (tt, s4, ch) part a scalar one (no per-load address
+    // registers).
     auto load_s = [&](int ch) {
 #pragma unroll
       for (int tt = 0; tt < NCT; ++tt)
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const int kk = 16 * tt + 4 * q + s4;
-          sv[tt][s4] = Sm[(int64_t)(kk / CC) * COLS + (ch * CC + kk % CC) * KH + 16 * wave + r];
-        }
+        for (int s4 = 0; s4 < 4; ++s4)
+          sv[tt][s4] = buffer_ld1(srs, svoff, (uint32_t)((2 * tt * COLS + (ch * CC + s4) * KH) * 4));
     };
     load_g(0);
 #pragma unroll 1
@@ -662,27 +662,29 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) sacc[ct] = f4{0.f, 0.f, 0.f, 0.f};
       // edges are taken in pairs of K steps; rows up to 64 are zero beyond cnt
-      for (int u = 0; u < ksteps; u += 2) {
-        const float a0 = hs[4 * u + q][16 * wave + r];
-        const float a1 = hs[4 * u + 4 + q][16 * wave + r];
-        float b0[NCT], b1[NCT];
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-          b0[ct] = dps[4 * u + q][16 * ct + r];
-          b1[ct] = dps[4 * u + 4 + q][16 * ct + r];
+      for (int uu = 0; uu < EP / 8; ++uu) {
+        if (2 * uu < ksteps) {
+          const int u = 2 * uu;
+          float b0[NCT], b1[NCT];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            b0[ct] = dps[4 * u + q][16 * ct + r];
+            b1[ct] = dps[4 * u + 4 + q][16 * ct + r];
+          }
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(hreg[u], b0[ct], sacc[ct]);
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(hreg[u + 1], b1[ct], sacc[ct]);
         }
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(a0, b0[ct], sacc[ct]);
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) sacc[ct] = mfma16x16x4(a1, b1[ct], sacc[ct]);
       }
+      // column 16 ct + r of the chunk is slot 2 ct + r/8, channel c0 + r%8
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
-        const int col = 16 * ct + r;
-        float* o = dSm + (int64_t)(col / CC) * COLS + (c0 + col % CC) * KH + 16 * wave + 4 * q;
+        const uint32_t so = (uint32_t)((2 * ct * COLS + c0 * KH) * 4);
         f4 v = sacc[ct];
-        if (!first) v += ld4(o);
-        st4(o, v);
+        if (!first) v += buffer_ld4(drs, dvoff, so);
+        buffer_st4(drs, dvoff, so, v);
       }
       if (threadIdx.x < DW) {
         const int col = threadIdx.x;
