@@ -26,6 +26,41 @@ __device__ __forceinline__ f4 mfma_k16(const f4& a, const f4& b, f4 acc) {
   return acc;
 }
 
+// ---- fp32 products from bf16 MFMA (v_mfma_f32_16x16x32_bf16, 16x the fp32 MFMA rate).
+// A float is split into three bf16 parts, a = h + m + l (each part the round-to-nearest bf16 of the
+// remainder so far; the remainders are exact in fp32), which keeps its 24 significant bits.  A product
+// keeps the six terms hh' + hm' + mh' + mm' + hl' + lh'; the dropped ml' + lm' + ll' are below 2^-23 of
+// |a b|, the size of one fp32 rounding, and the sums accumulate in fp32 inside the MFMA.  Lane (r, q)
+// of the MFMA supplies A[r][8q..8q+7] and B[8q..8q+7][r]; the result layout is that of the fp32 MFMA.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split3(const float (&v)[8], bf8& h, bf8& m, bf8& l) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const __bf16 hb = (__bf16)v[j];
+    const float r1 = v[j] - (float)hb;
+    const __bf16 mb = (__bf16)r1;
+    h[j] = hb;
+    m[j] = mb;
+    l[j] = (__bf16)(r1 - (float)mb);
+  }
+}
+
+__device__ __forceinline__ f4 mfma_bf16(const bf8& a, const bf8& b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// c += (ah + am + al)(bh + bm + bl) without the three smallest terms; small terms first.
+__device__ __forceinline__ f4 mfma_x6(const bf8& ah, const bf8& am, const bf8& al, const bf8& bh, const bf8& bm,
+                                      const bf8& bl, f4 c) {
+  c = mfma_bf16(al, bh, c);
+  c = mfma_bf16(ah, bl, c);
+  c = mfma_bf16(am, bm, c);
+  c = mfma_bf16(am, bh, c);
+  c = mfma_bf16(ah, bm, c);
+  return mfma_bf16(ah, bh, c);
+}
+
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ void st4(float* p, const f4& v) { *reinterpret_cast<f4*>(p) = v; }
 

@@ -40,9 +40,10 @@ __host__ __device__ inline int64_t s_node_stride(int C) { return (int64_t)NSLOT 
 
 // ---------------------------------------------------------------- weight preparation
 // bk1[p][col][a] (col < 64C: col = c*64+k -> L[(p,c,a),k]; col >= 64C: b[(p,c,a)])
-// bk6[p][a][col] (transpose of bk1[p]).
+// bk6[part][p][a][col]: the transpose of bk1[p] split into three bf16 parts (h, m, l; see split3),
+// one after another, for the split-bf16 products of node_expand_grad.
 __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __restrict__ b,
-                                    float* __restrict__ bk1, float* __restrict__ bk6, int C) {
+                                    float* __restrict__ bk1, __bf16* __restrict__ bk6, int C) {
   const int64_t cols = 65LL * C;
   const int64_t total = 6LL * cols * C;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
@@ -59,7 +60,13 @@ __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __
       v = b[(int64_t)p * C * C + (int64_t)c * C + a];
     }
     bk1[idx] = v;
-    bk6[((int64_t)p * C + a) * cols + col] = v;
+    const int64_t o = ((int64_t)p * C + a) * cols + col;
+    const __bf16 hb = (__bf16)v;
+    const float r1 = v - (float)hb;
+    const __bf16 mb = (__bf16)r1;
+    bk6[o] = hb;
+    bk6[total + o] = mb;
+    bk6[2 * total + o] = (__bf16)(r1 - (float)mb);
   }
 }
 
@@ -178,27 +185,28 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 // row (m, I) of path p, then dx[m][comp][a] = sum over the halves and the slots of comp
 // (node_expand_grad_combine).  A block's work unit is (path, 256-row tile, K half), one 64-row
 // strip per wave: all units are equally long, which keeps the blocks balanced although paths
-// 0-2 share component 0.  The four waves share the path's weights: each 32-column chunk of bk6
-// (C x 32) is loaded once per block into LDS (double-buffered) while the waves stream their own
-// dS rows, so a wave's loads are its dS strip and a quarter of the weight chunk.
+// 0-2 share component 0.  Products are split-bf16 (mfma_x6, fp32 accuracy at 2.7x the fp32 MFMA
+// rate): the weights come split (bk6 parts h, m, l), the dS rows are split in registers.  The four
+// waves share the path's weights: each 32-column chunk (C x 32 x 3 parts) is loaded once per block
+// into LDS (double-buffered) while the waves stream their own dS rows a chunk ahead.
 // Transposed product: bk6 rows (a) are the A operand, dS rows the B operand; tile at's A row
-// i is a = (C/4)*(i/4) + 4*at + i%4, so lane (r, q) ends with C/4 consecutive a of one row.
-// Chunk t+1 (dS in registers, bk6 via registers into the other LDS buffer) is loaded while
-// chunk t is multiplied.
+// i is a = (C/4)*(i/4) + 4*at + i%4, so lane (r, q) ends with C/4 consecutive a of one row; lane
+// group q holds chunk columns 8q..8q+7 of both operands.
 constexpr int NEG_ROWS = 256;   // slot rows per block
 
 template <int C>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
-                                                                  const float* __restrict__ bk6,
+                                                                  const __bf16* __restrict__ bk6,
                                                                   float* __restrict__ dxp,
                                                                   int64_t n_nodes, PathTiles tiles) {
   constexpr int COLS = 65 * C;
   constexpr int NA = C / 16;        // output a tiles
   constexpr int QW = C / 4;         // consecutive a per lane in the output
   constexpr int TPP = COLS / 32;    // K chunks per path
-  constexpr int NST = C * 8 / 256;  // float4 of a bk6 chunk per thread
-  static_assert(NST >= 1 && C * 8 % 256 == 0, "bk6 chunk staging assumes C % 32 == 0");
-  __shared__ f4 wsh[2][C][9];       // [buffer][a][4 consecutive K]; 9 avoids bank conflicts
+  constexpr int RS = 40;            // bf16 per LDS row: 32 + 8 padding
+  constexpr int NPC = 3 * C * 4;              // 16-byte pieces of a chunk (3 parts x C rows x 4)
+  constexpr int NST = (NPC + 255) / 256;      // per thread
+  __shared__ __align__(16) __bf16 wsh[2][3][C][RS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int kh = blockIdx.x & 1, bt = blockIdx.x >> 1;
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
     irow[rt] = I;
     rbase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 8 * q;
   }
-  const float* wp = bk6 + (int64_t)p * C * COLS;
+  const int64_t part = 6LL * C * COLS;   // bf16 per weight part
   f4 acc[4][NA];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
@@ -236,15 +244,22 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   auto load_w = [&](int t) {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      stg[i] = ld4(wp + (int64_t)(idx >> 3) * COLS + 32 * t + 4 * (idx & 7));
+      const int idx = threadIdx.x + 256 * i;   // (part, a, 8-column piece)
+      if (idx < NPC) {
+        const int pt = idx / (C * 4), rem = idx - pt * (C * 4);
+        stg[i] = *reinterpret_cast<const f4*>(bk6 + pt * part + ((int64_t)p * C + (rem >> 2)) * COLS + 32 * t +
+                                              8 * (rem & 3));
+      }
     }
   };
   auto store_w = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int idx = threadIdx.x + 256 * i;
-      wsh[buf][idx >> 3][idx & 7] = stg[i];
+      if (idx < NPC) {
+        const int pt = idx / (C * 4), rem = idx - pt * (C * 4);
+        *reinterpret_cast<f4*>(&wsh[buf][pt][rem >> 2][8 * (rem & 3)]) = stg[i];
+      }
     }
   };
   auto load_ds = [&](f4 (&b)[4][2], int t) {
@@ -265,14 +280,22 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
       load_ds(bn, t + 1);
     }
     __builtin_amdgcn_sched_barrier(0);
+    bf8 dh[4], dm[4], dl[4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int rt = 0; rt < 4; ++rt) {
+      const float v[8] = {bc[rt][0].x, bc[rt][0].y, bc[rt][0].z, bc[rt][0].w,
+                          bc[rt][1].x, bc[rt][1].y, bc[rt][1].z, bc[rt][1].w};
+      split3(v, dh[rt], dm[rt], dl[rt]);
+    }
 #pragma unroll
-      for (int at = 0; at < NA; ++at) {
-        const f4 a4 = wsh[buf][QW * (r >> 2) + 4 * at + (r & 3)][2 * q + u];
+    for (int at = 0; at < NA; ++at) {
+      const int a = QW * (r >> 2) + 4 * at + (r & 3);
+      const bf8 wh = *reinterpret_cast<const bf8*>(&wsh[buf][0][a][8 * q]);
+      const bf8 wm = *reinterpret_cast<const bf8*>(&wsh[buf][1][a][8 * q]);
+      const bf8 wl = *reinterpret_cast<const bf8*>(&wsh[buf][2][a][8 * q]);
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_k16(a4, bc[rt][u], acc[rt][at]);
-      }
+      for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_x6(wh, wm, wl, dh[rt], dm[rt], dl[rt], acc[rt][at]);
+    }
     if (t + 1 < te) {
       store_w(buf ^ 1);
 #pragma unroll
@@ -976,7 +999,8 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
     float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums (Gt is dead)
     {
       LaunchTimer tm("node_expand_grad", st);
-      node_expand_grad_kernel<C><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(dS, bk6, dxp, N, tiles);
+      node_expand_grad_kernel<C><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(
+          dS, reinterpret_cast<const __bf16*>(bk6), dxp, N, tiles);
     }
     if (check_launch("sparse node_expand_grad")) return 2;
     node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N);
@@ -1008,7 +1032,7 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
                                     float* bk1, float* bk6, hipStream_t stream) {
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_prepare_weights: channels must be 32 or 64");
   FSC_CHECK_ARG(w_last && b_last && bk1 && bk6, "fsc_sparse_conv_prepare_weights: null pointer");
-  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, bk1, bk6, channels);
+  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, bk1, reinterpret_cast<__bf16*>(bk6), channels);
   return check_launch("sparse prepare_weights") ? 2 : 0;
 }
 
