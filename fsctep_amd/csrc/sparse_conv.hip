@@ -39,11 +39,11 @@ constexpr int kPathL1H[6] = {0, 0, 0, 1, 1, 2};
 __host__ __device__ inline int64_t s_node_stride(int C) { return (int64_t)NSLOT * 65 * C; }
 
 // ---------------------------------------------------------------- weight preparation
-// bk1[p][col][a] (col < 64C: col = c*64+k -> L[(p,c,a),k]; col >= 64C: b[(p,c,a)])
-// bk6[part][p][a][col]: the transpose of bk1[p] split into three bf16 parts (h, m, l; see split3),
-// one after another, for the split-bf16 products of node_expand_grad.
+// bk1[part][p][col][a] (col < 64C: col = c*64+k -> L[(p,c,a),k]; col >= 64C: b[(p,c,a)]) and
+// bk6[part][p][a][col] (transpose of bk1[p]), each split into three bf16 parts (h, m, l; see split3)
+// stored one after another, for the split-bf16 products of node_expand and node_expand_grad.
 __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __restrict__ b,
-                                    float* __restrict__ bk1, __bf16* __restrict__ bk6, int C) {
+                                    __bf16* __restrict__ bk1, __bf16* __restrict__ bk6, int C) {
   const int64_t cols = 65LL * C;
   const int64_t total = 6LL * cols * C;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
@@ -59,23 +59,27 @@ __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __
       const int c = (int)(col - 64LL * C);
       v = b[(int64_t)p * C * C + (int64_t)c * C + a];
     }
-    bk1[idx] = v;
     const int64_t o = ((int64_t)p * C + a) * cols + col;
     const __bf16 hb = (__bf16)v;
     const float r1 = v - (float)hb;
     const __bf16 mb = (__bf16)r1;
+    const __bf16 lb = (__bf16)(r1 - (float)mb);
+    bk1[idx] = hb;
+    bk1[total + idx] = mb;
+    bk1[2 * total + idx] = lb;
     bk6[o] = hb;
     bk6[total + o] = mb;
-    bk6[2 * total + o] = (__bf16)(r1 - (float)mb);
+    bk6[2 * total + o] = lb;
   }
 }
 
 // ---------------------------------------------------------------- K1: node expansion
 // S[m][sbase(p)+I][col] = sum_a x[m][comp0(p)+I][a] * bk1[p][col][a].  A block takes 128 rows
 // (m, I) of one path (4 waves x 32 rows; blocks numbered path by path, `off` = first block of
-// each path) and a group of 80-column tiles.  The rows of x stay in registers; each column
-// tile of bk1 (80 x C) is staged in LDS, the next one loaded while the current one is
-// multiplied and written to the other LDS buffer before the current results are stored.
+// each path) and a group of 80-column tiles.  Products are split-bf16 (mfma_x6, K = C in steps of
+// 32): the rows of x are split once into registers; each column tile of bk1 (80 x C, three bf16
+// parts) is staged in LDS, the next one loaded while the current one is multiplied and written to
+// the other LDS buffer before the current results are stored.
 // Transposed product: bk1 rows are the MFMA A operand and x rows the B operand, and tile j's
 // A row i is column 16*j + i, so lane (r, q) ends with columns 16j+4q..16j+4q+3 of row r: the
 // four lanes of a row store 64 contiguous bytes per instruction.  Stores go through a buffer
@@ -88,14 +92,17 @@ constexpr int NE_TPB = 13;     // 80-column tiles per node_expand block
 
 template <int C>
 __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __restrict__ x,
-                                                             const float* __restrict__ bk1,
+                                                             const __bf16* __restrict__ bk1,
                                                              float* __restrict__ S, int64_t n_nodes,
                                                              PathTiles tiles) {
-  constexpr int COLS = 65 * C, NT = 5, WCOLS = 16 * NT, KT = C / 16, RW = C / 4 + 1;
+  constexpr int COLS = 65 * C, NT = 5, WCOLS = 16 * NT, KS = C / 32;
   constexpr int NTC = COLS / WCOLS;                  // column tiles (52 or 26)
   constexpr int NCG = (NTC + NE_TPB - 1) / NE_TPB;   // column groups
   constexpr int RT = NE_ROWS / 64;                   // 16-row tiles per wave
-  __shared__ f4 sb[2][WCOLS][RW];
+  constexpr int RW = C + 8;                          // bf16 per LDS row (padding against bank conflicts)
+  constexpr int NPC = 3 * WCOLS * (C / 8);           // 16-byte pieces of a tile
+  constexpr int NST = (NPC + 255) / 256;
+  __shared__ __align__(16) __bf16 sb[2][3][WCOLS][RW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int bt = blockIdx.x / NCG, cg = blockIdx.x % NCG;
@@ -108,14 +115,15 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   const int64_t rows = n_nodes * nI;
   const int64_t brow0 = (int64_t)(bt - tiles.off[p]) * NE_ROWS;
   const int64_t row0 = brow0 + wave * (16 * RT);
-  const float* bp = bk1 + (int64_t)p * COLS * C;
+  const int64_t part = 6LL * COLS * C;               // bf16 per weight part
+  const __bf16* bp = bk1 + (int64_t)p * COLS * C;
   const int ct0 = cg * NE_TPB, ct1 = min(NTC, ct0 + NE_TPB);
   // store window: the nodes of the block's rows (at most NE_ROWS nodes, well below 4 GiB)
   const int64_t mfirst = (uint32_t)brow0 / (uint32_t)nI;
   const int64_t mlast = min(n_nodes - 1, (int64_t)((uint32_t)(brow0 + NE_ROWS - 1) / (uint32_t)nI));
   const __amdgpu_buffer_rsrc_t out =
       buffer_rsrc(S + mfirst * s_node_stride(C), (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * 4));
-  f4 xb[RT][KT];
+  bf8 xh[RT][KS], xm[RT][KS], xl[RT][KS];
   uint32_t ooff[RT];   // byte offset of the lane's first column in the store window
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -123,27 +131,37 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
     const bool ok = row < rows;
     const int64_t m = ok ? (int64_t)((uint32_t)row / (uint32_t)nI) : mfirst;
     const int I = ok ? (int)(row - m * nI) : 0;
-    const float* xr = x + (m * NCOMP + comp0 + I) * C + 4 * q;
+    const float* xr = x + (m * NCOMP + comp0 + I) * C + 8 * q;
 #pragma unroll
-    for (int t = 0; t < KT; ++t) xb[rt][t] = ld4(xr + 16 * t);
+    for (int ks = 0; ks < KS; ++ks) {
+      const f4 x0 = ld4(xr + 32 * ks), x1 = ld4(xr + 32 * ks + 4);
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      split3(v, xh[rt][ks], xm[rt][ks], xl[rt][ks]);
+    }
     ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * 4)
                   : kDropOffset;
   }
-  constexpr int NSTG = (WCOLS * (C / 4) + 255) / 256;
-  f4 stg[NSTG];
+  f4 stg[NST];
   auto gload = [&](int ct) {
 #pragma unroll
-    for (int i = 0; i < NSTG; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      if (idx < WCOLS * (C / 4))
-        stg[i] = ld4(bp + (int64_t)(ct * WCOLS + idx / (C / 4)) * C + 4 * (idx % (C / 4)));
+    for (int i = 0; i < NST; ++i) {
+      const int idx = threadIdx.x + 256 * i;   // (part, column, 8-entry piece of a)
+      if (idx < NPC) {
+        const int pt = idx / (WCOLS * (C / 8)), rem = idx - pt * (WCOLS * (C / 8));
+        const int col = rem / (C / 8), a8 = rem % (C / 8);
+        stg[i] = *reinterpret_cast<const f4*>(bp + pt * part + (int64_t)(ct * WCOLS + col) * C + 8 * a8);
+      }
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < NSTG; ++i) {
+    for (int i = 0; i < NST; ++i) {
       const int idx = threadIdx.x + 256 * i;
-      if (idx < WCOLS * (C / 4)) sb[buf][idx / (C / 4)][idx % (C / 4)] = stg[i];
+      if (idx < NPC) {
+        const int pt = idx / (WCOLS * (C / 8)), rem = idx - pt * (WCOLS * (C / 8));
+        const int col = rem / (C / 8), a8 = rem % (C / 8);
+        *reinterpret_cast<f4*>(&sb[buf][pt][col][8 * a8]) = stg[i];
+      }
     }
   };
   gload(ct0);
@@ -152,11 +170,6 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   for (int ct = ct0; ct < ct1; ++ct) {
     const int buf = (ct - ct0) & 1;
     if (ct + 1 < ct1) gload(ct + 1);
-    f4 a4[NT][KT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int t = 0; t < KT; ++t) a4[j][t] = sb[buf][16 * j + r][4 * t + q];
     f4 acc[RT][NT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -165,9 +178,14 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf8 wh = *reinterpret_cast<const bf8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
+        const bf8 wm = *reinterpret_cast<const bf8*>(&sb[buf][1][16 * j + r][32 * ks + 8 * q]);
+        const bf8 wl = *reinterpret_cast<const bf8*>(&sb[buf][2][16 * j + r][32 * ks + 8 * q]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_k16(a4[j][t], xb[rt][t], acc[rt][j]);
+        for (int rt = 0; rt < RT; ++rt)
+          acc[rt][j] = mfma_x6(wh, wm, wl, xh[rt][ks], xm[rt][ks], xl[rt][ks], acc[rt][j]);
+      }
     // stage the next tile first: the waits for its loads then do not cover this tile's stores
     __builtin_amdgcn_sched_barrier(0);
     if (ct + 1 < ct1) sstore(buf ^ 1);
@@ -342,8 +360,9 @@ __global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, f
 
 // ---------------------------------------------------------------- K2: edge message
 // One block (3 waves) per source node; P[eid][col] = sum_k h[eid][k] S[m][col][k] + Sb[m][col].
-// Transposed product: S rows (columns of P) are the A operand, the node's edges (h rows,
-// staged in LDS) the B operand.  A wave takes 32-column blocks of P's chunk-major column order;
+// Transposed product: S rows (columns of P) are the A operand, the node's edges (h rows, split into
+// three bf16 planes in LDS) the B operand; products are split-bf16 (mfma_x6, K = 64 in two steps),
+// the S rows split in registers.  A wave takes 32-column blocks of P's chunk-major column order;
 // tile jt's A row i is column 8*(i/4) + 4*jt + i%4 of the block, so lane (r, q) ends with 8
 // consecutive columns of edge r: two float4 stores, 128 contiguous bytes per edge per block.
 constexpr int EP = 64;   // edges per pass held in LDS
@@ -354,7 +373,8 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
                                                            const int32_t* __restrict__ src_ptr,
                                                            const int32_t* __restrict__ src_perm,
                                                            float* __restrict__ P) {
-  __shared__ float hs[EP][KH + 4];
+  constexpr int HR = KH + 8;   // bf16 per LDS row: 64 + 8 padding
+  __shared__ __align__(16) __bf16 hs3[3][EP][HR];
   __shared__ int32_t eids[EP];
   const int m = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -367,8 +387,9 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
   constexpr int NCB = NCOL / BW;
   const float* Sm = S + (int64_t)m * s_node_stride(C);
 
-  // a[jt][0..3]: S row of A row r of tile jt (K = 64); a[jt][4]: the biases of the lane's four
-  // output columns of tile jt.  Column block cb+3 is loaded while block cb is multiplied.
+  // a[jt][0..3]: S row of A row r of tile jt at k = 8q..8q+7 (0, 1) and 32+8q..32+8q+7 (2, 3);
+  // a[jt][4]: the biases of the lane's four output columns of tile jt.  Column block cb+3 is loaded
+  // while block cb is multiplied.
   f4 a0[NJ][5], a1[NJ][5];
   // Columns are numbered in P's chunk-major order: col = ch*144 + slot*8 + cl for channel c = 8*ch + cl.
   auto load = [&](f4 (&a)[NJ][5], int cb) {
@@ -376,9 +397,11 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
     for (int jt = 0; jt < NJ; ++jt) {
       const int col = cb * BW + 4 * NJ * (r >> 2) + 4 * jt + (r & 3);
       const int rem = col % (8 * NSLOT), slot = rem / 8, c = 8 * (col / (8 * NSLOT)) + rem % 8;
-      const float* srow = Sm + (int64_t)slot * COLS + c * KH + 4 * q;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) a[jt][t] = ld4(srow + 16 * t);
+      const float* srow = Sm + (int64_t)slot * COLS + c * KH + 8 * q;
+      a[jt][0] = ld4(srow);
+      a[jt][1] = ld4(srow + 4);
+      a[jt][2] = ld4(srow + 32);
+      a[jt][3] = ld4(srow + 36);
       const int colq = cb * BW + 4 * NJ * q + 4 * jt;   // four consecutive channels of one slot
       const int remq = colq % (8 * NSLOT);
       a[jt][4] = ld4(Sm + (int64_t)(remq / 8) * COLS + 64 * C + 8 * (colq / (8 * NSLOT)) + remq % 8);
@@ -391,20 +414,18 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
     __syncthreads();
     if (threadIdx.x < EP) eids[threadIdx.x] = src_perm[pb + min((int)threadIdx.x, cnt - 1)];
     __syncthreads();
-    {
-      // rows e >= cnt repeat edge cnt-1 (their results are not stored)
-      constexpr int NV = (EP * KH / 4 + 191) / 192;
-      f4 v[NV];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int idx = threadIdx.x + 192 * i;
-        if (idx < EP * (KH / 4)) v[i] = ld4(h + (int64_t)eids[idx / (KH / 4)] * KH + (idx % (KH / 4)) * 4);
-      }
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int idx = threadIdx.x + 192 * i;
-        if (idx < EP * (KH / 4)) *reinterpret_cast<f4*>(&hs[idx / (KH / 4)][(idx % (KH / 4)) * 4]) = v[i];
-      }
+    // h rows split into the three planes, 8 consecutive k per thread; rows e >= cnt repeat edge cnt-1
+    // (their results are not stored)
+    for (int idx = threadIdx.x; idx < EP * (KH / 8); idx += 192) {
+      const int e = idx / (KH / 8), k8 = idx % (KH / 8);
+      const float* hp = h + (int64_t)eids[e] * KH + 8 * k8;
+      const f4 x0 = ld4(hp), x1 = ld4(hp + 4);
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      bf8 bh, bm, bl;
+      split3(v, bh, bm, bl);
+      *reinterpret_cast<bf8*>(&hs3[0][e][8 * k8]) = bh;
+      *reinterpret_cast<bf8*>(&hs3[1][e][8 * k8]) = bm;
+      *reinterpret_cast<bf8*>(&hs3[2][e][8 * k8]) = bl;
     }
     __syncthreads();
     const int nrt = (cnt + 15) / 16;
@@ -414,14 +435,26 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       for (int et = 0; et < 4; ++et)
 #pragma unroll
         for (int jt = 0; jt < NJ; ++jt) acc[et][jt] = f4{0.f, 0.f, 0.f, 0.f};
+      bf8 ah[NJ][2], am[NJ][2], al[NJ][2];
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const f4 x0 = a[jt][2 * ks], x1 = a[jt][2 * ks + 1];
+          const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          split3(v, ah[jt][ks], am[jt][ks], al[jt][ks]);
+        }
 #pragma unroll
       for (int et = 0; et < 4; ++et) {
         if (et < nrt) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const f4 b4 = *reinterpret_cast<const f4*>(&hs[16 * et + r][16 * t + 4 * q]);
+          for (int ks = 0; ks < 2; ++ks) {
+            const bf8 bh = *reinterpret_cast<const bf8*>(&hs3[0][16 * et + r][32 * ks + 8 * q]);
+            const bf8 bm = *reinterpret_cast<const bf8*>(&hs3[1][16 * et + r][32 * ks + 8 * q]);
+            const bf8 bl = *reinterpret_cast<const bf8*>(&hs3[2][16 * et + r][32 * ks + 8 * q]);
 #pragma unroll
-            for (int jt = 0; jt < NJ; ++jt) acc[et][jt] = mfma_k16(a[jt][t], b4, acc[et][jt]);
+            for (int jt = 0; jt < NJ; ++jt)
+              acc[et][jt] = mfma_x6(ah[jt][ks], am[jt][ks], al[jt][ks], bh, bm, bl, acc[et][jt]);
           }
         }
       }
@@ -959,7 +992,8 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
       tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + NE_ROWS - 1) / NE_ROWS);
     constexpr int ncg = ((65 * C) / 80 + NE_TPB - 1) / NE_TPB;
     LaunchTimer tm("node_expand", st);
-    node_expand_kernel<C><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(x, bk1, S, N, tiles);
+    node_expand_kernel<C><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(
+        x, reinterpret_cast<const __bf16*>(bk1), S, N, tiles);
   }
   if (check_launch("sparse node_expand")) return 2;
   {
@@ -1032,7 +1066,8 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
                                     float* bk1, float* bk6, hipStream_t stream) {
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_prepare_weights: channels must be 32 or 64");
   FSC_CHECK_ARG(w_last && b_last && bk1 && bk6, "fsc_sparse_conv_prepare_weights: null pointer");
-  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, bk1, reinterpret_cast<__bf16*>(bk6), channels);
+  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, reinterpret_cast<__bf16*>(bk1),
+                                                reinterpret_cast<__bf16*>(bk6), channels);
   return check_launch("sparse prepare_weights") ? 2 : 0;
 }
 

@@ -51,10 +51,10 @@ int fsc_timing_end(double* total_ms, int64_t* launches);
 int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels,
                               int64_t* s_floats, int64_t* p_floats);
 
-/* Re-layout fc.4.weight (6*C*C, 64) and fc.4.bias (6*C*C) into the two kernel operands:
- * bk1 (6*65*C*C floats) and bk6 (the transposed operand split into three bfloat16 parts of 6*65*C*C
- * values each, for fp32-accurate split-bf16 products; 6*65*C*C*3/2 floats of storage).  Both are
- * opaque to the caller.  Call again whenever those parameters change. */
+/* Re-layout fc.4.weight (6*C*C, 64) and fc.4.bias (6*C*C) into the two kernel operands bk1 and
+ * bk6 (the operand and its transpose, each split into three bfloat16 parts of 6*65*C*C values, for
+ * fp32-accurate split-bf16 products; 6*65*C*C*3/2 floats of storage each).  Both are opaque to the
+ * caller.  Call again whenever those parameters change. */
 int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, int32_t channels,
                                     float* bk1, float* bk6, hipStream_t stream);
 

@@ -45,7 +45,7 @@ int main(int argc, char** argv) {
   auto [Wf, Wb] = prep.call(W);
   auto t = at::empty({7, 9, 192}, meta);
   auto x = at::empty({10, 13, 64}, meta), h = at::empty({30, 64}, meta), nv = at::empty({30, 3}, meta);
-  auto bk = at::empty({6 * 65 * 64 * 64}, meta);
+  auto bk = at::empty({6 * 65 * 64 * 64 * 3 / 2}, meta);
   auto ip = at::empty({11}, at::device(at::kMeta).dtype(at::kInt)), ie = at::empty({30}, at::device(at::kMeta).dtype(at::kInt));
   auto sc = disp.findSchemaOrThrow("fsctep::sparse_conv", "")
                 .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(

@@ -66,7 +66,7 @@ def test_fake_kernels_trace_shapes():
         x = torch.empty(10, 13, 64)
         h = torch.empty(30, 64)
         n = torch.empty(30, 3)
-        bk = torch.empty(6 * 65 * 64 * 64)
+        bk = torch.empty(6 * 65 * 64 * 64 * 3 // 2)
         i = torch.empty(11, dtype=torch.int32)
         e = torch.empty(30, dtype=torch.int32)
         out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, 0.5)
