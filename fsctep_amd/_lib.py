@@ -33,7 +33,7 @@ SIGNATURES = {
     "fsc_ictd_conv_backward": [_p, _i64, _i64, _i32] + [_p] * 16,
     "fsc_ictd_conv1_forward": [_p, _i64, _i64, _i32] + [_p] * 7,
     "fsc_ictd_conv1_backward": [_p, _i64, _i64, _i32, _i32] + [_p] * 10,
-    "fsc_gram_sizes": [_i64, _i32, _i32, _pi64, _pi64],
+    "fsc_gram_sizes": [_i64, _i32, _i32, _pi64, _pi64, _pi64],
     "fsc_gram_prepare_weights": [_p, _i32, _i32, _p, _p, _p],
     "fsc_gram_forward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
     "fsc_gram_backward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],

@@ -49,17 +49,29 @@ __device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles
   tile = grp * TILE_GROUP + (rem - chunk * gsize);
 }
 
-// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).
+// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).  After the
+// P*256*S floats of Wb come the three bf16 planes (h, m, l; split3) of the same values, [plane][p][ab][o],
+// for the split-bf16 backward.
 __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
                                float* __restrict__ Wb) {
   const int I = blockIdx.y, J = blockIdx.x, nb = nC / 16;
   if (I > J) return;
   const int p = pair_index(I, J, nb);
+  const int64_t plane = (int64_t)n_pairs(nb) * 256 * S;
+  __bf16* wb3 = reinterpret_cast<__bf16*>(Wb + plane);
   for (int idx = threadIdx.x; idx < 256 * S; idx += blockDim.x) {
     const int o = idx % S, ab = idx / S, a = ab / 16, b = ab % 16;
     const float wij = W[((int64_t)o * nC + I * 16 + a) * nC + J * 16 + b];
     const float wji = W[((int64_t)o * nC + J * 16 + b) * nC + I * 16 + a];
-    Wb[((int64_t)p * 256 + ab) * S + o] = wij + wji;
+    const float v = wij + wji;
+    const int64_t e = ((int64_t)p * 256 + ab) * S + o;
+    Wb[e] = v;
+    const __bf16 hb = (__bf16)v;
+    const float r1 = v - (float)hb;
+    const __bf16 mb = (__bf16)r1;
+    wb3[e] = hb;
+    wb3[plane + e] = mb;
+    wb3[2 * plane + e] = (__bf16)(r1 - (float)mb);
     Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = (I == J) ? wij : wij + wji;
   }
 }
@@ -256,6 +268,124 @@ __global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float 
   }
 }
 
+// Split-bf16 version of backward_kernel (mfma_x6; fp32 accuracy, 2.7x the fp32 MFMA rate): the
+// (W + W^T) block is staged from its three bf16 planes, g is split once per wave, K = o runs in steps
+// of 32 (lane group q: o = 32 ks + 8q .. +7).  Same work split, contraction and output as above; the
+// planes take 1.5x the LDS of the fp32 block, so one workgroup runs per CU.
+template <int D, int S, int ILW>
+__global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, float scale,
+                                                            const float* __restrict__ g, const float* __restrict__ t,
+                                                            const __bf16* __restrict__ Wb3, float* __restrict__ dt) {
+  constexpr int NGRP = 16 / ILW;                 // waves sharing a node group
+  constexpr int NN = 16 * 8 / NGRP;              // nodes per workgroup
+  constexpr int KS = S / 32;
+  constexpr int RS = S + 8, AS = 16 * RS + 8, PS = 16 * AS;   // padded bf16 strides of b, a and a plane
+  constexpr int PW = 3 * 256 * S / 8 / 512;                   // 16-byte pieces of a block per thread
+  static_assert(3 * 256 * S / 8 % 512 == 0, "block staging");
+  __shared__ __align__(16) __bf16 wl[3 * PS];
+  const int nb = nC / 16, np = n_pairs(nb);
+  const int ntiles = (int)((N + NN - 1) / NN);
+  const int logical = xcd_logical(nb * ntiles);
+  if (logical < 0) return;
+  const int I = logical / ntiles, tile = logical - I * ntiles;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int il0 = (wave % NGRP) * ILW;
+  const int64_t n = (int64_t)tile * NN + (wave / NGRP) * 16 + r;
+  const bool valid = n < N;
+  const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  bf8 gh[KS], gm[KS], gl[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const f4 x0 = valid ? ld4(g + n * S + 32 * ks + 8 * q) : zero;
+    const f4 x1 = valid ? ld4(g + n * S + 32 * ks + 8 * q + 4) : zero;
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    split3(v, gh[ks], gm[ks], gl[ks]);
+  }
+  float acc[ILW][D];
+#pragma unroll
+  for (int i = 0; i < ILW; ++i)
+#pragma unroll
+    for (int m = 0; m < D; ++m) acc[i][m] = 0.f;
+  f4 pw[PW], tq[D];
+  const int64_t plane = (int64_t)np * 256 * S;
+  auto fetch = [&](int J) {
+    const int pr = (I <= J) ? pair_index(I, J, nb) : pair_index(J, I, nb);
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int idx = threadIdx.x + 512 * i;   // (plane, 8-value piece of the block)
+      const int pl = idx / (256 * S / 8), rem = idx - pl * (256 * S / 8);
+      pw[i] = *reinterpret_cast<const f4*>(Wb3 + pl * plane + (int64_t)pr * 256 * S + 8 * rem);
+    }
+#pragma unroll
+    for (int m = 0; m < D; ++m) tq[m] = ld4(t + (nl * D + m) * nC + J * 16 + 4 * q);
+  };
+  fetch(0);
+  for (int J = 0; J < nb; ++J) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int idx = threadIdx.x + 512 * i;
+      const int pl = idx / (256 * S / 8), rem = idx - pl * (256 * S / 8);
+      const int ab = rem / (S / 8), o8 = rem % (S / 8);
+      *reinterpret_cast<f4*>(&wl[pl * PS + (ab >> 4) * AS + (ab & 15) * RS + 8 * o8]) = pw[i];
+    }
+    __syncthreads();
+    f4 tc[D];
+#pragma unroll
+    for (int m = 0; m < D; ++m) tc[m] = tq[m];
+    if (J + 1 < nb) fetch(J + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // A[row = jl][k = o] = (W + W^T)[o][I0 + il][J0 + jl]: block [a = il][b = jl] if I <= J, else [a = jl][b = il]
+    const bool upper = I <= J;
+    const int rbase = (upper ? r * RS : r * AS) + 8 * q;
+    const int ilstep = upper ? AS : RS;
+#pragma unroll
+    for (int i4 = 0; i4 < ILW / 4; ++i4) {
+      f4 dd[4] = {zero, zero, zero, zero};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int off = rbase + (il0 + 4 * i4 + jj) * ilstep + 32 * ks;
+          const bf8 ah = *reinterpret_cast<const bf8*>(&wl[off]);
+          const bf8 am = *reinterpret_cast<const bf8*>(&wl[PS + off]);
+          const bf8 al = *reinterpret_cast<const bf8*>(&wl[2 * PS + off]);
+          dd[jj] = mfma_x6(ah, am, al, gh[ks], gm[ks], gl[ks], dd[jj]);
+        }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int m = 0; m < D; ++m)
+          acc[4 * i4 + jj][m] += dd[jj][0] * tc[m][0] + dd[jj][1] * tc[m][1] + dd[jj][2] * tc[m][2] +
+                                 dd[jj][3] * tc[m][3];
+    }
+  }
+  constexpr int H = ILW / 2, QR = ILW / 4;
+  const bool hi = (q & 2) != 0, odd = (q & 1) != 0;
+  float h1[H][D];
+#pragma unroll
+  for (int i = 0; i < H; ++i)
+#pragma unroll
+    for (int m = 0; m < D; ++m)
+      h1[i][m] = (hi ? acc[H + i][m] : acc[i][m]) + __shfl_xor(hi ? acc[i][m] : acc[H + i][m], 32, 64);
+  float h2[QR][D];
+#pragma unroll
+  for (int i = 0; i < QR; ++i)
+#pragma unroll
+    for (int m = 0; m < D; ++m)
+      h2[i][m] = (odd ? h1[QR + i][m] : h1[i][m]) + __shfl_xor(odd ? h1[i][m] : h1[QR + i][m], 16, 64);
+  if (valid) {
+#pragma unroll
+    for (int m = 0; m < D; ++m) {
+      float* o = dt + (n * D + m) * nC + I * 16 + il0 + QR * q;
+#pragma unroll
+      for (int i = 0; i < QR; ++i) o[i] = h2[i][m] * scale;
+    }
+  }
+}
+
 int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
   if (N < 0 || N >= (1LL << 31) || nC < 16 || nC % 16 != 0 || nC > 16 * 64 || !(S == 32 || S == 64) ||
       !(D == 1 || D == 3 || D == 5 || D == 7 || D == 9)) {
@@ -292,20 +422,23 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
 template <int S>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
-  // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8
+  // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8.  D <= 7 use the
+  // split-bf16 kernel; at D 9 its accumulators and plane staging exceed the registers, so the fp32 one.
   const int nn = (D <= 5) ? NODES : NODES / 2;
   const int ntiles = (int)((N + nn - 1) / nn);
   const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
+  const __bf16* Wb3 = reinterpret_cast<const __bf16*>(Wb + (int64_t)n_pairs(nC / 16) * 256 * S);
   LaunchTimer tm("gram_backward", st);
-#define FSC_GB(DD) backward_kernel<DD, S, (DD <= 5 ? 16 : 8)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt)
+#define FSC_GBB(DD) \
+  backward_bf16_kernel<DD, S, (DD <= 5 ? 16 : 8)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb3, dt)
   switch (D) {
-    case 1: FSC_GB(1); break;
-    case 3: FSC_GB(3); break;
-    case 5: FSC_GB(5); break;
-    case 7: FSC_GB(7); break;
-    default: FSC_GB(9); break;
+    case 1: FSC_GBB(1); break;
+    case 3: FSC_GBB(3); break;
+    case 5: FSC_GBB(5); break;
+    case 7: FSC_GBB(7); break;
+    default: backward_kernel<9, S, 8><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt); break;
   }
-#undef FSC_GB
+#undef FSC_GBB
   return check_launch("gram backward") ? 2 : 0;
 }
 
@@ -317,11 +450,13 @@ using namespace fsc::gram;
 
 extern "C" {
 
-int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* weight_floats, int64_t* workspace_floats) {
-  FSC_CHECK_ARG(weight_floats && workspace_floats, "fsc_gram_sizes: null pointer");
+int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, int64_t* wb_floats,
+                   int64_t* workspace_floats) {
+  FSC_CHECK_ARG(wf_floats && wb_floats && workspace_floats, "fsc_gram_sizes: null pointer");
   FSC_CHECK_ARG(n_nodes >= 0 && nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
                 "fsc_gram_sizes: nC must be a multiple of 16 (<= 1024), S 32 or 64");
-  *weight_floats = (int64_t)n_pairs(nC / 16) * 256 * S;
+  *wf_floats = (int64_t)n_pairs(nC / 16) * 256 * S;
+  *wb_floats = *wf_floats * 5 / 2;   // fp32 block pairs, then three bf16 planes
   *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S;
   return 0;
 }

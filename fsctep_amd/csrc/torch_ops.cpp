@@ -294,7 +294,8 @@ std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
   TORCH_CHECK(W_.dim() == 3 && W_.size(1) == W_.size(2), "W must be (S, nC, nC)");
   const int64_t S = W_.size(0), nC = W_.size(1), nb = nC / 16, P = nb * (nb + 1) / 2;
   Tensor W = f32c(W_);
-  Tensor Wf = at::empty({P, 16, S, 16}, fopts(W)), Wb = at::empty({P, 256, S}, fopts(W));
+  // Wb: the fp32 block pairs (P*256*S floats) followed by their three bf16 planes (1.5x that), flat
+  Tensor Wf = at::empty({P, 16, S, 16}, fopts(W)), Wb = at::empty({P * 256 * S * 5 / 2}, fopts(W));
   check(fsc_gram_prepare_weights(cf(W), (int32_t)S, (int32_t)nC, mf(Wf), mf(Wb), stream_of(W)),
         "fsc_gram_prepare_weights");
   return {Wf, Wb};
@@ -302,17 +303,17 @@ std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
 
 std::tuple<Tensor, Tensor> gram_prepare_weights_meta(const Tensor& W) {
   const int64_t S = W.size(0), nb = W.size(1) / 16, P = nb * (nb + 1) / 2;
-  return {at::empty({P, 16, S, 16}, fopts(W)), at::empty({P, 256, S}, fopts(W))};
+  return {at::empty({P, 16, S, 16}, fopts(W)), at::empty({P * 256 * S * 5 / 2}, fopts(W))};
 }
 
 Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale) {
   require_gpu({t_, Wf, Wb});
-  TORCH_CHECK(t_.dim() == 3 && Wb.dim() == 3, "t must be (N, D, nC) and Wb (P, 256, S)");
-  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wb.size(2);
+  TORCH_CHECK(t_.dim() == 3 && Wf.dim() == 4, "t must be (N, D, nC) and Wf (P, 16, S, 16)");
+  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wf.size(2);
   Tensor t = f32c(t_);
-  int64_t wn = 0, wsn = 0;
-  check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wn, &wsn), "fsc_gram_sizes");
-  TORCH_CHECK(Wf.numel() == wn && Wb.numel() == wn, "prepared Gram weights do not match nC = ", nC);
+  int64_t wfn = 0, wbn = 0, wsn = 0;
+  check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
+  TORCH_CHECK(Wf.numel() == wfn && Wb.numel() == wbn, "prepared Gram weights do not match nC = ", nC);
   Tensor ws = at::empty({std::max<int64_t>(wsn, 1)}, fopts(t)), out = at::empty({N, S}, fopts(t));
   check(fsc_gram_forward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(t), cf(Wf), mf(ws), mf(out),
                          stream_of(t)),
@@ -320,13 +321,17 @@ Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, doubl
   return out;
 }
 
-Tensor gram_bilinear_meta(const Tensor& t, const Tensor&, const Tensor& Wb, double) {
-  return at::empty({t.size(0), Wb.size(2)}, fopts(t));
+Tensor gram_bilinear_meta(const Tensor& t, const Tensor& Wf, const Tensor&, double) {
+  return at::empty({t.size(0), Wf.size(2)}, fopts(t));
 }
 
 Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t_, const Tensor& Wb, double scale) {
   require_gpu({grad_out, t_, Wb});
-  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wb.size(2);
+  TORCH_CHECK(grad_out.dim() == 2 && t_.dim() == 3, "grad_out must be (N, S) and t (N, D, nC)");
+  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = grad_out.size(1);
+  int64_t wfn = 0, wbn = 0, wsn = 0;
+  check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
+  TORCH_CHECK(Wb.numel() == wbn, "prepared Gram weights do not match nC = ", nC);
   Tensor g = f32c(grad_out), t = f32c(t_);
   Tensor dt = at::empty({N, D, nC}, fopts(t));
   check(fsc_gram_backward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(g), cf(t), cf(Wb), mf(dt),
@@ -460,12 +465,12 @@ std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorLis
   return {scalars, sq};
 }
 
-std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList, at::TensorList Wb,
+std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList Wf, at::TensorList,
                                                  at::ArrayRef<double>, const Tensor&, const Tensor&,
                                                  const Tensor& table) {
   const FscReadoutTable* T = readout_table_of(table);
   const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
-  return {at::empty({N, Wb[0].size(2)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
+  return {at::empty({N, Wf[0].size(2)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
 }
 
 // ============================================================== autograd

@@ -36,11 +36,11 @@ from . import _lib
 _lib.load_torch_ops()
 
 
-def gram_sizes(n_nodes: int, nC: int, S: int) -> tuple[int, int]:
-    """(floats of one prepared weight layout, floats of the forward workspace)."""
-    w, ws = ctypes.c_int64(), ctypes.c_int64()
-    _lib.call("fsc_gram_sizes", int(n_nodes), int(nC), int(S), ctypes.byref(w), ctypes.byref(ws))
-    return int(w.value), int(ws.value)
+def gram_sizes(n_nodes: int, nC: int, S: int) -> tuple[int, int, int]:
+    """(floats of the prepared Wf, floats of the prepared Wb, floats of the forward workspace)."""
+    wf, wb, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _lib.call("fsc_gram_sizes", int(n_nodes), int(nC), int(S), ctypes.byref(wf), ctypes.byref(wb), ctypes.byref(ws))
+    return int(wf.value), int(wb.value), int(ws.value)
 
 
 class GramWeights:

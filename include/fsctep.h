@@ -213,10 +213,13 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
  * models/pure_cartesian_ictd_layers_o3.py:1017-1018; one call per irrep, scale (2l+1)^{-1/2}).
  * ------------------------------------------------------------------------------------------- */
 
-/* Floats of each prepared weight layout (Wf and Wb) and of the forward workspace. */
-int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* weight_floats, int64_t* workspace_floats);
+/* Floats of the prepared weight layouts Wf and Wb and of the forward workspace. */
+int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, int64_t* wb_floats,
+                   int64_t* workspace_floats);
 
-/* Block-pair layouts of W: Wf[p][16][S][16] (forward) and Wb[p][256][S] (backward, W + W^T). */
+/* Block-pair layouts of W: Wf[p][16][S][16] (forward) and, for the backward, Wb[p][256][S] (W + W^T)
+ * followed by the same values split into three bfloat16 planes [3][p][256][S] (fp32-accurate
+ * split-bf16 products); Wb is opaque to the caller. */
 int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, float* Wb, hipStream_t stream);
 
 /* out [N][S]; part_ws holds fsc_gram_sizes' workspace_floats (per-chunk partial sums). */
