@@ -10,7 +10,9 @@
 //
 // Channels split into nb = nC/16 blocks.  G is symmetric, so the forward sums block pairs I <= J only:
 //   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
-// with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  The backward is
+// with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  Both directions multiply in fp32
+// precision on bf16 MFMA where the registers allow (each operand split into three bf16 parts, six
+// part products kept; common.h), with the weights split once when they are prepared.  The backward is
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
 // computed per (node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
@@ -50,8 +52,8 @@ __device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles
 }
 
 // Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).  After the
-// P*256*S floats of Wb come the three bf16 planes (h, m, l; split3) of the same values, [plane][p][ab][o],
-// for the split-bf16 backward.
+// P*256*S floats of each come three bf16 planes (h, m, l; split3) of the same values: [plane][p][ab][o]
+// for the split-bf16 backward and [plane][p][jl][il/8][o][il%8] for the split-bf16 forward.
 __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
                                float* __restrict__ Wb) {
   const int I = blockIdx.y, J = blockIdx.x, nb = nC / 16;
@@ -59,6 +61,7 @@ __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float
   const int p = pair_index(I, J, nb);
   const int64_t plane = (int64_t)n_pairs(nb) * 256 * S;
   __bf16* wb3 = reinterpret_cast<__bf16*>(Wb + plane);
+  __bf16* wf3 = reinterpret_cast<__bf16*>(Wf + plane);
   for (int idx = threadIdx.x; idx < 256 * S; idx += blockDim.x) {
     const int o = idx % S, ab = idx / S, a = ab / 16, b = ab % 16;
     const float wij = W[((int64_t)o * nC + I * 16 + a) * nC + J * 16 + b];
@@ -72,7 +75,15 @@ __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float
     wb3[e] = hb;
     wb3[plane + e] = mb;
     wb3[2 * plane + e] = (__bf16)(r1 - (float)mb);
-    Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = (I == J) ? wij : wij + wji;
+    const float f = (I == J) ? wij : wij + wji;
+    Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = f;
+    const int64_t ef = (int64_t)p * 256 * S + ((b * 2 + (a >> 3)) * S + o) * 8 + (a & 7);
+    const __bf16 fh = (__bf16)f;
+    const float f1 = f - (float)fh;
+    const __bf16 fm = (__bf16)f1;
+    wf3[ef] = fh;
+    wf3[plane + ef] = fm;
+    wf3[2 * plane + ef] = (__bf16)(f1 - (float)fm);
   }
 }
 
@@ -146,6 +157,149 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
     if (node >= N) continue;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 16 + r] = acc[ct][i];
+  }
+}
+
+// Forward with split-bf16 products on v_mfma_f32_32x32x16_bf16 (32 nodes x 32 outputs per MFMA).  A
+// workgroup is 256 nodes (8 waves x 32) x one chunk of PCHUNK pairs; lane (r, q) of a wave is node r
+// and K half q.  Step s (0..15) of a pair contracts K = 8q + j <-> (il = 8q + j, jl = s), so a lane
+// keeps t[n][m][I0 + 8q + j] (unchanged along a row of pairs) and streams t[n][m][J0 + s] four steps at
+// a time: the next group's loads are issued once the group's last G values are formed (TSB = 1, in
+// flight during that step's products) or a whole group ahead into a second buffer (TSB = 2, 4D more
+// registers; no faster at these sizes).  The pair's three
+// weight planes ([jl][il/8][o][il%8]: the 32 lanes of a K half read 512 contiguous bytes) are staged
+// in LDS and shared by the 8 waves; the next pair's planes are loaded a quarter at a time after each
+// group's t loads, so waiting for those never waits for the weights (one in-order load counter).
+constexpr int NODES_BF = 256;
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+template <int D, int S, int TSB>
+__global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, float scale,
+                                                           const float* __restrict__ t,
+                                                           const __bf16* __restrict__ Wf3, int nchunks,
+                                                           float* __restrict__ part) {
+  constexpr int NN = NODES_BF, CT = S / 32;
+  constexpr int PSZ = 256 * S;            // bf16 per plane of a pair
+  constexpr int PW = 3 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
+  constexpr int PWQ = (PW + 3) / 4;
+  static_assert((3 * PSZ / 8) % 512 == 0, "staging");
+  __shared__ __align__(16) __bf16 wl[3 * PSZ];
+  const int nb = nC / 16, np = n_pairs(nb);
+  const int ntiles = (int)((N + NN - 1) / NN);
+  const int logical = xcd_logical(nchunks * ntiles);
+  if (logical < 0) return;
+  int chunk, tile;
+  group_order(logical, nchunks, ntiles, chunk, tile);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, q = lane >> 5;
+  const int64_t n = (int64_t)tile * NN + wave * 32 + r;
+  const bool valid = n < N;
+  const float* tn = t + (valid ? n : 0) * D * nC;   // rows past N read node 0; their results are not stored
+  const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
+  int I = 0, rowstart = 0;
+  while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
+  int J = I + (p0 - rowstart);
+  f16v acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[ct][v] = 0.f;
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  const int64_t plane = (int64_t)np * PSZ;
+  f4 pw[PW];
+  auto fetch_part = [&](int p, int k) {
+#pragma unroll
+    for (int i = k * PWQ; i < min(PW, (k + 1) * PWQ); ++i) {
+      const int idx = threadIdx.x + 512 * i;
+      const int pl = idx / (PSZ / 8), rem = idx - pl * (PSZ / 8);
+      pw[i] = *reinterpret_cast<const f4*>(Wf3 + pl * plane + (int64_t)p * PSZ + 8 * rem);
+    }
+  };
+  float tc[D][8];
+  auto load_tc = [&](int Ib) {
+#pragma unroll
+    for (int m = 0; m < D; ++m) {
+      const f4 a = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q) : zero;
+      const f4 b = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q + 4) : zero;
+      tc[m][0] = a.x; tc[m][1] = a.y; tc[m][2] = a.z; tc[m][3] = a.w;
+      tc[m][4] = b.x; tc[m][5] = b.y; tc[m][6] = b.z; tc[m][7] = b.w;
+    }
+  };
+  f4 ts[TSB][D];
+  auto load_ts = [&](int b, int Jb, int sg) {
+#pragma unroll
+    for (int m = 0; m < D; ++m) ts[b][m] = valid ? ld4(tn + m * nC + Jb * 16 + 4 * sg) : zero;
+  };
+  load_tc(I);
+  load_ts(0, J, 0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) fetch_part(p0, k);
+  const __bf16* wp = wl + q * S * 8 + r * 8;
+  for (int p = p0; p < p1; ++p) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PW; ++i) reinterpret_cast<f4*>(wl)[threadIdx.x + 512 * i] = pw[i];
+    __syncthreads();
+    const bool more = p + 1 < p1;
+    int In = I, Jn = J + 1;
+    if (Jn == nb) { ++In; Jn = In; }
+#pragma unroll
+    for (int sg = 0; sg < 4; ++sg) {
+      const int cur = (TSB == 2) ? (sg & 1) : 0;
+      if constexpr (TSB == 2) {
+        if (sg < 3) load_ts((sg + 1) & 1, J, sg + 1);
+        else if (more) load_ts(0, Jn, 0);
+        if (more) fetch_part(p + 1, sg);
+      }
+#pragma unroll
+      for (int ss = 0; ss < 4; ++ss) {
+        const int s = 4 * sg + ss;
+        float gv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float a = 0.f;
+#pragma unroll
+          for (int m = 0; m < D; ++m) a += tc[m][j] * ts[cur][m][ss];
+          gv[j] = a;
+        }
+        if constexpr (TSB == 1) {
+          if (ss == 3) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (sg < 3) load_ts(0, J, sg + 1);
+            else if (more) load_ts(0, Jn, 0);
+            if (more) fetch_part(p + 1, sg);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        bf8 ah, am, al;
+        split3(gv, ah, am, al);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const __bf16* b = wp + (s * 2 * S + ct * 32) * 8;
+          const bf8 bh = *reinterpret_cast<const bf8*>(b);
+          const bf8 bm = *reinterpret_cast<const bf8*>(b + PSZ);
+          const bf8 bl = *reinterpret_cast<const bf8*>(b + 2 * PSZ);
+          f16v c = acc[ct];
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, c, 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
+        }
+      }
+    }
+    if (more && In != I) load_tc(In);
+    I = In;
+    J = Jn;
+  }
+  // result register v of lane (r, q) is node 8 (v / 4) + 4 q + v % 4 of the wave, output column r
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t node = (int64_t)tile * NN + wave * 32 + 8 * (v / 4) + 4 * q + (v % 4);
+    if (node >= N) continue;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 32 + r] = acc[ct][v] * scale;
   }
 }
 
@@ -398,12 +552,22 @@ int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
 template <int S>
 int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float* Wf, float* part, float* out,
               hipStream_t st) {
-  const int nchunks = (n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK;
-  const int ntiles = (int)((N + NODES - 1) / NODES);
+  // The split-bf16 kernel runs 256-node tiles at ~1.7x the fp32 kernel's rate per node, so a tile takes
+  // ~1.2x an fp32 128-node tile: with at most 128 of its workgroups (one partial round on 256 CUs) the
+  // fp32 kernel's twice as many smaller workgroups finish first.
+  const int np = n_pairs(nC / 16);
+  const int nchunks = (np + PCHUNK - 1) / PCHUNK;
+  const bool bf = (int64_t)nchunks * ((N + NODES_BF - 1) / NODES_BF) > 128;
+  const int ntiles = (int)((N + (bf ? NODES_BF : NODES) - 1) / (bf ? NODES_BF : NODES));
   const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
+  const __bf16* Wf3 = reinterpret_cast<const __bf16*>(Wf + (int64_t)np * 256 * S);
   {
     LaunchTimer tm("gram_forward", st);
-#define FSC_GF(DD) forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
+#define FSC_GF(DD)                                                                                 \
+  if (bf)                                                                                          \
+    forward_bf16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf3, nchunks, part);      \
+  else                                                                                             \
+    forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
     switch (D) {
       case 1: FSC_GF(1); break;
       case 3: FSC_GF(3); break;
@@ -455,8 +619,8 @@ int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, i
   FSC_CHECK_ARG(wf_floats && wb_floats && workspace_floats, "fsc_gram_sizes: null pointer");
   FSC_CHECK_ARG(n_nodes >= 0 && nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
                 "fsc_gram_sizes: nC must be a multiple of 16 (<= 1024), S 32 or 64");
-  *wf_floats = (int64_t)n_pairs(nC / 16) * 256 * S;
-  *wb_floats = *wf_floats * 5 / 2;   // fp32 block pairs, then three bf16 planes
+  *wf_floats = (int64_t)n_pairs(nC / 16) * 256 * S * 5 / 2;   // fp32 block pairs, then three bf16 planes
+  *wb_floats = *wf_floats;
   *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S;
   return 0;
 }

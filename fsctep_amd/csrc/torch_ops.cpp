@@ -294,8 +294,8 @@ std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
   TORCH_CHECK(W_.dim() == 3 && W_.size(1) == W_.size(2), "W must be (S, nC, nC)");
   const int64_t S = W_.size(0), nC = W_.size(1), nb = nC / 16, P = nb * (nb + 1) / 2;
   Tensor W = f32c(W_);
-  // Wb: the fp32 block pairs (P*256*S floats) followed by their three bf16 planes (1.5x that), flat
-  Tensor Wf = at::empty({P, 16, S, 16}, fopts(W)), Wb = at::empty({P * 256 * S * 5 / 2}, fopts(W));
+  // each flat: the fp32 block pairs (P*256*S floats) followed by their three bf16 planes (1.5x that)
+  Tensor Wf = at::empty({P * 256 * S * 5 / 2}, fopts(W)), Wb = at::empty({P * 256 * S * 5 / 2}, fopts(W));
   check(fsc_gram_prepare_weights(cf(W), (int32_t)S, (int32_t)nC, mf(Wf), mf(Wb), stream_of(W)),
         "fsc_gram_prepare_weights");
   return {Wf, Wb};
@@ -303,13 +303,21 @@ std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
 
 std::tuple<Tensor, Tensor> gram_prepare_weights_meta(const Tensor& W) {
   const int64_t S = W.size(0), nb = W.size(1) / 16, P = nb * (nb + 1) / 2;
-  return {at::empty({P, 16, S, 16}, fopts(W)), at::empty({P * 256 * S * 5 / 2}, fopts(W))};
+  return {at::empty({P * 256 * S * 5 / 2}, fopts(W)), at::empty({P * 256 * S * 5 / 2}, fopts(W))};
+}
+
+// Output width S of prepared forward weights for nC channels (P*640*S floats, P block pairs).
+int64_t gram_width(const Tensor& Wf, int64_t nC) {
+  const int64_t nb = nC / 16, per = nb * (nb + 1) / 2 * 640;
+  TORCH_CHECK(Wf.dim() == 1 && nC % 16 == 0 && nb > 0 && Wf.numel() % per == 0,
+              "prepared Gram weights do not match nC = ", nC);
+  return Wf.numel() / per;
 }
 
 Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale) {
   require_gpu({t_, Wf, Wb});
-  TORCH_CHECK(t_.dim() == 3 && Wf.dim() == 4, "t must be (N, D, nC) and Wf (P, 16, S, 16)");
-  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = Wf.size(2);
+  TORCH_CHECK(t_.dim() == 3, "t must be (N, D, nC)");
+  const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = gram_width(Wf, nC);
   Tensor t = f32c(t_);
   int64_t wfn = 0, wbn = 0, wsn = 0;
   check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
@@ -322,7 +330,7 @@ Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, doubl
 }
 
 Tensor gram_bilinear_meta(const Tensor& t, const Tensor& Wf, const Tensor&, double) {
-  return at::empty({t.size(0), Wf.size(2)}, fopts(t));
+  return at::empty({t.size(0), gram_width(Wf, t.size(2))}, fopts(t));
 }
 
 Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t_, const Tensor& Wb, double scale) {
@@ -470,7 +478,7 @@ std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::Tens
                                                  const Tensor& table) {
   const FscReadoutTable* T = readout_table_of(table);
   const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
-  return {at::empty({N, Wf[0].size(2)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
+  return {at::empty({N, gram_width(Wf[0], nC)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
 }
 
 // ============================================================== autograd

@@ -217,9 +217,10 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
 int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, int64_t* wb_floats,
                    int64_t* workspace_floats);
 
-/* Block-pair layouts of W: Wf[p][16][S][16] (forward) and, for the backward, Wb[p][256][S] (W + W^T)
- * followed by the same values split into three bfloat16 planes [3][p][256][S] (fp32-accurate
- * split-bf16 products); Wb is opaque to the caller. */
+/* Block-pair layouts of W, each followed by the same values split into three bfloat16 planes
+ * (fp32-accurate split-bf16 products): Wf, the forward's W_IJ + W_JI^T (W_II on the diagonal) as
+ * [p][16][S][16] then [3][p][16][2][S][8], and Wb, the backward's W + W^T as [p][256][S] then
+ * [3][p][256][S]; both are opaque to the caller and hold fsc_gram_sizes' counts. */
 int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, float* Wb, hipStream_t stream);
 
 /* out [N][S]; part_ws holds fsc_gram_sizes' workspace_floats (per-chunk partial sums). */
