@@ -22,6 +22,11 @@
 namespace fsc {
 namespace ictd {
 
+// 16-row tiles per wave in the channel mix: more reuse of each weight load (the L2 traffic of the
+// weights falls 4x at 4 tiles; 10k atoms, C 128: 0.56 -> 0.40 ms, 2 tiles 0.50 ms) against fewer waves
+// (4k atoms, C 64, where the weights are 4x smaller: one tile is fastest)
+template <int C>
+constexpr int mix_rt() { return C >= 128 ? 4 : 1; }
 constexpr int EB = 16;    // edges per LDS chunk (power of two: K rows are ordered m1-major, row = m1*EB + e)
 
 // Shared-memory carve-up of the projection kernels (offsets in 4-byte words, regions 16-byte aligned).
@@ -271,8 +276,10 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
 }
 
 // ---------------------------------------------------------------- channel mix, forward
-// out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i]; grid (rows/64, NK).
-template <int C>
+// out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i]; grid (rows/(64 RT), NK).
+// A wave takes RT 16-row tiles, so every weight float4 it loads feeds RT MFMAs (the weights of a path
+// are 4 C^2 bytes, re-read from L2 once per 16 RT rows).
+template <int C, int RT>
 __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const float* __restrict__ Z,
                                                       const float* __restrict__ W, float* __restrict__ out,
                                                       int64_t N) {
@@ -282,41 +289,60 @@ __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const flo
   const int key = blockIdx.y;
   const int oo = L.k_oo[key], d = L.k_d[key];
   const int64_t rows = N * d;
-  const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   if (row0 >= rows) return;
-  const int64_t arow = row0 + r;
-  const bool ok = arow < rows;
-  const int64_t an = ok ? arow / d : 0;
-  const int ak = ok ? (int)(arow % d) : 0;
-  f4 acc[CT];
+  int64_t an[RT];
+  int ak[RT];
+  bool ok[RT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) acc[ct] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < RT; ++u) {
+    const int64_t arow = row0 + 16 * u + r;
+    ok[u] = arow < rows;
+    an[u] = ok[u] ? arow / d : 0;
+    ak[u] = ok[u] ? (int)(arow % d) : 0;
+  }
+  f4 acc[RT][CT];
+#pragma unroll
+  for (int u = 0; u < RT; ++u)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
   for (int p = 0; p < L.NP; ++p) {
     if (L.p_oo[p] != oo) continue;
-    const float* zr = Z + (an * L.KT + L.p_koff[p] + ak) * C;
-    const float* wp = W + (int64_t)L.p_gate[p] * C * C;
+    const float* wp = W + (int64_t)L.p_gate[p] * C * C + r * C + 4 * q;
+    const float* zr[RT];
+#pragma unroll
+    for (int u = 0; u < RT; ++u) zr[u] = Z + (an[u] * L.KT + L.p_koff[p] + ak[u]) * C + 4 * q;
 #pragma unroll 2
     for (int t = 0; t < C / 16; ++t) {
-      const f4 a4 = ok ? ld4(zr + 16 * t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
+      f4 a4[RT], b4[CT];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_k16(a4, ld4(wp + (16 * ct + r) * C + 16 * t + 4 * q), acc[ct]);
+      for (int u = 0; u < RT; ++u) a4[u] = ok[u] ? ld4(zr[u] + 16 * t) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) b4[ct] = ld4(wp + 16 * ct * C + 16 * t);
+#pragma unroll
+      for (int u = 0; u < RT; ++u)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[u][ct] = mfma_k16(a4[u], b4[ct], acc[u][ct]);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + 4 * q + i;
-    if (row >= rows) continue;
-    const int64_t nn = row / d;
-    const int m = (int)(row % d);
-    float* o = out + (nn * L.M + oo + m) * C;
+  for (int u = 0; u < RT; ++u)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[ct][i];
-  }
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + 16 * u + 4 * q + i;
+      if (row >= rows) continue;
+      const int64_t nn = row / d;
+      const int m = (int)(row % d);
+      float* o = out + (nn * L.M + oo + m) * C;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i];
+    }
 }
 
 // ---------------------------------------------------------------- channel mix, backward
-// dZ[n][koff_p + m][i] = sum_o Wt[gate_p][i][o] G[n][oo_p + m][o]; grid (rows/64, NP).
-template <int C>
+// dZ[n][koff_p + m][i] = sum_o Wt[gate_p][i][o] G[n][oo_p + m][o]; grid (rows/(64 RT), NP), RT row tiles
+// per wave as in the forward.
+template <int C, int RT>
 __global__ __launch_bounds__(256) void mix_bwd_kernel(FscIctdLayout L, const float* __restrict__ G,
                                                       const float* __restrict__ Wt, float* __restrict__ dZ,
                                                       int64_t N) {
@@ -326,33 +352,48 @@ __global__ __launch_bounds__(256) void mix_bwd_kernel(FscIctdLayout L, const flo
   const int p = blockIdx.y;
   const int d = L.p_d3[p], oo = L.p_oo[p], koff = L.p_koff[p];
   const int64_t rows = N * d;
-  const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   if (row0 >= rows) return;
-  const int64_t arow = row0 + r;
-  const bool ok = arow < rows;
-  const int64_t an = ok ? arow / d : 0;
-  const int ak = ok ? (int)(arow % d) : 0;
-  const float* gr = G + (an * L.M + oo + ak) * C;
-  const float* wp = Wt + (int64_t)L.p_gate[p] * C * C;
-  f4 acc[CT];
+  const float* gr[RT];
+  bool ok[RT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) acc[ct] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < RT; ++u) {
+    const int64_t arow = row0 + 16 * u + r;
+    ok[u] = arow < rows;
+    const int64_t an = ok[u] ? arow / d : 0;
+    const int ak = ok[u] ? (int)(arow % d) : 0;
+    gr[u] = G + (an * L.M + oo + ak) * C + 4 * q;
+  }
+  const float* wp = Wt + (int64_t)L.p_gate[p] * C * C + r * C + 4 * q;
+  f4 acc[RT][CT];
+#pragma unroll
+  for (int u = 0; u < RT; ++u)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
   for (int t = 0; t < C / 16; ++t) {
-    const f4 a4 = ok ? ld4(gr + 16 * t + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
+    f4 a4[RT], b4[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_k16(a4, ld4(wp + (16 * ct + r) * C + 16 * t + 4 * q), acc[ct]);
+    for (int u = 0; u < RT; ++u) a4[u] = ok[u] ? ld4(gr[u] + 16 * t) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) b4[ct] = ld4(wp + 16 * ct * C + 16 * t);
+#pragma unroll
+    for (int u = 0; u < RT; ++u)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[u][ct] = mfma_k16(a4[u], b4[ct], acc[u][ct]);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + 4 * q + i;
-    if (row >= rows) continue;
-    const int64_t nn = row / d;
-    const int m = (int)(row % d);
-    float* o = dZ + (nn * L.KT + koff + m) * C;
+  for (int u = 0; u < RT; ++u)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[ct][i];
-  }
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + 16 * u + 4 * q + i;
+      if (row >= rows) continue;
+      const int64_t nn = row / d;
+      const int m = (int)(row % d);
+      float* o = dZ + (nn * L.KT + koff + m) * C;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i];
+    }
 }
 
 // ---------------------------------------------------------------- backward projection (one block per receiver)
@@ -730,8 +771,9 @@ int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const i
   for (int k = 0; k < L.NK; ++k) dmax = max(dmax, L.k_d[k]);
   {
     LaunchTimer tm("ictd_mix", st);
-    dim3 grid((unsigned)((N * dmax + 63) / 64), (unsigned)L.NK);
-    mix_fwd_kernel<C><<<grid, 256, 0, st>>>(L, Z, W, out, N);
+    constexpr int RT = mix_rt<C>();
+    dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NK);
+    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, W, out, N);
   }
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
@@ -745,8 +787,9 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   for (int p = 0; p < L.NP; ++p) dmax = max(dmax, L.p_d3[p]);
   {
     LaunchTimer tm("ictd_mix_grad", st);
-    dim3 grid((unsigned)((N * dmax + 63) / 64), (unsigned)L.NP);
-    mix_bwd_kernel<C><<<grid, 256, 0, st>>>(L, G, Wt, dZ, N);
+    constexpr int RT = mix_rt<C>();
+    dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NP);
+    mix_bwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, G, Wt, dZ, N);
   }
   if (check_launch("ictd mix_bwd")) return 2;
   {
