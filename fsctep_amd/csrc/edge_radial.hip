@@ -18,6 +18,27 @@ namespace radial {
 constexpr int HID = 64;     // hidden width of the radial MLP (fixed by the reference's fc)
 constexpr int NBMAX = 16;   // radial basis functions supported
 
+// sin x and cos x for 0 <= x < 2^7: Cody-Waite reduction by pi/2 in two parts (the fma keeps
+// x - n*P1 to one rounding, and n*(pi/2 - P1 - P2) is below 2^-30 here), then the Taylor series on
+// [-pi/4, pi/4] to x^11 / x^12 (truncation below 1e-11) and the quadrant.  The basis argument is at
+// most nb*pi; the library sinf/cosf carry a large-argument path whose registers the radial MLP kernels
+// cannot spare.
+__device__ __forceinline__ void sincos_small(float x, float& s, float& c) {
+  constexpr float P1 = 1.57079637050628662109375f;       // pi/2 rounded to float
+  constexpr float P2 = -4.37113900018624283e-8f;         // pi/2 - P1
+  const float n = rintf(x * 0.636619772367581343f);      // x / (pi/2)
+  float t = fmaf(-n, P1, x);
+  t = fmaf(-n, P2, t);
+  const float t2 = t * t;
+  const float sp = t + t * t2 * (-1.f / 6.f + t2 * (1.f / 120.f + t2 * (-1.f / 5040.f + t2 * (1.f / 362880.f +
+                                                                      t2 * (-1.f / 39916800.f)))));
+  const float cp = 1.f + t2 * (-0.5f + t2 * (1.f / 24.f + t2 * (-1.f / 720.f + t2 * (1.f / 40320.f +
+                                                                  t2 * (-1.f / 3628800.f + t2 * (1.f / 479001600.f))))));
+  const int qd = ((int)n) & 3;
+  s = (qd == 0) ? sp : (qd == 1) ? cp : (qd == 2) ? -sp : -cp;
+  c = (qd == 0) ? cp : (qd == 1) ? -sp : (qd == 2) ? -cp : sp;
+}
+
 // emb_k(r) and d emb_k / dr for k < nb (basis 0: Bessel, 1: Gaussian), matching the device
 // formula used by the model code (bessel: sqrt(2/rc) sin(k pi r/rc)/r on (0, rc); gaussian:
 // exp(-((r - mu_k)/step)^2)/1.12 with mu_k = k*step, step = rc/(nb+1)), times sqrt(nb).
@@ -29,12 +50,14 @@ __device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int
     const bool inside = (r / rc < 1.f) && (r > 0.f);
     const float a = sqrtf(2.f / rc) * snb;
     const float rr = inside ? r : 1.f;
-    const float x = w * rr, s = sinf(x);
+    const float x = w * rr;
+    float s, c;
+    sincos_small(x, s, c);
     f = inside ? a * s / rr : 0.f;
     if (DERIV) {
       // d/dr sin(wr)/r = w^2 (x cos x - sin x)/x^2; below x = 0.3 the Taylor series avoids the
       // cancellation (-x/3 + x^3/30 - x^5/840, truncation below 1e-8 relative)
-      const float c = cosf(x), x2 = x * x;
+      const float x2 = x * x;
       const float g = (x < 0.3f) ? x * (-1.f / 3.f + x2 * (1.f / 30.f - x2 * (1.f / 840.f))) : (x * c - s) / x2;
       df = inside ? a * w * w * g : 0.f;
     }
@@ -119,6 +142,8 @@ __device__ __forceinline__ void dense64(const float (*W)[WS], const float* b, co
       for (int i = 0; i < 4; ++i) acc[i] += b[16 * ot + 4 * q + i];
     }
     out[ot] = acc;
+    // keep each output tile's 16 weight reads with its products (hoisting them all costs 64 VGPRs)
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -135,6 +160,7 @@ __device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&e
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] += sm.b0[16 * jt + 4 * q + i];
     u0[jt] = acc;
+    __builtin_amdgcn_sched_barrier(0);
   }
   f4 a0[4];
 #pragma unroll
@@ -166,7 +192,11 @@ __device__ __forceinline__ void lane_basis_deriv(float rr, int nb, float rc, int
   }
 }
 
-__global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
+// Blocks of RAD_WAVES waves share one LDS copy of the weights; two blocks per CU give 4 waves per SIMD
+// (at most 128 VGPRs), enough to overlap the dependent layers of one 16-edge tile with other tiles.
+constexpr int RAD_WAVES = 8;
+
+__global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_forward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
                                                                  const float* __restrict__ b0, const float* __restrict__ W2,
                                                                  const float* __restrict__ b2, const float* __restrict__ W4,
                                                                  const float* __restrict__ b4, int nout, int nb, float rc,
@@ -178,7 +208,7 @@ __global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __
   const int r = lane & 15, q = lane >> 4;
   const int nks = (nb + 3) / 4;
   const int64_t ntiles = (n_edges + 15) / 16;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+  for (int64_t t = (int64_t)blockIdx.x * RAD_WAVES + wave; t < ntiles; t += (int64_t)gridDim.x * RAD_WAVES) {
     const int64_t e = 16 * t + r;
     const float rr = (e < n_edges) ? rad[e] : 1.f;
     float emb[NBMAX / 4];
@@ -210,7 +240,7 @@ __global__ __launch_bounds__(256) void radial_mlp_forward_kernel(const float* __
 
 // dr[e] = sum_k d emb_k/dr * (W0^T (silu'(u0) * W2^T (silu'(u2) * dh)))_k, with dh = W4^T dout when the
 // last Linear is fused.
-__global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
+__global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(const float* __restrict__ rad, const float* __restrict__ W0,
                                                                   const float* __restrict__ b0, const float* __restrict__ W2,
                                                                   const float* __restrict__ b2, const float* __restrict__ W4,
                                                                   int nout, int nb, float rc, int basis, int64_t n_edges,
@@ -222,7 +252,7 @@ __global__ __launch_bounds__(256) void radial_mlp_backward_kernel(const float* _
   const int r = lane & 15, q = lane >> 4;
   const int nks = (nb + 3) / 4;
   const int64_t ntiles = (n_edges + 15) / 16;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+  for (int64_t t = (int64_t)blockIdx.x * RAD_WAVES + wave; t < ntiles; t += (int64_t)gridDim.x * RAD_WAVES) {
     const int64_t e = 16 * t + r;
     const bool ok = e < n_edges;
     const float rr = ok ? rad[e] : 1.f;
@@ -457,8 +487,8 @@ int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* gr
 
 static unsigned radial_grid(int64_t n_edges) {
   const int64_t tiles = (n_edges + 15) / 16;
-  // about two blocks per CU: the weights are staged in LDS once per block
-  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + 3) / 4, 512));
+  // two blocks per CU: the weights are staged in LDS once per block
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((tiles + RAD_WAVES - 1) / RAD_WAVES, 512));
 }
 
 int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, const float* b0, const float* w2,
@@ -472,7 +502,7 @@ int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, con
   if (n_edges == 0) return 0;
   FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && out, "fsc_radial_mlp_forward: null pointer");
   LaunchTimer tm("radial_mlp", stream);
-  radial_mlp_forward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, w4, b4, w4 ? n_out : HID,
+  radial_mlp_forward_kernel<<<radial_grid(n_edges), 64 * RAD_WAVES, 0, stream>>>(r, w0, b0, w2, b2, w4, b4, w4 ? n_out : HID,
                                                                      n_basis, r_cut, basis, n_edges, out);
   return check_launch("radial mlp forward") ? 2 : 0;
 }
@@ -488,7 +518,7 @@ int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, co
   if (n_edges == 0) return 0;
   FSC_CHECK_ARG(r && w0 && b0 && w2 && b2 && grad_out && grad_r, "fsc_radial_mlp_backward: null pointer");
   LaunchTimer tm("radial_mlp_grad", stream);
-  radial_mlp_backward_kernel<<<radial_grid(n_edges), 256, 0, stream>>>(r, w0, b0, w2, b2, w4, w4 ? n_out : HID,
+  radial_mlp_backward_kernel<<<radial_grid(n_edges), 64 * RAD_WAVES, 0, stream>>>(r, w0, b0, w2, b2, w4, w4 ? n_out : HID,
                                                                       n_basis, r_cut, basis, n_edges, grad_out, grad_r);
   return check_launch("radial mlp backward") ? 2 : 0;
 }
