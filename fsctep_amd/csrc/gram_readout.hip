@@ -39,16 +39,17 @@ __device__ __forceinline__ int xcd_logical(int nwg) {
   return logical < nwg ? logical : -1;
 }
 
-// Forward work order: groups of TILE_GROUP node tiles, and within a group all pair chunks of its
-// tiles with the tiles innermost.  Workgroups that run together on an XCD then share both the
+// Forward work order: groups of (at most TILE_GROUP) node tiles, and within a group all pair chunks of
+// its tiles with the tiles innermost.  Workgroups that run together on an XCD then share both the
 // weight chunk (read by the group's tiles) and the t rows of the group, which stay in its L2.
 constexpr int TILE_GROUP = 4;
-__device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles, int& chunk, int& tile) {
-  const int grp = logical / (TILE_GROUP * nchunks);
-  const int gsize = min(TILE_GROUP, ntiles - grp * TILE_GROUP);
-  const int rem = logical - grp * TILE_GROUP * nchunks;
+__device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles, int& chunk, int& tile,
+                                            int tgroup = TILE_GROUP) {
+  const int grp = logical / (tgroup * nchunks);
+  const int gsize = min(tgroup, ntiles - grp * tgroup);
+  const int rem = logical - grp * tgroup * nchunks;
   chunk = rem / gsize;
-  tile = grp * TILE_GROUP + (rem - chunk * gsize);
+  tile = grp * tgroup + (rem - chunk * gsize);
 }
 
 // Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).  After the
@@ -177,7 +178,7 @@ template <int D, int S, int TSB>
 __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, float scale,
                                                            const float* __restrict__ t,
                                                            const __bf16* __restrict__ Wf3, int nchunks,
-                                                           float* __restrict__ part) {
+                                                           float* __restrict__ part, int tgroup) {
   constexpr int NN = NODES_BF, CT = S / 32;
   constexpr int PSZ = 256 * S;            // bf16 per plane of a pair
   constexpr int PW = 3 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
   const int logical = xcd_logical(nchunks * ntiles);
   if (logical < 0) return;
   int chunk, tile;
-  group_order(logical, nchunks, ntiles, chunk, tile);
+  group_order(logical, nchunks, ntiles, chunk, tile, tgroup);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, q = lane >> 5;
   const int64_t n = (int64_t)tile * NN + wave * 32 + r;
@@ -561,11 +562,15 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   const int ntiles = (int)((N + (bf ? NODES_BF : NODES) - 1) / (bf ? NODES_BF : NODES));
   const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
   const __bf16* Wf3 = reinterpret_cast<const __bf16*>(Wf + (int64_t)np * 256 * S);
+  // tiles per group: as many as keep the group's t rows within about half an XCD's 4 MB L2 (at D 7,
+  // nC 384 a 256-node tile alone is 2.75 MB; larger groups re-fetch t for every pair chunk)
+  const int64_t tile_bytes = (int64_t)NODES_BF * D * nC * 4;
+  const int tg = (int)std::max<int64_t>(1, std::min<int64_t>(TILE_GROUP, (2 << 20) / tile_bytes));
   {
     LaunchTimer tm("gram_forward", st);
 #define FSC_GF(DD)                                                                                 \
   if (bf)                                                                                          \
-    forward_bf16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf3, nchunks, part);      \
+    forward_bf16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf3, nchunks, part, tg);  \
   else                                                                                             \
     forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
     switch (D) {

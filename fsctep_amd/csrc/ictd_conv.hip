@@ -343,7 +343,7 @@ __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const flo
 // dZ[n][koff_p + m][i] = sum_o Wt[gate_p][i][o] G[n][oo_p + m][o]; grid (rows/(64 RT), NP), RT row tiles
 // per wave as in the forward.
 template <int C, int RT>
-__global__ __launch_bounds__(256) void mix_bwd_kernel(FscIctdLayout L, const float* __restrict__ G,
+__global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const float* __restrict__ G,
                                                       const float* __restrict__ Wt, float* __restrict__ dZ,
                                                       int64_t N) {
   constexpr int CT = C / 16;
