@@ -224,7 +224,8 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
       const int d1 = L.g_d1[g], o1 = L.g_o1[g], kpad = L.g_kpad[g];
       const float* arow = bg + L.g_bgoff[g] + (kt - L.g_tile0[g]) * 16 + r;
       const float* xcol = x + o1 * C + span * SPAN + V * r;
-      // K rows m1*EB + e, e = 4u + q; the gathers of component m1+1 are in flight while m1 is multiplied
+      // K rows m1*EB + e, e = 4u + q; the gathers of components m1+1 and m1+2 are in flight while m1 is
+      // multiplied
       auto load_k = [&](int m1, float (&a)[EB / 4], VecF<V> (&b)[EB / 4]) {
 #pragma unroll
         for (int u = 0; u < EB / 4; ++u) {
@@ -239,17 +240,23 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
 #pragma unroll
           for (int j = 0; j < V; ++j) acc[lt][j] = mfma16x16x4(a[u], b[u].v[j], acc[lt][j]);
       };
-      float a0[EB / 4], a1[EB / 4];
-      VecF<V> b0[EB / 4], b1[EB / 4];
+      float a0[EB / 4], a1[EB / 4], a2[EB / 4];
+      VecF<V> b0[EB / 4], b1[EB / 4], b2[EB / 4];
       load_k(0, a0, b0);
-      for (int m1 = 0; m1 < d1; m1 += 2) {
-        if (m1 + 1 < d1) load_k(m1 + 1, a1, b1);
+      if (1 < d1) load_k(1, a1, b1);
+      for (int m1 = 0; m1 < d1; m1 += 3) {
+        if (m1 + 2 < d1) load_k(m1 + 2, a2, b2);
         __builtin_amdgcn_sched_barrier(0);
         mul_k(a0, b0);
         if (m1 + 1 < d1) {
-          if (m1 + 2 < d1) load_k(m1 + 2, a0, b0);
+          if (m1 + 3 < d1) load_k(m1 + 3, a0, b0);
           __builtin_amdgcn_sched_barrier(0);
           mul_k(a1, b1);
+        }
+        if (m1 + 2 < d1) {
+          if (m1 + 4 < d1) load_k(m1 + 4, a1, b1);
+          __builtin_amdgcn_sched_barrier(0);
+          mul_k(a2, b2);
         }
       }
     }

@@ -820,11 +820,15 @@ __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float
   }
 }
 
-// Q[e][p*C + c] = sum_k h[e][k] mb[pair][p][c][k] + mf[pair][p][64][c] for one 16-edge tile of
-// one species pair per wave.  pair_tiles = [16*n_tiles padded edge ids (-1: none) | n_tiles
-// pair ids]; a tile's first entry is always an edge.  Transposed product: table rows (p, c)
-// are the A operand and the tile's h rows the B operand, so lane (r, q) ends with four
-// consecutive (p, c) columns of edge r.
+// Q[e][p*C + c] = sum_k h[e][k] mb[pair][p][c][k] + mf[pair][p][64][c] for 16-edge tiles of one species
+// pair.  pair_tiles = [16*n_tiles padded edge ids (-1: none) | n_tiles pair ids]; a tile's first entry is
+// always an edge, and the tiles of a pair are consecutive.  Transposed product: table rows (p, c) are the
+// A operand and the tile's h rows the B operand, so lane (r, q) ends with four consecutive (p, c) columns
+// of edge r.  A wave takes C1_TPW consecutive tiles: when they share a pair (all but a few waves per
+// pair) each table row block is loaded once for all of them (the table is 48 KB per pair at C 64, which
+// one-tile waves re-read from L2 for every 16 edges).
+constexpr int C1_TPW = 4;
+
 template <int C>
 __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __restrict__ h,
                                                               const float* __restrict__ mf,
@@ -834,27 +838,49 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   constexpr int NRT = 3 * C / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= n_tiles) return;   // whole wave
-  const int32_t e = pair_tiles[16 * t + r];
-  const int32_t eld = (e >= 0) ? e : pair_tiles[16 * t];
-  const int pair = pair_tiles[16 * n_tiles + t];
-  f4 hb[4];
+  const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
+  if (t0 >= n_tiles) return;   // whole wave
+  const int nt = min(C1_TPW, n_tiles - t0);
+  const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
+  int32_t e[C1_TPW];
+  f4 hb[C1_TPW][4];
+  bool same = true;
 #pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4) hb[t4] = ld4(h + (int64_t)eld * KH + 16 * t4 + 4 * q);
-  const float* mp = mb + (int64_t)pair * 3 * C * MB_STRIDE;
-  const float* fp = mf + (int64_t)pair * 3 * 65 * C;
+  for (int u = 0; u < C1_TPW; ++u) {
+    const int t = t0 + min(u, nt - 1);
+    same = same && tpair[t] == tpair[t0];
+    const int32_t eu = pair_tiles[16 * t + r];
+    e[u] = (u < nt) ? eu : -1;   // tiles past n_tiles repeat the last one and are not stored
+    const int32_t eld = (eu >= 0) ? eu : pair_tiles[16 * t];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) hb[u][t4] = ld4(h + (int64_t)eld * KH + 16 * t4 + 4 * q);
+  }
+  auto tile_rows = [&](int pair, int u0, int u1) {   // tiles u0..u1-1 against the table of `pair`
+    const float* mp = mb + (int64_t)pair * 3 * C * MB_STRIDE;
+    const float* fp = mf + (int64_t)pair * 3 * 65 * C;
 #pragma unroll 3
-  for (int rt = 0; rt < NRT; ++rt) {
-    f4 a[4];
+    for (int rt = 0; rt < NRT; ++rt) {
+      f4 a[4];
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) a[t4] = ld4(mp + (int64_t)(16 * rt + r) * MB_STRIDE + 16 * t4 + 4 * q);
-    const int row = 16 * rt + 4 * q;   // first of the lane's four (p, c) outputs
-    const f4 bias = ld4(fp + (row / C) * 65 * C + 64 * C + row % C);
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int t4 = 0; t4 < 4; ++t4) a[t4] = ld4(mp + (int64_t)(16 * rt + r) * MB_STRIDE + 16 * t4 + 4 * q);
+      const int row = 16 * rt + 4 * q;   // first of the lane's four (p, c) outputs
+      const f4 bias = ld4(fp + (row / C) * 65 * C + 64 * C + row % C);
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) acc = mfma_k16(a[t4], hb[t4], acc);
-    if (e >= 0) st4(Q + (int64_t)e * 3 * C + row, acc + bias);
+      for (int u = 0; u < C1_TPW; ++u) {
+        if (u < u0 || u >= u1) continue;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) acc = mfma_k16(a[t4], hb[u][t4], acc);
+        if (e[u] >= 0) st4(Q + (int64_t)e[u] * 3 * C + row, acc + bias);
+      }
+    }
+  };
+  if (same) {   // wave-uniform
+    tile_rows(tpair[t0], 0, C1_TPW);
+  } else {
+#pragma unroll
+    for (int u = 0; u < C1_TPW; ++u)
+      if (u < nt) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
 
@@ -944,9 +970,9 @@ __global__ __launch_bounds__(256) void conv1_receiver_grad_kernel(const float* _
   }
 }
 
-// dh[e][k] = sum_{p,c} dQ[e][p][c] mf[pair][p][k][c] for one 16-edge tile of one pair per
-// wave; transposed product (table rows k are the A operand), lane (r, q) ends with four
-// consecutive k of edge r per k tile.
+// dh[e][k] = sum_{p,c} dQ[e][p][c] mf[pair][p][k][c] for C1_TPW consecutive 16-edge tiles per wave
+// (one table load for all of them when they share a pair, as in the forward); transposed product
+// (table rows k are the A operand), lane (r, q) ends with four consecutive k of edge r per k tile.
 template <int C>
 __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* __restrict__ dQ,
                                                                    const float* __restrict__ mf,
@@ -954,27 +980,56 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
                                                                    int n_tiles, float* __restrict__ dh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= n_tiles) return;   // whole wave
-  const int32_t e = pair_tiles[16 * t + r];
-  const int32_t eld = (e >= 0) ? e : pair_tiles[16 * t];
-  const int pair = pair_tiles[16 * n_tiles + t];
-  const float* fp = mf + (int64_t)pair * 3 * 65 * C;
-  const float* dq = dQ + (int64_t)eld * 3 * C + 4 * q;
-  f4 acc[4] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll 3
-  for (int kc = 0; kc < 3 * C / 16; ++kc) {   // K chunk: path p = kc / (C/16), channels c0..c0+15
-    const int p = kc / (C / 16), c0 = 16 * (kc % (C / 16));
-    const f4 b = ld4(dq + p * C + c0);
-    f4 a[4];
+  const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
+  if (t0 >= n_tiles) return;   // whole wave
+  const int nt = min(C1_TPW, n_tiles - t0);
+  const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
+  int32_t e[C1_TPW];
+  const float* dq[C1_TPW];
+  bool same = true;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) a[kt] = ld4(fp + (int64_t)(p * 65 + 16 * kt + r) * C + c0 + 4 * q);
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) acc[kt] = mfma_k16(a[kt], b, acc[kt]);
+  for (int u = 0; u < C1_TPW; ++u) {
+    const int t = t0 + min(u, nt - 1);
+    same = same && tpair[t] == tpair[t0];
+    const int32_t eu = pair_tiles[16 * t + r];
+    e[u] = (u < nt) ? eu : -1;   // tiles past n_tiles repeat the last one and are not stored
+    const int32_t eld = (eu >= 0) ? eu : pair_tiles[16 * t];
+    dq[u] = dQ + (int64_t)eld * 3 * C + 4 * q;
   }
-  if (e >= 0) {
+  auto tile_rows = [&](int pair, int u0, int u1) {   // tiles u0..u1-1 against the table of `pair`
+    const float* fp = mf + (int64_t)pair * 3 * 65 * C;
+    f4 acc[C1_TPW][4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) st4(dh + (int64_t)e * KH + 16 * kt + 4 * q, acc[kt]);
+    for (int u = 0; u < C1_TPW; ++u)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) acc[u][kt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (int kc = 0; kc < 3 * C / 16; ++kc) {   // K chunk: path p = kc / (C/16), channels c0..c0+15
+      const int p = kc / (C / 16), c0 = 16 * (kc % (C / 16));
+      f4 a[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) a[kt] = ld4(fp + (int64_t)(p * 65 + 16 * kt + r) * C + c0 + 4 * q);
+#pragma unroll
+      for (int u = 0; u < C1_TPW; ++u) {
+        if (u < u0 || u >= u1) continue;
+        const f4 b = ld4(dq[u] + p * C + c0);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) acc[u][kt] = mfma_k16(a[kt], b, acc[u][kt]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C1_TPW; ++u) {
+      if (u < u0 || u >= u1 || e[u] < 0) continue;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) st4(dh + (int64_t)e[u] * KH + 16 * kt + 4 * q, acc[u][kt]);
+    }
+  };
+  if (same) {   // wave-uniform
+    tile_rows(tpair[t0], 0, C1_TPW);
+  } else {
+#pragma unroll
+    for (int u = 0; u < C1_TPW; ++u)
+      if (u < nt) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
 
@@ -1134,7 +1189,7 @@ int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_forward", stream);
-  const unsigned tgrid = (unsigned)((n_tiles + 3) / 4), ngrid = (unsigned)((n_nodes + 3) / 4);
+  const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
   if (channels == 64) {
     if (n_tiles) conv1_pair_gemm_kernel<64><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
     conv1_receiver_kernel<64><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
@@ -1159,7 +1214,7 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                 "fsc_sparse_conv1_backward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_backward", stream);
-  const unsigned tgrid = (unsigned)((n_tiles + 3) / 4), ngrid = (unsigned)((n_nodes + 3) / 4);
+  const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
   if (channels == 64) {
     conv1_receiver_grad_kernel<64><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
     if (n_tiles) conv1_pair_gemm_grad_kernel<64><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
