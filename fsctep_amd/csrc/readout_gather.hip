@@ -107,6 +107,78 @@ __global__ void scatter_kernel(FscReadoutTable T, int64_t N, KeyPtrs dt, const f
   }
 }
 
+// One block per node when a node's n_layers*M*C entries fit in LDS (ROW_LDS floats): the node's row is
+// read once, coalesced, and permuted out of LDS, so both the reads and the writes stay contiguous (the
+// element-wise kernels above gather or scatter through the permutation in global memory).
+constexpr int ROW_LDS = 12288;
+
+__global__ __launch_bounds__(256) void gather_node_kernel(FscReadoutTable T, int64_t N, LayerPtrs X,
+                                                          const int32_t* __restrict__ srcmap,
+                                                          float* __restrict__ t_all, float* __restrict__ sq) {
+  extern __shared__ float xs[];
+  const int C = T.C, MC = T.M * C, nC = T.n_layers * C, P = T.n_layers * MC;
+  for (int64_t n = blockIdx.x; n < N; n += gridDim.x) {
+    __syncthreads();
+    for (int l = 0; l < T.n_layers; ++l)
+      for (int j = threadIdx.x; j < MC; j += blockDim.x) xs[l * MC + j] = X.p[l][n * MC + j];
+    __syncthreads();
+    int col0 = 0;
+    for (int k = 0; k < T.n_keys; ++k) {   // key k's columns of node n are contiguous in t_k
+      const int len = T.key_dim[k] * nC;
+      float* dst = t_all + N * col0 + n * (int64_t)len;
+      for (int j = threadIdx.x; j < len; j += blockDim.x)
+        dst[j] = xs[min(max(srcmap[col0 + j], 0), P - 1)];   // host-checked permutation; stay in bounds
+      float* sk = sq + (n * T.n_keys + k) * (int64_t)nC;
+      for (int lc = threadIdx.x; lc < nC; lc += blockDim.x) {
+        const int l = lc / C;
+        const float* x = xs + l * MC + T.key_comp0[k] * C + (lc - l * C);
+        float s2 = 0.f;
+        for (int m = 0; m < T.key_dim[k]; ++m) s2 += x[m * C] * x[m * C];
+        sk[lc] = s2;
+      }
+      col0 += len;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_node_kernel(FscReadoutTable T, int64_t N, KeyPtrs dt,
+                                                           const float* __restrict__ dsq, LayerPtrs X,
+                                                           const int32_t* __restrict__ gmap, OutPtrs dX) {
+  extern __shared__ float ds[];
+  const int C = T.C, MC = T.M * C, nC = T.n_layers * C, P = T.n_layers * MC, rows = T.n_layers * T.M;
+  // a pass covers R component rows of C channels (R = blockDim / C when C divides it, else one row
+  // with a channel loop)
+  const bool fits = C <= (int)blockDim.x && blockDim.x % C == 0;
+  const int R = fits ? blockDim.x / C : 1;
+  const int rsub = fits ? threadIdx.x / C : 0;
+  const int c0 = fits ? threadIdx.x - rsub * C : threadIdx.x;
+  const int cstep = fits ? C : blockDim.x;
+  for (int64_t n = blockIdx.x; n < N; n += gridDim.x) {
+    __syncthreads();
+    int col0 = 0;
+    for (int k = 0; k < T.n_keys; ++k) {
+      const int len = T.key_dim[k] * nC;
+      const float* src = dt.p[k] ? dt.p[k] + n * (int64_t)len : nullptr;
+      for (int j = threadIdx.x; j < len; j += blockDim.x) ds[col0 + j] = src ? src[j] : 0.f;
+      col0 += len;
+    }
+    __syncthreads();
+    for (int row = rsub; row < rows; row += R) {
+      const int l = row / T.M, m = row - l * T.M;
+      const int kk = key_of(T, m);
+      const float* xr = X.p[l] + n * MC + m * C;
+      float* o = dX.p[l] + n * MC + m * C;
+      const int32_t* gr = gmap + l * MC + m * C;
+      const float* dq = dsq ? dsq + (n * T.n_keys + kk) * (int64_t)nC + l * C : nullptr;
+      for (int c = c0; c < C; c += cstep) {
+        float v = ds[min(max(gr[c], 0), P - 1)];
+        if (dq) v += 2.f * xr[c] * dq[c];
+        o[c] = v;
+      }
+    }
+  }
+}
+
 int check_table(const FscReadoutTable* T, const char* who) {
   if (!T) {
     set_error(std::string(who) + ": null table");
@@ -154,6 +226,11 @@ int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const floa
     X.p[l] = layers[l];
   }
   const int64_t P = (int64_t)table->n_layers * table->M * table->C;
+  if (P <= ROW_LDS) {
+    const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, 65536);
+    gather_node_kernel<<<grid, 256, P * sizeof(float), stream>>>(*table, n_nodes, X, srcmap, t_all, sq);
+    return check_launch("readout gather") ? 2 : 0;
+  }
   gather_kernel<<<grid_for(n_nodes * P), 256, 0, stream>>>(*table, n_nodes, X, srcmap, t_all);
   if (check_launch("readout gather")) return 2;
   const int64_t S = n_nodes * table->n_keys * table->n_layers * table->C;
@@ -177,7 +254,13 @@ int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const flo
     X.p[l] = layers[l];
     dX.p[l] = grad_layers[l];
   }
-  const int64_t total = (int64_t)table->n_layers * n_nodes * table->M * table->C;
+  const int64_t P = (int64_t)table->n_layers * table->M * table->C;
+  if (P <= ROW_LDS) {
+    const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, 65536);
+    scatter_node_kernel<<<grid, 256, P * sizeof(float), stream>>>(*table, n_nodes, dt, grad_sq, X, gmap, dX);
+    return check_launch("readout scatter") ? 2 : 0;
+  }
+  const int64_t total = P * n_nodes;
   scatter_kernel<<<grid_for(total), 256, 0, stream>>>(*table, n_nodes, dt, grad_sq, X, gmap, dX);
   return check_launch("readout scatter") ? 2 : 0;
 }
