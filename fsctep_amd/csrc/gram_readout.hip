@@ -427,7 +427,7 @@ __global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float 
 // (W + W^T) block is staged from its three bf16 planes, g is split once per wave, K = o runs in steps
 // of 32 (lane group q: o = 32 ks + 8q .. +7).  Same work split, contraction and output as above; the
 // planes take 1.5x the LDS of the fp32 block, so one workgroup runs per CU.
-template <int D, int S, int ILW>
+template <int D, int S, int ILW, bool PIPE>
 __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, float scale,
                                                             const float* __restrict__ g, const float* __restrict__ t,
                                                             const __bf16* __restrict__ Wb3, float* __restrict__ dt) {
@@ -496,6 +496,18 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
     const bool upper = I <= J;
     const int rbase = (upper ? r * RS : r * AS) + 8 * q;
     const int ilstep = upper ? AS : RS;
+    // PIPE: the operands of step u + 1 are read from LDS before the products of step u are issued (at 2
+    // waves per SIMD the compiler's own order waits on each read; costs 12 registers)
+    constexpr int NSTEP = (ILW / 4) * KS * 4;
+    bf8 oh[2], om[2], ol[2];
+    auto rd = [&](int u, int slot) {
+      const int i4 = u / (KS * 4), ks = (u / 4) % KS, jj = u % 4;
+      const int off = rbase + (il0 + 4 * i4 + jj) * ilstep + 32 * ks;
+      oh[slot] = *reinterpret_cast<const bf8*>(&wl[off]);
+      om[slot] = *reinterpret_cast<const bf8*>(&wl[PS + off]);
+      ol[slot] = *reinterpret_cast<const bf8*>(&wl[2 * PS + off]);
+    };
+    if constexpr (PIPE) rd(0, 0);
 #pragma unroll
     for (int i4 = 0; i4 < ILW / 4; ++i4) {
       f4 dd[4] = {zero, zero, zero, zero};
@@ -503,11 +515,14 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int off = rbase + (il0 + 4 * i4 + jj) * ilstep + 32 * ks;
-          const bf8 ah = *reinterpret_cast<const bf8*>(&wl[off]);
-          const bf8 am = *reinterpret_cast<const bf8*>(&wl[PS + off]);
-          const bf8 al = *reinterpret_cast<const bf8*>(&wl[2 * PS + off]);
-          dd[jj] = mfma_x6(ah, am, al, gh[ks], gm[ks], gl[ks], dd[jj]);
+          const int u = (i4 * KS + ks) * 4 + jj;
+          if constexpr (PIPE) {
+            if (u + 1 < NSTEP) rd(u + 1, (u + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+          } else {
+            rd(u, u & 1);
+          }
+          dd[jj] = mfma_x6(oh[u & 1], om[u & 1], ol[u & 1], gh[ks], gm[ks], gl[ks], dd[jj]);
         }
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
@@ -588,6 +603,9 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   return check_launch("gram reduce") ? 2 : 0;
 }
 
+// largest D whose backward has the registers for the operand pipeline
+constexpr int GB_PIPE_DMAX = 3;
+
 template <int S>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
@@ -599,7 +617,7 @@ int backward_s(int64_t N, int D, int nC, float scale, const float* g, const floa
   const __bf16* Wb3 = reinterpret_cast<const __bf16*>(Wb + (int64_t)n_pairs(nC / 16) * 256 * S);
   LaunchTimer tm("gram_backward", st);
 #define FSC_GBB(DD) \
-  backward_bf16_kernel<DD, S, (DD <= 5 ? 16 : 8)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb3, dt)
+  backward_bf16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb3, dt)
   switch (D) {
     case 1: FSC_GBB(1); break;
     case 3: FSC_GBB(3); break;
