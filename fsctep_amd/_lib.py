@@ -31,7 +31,7 @@ SIGNATURES = {
     "fsc_ictd_conv_forward": [_p, _i64, _i64, _i32] + [_p] * 10,
     "fsc_ictd_prepare_weights": [_p, _i32, _i32, _p, _p],
     "fsc_ictd_conv_backward": [_p, _i64, _i64, _i32] + [_p] * 16,
-    "fsc_ictd_conv1_forward": [_p, _i64, _i64, _i32] + [_p] * 7,
+    "fsc_ictd_conv1_forward": [_p, _i64, _i64, _i32, _i32] + [_p] * 8,
     "fsc_ictd_conv1_backward": [_p, _i64, _i64, _i32, _i32] + [_p] * 10,
     "fsc_gram_sizes": [_i64, _i32, _i32, _pi64, _pi64, _pi64],
     "fsc_gram_prepare_weights": [_p, _i32, _i32, _p, _p, _p],

@@ -595,35 +595,56 @@ __global__ __launch_bounds__(256) void source_sum_kernel(int M, const int32_t* _
 }
 
 // ---------------------------------------------------------------- conv1 (species-pair table)
+// out[n][comp(y)][o] = (1/deg) sum_{e->n} gate_e[p(y)] F_e[y] q[pair_e][p(y)][o].  The in-edges of n come
+// from at most NS species and share n's species, so the edge sum is first folded per source species,
+//   w[s][y] = sum_{e->n, src species s} gate_e[p(y)] F_e[y],
+// and the table is read once per (s, y) instead of once per edge (a per-edge loop re-read 16 C floats
+// of the table from L2 for every edge).
 template <int C, int NY>
-__global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, const int32_t* __restrict__ dst_ptr,
+__global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS, const int32_t* __restrict__ dst_ptr,
                                                         const int32_t* __restrict__ edge_pair,
+                                                        const int32_t* __restrict__ node_species,
                                                         const float* __restrict__ F,
                                                         const float* __restrict__ gates,
                                                         const float* __restrict__ qtab, float* __restrict__ out) {
-  const int n = blockIdx.x;
-  const int o = threadIdx.x;
-  if (o >= C) return;
+  __shared__ float w[8][NY];
+  __shared__ int ycomp[16];
+  const int n = blockIdx.x, t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
-  float acc[NY];
+  const int sn = node_species[n];
+  if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none)
+    int yy = -1;
 #pragma unroll
-  for (int y = 0; y < NY; ++y) acc[y] = 0.f;
-  for (int e = beg; e < end; ++e) {
-    const int64_t pair = edge_pair[e];
-    const float* fe = F + (int64_t)e * NY;
-    const float* ge = gates + (int64_t)e * L.NREF;
-#pragma unroll
-    for (int y = 0; y < NY; ++y) {
-      const int p = L.y_path1[y];
-      if (p >= 0) acc[y] += ge[L.c1_gate[p]] * qtab[(pair * L.NP1 + p) * C + o] * fe[y];
-    }
+    for (int y = 0; y < NY; ++y)
+      if (L.y_path1[y] >= 0 && L.y_oo1[y] == t) yy = y;
+    ycomp[t] = yy;
   }
+  if (t < NS * NY) {   // thread (s, y), edges in order
+    const int s = t / NY, y = t - s * NY, p = L.y_path1[y];
+    float a = 0.f;
+    if (p >= 0) {
+      const int gi = L.c1_gate[p];
+#pragma unroll 4
+      for (int e = beg; e < end; ++e) {
+        const float v = gates[(int64_t)e * L.NREF + gi] * F[(int64_t)e * NY + y];
+        a += (edge_pair[e] / NS == s) ? v : 0.f;
+      }
+    }
+    w[s][y] = a;
+  }
+  __syncthreads();
   const float scale = 1.f / (float)max(end - beg, 1);
-  float* on = out + (int64_t)n * L.M * C + o;
-  for (int c = 0; c < L.M; ++c) on[c * C] = 0.f;
-#pragma unroll
-  for (int y = 0; y < NY; ++y)
-    if (L.y_path1[y] >= 0) on[L.y_oo1[y] * C] = acc[y] * scale;
+  float* on = out + (int64_t)n * L.M * C;
+  for (int i = t; i < L.M * C; i += blockDim.x) {
+    const int c = i / C, o = i - c * C;
+    const int yy = ycomp[c];
+    float v = 0.f;
+    if (yy >= 0) {
+      const float* qp = qtab + ((int64_t)sn * L.NP1 + L.y_path1[yy]) * C + o;   // pair (s, sn) = s*NS + sn
+      for (int s2 = 0; s2 < NS; ++s2) v += w[s2][yy] * qp[(int64_t)s2 * NS * L.NP1 * C];
+    }
+    on[i] = v * scale;
+  }
 }
 
 template <int C, int NY>
@@ -634,35 +655,33 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ gates,
                                                         const float* __restrict__ qtab,
                                                         float* __restrict__ dF, float* __restrict__ dgates) {
-  __shared__ float red[NY][256];
+  __shared__ float gsh[NY][C];
   __shared__ float T[8][NY];
   const int n = blockIdx.x;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   if (beg == end) return;                      // uniform over the block
   const float scale = 1.f / (float)(end - beg);
   const int sn = node_species[n];
-  float gl[NY];
-#pragma unroll
-  for (int y = 0; y < NY; ++y)
-    gl[y] = (t < C && L.y_path1[y] >= 0) ? G[((int64_t)n * L.M + L.y_oo1[y]) * C + t] : 0.f;
-  // T[s][y] = (1/deg) sum_o G[n][comp(y)][o] Q[(s, sn)][p(y)][o]
-  for (int s = 0; s < NS; ++s) {
-    const int64_t pair = (int64_t)s * NS + sn;
-#pragma unroll
-    for (int y = 0; y < NY; ++y) {
-      const int p = L.y_path1[y];
-      red[y][t] = (t < C && p >= 0) ? gl[y] * qtab[(pair * L.NP1 + p) * C + t] : 0.f;
-    }
-    __syncthreads();
-    if (t < NY) {
-      float sacc = 0.f;
-      for (int j = 0; j < 256; ++j) sacc += red[t][j];
-      T[s][t] = sacc * scale;
-    }
-    __syncthreads();
+  for (int i = t; i < NY * C; i += blockDim.x) {
+    const int y = i / C, o = i - y * C;
+    gsh[y][o] = (L.y_path1[y] >= 0) ? G[((int64_t)n * L.M + L.y_oo1[y]) * C + o] : 0.f;
   }
-  // per edge: dF[e][y] = gate_p(y) T[s_src][y];  dgate[e][p] = sum_{y in p} T[s_src][y] F[e][y]
+  __syncthreads();
+  // T[s][y] = (1/deg) sum_o G[n][comp(y)][o] Q[(s, sn)][p(y)][o]: one wave per (s, y), lanes over o
+  for (int j = wave; j < NS * NY; j += 4) {
+    const int s = j / NY, y = j - s * NY;
+    const int p = L.y_path1[y];
+    float part = 0.f;
+    if (p >= 0) {
+      const float* qp = qtab + (((int64_t)s * NS + sn) * L.NP1 + p) * C;
+      for (int o = lane; o < C; o += 64) part += gsh[y][o] * qp[o];
+    }
+    part = wave_sum(part);
+    if (lane == 0) T[s][y] = part * scale;
+  }
+  __syncthreads();
+// per edge: dF[e][y] = gate_p(y) T[s_src][y];  dgate[e][p] = sum_{y in p} T[s_src][y] F[e][y]
   const int ne = end - beg;
   for (int idx = t; idx < ne * NY; idx += blockDim.x) {
     const int e = beg + idx / NY, y = idx % NY;
@@ -869,19 +888,22 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
 }
 
 int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                           const int32_t* dst_ptr, const int32_t* edge_pair, const float* F, const float* gates,
-                           const float* qtab, float* out, hipStream_t stream) {
+                           int32_t n_species, const int32_t* dst_ptr, const int32_t* edge_pair,
+                           const int32_t* node_species, const float* F, const float* gates, const float* qtab,
+                           float* out, hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv1_forward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv1_forward: bad size");
-  FSC_CHECK_ARG(dst_ptr && qtab && out, "fsc_ictd_conv1_forward: null pointer");
+  FSC_CHECK_ARG(n_species >= 1 && n_species <= 8, "fsc_ictd_conv1_forward: 1..8 species supported");
+  FSC_CHECK_ARG(dst_ptr && node_species && qtab && out, "fsc_ictd_conv1_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && F && gates), "fsc_ictd_conv1_forward: null edge pointer");
   FSC_CHECK_ARG(layout->NY == 9 || layout->NY == 16, "fsc_ictd_conv1_forward: lmax must be 2 or 3");
   if (n_nodes == 0) return 0;
   const FscIctdLayout& L = *layout;
   LaunchTimer tm("ictd_conv1", stream);
   const unsigned grid = (unsigned)n_nodes;
-#define FSC_C1F(CC, NYY) conv1_fwd_kernel<CC, NYY><<<grid, 256, 0, stream>>>(L, dst_ptr, edge_pair, F, gates, qtab, out)
+#define FSC_C1F(CC, NYY) \
+  conv1_fwd_kernel<CC, NYY><<<grid, 256, 0, stream>>>(L, n_species, dst_ptr, edge_pair, node_species, F, gates, qtab, out)
   if (L.NY == 9) {
     if (channels == 128) FSC_C1F(128, 9); else if (channels == 64) FSC_C1F(64, 9); else FSC_C1F(32, 9);
   } else {

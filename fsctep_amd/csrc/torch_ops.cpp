@@ -256,8 +256,9 @@ Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, c
   const int64_t C = qtab_.size(-1), E = F_.size(0);
   Tensor F = f32c(F_), gates = f32c(gates_), qtab = f32c(qtab_);
   Tensor out = at::empty({n_nodes, L->M, C}, fopts(F));
-  check(fsc_ictd_conv1_forward(L, n_nodes, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")),
-                               ci(i32c(edge_pair, "edge_pair")), cf(F), cf(gates), cf(qtab), mf(out), stream_of(F)),
+  check(fsc_ictd_conv1_forward(L, n_nodes, E, (int32_t)C, (int32_t)n_species, ci(i32c(dst_ptr, "dst_ptr")),
+                               ci(i32c(edge_pair, "edge_pair")), ci(i32c(node_species, "node_species")), cf(F),
+                               cf(gates), cf(qtab), mf(out), stream_of(F)),
         "fsc_ictd_conv1_forward");
   return out;
 }

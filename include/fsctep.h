@@ -190,11 +190,13 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
 /* conv1 (ICTDIrrepsE3Conv / ICTDO3E3Conv, pure_cartesian_ictd_layers_full.py:341-473,
  * pure_cartesian_ictd_layers_o3.py:424-532): both operands depend only on the species, and
  * C(l,0,l) is the identity, so out[n][comp(l)][o] = (1/indeg) sum_e gate[e][p_l] Q[pair][p_l][o] F[e][l^2+k]
- * with Q[pair][p][o] = sum_ij W1[p][o][i][j] A_src[i] A_dst[j] (qtab [NS*NS][NP1][C]) and
- * F = Y plus the embedded external field on the l=1 block. */
+ * with Q[pair][p][o] = sum_ij W1[p][o][i][j] A_src[i] A_dst[j] (qtab [NS*NS][NP1][C], pair = s_src*NS +
+ * s_dst, n_species = NS <= 8; node_species [N] gives s_dst) and F = Y plus the embedded external field on
+ * the l=1 block. */
 int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                           const int32_t* dst_ptr, const int32_t* edge_pair, const float* F, const float* gates,
-                           const float* qtab, float* out, hipStream_t stream);
+                           int32_t n_species, const int32_t* dst_ptr, const int32_t* edge_pair,
+                           const int32_t* node_species, const float* F, const float* gates, const float* qtab,
+                           float* out, hipStream_t stream);
 
 /* grad_F [E][NY], grad_gates [E][NREF] (caller zero-fills) from grad_out [N][M][C]. */
 int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
