@@ -36,6 +36,12 @@ struct ProjSmem {
 
 __host__ __device__ inline int up4(int v) { return (v + 3) & ~3; }
 
+// Row stride (floats) of the per-edge gated coupling table in LDS: NBGP (a multiple of 4) rounded to
+// 4 mod 8, so that rows of consecutive edges start in different bank quadruples (a stride of 0 mod 8,
+// e.g. 496, puts every fourth row on the same banks: the DX product's float4 reads and the coupling
+// contraction's per-edge reads then conflict).
+__host__ __device__ inline int bg_stride(const FscIctdLayout& L) { return (L.NBGP % 8 == 4) ? L.NBGP : L.NBGP + 4; }
+
 __host__ __device__ inline ProjSmem proj_smem(const FscIctdLayout& L, int ncg, bool bwd) {
   ProjSmem s;
   int TT = 0;
@@ -48,7 +54,7 @@ __host__ __device__ inline ProjSmem proj_smem(const FscIctdLayout& L, int ncg, b
   s.gs = o;    o += up4(EB * L.NREF);
   s.srcs = o;  o += EB;
   s.wtask = o; o += 32;                    // per wave: task count + up to 4 task ids
-  s.bg = o;    o += EB * L.NBGP;
+  s.bg = o;    o += EB * bg_stride(L);
   s.T = s.tmap = s.toff = o;
   if (bwd) {
     s.T = o;    o += up4(EB * TT);
@@ -97,10 +103,12 @@ __device__ __forceinline__ void stage_chunk(const FscIctdLayout& L, int eb, int 
   if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
 }
 
-// Gated coupling table of the chunk: bg[e][j] = gate_e[p] sum_m2 Y_e[oy_p + m2] C_p[m1][m2][m3] (LDS only).
+// Gated coupling table of the chunk: bg[e][j] = gate_e[p] sum_m2 Y_e[oy_p + m2] C_p[m1][m2][m3] (LDS only,
+// rows bg_stride apart).
 __device__ __forceinline__ void build_bg(const FscIctdLayout& L, const float* __restrict__ cgs,
                                          const int2* __restrict__ desc, const float* __restrict__ ys,
                                          const float* __restrict__ gs, float* __restrict__ bg) {
+  const int bgs = bg_stride(L);
   for (int j = threadIdx.x; j < L.NBGP; j += blockDim.x) {
     const int2 d = desc[j];
     float s[EB];
@@ -117,7 +125,7 @@ __device__ __forceinline__ void build_bg(const FscIctdLayout& L, const float* __
       for (int e = 0; e < EB; ++e) s[e] *= gs[e * L.NREF + gate];
     }
 #pragma unroll
-    for (int e = 0; e < EB; ++e) bg[e * L.NBGP + j] = s[e];
+    for (int e = 0; e < EB; ++e) bg[e * bgs + j] = s[e];
   }
 }
 
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
 #pragma unroll
         for (int u = 0; u < EB / 4; ++u) {
           const int e = 4 * u + q;
-          a[u] = arow[e * L.NBGP + m1 * kpad];
+          a[u] = arow[e * bg_stride(L) + m1 * kpad];
           b[u] = ldv<V>(xcol + ((int64_t)srcs[e] * L.M + m1) * C);
         }
       };
@@ -467,7 +475,7 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
       int g = 0;
       while (g + 1 < L.NG && m >= L.g_o1[g + 1]) ++g;
       const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
-      const float* arow = bg + r * L.NBGP + L.g_bgoff[g] + m1 * kpad + 4 * q;
+      const float* arow = bg + r * bg_stride(L) + L.g_bgoff[g] + m1 * kpad + 4 * q;
       const float* bcol = gn + (int64_t)L.g_kstart[g] * C + span * SPAN + V * r;
       f4 acc[V];
 #pragma unroll
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
         if (kt >= nkt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          bg[(4 * q + i) * L.NBGP + L.g_bgoff[g] + m1 * kpad + kt * 16 + r] = acc[kt][i] * scale;
+          bg[(4 * q + i) * bg_stride(L) + L.g_bgoff[g] + m1 * kpad + kt * 16 + r] = acc[kt][i] * scale;
       }
     }
     __syncthreads();
@@ -547,7 +555,7 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
       const int p = tmap[j], m2 = j - toff[p];
       const int g = L.p_group[p];
       const int d1 = L.g_d1[g], kpad = L.g_kpad[g], d2 = L.p_d2[p], d3 = L.p_d3[p];
-      const float* h = bg + e * L.NBGP + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
+      const float* h = bg + e * bg_stride(L) + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
       const float* c = cgs + L.p_cgoff[p] + m2 * d3;
       float acc = 0.f;
       for (int m1 = 0; m1 < d1; ++m1)
