@@ -61,6 +61,43 @@ __device__ __forceinline__ f4 mfma_x6(const bf8& ah, const bf8& am, const bf8& a
   return mfma_bf16(ah, bh, c);
 }
 
+// ---- fp32 products from fp16 MFMA (v_mfma_f32_16x16x32_f16 / 32x32x16_f16, the bf16 rate), half the
+// MFMAs of split-bf16.  An operand is first scaled by a power of two s with |a s| < 2^14 (one s per MFMA
+// row or column, undone on the fp32 result), then split into two fp16 parts a s = h + l (h the
+// round-to-nearest fp16 of a s, l that of the remainder, which is exact in fp32): 22 significant bits.
+// A product keeps hh' + hl' + lh'; the dropped ll' is below 2^-22 of |a b|.  Parts under fp16's normal
+// range (2^-14) keep an absolute accuracy of 2^-25, i.e. 2^-38 of the largest scaled value.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// 2^k with bound * 2^k in [2^13, 2^14) (k within +-100; 1 for a zero, negative or non-finite bound)
+__device__ __forceinline__ float pow2_scale(float bound) {
+  if (!(bound > 0.f) || !(bound <= 3.4e38f)) return 1.f;
+  int e;
+  frexpf(bound, &e);   // bound = f 2^e, f in [0.5, 1)
+  return ldexpf(1.f, min(max(14 - e, -100), 100));
+}
+
+__device__ __forceinline__ void split2h(const float (&v)[8], float s, h8& h, h8& l) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = v[j] * s;
+    const _Float16 hh = (_Float16)x;
+    h[j] = hh;
+    l[j] = (_Float16)(x - (float)hh);
+  }
+}
+
+__device__ __forceinline__ f4 mfma_h16(const h8& a, const h8& b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// c += (ah + al)(bh + bl) without al bl; small terms first.
+__device__ __forceinline__ f4 mfma_x3(const h8& ah, const h8& al, const h8& bh, const h8& bl, f4 c) {
+  c = mfma_h16(al, bh, c);
+  c = mfma_h16(ah, bl, c);
+  return mfma_h16(ah, bh, c);
+}
+
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ void st4(float* p, const f4& v) { *reinterpret_cast<f4*>(p) = v; }
 

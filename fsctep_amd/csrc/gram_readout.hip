@@ -11,8 +11,9 @@
 // Channels split into nb = nC/16 blocks.  G is symmetric, so the forward sums block pairs I <= J only:
 //   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
 // with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  Both directions multiply in fp32
-// precision on bf16 MFMA where the registers allow (each operand split into three bf16 parts, six
-// part products kept; common.h), with the weights split once when they are prepared.  The backward is
+// precision on fp16 MFMA where the registers allow (each operand scaled by a power of two and split
+// into two fp16 parts, three part products kept; common.h), with the weights split once when they are
+// prepared and the Gram values / output gradients scaled per node.  The backward is
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
 // computed per (node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
@@ -52,17 +53,45 @@ __device__ __forceinline__ void group_order(int logical, int nchunks, int ntiles
   tile = grp * tgroup + (rem - chunk * gsize);
 }
 
-// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb).  After the
-// P*256*S floats of each come three bf16 planes (h, m, l; split3) of the same values: [plane][p][ab][o]
-// for the split-bf16 backward and [plane][p][jl][il/8][o][il%8] for the split-bf16 forward.
-__global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
-                               float* __restrict__ Wb) {
+// Block-pair weight buffers (floats): the fp32 pairs (P*256*S), two fp16 planes (h, l; split2h) of the
+// same values times the power of two sw with 2 max|W| sw < 2^14 (P*256*S floats together), then a tail
+// of GW_TAIL floats: [0] = 1/sw, [256..511] the partial maxima of |W| (Wf only).
+constexpr int GW_TAIL = 512;
+constexpr int WMAX_BLOCKS = 256;
+__host__ __device__ inline int64_t gram_weight_floats(int nb, int S) { return (int64_t)n_pairs(nb) * 512 * S + GW_TAIL; }
+
+// wmax[b] = max |W| over the grid-stride share of block b (grid WMAX_BLOCKS x 256).
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ W, int64_t n, float* __restrict__ wmax) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) m = fmaxf(m, fabsf(W[i]));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) wmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb), 256 threads.
+// The fp16 planes are [plane][p][ab][o] for the backward and [plane][p][jl][il/8][o][il%8] for the
+// forward.  Every block reduces the partial maxima itself, so all use the same sw.
+__global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
+                                                      float* __restrict__ Wb, const float* __restrict__ wmax) {
   const int I = blockIdx.y, J = blockIdx.x, nb = nC / 16;
+  __shared__ float red[4];
+  float mx = wmax[threadIdx.x];
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  const float sw = pow2_scale(2.f * fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  const int64_t plane = (int64_t)n_pairs(nb) * 256 * S;
+  if (I == 0 && J == 0 && threadIdx.x == 0) {
+    Wf[2 * plane] = 1.f / sw;
+    Wb[2 * plane] = 1.f / sw;
+  }
   if (I > J) return;
   const int p = pair_index(I, J, nb);
-  const int64_t plane = (int64_t)n_pairs(nb) * 256 * S;
-  __bf16* wb3 = reinterpret_cast<__bf16*>(Wb + plane);
-  __bf16* wf3 = reinterpret_cast<__bf16*>(Wf + plane);
+  _Float16* wb2 = reinterpret_cast<_Float16*>(Wb + plane);
+  _Float16* wf2 = reinterpret_cast<_Float16*>(Wf + plane);
   for (int idx = threadIdx.x; idx < 256 * S; idx += blockDim.x) {
     const int o = idx % S, ab = idx / S, a = ab / 16, b = ab % 16;
     const float wij = W[((int64_t)o * nC + I * 16 + a) * nC + J * 16 + b];
@@ -70,22 +99,38 @@ __global__ void prepare_kernel(const float* __restrict__ W, int S, int nC, float
     const float v = wij + wji;
     const int64_t e = ((int64_t)p * 256 + ab) * S + o;
     Wb[e] = v;
-    const __bf16 hb = (__bf16)v;
-    const float r1 = v - (float)hb;
-    const __bf16 mb = (__bf16)r1;
-    wb3[e] = hb;
-    wb3[plane + e] = mb;
-    wb3[2 * plane + e] = (__bf16)(r1 - (float)mb);
+    const _Float16 hb = (_Float16)(v * sw);
+    wb2[e] = hb;
+    wb2[plane + e] = (_Float16)(v * sw - (float)hb);
     const float f = (I == J) ? wij : wij + wji;
     Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = f;
     const int64_t ef = (int64_t)p * 256 * S + ((b * 2 + (a >> 3)) * S + o) * 8 + (a & 7);
-    const __bf16 fh = (__bf16)f;
-    const float f1 = f - (float)fh;
-    const __bf16 fm = (__bf16)f1;
-    wf3[ef] = fh;
-    wf3[plane + ef] = fm;
-    wf3[2 * plane + ef] = (__bf16)(f1 - (float)fm);
+    const _Float16 fh = (_Float16)(f * sw);
+    wf2[ef] = fh;
+    wf2[plane + ef] = (_Float16)(f * sw - (float)fh);
   }
+}
+
+// Per-node power of two for the forward's fp16 Gram operands: |G_n[i][j]| <= max_i sum_m t[n][m][i]^2
+// (Cauchy-Schwarz), so nsc[n] = pow2_scale of that bound keeps every scaled Gram value below 2^14.
+// One wave per node.
+__global__ __launch_bounds__(256) void node_scale_kernel(int64_t N, int D, int nC, const float* __restrict__ t,
+                                                         float* __restrict__ nsc) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;   // uniform over the wave
+  const float* tn = t + n * D * nC;
+  float mx = 0.f;
+  for (int i = lane; i < nC; i += 64) {
+    float s = 0.f;
+    for (int m = 0; m < D; ++m) {
+      const float v = tn[m * nC + i];
+      s += v * v;
+    }
+    mx = fmaxf(mx, s);
+  }
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) nsc[n] = pow2_scale(mx);
 }
 
 // Forward partial sums over PCHUNK block pairs: part[chunk][n][o].  A workgroup is 128 nodes (8 waves x
@@ -161,13 +206,14 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
   }
 }
 
-// Forward with split-bf16 products on v_mfma_f32_32x32x16_bf16 (32 nodes x 32 outputs per MFMA).  A
+// Forward with split-fp16 products on v_mfma_f32_32x32x16_f16 (32 nodes x 32 outputs per MFMA; the
+// Gram values of node n are scaled by nsc[n], the weights by sw, both undone on the result).  A
 // workgroup is 256 nodes (8 waves x 32) x one chunk of PCHUNK pairs; lane (r, q) of a wave is node r
 // and K half q.  Step s (0..15) of a pair contracts K = 8q + j <-> (il = 8q + j, jl = s), so a lane
 // keeps t[n][m][I0 + 8q + j] (unchanged along a row of pairs) and streams t[n][m][J0 + s] four steps at
 // a time: the next group's loads are issued once the group's last G values are formed (TSB = 1, in
 // flight during that step's products) or a whole group ahead into a second buffer (TSB = 2, 4D more
-// registers; no faster at these sizes).  The pair's three
+// registers; no faster at these sizes).  The pair's two
 // weight planes ([jl][il/8][o][il%8]: the 32 lanes of a K half read 512 contiguous bytes) are staged
 // in LDS and shared by the 8 waves; the next pair's planes are loaded a quarter at a time after each
 // group's t loads, so waiting for those never waits for the weights (one in-order load counter).
@@ -175,16 +221,18 @@ constexpr int NODES_BF = 256;
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 template <int D, int S, int TSB>
-__global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, float scale,
-                                                           const float* __restrict__ t,
-                                                           const __bf16* __restrict__ Wf3, int nchunks,
-                                                           float* __restrict__ part, int tgroup) {
+__global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, float scale,
+                                                          const float* __restrict__ t,
+                                                          const _Float16* __restrict__ Wf2,
+                                                          const float* __restrict__ winv,
+                                                          const float* __restrict__ nsc, int nchunks,
+                                                          float* __restrict__ part, int tgroup) {
   constexpr int NN = NODES_BF, CT = S / 32;
-  constexpr int PSZ = 256 * S;            // bf16 per plane of a pair
-  constexpr int PW = 3 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
+  constexpr int PSZ = 256 * S;            // fp16 per plane of a pair
+  constexpr int PW = 2 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
   constexpr int PWQ = (PW + 3) / 4;
-  static_assert((3 * PSZ / 8) % 512 == 0, "staging");
-  __shared__ __align__(16) __bf16 wl[3 * PSZ];
+  static_assert((2 * PSZ / 8) % 512 == 0, "staging");
+  __shared__ __align__(16) _Float16 wl[2 * PSZ];
   const int nb = nC / 16, np = n_pairs(nb);
   const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nchunks * ntiles);
@@ -196,6 +244,7 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
   const int64_t n = (int64_t)tile * NN + wave * 32 + r;
   const bool valid = n < N;
   const float* tn = t + (valid ? n : 0) * D * nC;   // rows past N read node 0; their results are not stored
+  const float sn = valid ? nsc[n] : 1.f;
   const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
   int I = 0, rowstart = 0;
   while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
@@ -213,7 +262,7 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
     for (int i = k * PWQ; i < min(PW, (k + 1) * PWQ); ++i) {
       const int idx = threadIdx.x + 512 * i;
       const int pl = idx / (PSZ / 8), rem = idx - pl * (PSZ / 8);
-      pw[i] = *reinterpret_cast<const f4*>(Wf3 + pl * plane + (int64_t)p * PSZ + 8 * rem);
+      pw[i] = *reinterpret_cast<const f4*>(Wf2 + pl * plane + (int64_t)p * PSZ + 8 * rem);
     }
   };
   float tc[D][8];
@@ -235,7 +284,7 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
   load_ts(0, J, 0);
 #pragma unroll
   for (int k = 0; k < 4; ++k) fetch_part(p0, k);
-  const __bf16* wp = wl + q * S * 8 + r * 8;
+  const _Float16* wp = wl + q * S * 8 + r * 8;
   for (int p = p0; p < p1; ++p) {
     __syncthreads();
 #pragma unroll
@@ -272,21 +321,17 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        bf8 ah, am, al;
-        split3(gv, ah, am, al);
+        h8 ah, al;
+        split2h(gv, sn, ah, al);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-          const __bf16* b = wp + (s * 2 * S + ct * 32) * 8;
-          const bf8 bh = *reinterpret_cast<const bf8*>(b);
-          const bf8 bm = *reinterpret_cast<const bf8*>(b + PSZ);
-          const bf8 bl = *reinterpret_cast<const bf8*>(b + 2 * PSZ);
+          const _Float16* b = wp + (s * 2 * S + ct * 32) * 8;
+          const h8 bh = *reinterpret_cast<const h8*>(b);
+          const h8 bl = *reinterpret_cast<const h8*>(b + PSZ);
           f16v c = acc[ct];
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, c, 0, 0, 0);
-          acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, c, 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, c, 0, 0, 0);
         }
       }
     }
@@ -295,12 +340,14 @@ __global__ __launch_bounds__(512) void forward_bf16_kernel(int64_t N, int nC, fl
     J = Jn;
   }
   // result register v of lane (r, q) is node 8 (v / 4) + 4 q + v % 4 of the wave, output column r
+  const float f = scale * winv[0];
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int64_t node = (int64_t)tile * NN + wave * 32 + 8 * (v / 4) + 4 * q + (v % 4);
     if (node >= N) continue;
+    const float fn = f / nsc[node];   // nsc is a power of two: exact
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 32 + r] = acc[ct][v] * scale;
+    for (int ct = 0; ct < CT; ++ct) part[((int64_t)chunk * N + node) * S + ct * 32 + r] = acc[ct][v] * fn;
   }
 }
 
@@ -423,21 +470,22 @@ __global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float 
   }
 }
 
-// Split-bf16 version of backward_kernel (mfma_x6; fp32 accuracy, 2.7x the fp32 MFMA rate): the
-// (W + W^T) block is staged from its three bf16 planes, g is split once per wave, K = o runs in steps
-// of 32 (lane group q: o = 32 ks + 8q .. +7).  Same work split, contraction and output as above; the
-// planes take 1.5x the LDS of the fp32 block, so one workgroup runs per CU.
+// Split-fp16 version of backward_kernel (mfma_x3; fp32 accuracy at 5x the fp32 MFMA rate): the
+// (W + W^T) block is staged from its two fp16 planes (scaled by sw), each node's g is scaled by a power
+// of two from its own max |g| and split once per wave, K = o runs in steps of 32 (lane group q:
+// o = 32 ks + 8q .. +7).  Same work split, contraction and output as above, both scales undone at the end.
 template <int D, int S, int ILW, bool PIPE>
-__global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, float scale,
-                                                            const float* __restrict__ g, const float* __restrict__ t,
-                                                            const __bf16* __restrict__ Wb3, float* __restrict__ dt) {
+__global__ __launch_bounds__(512) void backward_h16_kernel(int64_t N, int nC, float scale,
+                                                           const float* __restrict__ g, const float* __restrict__ t,
+                                                           const _Float16* __restrict__ Wb2,
+                                                           const float* __restrict__ winv, float* __restrict__ dt) {
   constexpr int NGRP = 16 / ILW;                 // waves sharing a node group
   constexpr int NN = 16 * 8 / NGRP;              // nodes per workgroup
   constexpr int KS = S / 32;
-  constexpr int RS = S + 8, AS = 16 * RS + 8, PS = 16 * AS;   // padded bf16 strides of b, a and a plane
-  constexpr int PW = 3 * 256 * S / 8 / 512;                   // 16-byte pieces of a block per thread
-  static_assert(3 * 256 * S / 8 % 512 == 0, "block staging");
-  __shared__ __align__(16) __bf16 wl[3 * PS];
+  constexpr int RS = S + 8, AS = 16 * RS + 8, PS = 16 * AS;   // padded fp16 strides of b, a and a plane
+  constexpr int PW = 2 * 256 * S / 8 / 512;                   // 16-byte pieces of a block per thread
+  static_assert(2 * 256 * S / 8 % 512 == 0, "block staging");
+  __shared__ __align__(16) _Float16 wl[2 * PS];
   const int nb = nC / 16, np = n_pairs(nb);
   const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nb * ntiles);
@@ -450,14 +498,24 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
   const bool valid = n < N;
   const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
-  bf8 gh[KS], gm[KS], gl[KS];
+  // the S values of a node's g are spread over lanes r, r + 16, r + 32, r + 48
+  float gv[KS][8];
+  float gmax = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const f4 x0 = valid ? ld4(g + n * S + 32 * ks + 8 * q) : zero;
     const f4 x1 = valid ? ld4(g + n * S + 32 * ks + 8 * q + 4) : zero;
-    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    split3(v, gh[ks], gm[ks], gl[ks]);
+    gv[ks][0] = x0.x; gv[ks][1] = x0.y; gv[ks][2] = x0.z; gv[ks][3] = x0.w;
+    gv[ks][4] = x1.x; gv[ks][5] = x1.y; gv[ks][6] = x1.z; gv[ks][7] = x1.w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gmax = fmaxf(gmax, fabsf(gv[ks][j]));
   }
+  gmax = fmaxf(gmax, __shfl_xor(gmax, 16, 64));
+  gmax = fmaxf(gmax, __shfl_xor(gmax, 32, 64));
+  const float sg = pow2_scale(gmax);
+  h8 gh[KS], gl[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) split2h(gv[ks], sg, gh[ks], gl[ks]);
   float acc[ILW][D];
 #pragma unroll
   for (int i = 0; i < ILW; ++i)
@@ -471,7 +529,7 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
     for (int i = 0; i < PW; ++i) {
       const int idx = threadIdx.x + 512 * i;   // (plane, 8-value piece of the block)
       const int pl = idx / (256 * S / 8), rem = idx - pl * (256 * S / 8);
-      pw[i] = *reinterpret_cast<const f4*>(Wb3 + pl * plane + (int64_t)pr * 256 * S + 8 * rem);
+      pw[i] = *reinterpret_cast<const f4*>(Wb2 + pl * plane + (int64_t)pr * 256 * S + 8 * rem);
     }
 #pragma unroll
     for (int m = 0; m < D; ++m) tq[m] = ld4(t + (nl * D + m) * nC + J * 16 + 4 * q);
@@ -499,13 +557,12 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
     // PIPE: the operands of step u + 1 are read from LDS before the products of step u are issued (at 2
     // waves per SIMD the compiler's own order waits on each read; costs 12 registers)
     constexpr int NSTEP = (ILW / 4) * KS * 4;
-    bf8 oh[2], om[2], ol[2];
+    h8 oh[2], ol[2];
     auto rd = [&](int u, int slot) {
       const int i4 = u / (KS * 4), ks = (u / 4) % KS, jj = u % 4;
       const int off = rbase + (il0 + 4 * i4 + jj) * ilstep + 32 * ks;
-      oh[slot] = *reinterpret_cast<const bf8*>(&wl[off]);
-      om[slot] = *reinterpret_cast<const bf8*>(&wl[PS + off]);
-      ol[slot] = *reinterpret_cast<const bf8*>(&wl[2 * PS + off]);
+      oh[slot] = *reinterpret_cast<const h8*>(&wl[off]);
+      ol[slot] = *reinterpret_cast<const h8*>(&wl[PS + off]);
     };
     if constexpr (PIPE) rd(0, 0);
 #pragma unroll
@@ -522,7 +579,7 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
           } else {
             rd(u, u & 1);
           }
-          dd[jj] = mfma_x6(oh[u & 1], om[u & 1], ol[u & 1], gh[ks], gm[ks], gl[ks], dd[jj]);
+          dd[jj] = mfma_x3(oh[u & 1], ol[u & 1], gh[ks], gl[ks], dd[jj]);
         }
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
@@ -547,11 +604,12 @@ __global__ __launch_bounds__(512) void backward_bf16_kernel(int64_t N, int nC, f
     for (int m = 0; m < D; ++m)
       h2[i][m] = (odd ? h1[QR + i][m] : h1[i][m]) + __shfl_xor(odd ? h1[i][m] : h1[QR + i][m], 16, 64);
   if (valid) {
+    const float f = scale * winv[0] / sg;   // sg is a power of two: exact
 #pragma unroll
     for (int m = 0; m < D; ++m) {
       float* o = dt + (n * D + m) * nC + I * 16 + il0 + QR * q;
 #pragma unroll
-      for (int i = 0; i < QR; ++i) o[i] = h2[i][m] * scale;
+      for (int i = 0; i < QR; ++i) o[i] = h2[i][m] * f;
     }
   }
 }
@@ -568,15 +626,21 @@ int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
 template <int S>
 int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float* Wf, float* part, float* out,
               hipStream_t st) {
-  // The split-bf16 kernel runs 256-node tiles at ~1.7x the fp32 kernel's rate per node, so a tile takes
-  // ~1.2x an fp32 128-node tile: with at most 128 of its workgroups (one partial round on 256 CUs) the
-  // fp32 kernel's twice as many smaller workgroups finish first.
+  // The split-fp16 kernel runs 256-node tiles at several times the fp32 kernel's rate per node; with at
+  // most 128 of its workgroups (one partial round on 256 CUs) the fp32 kernel's twice as many smaller
+  // workgroups finish first.
   const int np = n_pairs(nC / 16);
   const int nchunks = (np + PCHUNK - 1) / PCHUNK;
   const bool bf = (int64_t)nchunks * ((N + NODES_BF - 1) / NODES_BF) > 128;
   const int ntiles = (int)((N + (bf ? NODES_BF : NODES) - 1) / (bf ? NODES_BF : NODES));
   const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
-  const __bf16* Wf3 = reinterpret_cast<const __bf16*>(Wf + (int64_t)np * 256 * S);
+  const _Float16* Wf2 = reinterpret_cast<const _Float16*>(Wf + (int64_t)np * 256 * S);
+  const float* winv = Wf + (int64_t)np * 512 * S;
+  float* nsc = part + (int64_t)nchunks * N * S;
+  if (bf) {
+    node_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, D, nC, t, nsc);
+    if (check_launch("gram node scales")) return 2;
+  }
   // tiles per group: as many as keep the group's t rows within about half an XCD's 4 MB L2 (at D 7,
   // nC 384 a 256-node tile alone is 2.75 MB; larger groups re-fetch t for every pair chunk)
   const int64_t tile_bytes = (int64_t)NODES_BF * D * nC * 4;
@@ -585,7 +649,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
     LaunchTimer tm("gram_forward", st);
 #define FSC_GF(DD)                                                                                 \
   if (bf)                                                                                          \
-    forward_bf16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf3, nchunks, part, tg);  \
+    forward_h16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, part, tg); \
   else                                                                                             \
     forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
     switch (D) {
@@ -610,14 +674,16 @@ template <int S>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
   // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8.  D <= 7 use the
-  // split-bf16 kernel; at D 9 its accumulators and plane staging exceed the registers, so the fp32 one.
+  // split-fp16 kernel; at D 9 its accumulators and plane staging exceed the registers, so the fp32 one.
   const int nn = (D <= 5) ? NODES : NODES / 2;
   const int ntiles = (int)((N + nn - 1) / nn);
   const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
-  const __bf16* Wb3 = reinterpret_cast<const __bf16*>(Wb + (int64_t)n_pairs(nC / 16) * 256 * S);
+  const _Float16* Wb2 = reinterpret_cast<const _Float16*>(Wb + (int64_t)n_pairs(nC / 16) * 256 * S);
+  const float* winv = Wb + (int64_t)n_pairs(nC / 16) * 512 * S;
   LaunchTimer tm("gram_backward", st);
 #define FSC_GBB(DD) \
-  backward_bf16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb3, dt)
+  backward_h16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb2, \
+                                                                                            winv, dt)
   switch (D) {
     case 1: FSC_GBB(1); break;
     case 3: FSC_GBB(3); break;
@@ -642,9 +708,10 @@ int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, i
   FSC_CHECK_ARG(wf_floats && wb_floats && workspace_floats, "fsc_gram_sizes: null pointer");
   FSC_CHECK_ARG(n_nodes >= 0 && nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
                 "fsc_gram_sizes: nC must be a multiple of 16 (<= 1024), S 32 or 64");
-  *wf_floats = (int64_t)n_pairs(nC / 16) * 256 * S * 5 / 2;   // fp32 block pairs, then three bf16 planes
+  *wf_floats = gram_weight_floats(nC / 16, S);   // fp32 block pairs, two fp16 planes, scale and maxima
   *wb_floats = *wf_floats;
-  *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S;
+  // per-chunk partial sums, then one scale per node
+  *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S + n_nodes;
   return 0;
 }
 
@@ -653,7 +720,10 @@ int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, f
   FSC_CHECK_ARG(nC >= 16 && nC % 16 == 0 && nC <= 1024 && (S == 32 || S == 64),
                 "fsc_gram_prepare_weights: nC must be a multiple of 16 (<= 1024), S 32 or 64");
   const int nb = nC / 16;
-  prepare_kernel<<<dim3(nb, nb), 256, 0, stream>>>(W, S, nC, Wf, Wb);
+  float* wmax = Wf + gram_weight_floats(nb, S) - GW_TAIL + 256;
+  absmax_kernel<<<WMAX_BLOCKS, 256, 0, stream>>>(W, (int64_t)S * nC * nC, wmax);
+  if (check_launch("gram weight maximum")) return 2;
+  prepare_kernel<<<dim3(nb, nb), 256, 0, stream>>>(W, S, nC, Wf, Wb, wmax);
   return check_launch("gram prepare") ? 2 : 0;
 }
 

@@ -293,26 +293,33 @@ std::tuple<Tensor, Tensor> ictd_conv1_backward_meta(const Tensor&, const Tensor&
 std::tuple<Tensor, Tensor> gram_prepare_weights(const Tensor& W_) {
   require_gpu({W_});
   TORCH_CHECK(W_.dim() == 3 && W_.size(1) == W_.size(2), "W must be (S, nC, nC)");
-  const int64_t S = W_.size(0), nC = W_.size(1), nb = nC / 16, P = nb * (nb + 1) / 2;
+  const int64_t S = W_.size(0), nC = W_.size(1);
   Tensor W = f32c(W_);
-  // each flat: the fp32 block pairs (P*256*S floats) followed by their three bf16 planes (1.5x that)
-  Tensor Wf = at::empty({P * 256 * S * 5 / 2}, fopts(W)), Wb = at::empty({P * 256 * S * 5 / 2}, fopts(W));
+  // each flat: the fp32 block pairs (P*256*S floats), their two fp16 planes (as many floats) and a tail
+  int64_t wfn = 0, wbn = 0, wsn = 0;
+  check(fsc_gram_sizes(0, (int32_t)nC, (int32_t)S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
+  Tensor Wf = at::empty({wfn}, fopts(W)), Wb = at::empty({wbn}, fopts(W));
   check(fsc_gram_prepare_weights(cf(W), (int32_t)S, (int32_t)nC, mf(Wf), mf(Wb), stream_of(W)),
         "fsc_gram_prepare_weights");
   return {Wf, Wb};
 }
 
 std::tuple<Tensor, Tensor> gram_prepare_weights_meta(const Tensor& W) {
-  const int64_t S = W.size(0), nb = W.size(1) / 16, P = nb * (nb + 1) / 2;
-  return {at::empty({P * 256 * S * 5 / 2}, fopts(W)), at::empty({P * 256 * S * 5 / 2}, fopts(W))};
+  int64_t wfn = 0, wbn = 0, wsn = 0;
+  check(fsc_gram_sizes(0, (int32_t)W.size(1), (int32_t)W.size(0), &wfn, &wbn, &wsn), "fsc_gram_sizes");
+  return {at::empty({wfn}, fopts(W)), at::empty({wbn}, fopts(W))};
 }
 
-// Output width S of prepared forward weights for nC channels (P*640*S floats, P block pairs).
+// Output width S of prepared forward weights for nC channels (S 32 or 64; fsc_gram_sizes' count).
 int64_t gram_width(const Tensor& Wf, int64_t nC) {
-  const int64_t nb = nC / 16, per = nb * (nb + 1) / 2 * 640;
-  TORCH_CHECK(Wf.dim() == 1 && nC % 16 == 0 && nb > 0 && Wf.numel() % per == 0,
-              "prepared Gram weights do not match nC = ", nC);
-  return Wf.numel() / per;
+  TORCH_CHECK(Wf.dim() == 1 && nC % 16 == 0 && nC >= 16 && nC <= 1024, "prepared Gram weights do not match nC = ", nC);
+  for (int32_t S : {32, 64}) {
+    int64_t wfn = 0, wbn = 0, wsn = 0;
+    check(fsc_gram_sizes(0, (int32_t)nC, S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
+    if (Wf.numel() == wfn) return S;
+  }
+  TORCH_CHECK(false, "prepared Gram weights do not match nC = ", nC);
+  return 0;
 }
 
 Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale) {

@@ -219,13 +219,14 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
 int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, int64_t* wb_floats,
                    int64_t* workspace_floats);
 
-/* Block-pair layouts of W, each followed by the same values split into three bfloat16 planes
- * (fp32-accurate split-bf16 products): Wf, the forward's W_IJ + W_JI^T (W_II on the diagonal) as
- * [p][16][S][16] then [3][p][16][2][S][8], and Wb, the backward's W + W^T as [p][256][S] then
- * [3][p][256][S]; both are opaque to the caller and hold fsc_gram_sizes' counts. */
+/* Block-pair layouts of W, each followed by the same values times a power of two sw (2 max|W| sw <
+ * 2^14) split into two fp16 planes (fp32-accurate split-fp16 products) and a 512-float tail holding
+ * 1/sw: Wf, the forward's W_IJ + W_JI^T (W_II on the diagonal) as [p][16][S][16] then
+ * [2][p][16][2][S][8], and Wb, the backward's W + W^T as [p][256][S] then [2][p][256][S]; both are
+ * opaque to the caller and hold fsc_gram_sizes' counts. */
 int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, float* Wb, hipStream_t stream);
 
-/* out [N][S]; part_ws holds fsc_gram_sizes' workspace_floats (per-chunk partial sums). */
+/* out [N][S]; part_ws holds fsc_gram_sizes' workspace_floats (per-chunk partial sums, per-node scales). */
 int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
                      const float* Wf, float* part_ws, float* out, hipStream_t stream);
 

@@ -77,13 +77,13 @@ def test_gram_sizes_and_fake_kernels():
     from torch._subclasses.fake_tensor import FakeTensorMode
     from fsctep_amd import readout_ops
     wf, wb, ws = readout_ops.gram_sizes(1000, 384, 64)
-    assert ws == 38 * 1000 * 64                              # 24 blocks -> 300 pairs -> 38 chunks of 8
-    assert wf == wb == 300 * 256 * 64 * 5 // 2               # fp32 pairs + three bf16 planes
+    assert ws == 38 * 1000 * 64 + 1000                       # 24 blocks -> 300 pairs -> 38 chunks of 8; node scales
+    assert wf == wb == 300 * 256 * 64 * 2 + 512              # fp32 pairs + two fp16 planes + scale/maxima tail
     with pytest.raises(RuntimeError, match="multiple of 16"):
         readout_ops.gram_sizes(10, 40, 64)
     with FakeTensorMode():
         W = torch.empty(64, 192, 192)
         Wf, Wb = torch.ops.fsctep.gram_prepare_weights(W)
-        assert Wf.shape == Wb.shape == (78 * 256 * 64 * 5 // 2,)
+        assert Wf.shape == Wb.shape == (78 * 256 * 64 * 2 + 512,)
         out = torch.ops.fsctep.gram_bilinear(torch.empty(7, 9, 192), Wf, Wb, 1.0)
         assert out.shape == (7, 64)
