@@ -11,9 +11,10 @@
 // Channels split into nb = nC/16 blocks.  G is symmetric, so the forward sums block pairs I <= J only:
 //   out[n][o] = sum_{I<=J} sum_{il,jl} Wf[IJ][il][o][jl] G_n[I0+il][J0+jl]
 // with Wf[IJ] = W_IJ + W_JI^T for I < J and W_II on the diagonal.  Both directions multiply in fp32
-// precision on fp16 MFMA where the registers allow (each operand scaled by a power of two and split
-// into two fp16 parts, three part products kept; common.h), with the weights split once when they are
-// prepared and the Gram values / output gradients scaled per node.  The backward is
+// precision on fp16 MFMA (each operand scaled by a power of two and split into two fp16 parts, three
+// part products kept; common.h), with the weights split once when they are prepared and the Gram
+// values / output gradients scaled per node; a forward over few node tiles runs on the fp32 MFMA
+// instead (more, smaller workgroups).  The backward is
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
 // computed per (node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
@@ -362,118 +363,15 @@ __global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__
 
 // Backward: one workgroup per (node tile, row block I); a wave takes 16 nodes x ILW rows il of the
 // block (ILW = 16: 128 nodes per workgroup, ILW = 8: two waves per node group, 64 nodes).  Per J the
-// (I,J) block of (W + W^T) [a][b][o] is staged in LDS (rows padded so both the direct and the
-// transposed reads are free of bank conflicts) and shared by the 8 waves; the next J's block and
-// t rows are loaded into registers meanwhile.  The MFMA takes A = (W + W^T) rows jl (K = o) and
-// B = g of the wave's 16 nodes, so lane (r = node, q) ends with A_n[il][4q..4q+3] and contracts
-// it on the VALU with its own t[n][m][J0+4q..J0+4q+3]; the partial sums over q are reduced once,
-// after the J loop, with a butterfly that leaves lane q the rows il of its quarter.
-template <int D, int S, int ILW>
-__global__ __launch_bounds__(512) void backward_kernel(int64_t N, int nC, float scale, const float* __restrict__ g,
-                                           const float* __restrict__ t, const float* __restrict__ Wb,
-                                           float* __restrict__ dt) {
-  constexpr int NGRP = 16 / ILW;                 // waves sharing a node group
-  constexpr int NN = 16 * 8 / NGRP;              // nodes per workgroup
-  constexpr int KT = S / 16;
-  constexpr int RS = S + 4, AS = 16 * RS + 4;    // padded LDS strides of b and a (floats)
-  constexpr int PW = 256 * S / 4 / 512;          // float4 of a Wb block per thread
-  __shared__ float wl[16 * AS];
-  const int nb = nC / 16;
-  const int ntiles = (int)((N + NN - 1) / NN);
-  const int logical = xcd_logical(nb * ntiles);
-  if (logical < 0) return;
-  const int I = logical / ntiles, tile = logical - I * ntiles;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, q = lane >> 4;
-  const int il0 = (wave % NGRP) * ILW;
-  const int64_t n = (int64_t)tile * NN + (wave / NGRP) * 16 + r;
-  const bool valid = n < N;
-  const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
-  const f4 zero = {0.f, 0.f, 0.f, 0.f};
-  f4 ga[KT];
-#pragma unroll
-  for (int k = 0; k < KT; ++k) ga[k] = valid ? ld4(g + n * S + 16 * k + 4 * q) : zero;
-  float acc[ILW][D];
-#pragma unroll
-  for (int i = 0; i < ILW; ++i)
-#pragma unroll
-    for (int m = 0; m < D; ++m) acc[i][m] = 0.f;
-  f4 pw[PW], tq[D];
-  auto fetch = [&](int J) {
-    const int pr = (I <= J) ? pair_index(I, J, nb) : pair_index(J, I, nb);
-    const f4* src = reinterpret_cast<const f4*>(Wb + (int64_t)pr * 256 * S);
-#pragma unroll
-    for (int i = 0; i < PW; ++i) pw[i] = src[threadIdx.x + 512 * i];
-#pragma unroll
-    for (int m = 0; m < D; ++m) tq[m] = ld4(t + (nl * D + m) * nC + J * 16 + 4 * q);
-  };
-  fetch(0);
-  for (int J = 0; J < nb; ++J) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-      const int idx = threadIdx.x + 512 * i;   // float4 index in [a][b][o]
-      const int o4 = idx % (S / 4), ab = idx / (S / 4);
-      *reinterpret_cast<f4*>(&wl[(ab >> 4) * AS + (ab & 15) * RS + 4 * o4]) = pw[i];
-    }
-    __syncthreads();
-    f4 tc[D];
-#pragma unroll
-    for (int m = 0; m < D; ++m) tc[m] = tq[m];
-    if (J + 1 < nb) fetch(J + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    // A[row = jl][k = o] = (W + W^T)[o][I0 + il][J0 + jl]: block [a = il][b = jl] if I <= J, else [a = jl][b = il]
-    const bool upper = I <= J;
-    const int rbase = (upper ? r * RS : r * AS) + 4 * q;
-    const int ilstep = upper ? AS : RS;
-#pragma unroll
-    for (int i4 = 0; i4 < ILW / 4; ++i4) {
-      f4 dd[4] = {zero, zero, zero, zero};
-#pragma unroll
-      for (int k = 0; k < KT; ++k)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const f4 a4 = *reinterpret_cast<const f4*>(&wl[rbase + (il0 + 4 * i4 + jj) * ilstep + 16 * k]);
-          dd[jj] = mfma_k16(a4, ga[k], dd[jj]);
-        }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int m = 0; m < D; ++m)
-          acc[4 * i4 + jj][m] += dd[jj][0] * tc[m][0] + dd[jj][1] * tc[m][1] + dd[jj][2] * tc[m][2] +
-                                 dd[jj][3] * tc[m][3];
-    }
-  }
-  // sum over q (lanes r + 16q): after the xor-32 step a lane keeps the half of the rows selected by
-  // q & 2, after the xor-16 step the quarter selected by q & 1, i.e. rows [q*ILW/4, (q+1)*ILW/4)
-  constexpr int H = ILW / 2, QR = ILW / 4;
-  const bool hi = (q & 2) != 0, odd = (q & 1) != 0;
-  float h1[H][D];
-#pragma unroll
-  for (int i = 0; i < H; ++i)
-#pragma unroll
-    for (int m = 0; m < D; ++m)
-      h1[i][m] = (hi ? acc[H + i][m] : acc[i][m]) + __shfl_xor(hi ? acc[i][m] : acc[H + i][m], 32, 64);
-  float h2[QR][D];
-#pragma unroll
-  for (int i = 0; i < QR; ++i)
-#pragma unroll
-    for (int m = 0; m < D; ++m)
-      h2[i][m] = (odd ? h1[QR + i][m] : h1[i][m]) + __shfl_xor(odd ? h1[i][m] : h1[QR + i][m], 16, 64);
-  if (valid) {
-#pragma unroll
-    for (int m = 0; m < D; ++m) {
-      float* o = dt + (n * D + m) * nC + I * 16 + il0 + QR * q;
-#pragma unroll
-      for (int i = 0; i < QR; ++i) o[i] = h2[i][m] * scale;
-    }
-  }
-}
-
-// Split-fp16 version of backward_kernel (mfma_x3; fp32 accuracy at 5x the fp32 MFMA rate): the
-// (W + W^T) block is staged from its two fp16 planes (scaled by sw), each node's g is scaled by a power
-// of two from its own max |g| and split once per wave, K = o runs in steps of 32 (lane group q:
-// o = 32 ks + 8q .. +7).  Same work split, contraction and output as above, both scales undone at the end.
+// (I,J) block of (W + W^T) [a][b][o] is staged in LDS from its two fp16 planes (scaled by sw; rows
+// padded so both the direct and the transposed reads are free of bank conflicts) and shared by the 8
+// waves; the next J's block and t rows are loaded into registers meanwhile.  The MFMA (split-fp16,
+// mfma_x3: fp32 accuracy at 5x the fp32 MFMA rate) takes A = (W + W^T) rows jl (K = o, in steps of 32:
+// lane group q holds o = 32 ks + 8q .. +7) and B = g of the wave's 16 nodes, each node's g scaled by a
+// power of two from its own max |g| and split once.  Lane (r = node, q) ends with A_n[il][4q..4q+3] and
+// contracts it on the VALU with its own t[n][m][J0+4q..J0+4q+3]; the partial sums over q are reduced
+// once, after the J loop, with a butterfly that leaves lane q the rows il of its quarter, and both
+// scales are undone on the result.
 template <int D, int S, int ILW, bool PIPE>
 __global__ __launch_bounds__(512) void backward_h16_kernel(int64_t N, int nC, float scale,
                                                            const float* __restrict__ g, const float* __restrict__ t,
@@ -667,14 +565,13 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   return check_launch("gram reduce") ? 2 : 0;
 }
 
-// largest D whose backward has the registers for the operand pipeline
-constexpr int GB_PIPE_DMAX = 3;
+// largest D whose backward has the registers for the operand pipeline (at D 9 it spills)
+constexpr int GB_PIPE_DMAX = 7;
 
 template <int S>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
-  // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8.  D <= 7 use the
-  // split-fp16 kernel; at D 9 its accumulators and plane staging exceed the registers, so the fp32 one.
+  // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8.
   const int nn = (D <= 5) ? NODES : NODES / 2;
   const int ntiles = (int)((N + nn - 1) / nn);
   const unsigned grid = (unsigned)(((int64_t)(nC / 16) * ntiles + 7) / 8 * 8);
@@ -689,7 +586,7 @@ int backward_s(int64_t N, int D, int nC, float scale, const float* g, const floa
     case 3: FSC_GBB(3); break;
     case 5: FSC_GBB(5); break;
     case 7: FSC_GBB(7); break;
-    default: backward_kernel<9, S, 8><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb, dt); break;
+    default: FSC_GBB(9); break;
   }
 #undef FSC_GBB
   return check_launch("gram backward") ? 2 : 0;

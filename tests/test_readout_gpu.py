@@ -82,3 +82,57 @@ def test_scripted_graph_matches_eager_with_cpp_autograd():
     (g1,) = torch.autograd.grad(y1.square().sum(), t1)
     (g2,) = torch.autograd.grad(y2.square().sum(), t2)
     assert torch.equal(y1, y2) and torch.equal(g1, g2)
+
+
+def _per_node_rel(a, b):
+    """max over nodes of |a_n - b_n|_inf / |b_n|_inf; rows where b is zero must be exactly zero."""
+    a = a.detach().double().cpu().reshape(a.shape[0], -1)
+    b = b.detach().double().cpu().reshape(b.shape[0], -1)
+    den, err = b.abs().amax(1), (a - b).abs().amax(1)
+    nz = den > 0
+    assert torch.equal(err[~nz], torch.zeros_like(err[~nz]))
+    return float((err[nz] / den[nz]).max())
+
+
+def _ref_chunked(t, W, G, scale, chunk=256):
+    """float64 forward and gradient on the GPU, 256 nodes at a time (the Gram of 10^3 nodes is GBs)."""
+    S, nC = W.shape[0], W.shape[1]
+    Wm = W.reshape(S, -1)
+    Ws = (W + W.transpose(1, 2)).reshape(S, -1)
+    outs, grads = [], []
+    for n0 in range(0, t.shape[0], chunk):
+        tc = t[n0:n0 + chunk]
+        gram = torch.bmm(tc.transpose(1, 2).contiguous(), tc) * scale           # (n, nC, nC)
+        outs.append(gram.reshape(gram.shape[0], -1) @ Wm.T)
+        A = (G[n0:n0 + chunk] @ Ws).reshape(-1, nC, nC)                            # A_n[i][j]
+        grads.append(torch.bmm(tc, A.transpose(1, 2).contiguous()) * scale)       # dt[n][m][i]
+    return torch.cat(outs), torch.cat(grads)
+
+
+# Node counts large enough for the split-fp16 forward (more than 128 workgroups of 256-node tiles);
+# node magnitudes spread over 8 decades, weight columns over 3, one all-zero node row and one
+# all-zero gradient row: the per-node power-of-two scales must keep every node's own relative error.
+WIDE = [(1100, 7, 384, 64), (1100, 3, 384, 64), (3400, 9, 192, 64), (2100, 1, 384, 32)]
+
+
+@pytest.mark.parametrize("N,D,nC,S", WIDE)
+def test_gram_bilinear_wide_dynamic_range(N, D, nC, S):
+    from fsctep_amd import readout_ops  # noqa: F401
+    g = torch.Generator().manual_seed(N + D)
+    f64 = dict(generator=g, dtype=torch.float64)
+    t = torch.randn(N, D, nC, **f64) * 10.0 ** (8 * torch.rand(N, 1, 1, **f64) - 4)
+    t[5] = 0.0
+    W = torch.randn(S, nC, nC, **f64) * 0.02 * 10.0 ** (-3 * torch.rand(S, 1, nC, **f64))
+    G = torch.randn(N, S, **f64) * 10.0 ** (8 * torch.rand(N, 1, **f64) - 4)
+    G[7] = 0.0
+    scale = 1.0 / D ** 0.5
+    tf, Wd, Gf = t.float(), W.float(), G.float()
+    ref, gref = _ref_chunked(tf.double().to(DEV), Wd.double().to(DEV), Gf.double().to(DEV), scale)
+
+    Wf, Wb = torch.ops.fsctep.gram_prepare_weights(Wd.to(DEV))
+    td = tf.to(DEV).requires_grad_(True)
+    out = torch.ops.fsctep.gram_bilinear(td, Wf, Wb, scale)
+    (gt,) = torch.autograd.grad(out, td, Gf.to(DEV))
+    torch.cuda.synchronize()
+    assert _per_node_rel(out, ref) < TOL
+    assert _per_node_rel(gt, gref) < TOL
