@@ -40,12 +40,45 @@ __host__ __device__ inline int64_t s_node_stride(int C) { return (int64_t)NSLOT 
 
 // ---------------------------------------------------------------- weight preparation
 // bk1[part][p][col][a] (col < 64C: col = c*64+k -> L[(p,c,a),k]; col >= 64C: b[(p,c,a)]) and
-// bk6[part][p][a][col] (transpose of bk1[p]), each split into three bf16 parts (h, m, l; see split3)
-// stored one after another, for the split-bf16 products of node_expand and node_expand_grad.
-__global__ void prep_weights_kernel(const float* __restrict__ L, const float* __restrict__ b,
-                                    __bf16* __restrict__ bk1, __bf16* __restrict__ bk6, int C) {
+// bk6[part][p][a][col] (transpose of bk1[p]): the values times the power of two sw (max |L|, |b|
+// times sw below 2^14) split into two fp16 parts (h, l; split2h), for the split-fp16 products of
+// node_expand and node_expand_grad.  Each buffer is the two parts (6*65*C*C fp16 each, as many floats
+// together) followed by a tail of SW_TAIL floats: [0] = 1/sw, [256..511] partial maxima (bk1 only).
+constexpr int SW_TAIL = 512;
+constexpr int SWMAX_BLOCKS = 256;
+__host__ __device__ inline int64_t sparse_weight_floats(int C) { return 6LL * 65 * C * C + SW_TAIL; }
+
+// wmax[block] = max |L|, |b| over the grid-stride share of the block (grid SWMAX_BLOCKS x 256).
+__global__ __launch_bounds__(256) void weight_absmax_kernel(const float* __restrict__ L, int64_t nl,
+                                                            const float* __restrict__ b, int64_t nb,
+                                                            float* __restrict__ wmax) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < nl + nb; i += (int64_t)gridDim.x * 256)
+    m = fmaxf(m, fabsf(i < nl ? L[i] : b[i - nl]));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) wmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// 256 threads per block; every block reduces the partial maxima itself, so all use the same sw.
+__global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restrict__ L, const float* __restrict__ b,
+                                                           float* __restrict__ bk1f, float* __restrict__ bk6f, int C) {
   const int64_t cols = 65LL * C;
   const int64_t total = 6LL * cols * C;
+  __shared__ float red[4];
+  float mx = bk1f[total + 256 + threadIdx.x];
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  const float sw = pow2_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    bk1f[total] = 1.f / sw;
+    bk6f[total] = 1.f / sw;
+  }
+  _Float16* bk1 = reinterpret_cast<_Float16*>(bk1f);
+  _Float16* bk6 = reinterpret_cast<_Float16*>(bk6f);
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int a = (int)(idx % C);
@@ -60,26 +93,24 @@ __global__ void prep_weights_kernel(const float* __restrict__ L, const float* __
       v = b[(int64_t)p * C * C + (int64_t)c * C + a];
     }
     const int64_t o = ((int64_t)p * C + a) * cols + col;
-    const __bf16 hb = (__bf16)v;
-    const float r1 = v - (float)hb;
-    const __bf16 mb = (__bf16)r1;
-    const __bf16 lb = (__bf16)(r1 - (float)mb);
+    const float vs = v * sw;
+    const _Float16 hb = (_Float16)vs;
+    const _Float16 lb = (_Float16)(vs - (float)hb);
     bk1[idx] = hb;
-    bk1[total + idx] = mb;
-    bk1[2 * total + idx] = lb;
+    bk1[total + idx] = lb;
     bk6[o] = hb;
-    bk6[total + o] = mb;
-    bk6[2 * total + o] = lb;
+    bk6[total + o] = lb;
   }
 }
 
 // ---------------------------------------------------------------- K1: node expansion
 // S[m][sbase(p)+I][col] = sum_a x[m][comp0(p)+I][a] * bk1[p][col][a].  A block takes 128 rows
 // (m, I) of one path (4 waves x 32 rows; blocks numbered path by path, `off` = first block of
-// each path) and a group of 80-column tiles.  Products are split-bf16 (mfma_x6, K = C in steps of
-// 32): the rows of x are split once into registers; each column tile of bk1 (80 x C, three bf16
-// parts) is staged in LDS, the next one loaded while the current one is multiplied and written to
-// the other LDS buffer before the current results are stored.
+// each path) and a group of 80-column tiles.  Products are split-fp16 (mfma_x3, K = C in steps of
+// 32): each row of x is scaled by a power of two from its own max |x| and split once into registers;
+// each column tile of bk1 (80 x C, two fp16 parts) is staged in LDS, the next one loaded while the
+// current one is multiplied and written to the other LDS buffer before the current results (both
+// scales undone) are stored.
 // Transposed product: bk1 rows are the MFMA A operand and x rows the B operand, and tile j's
 // A row i is column 16*j + i, so lane (r, q) ends with columns 16j+4q..16j+4q+3 of row r: the
 // four lanes of a row store 64 contiguous bytes per instruction.  Stores go through a buffer
@@ -92,17 +123,18 @@ constexpr int NE_TPB = 13;     // 80-column tiles per node_expand block
 
 template <int C>
 __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __restrict__ x,
-                                                             const __bf16* __restrict__ bk1,
+                                                             const _Float16* __restrict__ bk1,
+                                                             const float* __restrict__ winv,
                                                              float* __restrict__ S, int64_t n_nodes,
                                                              PathTiles tiles) {
   constexpr int COLS = 65 * C, NT = 5, WCOLS = 16 * NT, KS = C / 32;
   constexpr int NTC = COLS / WCOLS;                  // column tiles (52 or 26)
   constexpr int NCG = (NTC + NE_TPB - 1) / NE_TPB;   // column groups
   constexpr int RT = NE_ROWS / 64;                   // 16-row tiles per wave
-  constexpr int RW = C + 8;                          // bf16 per LDS row (padding against bank conflicts)
-  constexpr int NPC = 3 * WCOLS * (C / 8);           // 16-byte pieces of a tile
+  constexpr int RW = C + 8;                          // fp16 per LDS row (padding against bank conflicts)
+  constexpr int NPC = 2 * WCOLS * (C / 8);           // 16-byte pieces of a tile
   constexpr int NST = (NPC + 255) / 256;
-  __shared__ __align__(16) __bf16 sb[2][3][WCOLS][RW];
+  __shared__ __align__(16) _Float16 sb[2][2][WCOLS][RW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int bt = blockIdx.x / NCG, cg = blockIdx.x % NCG;
@@ -115,15 +147,16 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   const int64_t rows = n_nodes * nI;
   const int64_t brow0 = (int64_t)(bt - tiles.off[p]) * NE_ROWS;
   const int64_t row0 = brow0 + wave * (16 * RT);
-  const int64_t part = 6LL * COLS * C;               // bf16 per weight part
-  const __bf16* bp = bk1 + (int64_t)p * COLS * C;
+  const int64_t part = 6LL * COLS * C;               // fp16 per weight part
+  const _Float16* bp = bk1 + (int64_t)p * COLS * C;
   const int ct0 = cg * NE_TPB, ct1 = min(NTC, ct0 + NE_TPB);
   // store window: the nodes of the block's rows (at most NE_ROWS nodes, well below 4 GiB)
   const int64_t mfirst = (uint32_t)brow0 / (uint32_t)nI;
   const int64_t mlast = min(n_nodes - 1, (int64_t)((uint32_t)(brow0 + NE_ROWS - 1) / (uint32_t)nI));
   const __amdgpu_buffer_rsrc_t out =
       buffer_rsrc(S + mfirst * s_node_stride(C), (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * 4));
-  bf8 xh[RT][KS], xm[RT][KS], xl[RT][KS];
+  h8 xh[RT][KS], xl[RT][KS];
+  float oscale[RT];    // 1 / (sw * row scale)
   uint32_t ooff[RT];   // byte offset of the lane's first column in the store window
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -132,12 +165,23 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
     const int64_t m = ok ? (int64_t)((uint32_t)row / (uint32_t)nI) : mfirst;
     const int I = ok ? (int)(row - m * nI) : 0;
     const float* xr = x + (m * NCOMP + comp0 + I) * C + 8 * q;
+    float v[KS][8];
+    float vmax = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const f4 x0 = ld4(xr + 32 * ks), x1 = ld4(xr + 32 * ks + 4);
-      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      split3(v, xh[rt][ks], xm[rt][ks], xl[rt][ks]);
+      v[ks][0] = x0.x; v[ks][1] = x0.y; v[ks][2] = x0.z; v[ks][3] = x0.w;
+      v[ks][4] = x1.x; v[ks][5] = x1.y; v[ks][6] = x1.z; v[ks][7] = x1.w;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vmax = fmaxf(vmax, fabsf(v[ks][j]));
     }
+    // the C values of a row are spread over lanes r, r + 16, r + 32, r + 48
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 16, 64));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 32, 64));
+    const float sr = pow2_scale(vmax);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) split2h(v[ks], sr, xh[rt][ks], xl[rt][ks]);
+    oscale[rt] = winv[0] / sr;   // sr is a power of two: exact
     ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * 4)
                   : kDropOffset;
   }
@@ -179,12 +223,10 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf8 wh = *reinterpret_cast<const bf8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
-        const bf8 wm = *reinterpret_cast<const bf8*>(&sb[buf][1][16 * j + r][32 * ks + 8 * q]);
-        const bf8 wl = *reinterpret_cast<const bf8*>(&sb[buf][2][16 * j + r][32 * ks + 8 * q]);
+        const h8 wh = *reinterpret_cast<const h8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
+        const h8 wl = *reinterpret_cast<const h8*>(&sb[buf][1][16 * j + r][32 * ks + 8 * q]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          acc[rt][j] = mfma_x6(wh, wm, wl, xh[rt][ks], xm[rt][ks], xl[rt][ks], acc[rt][j]);
+        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_x3(wh, wl, xh[rt][ks], xl[rt][ks], acc[rt][j]);
       }
     // stage the next tile first: the waits for its loads then do not cover this tile's stores
     __builtin_amdgcn_sched_barrier(0);
@@ -193,7 +235,8 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) buffer_st4(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 4, acc[rt][j]);
+      for (int j = 0; j < NT; ++j)
+        buffer_st4(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 4, acc[rt][j] * oscale[rt]);
     __syncthreads();
   }
 }
@@ -203,8 +246,9 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 // row (m, I) of path p, then dx[m][comp][a] = sum over the halves and the slots of comp
 // (node_expand_grad_combine).  A block's work unit is (path, 256-row tile, K half), one 64-row
 // strip per wave: all units are equally long, which keeps the blocks balanced although paths
-// 0-2 share component 0.  Products are split-bf16 (mfma_x6, fp32 accuracy at 2.7x the fp32 MFMA
-// rate): the weights come split (bk6 parts h, m, l), the dS rows are split in registers.  The four
+// 0-2 share component 0.  Products are split-fp16 (mfma_x3, fp32 accuracy at 5x the fp32 MFMA
+// rate): the weights come split (bk6 parts h, l, scaled by sw), the dS rows are scaled by their node's
+// power of two (dscale, from edge_message_grad) and split in registers.  The four
 // waves share the path's weights: each 32-column chunk (C x 32 x 3 parts) is loaded once per block
 // into LDS (double-buffered) while the waves stream their own dS rows a chunk ahead.
 // Transposed product: bk6 rows (a) are the A operand, dS rows the B operand; tile at's A row
@@ -214,17 +258,19 @@ constexpr int NEG_ROWS = 256;   // slot rows per block
 
 template <int C>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
-                                                                  const __bf16* __restrict__ bk6,
+                                                                  const float* __restrict__ dscale,
+                                                                  const _Float16* __restrict__ bk6,
+                                                                  const float* __restrict__ winv,
                                                                   float* __restrict__ dxp,
                                                                   int64_t n_nodes, PathTiles tiles) {
   constexpr int COLS = 65 * C;
   constexpr int NA = C / 16;        // output a tiles
   constexpr int QW = C / 4;         // consecutive a per lane in the output
   constexpr int TPP = COLS / 32;    // K chunks per path
-  constexpr int RS = 40;            // bf16 per LDS row: 32 + 8 padding
-  constexpr int NPC = 3 * C * 4;              // 16-byte pieces of a chunk (3 parts x C rows x 4)
+  constexpr int RS = 40;            // fp16 per LDS row: 32 + 8 padding
+  constexpr int NPC = 2 * C * 4;              // 16-byte pieces of a chunk (2 parts x C rows x 4)
   constexpr int NST = (NPC + 255) / 256;      // per thread
-  __shared__ __align__(16) __bf16 wsh[2][3][C][RS];
+  __shared__ __align__(16) _Float16 wsh[2][2][C][RS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int kh = blockIdx.x & 1, bt = blockIdx.x >> 1;
@@ -239,6 +285,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   bool ok[4];
   int64_t rbase[4], mrow[4];
   int irow[4];
+  float rsc[4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     int64_t row = row0 + 16 * rt + r;
@@ -248,9 +295,10 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
     const int I = (int)(row - m * nI);
     mrow[rt] = m;
     irow[rt] = I;
+    rsc[rt] = dscale[m];
     rbase[rt] = m * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 8 * q;
   }
-  const int64_t part = 6LL * C * COLS;   // bf16 per weight part
+  const int64_t part = 6LL * C * COLS;   // fp16 per weight part
   f4 acc[4][NA];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
@@ -298,21 +346,20 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
       load_ds(bn, t + 1);
     }
     __builtin_amdgcn_sched_barrier(0);
-    bf8 dh[4], dm[4], dl[4];
+    h8 dh[4], dl[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const float v[8] = {bc[rt][0].x, bc[rt][0].y, bc[rt][0].z, bc[rt][0].w,
                           bc[rt][1].x, bc[rt][1].y, bc[rt][1].z, bc[rt][1].w};
-      split3(v, dh[rt], dm[rt], dl[rt]);
+      split2h(v, rsc[rt], dh[rt], dl[rt]);
     }
 #pragma unroll
     for (int at = 0; at < NA; ++at) {
       const int a = QW * (r >> 2) + 4 * at + (r & 3);
-      const bf8 wh = *reinterpret_cast<const bf8*>(&wsh[buf][0][a][8 * q]);
-      const bf8 wm = *reinterpret_cast<const bf8*>(&wsh[buf][1][a][8 * q]);
-      const bf8 wl = *reinterpret_cast<const bf8*>(&wsh[buf][2][a][8 * q]);
+      const h8 wh = *reinterpret_cast<const h8*>(&wsh[buf][0][a][8 * q]);
+      const h8 wl = *reinterpret_cast<const h8*>(&wsh[buf][1][a][8 * q]);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_x6(wh, wm, wl, dh[rt], dm[rt], dl[rt], acc[rt][at]);
+      for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_x3(wh, wl, dh[rt], dl[rt], acc[rt][at]);
     }
     if (t + 1 < te) {
       store_w(buf ^ 1);
@@ -328,8 +375,9 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   for (int rt = 0; rt < 4; ++rt) {
     if (!ok[rt]) continue;
     float* o = dxp + (((int64_t)kh * NSLOT + sbase + irow[rt]) * n_nodes + mrow[rt]) * C + QW * q;
+    const float f = winv[0] / rsc[rt];   // rsc is a power of two: exact
 #pragma unroll
-    for (int at = 0; at < NA; ++at) st4(o + 4 * at, acc[rt][at]);
+    for (int at = 0; at < NA; ++at) st4(o + 4 * at, acc[rt][at] * f);
   }
 }
 
@@ -557,7 +605,8 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
     const float* __restrict__ Gt, const float* __restrict__ nvec, const float* __restrict__ h,
     const float* __restrict__ S, const float* __restrict__ P, const int32_t* __restrict__ src_ptr,
     const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst, float scale,
-    float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, int64_t n_nodes) {
+    float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, float* __restrict__ dscale,
+    int64_t n_nodes) {
   constexpr int CC = 8;              // channels per chunk
   constexpr int NCH = C / CC;
   constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
@@ -569,6 +618,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   __shared__ int32_t dsts[EP];
   __shared__ float ns[EP][3];
   __shared__ float dnacc[EP][3];
+  __shared__ float amx[4];
   const int m = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -584,8 +634,10 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 
   if (end == beg) {   // no out-edges: dS of this node is zero (block-uniform branch)
     for (int idx = threadIdx.x; idx < NSLOT * COLS / 4; idx += 256) st4(dSm + 4 * idx, f4{0.f, 0.f, 0.f, 0.f});
+    if (threadIdx.x == 0) dscale[m] = 1.f;
     return;
   }
+  float amax = 0.f;   // max |dS| over the values stored by the last edge block (the final ones)
   int pb = beg;
   bool first = true;
   do {
@@ -741,6 +793,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
         f4 v = sacc[ct];
         if (!first) v += buffer_ld4(drs, dvoff, so);
         buffer_st4(drs, dvoff, so, v);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
       }
       if (threadIdx.x < DW) {
         const int col = threadIdx.x;
@@ -756,7 +809,9 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
         }
         const float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
         float* o = dSm + (int64_t)(col / CC) * COLS + 64 * C + c0 + col % CC;
-        *o = first ? sum : (*o + sum);
+        const float fin = first ? sum : (*o + sum);
+        *o = fin;
+        amax = fmaxf(amax, fabsf(fin));
       }
       __syncthreads();
     }
@@ -775,7 +830,13 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
     }
     first = false;
     pb += EP;
+    if (pb < end) amax = 0.f;   // block-uniform: only the last edge block's stores are final
   } while (pb < end);
+  // per-node power of two for the split-fp16 products of node_expand_grad
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if (lane == 0) amx[wave] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) dscale[m] = pow2_scale(fmaxf(fmaxf(amx[0], amx[1]), fmaxf(amx[2], amx[3])));
 }
 
 // ---------------------------------------------------------------- conv1 (species-pair form)
@@ -1048,7 +1109,7 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
     constexpr int ncg = ((65 * C) / 80 + NE_TPB - 1) / NE_TPB;
     LaunchTimer tm("node_expand", st);
     node_expand_kernel<C><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(
-        x, reinterpret_cast<const __bf16*>(bk1), S, N, tiles);
+        x, reinterpret_cast<const _Float16*>(bk1), bk1 + sparse_weight_floats(C) - SW_TAIL, S, N, tiles);
   }
   if (check_launch("sparse node_expand")) return 2;
   {
@@ -1071,13 +1132,14 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        hipStream_t st) {
   if (N == 0) return 0;
   // workspace tail (2 x 18 x N x C floats): first the chunk-major receiver gradient (13 x N x C), later
-  // the partial input gradients of node_expand_grad
+  // the partial input gradients of node_expand_grad; then N per-node scales of dS
   float* tail = dS + N * s_node_stride(C);
+  float* dscale = tail + 2LL * NSLOT * N * C;
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   {
     LaunchTimer tm("edge_message_grad", st);
     edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(tail, nvec, h, S, P, src_ptr, src_perm,
-                                                             edge_dst, scale, dh, dS, dn, N);
+                                                             edge_dst, scale, dh, dS, dn, dscale, N);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
   {
@@ -1089,7 +1151,8 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
     {
       LaunchTimer tm("node_expand_grad", st);
       node_expand_grad_kernel<C><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(
-          dS, reinterpret_cast<const __bf16*>(bk6), dxp, N, tiles);
+          dS, dscale, reinterpret_cast<const _Float16*>(bk6), bk6 + sparse_weight_floats(C) - SW_TAIL, dxp, N,
+          tiles);
     }
     if (check_launch("sparse node_expand_grad")) return 2;
     node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N);
@@ -1111,8 +1174,8 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_workspace: negative size");
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_workspace: channels must be 32 or 64");
   FSC_CHECK_ARG(s_floats && p_floats, "fsc_sparse_conv_workspace: null output");
-  // the tail (2 x 18 x N x C) holds the partial input gradients of the backward
-  *s_floats = n_nodes * s_node_stride(channels) + 2LL * NSLOT * n_nodes * channels;
+  // the tail (2 x 18 x N x C + N) holds the partial input gradients and per-node scales of the backward
+  *s_floats = n_nodes * s_node_stride(channels) + 2LL * NSLOT * n_nodes * channels + n_nodes;
   *p_floats = n_edges * (int64_t)NSLOT * channels;
   return 0;
 }
@@ -1121,8 +1184,11 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
                                     float* bk1, float* bk6, hipStream_t stream) {
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_prepare_weights: channels must be 32 or 64");
   FSC_CHECK_ARG(w_last && b_last && bk1 && bk6, "fsc_sparse_conv_prepare_weights: null pointer");
-  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, reinterpret_cast<__bf16*>(bk1),
-                                                reinterpret_cast<__bf16*>(bk6), channels);
+  const int64_t C = channels;
+  weight_absmax_kernel<<<SWMAX_BLOCKS, 256, 0, stream>>>(w_last, 6 * C * C * KH, b_last, 6 * C * C,
+                                                         bk1 + sparse_weight_floats(channels) - SW_TAIL + 256);
+  if (check_launch("sparse weight maximum")) return 2;
+  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, bk1, bk6, channels);
   return check_launch("sparse prepare_weights") ? 2 : 0;
 }
 

@@ -68,15 +68,15 @@ std::tuple<Tensor, Tensor> sparse_prepare_weights(const Tensor& w_last, const Te
   TORCH_CHECK(w_last.dim() == 2 && w_last.size(0) == 6 * C * C && w_last.size(1) == KH && b_last.numel() == 6 * C * C,
               "fc.4 of a sparse conv2 layer must be (6*C*C, 64)");
   Tensor w = f32c(w_last), b = f32c(b_last);
-  // bk1 and bk6 each hold three bf16 parts of 6*65*C*C values (1.5x the float count)
-  Tensor bk1 = at::empty({6 * 65 * C * C * 3 / 2}, fopts(w)), bk6 = at::empty_like(bk1);
+  // bk1 and bk6 each hold two fp16 parts of 6*65*C*C values (as many floats) and a 512-float tail
+  Tensor bk1 = at::empty({6 * 65 * C * C + 512}, fopts(w)), bk6 = at::empty_like(bk1);
   check(fsc_sparse_conv_prepare_weights(cf(w), cf(b), (int32_t)C, mf(bk1), mf(bk6), stream_of(w)),
         "fsc_sparse_conv_prepare_weights");
   return {bk1, bk6};
 }
 
 std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, const Tensor& b_last, int64_t C) {
-  return {at::empty({6 * 65 * C * C * 3 / 2}, fopts(w_last)), at::empty({6 * 65 * C * C * 3 / 2}, fopts(w_last))};
+  return {at::empty({6 * 65 * C * C + 512}, fopts(w_last)), at::empty({6 * 65 * C * C + 512}, fopts(w_last))};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,

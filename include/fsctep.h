@@ -52,9 +52,10 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
                               int64_t* s_floats, int64_t* p_floats);
 
 /* Re-layout fc.4.weight (6*C*C, 64) and fc.4.bias (6*C*C) into the two kernel operands bk1 and
- * bk6 (the operand and its transpose, each split into three bfloat16 parts of 6*65*C*C values, for
- * fp32-accurate split-bf16 products; 6*65*C*C*3/2 floats of storage each).  Both are opaque to the
- * caller.  Call again whenever those parameters change. */
+ * bk6 (the operand and its transpose, times a power of two and split into two fp16 parts of
+ * 6*65*C*C values, for fp32-accurate split-fp16 products, then a 512-float tail holding the scale;
+ * 6*65*C*C + 512 floats of storage each).  Both are opaque to the caller.  Call again whenever those
+ * parameters change. */
 int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, int32_t channels,
                                     float* bk1, float* bk6, hipStream_t stream);
 
