@@ -67,6 +67,59 @@ def test_conv2_op_matches_oracle(C):
     assert float(out[N - 1].abs().max()) == 0.0 and float(dx[N - 1].abs().max()) == 0.0
 
 
+def _rowwise_rel(a, b):
+    """max over rows (first axis) of |a_r - b_r|_inf / |b_r|_inf; rows where b is zero must be zero."""
+    a = a.detach().double().cpu().reshape(a.shape[0], -1)
+    b = b.detach().double().cpu().reshape(b.shape[0], -1)
+    den, err = b.abs().amax(1), (a - b).abs().amax(1)
+    nz = den > 0
+    assert float(err[~nz].max()) == 0.0 if (~nz).any() else True
+    return float((err[nz] / den[nz]).max())
+
+
+def test_conv2_op_wide_dynamic_range():
+    """The split-fp16 node expansion scales each x row by its own power of two and its gradient each
+    source node's dS: with x rows spread over 8 decades (per node and component), an all-zero node and
+    receiver gradients spread over 8 decades, every output row keeps its own relative accuracy."""
+    from fsctep_amd import ops
+    from fsctep_amd.graph import prepare_graph
+    C = 64
+    g = torch.Generator().manual_seed(17)
+    N = 40
+    src, dst = _graph_with_edge_cases(N, 400, 9)
+    E = src.shape[0]
+    x = torch.randn(N, 13, C, generator=g, dtype=torch.float64) * 10.0 ** (
+        8 * torch.rand(N, 13, 1, generator=g, dtype=torch.float64) - 4)
+    x[3] = 0.0
+    h = torch.randn(E, 64, generator=g, dtype=torch.float64)
+    v = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    n = v / v.norm(dim=1, keepdim=True)
+    L = torch.randn(6 * C * C, 64, generator=g, dtype=torch.float64) / 8
+    b = torch.randn(6 * C * C, generator=g, dtype=torch.float64) * 0.1
+    inv_norm = 1.0 / (E / N)
+    gr = prepare_graph(src.to(DEV), dst.to(DEV), torch.zeros(E, 3, device=DEV), N)
+    order = torch.argsort(dst, stable=True)
+    src_s, dst_s = src[order], dst[order]
+    h_s, n_s = h[order], n[order]
+    xf, hf, nf, Lf, bf = (t.float().double() for t in (x, h_s, n_s, L, b))   # the fp32 inputs, exactly
+    xo, ho, no = (t.clone().requires_grad_(True) for t in (xf, hf, nf))
+    ref = oracle_conv2(xo, ho, no, Lf, bf, src_s, dst_s, N, inv_norm)
+    G = (torch.randn(ref.shape, generator=g, dtype=torch.float64) *
+         10.0 ** (8 * torch.rand(N, 1, 1, generator=g, dtype=torch.float64) - 4)).float().double()
+    gx, gh, gn = torch.autograd.grad((ref * G).sum(), (xo, ho, no))
+    bk1, bk6 = torch.ops.fsctep.sparse_prepare_weights(Lf.float().to(DEV), bf.float().to(DEV), C)
+    xd = xf.float().to(DEV).requires_grad_(True)
+    hd = hf.float().to(DEV).requires_grad_(True)
+    nd = nf.float().to(DEV).requires_grad_(True)
+    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr, inv_norm)
+    dx, dh, dn = torch.autograd.grad(out, (xd, hd, nd), G.float().to(DEV))
+    torch.cuda.synchronize()
+    assert _rowwise_rel(out, ref) < TOL      # per receiver
+    assert _rowwise_rel(dx, gx) < TOL        # per source
+    assert _rowwise_rel(dh, gh) < TOL        # per edge
+    assert _rowwise_rel(dn, gn) < TOL
+
+
 def _inputs(g, dtype=torch.float32, device=DEV):
     n = g["pos"].shape[0]
     return dict(pos=torch.tensor(g["pos"], dtype=dtype, device=device),
