@@ -189,10 +189,11 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
                                                           const float* __restrict__ cg,
                                                           const int32_t* __restrict__ dst_ptr,
                                                           const int32_t* __restrict__ esrc,
-                                                          float* __restrict__ Z) {
+                                                          float* __restrict__ Z, float* __restrict__ zscale) {
   constexpr int SPAN = C < 64 ? C : 64;
   constexpr int V = SPAN / 16;
   extern __shared__ __align__(16) float smem[];
+  __shared__ float zmx[4];
   const ProjSmem sm = proj_smem(L, ncg, false);
   float* cgs = smem + sm.cgs;
   int2* desc = reinterpret_cast<int2*>(smem + sm.desc);
@@ -272,6 +273,7 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
   const float scale = 1.f / (float)max(end - beg, 1);
   __syncthreads();
   const int ntask = wtask[wave * 8];
+  float zmax = 0.f;
 #pragma unroll
   for (int lt = 0; lt < 4; ++lt) {
     if (lt >= ntask) break;
@@ -284,21 +286,31 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
       if (kkl >= L.g_kcount[g]) continue;
       VecF<V> o;
 #pragma unroll
-      for (int j = 0; j < V; ++j) o.v[j] = acc[lt][j][i] * scale;
+      for (int j = 0; j < V; ++j) {
+        o.v[j] = acc[lt][j][i] * scale;
+        zmax = fmaxf(zmax, fabsf(o.v[j]));
+      }
       stv<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + span * SPAN + V * r, o);
     }
   }
+  // per-node power of two for the split-fp16 channel mix
+  for (int off = 32; off > 0; off >>= 1) zmax = fmaxf(zmax, __shfl_xor(zmax, off, 64));
+  if (lane == 0) zmx[wave] = zmax;
+  __syncthreads();
+  if (threadIdx.x == 0) zscale[n] = pow2_scale(fmaxf(fmaxf(zmx[0], zmx[1]), fmaxf(zmx[2], zmx[3])));
 }
 
 // ---------------------------------------------------------------- channel mix, forward
 // out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i]; grid (rows/(64 RT), NK).
-// A wave takes RT 16-row tiles, so every weight float4 it loads feeds RT MFMAs (the weights of a path
-// are 4 C^2 bytes, re-read from L2 once per 16 RT rows).
+// A wave takes RT 16-row tiles, so every weight vector it loads feeds RT MFMAs (the weights of a path
+// are re-read from L2 once per 16 RT rows).  Split-fp16 products (mfma_x3, K = i in steps of 32): the
+// Z rows of node n are scaled by zscale[n] (from project_fwd), the weights by sw, both undone at the end.
 template <int C, int RT>
-__global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const float* __restrict__ Z,
-                                                      const float* __restrict__ W, float* __restrict__ out,
-                                                      int64_t N) {
-  constexpr int CT = C / 16;
+__global__ __launch_bounds__(256, 2) void mix_fwd_kernel(FscIctdLayout L, const float* __restrict__ Z,
+                                                      const float* __restrict__ zscale,
+                                                      const _Float16* __restrict__ Wh, const float* __restrict__ winv,
+                                                      float* __restrict__ out, int64_t N) {
+  constexpr int CT = C / 16, KS = C / 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int key = blockIdx.y;
@@ -306,15 +318,18 @@ __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const flo
   const int64_t rows = N * d;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   if (row0 >= rows) return;
+  const int64_t plane = (int64_t)L.NREF * C * C;
   int64_t an[RT];
   int ak[RT];
   bool ok[RT];
+  float zs[RT];
 #pragma unroll
   for (int u = 0; u < RT; ++u) {
     const int64_t arow = row0 + 16 * u + r;
     ok[u] = arow < rows;
     an[u] = ok[u] ? arow / d : 0;
     ak[u] = ok[u] ? (int)(arow % d) : 0;
+    zs[u] = zscale[an[u]];
   }
   f4 acc[RT][CT];
 #pragma unroll
@@ -323,23 +338,30 @@ __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const flo
     for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
   for (int p = 0; p < L.NP; ++p) {
     if (L.p_oo[p] != oo) continue;
-    const float* wp = W + (int64_t)L.p_gate[p] * C * C + r * C + 4 * q;
+    const _Float16* wp = Wh + (int64_t)L.p_gate[p] * C * C + r * C + 8 * q;   // row o = 16 ct + r
     const float* zr[RT];
 #pragma unroll
-    for (int u = 0; u < RT; ++u) zr[u] = Z + (an[u] * L.KT + L.p_koff[p] + ak[u]) * C + 4 * q;
-#pragma unroll 2
-    for (int t = 0; t < C / 16; ++t) {
-      f4 a4[RT], b4[CT];
+    for (int u = 0; u < RT; ++u) zr[u] = Z + (an[u] * L.KT + L.p_koff[p] + ak[u]) * C + 8 * q;
+#pragma unroll 1
+    for (int t = 0; t < KS; ++t) {
+      h8 ah[RT], al[RT];
 #pragma unroll
-      for (int u = 0; u < RT; ++u) a4[u] = ok[u] ? ld4(zr[u] + 16 * t) : f4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < RT; ++u) {
+        const f4 z0 = ok[u] ? ld4(zr[u] + 32 * t) : f4{0.f, 0.f, 0.f, 0.f};
+        const f4 z1 = ok[u] ? ld4(zr[u] + 32 * t + 4) : f4{0.f, 0.f, 0.f, 0.f};
+        const float v[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        split2h(v, zs[u], ah[u], al[u]);
+      }
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) b4[ct] = ld4(wp + 16 * ct * C + 16 * t);
+      for (int ct = 0; ct < CT; ++ct) {
+        const h8 bh = *reinterpret_cast<const h8*>(wp + 16 * ct * C + 32 * t);
+        const h8 bl = *reinterpret_cast<const h8*>(wp + plane + 16 * ct * C + 32 * t);
 #pragma unroll
-      for (int u = 0; u < RT; ++u)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[u][ct] = mfma_k16(a4[u], b4[ct], acc[u][ct]);
+        for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
+      }
     }
   }
+  const float wi = winv[0];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
@@ -348,20 +370,22 @@ __global__ __launch_bounds__(256) void mix_fwd_kernel(FscIctdLayout L, const flo
       if (row >= rows) continue;
       const int64_t nn = row / d;
       const int m = (int)(row % d);
+      const float f = wi / zscale[nn];   // a power of two: exact
       float* o = out + (nn * L.M + oo + m) * C;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i];
+      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
     }
 }
 
 // ---------------------------------------------------------------- channel mix, backward
 // dZ[n][koff_p + m][i] = sum_o Wt[gate_p][i][o] G[n][oo_p + m][o]; grid (rows/(64 RT), NP), RT row tiles
-// per wave as in the forward.
+// per wave as in the forward; the G rows of node n are scaled by gscale[n] (row_scale_kernel).
 template <int C, int RT>
 __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const float* __restrict__ G,
-                                                      const float* __restrict__ Wt, float* __restrict__ dZ,
-                                                      int64_t N) {
-  constexpr int CT = C / 16;
+                                                      const float* __restrict__ gscale,
+                                                      const _Float16* __restrict__ Wth, const float* __restrict__ winv,
+                                                      float* __restrict__ dZ, int64_t N) {
+  constexpr int CT = C / 16, KS = C / 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int p = blockIdx.y;
@@ -369,34 +393,44 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
   const int64_t rows = N * d;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   if (row0 >= rows) return;
+  const int64_t plane = (int64_t)L.NREF * C * C;
   const float* gr[RT];
   bool ok[RT];
+  float gs[RT];
 #pragma unroll
   for (int u = 0; u < RT; ++u) {
     const int64_t arow = row0 + 16 * u + r;
     ok[u] = arow < rows;
     const int64_t an = ok[u] ? arow / d : 0;
     const int ak = ok[u] ? (int)(arow % d) : 0;
-    gr[u] = G + (an * L.M + oo + ak) * C + 4 * q;
+    gr[u] = G + (an * L.M + oo + ak) * C + 8 * q;
+    gs[u] = gscale[an];
   }
-  const float* wp = Wt + (int64_t)L.p_gate[p] * C * C + r * C + 4 * q;
+  const _Float16* wp = Wth + (int64_t)L.p_gate[p] * C * C + r * C + 8 * q;   // row i = 16 ct + r
   f4 acc[RT][CT];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
-  for (int t = 0; t < C / 16; ++t) {
-    f4 a4[RT], b4[CT];
+  for (int t = 0; t < KS; ++t) {
+    h8 ah[RT], al[RT];
 #pragma unroll
-    for (int u = 0; u < RT; ++u) a4[u] = ok[u] ? ld4(gr[u] + 16 * t) : f4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < RT; ++u) {
+      const f4 g0 = ok[u] ? ld4(gr[u] + 32 * t) : f4{0.f, 0.f, 0.f, 0.f};
+      const f4 g1 = ok[u] ? ld4(gr[u] + 32 * t + 4) : f4{0.f, 0.f, 0.f, 0.f};
+      const float v[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      split2h(v, gs[u], ah[u], al[u]);
+    }
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) b4[ct] = ld4(wp + 16 * ct * C + 16 * t);
+    for (int ct = 0; ct < CT; ++ct) {
+      const h8 bh = *reinterpret_cast<const h8*>(wp + 16 * ct * C + 32 * t);
+      const h8 bl = *reinterpret_cast<const h8*>(wp + plane + 16 * ct * C + 32 * t);
 #pragma unroll
-    for (int u = 0; u < RT; ++u)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) acc[u][ct] = mfma_k16(a4[u], b4[ct], acc[u][ct]);
+      for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
+    }
   }
+  const float wi = winv[0];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
@@ -405,9 +439,10 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
       if (row >= rows) continue;
       const int64_t nn = row / d;
       const int m = (int)(row % d);
+      const float f = wi / gscale[nn];   // a power of two: exact
       float* o = dZ + (nn * L.KT + koff + m) * C;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i];
+      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
     }
 }
 
@@ -707,14 +742,63 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
   }
 }
 
-__global__ void transpose_weights_kernel(const float* __restrict__ W, float* __restrict__ Wt, int n_ref, int C) {
+// Prepared channel-mix weights (floats): W times the power of two sw (max |W| sw < 2^14) split into two
+// fp16 parts (split2h) as [2][NREF][C (o)][C (i)] for the forward, the same values with the last two axes
+// swapped, [2][NREF][C (i)][C (o)], for the backward, then a tail of MIXW_TAIL floats: [0] = 1/sw,
+// [256..511] the partial maxima of the preparation.
+constexpr int MIXW_TAIL = 512;
+__host__ __device__ inline int64_t mix_weight_floats(int n_ref, int C) { return 2LL * n_ref * C * C + MIXW_TAIL; }
+
+// wmax[b] = max |W| over the grid-stride share of block b (grid 256 x 256).
+__global__ __launch_bounds__(256) void mix_absmax_kernel(const float* __restrict__ W, int64_t n, float* __restrict__ wmax) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) m = fmaxf(m, fabsf(W[i]));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) wmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// 256 threads per block; every block reduces the 256 partial maxima itself, so all use the same sw.
+__global__ __launch_bounds__(256) void prepare_mix_kernel(const float* __restrict__ W, float* __restrict__ Wp,
+                                                          int n_ref, int C) {
   const int64_t total = (int64_t)n_ref * C * C;
+  __shared__ float red[4];
+  float mx = Wp[2 * total + 256 + threadIdx.x];
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  const float sw = pow2_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  if (blockIdx.x == 0 && threadIdx.x == 0) Wp[2 * total] = 1.f / sw;
+  _Float16* wf = reinterpret_cast<_Float16*>(Wp);
+  _Float16* wb = reinterpret_cast<_Float16*>(Wp + total);
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
     const int i = (int)(idx % C);
     const int o = (int)((idx / C) % C);
     const int64_t p = idx / ((int64_t)C * C);
-    Wt[(p * C + i) * C + o] = W[idx];
+    const float v = W[idx] * sw;
+    const _Float16 h = (_Float16)v;
+    const _Float16 l = (_Float16)(v - (float)h);
+    const int64_t t = (p * C + i) * C + o;
+    wf[idx] = h;
+    wf[total + idx] = l;
+    wb[t] = h;
+    wb[total + t] = l;
   }
+}
+
+// nsc[n] = pow2_scale(max |X[n][:]|) over rows of `len` floats; one wave per row.
+__global__ __launch_bounds__(256) void row_scale_kernel(int64_t N, int len, const float* __restrict__ X,
+                                                        float* __restrict__ nsc) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;   // uniform over the wave
+  const float* xr = X + n * len;
+  float mx = 0.f;
+  for (int i = lane; i < len; i += 64) mx = fmaxf(mx, fabsf(xr[i]));
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) nsc[n] = pow2_scale(mx);
 }
 
 // ---------------------------------------------------------------- host side
@@ -798,7 +882,8 @@ int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const i
   {
     LaunchTimer tm("ictd_project", st);
     const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
-    project_fwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z);
+    project_fwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
+                                                          Z + N * L.KT * C);
   }
   if (check_launch("ictd project_fwd")) return 2;
   int dmax = 1;
@@ -807,7 +892,8 @@ int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const i
     LaunchTimer tm("ictd_mix", st);
     constexpr int RT = mix_rt<C>();
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NK);
-    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, W, out, N);
+    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, reinterpret_cast<const _Float16*>(W),
+                                                 W + mix_weight_floats(L.NREF, C) - MIXW_TAIL, out, N);
   }
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
@@ -823,7 +909,11 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
     LaunchTimer tm("ictd_mix_grad", st);
     constexpr int RT = mix_rt<C>();
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NP);
-    mix_bwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, G, Wt, dZ, N);
+    float* gscale = dZ + N * L.KT * C;
+    row_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, L.M * C, G, gscale);
+    mix_bwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, G, gscale,
+                                                 reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
+                                                 Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, dZ, N);
   }
   if (check_launch("ictd mix_bwd")) return 2;
   {
@@ -867,8 +957,11 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
 
 int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wt, hipStream_t stream) {
   FSC_CHECK_ARG(W && Wt && n_ref > 0 && channels > 0, "fsc_ictd_prepare_weights: bad argument");
-  transpose_weights_kernel<<<256, 256, 0, stream>>>(W, Wt, n_ref, channels);
-  return check_launch("ictd transpose_weights") ? 2 : 0;
+  mix_absmax_kernel<<<256, 256, 0, stream>>>(W, (int64_t)n_ref * channels * channels,
+                                             Wt + mix_weight_floats(n_ref, channels) - MIXW_TAIL + 256);
+  if (check_launch("ictd weight maximum")) return 2;
+  prepare_mix_kernel<<<256, 256, 0, stream>>>(W, Wt, n_ref, channels);
+  return check_launch("ictd prepare_weights") ? 2 : 0;
 }
 
 int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,

@@ -191,16 +191,19 @@ std::tuple<Tensor, Tensor> sparse_conv1_backward_meta(const Tensor&, const Tenso
 
 // ============================================================== ICTD (pure-cartesian-ictd / -o3)
 
+// Prepared channel-mix weights: two fp16 planes of W, two of W with the channel axes swapped, a tail.
+int64_t ictd_weight_floats(int64_t n_ref, int64_t C) { return 2 * n_ref * C * C + 512; }
+
 Tensor ictd_prepare_weights(const Tensor& W) {
   require_gpu({W});
   const int64_t P = W.size(0), C = W.size(1);
   Tensor Wc = f32c(W).reshape({P, C, C});
-  Tensor Wt = at::empty_like(Wc);
-  check(fsc_ictd_prepare_weights(cf(Wc), (int32_t)P, (int32_t)C, mf(Wt), stream_of(Wc)), "fsc_ictd_prepare_weights");
-  return Wt;
+  Tensor Wp = at::empty({ictd_weight_floats(P, C)}, fopts(Wc));
+  check(fsc_ictd_prepare_weights(cf(Wc), (int32_t)P, (int32_t)C, mf(Wp), stream_of(Wc)), "fsc_ictd_prepare_weights");
+  return Wp;
 }
 
-Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({W.size(0), W.size(1), W.size(1)}, fopts(W)); }
+Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({ictd_weight_floats(W.size(0), W.size(1))}, fopts(W)); }
 
 Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
                  const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
@@ -209,10 +212,13 @@ Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const
   const FscIctdLayout* L = layout_of(layout);
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
   const int64_t N = x_.size(0), C = x_.size(2), E = Y_.size(0);
-  Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_), W = f32c(W_).reshape({W_.size(0), C, C});
-  Tensor z = at::empty({N, L->KT, C}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
+  Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
+  TORCH_CHECK(W_.size(0) == L->NREF && Wt.dim() == 1 && Wt.numel() == ictd_weight_floats(L->NREF, C),
+              "ictd_conv: Wt must be ictd_prepare_weights(W) of this layout's weights");
+  // z: N*KT*C floats of projections, then N per-node scales
+  Tensor z = at::empty({N * L->KT * C + N}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
   check(fsc_ictd_conv_forward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
-                              cf(x), cf(Y), cf(gates), cf(cg), cf(W), mf(z), mf(out), stream_of(x)),
+                              cf(x), cf(Y), cf(gates), cf(cg), cf(Wt), mf(z), mf(out), stream_of(x)),
         "fsc_ictd_conv_forward");
   return out;
 }
@@ -231,7 +237,9 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
   const FscIctdLayout* L = layout_of(layout);
   const int64_t N = x_.size(0), M = x_.size(1), C = x_.size(2), E = Y_.size(0);
   Tensor g = f32c(grad_out), x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
-  Tensor dz = at::empty({N, L->KT, C}, fopts(x)), dxe = at::empty({E, M, C}, fopts(x)), dx = at::empty({N, M, C}, fopts(x));
+  TORCH_CHECK(Wt.dim() == 1 && Wt.numel() == ictd_weight_floats(L->NREF, C),
+              "ictd_conv_backward: Wt must be ictd_prepare_weights(W) of this layout's weights");
+  Tensor dz = at::empty({N * L->KT * C + N}, fopts(x)), dxe = at::empty({E, M, C}, fopts(x)), dx = at::empty({N, M, C}, fopts(x));
   Tensor dgates = at::zeros({E, L->NREF}, fopts(x)), dY = at::empty({E, L->NY}, fopts(x));
   check(fsc_ictd_conv_backward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
                                ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")), cf(g), cf(x), cf(Y),

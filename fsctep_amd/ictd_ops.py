@@ -4,7 +4,7 @@ A layout (active irreps + live paths, see ``ictd_basis.Layout``) is turned into 
 ``FscIctdLayout`` once, registered under an integer id, and handed to the ops as a CPU int32
 tensor holding the struct.  The ops are registered in C++ by ``libfsctep_torch.so``:
 
-    ictd_prepare_weights(W) -> Wt
+    ictd_prepare_weights(W) -> Wt   (split-fp16 channel-mix weights, opaque)
     ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout) -> out
     ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout)
     ictd_conv1(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout)

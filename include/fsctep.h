@@ -170,22 +170,25 @@ typedef struct FscIctdLayout {
  * models/pure_cartesian_ictd_layers_full.py:938-954 (O3: pure_cartesian_ictd_layers_o3.py:956-973),
  * i.e. HarmonicFullyConnectedTensorProduct[O3].forward (models/ictd_irreps.py:971-1253, :1512-1695)
  * and the project/mix ops of the reference extension (csrc/ictd_tp.cpp:140-494).
- * gates [E][NREF]; W [NREF][C][C] (tp2.weight); cg: concatenated normalised C[m1][m2][m3] of the
- * live paths; z_ws [N][KT][C] scratch; out [N][M][C]. */
+ * gates [E][NREF]; Wp: fsc_ictd_prepare_weights of tp2.weight; cg: concatenated normalised C[m1][m2][m3]
+ * of the live paths; z_ws N*KT*C + N floats of scratch; out [N][M][C]. */
 int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                           const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
-                          const float* gates, const float* cg, const float* W, float* z_ws, float* out,
+                          const float* gates, const float* cg, const float* Wp, float* z_ws, float* out,
                           hipStream_t stream);
 
-/* Wt [NREF][C][C]: W with its last two axes swapped (call again when W changes). */
-int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wt, hipStream_t stream);
+/* Prepare tp2.weight W [NREF][C][C] for the channel mix: Wp holds 2*NREF*C*C + 512 floats (W times a
+ * power of two split into two fp16 planes, the same with the channel axes swapped, and the scale), opaque
+ * to the caller.  Call again when W changes. */
+int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wp, hipStream_t stream);
 
 /* Backward for forces: grad_x [N][M][C], grad_gates [E][NREF] (caller zero-fills: entries of paths
- * without a geometric operand stay 0), grad_Y [E][NY].  dz_ws [N][KT][C], dxe_ws [E][M][C] scratch. */
+ * without a geometric operand stay 0), grad_Y [E][NY].  Wp as for the forward; dz_ws N*KT*C + N floats,
+ * dxe_ws [E][M][C] scratch. */
 int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                            const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
                            const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
-                           const float* gates, const float* cg, const float* Wt, float* dz_ws,
+                           const float* gates, const float* cg, const float* Wp, float* dz_ws,
                            float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, hipStream_t stream);
 
 /* conv1 (ICTDIrrepsE3Conv / ICTDO3E3Conv, pure_cartesian_ictd_layers_full.py:341-473,
