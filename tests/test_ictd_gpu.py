@@ -86,6 +86,60 @@ def test_ictd_conv_op_matches_oracle(lname, C):
     assert float(out.detach()[N - 1].abs().max()) == 0.0 and float(dx[N - 1].abs().max()) == 0.0
 
 
+def _rowwise_rel(a, b):
+    """max over rows (first axis) of |a_r - b_r|_inf / |b_r|_inf; rows where b is zero must be zero."""
+    a = a.detach().double().cpu().reshape(a.shape[0], -1)
+    b = b.detach().double().cpu().reshape(b.shape[0], -1)
+    den, err = b.abs().amax(1), (a - b).abs().amax(1)
+    nz = den > 0
+    if (~nz).any():
+        assert float(err[~nz].max()) == 0.0
+    return float((err[nz] / den[nz]).max())
+
+
+def test_ictd_conv_op_wide_dynamic_range():
+    """The split-fp16 channel mix scales the projections of each receiver and the output gradient of each
+    node by their own powers of two: with node features and output gradients spread over 8 decades and an
+    all-zero node, every receiver's output and every node's input gradient keep their relative accuracy."""
+    from fsctep_amd import ictd_basis as B, ictd_ops
+    from fsctep_amd.graph import prepare_graph
+    lay, C = B.layout_full(3), 128
+    lid = ictd_ops.register_layout(lay)
+    g = torch.Generator().manual_seed(23)
+    N = 30
+    src, dst = _edges(N, 11)
+    order = torch.argsort(dst, stable=True)
+    src, dst = src[order], dst[order]
+    E = src.shape[0]
+    n = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    n = n / n.norm(dim=1, keepdim=True)
+    Y = torch.cat([I.direction_harmonics(n, l) for l in range(lay.lmax + 1)], dim=-1).float().double()
+    x = (torch.randn(N, lay.M, C, generator=g, dtype=torch.float64) *
+         10.0 ** (8 * torch.rand(N, 1, 1, generator=g, dtype=torch.float64) - 4)).float().double()
+    x[4] = 0.0
+    P = lay.n_ref_paths()
+    gates = torch.randn(E, P, generator=g, dtype=torch.float64).float().double()
+    W = (torch.randn(P, C, C, 1, generator=g, dtype=torch.float64) / np.sqrt(C)).float().double()
+    xo, Yo, go = (t.clone().requires_grad_(True) for t in (x, Y, gates))
+    ref = _oracle_conv(xo, Yo, go, W, src, dst, N, lay)
+    G = (torch.randn(ref.shape, generator=g, dtype=torch.float64) *
+         10.0 ** (8 * torch.rand(N, 1, 1, generator=g, dtype=torch.float64) - 4)).float().double()
+    gx, gY, gg = torch.autograd.grad((ref * G).sum(), (xo, Yo, go))
+
+    gr = prepare_graph(src.to(DEV), dst.to(DEV), torch.zeros(E, 3, device=DEV), N)
+    cg = torch.tensor(lay.cg_table(), dtype=torch.float32, device=DEV)
+    Wd = W.float().to(DEV)
+    Wt = torch.ops.fsctep.ictd_prepare_weights(Wd)
+    xd, Yd, gd = (t.float().to(DEV).requires_grad_(True) for t in (x, Y, gates))
+    out = ictd_ops.ictd_conv_apply(xd, Yd, gd, Wd, Wt, cg, gr, lid)
+    dx, dY, dg = torch.autograd.grad(out, (xd, Yd, gd), G.float().to(DEV))
+    torch.cuda.synchronize()
+    assert _rowwise_rel(out, ref) < TOL      # per receiver
+    assert _rowwise_rel(dx, gx) < TOL        # per source
+    assert _rowwise_rel(dY, gY) < TOL        # per edge
+    assert _rowwise_rel(dg, gg) < TOL
+
+
 CASES = ["ictd_open32_c32_l2", "ictd_pbc64_c128_l3", "ictdo3_pbc64_c64_l2_field"]
 
 
