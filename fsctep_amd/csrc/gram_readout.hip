@@ -373,7 +373,7 @@ __global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__
 // once, after the J loop, with a butterfly that leaves lane q the rows il of its quarter, and both
 // scales are undone on the result.
 template <int D, int S, int ILW, bool PIPE>
-__global__ __launch_bounds__(512) void backward_h16_kernel(int64_t N, int nC, float scale,
+__global__ __launch_bounds__(512, D == 1 ? 4 : 2) void backward_h16_kernel(int64_t N, int nC, float scale,
                                                            const float* __restrict__ g, const float* __restrict__ t,
                                                            const _Float16* __restrict__ Wb2,
                                                            const float* __restrict__ winv, float* __restrict__ dt) {
@@ -579,7 +579,8 @@ int backward_s(int64_t N, int D, int nC, float scale, const float* g, const floa
   const float* winv = Wb + (int64_t)n_pairs(nC / 16) * 512 * S;
   LaunchTimer tm("gram_backward", st);
 #define FSC_GBB(DD) \
-  backward_h16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, g, t, Wb2, \
+  backward_h16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD > 1 && DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, \
+                                                                                                    g, t, Wb2, \
                                                                                             winv, dt)
   switch (D) {
     case 1: FSC_GBB(1); break;
