@@ -381,6 +381,35 @@ __global__ __launch_bounds__(256) void geometry_backward_kernel(const float* __r
   }
 }
 
+// Geometry from caller-supplied edge vectors (input edge order) read through the receiver-sort
+// permutation `order`; the backward writes grad_vec in the input order (each edge once: no atomics).
+__global__ void vec_geometry_forward_kernel(const float* __restrict__ vec, const int32_t* __restrict__ order,
+                                            int64_t n_edges, float* __restrict__ nvec, float* __restrict__ rad) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  const int64_t i = order[e];
+  const float v0 = vec[3 * i], v1 = vec[3 * i + 1], v2 = vec[3 * i + 2];
+  const float r = sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
+  const float inv = 1.f / fmaxf(r, 1e-8f);
+  nvec[3 * e] = v0 * inv;
+  nvec[3 * e + 1] = v1 * inv;
+  nvec[3 * e + 2] = v2 * inv;
+  rad[e] = r;
+}
+
+__global__ void vec_geometry_backward_kernel(const float* __restrict__ gn, const float* __restrict__ gr,
+                                             const float* __restrict__ nvec, const float* __restrict__ rad,
+                                             const int32_t* __restrict__ order, int64_t n_edges,
+                                             float* __restrict__ gvec) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  float dv[3];
+  edge_dvec(gn, gr, nvec, rad, e, dv);
+  const int64_t i = order[e];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) gvec[3 * i + k] = dv[k];
+}
+
 // ---------------------------------------------------------------- direction harmonics (ICTD)
 // Y[e][l^2 + m] = sum_{k of degree l} M[k][m] n_x^a n_y^b n_z^c (M = multinomial * G_l B_l, the
 // ICTD harmonic basis); backward dn = sum_k (sum_m dY[l^2+m] M[k][m]) grad(n^abc).  One thread
@@ -483,6 +512,26 @@ int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* gr
   geometry_backward_kernel<<<(unsigned)((n_nodes + 3) / 4), 256, 0, stream>>>(grad_n, grad_r, n, r, dst_ptr,
                                                                               src_ptr, src_perm, n_nodes, grad_pos);
   return check_launch("edge geometry backward") ? 2 : 0;
+}
+
+int fsc_edge_vec_geometry_forward(int64_t n_edges, const float* edge_vec, const int32_t* order, float* n_out,
+                                  float* r_out, hipStream_t stream) {
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_edge_vec_geometry_forward: bad size");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(edge_vec && order && n_out && r_out, "fsc_edge_vec_geometry_forward: null pointer");
+  vec_geometry_forward_kernel<<<(unsigned)((n_edges + 255) / 256), 256, 0, stream>>>(edge_vec, order, n_edges,
+                                                                                     n_out, r_out);
+  return check_launch("edge vector geometry forward") ? 2 : 0;
+}
+
+int fsc_edge_vec_geometry_backward(int64_t n_edges, const float* grad_n, const float* grad_r, const float* n,
+                                   const float* r, const int32_t* order, float* grad_vec, hipStream_t stream) {
+  FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_edge_vec_geometry_backward: bad size");
+  if (n_edges == 0) return 0;
+  FSC_CHECK_ARG(n && r && order && grad_vec, "fsc_edge_vec_geometry_backward: null pointer");
+  vec_geometry_backward_kernel<<<(unsigned)((n_edges + 255) / 256), 256, 0, stream>>>(grad_n, grad_r, n, r, order,
+                                                                                      n_edges, grad_vec);
+  return check_launch("edge vector geometry backward") ? 2 : 0;
 }
 
 static unsigned radial_grid(int64_t n_edges) {

@@ -1,0 +1,335 @@
+// Graph preparation on the device: receiver sort, receiver CSR, source grouping, species pairs and
+// the species-pair tiles of the sparse conv1, with no host synchronisation and every output size a
+// function of (N, E, n_species) only.  Replaces the per-call `argsort(edge_dst)` and permutation of
+// the trunks (models/pure_cartesian_sparse_layers.py:745-748, models/pure_cartesian_ictd_layers_full.py:896-899,
+// models/pure_cartesian_ictd_layers_o3.py:924-927), run on every forward as the reference does.
+//
+// The receiver order is the stable one (ties in original edge order), so the result is deterministic.
+// Placement uses integer atomics per segment (counts, then cursors); the order inside a segment is then
+// fixed by ranking each entry against the other entries of its segment (rank = number of smaller
+// original ids), a sort of the segment that costs sum(deg^2) compares: ~27 M at 10k atoms (deg ~52).
+#include "common.h"
+#include "fsctep.h"
+
+namespace fsc {
+namespace {
+
+constexpr int SCAN_T = 256, SCAN_PER = 8, SCAN_TILE = SCAN_T * SCAN_PER;   // 2048 entries per block
+constexpr int64_t SCAN_MAX_BLOCKS = 4 * 1024 * SCAN_PER;                   // totals scanned by one block
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// Range checks (out-of-range ids are clamped so every later access stays in bounds; `status` gets a bit),
+// in/out degree counts, and the node species ids.
+__global__ __launch_bounds__(256) void count_kernel(int64_t E, int64_t N, const int64_t* __restrict__ src,
+                                                    const int64_t* __restrict__ dst, int32_t* __restrict__ cnt_in,
+                                                    int32_t* __restrict__ cnt_out, int32_t NS,
+                                                    const int64_t* __restrict__ species,
+                                                    int32_t* __restrict__ node_species, int32_t* __restrict__ status) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < E) {
+    int64_t s = src[i], d = dst[i];
+    if (s < 0 || s >= N || d < 0 || d >= N) {
+      atomicOr(status, 1);
+      s = s < 0 ? 0 : (s >= N ? N - 1 : s);
+      d = d < 0 ? 0 : (d >= N ? N - 1 : d);
+    }
+    atomicAdd(cnt_in + d, 1);
+    atomicAdd(cnt_out + s, 1);
+  }
+  if (NS > 0 && i < N) {
+    int64_t a = species[i];
+    if (a < 0 || a >= NS) {
+      atomicOr(status, 2);
+      a = a < 0 ? 0 : NS - 1;
+    }
+    node_species[i] = (int32_t)a;
+  }
+}
+
+__device__ __forceinline__ int64_t clamp_id(int64_t v, int64_t N) { return v < 0 ? 0 : (v >= N ? N - 1 : v); }
+
+// Exclusive scan of cnt[0..n) into out[0..n] (out[n] = total) in three passes: per-block scans with block
+// totals, one block scanning the totals, and the add-back.  blockIdx.y selects one of two arrays.
+struct ScanArgs {
+  const int32_t* cnt[2];
+  int32_t* out[2];
+  int32_t* tot[2];
+  int64_t n;
+};
+
+__device__ __forceinline__ int32_t block_exclusive_scan(int32_t v, int32_t* lds, int32_t& total) {
+  // 256 threads, wave64: scan in the wave, then across the 4 waves
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int32_t x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) lds[wave] = x;
+  __syncthreads();
+  int32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += lds[w];
+  total = lds[0] + lds[1] + lds[2] + lds[3];
+  __syncthreads();
+  return base + x - v;
+}
+
+__global__ __launch_bounds__(SCAN_T) void scan_blocks_kernel(ScanArgs a) {
+  __shared__ int32_t lds[4];
+  const int k = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * SCAN_TILE + (int64_t)threadIdx.x * SCAN_PER;
+  int32_t v[SCAN_PER], s = 0;
+#pragma unroll
+  for (int j = 0; j < SCAN_PER; ++j) {
+    v[j] = (base + j < a.n) ? a.cnt[k][base + j] : 0;
+    s += v[j];
+  }
+  int32_t total;
+  int32_t run = block_exclusive_scan(s, lds, total);
+#pragma unroll
+  for (int j = 0; j < SCAN_PER; ++j) {
+    if (base + j <= a.n) a.out[k][base + j] = run;
+    run += v[j];
+  }
+  if (threadIdx.x == 0) a.tot[k][blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(1024) void scan_totals_kernel(ScanArgs a, int nblocks) {
+  __shared__ int32_t lds[16];
+  const int k = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int PER = (int)(SCAN_MAX_BLOCKS / 1024);
+  int32_t v[PER], s = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int idx = threadIdx.x * PER + j;
+    v[j] = idx < nblocks ? a.tot[k][idx] : 0;
+    s += v[j];
+  }
+  int32_t x = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) lds[wave] = x;
+  __syncthreads();
+  int32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += lds[w];
+  int32_t run = base + x - s;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int idx = threadIdx.x * PER + j;
+    if (idx < nblocks) a.tot[k][idx] = run;
+    run += v[j];
+  }
+}
+
+__global__ __launch_bounds__(SCAN_T) void scan_add_kernel(ScanArgs a) {
+  const int k = blockIdx.y;
+  const int32_t add = a.tot[k][blockIdx.x];
+  const int64_t base = (int64_t)blockIdx.x * SCAN_TILE + (int64_t)threadIdx.x * SCAN_PER;
+#pragma unroll
+  for (int j = 0; j < SCAN_PER; ++j)
+    if (base + j <= a.n) a.out[k][base + j] += add;
+}
+
+// Unordered placement of each edge into its receiver segment.
+__global__ __launch_bounds__(256) void place_dst_kernel(int64_t E, int64_t N, const int64_t* __restrict__ dst,
+                                                        const int32_t* __restrict__ dst_ptr,
+                                                        int32_t* __restrict__ cursor, int32_t* __restrict__ tmp) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= E) return;
+  const int64_t d = clamp_id(dst[i], N);
+  tmp[dst_ptr[d] + atomicAdd(cursor + d, 1)] = (int32_t)i;
+}
+
+// Final receiver order: each entry's rank among the original ids of its segment.  Writes the permutation
+// and the permuted source / receiver ids and species pair.
+__global__ __launch_bounds__(256) void rank_dst_kernel(int64_t E, int64_t N, const int64_t* __restrict__ src,
+                                                       const int64_t* __restrict__ dst,
+                                                       const int32_t* __restrict__ dst_ptr,
+                                                       const int32_t* __restrict__ tmp, int32_t NS,
+                                                       const int32_t* __restrict__ node_species,
+                                                       int32_t* __restrict__ order, int32_t* __restrict__ src32,
+                                                       int32_t* __restrict__ dst32, int32_t* __restrict__ edge_pair) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= E) return;
+  const int32_t i = tmp[p];
+  const int64_t d = clamp_id(dst[i], N), s = clamp_id(src[i], N);
+  const int32_t a = dst_ptr[d], b = dst_ptr[d + 1];
+  int32_t rank = 0;
+  for (int32_t q = a; q < b; ++q) rank += tmp[q] < i;
+  const int32_t o = a + rank;
+  order[o] = i;
+  src32[o] = (int32_t)s;
+  dst32[o] = (int32_t)d;
+  if (NS > 0) edge_pair[o] = node_species[s] * NS + node_species[d];
+}
+
+__global__ __launch_bounds__(256) void place_src_kernel(int64_t E, const int32_t* __restrict__ src32,
+                                                        const int32_t* __restrict__ src_ptr,
+                                                        int32_t* __restrict__ cursor, int32_t* __restrict__ tmp) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= E) return;
+  const int32_t s = src32[p];
+  tmp[src_ptr[s] + atomicAdd(cursor + s, 1)] = (int32_t)p;
+}
+
+__global__ __launch_bounds__(256) void rank_src_kernel(int64_t E, const int32_t* __restrict__ src32,
+                                                       const int32_t* __restrict__ src_ptr,
+                                                       const int32_t* __restrict__ tmp,
+                                                       int32_t* __restrict__ src_perm) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= E) return;
+  const int32_t p = tmp[q];
+  const int32_t s = src32[p];
+  const int32_t a = src_ptr[s], b = src_ptr[s + 1];
+  int32_t rank = 0;
+  for (int32_t k = a; k < b; ++k) rank += tmp[k] < p;
+  src_perm[a + rank] = p;
+}
+
+// Species-pair tiles: per-pair counts, then one block lays the pairs' tiles out back to back (each pair's
+// edge list padded to a multiple of 16), then the edges are placed.  The order of edges inside a pair's
+// tiles does not affect any result (each tile row is one edge's own product), so it is left unordered.
+__global__ __launch_bounds__(256) void pair_count_kernel(int64_t E, const int32_t* __restrict__ edge_pair,
+                                                         int32_t* __restrict__ pcnt) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p < E) atomicAdd(pcnt + edge_pair[p], 1);
+}
+
+__global__ __launch_bounds__(256) void pair_layout_kernel(int32_t P, const int32_t* __restrict__ pcnt,
+                                                          int32_t* __restrict__ tstart, int64_t T_max,
+                                                          int32_t* __restrict__ tpair) {
+  __shared__ int32_t lds[4];
+  __shared__ int32_t s_start[256];
+  __shared__ int32_t s_total;
+  const int t = threadIdx.x;
+  const int32_t tiles = t < P ? (pcnt[t] + 15) / 16 : 0;
+  int32_t total;
+  const int32_t start = block_exclusive_scan(tiles, lds, total);
+  if (t < P) tstart[t] = start;
+  s_start[t] = start;
+  if (t == 0) s_total = total;
+  __syncthreads();
+  // tile -> pair (tiles past the used ones: pair 0, all ids -1)
+  for (int64_t k = t; k < T_max; k += 256) {
+    int32_t pr = 0;
+    if (k < s_total) {
+      int lo = 0, hi = P - 1;   // last pair whose start <= k (pairs without tiles share a start)
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_start[mid] <= k) lo = mid; else hi = mid - 1;
+      }
+      pr = lo;
+    }
+    tpair[k] = pr;
+  }
+}
+
+__global__ __launch_bounds__(256) void pair_place_kernel(int64_t E, const int32_t* __restrict__ edge_pair,
+                                                         const int32_t* __restrict__ tstart,
+                                                         int32_t* __restrict__ cursor, int32_t* __restrict__ ids) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= E) return;
+  const int32_t pr = edge_pair[p];
+  ids[(int64_t)tstart[pr] * 16 + atomicAdd(cursor + pr, 1)] = (int32_t)p;
+}
+
+unsigned grid_of(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+struct WsLayout {
+  int64_t cnt_in, cnt_out, cur_in, cur_out, tot, pcnt, pcur, tstart, tmp, total;
+};
+
+WsLayout ws_layout(int64_t N, int64_t E, int32_t NS) {
+  WsLayout w;
+  const int64_t nb = (N + 1 + SCAN_TILE - 1) / SCAN_TILE;
+  const int64_t P = (int64_t)NS * NS;
+  int64_t o = 0;
+  w.cnt_in = o;  o += N;
+  w.cnt_out = o; o += N;
+  w.cur_in = o;  o += N;
+  w.cur_out = o; o += N;
+  w.pcnt = o;    o += P;
+  w.pcur = o;    o += P;   // the zero-filled prefix ends here
+  w.tot = o;     o += 2 * nb;
+  w.tstart = o;  o += P;
+  w.tmp = o;     o += E;
+  w.total = o;
+  return w;
+}
+
+}  // namespace
+}  // namespace fsc
+
+extern "C" {
+
+int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t* n_tiles_max,
+                    int64_t* workspace_ints) {
+  FSC_CHECK_ARG(n_tiles_max && workspace_ints, "fsc_graph_sizes: null pointer");
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) - 1 && n_edges < (1LL << 31) - 1,
+                "fsc_graph_sizes: graph exceeds int32 indexing");
+  FSC_CHECK_ARG(n_species >= 0 && n_species <= 16, "fsc_graph_sizes: n_species must be 0..16");
+  *n_tiles_max = n_species > 0 ? (n_edges + 15) / 16 + (int64_t)n_species * n_species : 0;
+  *workspace_ints = fsc::ws_layout(n_nodes, n_edges, n_species).total;
+  return 0;
+}
+
+int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                      const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
+                      int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
+                      int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
+                      int32_t* workspace, hipStream_t stream) {
+  using namespace fsc;
+  int64_t T_max = 0, ws_ints = 0;
+  if (fsc_graph_sizes(n_nodes, n_edges, n_species, &T_max, &ws_ints)) return 1;
+  const int64_t N = n_nodes, E = n_edges;
+  FSC_CHECK_ARG(dst_ptr && src_ptr && status && workspace, "fsc_graph_prepare: null pointer");
+  FSC_CHECK_ARG(E == 0 || (N > 0 && edge_src && edge_dst && order && src32 && dst32 && src_perm),
+                "fsc_graph_prepare: null edge pointer (or edges without nodes)");
+  FSC_CHECK_ARG(n_species == 0 || N == 0 || (species && node_species), "fsc_graph_prepare: null species pointer");
+  FSC_CHECK_ARG(n_species == 0 || E == 0 || edge_pair, "fsc_graph_prepare: null edge_pair");
+  FSC_CHECK_ARG(n_species == 0 || pair_tiles, "fsc_graph_prepare: null pair_tiles");
+  const int64_t nb = (N + 1 + SCAN_TILE - 1) / SCAN_TILE;
+  FSC_CHECK_ARG(nb <= SCAN_MAX_BLOCKS, "fsc_graph_prepare: too many nodes for the scan");
+  const WsLayout w = ws_layout(N, E, n_species);
+  const int32_t P = n_species * n_species;
+  int32_t* ws = workspace;
+
+  if (w.tot > 0) fill_i32_kernel<<<grid_of(w.tot) < 1024 ? grid_of(w.tot) : 1024, 256, 0, stream>>>(ws, w.tot, 0);
+  fill_i32_kernel<<<1, 256, 0, stream>>>(status, 1, 0);
+  const int64_t cn = E > N ? E : N;
+  if (cn > 0)
+    count_kernel<<<grid_of(cn), 256, 0, stream>>>(E, N, edge_src, edge_dst, ws + w.cnt_in, ws + w.cnt_out, n_species,
+                                                  species, node_species, status);
+  ScanArgs sa;
+  sa.cnt[0] = ws + w.cnt_in;  sa.out[0] = dst_ptr; sa.tot[0] = ws + w.tot;
+  sa.cnt[1] = ws + w.cnt_out; sa.out[1] = src_ptr; sa.tot[1] = ws + w.tot + nb;
+  sa.n = N;
+  scan_blocks_kernel<<<dim3((unsigned)nb, 2), SCAN_T, 0, stream>>>(sa);
+  scan_totals_kernel<<<dim3(1, 2), 1024, 0, stream>>>(sa, (int)nb);
+  scan_add_kernel<<<dim3((unsigned)nb, 2), SCAN_T, 0, stream>>>(sa);
+  if (E > 0) {
+    place_dst_kernel<<<grid_of(E), 256, 0, stream>>>(E, N, edge_dst, dst_ptr, ws + w.cur_in, ws + w.tmp);
+    rank_dst_kernel<<<grid_of(E), 256, 0, stream>>>(E, N, edge_src, edge_dst, dst_ptr, ws + w.tmp, n_species,
+                                                    node_species, order, src32, dst32, edge_pair);
+    place_src_kernel<<<grid_of(E), 256, 0, stream>>>(E, src32, src_ptr, ws + w.cur_out, ws + w.tmp);
+    rank_src_kernel<<<grid_of(E), 256, 0, stream>>>(E, src32, src_ptr, ws + w.tmp, src_perm);
+  }
+  if (n_species > 0) {
+    fill_i32_kernel<<<grid_of(16 * T_max) < 1024 ? grid_of(16 * T_max) : 1024, 256, 0, stream>>>(pair_tiles,
+                                                                                                 16 * T_max, -1);
+    if (E > 0) pair_count_kernel<<<grid_of(E), 256, 0, stream>>>(E, edge_pair, ws + w.pcnt);
+    pair_layout_kernel<<<1, 256, 0, stream>>>(P, ws + w.pcnt, ws + w.tstart, T_max, pair_tiles + 16 * T_max);
+    if (E > 0) pair_place_kernel<<<grid_of(E), 256, 0, stream>>>(E, edge_pair, ws + w.tstart, ws + w.pcur, pair_tiles);
+  }
+  return check_launch("fsc_graph_prepare");
+}
+
+}  // extern "C"

@@ -642,7 +642,22 @@ __global__ __launch_bounds__(256) void source_sum_kernel(int M, const int32_t* _
 // from at most NS species and share n's species, so the edge sum is first folded per source species,
 //   w[s][y] = sum_{e->n, src species s} gate_e[p(y)] F_e[y],
 // and the table is read once per (s, y) instead of once per edge (a per-edge loop re-read 16 C floats
-// of the table from L2 for every edge).
+// of the table from L2 for every edge).  Species ids index the model's species table (NS <= 16 rows);
+// only the source species present among the node's in-edges are read.
+
+// Bit s set if some edge in [beg, end) has source species s (wave 0 computes it; every wave reads it).
+__device__ __forceinline__ unsigned src_species_mask(const int32_t* __restrict__ edge_pair, int NS, int beg, int end,
+                                                     unsigned* lds) {
+  if (threadIdx.x < 64) {
+    unsigned m = 0;
+    for (int e = beg + (int)threadIdx.x; e < end; e += 64) m |= 1u << (edge_pair[e] / NS);
+    for (int off = 32; off > 0; off >>= 1) m |= (unsigned)__shfl_xor((int)m, off, 64);
+    if (threadIdx.x == 0) *lds = m;
+  }
+  __syncthreads();
+  return *lds;
+}
+
 template <int C, int NY>
 __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS, const int32_t* __restrict__ dst_ptr,
                                                         const int32_t* __restrict__ edge_pair,
@@ -650,11 +665,13 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ F,
                                                         const float* __restrict__ gates,
                                                         const float* __restrict__ qtab, float* __restrict__ out) {
-  __shared__ float w[8][NY];
+  __shared__ float w[16][NY];
   __shared__ int ycomp[16];
+  __shared__ unsigned smask;
   const int n = blockIdx.x, t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const int sn = node_species[n];
+  const unsigned mask = src_species_mask(edge_pair, NS, beg, end, &smask);
   if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none)
     int yy = -1;
 #pragma unroll
@@ -665,7 +682,7 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
   if (t < NS * NY) {   // thread (s, y), edges in order
     const int s = t / NY, y = t - s * NY, p = L.y_path1[y];
     float a = 0.f;
-    if (p >= 0) {
+    if (p >= 0 && ((mask >> s) & 1u)) {
       const int gi = L.c1_gate[p];
 #pragma unroll 4
       for (int e = beg; e < end; ++e) {
@@ -684,7 +701,10 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
     float v = 0.f;
     if (yy >= 0) {
       const float* qp = qtab + ((int64_t)sn * L.NP1 + L.y_path1[yy]) * C + o;   // pair (s, sn) = s*NS + sn
-      for (int s2 = 0; s2 < NS; ++s2) v += w[s2][yy] * qp[(int64_t)s2 * NS * L.NP1 * C];
+      for (unsigned m = mask; m; m &= m - 1) {   // source species in increasing order
+        const int s2 = __builtin_ctz(m);
+        v += w[s2][yy] * qp[(int64_t)s2 * NS * L.NP1 * C];
+      }
     }
     on[i] = v * scale;
   }
@@ -699,13 +719,15 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ qtab,
                                                         float* __restrict__ dF, float* __restrict__ dgates) {
   __shared__ float gsh[NY][C];
-  __shared__ float T[8][NY];
+  __shared__ float T[16][NY];
+  __shared__ unsigned smask;
   const int n = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   if (beg == end) return;                      // uniform over the block
   const float scale = 1.f / (float)(end - beg);
   const int sn = node_species[n];
+  const unsigned mask = src_species_mask(edge_pair, NS, beg, end, &smask);
   for (int i = t; i < NY * C; i += blockDim.x) {
     const int y = i / C, o = i - y * C;
     gsh[y][o] = (L.y_path1[y] >= 0) ? G[((int64_t)n * L.M + L.y_oo1[y]) * C + o] : 0.f;
@@ -714,6 +736,7 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
   // T[s][y] = (1/deg) sum_o G[n][comp(y)][o] Q[(s, sn)][p(y)][o]: one wave per (s, y), lanes over o
   for (int j = wave; j < NS * NY; j += 4) {
     const int s = j / NY, y = j - s * NY;
+    if (!((mask >> s) & 1u)) continue;         // no in-edge reads T[s]
     const int p = L.y_path1[y];
     float part = 0.f;
     if (p >= 0) {
@@ -995,7 +1018,7 @@ int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
   if (check_layout(layout, channels, "fsc_ictd_conv1_forward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv1_forward: bad size");
-  FSC_CHECK_ARG(n_species >= 1 && n_species <= 8, "fsc_ictd_conv1_forward: 1..8 species supported");
+  FSC_CHECK_ARG(n_species >= 1 && n_species <= 16, "fsc_ictd_conv1_forward: 1..16 species supported");
   FSC_CHECK_ARG(dst_ptr && node_species && qtab && out, "fsc_ictd_conv1_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && F && gates), "fsc_ictd_conv1_forward: null edge pointer");
   FSC_CHECK_ARG(layout->NY == 9 || layout->NY == 16, "fsc_ictd_conv1_forward: lmax must be 2 or 3");
@@ -1022,7 +1045,7 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
   if (check_layout(layout, channels, "fsc_ictd_conv1_backward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv1_backward: bad size");
-  FSC_CHECK_ARG(n_species >= 1 && n_species <= 8, "fsc_ictd_conv1_backward: 1..8 species supported");
+  FSC_CHECK_ARG(n_species >= 1 && n_species <= 16, "fsc_ictd_conv1_backward: 1..16 species supported");
   FSC_CHECK_ARG(dst_ptr && node_species && grad_out && qtab, "fsc_ictd_conv1_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && F && gates && grad_F && grad_gates),
                 "fsc_ictd_conv1_backward: null edge pointer");

@@ -882,8 +882,9 @@ __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float
 }
 
 // Q[e][p*C + c] = sum_k h[e][k] mb[pair][p][c][k] + mf[pair][p][64][c] for 16-edge tiles of one species
-// pair.  pair_tiles = [16*n_tiles padded edge ids (-1: none) | n_tiles pair ids]; a tile's first entry is
-// always an edge, and the tiles of a pair are consecutive.  Transposed product: table rows (p, c) are the
+// pair.  pair_tiles = [16*n_tiles padded edge ids (-1: none) | n_tiles pair ids]; a used tile's first entry
+// is an edge, the tiles of a pair are consecutive, and unused tiles (first entry -1) come last and are
+// skipped.  Transposed product: table rows (p, c) are the
 // A operand and the tile's h rows the B operand, so lane (r, q) ends with four consecutive (p, c) columns
 // of edge r.  A wave takes C1_TPW consecutive tiles: when they share a pair (all but a few waves per
 // pair) each table row block is loaded once for all of them (the table is 48 KB per pair at C 64, which
@@ -900,19 +901,22 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
-  if (t0 >= n_tiles) return;   // whole wave
+  if (t0 >= n_tiles || pair_tiles[16 * (int64_t)t0] < 0) return;   // whole wave (unused tiles are at the end)
   const int nt = min(C1_TPW, n_tiles - t0);
   const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
   int32_t e[C1_TPW];
+  bool used[C1_TPW];
   f4 hb[C1_TPW][4];
   bool same = true;
 #pragma unroll
   for (int u = 0; u < C1_TPW; ++u) {
     const int t = t0 + min(u, nt - 1);
+    const int32_t first = pair_tiles[16 * t];
+    used[u] = u < nt && first >= 0;
     same = same && tpair[t] == tpair[t0];
     const int32_t eu = pair_tiles[16 * t + r];
-    e[u] = (u < nt) ? eu : -1;   // tiles past n_tiles repeat the last one and are not stored
-    const int32_t eld = (eu >= 0) ? eu : pair_tiles[16 * t];
+    e[u] = used[u] ? eu : -1;   // tiles past n_tiles repeat the last one, unused tiles are skipped
+    const int32_t eld = (eu >= 0) ? eu : (first >= 0 ? first : pair_tiles[16 * t0]);
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4) hb[u][t4] = ld4(h + (int64_t)eld * KH + 16 * t4 + 4 * q);
   }
@@ -941,7 +945,7 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   } else {
 #pragma unroll
     for (int u = 0; u < C1_TPW; ++u)
-      if (u < nt) tile_rows(tpair[t0 + u], u, u + 1);
+      if (used[u]) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
 
@@ -1042,19 +1046,22 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
-  if (t0 >= n_tiles) return;   // whole wave
+  if (t0 >= n_tiles || pair_tiles[16 * (int64_t)t0] < 0) return;   // whole wave (unused tiles are at the end)
   const int nt = min(C1_TPW, n_tiles - t0);
   const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
   int32_t e[C1_TPW];
+  bool used[C1_TPW];
   const float* dq[C1_TPW];
   bool same = true;
 #pragma unroll
   for (int u = 0; u < C1_TPW; ++u) {
     const int t = t0 + min(u, nt - 1);
+    const int32_t first = pair_tiles[16 * t];
+    used[u] = u < nt && first >= 0;
     same = same && tpair[t] == tpair[t0];
     const int32_t eu = pair_tiles[16 * t + r];
-    e[u] = (u < nt) ? eu : -1;   // tiles past n_tiles repeat the last one and are not stored
-    const int32_t eld = (eu >= 0) ? eu : pair_tiles[16 * t];
+    e[u] = used[u] ? eu : -1;   // tiles past n_tiles repeat the last one, unused tiles are skipped
+    const int32_t eld = (eu >= 0) ? eu : (first >= 0 ? first : pair_tiles[16 * t0]);
     dq[u] = dQ + (int64_t)eld * 3 * C + 4 * q;
   }
   auto tile_rows = [&](int pair, int u0, int u1) {   // tiles u0..u1-1 against the table of `pair`
@@ -1090,7 +1097,7 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
   } else {
 #pragma unroll
     for (int u = 0; u < C1_TPW; ++u)
-      if (u < nt) tile_rows(tpair[t0 + u], u, u + 1);
+      if (used[u]) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
 

@@ -62,6 +62,12 @@ const FscIctdLayout* layout_of(const Tensor& layout) {
 
 // ============================================================== sparse (pure-cartesian-sparse)
 
+// 1 / max(E/N, 1e-8): the conv2..n normalisation (models/pure_cartesian_sparse_layers.py:419-420), taken from
+// the tensor sizes at run time so that a traced graph stays valid for every system size.
+float avg_degree_inv(int64_t N, int64_t E) {
+  return (float)(1.0 / std::max((double)E / (double)std::max<int64_t>(N, 1), 1e-8));
+}
+
 std::tuple<Tensor, Tensor> sparse_prepare_weights(const Tensor& w_last, const Tensor& b_last, int64_t channels) {
   require_gpu({w_last, b_last});
   const int64_t C = channels;
@@ -82,7 +88,7 @@ std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, con
 std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,
                                                const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                const Tensor& src_ptr, const Tensor& src_perm,
-                                               const Tensor& edge_dst, double inv_norm) {
+                                               const Tensor& edge_dst) {
   require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst});
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == 13, "x must be (N, 13, C)");
   const int64_t N = x_.size(0), C = x_.size(2), E = h_.size(0);
@@ -92,14 +98,14 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
   Tensor S = at::empty({s_f}, fopts(x)), P = at::empty({p_f}, fopts(x)), out = at::empty({N, 13, C}, fopts(x));
   check(fsc_sparse_conv_forward(N, E, (int32_t)C, ci(dp), ci(sp), ci(pm), cf(x), cf(h), cf(n), cf(bk1),
-                                (float)inv_norm, mf(S), mf(P), mf(out), stream_of(x)),
+                                avg_degree_inv(N, E), mf(S), mf(P), mf(out), stream_of(x)),
         "fsc_sparse_conv_forward");
   return {out, S, P};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tensor& h, const Tensor&, const Tensor&,
                                                     const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                    const Tensor&, double) {
+                                                    const Tensor&) {
   const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
   int64_t s_f = 0, p_f = 0;
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
@@ -109,8 +115,7 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tenso
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_, const Tensor& n_,
                                                         const Tensor& bk6, const Tensor& S, const Tensor& P,
                                                         const Tensor& dst_ptr, const Tensor& src_ptr,
-                                                        const Tensor& src_perm, const Tensor& edge_dst,
-                                                        double inv_norm) {
+                                                        const Tensor& src_perm, const Tensor& edge_dst) {
   require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
   Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_);
@@ -118,7 +123,7 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
          dn = at::empty({E, 3}, fopts(g));
   check(fsc_sparse_conv_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(src_ptr, "src_ptr")),
                                  ci(i32c(src_perm, "src_perm")), ci(i32c(edge_dst, "edge_dst")), cf(g), cf(h), cf(n),
-                                 cf(bk6), cf(S), cf(P), (float)inv_norm, mf(dS), mf(dx), mf(dh), mf(dn),
+                                 cf(bk6), cf(S), cf(P), avg_degree_inv(N, E), mf(dS), mf(dx), mf(dh), mf(dn),
                                  stream_of(g)),
         "fsc_sparse_conv_backward");
   return {dx, dh, dn};
@@ -126,7 +131,7 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h, const Tensor&,
                                                              const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                             const Tensor&, const Tensor&, const Tensor&, double) {
+                                                             const Tensor&, const Tensor&, const Tensor&) {
   const int64_t E = h.size(0);
   return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h))};
 }
@@ -151,10 +156,9 @@ std::tuple<Tensor, Tensor> sparse_conv1_pair_table_meta(const Tensor& w_last, co
 }
 
 std::tuple<Tensor, Tensor> sparse_conv1(const Tensor& h_, const Tensor& n_, const Tensor& mf_, const Tensor& mb,
-                                        const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t n_nodes,
-                                        int64_t channels) {
+                                        const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t channels) {
   require_gpu({h_, n_, mf_, mb, dst_ptr, pair_tiles});
-  const int64_t E = h_.size(0), C = channels;
+  const int64_t E = h_.size(0), C = channels, n_nodes = dst_ptr.numel() - 1;
   TORCH_CHECK(pair_tiles.numel() % 17 == 0, "pair_tiles must hold 17 int32 per 16-edge tile");
   Tensor h = f32c(h_), n = f32c(n_);
   Tensor Q = at::empty({E * 3 * C}, fopts(h)), out = at::empty({n_nodes, 13, C}, fopts(h));
@@ -166,8 +170,8 @@ std::tuple<Tensor, Tensor> sparse_conv1(const Tensor& h_, const Tensor& n_, cons
 }
 
 std::tuple<Tensor, Tensor> sparse_conv1_meta(const Tensor& h, const Tensor&, const Tensor&, const Tensor&,
-                                             const Tensor&, const Tensor&, int64_t n_nodes, int64_t C) {
-  return {at::empty({n_nodes, 13, C}, fopts(h)), at::empty({h.size(0) * 3 * C}, fopts(h))};
+                                             const Tensor& dst_ptr, const Tensor&, int64_t C) {
+  return {at::empty({dst_ptr.numel() - 1, 13, C}, fopts(h)), at::empty({h.size(0) * 3 * C}, fopts(h))};
 }
 
 std::tuple<Tensor, Tensor> sparse_conv1_backward(const Tensor& grad_out, const Tensor& n_, const Tensor& mf_,
@@ -256,10 +260,11 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward_meta(const Tensor&, const 
 }
 
 Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, const Tensor& dst_ptr,
-                  const Tensor& edge_pair, const Tensor& node_species, int64_t n_nodes, int64_t n_species,
-                  int64_t n_comps, const Tensor& layout) {
+                  const Tensor& edge_pair, const Tensor& node_species, int64_t n_species, int64_t n_comps,
+                  const Tensor& layout) {
   require_gpu({F_, gates_, qtab_, dst_ptr, edge_pair, node_species});
   const FscIctdLayout* L = layout_of(layout);
+  const int64_t n_nodes = dst_ptr.numel() - 1;
   TORCH_CHECK(n_comps == L->M, "n_comps does not match the layout");
   const int64_t C = qtab_.size(-1), E = F_.size(0);
   Tensor F = f32c(F_), gates = f32c(gates_), qtab = f32c(qtab_);
@@ -271,9 +276,9 @@ Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, c
   return out;
 }
 
-Tensor ictd_conv1_meta(const Tensor& F, const Tensor&, const Tensor& qtab, const Tensor&, const Tensor&, const Tensor&,
-                       int64_t n_nodes, int64_t, int64_t n_comps, const Tensor&) {
-  return at::empty({n_nodes, n_comps, qtab.size(-1)}, fopts(F));
+Tensor ictd_conv1_meta(const Tensor& F, const Tensor&, const Tensor& qtab, const Tensor& dst_ptr, const Tensor&,
+                       const Tensor&, int64_t, int64_t n_comps, const Tensor&) {
+  return at::empty({dst_ptr.numel() - 1, n_comps, qtab.size(-1)}, fopts(F));
 }
 
 std::tuple<Tensor, Tensor> ictd_conv1_backward(const Tensor& grad_out, const Tensor& F_, const Tensor& gates_,
@@ -497,6 +502,87 @@ std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::Tens
   return {at::empty({N, gram_width(Wf[0], nC)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
 }
 
+
+// ============================================================== graph preparation
+
+Tensor i64c(const Tensor& t) { return t.to(at::kLong).contiguous(); }
+
+// The receiver sort and index structures of one neighbour list (fsc_graph_prepare), rebuilt per call as the
+// reference re-sorts per call; every output size follows from (N, E, n_species), so traces stay valid.
+std::vector<Tensor> graph_prepare(const Tensor& edge_src_, const Tensor& edge_dst_, const Tensor& species_,
+                                  int64_t n_species) {
+  require_gpu({edge_src_, edge_dst_, species_});
+  TORCH_CHECK(edge_src_.dim() == 1 && edge_dst_.dim() == 1 && edge_src_.numel() == edge_dst_.numel() &&
+                  species_.dim() == 1,
+              "graph_prepare: edge_src, edge_dst (E,) and species (N,)");
+  const int64_t E = edge_src_.numel(), N = species_.numel();
+  int64_t T = 0, ws_n = 0;
+  check(fsc_graph_sizes(N, E, (int32_t)n_species, &T, &ws_n), "fsc_graph_sizes");
+  Tensor src = i64c(edge_src_), dst = i64c(edge_dst_), sp = i64c(species_);
+  const auto io = src.options().dtype(at::kInt);
+  Tensor order = at::empty({E}, io), src32 = at::empty({E}, io), dst32 = at::empty({E}, io);
+  Tensor dst_ptr = at::empty({N + 1}, io), src_ptr = at::empty({N + 1}, io), src_perm = at::empty({E}, io);
+  Tensor node_species = at::empty({n_species > 0 ? N : 0}, io), edge_pair = at::empty({n_species > 0 ? E : 0}, io);
+  Tensor pair_tiles = at::empty({17 * T}, io), status = at::empty({1}, io), ws = at::empty({ws_n}, io);
+  auto ip = [](Tensor& t) { return t.numel() ? t.data_ptr<int32_t>() : nullptr; };
+  check(fsc_graph_prepare(N, E, (int32_t)n_species, E ? src.data_ptr<int64_t>() : nullptr,
+                          E ? dst.data_ptr<int64_t>() : nullptr, N ? sp.data_ptr<int64_t>() : nullptr, ip(order),
+                          ip(src32), ip(dst32), ip(dst_ptr), ip(src_ptr), ip(src_perm), ip(node_species), ip(edge_pair),
+                          ip(pair_tiles), ip(status), ip(ws), stream_of(src)),
+        "fsc_graph_prepare");
+  return {order, src32, dst32, dst_ptr, src_ptr, src_perm, node_species, edge_pair, pair_tiles, status};
+}
+
+std::vector<Tensor> graph_prepare_meta(const Tensor& edge_src, const Tensor&, const Tensor& species,
+                                       int64_t n_species) {
+  const int64_t E = edge_src.numel(), N = species.numel();
+  int64_t T = 0, ws_n = 0;
+  check(fsc_graph_sizes(N, E, (int32_t)n_species, &T, &ws_n), "fsc_graph_sizes");
+  const auto io = edge_src.options().dtype(at::kInt);
+  return {at::empty({E}, io), at::empty({E}, io), at::empty({E}, io), at::empty({N + 1}, io), at::empty({N + 1}, io),
+          at::empty({E}, io), at::empty({n_species > 0 ? N : 0}, io), at::empty({n_species > 0 ? E : 0}, io),
+          at::empty({17 * T}, io), at::empty({1}, io)};
+}
+
+// ============================================================== geometry from caller-supplied edge vectors
+
+std::tuple<Tensor, Tensor> edge_vec_geometry(const Tensor& edge_vec_, const Tensor& order) {
+  require_gpu({edge_vec_, order});
+  const int64_t E = order.numel();
+  TORCH_CHECK(edge_vec_.dim() == 2 && edge_vec_.size(0) == E && edge_vec_.size(1) == 3, "edge_vec must be (E, 3)");
+  Tensor v = f32c(edge_vec_);
+  Tensor n = at::empty({E, 3}, fopts(v)), r = at::empty({E}, fopts(v));
+  check(fsc_edge_vec_geometry_forward(E, cf(v), ci(i32c(order, "order")), mf(n), mf(r), stream_of(v)),
+        "fsc_edge_vec_geometry_forward");
+  return {n, r};
+}
+
+std::tuple<Tensor, Tensor> edge_vec_geometry_meta(const Tensor& edge_vec, const Tensor& order) {
+  const int64_t E = order.numel();
+  return {at::empty({E, 3}, fopts(edge_vec)), at::empty({E}, fopts(edge_vec))};
+}
+
+Tensor edge_vec_geometry_backward(const std::optional<Tensor>& grad_n, const std::optional<Tensor>& grad_r,
+                                  const Tensor& n_, const Tensor& r_, const Tensor& order) {
+  const bool has_n = grad_n.has_value() && grad_n->defined(), has_r = grad_r.has_value() && grad_r->defined();
+  require_gpu({n_, r_, order});
+  if (has_n) require_gpu({*grad_n});
+  if (has_r) require_gpu({*grad_r});
+  const int64_t E = r_.numel();
+  Tensor n = f32c(n_), r = f32c(r_);
+  Tensor gn = has_n ? f32c(*grad_n) : Tensor(), gr = has_r ? f32c(*grad_r) : Tensor();
+  Tensor gvec = at::empty({E, 3}, fopts(n));
+  check(fsc_edge_vec_geometry_backward(E, gn.defined() ? cf(gn) : nullptr, gr.defined() ? cf(gr) : nullptr, cf(n),
+                                       cf(r), ci(i32c(order, "order")), mf(gvec), stream_of(n)),
+        "fsc_edge_vec_geometry_backward");
+  return gvec;
+}
+
+Tensor edge_vec_geometry_backward_meta(const std::optional<Tensor>&, const std::optional<Tensor>&, const Tensor& n,
+                                       const Tensor&, const Tensor&) {
+  return at::empty({n.size(0), 3}, fopts(n));
+}
+
 // ============================================================== autograd
 
 // ============================================================== edge geometry and radial MLP
@@ -651,29 +737,27 @@ void refuse_param_grad(AutogradContext* ctx, std::initializer_list<int> idx, con
 
 struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
-                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, double inv_norm) {
+                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&,
                                                                   const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&, const Tensor&, const Tensor&, double)>(
+                                                                  const Tensor&, const Tensor&, const Tensor&)>(
         "fsctep::sparse_conv");
-    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm);
+    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst);
     ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
-    ctx->saved_data["inv_norm"] = inv_norm;
     ctx->mark_non_differentiable({S, P});
     ctx->set_materialize_grads(false);   // S and P are saved workspaces: no zero-filled gradients for them
     return {out, S, P};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(10);
+    variable_list res(9);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {3, 4}, "the sparse conv");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::sparse_conv_backward");
-    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8],
-                                ctx->saved_data["inv_norm"].toDouble());
+        const Tensor&, const Tensor&, const Tensor&)>("fsctep::sparse_conv_backward");
+    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8]);
     res[0] = dx;
     res[1] = dh;
     res[2] = dn;
@@ -684,26 +768,26 @@ struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const Tensor& h, const Tensor& n,
                                                         const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                         const Tensor& src_ptr, const Tensor& src_perm,
-                                                        const Tensor& edge_dst, double inv_norm) {
-  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm);
+                                                        const Tensor& edge_dst) {
+  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst);
   return {r[0], r[1], r[2]};
 }
 
 struct SparseConv1Fn : public torch::autograd::Function<SparseConv1Fn> {
   static variable_list forward(AutogradContext* ctx, Tensor h, Tensor n, Tensor mf_, Tensor mb, Tensor dst_ptr,
-                               Tensor pair_tiles, int64_t n_nodes, int64_t channels) {
+                               Tensor pair_tiles, int64_t channels) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                          const Tensor&, const Tensor&, int64_t, int64_t)>(
+                                                          const Tensor&, const Tensor&, int64_t)>(
         "fsctep::sparse_conv1");
-    auto [out, Q] = op.call(h, n, mf_, mb, dst_ptr, pair_tiles, n_nodes, channels);
+    auto [out, Q] = op.call(h, n, mf_, mb, dst_ptr, pair_tiles, channels);
     ctx->save_for_backward({n, mf_, Q, dst_ptr, pair_tiles});
     ctx->mark_non_differentiable({Q});
     ctx->set_materialize_grads(false);
     return {out, Q};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(8);
+    variable_list res(7);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {2, 3}, "the sparse conv1");
     auto s = ctx->get_saved_variables();
@@ -717,9 +801,8 @@ struct SparseConv1Fn : public torch::autograd::Function<SparseConv1Fn> {
 };
 
 std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& n, const Tensor& mf_, const Tensor& mb,
-                                                 const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t n_nodes,
-                                                 int64_t channels) {
-  auto r = SparseConv1Fn::apply(h, n, mf_, mb, dst_ptr, pair_tiles, n_nodes, channels);
+                                                 const Tensor& dst_ptr, const Tensor& pair_tiles, int64_t channels) {
+  auto r = SparseConv1Fn::apply(h, n, mf_, mb, dst_ptr, pair_tiles, channels);
   return {r[0], r[1]};
 }
 
@@ -758,18 +841,18 @@ Tensor ictd_conv_autograd(const Tensor& x, const Tensor& Y, const Tensor& gates,
 
 struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
   static variable_list forward(AutogradContext* ctx, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr,
-                               Tensor edge_pair, Tensor node_species, int64_t n_nodes, int64_t n_species,
-                               int64_t n_comps, Tensor layout) {
+                               Tensor edge_pair, Tensor node_species, int64_t n_species, int64_t n_comps,
+                               Tensor layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, int64_t, int64_t, int64_t, const Tensor&)>("fsctep::ictd_conv1");
-    Tensor out = op.call(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout);
+                                      const Tensor&, int64_t, int64_t, const Tensor&)>("fsctep::ictd_conv1");
+    Tensor out = op.call(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout);
     ctx->save_for_backward({F, gates, qtab, dst_ptr, edge_pair, node_species, layout});
     ctx->saved_data["n_species"] = n_species;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(10);
+    variable_list res(9);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {2}, "the ICTD conv1");
     auto s = ctx->get_saved_variables();
@@ -784,9 +867,9 @@ struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
 };
 
 Tensor ictd_conv1_autograd(const Tensor& F, const Tensor& gates, const Tensor& qtab, const Tensor& dst_ptr,
-                           const Tensor& edge_pair, const Tensor& node_species, int64_t n_nodes, int64_t n_species,
-                           int64_t n_comps, const Tensor& layout) {
-  return IctdConv1Fn::apply(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout)[0];
+                           const Tensor& edge_pair, const Tensor& node_species, int64_t n_species, int64_t n_comps,
+                           const Tensor& layout) {
+  return IctdConv1Fn::apply(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout)[0];
 }
 
 struct GramFn : public torch::autograd::Function<GramFn> {
@@ -922,6 +1005,34 @@ std::tuple<Tensor, Tensor> edge_geometry_autograd(const Tensor& pos, const Tenso
   return {r[0], r[1]};
 }
 
+
+struct EdgeVecGeometryFn : public torch::autograd::Function<EdgeVecGeometryFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor edge_vec, Tensor order) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&)>("fsctep::edge_vec_geometry");
+    auto [n, r] = op.call(edge_vec, order);
+    ctx->save_for_backward({n, r, order});
+    ctx->set_materialize_grads(false);
+    return {n, r};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(2);
+    if (!grads[0].defined() && !grads[1].defined()) return res;
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<Tensor(const std::optional<Tensor>&, const std::optional<Tensor>&, const Tensor&,
+                                      const Tensor&, const Tensor&)>("fsctep::edge_vec_geometry_backward");
+    const std::optional<Tensor> gn = grads[0].defined() ? std::optional<Tensor>(grads[0]) : std::nullopt;
+    const std::optional<Tensor> gr = grads[1].defined() ? std::optional<Tensor>(grads[1]) : std::nullopt;
+    res[0] = op.call(gn, gr, s[0], s[1], s[2]);
+    return res;
+  }
+};
+
+std::tuple<Tensor, Tensor> edge_vec_geometry_autograd(const Tensor& edge_vec, const Tensor& order) {
+  auto r = EdgeVecGeometryFn::apply(edge_vec, order);
+  return {r[0], r[1]};
+}
+
 struct RadialMlpFn : public torch::autograd::Function<RadialMlpFn> {
   static variable_list forward(AutogradContext* ctx, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2,
                                std::optional<Tensor> w4, std::optional<Tensor> b4, double r_cut, int64_t basis) {
@@ -992,11 +1103,11 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 TORCH_LIBRARY(fsctep, m) {
   m.def("sparse_prepare_weights(Tensor w_last, Tensor b_last, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv(Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6, Tensor dst_ptr, Tensor src_ptr, "
-        "Tensor src_perm, Tensor edge_dst, float inv_norm) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_perm, Tensor edge_dst) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
-        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, float inv_norm) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
-  m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, int n_nodes, "
+  m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, "
         "int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv1_backward(Tensor grad_out, Tensor n, Tensor mf, Tensor Q, Tensor dst_ptr, Tensor pair_tiles) "
         "-> (Tensor, Tensor)");
@@ -1006,7 +1117,7 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
         "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) -> (Tensor, Tensor, Tensor)");
   m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
-        "int n_nodes, int n_species, int n_comps, Tensor layout) -> Tensor");
+        "int n_species, int n_comps, Tensor layout) -> Tensor");
   m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "
         "Tensor edge_pair, Tensor node_species, int n_species, Tensor layout) -> (Tensor, Tensor)");
   m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
@@ -1026,6 +1137,9 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("readout_scatter(Tensor?[] grad_t, Tensor? grad_sq, Tensor[] layers, Tensor gmap, Tensor table) -> Tensor[]");
   m.def("readout_features(Tensor[] layers, Tensor[] Wf, Tensor[] Wb, float[] scales, Tensor srcmap, Tensor gmap, "
         "Tensor table) -> (Tensor, Tensor)");
+  m.def("graph_prepare(Tensor edge_src, Tensor edge_dst, Tensor species, int n_species) -> Tensor[]");
+  m.def("edge_vec_geometry(Tensor edge_vec, Tensor order) -> (Tensor, Tensor)");
+  m.def("edge_vec_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor order) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -1052,6 +1166,9 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("readout_gather", readout_gather);
   m.impl("readout_scatter", readout_scatter);
   m.impl("readout_features", readout_features);
+  m.impl("graph_prepare", graph_prepare);
+  m.impl("edge_vec_geometry", edge_vec_geometry);
+  m.impl("edge_vec_geometry_backward", edge_vec_geometry_backward);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -1078,6 +1195,9 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("readout_gather", readout_gather_meta);
   m.impl("readout_scatter", readout_scatter_meta);
   m.impl("readout_features", readout_features_meta);
+  m.impl("graph_prepare", graph_prepare_meta);
+  m.impl("edge_vec_geometry", edge_vec_geometry_meta);
+  m.impl("edge_vec_geometry_backward", edge_vec_geometry_backward_meta);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
@@ -1090,6 +1210,7 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
   m.impl("radial_mlp", radial_mlp_autograd);
   m.impl("edge_harmonics", edge_harmonics_autograd);
   m.impl("readout_features", readout_features_autograd);
+  m.impl("edge_vec_geometry", edge_vec_geometry_autograd);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
@@ -1098,6 +1219,7 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
-                           "readout_gather", "readout_scatter", "readout_features"})
+                           "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
+                           "edge_vec_geometry", "edge_vec_geometry_backward"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -1,8 +1,11 @@
-"""Receiver-sorted graph structures consumed by the kernels.
+"""Receiver-sorted graph structures consumed by the kernels, built on the device.
 
-Built once per neighbour list (as in MD between list rebuilds) from the reference's
-edge arrays (``edge_src``, ``edge_dst``, ``edge_shifts``; ``models/pure_cartesian_sparse_layers.py:745-748``
-sorts them by receiver on every call, here the sort is hoisted out of the step).
+``prepare_graph`` runs ``torch.ops.fsctep.graph_prepare`` (``fsc_graph_prepare``): the stable receiver
+sort of the reference's edge arrays (``edge_src``, ``edge_dst``, ``edge_shifts``), the receiver CSR, the
+source grouping, and the species-pair ids and tiles.  The reference sorts on every call
+(``models/pure_cartesian_sparse_layers.py:745-748``, ``models/pure_cartesian_ictd_layers_full.py:896-899``);
+the trunks' ``forward`` does the same through this function.  Nothing here synchronises the host and
+every tensor's size follows from (N, E, n_species), so the preparation can sit inside a traced graph.
 """
 
 from __future__ import annotations
@@ -11,76 +14,65 @@ from dataclasses import dataclass
 
 import torch
 
+from . import _lib
+
+_lib.load_torch_ops()
+
 
 @dataclass
 class Graph:
-    n_nodes: int
-    n_edges: int
-    src: torch.Tensor          # (E,) int64, receiver-sorted
-    dst: torch.Tensor          # (E,) int64, non-decreasing
-    shifts: torch.Tensor       # (E, 3) float, receiver-sorted
+    order: torch.Tensor        # (E,) int32: receiver-sorted position -> input edge id
+    src32: torch.Tensor        # (E,) int32 source of each receiver-sorted edge
+    dst32: torch.Tensor        # (E,) int32 receiver, non-decreasing
     dst_ptr: torch.Tensor      # (N+1,) int32 receiver CSR
     src_ptr: torch.Tensor      # (N+1,) int32 source CSR over src_perm
-    src_perm: torch.Tensor     # (E,) int32 receiver-sorted ids grouped by source (stable)
-    dst32: torch.Tensor        # (E,) int32
-    src32: torch.Tensor        # (E,) int32
-    in_degree: torch.Tensor    # (N,) int64
-    species_index: torch.Tensor | None = None   # (N,) int64 index into `species`
-    species: torch.Tensor | None = None         # (S,) int64 distinct atomic numbers (sorted)
-    edge_pair: torch.Tensor | None = None       # (E,) int32 species-pair index src*S+dst
-    pair_tiles: torch.Tensor | None = None      # (17*T,) int32: edge ids by pair in 16-tiles | tile pairs
-    species_index32: torch.Tensor | None = None # (N,) int32
+    src_perm: torch.Tensor     # (E,) int32 receiver-sorted ids grouped by source (ascending within a source)
+    shifts: torch.Tensor       # (E, 3) float, receiver-sorted
+    node_species: torch.Tensor  # (N,) int32 species-table row of each node (empty without species)
+    edge_pair: torch.Tensor    # (E,) int32 species pair node_species[src]*n_species + node_species[dst]
+    pair_tiles: torch.Tensor   # (17*T,) int32: edge ids by pair in 16-tiles | tile pairs (unused tiles last)
+    status: torch.Tensor       # (1,) int32: nonzero if an edge or species id was out of range
+    n_species: int = 0
+
+    @property
+    def n_nodes(self) -> int:
+        return int(self.dst_ptr.shape[0]) - 1
+
+    @property
+    def n_edges(self) -> int:
+        return int(self.src32.shape[0])
+
+    @property
+    def src(self) -> torch.Tensor:
+        return self.src32.long()
+
+    @property
+    def dst(self) -> torch.Tensor:
+        return self.dst32.long()
 
 
 def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: torch.Tensor,
-                  n_nodes: int, species: torch.Tensor | None = None) -> Graph:
-    """Sort by receiver (stable) and build the CSR / source-grouped permutations."""
-    dev = edge_dst.device
-    E = int(edge_dst.shape[0])
-    if E >= 2 ** 31 or n_nodes >= 2 ** 31:
-        raise ValueError("graph exceeds int32 indexing")
-    order = torch.argsort(edge_dst, stable=True)
-    src = edge_src[order].long().contiguous()
-    dst = edge_dst[order].long().contiguous()
-    shifts = edge_shifts[order].contiguous()
-    deg = torch.bincount(dst, minlength=n_nodes) if E else torch.zeros(n_nodes, dtype=torch.long, device=dev)
-    dst_ptr = torch.zeros(n_nodes + 1, dtype=torch.int64, device=dev)
-    dst_ptr[1:] = torch.cumsum(deg, 0)
-    src_perm = torch.argsort(src, stable=True) if E else torch.zeros(0, dtype=torch.long, device=dev)
-    odeg = torch.bincount(src, minlength=n_nodes) if E else torch.zeros(n_nodes, dtype=torch.long, device=dev)
-    src_ptr = torch.zeros(n_nodes + 1, dtype=torch.int64, device=dev)
-    src_ptr[1:] = torch.cumsum(odeg, 0)
-    g = Graph(n_nodes=n_nodes, n_edges=E, src=src, dst=dst, shifts=shifts,
-              dst_ptr=dst_ptr.to(torch.int32), src_ptr=src_ptr.to(torch.int32),
-              src_perm=src_perm.to(torch.int32).contiguous(), dst32=dst.to(torch.int32),
-              src32=src.to(torch.int32), in_degree=deg)
-    if species is not None:
-        uniq, inv = torch.unique(species.long(), sorted=True, return_inverse=True)
-        g.species = uniq
-        g.species_index = inv
-        g.species_index32 = inv.to(torch.int32).contiguous()
-        S = int(uniq.shape[0])
-        g.edge_pair = (inv[src] * S + inv[dst]).to(torch.int32).contiguous()
-        g.pair_tiles = pair_tiles(g.edge_pair, S * S)
-    return g
+                  n_nodes: int | None = None, species: torch.Tensor | None = None, n_species: int = 0) -> Graph:
+    """Stable receiver sort and index structures of one neighbour list.
+
+    ``species`` (N,) holds the atomic numbers used as rows of the model's species table of
+    ``n_species`` rows (<= 16); without species pass ``n_nodes`` (the pair structures stay empty)."""
+    if species is None:
+        if n_nodes is None:
+            raise ValueError("prepare_graph needs species or n_nodes")
+        species = torch.zeros(int(n_nodes), dtype=torch.long, device=edge_dst.device)
+        n_species = 0
+    elif n_nodes is not None and int(n_nodes) != species.shape[0]:
+        raise ValueError(f"n_nodes {n_nodes} != len(species) {species.shape[0]}")
+    (order, src32, dst32, dst_ptr, src_ptr, src_perm, node_species, edge_pair, pair_tiles,
+     status) = torch.ops.fsctep.graph_prepare(edge_src, edge_dst, species, int(n_species))
+    shifts = edge_shifts.index_select(0, order)
+    return Graph(order=order, src32=src32, dst32=dst32, dst_ptr=dst_ptr, src_ptr=src_ptr, src_perm=src_perm,
+                 shifts=shifts, node_species=node_species, edge_pair=edge_pair, pair_tiles=pair_tiles,
+                 status=status, n_species=int(n_species))
 
 
-def pair_tiles(edge_pair: torch.Tensor, n_pairs: int) -> torch.Tensor:
-    """Edge ids grouped by species pair, each group padded with -1 to a multiple of 16, followed by
-    the pair of each 16-entry tile: [16*T ids | T pairs] (int32).  The sparse conv1 runs one small
-    GEMM per tile with that pair's table."""
-    dev = edge_pair.device
-    E = int(edge_pair.shape[0])
-    pair = edge_pair.long()
-    counts = torch.bincount(pair, minlength=n_pairs) if E else torch.zeros(n_pairs, dtype=torch.long, device=dev)
-    tiles_per = (counts + 15) // 16
-    T = int(tiles_per.sum())
-    tile_start = torch.cumsum(tiles_per, 0) - tiles_per            # first tile of each pair
-    order = torch.argsort(pair, stable=True) if E else torch.zeros(0, dtype=torch.long, device=dev)
-    sorted_pair = pair[order]
-    first = torch.cumsum(counts, 0) - counts                        # first sorted position of each pair
-    pos = tile_start[sorted_pair] * 16 + (torch.arange(E, device=dev) - first[sorted_pair])
-    ids = torch.full((16 * T,), -1, dtype=torch.int32, device=dev)
-    ids[pos] = order.to(torch.int32)
-    tpair = torch.repeat_interleave(torch.arange(n_pairs, device=dev), tiles_per).to(torch.int32)
-    return torch.cat([ids, tpair]).contiguous()
+def poison_invalid(e: torch.Tensor, graph: Graph) -> torch.Tensor:
+    """NaN energies when the graph preparation found an out-of-range edge or species id (the ids were
+    clamped to keep every access in bounds), without a host synchronisation."""
+    return e + torch.where(graph.status != 0, float("nan"), 0.0).to(e.dtype)

@@ -21,8 +21,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ictd_ops
-from .readout_ops import GramWeights, ReadoutMaps, readout_features
-from .graph import Graph, prepare_graph
+from .readout_ops import ReadoutMaps, prepare_gram, readout_features
+from .graph import Graph, poison_invalid, prepare_graph
 from .ictd_basis import canonical, coupling, layout_full, layout_o3
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
 
@@ -90,6 +90,9 @@ class _ICTDTrunk(nn.Module):
             raise ValueError(f"num_interaction must be >= 2, got {self.num_interaction}")
         if self.channels not in (32, 64, 128) or output_size != 8:
             raise NotImplementedError("HIP ICTD path: hidden_dim_conv 32/64/128 and output_size 8")
+        if not 1 <= max_atomvalue <= 16:
+            raise NotImplementedError("HIP ICTD path: max_atomvalue (species table rows) 1..16")
+        self.n_species = int(max_atomvalue)
         self.invariant_channels = int(invariant_channels)
         self.max_radius = float(max_embed_radius)
         self.number_of_basis = int(main_number_of_basis)
@@ -127,7 +130,6 @@ class _ICTDTrunk(nn.Module):
             self.physical_tensor_heads = nn.ModuleDict(
                 {"dipole": nn.ModuleDict({"1": nn.Linear(nC, 1, bias=False)})})
             self._dipole = True
-        self._gram_w = [GramWeights() for _ in self.keys]
         self._cache = {}
 
     def _make_layout(self, preset, active, phys):
@@ -143,22 +145,16 @@ class _ICTDTrunk(nn.Module):
             self._cache[key] = (cg, torch.tensor(c1, device=device), factors)
         return self._cache[key]
 
-    def _wt(self, tp):
-        w = tp.weight
-        key = ("wt", id(tp), w.data_ptr(), w._version)
-        if key not in self._cache:
-            for k in [k for k in self._cache if k[0] == "wt" and k[1] == id(tp)]:
-                del self._cache[k]
-            with torch.no_grad():
-                self._cache[key] = torch.ops.fsctep.ictd_prepare_weights(w.detach())
-        return self._cache[key]
+    @staticmethod
+    def _wt(tp):
+        """Channel-mix operand of tp.weight from its current values (no cache: see prepare_gram)."""
+        with torch.no_grad():
+            return torch.ops.fsctep.ictd_prepare_weights(tp.weight.detach())
 
     # ------------------------------------------------------------------ forward
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
-        g = prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A)
-        if g.species.shape[0] > 8:
-            raise NotImplementedError("HIP ICTD conv1: at most 8 distinct species per system")
-        return g
+        """The receiver-sorted graph of one neighbour list (device op, no host synchronisation)."""
+        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species)
 
     def _check_inference(self):
         if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
@@ -168,35 +164,43 @@ class _ICTDTrunk(nn.Module):
     def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
                 sync_after_scatter=None, external_tensor=None, external_tensor_blocks=None, fidelity_ids=None,
                 return_physical_tensors=False, return_reciprocal_source=False):
+        """Reference signature (full :867-884, o3 :902-920).  The graph is prepared on every call, as the
+        reference sorts on every call.  With ``precomputed_edge_vec`` (E, 3) (caller edge order) the
+        geometry comes from it and forces flow back through it, as the reference's branch at full
+        :901-902 / o3 :928-929 (the LAMMPS / ML-IAP cores differentiate through edge_vec)."""
         if sync_after_scatter is not None or external_tensor_blocks is not None or fidelity_ids is not None:
             raise NotImplementedError("sync hooks, external blocks and fidelity ids are outside the HIP path")
-        key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (edge_src, edge_dst, edge_shifts, A))
-        if self._cache.get("graph_key") != key:
-            self._cache["graph"] = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
-            self._cache["graph_key"] = key
-        e, dip = self.forward_graph(pos, batch, cell, self._cache["graph"], external_tensor=external_tensor)
+        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+        e, dip = self.forward_graph(pos, batch, cell, g, external_tensor=external_tensor,
+                                    edge_vec=precomputed_edge_vec)
         if return_physical_tensors:
             return e, {"dipole": {1: dip}} if dip is not None else {}
         return e
 
-    def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None):
-        """((N,1) atomic energies, (G,1,3) dipole or None) for a prepared graph."""
+    def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None, edge_vec=None):
+        """((N,1) atomic energies, (G,1,3) dipole or None) for a prepared graph; ``edge_vec`` (E, 3), in the
+        caller's edge order, replaces the geometry from ``pos`` (differentiable w.r.t. it)."""
         self._check_inference()
         if not pos.is_cuda:
             raise RuntimeError("the HIP ICTD path runs on the GPU only")
         f32 = torch.float32
         pos, cell = pos.to(f32), cell.to(f32)
         cg, c1_gates, factors = self._consts(pos.device)
-        with torch.no_grad():
-            shift_vec = (g.shifts.to(f32).unsqueeze(-1) * cell[batch[g.src]]).sum(1)
-        n, r = ictd_ops.edge_geometry(pos, shift_vec, g)
+        src_batch = batch.index_select(0, g.src32)
+        if edge_vec is not None:
+            n, r = ictd_ops.edge_vec_geometry(edge_vec.to(f32), g)
+        else:
+            with torch.no_grad():
+                shift_vec = (g.shifts.to(f32).unsqueeze(-1) * cell.index_select(0, src_batch)).sum(1)
+            n, r = ictd_ops.edge_geometry(pos, shift_vec, g)
         Y = ictd_ops.edge_harmonics(n, self.lmax)
 
         c1 = self.e3_conv_emb
-        atab = c1.atom_mlp(c1.atom_embedding(g.species)).detach()
-        W1 = c1.tp2.weight.detach()[c1_gates]                                  # (NP1, C, 8, 8)
-        NS = atab.shape[0]
-        qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
+        NS = self.n_species
+        with torch.no_grad():   # species-table rows (atomic numbers 0..max_atomvalue-1)
+            atab = c1.atom_mlp(c1.atom_embedding(torch.arange(NS, device=pos.device))).detach()
+            W1 = c1.tp2.weight.detach()[c1_gates]                                  # (NP1, C, 8, 8)
+            qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
         F_in = Y
         if self.external_field:
             if external_tensor is None:
@@ -207,7 +211,7 @@ class _ICTDTrunk(nn.Module):
             else:
                 s = c1.external_tensor_scale_by_l[1]
             add = torch.zeros_like(Y)
-            add[:, 1:4] = fld[batch[g.src]] * s.detach()
+            add[:, 1:4] = fld.index_select(0, src_batch) * s.detach()
             F_in = Y + add
         elif external_tensor is not None:
             raise ValueError("external_tensor given but the model has no external field")
@@ -215,7 +219,8 @@ class _ICTDTrunk(nn.Module):
         for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
             feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, self._gates(fc2, r), tp.weight.detach(),
                                                   self._wt(tp), cg, g, self.layout_id))
-        return self.readout(feats, batch, factors)
+        e, dip = self.readout(feats, batch, factors)
+        return poison_invalid(e, g), dip
 
     def _gates(self, fc, r):
         """Per-path gates fc(radial_basis(r)) (E, P) by one fused kernel (P <= 64)."""
@@ -231,12 +236,12 @@ class _ICTDTrunk(nn.Module):
         """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included: the
         Gram inputs (the reference's channel-major flatten, layer concatenation and re-split by key)
         and the per-key squared norms of the layer concatenation come from one fused readout op."""
-        N, nL = feats[0].shape[0], len(feats)
+        nL = len(feats)
         key = ("maps", nL)
         if key not in self._cache:
             self._cache[key] = ReadoutMaps(nL, self.channels, [2 * k[0] + 1 for k in self.keys], resplit=True)
         maps = self._cache[key]
-        grams = [self._gram_w[i].get(self._wread(i, k)) for i, k in enumerate(self.keys)]
+        grams = [prepare_gram(self._wread(i, k)) for i, k in enumerate(self.keys)]
         scales = [1.0 / math.sqrt(2 * k[0] + 1) for k in self.keys]
         scalars, sq_all = readout_features(feats, grams, scales, maps)
         outs = []
@@ -253,7 +258,7 @@ class _ICTDTrunk(nn.Module):
             nC = nL * self.channels
             col0 = sum(d * nC for d in maps.key_dims[:i])
             idx = maps.on(feats[0].device)[0][col0:col0 + 3 * nC].long()
-            t = torch.cat([f.reshape(N, -1) for f in feats], dim=1).index_select(1, idx).view(N, 3, nC)
+            t = torch.cat([f.flatten(1) for f in feats], dim=1).index_select(1, idx).view(-1, 3, nC)
             W = self.physical_tensor_heads["dipole"]["1"].weight
             y = torch.matmul(t, W.t().contiguous()).transpose(1, 2)          # (N, o, 3) = einsum("ncm,oc->nom")
             G = int(batch.max()) + 1 if batch.numel() else 0

@@ -7,7 +7,7 @@ tensor holding the struct.  The ops are registered in C++ by ``libfsctep_torch.s
     ictd_prepare_weights(W) -> Wt   (split-fp16 channel-mix weights, opaque)
     ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout) -> out
     ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout)
-    ictd_conv1(F, gates, qtab, dst_ptr, edge_pair, node_species, n_nodes, n_species, n_comps, layout)
+    ictd_conv1(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout)
     ictd_conv1_backward(grad_out, F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, layout)
 """
 
@@ -21,7 +21,7 @@ from torch import Tensor
 
 from . import _lib
 from .ictd_basis import Layout
-from .ops import edge_geometry, radial_full, radial_hidden  # noqa: F401  (shared edge geometry / radial MLP ops)
+from .ops import edge_geometry, edge_vec_geometry, radial_full, radial_hidden  # noqa: F401  (shared geometry / radial ops)
 
 _lib.load_torch_ops()
 
@@ -160,6 +160,5 @@ def ictd_conv_apply(x, Y, gates, W, Wt, cg, graph, layout_id: int):
 
 def ictd_conv1_apply(F, gates, qtab, graph, layout_id: int):
     """Differentiable conv1: F (E,NY) harmonics (+ field), gates (E,NREF), qtab (NS*NS,NP1,C) -> (N,M,C)."""
-    return torch.ops.fsctep.ictd_conv1(F, gates, qtab, graph.dst_ptr, graph.edge_pair, graph.species_index32,
-                                       graph.n_nodes, int(graph.species.shape[0]), layout_struct(layout_id).M,
-                                       layout_tensor(layout_id))
+    return torch.ops.fsctep.ictd_conv1(F, gates, qtab, graph.dst_ptr, graph.edge_pair, graph.node_species,
+                                       int(graph.n_species), layout_struct(layout_id).M, layout_tensor(layout_id))

@@ -7,13 +7,19 @@ There is no CPU implementation: calling an op with CPU tensors raises.  Paramete
 produced (the path serves energy + forces).
 
     sparse_prepare_weights(w_last, b_last, channels) -> (bk1, bk6)
-    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm) -> (out, S, P)
-    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, inv_norm)
+    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst) -> (out, S, P)
+    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst)
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
-    sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, n_nodes, channels) -> (out, Q)
+    sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
+    graph_prepare(edge_src, edge_dst, species, n_species) -> [order, src32, dst32, dst_ptr, src_ptr,
+                                                              src_perm, node_species, edge_pair, pair_tiles, status]
     edge_geometry(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm) -> (n, r)
+    edge_vec_geometry(edge_vec, order) -> (n, r)
     radial_mlp(r, w0, b0, w2, b2, w4?, b4?, r_cut, basis) -> h (E,64) or the fused last Linear (E,P)
+
+Sizes are read from the tensors inside the ops (the conv2..n normalisation 1/max(E/N, 1e-8) included),
+so a traced graph holds no size constants.
 """
 
 from __future__ import annotations
@@ -25,17 +31,16 @@ _lib.load_torch_ops()
 import torch  # noqa: E402
 
 
-def sparse_conv_apply(x, h, n, bk1, bk6, graph, inv_norm: float):
-    """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C)."""
+def sparse_conv_apply(x, h, n, bk1, bk6, graph):
+    """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C), normalised by 1/max(E/N, 1e-8)."""
     out, _, _ = torch.ops.fsctep.sparse_conv(x, h, n, bk1, bk6, graph.dst_ptr, graph.src_ptr,
-                                             graph.src_perm, graph.dst32, float(inv_norm))
+                                             graph.src_perm, graph.dst32)
     return out
 
 
 def sparse_conv1_apply(h, n, mf, mb, graph, channels: int):
     """Differentiable conv1 message passing from the species-pair tables: -> (N,13,C)."""
-    out, _ = torch.ops.fsctep.sparse_conv1(h, n, mf, mb, graph.dst_ptr, graph.pair_tiles, graph.n_nodes,
-                                           int(channels))
+    out, _ = torch.ops.fsctep.sparse_conv1(h, n, mf, mb, graph.dst_ptr, graph.pair_tiles, int(channels))
     return out
 
 
@@ -47,6 +52,12 @@ def edge_geometry(pos, shift_vec, graph):
     ``shift_vec`` = edge_shifts @ cell (no gradient)."""
     return torch.ops.fsctep.edge_geometry(pos, shift_vec.detach(), graph.src32, graph.dst32, graph.dst_ptr,
                                           graph.src_ptr, graph.src_perm)
+
+
+def edge_vec_geometry(edge_vec, graph):
+    """Differentiable (w.r.t. ``edge_vec``, given in the caller's edge order) unit vectors n (E,3) and
+    lengths r (E,) of the receiver-sorted edges."""
+    return torch.ops.fsctep.edge_vec_geometry(edge_vec, graph.order)
 
 
 def radial_hidden(r, fc, r_cut: float, basis: str):

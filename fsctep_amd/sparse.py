@@ -24,8 +24,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .readout_ops import GramWeights, ReadoutMaps, readout_features
-from .graph import Graph, prepare_graph
+from .readout_ops import ReadoutMaps, prepare_gram, readout_features
+from .graph import Graph, poison_invalid, prepare_graph
 
 _COMPS = ((0, 1), (1, 4), (4, 13))   # component ranges of ranks 0, 1, 2
 
@@ -111,17 +111,13 @@ class PureCartesianSparseE3Conv2(nn.Module):
         self.Lmax = Lmax
         self.function_type = function_type
         self.fc = _radial_mlp(6 * channels_out * channels_in, number_of_basis)
-        self._prep_key = None
-        self._prep = None
 
     def prepared_weights(self):
-        w, b = self.fc[4].weight, self.fc[4].bias
-        key = (w.data_ptr(), w._version, b.data_ptr(), b._version, w.device)
-        if self._prep_key != key:
-            with torch.no_grad():
-                self._prep = torch.ops.fsctep.sparse_prepare_weights(w.detach(), b.detach(), self.channels_out)
-            self._prep_key = key
-        return self._prep
+        """The kernel operands (bk1, bk6) of fc.4, made from the current parameter values on every call
+        (no cache: an in-place update through ``.data`` does not change a parameter's version)."""
+        with torch.no_grad():
+            return torch.ops.fsctep.sparse_prepare_weights(self.fc[4].weight.detach(), self.fc[4].bias.detach(),
+                                                           self.channels_out)
 
 
 class PureCartesianSparseInvariantBilinear(nn.Module):
@@ -134,14 +130,13 @@ class PureCartesianSparseInvariantBilinear(nn.Module):
         self.Lmax = Lmax
         self.W = nn.ParameterList([nn.Parameter(torch.randn(out_channels, channels, channels) * 0.02)
                                    for _ in range(Lmax + 1)])
-        self._prepared = [GramWeights() for _ in range(Lmax + 1)]
 
     def forward(self, blocks):
         """blocks[L]: (N, 3^L, channels) -> (N, out_channels), by the fused Gram-bilinear kernel."""
         total = 0
         for L, t in enumerate(blocks):
             scale = 1.0 / math.sqrt(3 ** L) if L > 0 else 1.0
-            Wf, Wb = self._prepared[L].get(self.W[L])
+            Wf, Wb = prepare_gram(self.W[L])
             total = total + torch.ops.fsctep.gram_bilinear(t, Wf, Wb, scale)
         return total
 
@@ -170,6 +165,8 @@ class PureCartesianSparseTransformerLayer(nn.Module):
             raise TypeError(f"unexpected argument {k!r}")
         if output_size != 8:
             raise NotImplementedError("HIP sparse conv1 needs output_size 8")
+        if not 1 <= max_atomvalue <= 16:
+            raise NotImplementedError("HIP sparse path: max_atomvalue (species table rows) 1..16")
         if hidden_dim_conv not in (32, 64):
             raise NotImplementedError("HIP sparse path: hidden_dim_conv 32 or 64")
         if num_interaction < 2:
@@ -200,28 +197,24 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         self.number_of_basis = main_number_of_basis
         self._readout_cache = {}
         self.function_type = function_type_main
-        self._graph_key = None
-        self._graph = None
+        self.n_species = int(max_atomvalue)
 
     # ------------------------------------------------------------------ graph handling
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
-        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A)
-
-    def _cached_graph(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
-        key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (edge_src, edge_dst, edge_shifts, A))
-        key = key + (num_nodes, edge_dst.device)
-        if self._graph_key != key:
-            self._graph = self.prepare(edge_src, edge_dst, edge_shifts, num_nodes, A)
-            self._graph_key = key
-        return self._graph
+        """The receiver-sorted graph of one neighbour list (device op, no host synchronisation).  Reusing
+        it across calls with unchanged edges is the caller's choice (``forward_graph``)."""
+        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species)
 
     # ------------------------------------------------------------------ forward
     def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
                 external_tensor=None, fidelity_ids=None, return_physical_tensors=False,
                 return_reciprocal_source=False, **_unused):
+        """Reference signature (pure_cartesian_sparse_layers.py:723-735).  The graph is prepared on every
+        call, as the reference sorts on every call; ``precomputed_edge_vec`` is ignored, as in the
+        reference's sparse trunk (geometry from ``pos``, ``edge_shifts`` and ``cell``)."""
         if external_tensor is not None or fidelity_ids is not None or return_physical_tensors:
             raise NotImplementedError("external tensors / fidelity / physical tensors are outside the HIP path")
-        g = self._cached_graph(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
         e = self.forward_graph(pos, batch, cell, g)
         if return_reciprocal_source:
             return e, e.new_empty((e.shape[0], 0))
@@ -241,44 +234,45 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         dtype = torch.float32
         pos = pos.to(dtype)
         cell = cell.to(dtype)
-        N = pos.shape[0]
         with torch.no_grad():
-            shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * cell[batch[g.src]]).sum(1)   # elementwise: no batched GEMM
+            edge_cell = cell.index_select(0, batch.index_select(0, g.src32))
+            shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * edge_cell).sum(1)   # elementwise: no batched GEMM
         n, r = ops.edge_geometry(pos, shift_vec, g)
 
         conv1 = self.e3_conv_layers[0]
-        atab = conv1.atom_table(g.species).to(dtype)
-        mf, mb = torch.ops.fsctep.sparse_conv1_pair_table(conv1.fc[4].weight.detach(),
-                                                          conv1.fc[4].bias.detach(), atab.detach(),
-                                                          self.channels)
+        # species-table rows (atomic numbers 0..max_atomvalue-1), as atom_mlp(atom_embedding(A)) per atom
+        with torch.no_grad():
+            rows = torch.arange(self.n_species, device=pos.device)
+            atab = conv1.atom_table(rows).to(dtype)
+            mf, mb = torch.ops.fsctep.sparse_conv1_pair_table(conv1.fc[4].weight.detach(),
+                                                              conv1.fc[4].bias.detach(), atab, self.channels)
         h1 = ops.radial_hidden(r, conv1.fc, self.max_radius, self.function_type)
         feats = [ops.sparse_conv1_apply(h1, n, mf, mb, g, self.channels)]
-        inv_norm = 1.0 / max(g.n_edges / max(N, 1), 1e-8)
         for conv in self.e3_conv_layers[1:]:
             bk1, bk6 = conv.prepared_weights()
             h = ops.radial_hidden(r, conv.fc, self.max_radius, self.function_type)
-            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, inv_norm))
-        return self.readout(feats)
+            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g))
+        return poison_invalid(self.readout(feats), g)
 
     def readout(self, feats):
         """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features: the rank-L blocks of all
         layers (t_L = cat_l x_l[:, block L, :]) feed product_3 and their squared norms
         sum_m x^2 / 3^{L/2} the invariants, all assembled by one fused readout op."""
-        N, nL = feats[0].shape[0], len(feats)
+        nL = len(feats)
         key = ("maps", nL)
         if key not in self._readout_cache:
             self._readout_cache[key] = ReadoutMaps(nL, self.channels, [b - a for (a, b) in _COMPS], resplit=False)
         maps = self._readout_cache[key]
         p3 = self.product_3
         scales = [1.0 / math.sqrt(3 ** L) for L in range(len(_COMPS))]
-        grams = [p3._prepared[L].get(p3.W[L]) for L in range(len(_COMPS))]
+        grams = [prepare_gram(p3.W[L]) for L in range(len(_COMPS))]
         f3, sq = readout_features(feats, grams, scales, maps)
         skey = ("scales", str(sq.device))
         if skey not in self._readout_cache:
             self._readout_cache[skey] = torch.tensor(scales, dtype=sq.dtype, device=sq.device).view(1, -1, 1, 1)
         # invariants in the reference order: layer-major, then rank L
-        invs = (sq.view(N, len(_COMPS), nL, self.channels) * self._readout_cache[skey]).transpose(1, 2)
-        f5 = torch.cat([invs.reshape(N, -1), f3 * f3], dim=-1)
+        invs = (sq.view(-1, len(_COMPS), nL, self.channels) * self._readout_cache[skey]).transpose(1, 2)
+        f5 = torch.cat([invs.flatten(1), f3 * f3], dim=-1)
         return self.weighted_sum(self.proj_total(f5))
 
 

@@ -38,6 +38,34 @@ int fsc_abi_version(void);
 int fsc_timing_begin(const char* kernel_name);
 int fsc_timing_end(double* total_ms, int64_t* launches);
 
+/* ------------------------------------------------------------------ graph preparation
+ * Replaces the per-call receiver sort of the trunks, `sort_idx = argsort(edge_dst)` and the permutation
+ * of edge_src / edge_dst / edge_shifts (models/pure_cartesian_sparse_layers.py:745-748,
+ * models/pure_cartesian_ictd_layers_full.py:896-899, models/pure_cartesian_ictd_layers_o3.py:924-927), plus
+ * the index structures the kernels read.  The order is the stable one (ties keep the input order), so
+ * results are deterministic; the reference's unstable argsort differs only in the summation order.
+ * Every output size depends on (n_nodes, n_edges, n_species) only and nothing synchronises the host.
+ *
+ * fsc_graph_sizes: n_tiles_max = ceil(E/16) + n_species^2 (0 without species) and the int32 workspace. */
+int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t* n_tiles_max,
+                    int64_t* workspace_ints);
+
+/* Inputs: edge_src, edge_dst [E] int64 node ids; species [N] int64 atomic numbers (< n_species, the
+ * size of the model's species table, <= 16; null with n_species 0).  Outputs (int32):
+ * order [E] (receiver-sorted position -> input edge id), src32 / dst32 [E] (the permuted ids),
+ * dst_ptr [N+1] (receiver CSR), src_ptr [N+1] + src_perm [E] (receiver-sorted ids grouped by source,
+ * ascending within a source), node_species [N], edge_pair [E] = species[src]*n_species + species[dst],
+ * pair_tiles [17*n_tiles_max] (the receiver-sorted ids grouped by species pair, each pair padded with -1
+ * to a multiple of 16, then one pair id per tile; unused trailing tiles are all -1 with pair 0), and
+ * status [1]: bit 0 set if an edge id is outside [0, N), bit 1 if a species is outside [0, n_species);
+ * such ids are clamped (every access stays in bounds) and the results are meaningless.
+ * workspace: fsc_graph_sizes' workspace_ints. */
+int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                      const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
+                      int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
+                      int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
+                      int32_t* workspace, hipStream_t stream);
+
 /* ------------------------------------------------------------------ pure-cartesian-sparse
  * conv2..n.  Replaces, per interaction layer, the chain
  *   weights = fc(emb) ; tp(f_in[edge_src], e_flat, weights) ; scatter(., edge_dst) / (E/N)
@@ -95,7 +123,8 @@ int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const 
 
 /* out[N][13][C] = (1/max(indeg,1)) sum_{e->n} message_e; q_ws: [E][3][C] kept for backward.
  * pair_tiles: [16*n_tiles edge ids | n_tiles pair ids], the receiver-sorted edge ids grouped by
- * species pair, each pair's list padded with -1 to a multiple of 16 (fsctep_amd/graph.py). */
+ * species pair, each pair's list padded with -1 to a multiple of 16 (fsc_graph_prepare); tiles whose
+ * first id is -1 are skipped. */
 int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
                              int64_t n_tiles, const int32_t* pair_tiles, const float* h, const float* n,
                              const float* mf, const float* mb, float* q_ws, float* out, hipStream_t stream);
@@ -118,6 +147,16 @@ int fsc_edge_geometry_forward(int64_t n_edges, const float* pos, const float* sh
 int fsc_edge_geometry_backward(int64_t n_nodes, int64_t n_edges, const float* grad_n, const float* grad_r,
                                const float* n, const float* r, const int32_t* dst_ptr, const int32_t* src_ptr,
                                const int32_t* src_perm, float* grad_pos, hipStream_t stream);
+
+/* The same geometry from caller-supplied edge vectors, the `precomputed_edge_vec` branch of the ICTD trunks
+ * (models/pure_cartesian_ictd_layers_full.py:901-902, models/pure_cartesian_ictd_layers_o3.py:928-929)
+ * that the LAMMPS / ML-IAP cores differentiate through (interfaces/lammps_mliap.py:404).  edge_vec [E][3]
+ * is in the caller's edge order and read through `order` (fsc_graph_prepare); n_out, r_out are
+ * receiver-sorted.  The backward writes grad_vec [E][3] in the caller's order. */
+int fsc_edge_vec_geometry_forward(int64_t n_edges, const float* edge_vec, const int32_t* order, float* n_out,
+                                  float* r_out, hipStream_t stream);
+int fsc_edge_vec_geometry_backward(int64_t n_edges, const float* grad_n, const float* grad_r, const float* n,
+                                   const float* r, const int32_t* order, float* grad_vec, hipStream_t stream);
 
 /* Radial basis + a radial MLP (fc = Linear(nb,64), SiLU, Linear(64,64), SiLU, Linear(64,P);
  * models/pure_cartesian_sparse_layers.py:204-210,319-321,372-378,410-412,
@@ -195,7 +234,7 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
  * pure_cartesian_ictd_layers_o3.py:424-532): both operands depend only on the species, and
  * C(l,0,l) is the identity, so out[n][comp(l)][o] = (1/indeg) sum_e gate[e][p_l] Q[pair][p_l][o] F[e][l^2+k]
  * with Q[pair][p][o] = sum_ij W1[p][o][i][j] A_src[i] A_dst[j] (qtab [NS*NS][NP1][C], pair = s_src*NS +
- * s_dst, n_species = NS <= 8; node_species [N] gives s_dst) and F = Y plus the embedded external field on
+ * s_dst, n_species = NS <= 16, the rows of the species table; node_species [N] gives s_dst) and F = Y plus the embedded external field on
  * the l=1 block. */
 int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                            int32_t n_species, const int32_t* dst_ptr, const int32_t* edge_pair,

@@ -69,7 +69,7 @@ def test_fake_kernels_trace_shapes():
         bk = torch.empty(6 * 65 * 64 * 64 + 512)
         i = torch.empty(11, dtype=torch.int32)
         e = torch.empty(30, dtype=torch.int32)
-        out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, 0.5)
+        out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e)
         assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10,) and P.shape == (30 * 18 * 64,)
 
 

@@ -56,7 +56,7 @@ def test_conv2_op_matches_oracle(C):
     xd = x.float().to(DEV).requires_grad_(True)
     hd = h_s.float().to(DEV).requires_grad_(True)
     nd = n_s.float().to(DEV).requires_grad_(True)
-    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr, inv_norm)
+    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr)
     dx, dh, dn = torch.autograd.grad(out, (xd, hd, nd), G.float().to(DEV))
     torch.cuda.synchronize()
     assert rel_inf(out, ref) < TOL
@@ -111,7 +111,7 @@ def test_conv2_op_wide_dynamic_range():
     xd = xf.float().to(DEV).requires_grad_(True)
     hd = hf.float().to(DEV).requires_grad_(True)
     nd = nf.float().to(DEV).requires_grad_(True)
-    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr, inv_norm)
+    out = ops.sparse_conv_apply(xd, hd, nd, bk1, bk6, gr)
     dx, dh, dn = torch.autograd.grad(out, (xd, hd, nd), G.float().to(DEV))
     torch.cuda.synchronize()
     assert _rowwise_rel(out, ref) < TOL      # per receiver

@@ -17,7 +17,8 @@ OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_
        "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv", "ictd_conv_backward", "ictd_conv1",
        "ictd_conv1_backward", "gram_prepare_weights", "gram_bilinear", "gram_bilinear_backward", "edge_geometry",
        "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
-       "readout_gather", "readout_scatter", "readout_features"]
+       "readout_gather", "readout_scatter", "readout_features", "graph_prepare", "edge_vec_geometry",
+       "edge_vec_geometry_backward"]
 
 
 class GramProbe(torch.nn.Module):
@@ -34,7 +35,8 @@ def test_schemas_registered_in_cpp():
         # registered by the C++ library, not by Python
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "CUDA")
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "Meta")
-    for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear", "readout_features"):
+    for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear", "readout_features",
+                 "edge_geometry", "edge_vec_geometry", "radial_mlp", "edge_harmonics"):
         assert torch._C._dispatch_has_computed_kernel_for_dispatch_key(f"fsctep::{name}", "AutogradCUDA")
 
 
@@ -55,7 +57,7 @@ def test_ictd_layout_tensor_round_trips():
         x = torch.empty(10, s.M, 128)
         out = torch.ops.fsctep.ictd_conv1(torch.empty(40, s.NY), torch.empty(40, s.NREF), torch.empty(64, s.NP1, 128),
                                           torch.empty(11, dtype=torch.int32), torch.empty(40, dtype=torch.int32),
-                                          torch.empty(10, dtype=torch.int32), 10, 8, s.M, t)
+                                          torch.empty(10, dtype=torch.int32), 8, s.M, t)
         assert out.shape == x.shape
 
 
@@ -79,4 +81,4 @@ def test_python_free_process_loads_ops_and_runs_scripted_module(tmp_path):
     env = {k: v for k, v in os.environ.items() if not k.startswith("PYTHON")}
     run = subprocess.run([str(exe), _lib.TORCH_LIB_PATH, str(pt)], capture_output=True, text=True, timeout=300, env=env)
     assert run.returncode == 0, run.stdout + run.stderr
-    assert "fsctep ops registered: 23; scripted module -> [7, 64]" in run.stdout
+    assert f"fsctep ops registered: {len(OPS)}; scripted module -> [7, 64]" in run.stdout
