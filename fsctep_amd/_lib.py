@@ -47,6 +47,7 @@ SIGNATURES = {
     "fsc_radial_mlp_backward": [_i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p],
     "fsc_graph_sizes": [_i64, _i64, _i32, _pi64, _pi64],
     "fsc_graph_prepare": [_i64, _i64, _i32] + [_p] * 15,
+    "fsc_graph_prepare_noalloc": [_i64, _i64, _i32] + [_p] * 14,
     "fsc_edge_vec_geometry_forward": [_i64, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_backward": [_i64, _p, _p, _p, _p, _p, _p, _p],
 }

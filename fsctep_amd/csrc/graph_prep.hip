@@ -11,6 +11,16 @@
 #include "common.h"
 #include "fsctep.h"
 
+#include <mutex>
+#include <string>
+
+namespace fsc {
+constexpr int64_t kScratchInts = int64_t(1) << 23;
+}
+// Static workspace of fsc_graph_prepare_noalloc: 2^23 int32 (32 MiB) on every GPU the library runs on,
+// held from the first load of this code object on that device until the process ends.
+static __device__ __align__(256) int32_t scratch[fsc::kScratchInts];
+
 namespace fsc {
 namespace {
 
@@ -194,13 +204,41 @@ __global__ __launch_bounds__(256) void rank_src_kernel(int64_t E, const int32_t*
   src_perm[a + rank] = p;
 }
 
-// Species-pair tiles: per-pair counts, then one block lays the pairs' tiles out back to back (each pair's
-// edge list padded to a multiple of 16), then the edges are placed.  The order of edges inside a pair's
-// tiles does not affect any result (each tile row is one edge's own product), so it is left unordered.
-__global__ __launch_bounds__(256) void pair_count_kernel(int64_t E, const int32_t* __restrict__ edge_pair,
-                                                         int32_t* __restrict__ pcnt) {
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p < E) atomicAdd(pcnt + edge_pair[p], 1);
+// Species-pair tiles: the receiver-sorted positions grouped by pair, ascending within a pair (a stable
+// counting sort by pair, so the layout is deterministic).  Positions are cut into chunks of PAIR_CHUNK;
+// per-chunk pair counts are scanned over the chunks for every pair, one block lays the pairs' tiles out
+// back to back (each pair's list padded to a multiple of 16), and one wave per chunk places its positions.
+constexpr int PAIR_CHUNK = 2048;
+
+// cnt_blk[pr * nchunk + b] = number of positions of chunk b with pair pr (LDS counters).
+__global__ __launch_bounds__(256) void pair_chunk_count_kernel(int64_t E, int32_t P, int nchunk,
+                                                               const int32_t* __restrict__ edge_pair,
+                                                               int32_t* __restrict__ cnt_blk) {
+  __shared__ int32_t h[256];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * PAIR_CHUNK;
+  for (int j = threadIdx.x; j < PAIR_CHUNK; j += 256)
+    if (base + j < E) atomicAdd(&h[edge_pair[base + j]], 1);
+  __syncthreads();
+  if ((int)threadIdx.x < P) cnt_blk[(int64_t)threadIdx.x * nchunk + blockIdx.x] = h[threadIdx.x];
+}
+
+// One block per pair: exclusive scan of its chunk counts in place; the pair's total into pcnt.
+__global__ __launch_bounds__(256) void pair_chunk_scan_kernel(int nchunk, int32_t* __restrict__ cnt_blk,
+                                                              int32_t* __restrict__ pcnt) {
+  __shared__ int32_t lds[4];
+  int32_t* row = cnt_blk + (int64_t)blockIdx.x * nchunk;
+  int32_t carry = 0;
+  for (int base = 0; base < nchunk; base += 256) {   // uniform trip count over the block
+    const int i = base + (int)threadIdx.x;
+    const int32_t v = i < nchunk ? row[i] : 0;
+    int32_t total;
+    const int32_t ex = block_exclusive_scan(v, lds, total);
+    if (i < nchunk) row[i] = carry + ex;
+    carry += total;
+  }
+  if (threadIdx.x == 0) pcnt[blockIdx.x] = carry;
 }
 
 __global__ __launch_bounds__(256) void pair_layout_kernel(int32_t P, const int32_t* __restrict__ pcnt,
@@ -232,19 +270,44 @@ __global__ __launch_bounds__(256) void pair_layout_kernel(int32_t P, const int32
   }
 }
 
-__global__ __launch_bounds__(256) void pair_place_kernel(int64_t E, const int32_t* __restrict__ edge_pair,
-                                                         const int32_t* __restrict__ tstart,
-                                                         int32_t* __restrict__ cursor, int32_t* __restrict__ ids) {
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p >= E) return;
-  const int32_t pr = edge_pair[p];
-  ids[(int64_t)tstart[pr] * 16 + atomicAdd(cursor + pr, 1)] = (int32_t)p;
+// One wave per chunk, 64 positions at a time in order.  A position's slot = its pair's first slot + the
+// chunk's offset within the pair + the pair's count earlier in the chunk (run) + its rank among the lanes
+// holding the same pair (lanes matched by ballots over the 8 bits of the pair id).
+__global__ __launch_bounds__(64) void pair_chunk_place_kernel(int64_t E, int nchunk,
+                                                              const int32_t* __restrict__ edge_pair,
+                                                              const int32_t* __restrict__ tstart,
+                                                              const int32_t* __restrict__ cnt_blk,
+                                                              int32_t* __restrict__ ids) {
+  __shared__ int32_t run[256];
+  const int lane = threadIdx.x;
+  for (int k = lane; k < 256; k += 64) run[k] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * PAIR_CHUNK;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int j = 0; j < PAIR_CHUNK && base + j < E; j += 64) {   // uniform over the wave
+    const int64_t p = base + j + lane;
+    const bool valid = p < E;
+    const int pr = valid ? edge_pair[p] : 0;
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool b = (pr >> bit) & 1;
+      const uint64_t bb = __ballot(b);
+      same &= b ? bb : ~bb;
+    }
+    if (valid)
+      ids[(int64_t)tstart[pr] * 16 + cnt_blk[(int64_t)pr * nchunk + blockIdx.x] + run[pr] + __popcll(same & below)] =
+          (int32_t)p;
+    __syncthreads();                                             // every lane has read run[] for this step
+    if (valid && (same >> lane) == 1ull) run[pr] += __popcll(same);   // the pair's highest lane
+    __syncthreads();
+  }
 }
 
 unsigned grid_of(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 struct WsLayout {
-  int64_t cnt_in, cnt_out, cur_in, cur_out, tot, pcnt, pcur, tstart, tmp, total;
+  int64_t cnt_in, cnt_out, cur_in, cur_out, tot, pcnt, tstart, cnt_blk, tmp, total, nchunk;
 };
 
 WsLayout ws_layout(int64_t N, int64_t E, int32_t NS) {
@@ -252,52 +315,65 @@ WsLayout ws_layout(int64_t N, int64_t E, int32_t NS) {
   const int64_t nb = (N + 1 + SCAN_TILE - 1) / SCAN_TILE;
   const int64_t P = (int64_t)NS * NS;
   int64_t o = 0;
+  w.nchunk = NS > 0 ? (E + PAIR_CHUNK - 1) / PAIR_CHUNK : 0;
   w.cnt_in = o;  o += N;
   w.cnt_out = o; o += N;
   w.cur_in = o;  o += N;
-  w.cur_out = o; o += N;
-  w.pcnt = o;    o += P;
-  w.pcur = o;    o += P;   // the zero-filled prefix ends here
+  w.cur_out = o; o += N;   // the zero-filled prefix ends here
   w.tot = o;     o += 2 * nb;
+  w.pcnt = o;    o += P;
   w.tstart = o;  o += P;
+  w.cnt_blk = o; o += P * w.nchunk;
   w.tmp = o;     o += E;
   w.total = o;
   return w;
 }
 
-}  // namespace
-}  // namespace fsc
-
-extern "C" {
-
-int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t* n_tiles_max,
-                    int64_t* workspace_ints) {
-  FSC_CHECK_ARG(n_tiles_max && workspace_ints, "fsc_graph_sizes: null pointer");
-  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) - 1 && n_edges < (1LL << 31) - 1,
-                "fsc_graph_sizes: graph exceeds int32 indexing");
-  FSC_CHECK_ARG(n_species >= 0 && n_species <= 16, "fsc_graph_sizes: n_species must be 0..16");
-  *n_tiles_max = n_species > 0 ? (n_edges + 15) / 16 + (int64_t)n_species * n_species : 0;
-  *workspace_ints = fsc::ws_layout(n_nodes, n_edges, n_species).total;
+// The device address of `scratch` (the static workspace of fsc_graph_prepare_noalloc) on the current
+// device, resolved once per device with hipGetSymbolAddress.  In host code the array's name is a
+// stand-in, not a device address: only this pointer is ever passed to a kernel.
+int scratch_ptr(int32_t** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static int32_t* ptrs[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fsc_graph_prepare_noalloc: no current HIP device (or device id >= 64)");
+    return 1;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      set_error(std::string("fsc_graph_prepare_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                hipGetErrorString(err));
+      return 1;
+    }
+    ptrs[dev] = static_cast<int32_t*>(p);
+  }
+  *out = ptrs[dev];
   return 0;
 }
 
-int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
-                      const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
-                      int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
-                      int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
-                      int32_t* workspace, hipStream_t stream) {
-  using namespace fsc;
+}  // namespace
+
+static int prepare_impl(const char* name, int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                 const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32, int32_t* dst32,
+                 int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm, int32_t* node_species, int32_t* edge_pair,
+                 int32_t* pair_tiles, int32_t* status, int32_t* workspace, hipStream_t stream) {
+  const std::string nm(name);
   int64_t T_max = 0, ws_ints = 0;
   if (fsc_graph_sizes(n_nodes, n_edges, n_species, &T_max, &ws_ints)) return 1;
   const int64_t N = n_nodes, E = n_edges;
-  FSC_CHECK_ARG(dst_ptr && src_ptr && status && workspace, "fsc_graph_prepare: null pointer");
+  FSC_CHECK_ARG(dst_ptr && src_ptr && status, nm + ": null pointer");
   FSC_CHECK_ARG(E == 0 || (N > 0 && edge_src && edge_dst && order && src32 && dst32 && src_perm),
-                "fsc_graph_prepare: null edge pointer (or edges without nodes)");
-  FSC_CHECK_ARG(n_species == 0 || N == 0 || (species && node_species), "fsc_graph_prepare: null species pointer");
-  FSC_CHECK_ARG(n_species == 0 || E == 0 || edge_pair, "fsc_graph_prepare: null edge_pair");
-  FSC_CHECK_ARG(n_species == 0 || pair_tiles, "fsc_graph_prepare: null pair_tiles");
+                nm + ": null edge pointer (or edges without nodes)");
+  FSC_CHECK_ARG(n_species == 0 || N == 0 || (species && node_species), nm + ": null species pointer");
+  FSC_CHECK_ARG(n_species == 0 || E == 0 || edge_pair, nm + ": null edge_pair");
+  FSC_CHECK_ARG(n_species == 0 || pair_tiles, nm + ": null pair_tiles");
   const int64_t nb = (N + 1 + SCAN_TILE - 1) / SCAN_TILE;
-  FSC_CHECK_ARG(nb <= SCAN_MAX_BLOCKS, "fsc_graph_prepare: too many nodes for the scan");
+  FSC_CHECK_ARG(nb <= SCAN_MAX_BLOCKS, nm + ": too many nodes for the scan");
   const WsLayout w = ws_layout(N, E, n_species);
   const int32_t P = n_species * n_species;
   int32_t* ws = workspace;
@@ -325,11 +401,63 @@ int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const
   if (n_species > 0) {
     fill_i32_kernel<<<grid_of(16 * T_max) < 1024 ? grid_of(16 * T_max) : 1024, 256, 0, stream>>>(pair_tiles,
                                                                                                  16 * T_max, -1);
-    if (E > 0) pair_count_kernel<<<grid_of(E), 256, 0, stream>>>(E, edge_pair, ws + w.pcnt);
+    const int nchunk = (int)w.nchunk;
+    if (E > 0)
+      pair_chunk_count_kernel<<<nchunk, 256, 0, stream>>>(E, P, nchunk, edge_pair, ws + w.cnt_blk);
+    pair_chunk_scan_kernel<<<P, 256, 0, stream>>>(nchunk, ws + w.cnt_blk, ws + w.pcnt);
     pair_layout_kernel<<<1, 256, 0, stream>>>(P, ws + w.pcnt, ws + w.tstart, T_max, pair_tiles + 16 * T_max);
-    if (E > 0) pair_place_kernel<<<grid_of(E), 256, 0, stream>>>(E, edge_pair, ws + w.tstart, ws + w.pcur, pair_tiles);
+    if (E > 0)
+      pair_chunk_place_kernel<<<nchunk, 64, 0, stream>>>(E, nchunk, edge_pair, ws + w.tstart, ws + w.cnt_blk,
+                                                          pair_tiles);
   }
-  return check_launch("fsc_graph_prepare");
+  return check_launch(name) ? 2 : 0;
+}
+
+
+}  // namespace fsc
+
+extern "C" {
+
+int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t* n_tiles_max,
+                    int64_t* workspace_ints) {
+  FSC_CHECK_ARG(n_tiles_max && workspace_ints, "fsc_graph_sizes: null pointer");
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) - 1 && n_edges < (1LL << 31) - 1,
+                "fsc_graph_sizes: graph exceeds int32 indexing");
+  FSC_CHECK_ARG(n_species >= 0 && n_species <= 16, "fsc_graph_sizes: n_species must be 0..16");
+  *n_tiles_max = n_species > 0 ? (n_edges + 15) / 16 + (int64_t)n_species * n_species : 0;
+  *workspace_ints = fsc::ws_layout(n_nodes, n_edges, n_species).total;
+  return 0;
+}
+
+int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                      const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
+                      int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
+                      int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
+                      int32_t* workspace, hipStream_t stream) {
+  FSC_CHECK_ARG(workspace, "fsc_graph_prepare: null workspace");
+  return fsc::prepare_impl("fsc_graph_prepare", n_nodes, n_edges, n_species, edge_src, edge_dst, species, order, src32,
+                           dst32, dst_ptr, src_ptr, src_perm, node_species, edge_pair, pair_tiles, status, workspace,
+                           stream);
+}
+
+int fsc_graph_prepare_noalloc(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                              const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
+                              int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
+                              int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
+                              hipStream_t stream) {
+  int64_t T_max = 0, ws_ints = 0;
+  if (fsc_graph_sizes(n_nodes, n_edges, n_species, &T_max, &ws_ints)) return 1;
+  if (ws_ints > fsc::kScratchInts) {
+    fsc::set_error("fsc_graph_prepare_noalloc: the graph needs " + std::to_string(ws_ints) +
+                   " int32 of workspace, above the static scratch of " + std::to_string(fsc::kScratchInts) +
+                   " (about 4N + E + n_species^2 (2 + E/2048)); use fsc_graph_prepare with a caller workspace");
+    return 1;
+  }
+  int32_t* ws = nullptr;
+  if (fsc::scratch_ptr(&ws)) return 1;
+  return fsc::prepare_impl("fsc_graph_prepare_noalloc", n_nodes, n_edges, n_species, edge_src, edge_dst, species,
+                           order, src32, dst32, dst_ptr, src_ptr, src_perm, node_species, edge_pair, pair_tiles,
+                           status, ws, stream);
 }
 
 }  // extern "C"

@@ -55,8 +55,9 @@ int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t
  * order [E] (receiver-sorted position -> input edge id), src32 / dst32 [E] (the permuted ids),
  * dst_ptr [N+1] (receiver CSR), src_ptr [N+1] + src_perm [E] (receiver-sorted ids grouped by source,
  * ascending within a source), node_species [N], edge_pair [E] = species[src]*n_species + species[dst],
- * pair_tiles [17*n_tiles_max] (the receiver-sorted ids grouped by species pair, each pair padded with -1
- * to a multiple of 16, then one pair id per tile; unused trailing tiles are all -1 with pair 0), and
+ * pair_tiles [17*n_tiles_max] (the receiver-sorted ids grouped by species pair, ascending within a pair,
+ * each pair padded with -1 to a multiple of 16, then one pair id per tile; unused trailing tiles are
+ * all -1 with pair 0), and
  * status [1]: bit 0 set if an edge id is outside [0, N), bit 1 if a species is outside [0, n_species);
  * such ids are clamped (every access stays in bounds) and the results are meaningless.
  * workspace: fsc_graph_sizes' workspace_ints. */
@@ -65,6 +66,20 @@ int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const
                       int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
                       int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
                       int32_t* workspace, hipStream_t stream);
+
+/* fsc_graph_prepare without the workspace argument: allocates nothing.  No counterpart in the reference;
+ * it is for callers that cannot allocate (code under HIP graph capture, per-step MD loops, harnesses
+ * that forbid hipMalloc).  Its workspace is a static device array of 2^23 int32 (32 MiB) on each GPU the
+ * library runs on, held until the process ends; graphs whose fsc_graph_sizes workspace exceeds it
+ * (about 4N + E + n_species^2 (2 + E/2048) ints) are rejected with status 1.  Every call on one GPU
+ * shares that array (the counters are cleared at the start of each call), so calls that overlap on one GPU, on
+ * different streams or threads, race.  The stream must belong to the current device.  Outputs as for
+ * fsc_graph_prepare, bit for bit. */
+int fsc_graph_prepare_noalloc(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,
+                              const int64_t* edge_dst, const int64_t* species, int32_t* order, int32_t* src32,
+                              int32_t* dst32, int32_t* dst_ptr, int32_t* src_ptr, int32_t* src_perm,
+                              int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
+                              hipStream_t stream);
 
 /* ------------------------------------------------------------------ pure-cartesian-sparse
  * conv2..n.  Replaces, per interaction layer, the chain

@@ -67,6 +67,8 @@ def _check(src, dst, species, NS, g, sh):
             e = ids[k][ids[k] >= 0]
             assert (pair[e] == tp[k]).all()
             assert (ids[k][: e.shape[0]] >= 0).all()                           # padding only at the end
+        real = ids[ids >= 0]
+        np.testing.assert_array_equal(real, np.argsort(pair, kind="stable"))   # ascending within a pair
 
 
 @pytest.mark.gpu
@@ -102,8 +104,8 @@ def test_graph_sizes_without_gpu():
     t, w = ctypes.c_int64(), ctypes.c_int64()
     assert lib.fsc_graph_sizes(10000, 519338, 10, ctypes.byref(t), ctypes.byref(w)) == 0
     assert t.value == (519338 + 15) // 16 + 100
-    nb = (10000 + 1 + 2047) // 2048
-    assert w.value == 4 * 10000 + 2 * 100 + 2 * nb + 100 + 519338
+    nb, nchunk = (10000 + 1 + 2047) // 2048, (519338 + 2047) // 2048
+    assert w.value == 4 * 10000 + 2 * nb + 2 * 100 + 100 * nchunk + 519338
     assert lib.fsc_graph_sizes(10, 10, 17, ctypes.byref(t), ctypes.byref(w)) == 1
     assert b"n_species" in lib.fsc_last_error()
 
