@@ -3,6 +3,8 @@
 * ``libfsctep_hip.so``: the gfx950 HIP kernels behind the C ABI of ``include/fsctep.h``.
 * ``libfsctep_torch.so``: the ``torch.ops.fsctep.*`` registration (schemas, device, Meta and
   autograd kernels) over that C ABI; loadable by LibTorch processes without Python.
+* ``tests/cpp/core_run``: a LibTorch program with no Python that runs an exported core.pt the way the
+  LAMMPS engine does (used by the GPU tests of the TorchScript core).
 
     python -m fsctep_amd.build
 """
@@ -19,6 +21,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libfsctep_hip.so")
 TORCH_LIB = os.path.join(PKG, "libfsctep_torch.so")
+CORE_RUN_SRC = os.path.join(ROOT, "tests", "cpp", "core_run.cpp")
+CORE_RUN = os.path.join(ROOT, "tests", "cpp", "core_run")
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -57,11 +61,18 @@ def build(verbose: bool = False) -> str:
     torch_cc = [hipcc, "-std=c++17", "-O2", "-fPIC", "-c", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
                 "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"),
                 "-I", "/opt/rocm/include", *inc, os.path.join(CSRC, "torch_ops.cpp"), "-o", obj]
+    crun_tmp = CORE_RUN + ".tmp"
+    core_cc = ["g++", "-std=c++17", "-O1", "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc,
+               "-I", os.path.join(tinc, "torch", "csrc", "api", "include"), CORE_RUN_SRC, "-o", crun_tmp,
+               "-L", tlib, "-Wl,--no-as-needed", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip",
+               f"-Wl,-rpath,{tlib}", "-ldl"]
     if verbose:
-        print(" ".join(hip_cmd), "\n", " ".join(torch_cc), flush=True)
+        print(" ".join(hip_cmd), "\n", " ".join(torch_cc), "\n", " ".join(core_cc), flush=True)
     procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
-             for c in (hip_cmd, torch_cc)]
-    notes = [_check(None, procs[0], "libfsctep_hip.so"), _check(None, procs[1], "torch_ops.cpp")]
+             for c in (hip_cmd, torch_cc, core_cc)]
+    notes = [_check(None, procs[0], "libfsctep_hip.so"), _check(None, procs[1], "torch_ops.cpp"),
+             _check(None, procs[2], "tests/cpp/core_run")]
+    os.replace(crun_tmp, CORE_RUN)
     os.replace(tmp, LIB)
     ttmp = TORCH_LIB + ".tmp"
     link = [hipcc, "-shared", "-fPIC", obj, "-o", ttmp, "-L", PKG, "-lfsctep_hip", "-L", tlib, "-ltorch",

@@ -52,12 +52,17 @@ const int32_t* ci(const Tensor& t) { return t.numel() ? t.data_ptr<int32_t>() : 
 
 at::TensorOptions fopts(const Tensor& like) { return like.options().dtype(at::kFloat); }
 
-const FscIctdLayout* layout_of(const Tensor& layout) {
-  TORCH_CHECK(layout.device().is_cpu() && layout.scalar_type() == at::kInt && layout.is_contiguous() &&
-                  layout.numel() * 4 == (int64_t)sizeof(FscIctdLayout),
-              "layout must be a contiguous CPU int32 tensor holding an FscIctdLayout (",
-              sizeof(FscIctdLayout) / 4, " entries)");
-  return reinterpret_cast<const FscIctdLayout*>(layout.data_ptr<int32_t>());
+// Layout tables (FscIctdLayout, FscReadoutTable, FscHarmTable) travel as int[] arguments holding the
+// struct's 32-bit words: host values in every graph (a tensor constant would be moved to the GPU by
+// torch::jit::load(path, device), and reading it on the host would then need a synchronisation).
+template <typename S>
+S unpack_table(at::IntArrayRef words, const char* what) {
+  TORCH_CHECK((int64_t)words.size() * 4 == (int64_t)sizeof(S), what, " must be a list of ", sizeof(S) / 4,
+              " int32 words, got ", words.size());
+  S s;
+  int32_t* w = reinterpret_cast<int32_t*>(&s);
+  for (size_t i = 0; i < words.size(); ++i) w[i] = (int32_t)words[i];
+  return s;
 }
 
 // ============================================================== sparse (pure-cartesian-sparse)
@@ -211,9 +216,10 @@ Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({ictd_weigh
 
 Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
                  const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                 const Tensor& src_perm, const Tensor& layout) {
+                 const Tensor& src_perm, at::IntArrayRef layout) {
   require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
-  const FscIctdLayout* L = layout_of(layout);
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  const FscIctdLayout* L = &Lv;
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
   const int64_t N = x_.size(0), C = x_.size(2), E = Y_.size(0);
   Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
@@ -228,7 +234,7 @@ Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const
 }
 
 Tensor ictd_conv_meta(const Tensor& x, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&) {
+                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef) {
   return at::empty(x.sizes(), fopts(x));
 }
 
@@ -236,9 +242,10 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
                                                       const Tensor& gates_, const Tensor& Wt, const Tensor& cg,
                                                       const Tensor& dst_ptr, const Tensor& edge_src,
                                                       const Tensor& src_ptr, const Tensor& src_perm,
-                                                      const Tensor& layout) {
+                                                      at::IntArrayRef layout) {
   require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
-  const FscIctdLayout* L = layout_of(layout);
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  const FscIctdLayout* L = &Lv;
   const int64_t N = x_.size(0), M = x_.size(1), C = x_.size(2), E = Y_.size(0);
   Tensor g = f32c(grad_out), x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
   TORCH_CHECK(Wt.dim() == 1 && Wt.numel() == ictd_weight_floats(L->NREF, C),
@@ -255,15 +262,16 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
 std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward_meta(const Tensor&, const Tensor& x, const Tensor& Y,
                                                            const Tensor& gates, const Tensor&, const Tensor&,
                                                            const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                           const Tensor&) {
+                                                           at::IntArrayRef) {
   return {at::empty(x.sizes(), fopts(x)), at::empty(gates.sizes(), fopts(gates)), at::empty(Y.sizes(), fopts(Y))};
 }
 
 Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, const Tensor& dst_ptr,
                   const Tensor& edge_pair, const Tensor& node_species, int64_t n_species, int64_t n_comps,
-                  const Tensor& layout) {
+                  at::IntArrayRef layout) {
   require_gpu({F_, gates_, qtab_, dst_ptr, edge_pair, node_species});
-  const FscIctdLayout* L = layout_of(layout);
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  const FscIctdLayout* L = &Lv;
   const int64_t n_nodes = dst_ptr.numel() - 1;
   TORCH_CHECK(n_comps == L->M, "n_comps does not match the layout");
   const int64_t C = qtab_.size(-1), E = F_.size(0);
@@ -277,15 +285,16 @@ Tensor ictd_conv1(const Tensor& F_, const Tensor& gates_, const Tensor& qtab_, c
 }
 
 Tensor ictd_conv1_meta(const Tensor& F, const Tensor&, const Tensor& qtab, const Tensor& dst_ptr, const Tensor&,
-                       const Tensor&, int64_t, int64_t n_comps, const Tensor&) {
+                       const Tensor&, int64_t, int64_t n_comps, at::IntArrayRef) {
   return at::empty({dst_ptr.numel() - 1, n_comps, qtab.size(-1)}, fopts(F));
 }
 
 std::tuple<Tensor, Tensor> ictd_conv1_backward(const Tensor& grad_out, const Tensor& F_, const Tensor& gates_,
                                                const Tensor& qtab_, const Tensor& dst_ptr, const Tensor& edge_pair,
-                                               const Tensor& node_species, int64_t n_species, const Tensor& layout) {
+                                               const Tensor& node_species, int64_t n_species, at::IntArrayRef layout) {
   require_gpu({grad_out, F_, gates_, qtab_, dst_ptr, edge_pair, node_species});
-  const FscIctdLayout* L = layout_of(layout);
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  const FscIctdLayout* L = &Lv;
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = F_.size(0);
   Tensor g = f32c(grad_out), F = f32c(F_), gates = f32c(gates_), qtab = f32c(qtab_);
   Tensor dF = at::empty_like(F), dgates = at::zeros_like(gates);
@@ -297,7 +306,8 @@ std::tuple<Tensor, Tensor> ictd_conv1_backward(const Tensor& grad_out, const Ten
 }
 
 std::tuple<Tensor, Tensor> ictd_conv1_backward_meta(const Tensor&, const Tensor& F, const Tensor& gates, const Tensor&,
-                                                    const Tensor&, const Tensor&, const Tensor&, int64_t, const Tensor&) {
+                                                    const Tensor&, const Tensor&, const Tensor&, int64_t,
+                                                    at::IntArrayRef) {
   return {at::empty(F.sizes(), fopts(F)), at::empty(gates.sizes(), fopts(gates))};
 }
 
@@ -374,13 +384,6 @@ Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&
 }
 
 // -------------------------------------------------------------- readout feature assembly
-const FscReadoutTable* readout_table_of(const Tensor& table) {
-  TORCH_CHECK(table.device().is_cpu() && table.scalar_type() == at::kInt && table.is_contiguous() &&
-                  table.numel() * 4 == (int64_t)sizeof(FscReadoutTable),
-              "readout table must be a contiguous CPU int32 tensor holding an FscReadoutTable (",
-              sizeof(FscReadoutTable) / 4, " entries)");
-  return reinterpret_cast<const FscReadoutTable*>(table.data_ptr<int32_t>());
-}
 
 // The layers as float32 contiguous [N][M][C] tensors (kept alive by the caller).
 std::vector<Tensor> readout_layers(at::TensorList layers, const FscReadoutTable* T) {
@@ -402,8 +405,9 @@ Tensor readout_map(const Tensor& map, const FscReadoutTable* T, const char* what
   return i32c(map, what);
 }
 
-std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& srcmap, const Tensor& table) {
-  const FscReadoutTable* T = readout_table_of(table);
+std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& srcmap, at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
   std::vector<Tensor> X = readout_layers(layers, T);
   Tensor sm = readout_map(srcmap, T, "srcmap");
   const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C;
@@ -415,15 +419,17 @@ std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& s
   return {t_all, sq};
 }
 
-std::tuple<Tensor, Tensor> readout_gather_meta(at::TensorList layers, const Tensor&, const Tensor& table) {
-  const FscReadoutTable* T = readout_table_of(table);
+std::tuple<Tensor, Tensor> readout_gather_meta(at::TensorList layers, const Tensor&, at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
   const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
   return {at::empty({N * T->M * nC}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
 }
 
 std::vector<Tensor> readout_scatter(const c10::List<std::optional<Tensor>>& grad_t, const std::optional<Tensor>& grad_sq,
-                                    at::TensorList layers, const Tensor& gmap, const Tensor& table) {
-  const FscReadoutTable* T = readout_table_of(table);
+                                    at::TensorList layers, const Tensor& gmap, at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
   std::vector<Tensor> X = readout_layers(layers, T);
   Tensor gm = readout_map(gmap, T, "gmap");
   const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C;
@@ -462,7 +468,7 @@ std::vector<Tensor> readout_scatter(const c10::List<std::optional<Tensor>>& grad
 }
 
 std::vector<Tensor> readout_scatter_meta(const c10::List<std::optional<Tensor>>&, const std::optional<Tensor>&,
-                                         at::TensorList layers, const Tensor&, const Tensor&) {
+                                         at::TensorList layers, const Tensor&, at::IntArrayRef) {
   std::vector<Tensor> dX;
   for (const Tensor& x : layers) dX.push_back(at::empty(x.sizes(), fopts(x)));
   return dX;
@@ -479,8 +485,9 @@ Tensor gram_input(const Tensor& t_all, const FscReadoutTable* T, int64_t N, int 
 // scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.
 std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
                                             at::ArrayRef<double> scales, const Tensor& srcmap, const Tensor& gmap,
-                                            const Tensor& table) {
-  const FscReadoutTable* T = readout_table_of(table);
+                                            at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
   TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
                   (int64_t)scales.size() == T->n_keys,
               "one prepared Gram weight pair and scale per key");
@@ -496,8 +503,9 @@ std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorLis
 
 std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList Wf, at::TensorList,
                                                  at::ArrayRef<double>, const Tensor&, const Tensor&,
-                                                 const Tensor& table) {
-  const FscReadoutTable* T = readout_table_of(table);
+                                                 at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
   const int64_t N = layers[0].size(0), nC = (int64_t)T->n_layers * T->C;
   return {at::empty({N, gram_width(Wf[0], nC)}, fopts(layers[0])), at::empty({N, T->n_keys, nC}, fopts(layers[0]))};
 }
@@ -687,17 +695,11 @@ Tensor radial_mlp_backward_meta(const Tensor&, const Tensor& r, const Tensor&, c
   return at::empty({r.numel()}, fopts(r));
 }
 
-const FscHarmTable* harm_table_of(const Tensor& table) {
-  TORCH_CHECK(table.device().is_cpu() && table.scalar_type() == at::kInt && table.is_contiguous() &&
-                  table.numel() * 4 == (int64_t)sizeof(FscHarmTable),
-              "harmonics table must be a contiguous CPU int32 tensor holding an FscHarmTable (",
-              sizeof(FscHarmTable) / 4, " entries)");
-  return reinterpret_cast<const FscHarmTable*>(table.data_ptr<int32_t>());
-}
 
-Tensor edge_harmonics(const Tensor& n_, const Tensor& table) {
+Tensor edge_harmonics(const Tensor& n_, at::IntArrayRef table) {
   require_gpu({n_});
-  const FscHarmTable* T = harm_table_of(table);
+  const FscHarmTable Tv = unpack_table<FscHarmTable>(table, "harmonics table");
+  const FscHarmTable* T = &Tv;
   const int64_t E = n_.size(0), NY = (T->lmax + 1) * (T->lmax + 1);
   Tensor n = f32c(n_);
   Tensor Y = at::empty({E, NY}, fopts(n));
@@ -705,14 +707,16 @@ Tensor edge_harmonics(const Tensor& n_, const Tensor& table) {
   return Y;
 }
 
-Tensor edge_harmonics_meta(const Tensor& n, const Tensor& table) {
-  const FscHarmTable* T = harm_table_of(table);
+Tensor edge_harmonics_meta(const Tensor& n, at::IntArrayRef table) {
+  const FscHarmTable Tv = unpack_table<FscHarmTable>(table, "harmonics table");
+  const FscHarmTable* T = &Tv;
   return at::empty({n.size(0), (T->lmax + 1) * (T->lmax + 1)}, fopts(n));
 }
 
-Tensor edge_harmonics_backward(const Tensor& grad_Y, const Tensor& n_, const Tensor& table) {
+Tensor edge_harmonics_backward(const Tensor& grad_Y, const Tensor& n_, at::IntArrayRef table) {
   require_gpu({grad_Y, n_});
-  const FscHarmTable* T = harm_table_of(table);
+  const FscHarmTable Tv = unpack_table<FscHarmTable>(table, "harmonics table");
+  const FscHarmTable* T = &Tv;
   const int64_t E = n_.size(0);
   Tensor n = f32c(n_), g = f32c(grad_Y);
   Tensor dn = at::empty({E, 3}, fopts(n));
@@ -720,7 +724,7 @@ Tensor edge_harmonics_backward(const Tensor& grad_Y, const Tensor& n_, const Ten
   return dn;
 }
 
-Tensor edge_harmonics_backward_meta(const Tensor&, const Tensor& n, const Tensor&) {
+Tensor edge_harmonics_backward_meta(const Tensor&, const Tensor& n, at::IntArrayRef) {
   return at::empty({n.size(0), 3}, fopts(n));
 }
 
@@ -808,13 +812,15 @@ std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& 
 
 struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg,
-                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) {
+                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm,
+                               std::vector<int64_t> layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                       const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&)>("fsctep::ictd_conv");
+                                      at::IntArrayRef)>("fsctep::ictd_conv");
     Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout);
-    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout});
+    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+    ctx->saved_data["layout"] = layout;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
@@ -824,8 +830,9 @@ struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&)>("fsctep::ictd_conv_backward");
-    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9]);
+        const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv_backward");
+    const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
+    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], layout);
     res[0] = dx;
     res[1] = dY;
     res[2] = dgates;
@@ -835,20 +842,21 @@ struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
 
 Tensor ictd_conv_autograd(const Tensor& x, const Tensor& Y, const Tensor& gates, const Tensor& W, const Tensor& Wt,
                           const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                          const Tensor& src_perm, const Tensor& layout) {
-  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout)[0];
+                          const Tensor& src_perm, at::IntArrayRef layout) {
+  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout.vec())[0];
 }
 
 struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
   static variable_list forward(AutogradContext* ctx, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr,
                                Tensor edge_pair, Tensor node_species, int64_t n_species, int64_t n_comps,
-                               Tensor layout) {
+                               std::vector<int64_t> layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, int64_t, int64_t, const Tensor&)>("fsctep::ictd_conv1");
+                                      const Tensor&, int64_t, int64_t, at::IntArrayRef)>("fsctep::ictd_conv1");
     Tensor out = op.call(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout);
-    ctx->save_for_backward({F, gates, qtab, dst_ptr, edge_pair, node_species, layout});
+    ctx->save_for_backward({F, gates, qtab, dst_ptr, edge_pair, node_species});
     ctx->saved_data["n_species"] = n_species;
+    ctx->saved_data["layout"] = layout;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
@@ -858,8 +866,10 @@ struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                                           const Tensor&, const Tensor&, const Tensor&, int64_t,
-                                                          const Tensor&)>("fsctep::ictd_conv1_backward");
-    auto [dF, dgates] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], ctx->saved_data["n_species"].toInt(), s[6]);
+                                                          at::IntArrayRef)>("fsctep::ictd_conv1_backward");
+    const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
+    auto [dF, dgates] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], ctx->saved_data["n_species"].toInt(),
+                                layout);
     res[0] = dF;
     res[1] = dgates;
     return res;
@@ -868,8 +878,8 @@ struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
 
 Tensor ictd_conv1_autograd(const Tensor& F, const Tensor& gates, const Tensor& qtab, const Tensor& dst_ptr,
                            const Tensor& edge_pair, const Tensor& node_species, int64_t n_species, int64_t n_comps,
-                           const Tensor& layout) {
-  return IctdConv1Fn::apply(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout)[0];
+                           at::IntArrayRef layout) {
+  return IctdConv1Fn::apply(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout.vec())[0];
 }
 
 struct GramFn : public torch::autograd::Function<GramFn> {
@@ -901,12 +911,13 @@ Tensor gram_bilinear_autograd(const Tensor& t, const Tensor& Wf, const Tensor& W
 // backward and the squared-norm gradient (no per-slice zero fills or accumulations).
 struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
   static variable_list forward(AutogradContext* ctx, at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
-                               std::vector<double> scales, Tensor srcmap, Tensor gmap, Tensor table) {
+                               std::vector<double> scales, Tensor srcmap, Tensor gmap, std::vector<int64_t> table) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto gather =
-        op_handle<std::tuple<Tensor, Tensor>(at::TensorList, const Tensor&, const Tensor&)>("fsctep::readout_gather");
+        op_handle<std::tuple<Tensor, Tensor>(at::TensorList, const Tensor&, at::IntArrayRef)>("fsctep::readout_gather");
     static auto gram = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear");
-    const FscReadoutTable* T = readout_table_of(table);
+    const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
     TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
                     (int64_t)scales.size() == T->n_keys,
                 "one prepared Gram weight pair and scale per key");
@@ -921,8 +932,8 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
     keep.push_back(t_all);
     for (const Tensor& w : Wb) keep.push_back(w);
     keep.push_back(gmap);
-    keep.push_back(table);
     ctx->save_for_backward(keep);
+    ctx->saved_data["table"] = table;
     ctx->saved_data["n_layers"] = (int64_t)layers.size();
     ctx->saved_data["scales"] = c10::IValue(c10::ArrayRef<double>(scales));
     ctx->set_materialize_grads(false);   // an unused output skips its part of the backward
@@ -942,12 +953,13 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
         op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear_backward");
     static auto scatter = op_handle<std::vector<Tensor>(const c10::List<std::optional<Tensor>>&,
                                                         const std::optional<Tensor>&, at::TensorList, const Tensor&,
-                                                        const Tensor&)>("fsctep::readout_scatter");
+                                                        at::IntArrayRef)>("fsctep::readout_scatter");
     std::vector<Tensor> layers(s.begin(), s.begin() + nL);
     const Tensor& t_all = s[nL];
     const Tensor& gmap = s[nL + 1 + nK];
-    const Tensor& table = s[nL + 2 + nK];
-    const FscReadoutTable* T = readout_table_of(table);
+    const std::vector<int64_t> table = ctx->saved_data["table"].toIntVector();
+    const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  const FscReadoutTable* T = &Tv;
     const int64_t N = layers[0].size(0);
     c10::List<std::optional<Tensor>> dt;
     for (int k = 0; k < nK; ++k) {
@@ -966,8 +978,8 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
 
 std::tuple<Tensor, Tensor> readout_features_autograd(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
                                                      at::ArrayRef<double> scales, const Tensor& srcmap,
-                                                     const Tensor& gmap, const Tensor& table) {
-  auto out = ReadoutFn::apply(layers, Wf, Wb, scales.vec(), srcmap, gmap, table);
+                                                     const Tensor& gmap, at::IntArrayRef table) {
+  auto out = ReadoutFn::apply(layers, Wf, Wb, scales.vec(), srcmap, gmap, table.vec());
   return {out[0], out[1]};
 }
 
@@ -1073,11 +1085,12 @@ Tensor radial_mlp_autograd(const Tensor& r, const Tensor& w0, const Tensor& b0, 
 }
 
 struct EdgeHarmonicsFn : public torch::autograd::Function<EdgeHarmonicsFn> {
-  static variable_list forward(AutogradContext* ctx, Tensor n, Tensor table) {
+  static variable_list forward(AutogradContext* ctx, Tensor n, std::vector<int64_t> table) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto op = op_handle<Tensor(const Tensor&, const Tensor&)>("fsctep::edge_harmonics");
+    static auto op = op_handle<Tensor(const Tensor&, at::IntArrayRef)>("fsctep::edge_harmonics");
     Tensor Y = op.call(n, table);
-    ctx->save_for_backward({n, table});
+    ctx->save_for_backward({n});
+    ctx->saved_data["table"] = table;
     ctx->set_materialize_grads(false);
     return {Y};
   }
@@ -1085,13 +1098,15 @@ struct EdgeHarmonicsFn : public torch::autograd::Function<EdgeHarmonicsFn> {
     variable_list res(2);
     if (!grads[0].defined()) return res;
     auto s = ctx->get_saved_variables();
-    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&)>("fsctep::edge_harmonics_backward");
-    res[0] = op.call(grads[0], s[0], s[1]);
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::edge_harmonics_backward");
+    res[0] = op.call(grads[0], s[0], ctx->saved_data["table"].toIntVector());
     return res;
   }
 };
 
-Tensor edge_harmonics_autograd(const Tensor& n, const Tensor& table) { return EdgeHarmonicsFn::apply(n, table)[0]; }
+Tensor edge_harmonics_autograd(const Tensor& n, at::IntArrayRef table) {
+  return EdgeHarmonicsFn::apply(n, table.vec())[0];
+}
 
 // CPU tensors: the HIP kernels are the only implementation, so say that instead of "no CPU kernel".
 void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
@@ -1113,13 +1128,13 @@ TORCH_LIBRARY(fsctep, m) {
         "-> (Tensor, Tensor)");
   m.def("ictd_prepare_weights(Tensor W) -> Tensor");
   m.def("ictd_conv(Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg, Tensor dst_ptr, "
-        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) -> Tensor");
+        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, int[] layout) -> Tensor");
   m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
-        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor layout) -> (Tensor, Tensor, Tensor)");
+        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, int[] layout) -> (Tensor, Tensor, Tensor)");
   m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
-        "int n_species, int n_comps, Tensor layout) -> Tensor");
+        "int n_species, int n_comps, int[] layout) -> Tensor");
   m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "
-        "Tensor edge_pair, Tensor node_species, int n_species, Tensor layout) -> (Tensor, Tensor)");
+        "Tensor edge_pair, Tensor node_species, int n_species, int[] layout) -> (Tensor, Tensor)");
   m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
   m.def("gram_bilinear(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
   m.def("gram_bilinear_backward(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
@@ -1129,14 +1144,14 @@ TORCH_LIBRARY(fsctep, m) {
         "Tensor src_perm) -> Tensor");
   m.def("radial_mlp(Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, Tensor? b4, float r_cut, "
         "int basis) -> Tensor");
-  m.def("edge_harmonics(Tensor n, Tensor table) -> Tensor");
-  m.def("edge_harmonics_backward(Tensor grad_Y, Tensor n, Tensor table) -> Tensor");
+  m.def("edge_harmonics(Tensor n, int[] table) -> Tensor");
+  m.def("edge_harmonics_backward(Tensor grad_Y, Tensor n, int[] table) -> Tensor");
   m.def("radial_mlp_backward(Tensor grad_out, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, "
         "float r_cut, int basis) -> Tensor");
-  m.def("readout_gather(Tensor[] layers, Tensor srcmap, Tensor table) -> (Tensor, Tensor)");
-  m.def("readout_scatter(Tensor?[] grad_t, Tensor? grad_sq, Tensor[] layers, Tensor gmap, Tensor table) -> Tensor[]");
+  m.def("readout_gather(Tensor[] layers, Tensor srcmap, int[] table) -> (Tensor, Tensor)");
+  m.def("readout_scatter(Tensor?[] grad_t, Tensor? grad_sq, Tensor[] layers, Tensor gmap, int[] table) -> Tensor[]");
   m.def("readout_features(Tensor[] layers, Tensor[] Wf, Tensor[] Wb, float[] scales, Tensor srcmap, Tensor gmap, "
-        "Tensor table) -> (Tensor, Tensor)");
+        "int[] table) -> (Tensor, Tensor)");
   m.def("graph_prepare(Tensor edge_src, Tensor edge_dst, Tensor species, int n_species) -> Tensor[]");
   m.def("edge_vec_geometry(Tensor edge_vec, Tensor order) -> (Tensor, Tensor)");
   m.def("edge_vec_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor order) -> Tensor");

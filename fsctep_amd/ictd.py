@@ -172,14 +172,16 @@ class _ICTDTrunk(nn.Module):
             raise NotImplementedError("sync hooks, external blocks and fidelity ids are outside the HIP path")
         g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
         e, dip = self.forward_graph(pos, batch, cell, g, external_tensor=external_tensor,
-                                    edge_vec=precomputed_edge_vec)
+                                    edge_vec=precomputed_edge_vec, with_dipole=bool(return_physical_tensors))
         if return_physical_tensors:
             return e, {"dipole": {1: dip}} if dip is not None else {}
         return e
 
-    def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None, edge_vec=None):
+    def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None, edge_vec=None, with_dipole=True):
         """((N,1) atomic energies, (G,1,3) dipole or None) for a prepared graph; ``edge_vec`` (E, 3), in the
-        caller's edge order, replaces the geometry from ``pos`` (differentiable w.r.t. it)."""
+        caller's edge order, replaces the geometry from ``pos`` (differentiable w.r.t. it).  The dipole head
+        runs when the model has one and ``with_dipole`` is set (its graph count reads ``batch`` on the host,
+        as the reference's does, pure_cartesian_ictd_layers_o3.py:983)."""
         self._check_inference()
         if not pos.is_cuda:
             raise RuntimeError("the HIP ICTD path runs on the GPU only")
@@ -219,7 +221,7 @@ class _ICTDTrunk(nn.Module):
         for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
             feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, self._gates(fc2, r), tp.weight.detach(),
                                                   self._wt(tp), cg, g, self.layout_id))
-        e, dip = self.readout(feats, batch, factors)
+        e, dip = self.readout(feats, batch, factors, with_dipole)
         return poison_invalid(e, g), dip
 
     def _gates(self, fc, r):
@@ -232,7 +234,7 @@ class _ICTDTrunk(nn.Module):
     def _wread(self, i, k):
         return self.W_read[_key_str(k)] if self.o3 else self.W_read[i]
 
-    def readout(self, feats, batch, factors):
+    def readout(self, feats, batch, factors, with_dipole=True):
         """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included: the
         Gram inputs (the reference's channel-major flatten, layer concatenation and re-split by key)
         and the per-key squared norms of the layer concatenation come from one fused readout op."""
@@ -252,7 +254,7 @@ class _ICTDTrunk(nn.Module):
             outs.append(sq * factors[i])
         e = self.weighted_sum(self.proj_total(torch.cat(outs, dim=-1)))
         dip = None
-        if self._dipole:
+        if self._dipole and with_dipole:
             # the (1, -1) Gram input, (N, d, n*C), by the same column map (differentiable gather)
             i = self.keys.index((1, -1))
             nC = nL * self.channels

@@ -1,8 +1,8 @@
 """ICTD kernel layout tables and helpers over the ``torch.ops.fsctep.ictd_*`` ops.
 
 A layout (active irreps + live paths, see ``ictd_basis.Layout``) is turned into the C struct
-``FscIctdLayout`` once, registered under an integer id, and handed to the ops as a CPU int32
-tensor holding the struct.  The ops are registered in C++ by ``libfsctep_torch.so``:
+``FscIctdLayout`` once, registered under an integer id, and handed to the ops as the list of the
+struct's int32 words (an ``int[]`` argument).  The ops are registered in C++ by ``libfsctep_torch.so``:
 
     ictd_prepare_weights(W) -> Wt   (split-fp16 channel-mix weights, opaque)
     ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout) -> out
@@ -102,17 +102,22 @@ def layout_struct(layout_id: int) -> FscIctdLayout:
     return _LAYOUTS[layout_id][2]
 
 
-def layout_tensor(layout_id: int) -> Tensor:
-    """The layout table as the CPU int32 tensor the ops take (one per layout, cached)."""
+def struct_words(st) -> list:
+    """A ctypes struct of 32-bit fields as the list of its int32 words (the ``int[]`` table arguments of the
+    ops: host values, so a traced graph keeps them on the host whatever device it is loaded to)."""
+    return np.frombuffer(ctypes.string_at(ctypes.addressof(st), ctypes.sizeof(st)), dtype=np.int32).tolist()
+
+
+def layout_words(layout_id: int) -> list:
+    """The layout table as the int32 word list the ops take (one per layout, cached)."""
     name, lay, st = _LAYOUTS[layout_id]
-    key = ("tensor", layout_id)
-    if key not in _TENSORS:
-        raw = np.frombuffer(ctypes.string_at(ctypes.addressof(st), ctypes.sizeof(st)), dtype=np.int32)
-        _TENSORS[key] = torch.from_numpy(raw.copy())
-    return _TENSORS[key]
+    key = ("words", layout_id)
+    if key not in _TABLES:
+        _TABLES[key] = struct_words(st)
+    return _TABLES[key]
 
 
-_TENSORS: dict = {}
+_TABLES: dict = {}
 
 
 class FscHarmTable(ctypes.Structure):
@@ -120,12 +125,12 @@ class FscHarmTable(ctypes.Structure):
                 ("coef", (ctypes.c_float * 7) * 20)]
 
 
-def harmonics_table(lmax: int) -> Tensor:
+def harmonics_table(lmax: int) -> list:
     """The ICTD direction-harmonics table (degree-l monomials and multinomial * G_l B_l, lmax <= 3) as the
-    CPU int32 tensor the ``edge_harmonics`` op takes (cached)."""
+    int32 word list the ``edge_harmonics`` op takes (cached)."""
     from .ictd_basis import harmonic_projection
     key = ("harm", lmax)
-    if key not in _TENSORS:
+    if key not in _TABLES:
         if not 0 <= lmax <= 3:
             raise NotImplementedError("the HIP direction harmonics support lmax <= 3")
         t = FscHarmTable()
@@ -142,9 +147,8 @@ def harmonics_table(lmax: int) -> Tensor:
                     t.coef[k][j] = float(M[i][j])
                 k += 1
         t.nmono = k
-        raw = np.frombuffer(ctypes.string_at(ctypes.addressof(t), ctypes.sizeof(t)), dtype=np.int32)
-        _TENSORS[key] = torch.from_numpy(raw.copy())
-    return _TENSORS[key]
+        _TABLES[key] = struct_words(t)
+    return _TABLES[key]
 
 
 def edge_harmonics(n: Tensor, lmax: int) -> Tensor:
@@ -155,10 +159,10 @@ def edge_harmonics(n: Tensor, lmax: int) -> Tensor:
 def ictd_conv_apply(x, Y, gates, W, Wt, cg, graph, layout_id: int):
     """Differentiable conv2..n: x (N,M,C), Y (E,NY), gates (E,NREF) -> (N,M,C)."""
     return torch.ops.fsctep.ictd_conv(x, Y, gates, W, Wt, cg, graph.dst_ptr, graph.src32, graph.src_ptr,
-                                      graph.src_perm, layout_tensor(layout_id))
+                                      graph.src_perm, layout_words(layout_id))
 
 
 def ictd_conv1_apply(F, gates, qtab, graph, layout_id: int):
     """Differentiable conv1: F (E,NY) harmonics (+ field), gates (E,NREF), qtab (NS*NS,NP1,C) -> (N,M,C)."""
     return torch.ops.fsctep.ictd_conv1(F, gates, qtab, graph.dst_ptr, graph.edge_pair, graph.node_species,
-                                       int(graph.n_species), layout_struct(layout_id).M, layout_tensor(layout_id))
+                                       int(graph.n_species), layout_struct(layout_id).M, layout_words(layout_id))

@@ -105,8 +105,7 @@ class ReadoutMaps:
         t.n_layers, t.M, t.C, t.n_keys = n_layers, M, C, len(dims)
         for k, d in enumerate(dims):
             t.key_comp0[k], t.key_dim[k] = int(comp0[k]), d
-        raw = np.frombuffer(ctypes.string_at(ctypes.addressof(t), ctypes.sizeof(t)), dtype=np.int32)
-        self.table = torch.from_numpy(raw.copy())
+        self.table = np.frombuffer(ctypes.string_at(ctypes.addressof(t), ctypes.sizeof(t)), dtype=np.int32).tolist()
         self.srcmap = torch.from_numpy(srcmap.astype(np.int32))
         self.gmap = torch.from_numpy(gmap.astype(np.int32))
         self.n_layers, self.M, self.C, self.key_dims = n_layers, M, C, dims

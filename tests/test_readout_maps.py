@@ -97,6 +97,6 @@ def test_resplit_moves_entries_across_keys():
 
 def test_table_layout():
     maps = ReadoutMaps(3, 64, [1, 3, 9], resplit=False)
-    t = maps.table.numpy()
+    t = np.asarray(maps.table)
     assert t[:4].tolist() == [3, 13, 64, 3]
     assert t[4:7].tolist() == [0, 1, 4] and t[12:15].tolist() == [1, 3, 9]
