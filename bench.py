@@ -11,8 +11,16 @@ boxes at 0.1 atoms/A^3, cutoff 5 A, 8 Bessel radial functions, min pair distance
 One step = energy and forces (F = -dE/dpos) of the whole system: edge geometry, radial
 basis and MLP, conv1..conv3 message passing (HIP kernels), readout, and the backward of
 all of it w.r.t. positions.  Inputs (positions, neighbour list, parameters) are resident
-in HBM before timing starts; the neighbour list and receiver sort are built once (as
-between MD list rebuilds) and not timed.  Prints one JSON line.
+in HBM before timing starts; the receiver-sorted graph is prepared once (as between MD list
+rebuilds) for the headline figure.  The line also carries the step through the reference-signature
+``forward()``, which prepares the graph on every call as the reference sorts on every call, and the
+cold and warm graph-preparation times.
+
+The default run (sparse, 10k atoms) prints the headline at the top level and the ICTD 10k and
+ICTD-O3 4k workloads under ``workloads``, each with its roofline kernel, a table of the TP/scatter
+kernels' rates, the parity of its energies, forces (and dipole) against the fp64 oracle's full-system
+values where a fixture for that exact system exists (tests/golden/oracle_<mode>_<atoms>.npz), and
+the CPU baseline.  Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -30,15 +38,35 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+PARITY_TOL = 1e-5
 
 WORKLOADS = {
     "sparse": dict(atoms=10000, species=4, seed=22, channels=64, layers=3, lmax=2, kernel="edge_message_grad",
-                   cpu_atoms=300),
+                   cpu_atoms=300,
+                   table=["node_expand", "edge_message", "receiver_sum", "edge_message_grad", "node_expand_grad"]),
     "ictd": dict(atoms=10000, species=8, seed=33, channels=128, layers=3, lmax=3, kernel="ictd_project_grad",
-                 cpu_atoms=200),
+                 cpu_atoms=200,
+                 table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_source_sum"]),
     "ictd-o3": dict(atoms=4000, species=4, seed=44, channels=64, layers=3, lmax=2, kernel="ictd_project_grad",
-                    cpu_atoms=200),
+                    cpu_atoms=200,
+                    table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_source_sum"]),
 }
+
+# Arithmetic of the products in each kernel family (every sum accumulates in fp32).  "split-fp16": each
+# operand times a power of two is split into two fp16 parts and a product keeps hh + hl + lh on fp16 MFMA
+# (22 significant bits; the dropped ll term is below 2^-22 |ab|).  "split-bf16": three bf16 parts per
+# operand, six of the nine part products on bf16 MFMA (the dropped ones are below 2^-23 |ab|).
+PRODUCTS = {
+    "sparse": {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
+               "edge_message_grad": "fp32 MFMA", "conv1 pair GEMMs": "fp32 MFMA", "radial_mlp": "fp32 MFMA",
+               "receiver_sum, edge geometry, readout assembly": "fp32 VALU",
+               "gram_forward, gram_backward": "split-fp16", "MainNet, atom MLP": "torch fp32"},
+    "ictd": {"ictd_project, ictd_project_grad": "fp32 MFMA", "ictd_mix, ictd_mix_grad": "split-fp16",
+             "ictd_conv1, source_sum, edge geometry, harmonics, readout assembly": "fp32 VALU",
+             "radial_mlp (gates)": "fp32 MFMA", "gram_forward, gram_backward": "split-fp16",
+             "MainNet, atom MLP": "torch fp32"},
+}
+PRODUCTS["ictd-o3"] = PRODUCTS["ictd"]
 
 
 # Per-kernel algorithmic work of one launch (one conv2..n layer with N nodes, E edges, C channels).
@@ -108,6 +136,21 @@ def _cpu_model() -> str:
     return ""
 
 
+def host_cores() -> tuple[int, str]:
+    """Cores available to this process: its affinity set, capped by a cgroup CPU quota if one is set."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            q, period = fh.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    cores = aff if quota is None else min(aff, quota)
+    return cores, f"affinity {aff}" + ("" if quota is None else f", cgroup quota {quota}")
+
+
 def _system(mode: str, n_atoms: int, seed: int):
     from fsctep_amd.synthetic import SPECIES_4, SPECIES_8, make_system
     w = WORKLOADS[mode]
@@ -121,12 +164,22 @@ def _field(n_graphs: int, seed: int):
     return np.random.Generator(np.random.PCG64(seed)).normal(0.0, 0.1, size=(n_graphs, 3))
 
 
+def system_digest(s) -> str:
+    """sha256 of the fp32/int64 arrays that define a system (the key of a full-size oracle fixture)."""
+    import numpy as np
+    h = hashlib.sha256()
+    for a in (s.pos.astype(np.float32), s.species.astype(np.int64), s.edge_src.astype(np.int64),
+              s.edge_dst.astype(np.int64), s.edge_shifts.astype(np.float32), s.cell.astype(np.float32)):
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
 def cpu_baseline(mode: str, n_atoms: int, steps: int, seed: int) -> dict:
-    """The oracle (the reference's algorithm restated in PyTorch on the CPU) on host cores."""
+    """The oracle (the reference's algorithm restated in PyTorch on the CPU) on the host cores."""
     import torch
     from fsctep_amd.synthetic import seeded_value
     w = WORKLOADS[mode]
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores, cdesc = host_cores()
     torch.set_num_threads(cores)
     s = _system(mode, n_atoms, seed)
     args = (torch.tensor(s.pos, dtype=torch.float32), torch.tensor(s.species),
@@ -148,13 +201,16 @@ def cpu_baseline(mode: str, n_atoms: int, steps: int, seed: int) -> dict:
         what = "per-path CG contractions with materialised per-edge weights, index_add"
     p = {k: torch.tensor(seeded_value(k, sh, 1), dtype=torch.float32) for k, sh in R.param_shapes(cfg)}
     run(p)
-    t0 = time.perf_counter()
+    dts = []
     for _ in range(steps):
+        t0 = time.perf_counter()
         run(p)
-    dt = (time.perf_counter() - t0) / steps
+        dts.append(time.perf_counter() - t0)
+    dt = statistics.median(dts)
     return {"value": round(n_atoms / dt, 3), "unit": "atom-steps/s", "cores": cores, "kind": "port",
             "sample": f"oracle ({what}), fp32, {n_atoms} atoms / {s.num_edges} edges of the same recipe, "
-                      f"{steps} timed steps after 1 warm-up, {dt:.2f} s/step, {cores} threads on {_cpu_model()}"}
+                      f"median of {steps} timed steps after 1 warm-up, {dt:.2f} s/step, {cores} threads "
+                      f"({cdesc}) on {_cpu_model()}"}
 
 
 def build_model(mode: str, dev):
@@ -192,6 +248,188 @@ def workload_name(mode: str, N: int, E: int) -> str:
             f"cutoff 5.0 A, 8 Bessel radial basis")
 
 
+def _rel_inf(a, b) -> float:
+    import numpy as np
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def parity_vs_fixture(mode: str, system, seed: int, e, f, dip) -> dict:
+    """Max-norm relative errors of the step's outputs against the fp64 oracle's full-system values."""
+    import numpy as np
+    N = system.num_atoms
+    path = os.path.join(ROOT, "tests", "golden", f"oracle_{mode}_{N}.npz")
+    rel = os.path.relpath(path, ROOT)
+    if not os.path.exists(path):
+        return {"fixture": None, "note": f"no fp64 oracle fixture for this system ({rel})"}
+    fx = np.load(path, allow_pickle=False)
+    if str(fx["system_sha256"]) != system_digest(system) or int(fx["seed"]) != seed:
+        return {"fixture": rel, "note": "fixture is for another system (digest mismatch): not compared"}
+    out = {"fixture": rel, "reference": "fp64 oracle on the whole system", "tolerance": PARITY_TOL,
+           "energy_rel": _rel_inf(e, fx["energy"]), "forces_rel": _rel_inf(f, fx["forces"]),
+           "energy_total_rel": abs(float(np.sum(np.asarray(e, np.float64))) - float(fx["energy_total"]))
+           / max(abs(float(fx["energy_total"])), 1e-30)}
+    if dip is not None and "dipole" in fx:
+        out["dipole_rel"] = _rel_inf(np.asarray(dip).reshape(-1, 3), fx["dipole"])
+    out["within_tolerance"] = all(v < PARITY_TOL for k, v in out.items() if k.endswith("_rel"))
+    for k in list(out):
+        if k.endswith("_rel"):
+            out[k] = float(f"{out[k]:.3e}")
+    return out
+
+
+def _rate(work: dict, avg_ms: float) -> dict:
+    """Achieved rate of one launch against its algorithmic bytes (HBM) and, for MFMA kernels, flops."""
+    gbs = work["bytes"] / (avg_ms * 1e-3) / 1e9
+    r = {"avg_launch_ms": round(avg_ms, 4), "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+         "bound": work["bound"]}
+    if work["bound"] == "mfma":
+        tf = work["flops"] / (avg_ms * 1e-3) / 1e12
+        r.update(tflops=round(tf, 2), mfma_frac=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+    return r
+
+
+def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: str, dev,
+            table: bool = True) -> dict:
+    import numpy as np
+    import torch
+    from fsctep_amd import _lib
+    w = WORKLOADS[mode]
+    t_build = time.perf_counter()
+    system = _system(mode, n_atoms, seed)
+    print(f"[bench] {mode}: {system.num_atoms} atoms, {system.num_edges} edges "
+          f"({time.perf_counter() - t_build:.1f} s to build)", file=sys.stderr, flush=True)
+    model = build_model(mode, dev)
+    C = w["channels"]
+    N, E = system.num_atoms, system.num_edges
+
+    pos = torch.tensor(system.pos, dtype=torch.float32, device=dev)
+    A = torch.tensor(system.species, device=dev)
+    batch = torch.zeros(N, dtype=torch.long, device=dev)
+    cell = torch.tensor(system.cell, dtype=torch.float32, device=dev)
+    src = torch.tensor(system.edge_src, device=dev)
+    dst = torch.tensor(system.edge_dst, device=dev)
+    shifts = torch.tensor(system.edge_shifts, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    t_g = time.perf_counter()
+    graph = model.prepare(src, dst, shifts, N, A, pos=pos)
+    torch.cuda.synchronize()
+    t_cold = time.perf_counter() - t_g
+    warm = []
+    for _ in range(5):
+        t_g = time.perf_counter()
+        model.prepare(src, dst, shifts, N, A, pos=pos)
+        torch.cuda.synchronize()
+        warm.append(time.perf_counter() - t_g)
+
+    field = torch.tensor(_field(1, seed), dtype=torch.float32, device=dev) if mode == "ictd-o3" else None
+    if mode == "sparse":
+        from fsctep_amd.sparse import energy_and_forces
+
+        def step():
+            e, f = energy_and_forces(model, pos, batch, cell, graph)
+            return e, f, None
+    else:
+        from fsctep_amd.ictd import energy_forces
+
+        def step():
+            return energy_forces(model, pos, batch, cell, graph, external_tensor=field)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    print(f"[bench] {mode}: warm-up done ({warmup} steps)", file=sys.stderr, flush=True)
+
+    # timed region: exactly `steps` steps, synchronised on both sides
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    with _lib.KernelTimer(kname) as kt:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev[0].record()
+        for i in range(steps):
+            res = step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    e, f, dip = res
+    step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    ms_per_step = elapsed * 1000.0 / steps
+    assert torch.isfinite(e).all() and torch.isfinite(f).all()
+    print(f"[bench] {mode}: timed {steps} steps: {ms_per_step:.3f} ms/step (median {statistics.median(step_ms):.3f}); "
+          f"E={float(e.sum()):.6f} max|F|={float(f.abs().max()):.4f}", file=sys.stderr, flush=True)
+
+    if mode == "sparse":
+        work_of = lambda k: sparse_kernel_work(k, N, E, C)
+    else:
+        from fsctep_amd import ictd_ops
+        lay = ictd_ops.layout_struct(model.layout_id)
+        work_of = lambda k: ictd_kernel_work(k, lay, N, E, C)
+    work = work_of(kname)
+    avg_ms = kt.total_ms / max(kt.launches, 1)
+    if work["bound"] == "mfma":
+        achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4)}
+    else:
+        achieved = work["bytes"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    roof["traffic"] = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{kname}_{mode}{N}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            tinfo = json.load(fh)
+        srcf = os.path.join(ROOT, tinfo.get("source", ""))
+        if os.path.isfile(srcf) and hashlib.sha256(open(srcf, "rb").read()).hexdigest() == tinfo.get("source_sha256"):
+            roof["traffic"] = tinfo.get("hbm_bytes_per_launch")   # measured for this exact kernel source
+    roof["kernel"] = kname
+    roof["avg_launch_ms"] = round(avg_ms, 4)
+    roof["launches"] = kt.launches
+    roof["algorithmic_per_launch"] = {"flops": work["flops"], "bytes": work["bytes"]}
+
+    out = {"ms_per_step": round(ms_per_step, 4), "median_ms_per_step": round(statistics.median(step_ms), 4),
+           "value": round(N / (ms_per_step * 1e-3), 1), "atoms": N, "edges": E, "roofline": roof}
+
+    # per-kernel rates of the TP / scatter kernels (a separate pass per kernel, outside the timed region)
+    if table:
+        kt_steps = max(3, min(steps, 10))
+        rates = {}
+        for k in w["table"]:
+            with _lib.KernelTimer(k) as t:
+                for _ in range(kt_steps):
+                    step()
+                torch.cuda.synchronize()
+            if t.launches:
+                rates[k] = dict(_rate(work_of(k), t.total_ms / t.launches), launches_per_step=t.launches // kt_steps)
+        out["kernels"] = rates
+
+    # the reference-signature forward: the graph is prepared inside every call
+    kw = {"external_tensor": field} if field is not None else {}
+
+    def ref_step():
+        p = pos.detach().requires_grad_(True)
+        en = model(p, A, batch, src, dst, shifts, cell, **kw)
+        (g,) = torch.autograd.grad(en.sum(), p)
+        return en, g
+
+    for _ in range(2):
+        ref_step()
+    torch.cuda.synchronize()
+    rs = max(3, steps // 2)
+    t0 = time.perf_counter()
+    for _ in range(rs):
+        ref_step()
+    torch.cuda.synchronize()
+    out["ms_per_step_with_graph_prepare"] = round((time.perf_counter() - t0) * 1000 / rs, 4)
+    out["graph_prepare_ms"] = {"cold": round(t_cold * 1000, 3), "warm_median": round(statistics.median(warm) * 1000, 3)}
+
+    out["parity"] = parity_vs_fixture(mode, system, seed, e.cpu().numpy(), f.cpu().numpy(),
+                                      None if dip is None else dip.cpu().numpy())
+    out["products"] = PRODUCTS[mode]
+    out["config"] = {"workload": workload_name(mode, N, E), "mode": mode, "atoms": N, "edges": E}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,8 +440,11 @@ def main():
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--roofline-kernel", default=None)
     ap.add_argument("--cpu-atoms", type=int, default=None)
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the selected workload (by default the sparse headline also runs ICTD 10k and ICTD-O3 4k)")
+    ap.add_argument("--no-kernel-table", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, copy a 1 GiB fp32 buffer 3 times (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -215,110 +456,32 @@ def main():
     n_atoms = w["atoms"] if args.atoms is None else args.atoms
     seed = w["seed"] if args.seed is None else args.seed
     kname = w["kernel"] if args.roofline_kernel is None else args.roofline_kernel
-    sparse = args.mode == "sparse"
 
     import torch
-    from fsctep_amd import _lib
-
     dev = torch.device("cuda:0")
-    t_build = time.perf_counter()
-    system = _system(args.mode, n_atoms, seed)
-    print(f"[bench] {args.mode}: {system.num_atoms} atoms, {system.num_edges} edges "
-          f"({time.perf_counter() - t_build:.1f} s to build)", file=sys.stderr, flush=True)
-    model = build_model(args.mode, dev)
-    C = w["channels"]
-
-    pos = torch.tensor(system.pos, dtype=torch.float32, device=dev)
-    A = torch.tensor(system.species, device=dev)
-    batch = torch.zeros(system.num_atoms, dtype=torch.long, device=dev)
-    cell = torch.tensor(system.cell, dtype=torch.float32, device=dev)
-    t_g = time.perf_counter()
-    graph = model.prepare(torch.tensor(system.edge_src, device=dev), torch.tensor(system.edge_dst, device=dev),
-                          torch.tensor(system.edge_shifts, dtype=torch.float32, device=dev),
-                          system.num_atoms, A)
-    torch.cuda.synchronize()
-    t_graph = time.perf_counter() - t_g
-    if sparse:
-        from fsctep_amd.sparse import energy_and_forces
-
-        def step():
-            return energy_and_forces(model, pos, batch, cell, graph)
-    else:
-        from fsctep_amd.ictd import energy_forces
-        field = (torch.tensor(_field(1, seed), dtype=torch.float32, device=dev)
-                 if args.mode == "ictd-o3" else None)
-
-        def step():
-            return energy_forces(model, pos, batch, cell, graph, external_tensor=field)
-
-    for i in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    print(f"[bench] warm-up done ({args.warmup} steps)", file=sys.stderr, flush=True)
-
-    # timed region: exactly `steps` steps, synchronised on both sides
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    with _lib.KernelTimer(kname) as kt:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        ev[0].record()
-        for i in range(args.steps):
-            res = step()
-            ev[i + 1].record()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-    e, f = res[0], res[1]
-    step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
-    ms_per_step = elapsed * 1000.0 / args.steps
-    assert torch.isfinite(e).all() and torch.isfinite(f).all()
-    print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step (median {statistics.median(step_ms):.3f}); "
-          f"E={float(e.sum()):.6f} max|F|={float(f.abs().max()):.4f}", file=sys.stderr, flush=True)
-
-    N, E = system.num_atoms, system.num_edges
-    if sparse:
-        work = sparse_kernel_work(kname, N, E, C)
-    else:
-        from fsctep_amd import ictd_ops
-        work = ictd_kernel_work(kname, ictd_ops.layout_struct(model.layout_id), N, E, C)
-    avg_ms = kt.total_ms / max(kt.launches, 1)
-    if work["bound"] == "mfma":
-        achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4)}
-    else:
-        achieved = work["bytes"] / (avg_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4)}
-    roof["traffic"] = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{kname}_{args.mode}{N}.json")
-    if os.path.exists(tfile):
-        with open(tfile) as fh:
-            tinfo = json.load(fh)
-        src = os.path.join(ROOT, tinfo.get("source", ""))
-        if os.path.isfile(src) and hashlib.sha256(open(src, "rb").read()).hexdigest() == tinfo.get("source_sha256"):
-            roof["traffic"] = tinfo.get("hbm_bytes_per_launch")   # measured for this exact kernel source
-    roof["kernel"] = kname
-    roof["avg_launch_ms"] = round(avg_ms, 4)
-    roof["launches"] = kt.launches
-    roof["algorithmic_per_launch"] = {"flops": work["flops"], "bytes": work["bytes"]}
-
+    head = measure(args.mode, n_atoms, seed, args.steps, args.warmup, kname, dev, table=not args.no_kernel_table)
+    N, E = head["atoms"], head["edges"]
     out = {
         "metric": "atom-steps/sec (energy+forces) at 10k atoms; TP kernel HBM GB/s vs peak",
-        "value": round(N / (ms_per_step * 1e-3), 1),
+        "value": head["value"],
         "unit": "atom-steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "median_ms_per_step": round(statistics.median(step_ms), 4),
+        "ms_per_step": head["ms_per_step"],
+        "median_ms_per_step": head["median_ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
+        "products": head["products"],
         "data": "synthetic (seeded random sequential addition, random-init seeded parameters)",
-        "config": {"workload": workload_name(args.mode, N, E), "mode": args.mode,
-                   "atoms": N, "edges": E, "graph_prep_ms_untimed": round(t_graph * 1000, 2)},
-        "roofline": roof,
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "kernels": head.get("kernels"),
+        "ms_per_step_with_graph_prepare": head["ms_per_step_with_graph_prepare"],
+        "graph_prepare_ms": head["graph_prepare_ms"],
+        "parity": head["parity"],
         "gpu": gpu_info(),
     }
     if args.copy_calibration:
@@ -328,11 +491,30 @@ def main():
             dst_buf.copy_(src_buf)
         torch.cuda.synchronize()
         del src_buf, dst_buf
+
+    extra = []
+    if not args.no_extra and args.mode == "sparse" and args.atoms is None:
+        extra = ["ictd", "ictd-o3"]
+    workloads = {}
+    for m in extra:
+        wm = WORKLOADS[m]
+        r = measure(m, wm["atoms"], wm["seed"], args.steps, args.warmup, wm["kernel"], dev,
+                    table=not args.no_kernel_table)
+        r.pop("atoms")
+        r.pop("edges")
+        workloads[m] = r
+    if workloads:
+        out["workloads"] = workloads
+
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         cpu_atoms = w["cpu_atoms"] if args.cpu_atoms is None else args.cpu_atoms
         out["cpu_baseline"] = cpu_baseline(args.mode, cpu_atoms, args.cpu_steps, seed)
         out["cpu_baseline"]["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+        for m, r in workloads.items():
+            wm = WORKLOADS[m]
+            r["cpu_baseline"] = cpu_baseline(m, wm["cpu_atoms"], args.cpu_steps, wm["seed"])
+            r["cpu_baseline"]["gpu_over_cpu"] = round(r["value"] / r["cpu_baseline"]["value"], 1)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -22,15 +22,15 @@ SIGNATURES = {
     "fsc_timing_end": [ctypes.POINTER(ctypes.c_double), _pi64],
     "fsc_sparse_conv_workspace": [_i64, _i64, _i32, _pi64, _pi64],
     "fsc_sparse_conv_prepare_weights": [_p, _p, _i32, _p, _p, _p],
-    "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p],
+    "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p],
     "fsc_sparse_conv_backward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f32,
-                                 _p, _p, _p, _p, _p],
+                                 _p, _p, _p, _p, _p, _p],
     "fsc_sparse_conv1_pair_table": [_p, _p, _p, _i32, _i32, _p, _p, _p],
     "fsc_sparse_conv1_forward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_sparse_conv1_backward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
-    "fsc_ictd_conv_forward": [_p, _i64, _i64, _i32] + [_p] * 10,
+    "fsc_ictd_conv_forward": [_p, _i64, _i64, _i32] + [_p] * 11,
     "fsc_ictd_prepare_weights": [_p, _i32, _i32, _p, _p],
-    "fsc_ictd_conv_backward": [_p, _i64, _i64, _i32] + [_p] * 16,
+    "fsc_ictd_conv_backward": [_p, _i64, _i64, _i32] + [_p] * 17,
     "fsc_ictd_conv1_forward": [_p, _i64, _i64, _i32, _i32] + [_p] * 8,
     "fsc_ictd_conv1_backward": [_p, _i64, _i64, _i32, _i32] + [_p] * 10,
     "fsc_gram_sizes": [_i64, _i32, _i32, _pi64, _pi64, _pi64],
@@ -48,6 +48,8 @@ SIGNATURES = {
     "fsc_graph_sizes": [_i64, _i64, _i32, _pi64, _pi64],
     "fsc_graph_prepare": [_i64, _i64, _i32] + [_p] * 15,
     "fsc_graph_prepare_noalloc": [_i64, _i64, _i32] + [_p] * 14,
+    "fsc_spatial_order_workspace": [_i64, _pi64],
+    "fsc_spatial_order": [_i64, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_forward": [_i64, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_backward": [_i64, _p, _p, _p, _p, _p, _p, _p],
 }

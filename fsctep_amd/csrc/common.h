@@ -138,6 +138,21 @@ __device__ __forceinline__ float group_sum(float v, int width) {
   return v;
 }
 
+// One-block-per-node launches over xcd_grid(n) workgroups.  Workgroup w runs on XCD w % 8, so XCD x
+// is given the contiguous run [x*per, (x+1)*per) of the node order; with a spatial order (nodes close
+// in space close in the order) the neighbour gathers of the blocks an XCD runs together then share its
+// L2.  `order` null: the identity.  Returns -1 for the padding workgroups (block-uniform).
+inline unsigned xcd_grid(int64_t n) { return (unsigned)(((n + 7) / 8) * 8); }
+__device__ __forceinline__ int xcd_node(int64_t n, const int32_t* __restrict__ order) {
+  const int64_t per = (n + 7) / 8;
+  const int64_t w = blockIdx.x;
+  const int64_t li = (w & 7) * per + (w >> 3);
+  if (li >= n) return -1;
+  if (!order) return (int)li;
+  const int v = order[li];
+  return (v >= 0 && v < n) ? v : -1;   // a malformed order leaves nodes unprocessed, never out of bounds
+}
+
 void set_error(const std::string& msg);
 int check_launch(const char* what);
 int timing_mark_begin(const char* kernel, hipStream_t st);

@@ -306,6 +306,121 @@ __global__ __launch_bounds__(64) void pair_chunk_place_kernel(int64_t E, int nch
 
 unsigned grid_of(int64_t n) { return (unsigned)((n + 255) / 256); }
 
+// ---------------------------------------------------------------- spatial node order
+// A permutation of the atoms along a Morton (Z-order) curve over a G x G x G grid spanning the bounding
+// box of the positions (G the smallest power of two with 2 G^3 >= N, at most 256), atoms of one cell in
+// ascending id: a counting sort by cell with the same place-then-rank step as the receiver sort, so the
+// order is deterministic.  Kernels that run one block per node walk this order, XCD by XCD, so that the
+// blocks an XCD runs together gather the features of the same neighbourhood.  Degenerate positions
+// (all equal, e.g. the zero positions of an edge-vector caller) give the identity; non-finite ones cell 0.
+__global__ __launch_bounds__(1024) void bbox_kernel(int64_t N, const float* __restrict__ pos, float* __restrict__ box) {
+  __shared__ float red[16][6];
+  float v[6] = {INFINITY, INFINITY, INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int64_t i = threadIdx.x; i < N; i += 1024) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const float x = pos[3 * i + k];
+      if (isfinite(x)) {
+        v[k] = fminf(v[k], x);
+        v[3 + k] = fmaxf(v[3 + k], x);
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    for (int off = 32; off > 0; off >>= 1) {
+      const float o = __shfl_xor(v[k], off, 64);
+      v[k] = k < 3 ? fminf(v[k], o) : fmaxf(v[k], o);
+    }
+    if (lane == 0) red[wave][k] = v[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const int k = threadIdx.x;
+    float r = red[0][k];
+    for (int w = 1; w < 16; ++w) r = k < 3 ? fminf(r, red[w][k]) : fmaxf(r, red[w][k]);
+    box[k] = r;
+  }
+}
+
+__device__ __forceinline__ uint32_t spread3(uint32_t v) {   // bit b of v (b < 8) to bit 3b
+  v &= 0xffu;
+  v = (v | (v << 8)) & 0x0f00fu;
+  v = (v | (v << 4)) & 0x0c30c3u;
+  v = (v | (v << 2)) & 0x249249u;
+  return v;
+}
+
+__global__ __launch_bounds__(256) void cell_kernel(int64_t N, const float* __restrict__ pos,
+                                                   const float* __restrict__ box, int G,
+                                                   int32_t* __restrict__ code, int32_t* __restrict__ cnt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N) return;
+  uint32_t c[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const float lo = box[k], hi = box[3 + k];
+    const float t = (hi > lo) ? (pos[3 * i + k] - lo) * ((float)G / (hi - lo)) : 0.f;
+    const float tc = fminf(fmaxf(t, 0.f), (float)(G - 1));   // NaN -> 0
+    c[k] = (uint32_t)tc;
+  }
+  const int32_t m = (int32_t)(spread3(c[0]) | (spread3(c[1]) << 1) | (spread3(c[2]) << 2));
+  code[i] = m;
+  atomicAdd(cnt + m, 1);
+}
+
+__global__ __launch_bounds__(256) void place_cell_kernel(int64_t N, const int32_t* __restrict__ code,
+                                                         const int32_t* __restrict__ cell_ptr,
+                                                         int32_t* __restrict__ cursor, int32_t* __restrict__ tmp) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N) return;
+  const int32_t c = code[i];
+  tmp[cell_ptr[c] + atomicAdd(cursor + c, 1)] = (int32_t)i;
+}
+
+__global__ __launch_bounds__(256) void rank_cell_kernel(int64_t N, const int32_t* __restrict__ code,
+                                                        const int32_t* __restrict__ cell_ptr,
+                                                        const int32_t* __restrict__ tmp, int32_t* __restrict__ order) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= N) return;
+  const int32_t i = tmp[p];
+  const int32_t c = code[i];
+  const int32_t a = cell_ptr[c], b = cell_ptr[c + 1];
+  int32_t rank = 0;
+  for (int32_t q = a; q < b; ++q) rank += tmp[q] < i;
+  order[a + rank] = i;
+}
+
+int order_grid(int64_t N) {
+  int G = 1;
+  while (G < 256 && 2LL * G * G * G < N) G *= 2;
+  return G;
+}
+
+struct OrderWs {
+  int64_t box, cnt, cur, cell_ptr, tot, code, tmp, total, cells, nb;
+};
+
+OrderWs order_ws(int64_t N) {
+  OrderWs w;
+  const int64_t G = order_grid(N);
+  w.cells = G * G * G;
+  w.nb = (w.cells + 1 + SCAN_TILE - 1) / SCAN_TILE;
+  int64_t o = 0;
+  w.cnt = o;      o += w.cells;
+  w.cur = o;      o += w.cells;    // the zero-filled prefix ends here
+  w.box = o;      o += 8;
+  w.cell_ptr = o; o += w.cells + 1;
+  w.tot = o;      o += w.nb;
+  w.code = o;     o += N;
+  w.tmp = o;      o += N;
+  w.total = o;
+  return w;
+}
+
+
+
 struct WsLayout {
   int64_t cnt_in, cnt_out, cur_in, cur_out, tot, pcnt, tstart, cnt_blk, tmp, total, nchunk;
 };
@@ -427,6 +542,39 @@ int fsc_graph_sizes(int64_t n_nodes, int64_t n_edges, int32_t n_species, int64_t
   *n_tiles_max = n_species > 0 ? (n_edges + 15) / 16 + (int64_t)n_species * n_species : 0;
   *workspace_ints = fsc::ws_layout(n_nodes, n_edges, n_species).total;
   return 0;
+}
+
+int fsc_spatial_order_workspace(int64_t n_nodes, int64_t* workspace_ints) {
+  FSC_CHECK_ARG(workspace_ints, "fsc_spatial_order_workspace: null pointer");
+  FSC_CHECK_ARG(n_nodes >= 0 && n_nodes < (1LL << 31) - 1, "fsc_spatial_order_workspace: bad node count");
+  *workspace_ints = fsc::order_ws(n_nodes).total;
+  return 0;
+}
+
+int fsc_spatial_order(int64_t n_nodes, const float* pos, int32_t* order, int32_t* workspace, hipStream_t stream) {
+  using namespace fsc;
+  FSC_CHECK_ARG(n_nodes >= 0 && n_nodes < (1LL << 31) - 1, "fsc_spatial_order: bad node count");
+  if (n_nodes == 0) return 0;
+  FSC_CHECK_ARG(pos && order && workspace, "fsc_spatial_order: null pointer");
+  const int64_t N = n_nodes;
+  const OrderWs w = order_ws(N);
+  FSC_CHECK_ARG(w.nb <= SCAN_MAX_BLOCKS, "fsc_spatial_order: too many cells for the scan");
+  int32_t* ws = workspace;
+  float* box = reinterpret_cast<float*>(ws + w.box);
+  fill_i32_kernel<<<grid_of(w.box) < 1024 ? grid_of(w.box) : 1024, 256, 0, stream>>>(ws, w.box, 0);
+  bbox_kernel<<<1, 1024, 0, stream>>>(N, pos, box);
+  cell_kernel<<<grid_of(N), 256, 0, stream>>>(N, pos, box, order_grid(N), ws + w.code, ws + w.cnt);
+  ScanArgs sa;
+  sa.cnt[0] = sa.cnt[1] = ws + w.cnt;
+  sa.out[0] = sa.out[1] = ws + w.cell_ptr;
+  sa.tot[0] = sa.tot[1] = ws + w.tot;
+  sa.n = w.cells;
+  scan_blocks_kernel<<<dim3((unsigned)w.nb, 1), SCAN_T, 0, stream>>>(sa);
+  scan_totals_kernel<<<dim3(1, 1), 1024, 0, stream>>>(sa, (int)w.nb);
+  scan_add_kernel<<<dim3((unsigned)w.nb, 1), SCAN_T, 0, stream>>>(sa);
+  place_cell_kernel<<<grid_of(N), 256, 0, stream>>>(N, ws + w.code, ws + w.cell_ptr, ws + w.cur, ws + w.tmp);
+  rank_cell_kernel<<<grid_of(N), 256, 0, stream>>>(N, ws + w.code, ws + w.cell_ptr, ws + w.tmp, order);
+  return check_launch("fsc_spatial_order") ? 2 : 0;
 }
 
 int fsc_graph_prepare(int64_t n_nodes, int64_t n_edges, int32_t n_species, const int64_t* edge_src,

@@ -189,7 +189,8 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
                                                           const float* __restrict__ cg,
                                                           const int32_t* __restrict__ dst_ptr,
                                                           const int32_t* __restrict__ esrc,
-                                                          float* __restrict__ Z, float* __restrict__ zscale) {
+                                                          float* __restrict__ Z, float* __restrict__ zscale,
+                                                          int64_t n_nodes, const int32_t* __restrict__ node_order) {
   constexpr int SPAN = C < 64 ? C : 64;
   constexpr int V = SPAN / 16;
   extern __shared__ __align__(16) float smem[];
@@ -203,7 +204,8 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
   int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
   float* bg = smem + sm.bg;
 
-  const int n = blockIdx.x;
+  const int n = xcd_node(n_nodes, node_order);
+  if (n < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
@@ -461,7 +463,8 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
                                                           const int32_t* __restrict__ dst_ptr,
                                                           const int32_t* __restrict__ esrc,
                                                           float* __restrict__ DX, float* __restrict__ dgates,
-                                                          float* __restrict__ dY) {
+                                                          float* __restrict__ dY, int64_t n_nodes,
+                                                          const int32_t* __restrict__ node_order) {
   constexpr int SPAN = C < 64 ? C : 64;
   constexpr int V = SPAN / 16;
   constexpr int NSPAN = C / SPAN;
@@ -477,7 +480,8 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
   int* tmap = reinterpret_cast<int*>(smem + sm.tmap);
   int* toff = reinterpret_cast<int*>(smem + sm.toff);
 
-  const int n = blockIdx.x;
+  const int n = xcd_node(n_nodes, node_order);
+  if (n < 0) return;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   if (beg == end) return;                               // uniform over the block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -900,13 +904,13 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
 template <int C>
 int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
               const float* Y, const float* gates, const float* cg, const float* W, float* Z, float* out,
-              hipStream_t st) {
+              const int32_t* node_order, hipStream_t st) {
   const int ncg = cg_length(L);
   {
     LaunchTimer tm("ictd_project", st);
     const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
-    project_fwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
-                                                          Z + N * L.KT * C);
+    project_fwd_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
+                                                          Z + N * L.KT * C, N, node_order);
   }
   if (check_launch("ictd project_fwd")) return 2;
   int dmax = 1;
@@ -925,7 +929,7 @@ template <int C>
 int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc,
                const int32_t* src_ptr, const int32_t* src_perm, const float* G, const float* x, const float* Y,
                const float* gates, const float* cg, const float* Wt, float* dZ, float* DX, float* dx,
-               float* dgates, float* dY, hipStream_t st) {
+               float* dgates, float* dY, const int32_t* node_order, hipStream_t st) {
   int dmax = 1;
   for (int p = 0; p < L.NP; ++p) dmax = max(dmax, L.p_d3[p]);
   {
@@ -943,8 +947,8 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
     LaunchTimer tm("ictd_project_grad", st);
     const int ncg = cg_length(L);
     const size_t lds = (size_t)proj_smem(L, ncg, true).total * sizeof(float);
-    project_bwd_kernel<C><<<(unsigned)N, 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, DX, dgates,
-                                                          dY);
+    project_bwd_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, DX, dgates,
+                                                          dY, N, node_order);
   }
   if (check_launch("ictd project_bwd")) return 2;
   {
@@ -965,7 +969,7 @@ extern "C" {
 int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                           const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
                           const float* gates, const float* cg, const float* W, float* z_ws, float* out,
-                          hipStream_t stream) {
+                          const int32_t* node_order, hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv_forward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv_forward: bad size");
@@ -973,9 +977,9 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
   FSC_CHECK_ARG(n_edges == 0 || (edge_src && Y && gates), "fsc_ictd_conv_forward: null edge pointer");
   if (n_nodes == 0) return 0;
   const FscIctdLayout& L = *layout;
-  if (channels == 128) return forward_c<128>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, stream);
-  if (channels == 64) return forward_c<64>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, stream);
-  return forward_c<32>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, stream);
+  if (channels == 128) return forward_c<128>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
+  if (channels == 64) return forward_c<64>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
+  return forward_c<32>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
 }
 
 int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wt, hipStream_t stream) {
@@ -991,7 +995,8 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
                            const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
                            const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
                            const float* gates, const float* cg, const float* Wt, float* dz_ws,
-                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, hipStream_t stream) {
+                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, const int32_t* node_order,
+                           hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv_backward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv_backward: bad size");
@@ -1003,12 +1008,12 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
   const FscIctdLayout& L = *layout;
   if (channels == 128)
     return backward_c<128>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                           dxe_ws, grad_x, grad_gates, grad_Y, stream);
+                           dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
   if (channels == 64)
     return backward_c<64>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                          dxe_ws, grad_x, grad_gates, grad_Y, stream);
+                          dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
   return backward_c<32>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                        dxe_ws, grad_x, grad_gates, grad_Y, stream);
+                        dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
 }
 
 int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,

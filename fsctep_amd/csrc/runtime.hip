@@ -95,6 +95,6 @@ int fsc_timing_end(double* total_ms, int64_t* launches) {
 
 const char* fsc_last_error(void) { return fsc::g_last_error.c_str(); }
 
-int fsc_abi_version(void) { return 1; }
+int fsc_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -420,11 +420,13 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
                                                            const float* __restrict__ S,
                                                            const int32_t* __restrict__ src_ptr,
                                                            const int32_t* __restrict__ src_perm,
-                                                           float* __restrict__ P) {
+                                                           float* __restrict__ P, int64_t n_nodes,
+                                                           const int32_t* __restrict__ node_order) {
   constexpr int HR = KH + 8;   // bf16 per LDS row: 64 + 8 padding
   __shared__ __align__(16) __bf16 hs3[3][EP][HR];
   __shared__ int32_t eids[EP];
-  const int m = blockIdx.x;
+  const int m = xcd_node(n_nodes, node_order);
+  if (m < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int beg = src_ptr[m], end = src_ptr[m + 1];
@@ -606,7 +608,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
     const float* __restrict__ S, const float* __restrict__ P, const int32_t* __restrict__ src_ptr,
     const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst, float scale,
     float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, float* __restrict__ dscale,
-    int64_t n_nodes) {
+    int64_t n_nodes, const int32_t* __restrict__ node_order) {
   constexpr int CC = 8;              // channels per chunk
   constexpr int NCH = C / CC;
   constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
@@ -619,7 +621,8 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   __shared__ float ns[EP][3];
   __shared__ float dnacc[EP][3];
   __shared__ float amx[4];
-  const int m = blockIdx.x;
+  const int m = xcd_node(n_nodes, node_order);
+  if (m < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int beg = src_ptr[m], end = src_ptr[m + 1];
@@ -1106,7 +1109,7 @@ template <int C>
 int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_t* src_ptr,
                       const int32_t* src_perm, const float* x, const float* h, const float* nvec,
                       const float* bk1, float scale, float* S, float* P, float* out,
-                      hipStream_t st) {
+                      const int32_t* node_order, hipStream_t st) {
   if (N == 0) return 0;
   {
     PathTiles tiles;
@@ -1121,7 +1124,7 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
   if (check_launch("sparse node_expand")) return 2;
   {
     LaunchTimer tm("edge_message", st);
-    edge_message_kernel<C><<<(unsigned)N, 192, 0, st>>>(h, S, src_ptr, src_perm, P);
+    edge_message_kernel<C><<<xcd_grid(N), 192, 0, st>>>(h, S, src_ptr, src_perm, P, N, node_order);
   }
   if (check_launch("sparse edge_message")) return 2;
   {
@@ -1136,7 +1139,7 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        const int32_t* src_perm, const int32_t* edge_dst, const float* G,
                        const float* h, const float* nvec, const float* bk6, const float* S,
                        const float* P, float scale, float* dS, float* dx, float* dh, float* dn,
-                       hipStream_t st) {
+                       const int32_t* node_order, hipStream_t st) {
   if (N == 0) return 0;
   // workspace tail (2 x 18 x N x C floats): first the chunk-major receiver gradient (13 x N x C), later
   // the partial input gradients of node_expand_grad; then N per-node scales of dS
@@ -1145,8 +1148,8 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   {
     LaunchTimer tm("edge_message_grad", st);
-    edge_message_grad_kernel<C><<<(unsigned)N, 256, 0, st>>>(tail, nvec, h, S, P, src_ptr, src_perm,
-                                                             edge_dst, scale, dh, dS, dn, dscale, N);
+    edge_message_grad_kernel<C><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, h, S, P, src_ptr, src_perm,
+                                                              edge_dst, scale, dh, dS, dn, dscale, N, node_order);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
   {
@@ -1203,17 +1206,17 @@ int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                             const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                             const float* x, const float* h, const float* n, const float* bk1,
                             float inv_norm, float* s_ws, float* p_ws, float* out,
-                            hipStream_t stream) {
+                            const int32_t* node_order, hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_forward: negative size");
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_forward: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && src_ptr && x && bk1 && s_ws && out, "fsc_sparse_conv_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && h && n && p_ws), "fsc_sparse_conv_forward: null edge pointer");
   if (channels == 64)
     return conv_forward_impl<64>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm,
-                                 s_ws, p_ws, out, stream);
+                                 s_ws, p_ws, out, node_order, stream);
   if (channels == 32)
     return conv_forward_impl<32>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm,
-                                 s_ws, p_ws, out, stream);
+                                 s_ws, p_ws, out, node_order, stream);
   set_error("fsc_sparse_conv_forward: channels must be 32 or 64");
   return 1;
 }
@@ -1223,7 +1226,7 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              const int32_t* edge_dst, const float* grad_out, const float* h,
                              const float* n, const float* bk6, const float* s_ws, const float* p_ws,
                              float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
-                             float* grad_n, hipStream_t stream) {
+                             float* grad_n, const int32_t* node_order, hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_backward: negative size");
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_backward: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && bk6 && s_ws && ds_ws && grad_x,
@@ -1232,10 +1235,10 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                 "fsc_sparse_conv_backward: null edge pointer");
   if (channels == 64)
     return conv_backward_impl<64>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n,
-                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, stream);
+                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, node_order, stream);
   if (channels == 32)
     return conv_backward_impl<32>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n,
-                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, stream);
+                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, node_order, stream);
   set_error("fsc_sparse_conv_backward: channels must be 32 or 64");
   return 1;
 }

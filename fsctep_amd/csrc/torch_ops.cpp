@@ -50,6 +50,14 @@ const float* cf(const Tensor& t) { return t.numel() ? t.data_ptr<float>() : null
 float* mf(Tensor& t) { return t.numel() ? t.data_ptr<float>() : nullptr; }
 const int32_t* ci(const Tensor& t) { return t.numel() ? t.data_ptr<int32_t>() : nullptr; }
 
+// node_order: empty (the identity) or an int32 permutation of the N nodes (spatial_order)
+const int32_t* order_ptr(const Tensor& order, int64_t N) {
+  if (order.numel() == 0) return nullptr;
+  TORCH_CHECK(order.scalar_type() == at::kInt && order.dim() == 1 && order.size(0) == N && order.is_contiguous(),
+              "node_order must be empty or a contiguous int32 permutation of the ", N, " nodes");
+  return order.data_ptr<int32_t>();
+}
+
 at::TensorOptions fopts(const Tensor& like) { return like.options().dtype(at::kFloat); }
 
 // Layout tables (FscIctdLayout, FscReadoutTable, FscHarmTable) travel as int[] arguments holding the
@@ -93,8 +101,8 @@ std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, con
 std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,
                                                const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                const Tensor& src_ptr, const Tensor& src_perm,
-                                               const Tensor& edge_dst) {
-  require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst});
+                                               const Tensor& edge_dst, const Tensor& node_order) {
+  require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == 13, "x must be (N, 13, C)");
   const int64_t N = x_.size(0), C = x_.size(2), E = h_.size(0);
   Tensor x = f32c(x_), h = f32c(h_), n = f32c(n_);
@@ -103,14 +111,14 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
   Tensor S = at::empty({s_f}, fopts(x)), P = at::empty({p_f}, fopts(x)), out = at::empty({N, 13, C}, fopts(x));
   check(fsc_sparse_conv_forward(N, E, (int32_t)C, ci(dp), ci(sp), ci(pm), cf(x), cf(h), cf(n), cf(bk1),
-                                avg_degree_inv(N, E), mf(S), mf(P), mf(out), stream_of(x)),
+                                avg_degree_inv(N, E), mf(S), mf(P), mf(out), order_ptr(node_order, N), stream_of(x)),
         "fsc_sparse_conv_forward");
   return {out, S, P};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tensor& h, const Tensor&, const Tensor&,
                                                     const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                    const Tensor&) {
+                                                    const Tensor&, const Tensor&) {
   const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
   int64_t s_f = 0, p_f = 0;
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
@@ -120,8 +128,9 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tenso
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_, const Tensor& n_,
                                                         const Tensor& bk6, const Tensor& S, const Tensor& P,
                                                         const Tensor& dst_ptr, const Tensor& src_ptr,
-                                                        const Tensor& src_perm, const Tensor& edge_dst) {
-  require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
+                                                        const Tensor& src_perm, const Tensor& edge_dst,
+                                                        const Tensor& node_order) {
+  require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
   Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_);
   Tensor dS = at::empty_like(S), dx = at::empty({N, 13, C}, fopts(g)), dh = at::empty({E, KH}, fopts(g)),
@@ -129,14 +138,14 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
   check(fsc_sparse_conv_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(src_ptr, "src_ptr")),
                                  ci(i32c(src_perm, "src_perm")), ci(i32c(edge_dst, "edge_dst")), cf(g), cf(h), cf(n),
                                  cf(bk6), cf(S), cf(P), avg_degree_inv(N, E), mf(dS), mf(dx), mf(dh), mf(dn),
-                                 stream_of(g)),
+                                 order_ptr(node_order, N), stream_of(g)),
         "fsc_sparse_conv_backward");
   return {dx, dh, dn};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h, const Tensor&,
                                                              const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                             const Tensor&, const Tensor&, const Tensor&) {
+                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&) {
   const int64_t E = h.size(0);
   return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h))};
 }
@@ -216,8 +225,8 @@ Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({ictd_weigh
 
 Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
                  const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                 const Tensor& src_perm, at::IntArrayRef layout) {
-  require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+                 const Tensor& src_perm, const Tensor& node_order, at::IntArrayRef layout) {
+  require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
   const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
   const FscIctdLayout* L = &Lv;
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
@@ -228,13 +237,14 @@ Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const
   // z: N*KT*C floats of projections, then N per-node scales
   Tensor z = at::empty({N * L->KT * C + N}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
   check(fsc_ictd_conv_forward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
-                              cf(x), cf(Y), cf(gates), cf(cg), cf(Wt), mf(z), mf(out), stream_of(x)),
+                              cf(x), cf(Y), cf(gates), cf(cg), cf(Wt), mf(z), mf(out), order_ptr(node_order, N),
+                              stream_of(x)),
         "fsc_ictd_conv_forward");
   return out;
 }
 
 Tensor ictd_conv_meta(const Tensor& x, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef) {
+                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef) {
   return at::empty(x.sizes(), fopts(x));
 }
 
@@ -242,8 +252,8 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
                                                       const Tensor& gates_, const Tensor& Wt, const Tensor& cg,
                                                       const Tensor& dst_ptr, const Tensor& edge_src,
                                                       const Tensor& src_ptr, const Tensor& src_perm,
-                                                      at::IntArrayRef layout) {
-  require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+                                                      const Tensor& node_order, at::IntArrayRef layout) {
+  require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
   const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
   const FscIctdLayout* L = &Lv;
   const int64_t N = x_.size(0), M = x_.size(1), C = x_.size(2), E = Y_.size(0);
@@ -254,7 +264,8 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
   Tensor dgates = at::zeros({E, L->NREF}, fopts(x)), dY = at::empty({E, L->NY}, fopts(x));
   check(fsc_ictd_conv_backward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
                                ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")), cf(g), cf(x), cf(Y),
-                               cf(gates), cf(cg), cf(Wt), mf(dz), mf(dxe), mf(dx), mf(dgates), mf(dY), stream_of(x)),
+                               cf(gates), cf(cg), cf(Wt), mf(dz), mf(dxe), mf(dx), mf(dgates), mf(dY),
+                               order_ptr(node_order, N), stream_of(x)),
         "fsc_ictd_conv_backward");
   return {dx, dgates, dY};
 }
@@ -262,7 +273,7 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
 std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward_meta(const Tensor&, const Tensor& x, const Tensor& Y,
                                                            const Tensor& gates, const Tensor&, const Tensor&,
                                                            const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                           at::IntArrayRef) {
+                                                           const Tensor&, at::IntArrayRef) {
   return {at::empty(x.sizes(), fopts(x)), at::empty(gates.sizes(), fopts(gates)), at::empty(Y.sizes(), fopts(Y))};
 }
 
@@ -552,6 +563,24 @@ std::vector<Tensor> graph_prepare_meta(const Tensor& edge_src, const Tensor&, co
           at::empty({17 * T}, io), at::empty({1}, io)};
 }
 
+// Spatial order of the atoms (fsc_spatial_order): the node_order argument of the conv ops.
+Tensor spatial_order(const Tensor& pos_) {
+  require_gpu({pos_});
+  TORCH_CHECK(pos_.dim() == 2 && pos_.size(1) == 3, "spatial_order: pos must be (N, 3)");
+  const int64_t N = pos_.size(0);
+  Tensor pos = f32c(pos_);
+  int64_t ws_n = 0;
+  check(fsc_spatial_order_workspace(N, &ws_n), "fsc_spatial_order_workspace");
+  const auto io = pos.options().dtype(at::kInt);
+  Tensor order = at::empty({N}, io), ws = at::empty({ws_n}, io);
+  check(fsc_spatial_order(N, cf(pos), N ? order.data_ptr<int32_t>() : nullptr, ws.data_ptr<int32_t>(),
+                          stream_of(pos)),
+        "fsc_spatial_order");
+  return order;
+}
+
+Tensor spatial_order_meta(const Tensor& pos) { return at::empty({pos.size(0)}, pos.options().dtype(at::kInt)); }
+
 // ============================================================== geometry from caller-supplied edge vectors
 
 std::tuple<Tensor, Tensor> edge_vec_geometry(const Tensor& edge_vec_, const Tensor& order) {
@@ -741,27 +770,27 @@ void refuse_param_grad(AutogradContext* ctx, std::initializer_list<int> idx, con
 
 struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
-                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst) {
+                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&,
                                                                   const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&, const Tensor&, const Tensor&)>(
-        "fsctep::sparse_conv");
-    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst);
-    ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst});
+                                                                  const Tensor&, const Tensor&, const Tensor&,
+                                                                  const Tensor&)>("fsctep::sparse_conv");
+    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order);
+    ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
     ctx->mark_non_differentiable({S, P});
     ctx->set_materialize_grads(false);   // S and P are saved workspaces: no zero-filled gradients for them
     return {out, S, P};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(9);
+    variable_list res(10);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {3, 4}, "the sparse conv");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&)>("fsctep::sparse_conv_backward");
-    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8]);
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&)>("fsctep::sparse_conv_backward");
+    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9]);
     res[0] = dx;
     res[1] = dh;
     res[2] = dn;
@@ -772,8 +801,8 @@ struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const Tensor& h, const Tensor& n,
                                                         const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                         const Tensor& src_ptr, const Tensor& src_perm,
-                                                        const Tensor& edge_dst) {
-  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst);
+                                                        const Tensor& edge_dst, const Tensor& node_order) {
+  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order);
   return {r[0], r[1], r[2]};
 }
 
@@ -812,27 +841,27 @@ std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& 
 
 struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg,
-                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm,
+                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order,
                                std::vector<int64_t> layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                       const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      at::IntArrayRef)>("fsctep::ictd_conv");
-    Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout);
-    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm});
+                                      const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv");
+    Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout);
+    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
     ctx->saved_data["layout"] = layout;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(11);
+    variable_list res(12);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {3, 4, 5}, "the ICTD conv");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv_backward");
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv_backward");
     const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
-    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], layout);
+    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], layout);
     res[0] = dx;
     res[1] = dY;
     res[2] = dgates;
@@ -842,8 +871,8 @@ struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
 
 Tensor ictd_conv_autograd(const Tensor& x, const Tensor& Y, const Tensor& gates, const Tensor& W, const Tensor& Wt,
                           const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                          const Tensor& src_perm, at::IntArrayRef layout) {
-  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, layout.vec())[0];
+                          const Tensor& src_perm, const Tensor& node_order, at::IntArrayRef layout) {
+  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout.vec())[0];
 }
 
 struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
@@ -1118,9 +1147,9 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 TORCH_LIBRARY(fsctep, m) {
   m.def("sparse_prepare_weights(Tensor w_last, Tensor b_last, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv(Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6, Tensor dst_ptr, Tensor src_ptr, "
-        "Tensor src_perm, Tensor edge_dst) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_perm, Tensor edge_dst, Tensor node_order) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
-        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, "
         "int channels) -> (Tensor, Tensor)");
@@ -1128,9 +1157,10 @@ TORCH_LIBRARY(fsctep, m) {
         "-> (Tensor, Tensor)");
   m.def("ictd_prepare_weights(Tensor W) -> Tensor");
   m.def("ictd_conv(Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg, Tensor dst_ptr, "
-        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, int[] layout) -> Tensor");
+        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order, int[] layout) -> Tensor");
   m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
-        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, int[] layout) -> (Tensor, Tensor, Tensor)");
+        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order, int[] layout) "
+        "-> (Tensor, Tensor, Tensor)");
   m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
         "int n_species, int n_comps, int[] layout) -> Tensor");
   m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "
@@ -1155,6 +1185,7 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("graph_prepare(Tensor edge_src, Tensor edge_dst, Tensor species, int n_species) -> Tensor[]");
   m.def("edge_vec_geometry(Tensor edge_vec, Tensor order) -> (Tensor, Tensor)");
   m.def("edge_vec_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor order) -> Tensor");
+  m.def("spatial_order(Tensor pos) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -1184,6 +1215,7 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("graph_prepare", graph_prepare);
   m.impl("edge_vec_geometry", edge_vec_geometry);
   m.impl("edge_vec_geometry_backward", edge_vec_geometry_backward);
+  m.impl("spatial_order", spatial_order);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -1213,6 +1245,7 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("graph_prepare", graph_prepare_meta);
   m.impl("edge_vec_geometry", edge_vec_geometry_meta);
   m.impl("edge_vec_geometry_backward", edge_vec_geometry_backward_meta);
+  m.impl("spatial_order", spatial_order_meta);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
@@ -1235,6 +1268,6 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                            "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                           "edge_vec_geometry", "edge_vec_geometry_backward"})
+                           "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -33,6 +33,7 @@ class Graph:
     pair_tiles: torch.Tensor   # (17*T,) int32: edge ids by pair in 16-tiles | tile pairs (unused tiles last)
     status: torch.Tensor       # (1,) int32: nonzero if an edge or species id was out of range
     n_species: int = 0
+    node_order: torch.Tensor | None = None   # (N,) int32 spatial order of the nodes, or empty (identity)
 
     @property
     def n_nodes(self) -> int:
@@ -52,11 +53,15 @@ class Graph:
 
 
 def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: torch.Tensor,
-                  n_nodes: int | None = None, species: torch.Tensor | None = None, n_species: int = 0) -> Graph:
+                  n_nodes: int | None = None, species: torch.Tensor | None = None, n_species: int = 0,
+                  pos: torch.Tensor | None = None) -> Graph:
     """Stable receiver sort and index structures of one neighbour list.
 
     ``species`` (N,) holds the atomic numbers used as rows of the model's species table of
-    ``n_species`` rows (<= 16); without species pass ``n_nodes`` (the pair structures stay empty)."""
+    ``n_species`` rows (<= 16); without species pass ``n_nodes`` (the pair structures stay empty).
+    With ``pos`` (N, 3) the graph also carries the spatial order of the atoms, which the per-node
+    kernels walk (XCD by XCD) so that neighbouring blocks share gathered rows in L2; results do not
+    depend on it."""
     if species is None:
         if n_nodes is None:
             raise ValueError("prepare_graph needs species or n_nodes")
@@ -67,9 +72,13 @@ def prepare_graph(edge_src: torch.Tensor, edge_dst: torch.Tensor, edge_shifts: t
     (order, src32, dst32, dst_ptr, src_ptr, src_perm, node_species, edge_pair, pair_tiles,
      status) = torch.ops.fsctep.graph_prepare(edge_src, edge_dst, species, int(n_species))
     shifts = edge_shifts.index_select(0, order)
+    if pos is not None:
+        node_order = torch.ops.fsctep.spatial_order(pos.detach())
+    else:
+        node_order = torch.empty(0, dtype=torch.int32, device=edge_dst.device)
     return Graph(order=order, src32=src32, dst32=dst32, dst_ptr=dst_ptr, src_ptr=src_ptr, src_perm=src_perm,
                  shifts=shifts, node_species=node_species, edge_pair=edge_pair, pair_tiles=pair_tiles,
-                 status=status, n_species=int(n_species))
+                 status=status, n_species=int(n_species), node_order=node_order)
 
 
 def poison_invalid(e: torch.Tensor, graph: Graph) -> torch.Tensor:

@@ -152,9 +152,9 @@ class _ICTDTrunk(nn.Module):
             return torch.ops.fsctep.ictd_prepare_weights(tp.weight.detach())
 
     # ------------------------------------------------------------------ forward
-    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
+    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A, pos=None) -> Graph:
         """The receiver-sorted graph of one neighbour list (device op, no host synchronisation)."""
-        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species)
+        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species, pos=pos)
 
     def _check_inference(self):
         if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
@@ -170,7 +170,7 @@ class _ICTDTrunk(nn.Module):
         :901-902 / o3 :928-929 (the LAMMPS / ML-IAP cores differentiate through edge_vec)."""
         if sync_after_scatter is not None or external_tensor_blocks is not None or fidelity_ids is not None:
             raise NotImplementedError("sync hooks, external blocks and fidelity ids are outside the HIP path")
-        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A, pos=pos)
         e, dip = self.forward_graph(pos, batch, cell, g, external_tensor=external_tensor,
                                     edge_vec=precomputed_edge_vec, with_dipole=bool(return_physical_tensors))
         if return_physical_tensors:

@@ -7,8 +7,8 @@ There is no CPU implementation: calling an op with CPU tensors raises.  Paramete
 produced (the path serves energy + forces).
 
     sparse_prepare_weights(w_last, b_last, channels) -> (bk1, bk6)
-    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst) -> (out, S, P)
-    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst)
+    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order) -> (out, S, P)
+    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order)
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
     sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
@@ -16,6 +16,7 @@ produced (the path serves energy + forces).
                                                               src_perm, node_species, edge_pair, pair_tiles, status]
     edge_geometry(pos, shift, edge_src, edge_dst, dst_ptr, src_ptr, src_perm) -> (n, r)
     edge_vec_geometry(edge_vec, order) -> (n, r)
+    spatial_order(pos) -> node_order (N,) int32, the Morton order of the atoms (empty node_order: identity)
     radial_mlp(r, w0, b0, w2, b2, w4?, b4?, r_cut, basis) -> h (E,64) or the fused last Linear (E,P)
 
 Sizes are read from the tensors inside the ops (the conv2..n normalisation 1/max(E/N, 1e-8) included),
@@ -34,7 +35,7 @@ import torch  # noqa: E402
 def sparse_conv_apply(x, h, n, bk1, bk6, graph):
     """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C), normalised by 1/max(E/N, 1e-8)."""
     out, _, _ = torch.ops.fsctep.sparse_conv(x, h, n, bk1, bk6, graph.dst_ptr, graph.src_ptr,
-                                             graph.src_perm, graph.dst32)
+                                             graph.src_perm, graph.dst32, graph.node_order)
     return out
 
 

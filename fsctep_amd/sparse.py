@@ -200,10 +200,10 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         self.n_species = int(max_atomvalue)
 
     # ------------------------------------------------------------------ graph handling
-    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A) -> Graph:
+    def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A, pos=None) -> Graph:
         """The receiver-sorted graph of one neighbour list (device op, no host synchronisation).  Reusing
         it across calls with unchanged edges is the caller's choice (``forward_graph``)."""
-        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species)
+        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species, pos=pos)
 
     # ------------------------------------------------------------------ forward
     def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
@@ -214,7 +214,7 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         reference's sparse trunk (geometry from ``pos``, ``edge_shifts`` and ``cell``)."""
         if external_tensor is not None or fidelity_ids is not None or return_physical_tensors:
             raise NotImplementedError("external tensors / fidelity / physical tensors are outside the HIP path")
-        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A)
+        g = self.prepare(edge_src, edge_dst, edge_shifts, pos.shape[0], A, pos=pos)
         e = self.forward_graph(pos, batch, cell, g)
         if return_reciprocal_source:
             return e, e.new_empty((e.shape[0], 0))

@@ -28,7 +28,7 @@ extern "C" {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* fsc_last_error(void);
-/* ABI revision of this header (1). */
+/* ABI revision of this header (2: node_order arguments of the conv entry points). */
 int fsc_abi_version(void);
 
 /* Measurement (no counterpart in the reference): while active, every launch of the named
@@ -81,6 +81,15 @@ int fsc_graph_prepare_noalloc(int64_t n_nodes, int64_t n_edges, int32_t n_specie
                               int32_t* node_species, int32_t* edge_pair, int32_t* pair_tiles, int32_t* status,
                               hipStream_t stream);
 
+/* Spatial order of the nodes: a permutation `order` [N] (int32) along a Morton curve over the bounding
+ * box of pos [N][3], atoms of one grid cell in ascending id.  No counterpart in the reference (whose
+ * kernels run one thread per output); passed as `node_order` to the conv entry points, whose per-node
+ * kernels then give each XCD a contiguous, spatially compact run of nodes, so that the neighbour-row
+ * gathers of its concurrently running blocks hit its L2.  Deterministic; workspace of
+ * fsc_spatial_order_workspace int32. */
+int fsc_spatial_order_workspace(int64_t n_nodes, int64_t* workspace_ints);
+int fsc_spatial_order(int64_t n_nodes, const float* pos, int32_t* order, int32_t* workspace, hipStream_t stream);
+
 /* ------------------------------------------------------------------ pure-cartesian-sparse
  * conv2..n.  Replaces, per interaction layer, the chain
  *   weights = fc(emb) ; tp(f_in[edge_src], e_flat, weights) ; scatter(., edge_dst) / (E/N)
@@ -106,22 +115,24 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
  * x: [N][13][C] input features; h: [E][64] radial hidden (output of fc.3, the second SiLU);
  * n: [E][3] unit edge directions (edge_rank_powers, models/pure_cartesian.py:292-317);
  * inv_norm: 1/max(E/N, 1e-8) as in pure_cartesian_sparse_layers.py:418-420.
- * s_ws, p_ws: workspaces from fsc_sparse_conv_workspace; keep them for the backward. */
+ * s_ws, p_ws: workspaces from fsc_sparse_conv_workspace; keep them for the backward.
+ * node_order: null, or a permutation of the nodes (fsc_spatial_order) that the per-node kernels walk
+ * (a performance hint: the results do not depend on it). */
 int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                             const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                             const float* x, const float* h, const float* n, const float* bk1,
                             float inv_norm, float* s_ws, float* p_ws, float* out,
-                            hipStream_t stream);
+                            const int32_t* node_order, hipStream_t stream);
 
 /* Backward of fsc_sparse_conv_forward for forces: grad_x [N][13][C], grad_h [E][64],
  * grad_n [E][3] from grad_out [N][13][C].  ds_ws: scratch of s_floats floats.
- * edge_dst: [E] receiver of each receiver-sorted edge. */
+ * edge_dst: [E] receiver of each receiver-sorted edge; node_order as for the forward. */
 int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                              const int32_t* edge_dst, const float* grad_out, const float* h,
                              const float* n, const float* bk6, const float* s_ws, const float* p_ws,
                              float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
-                             float* grad_n, hipStream_t stream);
+                             float* grad_n, const int32_t* node_order, hipStream_t stream);
 
 /* ------------------------------------------------------------------ conv1 (sparse)
  * Replaces the TP + scatter + in-degree normalisation of PureCartesianSparseE3Conv.forward
@@ -225,11 +236,12 @@ typedef struct FscIctdLayout {
  * i.e. HarmonicFullyConnectedTensorProduct[O3].forward (models/ictd_irreps.py:971-1253, :1512-1695)
  * and the project/mix ops of the reference extension (csrc/ictd_tp.cpp:140-494).
  * gates [E][NREF]; Wp: fsc_ictd_prepare_weights of tp2.weight; cg: concatenated normalised C[m1][m2][m3]
- * of the live paths; z_ws N*KT*C + N floats of scratch; out [N][M][C]. */
+ * of the live paths; z_ws N*KT*C + N floats of scratch; out [N][M][C].  node_order: null or a
+ * permutation of the nodes (fsc_spatial_order) for the per-receiver kernels (a performance hint). */
 int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                           const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
                           const float* gates, const float* cg, const float* Wp, float* z_ws, float* out,
-                          hipStream_t stream);
+                          const int32_t* node_order, hipStream_t stream);
 
 /* Prepare tp2.weight W [NREF][C][C] for the channel mix: Wp holds 2*NREF*C*C + 512 floats (W times a
  * power of two split into two fp16 planes, the same with the channel axes swapped, and the scale), opaque
@@ -238,12 +250,13 @@ int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, fl
 
 /* Backward for forces: grad_x [N][M][C], grad_gates [E][NREF] (caller zero-fills: entries of paths
  * without a geometric operand stay 0), grad_Y [E][NY].  Wp as for the forward; dz_ws N*KT*C + N floats,
- * dxe_ws [E][M][C] scratch. */
+ * dxe_ws [E][M][C] scratch; node_order as for the forward. */
 int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                            const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
                            const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
                            const float* gates, const float* cg, const float* Wp, float* dz_ws,
-                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, hipStream_t stream);
+                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y,
+                           const int32_t* node_order, hipStream_t stream);
 
 /* conv1 (ICTDIrrepsE3Conv / ICTDO3E3Conv, pure_cartesian_ictd_layers_full.py:341-473,
  * pure_cartesian_ictd_layers_o3.py:424-532): both operands depend only on the species, and

@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from .radial import soft_one_hot_linspace
+from .sparse_ref import edge_chunked
 from .sparse_ref import linear, main_net, edge_vectors, scatter_sum
 
 # ----------------------------------------------------------------------------- basis (float64)
@@ -246,12 +247,20 @@ def radial_mlp(emb, p, prefix):
     return linear(h, p, prefix + ".4")
 
 
-def conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field=None):
+def conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field=None, edge_chunk=None):
     """ICTDIrrepsE3Conv.forward (full :341-473) / ICTDO3E3Conv.forward (o3 :424-532)."""
-    keys = active_keys(cfg)
-    E = n.shape[0]
     e = F.embedding(A.long(), p["e3_conv_emb.atom_embedding.weight"])
     Ai = linear(F.silu(linear(e, p, "e3_conv_emb.atom_mlp.0")), p, "e3_conv_emb.atom_mlp.2")
+    cnt = scatter_sum(torch.ones_like(dst), dst, N).clamp(min=1).to(Ai.dtype)
+    eb = batch[src]
+    out = edge_chunked(lambda Ai, n, r, src, dst, eb: _conv1_msg(Ai, n, r, src, dst, eb, p, cfg, ext_field),
+                       edge_chunk, dst, N, Ai, n, r, src, dst, eb)
+    return out / cnt.unsqueeze(-1)
+
+
+def _conv1_msg(Ai, n, r, src, dst, edge_batch, p, cfg, ext_field):
+    keys = active_keys(cfg)
+    E = n.shape[0]
     C8 = cfg.output_size
     f_in = {k: Ai.new_zeros(E, C8, 2 * k[0] + 1) for k in keys}
     for l in range(cfg.lmax + 1):
@@ -260,7 +269,7 @@ def conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field=None):
             f_in[k] = Ai[src].unsqueeze(-1) * direction_harmonics(n, l).unsqueeze(-2)
     if ext_field is not None:
         # rank-1 cartesian field -> l=1 block in monomial order (z, y, x) (pure_cartesian_ictd_layers.py:68-110,303-379)
-        t = ext_field[:, [2, 1, 0]][batch][src].unsqueeze(-2) * Ai[src].unsqueeze(-1)
+        t = ext_field[:, [2, 1, 0]][edge_batch].unsqueeze(-2) * Ai[src].unsqueeze(-1)
         if cfg.o3:
             scale = p["e3_conv_emb.external_tensor_scale_by_irrep"][keys.index((1, -1))]
         else:
@@ -270,12 +279,18 @@ def conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field=None):
     x2[(0, 1)] = Ai[dst].unsqueeze(-1)
     gates = radial_mlp(radial_embedding(r, cfg), p, "e3_conv_emb.fc")
     out = fctp(f_in, x2, p["e3_conv_emb.tp2.weight"], gates, paths_conv1(cfg), keys)
-    cnt = scatter_sum(torch.ones_like(dst), dst, N).clamp(min=1).to(Ai.dtype)
-    return scatter_sum(merge_keys(out, keys), dst, N) / cnt.unsqueeze(-1)
+    return merge_keys(out, keys)
 
 
-def conv2(f, n, r, src, dst, N, p, layer, cfg):
+def conv2(f, n, r, src, dst, N, p, layer, cfg, edge_chunk=None):
     """conv2..n loop (full :938-954, o3 :956-973): gates = fc2(emb), x2 = Y_l, / in-degree."""
+    cnt = scatter_sum(torch.ones_like(dst), dst, N).clamp(min=1).to(f.dtype)
+    out = edge_chunked(lambda f, n, r, src: _conv2_msg(f, n, r, src, p, layer, cfg), edge_chunk, dst, N,
+                       f, n, r, src)
+    return out / cnt.unsqueeze(-1)
+
+
+def _conv2_msg(f, n, r, src, p, layer, cfg):
     keys = active_keys(cfg)
     x1 = {k: v[src] for k, v in split_keys(f, cfg.channels, keys).items()}
     Y = {}
@@ -285,8 +300,7 @@ def conv2(f, n, r, src, dst, N, p, layer, cfg):
             Y[k] = direction_harmonics(n, l).unsqueeze(-2)
     gates = radial_mlp(radial_embedding(r, cfg), p, f"fc2_layers.{layer}")
     out = fctp(x1, Y, p[f"tp2_layers.{layer}.weight"], gates, paths_conv2(cfg), keys)
-    cnt = scatter_sum(torch.ones_like(dst), dst, N).clamp(min=1).to(f.dtype)
-    return scatter_sum(merge_keys(out, keys), dst, N) / cnt.unsqueeze(-1)
+    return merge_keys(out, keys)
 
 
 def wread_key(cfg, k) -> str:
@@ -322,8 +336,8 @@ def readout(features, p, cfg, batch=None):
     return e, dip
 
 
-def forward(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field=None):
-    """(atomic energies (N,1), dipole (G,1,3) or None)."""
+def forward(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field=None, edge_chunk=None):
+    """(atomic energies (N,1), dipole (G,1,3) or None); ``edge_chunk`` as in sparse_ref.edge_chunked."""
     dtype = p["weighted_sum.weights"].dtype
     pos, cell, shifts = pos.to(dtype), cell.to(dtype), shifts.to(dtype)
     order = torch.argsort(dst, stable=True)
@@ -332,15 +346,15 @@ def forward(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field=None):
     r = vec.norm(dim=1)
     n = vec / r.clamp(min=1e-8).unsqueeze(-1)
     N = pos.shape[0]
-    feats = [conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field)]
+    feats = [conv1(A, n, r, src, dst, batch, N, p, cfg, ext_field, edge_chunk)]
     for layer in range(cfg.num_interaction - 1):
-        feats.append(conv2(feats[-1], n, r, src, dst, N, p, layer, cfg))
+        feats.append(conv2(feats[-1], n, r, src, dst, N, p, layer, cfg, edge_chunk))
     return readout(feats, p, cfg, batch)
 
 
-def energy_forces(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field=None):
+def energy_forces(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field=None, edge_chunk=None):
     pos = pos.detach().clone().requires_grad_(True)
-    e, dip = forward(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field)
+    e, dip = forward(pos, A, batch, src, dst, shifts, cell, p, cfg, ext_field, edge_chunk)
     (g,) = torch.autograd.grad(e.sum(), pos)
     return e.detach().squeeze(-1), -g, (dip.detach() if dip is not None else None)
 

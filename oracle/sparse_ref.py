@@ -164,6 +164,48 @@ def scatter_sum(src: torch.Tensor, index: torch.Tensor, n: int) -> torch.Tensor:
     return src.new_zeros((n,) + src.shape[1:]).index_add(0, index, src)
 
 
+class _Recomputed(torch.autograd.Function):
+    """y = part(*inputs) that keeps only its inputs for the backward and recomputes part there (the
+    per-edge intermediates of a chunk live only while that chunk's gradient is formed)."""
+
+    @staticmethod
+    def forward(ctx, part, *inputs):
+        ctx.part = part
+        ctx.save_for_backward(*inputs)
+        with torch.no_grad():
+            return part(*inputs)
+
+    @staticmethod
+    def backward(ctx, gy):
+        inputs = [t.detach().requires_grad_(t.is_floating_point()) for t in ctx.saved_tensors]
+        want = [t for t in inputs if t.requires_grad]
+        with torch.enable_grad():
+            y = ctx.part(*inputs)
+        got = iter(torch.autograd.grad(y, want, gy, allow_unused=True))
+        return (None,) + tuple(next(got) if t.requires_grad else None for t in inputs)
+
+
+def edge_chunked(part, edge_chunk, dst, n_nodes, node_input, *edge_tensors):
+    """scatter_sum(part(node_input, *edge_tensors), dst, n_nodes) for a `part` that returns per-edge messages.
+
+    An evaluation device for large systems, not part of the algorithm: the edges are taken in chunks of
+    `edge_chunk` whose per-edge intermediates (the materialised weights) are recomputed in the backward
+    instead of stored, and each chunk's messages are added into the receiver sum as they come (the same
+    sum in another order).  None: one chunk."""
+    E = dst.shape[0]
+    if edge_chunk is None or E <= edge_chunk:
+        return scatter_sum(part(node_input, *edge_tensors), dst, n_nodes)
+    out = None
+    for a in range(0, E, edge_chunk):
+        sl = [t[a:a + edge_chunk] for t in edge_tensors]
+        msg = _Recomputed.apply(part, node_input, *sl)
+        if out is None:
+            out = msg.new_zeros((n_nodes,) + msg.shape[1:])
+        # in place, and index_put_ saves no messages for the backward
+        out.index_put_((dst[a:a + edge_chunk],), msg, accumulate=True)
+    return out
+
+
 # ----------------------------------------------------------------------------- convolutions
 
 def atom_features(A, p, prefix="e3_conv_layers.0"):
@@ -173,10 +215,17 @@ def atom_features(A, p, prefix="e3_conv_layers.0"):
     return linear(h, p, prefix + ".atom_mlp.2")
 
 
-def conv1(A, vec, src, dst, n_nodes, p, cfg: SparseConfig):
+def conv1(A, vec, src, dst, n_nodes, p, cfg: SparseConfig, edge_chunk=None):
     """pure_cartesian_sparse_layers.py:227-330 (no external tensor, no fidelity)."""
-    C8, lmax, E = cfg.output_size, cfg.lmax, vec.shape[0]
     Ai = atom_features(A, p)
+    cnt = scatter_sum(torch.ones_like(dst), dst, n_nodes).clamp(min=1).to(Ai.dtype)
+    out = edge_chunked(lambda Ai, vec, src, dst: _conv1_msg(Ai, vec, src, dst, p, cfg), edge_chunk, dst, n_nodes,
+                       Ai, vec, src, dst)
+    return out / cnt.unsqueeze(-1)
+
+
+def _conv1_msg(Ai, vec, src, dst, p, cfg: SparseConfig):
+    C8, lmax, E = cfg.output_size, cfg.lmax, vec.shape[0]
     e = rank_powers(vec, lmax)
     a_src = Ai[src]
     f1 = {(0, 0): a_src, (1, 0): torch.zeros_like(a_src)}
@@ -194,16 +243,23 @@ def conv1(A, vec, src, dst, n_nodes, p, cfg: SparseConfig):
     x2 = merge_o3(x2b, C8, lmax)
     emb = radial_embedding(vec.norm(dim=1), cfg)
     w = radial_mlp(emb, p, "e3_conv_layers.0.fc")
-    msg = sparse_tp(f_in, x2, w, C8, C8, cfg.channels, lmax)
-    cnt = scatter_sum(torch.ones_like(dst), dst, n_nodes).clamp(min=1).to(msg.dtype)
-    return scatter_sum(msg, dst, n_nodes) / cnt.unsqueeze(-1)
+    return sparse_tp(f_in, x2, w, C8, C8, cfg.channels, lmax)
 
 
-def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig, avg_degree: float | None = None):
+def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig, avg_degree: float | None = None,
+          edge_chunk=None):
     """pure_cartesian_sparse_layers.py:382-421: x1 = f[src], x2 = [1, n, n(x)n] with C2=1, / (E/N).
 
     ``avg_degree`` replaces E/N, so that a cluster cut out of a larger system is normalised like
     its parent system (the normalisation is the only non-local term of the trunk)."""
+    E = vec.shape[0]
+    out = edge_chunked(lambda f, vec, src: _conv2_msg(f, vec, src, p, layer, cfg), edge_chunk, dst, n_nodes,
+                       f, vec, src)
+    avg = out.new_tensor(E / max(n_nodes, 1) if avg_degree is None else avg_degree).clamp_min(1e-8)
+    return out / avg
+
+
+def _conv2_msg(f, vec, src, p, layer: int, cfg: SparseConfig):
     lmax, E = cfg.lmax, vec.shape[0]
     e = rank_powers(vec, lmax)
     eb = {(0, 0): e[0].view(E, 1), (1, 0): torch.zeros(E, 1, dtype=vec.dtype)}
@@ -214,10 +270,7 @@ def conv2(f, vec, src, dst, n_nodes, p, layer: int, cfg: SparseConfig, avg_degre
     x2 = merge_o3(eb, 1, lmax)
     emb = radial_embedding(vec.norm(dim=1), cfg)
     w = radial_mlp(emb, p, f"e3_conv_layers.{layer}.fc")
-    msg = sparse_tp(f[src], x2, w, cfg.channels, 1, cfg.channels, lmax)
-    out = scatter_sum(msg, dst, n_nodes)
-    avg = msg.new_tensor(E / max(n_nodes, 1) if avg_degree is None else avg_degree).clamp_min(1e-8)
-    return out / avg
+    return sparse_tp(f[src], x2, w, cfg.channels, 1, cfg.channels, lmax)
 
 
 # ----------------------------------------------------------------------------- readout
@@ -275,7 +328,7 @@ def readout(features: list, p, cfg: SparseConfig):
 # ----------------------------------------------------------------------------- trunk
 
 def atom_energies(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseConfig,
-                  avg_degree: float | None = None):
+                  avg_degree: float | None = None, edge_chunk=None):
     """(N, 1) atomic energies of the sparse trunk (pure_cartesian_sparse_layers.py:723-855)."""
     dtype = p["weighted_sum.weights"].dtype
     pos, cell, shifts = pos.to(dtype), cell.to(dtype), shifts.to(dtype)
@@ -283,16 +336,16 @@ def atom_energies(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseCon
     src, dst, shifts = src[order], dst[order], shifts[order]
     vec = edge_vectors(pos, batch, src, dst, shifts, cell)
     N = pos.shape[0]
-    feats = [conv1(A, vec, src, dst, N, p, cfg)]
+    feats = [conv1(A, vec, src, dst, N, p, cfg, edge_chunk)]
     for layer in range(1, cfg.num_interaction):
-        feats.append(conv2(feats[-1], vec, src, dst, N, p, layer, cfg, avg_degree))
+        feats.append(conv2(feats[-1], vec, src, dst, N, p, layer, cfg, avg_degree, edge_chunk))
     return readout(feats, p, cfg)
 
 
-def energy_forces(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseConfig):
+def energy_forces(pos, A, batch, src, dst, shifts, cell, p: dict, cfg: SparseConfig, edge_chunk=None):
     """(per-atom energies (N,), forces (N,3)) with F = -dE/dpos."""
     pos = pos.detach().clone().requires_grad_(True)
-    e = atom_energies(pos, A, batch, src, dst, shifts, cell, p, cfg)
+    e = atom_energies(pos, A, batch, src, dst, shifts, cell, p, cfg, edge_chunk=edge_chunk)
     (g,) = torch.autograd.grad(e.sum(), pos)
     return e.detach().squeeze(-1), -g
 

@@ -27,7 +27,7 @@ int main(int argc, char** argv) {
                          "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                          "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                          "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                         "edge_vec_geometry", "edge_vec_geometry_backward"};
+                         "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order"};
   for (const char* n : names) {
     auto op = disp.findSchema({std::string("fsctep::") + n, ""});
     if (!op) {
@@ -51,8 +51,9 @@ int main(int argc, char** argv) {
   auto sc = disp.findSchemaOrThrow("fsctep::sparse_conv", "")
                 .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                    const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&)>();
-  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie);
+                    const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&)>();
+  auto no_order = at::empty({0}, at::device(at::kMeta).dtype(at::kInt));
+  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order);
   if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;

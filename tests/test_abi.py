@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
     assert len(syms) >= 9
     for s in syms:
         assert hasattr(lib, s), s
-    assert lib.fsc_abi_version() == 1
+    assert lib.fsc_abi_version() == 2
     # every declared entry point has a ctypes signature (or is a metadata call)
     for s in syms:
         assert s in _lib.SIGNATURES or s in ("fsc_last_error", "fsc_abi_version"), s
@@ -69,7 +69,7 @@ def test_fake_kernels_trace_shapes():
         bk = torch.empty(6 * 65 * 64 * 64 + 512)
         i = torch.empty(11, dtype=torch.int32)
         e = torch.empty(30, dtype=torch.int32)
-        out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e)
+        out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, torch.empty(0, dtype=torch.int32))
         assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10,) and P.shape == (30 * 18 * 64,)
 
 

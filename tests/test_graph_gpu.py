@@ -119,3 +119,82 @@ def test_graph_prepare_meta_shapes():
         shapes = [tuple(o.shape) for o in out]
     assert shapes == [(100,), (100,), (100,), (13,), (13,), (100,), (12,), (100,), (17 * (7 + 16),), (1,)]
     assert all(o.dtype == torch.int32 for o in out)
+
+
+# ---------------------------------------------------------------- spatial node order (fsc_spatial_order)
+
+def _spread3(v):
+    v = v.astype(np.int64) & 0xFF
+    v = (v | (v << 8)) & 0x0F00F
+    v = (v | (v << 4)) & 0x0C30C3
+    v = (v | (v << 2)) & 0x249249
+    return v
+
+
+def _morton_order(pos):
+    """numpy statement of the order: Morton code of the cell on a G^3 grid over the bounding box of the
+    finite coordinates (G the smallest power of two <= 256 with 2 G^3 >= N), ascending id within a cell."""
+    N = pos.shape[0]
+    G = 1
+    while G < 256 and 2 * G ** 3 < N:
+        G *= 2
+    p = pos.astype(np.float32)
+    fin = np.isfinite(p)
+    lo = np.array([p[fin[:, k], k].min() if fin[:, k].any() else np.inf for k in range(3)], np.float32)
+    hi = np.array([p[fin[:, k], k].max() if fin[:, k].any() else -np.inf for k in range(3)], np.float32)
+    c = np.zeros((N, 3), np.int64)
+    for k in range(3):
+        if hi[k] > lo[k]:
+            with np.errstate(invalid="ignore"):
+                t = (p[:, k] - lo[k]) * (np.float32(G) / (hi[k] - lo[k]))
+            t = np.where(np.isnan(t), np.float32(0), t)
+            c[:, k] = np.clip(t, 0, G - 1).astype(np.int64)
+    code = _spread3(c[:, 0]) | (_spread3(c[:, 1]) << 1) | (_spread3(c[:, 2]) << 2)
+    return np.argsort(code, kind="stable")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,kind", [(1, "box"), (7, "box"), (1000, "box"), (10000, "box"), (3000, "zeros"),
+                                    (500, "nan"), (40000, "slab")])
+def test_spatial_order_is_the_morton_permutation(N, kind):
+    rng = np.random.default_rng(N)
+    pos = rng.uniform(-3.0, 40.0, (N, 3)).astype(np.float32)
+    if kind == "zeros":
+        pos[:] = 0.0                               # edge-vector callers pass zero positions: identity
+    elif kind == "nan":
+        pos[::7, 1] = np.nan
+    elif kind == "slab":
+        pos[:, 2] *= 0.01
+    order = torch.ops.fsctep.spatial_order(torch.from_numpy(pos).to(DEV)).cpu().numpy()
+    np.testing.assert_array_equal(np.sort(order), np.arange(N))
+    np.testing.assert_array_equal(order, _morton_order(pos))
+    if kind == "zeros":
+        np.testing.assert_array_equal(order, np.arange(N))
+
+
+@pytest.mark.gpu
+def test_conv_results_do_not_depend_on_the_node_order():
+    """The per-node kernels walk graph.node_order: energies and forces are bitwise those of the identity."""
+    import bench
+    from fsctep_amd.ictd import energy_forces
+    from fsctep_amd.sparse import energy_and_forces
+    for mode, atoms in (("sparse", 1500), ("ictd-o3", 1200)):
+        w = bench.WORKLOADS[mode]
+        s = bench._system(mode, atoms, w["seed"])
+        model = bench.build_model(mode, torch.device(DEV))
+        pos = torch.tensor(s.pos, dtype=torch.float32, device=DEV)
+        A = torch.tensor(s.species, device=DEV)
+        batch = torch.zeros(atoms, dtype=torch.long, device=DEV)
+        cell = torch.tensor(s.cell, dtype=torch.float32, device=DEV)
+        args = (torch.tensor(s.edge_src, device=DEV), torch.tensor(s.edge_dst, device=DEV),
+                torch.tensor(s.edge_shifts, dtype=torch.float32, device=DEV), atoms, A)
+        g0 = model.prepare(*args)
+        g1 = model.prepare(*args, pos=pos)
+        assert g0.node_order.numel() == 0 and g1.node_order.numel() == atoms
+        assert not torch.equal(g1.node_order.cpu(), torch.arange(atoms, dtype=torch.int32))
+        if mode == "sparse":
+            r0, r1 = (energy_and_forces(model, pos, batch, cell, g) for g in (g0, g1))
+        else:
+            fld = torch.tensor(bench._field(1, w["seed"]), dtype=torch.float32, device=DEV)
+            r0, r1 = (energy_forces(model, pos, batch, cell, g, external_tensor=fld)[:2] for g in (g0, g1))
+        assert torch.equal(r0[0], r1[0]) and torch.equal(r0[1], r1[1]), mode

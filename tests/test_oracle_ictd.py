@@ -74,9 +74,9 @@ def test_planted_normalisation_mistake_fails_golden(monkeypatch):
     p = params_for(cfg, int(g["param_seed"]), torch.float64)
     orig = I.conv2
 
-    def wrong(f, n, r, src, dst, N, p_, layer, cfg_):
+    def wrong(f, n, r, src, dst, N, p_, layer, cfg_, edge_chunk=None):
         # global E/N (the sparse trunk's conv2 rule) instead of the ICTD per-receiver in-degree
-        out = orig(f, n, r, src, dst, N, p_, layer, cfg_)
+        out = orig(f, n, r, src, dst, N, p_, layer, cfg_, edge_chunk)
         cnt = I.scatter_sum(torch.ones_like(dst), dst, N).clamp(min=1).to(out.dtype)
         return out * cnt.unsqueeze(-1) / (n.shape[0] / N)
 

@@ -60,9 +60,9 @@ def test_planted_normalisation_mistake_fails_golden(monkeypatch):
     p = params_for(cfg, int(g["param_seed"]), torch.float64)
     orig = R.conv2
 
-    def wrong(f, vec, src, dst, n, p_, layer, cfg_, avg_degree=None):
+    def wrong(f, vec, src, dst, n, p_, layer, cfg_, avg_degree=None, edge_chunk=None):
         # per-receiver in-degree instead of the global E/N of the reference's conv2
-        out = orig(f, vec, src, dst, n, p_, layer, cfg_, avg_degree) * (vec.shape[0] / n)
+        out = orig(f, vec, src, dst, n, p_, layer, cfg_, avg_degree, edge_chunk) * (vec.shape[0] / n)
         cnt = R.scatter_sum(torch.ones_like(dst), dst, n).clamp(min=1).to(out.dtype)
         return out / cnt.unsqueeze(-1)
 
