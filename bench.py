@@ -423,6 +423,21 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
     out["ms_per_step_with_graph_prepare"] = round((time.perf_counter() - t0) * 1000 / rs, 4)
     out["graph_prepare_ms"] = {"cold": round(t_cold * 1000, 3), "warm_median": round(statistics.median(warm) * 1000, 3)}
 
+    # neighbour-list rebuild on the GPU (cell list, periodic images): the same edges as the host list
+    from fsctep_amd.neighbors import radius_graph_pbc_gpu
+    pos64 = torch.tensor(system.pos, dtype=torch.float64, device=dev)
+    cell64 = torch.tensor(system.cell, dtype=torch.float64, device=dev)
+    nl = radius_graph_pbc_gpu(pos64, 5.0, cell64)
+    same = bool(nl[0].shape[0] == E and torch.equal(nl[0].cpu(), src.cpu()) and torch.equal(nl[1].cpu(), dst.cpu()))
+    nl_t = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        radius_graph_pbc_gpu(pos64, 5.0, cell64)
+        torch.cuda.synchronize()
+        nl_t.append(time.perf_counter() - t0)
+    out["neighbor_list_ms"] = {"median": round(statistics.median(nl_t) * 1000, 3), "equals_host_list": same}
+
     out["parity"] = parity_vs_fixture(mode, system, seed, e.cpu().numpy(), f.cpu().numpy(),
                                       None if dip is None else dip.cpu().numpy())
     out["products"] = PRODUCTS[mode]

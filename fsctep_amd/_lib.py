@@ -50,6 +50,9 @@ SIGNATURES = {
     "fsc_graph_prepare_noalloc": [_i64, _i64, _i32] + [_p] * 14,
     "fsc_spatial_order_workspace": [_i64, _pi64],
     "fsc_spatial_order": [_i64, _p, _p, _p, _p],
+    "fsc_neighbor_workspace": [_i64, _pi64],
+    "fsc_neighbor_count": [_i64, _p, _p, _p, ctypes.c_double, _p, _p, _p],
+    "fsc_neighbor_fill": [_i64, _i64, _p, _p, _p, ctypes.c_double, _p, _p, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_forward": [_i64, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_backward": [_i64, _p, _p, _p, _p, _p, _p, _p],
 }

@@ -581,6 +581,36 @@ Tensor spatial_order(const Tensor& pos_) {
 
 Tensor spatial_order_meta(const Tensor& pos) { return at::empty({pos.size(0)}, pos.options().dtype(at::kInt)); }
 
+// Radius graph with periodic images (fsc_neighbor_count / fsc_neighbor_fill).  The edge count is data
+// dependent: it is read back after the count pass (one host synchronisation, as torch_cluster's radius).
+std::vector<Tensor> neighbor_list(const Tensor& pos_, const Tensor& cell_, double cutoff, at::IntArrayRef pbc) {
+  require_gpu({pos_, cell_});
+  TORCH_CHECK(pos_.dim() == 2 && pos_.size(1) == 3, "neighbor_list: pos must be (N, 3)");
+  TORCH_CHECK(cell_.numel() == 9, "neighbor_list: cell must hold 3x3 values (rows = lattice vectors)");
+  TORCH_CHECK(pbc.size() == 3, "neighbor_list: pbc must have 3 flags");
+  const int64_t N = pos_.size(0);
+  Tensor pos = pos_.to(at::kDouble).contiguous(), cell = cell_.to(at::kDouble).reshape({3, 3}).contiguous();
+  const int32_t flags[3] = {(int32_t)(pbc[0] != 0), (int32_t)(pbc[1] != 0), (int32_t)(pbc[2] != 0)};
+  int64_t ws_n = 0;
+  check(fsc_neighbor_workspace(N, &ws_n), "fsc_neighbor_workspace");
+  const auto io = pos.options().dtype(at::kInt);
+  Tensor ws = at::empty({ws_n}, io), dst_ptr = at::empty({N + 1}, io);
+  const double* pp = N ? pos.data_ptr<double>() : nullptr;
+  check(fsc_neighbor_count(N, pp, cell.data_ptr<double>(), flags, cutoff, dst_ptr.data_ptr<int32_t>(),
+                           ws.data_ptr<int32_t>(), stream_of(pos)),
+        "fsc_neighbor_count");
+  const int64_t E = dst_ptr.select(0, N).item<int32_t>();
+  TORCH_CHECK(E >= 0, "neighbor_list: edge count overflow");
+  Tensor src = at::empty({E}, pos.options().dtype(at::kLong)), dst = at::empty({E}, pos.options().dtype(at::kLong));
+  Tensor shifts = at::empty({E, 3}, pos.options()), fill_ws = at::empty({3 * E}, io);
+  check(fsc_neighbor_fill(N, E, pp, cell.data_ptr<double>(), flags, cutoff, dst_ptr.data_ptr<int32_t>(),
+                          ws.data_ptr<int32_t>(), E ? fill_ws.data_ptr<int32_t>() : nullptr,
+                          E ? src.data_ptr<int64_t>() : nullptr, E ? dst.data_ptr<int64_t>() : nullptr,
+                          E ? shifts.data_ptr<double>() : nullptr, stream_of(pos)),
+        "fsc_neighbor_fill");
+  return {src, dst, shifts, dst_ptr};
+}
+
 // ============================================================== geometry from caller-supplied edge vectors
 
 std::tuple<Tensor, Tensor> edge_vec_geometry(const Tensor& edge_vec_, const Tensor& order) {
@@ -1186,6 +1216,7 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("edge_vec_geometry(Tensor edge_vec, Tensor order) -> (Tensor, Tensor)");
   m.def("edge_vec_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor order) -> Tensor");
   m.def("spatial_order(Tensor pos) -> Tensor");
+  m.def("neighbor_list(Tensor pos, Tensor cell, float cutoff, int[] pbc) -> Tensor[]");
 }
 
 TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
@@ -1216,6 +1247,7 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("edge_vec_geometry", edge_vec_geometry);
   m.impl("edge_vec_geometry_backward", edge_vec_geometry_backward);
   m.impl("spatial_order", spatial_order);
+  m.impl("neighbor_list", neighbor_list);
 }
 
 TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
@@ -1268,6 +1300,6 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                            "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                           "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order"})
+                           "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "neighbor_list"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

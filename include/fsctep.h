@@ -90,6 +90,23 @@ int fsc_graph_prepare_noalloc(int64_t n_nodes, int64_t n_edges, int32_t n_specie
 int fsc_spatial_order_workspace(int64_t n_nodes, int64_t* workspace_ints);
 int fsc_spatial_order(int64_t n_nodes, const float* pos, int32_t* order, int32_t* workspace, hipStream_t stream);
 
+/* ------------------------------------------------------------------ neighbour list
+ * Replaces radius_graph_pbc_gpu (molecular_force_field/utils/graph_utils.py:192-257; one torch_cluster
+ * radius call per periodic image) and the LAMMPS-list-to-edge loop of pair_mff_torch.cpp:597-641.
+ * Edges: every (src i, dst j, s) with s_k in {-1,0,1} on axes with pbc[k] != 0 (0 otherwise), not (i == j,
+ * s == 0), and |(pos_j - pos_i) + s.cell|^2 < cutoff^2 in double precision (cell rows = lattice vectors);
+ * receiver-sorted, then ascending in (src, s).  Unlike torch_cluster's max_num_neighbors there is no cap.
+ * pos [N][3] and cell [3][3] are device doubles; pbc is a host array of 3 int32.
+ * Two calls: fsc_neighbor_count fills the receiver CSR dst_ptr [N+1] (the caller reads E = dst_ptr[N]),
+ * then fsc_neighbor_fill, with the same workspace (fsc_neighbor_workspace int32, left untouched in
+ * between) and fill_ws of 3E int32 (8-byte aligned), writes edge_src, edge_dst [E] and edge_shifts [E][3]. */
+int fsc_neighbor_workspace(int64_t n_nodes, int64_t* workspace_ints);
+int fsc_neighbor_count(int64_t n_nodes, const double* pos, const double* cell, const int32_t* pbc, double cutoff,
+                       int32_t* dst_ptr, int32_t* workspace, hipStream_t stream);
+int fsc_neighbor_fill(int64_t n_nodes, int64_t n_edges, const double* pos, const double* cell, const int32_t* pbc,
+                      double cutoff, const int32_t* dst_ptr, int32_t* workspace, int32_t* fill_ws, int64_t* edge_src,
+                      int64_t* edge_dst, double* edge_shifts, hipStream_t stream);
+
 /* ------------------------------------------------------------------ pure-cartesian-sparse
  * conv2..n.  Replaces, per interaction layer, the chain
  *   weights = fc(emb) ; tp(f_in[edge_src], e_flat, weights) ; scatter(., edge_dst) / (E/N)
