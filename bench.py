@@ -46,10 +46,12 @@ WORKLOADS = {
                    table=["node_expand", "edge_message", "receiver_sum", "edge_message_grad", "node_expand_grad"]),
     "ictd": dict(atoms=10000, species=8, seed=33, channels=128, layers=3, lmax=3, kernel="ictd_project_grad",
                  cpu_atoms=200,
-                 table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_source_sum"]),
+                 table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_dual_project",
+                        "ictd_dual_mix"]),
     "ictd-o3": dict(atoms=4000, species=4, seed=44, channels=64, layers=3, lmax=2, kernel="ictd_project_grad",
                     cpu_atoms=200,
-                    table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_source_sum"]),
+                    table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_dual_project",
+                        "ictd_dual_mix"]),
 }
 
 # Arithmetic of the products in each kernel family (every sum accumulates in fp32).  "split-fp16": each
@@ -109,11 +111,13 @@ def ictd_kernel_work(name: str, L, N: int, E: int, C: int) -> dict:
     if name == "ictd_project":
         return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * N, bound="hbm")
     if name == "ictd_project_grad":
-        return dict(flops=2 * 2 * E * pairs * C, bytes=z_b + x_b + edge_in + 4 * E * M * C + 4 * E * (NREF + NY),
-                    bound="hbm")
-    if name == "ictd_source_sum":
-        return dict(flops=E * M * C, bytes=4 * E * M * C + x_b + 4 * (E + N), bound="hbm")
-    if name in ("ictd_mix", "ictd_mix_grad"):
+        # H = x_src g^T per edge (the gate / harmonic gradients); writes dgates and dY
+        return dict(flops=2 * E * pairs * C, bytes=z_b + x_b + edge_in + 4 * E * (NREF + NY), bound="hbm")
+    if name == "ictd_dual_project":
+        # R = projection of the receiver gradients over the source grouping (the reversed paths: KT' = KT
+        # slots, the same pairs); reads G once per node, writes R
+        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * E + 4 * N, bound="hbm")
+    if name in ("ictd_mix", "ictd_mix_grad", "ictd_dual_mix"):
         return dict(flops=2 * N * KT * C * C, bytes=z_b + x_b + 4 * L.NP * C * C, bound="mfma")
     raise KeyError(name)
 

@@ -87,20 +87,43 @@ __device__ __forceinline__ void stage_tables(const FscIctdLayout& L, const float
   }
 }
 
-// Chunk inputs: harmonics, gates and source ids of edges [eb, eb + cnt) (zero / node 0 beyond cnt).
+// Chunk inputs: harmonics, gates and gathered-node ids of the edges at positions [eb, eb + cnt) of the
+// block's edge list (zero / node 0 beyond cnt).  The edge id at position j is eperm[j] (null: j).  With
+// gdeg (a receiver CSR) the gates of an edge are divided by the in-degree of its gathered node (the
+// receiver normalisation of the dual projection, applied per edge).
+template <bool DUAL = false>
 __device__ __forceinline__ void stage_chunk(const FscIctdLayout& L, int eb, int cnt, const float* __restrict__ Y,
                                             const float* __restrict__ gates, const int32_t* __restrict__ esrc,
+                                            const int32_t* __restrict__ eperm, const int32_t* __restrict__ gdeg,
                                             float* __restrict__ ys, float* __restrict__ gs,
                                             int32_t* __restrict__ srcs) {
-  for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
-    const int e = i / L.NY;
-    ys[i] = (e < cnt) ? Y[(int64_t)eb * L.NY + i] : 0.f;
+  if constexpr (!DUAL) {
+    for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
+      const int e = i / L.NY;
+      ys[i] = (e < cnt) ? Y[(int64_t)eb * L.NY + i] : 0.f;
+    }
+    for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
+      const int e = i / L.NREF;
+      gs[i] = (e < cnt) ? gates[(int64_t)eb * L.NREF + i] : 0.f;
+    }
+    if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
+  } else {
+    for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
+      const int e = i / L.NY;
+      ys[i] = (e < cnt) ? Y[(int64_t)eperm[eb + e] * L.NY + (i - e * L.NY)] : 0.f;
+    }
+    for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
+      const int e = i / L.NREF;
+      float v = 0.f;
+      if (e < cnt) {
+        const int64_t id = eperm[eb + e];
+        const int32_t s = esrc[id];
+        v = gates[id * L.NREF + (i - e * L.NREF)] * (1.f / (float)max(gdeg[s + 1] - gdeg[s], 1));
+      }
+      gs[i] = v;
+    }
+    if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eperm[eb + threadIdx.x]] : 0;
   }
-  for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
-    const int e = i / L.NREF;
-    gs[i] = (e < cnt) ? gates[(int64_t)eb * L.NREF + i] : 0.f;
-  }
-  if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
 }
 
 // Gated coupling table of the chunk: bg[e][j] = gate_e[p] sum_m2 Y_e[oy_p + m2] C_p[m1][m2][m3] (LDS only,
@@ -180,17 +203,22 @@ __device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int nsp
 
 // ---------------------------------------------------------------- forward projection (one block per receiver)
 // Z[n][kk][i] = (1/deg) sum_{(e,m1)} bg[e][m1][kk] x[src_e][o1 + m1][i], MFMA with K = (m1, e).
+// The same kernel runs the dual projection of the backward (dual_layout): blocks are sources, their edges
+// come through eperm (the source grouping), the gathered rows are receiver gradients divided by their
+// receiver's in-degree (gdeg), and there is no final normalisation.
 // Column tile j of a 16*V-channel span holds channels span0 + V*r + j, so each lane gathers V
 // consecutive channels of x with one vector load and stores V consecutive channels of Z.
-template <int C>
-__global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
+template <int C, bool DUAL>
+__global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
                                                           const float* __restrict__ Y,
                                                           const float* __restrict__ gates,
                                                           const float* __restrict__ cg,
                                                           const int32_t* __restrict__ dst_ptr,
                                                           const int32_t* __restrict__ esrc,
                                                           float* __restrict__ Z, float* __restrict__ zscale,
-                                                          int64_t n_nodes, const int32_t* __restrict__ node_order) {
+                                                          int64_t n_nodes, const int32_t* __restrict__ node_order,
+                                                          const int32_t* __restrict__ eperm,
+                                                          const int32_t* __restrict__ gdeg) {
   constexpr int SPAN = C < 64 ? C : 64;
   constexpr int V = SPAN / 16;
   extern __shared__ __align__(16) float smem[];
@@ -221,7 +249,7 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
   for (int eb = beg; eb < end; eb += EB) {
     const int cnt = min(EB, end - eb);
     __syncthreads();
-    stage_chunk(L, eb, cnt, Y, gates, esrc, ys, gs, srcs);
+    stage_chunk<DUAL>(L, eb, cnt, Y, gates, esrc, eperm, gdeg, ys, gs, srcs);
     __syncthreads();
     build_bg(L, cgs, desc, ys, gs, bg);
     __syncthreads();
@@ -272,7 +300,7 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(FscIctdLayout L, int n
       }
     }
   }
-  const float scale = 1.f / (float)max(end - beg, 1);
+  const float scale = DUAL ? 1.f : 1.f / (float)max(end - beg, 1);
   __syncthreads();
   const int ntask = wtask[wave * 8];
   float zmax = 0.f;
@@ -448,34 +476,31 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
     }
 }
 
-// ---------------------------------------------------------------- backward projection (one block per receiver)
+// ---------------------------------------------------------------- gate and harmonic gradients (one block per receiver)
 // With g = dZ[n] / deg, per chunk of EB receiver edges:
-//   (a) DX[e][o1+m1][i] = sum_kk bg[e][m1][kk] g[kk][i]     MFMA, K = kk; dZ rows read as V-channel vectors
-//   (b) H[e][m1][kk]    = sum_i x[src_e][o1+m1][i] g[kk][i]  MFMA, K = channels (H overwrites bg in LDS)
+//   (b) H[e][m1][kk]    = sum_i x[src_e][o1+m1][i] g[kk][i]  MFMA, K = channels (into LDS)
 //   (c) T[e][p][m2]     = sum_{m1,m3} H[e][m1][koff_p+m3] C_p[m1][m2][m3]
 //       dgate[e][p] = sum_m2 Y_e[oy_p+m2] T[e][p][m2];   dY[e][y] = sum_{p covers y} gate_e[p] T[e][p][y-oy_p]
+// The input gradient dx = sum_{e: src=m} bg_e^T g_dst(e) is not formed here: it is the dual projection
+// (project_fwd_kernel over the source grouping with the dual layout) followed by the channel mix with the
+// transposed weights, so no per-edge [M][C] gradient is stored.
 template <int C>
-__global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
-                                                          const float* __restrict__ x,
-                                                          const float* __restrict__ Y,
-                                                          const float* __restrict__ gates,
-                                                          const float* __restrict__ cg,
-                                                          const int32_t* __restrict__ dst_ptr,
-                                                          const int32_t* __restrict__ esrc,
-                                                          float* __restrict__ DX, float* __restrict__ dgates,
-                                                          float* __restrict__ dY, int64_t n_nodes,
-                                                          const int32_t* __restrict__ node_order) {
-  constexpr int SPAN = C < 64 ? C : 64;
-  constexpr int V = SPAN / 16;
-  constexpr int NSPAN = C / SPAN;
+__global__ __launch_bounds__(256) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
+                                                           const float* __restrict__ x,
+                                                           const float* __restrict__ Y,
+                                                           const float* __restrict__ gates,
+                                                           const float* __restrict__ cg,
+                                                           const int32_t* __restrict__ dst_ptr,
+                                                           const int32_t* __restrict__ esrc,
+                                                           float* __restrict__ dgates, float* __restrict__ dY,
+                                                           int64_t n_nodes, const int32_t* __restrict__ node_order) {
   extern __shared__ __align__(16) float smem[];
   const ProjSmem sm = proj_smem(L, ncg, true);
   float* cgs = smem + sm.cgs;
-  int2* desc = reinterpret_cast<int2*>(smem + sm.desc);
   float* ys = smem + sm.ys;
   float* gs = smem + sm.gs;
   int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
-  float* bg = smem + sm.bg;            // gated coupling table, then H
+  float* bg = smem + sm.bg;            // H of the chunk
   float* T = smem + sm.T;              // [TT][EB]
   int* tmap = reinterpret_cast<int*>(smem + sm.tmap);
   int* toff = reinterpret_cast<int*>(smem + sm.toff);
@@ -489,7 +514,7 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
   const int TT = sm.TT;
   const float scale = 1.f / (float)(end - beg);
   const float* gn = dZ + (int64_t)n * L.KT * C;
-  stage_tables(L, cg, ncg, cgs, desc);
+  for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
   if (threadIdx.x == 0) {
     int o = 0;
     for (int p = 0; p < L.NP; ++p) {
@@ -503,49 +528,7 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
   for (int eb = beg; eb < end; eb += EB) {
     const int cnt = min(EB, end - eb);
     __syncthreads();
-    stage_chunk(L, eb, cnt, Y, gates, esrc, ys, gs, srcs);
-    __syncthreads();
-    build_bg(L, cgs, desc, ys, gs, bg);
-    __syncthreads();
-
-    // (a) one task per (component m = o1 + m1, channel span): 16 edge rows x 16*V channels
-    for (int task = wave; task < L.M * NSPAN; task += 4) {
-      const int m = task / NSPAN, span = task - m * NSPAN;
-      int g = 0;
-      while (g + 1 < L.NG && m >= L.g_o1[g + 1]) ++g;
-      const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
-      const float* arow = bg + r * bg_stride(L) + L.g_bgoff[g] + m1 * kpad + 4 * q;
-      const float* bcol = gn + (int64_t)L.g_kstart[g] * C + span * SPAN + V * r;
-      f4 acc[V];
-#pragma unroll
-      for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
-      for (int t = 0; t < kpad; t += 16) {
-        const f4 a4 = *reinterpret_cast<const f4*>(arow + t);
-        VecF<V> bf[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int kkl = t + 4 * q + s;
-          if (kkl < kcount) {
-            bf[s] = ldv<V>(bcol + (int64_t)kkl * C);
-          } else {
-#pragma unroll
-            for (int j = 0; j < V; ++j) bf[s].v[j] = 0.f;
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < V; ++j)
-          acc[j] = mfma_k16(a4, f4{bf[0].v[j], bf[1].v[j], bf[2].v[j], bf[3].v[j]}, acc[j]);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = 4 * q + i;
-        if (e >= cnt) continue;
-        VecF<V> o;
-#pragma unroll
-        for (int j = 0; j < V; ++j) o.v[j] = acc[j][i] * scale;
-        stv<V>(DX + ((int64_t)(eb + e) * L.M + m) * C + span * SPAN + V * r, o);
-      }
-    }
+    stage_chunk<false>(L, eb, cnt, Y, gates, esrc, nullptr, nullptr, ys, gs, srcs);
     __syncthreads();
 
     // (b) one task per component m: 16 edge rows x (kpad of its group), K = channels
@@ -623,21 +606,6 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(FscIctdLayout L, int n
       }
       dY[(int64_t)(eb + e) * L.NY + yc] = acc;
     }
-  }
-}
-
-// dx[m][:][:] = sum over out-edges of m of DX[e][:][:] (receiver-sorted ids grouped by source)
-template <int C>
-__global__ __launch_bounds__(256) void source_sum_kernel(int M, const int32_t* __restrict__ src_ptr,
-                                                         const int32_t* __restrict__ src_perm,
-                                                         const float* __restrict__ DX, float* __restrict__ dx) {
-  const int m = blockIdx.x;
-  const int beg = src_ptr[m], end = src_ptr[m + 1];
-  const int tot = M * C;
-  for (int idx = threadIdx.x * 4; idx < tot; idx += blockDim.x * 4) {
-    f4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int j = beg; j < end; ++j) s += ld4(DX + (int64_t)src_perm[j] * tot + idx);
-    st4(dx + (int64_t)m * tot + idx, s);
   }
 }
 
@@ -901,35 +869,149 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
   return 0;
 }
 
-template <int C>
-int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
-              const float* Y, const float* gates, const float* cg, const float* W, float* Z, float* out,
-              const int32_t* node_order, hipStream_t st) {
+// ---------------------------------------------------------------- dual layout (input gradient)
+// dx_m[o1+m1][i] = sum_p sum_o W[p][o][i] R_m[(p,m1)][o],  R_m[(p,m1)][o] = sum_{e: src=m} sum_m3
+// bg_e[m1][(p,m3)] G_dst(e)[oo_p+m3][o] / deg(dst(e)).  R is the forward projection of the layout with every
+// path reversed (k3 -> k1: d1 and d3 swapped, coupling C^T[m3][m2][m1], the same gate and harmonic), paths
+// grouped by their output key, run over the source grouping of the edges; dx is then the forward channel
+// mix of that layout with W^T (the prepared weights hold both orientations).  Built on the host per call.
+struct DualMap {
+  int32_t p_of[64];   // dual path -> path of the layout
+};
+
+int dual_layout(const FscIctdLayout& L, FscIctdLayout& D, DualMap& map) {
+  D = L;
+  // dual paths: the layout's paths stably ordered by output component offset
+  int np = 0;
+  for (int pass = 0; pass < L.M; ++pass)
+    for (int p = 0; p < L.NP; ++p)
+      if (L.p_oo[p] == pass) map.p_of[np++] = p;
+  if (np != L.NP) return 1;
+  int ng = -1, koff = 0, cgoff = 0, bgoff = 0, tile0 = 0, prev_oo = -1;
+  for (int q = 0; q < np; ++q) {
+    const int p = map.p_of[q];
+    const int g1 = L.p_group[p];
+    const int d1 = L.g_d1[g1], d2 = L.p_d2[p], d3 = L.p_d3[p];
+    if (L.p_oo[p] != prev_oo) {                         // a new dual group: one output key of the layout
+      if (ng >= 0) {
+        D.g_kpad[ng] = 16 * ((D.g_kcount[ng] + 15) / 16);
+        D.g_bgoff[ng] = bgoff;
+        D.g_tile0[ng] = tile0;
+        bgoff += D.g_d1[ng] * D.g_kpad[ng];
+        tile0 += D.g_kpad[ng] / 16;
+      }
+      if (++ng >= 8) return 1;
+      prev_oo = L.p_oo[p];
+      D.g_o1[ng] = L.p_oo[p];
+      D.g_d1[ng] = d3;
+      D.g_kstart[ng] = koff;
+      D.g_kcount[ng] = 0;
+    }
+    D.g_kcount[ng] += d1;
+    D.p_gate[q] = L.p_gate[p];
+    D.p_oy[q] = L.p_oy[p];
+    D.p_d2[q] = d2;
+    D.p_d3[q] = d1;
+    D.p_koff[q] = koff;
+    D.p_cgoff[q] = cgoff;
+    D.p_group[q] = ng;
+    D.p_oo[q] = L.g_o1[g1];
+    if (koff + d1 > 128) return 1;
+    for (int k = 0; k < d1; ++k) D.kk_path[koff + k] = q;
+    koff += d1;
+    cgoff += d1 * d2 * d3;
+  }
+  D.g_kpad[ng] = 16 * ((D.g_kcount[ng] + 15) / 16);
+  D.g_bgoff[ng] = bgoff;
+  D.g_tile0[ng] = tile0;
+  bgoff += D.g_d1[ng] * D.g_kpad[ng];
+  tile0 += D.g_kpad[ng] / 16;
+  D.NG = ng + 1;
+  D.KT = koff;
+  D.NBGP = bgoff;
+  D.KTT = tile0;
+  if (D.KTT > 16) return 1;
+  for (int g = 0; g < D.NG; ++g)
+    for (int t = D.g_tile0[g]; t < D.g_tile0[g] + D.g_kpad[g] / 16; ++t) D.tile_group[t] = g;
+  // output keys of the dual mix: the layout's input keys (path groups)
+  D.NK = L.NG;
+  for (int g = 0; g < L.NG; ++g) {
+    D.k_oo[g] = L.g_o1[g];
+    D.k_d[g] = L.g_d1[g];
+  }
+  return 0;
+}
+
+// cgd[dual path q][m3][m2][m1] = cg[path p_of[q]][m1][m2][m3]
+__global__ __launch_bounds__(256) void transpose_cg_kernel(FscIctdLayout L, FscIctdLayout D, DualMap map,
+                                                           const float* __restrict__ cg, float* __restrict__ cgd) {
+  const int q = blockIdx.x;
+  const int p = map.p_of[q];
+  const int d1 = L.g_d1[L.p_group[p]], d2 = L.p_d2[p], d3 = L.p_d3[p];
+  const float* src = cg + L.p_cgoff[p];
+  float* dst = cgd + D.p_cgoff[q];
+  for (int idx = threadIdx.x; idx < d1 * d2 * d3; idx += blockDim.x) {
+    const int m3 = idx / (d2 * d1), m2 = (idx / d1) % d2, m1 = idx % d1;
+    dst[idx] = src[(m1 * d2 + m2) * d3 + m3];
+  }
+}
+
+// The projection and channel mix of a layout.  Forward: blocks are receivers (ptr = dst_ptr), the edge at
+// CSR position j is j and gathers x[esrc[j]]; dual (backward): ptr = src_ptr, eperm = src_perm, esrc the
+// receiver of each edge, gdeg = dst_ptr, and the mix weights are the transposed planes.
+template <int C, bool DUAL>
+int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const int32_t* esrc, const int32_t* eperm,
+                  const int32_t* gdeg, const float* x, const float* Y, const float* gates, const float* cg,
+                  const _Float16* Wh, const float* winv, float* Z, float* out, const int32_t* node_order,
+                  const char* timer_project, const char* timer_mix, hipStream_t st) {
   const int ncg = cg_length(L);
   {
-    LaunchTimer tm("ictd_project", st);
+    LaunchTimer tm(timer_project, st);
     const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
-    project_fwd_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
-                                                          Z + N * L.KT * C, N, node_order);
+    project_fwd_kernel<C, DUAL><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
+                                                          N, node_order, eperm, gdeg);
   }
   if (check_launch("ictd project_fwd")) return 2;
   int dmax = 1;
   for (int k = 0; k < L.NK; ++k) dmax = max(dmax, L.k_d[k]);
   {
-    LaunchTimer tm("ictd_mix", st);
+    LaunchTimer tm(timer_mix, st);
     constexpr int RT = mix_rt<C>();
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NK);
-    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, reinterpret_cast<const _Float16*>(W),
-                                                 W + mix_weight_floats(L.NREF, C) - MIXW_TAIL, out, N);
+    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, Wh, winv, out, N);
   }
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
 
 template <int C>
+int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
+              const float* Y, const float* gates, const float* cg, const float* W, float* Z, float* out,
+              const int32_t* node_order, hipStream_t st) {
+  return project_mix_c<C, false>(L, N, dst_ptr, esrc, nullptr, nullptr, x, Y, gates, cg,
+                          reinterpret_cast<const _Float16*>(W), W + mix_weight_floats(L.NREF, C) - MIXW_TAIL, Z, out,
+                          node_order, "ictd_project", "ictd_mix", st);
+}
+
+// Workspace of the backward: dZ [N][KT][C] + N scales; R [N][KT_dual][C] + N scales, then the dual
+// coupling table.
+int64_t dual_ws_floats(const FscIctdLayout& L, int64_t N, int C) {
+  int64_t kt = 0;
+  for (int p = 0; p < L.NP; ++p) kt += L.g_d1[L.p_group[p]];
+  return N * kt * C + N + cg_length(L);
+}
+
+template <int C>
 int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc,
-               const int32_t* src_ptr, const int32_t* src_perm, const float* G, const float* x, const float* Y,
-               const float* gates, const float* cg, const float* Wt, float* dZ, float* DX, float* dx,
+               const int32_t* src_ptr, const int32_t* src_perm, const int32_t* edst, const float* G, const float* x,
+               const float* Y, const float* gates, const float* cg, const float* Wt, float* dZ, float* Rw, float* dx,
                float* dgates, float* dY, const int32_t* node_order, hipStream_t st) {
+  FscIctdLayout D;
+  DualMap map;
+  if (dual_layout(L, D, map) || check_layout(&D, C, "ictd dual layout")) {
+    set_error("fsc_ictd_conv_backward: the layout has no valid dual (path table out of range)");
+    return 1;
+  }
+  // gate and harmonic gradients: g = dZ / deg with dZ = W^T G (per path), then H, T per edge
   int dmax = 1;
   for (int p = 0; p < L.NP; ++p) dmax = max(dmax, L.p_d3[p]);
   {
@@ -947,15 +1029,18 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
     LaunchTimer tm("ictd_project_grad", st);
     const int ncg = cg_length(L);
     const size_t lds = (size_t)proj_smem(L, ncg, true).total * sizeof(float);
-    project_bwd_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, DX, dgates,
-                                                          dY, N, node_order);
+    project_grad_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, dgates, dY,
+                                                           N, node_order);
   }
-  if (check_launch("ictd project_bwd")) return 2;
-  {
-    LaunchTimer tm("ictd_source_sum", st);
-    source_sum_kernel<C><<<(unsigned)N, 256, 0, st>>>(L.M, src_ptr, src_perm, DX, dx);
-  }
-  return check_launch("ictd source_sum") ? 2 : 0;
+  if (check_launch("ictd project_grad")) return 2;
+  // input gradient: dual projection over the source grouping, then the mix with W^T
+  float* cgd = Rw + N * D.KT * C + N;
+  transpose_cg_kernel<<<(unsigned)D.NP, 256, 0, st>>>(L, D, map, cg, cgd);
+  if (check_launch("ictd transpose_cg")) return 2;
+  return project_mix_c<C, true>(D, N, src_ptr, edst, src_perm, dst_ptr, G, Y, gates, cgd,
+                          reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
+                          Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, Rw, dx, node_order, "ictd_dual_project",
+                          "ictd_dual_mix", st);
 }
 
 }  // namespace ictd
@@ -991,29 +1076,38 @@ int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, fl
   return check_launch("ictd prepare_weights") ? 2 : 0;
 }
 
+int fsc_ictd_backward_workspace(const FscIctdLayout* layout, int64_t n_nodes, int32_t channels, int64_t* dz_floats,
+                                int64_t* r_floats) {
+  if (check_layout(layout, channels, "fsc_ictd_backward_workspace")) return 1;
+  FSC_CHECK_ARG(dz_floats && r_floats && n_nodes >= 0, "fsc_ictd_backward_workspace: bad argument");
+  *dz_floats = n_nodes * (int64_t)layout->KT * channels + n_nodes;
+  *r_floats = dual_ws_floats(*layout, n_nodes, channels);
+  return 0;
+}
+
 int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                            const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
-                           const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
-                           const float* gates, const float* cg, const float* Wt, float* dz_ws,
-                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y, const int32_t* node_order,
+                           const int32_t* src_perm, const int32_t* edge_dst, const float* grad_out, const float* x,
+                           const float* Y, const float* gates, const float* cg, const float* Wt, float* dz_ws,
+                           float* r_ws, float* grad_x, float* grad_gates, float* grad_Y, const int32_t* node_order,
                            hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv_backward")) return 1;
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
                 "fsc_ictd_conv_backward: bad size");
-  FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && x && cg && Wt && dz_ws && grad_x,
+  FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && x && cg && Wt && dz_ws && r_ws && grad_x,
                 "fsc_ictd_conv_backward: null pointer");
-  FSC_CHECK_ARG(n_edges == 0 || (edge_src && src_perm && Y && gates && dxe_ws && grad_gates && grad_Y),
+  FSC_CHECK_ARG(n_edges == 0 || (edge_src && src_perm && edge_dst && Y && gates && grad_gates && grad_Y),
                 "fsc_ictd_conv_backward: null edge pointer");
   if (n_nodes == 0) return 0;
   const FscIctdLayout& L = *layout;
   if (channels == 128)
-    return backward_c<128>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                           dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
+    return backward_c<128>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, grad_out, x, Y, gates, cg, Wt,
+                           dz_ws, r_ws, grad_x, grad_gates, grad_Y, node_order, stream);
   if (channels == 64)
-    return backward_c<64>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                          dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
-  return backward_c<32>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, grad_out, x, Y, gates, cg, Wt, dz_ws,
-                        dxe_ws, grad_x, grad_gates, grad_Y, node_order, stream);
+    return backward_c<64>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, grad_out, x, Y, gates, cg, Wt,
+                          dz_ws, r_ws, grad_x, grad_gates, grad_Y, node_order, stream);
+  return backward_c<32>(L, n_nodes, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, grad_out, x, Y, gates, cg, Wt,
+                        dz_ws, r_ws, grad_x, grad_gates, grad_Y, node_order, stream);
 }
 
 int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,

@@ -225,8 +225,8 @@ Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({ictd_weigh
 
 Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
                  const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                 const Tensor& src_perm, const Tensor& node_order, at::IntArrayRef layout) {
-  require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
+                 const Tensor& src_perm, const Tensor& edge_dst, const Tensor& node_order, at::IntArrayRef layout) {
+  require_gpu({x_, Y_, gates_, W_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
   const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
   const FscIctdLayout* L = &Lv;
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
@@ -244,7 +244,8 @@ Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const
 }
 
 Tensor ictd_conv_meta(const Tensor& x, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef) {
+                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                      at::IntArrayRef) {
   return at::empty(x.sizes(), fopts(x));
 }
 
@@ -252,20 +253,23 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
                                                       const Tensor& gates_, const Tensor& Wt, const Tensor& cg,
                                                       const Tensor& dst_ptr, const Tensor& edge_src,
                                                       const Tensor& src_ptr, const Tensor& src_perm,
-                                                      const Tensor& node_order, at::IntArrayRef layout) {
-  require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
+                                                      const Tensor& edge_dst, const Tensor& node_order,
+                                                      at::IntArrayRef layout) {
+  require_gpu({grad_out, x_, Y_, gates_, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
   const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
   const FscIctdLayout* L = &Lv;
   const int64_t N = x_.size(0), M = x_.size(1), C = x_.size(2), E = Y_.size(0);
   Tensor g = f32c(grad_out), x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
   TORCH_CHECK(Wt.dim() == 1 && Wt.numel() == ictd_weight_floats(L->NREF, C),
               "ictd_conv_backward: Wt must be ictd_prepare_weights(W) of this layout's weights");
-  Tensor dz = at::empty({N * L->KT * C + N}, fopts(x)), dxe = at::empty({E, M, C}, fopts(x)), dx = at::empty({N, M, C}, fopts(x));
+  int64_t dz_f = 0, r_f = 0;
+  check(fsc_ictd_backward_workspace(L, N, (int32_t)C, &dz_f, &r_f), "fsc_ictd_backward_workspace");
+  Tensor dz = at::empty({dz_f}, fopts(x)), rw = at::empty({r_f}, fopts(x)), dx = at::empty({N, M, C}, fopts(x));
   Tensor dgates = at::zeros({E, L->NREF}, fopts(x)), dY = at::empty({E, L->NY}, fopts(x));
   check(fsc_ictd_conv_backward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
-                               ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")), cf(g), cf(x), cf(Y),
-                               cf(gates), cf(cg), cf(Wt), mf(dz), mf(dxe), mf(dx), mf(dgates), mf(dY),
-                               order_ptr(node_order, N), stream_of(x)),
+                               ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")),
+                               ci(i32c(edge_dst, "edge_dst")), cf(g), cf(x), cf(Y), cf(gates), cf(cg), cf(Wt), mf(dz),
+                               mf(rw), mf(dx), mf(dgates), mf(dY), order_ptr(node_order, N), stream_of(x)),
         "fsc_ictd_conv_backward");
   return {dx, dgates, dY};
 }
@@ -273,7 +277,7 @@ std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, co
 std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward_meta(const Tensor&, const Tensor& x, const Tensor& Y,
                                                            const Tensor& gates, const Tensor&, const Tensor&,
                                                            const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                           const Tensor&, at::IntArrayRef) {
+                                                           const Tensor&, const Tensor&, at::IntArrayRef) {
   return {at::empty(x.sizes(), fopts(x)), at::empty(gates.sizes(), fopts(gates)), at::empty(Y.sizes(), fopts(Y))};
 }
 
@@ -871,27 +875,29 @@ std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& 
 
 struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg,
-                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order,
-                               std::vector<int64_t> layout) {
+                               Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor edge_dst,
+                               Tensor node_order, std::vector<int64_t> layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                                       const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv");
-    Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout);
-    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order});
+                                      const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv");
+    Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order, layout);
+    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
     ctx->saved_data["layout"] = layout;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(12);
+    variable_list res(13);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {3, 4, 5}, "the ICTD conv");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv_backward");
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+        at::IntArrayRef)>("fsctep::ictd_conv_backward");
     const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
-    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], layout);
+    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], s[10],
+                                    layout);
     res[0] = dx;
     res[1] = dY;
     res[2] = dgates;
@@ -901,8 +907,10 @@ struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
 
 Tensor ictd_conv_autograd(const Tensor& x, const Tensor& Y, const Tensor& gates, const Tensor& W, const Tensor& Wt,
                           const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
-                          const Tensor& src_perm, const Tensor& node_order, at::IntArrayRef layout) {
-  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout.vec())[0];
+                          const Tensor& src_perm, const Tensor& edge_dst, const Tensor& node_order,
+                          at::IntArrayRef layout) {
+  return IctdConvFn::apply(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order,
+                           layout.vec())[0];
 }
 
 struct IctdConv1Fn : public torch::autograd::Function<IctdConv1Fn> {
@@ -1187,10 +1195,10 @@ TORCH_LIBRARY(fsctep, m) {
         "-> (Tensor, Tensor)");
   m.def("ictd_prepare_weights(Tensor W) -> Tensor");
   m.def("ictd_conv(Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg, Tensor dst_ptr, "
-        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order, int[] layout) -> Tensor");
+        "Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, int[] layout) -> Tensor");
   m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
-        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor node_order, int[] layout) "
-        "-> (Tensor, Tensor, Tensor)");
+        "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, "
+        "int[] layout) -> (Tensor, Tensor, Tensor)");
   m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
         "int n_species, int n_comps, int[] layout) -> Tensor");
   m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "

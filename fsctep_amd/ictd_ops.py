@@ -5,8 +5,9 @@ A layout (active irreps + live paths, see ``ictd_basis.Layout``) is turned into 
 struct's int32 words (an ``int[]`` argument).  The ops are registered in C++ by ``libfsctep_torch.so``:
 
     ictd_prepare_weights(W) -> Wt   (split-fp16 channel-mix weights, opaque)
-    ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout) -> out
-    ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, node_order, layout)
+    ictd_conv(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order, layout) -> out
+    ictd_conv_backward(grad_out, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order,
+                       layout)
     ictd_conv1(F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, n_comps, layout)
     ictd_conv1_backward(grad_out, F, gates, qtab, dst_ptr, edge_pair, node_species, n_species, layout)
 """
@@ -159,7 +160,7 @@ def edge_harmonics(n: Tensor, lmax: int) -> Tensor:
 def ictd_conv_apply(x, Y, gates, W, Wt, cg, graph, layout_id: int):
     """Differentiable conv2..n: x (N,M,C), Y (E,NY), gates (E,NREF) -> (N,M,C)."""
     return torch.ops.fsctep.ictd_conv(x, Y, gates, W, Wt, cg, graph.dst_ptr, graph.src32, graph.src_ptr,
-                                      graph.src_perm, graph.node_order, layout_words(layout_id))
+                                      graph.src_perm, graph.dst32, graph.node_order, layout_words(layout_id))
 
 
 def ictd_conv1_apply(F, gates, qtab, graph, layout_id: int):

@@ -266,13 +266,17 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
 int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wp, hipStream_t stream);
 
 /* Backward for forces: grad_x [N][M][C], grad_gates [E][NREF] (caller zero-fills: entries of paths
- * without a geometric operand stay 0), grad_Y [E][NY].  Wp as for the forward; dz_ws N*KT*C + N floats,
- * dxe_ws [E][M][C] scratch; node_order as for the forward. */
+ * without a geometric operand stay 0), grad_Y [E][NY].  Wp as for the forward; edge_dst [E] the receiver
+ * of each receiver-sorted edge; dz_ws and r_ws scratch of fsc_ictd_backward_workspace floats; node_order as
+ * for the forward.  grad_x is formed per source (the projection over the source grouping with every path
+ * reversed, then the channel mix with W^T), so no per-edge gradient is stored. */
+int fsc_ictd_backward_workspace(const FscIctdLayout* layout, int64_t n_nodes, int32_t channels, int64_t* dz_floats,
+                                int64_t* r_floats);
 int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                            const int32_t* dst_ptr, const int32_t* edge_src, const int32_t* src_ptr,
-                           const int32_t* src_perm, const float* grad_out, const float* x, const float* Y,
-                           const float* gates, const float* cg, const float* Wp, float* dz_ws,
-                           float* dxe_ws, float* grad_x, float* grad_gates, float* grad_Y,
+                           const int32_t* src_perm, const int32_t* edge_dst, const float* grad_out, const float* x,
+                           const float* Y, const float* gates, const float* cg, const float* Wp, float* dz_ws,
+                           float* r_ws, float* grad_x, float* grad_gates, float* grad_Y,
                            const int32_t* node_order, hipStream_t stream);
 
 /* conv1 (ICTDIrrepsE3Conv / ICTDO3E3Conv, pure_cartesian_ictd_layers_full.py:341-473,
