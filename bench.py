@@ -294,16 +294,19 @@ def _rate(work: dict, avg_ms: float) -> dict:
 
 
 def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: str, dev,
-            table: bool = True) -> dict:
+            table: bool = True, precision: str = "fp32", keep: bool = False, extras: bool = True,
+            system=None) -> dict:
     import numpy as np
     import torch
     from fsctep_amd import _lib
     w = WORKLOADS[mode]
     t_build = time.perf_counter()
-    system = _system(mode, n_atoms, seed)
+    system = _system(mode, n_atoms, seed) if system is None else system
     print(f"[bench] {mode}: {system.num_atoms} atoms, {system.num_edges} edges "
           f"({time.perf_counter() - t_build:.1f} s to build)", file=sys.stderr, flush=True)
     model = build_model(mode, dev)
+    if precision != "fp32":
+        model.channel_mix_precision = precision
     C = w["channels"]
     N, E = system.num_atoms, system.num_edges
 
@@ -407,6 +410,16 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
                 rates[k] = dict(_rate(work_of(k), t.total_ms / t.launches), launches_per_step=t.launches // kt_steps)
         out["kernels"] = rates
 
+    if keep:
+        out["_ef"] = (e.double().cpu().numpy(), f.double().cpu().numpy())
+    out["products"] = PRODUCTS[mode] if precision == "fp32" else {
+        "node_expand, node_expand_grad, edge_message": "bf16 MFMA, one product, fp32 accumulation",
+        "everything else": "as in the fp32 configuration"}
+    out["config"] = {"workload": workload_name(mode, N, E), "mode": mode, "atoms": N, "edges": E,
+                     "channel_mix_precision": precision}
+    if not extras:
+        return out
+
     # the reference-signature forward: the graph is prepared inside every call
     kw = {"external_tensor": field} if field is not None else {}
 
@@ -444,8 +457,6 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
 
     out["parity"] = parity_vs_fixture(mode, system, seed, e.cpu().numpy(), f.cpu().numpy(),
                                       None if dip is None else dip.cpu().numpy())
-    out["products"] = PRODUCTS[mode]
-    out["config"] = {"workload": workload_name(mode, N, E), "mode": mode, "atoms": N, "edges": E}
     return out
 
 
@@ -464,6 +475,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="only the selected workload (by default the sparse headline also runs ICTD 10k and ICTD-O3 4k)")
     ap.add_argument("--no-kernel-table", action="store_true")
+    ap.add_argument("--no-large", action="store_true",
+                    help="skip the 100k-atom sparse workload (fp32 and the bf16 channel-mix variant)")
+    ap.add_argument("--channel-mix", choices=["fp32", "bf16"], default="fp32",
+                    help="products of the sparse channel mix for --mode sparse runs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, copy a 1 GiB fp32 buffer 3 times (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -478,7 +493,8 @@ def main():
 
     import torch
     dev = torch.device("cuda:0")
-    head = measure(args.mode, n_atoms, seed, args.steps, args.warmup, kname, dev, table=not args.no_kernel_table)
+    head = measure(args.mode, n_atoms, seed, args.steps, args.warmup, kname, dev, table=not args.no_kernel_table,
+                   precision=args.channel_mix if args.mode == "sparse" else "fp32")
     N, E = head["atoms"], head["edges"]
     out = {
         "metric": "atom-steps/sec (energy+forces) at 10k atoms; TP kernel HBM GB/s vs peak",
@@ -522,6 +538,21 @@ def main():
         r.pop("atoms")
         r.pop("edges")
         workloads[m] = r
+    if extra and not args.no_large:
+        # 100k-atom sparse domain: fp32-accurate products and the bf16 channel-mix variant, and the
+        # variant's error against the fp32 path on the same system
+        big = {}
+        sys100k = _system("sparse", 100000, WORKLOADS["sparse"]["seed"])
+        for prec in ("fp32", "bf16"):
+            r = measure("sparse", 100000, WORKLOADS["sparse"]["seed"], max(3, args.steps // 2), 2, "edge_message_grad",
+                        dev, table=False, precision=prec, keep=True, extras=False, system=sys100k)
+            big[prec] = r
+        (e32, f32), (e16, f16) = big["fp32"].pop("_ef"), big["bf16"].pop("_ef")
+        big["bf16_vs_fp32"] = {"energy_rel": float(f"{_rel_inf(e16, e32):.3e}"),
+                               "forces_rel": float(f"{_rel_inf(f16, f32):.3e}"),
+                               "energy_total_rel": float(f"{abs(e16.sum() - e32.sum()) / abs(e32.sum()):.3e}"),
+                               "speedup": round(big["fp32"]["ms_per_step"] / big["bf16"]["ms_per_step"], 3)}
+        workloads["sparse-100k"] = big
     if workloads:
         out["workloads"] = workloads
 

@@ -22,9 +22,9 @@ SIGNATURES = {
     "fsc_timing_end": [ctypes.POINTER(ctypes.c_double), _pi64],
     "fsc_sparse_conv_workspace": [_i64, _i64, _i32, _pi64, _pi64],
     "fsc_sparse_conv_prepare_weights": [_p, _p, _i32, _p, _p, _p],
-    "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p],
+    "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _i32, _p, _p],
     "fsc_sparse_conv_backward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f32,
-                                 _p, _p, _p, _p, _p, _p],
+                                 _p, _p, _p, _p, _i32, _p, _p],
     "fsc_sparse_conv1_pair_table": [_p, _p, _p, _i32, _i32, _p, _p, _p],
     "fsc_sparse_conv1_forward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_sparse_conv1_backward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],

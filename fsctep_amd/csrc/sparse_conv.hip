@@ -43,10 +43,12 @@ __host__ __device__ inline int64_t s_node_stride(int C) { return (int64_t)NSLOT 
 // bk6[part][p][a][col] (transpose of bk1[p]): the values times the power of two sw (max |L|, |b|
 // times sw below 2^14) split into two fp16 parts (h, l; split2h), for the split-fp16 products of
 // node_expand and node_expand_grad.  Each buffer is the two parts (6*65*C*C fp16 each, as many floats
-// together) followed by a tail of SW_TAIL floats: [0] = 1/sw, [256..511] partial maxima (bk1 only).
+// together) followed by a tail of SW_TAIL floats: [0] = 1/sw, [256..511] partial maxima (bk1 only), then
+// the same scaled values rounded to bf16 (one plane, 6*65*C*C bf16) for the bf16 channel-mix variant.
 constexpr int SW_TAIL = 512;
 constexpr int SWMAX_BLOCKS = 256;
 __host__ __device__ inline int64_t sparse_weight_floats(int C) { return 6LL * 65 * C * C + SW_TAIL; }
+__host__ __device__ inline int64_t sparse_weight_floats_all(int C) { return sparse_weight_floats(C) + 3LL * 65 * C * C; }
 
 // wmax[block] = max |L|, |b| over the grid-stride share of the block (grid SWMAX_BLOCKS x 256).
 __global__ __launch_bounds__(256) void weight_absmax_kernel(const float* __restrict__ L, int64_t nl,
@@ -79,6 +81,8 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
   }
   _Float16* bk1 = reinterpret_cast<_Float16*>(bk1f);
   _Float16* bk6 = reinterpret_cast<_Float16*>(bk6f);
+  __bf16* bk1b = reinterpret_cast<__bf16*>(bk1f + total + SW_TAIL);
+  __bf16* bk6b = reinterpret_cast<__bf16*>(bk6f + total + SW_TAIL);
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int a = (int)(idx % C);
@@ -100,6 +104,9 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
     bk1[total + idx] = lb;
     bk6[o] = hb;
     bk6[total + o] = lb;
+    const __bf16 bb = (__bf16)vs;
+    bk1b[idx] = bb;
+    bk6b[o] = bb;
   }
 }
 
@@ -115,13 +122,15 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
 // A row i is column 16*j + i, so lane (r, q) ends with columns 16j+4q..16j+4q+3 of row r: the
 // four lanes of a row store 64 contiguous bytes per instruction.  Stores go through a buffer
 // descriptor spanning the block's nodes; rows past the end are sent out of range and dropped.
+// BF16: the bf16 channel-mix variant, one bf16 MFMA per product (x rows and the weights rounded to bf16,
+// fp32 accumulation); the weights come from the bf16 plane of bk1.
 struct PathTiles {
   int off[7];
 };
 constexpr int NE_ROWS = 128;   // rows per node_expand block
 constexpr int NE_TPB = 13;     // 80-column tiles per node_expand block
 
-template <int C>
+template <int C, bool BF16>
 __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __restrict__ x,
                                                              const _Float16* __restrict__ bk1,
                                                              const float* __restrict__ winv,
@@ -132,7 +141,8 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   constexpr int NCG = (NTC + NE_TPB - 1) / NE_TPB;   // column groups
   constexpr int RT = NE_ROWS / 64;                   // 16-row tiles per wave
   constexpr int RW = C + 8;                          // fp16 per LDS row (padding against bank conflicts)
-  constexpr int NPC = 2 * WCOLS * (C / 8);           // 16-byte pieces of a tile
+  constexpr int NPART = BF16 ? 1 : 2;                // weight parts staged (fp16 h, l or one bf16 plane)
+  constexpr int NPC = NPART * WCOLS * (C / 8);       // 16-byte pieces of a tile
   constexpr int NST = (NPC + 255) / 256;
   __shared__ __align__(16) _Float16 sb[2][2][WCOLS][RW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -156,6 +166,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   const __amdgpu_buffer_rsrc_t out =
       buffer_rsrc(S + mfirst * s_node_stride(C), (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * 4));
   h8 xh[RT][KS], xl[RT][KS];
+  bf8 xb[RT][KS];
   float oscale[RT];    // 1 / (sw * row scale)
   uint32_t ooff[RT];   // byte offset of the lane's first column in the store window
 #pragma unroll
@@ -179,8 +190,15 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
     vmax = fmaxf(vmax, __shfl_xor(vmax, 16, 64));
     vmax = fmaxf(vmax, __shfl_xor(vmax, 32, 64));
     const float sr = pow2_scale(vmax);
+    if constexpr (BF16) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) split2h(v[ks], sr, xh[rt][ks], xl[rt][ks]);
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xb[rt][ks][j] = (__bf16)(v[ks][j] * sr);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) split2h(v[ks], sr, xh[rt][ks], xl[rt][ks]);
+    }
     oscale[rt] = winv[0] / sr;   // sr is a power of two: exact
     ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * 4)
                   : kDropOffset;
@@ -223,10 +241,16 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const h8 wh = *reinterpret_cast<const h8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
-        const h8 wl = *reinterpret_cast<const h8*>(&sb[buf][1][16 * j + r][32 * ks + 8 * q]);
+        if constexpr (BF16) {
+          const bf8 wb = *reinterpret_cast<const bf8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_x3(wh, wl, xh[rt][ks], xl[rt][ks], acc[rt][j]);
+          for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_bf16(wb, xb[rt][ks], acc[rt][j]);
+        } else {
+          const h8 wh = *reinterpret_cast<const h8*>(&sb[buf][0][16 * j + r][32 * ks + 8 * q]);
+          const h8 wl = *reinterpret_cast<const h8*>(&sb[buf][1][16 * j + r][32 * ks + 8 * q]);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_x3(wh, wl, xh[rt][ks], xl[rt][ks], acc[rt][j]);
+        }
       }
     // stage the next tile first: the waits for its loads then do not cover this tile's stores
     __builtin_amdgcn_sched_barrier(0);
@@ -256,7 +280,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 // group q holds chunk columns 8q..8q+7 of both operands.
 constexpr int NEG_ROWS = 256;   // slot rows per block
 
-template <int C>
+template <int C, bool BF16>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
                                                                   const float* __restrict__ dscale,
                                                                   const _Float16* __restrict__ bk6,
@@ -268,7 +292,8 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   constexpr int QW = C / 4;         // consecutive a per lane in the output
   constexpr int TPP = COLS / 32;    // K chunks per path
   constexpr int RS = 40;            // fp16 per LDS row: 32 + 8 padding
-  constexpr int NPC = 2 * C * 4;              // 16-byte pieces of a chunk (2 parts x C rows x 4)
+  constexpr int NPART = BF16 ? 1 : 2;         // fp16 h, l parts or one bf16 plane
+  constexpr int NPC = NPART * C * 4;          // 16-byte pieces of a chunk (parts x C rows x 4)
   constexpr int NST = (NPC + 255) / 256;      // per thread
   __shared__ __align__(16) _Float16 wsh[2][2][C][RS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -347,19 +372,31 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
     }
     __builtin_amdgcn_sched_barrier(0);
     h8 dh[4], dl[4];
+    bf8 db[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const float v[8] = {bc[rt][0].x, bc[rt][0].y, bc[rt][0].z, bc[rt][0].w,
                           bc[rt][1].x, bc[rt][1].y, bc[rt][1].z, bc[rt][1].w};
-      split2h(v, rsc[rt], dh[rt], dl[rt]);
+      if constexpr (BF16) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) db[rt][j] = (__bf16)(v[j] * rsc[rt]);
+      } else {
+        split2h(v, rsc[rt], dh[rt], dl[rt]);
+      }
     }
 #pragma unroll
     for (int at = 0; at < NA; ++at) {
       const int a = QW * (r >> 2) + 4 * at + (r & 3);
-      const h8 wh = *reinterpret_cast<const h8*>(&wsh[buf][0][a][8 * q]);
-      const h8 wl = *reinterpret_cast<const h8*>(&wsh[buf][1][a][8 * q]);
+      if constexpr (BF16) {
+        const bf8 wb = *reinterpret_cast<const bf8*>(&wsh[buf][0][a][8 * q]);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_x3(wh, wl, dh[rt], dl[rt], acc[rt][at]);
+        for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_bf16(wb, db[rt], acc[rt][at]);
+      } else {
+        const h8 wh = *reinterpret_cast<const h8*>(&wsh[buf][0][a][8 * q]);
+        const h8 wl = *reinterpret_cast<const h8*>(&wsh[buf][1][a][8 * q]);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) acc[rt][at] = mfma_x3(wh, wl, dh[rt], dl[rt], acc[rt][at]);
+      }
     }
     if (t + 1 < te) {
       store_w(buf ^ 1);
@@ -410,12 +447,12 @@ __global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, f
 // One block (3 waves) per source node; P[eid][col] = sum_k h[eid][k] S[m][col][k] + Sb[m][col].
 // Transposed product: S rows (columns of P) are the A operand, the node's edges (h rows, split into
 // three bf16 planes in LDS) the B operand; products are split-bf16 (mfma_x6, K = 64 in two steps),
-// the S rows split in registers.  A wave takes 32-column blocks of P's chunk-major column order;
+// the S rows split in registers (BF16: one bf16 MFMA per product, both operands rounded to bf16).  A wave takes 32-column blocks of P's chunk-major column order;
 // tile jt's A row i is column 8*(i/4) + 4*jt + i%4 of the block, so lane (r, q) ends with 8
 // consecutive columns of edge r: two float4 stores, 128 contiguous bytes per edge per block.
 constexpr int EP = 64;   // edges per pass held in LDS
 
-template <int C>
+template <int C, bool BF16>
 __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __restrict__ h,
                                                            const float* __restrict__ S,
                                                            const int32_t* __restrict__ src_ptr,
@@ -472,10 +509,16 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       const f4 x0 = ld4(hp), x1 = ld4(hp + 4);
       const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       bf8 bh, bm, bl;
-      split3(v, bh, bm, bl);
-      *reinterpret_cast<bf8*>(&hs3[0][e][8 * k8]) = bh;
-      *reinterpret_cast<bf8*>(&hs3[1][e][8 * k8]) = bm;
-      *reinterpret_cast<bf8*>(&hs3[2][e][8 * k8]) = bl;
+      if constexpr (BF16) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bh[j] = (__bf16)v[j];
+        *reinterpret_cast<bf8*>(&hs3[0][e][8 * k8]) = bh;
+      } else {
+        split3(v, bh, bm, bl);
+        *reinterpret_cast<bf8*>(&hs3[0][e][8 * k8]) = bh;
+        *reinterpret_cast<bf8*>(&hs3[1][e][8 * k8]) = bm;
+        *reinterpret_cast<bf8*>(&hs3[2][e][8 * k8]) = bl;
+      }
     }
     __syncthreads();
     const int nrt = (cnt + 15) / 16;
@@ -492,7 +535,12 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
         for (int ks = 0; ks < 2; ++ks) {
           const f4 x0 = a[jt][2 * ks], x1 = a[jt][2 * ks + 1];
           const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          split3(v, ah[jt][ks], am[jt][ks], al[jt][ks]);
+          if constexpr (BF16) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ah[jt][ks][j] = (__bf16)v[j];
+          } else {
+            split3(v, ah[jt][ks], am[jt][ks], al[jt][ks]);
+          }
         }
 #pragma unroll
       for (int et = 0; et < 4; ++et) {
@@ -500,11 +548,16 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
             const bf8 bh = *reinterpret_cast<const bf8*>(&hs3[0][16 * et + r][32 * ks + 8 * q]);
-            const bf8 bm = *reinterpret_cast<const bf8*>(&hs3[1][16 * et + r][32 * ks + 8 * q]);
-            const bf8 bl = *reinterpret_cast<const bf8*>(&hs3[2][16 * et + r][32 * ks + 8 * q]);
+            if constexpr (BF16) {
 #pragma unroll
-            for (int jt = 0; jt < NJ; ++jt)
-              acc[et][jt] = mfma_x6(ah[jt][ks], am[jt][ks], al[jt][ks], bh, bm, bl, acc[et][jt]);
+              for (int jt = 0; jt < NJ; ++jt) acc[et][jt] = mfma_bf16(ah[jt][ks], bh, acc[et][jt]);
+            } else {
+              const bf8 bm = *reinterpret_cast<const bf8*>(&hs3[1][16 * et + r][32 * ks + 8 * q]);
+              const bf8 bl = *reinterpret_cast<const bf8*>(&hs3[2][16 * et + r][32 * ks + 8 * q]);
+#pragma unroll
+              for (int jt = 0; jt < NJ; ++jt)
+                acc[et][jt] = mfma_x6(ah[jt][ks], am[jt][ks], al[jt][ks], bh, bm, bl, acc[et][jt]);
+            }
           }
         }
       }
@@ -1105,7 +1158,7 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
 }
 
 // ---------------------------------------------------------------- host launchers
-template <int C>
+template <int C, bool BF16>
 int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_t* src_ptr,
                       const int32_t* src_perm, const float* x, const float* h, const float* nvec,
                       const float* bk1, float scale, float* S, float* P, float* out,
@@ -1118,13 +1171,14 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
       tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + NE_ROWS - 1) / NE_ROWS);
     constexpr int ncg = ((65 * C) / 80 + NE_TPB - 1) / NE_TPB;
     LaunchTimer tm("node_expand", st);
-    node_expand_kernel<C><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(
-        x, reinterpret_cast<const _Float16*>(bk1), bk1 + sparse_weight_floats(C) - SW_TAIL, S, N, tiles);
+    const float* wplane = BF16 ? bk1 + sparse_weight_floats(C) : bk1;
+    node_expand_kernel<C, BF16><<<(unsigned)(tiles.off[6] * ncg), 256, 0, st>>>(
+        x, reinterpret_cast<const _Float16*>(wplane), bk1 + sparse_weight_floats(C) - SW_TAIL, S, N, tiles);
   }
   if (check_launch("sparse node_expand")) return 2;
   {
     LaunchTimer tm("edge_message", st);
-    edge_message_kernel<C><<<xcd_grid(N), 192, 0, st>>>(h, S, src_ptr, src_perm, P, N, node_order);
+    edge_message_kernel<C, BF16><<<xcd_grid(N), 192, 0, st>>>(h, S, src_ptr, src_perm, P, N, node_order);
   }
   if (check_launch("sparse edge_message")) return 2;
   {
@@ -1134,7 +1188,7 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
   return check_launch("sparse receiver_sum") ? 2 : 0;
 }
 
-template <int C>
+template <int C, bool BF16>
 int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_t* src_ptr,
                        const int32_t* src_perm, const int32_t* edge_dst, const float* G,
                        const float* h, const float* nvec, const float* bk6, const float* S,
@@ -1160,8 +1214,9 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
     float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums (Gt is dead)
     {
       LaunchTimer tm("node_expand_grad", st);
-      node_expand_grad_kernel<C><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(
-          dS, dscale, reinterpret_cast<const _Float16*>(bk6), bk6 + sparse_weight_floats(C) - SW_TAIL, dxp, N,
+      const float* wplane = BF16 ? bk6 + sparse_weight_floats(C) : bk6;
+      node_expand_grad_kernel<C, BF16><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(
+          dS, dscale, reinterpret_cast<const _Float16*>(wplane), bk6 + sparse_weight_floats(C) - SW_TAIL, dxp, N,
           tiles);
     }
     if (check_launch("sparse node_expand_grad")) return 2;
@@ -1205,18 +1260,19 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
 int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                             const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                             const float* x, const float* h, const float* n, const float* bk1,
-                            float inv_norm, float* s_ws, float* p_ws, float* out,
+                            float inv_norm, float* s_ws, float* p_ws, float* out, int32_t precision,
                             const int32_t* node_order, hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_forward: negative size");
+  FSC_CHECK_ARG(precision == 0 || precision == 1, "fsc_sparse_conv_forward: precision must be 0 (fp32) or 1 (bf16)");
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_forward: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && src_ptr && x && bk1 && s_ws && out, "fsc_sparse_conv_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && h && n && p_ws), "fsc_sparse_conv_forward: null edge pointer");
   if (channels == 64)
-    return conv_forward_impl<64>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm,
-                                 s_ws, p_ws, out, node_order, stream);
+    return (precision ? conv_forward_impl<64, true> : conv_forward_impl<64, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm, s_ws, p_ws, out, node_order, stream);
   if (channels == 32)
-    return conv_forward_impl<32>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm,
-                                 s_ws, p_ws, out, node_order, stream);
+    return (precision ? conv_forward_impl<32, true> : conv_forward_impl<32, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm, s_ws, p_ws, out, node_order, stream);
   set_error("fsc_sparse_conv_forward: channels must be 32 or 64");
   return 1;
 }
@@ -1226,19 +1282,22 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              const int32_t* edge_dst, const float* grad_out, const float* h,
                              const float* n, const float* bk6, const float* s_ws, const float* p_ws,
                              float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
-                             float* grad_n, const int32_t* node_order, hipStream_t stream) {
+                             float* grad_n, int32_t precision, const int32_t* node_order, hipStream_t stream) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_backward: negative size");
+  FSC_CHECK_ARG(precision == 0 || precision == 1, "fsc_sparse_conv_backward: precision must be 0 (fp32) or 1 (bf16)");
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_backward: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && bk6 && s_ws && ds_ws && grad_x,
                 "fsc_sparse_conv_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && edge_dst && h && n && p_ws && grad_h && grad_n),
                 "fsc_sparse_conv_backward: null edge pointer");
   if (channels == 64)
-    return conv_backward_impl<64>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n,
-                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, node_order, stream);
+    return (precision ? conv_backward_impl<64, true> : conv_backward_impl<64, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream);
   if (channels == 32)
-    return conv_backward_impl<32>(n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n,
-                                  bk6, s_ws, p_ws, inv_norm, ds_ws, grad_x, grad_h, grad_n, node_order, stream);
+    return (precision ? conv_backward_impl<32, true> : conv_backward_impl<32, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream);
   set_error("fsc_sparse_conv_backward: channels must be 32 or 64");
   return 1;
 }

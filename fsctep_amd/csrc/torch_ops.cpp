@@ -81,27 +81,30 @@ float avg_degree_inv(int64_t N, int64_t E) {
   return (float)(1.0 / std::max((double)E / (double)std::max<int64_t>(N, 1), 1e-8));
 }
 
+int64_t sparse_weight_floats(int64_t C) { return 6 * 65 * C * C + 512 + 3 * 65 * C * C; }
+
 std::tuple<Tensor, Tensor> sparse_prepare_weights(const Tensor& w_last, const Tensor& b_last, int64_t channels) {
   require_gpu({w_last, b_last});
   const int64_t C = channels;
   TORCH_CHECK(w_last.dim() == 2 && w_last.size(0) == 6 * C * C && w_last.size(1) == KH && b_last.numel() == 6 * C * C,
               "fc.4 of a sparse conv2 layer must be (6*C*C, 64)");
   Tensor w = f32c(w_last), b = f32c(b_last);
-  // bk1 and bk6 each hold two fp16 parts of 6*65*C*C values (as many floats) and a 512-float tail
-  Tensor bk1 = at::empty({6 * 65 * C * C + 512}, fopts(w)), bk6 = at::empty_like(bk1);
+  // bk1 and bk6 each hold two fp16 parts of 6*65*C*C values (as many floats), a 512-float tail and a
+  // bf16 plane of the same values (3*65*C*C floats)
+  Tensor bk1 = at::empty({sparse_weight_floats(C)}, fopts(w)), bk6 = at::empty_like(bk1);
   check(fsc_sparse_conv_prepare_weights(cf(w), cf(b), (int32_t)C, mf(bk1), mf(bk6), stream_of(w)),
         "fsc_sparse_conv_prepare_weights");
   return {bk1, bk6};
 }
 
 std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, const Tensor& b_last, int64_t C) {
-  return {at::empty({6 * 65 * C * C + 512}, fopts(w_last)), at::empty({6 * 65 * C * C + 512}, fopts(w_last))};
+  return {at::empty({sparse_weight_floats(C)}, fopts(w_last)), at::empty({sparse_weight_floats(C)}, fopts(w_last))};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,
                                                const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                const Tensor& src_ptr, const Tensor& src_perm,
-                                               const Tensor& edge_dst, const Tensor& node_order) {
+                                               const Tensor& edge_dst, const Tensor& node_order, int64_t precision) {
   require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == 13, "x must be (N, 13, C)");
   const int64_t N = x_.size(0), C = x_.size(2), E = h_.size(0);
@@ -111,14 +114,15 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
   Tensor S = at::empty({s_f}, fopts(x)), P = at::empty({p_f}, fopts(x)), out = at::empty({N, 13, C}, fopts(x));
   check(fsc_sparse_conv_forward(N, E, (int32_t)C, ci(dp), ci(sp), ci(pm), cf(x), cf(h), cf(n), cf(bk1),
-                                avg_degree_inv(N, E), mf(S), mf(P), mf(out), order_ptr(node_order, N), stream_of(x)),
+                                avg_degree_inv(N, E), mf(S), mf(P), mf(out), (int32_t)precision,
+                                order_ptr(node_order, N), stream_of(x)),
         "fsc_sparse_conv_forward");
   return {out, S, P};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tensor& h, const Tensor&, const Tensor&,
                                                     const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                    const Tensor&, const Tensor&) {
+                                                    const Tensor&, const Tensor&, int64_t) {
   const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
   int64_t s_f = 0, p_f = 0;
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
@@ -129,7 +133,7 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
                                                         const Tensor& bk6, const Tensor& S, const Tensor& P,
                                                         const Tensor& dst_ptr, const Tensor& src_ptr,
                                                         const Tensor& src_perm, const Tensor& edge_dst,
-                                                        const Tensor& node_order) {
+                                                        const Tensor& node_order, int64_t precision) {
   require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
   Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_);
@@ -138,14 +142,15 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
   check(fsc_sparse_conv_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(src_ptr, "src_ptr")),
                                  ci(i32c(src_perm, "src_perm")), ci(i32c(edge_dst, "edge_dst")), cf(g), cf(h), cf(n),
                                  cf(bk6), cf(S), cf(P), avg_degree_inv(N, E), mf(dS), mf(dx), mf(dh), mf(dn),
-                                 order_ptr(node_order, N), stream_of(g)),
+                                 (int32_t)precision, order_ptr(node_order, N), stream_of(g)),
         "fsc_sparse_conv_backward");
   return {dx, dh, dn};
 }
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h, const Tensor&,
                                                              const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&) {
+                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                             int64_t) {
   const int64_t E = h.size(0);
   return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h))};
 }
@@ -804,27 +809,30 @@ void refuse_param_grad(AutogradContext* ctx, std::initializer_list<int> idx, con
 
 struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
-                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order) {
+                               Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order,
+                               int64_t precision) {
     at::AutoDispatchBelowADInplaceOrView guard;
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&,
                                                                   const Tensor&, const Tensor&, const Tensor&,
                                                                   const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&)>("fsctep::sparse_conv");
-    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order);
+                                                                  const Tensor&, int64_t)>("fsctep::sparse_conv");
+    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision);
     ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
+    ctx->saved_data["precision"] = precision;
     ctx->mark_non_differentiable({S, P});
     ctx->set_materialize_grads(false);   // S and P are saved workspaces: no zero-filled gradients for them
     return {out, S, P};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(10);
+    variable_list res(11);
     if (!grads[0].defined()) return res;
     refuse_param_grad(ctx, {3, 4}, "the sparse conv");
     auto s = ctx->get_saved_variables();
     static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
         const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&)>("fsctep::sparse_conv_backward");
-    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9]);
+        const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t)>("fsctep::sparse_conv_backward");
+    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9],
+                                ctx->saved_data["precision"].toInt());
     res[0] = dx;
     res[1] = dh;
     res[2] = dn;
@@ -835,8 +843,9 @@ struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const Tensor& h, const Tensor& n,
                                                         const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                         const Tensor& src_ptr, const Tensor& src_perm,
-                                                        const Tensor& edge_dst, const Tensor& node_order) {
-  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order);
+                                                        const Tensor& edge_dst, const Tensor& node_order,
+                                                        int64_t precision) {
+  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision);
   return {r[0], r[1], r[2]};
 }
 
@@ -1185,9 +1194,10 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 TORCH_LIBRARY(fsctep, m) {
   m.def("sparse_prepare_weights(Tensor w_last, Tensor b_last, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv(Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6, Tensor dst_ptr, Tensor src_ptr, "
-        "Tensor src_perm, Tensor edge_dst, Tensor node_order) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_perm, Tensor edge_dst, Tensor node_order, int precision=0) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
-        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, int precision=0) "
+        "-> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, "
         "int channels) -> (Tensor, Tensor)");

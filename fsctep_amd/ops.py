@@ -7,8 +7,9 @@ There is no CPU implementation: calling an op with CPU tensors raises.  Paramete
 produced (the path serves energy + forces).
 
     sparse_prepare_weights(w_last, b_last, channels) -> (bk1, bk6)
-    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order) -> (out, S, P)
-    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order)
+    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision=0) -> (out, S, P)
+    sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision=0)
+        precision 0: fp32-accurate products; 1: the bf16 channel-mix variant (one bf16 MFMA per product)
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
     sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
@@ -32,10 +33,10 @@ _lib.load_torch_ops()
 import torch  # noqa: E402
 
 
-def sparse_conv_apply(x, h, n, bk1, bk6, graph):
+def sparse_conv_apply(x, h, n, bk1, bk6, graph, precision: int = 0):
     """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C), normalised by 1/max(E/N, 1e-8)."""
     out, _, _ = torch.ops.fsctep.sparse_conv(x, h, n, bk1, bk6, graph.dst_ptr, graph.src_ptr,
-                                             graph.src_perm, graph.dst32, graph.node_order)
+                                             graph.src_perm, graph.dst32, graph.node_order, int(precision))
     return out
 
 

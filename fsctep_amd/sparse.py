@@ -198,6 +198,9 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         self._readout_cache = {}
         self.function_type = function_type_main
         self.n_species = int(max_atomvalue)
+        # products of the conv2..n channel mix: "fp32" (fp32-accurate split products, the default) or "bf16"
+        # (one bf16 MFMA per product with fp32 accumulation; an MI355X option, not in the reference)
+        self.channel_mix_precision = "fp32"
 
     # ------------------------------------------------------------------ graph handling
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A, pos=None) -> Graph:
@@ -251,8 +254,14 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         for conv in self.e3_conv_layers[1:]:
             bk1, bk6 = conv.prepared_weights()
             h = ops.radial_hidden(r, conv.fc, self.max_radius, self.function_type)
-            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g))
+            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, self._precision_code()))
         return poison_invalid(self.readout(feats), g)
+
+    def _precision_code(self) -> int:
+        prec = getattr(self, "channel_mix_precision", "fp32")
+        if prec not in ("fp32", "bf16"):
+            raise ValueError(f"channel_mix_precision must be 'fp32' or 'bf16', got {prec!r}")
+        return 1 if prec == "bf16" else 0
 
     def readout(self, feats):
         """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features: the rank-L blocks of all

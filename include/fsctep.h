@@ -122,9 +122,9 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
 
 /* Re-layout fc.4.weight (6*C*C, 64) and fc.4.bias (6*C*C) into the two kernel operands bk1 and
  * bk6 (the operand and its transpose, times a power of two and split into two fp16 parts of
- * 6*65*C*C values, for fp32-accurate split-fp16 products, then a 512-float tail holding the scale;
- * 6*65*C*C + 512 floats of storage each).  Both are opaque to the caller.  Call again whenever those
- * parameters change. */
+ * 6*65*C*C values, for fp32-accurate split-fp16 products, then a 512-float tail holding the scale, then
+ * the same scaled values rounded to bf16 for the bf16 variant; 6*65*C*C + 512 + 3*65*C*C floats of storage
+ * each).  Both are opaque to the caller.  Call again whenever those parameters change. */
 int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, int32_t channels,
                                     float* bk1, float* bk6, hipStream_t stream);
 
@@ -133,23 +133,27 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
  * n: [E][3] unit edge directions (edge_rank_powers, models/pure_cartesian.py:292-317);
  * inv_norm: 1/max(E/N, 1e-8) as in pure_cartesian_sparse_layers.py:418-420.
  * s_ws, p_ws: workspaces from fsc_sparse_conv_workspace; keep them for the backward.
+ * precision 0: every product fp32-accurate (split-fp16 node expansion, split-bf16 edge message);
+ * precision 1: the bf16 channel-mix variant, one bf16 MFMA per product in the node expansion, the edge
+ * message and (backward) the node-expansion gradient, fp32 accumulation.  No counterpart in the reference
+ * (an MI355X option for large systems; the reference computes in the model dtype).
  * node_order: null, or a permutation of the nodes (fsc_spatial_order) that the per-node kernels walk
  * (a performance hint: the results do not depend on it). */
 int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                             const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                             const float* x, const float* h, const float* n, const float* bk1,
-                            float inv_norm, float* s_ws, float* p_ws, float* out,
+                            float inv_norm, float* s_ws, float* p_ws, float* out, int32_t precision,
                             const int32_t* node_order, hipStream_t stream);
 
 /* Backward of fsc_sparse_conv_forward for forces: grad_x [N][13][C], grad_h [E][64],
  * grad_n [E][3] from grad_out [N][13][C].  ds_ws: scratch of s_floats floats.
- * edge_dst: [E] receiver of each receiver-sorted edge; node_order as for the forward. */
+ * edge_dst: [E] receiver of each receiver-sorted edge; precision and node_order as for the forward. */
 int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                              const int32_t* edge_dst, const float* grad_out, const float* h,
                              const float* n, const float* bk6, const float* s_ws, const float* p_ws,
                              float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
-                             float* grad_n, const int32_t* node_order, hipStream_t stream);
+                             float* grad_n, int32_t precision, const int32_t* node_order, hipStream_t stream);
 
 /* ------------------------------------------------------------------ conv1 (sparse)
  * Replaces the TP + scatter + in-degree normalisation of PureCartesianSparseE3Conv.forward

@@ -46,14 +46,15 @@ int main(int argc, char** argv) {
   auto [Wf, Wb] = prep.call(W);
   auto t = at::empty({7, 9, 192}, meta);
   auto x = at::empty({10, 13, 64}, meta), h = at::empty({30, 64}, meta), nv = at::empty({30, 3}, meta);
-  auto bk = at::empty({6 * 65 * 64 * 64 + 512}, meta);
+  auto bk = at::empty({6 * 65 * 64 * 64 + 512 + 3 * 65 * 64 * 64}, meta);
   auto ip = at::empty({11}, at::device(at::kMeta).dtype(at::kInt)), ie = at::empty({30}, at::device(at::kMeta).dtype(at::kInt));
   auto sc = disp.findSchemaOrThrow("fsctep::sparse_conv", "")
                 .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                    const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&)>();
+                    const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                    int64_t)>();
   auto no_order = at::empty({0}, at::device(at::kMeta).dtype(at::kInt));
-  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order);
+  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order, 0);
   if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;
