@@ -516,6 +516,7 @@ def main():
         "kernels": head.get("kernels"),
         "ms_per_step_with_graph_prepare": head["ms_per_step_with_graph_prepare"],
         "graph_prepare_ms": head["graph_prepare_ms"],
+        "neighbor_list_ms": head["neighbor_list_ms"],
         "parity": head["parity"],
         "gpu": gpu_info(),
     }
