@@ -62,10 +62,11 @@ def build(verbose: bool = False) -> str:
                 "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"),
                 "-I", "/opt/rocm/include", *inc, os.path.join(CSRC, "torch_ops.cpp"), "-o", obj]
     crun_tmp = CORE_RUN + ".tmp"
-    core_cc = ["g++", "-std=c++17", "-O1", "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc,
-               "-I", os.path.join(tinc, "torch", "csrc", "api", "include"), CORE_RUN_SRC, "-o", crun_tmp,
+    core_cc = ["g++", "-std=c++17", "-O1", "-D_GLIBCXX_USE_CXX11_ABI=1", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+               "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"), "-I", "/opt/rocm/include",
+               CORE_RUN_SRC, "-o", crun_tmp,
                "-L", tlib, "-Wl,--no-as-needed", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip",
-               f"-Wl,-rpath,{tlib}", "-ldl"]
+               f"-Wl,-rpath,{tlib}", "-L", "/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib", "-ldl"]
     if verbose:
         print(" ".join(hip_cmd), "\n", " ".join(torch_cc), "\n", " ".join(core_cc), flush=True)
     procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)

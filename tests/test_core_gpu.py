@@ -119,3 +119,34 @@ def test_make_fx_energy_forces(name):
     e, f = gm(*[a.clone() for a in args])
     assert rel_inf(e.squeeze(-1), g["energy_f64"]) < TOL
     assert rel_inf(f, g["forces_f64"]) < TOL
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_libtorch_core_under_hip_graph_capture(name, tmp_path):
+    """The engine's CUDA-graph path (mff_torch_engine.cpp:648-737) in the Python-free runner: forward and
+    force backward captured once on a pool stream over static inputs, replayed on three position sets
+    with eager runs in between; every replay equals the eager step (energies bitwise, forces and dipole to
+    1e-6 of their largest entry: torch's index_add backward of the engine-side edge_vec gather and the
+    dipole's sum over atoms are atomic) and the first the golden."""
+    from fsctep_amd import _lib
+    from fsctep_amd.core import export_core
+    g = load_golden(name)
+    m = _model(name, g)
+    path = export_core(m, str(tmp_path / "core.pt"), device=DEV)
+    d = _inputs(g)
+    io = tmp_path / "io"
+    io.mkdir()
+    (io / "meta.txt").write_text(f"{d['N']} {d['E']} {d['ext'].numel()}\n")
+    for k, key, dt in (("pos", "pos.f32", np.float32), ("species", "A.i64", np.int64), ("edge_src", "src.i64", np.int64),
+                       ("edge_dst", "dst.i64", np.int64), ("edge_shifts", "shifts.f32", np.float32),
+                       ("cell", "cell.f32", np.float32)):
+        np.ascontiguousarray(np.asarray(g[k]).astype(dt)).tofile(io / key)
+    d["ext"].cpu().numpy().astype(np.float32).tofile(io / "external.f32")
+    env = {k: v for k, v in os.environ.items() if not k.startswith("PYTHON")}
+    run = subprocess.run([CORE_RUN, _lib.TORCH_LIB_PATH, path, str(io), "3", "graph"], capture_output=True, text=True,
+                         timeout=240, env=env)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "graph replays equal to eager: 3/3" in run.stdout, run.stdout
+    res = np.fromfile(io / "out.f32", dtype=np.float32)
+    N = d["N"]
+    _check(name, g, res[:N], res[N:4 * N].reshape(N, 3), res[4 * N:4 * N + 22].reshape(1, 22), res[4 * N + 22:])
