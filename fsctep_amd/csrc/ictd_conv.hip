@@ -481,11 +481,14 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
 //   (b) H[e][m1][kk]    = sum_i x[src_e][o1+m1][i] g[kk][i]  MFMA, K = channels (into LDS)
 //   (c) T[e][p][m2]     = sum_{m1,m3} H[e][m1][koff_p+m3] C_p[m1][m2][m3]
 //       dgate[e][p] = sum_m2 Y_e[oy_p+m2] T[e][p][m2];   dY[e][y] = sum_{p covers y} gate_e[p] T[e][p][y-oy_p]
+// g is the same for every chunk of the block: each wave owns at most two 16-row kk tiles (the snake
+// assignment of the forward, balanced by d1) and holds their g rows in registers for the whole block, so
+// per chunk only the gathered x rows are read.
 // The input gradient dx = sum_{e: src=m} bg_e^T g_dst(e) is not formed here: it is the dual projection
 // (project_fwd_kernel over the source grouping with the dual layout) followed by the channel mix with the
 // transposed weights, so no per-edge [M][C] gradient is stored.
 template <int C>
-__global__ __launch_bounds__(256) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
+__global__ __launch_bounds__(256, 3) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ Y,
                                                            const float* __restrict__ gates,
@@ -494,15 +497,16 @@ __global__ __launch_bounds__(256) void project_grad_kernel(FscIctdLayout L, int 
                                                            const int32_t* __restrict__ esrc,
                                                            float* __restrict__ dgates, float* __restrict__ dY,
                                                            int64_t n_nodes, const int32_t* __restrict__ node_order) {
+  constexpr int KS = C / 16;                           // K steps of 16 channels (4 MFMAs each)
   extern __shared__ __align__(16) float smem[];
   const ProjSmem sm = proj_smem(L, ncg, true);
   float* cgs = smem + sm.cgs;
   float* ys = smem + sm.ys;
   float* gs = smem + sm.gs;
   int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
+  int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
   float* bg = smem + sm.bg;            // H of the chunk
   float* T = smem + sm.T;              // [TT][EB]
-  int* tmap = reinterpret_cast<int*>(smem + sm.tmap);
   int* toff = reinterpret_cast<int*>(smem + sm.toff);
 
   const int n = xcd_node(n_nodes, node_order);
@@ -511,78 +515,115 @@ __global__ __launch_bounds__(256) void project_grad_kernel(FscIctdLayout L, int 
   if (beg == end) return;                               // uniform over the block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int TT = sm.TT;
   const float scale = 1.f / (float)(end - beg);
-  const float* gn = dZ + (int64_t)n * L.KT * C;
   for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
+  assign_fwd_tasks(L, 1, wtask);
   if (threadIdx.x == 0) {
     int o = 0;
     for (int p = 0; p < L.NP; ++p) {
       toff[p] = o;
-      for (int m2 = 0; m2 < L.p_d2[p]; ++m2) tmap[o + m2] = p;
       o += L.p_d2[p];
     }
     toff[L.NP] = o;
   }
+  __syncthreads();
+
+  // the wave's tiles: group, first-operand offset, component count, H column base; g rows (row kk of the
+  // tile at lane r, channels 16 s + 4 q .. + 3) scaled by 1/deg
+  const int ntile = wtask[wave * 8];
+  int tg[2], to1[2], td1[2], tcol[2];
+  f4 gb[2][KS];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = u < ntile ? wtask[wave * 8 + 1 + u] : 0;   // tile 0 stands in for a missing tile
+    const int g = L.tile_group[t];
+    const int kkl = (t - L.g_tile0[g]) * 16 + r;
+    tg[u] = g;
+    to1[u] = L.g_o1[g];
+    td1[u] = u < ntile ? L.g_d1[g] : 0;
+    tcol[u] = L.g_bgoff[g] + (t - L.g_tile0[g]) * 16 + r;
+    const bool ok = u < ntile && kkl < L.g_kcount[g];
+    const float* gr = dZ + ((int64_t)n * L.KT + L.g_kstart[g] + (ok ? kkl : 0)) * C + 4 * q;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const f4 v = ok ? ld4(gr + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
+      gb[u][s] = f4{v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+    }
+  }
+  const int bgs = bg_stride(L);
+
+  // (b) the wave's (tile, m1) products in sequence, each in two K halves; every half's x rows are loaded
+  // while the previous half multiplies, and the first half of the next chunk is requested before this
+  // chunk's coupling contractions.  Lane r gathers the x row of the chunk's edge r (the last edge stands
+  // in beyond the chunk: its H rows are not used).
+  constexpr int KH = KS / 2;
+  const int nprod = td1[0] + td1[1];
+  auto xrow_of = [&](int ebk) { return x + (int64_t)esrc[min(ebk + r, end - 1)] * L.M * C + 4 * q; };
+  auto load_half = [&](const float* xr, int j, int half, f4 (&a)[KH]) {
+    const int m = j < td1[0] ? to1[0] + j : to1[1] + (j - td1[0]);
+#pragma unroll
+    for (int s = 0; s < KH; ++s) a[s] = ld4(xr + m * C + 16 * (half * KH + s));
+  };
+  auto mul_half = [&](int u, int half, const f4 (&a)[KH], f4 acc) {
+    if (u == 0) {
+#pragma unroll
+      for (int s = 0; s < KH; ++s) acc = mfma_k16(a[s], gb[0][half * KH + s], acc);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KH; ++s) acc = mfma_k16(a[s], gb[1][half * KH + s], acc);
+    }
+    return acc;
+  };
+  f4 a0[KH], a1[KH];
+  const float* xr = xrow_of(beg);
+  if (nprod > 0) load_half(xr, 0, 0, a0);
 
   for (int eb = beg; eb < end; eb += EB) {
     const int cnt = min(EB, end - eb);
-    __syncthreads();
-    stage_chunk<false>(L, eb, cnt, Y, gates, esrc, nullptr, nullptr, ys, gs, srcs);
-    __syncthreads();
-
-    // (b) one task per component m: 16 edge rows x (kpad of its group), K = channels
-    for (int m = wave; m < L.M; m += 4) {
-      int g = 0;
-      while (g + 1 < L.NG && m >= L.g_o1[g + 1]) ++g;
-      const int m1 = m - L.g_o1[g], kpad = L.g_kpad[g], kcount = L.g_kcount[g];
-      const int nkt = kpad / 16;
-      const float* xr = x + ((int64_t)srcs[r] * L.M + m) * C + 4 * q;
-      f4 acc[2];
-      const float* br[2];
-      bool bok[2];
+    const bool more = eb + EB < end;
+    const float* xn = more ? xrow_of(eb + EB) : xr;
+    for (int j = 0; j < nprod; ++j) {
+      const int u = j < td1[0] ? 0 : 1;
+      const int m1 = u == 0 ? j : j - td1[0];
+      load_half(xr, j, 1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+      f4 acc = mul_half(u, 0, a0, f4{0.f, 0.f, 0.f, 0.f});
+      if (j + 1 < nprod) load_half(xr, j + 1, 0, a0);
+      else if (more) load_half(xn, 0, 0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = mul_half(u, 1, a1, acc);
+      const int kpad = L.g_kpad[tg[u]];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        acc[kt] = f4{0.f, 0.f, 0.f, 0.f};
-        const int kkl = kt * 16 + r;
-        bok[kt] = kt < nkt && kkl < kcount;
-        br[kt] = gn + (int64_t)(L.g_kstart[g] + (bok[kt] ? kkl : 0)) * C + 4 * q;
-      }
-      // every K step's gathered x row and gradient rows are requested before the first product
-      f4 av[C / 16], bv[2][C / 16];
-#pragma unroll
-      for (int s = 0; s < C / 16; ++s) {
-        av[s] = ld4(xr + 16 * s);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) bv[kt][s] = bok[kt] ? ld4(br[kt] + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int s = 0; s < C / 16; ++s)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          if (kt < nkt) acc[kt] = mfma_k16(av[s], bv[kt][s], acc[kt]);
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        if (kt >= nkt) break;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          bg[(4 * q + i) * bg_stride(L) + L.g_bgoff[g] + m1 * kpad + kt * 16 + r] = acc[kt][i] * scale;
-      }
+      for (int i = 0; i < 4; ++i) bg[(4 * q + i) * bgs + tcol[u] + m1 * kpad] = acc[i];
     }
+    xr = xn;
     __syncthreads();
+    // harmonics and gates of the chunk for (c2); the previous chunk's (c2) is done (it preceded the barrier)
+    stage_chunk<false>(L, eb, cnt, Y, gates, esrc, nullptr, nullptr, ys, gs, srcs);
 
-    // (c1) T[j][e], j = (path p, m2)
-    for (int idx = threadIdx.x; idx < TT * EB; idx += blockDim.x) {
-      const int j = idx / EB, e = idx & (EB - 1);
-      const int p = tmap[j], m2 = j - toff[p];
+    // (c1) T[(p, m2)][e] = sum_{k = (m1, m3)} H[e][m1][koff_p + m3] C_p[m1][m2][m3]: per path one MFMA
+    // column tile (m2 < d2 <= 15) over K = d1 d3, operands read from LDS; paths dealt to the waves in turn
+    for (int p = wave; p < L.NP; p += 4) {
       const int g = L.p_group[p];
       const int d1 = L.g_d1[g], kpad = L.g_kpad[g], d2 = L.p_d2[p], d3 = L.p_d3[p];
-      const float* h = bg + e * bg_stride(L) + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
-      const float* c = cgs + L.p_cgoff[p] + m2 * d3;
-      float acc = 0.f;
-      for (int m1 = 0; m1 < d1; ++m1)
-        for (int m3 = 0; m3 < d3; ++m3) acc += h[m1 * kpad + m3] * c[m1 * d2 * d3 + m3];
-      T[idx] = acc;
+      const int K = d1 * d3;
+      const float* hb = bg + r * bgs + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
+      const float* cb = cgs + L.p_cgoff[p] + r * d3;
+      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+      for (int k0 = 0; k0 < K; k0 += 4) {
+        const int k = k0 + q;
+        float a = 0.f, b = 0.f;
+        if (k < K) {
+          const int m1 = k / d3, m3 = k - m1 * d3;
+          a = hb[m1 * kpad + m3];                          // A[edge r][k]
+          if (r < d2) b = cb[m1 * d2 * d3 + m3];           // B[k][m2 = r]
+        }
+        acc = mfma16x16x4(a, b, acc);
+      }
+      if (r < d2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) T[(toff[p] + r) * EB + 4 * q + i] = acc[i];
+      }
     }
     __syncthreads();
 
