@@ -1033,6 +1033,20 @@ int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const i
                           node_order, "ictd_project", "ictd_mix", st);
 }
 
+// The receiver-normalised projection Z alone (the first half of the forward), for the weight gradient
+// dW[gate_p] = sum_n G_p^T Z_p of the training backward.
+template <int C>
+int project_only_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
+                   const float* Y, const float* gates, const float* cg, float* Z, const int32_t* node_order,
+                   hipStream_t st) {
+  const int ncg = cg_length(L);
+  LaunchTimer tm("ictd_project", st);
+  const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
+  project_fwd_kernel<C, false><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
+                                                               Z + N * L.KT * C, N, node_order, nullptr, nullptr);
+  return check_launch("ictd project") ? 2 : 0;
+}
+
 // Workspace of the backward: dZ [N][KT][C] + N scales; R [N][KT_dual][C] + N scales, then the dual
 // coupling table.
 int64_t dual_ws_floats(const FscIctdLayout& L, int64_t N, int C) {
@@ -1106,6 +1120,22 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
   if (channels == 128) return forward_c<128>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
   if (channels == 64) return forward_c<64>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
   return forward_c<32>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, W, z_ws, out, node_order, stream);
+}
+
+int fsc_ictd_project(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                     const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
+                     const float* gates, const float* cg, float* z_ws, const int32_t* node_order,
+                     hipStream_t stream) {
+  if (check_layout(layout, channels, "fsc_ictd_project")) return 1;
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+                "fsc_ictd_project: bad size");
+  FSC_CHECK_ARG(dst_ptr && x && cg && z_ws, "fsc_ictd_project: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (edge_src && Y && gates), "fsc_ictd_project: null edge pointer");
+  if (n_nodes == 0) return 0;
+  const FscIctdLayout& L = *layout;
+  if (channels == 128) return project_only_c<128>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, z_ws, node_order, stream);
+  if (channels == 64) return project_only_c<64>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, z_ws, node_order, stream);
+  return project_only_c<32>(L, n_nodes, dst_ptr, edge_src, x, Y, gates, cg, z_ws, node_order, stream);
 }
 
 int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, float* Wt, hipStream_t stream) {

@@ -8,8 +8,9 @@
 // RTLD_GLOBAL) gets the ops by loading it, and a TorchScript core.pt whose graph calls them runs
 // there with forces from C++ autograd (mff_torch_engine.cpp:818-820).
 //
-// Parameter gradients are not produced (the path serves energy and forces); the autograd kernels
-// raise if one is requested.  ICTD layout tables travel as a CPU int32 tensor holding the
+// Parameter gradients are not produced (the path serves energy and forces) except by the ICTD conv, whose
+// autograd also gives the weight gradient and the double backward of force training; the other autograd
+// kernels raise if a parameter gradient is requested.  ICTD layout tables travel as a CPU int32 tensor holding the
 // FscIctdLayout struct.
 
 #include <ATen/ATen.h>
@@ -252,6 +253,42 @@ Tensor ictd_conv_meta(const Tensor& x, const Tensor&, const Tensor&, const Tenso
                       const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                       at::IntArrayRef) {
   return at::empty(x.sizes(), fopts(x));
+}
+
+// Receiver-normalised projection Z (N, KT, C) of the forward (the weight gradient's operand).
+Tensor ictd_project(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& cg, const Tensor& dst_ptr,
+                    const Tensor& edge_src, const Tensor& node_order, at::IntArrayRef layout) {
+  require_gpu({x_, Y_, gates_, cg, dst_ptr, edge_src, node_order});
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  const FscIctdLayout* L = &Lv;
+  TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
+  const int64_t N = x_.size(0), C = x_.size(2), E = Y_.size(0);
+  Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
+  Tensor z = at::empty({N * L->KT * C + N}, fopts(x));
+  check(fsc_ictd_project(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")), cf(x),
+                         cf(Y), cf(gates), cf(cg), mf(z), order_ptr(node_order, N), stream_of(x)),
+        "fsc_ictd_project");
+  return z.narrow(0, 0, N * L->KT * C).view({N, L->KT, C});
+}
+
+Tensor ictd_project_meta(const Tensor& x, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                         const Tensor&, at::IntArrayRef layout) {
+  const FscIctdLayout Lv = unpack_table<FscIctdLayout>(layout, "layout");
+  return at::empty({x.size(0), Lv.KT, x.size(2)}, fopts(x));
+}
+
+// dW[gate_p][o][i] = sum_n sum_m3 G[n][oo_p + m3][o] Z[n][koff_p + m3][i]: one GEMM per live path (K = N d3),
+// accumulated per weight slot; slots of paths that are not live stay zero.
+Tensor ictd_weight_grad(const Tensor& G, const Tensor& Z, const FscIctdLayout& L, at::IntArrayRef wsizes) {
+  const int64_t C = G.size(2);
+  Tensor dW = at::zeros({L.NREF, C, C}, G.options());
+  for (int p = 0; p < L.NP; ++p) {
+    const int64_t d = L.p_d3[p];
+    const Tensor Gp = G.narrow(1, L.p_oo[p], d).reshape({-1, C});
+    const Tensor Zp = Z.narrow(1, L.p_koff[p], d).reshape({-1, C});
+    dW.select(0, L.p_gate[p]).addmm_(Gp.t(), Zp);
+  }
+  return dW.view(wsizes);
 }
 
 std::tuple<Tensor, Tensor, Tensor> ictd_conv_backward(const Tensor& grad_out, const Tensor& x_, const Tensor& Y_,
@@ -882,34 +919,148 @@ std::tuple<Tensor, Tensor> sparse_conv1_autograd(const Tensor& h, const Tensor& 
   return {r[0], r[1]};
 }
 
+// Backward of the ICTD conv as a function of (G, x, Y, gates, W): (dx, dgates, dY, dW), itself differentiable
+// once, which gives the double backward of force training (training/trainer.py:1292-1297; the reference's
+// project_dbl_bwd_grad_* / mix_dbl_bwd_grad_* kernels, csrc/ictd_tp_cuda.cu:536-971).  The conv
+// out = F(x, Y, gates, W) is linear in x, in W and in each of Y and gates, so its backward B(G) = grad <G, F>
+// has, for cotangents u = (ux, ug, uY, uW) of (dx, dgates, dY, dW),
+//   d<u, B>/dG = F(ux, Y, g, W) + F(x, uY, g, W) + F(x, Y, ug, W) + F(x, Y, g, uW)
+//   d<u, B>/dx = B_x(G; x, uY, g, W) + B_x(G; x, Y, ug, W) + B_x(G; x, Y, g, uW)
+//   d<u, B>/dY = B_Y(G; ux, Y, g, W) + B_Y(G; x, Y, ug, W) + B_Y(G; x, Y, g, uW)
+//   d<u, B>/dg = B_g(G; ux, Y, g, W) + B_g(G; x, uY, g, W) + B_g(G; x, Y, g, uW)
+//   d<u, B>/dW = B_W(G; ux, Y, g) + B_W(G; x, uY, g) + B_W(G; x, Y, ug)
+// (B_v: the v part of B with the named argument replaced), all evaluated with the same kernels.
+struct IctdConvBwdFn : public torch::autograd::Function<IctdConvBwdFn> {
+  using Conv = Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                      at::IntArrayRef);
+  using Bwd = std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                 const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                 const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                 at::IntArrayRef);
+  using Proj = Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                      const Tensor&, at::IntArrayRef);
+
+  static variable_list forward(AutogradContext* ctx, Tensor G, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt,
+                               Tensor cg, Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm,
+                               Tensor edge_dst, Tensor node_order, std::vector<int64_t> layout, bool want_dW) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto bwd = op_handle<Bwd>("fsctep::ictd_conv_backward");
+    static auto proj = op_handle<Proj>("fsctep::ictd_project");
+    auto [dx, dgates, dY] = bwd.call(G, x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst,
+                                     node_order, layout);
+    Tensor dW;
+    if (want_dW) {
+      const FscIctdLayout L = unpack_table<FscIctdLayout>(layout, "layout");
+      const Tensor Z = proj.call(x, Y, gates, cg, dst_ptr, edge_src, node_order, layout);
+      dW = ictd_weight_grad(f32c(G), Z, L, W.sizes());
+    } else {
+      dW = at::zeros({0}, G.options());
+    }
+    ctx->save_for_backward({G, x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
+    ctx->saved_data["layout"] = layout;
+    ctx->saved_data["want_dW"] = want_dW;
+    ctx->mark_non_differentiable(want_dW ? variable_list{} : variable_list{dW});
+    ctx->set_materialize_grads(false);
+    return {dx, dgates, dY, dW};
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list u) {
+    TORCH_CHECK(!torch::autograd::GradMode::is_enabled(),
+                "third derivatives of the ICTD conv are not implemented (create_graph in its double backward)");
+    static auto conv = op_handle<Conv>("fsctep::ictd_conv");
+    static auto bwd = op_handle<Bwd>("fsctep::ictd_conv_backward");
+    static auto proj = op_handle<Proj>("fsctep::ictd_project");
+    static auto prep = op_handle<Tensor(const Tensor&)>("fsctep::ictd_prepare_weights");
+    auto s = ctx->get_saved_variables();
+    const Tensor &G = s[0], &x = s[1], &Y = s[2], &g = s[3], &W = s[4], &Wt = s[5], &cg = s[6];
+    const Tensor &dst_ptr = s[7], &esrc = s[8], &src_ptr = s[9], &src_perm = s[10], &edst = s[11], &order = s[12];
+    const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
+    const bool want_dW = ctx->saved_data["want_dW"].toBool();
+    const Tensor ux = u[0], ug = u[1], uY = u[2];
+    const Tensor uW = (want_dW && u.size() > 3 && u[3].defined()) ? u[3] : Tensor();
+    refuse_param_grad(ctx, {5, 6}, "the ICTD conv (prepared weights, coupling table)");
+    variable_list res(15);
+    const bool nG = ctx->needs_input_grad(0), nx = ctx->needs_input_grad(1), nY = ctx->needs_input_grad(2),
+               ng = ctx->needs_input_grad(3), nW = ctx->needs_input_grad(4);
+    auto acc = [](Tensor& a, const Tensor& b) { a = a.defined() ? a + b : b; };
+    auto F = [&](const Tensor& xa, const Tensor& Ya, const Tensor& ga, const Tensor& Wta) {
+      return conv.call(xa, Ya, ga, W, Wta, cg, dst_ptr, esrc, src_ptr, src_perm, edst, order, layout);
+    };
+    auto B = [&](const Tensor& xa, const Tensor& Ya, const Tensor& ga, const Tensor& Wta) {
+      return bwd.call(G, xa, Ya, ga, Wta, cg, dst_ptr, esrc, src_ptr, src_perm, edst, order, layout);
+    };
+    auto P = [&](const Tensor& xa, const Tensor& Ya, const Tensor& ga) {
+      return proj.call(xa, Ya, ga, cg, dst_ptr, esrc, order, layout);
+    };
+    Tensor dG, dx, dY, dg, Zs;
+    const Tensor Wtu = uW.defined() ? prep.call(uW) : Tensor();
+    if (nG) {
+      if (ux.defined()) acc(dG, F(ux, Y, g, Wt));
+      if (uY.defined()) acc(dG, F(x, uY, g, Wt));
+      if (ug.defined()) acc(dG, F(x, Y, ug, Wt));
+      if (uW.defined()) acc(dG, F(x, Y, g, Wtu));
+    }
+    if (ux.defined() && (nY || ng)) {
+      auto [bx, bg, bY] = B(ux, Y, g, Wt);
+      if (nY) acc(dY, bY);
+      if (ng) acc(dg, bg);
+    }
+    if (uY.defined() && (nx || ng)) {
+      auto [bx, bg, bY] = B(x, uY, g, Wt);
+      if (nx) acc(dx, bx);
+      if (ng) acc(dg, bg);
+    }
+    if (ug.defined() && (nx || nY)) {
+      auto [bx, bg, bY] = B(x, Y, ug, Wt);
+      if (nx) acc(dx, bx);
+      if (nY) acc(dY, bY);
+    }
+    if (uW.defined() && (nx || nY || ng)) {
+      auto [bx, bg, bY] = B(x, Y, g, Wtu);
+      if (nx) acc(dx, bx);
+      if (nY) acc(dY, bY);
+      if (ng) acc(dg, bg);
+    }
+    if (nW) {
+      if (ux.defined()) acc(Zs, P(ux, Y, g));
+      if (uY.defined()) acc(Zs, P(x, uY, g));
+      if (ug.defined()) acc(Zs, P(x, Y, ug));
+      if (Zs.defined())
+        res[4] = ictd_weight_grad(f32c(G), Zs, unpack_table<FscIctdLayout>(layout, "layout"), W.sizes());
+    }
+    res[0] = dG;
+    res[1] = dx;
+    res[2] = dY;
+    res[3] = dg;
+    return res;
+  }
+};
+
 struct IctdConvFn : public torch::autograd::Function<IctdConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor Y, Tensor gates, Tensor W, Tensor Wt, Tensor cg,
                                Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor edge_dst,
                                Tensor node_order, std::vector<int64_t> layout) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                      const Tensor&, const Tensor&, at::IntArrayRef)>("fsctep::ictd_conv");
+    static auto op = op_handle<IctdConvBwdFn::Conv>("fsctep::ictd_conv");
     Tensor out = op.call(x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order, layout);
-    ctx->save_for_backward({x, Y, gates, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
+    ctx->save_for_backward({x, Y, gates, W, Wt, cg, dst_ptr, edge_src, src_ptr, src_perm, edge_dst, node_order});
     ctx->saved_data["layout"] = layout;
     return {out};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     variable_list res(13);
     if (!grads[0].defined()) return res;
-    refuse_param_grad(ctx, {3, 4, 5}, "the ICTD conv");
+    refuse_param_grad(ctx, {4, 5}, "the ICTD conv (prepared weights, coupling table)");
     auto s = ctx->get_saved_variables();
-    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        at::IntArrayRef)>("fsctep::ictd_conv_backward");
     const std::vector<int64_t> layout = ctx->saved_data["layout"].toIntVector();
-    auto [dx, dgates, dY] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], s[10],
-                                    layout);
-    res[0] = dx;
-    res[1] = dY;
-    res[2] = dgates;
+    const bool want_dW = ctx->needs_input_grad(3);
+    auto r = IctdConvBwdFn::apply(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], s[10], s[11],
+                                  layout, want_dW);
+    res[0] = r[0];
+    res[1] = r[2];
+    res[2] = r[1];
+    if (want_dW) res[3] = r[3];
     return res;
   }
 };
@@ -1209,6 +1360,8 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("ictd_conv_backward(Tensor grad_out, Tensor x, Tensor Y, Tensor gates, Tensor Wt, Tensor cg, "
         "Tensor dst_ptr, Tensor edge_src, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, "
         "int[] layout) -> (Tensor, Tensor, Tensor)");
+  m.def("ictd_project(Tensor x, Tensor Y, Tensor gates, Tensor cg, Tensor dst_ptr, Tensor edge_src, "
+        "Tensor node_order, int[] layout) -> Tensor");
   m.def("ictd_conv1(Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, Tensor edge_pair, Tensor node_species, "
         "int n_species, int n_comps, int[] layout) -> Tensor");
   m.def("ictd_conv1_backward(Tensor grad_out, Tensor F, Tensor gates, Tensor qtab, Tensor dst_ptr, "
@@ -1246,6 +1399,7 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("sparse_conv1_backward", sparse_conv1_backward);
   m.impl("ictd_prepare_weights", ictd_prepare_weights);
   m.impl("ictd_conv", ictd_conv);
+  m.impl("ictd_project", ictd_project);
   m.impl("ictd_conv_backward", ictd_conv_backward);
   m.impl("ictd_conv1", ictd_conv1);
   m.impl("ictd_conv1_backward", ictd_conv1_backward);
@@ -1277,6 +1431,7 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("sparse_conv1_backward", sparse_conv1_backward_meta);
   m.impl("ictd_prepare_weights", ictd_prepare_weights_meta);
   m.impl("ictd_conv", ictd_conv_meta);
+  m.impl("ictd_project", ictd_project_meta);
   m.impl("ictd_conv_backward", ictd_conv_backward_meta);
   m.impl("ictd_conv1", ictd_conv1_meta);
   m.impl("ictd_conv1_backward", ictd_conv1_backward_meta);
@@ -1314,7 +1469,7 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
   for (const char* name : {"sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table",
                            "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
-                           "ictd_conv_backward", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
+                           "ictd_conv_backward", "ictd_project", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                            "readout_gather", "readout_scatter", "readout_features", "graph_prepare",

@@ -264,6 +264,16 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
                           const float* gates, const float* cg, const float* Wp, float* z_ws, float* out,
                           const int32_t* node_order, hipStream_t stream);
 
+/* The receiver-normalised projection of the forward alone, Z[n][kk][i] = (1/indeg n) sum_{e->n} sum_m1
+ * BG_e[m1][kk] x_src[o1+m1][i] (kk = (path, m3), KT slots), into z_ws[0 .. N*KT*C) (N*KT*C + N floats):
+ * the operand of the weight gradient dW[gate_p][o][i] = sum_n sum_m3 G[n][oo_p+m3][o] Z[n][koff_p+m3][i]
+ * used by training.  Replaces project_bucket_forward with the receiver scatter
+ * (csrc/ictd_tp.cpp:140-176, models/ictd_irreps_cuda.py:314-336). */
+int fsc_ictd_project(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                     const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
+                     const float* gates, const float* cg, float* z_ws, const int32_t* node_order,
+                     hipStream_t stream);
+
 /* Prepare tp2.weight W [NREF][C][C] for the channel mix: Wp holds 2*NREF*C*C + 512 floats (W times a
  * power of two split into two fp16 planes, the same with the channel axes swapped, and the scale), opaque
  * to the caller.  Call again when W changes. */

@@ -27,7 +27,7 @@ int main(int argc, char** argv) {
                          "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                          "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                          "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                         "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order"};
+                         "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "ictd_project"};
   for (const char* n : names) {
     auto op = disp.findSchema({std::string("fsctep::") + n, ""});
     if (!op) {
