@@ -19,7 +19,8 @@
 // Layouts (fp32): node features x[N][13][C] (comp-major: 0 | 1..3 = i | 4..12 = 3i+j);
 // S[N][18][65*C]: per slot a row of C*64 (c-major, k-minor) then C bias entries;
 // P[E][C/8][18][8] at the receiver-sorted edge id (channel chunks of 8, slot-major inside a chunk, so
-// that a chunk of the backward reads one contiguous block per edge); h[E][64]; n[E][3] (unit vectors).
+// that a chunk of the backward reads one contiguous block per edge; inside a chunk the slots 1, 2, 6, 7, 8
+// that the backward reads come first, pos_of_slot); h[E][64]; n[E][3] (unit vectors).
 
 #include "common.h"
 
@@ -37,6 +38,16 @@ constexpr int kSlotBaseH[6] = {0, 1, 2, 3, 6, 9};
 constexpr int kPathL1H[6] = {0, 0, 0, 1, 1, 2};
 
 __host__ __device__ inline int64_t s_node_stride(int C) { return (int64_t)NSLOT * 65 * C; }
+
+// Order of the slots inside a channel chunk of P: the five slots the backward reads (P1, P2 and P4, slots
+// 1, 2, 6, 7, 8) occupy the first 160 bytes of the chunk's 576, so it fetches two 128-byte lines per edge
+// and chunk instead of three.
+__host__ __device__ constexpr int slot_at_pos(int pos) {
+  return pos < 2 ? pos + 1 : pos < 5 ? pos + 4 : pos == 5 ? 0 : pos < 9 ? pos - 3 : pos;
+}
+__host__ __device__ constexpr int pos_of_slot(int s) {
+  return s == 0 ? 5 : s < 3 ? s - 1 : s < 6 ? s + 3 : s < 9 ? s - 4 : s;
+}
 
 // ---------------------------------------------------------------- weight preparation
 // bk1[part][p][col][a] (col < 64C: col = c*64+k -> L[(p,c,a),k]; col >= 64C: b[(p,c,a)]) and
@@ -478,12 +489,13 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
   // a[jt][4]: the biases of the lane's four output columns of tile jt.  Column block cb+3 is loaded
   // while block cb is multiplied.
   f4 a0[NJ][5], a1[NJ][5];
-  // Columns are numbered in P's chunk-major order: col = ch*144 + slot*8 + cl for channel c = 8*ch + cl.
+  // Columns are numbered in P's chunk-major order: col = ch*144 + pos_of_slot(slot)*8 + cl for channel
+  // c = 8*ch + cl.
   auto load = [&](f4 (&a)[NJ][5], int cb) {
 #pragma unroll
     for (int jt = 0; jt < NJ; ++jt) {
       const int col = cb * BW + 4 * NJ * (r >> 2) + 4 * jt + (r & 3);
-      const int rem = col % (8 * NSLOT), slot = rem / 8, c = 8 * (col / (8 * NSLOT)) + rem % 8;
+      const int rem = col % (8 * NSLOT), slot = slot_at_pos(rem / 8), c = 8 * (col / (8 * NSLOT)) + rem % 8;
       const float* srow = Sm + (int64_t)slot * COLS + c * KH + 8 * q;
       a[jt][0] = ld4(srow);
       a[jt][1] = ld4(srow + 4);
@@ -491,7 +503,7 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       a[jt][3] = ld4(srow + 36);
       const int colq = cb * BW + 4 * NJ * q + 4 * jt;   // four consecutive channels of one slot
       const int remq = colq % (8 * NSLOT);
-      a[jt][4] = ld4(Sm + (int64_t)(remq / 8) * COLS + 64 * C + 8 * (colq / (8 * NSLOT)) + remq % 8);
+      a[jt][4] = ld4(Sm + (int64_t)slot_at_pos(remq / 8) * COLS + 64 * C + 8 * (colq / (8 * NSLOT)) + remq % 8);
     }
   };
 
@@ -603,19 +615,20 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
   for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg + sub; e < end; e += EPW) {
-    const float* pr = P + (int64_t)e * (NSLOT * C) + (c / 8) * (8 * NSLOT) + (c % 8);   // + 8 * slot
+    const float* pr = P + (int64_t)e * (NSLOT * C) + (c / 8) * (8 * NSLOT) + (c % 8);   // + 8 * pos
     const float n0 = nvec[3 * (int64_t)e], n1 = nvec[3 * (int64_t)e + 1], n2 = nvec[3 * (int64_t)e + 2];
     const float nn[3] = {n0, n1, n2};
-    const float p0 = pr[0], p1 = pr[8], p2 = pr[2 * 8];
+    auto ps = [&](int slot) { return pr[8 * pos_of_slot(slot)]; };
+    const float p0 = ps(0), p1 = ps(1), p2 = ps(2);
     o[0] += p0;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + pr[(3 + i) * 8];
+    for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + ps(3 + i);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      const float p4 = pr[(6 + i) * 8];
+      const float p4 = ps(6 + i);
       const float p2ni = p2 * nn[i];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + pr[(9 + 3 * i + j) * 8];
+      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + ps(9 + 3 * i + j);
     }
   }
   if (EPW > 1) {
@@ -740,11 +753,11 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 #pragma unroll
         for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * CC];
         const float* pp = P + (int64_t)eids[e] * NCOL + ch * (NSLOT * CC) + cl;
-        pN[hh][0] = pp[1 * CC];
-        pN[hh][1] = pp[2 * CC];
-        pN[hh][2] = pp[6 * CC];
-        pN[hh][3] = pp[7 * CC];
-        pN[hh][4] = pp[8 * CC];
+        pN[hh][0] = pp[pos_of_slot(1) * CC];
+        pN[hh][1] = pp[pos_of_slot(2) * CC];
+        pN[hh][2] = pp[pos_of_slot(6) * CC];
+        pN[hh][3] = pp[pos_of_slot(7) * CC];
+        pN[hh][4] = pp[pos_of_slot(8) * CC];
       }
     };
     // Chunk column kk = 16 tt + 4 q + s4 is slot kk/8 = 2 tt + q/2, channel ch*8 + 4 (q&1) + s4: the lane
