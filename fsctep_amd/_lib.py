@@ -25,6 +25,8 @@ SIGNATURES = {
     "fsc_sparse_conv_forward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _i32, _p, _p],
     "fsc_sparse_conv_backward": [_i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f32,
                                  _p, _p, _p, _p, _i32, _p, _p],
+    "fsc_sparse_conv_direction": [_i64, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p],
+    "fsc_sparse_conv_direction_backward": [_i64, _i64, _i32] + [_p] * 11 + [_f32, _p, _p, _p, _p, _i32, _p, _p],
     "fsc_sparse_conv1_pair_table": [_p, _p, _p, _i32, _i32, _p, _p, _p],
     "fsc_sparse_conv1_forward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_sparse_conv1_backward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],

@@ -598,10 +598,13 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
 }
 
 // ---------------------------------------------------------------- K3: receiver sum
-// One wave per receiver; lanes cover channels, 64/C edges in flight per wave.
-template <int C>
+// One wave per receiver; lanes cover channels, 64/C edges in flight per wave.  DIR (training double
+// backward): the derivative of the assembly along edge directions u (udir [E][3]),
+// m0' = 0, m1' = P1 u, m2' = P2 (u n^T + n u^T) + P4 u^T.
+template <int C, bool DIR = false>
 __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restrict__ P,
                                                            const float* __restrict__ nvec,
+                                                           const float* __restrict__ udir,
                                                            const int32_t* __restrict__ dst_ptr,
                                                            float scale, float* __restrict__ out,
                                                            int64_t n_nodes) {
@@ -620,15 +623,27 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
     const float nn[3] = {n0, n1, n2};
     auto ps = [&](int slot) { return pr[8 * pos_of_slot(slot)]; };
     const float p0 = ps(0), p1 = ps(1), p2 = ps(2);
-    o[0] += p0;
+    if constexpr (!DIR) {
+      o[0] += p0;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + ps(3 + i);
+      for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + ps(3 + i);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const float p4 = ps(6 + i);
-      const float p2ni = p2 * nn[i];
+      for (int i = 0; i < 3; ++i) {
+        const float p4 = ps(6 + i);
+        const float p2ni = p2 * nn[i];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + ps(9 + 3 * i + j);
+        for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + ps(9 + 3 * i + j);
+      }
+    } else {
+      const float uu[3] = {udir[3 * (int64_t)e], udir[3 * (int64_t)e + 1], udir[3 * (int64_t)e + 2]};
+#pragma unroll
+      for (int i = 0; i < 3; ++i) o[1 + i] += p1 * uu[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const float p4 = ps(6 + i);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2 * (uu[i] * nn[j] + nn[i] * uu[j]) + p4 * uu[j];
+      }
     }
   }
   if (EPW > 1) {
@@ -668,9 +683,13 @@ __global__ void grad_chunk_major_kernel(const float* __restrict__ G, float* __re
   st4(Gt + ((int64_t)(c4 / 2) * n_nodes * NCOMP + row) * 8 + 4 * (c4 % 2), ld4(G + row * C + 4 * c4));
 }
 
-template <int C>
+// DIR (training double backward): the same products for the derivative of the receiver assembly along
+// edge directions u (udir [E][3]): dP'_e = D_n dP_e [u] = (0, g1.u, u.g2.n + n.g2.u, 0, g2 u, 0), and in
+// place of the direction gradient the second-derivative term dn_e = sum_c P2 (g2 + g2^T) u.
+template <int C, bool DIR = false>
 __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
-    const float* __restrict__ Gt, const float* __restrict__ nvec, const float* __restrict__ h,
+    const float* __restrict__ Gt, const float* __restrict__ nvec, const float* __restrict__ udir,
+    const float* __restrict__ h,
     const float* __restrict__ S, const float* __restrict__ P, const int32_t* __restrict__ src_ptr,
     const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst, float scale,
     float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, float* __restrict__ dscale,
@@ -685,6 +704,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   __shared__ int32_t eids[EP];
   __shared__ int32_t dsts[EP];
   __shared__ float ns[EP][3];
+  __shared__ float us[DIR ? EP : 1][3];
   __shared__ float dnacc[EP][3];
   __shared__ float amx[4];
   const int m = xcd_node(n_nodes, node_order);
@@ -723,6 +743,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
       for (int k = 0; k < 3; ++k) {
         const float v = nvec[3 * (int64_t)id + k];
         ns[e][k] = (e < cnt) ? v : 0.f;
+        if constexpr (DIR) us[e][k] = (e < cnt) ? udir[3 * (int64_t)id + k] : 0.f;
         dnacc[e][k] = 0.f;
       }
     }
@@ -789,26 +810,48 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
         const float nn[3] = {ns[e][0], ns[e][1], ns[e][2]};
         const float p1 = pN[hh][0], p2 = pN[hh][1];
         const float p4[3] = {pN[hh][2], pN[hh][3], pN[hh][4]};
-        v[0] = g[0];
-        v[1] = g[1] * nn[0] + g[2] * nn[1] + g[3] * nn[2];
-        float nqn = 0.f;
+        if constexpr (!DIR) {
+          v[0] = g[0];
+          v[1] = g[1] * nn[0] + g[2] * nn[1] + g[3] * nn[2];
+          float nqn = 0.f;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          float row = 0.f, colv = 0.f, p4t = 0.f;
+          for (int i = 0; i < 3; ++i) {
+            float row = 0.f, colv = 0.f, p4t = 0.f;
 #pragma unroll
-          for (int j = 0; j < 3; ++j) {
-            row += g[4 + 3 * i + j] * nn[j];
-            colv += g[4 + 3 * j + i] * nn[j];
-            p4t += g[4 + 3 * j + i] * p4[j];
+            for (int j = 0; j < 3; ++j) {
+              row += g[4 + 3 * i + j] * nn[j];
+              colv += g[4 + 3 * j + i] * nn[j];
+              p4t += g[4 + 3 * j + i] * p4[j];
+            }
+            v[3 + i] = g[1 + i];
+            v[6 + i] = row;
+            nqn += row * nn[i];
+            t[i] = g[1 + i] * p1 + p2 * (row + colv) + p4t;
           }
-          v[3 + i] = g[1 + i];
-          v[6 + i] = row;
-          nqn += row * nn[i];
-          t[i] = g[1 + i] * p1 + p2 * (row + colv) + p4t;
-        }
-        v[2] = nqn;
+          v[2] = nqn;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) v[9 + i] = g[4 + i];
+          for (int i = 0; i < 9; ++i) v[9 + i] = g[4 + i];
+        } else {
+          const float uu[3] = {us[e][0], us[e][1], us[e][2]};
+#pragma unroll
+          for (int s4 = 0; s4 < NSLOT; ++s4) v[s4] = 0.f;
+          v[1] = g[1] * uu[0] + g[2] * uu[1] + g[3] * uu[2];
+          float cross = 0.f;
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            float g2u = 0.f, g2tu = 0.f, g2n = 0.f;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+              g2u += g[4 + 3 * i + j] * uu[j];
+              g2tu += g[4 + 3 * j + i] * uu[j];
+              g2n += g[4 + 3 * i + j] * nn[j];
+            }
+            v[6 + i] = g2u;
+            cross += uu[i] * g2n + nn[i] * g2u;
+            t[i] = p2 * (g2u + g2tu);
+          }
+          v[2] = cross;
+        }
         // rows e >= cnt hold zeros (g is masked)
 #pragma unroll
         for (int s4 = 0; s4 < NSLOT; ++s4) dps[e][s4 * CC + cl] = v[s4];
@@ -1196,17 +1239,18 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
   if (check_launch("sparse edge_message")) return 2;
   {
     LaunchTimer tm("receiver_sum", st);
-    receiver_sum_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(P, nvec, dst_ptr, scale, out, N);
+    receiver_sum_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(P, nvec, nullptr, dst_ptr, scale, out, N);
   }
   return check_launch("sparse receiver_sum") ? 2 : 0;
 }
 
-template <int C, bool BF16>
+// DIR: the gradients of <G, out'> for the direction derivative out' along udir (training double backward).
+template <int C, bool BF16, bool DIR = false>
 int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_t* src_ptr,
                        const int32_t* src_perm, const int32_t* edge_dst, const float* G,
                        const float* h, const float* nvec, const float* bk6, const float* S,
                        const float* P, float scale, float* dS, float* dx, float* dh, float* dn,
-                       const int32_t* node_order, hipStream_t st) {
+                       const int32_t* node_order, hipStream_t st, const float* udir = nullptr) {
   if (N == 0) return 0;
   // workspace tail (2 x 18 x N x C floats): first the chunk-major receiver gradient (13 x N x C), later
   // the partial input gradients of node_expand_grad; then N per-node scales of dS
@@ -1214,8 +1258,8 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
   float* dscale = tail + 2LL * NSLOT * N * C;
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   {
-    LaunchTimer tm("edge_message_grad", st);
-    edge_message_grad_kernel<C><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, h, S, P, src_ptr, src_perm,
+    LaunchTimer tm(DIR ? "edge_message_grad_direction" : "edge_message_grad", st);
+    edge_message_grad_kernel<C, DIR><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, udir, h, S, P, src_ptr, src_perm,
                                                               edge_dst, scale, dh, dS, dn, dscale, N, node_order);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
@@ -1290,6 +1334,50 @@ int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   return 1;
 }
 
+int fsc_sparse_conv_direction(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
+                              const float* p_ws, const float* n, const float* u, float inv_norm, float* out,
+                              hipStream_t stream) {
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_direction: negative size");
+  FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_direction: size exceeds int32 indexing");
+  FSC_CHECK_ARG(dst_ptr && out, "fsc_sparse_conv_direction: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (p_ws && n && u), "fsc_sparse_conv_direction: null edge pointer");
+  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_direction: channels must be 32 or 64");
+  if (n_nodes == 0) return 0;
+  const unsigned grid = (unsigned)((n_nodes + 3) / 4);
+  if (channels == 64)
+    receiver_sum_kernel<64, true><<<grid, 256, 0, stream>>>(p_ws, n, u, dst_ptr, inv_norm, out, n_nodes);
+  else
+    receiver_sum_kernel<32, true><<<grid, 256, 0, stream>>>(p_ws, n, u, dst_ptr, inv_norm, out, n_nodes);
+  return check_launch("sparse direction derivative") ? 2 : 0;
+}
+
+int fsc_sparse_conv_direction_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
+                                       const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
+                                       const int32_t* edge_dst, const float* grad_out, const float* h,
+                                       const float* n, const float* u, const float* bk6, const float* s_ws,
+                                       const float* p_ws, float inv_norm, float* ds_ws, float* grad_x,
+                                       float* grad_h, float* grad_n, int32_t precision, const int32_t* node_order,
+                                       hipStream_t stream) {
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_direction_backward: negative size");
+  FSC_CHECK_ARG(precision == 0 || precision == 1, "fsc_sparse_conv_direction_backward: precision must be 0 or 1");
+  FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+                "fsc_sparse_conv_direction_backward: size exceeds int32 indexing");
+  FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && bk6 && s_ws && ds_ws && grad_x,
+                "fsc_sparse_conv_direction_backward: null pointer");
+  FSC_CHECK_ARG(n_edges == 0 || (src_perm && edge_dst && h && n && u && p_ws && grad_h && grad_n),
+                "fsc_sparse_conv_direction_backward: null edge pointer");
+  if (channels == 64)
+    return (precision ? conv_backward_impl<64, true, true> : conv_backward_impl<64, false, true>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream, u);
+  if (channels == 32)
+    return (precision ? conv_backward_impl<32, true, true> : conv_backward_impl<32, false, true>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream, u);
+  set_error("fsc_sparse_conv_direction_backward: channels must be 32 or 64");
+  return 1;
+}
+
 int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
                              const int32_t* edge_dst, const float* grad_out, const float* h,
@@ -1306,11 +1394,11 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   if (channels == 64)
     return (precision ? conv_backward_impl<64, true> : conv_backward_impl<64, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
-        grad_x, grad_h, grad_n, node_order, stream);
+        grad_x, grad_h, grad_n, node_order, stream, nullptr);
   if (channels == 32)
     return (precision ? conv_backward_impl<32, true> : conv_backward_impl<32, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
-        grad_x, grad_h, grad_n, node_order, stream);
+        grad_x, grad_h, grad_n, node_order, stream, nullptr);
   set_error("fsc_sparse_conv_backward: channels must be 32 or 64");
   return 1;
 }

@@ -102,10 +102,13 @@ std::tuple<Tensor, Tensor> sparse_prepare_weights_meta(const Tensor& w_last, con
   return {at::empty({sparse_weight_floats(C)}, fopts(w_last)), at::empty({sparse_weight_floats(C)}, fopts(w_last))};
 }
 
+// w_last / b_last (optional): the raw last radial layer that bk1/bk6 were prepared from; the kernels read the
+// prepared buffers, autograd gives the weights' gradient when they are passed and require it.
 std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h_, const Tensor& n_,
                                                const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                const Tensor& src_ptr, const Tensor& src_perm,
-                                               const Tensor& edge_dst, const Tensor& node_order, int64_t precision) {
+                                               const Tensor& edge_dst, const Tensor& node_order, int64_t precision,
+                                               const std::optional<Tensor>&, const std::optional<Tensor>&) {
   require_gpu({x_, h_, n_, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == 13, "x must be (N, 13, C)");
   const int64_t N = x_.size(0), C = x_.size(2), E = h_.size(0);
@@ -123,18 +126,22 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv(const Tensor& x_, const Tensor& h
 
 std::tuple<Tensor, Tensor, Tensor> sparse_conv_meta(const Tensor& x, const Tensor& h, const Tensor&, const Tensor&,
                                                     const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                    const Tensor&, const Tensor&, int64_t) {
+                                                    const Tensor&, const Tensor&, int64_t, const std::optional<Tensor>&,
+                                                    const std::optional<Tensor>&) {
   const int64_t N = x.size(0), C = x.size(2), E = h.size(0);
   int64_t s_f = 0, p_f = 0;
   check(fsc_sparse_conv_workspace(N, E, (int32_t)C, &s_f, &p_f), "fsc_sparse_conv_workspace");
   return {at::empty({N, 13, C}, fopts(x)), at::empty({s_f}, fopts(x)), at::empty({p_f}, fopts(x))};
 }
 
-std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_, const Tensor& n_,
-                                                        const Tensor& bk6, const Tensor& S, const Tensor& P,
-                                                        const Tensor& dst_ptr, const Tensor& src_ptr,
-                                                        const Tensor& src_perm, const Tensor& edge_dst,
-                                                        const Tensor& node_order, int64_t precision) {
+// Returns (dx, dh, dn, dS): dS is the backward's workspace holding dS[N][18][65*C] (the gradient of the node
+// expansion, consumed by the weight gradient of training) followed by its scratch tail.
+std::tuple<Tensor, Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, const Tensor& h_,
+                                                                const Tensor& n_, const Tensor& bk6, const Tensor& S,
+                                                                const Tensor& P, const Tensor& dst_ptr,
+                                                                const Tensor& src_ptr, const Tensor& src_perm,
+                                                                const Tensor& edge_dst, const Tensor& node_order,
+                                                                int64_t precision) {
   require_gpu({grad_out, h_, n_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
   const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
   Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_);
@@ -145,15 +152,83 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward(const Tensor& grad_out, 
                                  cf(bk6), cf(S), cf(P), avg_degree_inv(N, E), mf(dS), mf(dx), mf(dh), mf(dn),
                                  (int32_t)precision, order_ptr(node_order, N), stream_of(g)),
         "fsc_sparse_conv_backward");
-  return {dx, dh, dn};
+  return {dx, dh, dn, dS};
 }
 
-std::tuple<Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h, const Tensor&,
-                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                             const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-                                                             int64_t) {
+std::tuple<Tensor, Tensor, Tensor, Tensor> sparse_conv_backward_meta(const Tensor& grad_out, const Tensor& h,
+                                                                     const Tensor&, const Tensor&, const Tensor& S,
+                                                                     const Tensor&, const Tensor&, const Tensor&,
+                                                                     const Tensor&, const Tensor&, const Tensor&,
+                                                                     int64_t) {
   const int64_t E = h.size(0);
-  return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h))};
+  return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h)), at::empty_like(S)};
+}
+
+// Derivative of the conv2..n output along edge directions u (the receiver assembly is quadratic in n):
+// out'_n = (1/avg deg) sum_{e->n} (0, P1 u, P2 (u n^T + n u^T) + P4 u^T), from the forward's messages P.
+Tensor sparse_conv_direction(const Tensor& P, const Tensor& n_, const Tensor& u_, const Tensor& dst_ptr,
+                             int64_t channels) {
+  require_gpu({P, n_, u_, dst_ptr});
+  const int64_t N = dst_ptr.numel() - 1, E = n_.size(0), C = channels;
+  Tensor n = f32c(n_), u = f32c(u_);
+  TORCH_CHECK(u.sizes() == n.sizes(), "sparse_conv_direction: u must have the shape of n");
+  Tensor out = at::empty({N, 13, C}, fopts(n));
+  check(fsc_sparse_conv_direction(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), cf(P), cf(n), cf(u),
+                                  avg_degree_inv(N, E), mf(out), stream_of(n)),
+        "fsc_sparse_conv_direction");
+  return out;
+}
+
+Tensor sparse_conv_direction_meta(const Tensor&, const Tensor& n, const Tensor&, const Tensor& dst_ptr, int64_t C) {
+  return at::empty({dst_ptr.size(0) - 1, 13, C}, fopts(n));
+}
+
+// Gradients of <grad_out, out'> for the direction derivative out' along u: (dx, dh, dn, dS); dn is the
+// second-derivative term sum_c P2 (g2 + g2^T) u.
+std::tuple<Tensor, Tensor, Tensor, Tensor> sparse_conv_direction_backward(
+    const Tensor& grad_out, const Tensor& h_, const Tensor& n_, const Tensor& u_, const Tensor& bk6, const Tensor& S,
+    const Tensor& P, const Tensor& dst_ptr, const Tensor& src_ptr, const Tensor& src_perm, const Tensor& edge_dst,
+    const Tensor& node_order, int64_t precision) {
+  require_gpu({grad_out, h_, n_, u_, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
+  const int64_t N = grad_out.size(0), C = grad_out.size(2), E = h_.size(0);
+  Tensor g = f32c(grad_out), h = f32c(h_), n = f32c(n_), u = f32c(u_);
+  Tensor dS = at::empty_like(S), dx = at::empty({N, 13, C}, fopts(g)), dh = at::empty({E, KH}, fopts(g)),
+         dn = at::empty({E, 3}, fopts(g));
+  check(fsc_sparse_conv_direction_backward(N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")),
+                                           ci(i32c(src_ptr, "src_ptr")), ci(i32c(src_perm, "src_perm")),
+                                           ci(i32c(edge_dst, "edge_dst")), cf(g), cf(h), cf(n), cf(u), cf(bk6),
+                                           cf(S), cf(P), avg_degree_inv(N, E), mf(dS), mf(dx), mf(dh), mf(dn),
+                                           (int32_t)precision, order_ptr(node_order, N), stream_of(g)),
+        "fsc_sparse_conv_direction_backward");
+  return {dx, dh, dn, dS};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> sparse_conv_direction_backward_meta(
+    const Tensor& grad_out, const Tensor& h, const Tensor&, const Tensor&, const Tensor&, const Tensor& S,
+    const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t) {
+  const int64_t E = h.size(0);
+  return {at::empty_like(grad_out), at::empty({E, KH}, fopts(h)), at::empty({E, 3}, fopts(h)), at::empty_like(S)};
+}
+
+// Weight gradient of the last radial layer from dS: with W_e[p,c,a] = sum_k L[(p,c,a),k] h_e[k] + b[(p,c,a)]
+// and S_m[s][c][k] = sum_a L[(p(s),c,a),k] x_m[comp(s)][a] (Sb likewise with b),
+//   dL[(p,c,a),k] = sum_m sum_{s in p} dS_m[s][c*64+k] x_m[comp(s)][a],  db[(p,c,a)] = ... dS_m[s][64C+c] ...
+// one GEMM per path (K = nodes x slots of the path; slots and components of a path are contiguous).
+std::tuple<Tensor, Tensor> sparse_weight_grad(const Tensor& dS, const Tensor& x_, int64_t C) {
+  static const int s0[6] = {0, 1, 2, 3, 6, 9}, sn[6] = {1, 1, 1, 3, 3, 9};
+  static const int c0[6] = {0, 0, 0, 1, 1, 4};
+  const Tensor x = f32c(x_);
+  const int64_t N = x.size(0);
+  const Tensor D = dS.narrow(0, 0, N * 18 * 65 * C).view({N, 18, 65 * C});
+  Tensor dL = at::empty({6, C, C, KH}, fopts(x)), db = at::empty({6, C, C}, fopts(x));
+  for (int p = 0; p < 6; ++p) {
+    const Tensor A = D.narrow(1, s0[p], sn[p]).reshape({-1, 65 * C});
+    const Tensor X = x.narrow(1, c0[p], sn[p]).reshape({-1, C});
+    const Tensor M = A.t().mm(X);                                             // (65 C, C): rows c*64+k, then 64C+c
+    dL.select(0, p).copy_(M.narrow(0, 0, KH * C).view({C, KH, C}).permute({0, 2, 1}));
+    db.select(0, p).copy_(M.narrow(0, KH * C, C));
+  }
+  return {dL.view({6 * C * C, KH}), db.view({6 * C * C})};
 }
 
 std::tuple<Tensor, Tensor> sparse_conv1_pair_table(const Tensor& w_last, const Tensor& b_last,
@@ -844,35 +919,177 @@ void refuse_param_grad(AutogradContext* ctx, std::initializer_list<int> idx, con
                 " are not implemented (energy/force inference only)");
 }
 
+// Backward of the sparse conv2..n as a function of (G, x, h, n, w_last, b_last): (dx, dh, dn, dL, db), itself
+// differentiable once (the double backward of force training).  With P = h S(x, W) + Sb(x, W) the
+// conv F = A_n(P) is linear in x and in W = (L, b), affine in h (its h-derivative is P with h -> uh and the
+// bias dropped: W0 = (L, 0)) and quadratic in n.  For cotangents u = (ux, uh, un, uW) of (dx, dh, dn, dW):
+//   d<u,B>/dG = F(ux,h,n,W) + F(x,uh,n,W0) + A'_n[un](P) + F(x,h,n,uW)
+//   d<u,B>/dx = B_x(G; h=uh, W0) + Bdir_x(G; un) + B_x(G; W=uW)
+//   d<u,B>/dh = B_h(G; x=ux) + Bdir_h(G; un) + B_h(G; W=uW)
+//   d<u,B>/dn = B_n(G; x=ux) + B_n(G; h=uh, W0) + Bdir_n(G; un) + B_n(G; W=uW)
+//   d<u,B>/dW = B_W(G; x=ux) + B_L(G; h=uh) + Bdir_W(G; un)
+// where A'_n[un] (sparse_conv_direction) is the derivative of the receiver assembly along un and Bdir
+// (sparse_conv_direction_backward) the gradients of <G, A'_n[un](P)>, its n part being the second-derivative
+// term.  Every term runs on the conv's own kernels.
+struct SparseConvBwdFn : public torch::autograd::Function<SparseConvBwdFn> {
+  using Fwd = std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                 const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                 const Tensor&, const Tensor&, int64_t, const std::optional<Tensor>&,
+                                                 const std::optional<Tensor>&);
+  using Bwd = std::tuple<Tensor, Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                         const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                         const Tensor&, const Tensor&, const Tensor&, int64_t);
+  using DirF = Tensor(const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t);
+  using DirB = std::tuple<Tensor, Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+                                                          int64_t);
+  using Prep = std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&, int64_t);
+
+  static variable_list forward(AutogradContext* ctx, Tensor G, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
+                               Tensor S, Tensor P, Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst,
+                               Tensor node_order, Tensor w_last, Tensor b_last, int64_t precision, bool want_W) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto bwd = op_handle<Bwd>("fsctep::sparse_conv_backward");
+    auto [dx, dh, dn, dS] = bwd.call(G, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision);
+    Tensor dL, db;
+    if (want_W) {
+      std::tie(dL, db) = sparse_weight_grad(dS, x, x.size(2));
+    } else {
+      dL = at::zeros({0}, G.options());
+      db = at::zeros({0}, G.options());
+    }
+    ctx->save_for_backward({G, x, h, n, bk1, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order, w_last,
+                            b_last});
+    ctx->saved_data["precision"] = precision;
+    ctx->saved_data["want_W"] = want_W;
+    if (!want_W) ctx->mark_non_differentiable({dL, db});
+    ctx->set_materialize_grads(false);
+    return {dx, dh, dn, dL, db};
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list u) {
+    TORCH_CHECK(!torch::autograd::GradMode::is_enabled(),
+                "third derivatives of the sparse conv are not implemented (create_graph in its double backward)");
+    static auto fwd = op_handle<Fwd>("fsctep::sparse_conv");
+    static auto bwd = op_handle<Bwd>("fsctep::sparse_conv_backward");
+    static auto dirf = op_handle<DirF>("fsctep::sparse_conv_direction");
+    static auto dirb = op_handle<DirB>("fsctep::sparse_conv_direction_backward");
+    static auto prep = op_handle<Prep>("fsctep::sparse_prepare_weights");
+    auto s = ctx->get_saved_variables();
+    const Tensor &G = s[0], &x = s[1], &h = s[2], &n = s[3], &bk1 = s[4], &bk6 = s[5], &S = s[6], &P = s[7];
+    const Tensor &dp = s[8], &sp = s[9], &pm = s[10], &ed = s[11], &ord = s[12], &wl = s[13], &bl = s[14];
+    const int64_t prec = ctx->saved_data["precision"].toInt();
+    const bool want_W = ctx->saved_data["want_W"].toBool();
+    const int64_t C = x.size(2);
+    const Tensor ux = u[0], uh = u[1], un = u[2];
+    const Tensor uL = (want_W && u[3].defined()) ? u[3] : Tensor(), ub = (want_W && u[4].defined()) ? u[4] : Tensor();
+    refuse_param_grad(ctx, {4, 5, 6, 7}, "the sparse conv (prepared weights, workspaces)");
+    const bool nG = ctx->needs_input_grad(0), nx = ctx->needs_input_grad(1), nh = ctx->needs_input_grad(2),
+               nn = ctx->needs_input_grad(3), nL = ctx->needs_input_grad(13), nb = ctx->needs_input_grad(14);
+    auto acc = [](Tensor& a, const Tensor& b) { a = a.defined() ? a + b : b; };
+    auto F = [&](const Tensor& xa, const Tensor& ha, const Tensor& k1, const Tensor& k6) {
+      return fwd.call(xa, ha, n, k1, k6, dp, sp, pm, ed, ord, prec, std::nullopt, std::nullopt);
+    };
+    auto B = [&](const Tensor& ha, const Tensor& k6, const Tensor& Sa, const Tensor& Pa) {
+      return bwd.call(G, ha, n, k6, Sa, Pa, dp, sp, pm, ed, ord, prec);
+    };
+    Tensor dG, dx, dh, dn, dL, db;
+    if (ux.defined() && (nG || nh || nn || nL || nb)) {            // x -> ux
+      auto [o, S1, P1] = F(ux, h, bk1, bk6);
+      if (nG) acc(dG, o);
+      if (nh || nn || nL || nb) {
+        auto [bx, bh, bn, bS] = B(h, bk6, S1, P1);
+        if (nh) acc(dh, bh);
+        if (nn) acc(dn, bn);
+        if (nL || nb) {
+          auto [gl, gb] = sparse_weight_grad(bS, ux, C);
+          if (nL) acc(dL, gl);
+          if (nb) acc(db, gb);
+        }
+      }
+    }
+    if (uh.defined() && (nG || nx || nn || nL)) {                   // h -> uh, bias dropped
+      TORCH_CHECK(wl.numel() > 0 && bl.numel() > 0,
+                  "the double backward of the sparse conv through h needs w_last and b_last passed to the op");
+      auto [k1, k6] = prep.call(wl.detach(), at::zeros_like(bl), C);
+      auto [o, S2, P2] = F(x, uh, k1, k6);
+      if (nG) acc(dG, o);
+      if (nx || nn || nL) {
+        auto [bx, bh, bn, bS] = B(uh, k6, S2, P2);
+        if (nx) acc(dx, bx);
+        if (nn) acc(dn, bn);
+        if (nL) acc(dL, std::get<0>(sparse_weight_grad(bS, x, C)));
+      }
+    }
+    if (un.defined()) {                                              // n -> un
+      if (nG) acc(dG, dirf.call(P, n, un, dp, C));
+      if (nx || nh || nn || nL || nb) {
+        auto [bx, bh, bn, bS] = dirb.call(G, h, n, un, bk6, S, P, dp, sp, pm, ed, ord, prec);
+        if (nx) acc(dx, bx);
+        if (nh) acc(dh, bh);
+        if (nn) acc(dn, bn);
+        if (nL || nb) {
+          auto [gl, gb] = sparse_weight_grad(bS, x, C);
+          if (nL) acc(dL, gl);
+          if (nb) acc(db, gb);
+        }
+      }
+    }
+    if ((uL.defined() || ub.defined()) && (nG || nx || nh || nn)) {  // W -> uW
+      auto [k1, k6] = prep.call(uL.defined() ? uL : at::zeros_like(wl), ub.defined() ? ub : at::zeros_like(bl), C);
+      auto [o, S4, P4] = F(x, h, k1, k6);
+      if (nG) acc(dG, o);
+      if (nx || nh || nn) {
+        auto [bx, bh, bn, bS] = B(h, k6, S4, P4);
+        if (nx) acc(dx, bx);
+        if (nh) acc(dh, bh);
+        if (nn) acc(dn, bn);
+      }
+    }
+    variable_list res(17);
+    res[0] = dG;
+    res[1] = dx;
+    res[2] = dh;
+    res[3] = dn;
+    if (dL.defined()) res[13] = dL.view(wl.sizes());
+    if (db.defined()) res[14] = db.view(bl.sizes());
+    return res;
+  }
+};
+
 struct SparseConvFn : public torch::autograd::Function<SparseConvFn> {
   static variable_list forward(AutogradContext* ctx, Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6,
                                Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order,
-                               int64_t precision) {
+                               Tensor w_last, Tensor b_last, int64_t precision) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&, const Tensor&, const Tensor&,
-                                                                  const Tensor&, int64_t)>("fsctep::sparse_conv");
-    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision);
-    ctx->save_for_backward({h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order});
+    static auto op = op_handle<SparseConvBwdFn::Fwd>("fsctep::sparse_conv");
+    auto [out, S, P] = op.call(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision,
+                               std::nullopt, std::nullopt);
+    ctx->save_for_backward({x, h, n, bk1, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order, w_last,
+                            b_last});
     ctx->saved_data["precision"] = precision;
     ctx->mark_non_differentiable({S, P});
     ctx->set_materialize_grads(false);   // S and P are saved workspaces: no zero-filled gradients for them
     return {out, S, P};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    variable_list res(11);
+    variable_list res(13);
     if (!grads[0].defined()) return res;
-    refuse_param_grad(ctx, {3, 4}, "the sparse conv");
+    refuse_param_grad(ctx, {3, 4}, "the sparse conv (prepared weights; pass w_last and b_last for their gradient)");
     auto s = ctx->get_saved_variables();
-    static auto op = op_handle<std::tuple<Tensor, Tensor, Tensor>(
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
-        const Tensor&, const Tensor&, const Tensor&, const Tensor&, int64_t)>("fsctep::sparse_conv_backward");
-    auto [dx, dh, dn] = op.call(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9],
-                                ctx->saved_data["precision"].toInt());
-    res[0] = dx;
-    res[1] = dh;
-    res[2] = dn;
+    // gradient slots follow the forward's arguments; needs_input_grad counts its tensor arguments
+    // (w_last and b_last are tensor arguments 10 and 11)
+    const bool want_W = ctx->needs_input_grad(10) || ctx->needs_input_grad(11);
+    auto r = SparseConvBwdFn::apply(grads[0], s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9], s[10],
+                                    s[11], s[12], s[13], ctx->saved_data["precision"].toInt(), want_W);
+    res[0] = r[0];
+    res[1] = r[1];
+    res[2] = r[2];
+    if (want_W) {
+      if (ctx->needs_input_grad(10)) res[10] = r[3].view(s[12].sizes());
+      if (ctx->needs_input_grad(11)) res[11] = r[4].view(s[13].sizes());
+    }
     return res;
   }
 };
@@ -881,8 +1098,12 @@ std::tuple<Tensor, Tensor, Tensor> sparse_conv_autograd(const Tensor& x, const T
                                                         const Tensor& bk1, const Tensor& bk6, const Tensor& dst_ptr,
                                                         const Tensor& src_ptr, const Tensor& src_perm,
                                                         const Tensor& edge_dst, const Tensor& node_order,
-                                                        int64_t precision) {
-  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision);
+                                                        int64_t precision, const std::optional<Tensor>& w_last,
+                                                        const std::optional<Tensor>& b_last) {
+  // absent weights travel as empty tensors (autograd inputs must be defined)
+  const Tensor none = at::empty({0}, x.options());
+  auto r = SparseConvFn::apply(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order,
+                               w_last.has_value() ? *w_last : none, b_last.has_value() ? *b_last : none, precision);
   return {r[0], r[1], r[2]};
 }
 
@@ -1345,10 +1566,15 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 TORCH_LIBRARY(fsctep, m) {
   m.def("sparse_prepare_weights(Tensor w_last, Tensor b_last, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv(Tensor x, Tensor h, Tensor n, Tensor bk1, Tensor bk6, Tensor dst_ptr, Tensor src_ptr, "
-        "Tensor src_perm, Tensor edge_dst, Tensor node_order, int precision=0) -> (Tensor, Tensor, Tensor)");
+        "Tensor src_perm, Tensor edge_dst, Tensor node_order, int precision=0, Tensor? w_last=None, "
+        "Tensor? b_last=None) -> (Tensor, Tensor, Tensor)");
   m.def("sparse_conv_backward(Tensor grad_out, Tensor h, Tensor n, Tensor bk6, Tensor S, Tensor P, Tensor dst_ptr, "
         "Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, int precision=0) "
-        "-> (Tensor, Tensor, Tensor)");
+        "-> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("sparse_conv_direction(Tensor P, Tensor n, Tensor u, Tensor dst_ptr, int channels) -> Tensor");
+  m.def("sparse_conv_direction_backward(Tensor grad_out, Tensor h, Tensor n, Tensor u, Tensor bk6, Tensor S, "
+        "Tensor P, Tensor dst_ptr, Tensor src_ptr, Tensor src_perm, Tensor edge_dst, Tensor node_order, "
+        "int precision=0) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("sparse_conv1_pair_table(Tensor w_last, Tensor b_last, Tensor atom_table, int channels) -> (Tensor, Tensor)");
   m.def("sparse_conv1(Tensor h, Tensor n, Tensor mf, Tensor mb, Tensor dst_ptr, Tensor pair_tiles, "
         "int channels) -> (Tensor, Tensor)");
@@ -1394,6 +1620,8 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("sparse_prepare_weights", sparse_prepare_weights);
   m.impl("sparse_conv", sparse_conv);
   m.impl("sparse_conv_backward", sparse_conv_backward);
+  m.impl("sparse_conv_direction", sparse_conv_direction);
+  m.impl("sparse_conv_direction_backward", sparse_conv_direction_backward);
   m.impl("sparse_conv1_pair_table", sparse_conv1_pair_table);
   m.impl("sparse_conv1", sparse_conv1);
   m.impl("sparse_conv1_backward", sparse_conv1_backward);
@@ -1426,6 +1654,8 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("sparse_prepare_weights", sparse_prepare_weights_meta);
   m.impl("sparse_conv", sparse_conv_meta);
   m.impl("sparse_conv_backward", sparse_conv_backward_meta);
+  m.impl("sparse_conv_direction", sparse_conv_direction_meta);
+  m.impl("sparse_conv_direction_backward", sparse_conv_direction_backward_meta);
   m.impl("sparse_conv1_pair_table", sparse_conv1_pair_table_meta);
   m.impl("sparse_conv1", sparse_conv1_meta);
   m.impl("sparse_conv1_backward", sparse_conv1_backward_meta);
@@ -1468,7 +1698,8 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
 
 TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
   for (const char* name : {"sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_conv1_pair_table",
-                           "sparse_conv1", "sparse_conv1_backward", "ictd_prepare_weights", "ictd_conv",
+                           "sparse_conv1", "sparse_conv1_backward", "sparse_conv_direction", "sparse_conv_direction_backward",
+                           "ictd_prepare_weights", "ictd_conv",
                            "ictd_conv_backward", "ictd_project", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
                            "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",

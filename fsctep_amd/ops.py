@@ -3,13 +3,18 @@
 The ops are registered in C++ by ``libfsctep_torch.so`` (``csrc/torch_ops.cpp``): a device kernel
 over the C ABI of ``libfsctep_hip.so`` launched on the current stream, a Meta kernel (shapes only,
 for ``make_fx`` / ``torch.export`` / tracing) and an autograd kernel whose backward is itself an op.
-There is no CPU implementation: calling an op with CPU tensors raises.  Parameter gradients are not
-produced (the path serves energy + forces).
+There is no CPU implementation: calling an op with CPU tensors raises.  Parameter gradients are produced
+only by the conv2..n op, for the last radial layer passed as w_last / b_last (training; its backward is
+differentiable once, for force losses); the other ops serve energy + forces.
 
     sparse_prepare_weights(w_last, b_last, channels) -> (bk1, bk6)
-    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision=0) -> (out, S, P)
+    sparse_conv(x, h, n, bk1, bk6, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision=0,
+                w_last=None, b_last=None) -> (out, S, P)
     sparse_conv_backward(grad_out, h, n, bk6, S, P, dst_ptr, src_ptr, src_perm, edge_dst, node_order, precision=0)
+        -> (dx, dh, dn, dS)
         precision 0: fp32-accurate products; 1: the bf16 channel-mix variant (one bf16 MFMA per product)
+    sparse_conv_direction(P, n, u, dst_ptr, channels), sparse_conv_direction_backward(...): the derivative of
+        the receiver assembly along edge directions u and its gradients (double backward)
     sparse_conv1_pair_table(w_last, b_last, atom_table, channels) -> (mf, mb)
     sparse_conv1(h, n, mf, mb, dst_ptr, pair_tiles, channels) -> (out, Q)
     sparse_conv1_backward(grad_out, n, mf, Q, dst_ptr, pair_tiles) -> (dh, dn)
@@ -33,10 +38,12 @@ _lib.load_torch_ops()
 import torch  # noqa: E402
 
 
-def sparse_conv_apply(x, h, n, bk1, bk6, graph, precision: int = 0):
-    """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C), normalised by 1/max(E/N, 1e-8)."""
+def sparse_conv_apply(x, h, n, bk1, bk6, graph, precision: int = 0, w_last=None, b_last=None):
+    """Differentiable conv2..n message passing: (N,13,C) -> (N,13,C), normalised by 1/max(E/N, 1e-8).
+    With ``w_last``/``b_last`` (the layer bk1/bk6 were prepared from) their gradients are produced too."""
     out, _, _ = torch.ops.fsctep.sparse_conv(x, h, n, bk1, bk6, graph.dst_ptr, graph.src_ptr,
-                                             graph.src_perm, graph.dst32, graph.node_order, int(precision))
+                                             graph.src_perm, graph.dst32, graph.node_order, int(precision),
+                                             w_last, b_last)
     return out
 
 

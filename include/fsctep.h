@@ -155,6 +155,26 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                              float inv_norm, float* ds_ws, float* grad_x, float* grad_h,
                              float* grad_n, int32_t precision, const int32_t* node_order, hipStream_t stream);
 
+/* Training double backward (no inference use).  The receiver assembly is quadratic in the edge directions,
+ * m1 = P1 n + P3, m2 = P2 n n^T + P4 n^T + P5; fsc_sparse_conv_direction writes its derivative along the
+ * directions u [E][3] from the forward's messages p_ws: out'[N][13][C] = inv_norm sum_{e->n}
+ * (0, P1 u, P2 (u n^T + n u^T) + P4 u^T).  fsc_sparse_conv_direction_backward gives the gradients of
+ * <grad_out, out'>: grad_x, grad_h and ds_ws (dS in its first N*18*65*C floats, for the weight gradient) as the
+ * backward above does for the message gradient dP' = D_n dP [u], and grad_n = sum_c P2 (g2 + g2^T) u (the
+ * second-derivative term).  They have no counterpart in the reference's sparse path, which trains through
+ * PyTorch autograd (pure_cartesian_sparse_layers.py:382-421); the reference's double-backward kernels serve
+ * its ICTD tensor product (csrc/ictd_tp_cuda.cu:536-971). */
+int fsc_sparse_conv_direction(int64_t n_nodes, int64_t n_edges, int32_t channels, const int32_t* dst_ptr,
+                              const float* p_ws, const float* n, const float* u, float inv_norm, float* out,
+                              hipStream_t stream);
+int fsc_sparse_conv_direction_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
+                                       const int32_t* dst_ptr, const int32_t* src_ptr, const int32_t* src_perm,
+                                       const int32_t* edge_dst, const float* grad_out, const float* h,
+                                       const float* n, const float* u, const float* bk6, const float* s_ws,
+                                       const float* p_ws, float inv_norm, float* ds_ws, float* grad_x,
+                                       float* grad_h, float* grad_n, int32_t precision, const int32_t* node_order,
+                                       hipStream_t stream);
+
 /* ------------------------------------------------------------------ conv1 (sparse)
  * Replaces the TP + scatter + in-degree normalisation of PureCartesianSparseE3Conv.forward
  * (models/pure_cartesian_sparse_layers.py:227-330) without external tensors or fidelity

@@ -27,7 +27,8 @@ int main(int argc, char** argv) {
                          "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
                          "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                          "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                         "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "ictd_project"};
+                         "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "ictd_project",
+                         "sparse_conv_direction", "sparse_conv_direction_backward"};
   for (const char* n : names) {
     auto op = disp.findSchema({std::string("fsctep::") + n, ""});
     if (!op) {
@@ -52,9 +53,9 @@ int main(int argc, char** argv) {
                 .typed<std::tuple<at::Tensor, at::Tensor, at::Tensor>(
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                     const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                    int64_t)>();
+                    int64_t, const std::optional<at::Tensor>&, const std::optional<at::Tensor>&)>();
   auto no_order = at::empty({0}, at::device(at::kMeta).dtype(at::kInt));
-  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order, 0);
+  auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order, 0, std::nullopt, std::nullopt);
   if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;

@@ -18,7 +18,8 @@ OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_
        "ictd_conv1_backward", "gram_prepare_weights", "gram_bilinear", "gram_bilinear_backward", "edge_geometry",
        "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
        "readout_gather", "readout_scatter", "readout_features", "graph_prepare", "edge_vec_geometry",
-       "edge_vec_geometry_backward", "spatial_order", "ictd_project"]
+       "edge_vec_geometry_backward", "spatial_order", "ictd_project", "sparse_conv_direction",
+       "sparse_conv_direction_backward"]
 
 
 class GramProbe(torch.nn.Module):
