@@ -61,18 +61,33 @@ constexpr int GW_TAIL = 512;
 constexpr int WMAX_BLOCKS = 256;
 __host__ __device__ inline int64_t gram_weight_floats(int nb, int S) { return (int64_t)n_pairs(nb) * 512 * S + GW_TAIL; }
 
-// wmax[b] = max |W| over the grid-stride share of block b (grid WMAX_BLOCKS x 256).
+// wmax[b] = max |W| over the grid-stride share of block b (grid WMAX_BLOCKS x 256); float4 loads, four in
+// flight per thread, when W is 16-byte aligned.
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ W, int64_t n, float* __restrict__ wmax) {
   __shared__ float red[4];
   float m = 0.f;
-  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) m = fmaxf(m, fabsf(W[i]));
+  const int64_t tid = blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
+  int64_t rest = 0;
+  if ((reinterpret_cast<uintptr_t>(W) & 15) == 0) {
+    const f4* W4 = reinterpret_cast<const f4*>(W);
+    const int64_t n4 = n / 4;
+    auto mx4 = [](const f4& v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+    int64_t i = tid;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+      const f4 a = W4[i], b = W4[i + stride], c = W4[i + 2 * stride], d = W4[i + 3 * stride];
+      m = fmaxf(m, fmaxf(fmaxf(mx4(a), mx4(b)), fmaxf(mx4(c), mx4(d))));
+    }
+    for (; i < n4; i += stride) m = fmaxf(m, mx4(W4[i]));
+    rest = 4 * n4;
+  }
+  for (int64_t i = rest + tid; i < n; i += stride) m = fmaxf(m, fabsf(W[i]));
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) wmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb), 256 threads.
+// Wf[p][il][o][jl] and Wb[p][a][b][o] for every block pair p = (I <= J); grid (nb, nb, S / 16), 256 threads.
 // The fp16 planes are [plane][p][ab][o] for the backward and [plane][p][jl][il/8][o][il%8] for the
 // forward.  Every block reduces the partial maxima itself, so all use the same sw.
 __global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ W, int S, int nC, float* __restrict__ Wf,
@@ -93,22 +108,47 @@ __global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ 
   const int p = pair_index(I, J, nb);
   _Float16* wb2 = reinterpret_cast<_Float16*>(Wb + plane);
   _Float16* wf2 = reinterpret_cast<_Float16*>(Wf + plane);
-  for (int idx = threadIdx.x; idx < 256 * S; idx += blockDim.x) {
-    const int o = idx % S, ab = idx / S, a = ab / 16, b = ab % 16;
-    const float wij = W[((int64_t)o * nC + I * 16 + a) * nC + J * 16 + b];
-    const float wji = W[((int64_t)o * nC + J * 16 + b) * nC + I * 16 + a];
-    const float v = wij + wji;
-    const int64_t e = ((int64_t)p * 256 + ab) * S + o;
-    Wb[e] = v;
-    const _Float16 hb = (_Float16)(v * sw);
-    wb2[e] = hb;
-    wb2[plane + e] = (_Float16)(v * sw - (float)hb);
-    const float f = (I == J) ? wij : wij + wji;
-    Wf[(((int64_t)p * 16 + a) * S + o) * 16 + b] = f;
-    const int64_t ef = (int64_t)p * 256 * S + ((b * 2 + (a >> 3)) * S + o) * 8 + (a & 7);
-    const _Float16 fh = (_Float16)(f * sw);
-    wf2[ef] = fh;
-    wf2[plane + ef] = (_Float16)(f * sw - (float)fh);
+  // 16 outputs o per block (blockIdx.z): both 16x16 blocks of W[o] (rows I, columns J and the transposed
+  // pair) are read row by row into LDS (64 contiguous bytes per row), then each output layout is written in
+  // its own order of contiguous runs
+  __shared__ float tij[16][16][17];   // [oo][a][b] = W[o][16I + a][16J + b]
+  __shared__ float tji[16][16][17];   // [oo][b][a] = W[o][16J + b][16I + a]
+  const int t = threadIdx.x;
+  {
+    const int o0 = blockIdx.z * 16;
+    for (int oo = 0; oo < 16; ++oo) {
+      const int r = t >> 4, c = t & 15;
+      const int64_t base = (int64_t)(o0 + oo) * nC;
+      tij[oo][r][c] = W[(base + I * 16 + r) * nC + J * 16 + c];
+      tji[oo][r][c] = W[(base + J * 16 + r) * nC + I * 16 + c];
+    }
+    __syncthreads();
+    // Wb and its fp16 planes, [pair][ab][o]: runs of 16 consecutive o
+    for (int aq = 0; aq < 16; ++aq) {
+      const int ab = aq * 16 + (t >> 4), oo = t & 15, a = ab >> 4, b = ab & 15;
+      const float v = tij[oo][a][b] + tji[oo][b][a];
+      const int64_t e = ((int64_t)p * 256 + ab) * S + o0 + oo;
+      Wb[e] = v;
+      const _Float16 hb = (_Float16)(v * sw);
+      wb2[e] = hb;
+      wb2[plane + e] = (_Float16)(v * sw - (float)hb);
+    }
+    // Wf, [pair][a][o][b]: runs of 16 consecutive b
+    for (int a = 0; a < 16; ++a) {
+      const int b = t & 15, oo = t >> 4;
+      const float wij = tij[oo][a][b];
+      Wf[(((int64_t)p * 16 + a) * S + o0 + oo) * 16 + b] = (I == J) ? wij : wij + tji[oo][b][a];
+    }
+    // Wf's fp16 planes, [pair][b][a/8][o][a%8]: runs of 16 o x 8 a
+    for (int b = 0; b < 16; ++b) {
+      const int a = ((t >> 7) << 3) | (t & 7), oo = (t >> 3) & 15;
+      const float wij = tij[oo][a][b];
+      const float f = (I == J) ? wij : wij + tji[oo][b][a];
+      const int64_t ef = (int64_t)p * 256 * S + ((b * 2 + (a >> 3)) * S + o0 + oo) * 8 + (a & 7);
+      const _Float16 fh = (_Float16)(f * sw);
+      wf2[ef] = fh;
+      wf2[plane + ef] = (_Float16)(f * sw - (float)fh);
+    }
   }
 }
 
@@ -621,7 +661,7 @@ int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, f
   float* wmax = Wf + gram_weight_floats(nb, S) - GW_TAIL + 256;
   absmax_kernel<<<WMAX_BLOCKS, 256, 0, stream>>>(W, (int64_t)S * nC * nC, wmax);
   if (check_launch("gram weight maximum")) return 2;
-  prepare_kernel<<<dim3(nb, nb), 256, 0, stream>>>(W, S, nC, Wf, Wb, wmax);
+  prepare_kernel<<<dim3(nb, nb, S / 16), 256, 0, stream>>>(W, S, nC, Wf, Wb, wmax);
   return check_launch("gram prepare") ? 2 : 0;
 }
 

@@ -94,19 +94,18 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
   _Float16* bk6 = reinterpret_cast<_Float16*>(bk6f);
   __bf16* bk1b = reinterpret_cast<__bf16*>(bk1f + total + SW_TAIL);
   __bf16* bk6b = reinterpret_cast<__bf16*>(bk6f + total + SW_TAIL);
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int a = (int)(idx % C);
-    const int64_t col = (idx / C) % cols;
-    const int p = (int)(idx / (C * cols));
-    float v;
-    if (col < 64LL * C) {
-      const int c = (int)(col / 64), k = (int)(col % 64);
-      v = L[((int64_t)p * C * C + (int64_t)c * C + a) * KH + k];
-    } else {
-      const int c = (int)(col - 64LL * C);
-      v = b[(int64_t)p * C * C + (int64_t)c * C + a];
-    }
+  // k fastest (k = 64: the bias): consecutive threads read consecutive entries of one row of L and write
+  // consecutive columns of bk6
+  for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < total;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    const int kk = (int)(it % 65);
+    const int a = (int)((it / 65) % C);
+    const int c = (int)((it / (65 * C)) % C);
+    const int p = (int)(it / (65LL * C * C));
+    const int64_t row = (int64_t)p * C * C + (int64_t)c * C + a;
+    const int64_t col = kk < 64 ? (int64_t)c * 64 + kk : 64LL * C + c;
+    const float v = kk < 64 ? L[row * KH + kk] : b[row];
+    const int64_t idx = ((int64_t)p * cols + col) * C + a;
     const int64_t o = ((int64_t)p * C + a) * cols + col;
     const float vs = v * sw;
     const _Float16 hb = (_Float16)vs;
@@ -967,10 +966,11 @@ __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float
                                         float* __restrict__ mf, float* __restrict__ mb) {
   const int64_t total = (int64_t)n_species * n_species * 3 * 65 * C;
   const int live[3] = {0, 3, 5};
+  // k fastest: consecutive threads read consecutive k of one row of L (coalesced 256-byte rows)
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(idx % C);
-    const int k = (int)((idx / C) % 65);
+    const int k = (int)(idx % 65);
+    const int c = (int)((idx / 65) % C);
     const int p3 = (int)((idx / (C * 65)) % 3);
     const int pair = (int)(idx / (C * 65 * 3));
     const int s = pair / n_species, t = pair % n_species;
@@ -984,7 +984,7 @@ __global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float
         acc += w * as * atab[t * 8 + bb];
       }
     }
-    mf[idx] = acc;                                                       // [pair][p3][k][c]
+    mf[(((int64_t)pair * 3 + p3) * 65 + k) * C + c] = acc;              // [pair][p3][k][c]
     mb[(((int64_t)pair * 3 + p3) * C + c) * MB_STRIDE + k] = acc;        // [pair][p3][c][k]
     if (k == 64) {
 #pragma unroll
