@@ -108,15 +108,18 @@ def ictd_kernel_work(name: str, L, N: int, E: int, C: int) -> dict:
     pairs = sum(L.g_d1[g] * L.g_kcount[g] for g in range(L.NG))
     edge_in = 4 * E * (1 + NY + NREF)        # source index, harmonics, gates
     x_b, z_b = 4 * N * M * C, 4 * N * KT * C
+    # The projections do 2 * pairs * C flop per edge on ~(M + KT) * C * 4 bytes per node: 50-100 flop per
+    # algorithmic byte at 52 neighbours, above the fp32 MFMA ridge (157.3 TFLOP/s / 8 TB/s = 19.7), so their
+    # roofline is the fp32 MFMA rate.
     if name == "ictd_project":
-        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * N, bound="hbm")
+        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * N, bound="mfma")
     if name == "ictd_project_grad":
         # H = x_src g^T per edge (the gate / harmonic gradients); writes dgates and dY
-        return dict(flops=2 * E * pairs * C, bytes=z_b + x_b + edge_in + 4 * E * (NREF + NY), bound="hbm")
+        return dict(flops=2 * E * pairs * C, bytes=z_b + x_b + edge_in + 4 * E * (NREF + NY), bound="mfma")
     if name == "ictd_dual_project":
         # R = projection of the receiver gradients over the source grouping (the reversed paths: KT' = KT
         # slots, the same pairs); reads G once per node, writes R
-        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * E + 4 * N, bound="hbm")
+        return dict(flops=2 * E * pairs * C, bytes=x_b + z_b + edge_in + 4 * E + 4 * N, bound="mfma")
     if name in ("ictd_mix", "ictd_mix_grad", "ictd_dual_mix"):
         return dict(flops=2 * N * KT * C * C, bytes=z_b + x_b + 4 * L.NP * C * C, bound="mfma")
     raise KeyError(name)
