@@ -18,9 +18,10 @@
 //
 // Layouts (fp32): node features x[N][13][C] (comp-major: 0 | 1..3 = i | 4..12 = 3i+j);
 // S[N][18][65*C]: per slot a row of C*64 (c-major, k-minor) then C bias entries;
-// P[E][C/8][18][8] at the receiver-sorted edge id (channel chunks of 8, slot-major inside a chunk, so
-// that a chunk of the backward reads one contiguous block per edge; inside a chunk the slots 1, 2, 6, 7, 8
-// that the backward reads come first, pos_of_slot); h[E][64]; n[E][3] (unit vectors).
+// P[E][18*C] at the receiver-sorted edge id: a row holds first the five slots the backward reads (1, 2, 6,
+// 7, 8: positions 0..4 of pos_of_slot) as [C/8][5][8], then the other thirteen as [C/8][13][8] (channel
+// chunks of 8, slot-major inside a chunk), so the backward's reads of an edge are one contiguous 20*C-byte
+// run, a chunk at a time (p_col); h[E][64]; n[E][3] (unit vectors).
 
 #include "common.h"
 
@@ -47,6 +48,24 @@ __host__ __device__ constexpr int slot_at_pos(int pos) {
 }
 __host__ __device__ constexpr int pos_of_slot(int s) {
   return s == 0 ? 5 : s < 3 ? s - 1 : s < 6 ? s + 3 : s < 9 ? s - 4 : s;
+}
+
+// Column of (slot position pos, channel c) in an edge's row of P, and back.
+template <int C>
+__host__ __device__ constexpr int p_col(int pos, int c) {
+  return pos < 5 ? (c >> 3) * 40 + pos * 8 + (c & 7) : 5 * C + (c >> 3) * 104 + (pos - 5) * 8 + (c & 7);
+}
+template <int C>
+__host__ __device__ inline void p_col_inverse(int col, int& pos, int& c) {
+  if (col < 5 * C) {
+    const int rem = col % 40;
+    pos = rem >> 3;
+    c = 8 * (col / 40) + (rem & 7);
+  } else {
+    const int cc = col - 5 * C, rem = cc % 104;
+    pos = 5 + (rem >> 3);
+    c = 8 * (cc / 104) + (rem & 7);
+  }
 }
 
 // ---------------------------------------------------------------- weight preparation
@@ -488,21 +507,23 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
   // a[jt][4]: the biases of the lane's four output columns of tile jt.  Column block cb+3 is loaded
   // while block cb is multiplied.
   f4 a0[NJ][5], a1[NJ][5];
-  // Columns are numbered in P's chunk-major order: col = ch*144 + pos_of_slot(slot)*8 + cl for channel
-  // c = 8*ch + cl.
+  // Columns are numbered in P's order (p_col): blocks of 32 consecutive columns are stored contiguously.
   auto load = [&](f4 (&a)[NJ][5], int cb) {
 #pragma unroll
     for (int jt = 0; jt < NJ; ++jt) {
       const int col = cb * BW + 4 * NJ * (r >> 2) + 4 * jt + (r & 3);
-      const int rem = col % (8 * NSLOT), slot = slot_at_pos(rem / 8), c = 8 * (col / (8 * NSLOT)) + rem % 8;
+      int pos, c;
+      p_col_inverse<C>(col, pos, c);
+      const int slot = slot_at_pos(pos);
       const float* srow = Sm + (int64_t)slot * COLS + c * KH + 8 * q;
       a[jt][0] = ld4(srow);
       a[jt][1] = ld4(srow + 4);
       a[jt][2] = ld4(srow + 32);
       a[jt][3] = ld4(srow + 36);
       const int colq = cb * BW + 4 * NJ * q + 4 * jt;   // four consecutive channels of one slot
-      const int remq = colq % (8 * NSLOT);
-      a[jt][4] = ld4(Sm + (int64_t)slot_at_pos(remq / 8) * COLS + 64 * C + 8 * (colq / (8 * NSLOT)) + remq % 8);
+      int posq, cq;
+      p_col_inverse<C>(colq, posq, cq);
+      a[jt][4] = ld4(Sm + (int64_t)slot_at_pos(posq) * COLS + 64 * C + cq);
     }
   };
 
@@ -617,10 +638,10 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
   for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg + sub; e < end; e += EPW) {
-    const float* pr = P + (int64_t)e * (NSLOT * C) + (c / 8) * (8 * NSLOT) + (c % 8);   // + 8 * pos
+    const float* pr = P + (int64_t)e * (NSLOT * C);
     const float n0 = nvec[3 * (int64_t)e], n1 = nvec[3 * (int64_t)e + 1], n2 = nvec[3 * (int64_t)e + 2];
     const float nn[3] = {n0, n1, n2};
-    auto ps = [&](int slot) { return pr[8 * pos_of_slot(slot)]; };
+    auto ps = [&](int slot) { return pr[p_col<C>(pos_of_slot(slot), c)]; };
     const float p0 = ps(0), p1 = ps(1), p2 = ps(2);
     if constexpr (!DIR) {
       o[0] += p0;
@@ -772,7 +793,7 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
         const float* gp = Gt + ((int64_t)ch * n_nodes + dsts[e]) * (NCOMP * CC) + cl;
 #pragma unroll
         for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * CC];
-        const float* pp = P + (int64_t)eids[e] * NCOL + ch * (NSLOT * CC) + cl;
+        const float* pp = P + (int64_t)eids[e] * NCOL + ch * 40 + cl;   // p_col of positions 0..4
         pN[hh][0] = pp[pos_of_slot(1) * CC];
         pN[hh][1] = pp[pos_of_slot(2) * CC];
         pN[hh][2] = pp[pos_of_slot(6) * CC];
