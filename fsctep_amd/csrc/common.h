@@ -118,6 +118,20 @@ __device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t rsrc, uint32_t
 __device__ __forceinline__ float buffer_ld1(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)voff, (int)soff, 0));
 }
+// bf16 storage of fp32 values: four values (8 bytes) stored, one value loaded and widened exactly.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc_bytes(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buffer_st4_bf16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off, const f4& v) {
+  typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const bf4 b = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, b), rsrc, (int)byte_off, 0, 0);
+}
+__device__ __forceinline__ float buffer_ld1_bf16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+  const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(rsrc, (int)voff, (int)soff, 0);
+  return __uint_as_float((uint32_t)u << 16);
+}
 __device__ __forceinline__ f4 buffer_ld4(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, (int)soff, 0));
 }

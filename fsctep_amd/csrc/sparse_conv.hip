@@ -192,8 +192,11 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
   // store window: the nodes of the block's rows (at most NE_ROWS nodes, well below 4 GiB)
   const int64_t mfirst = (uint32_t)brow0 / (uint32_t)nI;
   const int64_t mlast = min(n_nodes - 1, (int64_t)((uint32_t)(brow0 + NE_ROWS - 1) / (uint32_t)nI));
-  const __amdgpu_buffer_rsrc_t out =
-      buffer_rsrc(S + mfirst * s_node_stride(C), (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * 4));
+  // BF16: S is stored in bf16 (its consumers round it to bf16 for their products anyway)
+  constexpr int SBYTES = BF16 ? 2 : 4;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc_bytes(
+      reinterpret_cast<char*>(S) + mfirst * s_node_stride(C) * SBYTES,
+      (uint32_t)((mlast - mfirst + 1) * s_node_stride(C) * SBYTES));
   h8 xh[RT][KS], xl[RT][KS];
   bf8 xb[RT][KS];
   float oscale[RT];    // 1 / (sw * row scale)
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
       for (int ks = 0; ks < KS; ++ks) split2h(v[ks], sr, xh[rt][ks], xl[rt][ks]);
     }
     oscale[rt] = winv[0] / sr;   // sr is a power of two: exact
-    ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * 4)
+    ooff[rt] = ok ? (uint32_t)(((m - mfirst) * s_node_stride(C) + (int64_t)(sbase + I) * COLS + 4 * q) * SBYTES)
                   : kDropOffset;
   }
   f4 stg[NST];
@@ -288,8 +291,10 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-        buffer_st4(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 4, acc[rt][j] * oscale[rt]);
+      for (int j = 0; j < NT; ++j) {
+        if constexpr (BF16) buffer_st4_bf16(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 2, acc[rt][j] * oscale[rt]);
+        else buffer_st4(out, ooff[rt] + (uint32_t)(ct * WCOLS + 16 * j) * 4, acc[rt][j] * oscale[rt]);
+      }
     __syncthreads();
   }
 }
@@ -502,8 +507,10 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
   constexpr int BW = 16 * NJ;        // column block width
   constexpr int NCB = NCOL / BW;
   const float* Sm = S + (int64_t)m * s_node_stride(C);
+  const __bf16* Smb = reinterpret_cast<const __bf16*>(S) + (int64_t)m * s_node_stride(C);   // BF16: bf16 S
 
-  // a[jt][0..3]: S row of A row r of tile jt at k = 8q..8q+7 (0, 1) and 32+8q..32+8q+7 (2, 3);
+  // a[jt][0..3]: S row of A row r of tile jt at k = 8q..8q+7 (0, 1) and 32+8q..32+8q+7 (2, 3) (BF16: the
+  // eight bf16 values of k = 8q.. in a[jt][0] and of k = 32+8q.. in a[jt][2]);
   // a[jt][4]: the biases of the lane's four output columns of tile jt.  Column block cb+3 is loaded
   // while block cb is multiplied.
   f4 a0[NJ][5], a1[NJ][5];
@@ -515,15 +522,24 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       int pos, c;
       p_col_inverse<C>(col, pos, c);
       const int slot = slot_at_pos(pos);
-      const float* srow = Sm + (int64_t)slot * COLS + c * KH + 8 * q;
-      a[jt][0] = ld4(srow);
-      a[jt][1] = ld4(srow + 4);
-      a[jt][2] = ld4(srow + 32);
-      a[jt][3] = ld4(srow + 36);
       const int colq = cb * BW + 4 * NJ * q + 4 * jt;   // four consecutive channels of one slot
       int posq, cq;
       p_col_inverse<C>(colq, posq, cq);
-      a[jt][4] = ld4(Sm + (int64_t)slot_at_pos(posq) * COLS + 64 * C + cq);
+      if constexpr (BF16) {
+        typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+        const __bf16* srow = Smb + (int64_t)slot * COLS + c * KH + 8 * q;
+        a[jt][0] = *reinterpret_cast<const f4*>(srow);
+        a[jt][2] = *reinterpret_cast<const f4*>(srow + 32);
+        const bf4 bb = *reinterpret_cast<const bf4*>(Smb + (int64_t)slot_at_pos(posq) * COLS + 64 * C + cq);
+        a[jt][4] = f4{(float)bb[0], (float)bb[1], (float)bb[2], (float)bb[3]};
+      } else {
+        const float* srow = Sm + (int64_t)slot * COLS + c * KH + 8 * q;
+        a[jt][0] = ld4(srow);
+        a[jt][1] = ld4(srow + 4);
+        a[jt][2] = ld4(srow + 32);
+        a[jt][3] = ld4(srow + 36);
+        a[jt][4] = ld4(Sm + (int64_t)slot_at_pos(posq) * COLS + 64 * C + cq);
+      }
     }
   };
 
@@ -565,12 +581,11 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const f4 x0 = a[jt][2 * ks], x1 = a[jt][2 * ks + 1];
-          const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
           if constexpr (BF16) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ah[jt][ks][j] = (__bf16)v[j];
+            ah[jt][ks] = __builtin_bit_cast(bf8, a[jt][2 * ks]);
           } else {
+            const f4 x0 = a[jt][2 * ks], x1 = a[jt][2 * ks + 1];
+            const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             split3(v, ah[jt][ks], am[jt][ks], al[jt][ks]);
           }
         }
@@ -706,7 +721,7 @@ __global__ void grad_chunk_major_kernel(const float* __restrict__ G, float* __re
 // DIR (training double backward): the same products for the derivative of the receiver assembly along
 // edge directions u (udir [E][3]): dP'_e = D_n dP_e [u] = (0, g1.u, u.g2.n + n.g2.u, 0, g2 u, 0), and in
 // place of the direction gradient the second-derivative term dn_e = sum_c P2 (g2 + g2^T) u.
-template <int C, bool DIR = false>
+template <int C, bool DIR = false, bool BF16S = false>
 __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
     const float* __restrict__ Gt, const float* __restrict__ nvec, const float* __restrict__ udir,
     const float* __restrict__ h,
@@ -734,9 +749,13 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   const int beg = src_ptr[m], end = src_ptr[m + 1];
   const float* Sm = S + (int64_t)m * s_node_stride(C);
   float* dSm = dS + (int64_t)m * s_node_stride(C);
-  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(const_cast<float*>(Sm), (uint32_t)(s_node_stride(C) * 4));
+  // BF16S (the bf16 variant): S is held in bf16, read and widened to fp32 here
+  constexpr int SB = BF16S ? 2 : 4;
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc_bytes(
+      const_cast<char*>(reinterpret_cast<const char*>(S)) + (int64_t)m * s_node_stride(C) * SB,
+      (uint32_t)(s_node_stride(C) * SB));
   const __amdgpu_buffer_rsrc_t drs = buffer_rsrc(dSm, (uint32_t)(s_node_stride(C) * 4));
-  const uint32_t svoff = (uint32_t)(((q >> 1) * COLS + 4 * (q & 1) * KH + 16 * wave + r) * 4);
+  const uint32_t svoff = (uint32_t)(((q >> 1) * COLS + 4 * (q & 1) * KH + 16 * wave + r) * SB);
   const uint32_t dvoff = (uint32_t)(((r >> 3) * COLS + (r & 7) * KH + 16 * wave + 4 * q) * 4);
   const int cl = threadIdx.x & (CC - 1);   // dP builder: channel within the chunk
   const int eb = threadIdx.x / CC;         // dP builder: edges eb, eb + 32
@@ -809,7 +828,8 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
       for (int tt = 0; tt < NCT; ++tt)
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4)
-          sv[tt][s4] = buffer_ld1(srs, svoff, (uint32_t)((2 * tt * COLS + (ch * CC + s4) * KH) * 4));
+          sv[tt][s4] = BF16S ? buffer_ld1_bf16(srs, svoff, (uint32_t)((2 * tt * COLS + (ch * CC + s4) * KH) * SB))
+                             : buffer_ld1(srs, svoff, (uint32_t)((2 * tt * COLS + (ch * CC + s4) * KH) * SB));
     };
     load_g(0);
 #pragma unroll 1
@@ -1280,7 +1300,7 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   {
     LaunchTimer tm(DIR ? "edge_message_grad_direction" : "edge_message_grad", st);
-    edge_message_grad_kernel<C, DIR><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, udir, h, S, P, src_ptr, src_perm,
+    edge_message_grad_kernel<C, DIR, BF16><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, udir, h, S, P, src_ptr, src_perm,
                                                               edge_dst, scale, dh, dS, dn, dscale, N, node_order);
   }
   if (check_launch("sparse edge_message_grad")) return 2;
