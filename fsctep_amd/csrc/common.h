@@ -167,6 +167,25 @@ __device__ __forceinline__ int xcd_node(int64_t n, const int32_t* __restrict__ o
   return (v >= 0 && v < n) ? v : -1;   // a malformed order leaves nodes unprocessed, never out of bounds
 }
 
+// Persistent form: a grid of at most the resident capacity (persist_grid) whose block b walks the nodes
+// j = b/8, b/8 + G/8, ... of its XCD's range, so the blocks an XCD runs together still take neighbouring
+// nodes and per-block set-up is paid once per block, not once per node.  Returns the k-th node of the
+// block, -1 for an order entry to skip (block-uniform) and -2 past the end.
+__device__ __forceinline__ int xcd_node_k(int64_t n, const int32_t* __restrict__ order, int k) {
+  const int64_t per = (n + 7) / 8;
+  const int64_t j = (blockIdx.x >> 3) + (int64_t)k * (gridDim.x >> 3);
+  if (j >= per) return -2;
+  const int64_t li = (blockIdx.x & 7) * per + j;
+  if (li >= n) return -2;
+  if (!order) return (int)li;
+  const int v = order[li];
+  return (v >= 0 && v < n) ? v : -1;
+}
+
+// Grid of a persistent one-block-per-node launch of `kernel` (256 threads, lds bytes of dynamic LDS):
+// min(xcd_grid(n), the blocks the device holds at once), a multiple of 8.
+unsigned persist_grid(int64_t n, const void* kernel, size_t lds);
+
 void set_error(const std::string& msg);
 int check_launch(const char* what);
 int timing_mark_begin(const char* kernel, hipStream_t st);

@@ -7,7 +7,7 @@
 // Algebra (exact; only summation order changes).  For a live path p = (k1 = (l1,p1), Y_l2 -> k3):
 //   out_n[k3][o][m3] = (1/deg n) sum_{e->n} gate_e[p] sum_i W[p][o][i] sum_{m1,m2} x_src[k1][i][m1] Y_e[l2][m2] C_p[m1][m2][m3]
 // The channel mix W is linear, so it moves after the receiver sum:
-//   BG_e[p][m1][m3] = gate_e[p] sum_m2 Y_e[l2][m2] C_p[m1][m2][m3]                      (per edge, LDS)
+//   BG_e[p][m1][m3] = gate_e[p] sum_m2 Y_e[l2][m2] C_p[m1][m2][m3]                      (per edge, MFMA)
 //   Z_n[kk][i]      = (1/deg) sum_{e->n} sum_m1 BG_e[p(kk)][m1][kk] x_src[o1+m1][i]     (MFMA, K = edges x m1)
 //   out_n[k3][m3][o]= sum_{p->k3} sum_i W[p][o][i] Z_n[koff_p+m3][i]                    (MFMA, per node)
 // Paths are grouped by first-operand key (their kk ranges are contiguous); each group's kk range is
@@ -27,132 +27,12 @@ namespace ictd {
 // (4k atoms, C 64, where the weights are 4x smaller: one tile is fastest)
 template <int C>
 constexpr int mix_rt() { return C >= 128 ? 4 : 1; }
-constexpr int EB = 16;    // edges per LDS chunk (power of two: K rows are ordered m1-major, row = m1*EB + e)
+constexpr int EB = 16;    // edges per chunk: one 16-deep K block of the projection products
 
-// Shared-memory carve-up of the projection kernels (offsets in 4-byte words, regions 16-byte aligned).
-struct ProjSmem {
-  int cgs, desc, ys, gs, srcs, wtask, bg, T, tmap, toff, total, TT;
-};
-
+// LDS carve-ups are in 4-byte words, regions 16-byte aligned.
 __host__ __device__ inline int up4(int v) { return (v + 3) & ~3; }
 
-// Row stride (floats) of the per-edge gated coupling table in LDS: NBGP (a multiple of 4) rounded to
-// 4 mod 8, so that rows of consecutive edges start in different bank quadruples (a stride of 0 mod 8,
-// e.g. 496, puts every fourth row on the same banks: the DX product's float4 reads and the coupling
-// contraction's per-edge reads then conflict).
-__host__ __device__ inline int bg_stride(const FscIctdLayout& L) { return (L.NBGP % 8 == 4) ? L.NBGP : L.NBGP + 4; }
-
-__host__ __device__ inline ProjSmem proj_smem(const FscIctdLayout& L, int ncg, bool bwd) {
-  ProjSmem s;
-  int TT = 0;
-  for (int p = 0; p < L.NP; ++p) TT += L.p_d2[p];
-  s.TT = TT;
-  int o = 0;
-  s.cgs = o;   o += up4(ncg);
-  s.desc = o;  o += 2 * L.NBGP;            // int2 per coupling column
-  s.ys = o;    o += up4(EB * L.NY);
-  s.gs = o;    o += up4(EB * L.NREF);
-  s.srcs = o;  o += EB;
-  s.wtask = o; o += 32;                    // per wave: task count + up to 4 task ids
-  s.bg = o;    o += EB * bg_stride(L);
-  s.T = s.tmap = s.toff = o;
-  if (bwd) {
-    s.T = o;    o += up4(EB * TT);
-    s.tmap = o; o += up4(TT);
-    s.toff = o; o += up4(L.NP + 1);
-  }
-  s.total = o;
-  return s;
-}
-
-// Per-block constant tables: the coupling tensors and, per column j of a chunk row of the gated coupling
-// table, where its coupling coefficients live: desc[j] = {cg offset or -1, oy | d2 << 8 | d3 << 12 | gate << 16}.
-__device__ __forceinline__ void stage_tables(const FscIctdLayout& L, const float* __restrict__ cg, int ncg,
-                                             float* __restrict__ cgs, int2* __restrict__ desc) {
-  for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
-  for (int j = threadIdx.x; j < L.NBGP; j += blockDim.x) {
-    int g = 0;
-    while (g + 1 < L.NG && j >= L.g_bgoff[g + 1]) ++g;
-    const int rel = j - L.g_bgoff[g], kpad = L.g_kpad[g];
-    const int m1 = rel / kpad, kkl = rel - m1 * kpad;
-    int2 d = make_int2(-1, 0);
-    if (m1 < L.g_d1[g] && kkl < L.g_kcount[g]) {
-      const int kk = L.g_kstart[g] + kkl;
-      const int p = L.kk_path[kk];
-      const int d2 = L.p_d2[p], d3 = L.p_d3[p];
-      d.x = L.p_cgoff[p] + m1 * d2 * d3 + (kk - L.p_koff[p]);
-      d.y = L.p_oy[p] | (d2 << 8) | (d3 << 12) | (L.p_gate[p] << 16);
-    }
-    desc[j] = d;
-  }
-}
-
-// Chunk inputs: harmonics, gates and gathered-node ids of the edges at positions [eb, eb + cnt) of the
-// block's edge list (zero / node 0 beyond cnt).  The edge id at position j is eperm[j] (null: j).  With
-// gdeg (a receiver CSR) the gates of an edge are divided by the in-degree of its gathered node (the
-// receiver normalisation of the dual projection, applied per edge).
-template <bool DUAL = false>
-__device__ __forceinline__ void stage_chunk(const FscIctdLayout& L, int eb, int cnt, const float* __restrict__ Y,
-                                            const float* __restrict__ gates, const int32_t* __restrict__ esrc,
-                                            const int32_t* __restrict__ eperm, const int32_t* __restrict__ gdeg,
-                                            float* __restrict__ ys, float* __restrict__ gs,
-                                            int32_t* __restrict__ srcs) {
-  if constexpr (!DUAL) {
-    for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
-      const int e = i / L.NY;
-      ys[i] = (e < cnt) ? Y[(int64_t)eb * L.NY + i] : 0.f;
-    }
-    for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
-      const int e = i / L.NREF;
-      gs[i] = (e < cnt) ? gates[(int64_t)eb * L.NREF + i] : 0.f;
-    }
-    if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eb + threadIdx.x] : 0;
-  } else {
-    for (int i = threadIdx.x; i < EB * L.NY; i += blockDim.x) {
-      const int e = i / L.NY;
-      ys[i] = (e < cnt) ? Y[(int64_t)eperm[eb + e] * L.NY + (i - e * L.NY)] : 0.f;
-    }
-    for (int i = threadIdx.x; i < EB * L.NREF; i += blockDim.x) {
-      const int e = i / L.NREF;
-      float v = 0.f;
-      if (e < cnt) {
-        const int64_t id = eperm[eb + e];
-        const int32_t s = esrc[id];
-        v = gates[id * L.NREF + (i - e * L.NREF)] * (1.f / (float)max(gdeg[s + 1] - gdeg[s], 1));
-      }
-      gs[i] = v;
-    }
-    if (threadIdx.x < EB) srcs[threadIdx.x] = ((int)threadIdx.x < cnt) ? esrc[eperm[eb + threadIdx.x]] : 0;
-  }
-}
-
-// Gated coupling table of the chunk: bg[e][j] = gate_e[p] sum_m2 Y_e[oy_p + m2] C_p[m1][m2][m3] (LDS only,
-// rows bg_stride apart).
-__device__ __forceinline__ void build_bg(const FscIctdLayout& L, const float* __restrict__ cgs,
-                                         const int2* __restrict__ desc, const float* __restrict__ ys,
-                                         const float* __restrict__ gs, float* __restrict__ bg) {
-  const int bgs = bg_stride(L);
-  for (int j = threadIdx.x; j < L.NBGP; j += blockDim.x) {
-    const int2 d = desc[j];
-    float s[EB];
-#pragma unroll
-    for (int e = 0; e < EB; ++e) s[e] = 0.f;
-    if (d.x >= 0) {
-      const int oy = d.y & 255, d2 = (d.y >> 8) & 15, d3 = (d.y >> 12) & 15, gate = d.y >> 16;
-      for (int m2 = 0; m2 < d2; ++m2) {
-        const float c = cgs[d.x + m2 * d3];
-#pragma unroll
-        for (int e = 0; e < EB; ++e) s[e] += ys[e * L.NY + oy + m2] * c;
-      }
-#pragma unroll
-      for (int e = 0; e < EB; ++e) s[e] *= gs[e * L.NREF + gate];
-    }
-#pragma unroll
-    for (int e = 0; e < EB; ++e) bg[e * bgs + j] = s[e];
-  }
-}
-
-// V consecutive floats (V = 2 or 4) as an MFMA-operand bundle.
+// V consecutive floats (V = 2, 4 or 8) as an MFMA-operand bundle.
 template <int V>
 struct VecF {
   float v[V];
@@ -161,10 +41,13 @@ struct VecF {
 template <int V>
 __device__ __forceinline__ VecF<V> ldv(const float* p) {
   VecF<V> r;
-  if constexpr (V == 4) {
-    const f4 t = *reinterpret_cast<const f4*>(p);
+  if constexpr (V >= 4) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.v[j] = t[j];
+    for (int h = 0; h < V / 4; ++h) {
+      const f4 t = reinterpret_cast<const f4*>(p)[h];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.v[4 * h + j] = t[j];
+    }
   } else {
     const float2 t = *reinterpret_cast<const float2*>(p);
     r.v[0] = t.x;
@@ -175,24 +58,26 @@ __device__ __forceinline__ VecF<V> ldv(const float* p) {
 
 template <int V>
 __device__ __forceinline__ void stv(float* p, const VecF<V>& r) {
-  if constexpr (V == 4) {
-    *reinterpret_cast<f4*>(p) = f4{r.v[0], r.v[1], r.v[2], r.v[3]};
+  if constexpr (V >= 4) {
+#pragma unroll
+    for (int h = 0; h < V / 4; ++h)
+      reinterpret_cast<f4*>(p)[h] = f4{r.v[4 * h], r.v[4 * h + 1], r.v[4 * h + 2], r.v[4 * h + 3]};
   } else {
     *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
   }
 }
 
-// Forward tasks are (channel span, 16-row kk tile) pairs of cost d1(group).  Snake order over the
-// cost-sorted list gives every wave at most 4 tasks with near-equal cost.
-__device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int nspan, int* __restrict__ wtask) {
+// Tasks are the 16-row kk tiles, of cost d1(group).  Snake order over the cost-sorted list gives every
+// wave at most two of the KTT <= 8 tiles with near-equal cost.
+__device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int* __restrict__ wtask) {
   if (threadIdx.x != 0) return;
-  const int T = nspan * L.KTT;
+  const int T = L.KTT;
   for (int w = 0; w < 4; ++w) wtask[w * 8] = 0;
   for (int t = 0; t < T; ++t) {
-    const int ct = L.g_d1[L.tile_group[t % L.KTT]];
+    const int ct = L.g_d1[L.tile_group[t]];
     int rank = 0;
     for (int u = 0; u < T; ++u) {
-      const int cu = L.g_d1[L.tile_group[u % L.KTT]];
+      const int cu = L.g_d1[L.tile_group[u]];
       rank += (cu > ct) || (cu == ct && u < t);
     }
     const int round = rank >> 2, pos = rank & 3;
@@ -206,8 +91,103 @@ __device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int nsp
 // The same kernel runs the dual projection of the backward (dual_layout): blocks are sources, their edges
 // come through eperm (the source grouping), the gathered rows are receiver gradients divided by their
 // receiver's in-degree (gdeg), and there is no final normalisation.
-// Column tile j of a 16*V-channel span holds channels span0 + V*r + j, so each lane gathers V
-// consecutive channels of x with one vector load and stores V consecutive channels of Z.
+//
+// The gated coupling rows are formed on the MFMA, in the operand layout of the main product: for a 16-row
+// kk tile and component m1, BG[e][kk] = gate_e[p(kk)] sum_y Y_e[y] Cf[y][kk] over the 16 edges of a chunk
+// is one 16x16x16 product (4 MFMAs, A = the chunk's harmonics, B = Cf, the tile's coupling coefficients
+// zero-padded to all NY <= 16 harmonic components), whose result lane (r, q) holds edges 4q..4q+3 of kk
+// row r: exactly the A operand of the main product when K step u takes edge 4q+u.  So there is no per-edge
+// table in LDS and no barrier inside the edge loop: each wave walks the chunks on its own.  Cf is built
+// once per block in LDS (one float4 per lane per (tile, m1) slot).
+// A wave takes at most two of the KTT <= 8 kk tiles, each over all C channels: column tile j holds
+// channels V*r + j (V = C/16), so each lane gathers V consecutive channels of x with vector loads and
+// stores V consecutive channels of Z.
+struct FwdSmem {
+  int cgs, kd, gidx, slot0, wtask, cf, total;
+};
+
+__host__ __device__ inline int n_slots(const FscIctdLayout& L) {
+  int ns = 0;
+  for (int t = 0; t < L.KTT; ++t) ns += L.g_d1[L.tile_group[t]];
+  return ns;
+}
+
+__host__ __device__ inline FwdSmem fwd_smem(const FscIctdLayout& L, int ncg) {
+  FwdSmem s;
+  int o = 0;
+  s.cgs = o;   o += up4(ncg);
+  s.kd = o;    o += 4 * L.KT;              // per kk slot: coupling offset, oy | d2 << 8 | d3 << 16, gate, path
+  s.gidx = o;  o += 16 * L.KTT;            // gate column of each kk row of each tile
+  s.slot0 = o; o += up4(L.KTT + 1);        // first Cf slot of each tile
+  s.wtask = o; o += 32;
+  s.cf = o;    o += n_slots(L) * 256;
+  s.total = o;
+  return s;
+}
+
+// First stage of the per-block tables: the coupling tensors, one descriptor per kk slot (so that the
+// per-lane lookups of the second stage read LDS, not the layout argument) and the first Cf slot of each
+// tile.  kd[kk] = {offset of C_p[0][0][kk - koff_p], oy_p | d2 << 8 | d3 << 16, gate_p, p}.
+__device__ __forceinline__ void stage_descriptors(const FscIctdLayout& L, const float* __restrict__ cg, int ncg,
+                                                  float* __restrict__ cgs, int4* __restrict__ kd,
+                                                  int* __restrict__ slot0) {
+  for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
+  for (int kk = threadIdx.x; kk < L.KT; kk += blockDim.x) {
+    const int p = L.kk_path[kk];
+    kd[kk] = make_int4(L.p_cgoff[p] + kk - L.p_koff[p], L.p_oy[p] | (L.p_d2[p] << 8) | (L.p_d3[p] << 16),
+                       L.p_gate[p], p);
+  }
+  if (threadIdx.x == 0) {
+    int s = 0;
+    for (int t = 0; t < L.KTT; ++t) {
+      slot0[t] = s;
+      s += L.g_d1[L.tile_group[t]];
+    }
+    slot0[L.KTT] = s;
+  }
+}
+
+// Tile of slot sl (wave-uniform): the last tile whose first slot is <= sl.
+__device__ __forceinline__ int tile_of_slot(const FscIctdLayout& L, const int* __restrict__ slot0, int sl) {
+  int t = 0;
+  while (t + 1 < L.KTT && sl >= slot0[t + 1]) ++t;
+  return t;
+}
+
+// Cf[slot(kt) + m1][lane (r, q)][s] = C_p[m1][y - oy_p][kk - koff_p] for y = 4q + s in [oy_p, oy_p + d2),
+// kk = kstart + (kt - tile0)*16 + r a live row of tile kt (else 0); gidx[kt][r] = the gate of that row.
+__device__ __forceinline__ void stage_fwd_tables(const FscIctdLayout& L, const float* __restrict__ cg, int ncg,
+                                                 float* __restrict__ cgs, int4* __restrict__ kd,
+                                                 int* __restrict__ gidx, int* __restrict__ slot0,
+                                                 float* __restrict__ cf) {
+  stage_descriptors(L, cg, ncg, cgs, kd, slot0);
+  __syncthreads();
+  for (int i = threadIdx.x; i < 16 * L.KTT; i += blockDim.x) {
+    const int t = i >> 4, r = i & 15, g = L.tile_group[t];
+    const int kkl = (t - L.g_tile0[g]) * 16 + r;
+    gidx[i] = kkl < L.g_kcount[g] ? kd[L.g_kstart[g] + kkl].z : 0;
+  }
+  const int nslot = slot0[L.KTT];
+  for (int i = threadIdx.x; i < nslot * 64; i += blockDim.x) {
+    const int sl = __builtin_amdgcn_readfirstlane(i >> 6), lane = i & 63, r = lane & 15, q = lane >> 4;
+    const int t = tile_of_slot(L, slot0, sl);
+    const int g = L.tile_group[t], m1 = sl - slot0[t];
+    const int kkl = (t - L.g_tile0[g]) * 16 + r;
+    f4 v = f4{0.f, 0.f, 0.f, 0.f};
+    if (kkl < L.g_kcount[g]) {
+      const int4 d = kd[L.g_kstart[g] + kkl];
+      const int oy = d.y & 255, d2 = (d.y >> 8) & 255, d3 = d.y >> 16;
+      const int base = d.x + m1 * d2 * d3;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int m2 = 4 * q + s - oy;
+        if (m2 >= 0 && m2 < d2) v[s] = cgs[base + m2 * d3];
+      }
+    }
+    reinterpret_cast<f4*>(cf)[i] = v;
+  }
+}
+
 template <int C, bool DUAL>
 __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
                                                           const float* __restrict__ Y,
@@ -219,97 +199,126 @@ __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, in
                                                           int64_t n_nodes, const int32_t* __restrict__ node_order,
                                                           const int32_t* __restrict__ eperm,
                                                           const int32_t* __restrict__ gdeg) {
-  constexpr int SPAN = C < 64 ? C : 64;
-  constexpr int V = SPAN / 16;
+  constexpr int V = C / 16;
+  constexpr int DEPTH = V >= 8 ? 2 : 3;    // components of gathers in flight
   extern __shared__ __align__(16) float smem[];
-  __shared__ float zmx[4];
-  const ProjSmem sm = proj_smem(L, ncg, false);
-  float* cgs = smem + sm.cgs;
-  int2* desc = reinterpret_cast<int2*>(smem + sm.desc);
-  float* ys = smem + sm.ys;
-  float* gs = smem + sm.gs;
-  int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
+  __shared__ float zmx[2][4];
+  const FwdSmem sm = fwd_smem(L, ncg);
+  int* gidx = reinterpret_cast<int*>(smem + sm.gidx);
+  int* slot0 = reinterpret_cast<int*>(smem + sm.slot0);
   int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
-  float* bg = smem + sm.bg;
+  const f4* cf = reinterpret_cast<const f4*>(smem + sm.cf);
 
-  const int n = xcd_node(n_nodes, node_order);
-  if (n < 0) return;
+  if (xcd_node_k(n_nodes, node_order, 0) == -2) return;   // block-uniform
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
+  assign_fwd_tasks(L, wtask);
+  stage_fwd_tables(L, cg, ncg, smem + sm.cgs, reinterpret_cast<int4*>(smem + sm.kd), gidx, slot0, smem + sm.cf);
+  __syncthreads();
+  const int ntask = wtask[wave * 8];
+
+  int done = 0;
+  for (int k = 0;; ++k) {
+  const int n = xcd_node_k(n_nodes, node_order, k);
+  if (n == -2) break;
+  if (n < 0) continue;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
-  stage_tables(L, cg, ncg, cgs, desc);
-  assign_fwd_tasks(L, C / SPAN, wtask);
-
-  f4 acc[4][V];
+  const float scale = DUAL ? 1.f : 1.f / (float)max(end - beg, 1);
+  float zmax = 0.f;
+  // a wave's tiles one after the other, each over all the node's edges (one accumulator tile set live)
+  for (int lt = 0; lt < ntask; ++lt) {
+    const int kt = wtask[wave * 8 + 1 + lt];
+    const int g = L.tile_group[kt];
+    const int d1 = L.g_d1[g], o1 = L.g_o1[g];
+    const int gc = gidx[kt * 16 + r];
+    const f4* cft = cf + slot0[kt] * 64 + lane;
+    const float* xcol = x + o1 * C + V * r;
+    f4 acc[V];
 #pragma unroll
-  for (int lt = 0; lt < 4; ++lt)
+    for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int eb = beg; eb < end; eb += EB) {
+      const int cnt = min(EB, end - eb);
+      // chunk edge r: id, gathered node, harmonics (A operand of the coupling product: Y[e = r][4q..4q+3])
+      const int idr = r < cnt ? (DUAL ? eperm[eb + r] : eb + r) : -1;
+      const int srcr = idr >= 0 ? esrc[idr] : 0;
+      f4 yop = f4{0.f, 0.f, 0.f, 0.f};
+      if (idr >= 0) {
+        const float* yr = Y + (int64_t)idr * L.NY;
+        if (L.NY == 16 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+          yop = reinterpret_cast<const f4*>(yr)[q];
+        } else {
 #pragma unroll
-    for (int j = 0; j < V; ++j) acc[lt][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-  for (int eb = beg; eb < end; eb += EB) {
-    const int cnt = min(EB, end - eb);
-    __syncthreads();
-    stage_chunk<DUAL>(L, eb, cnt, Y, gates, esrc, eperm, gdeg, ys, gs, srcs);
-    __syncthreads();
-    build_bg(L, cgs, desc, ys, gs, bg);
-    __syncthreads();
-    const int ntask = wtask[wave * 8];
-#pragma unroll
-    for (int lt = 0; lt < 4; ++lt) {
-      if (lt >= ntask) break;
-      const int t = wtask[wave * 8 + 1 + lt];
-      const int span = t / L.KTT, kt = t - span * L.KTT;
-      const int g = L.tile_group[kt];
-      const int d1 = L.g_d1[g], o1 = L.g_o1[g], kpad = L.g_kpad[g];
-      const float* arow = bg + L.g_bgoff[g] + (kt - L.g_tile0[g]) * 16 + r;
-      const float* xcol = x + o1 * C + span * SPAN + V * r;
-      // K rows m1*EB + e, e = 4u + q; the gathers of components m1+1 and m1+2 are in flight while m1 is
-      // multiplied
-      auto load_k = [&](int m1, float (&a)[EB / 4], VecF<V> (&b)[EB / 4]) {
-#pragma unroll
-        for (int u = 0; u < EB / 4; ++u) {
-          const int e = 4 * u + q;
-          a[u] = arow[e * bg_stride(L) + m1 * kpad];
-          b[u] = ldv<V>(xcol + ((int64_t)srcs[e] * L.M + m1) * C);
+          for (int s = 0; s < 4; ++s)
+            if (4 * q + s < L.NY) yop[s] = yr[4 * q + s];
         }
-      };
-      auto mul_k = [&](const float (&a)[EB / 4], const VecF<V> (&b)[EB / 4]) {
+      }
+      float gsc = 1.f;
+      if constexpr (DUAL) gsc = 1.f / (float)max(gdeg[srcr + 1] - gdeg[srcr], 1);
+      // K step u of the main product takes chunk edge 4q + u
+      int src4[4];
+      float gt[4];
 #pragma unroll
-        for (int u = 0; u < EB / 4; ++u)
+      for (int u = 0; u < 4; ++u) {
+        src4[u] = __shfl(srcr, 4 * q + u, 64);
+        const int id = DUAL ? __shfl(idr, 4 * q + u, 64) : (4 * q + u < cnt ? eb + 4 * q + u : -1);
+        const float sc = DUAL ? __shfl(gsc, 4 * q + u, 64) : 1.f;
+        gt[u] = id >= 0 ? gates[(int64_t)id * L.NREF + gc] * sc : 0.f;
+      }
+      auto load_k = [&](int m1, VecF<V> (&b)[4]) {
 #pragma unroll
-          for (int j = 0; j < V; ++j) acc[lt][j] = mfma16x16x4(a[u], b[u].v[j], acc[lt][j]);
+        for (int u = 0; u < 4; ++u) b[u] = ldv<V>(xcol + ((int64_t)src4[u] * L.M + m1) * C);
       };
-      float a0[EB / 4], a1[EB / 4], a2[EB / 4];
-      VecF<V> b0[EB / 4], b1[EB / 4], b2[EB / 4];
-      load_k(0, a0, b0);
-      if (1 < d1) load_k(1, a1, b1);
-      for (int m1 = 0; m1 < d1; m1 += 3) {
-        if (m1 + 2 < d1) load_k(m1 + 2, a2, b2);
-        __builtin_amdgcn_sched_barrier(0);
-        mul_k(a0, b0);
-        if (m1 + 1 < d1) {
-          if (m1 + 3 < d1) load_k(m1 + 3, a0, b0);
+      // gated coupling rows of component m1: a[u] = BG[edge 4q+u][kk row r]
+      auto coupling = [&](int m1, float (&a)[4]) {
+        const f4 bg = mfma_k16(yop, cft[m1 * 64], f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = bg[u] * gt[u];
+      };
+      auto mul_k = [&](const float (&a)[4], const VecF<V> (&b)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < V; ++j) acc[j] = mfma16x16x4(a[u], b[u].v[j], acc[j]);
+      };
+      float a[4];
+      VecF<V> b0[4], b1[4];
+      load_k(0, b0);
+      if constexpr (DEPTH == 2) {
+        for (int m1 = 0; m1 < d1; m1 += 2) {
+          if (m1 + 1 < d1) load_k(m1 + 1, b1);
+          coupling(m1, a);
           __builtin_amdgcn_sched_barrier(0);
-          mul_k(a1, b1);
+          mul_k(a, b0);
+          if (m1 + 1 < d1) {
+            if (m1 + 2 < d1) load_k(m1 + 2, b0);
+            coupling(m1 + 1, a);
+            __builtin_amdgcn_sched_barrier(0);
+            mul_k(a, b1);
+          }
         }
-        if (m1 + 2 < d1) {
-          if (m1 + 4 < d1) load_k(m1 + 4, a1, b1);
+      } else {
+        VecF<V> b2[4];
+        if (1 < d1) load_k(1, b1);
+        for (int m1 = 0; m1 < d1; m1 += 3) {
+          if (m1 + 2 < d1) load_k(m1 + 2, b2);
+          coupling(m1, a);
           __builtin_amdgcn_sched_barrier(0);
-          mul_k(a2, b2);
+          mul_k(a, b0);
+          if (m1 + 1 < d1) {
+            if (m1 + 3 < d1) load_k(m1 + 3, b0);
+            coupling(m1 + 1, a);
+            __builtin_amdgcn_sched_barrier(0);
+            mul_k(a, b1);
+          }
+          if (m1 + 2 < d1) {
+            if (m1 + 4 < d1) load_k(m1 + 4, b1);
+            coupling(m1 + 2, a);
+            __builtin_amdgcn_sched_barrier(0);
+            mul_k(a, b2);
+          }
         }
       }
     }
-  }
-  const float scale = DUAL ? 1.f : 1.f / (float)max(end - beg, 1);
-  __syncthreads();
-  const int ntask = wtask[wave * 8];
-  float zmax = 0.f;
-#pragma unroll
-  for (int lt = 0; lt < 4; ++lt) {
-    if (lt >= ntask) break;
-    const int t = wtask[wave * 8 + 1 + lt];
-    const int span = t / L.KTT, kt = t - span * L.KTT;
-    const int g = L.tile_group[kt];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kkl = (kt - L.g_tile0[g]) * 16 + 4 * q + i;
@@ -317,17 +326,21 @@ __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, in
       VecF<V> o;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        o.v[j] = acc[lt][j][i] * scale;
+        o.v[j] = acc[j][i] * scale;
         zmax = fmaxf(zmax, fabsf(o.v[j]));
       }
-      stv<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + span * SPAN + V * r, o);
+      stv<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + V * r, o);
     }
   }
-  // per-node power of two for the split-fp16 channel mix
+  // per-node power of two for the split-fp16 channel mix (zmx alternates between the block's nodes, so
+  // one barrier per node suffices: a wave writes a buffer again only after the barrier that follows
+  // thread 0's last read of it)
   for (int off = 32; off > 0; off >>= 1) zmax = fmaxf(zmax, __shfl_xor(zmax, off, 64));
-  if (lane == 0) zmx[wave] = zmax;
+  float* zm = zmx[done++ & 1];
+  if (lane == 0) zm[wave] = zmax;
   __syncthreads();
-  if (threadIdx.x == 0) zscale[n] = pow2_scale(fmaxf(fmaxf(zmx[0], zmx[1]), fmaxf(zmx[2], zmx[3])));
+  if (threadIdx.x == 0) zscale[n] = pow2_scale(fmaxf(fmaxf(zm[0], zm[1]), fmaxf(zm[2], zm[3])));
+  }
 }
 
 // ---------------------------------------------------------------- channel mix, forward
@@ -477,16 +490,83 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
 }
 
 // ---------------------------------------------------------------- gate and harmonic gradients (one block per receiver)
-// With g = dZ[n] / deg, per chunk of EB receiver edges:
-//   (b) H[e][m1][kk]    = sum_i x[src_e][o1+m1][i] g[kk][i]  MFMA, K = channels (into LDS)
-//   (c) T[e][p][m2]     = sum_{m1,m3} H[e][m1][koff_p+m3] C_p[m1][m2][m3]
-//       dgate[e][p] = sum_m2 Y_e[oy_p+m2] T[e][p][m2];   dY[e][y] = sum_{p covers y} gate_e[p] T[e][p][y-oy_p]
-// g is the same for every chunk of the block: each wave owns at most two 16-row kk tiles (the snake
-// assignment of the forward, balanced by d1) and holds their g rows in registers for the whole block, so
-// per chunk only the gathered x rows are read.
+// With g = dZ[n] / deg, per edge e and column j = (m1, kk) of the projection:
+//   H[e][j]      = sum_i x[src_e][o1+m1][i] g[kk][i]                  (MFMA, K = channels)
+//   BG'[e][j]    = sum_y Y_e[y] Cf[y][j]                               (the ungated coupling rows, MFMA, K = y)
+//   dgate[e][p]  = sum_{j in p} H[e][j] BG'[e][j]
+//   dY[e][y]     = sum_j H[e][j] gate_e[p(j)] Cf[y][j]                 (MFMA, K = kk)
+// Every output belongs to one edge, so each wave takes whole 16-edge chunks of the receiver (chunk c goes
+// to wave c mod 4) over all kk tiles: no reduction crosses waves and the edge loop has no barrier.  H is
+// formed transposed (A = g rows, B = x rows: lane (r, q) holds H[edge r][kk rows 4q..4q+3]), which is the
+// A-operand layout of the dY product; the coupling rows come out in the same layout from A = Cf, B = Y.
+// The per-path sums of dgate are runs of kk rows inside a tile: the tile's products go to a wave-private
+// LDS block, the lanes of an edge sum different runs and accumulate them per edge and path.  The 1/deg of
+// g is applied to the outputs.
 // The input gradient dx = sum_{e: src=m} bg_e^T g_dst(e) is not formed here: it is the dual projection
 // (project_fwd_kernel over the source grouping with the dual layout) followed by the channel mix with the
 // transposed weights, so no per-edge [M][C] gradient is stored.
+struct GradSmem {
+  int cgs, kd, gidx, slot0, runs, nrun, cf, dgs, pl, total;
+};
+
+__host__ __device__ inline GradSmem grad_smem(const FscIctdLayout& L, int ncg) {
+  GradSmem s;
+  int o = 0;
+  s.cgs = o;   o += up4(ncg);
+  s.kd = o;    o += 4 * L.KT;
+  s.gidx = o;  o += 16 * L.KTT;
+  s.slot0 = o; o += up4(L.KTT + 1);
+  s.runs = o;  o += 16 * L.KTT;            // path runs of each tile: p | first row << 8 | end row << 16
+  s.nrun = o;  o += up4(L.KTT);
+  s.cf = o;    o += n_slots(L) * 256;      // Cf[slot][y][kk row], slot = (tile, m1)
+  s.dgs = o;   o += up4(4 * 16 * L.NP);   // per wave: dgate[e][p] of the chunk
+  s.pl = o;    o += 4 * 256;               // per wave: one tile's H.BG' row sums
+  s.total = o;
+  return s;
+}
+
+__device__ __forceinline__ void stage_grad_tables(const FscIctdLayout& L, const float* __restrict__ cg, int ncg,
+                                                  float* __restrict__ cgs, int4* __restrict__ kd,
+                                                  int* __restrict__ gidx, int* __restrict__ slot0,
+                                                  int* __restrict__ runs, int* __restrict__ nrun,
+                                                  float* __restrict__ cf) {
+  stage_descriptors(L, cg, ncg, cgs, kd, slot0);
+  __syncthreads();
+  if (threadIdx.x < L.KTT) {
+    const int t = threadIdx.x, g = L.tile_group[t];
+    const int tb = (t - L.g_tile0[g]) * 16, rows = min(16, L.g_kcount[g] - tb);
+    const int4* kt0 = kd + L.g_kstart[g] + tb;
+    int k = 0;
+    for (int rb = 0; rb < rows;) {
+      const int p = kt0[rb].w;
+      int re = rb + 1;
+      while (re < rows && kt0[re].w == p) ++re;
+      runs[t * 16 + k++] = p | (rb << 8) | (re << 16);
+      rb = re;
+    }
+    nrun[t] = k;
+  }
+  for (int i = threadIdx.x; i < 16 * L.KTT; i += blockDim.x) {
+    const int t = i >> 4, r = i & 15, g = L.tile_group[t];
+    const int kkl = (t - L.g_tile0[g]) * 16 + r;
+    gidx[i] = kkl < L.g_kcount[g] ? kd[L.g_kstart[g] + kkl].z : 0;
+  }
+  const int nslot = slot0[L.KTT];
+  for (int i = threadIdx.x; i < nslot * 256; i += blockDim.x) {
+    const int sl = __builtin_amdgcn_readfirstlane(i >> 8), y = (i >> 4) & 15, r = i & 15;
+    const int t = tile_of_slot(L, slot0, sl);
+    const int g = L.tile_group[t], m1 = sl - slot0[t];
+    const int kkl = (t - L.g_tile0[g]) * 16 + r;
+    float v = 0.f;
+    if (kkl < L.g_kcount[g]) {
+      const int4 d = kd[L.g_kstart[g] + kkl];
+      const int m2 = y - (d.y & 255), d2 = (d.y >> 8) & 255, d3 = d.y >> 16;
+      if (m2 >= 0 && m2 < d2) v = cgs[d.x + (m1 * d2 + m2) * d3];
+    }
+    cf[i] = v;
+  }
+}
+
 template <int C>
 __global__ __launch_bounds__(256, 3) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
                                                            const float* __restrict__ x,
@@ -499,154 +579,140 @@ __global__ __launch_bounds__(256, 3) void project_grad_kernel(FscIctdLayout L, i
                                                            int64_t n_nodes, const int32_t* __restrict__ node_order) {
   constexpr int KS = C / 16;                           // K steps of 16 channels (4 MFMAs each)
   extern __shared__ __align__(16) float smem[];
-  const ProjSmem sm = proj_smem(L, ncg, true);
-  float* cgs = smem + sm.cgs;
-  float* ys = smem + sm.ys;
-  float* gs = smem + sm.gs;
-  int32_t* srcs = reinterpret_cast<int32_t*>(smem + sm.srcs);
-  int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
-  float* bg = smem + sm.bg;            // H of the chunk
-  float* T = smem + sm.T;              // [TT][EB]
-  int* toff = reinterpret_cast<int*>(smem + sm.toff);
+  const GradSmem sm = grad_smem(L, ncg);
+  const int* gidx = reinterpret_cast<const int*>(smem + sm.gidx);
+  const int* slot0 = reinterpret_cast<const int*>(smem + sm.slot0);
+  const int* runs = reinterpret_cast<const int*>(smem + sm.runs);
+  const int* nrun = reinterpret_cast<const int*>(smem + sm.nrun);
+  const float* cf = smem + sm.cf;
 
-  const int n = xcd_node(n_nodes, node_order);
-  if (n < 0) return;
-  const int beg = dst_ptr[n], end = dst_ptr[n + 1];
-  if (beg == end) return;                               // uniform over the block
+  if (xcd_node_k(n_nodes, node_order, 0) == -2) return;   // block-uniform
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const float scale = 1.f / (float)(end - beg);
-  for (int i = threadIdx.x; i < ncg; i += blockDim.x) cgs[i] = cg[i];
-  assign_fwd_tasks(L, 1, wtask);
-  if (threadIdx.x == 0) {
-    int o = 0;
-    for (int p = 0; p < L.NP; ++p) {
-      toff[p] = o;
-      o += L.p_d2[p];
-    }
-    toff[L.NP] = o;
-  }
+  stage_grad_tables(L, cg, ncg, smem + sm.cgs, reinterpret_cast<int4*>(smem + sm.kd),
+                    reinterpret_cast<int*>(smem + sm.gidx),
+                    reinterpret_cast<int*>(smem + sm.slot0), reinterpret_cast<int*>(smem + sm.runs),
+                    reinterpret_cast<int*>(smem + sm.nrun), smem + sm.cf);
   __syncthreads();
-
-  // the wave's tiles: group, first-operand offset, component count, H column base; g rows (row kk of the
-  // tile at lane r, channels 16 s + 4 q .. + 3) scaled by 1/deg
-  const int ntile = wtask[wave * 8];
-  int tg[2], to1[2], td1[2], tcol[2];
-  f4 gb[2][KS];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = u < ntile ? wtask[wave * 8 + 1 + u] : 0;   // tile 0 stands in for a missing tile
-    const int g = L.tile_group[t];
-    const int kkl = (t - L.g_tile0[g]) * 16 + r;
-    tg[u] = g;
-    to1[u] = L.g_o1[g];
-    td1[u] = u < ntile ? L.g_d1[g] : 0;
-    tcol[u] = L.g_bgoff[g] + (t - L.g_tile0[g]) * 16 + r;
-    const bool ok = u < ntile && kkl < L.g_kcount[g];
-    const float* gr = dZ + ((int64_t)n * L.KT + L.g_kstart[g] + (ok ? kkl : 0)) * C + 4 * q;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const f4 v = ok ? ld4(gr + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
-      gb[u][s] = f4{v.x * scale, v.y * scale, v.z * scale, v.w * scale};
-    }
-  }
-  const int bgs = bg_stride(L);
-
-  // (b) the wave's (tile, m1) products in sequence, each in two K halves; every half's x rows are loaded
-  // while the previous half multiplies, and the first half of the next chunk is requested before this
-  // chunk's coupling contractions.  Lane r gathers the x row of the chunk's edge r (the last edge stands
-  // in beyond the chunk: its H rows are not used).
+  float* dgs = smem + sm.dgs + wave * 16 * L.NP + r * L.NP;   // edge r's path sums (lanes (r, *))
+  float* pl = smem + sm.pl + wave * 256;                       // the tile's H.BG' row sums, [edge][kk row]
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
   constexpr int KH = KS / 2;
-  const int nprod = td1[0] + td1[1];
-  auto xrow_of = [&](int ebk) { return x + (int64_t)esrc[min(ebk + r, end - 1)] * L.M * C + 4 * q; };
-  auto load_half = [&](const float* xr, int j, int half, f4 (&a)[KH]) {
-    const int m = j < td1[0] ? to1[0] + j : to1[1] + (j - td1[0]);
-#pragma unroll
-    for (int s = 0; s < KH; ++s) a[s] = ld4(xr + m * C + 16 * (half * KH + s));
-  };
-  auto mul_half = [&](int u, int half, const f4 (&a)[KH], f4 acc) {
-    if (u == 0) {
-#pragma unroll
-      for (int s = 0; s < KH; ++s) acc = mfma_k16(a[s], gb[0][half * KH + s], acc);
-    } else {
-#pragma unroll
-      for (int s = 0; s < KH; ++s) acc = mfma_k16(a[s], gb[1][half * KH + s], acc);
-    }
-    return acc;
-  };
-  f4 a0[KH], a1[KH];
-  const float* xr = xrow_of(beg);
-  if (nprod > 0) load_half(xr, 0, 0, a0);
 
-  for (int eb = beg; eb < end; eb += EB) {
-    const int cnt = min(EB, end - eb);
-    const bool more = eb + EB < end;
-    const float* xn = more ? xrow_of(eb + EB) : xr;
-    for (int j = 0; j < nprod; ++j) {
-      const int u = j < td1[0] ? 0 : 1;
-      const int m1 = u == 0 ? j : j - td1[0];
-      load_half(xr, j, 1, a1);
-      __builtin_amdgcn_sched_barrier(0);
-      f4 acc = mul_half(u, 0, a0, f4{0.f, 0.f, 0.f, 0.f});
-      if (j + 1 < nprod) load_half(xr, j + 1, 0, a0);
-      else if (more) load_half(xn, 0, 0, a0);
-      __builtin_amdgcn_sched_barrier(0);
-      acc = mul_half(u, 1, a1, acc);
-      const int kpad = L.g_kpad[tg[u]];
+  // the chunks of the block's nodes, in order, go to the waves in turn (flat index mod 4)
+  int flat = 0;
+  for (int k = 0;; ++k) {
+  const int n = xcd_node_k(n_nodes, node_order, k);
+  if (n == -2) break;
+  if (n < 0) continue;
+  const int beg = dst_ptr[n], end = dst_ptr[n + 1];
+  const float scale = 1.f / (float)max(end - beg, 1);
+  const int nchunk = (end - beg + EB - 1) / EB;
+  const int c0 = (wave - flat) & 3;
+  flat += nchunk;
+  for (int c = c0; c < nchunk; c += 4) {
+    const int eb = beg + c * EB, cnt = min(EB, end - eb);
+    const bool live = r < cnt;
+    const int er = min(eb + r, end - 1);                // the last edge stands in beyond the chunk
+    const float* xr = x + (int64_t)esrc[er] * L.M * C + 4 * q;
+    f4 yop = f4{0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      const float* yr = Y + (int64_t)er * L.NY;
+      if (L.NY == 16 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+        yop = reinterpret_cast<const f4*>(yr)[q];
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bg[(4 * q + i) * bgs + tcol[u] + m1 * kpad] = acc[i];
+        for (int s = 0; s < 4; ++s)
+          if (4 * q + s < L.NY) yop[s] = yr[4 * q + s];
+      }
     }
-    xr = xn;
-    __syncthreads();
-    // harmonics and gates of the chunk for (c2); the previous chunk's (c2) is done (it preceded the barrier)
-    stage_chunk<false>(L, eb, cnt, Y, gates, esrc, nullptr, nullptr, ys, gs, srcs);
+    for (int p = q; p < L.NP; p += 4) dgs[p] = 0.f;
+    f4 dy = f4{0.f, 0.f, 0.f, 0.f};
 
-    // (c1) T[(p, m2)][e] = sum_{k = (m1, m3)} H[e][m1][koff_p + m3] C_p[m1][m2][m3]: per path one MFMA
-    // column tile (m2 < d2 <= 15) over K = d1 d3, operands read from LDS; paths dealt to the waves in turn
-    for (int p = wave; p < L.NP; p += 4) {
-      const int g = L.p_group[p];
-      const int d1 = L.g_d1[g], kpad = L.g_kpad[g], d2 = L.p_d2[p], d3 = L.p_d3[p];
-      const int K = d1 * d3;
-      const float* hb = bg + r * bgs + L.g_bgoff[g] + (L.p_koff[p] - L.g_kstart[g]);
-      const float* cb = cgs + L.p_cgoff[p] + r * d3;
-      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-      for (int k0 = 0; k0 < K; k0 += 4) {
-        const int k = k0 + q;
-        float a = 0.f, b = 0.f;
-        if (k < K) {
-          const int m1 = k / d3, m3 = k - m1 * d3;
-          a = hb[m1 * kpad + m3];                          // A[edge r][k]
-          if (r < d2) b = cb[m1 * d2 * d3 + m3];           // B[k][m2 = r]
+    // g rows of tile kt (A operand: kk row r, channels 16 s + 4 q ..; zero beyond the group's rows) and the
+    // gates of its kk rows 4q..4q+3 for edge r
+    auto load_tile = [&](int kt, f4 (&ga)[KS], f4& gt) {
+      const int g = L.tile_group[kt];
+      const int tb = (kt - L.g_tile0[g]) * 16;
+      const bool okr = tb + r < L.g_kcount[g];
+      const float* gr = dZ + ((int64_t)n * L.KT + L.g_kstart[g] + (okr ? tb + r : 0)) * C + 4 * q;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) ga[s] = okr ? ld4(gr + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gt[i] = live ? gates[(int64_t)er * L.NREF + gidx[kt * 16 + 4 * q + i]] : 0.f;
+    };
+    // half h of the x row of component m (channels 16 (h KH + s) + 4 q ..)
+    auto load_half = [&](int m, int h, f4 (&b)[KH]) {
+#pragma unroll
+      for (int s = 0; s < KH; ++s) b[s] = ld4(xr + m * C + 16 * (h * KH + s));
+    };
+    // one tile: its (m1) products, with the next tile's operands requested at its start and the first
+    // half-row of the next product always in flight
+    auto tile = [&](int kt, const f4 (&ga)[KS], const f4& gt, f4 (&gn)[KS], f4& gtn, f4 (&h0)[KH], f4 (&h1)[KH]) {
+      const int g = L.tile_group[kt];
+      const int d1 = L.g_d1[g], o1 = L.g_o1[g];
+      const bool more = kt + 1 < L.KTT;
+      const int o1n = more ? L.g_o1[L.tile_group[kt + 1]] : 0;
+      if (more) load_tile(kt + 1, gn, gtn);
+      const float* cft = cf + slot0[kt] * 256;
+      f4 P = f4{0.f, 0.f, 0.f, 0.f};
+      for (int m1 = 0; m1 < d1; ++m1) {
+        load_half(o1 + m1, 1, h1);
+        __builtin_amdgcn_sched_barrier(0);
+        f4 ht = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KH; ++s) ht = mfma_k16(ga[s], h0[s], ht);
+        if (m1 + 1 < d1) load_half(o1 + m1 + 1, 0, h0);
+        else if (more) load_half(o1n, 0, h0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < KH; ++s) ht = mfma_k16(ga[KH + s], h1[s], ht);   // H[edge r][kk 4q+i]
+        const float* cs = cft + m1 * 256;
+        f4 ca;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ca[j] = cs[(4 * q + j) * 16 + r];          // Cf[y = 4q+j][kk = r]
+        const f4 ct = *reinterpret_cast<const f4*>(cs + r * 16 + 4 * q);      // Cf[y = r][kk = 4q..4q+3]
+        const f4 bgt = mfma_k16(ca, yop, f4{0.f, 0.f, 0.f, 0.f});              // BG'[edge r][kk 4q+i]
+        f4 hg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          P[i] += ht[i] * bgt[i];
+          hg[i] = ht[i] * gt[i];
         }
-        acc = mfma16x16x4(a, b, acc);
+        dy = mfma_k16(hg, ct, dy);                                             // dY[edge 4q+i][y = r]
       }
-      if (r < d2) {
+      // per-path sums of the tile's rows: lanes (r, q) take runs q, q + 4, ...
+      *reinterpret_cast<f4*>(pl + r * 16 + 4 * q) = P;
+      wave_sync();
+      for (int k = q; k < nrun[kt]; k += 4) {
+        const int run = runs[kt * 16 + k];
+        const int p = run & 255, rb = (run >> 8) & 255, re = run >> 16;
+        float sum = 0.f;
+        for (int i = rb; i < re; ++i) sum += pl[r * 16 + i];
+        dgs[p] += sum;
+      }
+      wave_sync();
+    };
+    f4 gaA[KS], gaB[KS], gtA, gtB, h0[KH], h1[KH];
+    load_tile(0, gaA, gtA);
+    load_half(L.g_o1[L.tile_group[0]], 0, h0);
+    for (int kt = 0; kt < L.KTT; kt += 2) {
+      tile(kt, gaA, gtA, gaB, gtB, h0, h1);
+      if (kt + 1 < L.KTT) tile(kt + 1, gaB, gtB, gaA, gtA, h0, h1);
+    }
+    if (live)
+      for (int p = q; p < L.NP; p += 4) dgates[(int64_t)(eb + r) * L.NREF + L.p_gate[p]] = dgs[p] * scale;
+    if (r < L.NY) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) T[(toff[p] + r) * EB + 4 * q + i] = acc[i];
-      }
+      for (int i = 0; i < 4; ++i)
+        if (4 * q + i < cnt) dY[(int64_t)(eb + 4 * q + i) * L.NY + r] = dy[i] * scale;
     }
-    __syncthreads();
-
-    // (c2) gate and harmonic gradients of the chunk's edges
-    for (int idx = threadIdx.x; idx < L.NP * EB; idx += blockDim.x) {
-      const int p = idx / EB, e = idx & (EB - 1);
-      if (e >= cnt) continue;
-      const int oy = L.p_oy[p], d2 = L.p_d2[p], t0 = toff[p];
-      float acc = 0.f;
-      for (int m2 = 0; m2 < d2; ++m2) acc += ys[e * L.NY + oy + m2] * T[(t0 + m2) * EB + e];
-      dgates[(int64_t)(eb + e) * L.NREF + L.p_gate[p]] = acc;
-    }
-    for (int idx = threadIdx.x; idx < L.NY * EB; idx += blockDim.x) {
-      const int yc = idx / EB, e = idx & (EB - 1);
-      if (e >= cnt) continue;
-      float acc = 0.f;
-      for (int p = 0; p < L.NP; ++p) {
-        const int m2 = yc - L.p_oy[p];
-        if (m2 < 0 || m2 >= L.p_d2[p]) continue;
-        acc += gs[e * L.NREF + L.p_gate[p]] * T[(toff[p] + m2) * EB + e];
-      }
-      dY[(int64_t)(eb + e) * L.NY + yc] = acc;
-    }
+    wave_sync();
+  }
   }
 }
 
@@ -903,7 +969,8 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
       return 1;
     }
   }
-  if ((size_t)proj_smem(*L, cg_length(*L), true).total * sizeof(float) > 65536) {
+  if ((size_t)grad_smem(*L, cg_length(*L)).total * sizeof(float) > 65536 ||
+      (size_t)fwd_smem(*L, cg_length(*L)).total * sizeof(float) > 65536) {
     set_error(std::string(who) + ": layout needs more than 64 KiB of LDS per block");
     return 1;
   }
@@ -1008,8 +1075,8 @@ int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const i
   const int ncg = cg_length(L);
   {
     LaunchTimer tm(timer_project, st);
-    const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
-    project_fwd_kernel<C, DUAL><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
+    const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
+    project_fwd_kernel<C, DUAL><<<persist_grid(N, (const void*)project_fwd_kernel<C, DUAL>, lds), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
                                                           N, node_order, eperm, gdeg);
   }
   if (check_launch("ictd project_fwd")) return 2;
@@ -1041,8 +1108,8 @@ int project_only_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, co
                    hipStream_t st) {
   const int ncg = cg_length(L);
   LaunchTimer tm("ictd_project", st);
-  const size_t lds = (size_t)proj_smem(L, ncg, false).total * sizeof(float);
-  project_fwd_kernel<C, false><<<xcd_grid(N), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
+  const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
+  project_fwd_kernel<C, false><<<persist_grid(N, (const void*)project_fwd_kernel<C, false>, lds), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
                                                                Z + N * L.KT * C, N, node_order, nullptr, nullptr);
   return check_launch("ictd project") ? 2 : 0;
 }
@@ -1083,8 +1150,8 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   {
     LaunchTimer tm("ictd_project_grad", st);
     const int ncg = cg_length(L);
-    const size_t lds = (size_t)proj_smem(L, ncg, true).total * sizeof(float);
-    project_grad_kernel<C><<<xcd_grid(N), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, dgates, dY,
+    const size_t lds = (size_t)grad_smem(L, ncg).total * sizeof(float);
+    project_grad_kernel<C><<<persist_grid(N, (const void*)project_grad_kernel<C>, lds), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, dgates, dY,
                                                            N, node_order);
   }
   if (check_launch("ictd project_grad")) return 2;

@@ -1,6 +1,7 @@
 // Error state and library metadata of the C ABI.
 #include "common.h"
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -17,6 +18,40 @@ int check_launch(const char* what) {
     return 1;
   }
   return 0;
+}
+
+// ---------------------------------------------------------------- persistent launches
+namespace {
+struct GridKey {
+  const void* kernel;
+  size_t lds;
+  int dev;
+  int64_t cap;
+};
+std::mutex g_grid_mu;
+std::vector<GridKey> g_grid_cache;
+}  // namespace
+
+unsigned persist_grid(int64_t n, const void* kernel, size_t lds) {
+  const unsigned full = xcd_grid(n);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return full;                      // the one-block-per-node grid is always correct
+  }
+  std::lock_guard<std::mutex> lk(g_grid_mu);
+  for (const GridKey& k : g_grid_cache)
+    if (k.kernel == kernel && k.lds == lds && k.dev == dev) return (unsigned)std::min<int64_t>(full, k.cap);
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || cus <= 0 ||
+      per_cu <= 0) {
+    (void)hipGetLastError();
+    return full;
+  }
+  const int64_t cap = std::max<int64_t>(8, (int64_t)cus * per_cu / 8 * 8);
+  g_grid_cache.push_back(GridKey{kernel, lds, dev, cap});
+  return (unsigned)std::min<int64_t>(full, cap);
 }
 
 // ---------------------------------------------------------------- launch timing
