@@ -99,9 +99,10 @@ __device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int* __
 // row r: exactly the A operand of the main product when K step u takes edge 4q+u.  So there is no per-edge
 // table in LDS and no barrier inside the edge loop: each wave walks the chunks on its own.  Cf is built
 // once per block in LDS (one float4 per lane per (tile, m1) slot).
-// A wave takes at most two of the KTT <= 8 kk tiles, each over all C channels: column tile j holds
-// channels V*r + j (V = C/16), so each lane gathers V consecutive channels of x with vector loads and
-// stores V consecutive channels of Z.
+// A wave takes at most two of the KTT <= 8 kk tiles, each over all C channels (64-channel spans at
+// 4 waves/SIMD measured slower at C 128: the coupling product is then formed once per span): column
+// tile j holds channels V*r + j (V = C/16), so each lane gathers V consecutive channels of x with vector
+// loads and stores V consecutive channels of Z.  3 waves/SIMD at C 128, 4 below.
 struct FwdSmem {
   int cgs, kd, gidx, slot0, wtask, cf, total;
 };
@@ -189,7 +190,7 @@ __device__ __forceinline__ void stage_fwd_tables(const FscIctdLayout& L, const f
 }
 
 template <int C, bool DUAL>
-__global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
+__global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
                                                           const float* __restrict__ Y,
                                                           const float* __restrict__ gates,
                                                           const float* __restrict__ cg,
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, in
                                                           const int32_t* __restrict__ eperm,
                                                           const int32_t* __restrict__ gdeg) {
   constexpr int V = C / 16;
-  constexpr int DEPTH = V >= 8 ? 2 : 3;    // components of gathers in flight
+  constexpr int DEPTH = 2;                 // components of gathers in flight (3 costs a wave per SIMD)
   extern __shared__ __align__(16) float smem[];
   __shared__ float zmx[2][4];
   const FwdSmem sm = fwd_smem(L, ncg);
@@ -236,11 +237,18 @@ __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, in
     f4 acc[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    // chunk edge r: id and gathered node, requested one chunk ahead (issued after the chunk's first
+    // gathers) so that a chunk's gathers never wait on its index loads
+    auto chunk_id = [&](int ebk) {
+      const int ck = min(EB, end - ebk);
+      return r < ck ? (DUAL ? eperm[ebk + r] : ebk + r) : -1;
+    };
+    int idr_n = beg < end ? chunk_id(beg) : -1;
+    int srcr_n = idr_n >= 0 ? esrc[idr_n] : 0;
     for (int eb = beg; eb < end; eb += EB) {
       const int cnt = min(EB, end - eb);
-      // chunk edge r: id, gathered node, harmonics (A operand of the coupling product: Y[e = r][4q..4q+3])
-      const int idr = r < cnt ? (DUAL ? eperm[eb + r] : eb + r) : -1;
-      const int srcr = idr >= 0 ? esrc[idr] : 0;
+      const int idr = idr_n, srcr = srcr_n;
+      // harmonics of edge r (A operand of the coupling product: Y[e = r][4q..4q+3])
       f4 yop = f4{0.f, 0.f, 0.f, 0.f};
       if (idr >= 0) {
         const float* yr = Y + (int64_t)idr * L.NY;
@@ -283,6 +291,10 @@ __global__ __launch_bounds__(256, 3) void project_fwd_kernel(FscIctdLayout L, in
       float a[4];
       VecF<V> b0[4], b1[4];
       load_k(0, b0);
+      if (eb + EB < end) {
+        idr_n = chunk_id(eb + EB);
+        srcr_n = idr_n >= 0 ? esrc[idr_n] : 0;
+      }
       if constexpr (DEPTH == 2) {
         for (int m1 = 0; m1 < d1; m1 += 2) {
           if (m1 + 1 < d1) load_k(m1 + 1, b1);
@@ -568,7 +580,7 @@ __device__ __forceinline__ void stage_grad_tables(const FscIctdLayout& L, const 
 }
 
 template <int C>
-__global__ __launch_bounds__(256, 3) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
+__global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ Y,
                                                            const float* __restrict__ gates,
@@ -663,14 +675,26 @@ __global__ __launch_bounds__(256, 3) void project_grad_kernel(FscIctdLayout L, i
       for (int m1 = 0; m1 < d1; ++m1) {
         load_half(o1 + m1, 1, h1);
         __builtin_amdgcn_sched_barrier(0);
-        f4 ht = f4{0.f, 0.f, 0.f, 0.f};
+        // two accumulation chains, so consecutive MFMAs do not wait on each other's result
+        f4 ht0 = f4{0.f, 0.f, 0.f, 0.f}, ht1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KH; ++s) ht = mfma_k16(ga[s], h0[s], ht);
+        for (int s = 0; s < KH; ++s) {
+          ht0 = mfma16x16x4(ga[s].x, h0[s].x, ht0);
+          ht1 = mfma16x16x4(ga[s].y, h0[s].y, ht1);
+          ht0 = mfma16x16x4(ga[s].z, h0[s].z, ht0);
+          ht1 = mfma16x16x4(ga[s].w, h0[s].w, ht1);
+        }
         if (m1 + 1 < d1) load_half(o1 + m1 + 1, 0, h0);
         else if (more) load_half(o1n, 0, h0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < KH; ++s) ht = mfma_k16(ga[KH + s], h1[s], ht);   // H[edge r][kk 4q+i]
+        for (int s = 0; s < KH; ++s) {
+          ht0 = mfma16x16x4(ga[KH + s].x, h1[s].x, ht0);
+          ht1 = mfma16x16x4(ga[KH + s].y, h1[s].y, ht1);
+          ht0 = mfma16x16x4(ga[KH + s].z, h1[s].z, ht0);
+          ht1 = mfma16x16x4(ga[KH + s].w, h1[s].w, ht1);
+        }
+        const f4 ht = ht0 + ht1;                                               // H[edge r][kk 4q+i]
         const float* cs = cft + m1 * 256;
         f4 ca;
 #pragma unroll
