@@ -26,7 +26,7 @@ namespace ictd {
 // weights falls 4x at 4 tiles; 10k atoms, C 128: 0.56 -> 0.40 ms, 2 tiles 0.50 ms) against fewer waves
 // (4k atoms, C 64, where the weights are 4x smaller: one tile is fastest)
 template <int C>
-constexpr int mix_rt() { return C >= 128 ? 4 : 1; }
+constexpr int mix_rt() { return C >= 128 ? 3 : 1; }
 constexpr int EB = 16;    // edges per chunk: one 16-deep K block of the projection products
 
 // LDS carve-ups are in 4-byte words, regions 16-byte aligned.
@@ -355,136 +355,128 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
   }
 }
 
-// ---------------------------------------------------------------- channel mix, forward
-// out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i]; grid (rows/(64 RT), NK).
-// A wave takes RT 16-row tiles, so every weight vector it loads feeds RT MFMAs (the weights of a path
-// are re-read from L2 once per 16 RT rows).  Split-fp16 products (mfma_x3, K = i in steps of 32): the
-// Z rows of node n are scaled by zscale[n] (from project_fwd), the weights by sw, both undone at the end.
-template <int C, int RT>
-__global__ __launch_bounds__(256, 2) void mix_fwd_kernel(FscIctdLayout L, const float* __restrict__ Z,
-                                                      const float* __restrict__ zscale,
-                                                      const _Float16* __restrict__ Wh, const float* __restrict__ winv,
-                                                      float* __restrict__ out, int64_t N) {
-  constexpr int CT = C / 16, KS = C / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, q = lane >> 4;
-  const int key = blockIdx.y;
-  const int oo = L.k_oo[key], d = L.k_d[key];
-  const int64_t rows = N * d;
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
-  if (row0 >= rows) return;
-  const int64_t plane = (int64_t)L.NREF * C * C;
-  int64_t an[RT];
-  int ak[RT];
-  bool ok[RT];
-  float zs[RT];
-#pragma unroll
-  for (int u = 0; u < RT; ++u) {
-    const int64_t arow = row0 + 16 * u + r;
-    ok[u] = arow < rows;
-    an[u] = ok[u] ? arow / d : 0;
-    ak[u] = ok[u] ? (int)(arow % d) : 0;
-    zs[u] = zscale[an[u]];
-  }
-  f4 acc[RT][CT];
-#pragma unroll
-  for (int u = 0; u < RT; ++u)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < L.NP; ++p) {
-    if (L.p_oo[p] != oo) continue;
-    const _Float16* wp = Wh + (int64_t)L.p_gate[p] * C * C + r * C + 8 * q;   // row o = 16 ct + r
-    const float* zr[RT];
-#pragma unroll
-    for (int u = 0; u < RT; ++u) zr[u] = Z + (an[u] * L.KT + L.p_koff[p] + ak[u]) * C + 8 * q;
-#pragma unroll 1
-    for (int t = 0; t < KS; ++t) {
-      h8 ah[RT], al[RT];
-#pragma unroll
-      for (int u = 0; u < RT; ++u) {
-        const f4 z0 = ok[u] ? ld4(zr[u] + 32 * t) : f4{0.f, 0.f, 0.f, 0.f};
-        const f4 z1 = ok[u] ? ld4(zr[u] + 32 * t + 4) : f4{0.f, 0.f, 0.f, 0.f};
-        const float v[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        split2h(v, zs[u], ah[u], al[u]);
-      }
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const h8 bh = *reinterpret_cast<const h8*>(wp + 16 * ct * C + 32 * t);
-        const h8 bl = *reinterpret_cast<const h8*>(wp + plane + 16 * ct * C + 32 * t);
-#pragma unroll
-        for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
-      }
-    }
-  }
-  const float wi = winv[0];
-#pragma unroll
-  for (int u = 0; u < RT; ++u)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + 16 * u + 4 * q + i;
-      if (row >= rows) continue;
-      const int64_t nn = row / d;
-      const int m = (int)(row % d);
-      const float f = wi / zscale[nn];   // a power of two: exact
-      float* o = out + (nn * L.M + oo + m) * C;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
-    }
-}
+// ---------------------------------------------------------------- channel mix (forward and backward)
+// Forward (blockIdx.y = output key k3): out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i].
+// Backward (blockIdx.y = path p):        dZ[n][koff_p + m][i] = sum_o W[gate_p][o][i] G[n][oo_p + m][o].
+// A GEMM over rows (n, m) with K = (path, input channel) in steps of 32 channels.  Split-fp16 products
+// (mfma_x3): the A rows of node n are scaled by ascale[n] (zscale from project_fwd, gscale from
+// row_scale_kernel) and split as they are loaded, the weights are split once by prepare_mix_kernel
+// and stored per (gate, K step) in MFMA lane order ([plane h/l][16-column tile][lane][8]), so one K step's
+// weights are a contiguous 64 C-half block: it is copied into LDS with direct-to-LDS loads (no registers)
+// one step ahead, double-buffered, and read conflict-free by every wave of the block (the weights are
+// read from L2 once per block instead of once per wave).  The A rows of the next step are requested
+// before the current step's products.  A wave takes RT 16-row tiles over all C output columns.
+template <int C>
+constexpr int mix_step_halves() { return 2 * (C / 16) * 512; }
 
-// ---------------------------------------------------------------- channel mix, backward
-// dZ[n][koff_p + m][i] = sum_o Wt[gate_p][i][o] G[n][oo_p + m][o]; grid (rows/(64 RT), NP), RT row tiles
-// per wave as in the forward; the G rows of node n are scaled by gscale[n] (row_scale_kernel).
-template <int C, int RT>
-__global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const float* __restrict__ G,
-                                                      const float* __restrict__ gscale,
-                                                      const _Float16* __restrict__ Wth, const float* __restrict__ winv,
-                                                      float* __restrict__ dZ, int64_t N) {
-  constexpr int CT = C / 16, KS = C / 32;
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int C, int RT, bool BWD>
+__global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const float* __restrict__ A,
+                                                  const float* __restrict__ ascale,
+                                                  const _Float16* __restrict__ Wsw, const float* __restrict__ winv,
+                                                  float* __restrict__ out, int64_t N) {
+  constexpr int CT = C / 16, KS = C / 32, SH = mix_step_halves<C>();
+  static_assert(SH % 512 == 0, "a K step's weights are whole 1 KiB wave copies");
+  __shared__ __align__(16) _Float16 sw[2][SH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int p = blockIdx.y;
-  const int d = L.p_d3[p], oo = L.p_oo[p], koff = L.p_koff[p];
+  int d, oo_or_koff, p0;
+  if constexpr (BWD) {
+    p0 = blockIdx.y;
+    d = L.p_d3[p0];
+    oo_or_koff = L.p_oo[p0];
+  } else {
+    const int key = blockIdx.y;
+    d = L.k_d[key];
+    oo_or_koff = L.k_oo[key];
+    p0 = 0;
+    while (p0 < L.NP && L.p_oo[p0] != oo_or_koff) ++p0;
+  }
+  // next path of the key after p (NP: none)
+  auto next_path = [&](int p) {
+    if constexpr (BWD) return L.NP;
+    ++p;
+    while (p < L.NP && L.p_oo[p] != oo_or_koff) ++p;
+    return p;
+  };
   const int64_t rows = N * d;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
-  if (row0 >= rows) return;
-  const int64_t plane = (int64_t)L.NREF * C * C;
-  const float* gr[RT];
-  bool ok[RT];
-  float gs[RT];
+  const bool active = row0 < rows;   // wave-uniform; inactive waves still copy weights and meet the barriers
+  // A row of tile u (+ koff_p in the forward; row indices < 2^31, checked by the host), -1: past the end
+  int abase[RT];
+  float as[RT];
 #pragma unroll
   for (int u = 0; u < RT; ++u) {
     const int64_t arow = row0 + 16 * u + r;
-    ok[u] = arow < rows;
-    const int64_t an = ok[u] ? arow / d : 0;
-    const int ak = ok[u] ? (int)(arow % d) : 0;
-    gr[u] = G + (an * L.M + oo + ak) * C + 8 * q;
-    gs[u] = gscale[an];
+    const bool ok = active && arow < rows;
+    const int64_t an = ok ? arow / d : 0;
+    const int am = ok ? (int)(arow % d) : 0;
+    abase[u] = ok ? (int)(BWD ? an * L.M + oo_or_koff + am : an * L.KT + am) : -1;
+    as[u] = ascale[an];
   }
-  const _Float16* wp = Wth + (int64_t)L.p_gate[p] * C * C + r * C + 8 * q;   // row i = 16 ct + r
+  const int64_t gstride = (int64_t)KS * SH;   // halves per gate
+  // one K step's weights into LDS buffer b: whole 1 KiB copies, 16 bytes per lane
+  auto stage = [&](int p, int t, int b) {
+    const _Float16* src = Wsw + L.p_gate[p] * gstride + (int64_t)t * SH;
+#pragma unroll
+    for (int c = wave * 512; c < SH; c += 4 * 512) {
+      __builtin_amdgcn_global_load_lds((global_void*)(src + c + lane * 8), (lds_void*)(&sw[b][c]), 16, 0, 0);
+    }
+  };
+  auto load_a = [&](int p, int t, f4 (&z)[RT][2]) {
+    const int koff = BWD ? 0 : L.p_koff[p];
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const float* ar = A + (int64_t)(abase[u] + koff) * C + 32 * t + 8 * q;
+      z[u][0] = abase[u] >= 0 ? ld4(ar) : f4{0.f, 0.f, 0.f, 0.f};
+      z[u][1] = abase[u] >= 0 ? ld4(ar + 4) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
   f4 acc[RT][CT];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-  for (int t = 0; t < KS; ++t) {
+  f4 z[RT][2];
+  int p = p0, t = 0, buf = 0;
+  if (p < L.NP) {
+    stage(p, 0, 0);
+    load_a(p, 0, z);
+  }
+  while (p < L.NP) {
+    // this step's weights are in LDS for every wave, and the other buffer is free
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int tn = t + 1 < KS ? t + 1 : 0;
+    const int pn = t + 1 < KS ? p : next_path(p);
+    if (pn < L.NP) stage(pn, tn, buf ^ 1);
     h8 ah[RT], al[RT];
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
-      const f4 g0 = ok[u] ? ld4(gr[u] + 32 * t) : f4{0.f, 0.f, 0.f, 0.f};
-      const f4 g1 = ok[u] ? ld4(gr[u] + 32 * t + 4) : f4{0.f, 0.f, 0.f, 0.f};
-      const float v[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-      split2h(v, gs[u], ah[u], al[u]);
+      const float v[8] = {z[u][0].x, z[u][0].y, z[u][0].z, z[u][0].w, z[u][1].x, z[u][1].y, z[u][1].z, z[u][1].w};
+      split2h(v, as[u], ah[u], al[u]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (pn < L.NP) load_a(pn, tn, z);
+    if (active) {
+      const _Float16* wb = &sw[buf][lane * 8];
+      // a column tile's weights are read from LDS while the previous tile's products run
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const h8 bh = *reinterpret_cast<const h8*>(wp + 16 * ct * C + 32 * t);
-      const h8 bl = *reinterpret_cast<const h8*>(wp + plane + 16 * ct * C + 32 * t);
+      for (int ct = 0; ct < CT; ++ct) {
+        const h8 bh = *reinterpret_cast<const h8*>(wb + ct * 512);
+        const h8 bl = *reinterpret_cast<const h8*>(wb + (CT + ct) * 512);
 #pragma unroll
-      for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
+        for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+    p = pn;
+    t = tn;
+    buf ^= 1;
   }
+  if (!active) return;
   const float wi = winv[0];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
@@ -494,8 +486,8 @@ __global__ __launch_bounds__(256, 2) void mix_bwd_kernel(FscIctdLayout L, const 
       if (row >= rows) continue;
       const int64_t nn = row / d;
       const int m = (int)(row % d);
-      const float f = wi / gscale[nn];   // a power of two: exact
-      float* o = dZ + (nn * L.KT + koff + m) * C;
+      const float f = wi / ascale[nn];   // a power of two: exact
+      float* o = out + (BWD ? nn * L.KT + L.p_koff[p0] + m : nn * L.M + oo_or_koff + m) * C;
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
     }
@@ -873,6 +865,14 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
 // swapped, [2][NREF][C (i)][C (o)], for the backward, then a tail of MIXW_TAIL floats: [0] = 1/sw,
 // [256..511] the partial maxima of the preparation.
 constexpr int MIXW_TAIL = 512;
+// Position (in halves) of weight (row, K column col, fp16 plane) of gate p in a prepared orientation: per
+// gate, per K step of 32 columns, [plane][16-row tile][MFMA lane (row % 16) + 16 ((col % 32) / 8)][col % 8],
+// the image mix_kernel copies into LDS per step.
+__host__ __device__ inline int64_t mix_pos(int C, int64_t p, int row, int col, int plane) {
+  const int CT = C / 16;
+  const int lane = (row & 15) + 16 * ((col & 31) >> 3);
+  return p * 2 * C * C + ((int64_t)((col >> 5) * 2 + plane) * CT + (row >> 4)) * 512 + lane * 8 + (col & 7);
+}
 __host__ __device__ inline int64_t mix_weight_floats(int n_ref, int C) { return 2LL * n_ref * C * C + MIXW_TAIL; }
 
 // wmax[b] = max |W| over the grid-stride share of block b (grid 256 x 256).
@@ -906,11 +906,11 @@ __global__ __launch_bounds__(256) void prepare_mix_kernel(const float* __restric
     const float v = W[idx] * sw;
     const _Float16 h = (_Float16)v;
     const _Float16 l = (_Float16)(v - (float)h);
-    const int64_t t = (p * C + i) * C + o;
-    wf[idx] = h;
-    wf[total + idx] = l;
-    wb[t] = h;
-    wb[total + t] = l;
+    // forward orientation: rows o, K = i; transposed: rows i, K = o
+    wf[mix_pos(C, p, o, i, 0)] = h;
+    wf[mix_pos(C, p, o, i, 1)] = l;
+    wb[mix_pos(C, p, i, o, 0)] = h;
+    wb[mix_pos(C, p, i, o, 1)] = l;
   }
 }
 
@@ -1110,7 +1110,7 @@ int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const i
     LaunchTimer tm(timer_mix, st);
     constexpr int RT = mix_rt<C>();
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NK);
-    mix_fwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, Wh, winv, out, N);
+    mix_kernel<C, RT, false><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, Wh, winv, out, N);
   }
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
@@ -1166,7 +1166,7 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NP);
     float* gscale = dZ + N * L.KT * C;
     row_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, L.M * C, G, gscale);
-    mix_bwd_kernel<C, RT><<<grid, 256, 0, st>>>(L, G, gscale,
+    mix_kernel<C, RT, true><<<grid, 256, 0, st>>>(L, G, gscale,
                                                  reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
                                                  Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, dZ, N);
   }
