@@ -409,11 +409,11 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
   float as[RT];
 #pragma unroll
   for (int u = 0; u < RT; ++u) {
-    const int64_t arow = row0 + 16 * u + r;
+    const int arow = (int)row0 + 16 * u + r;
     const bool ok = active && arow < rows;
-    const int64_t an = ok ? arow / d : 0;
-    const int am = ok ? (int)(arow % d) : 0;
-    abase[u] = ok ? (int)(BWD ? an * L.M + oo_or_koff + am : an * L.KT + am) : -1;
+    const int an = ok ? arow / d : 0;
+    const int am = ok ? arow - an * d : 0;
+    abase[u] = ok ? (BWD ? an * L.M + oo_or_koff + am : an * L.KT + am) : -1;
     as[u] = ascale[an];
   }
   const int64_t gstride = (int64_t)KS * SH;   // halves per gate
@@ -439,13 +439,14 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
   for (int u = 0; u < RT; ++u)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
-  f4 z[RT][2];
+  // K steps in pairs with fixed A buffers (no loop-carried register moves)
+  f4 za[RT][2], zb[RT][2];
   int p = p0, t = 0, buf = 0;
   if (p < L.NP) {
     stage(p, 0, 0);
-    load_a(p, 0, z);
+    load_a(p, 0, za);
   }
-  while (p < L.NP) {
+  auto step = [&](const f4 (&zc)[RT][2], f4 (&zn)[RT][2]) {
     // this step's weights are in LDS for every wave, and the other buffer is free
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -455,11 +456,12 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     h8 ah[RT], al[RT];
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
-      const float v[8] = {z[u][0].x, z[u][0].y, z[u][0].z, z[u][0].w, z[u][1].x, z[u][1].y, z[u][1].z, z[u][1].w};
+      const float v[8] = {zc[u][0].x, zc[u][0].y, zc[u][0].z, zc[u][0].w,
+                          zc[u][1].x, zc[u][1].y, zc[u][1].z, zc[u][1].w};
       split2h(v, as[u], ah[u], al[u]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (pn < L.NP) load_a(pn, tn, z);
+    if (pn < L.NP) load_a(pn, tn, zn);
     if (active) {
       const _Float16* wb = &sw[buf][lane * 8];
       // a column tile's weights are read from LDS while the previous tile's products run
@@ -475,6 +477,11 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     p = pn;
     t = tn;
     buf ^= 1;
+  };
+  while (p < L.NP) {
+    step(za, zb);
+    if (p >= L.NP) break;
+    step(zb, za);
   }
   if (!active) return;
   const float wi = winv[0];
@@ -482,12 +489,12 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
   for (int u = 0; u < RT; ++u)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + 16 * u + 4 * q + i;
+      const int row = (int)row0 + 16 * u + 4 * q + i;
       if (row >= rows) continue;
-      const int64_t nn = row / d;
-      const int m = (int)(row % d);
+      const int nn = row / d;
+      const int m = row - nn * d;
       const float f = wi / ascale[nn];   // a power of two: exact
-      float* o = out + (BWD ? nn * L.KT + L.p_koff[p0] + m : nn * L.M + oo_or_koff + m) * C;
+      float* o = out + (int64_t)(BWD ? nn * L.KT + L.p_koff[p0] + m : nn * L.M + oo_or_koff + m) * C;
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
     }
@@ -1202,7 +1209,7 @@ int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t 
                           const float* gates, const float* cg, const float* W, float* z_ws, float* out,
                           const int32_t* node_order, hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv_forward")) return 1;
-  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 24) && n_edges < (1LL << 31),
                 "fsc_ictd_conv_forward: bad size");
   FSC_CHECK_ARG(dst_ptr && x && cg && W && z_ws && out, "fsc_ictd_conv_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_src && Y && gates), "fsc_ictd_conv_forward: null edge pointer");
@@ -1218,7 +1225,7 @@ int fsc_ictd_project(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edg
                      const float* gates, const float* cg, float* z_ws, const int32_t* node_order,
                      hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_project")) return 1;
-  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 24) && n_edges < (1LL << 31),
                 "fsc_ictd_project: bad size");
   FSC_CHECK_ARG(dst_ptr && x && cg && z_ws, "fsc_ictd_project: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_src && Y && gates), "fsc_ictd_project: null edge pointer");
@@ -1254,7 +1261,7 @@ int fsc_ictd_conv_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
                            float* r_ws, float* grad_x, float* grad_gates, float* grad_Y, const int32_t* node_order,
                            hipStream_t stream) {
   if (check_layout(layout, channels, "fsc_ictd_conv_backward")) return 1;
-  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 31) && n_edges < (1LL << 31),
+  FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0 && n_nodes < (1LL << 24) && n_edges < (1LL << 31),
                 "fsc_ictd_conv_backward: bad size");
   FSC_CHECK_ARG(dst_ptr && src_ptr && grad_out && x && cg && Wt && dz_ws && r_ws && grad_x,
                 "fsc_ictd_conv_backward: null pointer");

@@ -278,7 +278,8 @@ typedef struct FscIctdLayout {
  * and the project/mix ops of the reference extension (csrc/ictd_tp.cpp:140-494).
  * gates [E][NREF]; Wp: fsc_ictd_prepare_weights of tp2.weight; cg: concatenated normalised C[m1][m2][m3]
  * of the live paths; z_ws N*KT*C + N floats of scratch; out [N][M][C].  node_order: null or a
- * permutation of the nodes (fsc_spatial_order) for the per-receiver kernels (a performance hint). */
+ * permutation of the nodes (fsc_spatial_order) for the per-receiver kernels (a performance hint).
+ * n_nodes < 2^24 here, in fsc_ictd_project and in fsc_ictd_conv_backward. */
 int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                           const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
                           const float* gates, const float* cg, const float* Wp, float* z_ws, float* out,
