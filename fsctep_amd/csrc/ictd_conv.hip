@@ -500,6 +500,127 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     }
 }
 
+// Backward of the channel mix, dZ[n][koff_p + m][i] = sum_o W[gate_p][o][i] G[n][oo_p + m][o]
+// (blockIdx.y = path p): one path per block, so all its K steps stay in LDS (2 C^2 halves, staged once)
+// and the block runs TPB row tiles of 64 RT rows with no further barrier; each wave walks its 16 RT-row
+// tiles with the A rows of the next K step (possibly of its next tile) requested before the current
+// products.  Split-fp16 as in mix_kernel.
+template <int C, int RT, int TPB>
+__global__ __launch_bounds__(256, 2) void mix_grad_kernel(FscIctdLayout L, const float* __restrict__ G,
+                                                       const float* __restrict__ gscale,
+                                                       const _Float16* __restrict__ Wsw,
+                                                       const float* __restrict__ winv, float* __restrict__ dZ,
+                                                       int64_t N) {
+  constexpr int CT = C / 16, KS = C / 32, SH = mix_step_halves<C>();
+  __shared__ __align__(16) _Float16 sw[KS * SH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int p = blockIdx.y;
+  const int d = L.p_d3[p], oo = L.p_oo[p], koff = L.p_koff[p];
+  const int rows = (int)(N * d);
+  const int wtiles = (rows + 16 * RT - 1) / (16 * RT);            // 16 RT-row wave tiles of the path
+  const int w0 = blockIdx.x * 4 * TPB;
+  if (w0 >= wtiles) return;                                        // block-uniform
+  {
+    const _Float16* src = Wsw + (int64_t)L.p_gate[p] * KS * SH;
+    for (int c = wave * 512; c < KS * SH; c += 4 * 512)
+      __builtin_amdgcn_global_load_lds((global_void*)(src + c + lane * 8), (lds_void*)(&sw[c]), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  const int wend = min(w0 + 4 * TPB, wtiles);
+  // A rows of wave tile wt: base index of G row (n, oo + m), -1 past the end; the node's scale
+  auto rows_of = [&](int wt, int (&ab)[RT], float (&as)[RT]) {
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const int arow = wt * 16 * RT + 16 * u + r;
+      const bool ok = wt < wend && arow < rows;
+      const int an = ok ? arow / d : 0;
+      ab[u] = ok ? an * L.M + oo + (arow - an * d) : -1;
+      as[u] = gscale[an];
+    }
+  };
+  auto load_a = [&](const int (&ab)[RT], int t, f4 (&z)[RT][2]) {
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const float* ar = G + (int64_t)ab[u] * C + 32 * t + 8 * q;
+      z[u][0] = ab[u] >= 0 ? ld4(ar) : f4{0.f, 0.f, 0.f, 0.f};
+      z[u][1] = ab[u] >= 0 ? ld4(ar + 4) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  const float wi = winv[0];
+  int wt = w0 + wave;
+  if (wt >= wend) return;                                          // wave-uniform, no barrier follows
+  int ab[RT], abn[RT];
+  float as[RT], asn[RT];
+  rows_of(wt, ab, as);
+  f4 za[RT][2], zb[RT][2];
+  load_a(ab, 0, za);
+  // one wave tile, its A rows for K step 0 in z0; the K steps alternate between the two buffers, and the
+  // last one requests the next tile's first step (into z0 when KS is even, else into z1)
+  auto tile = [&](f4 (&z0)[RT][2], f4 (&z1)[RT][2]) {
+    f4 acc[RT][CT];
+#pragma unroll
+    for (int u = 0; u < RT; ++u)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[u][ct] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      __builtin_amdgcn_sched_barrier(0);
+      f4 (&zc)[RT][2] = (t & 1) ? z1 : z0;
+      f4 (&zn)[RT][2] = (t & 1) ? z0 : z1;
+      h8 ah[RT], al[RT];
+#pragma unroll
+      for (int u = 0; u < RT; ++u) {
+        const float v[8] = {zc[u][0].x, zc[u][0].y, zc[u][0].z, zc[u][0].w,
+                            zc[u][1].x, zc[u][1].y, zc[u][1].z, zc[u][1].w};
+        split2h(v, as[u], ah[u], al[u]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < KS) {
+        load_a(ab, t + 1, zn);
+      } else {
+        rows_of(wt + 4, abn, asn);
+        load_a(abn, 0, zn);
+      }
+      const _Float16* wb = &sw[t * SH + lane * 8];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const h8 bh = *reinterpret_cast<const h8*>(wb + ct * 512);
+        const h8 bl = *reinterpret_cast<const h8*>(wb + (CT + ct) * 512);
+#pragma unroll
+        for (int u = 0; u < RT; ++u) acc[u][ct] = mfma_x3(ah[u], al[u], bh, bl, acc[u][ct]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RT; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wt * 16 * RT + 16 * u + 4 * q + i;
+        if (row >= rows) continue;
+        const int nn = row / d;
+        const float f = wi / gscale[nn];   // a power of two: exact
+        float* o = dZ + (int64_t)(nn * L.KT + koff + row - nn * d) * C;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
+      }
+    wt += 4;
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      ab[u] = abn[u];
+      as[u] = asn[u];
+    }
+  };
+  while (wt < wend) {
+    tile(za, zb);
+    if constexpr (KS % 2 == 1) {
+      if (wt >= wend) break;
+      tile(zb, za);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- gate and harmonic gradients (one block per receiver)
 // With g = dZ[n] / deg, per edge e and column j = (m1, kk) of the projection:
 //   H[e][j]      = sum_i x[src_e][o1+m1][i] g[kk][i]                  (MFMA, K = channels)
@@ -1169,13 +1290,14 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   for (int p = 0; p < L.NP; ++p) dmax = max(dmax, L.p_d3[p]);
   {
     LaunchTimer tm("ictd_mix_grad", st);
-    constexpr int RT = mix_rt<C>();
-    dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NP);
+    constexpr int RT = mix_rt<C>(), TPB = 2;
+    const int64_t wtiles = (N * dmax + 16 * RT - 1) / (16 * RT);
+    dim3 grid((unsigned)((wtiles + 4 * TPB - 1) / (4 * TPB)), (unsigned)L.NP);
     float* gscale = dZ + N * L.KT * C;
     row_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, L.M * C, G, gscale);
-    mix_kernel<C, RT, true><<<grid, 256, 0, st>>>(L, G, gscale,
-                                                 reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
-                                                 Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, dZ, N);
+    mix_grad_kernel<C, RT, TPB><<<grid, 256, 0, st>>>(L, G, gscale,
+                                                      reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
+                                                      Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, dZ, N);
   }
   if (check_launch("ictd mix_bwd")) return 2;
   {
