@@ -355,12 +355,11 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
   }
 }
 
-// ---------------------------------------------------------------- channel mix (forward and backward)
-// Forward (blockIdx.y = output key k3): out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i].
-// Backward (blockIdx.y = path p):        dZ[n][koff_p + m][i] = sum_o W[gate_p][o][i] G[n][oo_p + m][o].
+// ---------------------------------------------------------------- channel mix
+// out[n][oo_k3 + m][o] = sum_{p -> k3} sum_i W[gate_p][o][i] Z[n][koff_p + m][i] (blockIdx.y = output key k3).
 // A GEMM over rows (n, m) with K = (path, input channel) in steps of 32 channels.  Split-fp16 products
-// (mfma_x3): the A rows of node n are scaled by ascale[n] (zscale from project_fwd, gscale from
-// row_scale_kernel) and split as they are loaded, the weights are split once by prepare_mix_kernel
+// (mfma_x3): the A rows of node n are scaled by ascale[n] (zscale from project_fwd) and split as they
+// are loaded, the weights are split once by prepare_mix_kernel
 // and stored per (gate, K step) in MFMA lane order ([plane h/l][16-column tile][lane][8]), so one K step's
 // weights are a contiguous 64 C-half block: it is copied into LDS with direct-to-LDS loads (no registers)
 // one step ahead, double-buffered, and read conflict-free by every wave of the block (the weights are
@@ -372,7 +371,7 @@ constexpr int mix_step_halves() { return 2 * (C / 16) * 512; }
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int C, int RT, bool BWD>
+template <int C, int RT>
 __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const float* __restrict__ A,
                                                   const float* __restrict__ ascale,
                                                   const _Float16* __restrict__ Wsw, const float* __restrict__ winv,
@@ -382,29 +381,20 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
   __shared__ __align__(16) _Float16 sw[2][SH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  int d, oo_or_koff, p0;
-  if constexpr (BWD) {
-    p0 = blockIdx.y;
-    d = L.p_d3[p0];
-    oo_or_koff = L.p_oo[p0];
-  } else {
-    const int key = blockIdx.y;
-    d = L.k_d[key];
-    oo_or_koff = L.k_oo[key];
-    p0 = 0;
-    while (p0 < L.NP && L.p_oo[p0] != oo_or_koff) ++p0;
-  }
+  const int key = blockIdx.y;
+  const int d = L.k_d[key], oo = L.k_oo[key];
+  int p0 = 0;
+  while (p0 < L.NP && L.p_oo[p0] != oo) ++p0;
   // next path of the key after p (NP: none)
   auto next_path = [&](int p) {
-    if constexpr (BWD) return L.NP;
     ++p;
-    while (p < L.NP && L.p_oo[p] != oo_or_koff) ++p;
+    while (p < L.NP && L.p_oo[p] != oo) ++p;
     return p;
   };
   const int64_t rows = N * d;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   const bool active = row0 < rows;   // wave-uniform; inactive waves still copy weights and meet the barriers
-  // A row of tile u (+ koff_p in the forward; row indices < 2^31, checked by the host), -1: past the end
+  // Z row of tile u (+ koff_p; row indices < 2^31, checked by the host), -1: past the end
   int abase[RT];
   float as[RT];
 #pragma unroll
@@ -413,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     const bool ok = active && arow < rows;
     const int an = ok ? arow / d : 0;
     const int am = ok ? arow - an * d : 0;
-    abase[u] = ok ? (BWD ? an * L.M + oo_or_koff + am : an * L.KT + am) : -1;
+    abase[u] = ok ? an * L.KT + am : -1;
     as[u] = ascale[an];
   }
   const int64_t gstride = (int64_t)KS * SH;   // halves per gate
@@ -426,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     }
   };
   auto load_a = [&](int p, int t, f4 (&z)[RT][2]) {
-    const int koff = BWD ? 0 : L.p_koff[p];
+    const int koff = L.p_koff[p];
 #pragma unroll
     for (int u = 0; u < RT; ++u) {
       const float* ar = A + (int64_t)(abase[u] + koff) * C + 32 * t + 8 * q;
@@ -494,7 +484,7 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
       const int nn = row / d;
       const int m = row - nn * d;
       const float f = wi / ascale[nn];   // a power of two: exact
-      float* o = out + (int64_t)(BWD ? nn * L.KT + L.p_koff[p0] + m : nn * L.M + oo_or_koff + m) * C;
+      float* o = out + (int64_t)(nn * L.M + oo + m) * C;
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) o[16 * ct + r] = acc[u][ct][i] * f;
     }
@@ -1238,7 +1228,7 @@ int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const i
     LaunchTimer tm(timer_mix, st);
     constexpr int RT = mix_rt<C>();
     dim3 grid((unsigned)((N * dmax + 64 * RT - 1) / (64 * RT)), (unsigned)L.NK);
-    mix_kernel<C, RT, false><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, Wh, winv, out, N);
+    mix_kernel<C, RT><<<grid, 256, 0, st>>>(L, Z, Z + N * L.KT * C, Wh, winv, out, N);
   }
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
