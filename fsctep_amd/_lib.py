@@ -59,6 +59,15 @@ SIGNATURES = {
     "fsc_neighbor_fill": [_i64, _i64, _p, _p, _p, ctypes.c_double, _p, _p, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_forward": [_i64, _p, _p, _p, _p, _p],
     "fsc_edge_vec_geometry_backward": [_i64, _p, _p, _p, _p, _p, _p, _p],
+    "fsc_bucket_project": [_i64] + [_i32] * 5 + [_p] * 4 + [_i32, _p],
+    "fsc_bucket_project_transpose_a": [_i64] + [_i32] * 5 + [_p] * 4 + [_i32, _p],
+    "fsc_bucket_project_workspace": [_i64] + [_i32] * 5 + [_pi64],
+    "fsc_bucket_project_transpose_vu": [_i64] + [_i32] * 5 + [_p] * 6 + [_i32, _p, _p],
+    "fsc_bucket_mix": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p],
+    "fsc_bucket_mix_workspace": [_i64] + [_i32] * 4 + [_pi64],
+    "fsc_bucket_mix_transpose_y": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p, _p],
+    "fsc_bucket_mix_transpose_w": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p, _p],
+    "fsc_bucket_mix_transpose_g": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p],
 }
 
 _lib = None

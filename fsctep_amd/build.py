@@ -57,10 +57,12 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     hip_cmd = [hipcc, *HIP_FLAGS, *inc, *sources(), "-o", tmp]
     tinc, tlib = _torch_dirs()
-    obj = os.path.join(PKG, "torch_ops.o.tmp")
-    torch_cc = [hipcc, "-std=c++17", "-O2", "-fPIC", "-c", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
-                "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"),
-                "-I", "/opt/rocm/include", *inc, os.path.join(CSRC, "torch_ops.cpp"), "-o", obj]
+    torch_srcs = ["torch_ops.cpp", "torch_bucket_ops.cpp"]
+    objs = [os.path.join(PKG, src.replace(".cpp", ".o.tmp")) for src in torch_srcs]
+    torch_ccs = [[hipcc, "-std=c++17", "-O2", "-fPIC", "-c", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+                  "-D_GLIBCXX_USE_CXX11_ABI=1", "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"),
+                  "-I", "/opt/rocm/include", *inc, os.path.join(CSRC, src), "-o", obj]
+                 for src, obj in zip(torch_srcs, objs)]
     crun_tmp = CORE_RUN + ".tmp"
     core_cc = ["g++", "-std=c++17", "-O1", "-D_GLIBCXX_USE_CXX11_ABI=1", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
                "-I", tinc, "-I", os.path.join(tinc, "torch", "csrc", "api", "include"), "-I", "/opt/rocm/include",
@@ -68,21 +70,24 @@ def build(verbose: bool = False) -> str:
                "-L", tlib, "-Wl,--no-as-needed", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip",
                f"-Wl,-rpath,{tlib}", "-L", "/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib", "-ldl"]
     if verbose:
-        print(" ".join(hip_cmd), "\n", " ".join(torch_cc), "\n", " ".join(core_cc), flush=True)
+        print(" ".join(hip_cmd), "\n", "\n ".join(" ".join(c) for c in torch_ccs), "\n", " ".join(core_cc),
+              flush=True)
     procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
-             for c in (hip_cmd, torch_cc, core_cc)]
-    notes = [_check(None, procs[0], "libfsctep_hip.so"), _check(None, procs[1], "torch_ops.cpp"),
-             _check(None, procs[2], "tests/cpp/core_run")]
+             for c in (hip_cmd, *torch_ccs, core_cc)]
+    notes = [_check(None, procs[0], "libfsctep_hip.so")]
+    notes += [_check(None, pr, src) for pr, src in zip(procs[1:-1], torch_srcs)]
+    notes.append(_check(None, procs[-1], "tests/cpp/core_run"))
     os.replace(crun_tmp, CORE_RUN)
     os.replace(tmp, LIB)
     ttmp = TORCH_LIB + ".tmp"
-    link = [hipcc, "-shared", "-fPIC", obj, "-o", ttmp, "-L", PKG, "-lfsctep_hip", "-L", tlib, "-ltorch",
+    link = [hipcc, "-shared", "-fPIC", *objs, "-o", ttmp, "-L", PKG, "-lfsctep_hip", "-L", tlib, "-ltorch",
             "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}"]
     res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("linking libfsctep_torch.so failed")
-    os.remove(obj)
+    for obj in objs:
+        os.remove(obj)
     os.replace(ttmp, TORCH_LIB)
     if verbose and any(notes):
         print("\n".join(n for n in notes if n))

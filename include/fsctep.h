@@ -332,6 +332,51 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
                             const float* gates, const float* qtab, float* grad_F, float* grad_gates,
                             hipStream_t stream);
 
+/* ------------------------------------------------------------------ per-edge (bucketed) ICTD TP
+ * The operations of the reference's native extension molecular_force_field._C_ictd_tp
+ * (csrc/ictd_tp.cpp:498-522; einsum semantics models/ictd_irreps_cuda.py:169-288), for the arguments its
+ * CUDA path takes: fp32, mul_in2 == 1.  B batch (edges), I = mul_in1, O = mul_out, K = kdim, P paths.
+ *   project:  y[b][p][k][i] = sum_{m,n} a[b][i][m] v[b][n] u[m*m2+n][p*K+k]
+ *   mix:      out[b][o][k]  = sum_p gates[b][p] sum_i y[b][p][k][i] w[p][o][i]
+ * Layouts: a [B][I][m1], v [B][1][m2], u [m1*m2][P*K], y [B][P][K][I], w [P][O][I], gates [B][P],
+ * out [B][O][K].  accumulate != 0 adds to the output instead of overwriting it (the double-backward
+ * sums).  Limits: m1, m2 <= 9, P*K <= 64 (projection; the U gradient also m1*m2*P*K <= 2048);
+ * I, O multiples of 4 and K <= 128 (mix).  The U and W gradients sum over the batch through the
+ * caller's workspace in a fixed order (deterministic). */
+/* project_bucket_forward (csrc/ictd_tp.cpp:140-176): y from a, v, u. */
+int fsc_bucket_project(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K, const float* a,
+                       const float* v, const float* u, float* y, int32_t accumulate, hipStream_t stream);
+/* project_bucket_transpose_a (csrc/ictd_tp.cpp:178-208): grad_a [B][I][m1] from grad_y, v, u. */
+int fsc_bucket_project_transpose_a(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
+                                   const float* grad_y, const float* v, const float* u, float* grad_a,
+                                   int32_t accumulate, hipStream_t stream);
+/* Floats of the workspace of fsc_bucket_project_transpose_vu when grad_u is requested. */
+int fsc_bucket_project_workspace(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
+                                 int64_t* workspace_floats);
+/* project_bucket_transpose_b and _u (csrc/ictd_tp.cpp:210-269): grad_v [B][1][m2] and/or grad_u
+ * [m1*m2][P*K] (either may be null) from grad_y, a, v, u. */
+int fsc_bucket_project_transpose_vu(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
+                                    const float* grad_y, const float* a, const float* v, const float* u,
+                                    float* grad_v, float* grad_u, int32_t accumulate, float* workspace,
+                                    hipStream_t stream);
+/* mix_bucket_forward (csrc/ictd_tp.cpp:271-294): out from y, w, gates. */
+int fsc_bucket_mix(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* y, const float* w,
+                   const float* gates, float* out, int32_t accumulate, hipStream_t stream);
+/* Floats of the workspace of fsc_bucket_mix_transpose_y and _w. */
+int fsc_bucket_mix_workspace(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, int64_t* workspace_floats);
+/* mix_bucket_transpose_y (csrc/ictd_tp.cpp:296-322): grad_y [B][P][K][I] from grad_out, w, gates. */
+int fsc_bucket_mix_transpose_y(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
+                               const float* w, const float* gates, float* grad_y, int32_t accumulate,
+                               float* workspace, hipStream_t stream);
+/* mix_bucket_transpose_w (csrc/ictd_tp.cpp:324-345): grad_w [P][O][I] from grad_out, y, gates. */
+int fsc_bucket_mix_transpose_w(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
+                               const float* y, const float* gates, float* grad_w, int32_t accumulate,
+                               float* workspace, hipStream_t stream);
+/* mix_bucket_transpose_g (csrc/ictd_tp.cpp:347-373): grad_gates [B][P] from grad_out, y, w. */
+int fsc_bucket_mix_transpose_g(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
+                               const float* y, const float* w, float* grad_gates, int32_t accumulate,
+                               hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Readout invariant Gram bilinear: out[n][o] = sum_{i,j} W[o][i][j] G_n[i][j],
  * G_n[i][j] = scale * sum_m t[n][m][i] t[n][m][j], for t [N][D][nC] (D in {1,3,5,7,9}, nC a

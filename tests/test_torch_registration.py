@@ -19,7 +19,13 @@ OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_
        "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
        "readout_gather", "readout_scatter", "readout_features", "graph_prepare", "edge_vec_geometry",
        "edge_vec_geometry_backward", "spatial_order", "ictd_project", "sparse_conv_direction",
-       "sparse_conv_direction_backward"]
+       "sparse_conv_direction_backward",
+       # the per-edge (bucketed) ICTD ops under the reference extension's names (csrc/ictd_tp.cpp:498-521)
+       "project_bucket_forward", "project_bucket_transpose_a", "project_bucket_transpose_b",
+       "project_bucket_transpose_u", "mix_bucket_forward", "mix_bucket_transpose_y", "mix_bucket_transpose_w",
+       "mix_bucket_transpose_g", "bucketed_tp_forward", "project_dbl_bwd_grad_h", "project_dbl_bwd_grad_a",
+       "project_dbl_bwd_grad_b", "project_dbl_bwd_grad_u", "mix_dbl_bwd_grad_g_out", "mix_dbl_bwd_grad_y",
+       "mix_dbl_bwd_grad_w", "mix_dbl_bwd_grad_g"]
 
 
 class GramProbe(torch.nn.Module):
