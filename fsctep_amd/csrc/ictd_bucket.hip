@@ -35,15 +35,24 @@ struct Dims {
   int I, m1, m2, P, K, O;
 };
 
-// Factor of the projection for element b: ub[m][pk] = sum_n v[b][n] U[m*m2+n][pk] (us: U in LDS).
+// Factor of the projection for element b, padded to MAXM rows: ub[m][pk] = sum_n v[b][n] U[m*m2+n][pk] for
+// m < m1 and zero for m1 <= m < MAXM (us: U in LDS), so that the contractions below run over MAXM rows with
+// no branch (a branch per row would make every product wait for all outstanding stores).
 __device__ __forceinline__ void form_ub(const Dims& d, int PK, const float* __restrict__ v, const float* us, float* ub,
                                         int64_t b, bool ok, int lane) {
-  for (int idx = lane; idx < d.m1 * PK; idx += 64) {
+  float vb[MAXM];   // v[b][n], zero past m2: all loads issued together (one wait)
+#pragma unroll
+  for (int n = 0; n < MAXM; ++n) {
+    const float x = v[(ok ? b : 0) * d.m2 + min(n, d.m2 - 1)];
+    vb[n] = (ok && n < d.m2) ? x : 0.f;
+  }
+  for (int idx = lane; idx < MAXM * PK; idx += 64) {
     const int m = idx / PK, pk = idx - m * PK;
+    const int mc = min(m, d.m1 - 1);
     float s = 0.f;
-    if (ok)
-      for (int n = 0; n < d.m2; ++n) s += v[b * d.m2 + n] * us[(m * d.m2 + n) * PK + pk];
-    ub[idx] = s;
+#pragma unroll
+    for (int n = 0; n < MAXM; ++n) s += vb[n] * us[(mc * d.m2 + min(n, d.m2 - 1)) * PK + pk];
+    ub[idx] = m < d.m1 ? s : 0.f;
   }
 }
 
@@ -51,15 +60,16 @@ __device__ __forceinline__ void put(float* p, float v, int acc) { *p = acc ? *p 
 
 // TA false: y[b][pk][i] (+)= sum_m a[b][i][m] ub[m][pk]        (src = a, dst = y)
 // TA true:  grad_a[b][i][m] (+)= sum_pk gy[b][pk][i] ub[m][pk]  (src = gy, dst = grad_a)
-// Four waves per block, one batch element per wave per step; U staged in LDS once per block.
-template <bool TA>
+// Four waves per block, one batch element per wave per step; U staged in LDS once per block.  Lane i holds
+// its a row (MAXM values, zero past m1; the loads clamp their index) or its gy values eight at a time.
+template <bool TA, bool ACC>
 __global__ __launch_bounds__(256) void project_kernel(Dims d, const float* __restrict__ src, const float* __restrict__ v,
-                                                      const float* __restrict__ U, float* __restrict__ dst, int acc) {
+                                                      const float* __restrict__ U, float* __restrict__ dst) {
   extern __shared__ float sm[];
   const int PK = d.P * d.K, MN = d.m1 * d.m2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float* us = sm;
-  float* ub = sm + MN * PK + wave * d.m1 * PK;
+  float* ub = sm + MN * PK + wave * MAXM * PK;
   for (int idx = threadIdx.x; idx < MN * PK; idx += 256) us[idx] = U[idx];
   __syncthreads();
   // the trip count is the same for every wave of the block (barriers inside)
@@ -68,32 +78,51 @@ __global__ __launch_bounds__(256) void project_kernel(Dims d, const float* __res
     const bool ok = b < d.B;
     form_ub(d, PK, v, us, ub, b, ok, lane);
     __syncthreads();
-    if (ok) {
+    if (ok) {   // wave-uniform
       for (int i = lane; i < d.I; i += 64) {
         if constexpr (!TA) {
+          const float* ar = src + (b * d.I + i) * d.m1;
           float av[MAXM];
 #pragma unroll
-          for (int m = 0; m < MAXM; ++m) av[m] = m < d.m1 ? src[(b * d.I + i) * d.m1 + m] : 0.f;
+          for (int m = 0; m < MAXM; ++m) {
+            const float x = ar[min(m, d.m1 - 1)];
+            av[m] = m < d.m1 ? x : 0.f;
+          }
+          float* yo = dst + b * PK * d.I + i;
           for (int pk = 0; pk < PK; ++pk) {
             float s = 0.f;
 #pragma unroll
-            for (int m = 0; m < MAXM; ++m)
-              if (m < d.m1) s += av[m] * ub[m * PK + pk];
-            put(dst + (b * PK + pk) * d.I + i, s, acc);
+            for (int m = 0; m < MAXM; ++m) s += av[m] * ub[m * PK + pk];
+            if constexpr (ACC) s += yo[(int64_t)pk * d.I];
+            yo[(int64_t)pk * d.I] = s;
           }
         } else {
+          const float* gp = src + b * PK * d.I + i;
           float sa[MAXM];
 #pragma unroll
           for (int m = 0; m < MAXM; ++m) sa[m] = 0.f;
-          for (int pk = 0; pk < PK; ++pk) {
-            const float gv = src[(b * PK + pk) * d.I + i];
+          for (int pk0 = 0; pk0 < PK; pk0 += 8) {
+            float g8[8];
+            int pc[8];
 #pragma unroll
-            for (int m = 0; m < MAXM; ++m)
-              if (m < d.m1) sa[m] += gv * ub[m * PK + pk];
+            for (int j = 0; j < 8; ++j) {
+              pc[j] = min(pk0 + j, PK - 1);
+              const float x = gp[(int64_t)pc[j] * d.I];
+              g8[j] = pk0 + j < PK ? x : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+              for (int m = 0; m < MAXM; ++m) sa[m] += g8[j] * ub[m * PK + pc[j]];
           }
+          float* o = dst + (b * d.I + i) * d.m1;
 #pragma unroll
           for (int m = 0; m < MAXM; ++m)
-            if (m < d.m1) put(dst + (b * d.I + i) * d.m1 + m, sa[m], acc);
+            if (m < d.m1) {
+              float val = sa[m];
+              if constexpr (ACC) val += o[m];
+              o[m] = val;
+            }
         }
       }
     }
@@ -112,7 +141,7 @@ __global__ __launch_bounds__(256) void project_t_kernel(Dims d, const float* __r
                                                         float* __restrict__ grad_v, int acc, float* __restrict__ upart) {
   extern __shared__ float sm[];
   const int PK = d.P * d.K, MN = d.m1 * d.m2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int per_wave = IC * d.m1 + IC * (PK + 1) + d.m1 * PK;
   float* us = sm;
   float* as = sm + MN * PK + wave * per_wave;   // [IC][m1]
@@ -216,7 +245,7 @@ __global__ __launch_bounds__(256) void mix_kernel(Dims d, const float* __restric
                                                   const float* __restrict__ g, const float* __restrict__ go,
                                                   float* __restrict__ out, int acc) {
   __shared__ float rs[128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int K = d.K, P = d.P, I = d.I, O = d.O;
   const int64_t R = d.B * K;
@@ -252,30 +281,48 @@ __global__ __launch_bounds__(256) void mix_kernel(Dims d, const float* __restric
     bool cv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) cv[j] = o0 + 16 * j + r < O;
+    // K steps (path p, channels i0 .. i0 + 15) in order; the operands of the next step are requested before
+    // the products of the current one (two register sets, no copies).  Loads are unconditional at clamped
+    // addresses and nothing reads them before the products: rows and columns past the end accumulate values
+    // that are never stored, and the channel tail (I % 16) is cut by a zero scale on the A rows, applied with
+    // the gate when the step is multiplied.
     const int pb = TG ? p_only : 0, pe = TG ? p_only + 1 : P;
-    for (int p = pb; p < pe; ++p) {
-      float gt[2];
-      const float* yr[2];
+    const int nis = (I + 15) / 16, nst = (pe - pb) * nis;
+    int oc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) oc[j] = cv[j] ? o0 + 16 * j + r : 0;
+    auto load = [&](int st, f4 (&av)[2], float (&gs)[2], f4 (&bw)[8]) {
+      const int p = pb + st / nis, ii = (st % nis) * 16 + 4 * q;
+      const bool iv = ii < I;   // I % 4 == 0: the whole float4 is in range
+      const int ic = iv ? ii : 0;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        gt[t] = (!rv[t]) ? 0.f : (TG ? 1.f : g[rb[t] * P + p]);
-        yr[t] = y + ((rb[t] * P + p) * K + rk[t]) * I;
+        gs[t] = TG ? 1.f : g[rb[t] * P + p];
+        if (!iv) gs[t] = 0.f;
+        av[t] = ld4(y + ((rb[t] * P + p) * K + rk[t]) * I + ic);
       }
-      const float* wr[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) wr[j] = W + ((int64_t)p * O + (cv[j] ? o0 + 16 * j + r : 0)) * I;
-      for (int i0 = 0; i0 < I; i0 += 16) {
-        const int ii = i0 + 4 * q;
-        const bool iv = ii < I;   // I % 4 == 0: the whole float4 is in range
-        f4 av[2], bw[8];
+      for (int j = 0; j < 8; ++j) bw[j] = ld4(W + ((int64_t)p * O + oc[j]) * I + ic);
+    };
+    auto mma = [&](const f4 (&av)[2], const float (&gs)[2], const f4 (&bw)[8]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) av[t] = iv ? ld4(yr[t] + ii) * gt[t] : f4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < 2; ++t) {
+        const f4 a = av[t] * gs[t];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bw[j] = (iv && cv[j]) ? ld4(wr[j] + ii) : f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) accm[t][j] = mfma_k16(av[t], bw[j], accm[t][j]);
+        for (int j = 0; j < 8; ++j) accm[t][j] = mfma_k16(a, bw[j], accm[t][j]);
+      }
+    };
+    f4 a0[2], b0[8], a1[2], b1[8];
+    float g0[2], g1[2];
+    if (nst > 0) load(0, a0, g0, b0);
+    for (int st = 0; st < nst; st += 2) {
+      if (st + 1 < nst) load(st + 1, a1, g1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(a0, g0, b0);
+      if (st + 1 < nst) {
+        if (st + 2 < nst) load(st + 2, a0, g0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, g1, b1);
       }
     }
 #pragma unroll
@@ -333,7 +380,7 @@ __global__ void transpose_w_kernel(int P, int O, int I, const float* __restrict_
 // (path, 128-column block).  B from the transposed weights Wt[p][i][o] (float4 along o).
 __global__ __launch_bounds__(256) void mix_ty_kernel(Dims d, const float* __restrict__ go, const float* __restrict__ Wt,
                                                      const float* __restrict__ g, float* __restrict__ gy, int acc) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int K = d.K, P = d.P, I = d.I, O = d.O;
   const int64_t R = d.B * K;
@@ -401,7 +448,7 @@ __global__ __launch_bounds__(256) void mix_ty_kernel(Dims d, const float* __rest
 __global__ __launch_bounds__(256) void mix_tw_kernel(Dims d, const float* __restrict__ go, const float* __restrict__ y,
                                                      const float* __restrict__ g, int64_t rows_per_split,
                                                      float* __restrict__ part) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int K = d.K, P = d.P, I = d.I, O = d.O;
   const int64_t R = d.B * K;
@@ -499,8 +546,11 @@ extern "C" int fsc_bucket_project(int64_t B, int32_t I, int32_t m1, int32_t m2, 
   const Dims d{B, I, m1, m2, P, K, 0};
   if (bucket::check_dims(d, true)) return 1;
   if (B == 0) return 0;
-  const size_t lds = (size_t)(m1 * m2 * P * K + 4 * m1 * P * K) * 4;
-  bucket::project_kernel<false><<<bucket::batch_grid(B), 256, lds, st>>>(d, a, v, u, y, accumulate);
+  const size_t lds = (size_t)(m1 * m2 * P * K + 4 * bucket::MAXM * P * K) * 4;
+  if (accumulate)
+    bucket::project_kernel<false, true><<<bucket::batch_grid(B), 256, lds, st>>>(d, a, v, u, y);
+  else
+    bucket::project_kernel<false, false><<<bucket::batch_grid(B), 256, lds, st>>>(d, a, v, u, y);
   return check_launch("bucket project") ? 2 : 0;
 }
 
@@ -510,8 +560,11 @@ extern "C" int fsc_bucket_project_transpose_a(int64_t B, int32_t I, int32_t m1, 
   const Dims d{B, I, m1, m2, P, K, 0};
   if (bucket::check_dims(d, true)) return 1;
   if (B == 0) return 0;
-  const size_t lds = (size_t)(m1 * m2 * P * K + 4 * m1 * P * K) * 4;
-  bucket::project_kernel<true><<<bucket::batch_grid(B), 256, lds, st>>>(d, grad_y, v, u, grad_a, accumulate);
+  const size_t lds = (size_t)(m1 * m2 * P * K + 4 * bucket::MAXM * P * K) * 4;
+  if (accumulate)
+    bucket::project_kernel<true, true><<<bucket::batch_grid(B), 256, lds, st>>>(d, grad_y, v, u, grad_a);
+  else
+    bucket::project_kernel<true, false><<<bucket::batch_grid(B), 256, lds, st>>>(d, grad_y, v, u, grad_a);
   return check_launch("bucket project_transpose_a") ? 2 : 0;
 }
 
