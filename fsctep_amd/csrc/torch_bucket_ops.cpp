@@ -126,7 +126,7 @@ Tensor mix_ws(const Mix& s, const Tensor& like) {
 
 void myt(const Mix& s, const Tensor& go, const Tensor& w, const Tensor& g, Tensor& gy, int acc) {
   const Tensor oc = go.contiguous(), wc = w.contiguous(), gc = g.contiguous();
-  Tensor ws = mix_ws(s, go);
+  Tensor ws = at::empty({std::max<int64_t>(s.P * s.O * s.I, 1)}, go.options());   // the transposed weights
   check(fsc_bucket_mix_transpose_y(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp(oc), cp(wc), cp(gc),
                                    mp(gy), acc, mp(ws), stream_of(gy)),
         "mix_bucket_transpose_y");

@@ -362,7 +362,8 @@ int fsc_bucket_project_transpose_vu(int64_t B, int32_t I, int32_t m1, int32_t m2
 /* mix_bucket_forward (csrc/ictd_tp.cpp:271-294): out from y, w, gates. */
 int fsc_bucket_mix(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* y, const float* w,
                    const float* gates, float* out, int32_t accumulate, hipStream_t stream);
-/* Floats of the workspace of fsc_bucket_mix_transpose_y and _w. */
+/* Floats of the workspace of fsc_bucket_mix_transpose_w (per-split partial sums; fsc_bucket_mix_transpose_y
+ * needs only P*O*I floats, the transposed weights). */
 int fsc_bucket_mix_workspace(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, int64_t* workspace_floats);
 /* mix_bucket_transpose_y (csrc/ictd_tp.cpp:296-322): grad_y [B][P][K][I] from grad_out, w, gates. */
 int fsc_bucket_mix_transpose_y(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
