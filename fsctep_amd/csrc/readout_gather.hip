@@ -179,6 +179,128 @@ __global__ __launch_bounds__(256) void scatter_node_kernel(FscReadoutTable T, in
   }
 }
 
+// Vectorised per-node forms (C a multiple of 4, 16-byte aligned arrays): a thread owns NQ quads of four
+// consecutive entries of a node, and its map indices and offsets, the same for every node, stay in registers
+// while the block walks its nodes.  The next node's row is requested before the current node's outputs are
+// stored, so each node costs one round trip to memory instead of one per output.
+template <int NQ>
+__global__ __launch_bounds__(256) void gather_node4_kernel(FscReadoutTable T, int64_t N, LayerPtrs X,
+                                                           const int32_t* __restrict__ srcmap,
+                                                           float* __restrict__ t_all, float* __restrict__ sq) {
+  extern __shared__ __align__(16) float xs[];
+  const int C = T.C, MC = T.M * C, nC = T.n_layers * C, P = T.n_layers * MC, P4 = P / 4;
+  const int K = T.n_keys, S4 = K * nC / 4;
+  // phase 1 (a node's layers, (l, m, c) order) and phase 2 (key-major columns) share the quad index g
+  int xl[NQ], xo[NQ], ko[NQ], kl[NQ];
+  int64_t kb[NQ];
+  int4 si[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int g = min((int)threadIdx.x + 256 * u, P4 - 1);   // threads past P4 repeat the last quad (not stored)
+    const int e = 4 * g;
+    xl[u] = e / MC;
+    xo[u] = e - xl[u] * MC;
+    int col0;
+    const int k = key_of_column(T, nC, e, col0);
+    kb[u] = N * (int64_t)col0;
+    kl[u] = T.key_dim[k] * nC;
+    ko[u] = e - col0;
+    const int4 m4 = *reinterpret_cast<const int4*>(srcmap + e);
+    si[u] = int4{min(max(m4.x, 0), P - 1), min(max(m4.y, 0), P - 1), min(max(m4.z, 0), P - 1),
+                 min(max(m4.w, 0), P - 1)};
+  }
+  f4 pre[NQ];
+  auto load_row = [&](int64_t n) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) pre[u] = ld4(X.p[xl[u]] + n * MC + xo[u]);
+  };
+  int64_t n = blockIdx.x;
+  if (n < N) load_row(n);
+  for (; n < N; n += gridDim.x) {
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+      if ((int)threadIdx.x + 256 * u < P4) *reinterpret_cast<f4*>(xs + 4 * ((int)threadIdx.x + 256 * u)) = pre[u];
+    __syncthreads();
+    if (n + gridDim.x < N) load_row(n + gridDim.x);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      if ((int)threadIdx.x + 256 * u >= P4) continue;
+      const f4 v = {xs[si[u].x], xs[si[u].y], xs[si[u].z], xs[si[u].w]};
+      st4(t_all + kb[u] + n * (int64_t)kl[u] + ko[u], v);
+    }
+    for (int g = threadIdx.x; g < S4; g += 256) {   // squared norms, four channels per thread
+      const int k = (4 * g) / nC, lc = 4 * g - k * nC, l = lc / C, c = lc - l * C;
+      const float* x = xs + l * MC + T.key_comp0[k] * C + c;
+      f4 s2 = {0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < T.key_dim[k]; ++m) {
+        const f4 v = *reinterpret_cast<const f4*>(x + m * C);
+        s2 += v * v;
+      }
+      st4(sq + (n * K + k) * (int64_t)nC + lc, s2);
+    }
+  }
+}
+
+template <int NQ>
+__global__ __launch_bounds__(256) void scatter_node4_kernel(FscReadoutTable T, int64_t N, KeyPtrs dt,
+                                                            const float* __restrict__ dsq, LayerPtrs X,
+                                                            const int32_t* __restrict__ gmap, OutPtrs dX) {
+  extern __shared__ __align__(16) float ds[];
+  const int C = T.C, MC = T.M * C, nC = T.n_layers * C, P = T.n_layers * MC, P4 = P / 4;
+  const int K = T.n_keys;
+  // phase 1 (key-major dt columns) and phase 2 ((l, m, c) entries) share the quad index g
+  int kd[NQ], ko[NQ], kl[NQ], xl[NQ], xo[NQ], qo[NQ];
+  int4 gi[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int g = min((int)threadIdx.x + 256 * u, P4 - 1);   // threads past P4 repeat the last quad (not stored)
+    const int e = 4 * g;
+    int col0;
+    kd[u] = key_of_column(T, nC, e, col0);
+    kl[u] = T.key_dim[kd[u]] * nC;
+    ko[u] = e - col0;
+    xl[u] = e / MC;
+    xo[u] = e - xl[u] * MC;
+    const int m = xo[u] / C, c = xo[u] - m * C;
+    qo[u] = key_of(T, m) * nC + xl[u] * C + c;
+    const int4 m4 = *reinterpret_cast<const int4*>(gmap + e);
+    gi[u] = int4{min(max(m4.x, 0), P - 1), min(max(m4.y, 0), P - 1), min(max(m4.z, 0), P - 1),
+                 min(max(m4.w, 0), P - 1)};
+  }
+  f4 pre[NQ];
+  auto load_dt = [&](int64_t n) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const float* d = dt.p[kd[u]];
+      pre[u] = d ? ld4(d + n * (int64_t)kl[u] + ko[u]) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  int64_t n = blockIdx.x;
+  if (n < N) load_dt(n);
+  for (; n < N; n += gridDim.x) {
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+      if ((int)threadIdx.x + 256 * u < P4) *reinterpret_cast<f4*>(ds + 4 * ((int)threadIdx.x + 256 * u)) = pre[u];
+    __syncthreads();
+    f4 xv[NQ], qv[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      xv[u] = ld4(X.p[xl[u]] + n * MC + xo[u]);
+      qv[u] = dsq ? ld4(dsq + n * K * (int64_t)nC + qo[u]) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (n + gridDim.x < N) load_dt(n + gridDim.x);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      if ((int)threadIdx.x + 256 * u >= P4) continue;
+      f4 v = {ds[gi[u].x], ds[gi[u].y], ds[gi[u].z], ds[gi[u].w]};
+      v += 2.f * xv[u] * qv[u];
+      st4(dX.p[xl[u]] + n * MC + xo[u], v);
+    }
+  }
+}
+
 int check_table(const FscReadoutTable* T, const char* who) {
   if (!T) {
     set_error(std::string(who) + ": null table");
@@ -206,6 +328,10 @@ int check_table(const FscReadoutTable* T, const char* who) {
 
 unsigned grid_for(int64_t total) { return (unsigned)std::min<int64_t>((total + 255) / 256, 8192); }
 
+// blocks of the vectorised per-node kernels (each walks about N / NODE_GRID nodes)
+constexpr int64_t NODE_GRID = 2048;
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace readout
 }  // namespace fsc
 
@@ -226,6 +352,26 @@ int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const floa
     X.p[l] = layers[l];
   }
   const int64_t P = (int64_t)table->n_layers * table->M * table->C;
+  const int nq = (int)((P / 4 + 255) / 256);
+  bool aligned = aligned16(srcmap) && aligned16(t_all) && aligned16(sq);
+  for (int l = 0; l < table->n_layers; ++l) aligned = aligned && aligned16(X.p[l]);
+  if (table->C % 4 == 0 && P <= ROW_LDS && nq <= 8 && aligned) {
+    const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, NODE_GRID);
+    const size_t lds = P * sizeof(float);
+#define FSC_G4(Q) gather_node4_kernel<Q><<<grid, 256, lds, stream>>>(*table, n_nodes, X, srcmap, t_all, sq)
+    switch (nq) {
+      case 1: FSC_G4(1); break;
+      case 2: FSC_G4(2); break;
+      case 3: FSC_G4(3); break;
+      case 4: FSC_G4(4); break;
+      case 5: FSC_G4(5); break;
+      case 6: FSC_G4(6); break;
+      case 7: FSC_G4(7); break;
+      default: FSC_G4(8); break;
+    }
+#undef FSC_G4
+    return check_launch("readout gather") ? 2 : 0;
+  }
   if (P <= ROW_LDS) {
     const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, 65536);
     gather_node_kernel<<<grid, 256, P * sizeof(float), stream>>>(*table, n_nodes, X, srcmap, t_all, sq);
@@ -255,6 +401,27 @@ int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const flo
     dX.p[l] = grad_layers[l];
   }
   const int64_t P = (int64_t)table->n_layers * table->M * table->C;
+  const int nq = (int)((P / 4 + 255) / 256);
+  bool aligned = aligned16(gmap) && aligned16(grad_sq);
+  for (int k = 0; k < table->n_keys; ++k) aligned = aligned && aligned16(dt.p[k]);
+  for (int l = 0; l < table->n_layers; ++l) aligned = aligned && aligned16(X.p[l]) && aligned16(dX.p[l]);
+  if (table->C % 4 == 0 && P <= ROW_LDS && nq <= 8 && aligned) {
+    const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, NODE_GRID);
+    const size_t lds = P * sizeof(float);
+#define FSC_S4(Q) scatter_node4_kernel<Q><<<grid, 256, lds, stream>>>(*table, n_nodes, dt, grad_sq, X, gmap, dX)
+    switch (nq) {
+      case 1: FSC_S4(1); break;
+      case 2: FSC_S4(2); break;
+      case 3: FSC_S4(3); break;
+      case 4: FSC_S4(4); break;
+      case 5: FSC_S4(5); break;
+      case 6: FSC_S4(6); break;
+      case 7: FSC_S4(7); break;
+      default: FSC_S4(8); break;
+    }
+#undef FSC_S4
+    return check_launch("readout scatter") ? 2 : 0;
+  }
   if (P <= ROW_LDS) {
     const unsigned grid = (unsigned)std::min<int64_t>(n_nodes, 65536);
     scatter_node_kernel<<<grid, 256, P * sizeof(float), stream>>>(*table, n_nodes, dt, grad_sq, X, gmap, dX);
