@@ -32,19 +32,25 @@ constexpr int EB = 16;    // edges per chunk: one 16-deep K block of the project
 // LDS carve-ups are in 4-byte words, regions 16-byte aligned.
 __host__ __device__ inline int up4(int v) { return (v + 3) & ~3; }
 
-// V consecutive floats (V = 2, 4 or 8) as an MFMA-operand bundle.
+// V floats (V = 2, 4 or 8) of one lane as an MFMA-operand bundle.
 template <int V>
 struct VecF {
   float v[V];
 };
 
+// Quad-interleaved bundle of V channels for lane r of a 16-lane row: quad h holds channels 64h + 4r ..
+// 64h + 4r + 3 (V >= 4), so each of the V/4 vector loads of a 16-lane row reads 256 contiguous bytes; V = 2:
+// channels 2r, 2r + 1.  p points at the row's channel lane_chan<V>(r).
 template <int V>
-__device__ __forceinline__ VecF<V> ldv(const float* p) {
+__device__ __forceinline__ int lane_chan(int r) { return V >= 4 ? 4 * r : V * r; }
+
+template <int V>
+__device__ __forceinline__ VecF<V> ldq(const float* p) {
   VecF<V> r;
   if constexpr (V >= 4) {
 #pragma unroll
     for (int h = 0; h < V / 4; ++h) {
-      const f4 t = reinterpret_cast<const f4*>(p)[h];
+      const f4 t = *reinterpret_cast<const f4*>(p + 64 * h);
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.v[4 * h + j] = t[j];
     }
@@ -57,11 +63,11 @@ __device__ __forceinline__ VecF<V> ldv(const float* p) {
 }
 
 template <int V>
-__device__ __forceinline__ void stv(float* p, const VecF<V>& r) {
+__device__ __forceinline__ void stq(float* p, const VecF<V>& r) {
   if constexpr (V >= 4) {
 #pragma unroll
     for (int h = 0; h < V / 4; ++h)
-      reinterpret_cast<f4*>(p)[h] = f4{r.v[4 * h], r.v[4 * h + 1], r.v[4 * h + 2], r.v[4 * h + 3]};
+      *reinterpret_cast<f4*>(p + 64 * h) = f4{r.v[4 * h], r.v[4 * h + 1], r.v[4 * h + 2], r.v[4 * h + 3]};
   } else {
     *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
   }
@@ -101,8 +107,8 @@ __device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int* __
 // once per block in LDS (one float4 per lane per (tile, m1) slot).
 // A wave takes at most two of the KTT <= 8 kk tiles, each over all C channels (64-channel spans at
 // 4 waves/SIMD measured slower at C 128: the coupling product is then formed once per span): column
-// tile j holds channels V*r + j (V = C/16), so each lane gathers V consecutive channels of x with vector
-// loads and stores V consecutive channels of Z.  3 waves/SIMD at C 128, 4 below.
+// tile j holds channel 64(j/4) + 4r + j%4 (V = C/16 >= 4; 2r + j for V = 2), so each lane gathers its V
+// channels of x as quads whose 16-lane rows are contiguous 256-byte runs, and stores Z the same way.  3 waves/SIMD at C 128, 4 below.
 struct FwdSmem {
   int cgs, kd, gidx, slot0, wtask, cf, total;
 };
@@ -233,7 +239,7 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
     const int d1 = L.g_d1[g], o1 = L.g_o1[g];
     const int gc = gidx[kt * 16 + r];
     const f4* cft = cf + slot0[kt] * 64 + lane;
-    const float* xcol = x + o1 * C + V * r;
+    const float* xcol = x + o1 * C + lane_chan<V>(r);
     f4 acc[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
       }
       auto load_k = [&](int m1, VecF<V> (&b)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) b[u] = ldv<V>(xcol + ((int64_t)src4[u] * L.M + m1) * C);
+        for (int u = 0; u < 4; ++u) b[u] = ldq<V>(xcol + ((int64_t)src4[u] * L.M + m1) * C);
       };
       // gated coupling rows of component m1: a[u] = BG[edge 4q+u][kk row r]
       auto coupling = [&](int m1, float (&a)[4]) {
@@ -341,7 +347,7 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
         o.v[j] = acc[j][i] * scale;
         zmax = fmaxf(zmax, fabsf(o.v[j]));
       }
-      stv<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + V * r, o);
+      stq<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + lane_chan<V>(r), o);
     }
   }
   // per-node power of two for the split-fp16 channel mix (zmx alternates between the block's nodes, so
