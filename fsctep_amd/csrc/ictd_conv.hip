@@ -864,12 +864,19 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(Fsc
 // of the table from L2 for every edge).  Species ids index the model's species table (NS <= 16 rows);
 // only the source species present among the node's in-edges are read.
 
+// ssp[pair] = the source species of species pair (s, t) = s * NS + t, for all 256 pair ids a block may
+// look up (NS <= 16).  Filled by a 256-thread block before its first barrier.
+__device__ __forceinline__ void fill_pair_species(int NS, int* __restrict__ ssp) {
+  ssp[threadIdx.x] = min((int)threadIdx.x / NS, 15);   // ids >= NS * NS are not pairs; kept in bounds
+}
+
 // Bit s set if some edge in [beg, end) has source species s (wave 0 computes it; every wave reads it).
-__device__ __forceinline__ unsigned src_species_mask(const int32_t* __restrict__ edge_pair, int NS, int beg, int end,
-                                                     unsigned* lds) {
+// Ends with a barrier, after which ssp (filled before the call) is visible to the block.
+__device__ __forceinline__ unsigned src_species_mask(const int32_t* __restrict__ edge_pair, const int* __restrict__ ssp,
+                                                     int NS, int beg, int end, unsigned* lds) {
   if (threadIdx.x < 64) {
     unsigned m = 0;
-    for (int e = beg + (int)threadIdx.x; e < end; e += 64) m |= 1u << (edge_pair[e] / NS);
+    for (int e = beg + (int)threadIdx.x; e < end; e += 64) m |= 1u << min((edge_pair[e] & 255) / NS, 15);
     for (int off = 32; off > 0; off >>= 1) m |= (unsigned)__shfl_xor((int)m, off, 64);
     if (threadIdx.x == 0) *lds = m;
   }
@@ -886,11 +893,13 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ qtab, float* __restrict__ out) {
   __shared__ float w[16][NY];
   __shared__ int ycomp[16];
+  __shared__ int ssp[256];
   __shared__ unsigned smask;
   const int n = blockIdx.x, t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const int sn = node_species[n];
-  const unsigned mask = src_species_mask(edge_pair, NS, beg, end, &smask);
+  fill_pair_species(NS, ssp);
+  const unsigned mask = src_species_mask(edge_pair, ssp, NS, beg, end, &smask);
   if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none)
     int yy = -1;
 #pragma unroll
@@ -906,7 +915,7 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
 #pragma unroll 4
       for (int e = beg; e < end; ++e) {
         const float v = gates[(int64_t)e * L.NREF + gi] * F[(int64_t)e * NY + y];
-        a += (edge_pair[e] / NS == s) ? v : 0.f;
+        a += (ssp[edge_pair[e] & 255] == s) ? v : 0.f;
       }
     }
     w[s][y] = a;
@@ -937,50 +946,69 @@ __global__ __launch_bounds__(256) void conv1_bwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ gates,
                                                         const float* __restrict__ qtab,
                                                         float* __restrict__ dF, float* __restrict__ dgates) {
-  __shared__ float gsh[NY][C];
+  __shared__ __align__(16) float gsh[NY][C + 4];   // rows padded: the T threads read 16 rows at once
   __shared__ float T[16][NY];
+  __shared__ int ssp[256];
   __shared__ unsigned smask;
   const int n = blockIdx.x;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   if (beg == end) return;                      // uniform over the block
   const float scale = 1.f / (float)(end - beg);
   const int sn = node_species[n];
-  const unsigned mask = src_species_mask(edge_pair, NS, beg, end, &smask);
+  fill_pair_species(NS, ssp);
   for (int i = t; i < NY * C; i += blockDim.x) {
     const int y = i / C, o = i - y * C;
     gsh[y][o] = (L.y_path1[y] >= 0) ? G[((int64_t)n * L.M + L.y_oo1[y]) * C + o] : 0.f;
   }
-  __syncthreads();
-  // T[s][y] = (1/deg) sum_o G[n][comp(y)][o] Q[(s, sn)][p(y)][o]: one wave per (s, y), lanes over o
-  for (int j = wave; j < NS * NY; j += 4) {
+  const unsigned mask = src_species_mask(edge_pair, ssp, NS, beg, end, &smask);   // its barrier publishes gsh
+  // T[s][y] = (1/deg) sum_o G[n][comp(y)][o] Q[(s, sn)][p(y)][o]: threads (j = (s, y), h) sum the half
+  // h of o as float4 runs; a lane exchange adds the two halves.  Rows of absent source species are 0.
+  constexpr int HC = C / 2;
+  const bool qal = (reinterpret_cast<uintptr_t>(qtab) & 15) == 0;
+  for (int j0 = 0; j0 < NS * NY; j0 += 128) {
+    const int j = j0 + (t >> 1), h = t & 1;
     const int s = j / NY, y = j - s * NY;
-    if (!((mask >> s) & 1u)) continue;         // no in-edge reads T[s]
-    const int p = L.y_path1[y];
+    const int p = j < NS * NY ? L.y_path1[y] : -1;
     float part = 0.f;
-    if (p >= 0) {
-      const float* qp = qtab + (((int64_t)s * NS + sn) * L.NP1 + p) * C;
-      for (int o = lane; o < C; o += 64) part += gsh[y][o] * qp[o];
+    if (p >= 0 && ((mask >> s) & 1u)) {
+      const float* qp = qtab + (((int64_t)s * NS + sn) * L.NP1 + p) * C + h * HC;
+      const f4* gp = reinterpret_cast<const f4*>(&gsh[y][h * HC]);
+      if (qal) {
+#pragma unroll 4
+        for (int k = 0; k < HC / 4; ++k) {
+          const f4 a = reinterpret_cast<const f4*>(qp)[k], g = gp[k];
+          part += a[0] * g[0] + a[1] * g[1] + a[2] * g[2] + a[3] * g[3];
+        }
+      } else {
+        for (int k = 0; k < HC / 4; ++k) {
+          const f4 g = gp[k];
+          part += qp[4 * k] * g[0] + qp[4 * k + 1] * g[1] + qp[4 * k + 2] * g[2] + qp[4 * k + 3] * g[3];
+        }
+      }
     }
-    part = wave_sum(part);
-    if (lane == 0) T[s][y] = part * scale;
+    part += __shfl_xor(part, 1, 64);
+    if (h == 0 && j < NS * NY) T[s][y] = part * scale;
   }
   __syncthreads();
-// per edge: dF[e][y] = gate_p(y) T[s_src][y];  dgate[e][p] = sum_{y in p} T[s_src][y] F[e][y]
+  // per edge: dF[e][y] = gate_p(y) T[s_src][y];  dgate[e][p] = sum_{y in p} T[s_src][y] F[e][y]
   const int ne = end - beg;
   for (int idx = t; idx < ne * NY; idx += blockDim.x) {
     const int e = beg + idx / NY, y = idx % NY;
     const int p = L.y_path1[y];
-    const int ss = edge_pair[e] / NS;
+    const int ss = ssp[edge_pair[e] & 255];
     dF[(int64_t)e * NY + y] = (p >= 0) ? gates[(int64_t)e * L.NREF + L.c1_gate[p]] * T[ss][y] : 0.f;
   }
-  for (int idx = t; idx < ne * L.NP1; idx += blockDim.x) {
-    const int e = beg + idx / L.NP1, p = idx % L.NP1;
-    const int ss = edge_pair[e] / NS;
-    float acc = 0.f;
-    for (int y = 0; y < NY; ++y)
-      if (L.y_path1[y] == p) acc += T[ss][y] * F[(int64_t)e * NY + y];
-    dgates[(int64_t)e * L.NREF + L.c1_gate[p]] = acc;
+  for (int p = 0; p < L.NP1; ++p) {
+    const int gi = L.c1_gate[p];
+    for (int e = beg + t; e < end; e += blockDim.x) {
+      const int ss = ssp[edge_pair[e] & 255];
+      float acc = 0.f;
+#pragma unroll
+      for (int y = 0; y < NY; ++y)
+        if (L.y_path1[y] == p) acc += T[ss][y] * F[(int64_t)e * NY + y];
+      dgates[(int64_t)e * L.NREF + gi] = acc;
+    }
   }
 }
 
