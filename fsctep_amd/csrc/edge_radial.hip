@@ -413,16 +413,13 @@ __global__ void vec_geometry_backward_kernel(const float* __restrict__ gn, const
 // ---------------------------------------------------------------- direction harmonics (ICTD)
 // Y[e][l^2 + m] = sum_{k of degree l} M[k][m] n_x^a n_y^b n_z^c (M = multinomial * G_l B_l, the
 // ICTD harmonic basis); backward dn = sum_k (sum_m dY[l^2+m] M[k][m]) grad(n^abc).  One thread
-// per edge; the table travels as a kernel argument.
-__device__ __forceinline__ float ipow(const float (&p)[4], int e) {
-  return e == 0 ? p[0] : (e == 1 ? p[1] : (e == 2 ? p[2] : p[3]));
-}
+// per edge, 256 edges per block; the table travels as a kernel argument.  The block's rows of Y (dY)
+// are one contiguous run of 256 (lmax+1)^2 floats, moved between HBM and LDS by all threads in order
+// (coalesced) and read or written per edge from LDS (rows padded to 17 floats).
+constexpr int HARM_ROW = 17;
 
-__global__ void harmonics_forward_kernel(FscHarmTable tab, int64_t n_edges, const float* __restrict__ nvec,
-                                         float* __restrict__ Y) {
-  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (e >= n_edges) return;
-  float px[4], py[4], pz[4];
+__device__ __forceinline__ void harm_powers(const float* __restrict__ nvec, int64_t e, float (&px)[4], float (&py)[4],
+                                            float (&pz)[4]) {
   px[0] = py[0] = pz[0] = 1.f;
   const float x = nvec[3 * e], y = nvec[3 * e + 1], z = nvec[3 * e + 2];
 #pragma unroll
@@ -431,54 +428,108 @@ __global__ void harmonics_forward_kernel(FscHarmTable tab, int64_t n_edges, cons
     py[i] = py[i - 1] * y;
     pz[i] = pz[i - 1] * z;
   }
-  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
-  float out[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) out[i] = 0.f;
-  for (int k = 0; k < tab.nmono; ++k) {
-    const int l = tab.mono_l[k];
-    const float m = ipow(px, tab.mono_exp[k][0]) * ipow(py, tab.mono_exp[k][1]) * ipow(pz, tab.mono_exp[k][2]);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int jj = j - l * l;
-      if (jj >= 0 && jj < 2 * l + 1) out[j] += m * tab.coef[k][jj];
-    }
-  }
-  for (int j = 0; j < ny; ++j) Y[e * ny + j] = out[j];
 }
 
-__global__ void harmonics_backward_kernel(FscHarmTable tab, int64_t n_edges, const float* __restrict__ nvec,
-                                          const float* __restrict__ dY, float* __restrict__ dn) {
-  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (e >= n_edges) return;
-  float px[4], py[4], pz[4];
-  px[0] = py[0] = pz[0] = 1.f;
-  const float x = nvec[3 * e], y = nvec[3 * e + 1], z = nvec[3 * e + 2];
-#pragma unroll
-  for (int i = 1; i < 4; ++i) {
-    px[i] = px[i - 1] * x;
-    py[i] = py[i - 1] * y;
-    pz[i] = pz[i - 1] * z;
-  }
-  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
-  float g[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) g[j] = (j < ny) ? dY[e * ny + j] : 0.f;
-  float d[3] = {0.f, 0.f, 0.f};
-  for (int k = 0; k < tab.nmono; ++k) {
-    const int l = tab.mono_l[k];
-    float dm = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int jj = j - l * l;
-      if (jj >= 0 && jj < 2 * l + 1) dm += g[j] * tab.coef[k][jj];
-    }
+// Monomials n_x^a n_y^b n_z^c of degree l = a + b + c <= 3 in a fixed order: by l, then r = b + c, then c.
+__device__ __forceinline__ int harm_canon(int a, int b, int c) {
+  const int l = a + b + c, r = b + c;
+  return l * (l + 1) * (l + 2) / 6 + r * (r + 1) / 2 + c;
+}
+
+// The table as a dense [20 monomials (fixed order)][16 outputs] matrix in LDS, zero where a monomial is
+// absent or its degree is not the output's l, so that the per-edge loops are straight-line code with
+// the exponents known at compile time.  Ends with a barrier.
+__device__ __forceinline__ void stage_harm_matrix(const FscHarmTable& tab, f4 (&Mt)[20][4]) {
+  float* m = reinterpret_cast<float*>(Mt);
+  for (int i = threadIdx.x; i < 20 * 16; i += blockDim.x) m[i] = 0.f;
+  __syncthreads();
+  for (int i = threadIdx.x; i < tab.nmono * 16; i += blockDim.x) {
+    const int k = i >> 4, j = i & 15;
     const int a = tab.mono_exp[k][0], b = tab.mono_exp[k][1], c = tab.mono_exp[k][2];
-    const float fx = ipow(px, a), fy = ipow(py, b), fz = ipow(pz, c);
-    if (a) d[0] += dm * (float)a * ipow(px, a - 1) * fy * fz;
-    if (b) d[1] += dm * (float)b * fx * ipow(py, b - 1) * fz;
-    if (c) d[2] += dm * (float)c * fx * fy * ipow(pz, c - 1);
+    const int l = tab.mono_l[k], jj = j - l * l;
+    if (a >= 0 && b >= 0 && c >= 0 && a + b + c == l && l <= 3 && jj >= 0 && jj < 2 * l + 1)
+      m[harm_canon(a, b, c) * 16 + j] = tab.coef[k][jj];
   }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void harmonics_forward_kernel(FscHarmTable tab, int64_t n_edges,
+                                                                const float* __restrict__ nvec,
+                                                                float* __restrict__ Y) {
+  __shared__ float rows[256 * HARM_ROW];
+  __shared__ f4 Mt[20][4];
+  const int64_t e0 = (int64_t)blockIdx.x * 256;
+  const int64_t e = e0 + threadIdx.x;
+  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
+  const int nb = (int)min((int64_t)256, n_edges - e0);   // edges of this block (uniform)
+  stage_harm_matrix(tab, Mt);
+  if (e < n_edges) {
+    float px[4], py[4], pz[4];
+    harm_powers(nvec, e, px, py, pz);
+    f4 out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = f4{0.f, 0.f, 0.f, 0.f};
+    int ck = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+      for (int r = 0; r <= l; ++r)
+#pragma unroll
+        for (int c = 0; c <= r; ++c, ++ck) {
+          const float m = px[l - r] * py[r - c] * pz[c];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[i] += m * Mt[ck][i];
+        }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rows[threadIdx.x * HARM_ROW + j] = out[j >> 2][j & 3];
+  }
+  __syncthreads();
+  float* yb = Y + e0 * ny;
+  for (int i = threadIdx.x; i < nb * ny; i += 256) {
+    const int r = i / ny;
+    yb[i] = rows[r * HARM_ROW + (i - r * ny)];
+  }
+}
+
+__global__ __launch_bounds__(256) void harmonics_backward_kernel(FscHarmTable tab, int64_t n_edges,
+                                                                 const float* __restrict__ nvec,
+                                                                 const float* __restrict__ dY,
+                                                                 float* __restrict__ dn) {
+  __shared__ float rows[256 * HARM_ROW];
+  __shared__ f4 Mt[20][4];
+  const int64_t e0 = (int64_t)blockIdx.x * 256;
+  const int64_t e = e0 + threadIdx.x;
+  const int ny = (tab.lmax + 1) * (tab.lmax + 1);
+  const int nb = (int)min((int64_t)256, n_edges - e0);
+  const float* gb = dY + e0 * ny;
+  for (int i = threadIdx.x; i < nb * ny; i += 256) {
+    const int r = i / ny;
+    rows[r * HARM_ROW + (i - r * ny)] = gb[i];
+  }
+  stage_harm_matrix(tab, Mt);   // its barriers also publish rows
+  if (e >= n_edges) return;
+  float px[4], py[4], pz[4];
+  harm_powers(nvec, e, px, py, pz);
+  f4 g[4];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) g[j >> 2][j & 3] = (j < ny) ? rows[threadIdx.x * HARM_ROW + j] : 0.f;
+  float d[3] = {0.f, 0.f, 0.f};
+  int ck = 0;
+#pragma unroll
+  for (int l = 0; l < 4; ++l)
+#pragma unroll
+    for (int r = 0; r <= l; ++r)
+#pragma unroll
+      for (int c = 0; c <= r; ++c, ++ck) {
+        const int a = l - r, b = r - c;
+        f4 t = g[0] * Mt[ck][0];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) t += g[i] * Mt[ck][i];
+        const float dm = (t[0] + t[1]) + (t[2] + t[3]);
+        if (a) d[0] += dm * (float)a * px[a - 1] * py[b] * pz[c];
+        if (b) d[1] += dm * (float)b * px[a] * py[b - 1] * pz[c];
+        if (c) d[2] += dm * (float)c * px[a] * py[b] * pz[c - 1];
+      }
 #pragma unroll
   for (int i = 0; i < 3; ++i) dn[3 * e + i] = d[i];
 }
