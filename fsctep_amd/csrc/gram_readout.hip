@@ -162,13 +162,30 @@ __global__ __launch_bounds__(256) void node_scale_kernel(int64_t N, int D, int n
   if (n >= N) return;   // uniform over the wave
   const float* tn = t + n * D * nC;
   float mx = 0.f;
-  for (int i = lane; i < nC; i += 64) {
-    float s = 0.f;
-    for (int m = 0; m < D; ++m) {
-      const float v = tn[m * nC + i];
-      s += v * v;
+  if ((nC & 3) == 0 && D <= 9 && (reinterpret_cast<uintptr_t>(t) & 15) == 0) {
+    // four columns per lane, all D rows requested before the sums (same sums, same order per column)
+    const f4* t4 = reinterpret_cast<const f4*>(tn);
+    const int nq = nC >> 2;
+    for (int c = lane; c < nq; c += 64) {
+      f4 v[9];
+#pragma unroll
+      for (int m = 0; m < 9; ++m)
+        if (m < D) v[m] = t4[m * nq + c];
+      f4 s = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 9; ++m)
+        if (m < D) s += v[m] * v[m];
+      mx = fmaxf(mx, fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
     }
-    mx = fmaxf(mx, s);
+  } else {
+    for (int i = lane; i < nC; i += 64) {
+      float s = 0.f;
+      for (int m = 0; m < D; ++m) {
+        const float v = tn[m * nC + i];
+        s += v * v;
+      }
+      mx = fmaxf(mx, s);
+    }
   }
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if (lane == 0) nsc[n] = pow2_scale(mx);
@@ -392,9 +409,23 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   }
 }
 
-// out[n][o] = sum over chunks of part[chunk][n][o] (fixed order: deterministic).
-__global__ void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__ part, float* __restrict__ out) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < NS; i += (int64_t)gridDim.x * blockDim.x) {
+// out[n][o] = sum over chunks of part[chunk][n][o] (fixed order: deterministic).  Four outputs per thread
+// as float4s when NS is a multiple of 4 and the buffers are 16-byte aligned; eight chunks' loads in flight.
+__global__ __launch_bounds__(256) void reduce_kernel(int64_t NS, int nchunks, const float* __restrict__ part,
+                                                     float* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if ((NS & 3) == 0 && ((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
+    const int64_t NS4 = NS >> 2;
+    const f4* p4 = reinterpret_cast<const f4*>(part);
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < NS4; i += stride) {
+      f4 s = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int c = 0; c < nchunks; ++c) s += p4[(int64_t)c * NS4 + i];
+      reinterpret_cast<f4*>(out)[i] = s;
+    }
+    return;
+  }
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < NS; i += stride) {
     float s = 0.f;
     for (int c = 0; c < nchunks; ++c) s += part[(int64_t)c * NS + i];
     out[i] = s;
@@ -601,7 +632,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   }
   if (check_launch("gram forward")) return 2;
   const int64_t NS = N * S;
-  reduce_kernel<<<(unsigned)std::min<int64_t>((NS + 255) / 256, 4096), 256, 0, st>>>(NS, nchunks, part, out);
+  reduce_kernel<<<(unsigned)std::min<int64_t>(((NS + 3) / 4 + 255) / 256, 4096), 256, 0, st>>>(NS, nchunks, part, out);
   return check_launch("gram reduce") ? 2 : 0;
 }
 
