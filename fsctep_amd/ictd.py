@@ -247,8 +247,9 @@ class _ICTDTrunk(nn.Module):
         scales = [1.0 / math.sqrt(2 * k[0] + 1) for k in self.keys]
         scalars, sq_all = readout_features(feats, grams, scales, maps)
         outs = []
-        for i, k in enumerate(self.keys):
-            sq = sq_all[:, i, :]
+        # unbind: its backward stacks the per-key gradients in one copy (a select per key would zero-fill,
+        # copy and accumulate the whole (N, keys, n*C) gradient once per key)
+        for i, (k, sq) in enumerate(zip(self.keys, sq_all.unbind(1))):
             if k == (0, 1):
                 sq = torch.cat([sq, scalars * scalars], dim=-1)
             outs.append(sq * factors[i])
