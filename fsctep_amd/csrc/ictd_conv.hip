@@ -398,6 +398,8 @@ __global__ __launch_bounds__(256, 2) void mix_kernel(FscIctdLayout L, const floa
     return p;
   };
   const int64_t rows = N * d;
+  // the grid is sized for the key with the most components: blocks past this key's rows have no work
+  if ((int64_t)blockIdx.x * 4 * 16 * RT >= rows) return;   // block-uniform
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RT;
   const bool active = row0 < rows;   // wave-uniform; inactive waves still copy weights and meet the barriers
   // Z row of tile u (+ koff_p; row indices < 2^31, checked by the host), -1: past the end
