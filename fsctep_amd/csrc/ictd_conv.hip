@@ -894,49 +894,77 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ gates,
                                                         const float* __restrict__ qtab, float* __restrict__ out) {
   __shared__ float w[16][NY];
-  __shared__ int ycomp[16];
+  __shared__ float part[16][16][NY];   // [edge lane][source species][y]
+  __shared__ int ycomp[16], yrow[16];
   __shared__ int ssp[256];
   __shared__ unsigned smask;
   const int n = blockIdx.x, t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const int sn = node_species[n];
   fill_pair_species(NS, ssp);
-  const unsigned mask = src_species_mask(edge_pair, ssp, NS, beg, end, &smask);
-  if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none)
+  if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none) and that path's table row
     int yy = -1;
 #pragma unroll
     for (int y = 0; y < NY; ++y)
       if (L.y_path1[y] >= 0 && L.y_oo1[y] == t) yy = y;
     ycomp[t] = yy;
+    yrow[t] = yy >= 0 ? L.y_path1[yy] : 0;
   }
-  if (t < NS * NY) {   // thread (s, y), edges in order
-    const int s = t / NY, y = t - s * NY, p = L.y_path1[y];
-    float a = 0.f;
-    if (p >= 0 && ((mask >> s) & 1u)) {
+  const unsigned mask = src_species_mask(edge_pair, ssp, NS, beg, end, &smask);   // barrier: ssp, ycomp
+  {  // thread (edge lane k, y): partial sums over edges beg + k + 16 i, per source species
+    const int y = t & 15, k = t >> 4;
+    float acc[16];
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) acc[s2] = 0.f;
+    const int p = y < NY ? L.y_path1[y] : -1;
+    if (p >= 0) {
       const int gi = L.c1_gate[p];
-#pragma unroll 4
-      for (int e = beg; e < end; ++e) {
+      for (int e = beg + k; e < end; e += 16) {
         const float v = gates[(int64_t)e * L.NREF + gi] * F[(int64_t)e * NY + y];
-        a += (ssp[edge_pair[e] & 255] == s) ? v : 0.f;
+        const int ss = ssp[edge_pair[e] & 255];
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) acc[s2] += (ss == s2) ? v : 0.f;
       }
     }
-    w[s][y] = a;
+    if (y < NY) {
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) part[k][s2][y] = acc[s2];
+    }
+  }
+  __syncthreads();
+  if (t < 16 * NY) {   // w[s][y]: the edge lanes added in a fixed order
+    const int s2 = t / NY, y = t - s2 * NY;
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a += part[k][s2][y];
+    w[s2][y] = a;
   }
   __syncthreads();
   const float scale = 1.f / (float)max(end - beg, 1);
   float* on = out + (int64_t)n * L.M * C;
-  for (int i = t; i < L.M * C; i += blockDim.x) {
-    const int c = i / C, o = i - c * C;
-    const int yy = ycomp[c];
-    float v = 0.f;
-    if (yy >= 0) {
-      const float* qp = qtab + ((int64_t)sn * L.NP1 + L.y_path1[yy]) * C + o;   // pair (s, sn) = s*NS + sn
-      for (unsigned m = mask; m; m &= m - 1) {   // source species in increasing order
-        const int s2 = __builtin_ctz(m);
-        v += w[s2][yy] * qp[(int64_t)s2 * NS * L.NP1 * C];
+  const int MC = L.M * C;                 // <= 16 * 128 = 8 * 256
+  float v[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v[u] = 0.f;
+  // source species outermost (increasing order), the thread's outputs innermost: their table reads are
+  // independent and go out together
+  for (unsigned m = mask; m; m &= m - 1) {
+    const int s2 = __builtin_ctz(m);
+    const float* qs = qtab + ((int64_t)(s2 * NS + sn) * L.NP1) * C;   // pair (s2, sn)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = t + 256 * u;
+      if (i < MC) {
+        const int c = i / C, o = i - c * C;
+        const int yy = ycomp[c];
+        if (yy >= 0) v[u] += w[s2][yy] * qs[yrow[c] * C + o];
       }
     }
-    on[i] = v * scale;
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int i = t + 256 * u;
+    if (i < MC) on[i] = v[u] * scale;
   }
 }
 
