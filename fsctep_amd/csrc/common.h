@@ -183,8 +183,8 @@ __device__ __forceinline__ int xcd_node_k(int64_t n, const int32_t* __restrict__
 }
 
 // Grid of a persistent one-block-per-node launch of `kernel` (256 threads, lds bytes of dynamic LDS):
-// min(xcd_grid(n), the blocks the device holds at once), a multiple of 8.
-unsigned persist_grid(int64_t n, const void* kernel, size_t lds);
+// min(xcd_grid(n), the blocks the device holds at once, at most max_per_cu per CU), a multiple of 8.
+unsigned persist_grid(int64_t n, const void* kernel, size_t lds, int max_per_cu = 1 << 20);
 
 void set_error(const std::string& msg);
 int check_launch(const char* what);

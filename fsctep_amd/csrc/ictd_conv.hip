@@ -1298,7 +1298,10 @@ int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const i
   {
     LaunchTimer tm(timer_project, st);
     const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
-    project_fwd_kernel<C, DUAL><<<persist_grid(N, (const void*)project_fwd_kernel<C, DUAL>, lds), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
+    // receiver-grouped gathers at C 128: two blocks per CU keep the sources of the receivers an XCD has in
+    // flight closer to its L2 (measured faster than three); the source-grouped dual pass prefers three
+    const int cap = (!DUAL && C >= 128) ? 2 : (1 << 20);
+    project_fwd_kernel<C, DUAL><<<persist_grid(N, (const void*)project_fwd_kernel<C, DUAL>, lds, cap), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
                                                           N, node_order, eperm, gdeg);
   }
   if (check_launch("ictd project_fwd")) return 2;
@@ -1331,7 +1334,7 @@ int project_only_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, co
   const int ncg = cg_length(L);
   LaunchTimer tm("ictd_project", st);
   const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
-  project_fwd_kernel<C, false><<<persist_grid(N, (const void*)project_fwd_kernel<C, false>, lds), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
+  project_fwd_kernel<C, false><<<persist_grid(N, (const void*)project_fwd_kernel<C, false>, lds, C >= 128 ? 2 : (1 << 20)), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
                                                                Z + N * L.KT * C, N, node_order, nullptr, nullptr);
   return check_launch("ictd project") ? 2 : 0;
 }

@@ -26,13 +26,14 @@ struct GridKey {
   const void* kernel;
   size_t lds;
   int dev;
+  int max_per_cu;
   int64_t cap;
 };
 std::mutex g_grid_mu;
 std::vector<GridKey> g_grid_cache;
 }  // namespace
 
-unsigned persist_grid(int64_t n, const void* kernel, size_t lds) {
+unsigned persist_grid(int64_t n, const void* kernel, size_t lds, int max_per_cu) {
   const unsigned full = xcd_grid(n);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
@@ -41,7 +42,8 @@ unsigned persist_grid(int64_t n, const void* kernel, size_t lds) {
   }
   std::lock_guard<std::mutex> lk(g_grid_mu);
   for (const GridKey& k : g_grid_cache)
-    if (k.kernel == kernel && k.lds == lds && k.dev == dev) return (unsigned)std::min<int64_t>(full, k.cap);
+    if (k.kernel == kernel && k.lds == lds && k.dev == dev && k.max_per_cu == max_per_cu)
+      return (unsigned)std::min<int64_t>(full, k.cap);
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || cus <= 0 ||
@@ -49,8 +51,9 @@ unsigned persist_grid(int64_t n, const void* kernel, size_t lds) {
     (void)hipGetLastError();
     return full;
   }
+  per_cu = std::min(per_cu, max_per_cu);
   const int64_t cap = std::max<int64_t>(8, (int64_t)cus * per_cu / 8 * 8);
-  g_grid_cache.push_back(GridKey{kernel, lds, dev, cap});
+  g_grid_cache.push_back(GridKey{kernel, lds, dev, max_per_cu, cap});
   return (unsigned)std::min<int64_t>(full, cap);
 }
 
