@@ -16,11 +16,14 @@ rebuilds) for the headline figure.  The line also carries the step through the r
 ``forward()``, which prepares the graph on every call as the reference sorts on every call, and the
 cold and warm graph-preparation times.
 
-The default run (sparse, 10k atoms) prints the headline at the top level and the ICTD 10k and
-ICTD-O3 4k workloads under ``workloads``, each with its roofline kernel, a table of the TP/scatter
-kernels' rates, the parity of its energies, forces (and dipole) against the fp64 oracle's full-system
-values where a fixture for that exact system exists (tests/golden/oracle_<mode>_<atoms>.npz), and
-the CPU baseline.  Prints one JSON line.
+The default run (sparse, 10k atoms) prints the headline at the top level and, under ``workloads``, the
+ICTD 10k and ICTD-O3 4k workloads, the 100k-atom sparse domain (fp32 and the bf16 channel-mix
+variant), and the two launch-bound sparse systems (1,000 atoms, and the 32-atom golden system), which
+are timed eagerly and replayed from a HIP graph.  Each carries its roofline kernel, a table of the
+TP/scatter kernels' rates (MFMA kernels priced against the peak of their own product arithmetic), the
+parity of its energies, forces (and dipole) against the fp64 oracle's full-system values where a
+fixture for that exact system exists (tests/golden/oracle_<mode>_<atoms>.npz) or the reference golden
+vector, and the CPU baseline.  Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -38,7 +41,25 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2500.0          # dense fp16 and bf16 MFMA
 PARITY_TOL = 1e-5
+
+# Peak rate of fp32-accurate products for each product arithmetic: a split-fp16 product is 3 fp16 MFMA
+# products (hh + hl + lh), a split-bf16 product 6 bf16 ones; "bf16" is one bf16 product (the bf16
+# channel-mix variant).  A kernel's mfma_frac is its useful flops over the peak of its own arithmetic.
+PRODUCT_PEAK_TFLOPS = {"fp32": FP32_MFMA_PEAK_TFLOPS, "split-fp16": FP16_MFMA_PEAK_TFLOPS / 3,
+                       "split-bf16": FP16_MFMA_PEAK_TFLOPS / 6, "bf16": FP16_MFMA_PEAK_TFLOPS}
+KERNEL_PRODUCTS = {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
+                   "edge_message_grad": "fp32", "receiver_sum": "fp32",
+                   "ictd_project": "fp32", "ictd_project_grad": "fp32", "ictd_dual_project": "fp32",
+                   "ictd_mix": "split-fp16", "ictd_mix_grad": "split-fp16", "ictd_dual_mix": "split-fp16"}
+BF16_VARIANT = {"node_expand", "node_expand_grad", "edge_message"}
+
+
+def kernel_products(name: str, precision: str = "fp32") -> str:
+    if precision == "bf16" and name in BF16_VARIANT:
+        return "bf16"
+    return KERNEL_PRODUCTS.get(name, "fp32")
 
 WORKLOADS = {
     "sparse": dict(atoms=10000, species=4, seed=22, channels=64, layers=3, lmax=2, kernel="edge_message_grad",
@@ -285,14 +306,19 @@ def parity_vs_fixture(mode: str, system, seed: int, e, f, dip) -> dict:
     return out
 
 
-def _rate(work: dict, avg_ms: float) -> dict:
-    """Achieved rate of one launch against its algorithmic bytes (HBM) and, for MFMA kernels, flops."""
+def _rate(work: dict, avg_ms: float, products: str = "fp32") -> dict:
+    """Achieved rate of one launch against its algorithmic bytes (HBM) and, for MFMA kernels, flops
+    against the peak of the kernel's own product arithmetic (PRODUCT_PEAK_TFLOPS)."""
     gbs = work["bytes"] / (avg_ms * 1e-3) / 1e9
     r = {"avg_launch_ms": round(avg_ms, 4), "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
          "bound": work["bound"]}
     if work["bound"] == "mfma":
         tf = work["flops"] / (avg_ms * 1e-3) / 1e12
-        r.update(tflops=round(tf, 2), mfma_frac=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+        peak = PRODUCT_PEAK_TFLOPS[products]
+        r.update(tflops=round(tf, 2), products=products, mfma_peak_tflops=round(peak, 1),
+                 mfma_frac=round(tf / peak, 4))
+        if tf > peak:   # a useful-flop count above the arithmetic's peak means the accounting is wrong
+            print(f"[bench] WARNING: {tf:.1f} TFLOP/s above the {products} peak {peak:.1f}", file=sys.stderr)
     return r
 
 
@@ -378,8 +404,9 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
     avg_ms = kt.total_ms / max(kt.launches, 1)
     if work["bound"] == "mfma":
         achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4)}
+        peak = PRODUCT_PEAK_TFLOPS[kernel_products(kname, precision)]
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 1), "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "products": kernel_products(kname, precision)}
     else:
         achieved = work["bytes"] / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -410,7 +437,8 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
                     step()
                 torch.cuda.synchronize()
             if t.launches:
-                rates[k] = dict(_rate(work_of(k), t.total_ms / t.launches), launches_per_step=t.launches // kt_steps)
+                rates[k] = dict(_rate(work_of(k), t.total_ms / t.launches, kernel_products(k, precision)),
+                                launches_per_step=t.launches // kt_steps)
         out["kernels"] = rates
 
     if keep:
@@ -463,6 +491,143 @@ def measure(mode: str, n_atoms: int, seed: int, steps: int, warmup: int, kname: 
     return out
 
 
+# The two smaller sparse configurations: the 32-atom CPU-runnable plumbing system (the reference-written
+# golden system itself: 32 atoms of 4 species in a 10 A open box, C 32, 2 layers) and the 1,000-atom
+# periodic box (C 64, 3 layers).  Both are launch-bound, so each is timed eagerly and replayed from a
+# HIP graph (fsctep_amd.capture); `value` is the replayed rate.
+SMALL = {
+    "sparse-1k": dict(atoms=1000, seed=22, channels=64, layers=3, kernel="edge_message_grad"),
+    "sparse-32": dict(golden="sparse_open32_c32_l2", channels=32, layers=2, kernel="edge_message_grad"),
+}
+
+
+def _small_model(name: str, dev):
+    from fsctep_amd.sparse import PureCartesianSparseTransformerLayer
+    from fsctep_amd.synthetic import apply_seeded_parameters
+    w = SMALL[name]
+    seed = 1
+    if "golden" in w:
+        import numpy as np
+        seed = int(np.load(os.path.join(ROOT, "tests", "golden", w["golden"] + ".npz"))["param_seed"])
+    C = w["channels"]
+    model = PureCartesianSparseTransformerLayer(
+        max_embed_radius=5.0, main_max_radius=5.0, main_number_of_basis=8, hidden_dim_conv=C, hidden_dim_sh=C,
+        hidden_dim=64, channel_in2=32, embedding_dim=16, max_atomvalue=10, output_size=8, invariant_channels=32,
+        embed_size=[128, 128, 128], num_interaction=w["layers"], function_type_main="bessel", lmax=2,
+        max_rank_other=1, k_policy="k0")
+    apply_seeded_parameters(model, seed)
+    return model.to(dev).eval().requires_grad_(False), seed
+
+
+def _small_system(name: str):
+    from fsctep_amd.synthetic import AtomicSystem
+    w = SMALL[name]
+    if "golden" in w:
+        import numpy as np
+        g = np.load(os.path.join(ROOT, "tests", "golden", w["golden"] + ".npz"), allow_pickle=False)
+        return AtomicSystem(pos=g["pos"], species=g["species"], cell=g["cell"], periodic=bool(g["periodic"]),
+                            edge_src=g["edge_src"], edge_dst=g["edge_dst"], edge_shifts=g["edge_shifts"]), g
+    return _system("sparse", w["atoms"], w["seed"]), None
+
+
+def measure_small(name: str, steps: int, warmup: int, dev) -> dict:
+    """Eager and HIP-graph-replayed energy + forces of a small sparse system; parity of both against the
+    reference golden (32 atoms) or the fp64 oracle fixture (1,000 atoms)."""
+    import numpy as np
+    import torch
+    from fsctep_amd import _lib
+    from fsctep_amd.capture import CapturedEnergyForces
+    from fsctep_amd.sparse import energy_and_forces
+    w = SMALL[name]
+    system, golden = _small_system(name)
+    model, pseed = _small_model(name, dev)
+    N, E, C = system.num_atoms, system.num_edges, w["channels"]
+    pos = torch.tensor(system.pos, dtype=torch.float32, device=dev)
+    A = torch.tensor(system.species, device=dev)
+    batch = torch.zeros(N, dtype=torch.long, device=dev)
+    cell = torch.tensor(system.cell, dtype=torch.float32, device=dev)
+    graph = model.prepare(torch.tensor(system.edge_src, device=dev), torch.tensor(system.edge_dst, device=dev),
+                          torch.tensor(system.edge_shifts, dtype=torch.float32, device=dev), N, A, pos=pos)
+    step = lambda: energy_and_forces(model, pos, batch, cell, graph)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    def timed(fn, k):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            res = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0 / k, res
+
+    with _lib.KernelTimer(w["kernel"]) as kt:
+        eager_ms, (e_eager, f_eager) = timed(step, steps)
+    cap = CapturedEnergyForces(model, pos, batch, cell, graph, warmup=2)
+    for _ in range(warmup):
+        cap()
+    graph_ms, (e_cap, f_cap, _) = timed(cap, steps)
+    same = bool(torch.equal(e_cap, e_eager) and torch.equal(f_cap, f_eager))
+    print(f"[bench] {name}: {N} atoms, {E} edges: eager {eager_ms:.3f} ms/step, HIP graph {graph_ms:.3f} ms/step, "
+          f"replay equals eager bitwise: {same}", file=sys.stderr, flush=True)
+
+    work = sparse_kernel_work(w["kernel"], N, E, C)
+    avg_ms = kt.total_ms / max(kt.launches, 1)
+    peak = PRODUCT_PEAK_TFLOPS[kernel_products(w["kernel"])]
+    achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 1), "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "products": kernel_products(w["kernel"]), "traffic": None,
+            "kernel": w["kernel"], "avg_launch_ms": round(avg_ms, 4), "launches": kt.launches,
+            "algorithmic_per_launch": {"flops": work["flops"], "bytes": work["bytes"]},
+            "note": "launch-bound system: the kernel is a few microseconds; the step time is set by launches"}
+    e_np, f_np = e_cap.double().cpu().numpy(), f_cap.double().cpu().numpy()
+    if golden is not None:
+        parity = {"fixture": f"tests/golden/{w['golden']}.npz", "reference": "the reference trunk in fp64 "
+                  "(golden vector written by the imported reference)", "tolerance": PARITY_TOL,
+                  "energy_rel": float(f"{_rel_inf(e_np, golden['energy_f64']):.3e}"),
+                  "forces_rel": float(f"{_rel_inf(f_np, golden['forces_f64']):.3e}")}
+        parity["within_tolerance"] = parity["energy_rel"] < PARITY_TOL and parity["forces_rel"] < PARITY_TOL
+    else:
+        parity = parity_vs_fixture("sparse", system, w["seed"], e_np, f_np, None)
+    return {"ms_per_step": round(graph_ms, 4), "value": round(N / (graph_ms * 1e-3), 1),
+            "ms_per_step_eager": round(eager_ms, 4), "value_eager": round(N / (eager_ms * 1e-3), 1),
+            "replay_equals_eager_bitwise": same, "roofline": roof, "parity": parity,
+            "config": {"workload": f"pure-cartesian-sparse energy+forces, {N} atoms, {E} edges, "
+                       + ("10 A open box (the reference golden system)" if golden is not None else
+                          "periodic cubic box, density 0.1/A^3") + f", 4 species, {w['layers']} interaction layers, "
+                       f"{C} channels, ranks 0..2, cutoff 5.0 A, 8 Bessel radial basis, parameters seed {pseed}; "
+                       "step replayed from a HIP graph", "mode": "sparse", "atoms": N, "edges": E}}
+
+
+def cpu_baseline_small(name: str, steps: int) -> dict:
+    """The oracle on the host cores on the small system itself (the whole system, not a sample)."""
+    import torch
+    from fsctep_amd.synthetic import seeded_value
+    from oracle import sparse_ref as R
+    w = SMALL[name]
+    cores, cdesc = host_cores()
+    torch.set_num_threads(cores)
+    s, _ = _small_system(name)
+    _, pseed = _small_model(name, "cpu")
+    n = s.num_atoms
+    args = (torch.tensor(s.pos, dtype=torch.float32), torch.tensor(s.species), torch.zeros(n, dtype=torch.long),
+            torch.tensor(s.edge_src), torch.tensor(s.edge_dst), torch.tensor(s.edge_shifts, dtype=torch.float32),
+            torch.tensor(s.cell, dtype=torch.float32))
+    cfg = R.SparseConfig(channels=w["channels"], num_interaction=w["layers"], function_type="bessel")
+    p = {k: torch.tensor(seeded_value(k, sh, pseed), dtype=torch.float32) for k, sh in R.param_shapes(cfg)}
+    R.energy_forces(*args, p, cfg)
+    dts = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        R.energy_forces(*args, p, cfg)
+        dts.append(time.perf_counter() - t0)
+    dt = statistics.median(dts)
+    return {"value": round(n / dt, 3), "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (materialised per-edge weights, per-path einsums, index_add), fp32, the whole "
+                      f"{n}-atom / {s.num_edges}-edge system, median of {steps} timed steps after 1 warm-up, "
+                      f"{dt:.3f} s/step, {cores} threads ({cdesc}) on {_cpu_model()}"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,6 +645,8 @@ def main():
     ap.add_argument("--no-kernel-table", action="store_true")
     ap.add_argument("--no-large", action="store_true",
                     help="skip the 100k-atom sparse workload (fp32 and the bf16 channel-mix variant)")
+    ap.add_argument("--no-small", action="store_true",
+                    help="skip the 32-atom and 1,000-atom sparse workloads (eager and HIP-graph replay)")
     ap.add_argument("--channel-mix", choices=["fp32", "bf16"], default="fp32",
                     help="products of the sparse channel mix for --mode sparse runs")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -557,6 +724,9 @@ def main():
                                "energy_total_rel": float(f"{abs(e16.sum() - e32.sum()) / abs(e32.sum()):.3e}"),
                                "speedup": round(big["fp32"]["ms_per_step"] / big["bf16"]["ms_per_step"], 3)}
         workloads["sparse-100k"] = big
+    if extra and not args.no_small:
+        for name in ("sparse-1k", "sparse-32"):
+            workloads[name] = measure_small(name, max(args.steps, 50), args.warmup, dev)
     if workloads:
         out["workloads"] = workloads
 
@@ -566,6 +736,11 @@ def main():
         out["cpu_baseline"] = cpu_baseline(args.mode, cpu_atoms, args.cpu_steps, seed)
         out["cpu_baseline"]["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
         for m, r in workloads.items():
+            if m in SMALL:
+                # the whole system: 32 atoms take ~0.04 s a step, 1,000 atoms ~15 s on 16 cores
+                r["cpu_baseline"] = cpu_baseline_small(m, 10 if m == "sparse-32" else 1)
+                r["cpu_baseline"]["gpu_over_cpu"] = round(r["value"] / r["cpu_baseline"]["value"], 1)
+                continue
             if m not in WORKLOADS:        # the 100k-atom sparse domain: same per-atom oracle as the headline
                 continue
             wm = WORKLOADS[m]

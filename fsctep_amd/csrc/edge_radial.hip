@@ -39,20 +39,30 @@ __device__ __forceinline__ void sincos_small(float x, float& s, float& c) {
   c = (qd == 0) ? cp : (qd == 1) ? -sp : (qd == 2) ? -cp : sp;
 }
 
-// emb_k(r) and d emb_k / dr for k < nb (basis 0: Bessel, 1: Gaussian), matching the device
-// formula used by the model code (bessel: sqrt(2/rc) sin(k pi r/rc)/r on (0, rc); gaussian:
-// exp(-((r - mu_k)/step)^2)/1.12 with mu_k = k*step, step = rc/(nb+1)), times sqrt(nb).
+// emb_k(r) and d emb_k / dr for k < nb, e3nn's soft_one_hot_linspace(r, 0, rc, nb, basis, cutoff=True)
+// times sqrt(nb), with step = rc/(nb+1), centres mu_k = (k+1)*step and d = (r - mu_k)/step:
+//   0 bessel         sqrt(2/rc) sin((k+1) pi r/rc)/r                     on 0 < r < rc
+//   1 gaussian       exp(-d^2)/1.12
+//   2 fourier        sin((k+1) pi r/rc)/sqrt(0.25 + nb/2)                on 0 < r < rc
+//   3 cosine         cos(pi d/2)                                         on |d| < 1
+//   4 smooth_finite  1.14136 e^2 exp(-1/(1+d)) exp(-1/(1-d)) = 1.14136 e^2 exp(-2/(1-d^2))   on |d| < 1
 template <bool DERIV>
 __device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int basis, float& f, float& df) {
   const float snb = sqrtf((float)nb);
-  if (basis == 0) {
+  if (basis == 0 || basis == 2) {
     const float w = (float)(k + 1) * (3.14159265358979323846f / rc);
     const bool inside = (r / rc < 1.f) && (r > 0.f);
-    const float a = sqrtf(2.f / rc) * snb;
     const float rr = inside ? r : 1.f;
     const float x = w * rr;
     float s, c;
     sincos_small(x, s, c);
+    if (basis == 2) {
+      const float a = snb * rsqrtf(0.25f + 0.5f * (float)nb);
+      f = inside ? a * s : 0.f;
+      if (DERIV) df = inside ? a * w * c : 0.f;
+      return;
+    }
+    const float a = sqrtf(2.f / rc) * snb;
     f = inside ? a * s / rr : 0.f;
     if (DERIV) {
       // d/dr sin(wr)/r = w^2 (x cos x - sin x)/x^2; below x = 0.3 the Taylor series avoids the
@@ -61,12 +71,26 @@ __device__ __forceinline__ void basis_eval(float r, int k, int nb, float rc, int
       const float g = (x < 0.3f) ? x * (-1.f / 3.f + x2 * (1.f / 30.f - x2 * (1.f / 840.f))) : (x * c - s) / x2;
       df = inside ? a * w * w * g : 0.f;
     }
-  } else {
-    const float step = rc / (float)(nb + 1);
-    const float d = (r - (float)(k + 1) * step) / step;
+    return;
+  }
+  const float step = rc / (float)(nb + 1);
+  const float d = (r - (float)(k + 1) * step) / step;
+  if (basis == 1) {
     const float e = expf(-d * d) / 1.12f * snb;
     f = e;
     if (DERIV) df = e * (-2.f * d / step);
+  } else if (basis == 3) {
+    const bool inside = (d < 1.f) && (d > -1.f);
+    float s, c;
+    sincos_small(fminf(fabsf(d), 2.f) * 1.57079632679489662f, s, c);
+    f = inside ? c * snb : 0.f;
+    if (DERIV) df = inside ? -copysignf(s, d) * (1.57079632679489662f / step) * snb : 0.f;
+  } else {
+    const bool inside = (d < 1.f) && (d > -1.f);
+    const float q = inside ? 1.f - d * d : 1.f;
+    const float e = inside ? 1.14136f * 7.38905609893065023f * expf(-2.f / q) * snb : 0.f;
+    f = e;
+    if (DERIV) df = e * (-4.f * d / (q * q)) / step;
   }
 }
 
@@ -596,7 +620,7 @@ int fsc_radial_mlp_forward(int64_t n_edges, const float* r, const float* w0, con
                            float r_cut, int32_t basis, float* out, hipStream_t stream) {
   FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_forward: bad size");
   FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_forward: n_basis must be 1..16");
-  FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_forward: basis must be 0 (bessel) or 1 (gaussian)");
+  FSC_CHECK_ARG(basis >= 0 && basis <= 4, "fsc_radial_mlp_forward: basis must be 0..4 (bessel, gaussian, fourier, cosine, smooth_finite)");
   FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_forward: r_cut must be positive");
   FSC_CHECK_ARG(!w4 || (b4 && n_out >= 1 && n_out <= HID), "fsc_radial_mlp_forward: last Linear needs 1..64 outputs");
   if (n_edges == 0) return 0;
@@ -612,7 +636,7 @@ int fsc_radial_mlp_backward(int64_t n_edges, const float* r, const float* w0, co
                             int32_t basis, const float* grad_out, float* grad_r, hipStream_t stream) {
   FSC_CHECK_ARG(n_edges >= 0 && n_edges < (1LL << 31), "fsc_radial_mlp_backward: bad size");
   FSC_CHECK_ARG(n_basis >= 1 && n_basis <= NBMAX, "fsc_radial_mlp_backward: n_basis must be 1..16");
-  FSC_CHECK_ARG(basis == 0 || basis == 1, "fsc_radial_mlp_backward: basis must be 0 (bessel) or 1 (gaussian)");
+  FSC_CHECK_ARG(basis >= 0 && basis <= 4, "fsc_radial_mlp_backward: basis must be 0..4 (bessel, gaussian, fourier, cosine, smooth_finite)");
   FSC_CHECK_ARG(r_cut > 0.f, "fsc_radial_mlp_backward: r_cut must be positive");
   FSC_CHECK_ARG(!w4 || (n_out >= 1 && n_out <= HID), "fsc_radial_mlp_backward: last Linear needs 1..64 outputs");
   if (n_edges == 0) return 0;

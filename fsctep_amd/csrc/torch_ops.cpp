@@ -819,7 +819,7 @@ Tensor edge_geometry_backward_meta(const std::optional<Tensor>&, const std::opti
 }
 
 int32_t basis_code(int64_t basis) {
-  TORCH_CHECK(basis == 0 || basis == 1, "radial basis: 0 (bessel) or 1 (gaussian)");
+  TORCH_CHECK(basis >= 0 && basis <= 4, "radial basis: 0 bessel, 1 gaussian, 2 fourier, 3 cosine, 4 smooth_finite");
   return (int32_t)basis;
 }
 

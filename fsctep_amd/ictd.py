@@ -22,7 +22,7 @@ import torch.nn.functional as F
 
 from . import ictd_ops
 from .readout_ops import ReadoutMaps, prepare_gram, readout_features
-from .graph import Graph, poison_invalid, prepare_graph
+from .graph import Graph, poison_invalid, prepare_species_graph, species_rows
 from .ictd_basis import canonical, coupling, layout_full, layout_o3
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
 
@@ -90,8 +90,12 @@ class _ICTDTrunk(nn.Module):
             raise ValueError(f"num_interaction must be >= 2, got {self.num_interaction}")
         if self.channels not in (32, 64, 128) or output_size != 8:
             raise NotImplementedError("HIP ICTD path: hidden_dim_conv 32/64/128 and output_size 8")
-        if not 1 <= max_atomvalue <= 16:
-            raise NotImplementedError("HIP ICTD path: max_atomvalue (species table rows) 1..16")
+        if max_atomvalue < 1:
+            raise ValueError(f"max_atomvalue must be >= 1, got {max_atomvalue}")
+        from .ops import check_basis
+        check_basis(function_type_main)
+        if not 1 <= main_number_of_basis <= 16:
+            raise NotImplementedError("HIP ICTD path: main_number_of_basis 1..16")
         self.n_species = int(max_atomvalue)
         self.invariant_channels = int(invariant_channels)
         self.max_radius = float(max_embed_radius)
@@ -153,8 +157,11 @@ class _ICTDTrunk(nn.Module):
 
     # ------------------------------------------------------------------ forward
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A, pos=None) -> Graph:
-        """The receiver-sorted graph of one neighbour list (device op, no host synchronisation)."""
-        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species, pos=pos)
+        """The receiver-sorted graph of one neighbour list (device op, no host synchronisation); species
+        tables above 16 rows are served by mapping the species present (at most 16) to rows."""
+        if int(num_nodes) != A.shape[0]:
+            raise ValueError(f"num_nodes {num_nodes} != len(A) {A.shape[0]}")
+        return prepare_species_graph(edge_src, edge_dst, edge_shifts, A, self.n_species, pos=pos)
 
     def _check_inference(self):
         if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
@@ -180,8 +187,9 @@ class _ICTDTrunk(nn.Module):
     def forward_graph(self, pos, batch, cell, g: Graph, external_tensor=None, edge_vec=None, with_dipole=True):
         """((N,1) atomic energies, (G,1,3) dipole or None) for a prepared graph; ``edge_vec`` (E, 3), in the
         caller's edge order, replaces the geometry from ``pos`` (differentiable w.r.t. it).  The dipole head
-        runs when the model has one and ``with_dipole`` is set (its graph count reads ``batch`` on the host,
-        as the reference's does, pure_cartesian_ictd_layers_o3.py:983)."""
+        runs when the model has one and ``with_dipole`` is set; it has one row per graph of ``cell`` (G, 3, 3),
+        which the reference sizes as max(batch) + 1 (pure_cartesian_ictd_layers_o3.py:983): the same for
+        every batch whose last graph has atoms, and read here without a host synchronisation."""
         self._check_inference()
         if not pos.is_cuda:
             raise RuntimeError("the HIP ICTD path runs on the GPU only")
@@ -198,16 +206,16 @@ class _ICTDTrunk(nn.Module):
         Y = ictd_ops.edge_harmonics(n, self.lmax)
 
         c1 = self.e3_conv_emb
-        NS = self.n_species
-        with torch.no_grad():   # species-table rows (atomic numbers 0..max_atomvalue-1)
-            atab = c1.atom_mlp(c1.atom_embedding(torch.arange(NS, device=pos.device))).detach()
+        NS = g.n_species
+        with torch.no_grad():   # species-table rows
+            atab = c1.atom_mlp(c1.atom_embedding(species_rows(g, pos.device))).detach()
             W1 = c1.tp2.weight.detach()[c1_gates]                                  # (NP1, C, 8, 8)
             qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
         F_in = Y
         if self.external_field:
             if external_tensor is None:
                 raise ValueError("this model was built with an external field; pass external_tensor")
-            fld = external_tensor.to(f32).reshape(-1, 3)[:, [2, 1, 0]]      # rank-1 -> l=1 block order (z,y,x)
+            fld = external_tensor.to(f32).reshape(-1, 3).flip(-1)            # rank-1 -> l=1 block order (z,y,x)
             if self.o3:
                 s = c1.external_tensor_scale_by_irrep[self.keys.index((1, -1))]
             else:
@@ -221,8 +229,8 @@ class _ICTDTrunk(nn.Module):
         for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
             feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, self._gates(fc2, r), tp.weight.detach(),
                                                   self._wt(tp), cg, g, self.layout_id))
-        e, dip = self.readout(feats, batch, factors, with_dipole)
-        return poison_invalid(e, g), dip
+        e, dip = self.readout(feats, batch, cell.shape[0], factors, with_dipole)
+        return poison_invalid(e, g, pos, edge_vec), dip
 
     def _gates(self, fc, r):
         """Per-path gates fc(radial_basis(r)) (E, P) by one fused kernel (P <= 64)."""
@@ -234,7 +242,7 @@ class _ICTDTrunk(nn.Module):
     def _wread(self, i, k):
         return self.W_read[_key_str(k)] if self.o3 else self.W_read[i]
 
-    def readout(self, feats, batch, factors, with_dipole=True):
+    def readout(self, feats, batch, n_graphs, factors, with_dipole=True):
         """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included: the
         Gram inputs (the reference's channel-major flatten, layer concatenation and re-split by key)
         and the per-key squared norms of the layer concatenation come from one fused readout op."""
@@ -264,8 +272,9 @@ class _ICTDTrunk(nn.Module):
             t = torch.cat([f.flatten(1) for f in feats], dim=1).index_select(1, idx).view(-1, 3, nC)
             W = self.physical_tensor_heads["dipole"]["1"].weight
             y = torch.matmul(t, W.t().contiguous()).transpose(1, 2)          # (N, o, 3) = einsum("ncm,oc->nom")
-            G = int(batch.max()) + 1 if batch.numel() else 0
-            dip = y.new_zeros(G, 1, 3).index_add(0, batch, y)
+            # per-graph sum as a (G, N) one-hot product: a fixed summation order (index_add's atomics are not)
+            onehot = (torch.arange(n_graphs, device=batch.device).unsqueeze(1) == batch.unsqueeze(0)).to(y.dtype)
+            dip = torch.matmul(onehot, y.reshape(-1, 3)).view(n_graphs, 1, 3)
         return e, dip
 
 
@@ -280,21 +289,83 @@ class PureCartesianICTDTransformerLayer(_ICTDTrunk):
         return layout_full(self.lmax)
 
 
+def _parse_irreps(spec, lmax: int) -> list:
+    """'0e,1o + 2e' or ['0e', '1o'] -> [(l, parity)], multiplicity 1 only (models/pure_cartesian_ictd_layers_o3.py:66-86)."""
+    items = spec.replace(",", " ").replace("+", " ").split() if isinstance(spec, str) else [str(x) for x in spec]
+    out = []
+    for it in items:
+        it = it.strip()
+        if not it:
+            continue
+        mul, _, ir = it.rpartition("x")
+        if mul not in ("", "1") or len(ir) < 2 or ir[-1] not in "eo" or not ir[:-1].isdigit():
+            raise ValueError(f"o3 irreps: multiplicity-1 entries like '1o' expected, got {it!r}")
+        l = int(ir[:-1])
+        if not 0 <= l <= lmax:
+            raise ValueError(f"o3 irreps entry {it!r} outside 0..{lmax}")
+        out.append((l, 1 if ir[-1] == "e" else -1))
+    return out
+
+
+def _sorted_keys(keys) -> list:
+    return sorted(set(keys), key=lambda k: (k[0], 0 if k[1] > 0 else 1))
+
+
+def resolve_o3_keys(lmax: int, preset="auto", explicit=None, external_irrep=None, physical_tensor_outputs=None):
+    """Active irreps of the O3 trunk, as the reference resolves them
+    (models/pure_cartesian_ictd_layers_o3.py:88-180): the required ones (0e, the external field's irrep,
+    the physical-tensor heads' irreps) joined to an explicit list, or to the preset: 'auto' adds the
+    geometric irreps (l, (-1)^l), 'full' is every (l, +-1), 'minimal' the required ones alone, and
+    'balanced' the geometric and required ones plus every (l3, p1 p2) their products with the geometric
+    irreps reach up to lmax."""
+    required = [(0, 1)]
+    if external_irrep is not None:
+        required += [k for k in _parse_irreps(external_irrep, 10 ** 6) if k[0] <= lmax]
+    for spec in (physical_tensor_outputs or {}).values():
+        if spec.get("irreps") is not None:
+            required += [k for k in _parse_irreps(spec["irreps"], 10 ** 6) if k[0] <= lmax]
+        else:
+            required += [canonical(int(l)) for l in spec.get("ls", [])]
+    required = _sorted_keys(required)
+    if explicit is not None and (not isinstance(explicit, str) or explicit.strip()):
+        parsed = _parse_irreps(explicit, lmax)
+        if parsed:
+            return _sorted_keys(parsed + required)
+    preset = str(preset or "auto").strip().lower()
+    geom = [canonical(l) for l in range(lmax + 1)]
+    if preset == "full":
+        return _sorted_keys([(l, p) for l in range(lmax + 1) for p in (1, -1)])
+    if preset == "minimal":
+        return required
+    if preset == "auto":
+        return _sorted_keys(geom + required)
+    if preset == "balanced":
+        seed = _sorted_keys(geom + required)
+        out = set(seed)
+        for l1, p1 in seed:
+            for l2, p2 in geom:
+                for l3 in range(abs(l1 - l2), min(l1 + l2, lmax) + 1):
+                    out.add((l3, p1 * p2))
+        return _sorted_keys(out)
+    raise ValueError(f"Unknown o3_irrep_preset={preset!r}; expected auto|minimal|balanced|full")
+
+
 class PureCartesianICTDO3TransformerLayer(_ICTDTrunk):
-    """Drop-in for the reference ``pure-cartesian-ictd-o3`` trunk with explicit active irreps."""
+    """Drop-in for the reference ``pure-cartesian-ictd-o3`` trunk: active irreps from ``o3_active_irreps``
+    or the ``o3_irrep_preset`` (auto, minimal, balanced, full), resolved as the reference does."""
 
     o3 = True
 
     def _make_layout(self, preset, active, phys):
-        if active is None:
-            raise NotImplementedError("HIP ICTD-O3 path: pass o3_active_irreps explicitly")
-        items = active.replace(",", " ").replace("+", " ").split() if isinstance(active, str) else list(active)
-        keys = [(int(s[:-1]), 1 if s[-1] == "e" else -1) for s in items]
-        if self.external_field and (1, -1) not in keys:
-            keys.append((1, -1))
+        keys = resolve_o3_keys(self.lmax, preset, active, "1o" if self.external_field else None, phys)
         for l in range(self.lmax + 1):
             if canonical(l) not in keys:
-                raise NotImplementedError("HIP ICTD-O3 path: the geometric irreps 0e,1o,2e,.. must be active")
+                raise NotImplementedError(f"HIP ICTD-O3 path: active irreps {keys} lack the geometric irrep "
+                                          f"{canonical(l)}; the kernels need 0e,1o,2e,.. up to lmax")
+        M = sum(2 * l + 1 for l, _ in keys)
+        if M > 16:
+            raise NotImplementedError(f"HIP ICTD-O3 path: active irreps {[_key_str(k) for k in keys]} have {M} "
+                                      "components per channel; the kernels take at most 16")
         return layout_o3(self.lmax, keys)
 
 

@@ -53,7 +53,15 @@ def sparse_conv1_apply(h, n, mf, mb, graph, channels: int):
     return out
 
 
-BASIS = {"bessel": 0, "gaussian": 1}
+# radial bases of e3nn's soft_one_hot_linspace that the reference offers (cli/train.py:589-590)
+BASIS = {"bessel": 0, "gaussian": 1, "fourier": 2, "cosine": 3, "smooth_finite": 4}
+
+
+def check_basis(basis: str) -> int:
+    """The kernel code of a radial basis name; raises for a name the reference does not offer."""
+    if basis not in BASIS:
+        raise ValueError(f"radial basis {basis!r}: expected one of {sorted(BASIS)}")
+    return BASIS[basis]
 
 
 def edge_geometry(pos, shift_vec, graph):
@@ -71,16 +79,12 @@ def edge_vec_geometry(edge_vec, graph):
 
 def radial_hidden(r, fc, r_cut: float, basis: str):
     """fc[:4](radial_basis(r)) = silu(fc[2](silu(fc[0](emb)))) on the device: (E, 64)."""
-    if basis not in BASIS:
-        raise ValueError(f"radial basis {basis!r} is not supported by the HIP path")
     return torch.ops.fsctep.radial_mlp(r, fc[0].weight.detach(), fc[0].bias.detach(), fc[2].weight.detach(),
-                                       fc[2].bias.detach(), None, None, float(r_cut), BASIS[basis])
+                                       fc[2].bias.detach(), None, None, float(r_cut), check_basis(basis))
 
 
 def radial_full(r, fc, r_cut: float, basis: str):
     """The whole radial MLP fc(radial_basis(r)) including its last Linear (<= 64 outputs): (E, P)."""
-    if basis not in BASIS:
-        raise ValueError(f"radial basis {basis!r} is not supported by the HIP path")
     return torch.ops.fsctep.radial_mlp(r, fc[0].weight.detach(), fc[0].bias.detach(), fc[2].weight.detach(),
                                        fc[2].bias.detach(), fc[4].weight.detach(), fc[4].bias.detach(),
-                                       float(r_cut), BASIS[basis])
+                                       float(r_cut), check_basis(basis))

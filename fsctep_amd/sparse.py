@@ -25,7 +25,7 @@ import torch.nn.functional as F
 
 from . import ops
 from .readout_ops import ReadoutMaps, prepare_gram, readout_features
-from .graph import Graph, poison_invalid, prepare_graph
+from .graph import Graph, poison_invalid, prepare_species_graph, species_rows
 
 _COMPS = ((0, 1), (1, 4), (4, 13))   # component ranges of ranks 0, 1, 2
 
@@ -165,8 +165,11 @@ class PureCartesianSparseTransformerLayer(nn.Module):
             raise TypeError(f"unexpected argument {k!r}")
         if output_size != 8:
             raise NotImplementedError("HIP sparse conv1 needs output_size 8")
-        if not 1 <= max_atomvalue <= 16:
-            raise NotImplementedError("HIP sparse path: max_atomvalue (species table rows) 1..16")
+        if max_atomvalue < 1:
+            raise ValueError(f"max_atomvalue must be >= 1, got {max_atomvalue}")
+        ops.check_basis(function_type_main)
+        if not 1 <= main_number_of_basis <= 16:
+            raise NotImplementedError("HIP sparse path: main_number_of_basis 1..16")
         if hidden_dim_conv not in (32, 64):
             raise NotImplementedError("HIP sparse path: hidden_dim_conv 32 or 64")
         if num_interaction < 2:
@@ -205,8 +208,12 @@ class PureCartesianSparseTransformerLayer(nn.Module):
     # ------------------------------------------------------------------ graph handling
     def prepare(self, edge_src, edge_dst, edge_shifts, num_nodes, A, pos=None) -> Graph:
         """The receiver-sorted graph of one neighbour list (device op, no host synchronisation).  Reusing
-        it across calls with unchanged edges is the caller's choice (``forward_graph``)."""
-        return prepare_graph(edge_src, edge_dst, edge_shifts, num_nodes, species=A, n_species=self.n_species, pos=pos)
+        it across calls with unchanged edges is the caller's choice (``forward_graph``).  Up to 16
+        species-table rows (max_atomvalue) the atomic number is the row; a larger table is served by
+        mapping the species present (at most 16) to rows on the device."""
+        if int(num_nodes) != A.shape[0]:
+            raise ValueError(f"num_nodes {num_nodes} != len(A) {A.shape[0]}")
+        return prepare_species_graph(edge_src, edge_dst, edge_shifts, A, self.n_species, pos=pos)
 
     # ------------------------------------------------------------------ forward
     def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
@@ -243,10 +250,9 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         n, r = ops.edge_geometry(pos, shift_vec, g)
 
         conv1 = self.e3_conv_layers[0]
-        # species-table rows (atomic numbers 0..max_atomvalue-1), as atom_mlp(atom_embedding(A)) per atom
+        # species-table rows, as atom_mlp(atom_embedding(A)) per atom
         with torch.no_grad():
-            rows = torch.arange(self.n_species, device=pos.device)
-            atab = conv1.atom_table(rows).to(dtype)
+            atab = conv1.atom_table(species_rows(g, pos.device)).to(dtype)
             mf, mb = torch.ops.fsctep.sparse_conv1_pair_table(conv1.fc[4].weight.detach(),
                                                               conv1.fc[4].bias.detach(), atab, self.channels)
         h1 = ops.radial_hidden(r, conv1.fc, self.max_radius, self.function_type)
@@ -255,7 +261,7 @@ class PureCartesianSparseTransformerLayer(nn.Module):
             bk1, bk6 = conv.prepared_weights()
             h = ops.radial_hidden(r, conv.fc, self.max_radius, self.function_type)
             feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, self._precision_code()))
-        return poison_invalid(self.readout(feats), g)
+        return poison_invalid(self.readout(feats), g, pos)
 
     def _precision_code(self) -> int:
         prec = getattr(self, "channel_mix_precision", "fp32")

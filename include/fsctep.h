@@ -229,7 +229,8 @@ int fsc_edge_vec_geometry_backward(int64_t n_edges, const float* grad_n, const f
  * models/pure_cartesian_sparse_layers.py:204-210,319-321,372-378,410-412,
  * models/pure_cartesian_ictd_layers_full.py:277-283,464-465,693-699,930-937):
  * h = silu(w2 silu(w0 emb(r) + b0) + b2), emb = soft_one_hot_linspace(r, 0, r_cut, n_basis, basis,
- * cutoff=True) * sqrt(n_basis); basis 0 = bessel, 1 = gaussian; weights in torch Linear layout
+ * cutoff=True) * sqrt(n_basis); basis 0 = bessel, 1 = gaussian, 2 = fourier, 3 = cosine,
+ * 4 = smooth_finite; weights in torch Linear layout
  * (w0 [64][n_basis], w2 [64][64]).  With w4 == NULL the output is h [E][64] (the sparse trunk's
  * fc[:4]); with w4 [n_out][64], b4 [n_out] (n_out <= 64) it is w4 h + b4 [E][n_out] (the ICTD gates,
  * the whole fc).  The backward gives grad_r [E] from grad_out (activations recomputed). */

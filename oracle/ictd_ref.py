@@ -233,7 +233,8 @@ def split_keys(x: torch.Tensor, C: int, keys) -> dict:
 
 
 def merge_keys(blocks: dict, keys) -> torch.Tensor:
-    return torch.cat([blocks[k].reshape(*blocks[k].shape[:-2], -1) for k in keys], dim=-1)
+    return torch.cat([blocks[k].reshape(*blocks[k].shape[:-2], blocks[k].shape[-2] * blocks[k].shape[-1])
+                      for k in keys], dim=-1)
 
 
 def radial_embedding(r, cfg):

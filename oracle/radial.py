@@ -21,7 +21,7 @@ import torch
 
 def soft_one_hot_linspace(x: torch.Tensor, start: float, end: float, number: int,
                           basis: str, cutoff: bool) -> torch.Tensor:
-    """``(..., number)`` basis values of ``x``; e3nn semantics for gaussian/bessel/cosine/fourier."""
+    """``(..., number)`` basis values of ``x``; e3nn semantics for gaussian/bessel/cosine/fourier/smooth_finite."""
     if cutoff:
         values = torch.linspace(start, end, number + 2, dtype=x.dtype, device=x.device)
         step = values[1] - values[0]
@@ -35,6 +35,15 @@ def soft_one_hot_linspace(x: torch.Tensor, start: float, end: float, number: int
     if basis == "cosine":
         diff = (x[..., None] - values) / step
         return torch.cos(math.pi / 2 * diff) * (diff < 1) * (-1 < diff)
+    if basis == "smooth_finite":
+        # soft_unit_step(x) = exp(-1/x) for x > 0, else 0
+        diff = (x[..., None] - values) / step
+
+        def sus(v):
+            return torch.where(v > 0, torch.exp(-1.0 / torch.where(v > 0, v, torch.ones_like(v))),
+                               torch.zeros_like(v))
+
+        return 1.14136 * math.exp(2.0) * sus(diff + 1) * sus(1 - diff)
     if basis == "fourier":
         u = (x[..., None] - start) / (end - start)
         if not cutoff:

@@ -25,7 +25,9 @@ def _hidden_ref(r, w0, b0, w2, b2, rc, nb, basis):
     return F.silu(F.silu(emb @ w0.T + b0) @ w2.T + b2)
 
 
-@pytest.mark.parametrize("basis,nb", [("bessel", 8), ("gaussian", 8), ("bessel", 5), ("gaussian", 3), ("bessel", 16)])
+@pytest.mark.parametrize("basis,nb", [("bessel", 8), ("gaussian", 8), ("bessel", 5), ("gaussian", 3), ("bessel", 16),
+                                      ("fourier", 8), ("cosine", 8), ("smooth_finite", 8), ("cosine", 5),
+                                      ("smooth_finite", 16)])
 def test_radial_mlp_matches_torch(basis, nb):
     from fsctep_amd import ops
     g = torch.Generator().manual_seed(nb + 100 * len(basis))
@@ -45,8 +47,15 @@ def test_radial_mlp_matches_torch(basis, nb):
     href = _hidden_ref(rr, w0, b0, w2, b2, rc, nb, basis)
     (grr,) = torch.autograd.grad(href, rr, dh)
     assert rel(h, href) < 1e-5
-    # d/dr of the basis: relative to the largest entry; near r -> 0 the Bessel slope is large
-    assert rel(gr, grr) < 1e-5
+    # d/dr of the basis: relative to the largest entry; near r -> 0 the Bessel slope is large.  The cosine
+    # bumps have a kink one step from their centre (slope pi/(2 step) inside, 0 outside): points within
+    # 1e-5 steps of a kink fall on either side in fp32 and fp64, so they are left out of the slope check.
+    keep = torch.ones(E, dtype=torch.bool)
+    if basis == "cosine":
+        step = rc / (nb + 1)
+        d = (r[:, None] - step * torch.arange(1, nb + 1, dtype=torch.float64)) / step
+        keep = ((d.abs() - 1).abs() > 1e-5).all(1)
+    assert rel(gr.cpu()[keep], grr[keep]) < 1e-5
 
 
 @pytest.mark.parametrize("P", [23, 17, 64, 1])
