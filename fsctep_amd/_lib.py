@@ -69,6 +69,10 @@ SIGNATURES = {
     "fsc_bucket_mix_transpose_w": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p, _p],
     "fsc_bucket_mix_transpose_g": [_i64] + [_i32] * 4 + [_p] * 4 + [_i32, _p],
 }
+# the fp64 twins of the bucket functions take the same arguments (double arrays)
+SIGNATURES.update({n + "_f64": SIGNATURES[n] for n in (
+    "fsc_bucket_project", "fsc_bucket_project_transpose_a", "fsc_bucket_project_transpose_vu", "fsc_bucket_mix",
+    "fsc_bucket_mix_transpose_y", "fsc_bucket_mix_transpose_w", "fsc_bucket_mix_transpose_g")})
 
 _lib = None
 

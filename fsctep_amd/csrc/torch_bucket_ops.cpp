@@ -4,8 +4,9 @@
 // fsc_bucket_*).  Each call allocates its outputs, as the reference's do, and launches on the current
 // stream (the reference's extension uses the default stream, csrc/ictd_tp_cuda.cu:178).  Argument errors
 // raise RuntimeError with the reference's messages (csrc/ictd_tp.cpp:78-105).  The HIP path takes what the
-// reference's CUDA path takes, mul_in2 == 1, in fp32; other arguments raise (the reference falls back to
-// ATen for them, its double-backward functions raise likewise without CUDA).  The double-backward
+// reference's CUDA path takes, mul_in2 == 1, in fp32 or fp64 (csrc/ictd_tp_cuda.cu:1230-1236 dispatches
+// both; the fp64 calls go to the fsc_bucket_*_f64 kernels); other arguments raise (the reference falls back
+// to ATen for them, its double-backward functions raise likewise without CUDA).  The double-backward
 // functions are the sums of csrc/ictd_tp_cuda.cu:528-533 and 796-802, formed by the same kernels
 // accumulating into one output.
 
@@ -23,10 +24,15 @@ hipStream_t stream_of(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.
 
 void check(int rc, const char* name) { TORCH_CHECK(rc == 0, name, " failed (", rc, "): ", fsc_last_error()); }
 
-void gpu_f32(std::initializer_list<std::reference_wrapper<const Tensor>> ts, const char* name) {
+// every argument on the GPU, float32 or float64, all of one dtype
+void gpu_float(std::initializer_list<std::reference_wrapper<const Tensor>> ts, const char* name) {
+  const at::ScalarType st = ts.begin()->get().scalar_type();
   for (const Tensor& t : ts) {
     TORCH_CHECK(t.is_cuda(), name, ": the HIP kernels take GPU tensors, got a ", t.device(), " tensor");
-    TORCH_CHECK(t.scalar_type() == at::kFloat, name, ": the HIP kernels take float32, got ", t.scalar_type());
+    TORCH_CHECK(t.scalar_type() == at::kFloat || t.scalar_type() == at::kDouble, name,
+                ": the HIP kernels take float32 or float64, got ", t.scalar_type());
+    TORCH_CHECK(t.scalar_type() == st, name, ": all arguments must have one dtype, got ", st, " and ",
+                t.scalar_type());
   }
 }
 
@@ -35,8 +41,45 @@ void mul_in2_one(int64_t mul_in2, const char* name) {
               " is not supported (the HIP kernels, like the reference's CUDA kernels, take mul_in2 == 1)");
 }
 
-const float* cp(const Tensor& t) { return t.numel() ? t.data_ptr<float>() : nullptr; }
-float* mp(Tensor& t) { return t.numel() ? t.data_ptr<float>() : nullptr; }
+template <typename T>
+const T* cp(const Tensor& t) {
+  return t.numel() ? t.data_ptr<T>() : nullptr;
+}
+template <typename T>
+T* mp(Tensor& t) {
+  return t.numel() ? t.data_ptr<T>() : nullptr;
+}
+
+// The C ABI by element type (fsc_bucket_<op> for float, fsc_bucket_<op>_f64 for double).
+#define FSC_ABI_PAIR(NAME, PARAMS, ARGS)                                                                        \
+  inline int abi_##NAME(PARAMS(float)) { return fsc_bucket_##NAME ARGS; }                                     \
+  inline int abi_##NAME(PARAMS(double)) { return fsc_bucket_##NAME##_f64 ARGS; }
+#define P_PROJECT(T) int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K, const T* a, const T* v, \
+                     const T* u, T* y, int32_t acc, hipStream_t st
+FSC_ABI_PAIR(project, P_PROJECT, (B, I, m1, m2, P, K, a, v, u, y, acc, st))
+FSC_ABI_PAIR(project_transpose_a, P_PROJECT, (B, I, m1, m2, P, K, a, v, u, y, acc, st))
+#define P_PROJECT_VU(T) int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K, const T* gy, const T* a, \
+                        const T* v, const T* u, T* gv, T* gu, int32_t acc, T* ws, hipStream_t st
+FSC_ABI_PAIR(project_transpose_vu, P_PROJECT_VU, (B, I, m1, m2, P, K, gy, a, v, u, gv, gu, acc, ws, st))
+#define P_MIX(T) int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const T* x, const T* w, const T* g, T* out, \
+                 int32_t acc, hipStream_t st
+FSC_ABI_PAIR(mix, P_MIX, (B, P, K, I, O, x, w, g, out, acc, st))
+FSC_ABI_PAIR(mix_transpose_g, P_MIX, (B, P, K, I, O, x, w, g, out, acc, st))
+#define P_MIX_WS(T) int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const T* x, const T* w, const T* g, \
+                    T* out, int32_t acc, T* ws, hipStream_t st
+FSC_ABI_PAIR(mix_transpose_y, P_MIX_WS, (B, P, K, I, O, x, w, g, out, acc, ws, st))
+FSC_ABI_PAIR(mix_transpose_w, P_MIX_WS, (B, P, K, I, O, x, w, g, out, acc, ws, st))
+#undef FSC_ABI_PAIR
+
+// runs the statements with T the element type of t (float or double)
+#define BY_DTYPE(t, ...)                      \
+  if ((t).scalar_type() == at::kDouble) {     \
+    using T = double;                         \
+    __VA_ARGS__;                              \
+  } else {                                    \
+    using T = float;                          \
+    __VA_ARGS__;                              \
+  }
 
 // csrc/ictd_tp.cpp:78-91
 void check_projection_args(const Tensor& a, const Tensor& b, const Tensor& u) {
@@ -73,16 +116,18 @@ struct Proj {
 
 void pf(const Proj& s, const Tensor& a, const Tensor& b, const Tensor& u, Tensor& y, int acc) {
   const Tensor ac = a.contiguous(), bc = b.contiguous(), uc = u.contiguous();
-  check(fsc_bucket_project(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K, cp(ac), cp(bc),
-                           cp(uc), mp(y), acc, stream_of(y)),
-        "project_bucket_forward");
+  BY_DTYPE(y,
+    check(abi_project(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K, cp<T>(ac),
+                      cp<T>(bc), cp<T>(uc), mp<T>(y), acc, stream_of(y)),
+          "project_bucket_forward"))
 }
 
 void pat(const Proj& s, const Tensor& gy, const Tensor& b, const Tensor& u, Tensor& ga, int acc) {
   const Tensor gc = gy.contiguous(), bc = b.contiguous(), uc = u.contiguous();
-  check(fsc_bucket_project_transpose_a(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K,
-                                       cp(gc), cp(bc), cp(uc), mp(ga), acc, stream_of(ga)),
-        "project_bucket_transpose_a");
+  BY_DTYPE(ga,
+    check(abi_project_transpose_a(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K,
+                                  cp<T>(gc), cp<T>(bc), cp<T>(uc), mp<T>(ga), acc, stream_of(ga)),
+          "project_bucket_transpose_a"))
 }
 
 // grad_b (gb) and/or grad_u (gu), either undefined
@@ -97,11 +142,12 @@ void pvu(const Proj& s, const Tensor& gy, const Tensor& a, const Tensor& b, cons
           "project_bucket_transpose_u");
     ws = at::empty({std::max<int64_t>(n, 1)}, gy.options());
   }
-  check(fsc_bucket_project_transpose_vu(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K,
-                                        cp(gc), cp(ac), bc.defined() ? cp(bc) : nullptr, uc.defined() ? cp(uc) : nullptr,
-                                        gb ? mp(*gb) : nullptr, gu ? mp(*gu) : nullptr, acc,
-                                        gu ? mp(ws) : nullptr, stream_of(gy)),
-        gb ? "project_bucket_transpose_b" : "project_bucket_transpose_u");
+  BY_DTYPE(gy,
+    check(abi_project_transpose_vu(s.B, (int32_t)s.I, (int32_t)s.m1, (int32_t)s.m2, (int32_t)s.P, (int32_t)s.K,
+                                   cp<T>(gc), cp<T>(ac), bc.defined() ? cp<T>(bc) : nullptr,
+                                   uc.defined() ? cp<T>(uc) : nullptr, gb ? mp<T>(*gb) : nullptr,
+                                   gu ? mp<T>(*gu) : nullptr, acc, gu ? mp<T>(ws) : nullptr, stream_of(gy)),
+          gb ? "project_bucket_transpose_b" : "project_bucket_transpose_u"))
 }
 
 // ---------------------------------------------------------------- mix primitives
@@ -113,9 +159,10 @@ Mix mix_sizes(const Tensor& y, const Tensor& w) { return Mix{y.size(0), y.size(1
 
 void mf(const Mix& s, const Tensor& y, const Tensor& w, const Tensor& g, Tensor& out, int acc) {
   const Tensor yc = y.contiguous(), wc = w.contiguous(), gc = g.contiguous();
-  check(fsc_bucket_mix(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp(yc), cp(wc), cp(gc), mp(out), acc,
-                       stream_of(out)),
-        "mix_bucket_forward");
+  BY_DTYPE(out,
+    check(abi_mix(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp<T>(yc), cp<T>(wc), cp<T>(gc),
+                  mp<T>(out), acc, stream_of(out)),
+          "mix_bucket_forward"))
 }
 
 Tensor mix_ws(const Mix& s, const Tensor& like) {
@@ -127,24 +174,27 @@ Tensor mix_ws(const Mix& s, const Tensor& like) {
 void myt(const Mix& s, const Tensor& go, const Tensor& w, const Tensor& g, Tensor& gy, int acc) {
   const Tensor oc = go.contiguous(), wc = w.contiguous(), gc = g.contiguous();
   Tensor ws = at::empty({std::max<int64_t>(s.P * s.O * s.I, 1)}, go.options());   // the transposed weights
-  check(fsc_bucket_mix_transpose_y(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp(oc), cp(wc), cp(gc),
-                                   mp(gy), acc, mp(ws), stream_of(gy)),
-        "mix_bucket_transpose_y");
+  BY_DTYPE(gy,
+    check(abi_mix_transpose_y(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp<T>(oc), cp<T>(wc),
+                              cp<T>(gc), mp<T>(gy), acc, mp<T>(ws), stream_of(gy)),
+          "mix_bucket_transpose_y"))
 }
 
 void mwt(const Mix& s, const Tensor& go, const Tensor& y, const Tensor& g, Tensor& gw, int acc) {
   const Tensor oc = go.contiguous(), yc = y.contiguous(), gc = g.contiguous();
   Tensor ws = mix_ws(s, go);
-  check(fsc_bucket_mix_transpose_w(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp(oc), cp(yc), cp(gc),
-                                   mp(gw), acc, mp(ws), stream_of(gw)),
-        "mix_bucket_transpose_w");
+  BY_DTYPE(gw,
+    check(abi_mix_transpose_w(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp<T>(oc), cp<T>(yc),
+                              cp<T>(gc), mp<T>(gw), acc, mp<T>(ws), stream_of(gw)),
+          "mix_bucket_transpose_w"))
 }
 
 void mgt(const Mix& s, const Tensor& go, const Tensor& y, const Tensor& w, Tensor& gg, int acc) {
   const Tensor oc = go.contiguous(), yc = y.contiguous(), wc = w.contiguous();
-  check(fsc_bucket_mix_transpose_g(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp(oc), cp(yc), cp(wc),
-                                   mp(gg), acc, stream_of(gg)),
-        "mix_bucket_transpose_g");
+  BY_DTYPE(gg,
+    check(abi_mix_transpose_g(s.B, (int32_t)s.P, (int32_t)s.K, (int32_t)s.I, (int32_t)s.O, cp<T>(oc), cp<T>(yc),
+                              cp<T>(wc), mp<T>(gg), acc, stream_of(gg)),
+          "mix_bucket_transpose_g"))
 }
 
 // ---------------------------------------------------------------- the reference's functions
@@ -152,7 +202,7 @@ Tensor project_bucket_forward(const Tensor& a, const Tensor& b, const Tensor& u,
   check_projection_args(a, b, u);
   TORCH_CHECK(num_paths > 0, "num_paths must be positive");
   TORCH_CHECK(u.size(1) % num_paths == 0, "u_bucket second dim must be divisible by num_paths");
-  gpu_f32({a, b, u}, "project_bucket_forward");
+  gpu_float({a, b, u}, "project_bucket_forward");
   mul_in2_one(b.size(1), "project_bucket_forward");
   const Proj s{a.size(0), a.size(1), a.size(2), b.size(2), num_paths, u.size(1) / num_paths};
   Tensor y = at::empty({s.B, s.P, s.K, s.I}, a.options());
@@ -174,7 +224,7 @@ Tensor project_bucket_transpose_a(const Tensor& grad_y, const Tensor& b, const T
   const int64_t m2 = b.size(2), m1 = u.size(0) / std::max<int64_t>(m2, 1);
   TORCH_CHECK(m1 * m2 == u.size(0), "u_bucket first dim must factor into m1*m2");
   TORCH_CHECK(u.size(1) == grad_y.size(1) * grad_y.size(2), "u_bucket second dim must equal P*kdim");
-  gpu_f32({grad_y, b, u}, "project_bucket_transpose_a");
+  gpu_float({grad_y, b, u}, "project_bucket_transpose_a");
   mul_in2_one(b.size(1), "project_bucket_transpose_a");
   const Proj s = proj_from_grad(grad_y, grad_y.size(3), m1, m2);
   Tensor ga = at::empty({s.B, s.I, m1}, grad_y.options());
@@ -191,7 +241,7 @@ Tensor project_bucket_transpose_b(const Tensor& grad_y, const Tensor& a, const T
   const int64_t m1 = a.size(2), m2 = u.size(0) / std::max<int64_t>(m1, 1);
   TORCH_CHECK(m1 * m2 == u.size(0), "u_bucket first dim must factor into m1*m2");
   TORCH_CHECK(u.size(1) == grad_y.size(1) * grad_y.size(2), "u_bucket second dim must equal P*kdim");
-  gpu_f32({grad_y, a, u}, "project_bucket_transpose_b");
+  gpu_float({grad_y, a, u}, "project_bucket_transpose_b");
   mul_in2_one(grad_y.size(3) / a.size(1), "project_bucket_transpose_b");
   const Proj s = proj_from_grad(grad_y, a.size(1), m1, m2);
   Tensor gb = at::empty({s.B, 1, m2}, grad_y.options());
@@ -207,7 +257,7 @@ Tensor project_bucket_transpose_u(const Tensor& grad_y, const Tensor& a, const T
   TORCH_CHECK(grad_y.dim() == 4 && grad_y.size(0) == a.size(0) && b.size(0) == a.size(0) &&
                   grad_y.size(3) == a.size(1) * b.size(1),
               "grad_y must have shape (B, P, kdim, mul_in1*mul_in2)");
-  gpu_f32({grad_y, a, b}, "project_bucket_transpose_u");
+  gpu_float({grad_y, a, b}, "project_bucket_transpose_u");
   mul_in2_one(b.size(1), "project_bucket_transpose_u");
   const Proj s = proj_from_grad(grad_y, a.size(1), a.size(2), b.size(2));
   Tensor gu = at::empty({s.m1 * s.m2, s.P * s.K}, grad_y.options());
@@ -217,7 +267,7 @@ Tensor project_bucket_transpose_u(const Tensor& grad_y, const Tensor& a, const T
 
 Tensor mix_bucket_forward(const Tensor& y, const Tensor& w, const Tensor& gates) {
   check_mix_args(y, w, gates);
-  gpu_f32({y, w, gates}, "mix_bucket_forward");
+  gpu_float({y, w, gates}, "mix_bucket_forward");
   const Mix s = mix_sizes(y, w);
   Tensor out = at::empty({s.B, s.O, s.K}, y.options());
   mf(s, y, w, gates, out, 0);
@@ -230,7 +280,7 @@ Tensor mix_bucket_transpose_y(const Tensor& grad_out, const Tensor& w, const Ten
   TORCH_CHECK(gates.dim() == 2, "gates must have shape (B, P)");
   TORCH_CHECK(w.size(1) == grad_out.size(1), "w output dim must match grad_out");
   TORCH_CHECK(gates.size(0) == grad_out.size(0) && gates.size(1) == w.size(0), "gates must match grad_out and w");
-  gpu_f32({grad_out, w, gates}, "mix_bucket_transpose_y");
+  gpu_float({grad_out, w, gates}, "mix_bucket_transpose_y");
   const Mix s{grad_out.size(0), w.size(0), grad_out.size(2), w.size(2), w.size(1)};
   Tensor gy = at::empty({s.B, s.P, s.K, s.I}, grad_out.options());
   myt(s, grad_out, w, gates, gy, 0);
@@ -244,7 +294,7 @@ Tensor mix_bucket_transpose_w(const Tensor& grad_out, const Tensor& y, const Ten
   TORCH_CHECK(y.size(0) == gates.size(0), "gates batch dim must match y");
   TORCH_CHECK(y.size(1) == gates.size(1), "gates path dim must match y");
   TORCH_CHECK(grad_out.size(0) == y.size(0) && grad_out.size(2) == y.size(2), "grad_out must match y");
-  gpu_f32({grad_out, y, gates}, "mix_bucket_transpose_w");
+  gpu_float({grad_out, y, gates}, "mix_bucket_transpose_w");
   const Mix s{y.size(0), y.size(1), y.size(2), y.size(3), grad_out.size(1)};
   Tensor gw = at::empty({s.P, s.O, s.I}, y.options());
   mwt(s, grad_out, y, gates, gw, 0);
@@ -258,7 +308,7 @@ Tensor mix_bucket_transpose_g(const Tensor& grad_out, const Tensor& y, const Ten
   TORCH_CHECK(grad_out.size(0) == y.size(0) && grad_out.size(2) == y.size(2), "grad_out must match y");
   TORCH_CHECK(w.size(0) == y.size(1) && w.size(1) == grad_out.size(1) && w.size(2) == y.size(3),
               "w must match y and grad_out");
-  gpu_f32({grad_out, y, w}, "mix_bucket_transpose_g");
+  gpu_float({grad_out, y, w}, "mix_bucket_transpose_g");
   const Mix s = mix_sizes(y, w);
   Tensor gg = at::empty({s.B, s.P}, y.options());
   mgt(s, grad_out, y, w, gg, 0);
@@ -281,7 +331,7 @@ Tensor project_dbl_bwd_grad_h(const Tensor& a, const Tensor& gga, const Tensor& 
   check_projection_args(a, b, u);
   check_projection_args(gga, ggb, ggu);
   TORCH_CHECK(num_paths > 0 && u.size(1) % num_paths == 0, "u_bucket second dim must be divisible by num_paths");
-  gpu_f32({a, gga, b, ggb, u, ggu}, "project_dbl_bwd_grad_h");
+  gpu_float({a, gga, b, ggb, u, ggu}, "project_dbl_bwd_grad_h");
   mul_in2_one(b.size(1), "project_dbl_bwd_grad_h");
   const Proj s{a.size(0), a.size(1), a.size(2), b.size(2), num_paths, u.size(1) / num_paths};
   Tensor out = at::empty({s.B, s.P, s.K, s.I}, a.options());
@@ -296,7 +346,7 @@ Tensor project_dbl_bwd_grad_a(const Tensor& h, const Tensor& b, const Tensor& gg
   Tensor out = project_bucket_transpose_a(h, ggb, u);
   const Proj s = proj_from_grad(h, h.size(3), out.size(2), b.size(2));
   TORCH_CHECK(b.sizes() == ggb.sizes() && u.sizes() == ggu.sizes(), "b/ggb and u/ggu must have the same shapes");
-  gpu_f32({b, ggu}, "project_dbl_bwd_grad_a");
+  gpu_float({b, ggu}, "project_dbl_bwd_grad_a");
   pat(s, h, b, ggu, out, 1);
   return out;
 }
@@ -306,7 +356,7 @@ Tensor project_dbl_bwd_grad_b(const Tensor& h, const Tensor& a, const Tensor& gg
   Tensor out = project_bucket_transpose_b(h, gga, u);
   const Proj s = proj_from_grad(h, a.size(1), a.size(2), out.size(2));
   TORCH_CHECK(a.sizes() == gga.sizes() && u.sizes() == ggu.sizes(), "a/gga and u/ggu must have the same shapes");
-  gpu_f32({a, ggu}, "project_dbl_bwd_grad_b");
+  gpu_float({a, ggu}, "project_dbl_bwd_grad_b");
   pvu(s, h, a, Tensor(), ggu, &out, nullptr, 1);
   return out;
 }
@@ -315,7 +365,7 @@ Tensor project_dbl_bwd_grad_b(const Tensor& h, const Tensor& a, const Tensor& gg
 Tensor project_dbl_bwd_grad_u(const Tensor& h, const Tensor& a, const Tensor& gga, const Tensor& b, const Tensor& ggb) {
   Tensor out = project_bucket_transpose_u(h, gga, b);
   TORCH_CHECK(a.sizes() == gga.sizes() && b.sizes() == ggb.sizes(), "a/gga and b/ggb must have the same shapes");
-  gpu_f32({a, ggb}, "project_dbl_bwd_grad_u");
+  gpu_float({a, ggb}, "project_dbl_bwd_grad_u");
   const Proj s = proj_from_grad(h, a.size(1), a.size(2), b.size(2));
   pvu(s, h, a, ggb, Tensor(), nullptr, &out, 1);
   return out;
@@ -326,7 +376,7 @@ Tensor mix_dbl_bwd_grad_g_out(const Tensor& y, const Tensor& ggy, const Tensor& 
                               const Tensor& gates, const Tensor& ggg) {
   Tensor out = mix_bucket_forward(ggy, w, gates);
   check_mix_args(y, ggw, ggg);
-  gpu_f32({y, ggw, ggg}, "mix_dbl_bwd_grad_g_out");
+  gpu_float({y, ggw, ggg}, "mix_dbl_bwd_grad_g_out");
   TORCH_CHECK(y.sizes() == ggy.sizes() && w.sizes() == ggw.sizes() && gates.sizes() == ggg.sizes(),
               "y/ggy, w/ggw and gates/ggg must have the same shapes");
   const Mix s = mix_sizes(y, w);
@@ -340,7 +390,7 @@ Tensor mix_dbl_bwd_grad_y(const Tensor& g_out, const Tensor& w, const Tensor& gg
                           const Tensor& ggg) {
   Tensor out = mix_bucket_transpose_y(g_out, ggw, gates);
   TORCH_CHECK(w.sizes() == ggw.sizes() && gates.sizes() == ggg.sizes(), "w/ggw and gates/ggg must have the same shapes");
-  gpu_f32({w, ggg}, "mix_dbl_bwd_grad_y");
+  gpu_float({w, ggg}, "mix_dbl_bwd_grad_y");
   const Mix s{g_out.size(0), w.size(0), g_out.size(2), w.size(2), w.size(1)};
   myt(s, g_out, w, ggg, out, 1);
   return out;
@@ -351,7 +401,7 @@ Tensor mix_dbl_bwd_grad_w(const Tensor& g_out, const Tensor& y, const Tensor& gg
                           const Tensor& ggg) {
   Tensor out = mix_bucket_transpose_w(g_out, ggy, gates);
   TORCH_CHECK(y.sizes() == ggy.sizes() && gates.sizes() == ggg.sizes(), "y/ggy and gates/ggg must have the same shapes");
-  gpu_f32({y, ggg}, "mix_dbl_bwd_grad_w");
+  gpu_float({y, ggg}, "mix_dbl_bwd_grad_w");
   const Mix s{y.size(0), y.size(1), y.size(2), y.size(3), g_out.size(1)};
   mwt(s, g_out, y, ggg, out, 1);
   return out;
@@ -361,7 +411,7 @@ Tensor mix_dbl_bwd_grad_w(const Tensor& g_out, const Tensor& y, const Tensor& gg
 Tensor mix_dbl_bwd_grad_g(const Tensor& g_out, const Tensor& y, const Tensor& ggy, const Tensor& w, const Tensor& ggw) {
   Tensor out = mix_bucket_transpose_g(g_out, ggy, w);
   TORCH_CHECK(y.sizes() == ggy.sizes() && w.sizes() == ggw.sizes(), "y/ggy and w/ggw must have the same shapes");
-  gpu_f32({y, ggw}, "mix_dbl_bwd_grad_g");
+  gpu_float({y, ggw}, "mix_dbl_bwd_grad_g");
   const Mix s = mix_sizes(y, w);
   mgt(s, g_out, y, ggw, out, 1);
   return out;

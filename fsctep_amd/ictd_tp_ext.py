@@ -11,8 +11,9 @@ reference imports it::
     from fsctep_amd import ictd_tp_ext
     ictd_tp_ext.install()   # sys.modules["molecular_force_field._C_ictd_tp"] = ictd_tp_ext
 
-The kernels take what the reference's CUDA kernels take: GPU float32 tensors with mul_in2 == 1 (the
-trunks' conv2..n). Other arguments raise RuntimeError; there is no CPU path.
+The kernels take what the reference's CUDA kernels take (csrc/ictd_tp_cuda.cu:1230-1236): GPU float32 or
+float64 tensors, all of one dtype, with mul_in2 == 1 (the trunks' conv2..n).  Other arguments raise
+RuntimeError; there is no CPU path.
 """
 
 from __future__ import annotations

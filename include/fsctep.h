@@ -336,7 +336,9 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
 /* ------------------------------------------------------------------ per-edge (bucketed) ICTD TP
  * The operations of the reference's native extension molecular_force_field._C_ictd_tp
  * (csrc/ictd_tp.cpp:498-522; einsum semantics models/ictd_irreps_cuda.py:169-288), for the arguments its
- * CUDA path takes: fp32, mul_in2 == 1.  B batch (edges), I = mul_in1, O = mul_out, K = kdim, P paths.
+ * CUDA path takes: fp32 and fp64 (csrc/ictd_tp_cuda.cu:1230-1236 dispatches both), mul_in2 == 1.  The
+ * functions below take float arrays; each has an fp64 twin of the same name with the suffix _f64 and
+ * double arrays (declared after them).  B batch (edges), I = mul_in1, O = mul_out, K = kdim, P paths.
  *   project:  y[b][p][k][i] = sum_{m,n} a[b][i][m] v[b][n] u[m*m2+n][p*K+k]
  *   mix:      out[b][o][k]  = sum_p gates[b][p] sum_i y[b][p][k][i] w[p][o][i]
  * Layouts: a [B][I][m1], v [B][1][m2], u [m1*m2][P*K], y [B][P][K][I], w [P][O][I], gates [B][P],
@@ -351,7 +353,8 @@ int fsc_bucket_project(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, 
 int fsc_bucket_project_transpose_a(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
                                    const float* grad_y, const float* v, const float* u, float* grad_a,
                                    int32_t accumulate, hipStream_t stream);
-/* Floats of the workspace of fsc_bucket_project_transpose_vu when grad_u is requested. */
+/* Elements (float or double, as the op) of the workspace of fsc_bucket_project_transpose_vu[_f64] when
+ * grad_u is requested. */
 int fsc_bucket_project_workspace(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
                                  int64_t* workspace_floats);
 /* project_bucket_transpose_b and _u (csrc/ictd_tp.cpp:210-269): grad_v [B][1][m2] and/or grad_u
@@ -363,8 +366,8 @@ int fsc_bucket_project_transpose_vu(int64_t B, int32_t I, int32_t m1, int32_t m2
 /* mix_bucket_forward (csrc/ictd_tp.cpp:271-294): out from y, w, gates. */
 int fsc_bucket_mix(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* y, const float* w,
                    const float* gates, float* out, int32_t accumulate, hipStream_t stream);
-/* Floats of the workspace of fsc_bucket_mix_transpose_w (per-split partial sums; fsc_bucket_mix_transpose_y
- * needs only P*O*I floats, the transposed weights). */
+/* Elements of the workspace of fsc_bucket_mix_transpose_w[_f64] (per-split partial sums;
+ * fsc_bucket_mix_transpose_y[_f64] needs only P*O*I elements, the transposed weights). */
 int fsc_bucket_mix_workspace(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, int64_t* workspace_floats);
 /* mix_bucket_transpose_y (csrc/ictd_tp.cpp:296-322): grad_y [B][P][K][I] from grad_out, w, gates. */
 int fsc_bucket_mix_transpose_y(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
@@ -378,6 +381,28 @@ int fsc_bucket_mix_transpose_w(int64_t B, int32_t P, int32_t K, int32_t I, int32
 int fsc_bucket_mix_transpose_g(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const float* grad_out,
                                const float* y, const float* w, float* grad_gates, int32_t accumulate,
                                hipStream_t stream);
+/* fp64 twins of the seven functions above (the same reference functions for float64 tensors; mixes on
+ * v_mfma_f64_16x16x4_f64). */
+int fsc_bucket_project_f64(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K, const double* a,
+                           const double* v, const double* u, double* y, int32_t accumulate, hipStream_t stream);
+int fsc_bucket_project_transpose_a_f64(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
+                                       const double* grad_y, const double* v, const double* u, double* grad_a,
+                                       int32_t accumulate, hipStream_t stream);
+int fsc_bucket_project_transpose_vu_f64(int64_t B, int32_t I, int32_t m1, int32_t m2, int32_t P, int32_t K,
+                                        const double* grad_y, const double* a, const double* v, const double* u,
+                                        double* grad_v, double* grad_u, int32_t accumulate, double* workspace,
+                                        hipStream_t stream);
+int fsc_bucket_mix_f64(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const double* y, const double* w,
+                       const double* gates, double* out, int32_t accumulate, hipStream_t stream);
+int fsc_bucket_mix_transpose_y_f64(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const double* grad_out,
+                                   const double* w, const double* gates, double* grad_y, int32_t accumulate,
+                                   double* workspace, hipStream_t stream);
+int fsc_bucket_mix_transpose_w_f64(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const double* grad_out,
+                                   const double* y, const double* gates, double* grad_w, int32_t accumulate,
+                                   double* workspace, hipStream_t stream);
+int fsc_bucket_mix_transpose_g_f64(int64_t B, int32_t P, int32_t K, int32_t I, int32_t O, const double* grad_out,
+                                   const double* y, const double* w, double* grad_gates, int32_t accumulate,
+                                   hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Readout invariant Gram bilinear: out[n][o] = sum_{i,j} W[o][i][j] G_n[i][j],

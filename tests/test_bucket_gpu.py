@@ -1,9 +1,11 @@
 """The per-edge (bucketed) ICTD operations under the reference extension's names
 (molecular_force_field._C_ictd_tp, csrc/ictd_tp.cpp:498-522), run through fsctep_amd.ictd_tp_ext on the
-HIP kernels, against the fp64 oracle (oracle/ictd_bucket_ref.py, pinned in tests/test_oracle_bucket.py).
-Tolerance: max-norm relative error 1e-5 per output (fp32 products, fp32 sums).  Also: summed over the
-bucket table the ops reproduce the trunk's fully connected TP (oracle fctp); argument errors; an empty
-batch; bitwise-deterministic batch sums; the module passes the reference's availability probe."""
+HIP kernels, against the fp64 oracle (oracle/ictd_bucket_ref.py, pinned in tests/test_oracle_bucket.py),
+in float32 and float64 (the reference's kernels dispatch both, csrc/ictd_tp_cuda.cu:1230-1236).
+Tolerance: max-norm relative error per output, 1e-5 in float32 (fp32 products and sums) and 1e-10 in
+float64 (the reference's fp64 rtol, test/test_ictd_tp_backend.py:383-714).  Also: summed over the bucket
+table the ops reproduce the trunk's fully connected TP (oracle fctp); argument errors; an empty batch;
+bitwise-deterministic batch sums; the module passes the reference's availability probe."""
 
 import sys
 
@@ -14,7 +16,9 @@ from oracle import ictd_bucket_ref as BR
 from oracle import ictd_ref as R
 
 pytestmark = pytest.mark.gpu
-TOL = 1e-5
+TOLS = {torch.float32: 1e-5, torch.float64: 1e-10}
+DTYPES = pytest.mark.parametrize("dt", [torch.float32, torch.float64], ids=["fp32", "fp64"])
+TOL = TOLS[torch.float32]
 DEV = "cuda"
 
 
@@ -33,8 +37,8 @@ def rnd(*shape, seed):
     return torch.randn(*shape, generator=g, dtype=torch.float64)
 
 
-def gpu(t):
-    return t.to(DEV, torch.float32)
+def gpu(t, dt=torch.float32):
+    return t.to(DEV, dt)
 
 
 # (B, I, m1, m2, P, K)
@@ -45,15 +49,18 @@ MIX = [(37, 2, 3, 32, 32), (200, 1, 7, 128, 128), (50, 3, 5, 64, 144), (1, 4, 1,
        (33, 2, 9, 20, 12)]
 
 
+@DTYPES
 @pytest.mark.parametrize("case", PROJ)
-def test_projection_ops(case):
+def test_projection_ops(case, dt):
     B, I, m1, m2, P, K = case
     E = ext()
+    TOL = TOLS[dt]
+    gpu = lambda t: t.to(DEV, dt)
     s = sum(case)
     a, b, u = rnd(B, I, m1, seed=s), rnd(B, 1, m2, seed=s + 1), rnd(m1 * m2, P * K, seed=s + 2)
     gy = rnd(B, P, K, I, seed=s + 3)
     y = E.project_bucket_forward(gpu(a), gpu(b), gpu(u), P)
-    assert y.shape == (B, P, K, I)
+    assert y.shape == (B, P, K, I) and y.dtype == dt
     assert rel(y, BR.project_forward(a, b, u, P)) < TOL
     ta, tb, tu = BR.project_transpose(gy, a, b, u)
     ga = E.project_bucket_transpose_a(gpu(gy), gpu(b), gpu(u))
@@ -64,15 +71,18 @@ def test_projection_ops(case):
     assert max(errs.values()) < TOL, errs
 
 
+@DTYPES
 @pytest.mark.parametrize("case", MIX)
-def test_mix_ops(case):
+def test_mix_ops(case, dt):
     B, P, K, I, O = case
     E = ext()
+    TOL = TOLS[dt]
+    gpu = lambda t: t.to(DEV, dt)
     s = sum(case) + 1000
     y, w, g = rnd(B, P, K, I, seed=s), rnd(P, O, I, seed=s + 1), rnd(B, P, seed=s + 2)
     go = rnd(B, O, K, seed=s + 3)
     out = E.mix_bucket_forward(gpu(y), gpu(w), gpu(g))
-    assert out.shape == (B, O, K)
+    assert out.shape == (B, O, K) and out.dtype == dt
     assert rel(out, BR.mix_forward(y, w, g)) < TOL
     ty, tw, tg = BR.mix_transpose(go, y, w, g)
     gy = E.mix_bucket_transpose_y(gpu(go), gpu(w), gpu(g))
@@ -83,8 +93,11 @@ def test_mix_ops(case):
     assert max(errs.values()) < TOL, errs
 
 
-def test_bucketed_tp_forward_and_double_backward():
+@DTYPES
+def test_bucketed_tp_forward_and_double_backward(dt):
     E = ext()
+    TOL = TOLS[dt]
+    gpu = lambda t: t.to(DEV, dt)
     B, I, m1, m2, P, K, O = 90, 64, 5, 3, 2, 3, 64
     a, b, u = rnd(B, I, m1, seed=1), rnd(B, 1, m2, seed=2), rnd(m1 * m2, P * K, seed=3)
     gga, ggb, ggu = rnd(B, I, m1, seed=4), rnd(B, 1, m2, seed=5), rnd(m1 * m2, P * K, seed=6)
@@ -112,10 +125,13 @@ def test_bucketed_tp_forward_and_double_backward():
     assert max(errs) < TOL, errs
 
 
-def test_buckets_reproduce_the_fully_connected_tp():
+@DTYPES
+def test_buckets_reproduce_the_fully_connected_tp(dt):
     """The reference trunk's cuda_ext dispatch (models/ictd_irreps.py:1035-1070) over the bucket table, with
     these ops, equals the fully connected TP at C 64, lmax 3."""
     E = ext()
+    TOL = TOLS[dt]
+    gpu = lambda t: t.to(DEV, dt)
     lmax, C, n = 3, 64, 300
     keys = [(l, (-1) ** l) for l in range(lmax + 1)]
     paths = R.tp_paths(keys, keys, keys, lmax)
@@ -124,7 +140,7 @@ def test_buckets_reproduce_the_fully_connected_tp():
     W = rnd(len(paths), C, C, 1, seed=40) / C
     gates = rnd(n, len(paths), seed=41)
     ref = R.fctp(x1, x2, W, gates, paths, keys)
-    out = {k: torch.zeros(n, C, 2 * k[0] + 1, device=DEV) for k in keys}
+    out = {k: torch.zeros(n, C, 2 * k[0] + 1, device=DEV, dtype=dt) for k in keys}
     for k1, k2, k3, kdim, pidx, U in BR.buckets(paths):
         out[k3] += E.bucketed_tp_forward(gpu(x1[k1]), gpu(x2[k2]), gpu(U), gpu(W[pidx].reshape(len(pidx), C, C)),
                                          gpu(gates[:, pidx]))
@@ -135,8 +151,10 @@ def test_buckets_reproduce_the_fully_connected_tp():
 def test_argument_errors():
     E = ext()
     a, b, u = torch.randn(4, 8, 3, device=DEV), torch.randn(4, 1, 3, device=DEV), torch.randn(9, 6, device=DEV)
-    with pytest.raises(RuntimeError, match="float32"):
-        E.project_bucket_forward(a.double(), b.double(), u.double(), 2)
+    with pytest.raises(RuntimeError, match="float32 or float64"):
+        E.project_bucket_forward(a.half(), b.half(), u.half(), 2)
+    with pytest.raises(RuntimeError, match="same dtype"):
+        E.project_bucket_forward(a.double(), b, u, 2)
     with pytest.raises(RuntimeError, match="mul_in2"):
         E.project_bucket_forward(a, torch.randn(4, 2, 3, device=DEV), torch.randn(9, 6, device=DEV), 2)
     with pytest.raises(RuntimeError, match="a and b batch dimensions must match"):
@@ -165,8 +183,11 @@ def test_empty_batch():
     assert E.mix_bucket_forward(y, torch.randn(2, 4, 8, device=DEV), g).shape == (0, 4, 3)
 
 
-def test_batch_sums_are_deterministic():
+@DTYPES
+def test_batch_sums_are_deterministic(dt):
     E = ext()
+    TOL = TOLS[dt]
+    gpu = lambda t: t.to(DEV, dt)
     B, I, m1, m2, P, K, O = 5000, 64, 5, 5, 2, 5, 64
     a, b, u = gpu(rnd(B, I, m1, seed=50)), gpu(rnd(B, 1, m2, seed=51)), gpu(rnd(m1 * m2, P * K, seed=52))
     gy, g, go = gpu(rnd(B, P, K, I, seed=53)), gpu(rnd(B, P, seed=54)), gpu(rnd(B, O, K, seed=55))
