@@ -163,10 +163,11 @@ class _ICTDTrunk(nn.Module):
             raise ValueError(f"num_nodes {num_nodes} != len(A) {A.shape[0]}")
         return prepare_species_graph(edge_src, edge_dst, edge_shifts, A, self.n_species, pos=pos)
 
-    def _check_inference(self):
-        if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            raise NotImplementedError("the HIP ICTD path computes energies and forces only; call .eval() or "
-                                      ".requires_grad_(False)")
+    def _training_step(self) -> bool:
+        """True when parameter gradients are wanted (train() mode, grad enabled, parameters that require
+        grad): the step is then built from differentiable parts (fsctep_amd.train_ops and the conv2..n op
+        with its weight gradient and double backward), so that a force loss trains every parameter."""
+        return self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())
 
     def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, precomputed_edge_vec=None,
                 sync_after_scatter=None, external_tensor=None, external_tensor_blocks=None, fidelity_ids=None,
@@ -190,9 +191,10 @@ class _ICTDTrunk(nn.Module):
         runs when the model has one and ``with_dipole`` is set; it has one row per graph of ``cell`` (G, 3, 3),
         which the reference sizes as max(batch) + 1 (pure_cartesian_ictd_layers_o3.py:983): the same for
         every batch whose last graph has atoms, and read here without a host synchronisation."""
-        self._check_inference()
         if not pos.is_cuda:
             raise RuntimeError("the HIP ICTD path runs on the GPU only")
+        if self._training_step():
+            return self._forward_train(pos, batch, cell, g, external_tensor, edge_vec, with_dipole)
         f32 = torch.float32
         pos, cell = pos.to(f32), cell.to(f32)
         cg, c1_gates, factors = self._consts(pos.device)
@@ -211,25 +213,60 @@ class _ICTDTrunk(nn.Module):
             atab = c1.atom_mlp(c1.atom_embedding(species_rows(g, pos.device))).detach()
             W1 = c1.tp2.weight.detach()[c1_gates]                                  # (NP1, C, 8, 8)
             qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
-        F_in = Y
-        if self.external_field:
-            if external_tensor is None:
-                raise ValueError("this model was built with an external field; pass external_tensor")
-            fld = external_tensor.to(f32).reshape(-1, 3).flip(-1)            # rank-1 -> l=1 block order (z,y,x)
-            if self.o3:
-                s = c1.external_tensor_scale_by_irrep[self.keys.index((1, -1))]
-            else:
-                s = c1.external_tensor_scale_by_l[1]
-            add = torch.zeros_like(Y)
-            add[:, 1:4] = fld.index_select(0, src_batch) * s.detach()
-            F_in = Y + add
-        elif external_tensor is not None:
-            raise ValueError("external_tensor given but the model has no external field")
+        F_in = self._field_term(Y, external_tensor, src_batch, detach=True)
         feats = [ictd_ops.ictd_conv1_apply(F_in, self._gates(c1.fc, r), qtab, g, self.layout_id)]
         for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
             feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, self._gates(fc2, r), tp.weight.detach(),
                                                   self._wt(tp), cg, g, self.layout_id))
         e, dip = self.readout(feats, batch, cell.shape[0], factors, with_dipole)
+        return poison_invalid(e, g, pos, edge_vec), dip
+
+    def _field_term(self, Y, external_tensor, src_batch, detach: bool):
+        """Y plus the external field embedded in the l=1 block of conv1's first operand (z, y, x order)."""
+        if not self.external_field:
+            if external_tensor is not None:
+                raise ValueError("external_tensor given but the model has no external field")
+            return Y
+        if external_tensor is None:
+            raise ValueError("this model was built with an external field; pass external_tensor")
+        c1 = self.e3_conv_emb
+        fld = external_tensor.to(Y.dtype).reshape(-1, 3).flip(-1)
+        if self.o3:
+            s = c1.external_tensor_scale_by_irrep[self.keys.index((1, -1))]
+        else:
+            s = c1.external_tensor_scale_by_l[1]
+        s = s.detach() if detach else s
+        blk = fld.index_select(0, src_batch) * s
+        return Y + torch.cat([torch.zeros_like(Y[:, :1]), blk, torch.zeros_like(Y[:, 4:])], dim=1)
+
+    def _forward_train(self, pos, batch, cell, g: Graph, external_tensor, edge_vec, with_dipole):
+        """The training step: geometry, harmonics, radial MLPs, conv1 and the readout Gram as differentiable
+        GPU torch formulations (train_ops), conv2..n on the HIP op with its weight gradient and double
+        backward."""
+        from . import train_ops as T
+        f32 = torch.float32
+        pos, cell = pos.to(f32), cell.to(f32)
+        cg, c1_gates, factors = self._consts(pos.device)
+        src_batch = batch.index_select(0, g.src32)
+        if edge_vec is not None:
+            n, r = T.edge_vec_geometry(edge_vec.to(f32), g)
+        else:
+            shift_vec = (g.shifts.to(f32).unsqueeze(-1) * cell.index_select(0, src_batch)).sum(1)
+            n, r = T.edge_geometry(pos, shift_vec, g)
+        Y = T.harmonics(n, self.lmax)
+        c1 = self.e3_conv_emb
+        NS = g.n_species
+        atab = c1.atom_mlp(c1.atom_embedding(species_rows(g, pos.device)))
+        W1 = c1.tp2.weight.index_select(0, c1_gates)                                 # (NP1, C, 8, 8)
+        qtab = torch.einsum("pcij,si,tj->stpc", W1, atab, atab).reshape(NS * NS, W1.shape[0], self.channels)
+        F_in = self._field_term(Y, external_tensor, src_batch, detach=False)
+        gates1 = T.radial_full(r, c1.fc, self.max_radius, self.function_type)
+        feats = [T.ictd_conv1(F_in, gates1, qtab, g, self.layout)]
+        for tp, fc2 in zip(self.tp2_layers, self.fc2_layers):
+            gates = T.radial_full(r, fc2, self.max_radius, self.function_type)
+            feats.append(ictd_ops.ictd_conv_apply(feats[-1], Y, gates, tp.weight, self._wt(tp), cg, g,
+                                                  self.layout_id))
+        e, dip = self.readout(feats, batch, cell.shape[0], factors, with_dipole, train=True)
         return poison_invalid(e, g, pos, edge_vec), dip
 
     def _gates(self, fc, r):
@@ -242,18 +279,24 @@ class _ICTDTrunk(nn.Module):
     def _wread(self, i, k):
         return self.W_read[_key_str(k)] if self.o3 else self.W_read[i]
 
-    def readout(self, feats, batch, n_graphs, factors, with_dipole=True):
+    def readout(self, feats, batch, n_graphs, factors, with_dipole=True, train=False):
         """Gram bilinear + 0e products + MainNet (full :977-1033, o3 :987-1030), re-split included: the
         Gram inputs (the reference's channel-major flatten, layer concatenation and re-split by key)
-        and the per-key squared norms of the layer concatenation come from one fused readout op."""
+        and the per-key squared norms of the layer concatenation come from one fused readout op
+        (``train``: from its differentiable torch formulation, for parameter gradients)."""
         nL = len(feats)
         key = ("maps", nL)
         if key not in self._cache:
             self._cache[key] = ReadoutMaps(nL, self.channels, [2 * k[0] + 1 for k in self.keys], resplit=True)
         maps = self._cache[key]
-        grams = [prepare_gram(self._wread(i, k)) for i, k in enumerate(self.keys)]
         scales = [1.0 / math.sqrt(2 * k[0] + 1) for k in self.keys]
-        scalars, sq_all = readout_features(feats, grams, scales, maps)
+        if train:
+            from . import train_ops as T
+            scalars, sq_all = T.readout_features(feats, [self._wread(i, k) for i, k in enumerate(self.keys)],
+                                                 scales, maps)
+        else:
+            grams = [prepare_gram(self._wread(i, k)) for i, k in enumerate(self.keys)]
+            scalars, sq_all = readout_features(feats, grams, scales, maps)
         outs = []
         # unbind: its backward stacks the per-key gradients in one copy (a select per key would zero-fill,
         # copy and accumulate the whole (N, keys, n*C) gradient once per key)

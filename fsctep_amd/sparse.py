@@ -12,7 +12,9 @@ unchanged.  Its message passing runs in ``libfsctep_hip.so``:
 Edge geometry and the radial MLP fc[:4] (``:745-756``, ``:204-210``, ``:319-321``, ``:372-378``,
 ``:410-412``) run as ``torch.ops.fsctep.edge_geometry`` / ``radial_mlp``; the rest of the readout
 (``:769-833``) stays in PyTorch, on the same internal feature layout x[N][13][C]
-(component-major; the reference's pseudo half is identically zero and is not stored).
+(component-major; the reference's pseudo half is identically zero and is not stored).  In train()
+mode (force-loss training) the light ops switch to their differentiable formulations in
+``train_ops`` and conv2..n keeps its HIP op, which gives its weight gradient and double backward.
 """
 
 from __future__ import annotations
@@ -230,17 +232,19 @@ class PureCartesianSparseTransformerLayer(nn.Module):
             return e, e.new_empty((e.shape[0], 0))
         return e
 
-    def _check_inference(self):
-        if self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            raise NotImplementedError("the HIP sparse path computes energies and forces only; parameter "
-                                      "gradients (training) are not implemented: call .eval() or "
-                                      ".requires_grad_(False)")
+    def _training_step(self) -> bool:
+        """True when parameter gradients are wanted (train() mode, grad enabled, parameters that require
+        grad): the step is then built from differentiable parts (fsctep_amd.train_ops and the conv2..n op
+        with its double backward), so that a force loss trains every parameter."""
+        return self.training and torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())
 
     def forward_graph(self, pos, batch, cell, g: Graph):
-        """(N, 1) atomic energies for a prepared graph; differentiable w.r.t. ``pos``."""
-        self._check_inference()
+        """(N, 1) atomic energies for a prepared graph; differentiable w.r.t. ``pos`` (and, in train() mode,
+        twice differentiable w.r.t. ``pos`` and the parameters)."""
         if not pos.is_cuda:
             raise RuntimeError("the HIP sparse path runs on the GPU only")
+        if self._training_step():
+            return self._forward_train(pos, batch, cell, g)
         dtype = torch.float32
         pos = pos.to(dtype)
         cell = cell.to(dtype)
@@ -263,16 +267,38 @@ class PureCartesianSparseTransformerLayer(nn.Module):
             feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, self._precision_code()))
         return poison_invalid(self.readout(feats), g, pos)
 
+    def _forward_train(self, pos, batch, cell, g: Graph):
+        """The training step: geometry, radial MLPs, conv1 and readout as differentiable GPU torch
+        formulations (train_ops), conv2..n on the HIP op with its weight gradient and double backward."""
+        from . import train_ops as T
+        dtype = torch.float32
+        pos = pos.to(dtype)
+        cell = cell.to(dtype)
+        edge_cell = cell.index_select(0, batch.index_select(0, g.src32))
+        shift_vec = (g.shifts.to(dtype).unsqueeze(-1) * edge_cell).sum(1)
+        n, r = T.edge_geometry(pos, shift_vec, g)
+        conv1 = self.e3_conv_layers[0]
+        atab = conv1.atom_table(species_rows(g, pos.device)).to(dtype)
+        h1 = T.radial_hidden(r, conv1.fc, self.max_radius, self.function_type)
+        feats = [T.sparse_conv1(h1, n, conv1.fc[4].weight, conv1.fc[4].bias, atab, g, self.channels)]
+        for conv in self.e3_conv_layers[1:]:
+            bk1, bk6 = conv.prepared_weights()
+            h = T.radial_hidden(r, conv.fc, self.max_radius, self.function_type)
+            feats.append(ops.sparse_conv_apply(feats[-1], h, n, bk1, bk6, g, self._precision_code(),
+                                               conv.fc[4].weight, conv.fc[4].bias))
+        return poison_invalid(self.readout(feats, train=True), g, pos)
+
     def _precision_code(self) -> int:
         prec = getattr(self, "channel_mix_precision", "fp32")
         if prec not in ("fp32", "bf16"):
             raise ValueError(f"channel_mix_precision must be 'fp32' or 'bf16', got {prec!r}")
         return 1 if prec == "bf16" else 0
 
-    def readout(self, feats):
+    def readout(self, feats, train: bool = False):
         """pure_cartesian_sparse_layers.py:769-833 on x[N][13][C] features: the rank-L blocks of all
         layers (t_L = cat_l x_l[:, block L, :]) feed product_3 and their squared norms
-        sum_m x^2 / 3^{L/2} the invariants, all assembled by one fused readout op."""
+        sum_m x^2 / 3^{L/2} the invariants, all assembled by one fused readout op (``train``: by its
+        differentiable torch formulation, for parameter gradients)."""
         nL = len(feats)
         key = ("maps", nL)
         if key not in self._readout_cache:
@@ -280,8 +306,12 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         maps = self._readout_cache[key]
         p3 = self.product_3
         scales = [1.0 / math.sqrt(3 ** L) for L in range(len(_COMPS))]
-        grams = [prepare_gram(p3.W[L]) for L in range(len(_COMPS))]
-        f3, sq = readout_features(feats, grams, scales, maps)
+        if train:
+            from . import train_ops as T
+            f3, sq = T.readout_features(feats, [p3.W[L] for L in range(len(_COMPS))], scales, maps)
+        else:
+            grams = [prepare_gram(p3.W[L]) for L in range(len(_COMPS))]
+            f3, sq = readout_features(feats, grams, scales, maps)
         skey = ("scales", str(sq.device))
         if skey not in self._readout_cache:
             self._readout_cache[skey] = torch.tensor(scales, dtype=sq.dtype, device=sq.device).view(1, -1, 1, 1)
