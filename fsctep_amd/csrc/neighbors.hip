@@ -10,9 +10,9 @@
 // so graph preparation's stable receiver sort keeps it.
 //
 // Steps: bounding box and grid (cells of side >= r where the cell budget allows), atoms bucketed by cell
-// (counting sort), one thread per receiver counting its neighbours over the image points pos_j + s.cell,
-// a scan into the receiver CSR (the caller reads the edge count), then the same walk writing (src, s)
-// keys, and a per-receiver rank sort of the keys.
+// (counting sort), 16 lanes per receiver counting its neighbours over the image points pos_j + s.cell
+// (the lanes split each cell's candidates), a scan into the receiver CSR (the caller reads the edge count),
+// then the same walk writing (src, s) keys, and a per-receiver rank sort of the keys.
 #include "common.h"
 #include "fsctep.h"
 #include "scan.h"
@@ -132,15 +132,23 @@ struct Walk {
   double r2, reach;     // r^2 for the test; r (1 + 1e-9) for the cell range
 };
 
-// Visits every (i, s) within r of receiver j (see the file comment) in a fixed loop order and calls
-// f(i, key).  Returns the number visited.
+// A group of RL = 16 consecutive lanes per receiver j (four receivers per wave) visits every (i, s) within
+// r of j (see the file comment).  The loops over the image shifts and the cells in range are uniform in
+// the group; its lanes split each cell's atoms (16 candidates per step, about a cell's content at the
+// benchmark densities), and a step's hits are numbered in lane order by a ballot and a prefix popcount
+// over the group's bits.  For each step with hits, f(hit, i, key, rank, count) is called by every lane of
+// the group (hit: this lane's candidate is a neighbour; rank: its position among the receiver's hits so
+// far; count: the step's hits).  Returns the number visited (the same in every lane of the group).
+constexpr int RL = 16;
 template <typename F>
-__device__ __forceinline__ int32_t walk_receiver(const Walk& w, int64_t j, F&& f) {
+__device__ __forceinline__ int32_t walk_receiver_wave(const Walk& w, int64_t j, int lane, F&& f) {
+  const int sub = lane & (RL - 1), gshift = lane & ~(RL - 1);
   const GridParams g = *w.grid;
   const double pj[3] = {w.pos[3 * j], w.pos[3 * j + 1], w.pos[3 * j + 2]};
   double a[9];
 #pragma unroll
   for (int t = 0; t < 9; ++t) a[t] = w.cell[t];
+  const uint64_t below = sub ? (~0ull >> (64 - sub)) : 0ull;
   int32_t n = 0;
   for (int sx = -w.pbc[0]; sx <= w.pbc[0]; ++sx)
     for (int sy = -w.pbc[1]; sy <= w.pbc[1]; ++sy)
@@ -164,16 +172,27 @@ __device__ __forceinline__ int32_t walk_receiver(const Walk& w, int64_t j, F&& f
           for (int cy = clo[1]; cy <= chi[1]; ++cy)
             for (int cz = clo[2]; cz <= chi[2]; ++cz) {
               const int c = (cx * g.G[1] + cy) * g.G[2] + cz;
-              for (int32_t q = w.cell_start[c]; q < w.cell_start[c + 1]; ++q) {
-                const int32_t i = w.cell_atoms[q];
-                if (self_image && i == j) continue;
-                const double dx = dadd(pj[0] - w.pos[3 * (int64_t)i], sv[0]);
-                const double dy = dadd(pj[1] - w.pos[3 * (int64_t)i + 1], sv[1]);
-                const double dz = dadd(pj[2] - w.pos[3 * (int64_t)i + 2], sv[2]);
-                const double d2 = dadd(dadd(dmul(dx, dx), dmul(dy, dy)), dmul(dz, dz));
-                if (d2 < w.r2) {
-                  f(i, (int64_t)i * KEY_IMAGES + code);
-                  ++n;
+              const int32_t qb = w.cell_start[c], qe = w.cell_start[c + 1];
+              for (int32_t q0 = qb; q0 < qe; q0 += RL) {
+                const int32_t q = q0 + sub;
+                bool hit = false;
+                int32_t i = 0;
+                if (q < qe) {
+                  i = w.cell_atoms[q];
+                  if (!(self_image && i == j)) {
+                    const double dx = dadd(pj[0] - w.pos[3 * (int64_t)i], sv[0]);
+                    const double dy = dadd(pj[1] - w.pos[3 * (int64_t)i + 1], sv[1]);
+                    const double dz = dadd(pj[2] - w.pos[3 * (int64_t)i + 2], sv[2]);
+                    const double d2 = dadd(dadd(dmul(dx, dx), dmul(dy, dy)), dmul(dz, dz));
+                    hit = d2 < w.r2;
+                  }
+                }
+                // this group's bits of the ballot of the lanes still in the loop
+                const uint64_t mask = (__ballot(hit) >> gshift) & ((1ull << RL) - 1);
+                if (mask) {
+                  const int cnt = __popcll(mask);
+                  f(hit, i, (int64_t)i * KEY_IMAGES + code, n + __popcll(mask & below), cnt);
+                  n += cnt;
                 }
               }
             }
@@ -182,23 +201,25 @@ __device__ __forceinline__ int32_t walk_receiver(const Walk& w, int64_t j, F&& f
 }
 
 __global__ __launch_bounds__(256) void count_kernel(Walk w, int32_t* __restrict__ deg) {
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (j >= w.N) return;
-  deg[j] = walk_receiver(w, j, [](int32_t, int64_t) {});
+  const int64_t j = (int64_t)blockIdx.x * (256 / RL) + threadIdx.x / RL;
+  if (j >= w.N) return;   // uniform in the lane group
+  const int lane = threadIdx.x & 63;
+  const int32_t n = walk_receiver_wave(w, j, lane, [](bool, int32_t, int64_t, int32_t, int) {});
+  if ((lane & (RL - 1)) == 0) deg[j] = n;
 }
 
 __global__ __launch_bounds__(256) void fill_kernel(Walk w, const int32_t* __restrict__ dst_ptr, int64_t E,
                                                    int64_t* __restrict__ keys, int32_t* __restrict__ key_dst) {
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (j >= w.N) return;
+  const int64_t j = (int64_t)blockIdx.x * (256 / RL) + threadIdx.x / RL;
+  if (j >= w.N) return;   // uniform in the lane group
+  const int lane = threadIdx.x & 63;
   const int64_t beg = dst_ptr[j], end = dst_ptr[j + 1];
-  int64_t o = beg;
-  walk_receiver(w, j, [&](int32_t, int64_t key) {
-    if (o < end && o < E) {   // the counts came from the same walk: never false, kept as a bound
+  walk_receiver_wave(w, j, lane, [&](bool hit, int32_t, int64_t key, int32_t rank, int) {
+    const int64_t o = beg + rank;
+    if (hit && o < end && o < E) {   // the counts came from the same walk: never false, kept as a bound
       keys[o] = key;
       key_dst[o] = (int32_t)j;
     }
-    ++o;
   });
 }
 
@@ -313,7 +334,7 @@ int fsc_neighbor_count(int64_t n_nodes, const double* pos, const double* cell, c
   scan_add_kernel<<<dim3((unsigned)w.nb, 1), SCAN_T, 0, stream>>>(sa);
   place_kernel<<<grid_of(N), 256, 0, stream>>>(N, ws + w.atom_cell, ws + w.cell_start, ws + w.cur, ws + w.cell_atoms);
   const Walk walk = make_walk(N, pos, cell, pbc, cutoff, ws, w);
-  count_kernel<<<grid_of(N), 256, 0, stream>>>(walk, ws + w.deg);
+  count_kernel<<<(unsigned)((N + 256 / RL - 1) / (256 / RL)), 256, 0, stream>>>(walk, ws + w.deg);
   // receiver CSR: exclusive scan of the degrees into dst_ptr[0..N]
   const int64_t nbn = (N + 1 + SCAN_TILE - 1) / SCAN_TILE;
   FSC_CHECK_ARG(nbn <= SCAN_MAX_BLOCKS, "fsc_neighbor_count: too many nodes for the scan");
@@ -340,7 +361,7 @@ int fsc_neighbor_fill(int64_t n_nodes, int64_t n_edges, const double* pos, const
   int64_t* keys = reinterpret_cast<int64_t*>(fill_ws);   // 2E int32, 8-byte aligned by the caller
   int32_t* key_dst = fill_ws + 2 * E;
   const Walk walk = make_walk(N, pos, cell, pbc, cutoff, workspace, w);
-  fill_kernel<<<grid_of(N), 256, 0, stream>>>(walk, dst_ptr, E, keys, key_dst);
+  fill_kernel<<<(unsigned)((N + 256 / RL - 1) / (256 / RL)), 256, 0, stream>>>(walk, dst_ptr, E, keys, key_dst);
   rank_kernel<<<grid_of(E), 256, 0, stream>>>(N, E, dst_ptr, keys, key_dst, edge_src, edge_dst, edge_shifts);
   return check_launch("fsc_neighbor_fill") ? 2 : 0;
 }
