@@ -191,12 +191,13 @@ __global__ __launch_bounds__(256) void node_scale_kernel(int64_t N, int D, int n
   if (lane == 0) nsc[n] = pow2_scale(mx);
 }
 
-// Forward partial sums over PCHUNK block pairs: part[chunk][n][o].  A workgroup is 128 nodes (8 waves x
+// Forward partial sums over pchunk block pairs: part[chunk][n][o].  A workgroup is 128 nodes (8 waves x
 // 16 MFMA rows) x one chunk; each pair's Wf block [il][o][jl] (256*S floats) is staged in LDS and shared
 // by the 8 waves, the next pair's block is loaded into registers while the current one is multiplied.
 template <int D, int S>
 __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float scale, const float* __restrict__ t,
-                                           const float* __restrict__ Wf, int nchunks, float* __restrict__ part) {
+                                           const float* __restrict__ Wf, int nchunks, float* __restrict__ part,
+                                           int pchunk) {
   constexpr int NN = NODES, CT = S / 16;
   constexpr int WBF4 = 256 * S / 4, PW = (WBF4 + 511) / 512;
   __shared__ f4 wl[WBF4];
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
   const int64_t n = (int64_t)tile * NN + wave * 16 + r;
   const bool valid = n < N;
   const float* tn = t + (valid ? n : 0) * D * nC;
-  const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
+  const int p0 = chunk * pchunk, p1 = min(p0 + pchunk, np);
   int I = 0, rowstart = 0;
   while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
   int J = I + (p0 - rowstart);
@@ -592,15 +593,35 @@ int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
   return 0;
 }
 
+// Forward kernel choice and block pairs per workgroup.  The split-fp16 kernel runs 256-node tiles at
+// several times the fp32 kernel's rate per node; with at most 128 of its workgroups (one partial round
+// on 256 CUs) the fp32 kernel's twice as many smaller workgroups finish first.  The fp32 kernel (few
+// nodes) takes fewer pairs per workgroup, down to one, until there are about two workgroups per CU:
+// at 1,000 nodes and nC 192 that is 624 workgroups of one pair instead of 80 of eight.
+struct FwdPlan {
+  bool bf;
+  int pchunk, nchunks;
+};
+FwdPlan fwd_plan(int64_t N, int nC) {
+  const int np = n_pairs(nC / 16);
+  FwdPlan pl;
+  pl.bf = (int64_t)((np + PCHUNK - 1) / PCHUNK) * ((N + NODES_BF - 1) / NODES_BF) > 128;
+  pl.pchunk = PCHUNK;
+  if (!pl.bf) {
+    const int64_t ntiles = (N + NODES - 1) / NODES;
+    while (pl.pchunk > 1 && (int64_t)((np + pl.pchunk - 1) / pl.pchunk) * ntiles < 512) pl.pchunk /= 2;
+  }
+  pl.nchunks = (np + pl.pchunk - 1) / pl.pchunk;
+  return pl;
+}
+
 template <int S>
 int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float* Wf, float* part, float* out,
               hipStream_t st) {
-  // The split-fp16 kernel runs 256-node tiles at several times the fp32 kernel's rate per node; with at
-  // most 128 of its workgroups (one partial round on 256 CUs) the fp32 kernel's twice as many smaller
-  // workgroups finish first.
   const int np = n_pairs(nC / 16);
-  const int nchunks = (np + PCHUNK - 1) / PCHUNK;
-  const bool bf = (int64_t)nchunks * ((N + NODES_BF - 1) / NODES_BF) > 128;
+  const FwdPlan pl = fwd_plan(N, nC);
+  const int nchunks = pl.nchunks, pchunk = pl.pchunk;
+  const bool bf = pl.bf;
   const int ntiles = (int)((N + (bf ? NODES_BF : NODES) - 1) / (bf ? NODES_BF : NODES));
   const unsigned grid = (unsigned)(((int64_t)nchunks * ntiles + 7) / 8 * 8);
   const _Float16* Wf2 = reinterpret_cast<const _Float16*>(Wf + (int64_t)np * 256 * S);
@@ -620,7 +641,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   if (bf)                                                                                          \
     forward_h16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, part, tg); \
   else                                                                                             \
-    forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part)
+    forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part, pchunk)
     switch (D) {
       case 1: FSC_GF(1); break;
       case 3: FSC_GF(3); break;
@@ -680,7 +701,7 @@ int fsc_gram_sizes(int64_t n_nodes, int32_t nC, int32_t S, int64_t* wf_floats, i
   *wf_floats = gram_weight_floats(nC / 16, S);   // fp32 block pairs, two fp16 planes, scale and maxima
   *wb_floats = *wf_floats;
   // per-chunk partial sums, then one scale per node
-  *workspace_floats = (int64_t)((n_pairs(nC / 16) + PCHUNK - 1) / PCHUNK) * n_nodes * S + n_nodes;
+  *workspace_floats = (int64_t)fwd_plan(n_nodes, nC).nchunks * n_nodes * S + n_nodes;
   return 0;
 }
 

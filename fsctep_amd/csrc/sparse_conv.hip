@@ -23,6 +23,8 @@
 // chunks of 8, slot-major inside a chunk), so the backward's reads of an edge are one contiguous 20*C-byte
 // run, a chunk at a time (p_col); h[E][64]; n[E][3] (unit vectors).
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace fsc {
@@ -94,12 +96,15 @@ __global__ __launch_bounds__(256) void weight_absmax_kernel(const float* __restr
   if (threadIdx.x == 0) wmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// 256 threads per block; every block reduces the partial maxima itself, so all use the same sw.
+// One block of 256 threads per (path p, output channel c): the C x 65 tile of (a, column) values passes
+// through LDS, so that both layouts are written in contiguous runs (bk6 rows along the column, bk1 rows
+// along a).  Every block reduces the partial maxima itself, so all use the same sw.
 __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restrict__ L, const float* __restrict__ b,
                                                            float* __restrict__ bk1f, float* __restrict__ bk6f, int C) {
   const int64_t cols = 65LL * C;
   const int64_t total = 6LL * cols * C;
   __shared__ float red[4];
+  __shared__ float tile[64][65];   // [a][kk], C <= 64
   float mx = bk1f[total + 256 + threadIdx.x];
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -113,29 +118,35 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
   _Float16* bk6 = reinterpret_cast<_Float16*>(bk6f);
   __bf16* bk1b = reinterpret_cast<__bf16*>(bk1f + total + SW_TAIL);
   __bf16* bk6b = reinterpret_cast<__bf16*>(bk6f + total + SW_TAIL);
-  // k fastest (k = 64: the bias): consecutive threads read consecutive entries of one row of L and write
-  // consecutive columns of bk6
-  for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < total;
-       it += (int64_t)gridDim.x * blockDim.x) {
-    const int kk = (int)(it % 65);
-    const int a = (int)((it / 65) % C);
-    const int c = (int)((it / (65 * C)) % C);
-    const int p = (int)(it / (65LL * C * C));
-    const int64_t row = (int64_t)p * C * C + (int64_t)c * C + a;
+  const int p = blockIdx.x / C, c = blockIdx.x % C;
+  const int64_t row0 = (int64_t)p * C * C + (int64_t)c * C;    // row of (p, c, a = 0)
+  // values times sw, kk fastest: rows of L read 256 contiguous bytes at a time
+  for (int i = threadIdx.x; i < C * 65; i += 256) {
+    const int a = i / 65, kk = i - a * 65;
+    tile[a][kk] = (kk < 64 ? L[(row0 + a) * KH + kk] : b[row0 + a]) * sw;
+  }
+  __syncthreads();
+  // bk6[p][a][col], col = c*64 + kk (kk < 64) or 64C + c (bias)
+  for (int i = threadIdx.x; i < C * 65; i += 256) {
+    const int a = i / 65, kk = i - a * 65;
     const int64_t col = kk < 64 ? (int64_t)c * 64 + kk : 64LL * C + c;
-    const float v = kk < 64 ? L[row * KH + kk] : b[row];
-    const int64_t idx = ((int64_t)p * cols + col) * C + a;
     const int64_t o = ((int64_t)p * C + a) * cols + col;
-    const float vs = v * sw;
+    const float vs = tile[a][kk];
     const _Float16 hb = (_Float16)vs;
-    const _Float16 lb = (_Float16)(vs - (float)hb);
-    bk1[idx] = hb;
-    bk1[total + idx] = lb;
     bk6[o] = hb;
-    bk6[total + o] = lb;
-    const __bf16 bb = (__bf16)vs;
-    bk1b[idx] = bb;
-    bk6b[o] = bb;
+    bk6[total + o] = (_Float16)(vs - (float)hb);
+    bk6b[o] = (__bf16)vs;
+  }
+  // bk1[p][col][a], a fastest
+  for (int i = threadIdx.x; i < C * 65; i += 256) {
+    const int kk = i / C, a = i - kk * C;
+    const int64_t col = kk < 64 ? (int64_t)c * 64 + kk : 64LL * C + c;
+    const int64_t idx = ((int64_t)p * cols + col) * C + a;
+    const float vs = tile[a][kk];
+    const _Float16 hb = (_Float16)vs;
+    bk1[idx] = hb;
+    bk1[total + idx] = (_Float16)(vs - (float)hb);
+    bk1b[idx] = (__bf16)vs;
   }
 }
 
@@ -1002,34 +1013,49 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
 // padded edge list `pair_tiles`); the receiver sum then reads Q in receiver order.
 constexpr int MB_STRIDE = 68;
 
-__global__ void conv1_pair_table_kernel(const float* __restrict__ L, const float* __restrict__ b,
-                                        const float* __restrict__ atab, int n_species, int C,
-                                        float* __restrict__ mf, float* __restrict__ mb) {
-  const int64_t total = (int64_t)n_species * n_species * 3 * 65 * C;
+// One thread per (receiver species t, live path, channel c, column k), all source species s: the inner
+// sum u[a] = sum_b L[(p,c,a,b),k] A_t[b] is formed once and reused for every s (each L entry is read once
+// per t instead of once per (s, t)); consecutive threads take consecutive k (coalesced rows of L).
+__global__ __launch_bounds__(256) void conv1_pair_table_kernel(const float* __restrict__ L,
+                                                               const float* __restrict__ b,
+                                                               const float* __restrict__ atab, int n_species,
+                                                               int C, float* __restrict__ mf,
+                                                               float* __restrict__ mb) {
+  const int64_t total = (int64_t)n_species * 3 * 65 * C;
   const int live[3] = {0, 3, 5};
-  // k fastest: consecutive threads read consecutive k of one row of L (coalesced 256-byte rows)
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int k = (int)(idx % 65);
     const int c = (int)((idx / 65) % C);
     const int p3 = (int)((idx / (C * 65)) % 3);
-    const int pair = (int)(idx / (C * 65 * 3));
-    const int s = pair / n_species, t = pair % n_species;
+    const int t = (int)(idx / (C * 65 * 3));
     const int p = live[p3];
-    float acc = 0.f;
+    float at[8];
+#pragma unroll
+    for (int bb = 0; bb < 8; ++bb) at[bb] = atab[t * 8 + bb];
+    float u[8];
+#pragma unroll
     for (int a = 0; a < 8; ++a) {
-      const float as = atab[s * 8 + a];
+      float acc = 0.f;
+#pragma unroll
       for (int bb = 0; bb < 8; ++bb) {
         const int64_t row = (int64_t)p * C * 64 + (int64_t)c * 64 + a * 8 + bb;
         const float w = (k < 64) ? L[row * KH + k] : b[row];
-        acc += w * as * atab[t * 8 + bb];
+        acc += w * at[bb];
       }
+      u[a] = acc;
     }
-    mf[(((int64_t)pair * 3 + p3) * 65 + k) * C + c] = acc;              // [pair][p3][k][c]
-    mb[(((int64_t)pair * 3 + p3) * C + c) * MB_STRIDE + k] = acc;        // [pair][p3][c][k]
-    if (k == 64) {
+    for (int s = 0; s < n_species; ++s) {
+      float acc = 0.f;
 #pragma unroll
-      for (int z = 65; z < MB_STRIDE; ++z) mb[(((int64_t)pair * 3 + p3) * C + c) * MB_STRIDE + z] = 0.f;
+      for (int a = 0; a < 8; ++a) acc += atab[s * 8 + a] * u[a];
+      const int64_t pair = (int64_t)s * n_species + t;
+      mf[((pair * 3 + p3) * 65 + k) * C + c] = acc;              // [pair][p3][k][c]
+      mb[((pair * 3 + p3) * C + c) * MB_STRIDE + k] = acc;        // [pair][p3][c][k]
+      if (k == 64) {
+#pragma unroll
+        for (int z = 65; z < MB_STRIDE; ++z) mb[((pair * 3 + p3) * C + c) * MB_STRIDE + z] = 0.f;
+      }
     }
   }
 }
@@ -1351,7 +1377,7 @@ int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, in
   weight_absmax_kernel<<<SWMAX_BLOCKS, 256, 0, stream>>>(w_last, 6 * C * C * KH, b_last, 6 * C * C,
                                                          bk1 + sparse_weight_floats(channels) - SW_TAIL + 256);
   if (check_launch("sparse weight maximum")) return 2;
-  prep_weights_kernel<<<512, 256, 0, stream>>>(w_last, b_last, bk1, bk6, channels);
+  prep_weights_kernel<<<(unsigned)(6 * C), 256, 0, stream>>>(w_last, b_last, bk1, bk6, channels);
   return check_launch("sparse prepare_weights") ? 2 : 0;
 }
 
@@ -1450,7 +1476,9 @@ int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const 
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_pair_table: channels must be 32 or 64");
   FSC_CHECK_ARG(n_species >= 1 && n_species <= 128, "fsc_sparse_conv1_pair_table: n_species out of range");
   FSC_CHECK_ARG(w_last && b_last && atom_table && mf && mb, "fsc_sparse_conv1_pair_table: null pointer");
-  conv1_pair_table_kernel<<<256, 256, 0, stream>>>(w_last, b_last, atom_table, n_species, channels, mf, mb);
+  const int64_t work = (int64_t)n_species * 3 * 65 * channels;
+  conv1_pair_table_kernel<<<(unsigned)std::min<int64_t>((work + 255) / 256, 1024), 256, 0, stream>>>(
+      w_last, b_last, atom_table, n_species, channels, mf, mb);
   return check_launch("sparse conv1_pair_table") ? 2 : 0;
 }
 
