@@ -50,7 +50,7 @@ PARITY_TOL = 1e-5
 PRODUCT_PEAK_TFLOPS = {"fp32": FP32_MFMA_PEAK_TFLOPS, "split-fp16": FP16_MFMA_PEAK_TFLOPS / 3,
                        "split-bf16": FP16_MFMA_PEAK_TFLOPS / 6, "bf16": FP16_MFMA_PEAK_TFLOPS}
 KERNEL_PRODUCTS = {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
-                   "edge_message_grad": "fp32", "receiver_sum": "fp32",
+                   "edge_message_grad": "split-fp16", "receiver_sum": "fp32",
                    "ictd_project": "fp32", "ictd_project_grad": "fp32", "ictd_dual_project": "fp32",
                    "ictd_mix": "split-fp16", "ictd_mix_grad": "split-fp16", "ictd_dual_mix": "split-fp16"}
 BF16_VARIANT = {"node_expand", "node_expand_grad", "edge_message"}
@@ -81,7 +81,7 @@ WORKLOADS = {
 # operand, six of the nine part products on bf16 MFMA (the dropped ones are below 2^-23 |ab|).
 PRODUCTS = {
     "sparse": {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
-               "edge_message_grad": "fp32 MFMA", "conv1 pair GEMMs": "fp32 MFMA", "radial_mlp": "fp32 MFMA",
+               "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "fp32 MFMA", "radial_mlp": "fp32 MFMA",
                "receiver_sum, edge geometry, readout assembly": "fp32 VALU",
                "gram_forward, gram_backward": "split-fp16", "MainNet, atom MLP": "torch fp32"},
     "ictd": {"ictd_project, ictd_project_grad": "fp32 MFMA", "ictd_mix, ictd_mix_grad": "split-fp16",
@@ -100,11 +100,12 @@ def sparse_kernel_work(name: str, N: int, E: int, C: int) -> dict:
     s_bytes = 4 * N * 18 * 65 * C            # node expansion S (or dS)
     p_bytes = 4 * E * 18 * C                 # edge messages P
     if name == "edge_message_grad":
-        # dh and dS products; the fused direction gradient reads P slots 1, 2, 6, 7, 8 and writes dn
+        # dh and dS products (split-fp16: their MFMA time is a fraction of the kernel's, which is set by
+        # reading S and writing dS); the fused direction gradient reads P slots 1, 2, 6, 7, 8 and writes dn
         flops = 2 * (2 * E * 18 * C * K) + E * 18 * C + 2 * E * 30 * C
         byts = (s_bytes + s_bytes + 4 * E * K * 2 + 4 * N * 13 * C + 4 * E * 3 * 2 + 4 * E * 5 * C
                 + 4 * E * 2)
-        return dict(flops=flops, bytes=byts, bound="mfma")
+        return dict(flops=flops, bytes=byts, bound="hbm")
     if name == "edge_message":
         flops = 2 * E * 18 * C * K
         byts = s_bytes + p_bytes + 4 * E * K + 4 * E

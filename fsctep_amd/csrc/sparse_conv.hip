@@ -1002,6 +1002,351 @@ __global__ __launch_bounds__(256, 2) void edge_message_grad_kernel(
   if (threadIdx.x == 0) dscale[m] = pow2_scale(fmaxf(fmaxf(amx[0], amx[1]), fmaxf(amx[2], amx[3])));
 }
 
+// Per-node bound of the receiver gradient for the split-fp16 message gradient: gmax[n] = max |G[n][comp][c]|.
+// One wave per node (13 C values).
+template <int C>
+__global__ __launch_bounds__(256) void grad_absmax_kernel(const float* __restrict__ G, float* __restrict__ gmax,
+                                                          int64_t n_nodes) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= n_nodes) return;   // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const float* g = G + n * NCOMP * C;
+  float m = 0.f;
+  for (int i = lane; i < NCOMP * C / 4; i += 64) {
+    const f4 v = ld4(g + 4 * i);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) gmax[n] = m;
+}
+
+// The message gradient with both products on fp16 MFMA in fp32 precision (split-fp16, common.h): the same
+// sums as edge_message_grad_kernel, per source node m and 64-edge block, 8-channel chunk by chunk.
+//   dh[e][k]  = sum_{(slot,c)} dP[e][(slot,c)] S[m][(slot,c)][k]        A = dP rows, B = S      (K = 144)
+//   dS[k][col] = sum_e h[e][k] dP[e][col]                                A = h^T,     B = dP     (K = edges)
+// dP is held once, in LDS, as two fp16 planes of dP[e] * s_e, s_e the power of two of an upper bound of the
+// edge's row: |dP| <= 3 max|g| (|n| = 1: |g1.n|, |(g2 n)_i| <= sqrt 3 max|g|, |n.g2.n| <= 3 max|g|), from the
+// receiver's max |G| (grad_absmax_kernel).  The dh product undoes s_e per row; the dS product, whose K runs
+// over edges, takes h[e][k] / s_e as its A operand (exact: powers of two), scaled per k by the power of two of
+// that column's max, so the sum over edges needs no rescaling.  S is scaled per (chunk, k) by its own max and
+// each chunk's dh product is undone and added to the fp32 dh separately.  The bias column sums the two
+// planes over the edges on the VALU.  A lane's dh B operand is 8 consecutive chunk columns of one k (S
+// loads at a fixed stride, as in the fp32 kernel); a lane's dS B operand is 8 consecutive edges of one
+// column (eight 2-byte LDS reads per plane).  K = 144 is four 32-deep steps and a 16-deep one.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+constexpr int DPS = 144;   // fp16 row stride of dP in LDS (144 columns, 288 bytes: 16-byte aligned rows)
+
+template <int C>
+__global__ __launch_bounds__(256, 4) void edge_message_grad_h16_kernel(
+    const float* __restrict__ Gt, const float* __restrict__ gmax, const float* __restrict__ nvec,
+    const float* __restrict__ h, const float* __restrict__ S, const float* __restrict__ P,
+    const int32_t* __restrict__ src_ptr, const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst,
+    float scale, float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, float* __restrict__ dscale,
+    int64_t n_nodes, const int32_t* __restrict__ node_order) {
+  constexpr int CC = 8;              // channels per chunk
+  constexpr int NCH = C / CC;
+  constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
+  constexpr int NCT = DW / 16;       // 16-wide column tiles per chunk
+  constexpr int COLS = 65 * C;
+  constexpr int NCOL = NSLOT * C;
+  __shared__ __align__(16) _Float16 dpl[2][EP][DPS];   // planes h, l of dP[e] * s_e
+  __shared__ int32_t eids[EP];
+  __shared__ int32_t dsts[EP];
+  __shared__ float ns[EP][3];
+  __shared__ float dnacc[EP][3];
+  __shared__ float esc[EP];          // s_e
+  __shared__ float einv[EP];         // 1 / s_e
+  __shared__ float amx[4];
+  const int m = xcd_node(n_nodes, node_order);
+  if (m < 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int beg = src_ptr[m], end = src_ptr[m + 1];
+  float* dSm = dS + (int64_t)m * s_node_stride(C);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc_bytes(
+      const_cast<char*>(reinterpret_cast<const char*>(S)) + (int64_t)m * s_node_stride(C) * 4,
+      (uint32_t)(s_node_stride(C) * 4));
+  const __amdgpu_buffer_rsrc_t drs = buffer_rsrc(dSm, (uint32_t)(s_node_stride(C) * 4));
+  // dh B operand: K step s, lane group q -> slot 4s + q, channels c0 + j; the 16-deep tail: slot 16 + q/2,
+  // channels c0 + 4 (q & 1) + j
+  const uint32_t svoff = (uint32_t)((q * COLS + 16 * wave + r) * 4);
+  const uint32_t svoff_t = (uint32_t)(((q >> 1) * COLS + 4 * (q & 1) * KH + 16 * wave + r) * 4);
+  const uint32_t dvoff = (uint32_t)(((r >> 3) * COLS + (r & 7) * KH + 16 * wave + 4 * q) * 4);
+  const int cl = threadIdx.x & (CC - 1);   // dP builder: channel within the chunk
+  const int eb = threadIdx.x / CC;         // dP builder: edges eb, eb + 32
+
+  if (end == beg) {   // no out-edges: dS of this node is zero (block-uniform branch)
+    for (int idx = threadIdx.x; idx < NSLOT * COLS / 4; idx += 256) st4(dSm + 4 * idx, f4{0.f, 0.f, 0.f, 0.f});
+    if (threadIdx.x == 0) dscale[m] = 1.f;
+    return;
+  }
+  float amax = 0.f;   // max |dS| over the values stored by the last edge block (the final ones)
+  int pb = beg;
+  bool first = true;
+  do {
+    const int cnt = min(EP, end - pb);   // >= 1
+    __syncthreads();
+    // Rows e >= cnt point at edge cnt-1, so every load below stays unconditional; their direction and h
+    // rows are zero and their dP is masked to zero.
+    if (threadIdx.x < EP) {
+      const int e = threadIdx.x;
+      const int32_t id = src_perm[pb + min(e, cnt - 1)];
+      const int32_t d = edge_dst[id];
+      eids[e] = id;
+      dsts[e] = d;
+      const float se = pow2_scale(3.f * gmax[d] * scale);
+      esc[e] = se;
+      einv[e] = 1.f / se;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const float v = nvec[3 * (int64_t)id + k];
+        ns[e][k] = (e < cnt) ? v : 0.f;
+        dnacc[e][k] = 0.f;
+      }
+    }
+    __syncthreads();
+    // A operand of the dS product for the whole edge block: lane (r, q) of wave w holds h[e][k] / s_e
+    // for k = 16 w + r and edges e = 32 s + 8 q + j, times the power of two of the column's max
+    h8 ah[2], al[2];
+    float invsh;
+    {
+      float hv[2][8];
+      float mx = 0.f;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = 32 * s + 8 * q + j;
+          const float v = (e < cnt) ? h[(int64_t)eids[e] * KH + 16 * wave + r] * einv[e] : 0.f;
+          hv[s][j] = v;
+          mx = fmaxf(mx, fabsf(v));
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float sh = pow2_scale(mx);
+      invsh = 1.f / sh;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) split2h(hv[s], sh, ah[s], al[s]);
+    }
+    const int nrt = (cnt + 15) / 16;
+    const int nks = (cnt + 31) / 32;
+    f4 dacc[4];
+#pragma unroll
+    for (int et = 0; et < 4; ++et) dacc[et] = f4{0.f, 0.f, 0.f, 0.f};
+
+    float gN[2][NCOMP], pN[2][5], sv[36];
+    auto load_g = [&](int ch) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int e = eb + 32 * hh;
+        const float* gp = Gt + ((int64_t)ch * n_nodes + dsts[e]) * (NCOMP * CC) + cl;
+#pragma unroll
+        for (int i = 0; i < NCOMP; ++i) gN[hh][i] = gp[i * CC];
+        const float* pp = P + (int64_t)eids[e] * NCOL + ch * 40 + cl;   // p_col of positions 0..4
+        pN[hh][0] = pp[pos_of_slot(1) * CC];
+        pN[hh][1] = pp[pos_of_slot(2) * CC];
+        pN[hh][2] = pp[pos_of_slot(6) * CC];
+        pN[hh][3] = pp[pos_of_slot(7) * CC];
+        pN[hh][4] = pp[pos_of_slot(8) * CC];
+      }
+    };
+    auto load_s = [&](int ch) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          sv[8 * s + j] = buffer_ld1(srs, svoff, (uint32_t)((4 * s * COLS + (ch * CC + j) * KH) * 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sv[32 + j] = buffer_ld1(srs, svoff_t, (uint32_t)((16 * COLS + (ch * CC + j) * KH) * 4));
+    };
+#pragma unroll 1
+    for (int ch = 0; ch < NCH; ++ch) {
+      const int c0 = ch * CC;
+      load_g(ch);
+      // ---- dP for edges eb, eb+32 and channel c0+cl (scaled by s_e, split into the two planes);
+      //      direction-gradient partials in fp32
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int e = eb + 32 * hh;
+        float v[NSLOT];
+        float t[3];
+        float g[NCOMP];
+        const float sc = (e < cnt) ? scale : 0.f;
+#pragma unroll
+        for (int i = 0; i < NCOMP; ++i) g[i] = gN[hh][i] * sc;
+        const float nn[3] = {ns[e][0], ns[e][1], ns[e][2]};
+        const float p1 = pN[hh][0], p2 = pN[hh][1];
+        const float p4[3] = {pN[hh][2], pN[hh][3], pN[hh][4]};
+        v[0] = g[0];
+        v[1] = g[1] * nn[0] + g[2] * nn[1] + g[3] * nn[2];
+        float nqn = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          float row = 0.f, colv = 0.f, p4t = 0.f;
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            row += g[4 + 3 * i + j] * nn[j];
+            colv += g[4 + 3 * j + i] * nn[j];
+            p4t += g[4 + 3 * j + i] * p4[j];
+          }
+          v[3 + i] = g[1 + i];
+          v[6 + i] = row;
+          nqn += row * nn[i];
+          t[i] = g[1 + i] * p1 + p2 * (row + colv) + p4t;
+        }
+        v[2] = nqn;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) v[9 + i] = g[4 + i];
+        const float se = esc[e];
+#pragma unroll
+        for (int s4 = 0; s4 < NSLOT; ++s4) {
+          const float x = v[s4] * se;
+          const _Float16 xh = (_Float16)x;
+          dpl[0][e][s4 * CC + cl] = xh;
+          dpl[1][e][s4 * CC + cl] = (_Float16)(x - (float)xh);
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) t[k] = group_sum(t[k], CC);
+        if (cl == 0 && e < cnt) {
+#pragma unroll
+          for (int k = 0; k < 3; ++k) dnacc[e][k] += t[k];
+        }
+      }
+      // ---- dh B operand: the chunk's S values of column k = 16 w + r, scaled by their own power of two
+      load_s(ch);
+      h8 bh[4], bl[4];
+      h4 bth, btl;
+      float invss;
+      {
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 36; ++i) mx = fmaxf(mx, fabsf(sv[i]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float ss = pow2_scale(mx);
+        invss = 1.f / ss;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float t8[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t8[j] = sv[8 * s + j];
+          split2h(t8, ss, bh[s], bl[s]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = sv[32 + j] * ss;
+          const _Float16 xh = (_Float16)x;
+          bth[j] = xh;
+          btl[j] = (_Float16)(x - (float)xh);
+        }
+      }
+      __syncthreads();
+      // ---- dh: rows = edges (tile et), columns = k in [16*wave, 16*wave+16), K = chunk columns
+#pragma unroll
+      for (int et = 0; et < 4; ++et) {
+        if (et < nrt) {
+          const int row = 16 * et + r;
+          f4 c4 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const h8 xh = *reinterpret_cast<const h8*>(&dpl[0][row][32 * s + 8 * q]);
+            const h8 xl = *reinterpret_cast<const h8*>(&dpl[1][row][32 * s + 8 * q]);
+            c4 = mfma_x3(xh, xl, bh[s], bl[s], c4);
+          }
+          const h4 th = *reinterpret_cast<const h4*>(&dpl[0][row][128 + 4 * q]);
+          const h4 tl = *reinterpret_cast<const h4*>(&dpl[1][row][128 + 4 * q]);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x16f16(tl, bth, c4, 0, 0, 0);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x16f16(th, btl, c4, 0, 0, 0);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x16f16(th, bth, c4, 0, 0, 0);
+          // result row 4q + j of the tile is edge 16 et + 4 q + j, column r is k
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dacc[et][j] += c4[j] * (einv[16 * et + 4 * q + j] * invss);
+        }
+      }
+      // ---- dS^T: rows = k in [16*wave, 16*wave+16), columns = chunk columns, K = edges; the column tiles
+      //      in groups of CTG, each group's results stored before the next group's products
+      // result row 4q + j is k = 16 w + 4 q + j (its 1 / scale held by lane 4 q + j), column r is chunk
+      // column 16 ct + r = slot 2 ct + r/8, channel c0 + r%8
+      float rinv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rinv[j] = __shfl(invsh, 4 * q + j, 64);
+      constexpr int CTG = 3;
+#pragma unroll
+      for (int cg = 0; cg < NCT; cg += CTG) {
+        f4 sacc[CTG];
+#pragma unroll
+        for (int u = 0; u < CTG; ++u) sacc[u] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (s < nks) {
+#pragma unroll
+            for (int u = 0; u < CTG; ++u) {
+              const int ct = cg + u;
+              h8 xh, xl;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                xh[j] = dpl[0][32 * s + 8 * q + j][16 * ct + r];
+                xl[j] = dpl[1][32 * s + 8 * q + j][16 * ct + r];
+              }
+              sacc[u] = mfma_x3(ah[s], al[s], xh, xl, sacc[u]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < CTG; ++u) {
+          const int ct = cg + u;
+          const uint32_t so = (uint32_t)((2 * ct * COLS + c0 * KH) * 4);
+          f4 v = sacc[u];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] *= rinv[j];
+          if (!first) v += buffer_ld4(drs, dvoff, so);
+          buffer_st4(drs, dvoff, so, v);
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        }
+      }
+      if (threadIdx.x < DW) {
+        const int col = threadIdx.x;
+        // rows >= cnt hold zeros: run to a multiple of 8
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+        const int e8 = (cnt + 7) & ~7;
+        for (int e = 0; e < e8; e += 8) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            s4[u & 3] += ((float)dpl[0][e + u][col] + (float)dpl[1][e + u][col]) * einv[e + u];
+        }
+        const float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        float* o = dSm + (int64_t)(col / CC) * COLS + 64 * C + c0 + col % CC;
+        const float fin = first ? sum : (*o + sum);
+        *o = fin;
+        amax = fmaxf(amax, fabsf(fin));
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int et = 0; et < 4; ++et) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 16 * et + 4 * q + j;
+        if (e < cnt) dh[(int64_t)eids[e] * KH + 16 * wave + r] = dacc[et][j];
+      }
+    }
+    if (threadIdx.x < cnt) {
+      const int e = threadIdx.x;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) dn[3 * (int64_t)eids[e] + k] = dnacc[e][k];
+    }
+    first = false;
+    pb += EP;
+    if (pb < end) amax = 0.f;   // block-uniform: only the last edge block's stores are final
+  } while (pb < end);
+  // per-node power of two for the split-fp16 products of node_expand_grad
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if (lane == 0) amx[wave] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) dscale[m] = pow2_scale(fmaxf(fmaxf(amx[0], amx[1]), fmaxf(amx[2], amx[3])));
+}
+
 // ---------------------------------------------------------------- conv1 (species-pair form)
 // conv1 operands depend on the source and receiver only through their species
 // (A_i = atom_mlp(embedding(Z_i))), so the weight contraction over (a, b) is done once
@@ -1324,7 +1669,14 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
   float* tail = dS + N * s_node_stride(C);
   float* dscale = tail + 2LL * NSLOT * N * C;
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
-  {
+  if constexpr (!DIR && !BF16) {
+    // the fp32 message gradient: both products split-fp16, scaled by the receiver gradients' bound
+    float* gmax = tail + (int64_t)NCOMP * N * C;   // after the chunk-major gradient, inside the tail
+    grad_absmax_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(G, gmax, N);
+    LaunchTimer tm("edge_message_grad", st);
+    edge_message_grad_h16_kernel<C><<<xcd_grid(N), 256, 0, st>>>(tail, gmax, nvec, h, S, P, src_ptr, src_perm,
+                                                                 edge_dst, scale, dh, dS, dn, dscale, N, node_order);
+  } else {
     LaunchTimer tm(DIR ? "edge_message_grad_direction" : "edge_message_grad", st);
     edge_message_grad_kernel<C, DIR, BF16><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, udir, h, S, P, src_ptr, src_perm,
                                                               edge_dst, scale, dh, dS, dn, dscale, N, node_order);
