@@ -697,21 +697,63 @@ __device__ __forceinline__ void stage_grad_tables(const FscIctdLayout& L, const 
   }
 }
 
+// The product H = g x^T, whose K dimension is the channels, runs on v_mfma_f32_16x16x32_f16 with three
+// products per K step (mfma_x3, 22 significant bits).  The x rows come pre-split per node
+// (split_rows_h16_kernel: two fp16 planes of x[n] nu_n, nu_n a power of two per node, and 1/nu_n), so the
+// edge loop only loads them; the g rows of a tile are split as they arrive, each kk row with its own power
+// of two (a row spans the four lanes (r, 0..3), K = 8q..8q+7 of every 32-channel step).  H[edge r][kk 4q+i]
+// is then unscaled by 1/(a_kk nu_src), exact powers of two.  K step s takes channels 32s + 8q .. 32s + 8q + 7
+// in both operands.  The chunk walks the path groups in order, so the one or two kk tiles of a group share
+// each loaded x row (a row is gathered once per chunk); a component's row (both planes, all K steps) is
+// loaded one component ahead, across group boundaries.  At C 128 the kernel holds both tiles' split g rows
+// and two x rows: 2 waves/SIMD (measured faster than 3 with the spills that needs).
+__global__ __launch_bounds__(256) void split_rows_h16_kernel(int64_t N, int len, const float* __restrict__ X,
+                                                             _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                             float* __restrict__ inv_scale) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;   // uniform over the wave
+  const f4* x4 = reinterpret_cast<const f4*>(X + n * len);
+  const int n4 = len >> 2;   // len is a multiple of 4 (C >= 32)
+  float mx = 0.f;
+  for (int i = lane; i < n4; i += 64) {
+    const f4 a = x4[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(a[j]));
+  }
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  const float s = pow2_scale(mx);
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  h4* h = reinterpret_cast<h4*>(hi + n * len);
+  h4* l = reinterpret_cast<h4*>(lo + n * len);
+  for (int i = lane; i < n4; i += 64) {
+    const f4 a = x4[i];
+    h4 vh, vl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = a[j] * s;
+      const _Float16 t = (_Float16)v;
+      vh[j] = t;
+      vl[j] = (_Float16)(v - (float)t);
+    }
+    h[i] = vh;
+    l[i] = vl;
+  }
+  if (lane == 0) inv_scale[n] = 1.f / s;   // exact: s is a power of two
+}
+
 template <int C>
-__global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(FscIctdLayout L, int ncg, const float* __restrict__ dZ,
-                                                           const float* __restrict__ x,
-                                                           const float* __restrict__ Y,
-                                                           const float* __restrict__ gates,
-                                                           const float* __restrict__ cg,
-                                                           const int32_t* __restrict__ dst_ptr,
-                                                           const int32_t* __restrict__ esrc,
-                                                           float* __restrict__ dgates, float* __restrict__ dY,
-                                                           int64_t n_nodes, const int32_t* __restrict__ node_order) {
-  constexpr int KS = C / 16;                           // K steps of 16 channels (4 MFMAs each)
+__global__ __launch_bounds__(256, C >= 128 ? 2 : 3) void project_grad_h16_kernel(
+    FscIctdLayout L, int ncg, const float* __restrict__ dZ, const _Float16* __restrict__ xhi,
+    const _Float16* __restrict__ xlo, const float* __restrict__ xinv, const float* __restrict__ Y,
+    const float* __restrict__ gates, const float* __restrict__ cg, const int32_t* __restrict__ dst_ptr,
+    const int32_t* __restrict__ esrc, float* __restrict__ dgates, float* __restrict__ dY, int64_t n_nodes,
+    const int32_t* __restrict__ node_order) {
+  constexpr int KS = C / 32;                           // K steps of 32 channels (3 fp16 MFMAs each)
   extern __shared__ __align__(16) float smem[];
   const GradSmem sm = grad_smem(L, ncg);
-  const int* gidx = reinterpret_cast<const int*>(smem + sm.gidx);
   const int* slot0 = reinterpret_cast<const int*>(smem + sm.slot0);
+  const int* gidx = reinterpret_cast<const int*>(smem + sm.gidx);
   const int* runs = reinterpret_cast<const int*>(smem + sm.runs);
   const int* nrun = reinterpret_cast<const int*>(smem + sm.nrun);
   const float* cf = smem + sm.cf;
@@ -731,9 +773,7 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(Fsc
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  constexpr int KH = KS / 2;
 
-  // the chunks of the block's nodes, in order, go to the waves in turn (flat index mod 4)
   int flat = 0;
   for (int k = 0;; ++k) {
   const int n = xcd_node_k(n_nodes, node_order, k);
@@ -748,7 +788,10 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(Fsc
     const int eb = beg + c * EB, cnt = min(EB, end - eb);
     const bool live = r < cnt;
     const int er = min(eb + r, end - 1);                // the last edge stands in beyond the chunk
-    const float* xr = x + (int64_t)esrc[er] * L.M * C + 4 * q;
+    const int src = esrc[er];
+    const _Float16* xhr = xhi + (int64_t)src * L.M * C + 8 * q;
+    const _Float16* xlr = xlo + (int64_t)src * L.M * C + 8 * q;
+    const float xi = xinv[src];
     f4 yop = f4{0.f, 0.f, 0.f, 0.f};
     if (live) {
       const float* yr = Y + (int64_t)er * L.NY;
@@ -763,88 +806,126 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_grad_kernel(Fsc
     for (int p = q; p < L.NP; p += 4) dgs[p] = 0.f;
     f4 dy = f4{0.f, 0.f, 0.f, 0.f};
 
-    // g rows of tile kt (A operand: kk row r, channels 16 s + 4 q ..; zero beyond the group's rows) and the
-    // gates of its kk rows 4q..4q+3 for edge r
-    auto load_tile = [&](int kt, f4 (&ga)[KS], f4& gt) {
+    // g rows of tile kt (A operand: kk row r, channels 32 s + 8 q ..; zero beyond the group's rows) split
+    // with a power of two a_kk per kk row; inv = 1/(a_kk nu_src) of result rows kk = 4q + i; gt = the gates
+    // of kk rows 4q..4q+3 for edge r
+    auto load_tile = [&](int kt, h8 (&ah)[KS], h8 (&al)[KS], f4& inv, f4& gt) {
       const int g = L.tile_group[kt];
       const int tb = (kt - L.g_tile0[g]) * 16;
       const bool okr = tb + r < L.g_kcount[g];
-      const float* gr = dZ + ((int64_t)n * L.KT + L.g_kstart[g] + (okr ? tb + r : 0)) * C + 4 * q;
+      const float* gr = dZ + ((int64_t)n * L.KT + L.g_kstart[g] + (okr ? tb + r : 0)) * C + 8 * q;
+      f4 ga[2 * KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) ga[s] = okr ? ld4(gr + 16 * s) : f4{0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < KS; ++s) {
+        ga[2 * s] = okr ? ld4(gr + 32 * s) : f4{0.f, 0.f, 0.f, 0.f};
+        ga[2 * s + 1] = okr ? ld4(gr + 32 * s + 4) : f4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) gt[i] = live ? gates[(int64_t)er * L.NREF + gidx[kt * 16 + 4 * q + i]] : 0.f;
-    };
-    // half h of the x row of component m (channels 16 (h KH + s) + 4 q ..)
-    auto load_half = [&](int m, int h, f4 (&b)[KH]) {
+      float mx = 0.f;
 #pragma unroll
-      for (int s = 0; s < KH; ++s) b[s] = ld4(xr + m * C + 16 * (h * KH + s));
+      for (int s = 0; s < 2 * KS; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(ga[s][j]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float a = pow2_scale(mx);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const float v[8] = {ga[2 * s].x, ga[2 * s].y, ga[2 * s].z, ga[2 * s].w,
+                            ga[2 * s + 1].x, ga[2 * s + 1].y, ga[2 * s + 1].z, ga[2 * s + 1].w};
+        split2h(v, a, ah[s], al[s]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) inv[i] = __shfl(1.f / a, 4 * q + i, 64) * xi;   // exact: powers of two
     };
-    // one tile: its (m1) products, with the next tile's operands requested at its start and the first
-    // half-row of the next product always in flight
-    auto tile = [&](int kt, const f4 (&ga)[KS], const f4& gt, f4 (&gn)[KS], f4& gtn, f4 (&h0)[KH], f4 (&h1)[KH]) {
-      const int g = L.tile_group[kt];
+    // x row of component m, both planes, every K step
+    auto load_row = [&](int m, h8 (&bh)[KS], h8 (&bl)[KS]) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        bh[s] = *reinterpret_cast<const h8*>(xhr + m * C + 32 * s);
+        bl[s] = *reinterpret_cast<const h8*>(xlr + m * C + 32 * s);
+      }
+    };
+    // the products of component m1 of tile kt from the x row in (bh, bl)
+    auto product = [&](int kt, int m1, const h8 (&bh)[KS], const h8 (&bl)[KS], const h8 (&ah)[KS],
+                       const h8 (&al)[KS], const f4& inv, const f4& gt, f4& P) {
+      f4 ht = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) ht = mfma_x3(ah[s], al[s], bh[s], bl[s], ht);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ht[i] *= inv[i];                             // H[edge r][kk 4q+i]
+      const float* cs = cf + (slot0[kt] + m1) * 256;
+      f4 ca;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ca[j] = cs[(4 * q + j) * 16 + r];          // Cf[y = 4q+j][kk = r]
+      const f4 ct = *reinterpret_cast<const f4*>(cs + r * 16 + 4 * q);      // Cf[y = r][kk = 4q..4q+3]
+      const f4 bgt = mfma_k16(ca, yop, f4{0.f, 0.f, 0.f, 0.f});              // BG'[edge r][kk 4q+i]
+      f4 hg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        P[i] += ht[i] * bgt[i];
+        hg[i] = ht[i] * gt[i];
+      }
+      dy = mfma_k16(hg, ct, dy);                                             // dY[edge 4q+i][y = r]
+    };
+    // groups in order; a group's (one or two) tiles share each loaded x row
+    h8 b0h[KS], b0l[KS], b1h[KS], b1l[KS];
+    load_row(L.g_o1[0], b0h, b0l);
+    for (int g = 0; g < L.NG; ++g) {
       const int d1 = L.g_d1[g], o1 = L.g_o1[g];
-      const bool more = kt + 1 < L.KTT;
-      const int o1n = more ? L.g_o1[L.tile_group[kt + 1]] : 0;
-      if (more) load_tile(kt + 1, gn, gtn);
-      const float* cft = cf + slot0[kt] * 256;
-      f4 P = f4{0.f, 0.f, 0.f, 0.f};
-      for (int m1 = 0; m1 < d1; ++m1) {
-        load_half(o1 + m1, 1, h1);
-        __builtin_amdgcn_sched_barrier(0);
-        // two accumulation chains, so consecutive MFMAs do not wait on each other's result
-        f4 ht0 = f4{0.f, 0.f, 0.f, 0.f}, ht1 = f4{0.f, 0.f, 0.f, 0.f};
+      const int t0 = L.g_tile0[g], nt = L.g_kpad[g] / 16;      // 1 or 2
+      const bool more = g + 1 < L.NG;
+      const int o1n = more ? L.g_o1[g + 1] : 0;
+      h8 ah[2][KS], al[2][KS];
+      f4 inv[2], gt[2], P[2];
 #pragma unroll
-        for (int s = 0; s < KH; ++s) {
-          ht0 = mfma16x16x4(ga[s].x, h0[s].x, ht0);
-          ht1 = mfma16x16x4(ga[s].y, h0[s].y, ht1);
-          ht0 = mfma16x16x4(ga[s].z, h0[s].z, ht0);
-          ht1 = mfma16x16x4(ga[s].w, h0[s].w, ht1);
-        }
-        if (m1 + 1 < d1) load_half(o1 + m1 + 1, 0, h0);
-        else if (more) load_half(o1n, 0, h0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = 0; s < KH; ++s) {
-          ht0 = mfma16x16x4(ga[KH + s].x, h1[s].x, ht0);
-          ht1 = mfma16x16x4(ga[KH + s].y, h1[s].y, ht1);
-          ht0 = mfma16x16x4(ga[KH + s].z, h1[s].z, ht0);
-          ht1 = mfma16x16x4(ga[KH + s].w, h1[s].w, ht1);
-        }
-        const f4 ht = ht0 + ht1;                                               // H[edge r][kk 4q+i]
-        const float* cs = cft + m1 * 256;
-        f4 ca;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ca[j] = cs[(4 * q + j) * 16 + r];          // Cf[y = 4q+j][kk = r]
-        const f4 ct = *reinterpret_cast<const f4*>(cs + r * 16 + 4 * q);      // Cf[y = r][kk = 4q..4q+3]
-        const f4 bgt = mfma_k16(ca, yop, f4{0.f, 0.f, 0.f, 0.f});              // BG'[edge r][kk 4q+i]
-        f4 hg;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          P[i] += ht[i] * bgt[i];
-          hg[i] = ht[i] * gt[i];
-        }
-        dy = mfma_k16(hg, ct, dy);                                             // dY[edge 4q+i][y = r]
+      for (int tt = 0; tt < 2; ++tt) {
+        P[tt] = f4{0.f, 0.f, 0.f, 0.f};
+        if (tt < nt) load_tile(t0 + tt, ah[tt], al[tt], inv[tt], gt[tt]);
       }
-      // per-path sums of the tile's rows: lanes (r, q) take runs q, q + 4, ...
-      *reinterpret_cast<f4*>(pl + r * 16 + 4 * q) = P;
-      wave_sync();
-      for (int k = q; k < nrun[kt]; k += 4) {
-        const int run = runs[kt * 16 + k];
-        const int p = run & 255, rb = (run >> 8) & 255, re = run >> 16;
-        float sum = 0.f;
-        for (int i = rb; i < re; ++i) sum += pl[r * 16 + i];
-        dgs[p] += sum;
+      auto products = [&](int m1, const h8 (&bh)[KS], const h8 (&bl)[KS]) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          if (tt < nt) product(t0 + tt, m1, bh, bl, ah[tt], al[tt], inv[tt], gt[tt], P[tt]);
+      };
+      // b0 holds the row of component m1 on entry to each pair; the row after the group's last is the
+      // next group's first
+      for (int m1 = 0; m1 < d1; m1 += 2) {
+        if (m1 + 1 < d1) load_row(o1 + m1 + 1, b1h, b1l);
+        else if (more) load_row(o1n, b1h, b1l);
+        __builtin_amdgcn_sched_barrier(0);
+        products(m1, b0h, b0l);
+        if (m1 + 1 < d1) {
+          if (m1 + 2 < d1) load_row(o1 + m1 + 2, b0h, b0l);
+          else if (more) load_row(o1n, b0h, b0l);
+          __builtin_amdgcn_sched_barrier(0);
+          products(m1 + 1, b1h, b1l);
+        }
       }
-      wave_sync();
-    };
-    f4 gaA[KS], gaB[KS], gtA, gtB, h0[KH], h1[KH];
-    load_tile(0, gaA, gtA);
-    load_half(L.g_o1[L.tile_group[0]], 0, h0);
-    for (int kt = 0; kt < L.KTT; kt += 2) {
-      tile(kt, gaA, gtA, gaB, gtB, h0, h1);
-      if (kt + 1 < L.KTT) tile(kt + 1, gaB, gtB, gaA, gtA, h0, h1);
+      if ((d1 & 1) && more) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          b0h[s] = b1h[s];
+          b0l[s] = b1l[s];
+        }
+      }
+      // per-path sums of each tile's rows: lanes (r, q) take runs q, q + 4, ...
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        if (tt >= nt) continue;
+        const int kt = t0 + tt;
+        *reinterpret_cast<f4*>(pl + r * 16 + 4 * q) = P[tt];
+        wave_sync();
+        for (int k2 = q; k2 < nrun[kt]; k2 += 4) {
+          const int run = runs[kt * 16 + k2];
+          const int p = run & 255, rb = (run >> 8) & 255, re = run >> 16;
+          float sum = 0.f;
+          for (int i = rb; i < re; ++i) sum += pl[r * 16 + i];
+          dgs[p] += sum;
+        }
+        wave_sync();
+      }
     }
     if (live)
       for (int p = q; p < L.NP; p += 4) dgates[(int64_t)(eb + r) * L.NREF + L.p_gate[p]] = dgs[p] * scale;
@@ -1374,11 +1455,17 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   }
   if (check_launch("ictd mix_bwd")) return 2;
   {
+    // x split into fp16 planes with a power of two per node, in the dual workspace (free until the dual
+    // projection: N D.KT C + N floats hold the N M C halves of each plane and the N scales, D.KT >= M)
+    _Float16* xhi = reinterpret_cast<_Float16*>(Rw);
+    _Float16* xlo = xhi + N * L.M * C;
+    float* xinv = Rw + N * L.M * C;
+    split_rows_h16_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, L.M * C, x, xhi, xlo, xinv);
     LaunchTimer tm("ictd_project_grad", st);
     const int ncg = cg_length(L);
     const size_t lds = (size_t)grad_smem(L, ncg).total * sizeof(float);
-    project_grad_kernel<C><<<persist_grid(N, (const void*)project_grad_kernel<C>, lds), 256, lds, st>>>(L, ncg, dZ, x, Y, gates, cg, dst_ptr, esrc, dgates, dY,
-                                                           N, node_order);
+    project_grad_h16_kernel<C><<<persist_grid(N, (const void*)project_grad_h16_kernel<C>, lds), 256, lds, st>>>(
+        L, ncg, dZ, xhi, xlo, xinv, Y, gates, cg, dst_ptr, esrc, dgates, dY, N, node_order);
   }
   if (check_launch("ictd project_grad")) return 2;
   // input gradient: dual projection over the source grouping, then the mix with W^T
