@@ -554,9 +554,14 @@ __global__ __launch_bounds__(512, D == 1 ? 4 : 2) void backward_h16_kernel(int64
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-        for (int m = 0; m < D; ++m)
-          acc[4 * i4 + jj][m] += dd[jj][0] * tc[m][0] + dd[jj][1] * tc[m][1] + dd[jj][2] * tc[m][2] +
-                                 dd[jj][3] * tc[m][3];
+        for (int m = 0; m < D; ++m) {
+          // one fma per product into the running sum (a sum of products added at the end costs a mul
+          // and an add more per four products)
+          float a = acc[4 * i4 + jj][m];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) a = fmaf(dd[jj][k], tc[m][k], a);
+          acc[4 * i4 + jj][m] = a;
+        }
     }
   }
   constexpr int H = ILW / 2, QR = ILW / 4;
