@@ -311,11 +311,13 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 }
 
 // ---------------------------------------------------------------- K6: node expansion grad
-// dxp[kh][slot][m][a] = sum_{col in half kh} dS[m][slot][col] * bk6[p][a][col] for every slot
-// row (m, I) of path p, then dx[m][comp][a] = sum over the halves and the slots of comp
-// (node_expand_grad_combine).  A block's work unit is (path, 256-row tile, K half), one 64-row
+// dxp[kh][slot][m][a] = sum_{col in K part kh} dS[m][slot][col] * bk6[p][a][col] for every slot
+// row (m, I) of path p, then dx[m][comp][a] = sum over the K parts and the slots of comp
+// (node_expand_grad_combine).  A block's work unit is (path, 256-row tile, K part), one 64-row
 // strip per wave: all units are equally long, which keeps the blocks balanced although paths
-// 0-2 share component 0.  Products are split-fp16 (mfma_x3, fp32 accuracy at 5x the fp32 MFMA
+// 0-2 share component 0.  K is split in ks parts (neg_ksplit: 2, more while the grid of
+// (path, tile) units is small, so that a few hundred atoms do not leave a handful of blocks each
+// walking 65 K chunks in sequence).  Products are split-fp16 (mfma_x3, fp32 accuracy at 5x the fp32 MFMA
 // rate): the weights come split (bk6 parts h, l, scaled by sw), the dS rows are scaled by their node's
 // power of two (dscale, from edge_message_grad) and split in registers.  The four
 // waves share the path's weights: each 32-column chunk (C x 32 x 3 parts) is loaded once per block
@@ -324,6 +326,21 @@ __global__ __launch_bounds__(256, 2) void node_expand_kernel(const float* __rest
 // i is a = (C/4)*(i/4) + 4*at + i%4, so lane (r, q) ends with C/4 consecutive a of one row; lane
 // group q holds chunk columns 8q..8q+7 of both operands.
 constexpr int NEG_ROWS = 256;   // slot rows per block
+constexpr int NEG_KSPLIT_MAX = 16;
+
+// (path, row tile) units of node_expand_grad, and its K parts: a function of N alone, since the
+// workspace holds one partial input gradient per part
+inline int neg_tiles(int64_t N) {
+  int64_t t = 0;
+  for (int p = 0; p < 6; ++p) t += (N * kNumI[kPathL1H[p]] + NEG_ROWS - 1) / NEG_ROWS;
+  return (int)std::min<int64_t>(t, 1 << 30);
+}
+inline int neg_ksplit(int64_t N) {
+  const int64_t tiles = neg_tiles(N);
+  int ks = 2;
+  while (ks < NEG_KSPLIT_MAX && tiles * ks < 512) ks *= 2;
+  return ks;
+}
 
 template <int C, bool BF16>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
@@ -331,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
                                                                   const _Float16* __restrict__ bk6,
                                                                   const float* __restrict__ winv,
                                                                   float* __restrict__ dxp,
-                                                                  int64_t n_nodes, PathTiles tiles) {
+                                                                  int64_t n_nodes, PathTiles tiles, int ks) {
   constexpr int COLS = 65 * C;
   constexpr int NA = C / 16;        // output a tiles
   constexpr int QW = C / 4;         // consecutive a per lane in the output
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   __shared__ __align__(16) _Float16 wsh[2][2][C][RS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int kh = blockIdx.x & 1, bt = blockIdx.x >> 1;
+  const int kh = (int)(blockIdx.x % (unsigned)ks), bt = (int)(blockIdx.x / (unsigned)ks);
   int p = 0;
   while (p < 5 && bt >= tiles.off[p + 1]) ++p;
   const int L1 = kPathL1[p];
@@ -375,7 +392,7 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
 #pragma unroll
     for (int at = 0; at < NA; ++at) acc[rt][at] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int tb = kh ? TPP / 2 : 0, te = kh ? TPP : TPP / 2;
+  const int tb = kh * TPP / ks, te = (kh + 1) * TPP / ks;   // ks <= 16 < TPP: every part is non-empty
   f4 stg[NST], bc[4][2], bn[4][2];
   auto load_w = [&](int t) {
 #pragma unroll
@@ -463,11 +480,11 @@ __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* _
   }
 }
 
-// dx[m][comp][a] = sum over the two K halves and the slots of comp: comp 0 <- slots 0,1,2;
+// dx[m][comp][a] = sum over the K parts and the slots of comp: comp 0 <- slots 0,1,2;
 // comp 1+i <- slots 3+i, 6+i; comp 4+ij <- slot 9+ij.
 template <int C>
 __global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, float* __restrict__ dx,
-                                                int64_t n_nodes) {
+                                                int64_t n_nodes, int ks) {
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // over N*13*C/4
   if (idx >= n_nodes * NCOMP * (C / 4)) return;
   const int a4 = (int)(idx % (C / 4));
@@ -482,9 +499,13 @@ __global__ void node_expand_grad_combine_kernel(const float* __restrict__ dxp, f
   } else {
     sl[0] = 5 + comp; sl[1] = 0; sl[2] = 0; ns = 1;
   }
+  // slot by slot, the K parts in order (unrolled: their loads go out together)
   f4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int kh = 0; kh < 2; ++kh)
-    for (int i = 0; i < ns; ++i) s += ld4(dxp + (((int64_t)kh * NSLOT + sl[i]) * n_nodes + m) * C + 4 * a4);
+  for (int i = 0; i < ns; ++i) {
+    const float* base = dxp + ((int64_t)sl[i] * n_nodes + m) * C + 4 * a4;
+#pragma unroll 8
+    for (int kh = 0; kh < ks; ++kh) s += ld4(base + (int64_t)kh * NSLOT * n_nodes * C);
+  }
   st4(dx + (m * NCOMP + comp) * C + 4 * a4, s);
 }
 
@@ -1664,10 +1685,12 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
                        const float* P, float scale, float* dS, float* dx, float* dh, float* dn,
                        const int32_t* node_order, hipStream_t st, const float* udir = nullptr) {
   if (N == 0) return 0;
-  // workspace tail (2 x 18 x N x C floats): first the chunk-major receiver gradient (13 x N x C), later
-  // the partial input gradients of node_expand_grad; then N per-node scales of dS
+  // workspace tail (ks x 18 x N x C floats, ks = neg_ksplit(N) >= 2): first the chunk-major receiver
+  // gradient (13 x N x C), later the partial input gradients of node_expand_grad; then N per-node
+  // scales of dS
+  const int ks = neg_ksplit(N);
   float* tail = dS + N * s_node_stride(C);
-  float* dscale = tail + 2LL * NSLOT * N * C;
+  float* dscale = tail + (int64_t)ks * NSLOT * N * C;
   grad_chunk_major_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(G, tail, N);
   if constexpr (!DIR && !BF16) {
     // the fp32 message gradient: both products split-fp16, scaled by the receiver gradients' bound
@@ -1687,16 +1710,17 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
     tiles.off[0] = 0;
     for (int p = 0; p < 6; ++p)
       tiles.off[p + 1] = tiles.off[p] + (int)((N * kNumI[kPathL1H[p]] + NEG_ROWS - 1) / NEG_ROWS);
-    float* dxp = dS + N * s_node_stride(C);   // workspace tail: 2 x 18 x N x C partial sums (Gt is dead)
+    float* dxp = dS + N * s_node_stride(C);   // workspace tail: ks x 18 x N x C partial sums (Gt is dead)
     {
       LaunchTimer tm("node_expand_grad", st);
       const float* wplane = BF16 ? bk6 + sparse_weight_floats(C) : bk6;
-      node_expand_grad_kernel<C, BF16><<<(unsigned)(2 * tiles.off[6]), 256, 0, st>>>(
+      node_expand_grad_kernel<C, BF16><<<(unsigned)(ks * tiles.off[6]), 256, 0, st>>>(
           dS, dscale, reinterpret_cast<const _Float16*>(wplane), bk6 + sparse_weight_floats(C) - SW_TAIL, dxp, N,
-          tiles);
+          tiles, ks);
     }
     if (check_launch("sparse node_expand_grad")) return 2;
-    node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N);
+    node_expand_grad_combine_kernel<C><<<(unsigned)((N * NCOMP * (C / 4) + 255) / 256), 256, 0, st>>>(dxp, dx, N,
+                                                                                                     ks);
   }
   return check_launch("sparse node_expand_grad") ? 2 : 0;
 }
@@ -1715,8 +1739,9 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_workspace: negative size");
   FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_workspace: channels must be 32 or 64");
   FSC_CHECK_ARG(s_floats && p_floats, "fsc_sparse_conv_workspace: null output");
-  // the tail (2 x 18 x N x C + N) holds the partial input gradients and per-node scales of the backward
-  *s_floats = n_nodes * s_node_stride(channels) + 2LL * NSLOT * n_nodes * channels + n_nodes;
+  // the tail (ks x 18 x N x C + N, ks = neg_ksplit(N)) holds the partial input gradients and per-node
+  // scales of the backward
+  *s_floats = n_nodes * s_node_stride(channels) + (int64_t)neg_ksplit(n_nodes) * NSLOT * n_nodes * channels + n_nodes;
   *p_floats = n_edges * (int64_t)NSLOT * channels;
   return 0;
 }

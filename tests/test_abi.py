@@ -34,7 +34,11 @@ def test_argument_errors_are_reported_without_a_gpu():
     lib = _lib.load()
     s, p = ctypes.c_int64(), ctypes.c_int64()
     assert lib.fsc_sparse_conv_workspace(10, 20, 64, ctypes.byref(s), ctypes.byref(p)) == 0
-    assert s.value == 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10 and p.value == 20 * 18 * 64
+    # the tail holds ks partial input gradients of the node-expansion gradient: ks = 16 for ten nodes (six
+    # row tiles), 2 from about 5,000 nodes on
+    assert s.value == 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10 and p.value == 20 * 18 * 64
+    assert lib.fsc_sparse_conv_workspace(10000, 20, 64, ctypes.byref(s), ctypes.byref(p)) == 0
+    assert s.value == 10000 * 18 * 65 * 64 + 2 * 18 * 10000 * 64 + 10000
     assert lib.fsc_sparse_conv_workspace(10, 20, 48, ctypes.byref(s), ctypes.byref(p)) == 1
     assert b"channels" in lib.fsc_last_error()
     with pytest.raises(RuntimeError, match="negative"):
@@ -70,7 +74,7 @@ def test_fake_kernels_trace_shapes():
         i = torch.empty(11, dtype=torch.int32)
         e = torch.empty(30, dtype=torch.int32)
         out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, torch.empty(0, dtype=torch.int32))
-        assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10,) and P.shape == (30 * 18 * 64,)
+        assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10,) and P.shape == (30 * 18 * 64,)
 
 
 def test_gram_sizes_and_fake_kernels():
