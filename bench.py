@@ -576,13 +576,21 @@ def measure_small(name: str, steps: int, warmup: int, dev) -> dict:
 
     work = sparse_kernel_work(w["kernel"], N, E, C)
     avg_ms = kt.total_ms / max(kt.launches, 1)
-    peak = PRODUCT_PEAK_TFLOPS[kernel_products(w["kernel"])]
-    achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 1), "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "products": kernel_products(w["kernel"]), "traffic": None,
-            "kernel": w["kernel"], "avg_launch_ms": round(avg_ms, 4), "launches": kt.launches,
-            "algorithmic_per_launch": {"flops": work["flops"], "bytes": work["bytes"]},
-            "note": "launch-bound system: the kernel is a few microseconds; the step time is set by launches"}
+    if work["bound"] == "mfma":
+        peak = PRODUCT_PEAK_TFLOPS[kernel_products(w["kernel"])]
+        achieved = work["flops"] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 1), "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "products": kernel_products(w["kernel"])}
+    else:
+        achieved = work["bytes"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    launch_bound = graph_ms < 0.8 * eager_ms
+    roof.update({"traffic": None, "kernel": w["kernel"], "avg_launch_ms": round(avg_ms, 4), "launches": kt.launches,
+                 "algorithmic_per_launch": {"flops": work["flops"], "bytes": work["bytes"]},
+                 "note": (f"HIP-graph replay {graph_ms:.3f} ms/step against {eager_ms:.3f} eager: "
+                          + ("launch-bound at this size (the kernel is tens of microseconds)" if launch_bound else
+                             "kernel-bound at this size (launches cost little)"))})
     e_np, f_np = e_cap.double().cpu().numpy(), f_cap.double().cpu().numpy()
     if golden is not None:
         parity = {"fixture": f"tests/golden/{w['golden']}.npz", "reference": "the reference trunk in fp64 "
