@@ -1571,18 +1571,26 @@ int fsc_ictd_conv1_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t
   FSC_CHECK_ARG(n_species >= 1 && n_species <= 16, "fsc_ictd_conv1_forward: 1..16 species supported");
   FSC_CHECK_ARG(dst_ptr && node_species && qtab && out, "fsc_ictd_conv1_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && F && gates), "fsc_ictd_conv1_forward: null edge pointer");
-  FSC_CHECK_ARG(layout->NY == 9 || layout->NY == 16, "fsc_ictd_conv1_forward: lmax must be 2 or 3");
+  FSC_CHECK_ARG(layout->NY == 1 || layout->NY == 4 || layout->NY == 9 || layout->NY == 16,
+                "fsc_ictd_conv1_forward: lmax must be 0, 1, 2 or 3");
   if (n_nodes == 0) return 0;
   const FscIctdLayout& L = *layout;
   LaunchTimer tm("ictd_conv1", stream);
   const unsigned grid = (unsigned)n_nodes;
 #define FSC_C1F(CC, NYY) \
   conv1_fwd_kernel<CC, NYY><<<grid, 256, 0, stream>>>(L, n_species, dst_ptr, edge_pair, node_species, F, gates, qtab, out)
-  if (L.NY == 9) {
-    if (channels == 128) FSC_C1F(128, 9); else if (channels == 64) FSC_C1F(64, 9); else FSC_C1F(32, 9);
+#define FSC_C1F_NY(NYY) \
+  if (channels == 128) FSC_C1F(128, NYY); else if (channels == 64) FSC_C1F(64, NYY); else FSC_C1F(32, NYY)
+  if (L.NY == 1) {
+    FSC_C1F_NY(1);
+  } else if (L.NY == 4) {
+    FSC_C1F_NY(4);
+  } else if (L.NY == 9) {
+    FSC_C1F_NY(9);
   } else {
-    if (channels == 128) FSC_C1F(128, 16); else if (channels == 64) FSC_C1F(64, 16); else FSC_C1F(32, 16);
+    FSC_C1F_NY(16);
   }
+#undef FSC_C1F_NY
 #undef FSC_C1F
   return check_launch("ictd conv1_fwd") ? 2 : 0;
 }
@@ -1599,18 +1607,26 @@ int fsc_ictd_conv1_backward(const FscIctdLayout* layout, int64_t n_nodes, int64_
   FSC_CHECK_ARG(dst_ptr && node_species && grad_out && qtab, "fsc_ictd_conv1_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (edge_pair && F && gates && grad_F && grad_gates),
                 "fsc_ictd_conv1_backward: null edge pointer");
-  FSC_CHECK_ARG(layout->NY == 9 || layout->NY == 16, "fsc_ictd_conv1_backward: lmax must be 2 or 3");
+  FSC_CHECK_ARG(layout->NY == 1 || layout->NY == 4 || layout->NY == 9 || layout->NY == 16,
+                "fsc_ictd_conv1_backward: lmax must be 0, 1, 2 or 3");
   if (n_nodes == 0) return 0;
   const FscIctdLayout& L = *layout;
   LaunchTimer tm("ictd_conv1_grad", stream);
   const unsigned grid = (unsigned)n_nodes;
 #define FSC_C1B(CC, NYY) conv1_bwd_kernel<CC, NYY><<<grid, 256, 0, stream>>>(L, n_species, dst_ptr, edge_pair, \
       node_species, grad_out, F, gates, qtab, grad_F, grad_gates)
-  if (L.NY == 9) {
-    if (channels == 128) FSC_C1B(128, 9); else if (channels == 64) FSC_C1B(64, 9); else FSC_C1B(32, 9);
+#define FSC_C1B_NY(NYY) \
+  if (channels == 128) FSC_C1B(128, NYY); else if (channels == 64) FSC_C1B(64, NYY); else FSC_C1B(32, NYY)
+  if (L.NY == 1) {
+    FSC_C1B_NY(1);
+  } else if (L.NY == 4) {
+    FSC_C1B_NY(4);
+  } else if (L.NY == 9) {
+    FSC_C1B_NY(9);
   } else {
-    if (channels == 128) FSC_C1B(128, 16); else if (channels == 64) FSC_C1B(64, 16); else FSC_C1B(32, 16);
+    FSC_C1B_NY(16);
   }
+#undef FSC_C1B_NY
 #undef FSC_C1B
   return check_launch("ictd conv1_bwd") ? 2 : 0;
 }

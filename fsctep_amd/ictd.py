@@ -26,6 +26,8 @@ from .graph import Graph, poison_invalid, prepare_species_graph, species_rows
 from .ictd_basis import canonical, coupling, layout_full, layout_o3
 from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
 
+LMAX_KERNELS = 3     # (lmax + 1)^2 <= 16 harmonic components in the projection and conv1 kernels
+
 
 def _key_str(k) -> str:
     return f"{k[0]}{'e' if k[1] > 0 else 'o'}"
@@ -322,13 +324,14 @@ class _ICTDTrunk(nn.Module):
 
 
 class PureCartesianICTDTransformerLayer(_ICTDTrunk):
-    """Drop-in for the reference ``pure-cartesian-ictd`` trunk (lmax 2 or 3)."""
+    """Drop-in for the reference ``pure-cartesian-ictd`` trunk (lmax 0 to 3)."""
 
     o3 = False
 
     def _make_layout(self, preset, active, phys):
-        if self.lmax not in (2, 3):
-            raise NotImplementedError("HIP ICTD path: lmax 2 or 3")
+        if not 0 <= self.lmax <= LMAX_KERNELS:
+            raise NotImplementedError(f"HIP ICTD path: lmax 0 to {LMAX_KERNELS} (the kernels take at most "
+                                      "16 harmonic and 16 feature components)")
         return layout_full(self.lmax)
 
 
@@ -400,6 +403,9 @@ class PureCartesianICTDO3TransformerLayer(_ICTDTrunk):
     o3 = True
 
     def _make_layout(self, preset, active, phys):
+        if not 0 <= self.lmax <= LMAX_KERNELS:
+            raise NotImplementedError(f"HIP ICTD-O3 path: lmax 0 to {LMAX_KERNELS} (the kernels take at most "
+                                      "16 harmonic components)")
         keys = resolve_o3_keys(self.lmax, preset, active, "1o" if self.external_field else None, phys)
         for l in range(self.lmax + 1):
             if canonical(l) not in keys:

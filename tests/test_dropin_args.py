@@ -80,3 +80,16 @@ def test_o3_presets_the_kernels_cannot_run_are_refused():
         PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="balanced")      # 17 components
     with pytest.raises(NotImplementedError, match="geometric"):
         PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="minimal")       # no 1o, 2e
+
+
+def test_lmax_range_is_checked_at_construction():
+    """lmax 0 to 3 construct (the kernels' 16 harmonic components); lmax 4 is refused before any forward."""
+    for lmax in (0, 1, 3):
+        m = PureCartesianICTDTransformerLayer(**BASE, lmax=lmax)
+        assert m.layout.NY == (lmax + 1) ** 2
+    m = PureCartesianICTDO3TransformerLayer(**BASE, lmax=1, o3_active_irreps="0e,1o")
+    assert m.keys == [E0, O1]
+    with pytest.raises(NotImplementedError, match="lmax 0 to 3"):
+        PureCartesianICTDTransformerLayer(**BASE, lmax=4)
+    with pytest.raises(NotImplementedError, match="lmax 0 to 3"):
+        PureCartesianICTDO3TransformerLayer(**BASE, lmax=4, o3_active_irreps="0e,1o,2e,3o,4e")
