@@ -63,7 +63,7 @@ int main(int argc, char** argv) {
                     int64_t, const std::optional<at::Tensor>&, const std::optional<at::Tensor>&)>();
   auto no_order = at::empty({0}, at::device(at::kMeta).dtype(at::kInt));
   auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order, 0, std::nullopt, std::nullopt);
-  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 2 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
+  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;
   }
