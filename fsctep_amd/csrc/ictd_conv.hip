@@ -976,14 +976,14 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
                                                         const float* __restrict__ qtab, float* __restrict__ out) {
   __shared__ float w[16][NY];
   __shared__ float part[16][16][NY];   // [edge lane][source species][y]
-  __shared__ int ycomp[16], yrow[16];
+  __shared__ int ycomp[32], yrow[32];   // M <= 32 components
   __shared__ int ssp[256];
   __shared__ unsigned smask;
   const int n = blockIdx.x, t = threadIdx.x;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const int sn = node_species[n];
   fill_pair_species(NS, ssp);
-  if (t < 16) {   // component -> the harmonic y whose path writes it (-1: none) and that path's table row
+  if (t < 32) {   // component -> the harmonic y whose path writes it (-1: none) and that path's table row
     int yy = -1;
 #pragma unroll
     for (int y = 0; y < NY; ++y)
@@ -1023,29 +1023,31 @@ __global__ __launch_bounds__(256) void conv1_fwd_kernel(FscIctdLayout L, int NS,
   __syncthreads();
   const float scale = 1.f / (float)max(end - beg, 1);
   float* on = out + (int64_t)n * L.M * C;
-  const int MC = L.M * C;                 // <= 16 * 128 = 8 * 256
-  float v[8];
+  const int MC = L.M * C;                 // <= 32 * 128: at most two passes of 8 * 256 outputs
+  for (int base = 0; base < MC; base += 8 * 256) {
+    float v[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) v[u] = 0.f;
-  // source species outermost (increasing order), the thread's outputs innermost: their table reads are
-  // independent and go out together
-  for (unsigned m = mask; m; m &= m - 1) {
-    const int s2 = __builtin_ctz(m);
-    const float* qs = qtab + ((int64_t)(s2 * NS + sn) * L.NP1) * C;   // pair (s2, sn)
+    for (int u = 0; u < 8; ++u) v[u] = 0.f;
+    // source species outermost (increasing order), the thread's outputs innermost: their table reads are
+    // independent and go out together
+    for (unsigned m = mask; m; m &= m - 1) {
+      const int s2 = __builtin_ctz(m);
+      const float* qs = qtab + ((int64_t)(s2 * NS + sn) * L.NP1) * C;   // pair (s2, sn)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u;
-      if (i < MC) {
-        const int c = i / C, o = i - c * C;
-        const int yy = ycomp[c];
-        if (yy >= 0) v[u] += w[s2][yy] * qs[yrow[c] * C + o];
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + t + 256 * u;
+        if (i < MC) {
+          const int c = i / C, o = i - c * C;
+          const int yy = ycomp[c];
+          if (yy >= 0) v[u] += w[s2][yy] * qs[yrow[c] * C + o];
+        }
       }
     }
-  }
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int i = t + 256 * u;
-    if (i < MC) on[i] = v[u] * scale;
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + t + 256 * u;
+      if (i < MC) on[i] = v[u] * scale;
+    }
   }
 }
 
@@ -1218,7 +1220,7 @@ int check_layout(const FscIctdLayout* L, int32_t C, const char* who) {
   if (!L) { set_error(std::string(who) + ": null layout"); return 1; }
   if (!(C == 32 || C == 64 || C == 128)) { set_error(std::string(who) + ": channels must be 32, 64 or 128"); return 1; }
   if (L->NG < 1 || L->NG > 8 || L->NP < 1 || L->NP > 64 || L->KT < 1 || L->KT > 128 || L->KTT < 1 ||
-      L->KTT > 8 || L->NY < 1 || L->NY > 16 || L->M < 1 || L->M > 16 || L->NREF < L->NP || L->NK < 1 ||
+      L->KTT > 8 || L->NY < 1 || L->NY > 16 || L->M < 1 || L->M > 32 || L->NREF < L->NP || L->NK < 1 ||
       L->NK > 16 || L->NP1 < 0 || L->NP1 > 16 || L->NBGP < 1 || (L->NBGP % 4) != 0) {
     set_error(std::string(who) + ": layout table out of range");
     return 1;

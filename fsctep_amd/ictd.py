@@ -411,11 +411,12 @@ class PureCartesianICTDO3TransformerLayer(_ICTDTrunk):
             if canonical(l) not in keys:
                 raise NotImplementedError(f"HIP ICTD-O3 path: active irreps {keys} lack the geometric irrep "
                                           f"{canonical(l)}; the kernels need 0e,1o,2e,.. up to lmax")
-        M = sum(2 * l + 1 for l, _ in keys)
-        if M > 16:
-            raise NotImplementedError(f"HIP ICTD-O3 path: active irreps {[_key_str(k) for k in keys]} have {M} "
-                                      "components per channel; the kernels take at most 16")
-        return layout_o3(self.lmax, keys)
+        lay = layout_o3(self.lmax, keys)
+        problems = ictd_ops.kernel_limits(lay)
+        if problems:
+            raise NotImplementedError(f"HIP ICTD-O3 path: active irreps {[_key_str(k) for k in keys]} exceed the "
+                                      "kernels' tables: " + "; ".join(problems))
+        return lay
 
 
 def energy_forces(model, pos, batch, cell, graph, external_tensor=None):

@@ -38,6 +38,36 @@ class FscIctdLayout(ctypes.Structure):
          ("NP1", _i32), ("y_path1", _i32 * 16), ("y_oo1", _i32 * 16), ("c1_gate", _i32 * 16)]
 
 
+def kernel_limits(lay: Layout) -> list:
+    """What of ``lay`` exceeds the ICTD kernels' tables (empty: the kernels run it): at most 32 components
+    and 16 harmonic components, 64 live paths and 128 kk rows, 8 path groups of at most 32 kk rows and 8 kk
+    tiles in all, in the layout and in its dual (the paths reversed, grouped by output key)."""
+    paths = lay.conv2_paths()
+    out = []
+    if lay.M > 32:
+        out.append(f"{lay.M} components per channel (at most 32)")
+    if lay.NY > 16:
+        out.append(f"{lay.NY} harmonic components (at most 16, lmax <= 3)")
+    if len(paths) > 64:
+        out.append(f"{len(paths)} live paths (at most 64)")
+    for name, key in (("", "o1"), ("dual ", "oo")):
+        size = "d3" if key == "o1" else "d1"
+        groups: dict = {}
+        for p in paths:
+            groups[p[key]] = groups.get(p[key], 0) + p[size]
+        rows = sum(groups.values())
+        tiles = sum((k + 15) // 16 for k in groups.values())
+        if rows > 128:
+            out.append(f"{name}kk rows {rows} (at most 128)")
+        if len(groups) > 8:
+            out.append(f"{len(groups)} {name}path groups (at most 8)")
+        if max(groups.values(), default=0) > 32:
+            out.append(f"a {name}path group of {max(groups.values())} kk rows (at most 32)")
+        if tiles > 8:
+            out.append(f"{tiles} {name}kk tiles (at most 8)")
+    return out
+
+
 def build_layout_struct(lay: Layout) -> FscIctdLayout:
     paths = lay.conv2_paths()
     s = FscIctdLayout()

@@ -74,12 +74,15 @@ def test_o3_presets_the_kernels_cannot_run_are_refused():
     m = PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="auto", external_tensor_rank=1,
                                             external_tensor_irrep="1o")
     assert m.keys == [E0, O1, E2]
-    with pytest.raises(NotImplementedError, match="at most 16"):
-        PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="full")          # 18 components
-    with pytest.raises(NotImplementedError, match="at most 16"):
-        PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="balanced")      # 17 components
+    assert PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="full").layout.M == 18
+    assert PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="balanced").layout.M == 17
     with pytest.raises(NotImplementedError, match="geometric"):
         PureCartesianICTDO3TransformerLayer(**kw, o3_irrep_preset="minimal")       # no 1o, 2e
+    kw3 = dict(**BASE, lmax=3)
+    with pytest.raises(NotImplementedError, match="kk rows 198"):
+        PureCartesianICTDO3TransformerLayer(**kw3, o3_irrep_preset="full")         # 28 components, 198 kk rows
+    with pytest.raises(NotImplementedError, match="kk tiles"):
+        PureCartesianICTDO3TransformerLayer(**kw3, o3_irrep_preset="balanced")
 
 
 def test_lmax_range_is_checked_at_construction():

@@ -1,7 +1,9 @@
-"""ICTD trunks at lmax 0 and 1 (the kernels take lmax 0 to 3; the reference takes any lmax).
+"""ICTD trunks at lmax 0 and 1 and the larger O3 irrep sets (the kernels take lmax 0 to 3 and up to 32
+components per channel; the reference takes any lmax).
 
 * the conv2..n op against the reference conv2 semantics of the oracle (fctp per path, scatter, / in-degree),
-  forward and the three input gradients, full layouts at lmax 0 and 1 and an O3 layout at lmax 1;
+  forward and the three input gradients: full layouts at lmax 0 and 1, O3 layouts at lmax 1 and the O3
+  presets "balanced" (17 components) and "full" (18) at lmax 2;
 * whole trunks (energies and forces; O3 with an external field and the dipole head) against the fp64 oracle
   (oracle/ictd_ref.py, the restatement pinned by the reference golden vectors at lmax 2 and 3, whose code
   is the same for every lmax) on the 32-atom golden system, with seeded parameters shared by name.
@@ -21,12 +23,18 @@ DEV = "cuda:0"
 TOL = 1e-5
 
 
-@pytest.mark.parametrize("lname,C", [("full_l0", 32), ("full_l1", 64), ("o3_l1", 32)])
+O3_BALANCED_L2 = [(0, 1), (1, 1), (1, -1), (2, 1), (2, -1)]
+O3_FULL_L2 = [(0, 1), (0, -1), (1, 1), (1, -1), (2, 1), (2, -1)]
+
+
+@pytest.mark.parametrize("lname,C", [("full_l0", 32), ("full_l1", 64), ("o3_l1", 32), ("o3_balanced_l2", 32),
+                                     ("o3_full_l2", 64), ("o3_full_l2", 128)])
 def test_ictd_conv_op_at_low_lmax(lname, C):
     from fsctep_amd import ictd_basis as B, ictd_ops
     from fsctep_amd.graph import prepare_graph
     lay = {"full_l0": B.layout_full(0), "full_l1": B.layout_full(1),
-           "o3_l1": B.layout_o3(1, [(0, 1), (1, 1), (1, -1)])}[lname]
+           "o3_l1": B.layout_o3(1, [(0, 1), (1, 1), (1, -1)]),
+           "o3_balanced_l2": B.layout_o3(2, O3_BALANCED_L2), "o3_full_l2": B.layout_o3(2, O3_FULL_L2)}[lname]
     lid = ictd_ops.register_layout(lay)
     torch.manual_seed(11)
     N = 30
@@ -66,15 +74,16 @@ KW = dict(max_embed_radius=5.0, main_max_radius=5.0, main_number_of_basis=8, hid
           ictd_tp_path_policy="full", invariant_channels=32)
 
 
-@pytest.mark.parametrize("lmax,o3", [(0, False), (1, False), (1, True)])
+@pytest.mark.parametrize("lmax,o3", [(0, False), (1, False), (1, "0e,1o"), (2, "full"), (2, "balanced")])
 def test_ictd_trunk_at_low_lmax_matches_oracle(lmax, o3):
     from fsctep_amd.ictd import (PureCartesianICTDO3TransformerLayer, PureCartesianICTDTransformerLayer,
                                  energy_forces)
     g = load_golden("ictd_open32_c32_l2")          # the geometry of the reference's 32-atom system
     seed = 17
     if o3:
+        irreps = {"o3_active_irreps": o3} if "," in o3 else {"o3_irrep_preset": o3}
         m = PureCartesianICTDO3TransformerLayer(
-            **KW, lmax=lmax, o3_active_irreps="0e,1o", external_tensor_rank=1, external_tensor_irrep="1o",
+            **KW, lmax=lmax, **irreps, external_tensor_rank=1, external_tensor_irrep="1o",
             physical_tensor_outputs={"dipole": {"irreps": ["1o"], "channels_out": 1, "reduce": "sum"}})
     else:
         m = PureCartesianICTDTransformerLayer(**KW, lmax=lmax)
@@ -82,8 +91,9 @@ def test_ictd_trunk_at_low_lmax_matches_oracle(lmax, o3):
         for name, p in m.named_parameters():
             p.copy_(torch.from_numpy(seeded_value(name, tuple(p.shape), seed)).to(p.dtype))
     m = m.eval().requires_grad_(False).to(DEV)
+    o3 = bool(o3)
     cfg = I.ICTDConfig(channels=32, lmax=lmax, num_interaction=2, function_type="gaussian", o3=o3,
-                       active=((0, 1), (1, -1)) if o3 else (), external_field=o3, dipole=o3)
+                       active=tuple(m.keys) if o3 else (), external_field=o3, dipole=o3)
     prm = {k: torch.tensor(seeded_value(k, s, seed), dtype=torch.float64) for k, s in I.param_shapes(cfg)}
     assert set(prm) == {k for k, _ in m.named_parameters()}
     n = g["pos"].shape[0]
