@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restri
   const int64_t cols = 65LL * C;
   const int64_t total = 6LL * cols * C;
   __shared__ float red[4];
-  __shared__ float tile[64][65];   // [a][kk], C <= 64
+  __shared__ float tile[128][65];   // [a][kk], C <= 128
   float mx = bk1f[total + 256 + threadIdx.x];
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -665,9 +665,9 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
 }
 
 // ---------------------------------------------------------------- K3: receiver sum
-// One wave per receiver; lanes cover channels, 64/C edges in flight per wave.  DIR (training double
-// backward): the derivative of the assembly along edge directions u (udir [E][3]),
-// m0' = 0, m1' = P1 u, m2' = P2 (u n^T + n u^T) + P4 u^T.
+// One wave per receiver; lanes cover channels (C/64 channels per lane above 64), 64/C edges in flight per
+// wave below.  DIR (training double backward): the derivative of the assembly along edge directions u
+// (udir [E][3]), m0' = 0, m1' = P1 u, m2' = P2 (u n^T + n u^T) + P4 u^T.
 template <int C, bool DIR = false>
 __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restrict__ P,
                                                            const float* __restrict__ nvec,
@@ -678,50 +678,61 @@ __global__ __launch_bounds__(256) void receiver_sum_kernel(const float* __restri
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= n_nodes) return;
-  constexpr int EPW = 64 / C;
-  const int c = lane % C, sub = lane / C;
-  float o[NCOMP];
+  constexpr int EPW = C < 64 ? 64 / C : 1;    // edges in flight per wave
+  constexpr int CPL = C > 64 ? C / 64 : 1;    // channels per lane: c, c + 64, ..
+  constexpr int CW = C < 64 ? C : 64;         // lanes per edge
+  const int c0 = lane % CW, sub = lane / CW;
+  float o[CPL][NCOMP];
 #pragma unroll
-  for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int i = 0; i < NCOMP; ++i) o[k][i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg + sub; e < end; e += EPW) {
     const float* pr = P + (int64_t)e * (NSLOT * C);
     const float n0 = nvec[3 * (int64_t)e], n1 = nvec[3 * (int64_t)e + 1], n2 = nvec[3 * (int64_t)e + 2];
     const float nn[3] = {n0, n1, n2};
-    auto ps = [&](int slot) { return pr[p_col<C>(pos_of_slot(slot), c)]; };
-    const float p0 = ps(0), p1 = ps(1), p2 = ps(2);
-    if constexpr (!DIR) {
-      o[0] += p0;
 #pragma unroll
-      for (int i = 0; i < 3; ++i) o[1 + i] += p1 * nn[i] + ps(3 + i);
+    for (int k = 0; k < CPL; ++k) {
+      const int c = c0 + 64 * k;
+      auto ps = [&](int slot) { return pr[p_col<C>(pos_of_slot(slot), c)]; };
+      const float p0 = ps(0), p1 = ps(1), p2 = ps(2);
+      if constexpr (!DIR) {
+        o[k][0] += p0;
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const float p4 = ps(6 + i);
-        const float p2ni = p2 * nn[i];
+        for (int i = 0; i < 3; ++i) o[k][1 + i] += p1 * nn[i] + ps(3 + i);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + ps(9 + 3 * i + j);
-      }
-    } else {
-      const float uu[3] = {udir[3 * (int64_t)e], udir[3 * (int64_t)e + 1], udir[3 * (int64_t)e + 2]};
+        for (int i = 0; i < 3; ++i) {
+          const float p4 = ps(6 + i);
+          const float p2ni = p2 * nn[i];
 #pragma unroll
-      for (int i = 0; i < 3; ++i) o[1 + i] += p1 * uu[i];
+          for (int j = 0; j < 3; ++j) o[k][4 + 3 * i + j] += p2ni * nn[j] + p4 * nn[j] + ps(9 + 3 * i + j);
+        }
+      } else {
+        const float uu[3] = {udir[3 * (int64_t)e], udir[3 * (int64_t)e + 1], udir[3 * (int64_t)e + 2]};
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const float p4 = ps(6 + i);
+        for (int i = 0; i < 3; ++i) o[k][1 + i] += p1 * uu[i];
 #pragma unroll
-        for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += p2 * (uu[i] * nn[j] + nn[i] * uu[j]) + p4 * uu[j];
+        for (int i = 0; i < 3; ++i) {
+          const float p4 = ps(6 + i);
+#pragma unroll
+          for (int j = 0; j < 3; ++j) o[k][4 + 3 * i + j] += p2 * (uu[i] * nn[j] + nn[i] * uu[j]) + p4 * uu[j];
+        }
       }
     }
   }
   if (EPW > 1) {
 #pragma unroll
     for (int i = 0; i < NCOMP; ++i)
-      for (int off = C; off < 64; off <<= 1) o[i] += __shfl_xor(o[i], off, 64);
+      for (int off = C; off < 64; off <<= 1) o[0][i] += __shfl_xor(o[0][i], off, 64);
   }
   if (sub == 0) {
-    float* orow = out + n * NCOMP * C + c;
 #pragma unroll
-    for (int i = 0; i < NCOMP; ++i) orow[i * C] = o[i] * scale;
+    for (int k = 0; k < CPL; ++k) {
+      float* orow = out + n * NCOMP * C + c0 + 64 * k;
+#pragma unroll
+      for (int i = 0; i < NCOMP; ++i) orow[i * C] = o[k][i] * scale;
+    }
   }
 }
 
@@ -1494,43 +1505,54 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   }
 }
 
-// out[n] = (1/max(indeg,1)) sum_{e->n} [Q0, Q1 n, Q2 n n]; one wave per receiver, lane = channel.
+// out[n] = (1/max(indeg,1)) sum_{e->n} [Q0, Q1 n, Q2 n n]; one wave per receiver, lane = channel (and
+// channel + 64 at C 128).
 template <int C>
 __global__ __launch_bounds__(256) void conv1_receiver_kernel(const float* __restrict__ Q,
                                                              const float* __restrict__ nvec,
                                                              const int32_t* __restrict__ dst_ptr,
                                                              float* __restrict__ out, int64_t n_nodes) {
+  constexpr int CPL = C > 64 ? C / 64 : 1;
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= n_nodes) return;
-  const int c = lane & (C - 1);
-  float o[NCOMP];
+  const int c0 = C < 64 ? (lane & (C - 1)) : lane;
+  float o[CPL][NCOMP];
 #pragma unroll
-  for (int i = 0; i < NCOMP; ++i) o[i] = 0.f;
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int i = 0; i < NCOMP; ++i) o[k][i] = 0.f;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   for (int e = beg; e < end; ++e) {
-    const float* qr = Q + (int64_t)e * 3 * C + c;
-    const float q0 = qr[0], q1 = qr[C], q2 = qr[2 * C];
     const float nn[3] = {nvec[3 * (int64_t)e], nvec[3 * (int64_t)e + 1], nvec[3 * (int64_t)e + 2]};
-    o[0] += q0;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      o[1 + i] += q1 * nn[i];
-      const float q2n = q2 * nn[i];
+    for (int k = 0; k < CPL; ++k) {
+      const float* qr = Q + (int64_t)e * 3 * C + c0 + 64 * k;
+      const float q0 = qr[0], q1 = qr[C], q2 = qr[2 * C];
+      o[k][0] += q0;
 #pragma unroll
-      for (int j = 0; j < 3; ++j) o[4 + 3 * i + j] += q2n * nn[j];
+      for (int i = 0; i < 3; ++i) {
+        o[k][1 + i] += q1 * nn[i];
+        const float q2n = q2 * nn[i];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) o[k][4 + 3 * i + j] += q2n * nn[j];
+      }
     }
   }
   if (lane < C) {
     const float scale = 1.f / (float)max(end - beg, 1);
-    float* orow = out + n * NCOMP * C + c;
 #pragma unroll
-    for (int i = 0; i < NCOMP; ++i) orow[i * C] = o[i] * scale;
+    for (int k = 0; k < CPL; ++k) {
+      float* orow = out + n * NCOMP * C + c0 + 64 * k;
+#pragma unroll
+      for (int i = 0; i < NCOMP; ++i) orow[i * C] = o[k][i] * scale;
+    }
   }
 }
 
 // Receiver side of the backward: dQ[e] = (g0, g1.n, n.g2.n) with g = G[n]/max(indeg,1), and
-// dn_e[k] = sum_c g1[k] Q1 + Q2 ((g2 n)[k] + (g2^T n)[k]).  One wave per receiver, lane = channel.
+// dn_e[k] = sum_c g1[k] Q1 + Q2 ((g2 n)[k] + (g2^T n)[k]).  One wave per receiver, lane = channel (and
+// channel + 64 at C 128).
 template <int C>
 __global__ __launch_bounds__(256) void conv1_receiver_grad_kernel(const float* __restrict__ G,
                                                                   const float* __restrict__ nvec,
@@ -1538,38 +1560,45 @@ __global__ __launch_bounds__(256) void conv1_receiver_grad_kernel(const float* _
                                                                   const int32_t* __restrict__ dst_ptr,
                                                                   float* __restrict__ dQ,
                                                                   float* __restrict__ dn, int64_t n_nodes) {
+  constexpr int CPL = C > 64 ? C / 64 : 1;
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= n_nodes) return;   // whole wave
-  const int c = lane & (C - 1);
+  const int c0 = C < 64 ? (lane & (C - 1)) : lane;
   const bool act = lane < C;
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const float scale = 1.f / (float)max(end - beg, 1);
-  float g[NCOMP];
+  float g[CPL][NCOMP];
 #pragma unroll
-  for (int i = 0; i < NCOMP; ++i) g[i] = act ? G[(n * NCOMP + i) * C + c] * scale : 0.f;
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int i = 0; i < NCOMP; ++i) g[k][i] = act ? G[(n * NCOMP + i) * C + c0 + 64 * k] * scale : 0.f;
   for (int e = beg; e < end; ++e) {
     const float nn[3] = {nvec[3 * (int64_t)e], nvec[3 * (int64_t)e + 1], nvec[3 * (int64_t)e + 2]};
-    const float* qr = Q + (int64_t)e * 3 * C + c;
-    const float q1 = qr[C], q2 = qr[2 * C];
-    float d1 = 0.f, d2 = 0.f, t[3];
+    float t[3] = {0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      float row = 0.f, colv = 0.f;
+    for (int k = 0; k < CPL; ++k) {
+      const float* qr = Q + (int64_t)e * 3 * C + c0 + 64 * k;
+      const float q1 = qr[C], q2 = qr[2 * C];
+      float d1 = 0.f, d2 = 0.f;
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        row += g[4 + 3 * k + j] * nn[j];
-        colv += g[4 + 3 * j + k] * nn[j];
+      for (int kk = 0; kk < 3; ++kk) {
+        float row = 0.f, colv = 0.f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          row += g[k][4 + 3 * kk + j] * nn[j];
+          colv += g[k][4 + 3 * j + kk] * nn[j];
+        }
+        d1 += g[k][1 + kk] * nn[kk];
+        d2 += row * nn[kk];
+        t[kk] += act ? g[k][1 + kk] * q1 + q2 * (row + colv) : 0.f;
       }
-      d1 += g[1 + k] * nn[k];
-      d2 += row * nn[k];
-      t[k] = act ? g[1 + k] * q1 + q2 * (row + colv) : 0.f;
-    }
-    if (act) {
-      float* dq = dQ + (int64_t)e * 3 * C + c;
-      dq[0] = g[0];
-      dq[C] = d1;
-      dq[2 * C] = d2;
+      if (act) {
+        float* dq = dQ + (int64_t)e * 3 * C + c0 + 64 * k;
+        dq[0] = g[k][0];
+        dq[C] = d1;
+        dq[2 * C] = d2;
+      }
     }
     const float t0 = wave_sum(t[0]), t1 = wave_sum(t[1]), t2 = wave_sum(t[2]);
     if (lane == 0) {
@@ -1732,12 +1761,14 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
 using namespace fsc;
 using namespace fsc::sparse;
 
+static bool sparse_channels_ok(int32_t c) { return c == 32 || c == 64 || c == 128; }
+
 extern "C" {
 
 int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels,
                               int64_t* s_floats, int64_t* p_floats) {
   FSC_CHECK_ARG(n_nodes >= 0 && n_edges >= 0, "fsc_sparse_conv_workspace: negative size");
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_workspace: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv_workspace: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(s_floats && p_floats, "fsc_sparse_conv_workspace: null output");
   // the tail (ks x 18 x N x C + N, ks = neg_ksplit(N)) holds the partial input gradients and per-node
   // scales of the backward
@@ -1748,7 +1779,7 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
 
 int fsc_sparse_conv_prepare_weights(const float* w_last, const float* b_last, int32_t channels,
                                     float* bk1, float* bk6, hipStream_t stream) {
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_prepare_weights: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv_prepare_weights: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(w_last && b_last && bk1 && bk6, "fsc_sparse_conv_prepare_weights: null pointer");
   const int64_t C = channels;
   weight_absmax_kernel<<<SWMAX_BLOCKS, 256, 0, stream>>>(w_last, 6 * C * C * KH, b_last, 6 * C * C,
@@ -1768,13 +1799,16 @@ int fsc_sparse_conv_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_forward: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && src_ptr && x && bk1 && s_ws && out, "fsc_sparse_conv_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && h && n && p_ws), "fsc_sparse_conv_forward: null edge pointer");
+  if (channels == 128)
+    return (precision ? conv_forward_impl<128, true> : conv_forward_impl<128, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm, s_ws, p_ws, out, node_order, stream);
   if (channels == 64)
     return (precision ? conv_forward_impl<64, true> : conv_forward_impl<64, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm, s_ws, p_ws, out, node_order, stream);
   if (channels == 32)
     return (precision ? conv_forward_impl<32, true> : conv_forward_impl<32, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, x, h, n, bk1, inv_norm, s_ws, p_ws, out, node_order, stream);
-  set_error("fsc_sparse_conv_forward: channels must be 32 or 64");
+  set_error("fsc_sparse_conv_forward: channels must be 32, 64 or 128");
   return 1;
 }
 
@@ -1785,10 +1819,12 @@ int fsc_sparse_conv_direction(int64_t n_nodes, int64_t n_edges, int32_t channels
   FSC_CHECK_ARG(n_nodes < (1LL << 31) && n_edges < (1LL << 31), "fsc_sparse_conv_direction: size exceeds int32 indexing");
   FSC_CHECK_ARG(dst_ptr && out, "fsc_sparse_conv_direction: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (p_ws && n && u), "fsc_sparse_conv_direction: null edge pointer");
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv_direction: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv_direction: channels must be 32, 64 or 128");
   if (n_nodes == 0) return 0;
   const unsigned grid = (unsigned)((n_nodes + 3) / 4);
-  if (channels == 64)
+  if (channels == 128)
+    receiver_sum_kernel<128, true><<<grid, 256, 0, stream>>>(p_ws, n, u, dst_ptr, inv_norm, out, n_nodes);
+  else if (channels == 64)
     receiver_sum_kernel<64, true><<<grid, 256, 0, stream>>>(p_ws, n, u, dst_ptr, inv_norm, out, n_nodes);
   else
     receiver_sum_kernel<32, true><<<grid, 256, 0, stream>>>(p_ws, n, u, dst_ptr, inv_norm, out, n_nodes);
@@ -1810,6 +1846,10 @@ int fsc_sparse_conv_direction_backward(int64_t n_nodes, int64_t n_edges, int32_t
                 "fsc_sparse_conv_direction_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && edge_dst && h && n && u && p_ws && grad_h && grad_n),
                 "fsc_sparse_conv_direction_backward: null edge pointer");
+  if (channels == 128)
+    return (precision ? conv_backward_impl<128, true, true> : conv_backward_impl<128, false, true>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream, u);
   if (channels == 64)
     return (precision ? conv_backward_impl<64, true, true> : conv_backward_impl<64, false, true>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
@@ -1818,7 +1858,7 @@ int fsc_sparse_conv_direction_backward(int64_t n_nodes, int64_t n_edges, int32_t
     return (precision ? conv_backward_impl<32, true, true> : conv_backward_impl<32, false, true>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
         grad_x, grad_h, grad_n, node_order, stream, u);
-  set_error("fsc_sparse_conv_direction_backward: channels must be 32 or 64");
+  set_error("fsc_sparse_conv_direction_backward: channels must be 32, 64 or 128");
   return 1;
 }
 
@@ -1835,6 +1875,10 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                 "fsc_sparse_conv_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (src_perm && edge_dst && h && n && p_ws && grad_h && grad_n),
                 "fsc_sparse_conv_backward: null edge pointer");
+  if (channels == 128)
+    return (precision ? conv_backward_impl<128, true> : conv_backward_impl<128, false>)(
+        n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
+        grad_x, grad_h, grad_n, node_order, stream, nullptr);
   if (channels == 64)
     return (precision ? conv_backward_impl<64, true> : conv_backward_impl<64, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
@@ -1843,14 +1887,14 @@ int fsc_sparse_conv_backward(int64_t n_nodes, int64_t n_edges, int32_t channels,
     return (precision ? conv_backward_impl<32, true> : conv_backward_impl<32, false>)(
         n_nodes, n_edges, dst_ptr, src_ptr, src_perm, edge_dst, grad_out, h, n, bk6, s_ws, p_ws, inv_norm, ds_ws,
         grad_x, grad_h, grad_n, node_order, stream, nullptr);
-  set_error("fsc_sparse_conv_backward: channels must be 32 or 64");
+  set_error("fsc_sparse_conv_backward: channels must be 32, 64 or 128");
   return 1;
 }
 
 int fsc_sparse_conv1_pair_table(const float* w_last, const float* b_last, const float* atom_table,
                                 int32_t n_species, int32_t channels, float* mf, float* mb,
                                 hipStream_t stream) {
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_pair_table: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv1_pair_table: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(n_species >= 1 && n_species <= 128, "fsc_sparse_conv1_pair_table: n_species out of range");
   FSC_CHECK_ARG(w_last && b_last && atom_table && mf && mb, "fsc_sparse_conv1_pair_table: null pointer");
   const int64_t work = (int64_t)n_species * 3 * 65 * channels;
@@ -1866,13 +1910,16 @@ int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
                 "fsc_sparse_conv1_forward: bad size");
   FSC_CHECK_ARG(n_tiles >= 0 && n_tiles < (1LL << 27) && n_tiles * 16 >= n_edges,
                 "fsc_sparse_conv1_forward: pair tiles do not cover the edges");
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_forward: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv1_forward: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(dst_ptr && mf && mb && out, "fsc_sparse_conv1_forward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_forward", stream);
   const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
-  if (channels == 64) {
+  if (channels == 128) {
+    if (n_tiles) conv1_pair_gemm_kernel<128><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
+    conv1_receiver_kernel<128><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
+  } else if (channels == 64) {
     if (n_tiles) conv1_pair_gemm_kernel<64><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
     conv1_receiver_kernel<64><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
   } else {
@@ -1890,14 +1937,17 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                 "fsc_sparse_conv1_backward: bad size");
   FSC_CHECK_ARG(n_tiles >= 0 && n_tiles < (1LL << 27) && n_tiles * 16 >= n_edges,
                 "fsc_sparse_conv1_backward: pair tiles do not cover the edges");
-  FSC_CHECK_ARG(channels == 32 || channels == 64, "fsc_sparse_conv1_backward: channels must be 32 or 64");
+  FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv1_backward: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(dst_ptr && grad_out && mf, "fsc_sparse_conv1_backward: null pointer");
   FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && n && q_ws && dq_ws && grad_h && grad_n),
                 "fsc_sparse_conv1_backward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_backward", stream);
   const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
-  if (channels == 64) {
+  if (channels == 128) {
+    conv1_receiver_grad_kernel<128><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
+    if (n_tiles) conv1_pair_gemm_grad_kernel<128><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
+  } else if (channels == 64) {
     conv1_receiver_grad_kernel<64><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
     if (n_tiles) conv1_pair_gemm_grad_kernel<64><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
   } else {

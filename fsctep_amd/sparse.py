@@ -172,8 +172,8 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         ops.check_basis(function_type_main)
         if not 1 <= main_number_of_basis <= 16:
             raise NotImplementedError("HIP sparse path: main_number_of_basis 1..16")
-        if hidden_dim_conv not in (32, 64):
-            raise NotImplementedError("HIP sparse path: hidden_dim_conv 32 or 64")
+        if hidden_dim_conv not in (32, 64, 128):
+            raise NotImplementedError("HIP sparse path: hidden_dim_conv 32, 64 or 128")
         if num_interaction < 2:
             raise ValueError(f"num_interaction must be >= 2, got {num_interaction}")
         embed_size = [128, 128, 128] if embed_size is None else list(embed_size)

@@ -113,7 +113,7 @@ int fsc_neighbor_fill(int64_t n_nodes, int64_t n_edges, const double* pos, const
  * of PureCartesianSparseE3Conv2.forward (models/pure_cartesian_sparse_layers.py:382-421),
  * i.e. the last radial-MLP Linear (fc.4), PureCartesianTensorProductO3Sparse.forward
  * (models/pure_cartesian.py:790-863) and utils/scatter.py:63-116.
- * Supported: lmax 2, max_rank_other 1, k_policy "k0", channels 32 or 64.
+ * Supported: lmax 2, max_rank_other 1, k_policy "k0", channels 32, 64 or 128.
  */
 
 /* Workspace sizes, in floats: s (node expansion, also the size of ds) and p (edge messages). */

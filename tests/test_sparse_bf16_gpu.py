@@ -16,7 +16,7 @@ DEV = "cuda:0"
 TOL_BF16 = 2e-2
 
 
-@pytest.mark.parametrize("C", [64, 32])
+@pytest.mark.parametrize("C", [64, 32, 128])
 def test_bf16_conv2_op_against_oracle(C):
     from fsctep_amd import ops
     from fsctep_amd.graph import prepare_graph

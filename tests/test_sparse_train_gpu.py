@@ -56,7 +56,7 @@ def _leaves(ts, dev=None, dtype=None):
     return [t.detach().to(device=dev or t.device, dtype=dtype or t.dtype).requires_grad_(True) for t in ts]
 
 
-@pytest.mark.parametrize("C", [64, 32])
+@pytest.mark.parametrize("C", [64, 32, 128])
 def test_weight_gradient_matches_oracle(C):
     src, dst, N, x, h, n, L, b, g = _case(C, 3)
     ref_leaves = _leaves((x, h, n, L, b))
@@ -73,7 +73,7 @@ def test_weight_gradient_matches_oracle(C):
         assert rel_inf(a, b_) < TOL1, name
 
 
-@pytest.mark.parametrize("C", [64, 32])
+@pytest.mark.parametrize("C", [64, 32, 128])
 def test_double_backward_matches_oracle(C):
     """s = <Vx,dx> + <Vh,dh> + <Vn,dn> + <VL,dL> + <Vb,db> of the conv's backward at G (create_graph), then
     the gradient of s with respect to x, h, n, L, b and G."""
