@@ -9,6 +9,8 @@
 // and the force backward: dr from dh (activations recomputed), dvec from (dn, dr), and
 // dpos[m] = sum_{e: dst(e)=m} dvec_e - sum_{e: src(e)=m} dvec_e as two deterministic segmented
 // sums over the receiver CSR and the source grouping (no atomics).
+#include <type_traits>
+
 #include "common.h"
 #include "fsctep.h"
 
@@ -17,6 +19,7 @@ namespace radial {
 
 constexpr int HID = 64;     // hidden width of the radial MLP (fixed by the reference's fc)
 constexpr int NBMAX = 16;   // radial basis functions supported
+constexpr int RADW_RED = 16;   // block-reduction slots (at most 16 waves per block)
 
 // sin x and cos x for 0 <= x < 2^7: Cody-Waite reduction by pi/2 in two parts (the fma keeps
 // x - n*P1 to one rounding, and n*(pi/2 - P1 - P2) is below 2^-30 here), then the Taylor series on
@@ -99,23 +102,62 @@ __device__ __forceinline__ float sigm(float x) { return __fdividef(1.f, 1.f + __
 
 // One wave per 16-edge tile; lane (r, q) works for edge e0 + r.  The hidden units are laid
 // out as the MFMA output: lane (r, q) holds unit j = 16*jt + 4*q + i in register (jt, i), so
-// one layer's output is directly the next product's B operand (K index q <-> 16*jt + 4*q + i).
-// Weights are staged in LDS with rows padded to a multiple of four so that the four K values a
-// lane needs come in one 16-byte read: W0 [64][NBMAX] and W0^T [NBMAX][68], W2 [64][68] and
-// W2^T [64][68], W4 [64][68] (an optional last Linear with up to 64 outputs, zero rows beyond).
+// one layer's output is directly the next product's B operand.
+// The first layer (K = nb <= 16) runs on the fp32 MFMA from W0 [64][NBMAX] (and W0^T [NBMAX][68] in the
+// backward), rows padded so the four K values a lane needs come in one 16-byte read.  The 64-wide layers
+// (W2, the optional last Linear W4 with up to 64 outputs, and their transposes in the backward) run on
+// v_mfma_f32_16x16x32_f16 with fp32-accurate split-fp16 products (mfma_x3, common.h): each layer's weights
+// are staged in LDS as two fp16 planes of W sw (one power of two per layer from max |W|), in the K order of
+// the activations a lane holds, so the activations need no exchange: K step s takes units
+// 32 s + 4 q + j (j < 4) and 32 s + 16 + 4 q + j - 4 (j >= 4), i.e. registers jt = 2s and 2s + 1.  The
+// activations of an edge (its 64 units sit in the four lanes (r, 0..3)) get one power of two per edge.
 constexpr int WS = HID + 4;
+constexpr int HS = HID + 8;   // fp16 row stride of a layer's planes (144 bytes)
+struct LayerH16 {
+  _Float16 p[2][HID][HS];     // [plane][output row][K slot]
+};
+struct NoLayer {};
 template <bool BWD>
 struct Smem {
   float w0[HID][NBMAX];
   float w0t[BWD ? NBMAX : 1][WS];
-  float w2[HID][WS];
-  float w2t[BWD ? HID : 1][WS];
-  float w4[BWD ? 1 : HID][WS];
-  float w4t[BWD ? HID : 1][WS];
+  LayerH16 w2;                                      // W2 (forward product; recomputed in the backward)
+  std::conditional_t<BWD, LayerH16, NoLayer> w2t;   // W2^T (backward)
+  LayerH16 w4;                                      // W4 in the forward, W4^T in the backward
   float b0[HID];
   float b2[HID];
   float b4[HID];
+  float winv[3];                // 1/sw of w2, w2t, w4
+  float red[RADW_RED];
 };
+
+// K slot of hidden unit u in a layer's planes
+__host__ __device__ constexpr int kslot(int u) {
+  return 32 * (u >> 5) + 8 * ((u >> 2) & 3) + 4 * ((u >> 4) & 1) + (u & 3);
+}
+
+// Planes of M (64 rows o, 64 columns u): p[h/l][o][kslot(u)] = split of M[o][u] sw, sw from the block's max
+// |M|; returns 1/sw (all threads).  get(o, u) reads M.
+template <typename Get>
+__device__ float stage_h16(LayerH16& L, float* red, Get get) {
+  float mx = 0.f;
+  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) mx = fmaxf(mx, fabsf(get(i / HID, i % HID)));
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  __syncthreads();   // red is free (a previous call's readers are done)
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, red[w]);
+  const float sw = pow2_scale(mx);
+  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) {
+    const int o = i / HID, u = i % HID;
+    const float v = get(o, u) * sw;
+    const _Float16 h = (_Float16)v;
+    L.p[0][o][kslot(u)] = h;
+    L.p[1][o][kslot(u)] = (_Float16)(v - (float)h);
+  }
+  return 1.f / sw;   // exact: a power of two
+}
 
 template <bool BWD>
 __device__ void stage_weights(Smem<BWD>& sm, const float* __restrict__ W0, const float* __restrict__ b0,
@@ -127,46 +169,63 @@ __device__ void stage_weights(Smem<BWD>& sm, const float* __restrict__ W0, const
     sm.w0[j][k] = v;
     if (BWD) sm.w0t[k][j] = v;
   }
-  for (int i = threadIdx.x; i < HID * HID; i += blockDim.x) {
-    const int a = i / HID, b = i % HID;
-    sm.w2[a][b] = W2[i];
-    if (BWD) sm.w2t[b][a] = W2[i];
-    if (W4) {
-      const float v = (a < nout) ? W4[a * HID + b] : 0.f;
-      if (BWD)
-        sm.w4t[b][a] = v;
-      else
-        sm.w4[a][b] = v;
-    }
-  }
   for (int i = threadIdx.x; i < HID; i += blockDim.x) {
     sm.b0[i] = b0[i];
     sm.b2[i] = b2[i];
     sm.b4[i] = (W4 && i < nout && b4) ? b4[i] : 0.f;
   }
+  const float w2i = stage_h16(sm.w2, sm.red, [&](int o, int u) { return W2[o * HID + u]; });
+  float w2ti = 1.f, w4i = 1.f;
+  if constexpr (BWD) w2ti = stage_h16(sm.w2t, sm.red, [&](int o, int u) { return W2[u * HID + o]; });
+  if (W4) {
+    if constexpr (BWD)   // W4^T [64 hidden][nout], zero columns beyond nout
+      w4i = stage_h16(sm.w4, sm.red, [&](int o, int u) { return u < nout ? W4[u * HID + o] : 0.f; });
+    else
+      w4i = stage_h16(sm.w4, sm.red, [&](int o, int u) { return o < nout ? W4[o * HID + u] : 0.f; });
+  }
+  if (threadIdx.x == 0) {
+    sm.winv[0] = w2i;
+    sm.winv[1] = w2ti;
+    sm.winv[2] = w4i;
+  }
 }
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-// out = W x + b for a 64-wide layer: x in the MFMA layout (x[jt][i] = unit 16 jt + 4 q + i),
-// W [64][WS] row-major; A operand row r of output tile ot reads W[16 ot + r][16 jt + 4q .. +3].
-__device__ __forceinline__ void dense64(const float (*W)[WS], const float* b, const f4 (&x)[4], int r, int q,
-                                        f4 (&out)[4]) {
+// out = W x + b for a 64-wide layer on split-fp16 MFMA: x in the MFMA layout (x[jt][i] = unit 16 jt + 4 q + i
+// of the lane's edge r); the edge's activations scaled by a power of two from their max |x| over the four
+// lanes of the edge and split once; A operand row r of output tile ot reads K slots 8q .. 8q + 7 of
+// W row 16 ot + r from both planes; both scales undone on the fp32 result.
+__device__ __forceinline__ void dense64(const LayerH16& W, float winv, const float* b, const f4 (&x)[4], int r,
+                                        int q, f4 (&out)[4]) {
+  float mx = 0.f;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(x[jt][i]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float sx = pow2_scale(mx);
+  h8 xh[2], xl[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const float v[8] = {x[2 * st][0], x[2 * st][1], x[2 * st][2], x[2 * st][3],
+                        x[2 * st + 1][0], x[2 * st + 1][1], x[2 * st + 1][2], x[2 * st + 1][3]};
+    split2h(v, sx, xh[st], xl[st]);
+  }
+  const float f = winv / sx;   // exact: powers of two
 #pragma unroll
   for (int ot = 0; ot < 4; ++ot) {
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      const f4 a = lds4(&W[16 * ot + r][16 * jt + 4 * q]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc = mfma16x16x4(a[i], x[jt][i], acc);
+    for (int st = 0; st < 2; ++st) {
+      const h8 wh = *reinterpret_cast<const h8*>(&W.p[0][16 * ot + r][32 * st + 8 * q]);
+      const h8 wl = *reinterpret_cast<const h8*>(&W.p[1][16 * ot + r][32 * st + 8 * q]);
+      acc = mfma_x3(wh, wl, xh[st], xl[st], acc);
     }
-    if (b) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += b[16 * ot + 4 * q + i];
-    }
+    for (int i = 0; i < 4; ++i) acc[i] = acc[i] * f + (b ? b[16 * ot + 4 * q + i] : 0.f);
     out[ot] = acc;
-    // keep each output tile's 16 weight reads with its products (hoisting them all costs 64 VGPRs)
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -191,7 +250,7 @@ __device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&e
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) a0[jt][i] = u0[jt][i] * sigm(u0[jt][i]);
-  dense64(sm.w2, sm.b2, a0, r, q, u2);
+  dense64(sm.w2, sm.winv[0], sm.b2, a0, r, q, u2);
 }
 
 // The basis values a lane feeds to the first product: emb[4*ks + q] for ks < nks (lane group q).
@@ -245,7 +304,7 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_forward_kernel(c
       for (int i = 0; i < 4; ++i) a2[ot][i] = u2[ot][i] * sigm(u2[ot][i]);
     if (W4) {
       f4 o[4];
-      dense64(sm.w4, sm.b4, a2, r, q, o);
+      dense64(sm.w4, sm.winv[2], sm.b4, a2, r, q, o);
       if (e < n_edges) {
 #pragma unroll
         for (int ot = 0; ot < 4; ++ot)
@@ -295,7 +354,7 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(
           const int j = 16 * ot + 4 * q + i;
           d[ot][i] = (ok && j < nout) ? dout[e * nout + j] : 0.f;
         }
-      dense64(sm.w4t, nullptr, d, r, q, dh);
+      dense64(sm.w4, sm.winv[2], nullptr, d, r, q, dh);
     } else {
 #pragma unroll
       for (int ot = 0; ot < 4; ++ot) dh[ot] = ok ? ld4(dout + e * HID + 16 * ot + 4 * q) : f4{0.f, 0.f, 0.f, 0.f};
@@ -309,7 +368,7 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(
         g2[ot][i] = dh[ot][i] * s * (1.f + u2[ot][i] * (1.f - s));
       }
     f4 da0[4], g0[4];
-    dense64(sm.w2t, nullptr, g2, r, q, da0);
+    dense64(sm.w2t, sm.winv[1], nullptr, g2, r, q, da0);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
