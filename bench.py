@@ -51,7 +51,7 @@ PRODUCT_PEAK_TFLOPS = {"fp32": FP32_MFMA_PEAK_TFLOPS, "split-fp16": FP16_MFMA_PE
                        "split-bf16": FP16_MFMA_PEAK_TFLOPS / 6, "bf16": FP16_MFMA_PEAK_TFLOPS}
 KERNEL_PRODUCTS = {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
                    "edge_message_grad": "split-fp16", "receiver_sum": "fp32",
-                   "ictd_project": "fp32", "ictd_project_grad": "split-fp16", "ictd_dual_project": "fp32",
+                   "ictd_project": "split-fp16", "ictd_project_grad": "split-fp16", "ictd_dual_project": "split-fp16",
                    "ictd_mix": "split-fp16", "ictd_mix_grad": "split-fp16", "ictd_dual_mix": "split-fp16"}
 BF16_VARIANT = {"node_expand", "node_expand_grad", "edge_message"}
 
@@ -65,7 +65,7 @@ WORKLOADS = {
     "sparse": dict(atoms=10000, species=4, seed=22, channels=64, layers=3, lmax=2, kernel="edge_message_grad",
                    cpu_atoms=300,
                    table=["node_expand", "edge_message", "receiver_sum", "edge_message_grad", "node_expand_grad"]),
-    "ictd": dict(atoms=10000, species=8, seed=33, channels=128, layers=3, lmax=3, kernel="ictd_dual_project",
+    "ictd": dict(atoms=10000, species=8, seed=33, channels=128, layers=3, lmax=3, kernel="ictd_project_grad",
                  cpu_atoms=200,
                  table=["ictd_project", "ictd_mix", "ictd_mix_grad", "ictd_project_grad", "ictd_dual_project",
                         "ictd_dual_mix"]),
@@ -81,14 +81,16 @@ WORKLOADS = {
 # operand, six of the nine part products on bf16 MFMA (the dropped ones are below 2^-23 |ab|).
 PRODUCTS = {
     "sparse": {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
-               "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "fp32 MFMA", "radial_mlp": "fp32 MFMA",
+               "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "fp32 MFMA",
+               "radial_mlp": "fp32 MFMA (first layer), split-fp16 (64-wide layers)",
                "receiver_sum, edge geometry, readout assembly": "fp32 VALU",
                "gram_forward, gram_backward": "split-fp16", "MainNet, atom MLP": "torch fp32"},
-    "ictd": {"ictd_project, ictd_dual_project": "fp32 MFMA",
+    "ictd": {"ictd_project, ictd_dual_project": "split-fp16 (main product), fp32 MFMA (coupling rows)",
              "ictd_project_grad": "split-fp16 (H = g x^T), fp32 MFMA (coupling rows, dY)",
              "ictd_mix, ictd_mix_grad": "split-fp16",
              "ictd_conv1, source_sum, edge geometry, harmonics, readout assembly": "fp32 VALU",
-             "radial_mlp (gates)": "fp32 MFMA", "gram_forward, gram_backward": "split-fp16",
+             "radial_mlp (gates)": "fp32 MFMA (first layer), split-fp16 (64-wide layers)",
+             "gram_forward, gram_backward": "split-fp16",
              "MainNet, atom MLP": "torch fp32"},
 }
 PRODUCTS["ictd-o3"] = PRODUCTS["ictd"]

@@ -30,6 +30,7 @@ SIGNATURES = {
     "fsc_sparse_conv1_pair_table": [_p, _p, _p, _i32, _i32, _p, _p, _p],
     "fsc_sparse_conv1_forward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_sparse_conv1_backward": [_i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "fsc_ictd_forward_workspace": [_p, _i64, _i32, _pi64],
     "fsc_ictd_conv_forward": [_p, _i64, _i64, _i32] + [_p] * 11,
     "fsc_ictd_prepare_weights": [_p, _i32, _i32, _p, _p],
     "fsc_ictd_project": [_p, _i64, _i64, _i32] + [_p] * 9,

@@ -106,11 +106,10 @@ __device__ __forceinline__ void assign_fwd_tasks(const FscIctdLayout& L, int* __
 // table in LDS and no barrier inside the edge loop: each wave walks the chunks on its own.  Cf is built
 // once per block in LDS (one float4 per lane per (tile, m1) slot).
 // A wave takes at most two of the KTT <= 8 kk tiles, each over all C channels (64-channel spans at
-// 4 waves/SIMD measured slower at C 128: the coupling product is then formed once per span): column
-// tile j holds channel 64(j/4) + 4r + j%4 (V = C/16 >= 4; 2r + j for V = 2), so each lane gathers its V
-// channels of x as quads whose 16-lane rows are contiguous 256-byte runs, and stores Z the same way.  3 waves/SIMD at C 128, 4 below.
+// 4 waves/SIMD measured slower at C 128: the coupling product is then formed once per span).  The main
+// product runs in split-fp16 (project_fwd_h16_kernel below).
 struct FwdSmem {
-  int cgs, kd, gidx, slot0, wtask, cf, total;
+  int cgs, kd, gidx, slot0, wtask, cb, cf, total;
 };
 
 __host__ __device__ inline int n_slots(const FscIctdLayout& L) {
@@ -127,6 +126,7 @@ __host__ __device__ inline FwdSmem fwd_smem(const FscIctdLayout& L, int ncg) {
   s.gidx = o;  o += 16 * L.KTT;            // gate column of each kk row of each tile
   s.slot0 = o; o += up4(L.KTT + 1);        // first Cf slot of each tile
   s.wtask = o; o += 32;
+  s.cb = o;    o += 16 * L.KTT;            // bound of each kk row's coupling coefficients (split-fp16 scale)
   s.cf = o;    o += n_slots(L) * 256;
   s.total = o;
   return s;
@@ -195,25 +195,70 @@ __device__ __forceinline__ void stage_fwd_tables(const FscIctdLayout& L, const f
   }
 }
 
+// ---------------------------------------------------------------- forward projection, split-fp16 products
+// Over the blocks, tiles, chunks and coupling rows described above, the main product runs on
+// v_mfma_f32_16x16x16_f16 with three products per K step (fp32-accurate to 22 significant bits): the 16-deep
+// K step is one chunk of 16 edges for one component m1, lane (r, q) supplying edges 4q .. 4q + 3, which are
+// the coupling values it holds and the four rows it gathers, so one fp16 MFMA does the work of four fp32 ones.
+//  * The gathered rows come pre-split (split_rows_il_kernel: fp16 parts of x[n] nu_n and 1/nu_n, the two
+//    parts of a lane's V channels side by side, so a row is one 4V-byte load per lane); B is the four rows'
+//    halves of one channel, packed with v_perm_b32, and 1/nu_src goes into the A operand (a power of two:
+//    exact).
+//  * A, the gated coupling values times 1/nu_src, carries a power of two s_r per kk row r so that |A s_r| <
+//    2^14 over all of the node's edges: each chunk bounds its row by max_e |gate_e / nu_src(e)| max_y |Y_e[y]|
+//    times cb[r] = max_m1 sum_y |Cf[m1][y][r]|, and when that bound lowers s_r the accumulated row is scaled
+//    by the ratio (a power of two: exact).  The store undoes s_r.
+//  * Lane r takes channels V r .. V r + V - 1 (column tile j is channel V r + j): V contiguous floats per kk
+//    row at the store.
+// A gathered row's V channels of one lane as 32-bit words (split_rows_il_kernel layout): w[0 .. V/2) the
+// high halves, two channels a word, w[V/2 .. V) the low halves.  Words rather than half vectors, so the
+// operand repacking below stays in registers.
+template <int V>
+struct RowW {
+  uint32_t w[V];
+};
+
+template <int V>
+__device__ __forceinline__ RowW<V> ld_row(const _Float16* p) {
+  RowW<V> r;
+  if constexpr (V >= 4) {
+#pragma unroll
+    for (int h = 0; h < V / 4; ++h) {
+      const uint4 a = *reinterpret_cast<const uint4*>(p + 8 * h);
+      r.w[4 * h] = a.x;
+      r.w[4 * h + 1] = a.y;
+      r.w[4 * h + 2] = a.z;
+      r.w[4 * h + 3] = a.w;
+    }
+  } else {
+    const uint2 a = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = a.x;
+    r.w[1] = a.y;
+  }
+  return r;
+}
+
+// {half s of a, half s of b} as one word (s = 0 low, 1 high)
+__device__ __forceinline__ uint32_t pack_halves(uint32_t a, uint32_t b, int s) {
+  return __builtin_amdgcn_perm(b, a, s ? 0x07060302u : 0x05040100u);
+}
+
 template <int C, bool DUAL>
-__global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscIctdLayout L, int ncg, const float* __restrict__ x,
-                                                          const float* __restrict__ Y,
-                                                          const float* __restrict__ gates,
-                                                          const float* __restrict__ cg,
-                                                          const int32_t* __restrict__ dst_ptr,
-                                                          const int32_t* __restrict__ esrc,
-                                                          float* __restrict__ Z, float* __restrict__ zscale,
-                                                          int64_t n_nodes, const int32_t* __restrict__ node_order,
-                                                          const int32_t* __restrict__ eperm,
-                                                          const int32_t* __restrict__ gdeg) {
+__global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_h16_kernel(
+    FscIctdLayout L, int ncg, const _Float16* __restrict__ xs, const float* __restrict__ xinv,
+    const float* __restrict__ Y, const float* __restrict__ gates,
+    const float* __restrict__ cg, const int32_t* __restrict__ dst_ptr, const int32_t* __restrict__ esrc,
+    float* __restrict__ Z, float* __restrict__ zscale, int64_t n_nodes, const int32_t* __restrict__ node_order,
+    const int32_t* __restrict__ eperm, const int32_t* __restrict__ gdeg) {
   constexpr int V = C / 16;
-  constexpr int DEPTH = 2;                 // components of gathers in flight (3 costs a wave per SIMD)
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) float smem[];
   __shared__ float zmx[2][4];
   const FwdSmem sm = fwd_smem(L, ncg);
   int* gidx = reinterpret_cast<int*>(smem + sm.gidx);
   int* slot0 = reinterpret_cast<int*>(smem + sm.slot0);
   int* wtask = reinterpret_cast<int*>(smem + sm.wtask);
+  float* cb = smem + sm.cb;
   const f4* cf = reinterpret_cast<const f4*>(smem + sm.cf);
 
   if (xcd_node_k(n_nodes, node_order, 0) == -2) return;   // block-uniform
@@ -221,6 +266,21 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
   const int r = lane & 15, q = lane >> 4;
   assign_fwd_tasks(L, wtask);
   stage_fwd_tables(L, cg, ncg, smem + sm.cgs, reinterpret_cast<int4*>(smem + sm.kd), gidx, slot0, smem + sm.cf);
+  __syncthreads();
+  for (int i = threadIdx.x; i < 16 * L.KTT; i += blockDim.x) {
+    const int t = i >> 4, rr = i & 15, d1 = L.g_d1[L.tile_group[t]];
+    float m = 0.f;
+    for (int m1 = 0; m1 < d1; ++m1) {
+      float s = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const f4 c = cf[(slot0[t] + m1) * 64 + 16 * qq + rr];
+        s += (fabsf(c.x) + fabsf(c.y)) + (fabsf(c.z) + fabsf(c.w));
+      }
+      m = fmaxf(m, s);
+    }
+    cb[i] = m;
+  }
   __syncthreads();
   const int ntask = wtask[wave * 8];
 
@@ -232,19 +292,18 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
   const int beg = dst_ptr[n], end = dst_ptr[n + 1];
   const float scale = DUAL ? 1.f : 1.f / (float)max(end - beg, 1);
   float zmax = 0.f;
-  // a wave's tiles one after the other, each over all the node's edges (one accumulator tile set live)
   for (int lt = 0; lt < ntask; ++lt) {
     const int kt = wtask[wave * 8 + 1 + lt];
     const int g = L.tile_group[kt];
     const int d1 = L.g_d1[g], o1 = L.g_o1[g];
     const int gc = gidx[kt * 16 + r];
+    const float cbr = cb[kt * 16 + r];
     const f4* cft = cf + slot0[kt] * 64 + lane;
-    const float* xcol = x + o1 * C + lane_chan<V>(r);
+    const _Float16* xcol = xs + 2 * ((int64_t)o1 * C + V * r);
     f4 acc[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
-    // chunk edge r: id and gathered node, requested one chunk ahead (issued after the chunk's first
-    // gathers) so that a chunk's gathers never wait on its index loads
+    float srow = 0x1p100f;   // power of two of kk row r (lanes (r, *)), lowered as chunks need
     auto chunk_id = [&](int ebk) {
       const int ck = min(EB, end - ebk);
       return r < ck ? (DUAL ? eperm[ebk + r] : ebk + r) : -1;
@@ -254,7 +313,6 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
     for (int eb = beg; eb < end; eb += EB) {
       const int cnt = min(EB, end - eb);
       const int idr = idr_n, srcr = srcr_n;
-      // harmonics of edge r (A operand of the coupling product: Y[e = r][4q..4q+3])
       f4 yop = f4{0.f, 0.f, 0.f, 0.f};
       if (idr >= 0) {
         const float* yr = Y + (int64_t)idr * L.NY;
@@ -268,91 +326,111 @@ __global__ __launch_bounds__(256, C >= 128 ? 3 : 4) void project_fwd_kernel(FscI
       }
       float gsc = 1.f;
       if constexpr (DUAL) gsc = 1.f / (float)max(gdeg[srcr + 1] - gdeg[srcr], 1);
-      // K step u of the main product takes chunk edge 4q + u
+      const float xi = idr >= 0 ? xinv[srcr] : 0.f;   // 1/nu of chunk edge r's gathered row
       int src4[4];
-      float gt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) src4[u] = __shfl(srcr, 4 * q + u, 64);
+      auto load_k = [&](int m1, RowW<V> (&b)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) b[u] = ld_row<V>(xcol + 2 * ((int64_t)src4[u] * L.M + m1) * C);
+      };
+      RowW<V> b0[4], b1[4];
+      load_k(0, b0);
+      // A factors of edges 4q + u (gate / nu_src) and the chunk's bound on row r
+      float ym = fmaxf(fmaxf(fabsf(yop.x), fabsf(yop.y)), fmaxf(fabsf(yop.z), fabsf(yop.w)));
+      ym = fmaxf(ym, __shfl_xor(ym, 16, 64));
+      ym = fmaxf(ym, __shfl_xor(ym, 32, 64));   // max_y |Y| of chunk edge r
+      float ga[4], bnd = 0.f;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        src4[u] = __shfl(srcr, 4 * q + u, 64);
         const int id = DUAL ? __shfl(idr, 4 * q + u, 64) : (4 * q + u < cnt ? eb + 4 * q + u : -1);
         const float sc = DUAL ? __shfl(gsc, 4 * q + u, 64) : 1.f;
-        gt[u] = id >= 0 ? gates[(int64_t)id * L.NREF + gc] * sc : 0.f;
+        const float xu = __shfl(xi, 4 * q + u, 64), yu = __shfl(ym, 4 * q + u, 64);
+        ga[u] = id >= 0 ? gates[(int64_t)id * L.NREF + gc] * sc * xu : 0.f;
+        bnd = fmaxf(bnd, fabsf(ga[u]) * yu);
       }
-      auto load_k = [&](int m1, VecF<V> (&b)[4]) {
+      bnd = fmaxf(bnd, __shfl_xor(bnd, 16, 64));
+      bnd = fmaxf(bnd, __shfl_xor(bnd, 32, 64));
+      bnd *= cbr;
+      const float snew = bnd > 0.f ? fminf(srow, pow2_scale(bnd)) : srow;
+      const float ratio = snew / srow;   // a power of two (1 while the scale holds)
+      srow = snew;
+      if (__ballot(ratio != 1.f)) {      // wave-uniform: rescale the accumulated rows 4q + i
 #pragma unroll
-        for (int u = 0; u < 4; ++u) b[u] = ldq<V>(xcol + ((int64_t)src4[u] * L.M + m1) * C);
-      };
-      // gated coupling rows of component m1: a[u] = BG[edge 4q+u][kk row r]
-      auto coupling = [&](int m1, float (&a)[4]) {
-        const f4 bg = mfma_k16(yop, cft[m1 * 64], f4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i) {
+          const float ri = __shfl(ratio, 4 * q + i, 64);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = bg[u] * gt[u];
-      };
-      auto mul_k = [&](const float (&a)[4], const VecF<V> (&b)[4]) {
+          for (int j = 0; j < V; ++j) acc[j][i] *= ri;
+        }
+      }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int j = 0; j < V; ++j) acc[j] = mfma16x16x4(a[u], b[u].v[j], acc[j]);
-      };
-      float a[4];
-      VecF<V> b0[4], b1[4];
-      load_k(0, b0);
+      for (int u = 0; u < 4; ++u) ga[u] *= srow;
       if (eb + EB < end) {
         idr_n = chunk_id(eb + EB);
         srcr_n = idr_n >= 0 ? esrc[idr_n] : 0;
       }
-      if constexpr (DEPTH == 2) {
-        for (int m1 = 0; m1 < d1; m1 += 2) {
-          if (m1 + 1 < d1) load_k(m1 + 1, b1);
-          coupling(m1, a);
-          __builtin_amdgcn_sched_barrier(0);
-          mul_k(a, b0);
-          if (m1 + 1 < d1) {
-            if (m1 + 2 < d1) load_k(m1 + 2, b0);
-            coupling(m1 + 1, a);
-            __builtin_amdgcn_sched_barrier(0);
-            mul_k(a, b1);
-          }
+      // split gated coupling values of component m1: A[row r][edge 4q + u]
+      auto coupling = [&](int m1, h4& ah, h4& al) {
+        const f4 bg = mfma_k16(yop, cft[m1 * 64], f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          // v rounded to fp32 before the split: fused into the low part's fma_mix, the exact product would
+          // pair with a high part rounded from the fp32 product, off by an fp16 ulp where those differ
+          float v = bg[u] * ga[u];
+          asm volatile("" : "+v"(v));
+          const _Float16 h = (_Float16)v;
+          ah[u] = h;
+          al[u] = (_Float16)(v - (float)h);
         }
-      } else {
-        VecF<V> b2[4];
-        if (1 < d1) load_k(1, b1);
-        for (int m1 = 0; m1 < d1; m1 += 3) {
-          if (m1 + 2 < d1) load_k(m1 + 2, b2);
-          coupling(m1, a);
+      };
+      auto mul_k = [&](const h4& ah, const h4& al, const RowW<V> (&b)[4]) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const int d = j >> 1, hs = j & 1;   // word and half of channel j in each part
+          const uint2 wh = {pack_halves(b[0].w[d], b[1].w[d], hs), pack_halves(b[2].w[d], b[3].w[d], hs)};
+          const uint2 wl = {pack_halves(b[0].w[V / 2 + d], b[1].w[V / 2 + d], hs),
+                            pack_halves(b[2].w[V / 2 + d], b[3].w[V / 2 + d], hs)};
+          const h4 ph = __builtin_bit_cast(h4, wh), pl = __builtin_bit_cast(h4, wl);
+          f4 c = acc[j];
+          c = __builtin_amdgcn_mfma_f32_16x16x16f16(al, ph, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, pl, c, 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, ph, c, 0, 0, 0);
+        }
+      };
+      h4 ah, al;
+      for (int m1 = 0; m1 < d1; m1 += 2) {
+        if (m1 + 1 < d1) load_k(m1 + 1, b1);
+        coupling(m1, ah, al);
+        __builtin_amdgcn_sched_barrier(0);
+        mul_k(ah, al, b0);
+        if (m1 + 1 < d1) {
+          if (m1 + 2 < d1) load_k(m1 + 2, b0);
+          coupling(m1 + 1, ah, al);
           __builtin_amdgcn_sched_barrier(0);
-          mul_k(a, b0);
-          if (m1 + 1 < d1) {
-            if (m1 + 3 < d1) load_k(m1 + 3, b0);
-            coupling(m1 + 1, a);
-            __builtin_amdgcn_sched_barrier(0);
-            mul_k(a, b1);
-          }
-          if (m1 + 2 < d1) {
-            if (m1 + 4 < d1) load_k(m1 + 4, b1);
-            coupling(m1 + 2, a);
-            __builtin_amdgcn_sched_barrier(0);
-            mul_k(a, b2);
-          }
+          mul_k(ah, al, b1);
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const float f = scale / __shfl(srow, 4 * q + i, 64);   // 1/s of row 4q + i is exact
       const int kkl = (kt - L.g_tile0[g]) * 16 + 4 * q + i;
       if (kkl >= L.g_kcount[g]) continue;
-      VecF<V> o;
+      float o[V];
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        o.v[j] = acc[j][i] * scale;
-        zmax = fmaxf(zmax, fabsf(o.v[j]));
+        o[j] = acc[j][i] * f;
+        zmax = fmaxf(zmax, fabsf(o[j]));
       }
-      stq<V>(Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + lane_chan<V>(r), o);
+      float* zp = Z + ((int64_t)n * L.KT + L.g_kstart[g] + kkl) * C + V * r;
+      if constexpr (V >= 4) {
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) st4(zp + 4 * h, f4{o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]});
+      } else {
+        *reinterpret_cast<float2*>(zp) = make_float2(o[0], o[1]);
+      }
     }
   }
-  // per-node power of two for the split-fp16 channel mix (zmx alternates between the block's nodes, so
-  // one barrier per node suffices: a wave writes a buffer again only after the barrier that follows
-  // thread 0's last read of it)
   for (int off = 32; off > 0; off >>= 1) zmax = fmaxf(zmax, __shfl_xor(zmax, off, 64));
   float* zm = zmx[done++ & 1];
   if (lane == 0) zm[wave] = zmax;
@@ -633,7 +711,7 @@ __global__ __launch_bounds__(256, 2) void mix_grad_kernel(FscIctdLayout L, const
 // LDS block, the lanes of an edge sum different runs and accumulate them per edge and path.  The 1/deg of
 // g is applied to the outputs.
 // The input gradient dx = sum_{e: src=m} bg_e^T g_dst(e) is not formed here: it is the dual projection
-// (project_fwd_kernel over the source grouping with the dual layout) followed by the channel mix with the
+// (project_fwd_h16_kernel over the source grouping with the dual layout) followed by the channel mix with the
 // transposed weights, so no per-edge [M][C] gradient is stored.
 struct GradSmem {
   int cgs, kd, gidx, slot0, runs, nrun, cf, dgs, pl, total;
@@ -738,6 +816,52 @@ __global__ __launch_bounds__(256) void split_rows_h16_kernel(int64_t N, int len,
     }
     h[i] = vh;
     l[i] = vl;
+  }
+  if (lane == 0) inv_scale[n] = 1.f / s;   // exact: s is a power of two
+}
+
+// The split of split_rows_h16_kernel in the layout of project_fwd_h16_kernel: per row, the C channels in
+// groups of V, each group its V high halves followed by its V low halves (2C halves per row).
+template <int V>
+__global__ __launch_bounds__(256) void split_rows_il_kernel(int64_t N, int len, const float* __restrict__ X,
+                                                            _Float16* __restrict__ xs, float* __restrict__ inv_scale) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;   // uniform over the wave
+  const f4* x4 = reinterpret_cast<const f4*>(X + n * len);
+  const int n4 = len >> 2;   // len is a multiple of 4 (C >= 32)
+  float mx = 0.f;
+  for (int i = lane; i < n4; i += 64) {
+    const f4 a = x4[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(a[j]));
+  }
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  const float s = pow2_scale(mx);
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  _Float16* row = xs + 2 * n * len;
+  for (int i = lane; i < n4; i += 64) {
+    const f4 a = x4[i];
+    h4 vh, vl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = a[j] * s;
+      const _Float16 t = (_Float16)v;
+      vh[j] = t;
+      vl[j] = (_Float16)(v - (float)t);
+    }
+    const int c = 4 * i;   // first of the four values within the node's len
+    if constexpr (V >= 4) {
+      _Float16* g = row + 2 * (c - c % V) + c % V;
+      *reinterpret_cast<h4*>(g) = vh;
+      *reinterpret_cast<h4*>(g + V) = vl;
+    } else {   // V = 2: two groups
+      *reinterpret_cast<h2*>(row + 2 * c) = h2{vh[0], vh[1]};
+      *reinterpret_cast<h2*>(row + 2 * c + 2) = h2{vl[0], vl[1]};
+      *reinterpret_cast<h2*>(row + 2 * c + 4) = h2{vh[2], vh[3]};
+      *reinterpret_cast<h2*>(row + 2 * c + 6) = h2{vl[2], vl[3]};
+    }
   }
   if (lane == 0) inv_scale[n] = 1.f / s;   // exact: s is a power of two
 }
@@ -1369,25 +1493,37 @@ __global__ __launch_bounds__(256) void transpose_cg_kernel(FscIctdLayout L, FscI
   }
 }
 
-// The projection and channel mix of a layout.  Forward: blocks are receivers (ptr = dst_ptr), the edge at
-// CSR position j is j and gathers x[esrc[j]]; dual (backward): ptr = src_ptr, eperm = src_perm, esrc the
-// receiver of each edge, gdeg = dst_ptr, and the mix weights are the transposed planes.
+
+// The projection of a layout into Z [N][KT][C] + N scales.  Forward: blocks are receivers (ptr = dst_ptr),
+// the edge at CSR position j is j and gathers x[esrc[j]]; dual (backward): ptr = src_ptr, eperm = src_perm,
+// esrc the receiver of each edge, gdeg = dst_ptr.  xws: N*M*C + N floats for the split copy of x.
+template <int C, bool DUAL>
+int project_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const int32_t* esrc, const int32_t* eperm,
+              const int32_t* gdeg, const float* x, float* xws, const float* Y, const float* gates, const float* cg,
+              float* Z, const int32_t* node_order, const char* timer, hipStream_t st) {
+  // the gathered rows as fp16 parts with a power of two per node: 2 N*M*C halves, then N scales
+  _Float16* xs = reinterpret_cast<_Float16*>(xws);
+  float* xinv = xws + N * L.M * C;
+  split_rows_il_kernel<C / 16><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, L.M * C, x, xs, xinv);
+  if (check_launch("ictd split_rows")) return 2;
+  const int ncg = cg_length(L);
+  LaunchTimer tm(timer, st);
+  const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
+  project_fwd_h16_kernel<C, DUAL><<<persist_grid(N, (const void*)project_fwd_h16_kernel<C, DUAL>, lds), 256,
+                                    lds, st>>>(L, ncg, xs, xinv, Y, gates, cg, ptr, esrc, Z,
+                                               Z + N * L.KT * C, N, node_order, eperm, gdeg);
+  return check_launch("ictd project") ? 2 : 0;
+}
+
+// The projection and channel mix of a layout (project_c, then the mix of Z with the prepared planes Wh).
 template <int C, bool DUAL>
 int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const int32_t* esrc, const int32_t* eperm,
-                  const int32_t* gdeg, const float* x, const float* Y, const float* gates, const float* cg,
+                  const int32_t* gdeg, const float* x, float* xws, const float* Y, const float* gates, const float* cg,
                   const _Float16* Wh, const float* winv, float* Z, float* out, const int32_t* node_order,
                   const char* timer_project, const char* timer_mix, hipStream_t st) {
-  const int ncg = cg_length(L);
-  {
-    LaunchTimer tm(timer_project, st);
-    const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
-    // receiver-grouped gathers at C 128: two blocks per CU keep the sources of the receivers an XCD has in
-    // flight closer to its L2 (measured faster than three); the source-grouped dual pass prefers three
-    const int cap = (!DUAL && C >= 128) ? 2 : (1 << 20);
-    project_fwd_kernel<C, DUAL><<<persist_grid(N, (const void*)project_fwd_kernel<C, DUAL>, lds, cap), 256, lds, st>>>(L, ncg, x, Y, gates, cg, ptr, esrc, Z, Z + N * L.KT * C,
-                                                          N, node_order, eperm, gdeg);
-  }
-  if (check_launch("ictd project_fwd")) return 2;
+  if (const int rc = project_c<C, DUAL>(L, N, ptr, esrc, eperm, gdeg, x, xws, Y, gates, cg, Z, node_order,
+                                        timer_project, st))
+    return rc;
   int dmax = 1;
   for (int k = 0; k < L.NK; ++k) dmax = max(dmax, L.k_d[k]);
   {
@@ -1399,13 +1535,23 @@ int project_mix_c(const FscIctdLayout& L, int64_t N, const int32_t* ptr, const i
   return check_launch("ictd mix_fwd") ? 2 : 0;
 }
 
+// Workspace of the forward and of the projection alone: Z [N][KT][C] + N scales, then (256-byte aligned) the
+// split copy of x.
+int64_t fwd_split_offset(const FscIctdLayout& L, int64_t N, int C) {
+  return (N * (int64_t)L.KT * C + N + 63) / 64 * 64;
+}
+
+int64_t fwd_ws_floats(const FscIctdLayout& L, int64_t N, int C) {
+  return fwd_split_offset(L, N, C) + N * (int64_t)L.M * C + N;
+}
+
 template <int C>
 int forward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
               const float* Y, const float* gates, const float* cg, const float* W, float* Z, float* out,
               const int32_t* node_order, hipStream_t st) {
-  return project_mix_c<C, false>(L, N, dst_ptr, esrc, nullptr, nullptr, x, Y, gates, cg,
-                          reinterpret_cast<const _Float16*>(W), W + mix_weight_floats(L.NREF, C) - MIXW_TAIL, Z, out,
-                          node_order, "ictd_project", "ictd_mix", st);
+  return project_mix_c<C, false>(L, N, dst_ptr, esrc, nullptr, nullptr, x, Z + fwd_split_offset(L, N, C), Y, gates, cg,
+                                 reinterpret_cast<const _Float16*>(W), W + mix_weight_floats(L.NREF, C) - MIXW_TAIL,
+                                 Z, out, node_order, "ictd_project", "ictd_mix", st);
 }
 
 // The receiver-normalised projection Z alone (the first half of the forward), for the weight gradient
@@ -1414,16 +1560,16 @@ template <int C>
 int project_only_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const int32_t* esrc, const float* x,
                    const float* Y, const float* gates, const float* cg, float* Z, const int32_t* node_order,
                    hipStream_t st) {
-  const int ncg = cg_length(L);
-  LaunchTimer tm("ictd_project", st);
-  const size_t lds = (size_t)fwd_smem(L, ncg).total * sizeof(float);
-  project_fwd_kernel<C, false><<<persist_grid(N, (const void*)project_fwd_kernel<C, false>, lds, C >= 128 ? 2 : (1 << 20)), 256, lds, st>>>(L, ncg, x, Y, gates, cg, dst_ptr, esrc, Z,
-                                                               Z + N * L.KT * C, N, node_order, nullptr, nullptr);
-  return check_launch("ictd project") ? 2 : 0;
+  return project_c<C, false>(L, N, dst_ptr, esrc, nullptr, nullptr, x, Z + fwd_split_offset(L, N, C), Y, gates, cg, Z,
+                             node_order, "ictd_project", st);
 }
 
-// Workspace of the backward: dZ [N][KT][C] + N scales; R [N][KT_dual][C] + N scales, then the dual
-// coupling table.
+// Workspace of the backward: dZ [N][KT][C] + N scales, which once dZ is used hold the split rows of the
+// output gradient (N*M*C + N floats); R [N][KT_dual][C] + N scales, then the dual coupling table.
+int64_t dz_ws_floats(const FscIctdLayout& L, int64_t N, int C) {
+  return N * (int64_t)max(L.KT, L.M) * C + N;
+}
+
 int64_t dual_ws_floats(const FscIctdLayout& L, int64_t N, int C) {
   int64_t kt = 0;
   for (int p = 0; p < L.NP; ++p) kt += L.g_d1[L.p_group[p]];
@@ -1474,7 +1620,7 @@ int backward_c(const FscIctdLayout& L, int64_t N, const int32_t* dst_ptr, const 
   float* cgd = Rw + N * D.KT * C + N;
   transpose_cg_kernel<<<(unsigned)D.NP, 256, 0, st>>>(L, D, map, cg, cgd);
   if (check_launch("ictd transpose_cg")) return 2;
-  return project_mix_c<C, true>(D, N, src_ptr, edst, src_perm, dst_ptr, G, Y, gates, cgd,
+  return project_mix_c<C, true>(D, N, src_ptr, edst, src_perm, dst_ptr, G, dZ, Y, gates, cgd,
                           reinterpret_cast<const _Float16*>(Wt + (int64_t)L.NREF * C * C),
                           Wt + mix_weight_floats(L.NREF, C) - MIXW_TAIL, Rw, dx, node_order, "ictd_dual_project",
                           "ictd_dual_mix", st);
@@ -1529,11 +1675,18 @@ int fsc_ictd_prepare_weights(const float* W, int32_t n_ref, int32_t channels, fl
   return check_launch("ictd prepare_weights") ? 2 : 0;
 }
 
+int fsc_ictd_forward_workspace(const FscIctdLayout* layout, int64_t n_nodes, int32_t channels, int64_t* z_floats) {
+  if (check_layout(layout, channels, "fsc_ictd_forward_workspace")) return 1;
+  FSC_CHECK_ARG(z_floats && n_nodes >= 0, "fsc_ictd_forward_workspace: bad argument");
+  *z_floats = fwd_ws_floats(*layout, n_nodes, channels);
+  return 0;
+}
+
 int fsc_ictd_backward_workspace(const FscIctdLayout* layout, int64_t n_nodes, int32_t channels, int64_t* dz_floats,
                                 int64_t* r_floats) {
   if (check_layout(layout, channels, "fsc_ictd_backward_workspace")) return 1;
   FSC_CHECK_ARG(dz_floats && r_floats && n_nodes >= 0, "fsc_ictd_backward_workspace: bad argument");
-  *dz_floats = n_nodes * (int64_t)layout->KT * channels + n_nodes;
+  *dz_floats = dz_ws_floats(*layout, n_nodes, channels);
   *r_floats = dual_ws_floats(*layout, n_nodes, channels);
   return 0;
 }

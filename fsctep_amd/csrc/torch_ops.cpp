@@ -304,6 +304,12 @@ Tensor ictd_prepare_weights(const Tensor& W) {
 
 Tensor ictd_prepare_weights_meta(const Tensor& W) { return at::empty({ictd_weight_floats(W.size(0), W.size(1))}, fopts(W)); }
 
+int64_t ictd_forward_ws(const FscIctdLayout* L, int64_t N, int64_t C) {
+  int64_t z = 0;
+  check(fsc_ictd_forward_workspace(L, N, (int32_t)C, &z), "fsc_ictd_forward_workspace");
+  return z;
+}
+
 Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const Tensor& W_, const Tensor& Wt,
                  const Tensor& cg, const Tensor& dst_ptr, const Tensor& edge_src, const Tensor& src_ptr,
                  const Tensor& src_perm, const Tensor& edge_dst, const Tensor& node_order, at::IntArrayRef layout) {
@@ -315,8 +321,8 @@ Tensor ictd_conv(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, const
   Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
   TORCH_CHECK(W_.size(0) == L->NREF && Wt.dim() == 1 && Wt.numel() == ictd_weight_floats(L->NREF, C),
               "ictd_conv: Wt must be ictd_prepare_weights(W) of this layout's weights");
-  // z: N*KT*C floats of projections, then N per-node scales
-  Tensor z = at::empty({N * L->KT * C + N}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
+  // z: N*KT*C floats of projections, N per-node scales, then the kernels' split copy of x
+  Tensor z = at::empty({ictd_forward_ws(L, N, C)}, fopts(x)), out = at::empty({N, L->M, C}, fopts(x));
   check(fsc_ictd_conv_forward(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")),
                               cf(x), cf(Y), cf(gates), cf(cg), cf(Wt), mf(z), mf(out), order_ptr(node_order, N),
                               stream_of(x)),
@@ -339,7 +345,7 @@ Tensor ictd_project(const Tensor& x_, const Tensor& Y_, const Tensor& gates_, co
   TORCH_CHECK(x_.dim() == 3 && x_.size(1) == L->M, "x must be (N, M, C) for this layout");
   const int64_t N = x_.size(0), C = x_.size(2), E = Y_.size(0);
   Tensor x = f32c(x_), Y = f32c(Y_), gates = f32c(gates_);
-  Tensor z = at::empty({N * L->KT * C + N}, fopts(x));
+  Tensor z = at::empty({ictd_forward_ws(L, N, C)}, fopts(x));
   check(fsc_ictd_project(L, N, E, (int32_t)C, ci(i32c(dst_ptr, "dst_ptr")), ci(i32c(edge_src, "edge_src")), cf(x),
                          cf(Y), cf(gates), cf(cg), mf(z), order_ptr(node_order, N), stream_of(x)),
         "fsc_ictd_project");

@@ -278,16 +278,18 @@ typedef struct FscIctdLayout {
  * i.e. HarmonicFullyConnectedTensorProduct[O3].forward (models/ictd_irreps.py:971-1253, :1512-1695)
  * and the project/mix ops of the reference extension (csrc/ictd_tp.cpp:140-494).
  * gates [E][NREF]; Wp: fsc_ictd_prepare_weights of tp2.weight; cg: concatenated normalised C[m1][m2][m3]
- * of the live paths; z_ws N*KT*C + N floats of scratch; out [N][M][C].  node_order: null or a
- * permutation of the nodes (fsc_spatial_order) for the per-receiver kernels (a performance hint).
+ * of the live paths; z_ws scratch of fsc_ictd_forward_workspace floats; out [N][M][C].  node_order: null
+ * or a permutation of the nodes (fsc_spatial_order) for the per-receiver kernels (a performance hint).
  * n_nodes < 2^24 here, in fsc_ictd_project and in fsc_ictd_conv_backward. */
+int fsc_ictd_forward_workspace(const FscIctdLayout* layout, int64_t n_nodes, int32_t channels, int64_t* z_floats);
 int fsc_ictd_conv_forward(const FscIctdLayout* layout, int64_t n_nodes, int64_t n_edges, int32_t channels,
                           const int32_t* dst_ptr, const int32_t* edge_src, const float* x, const float* Y,
                           const float* gates, const float* cg, const float* Wp, float* z_ws, float* out,
                           const int32_t* node_order, hipStream_t stream);
 
 /* The receiver-normalised projection of the forward alone, Z[n][kk][i] = (1/indeg n) sum_{e->n} sum_m1
- * BG_e[m1][kk] x_src[o1+m1][i] (kk = (path, m3), KT slots), into z_ws[0 .. N*KT*C) (N*KT*C + N floats):
+ * BG_e[m1][kk] x_src[o1+m1][i] (kk = (path, m3), KT slots), into z_ws[0 .. N*KT*C) (z_ws of
+ * fsc_ictd_forward_workspace floats):
  * the operand of the weight gradient dW[gate_p][o][i] = sum_n sum_m3 G[n][oo_p+m3][o] Z[n][koff_p+m3][i]
  * used by training.  Replaces project_bucket_forward with the receiver scatter
  * (csrc/ictd_tp.cpp:140-176, models/ictd_irreps_cuda.py:314-336). */
