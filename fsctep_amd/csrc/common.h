@@ -87,6 +87,34 @@ __device__ __forceinline__ void split2h(const float (&v)[8], float s, h8& h, h8&
   }
 }
 
+// split2h without a scale (the caller's values are already scaled) in 12 VALU operations for 8 values: the
+// high parts two at a time by v_cvt_pk_f16_f32, each low part by one v_fma_mix reading its high part from
+// the packed word (v - h, exact in fp32, rounded to fp16).  The compiler's own form converts each high part
+// twice (28 operations).  Register hazards of asm-written VGPRs are not tracked by the compiler, so the block
+// ends with the two wait states a VALU write needs before an MFMA reads it.
+__device__ __forceinline__ void split2h_pk(const float (&v)[8], h8& h, h8& l) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  u4 hw, lw;
+  asm volatile(
+      "v_cvt_pk_f16_f32 %0, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %1, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %2, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %3, %14, %15\n\t"
+      "v_fma_mixlo_f16 %4, %8, 1.0, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %4, %9, 1.0, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixlo_f16 %5, %10, 1.0, -%1 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %5, %11, 1.0, -%1 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixlo_f16 %6, %12, 1.0, -%2 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %6, %13, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixlo_f16 %7, %14, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %7, %15, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "s_nop 1"
+      : "=&v"(hw.x), "=&v"(hw.y), "=&v"(hw.z), "=&v"(hw.w), "=&v"(lw.x), "=&v"(lw.y), "=&v"(lw.z), "=&v"(lw.w)
+      : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+  h = __builtin_bit_cast(h8, hw);
+  l = __builtin_bit_cast(h8, lw);
+}
+
 __device__ __forceinline__ f4 mfma_h16(const h8& a, const h8& b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

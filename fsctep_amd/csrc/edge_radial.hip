@@ -103,8 +103,9 @@ __device__ __forceinline__ float sigm(float x) { return __fdividef(1.f, 1.f + __
 // One wave per 16-edge tile; lane (r, q) works for edge e0 + r.  The hidden units are laid
 // out as the MFMA output: lane (r, q) holds unit j = 16*jt + 4*q + i in register (jt, i), so
 // one layer's output is directly the next product's B operand.
-// The first layer (K = nb <= 16) runs on the fp32 MFMA from W0 [64][NBMAX] (and W0^T [NBMAX][68] in the
-// backward), rows padded so the four K values a lane needs come in one 16-byte read.  The 64-wide layers
+// The first layer (K = nb <= 16) runs on the fp32 MFMA from W0 [64][NBMAX + 1] (rows padded so the 64 lanes'
+// reads of one K step fall in distinct banks) and, in the backward, W0^T [NBMAX][68] (rows padded so the four
+// K values a lane needs come in one 16-byte read).  The 64-wide layers
 // (W2, the optional last Linear W4 with up to 64 outputs, and their transposes in the backward) run on
 // v_mfma_f32_16x16x32_f16 with fp32-accurate split-fp16 products (mfma_x3, common.h): each layer's weights
 // are staged in LDS as two fp16 planes of W sw (one power of two per layer from max |W|), in the K order of
@@ -119,7 +120,7 @@ struct LayerH16 {
 struct NoLayer {};
 template <bool BWD>
 struct Smem {
-  float w0[HID][NBMAX];
+  float w0[HID][NBMAX + 1];
   float w0t[BWD ? NBMAX : 1][WS];
   LayerH16 w2;                                      // W2 (forward product; recomputed in the backward)
   std::conditional_t<BWD, LayerH16, NoLayer> w2t;   // W2^T (backward)
@@ -290,10 +291,14 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_forward_kernel(c
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int nks = (nb + 3) / 4;
-  const int64_t ntiles = (n_edges + 15) / 16;
-  for (int64_t t = (int64_t)blockIdx.x * RAD_WAVES + wave; t < ntiles; t += (int64_t)gridDim.x * RAD_WAVES) {
+  const int64_t ntiles = (n_edges + 15) / 16, tstride = (int64_t)gridDim.x * RAD_WAVES;
+  // each tile's radii are requested one tile ahead
+  auto radius = [&](int64_t t) { return (t < ntiles && 16 * t + r < n_edges) ? rad[16 * t + r] : 1.f; };
+  float rr_next = radius((int64_t)blockIdx.x * RAD_WAVES + wave);
+  for (int64_t t = (int64_t)blockIdx.x * RAD_WAVES + wave; t < ntiles; t += tstride) {
     const int64_t e = 16 * t + r;
-    const float rr = (e < n_edges) ? rad[e] : 1.f;
+    const float rr = rr_next;
+    rr_next = radius(t + tstride);
     float emb[NBMAX / 4];
     lane_basis(rr, nb, rc, basis, q, emb);
     f4 u0[4], u2[4], a2[4];

@@ -324,14 +324,15 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
       pw[i] = *reinterpret_cast<const f4*>(Wf2 + pl * plane + (int64_t)p * PSZ + 8 * rem);
     }
   };
+  // t[n][m][I0 + 8q + j] times the node's power of two (exact), so the Gram values come out scaled
   float tc[D][8];
   auto load_tc = [&](int Ib) {
 #pragma unroll
     for (int m = 0; m < D; ++m) {
       const f4 a = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q) : zero;
       const f4 b = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q + 4) : zero;
-      tc[m][0] = a.x; tc[m][1] = a.y; tc[m][2] = a.z; tc[m][3] = a.w;
-      tc[m][4] = b.x; tc[m][5] = b.y; tc[m][6] = b.z; tc[m][7] = b.w;
+      tc[m][0] = a.x * sn; tc[m][1] = a.y * sn; tc[m][2] = a.z * sn; tc[m][3] = a.w * sn;
+      tc[m][4] = b.x * sn; tc[m][5] = b.y * sn; tc[m][6] = b.z * sn; tc[m][7] = b.w * sn;
     }
   };
   f4 ts[TSB][D];
@@ -381,7 +382,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
           }
         }
         h8 ah, al;
-        split2h(gv, sn, ah, al);
+        split2h_pk(gv, ah, al);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
           const _Float16* b = wp + (s * 2 * S + ct * 32) * 8;

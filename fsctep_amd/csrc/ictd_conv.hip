@@ -717,6 +717,11 @@ struct GradSmem {
   int cgs, kd, gidx, slot0, runs, nrun, cf, dgs, pl, total;
 };
 
+// Row stride (floats) of a slot's Cf[y][kk] in the gradient kernel's LDS: with 20, a lane (r, q) reading
+// Cf[4q + j][r] (fixed j) and one reading the float4 Cf[r][4q .. 4q + 3] both meet every bank once per
+// 16-lane group (16 was four lanes per bank).
+constexpr int CFS = 20;
+
 __host__ __device__ inline GradSmem grad_smem(const FscIctdLayout& L, int ncg) {
   GradSmem s;
   int o = 0;
@@ -726,9 +731,9 @@ __host__ __device__ inline GradSmem grad_smem(const FscIctdLayout& L, int ncg) {
   s.slot0 = o; o += up4(L.KTT + 1);
   s.runs = o;  o += 16 * L.KTT;            // path runs of each tile: p | first row << 8 | end row << 16
   s.nrun = o;  o += up4(L.KTT);
-  s.cf = o;    o += n_slots(L) * 256;      // Cf[slot][y][kk row], slot = (tile, m1)
+  s.cf = o;    o += n_slots(L) * 16 * CFS; // Cf[slot][y][kk row], slot = (tile, m1), rows CFS apart
   s.dgs = o;   o += up4(4 * 16 * L.NP);   // per wave: dgate[e][p] of the chunk
-  s.pl = o;    o += 4 * 256;               // per wave: one tile's H.BG' row sums
+  s.pl = o;    o += 4 * 16 * CFS;          // per wave: one tile's H.BG' row sums, rows CFS apart
   s.total = o;
   return s;
 }
@@ -771,7 +776,7 @@ __device__ __forceinline__ void stage_grad_tables(const FscIctdLayout& L, const 
       const int m2 = y - (d.y & 255), d2 = (d.y >> 8) & 255, d3 = d.y >> 16;
       if (m2 >= 0 && m2 < d2) v = cgs[d.x + (m1 * d2 + m2) * d3];
     }
-    cf[i] = v;
+    cf[(sl * 16 + y) * CFS + r] = v;
   }
 }
 
@@ -891,7 +896,7 @@ __global__ __launch_bounds__(256, C >= 128 ? 2 : 3) void project_grad_h16_kernel
                     reinterpret_cast<int*>(smem + sm.nrun), smem + sm.cf);
   __syncthreads();
   float* dgs = smem + sm.dgs + wave * 16 * L.NP + r * L.NP;   // edge r's path sums (lanes (r, *))
-  float* pl = smem + sm.pl + wave * 256;                       // the tile's H.BG' row sums, [edge][kk row]
+  float* pl = smem + sm.pl + wave * 16 * CFS;                  // the tile's H.BG' row sums, [edge][kk row]
   auto wave_sync = [] {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -979,11 +984,11 @@ __global__ __launch_bounds__(256, C >= 128 ? 2 : 3) void project_grad_h16_kernel
       for (int s = 0; s < KS; ++s) ht = mfma_x3(ah[s], al[s], bh[s], bl[s], ht);
 #pragma unroll
       for (int i = 0; i < 4; ++i) ht[i] *= inv[i];                             // H[edge r][kk 4q+i]
-      const float* cs = cf + (slot0[kt] + m1) * 256;
+      const float* cs = cf + (slot0[kt] + m1) * 16 * CFS;
       f4 ca;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ca[j] = cs[(4 * q + j) * 16 + r];          // Cf[y = 4q+j][kk = r]
-      const f4 ct = *reinterpret_cast<const f4*>(cs + r * 16 + 4 * q);      // Cf[y = r][kk = 4q..4q+3]
+      for (int j = 0; j < 4; ++j) ca[j] = cs[(4 * q + j) * CFS + r];        // Cf[y = 4q+j][kk = r]
+      const f4 ct = *reinterpret_cast<const f4*>(cs + r * CFS + 4 * q);     // Cf[y = r][kk = 4q..4q+3]
       const f4 bgt = mfma_k16(ca, yop, f4{0.f, 0.f, 0.f, 0.f});              // BG'[edge r][kk 4q+i]
       f4 hg;
 #pragma unroll
@@ -1039,13 +1044,13 @@ __global__ __launch_bounds__(256, C >= 128 ? 2 : 3) void project_grad_h16_kernel
       for (int tt = 0; tt < 2; ++tt) {
         if (tt >= nt) continue;
         const int kt = t0 + tt;
-        *reinterpret_cast<f4*>(pl + r * 16 + 4 * q) = P[tt];
+        *reinterpret_cast<f4*>(pl + r * CFS + 4 * q) = P[tt];
         wave_sync();
         for (int k2 = q; k2 < nrun[kt]; k2 += 4) {
           const int run = runs[kt * 16 + k2];
           const int p = run & 255, rb = (run >> 8) & 255, re = run >> 16;
           float sum = 0.f;
-          for (int i = rb; i < re; ++i) sum += pl[r * 16 + i];
+          for (int i = rb; i < re; ++i) sum += pl[r * CFS + i];
           dgs[p] += sum;
         }
         wave_sync();
