@@ -210,9 +210,9 @@ __device__ __forceinline__ void dense64(const LayerH16& W, float winv, const flo
   h8 xh[2], xl[2];
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    const float v[8] = {x[2 * st][0], x[2 * st][1], x[2 * st][2], x[2 * st][3],
-                        x[2 * st + 1][0], x[2 * st + 1][1], x[2 * st + 1][2], x[2 * st + 1][3]};
-    split2h(v, sx, xh[st], xl[st]);
+    const float v[8] = {x[2 * st][0] * sx, x[2 * st][1] * sx, x[2 * st][2] * sx, x[2 * st][3] * sx,
+                        x[2 * st + 1][0] * sx, x[2 * st + 1][1] * sx, x[2 * st + 1][2] * sx, x[2 * st + 1][3] * sx};
+    split2h_pk(v, xh[st], xl[st]);
   }
   const float f = winv / sx;   // exact: powers of two
 #pragma unroll
@@ -231,10 +231,10 @@ __device__ __forceinline__ void dense64(const LayerH16& W, float winv, const flo
   }
 }
 
-// u0 = W0 emb + b0 and u2 = W2 silu(u0) + b2 for the lane's edge (MFMA layout above).
+// u0 = W0 emb + b0 for the lane's edge (MFMA layout above).
 template <bool BWD>
-__device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&emb)[NBMAX / 4], int nks, int r, int q,
-                                            f4 (&u0)[4], f4 (&u2)[4]) {
+__device__ __forceinline__ void first_layer(const Smem<BWD>& sm, const float (&emb)[NBMAX / 4], int nks, int r, int q,
+                                            f4 (&u0)[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
     f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -246,6 +246,13 @@ __device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&e
     u0[jt] = acc;
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// u0 = W0 emb + b0 and u2 = W2 silu(u0) + b2 for the lane's edge (MFMA layout above).
+template <bool BWD>
+__device__ __forceinline__ void mlp_forward(const Smem<BWD>& sm, const float (&emb)[NBMAX / 4], int nks, int r, int q,
+                                            f4 (&u0)[4], f4 (&u2)[4]) {
+  first_layer(sm, emb, nks, r, q, u0);
   f4 a0[4];
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
@@ -344,11 +351,13 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(
     const int64_t e = 16 * t + r;
     const bool ok = e < n_edges;
     const float rr = ok ? rad[e] : 1.f;
-    float emb[NBMAX / 4], demb[4];
+    float emb[NBMAX / 4];
     lane_basis(rr, nb, rc, basis, q, emb);
-    lane_basis_deriv(rr, nb, rc, basis, q, demb);
-    f4 u0[4], u2[4];
-    mlp_forward(sm, emb, nks, r, q, u0, u2);
+    f4 u2[4];
+    {
+      f4 u0[4];   // recomputed below rather than held across the two 64-wide products (register pressure)
+      mlp_forward(sm, emb, nks, r, q, u0, u2);
+    }
     f4 dh[4];
     if (W4) {
       f4 d[4];
@@ -372,8 +381,9 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(
         const float s = sigm(u2[ot][i]);
         g2[ot][i] = dh[ot][i] * s * (1.f + u2[ot][i] * (1.f - s));
       }
-    f4 da0[4], g0[4];
+    f4 da0[4], g0[4], u0[4];
     dense64(sm.w2t, sm.winv[1], nullptr, g2, r, q, da0);
+    first_layer(sm, emb, nks, r, q, u0);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
@@ -389,6 +399,8 @@ __global__ __launch_bounds__(64 * RAD_WAVES, 4) void radial_mlp_backward_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) de = mfma16x16x4(a[i], g0[jt][i], de);
     }
+    float demb[4];   // formed here, not held across the products
+    lane_basis_deriv(rr, nb, rc, basis, q, demb);
     float part = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) part += de[i] * demb[i];
