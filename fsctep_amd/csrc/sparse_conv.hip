@@ -342,6 +342,21 @@ inline int neg_ksplit(int64_t N) {
   return ks;
 }
 
+// Blocks per source node of the edge message and its gradient: one per node on large graphs; on small ones
+// (one block per node leaves most of the 256 CUs idle or waiting on the highest-degree node) the message's
+// column blocks and the gradient's channel chunks are split over 2 or 4 blocks.
+inline int msg_parts(int64_t N) { return N <= 256 ? 4 : N < 2048 ? 2 : 1; }
+
+// Start (floats from dS) and size of the partial dh, dn and dS maxima of a split message gradient, after the
+// backward's tail and per-node scales, 256-byte aligned.
+inline int64_t msg_parts_offset(int64_t N, int C) {
+  return (N * s_node_stride(C) + (int64_t)neg_ksplit(N) * NSLOT * N * C + N + 63) / 64 * 64;
+}
+inline int64_t msg_parts_floats(int64_t N, int64_t E) {
+  const int np = msg_parts(N);
+  return np > 1 ? (int64_t)np * (E * (KH + 3) + N) : 0;
+}
+
 template <int C, bool BF16>
 __global__ __launch_bounds__(256, 2) void node_expand_grad_kernel(const float* __restrict__ dS,
                                                                   const float* __restrict__ dscale,
@@ -575,9 +590,11 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
     }
   };
 
+  // this block's column blocks: part blockIdx.y of gridDim.y (msg_parts)
+  const int cb0 = (int)(blockIdx.y * NCB / gridDim.y), cb1 = (int)((blockIdx.y + 1) * NCB / gridDim.y);
   for (int pb = beg; pb < end; pb += EP) {
     const int cnt = min(EP, end - pb);
-    if (wave < NCB) load(a0, wave);   // independent of the staging below
+    if (cb0 + wave < cb1) load(a0, cb0 + wave);   // independent of the staging below
     __syncthreads();
     if (threadIdx.x < EP) eids[threadIdx.x] = src_perm[pb + min((int)threadIdx.x, cnt - 1)];
     __syncthreads();
@@ -651,12 +668,12 @@ __global__ __launch_bounds__(192, 2) void edge_message_kernel(const float* __res
       }
     };
 #pragma unroll 1
-    for (int cb = wave; cb < NCB; cb += 6) {
-      if (cb + 3 < NCB) load(a1, cb + 3);
+    for (int cb = cb0 + wave; cb < cb1; cb += 6) {
+      if (cb + 3 < cb1) load(a1, cb + 3);
       __builtin_amdgcn_sched_barrier(0);
       run(a0, cb);
-      if (cb + 3 < NCB) {
-        if (cb + 6 < NCB) load(a0, cb + 6);
+      if (cb + 3 < cb1) {
+        if (cb + 6 < cb1) load(a0, cb + 6);
         __builtin_amdgcn_sched_barrier(0);
         run(a1, cb + 3);
       }
@@ -1074,13 +1091,23 @@ __global__ __launch_bounds__(256, 4) void edge_message_grad_h16_kernel(
     const float* __restrict__ h, const float* __restrict__ S, const float* __restrict__ P,
     const int32_t* __restrict__ src_ptr, const int32_t* __restrict__ src_perm, const int32_t* __restrict__ edge_dst,
     float scale, float* __restrict__ dh, float* __restrict__ dS, float* __restrict__ dn, float* __restrict__ dscale,
-    int64_t n_nodes, const int32_t* __restrict__ node_order) {
+    int64_t n_nodes, const int32_t* __restrict__ node_order, int64_t n_edges) {
   constexpr int CC = 8;              // channels per chunk
   constexpr int NCH = C / CC;
   constexpr int DW = NSLOT * CC;     // dP columns per chunk, column = slot*CC + c
   constexpr int NCT = DW / 16;       // 16-wide column tiles per chunk
   constexpr int COLS = 65 * C;
   constexpr int NCOL = NSLOT * C;
+  // this block's channel chunks: part blockIdx.y of gridDim.y (msg_parts).  With more than one part, dh, dn
+  // and the dS maximum are partial: each part writes its own (dh + part E KH, dn + part 3E, dscale + part N,
+  // the maximum itself) and msg_grad_combine_kernel adds them.
+  const int part = (int)blockIdx.y, nparts = (int)gridDim.y;
+  const int ch0 = part * NCH / nparts, ch1 = (part + 1) * NCH / nparts;
+  if (nparts > 1) {
+    dh += (int64_t)part * n_edges * KH;
+    dn += (int64_t)part * n_edges * 3;
+    dscale += (int64_t)part * n_nodes;
+  }
   __shared__ __align__(16) _Float16 dpl[2][EP][DPS];   // planes h, l of dP[e] * s_e
   __shared__ int32_t eids[EP];
   __shared__ int32_t dsts[EP];
@@ -1107,9 +1134,10 @@ __global__ __launch_bounds__(256, 4) void edge_message_grad_h16_kernel(
   const int cl = threadIdx.x & (CC - 1);   // dP builder: channel within the chunk
   const int eb = threadIdx.x / CC;         // dP builder: edges eb, eb + 32
 
-  if (end == beg) {   // no out-edges: dS of this node is zero (block-uniform branch)
-    for (int idx = threadIdx.x; idx < NSLOT * COLS / 4; idx += 256) st4(dSm + 4 * idx, f4{0.f, 0.f, 0.f, 0.f});
-    if (threadIdx.x == 0) dscale[m] = 1.f;
+  if (end == beg) {   // no out-edges: dS of this node is zero (block-uniform branch; part 0 writes it)
+    if (part == 0)
+      for (int idx = threadIdx.x; idx < NSLOT * COLS / 4; idx += 256) st4(dSm + 4 * idx, f4{0.f, 0.f, 0.f, 0.f});
+    if (threadIdx.x == 0) dscale[m] = nparts > 1 ? 0.f : 1.f;
     return;
   }
   float amax = 0.f;   // max |dS| over the values stored by the last edge block (the final ones)
@@ -1193,7 +1221,7 @@ __global__ __launch_bounds__(256, 4) void edge_message_grad_h16_kernel(
         sv[32 + j] = buffer_ld1(srs, svoff_t, (uint32_t)((16 * COLS + (ch * CC + j) * KH) * 4));
     };
 #pragma unroll 1
-    for (int ch = 0; ch < NCH; ++ch) {
+    for (int ch = ch0; ch < ch1; ++ch) {
       const int c0 = ch * CC;
       load_g(ch);
       // ---- dP for edges eb, eb+32 and channel c0+cl (scaled by s_e, split into the two planes);
@@ -1376,7 +1404,37 @@ __global__ __launch_bounds__(256, 4) void edge_message_grad_h16_kernel(
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
   if (lane == 0) amx[wave] = amax;
   __syncthreads();
-  if (threadIdx.x == 0) dscale[m] = pow2_scale(fmaxf(fmaxf(amx[0], amx[1]), fmaxf(amx[2], amx[3])));
+  if (threadIdx.x == 0) {
+    const float mx = fmaxf(fmaxf(amx[0], amx[1]), fmaxf(amx[2], amx[3]));
+    dscale[m] = nparts > 1 ? mx : pow2_scale(mx);
+  }
+}
+
+// The parts of a split message gradient: dh and dn summed over the parts in order, the dS scale from the
+// maximum over the parts.  One float4 of dh, one float of dn or one node per thread.
+__global__ __launch_bounds__(256) void msg_grad_combine_kernel(const float* __restrict__ dhp,
+                                                               const float* __restrict__ dnp,
+                                                               const float* __restrict__ dsp, int nparts,
+                                                               int64_t n_edges, int64_t n_nodes,
+                                                               float* __restrict__ dh, float* __restrict__ dn,
+                                                               float* __restrict__ dscale) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t n4 = n_edges * KH / 4, nd = 3 * n_edges;
+  if (i < n4) {
+    f4 s = ld4(dhp + 4 * i);
+    for (int p = 1; p < nparts; ++p) s += ld4(dhp + (int64_t)p * n_edges * KH + 4 * i);
+    st4(dh + 4 * i, s);
+  } else if (i < n4 + nd) {
+    const int64_t j = i - n4;
+    float s = dnp[j];
+    for (int p = 1; p < nparts; ++p) s += dnp[(int64_t)p * nd + j];
+    dn[j] = s;
+  } else if (i < n4 + nd + n_nodes) {
+    const int64_t m = i - n4 - nd;
+    float mx = dsp[m];
+    for (int p = 1; p < nparts; ++p) mx = fmaxf(mx, dsp[(int64_t)p * n_nodes + m]);
+    dscale[m] = pow2_scale(mx);
+  }
 }
 
 // ---------------------------------------------------------------- conv1 (species-pair form)
@@ -1696,7 +1754,8 @@ int conv_forward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32_
   if (check_launch("sparse node_expand")) return 2;
   {
     LaunchTimer tm("edge_message", st);
-    edge_message_kernel<C, BF16><<<xcd_grid(N), 192, 0, st>>>(h, S, src_ptr, src_perm, P, N, node_order);
+    edge_message_kernel<C, BF16><<<dim3(xcd_grid(N), msg_parts(N)), 192, 0, st>>>(h, S, src_ptr, src_perm, P, N,
+                                                                              node_order);
   }
   if (check_launch("sparse edge_message")) return 2;
   {
@@ -1726,8 +1785,18 @@ int conv_backward_impl(int64_t N, int64_t E, const int32_t* dst_ptr, const int32
     float* gmax = tail + (int64_t)NCOMP * N * C;   // after the chunk-major gradient, inside the tail
     grad_absmax_kernel<C><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(G, gmax, N);
     LaunchTimer tm("edge_message_grad", st);
-    edge_message_grad_h16_kernel<C><<<xcd_grid(N), 256, 0, st>>>(tail, gmax, nvec, h, S, P, src_ptr, src_perm,
-                                                                 edge_dst, scale, dh, dS, dn, dscale, N, node_order);
+    const int np = msg_parts(N);
+    float* dhp = dS + msg_parts_offset(N, C);   // the parts of a split message gradient
+    float* dnp = dhp + (int64_t)np * E * KH;
+    float* dsp = dnp + (int64_t)np * E * 3;
+    edge_message_grad_h16_kernel<C><<<dim3(xcd_grid(N), np), 256, 0, st>>>(
+        tail, gmax, nvec, h, S, P, src_ptr, src_perm, edge_dst, scale, np > 1 ? dhp : dh, dS, np > 1 ? dnp : dn,
+        np > 1 ? dsp : dscale, N, node_order, E);
+    if (np > 1) {
+      if (check_launch("sparse edge_message_grad")) return 2;
+      msg_grad_combine_kernel<<<(unsigned)((E * KH / 4 + 3 * E + N + 255) / 256), 256, 0, st>>>(
+          dhp, dnp, dsp, np, E, N, dh, dn, dscale);
+    }
   } else {
     LaunchTimer tm(DIR ? "edge_message_grad_direction" : "edge_message_grad", st);
     edge_message_grad_kernel<C, DIR, BF16><<<xcd_grid(N), 256, 0, st>>>(tail, nvec, udir, h, S, P, src_ptr, src_perm,
@@ -1771,8 +1840,10 @@ int fsc_sparse_conv_workspace(int64_t n_nodes, int64_t n_edges, int32_t channels
   FSC_CHECK_ARG(sparse_channels_ok(channels), "fsc_sparse_conv_workspace: channels must be 32, 64 or 128");
   FSC_CHECK_ARG(s_floats && p_floats, "fsc_sparse_conv_workspace: null output");
   // the tail (ks x 18 x N x C + N, ks = neg_ksplit(N)) holds the partial input gradients and per-node
-  // scales of the backward
-  *s_floats = n_nodes * s_node_stride(channels) + (int64_t)neg_ksplit(n_nodes) * NSLOT * n_nodes * channels + n_nodes;
+  // scales of the backward; on small graphs (msg_parts) the parts of the split message gradient follow
+  *s_floats = msg_parts_floats(n_nodes, n_edges) > 0
+                  ? msg_parts_offset(n_nodes, channels) + msg_parts_floats(n_nodes, n_edges)
+                  : n_nodes * s_node_stride(channels) + (int64_t)neg_ksplit(n_nodes) * NSLOT * n_nodes * channels + n_nodes;
   *p_floats = n_edges * (int64_t)NSLOT * channels;
   return 0;
 }

@@ -63,7 +63,11 @@ int main(int argc, char** argv) {
                     int64_t, const std::optional<at::Tensor>&, const std::optional<at::Tensor>&)>();
   auto no_order = at::empty({0}, at::device(at::kMeta).dtype(at::kInt));
   auto [out, S, P] = sc.call(x, h, nv, bk, bk, ip, ip, ie, ie, no_order, 0, std::nullopt, std::nullopt);
-  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10 || P.numel() != 30 * 18 * 64) {
+  // S: the backward's tail (16 node-expansion K parts at ten nodes), 256-byte aligned, then the four parts
+  // of the split message gradient (dh, dn, dS maxima)
+  const int64_t tail = 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10;
+  if (out.sizes() != at::IntArrayRef({10, 13, 64}) || S.numel() != (tail + 63) / 64 * 64 + 4 * (30 * 67 + 10) ||
+      P.numel() != 30 * 18 * 64) {
     std::fprintf(stderr, "sparse_conv meta shapes wrong\n");
     return 1;
   }

@@ -35,8 +35,11 @@ def test_argument_errors_are_reported_without_a_gpu():
     s, p = ctypes.c_int64(), ctypes.c_int64()
     assert lib.fsc_sparse_conv_workspace(10, 20, 64, ctypes.byref(s), ctypes.byref(p)) == 0
     # the tail holds ks partial input gradients of the node-expansion gradient: ks = 16 for ten nodes (six
-    # row tiles), 2 from about 5,000 nodes on
-    assert s.value == 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10 and p.value == 20 * 18 * 64
+    # row tiles), 2 from about 5,000 nodes on; below 2,048 nodes the message gradient is split over 2 (4 up
+    # to 256 nodes) blocks per node, whose partial dh (E x 64), dn (E x 3) and dS maxima (N) follow,
+    # 256-byte aligned
+    tail = 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10
+    assert s.value == (tail + 63) // 64 * 64 + 4 * (20 * 67 + 10) and p.value == 20 * 18 * 64
     assert lib.fsc_sparse_conv_workspace(10000, 20, 64, ctypes.byref(s), ctypes.byref(p)) == 0
     assert s.value == 10000 * 18 * 65 * 64 + 2 * 18 * 10000 * 64 + 10000
     assert lib.fsc_sparse_conv_workspace(10, 20, 48, ctypes.byref(s), ctypes.byref(p)) == 1
@@ -74,7 +77,9 @@ def test_fake_kernels_trace_shapes():
         i = torch.empty(11, dtype=torch.int32)
         e = torch.empty(30, dtype=torch.int32)
         out, S, P = torch.ops.fsctep.sparse_conv(x, h, n, bk, bk, i, i, e, e, torch.empty(0, dtype=torch.int32))
-        assert out.shape == (10, 13, 64) and S.shape == (10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10,) and P.shape == (30 * 18 * 64,)
+        tail = 10 * 18 * 65 * 64 + 16 * 18 * 10 * 64 + 10
+        assert out.shape == (10, 13, 64) and S.shape == ((tail + 63) // 64 * 64 + 4 * (30 * 67 + 10),)
+        assert P.shape == (30 * 18 * 64,)
 
 
 def test_gram_sizes_and_fake_kernels():
