@@ -84,14 +84,15 @@ PRODUCTS = {
                "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "fp32 MFMA",
                "radial_mlp": "fp32 MFMA (first layer), split-fp16 (64-wide layers)",
                "receiver_sum, edge geometry, readout assembly": "fp32 VALU",
-               "gram_forward, gram_backward": "split-fp16", "MainNet, atom MLP": "torch fp32"},
+               "gram_forward, gram_backward": "split-fp16",
+               "readout_mlp (MainNet + weighted sum)": "fp32 MFMA", "atom MLP (species table)": "torch fp32"},
     "ictd": {"ictd_project, ictd_dual_project": "split-fp16 (main product), fp32 MFMA (coupling rows)",
              "ictd_project_grad": "split-fp16 (H = g x^T), fp32 MFMA (coupling rows, dY)",
              "ictd_mix, ictd_mix_grad": "split-fp16",
              "ictd_conv1, source_sum, edge geometry, harmonics, readout assembly": "fp32 VALU",
              "radial_mlp (gates)": "fp32 MFMA (first layer), split-fp16 (64-wide layers)",
              "gram_forward, gram_backward": "split-fp16",
-             "MainNet, atom MLP": "torch fp32"},
+             "readout_mlp (MainNet + weighted sum)": "fp32 MFMA", "atom MLP (species table)": "torch fp32"},
 }
 PRODUCTS["ictd-o3"] = PRODUCTS["ictd"]
 

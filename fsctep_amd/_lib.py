@@ -48,6 +48,10 @@ SIGNATURES = {
     "fsc_edge_harmonics_backward": [_p, _i64, _p, _p, _p, _p],
     "fsc_readout_gather": [_p, _i64, _p, _p, _p, _p, _p],
     "fsc_readout_scatter": [_p, _i64, _p, _p, _p, _p, _p, _p],
+    "fsc_readout_mlp_weights_floats": [_p, _pi64],
+    "fsc_readout_mlp_prepare": [_p, _p, _p, _p],
+    "fsc_readout_mlp_forward": [_p, _i64, _p, _p, _p, _p],
+    "fsc_readout_mlp_backward": [_p, _i64, _p, _p, _p, _p, _p],
     "fsc_radial_mlp_forward": [_i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p, _p],
     "fsc_radial_mlp_backward": [_i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p],
     "fsc_graph_sizes": [_i64, _i64, _i32, _pi64, _pi64],

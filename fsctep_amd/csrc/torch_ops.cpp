@@ -521,6 +521,100 @@ Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&
   return at::empty(t.sizes(), fopts(t));
 }
 
+// ============================================================== readout MLP (energy head)
+
+// dims = [K, H, NH, O], eps = [input LayerNorm eps, hidden LayerNorms' eps...]
+FscMlpDims mlp_dims(at::IntArrayRef dims, at::ArrayRef<double> eps) {
+  TORCH_CHECK(dims.size() == 4, "readout mlp dims must be [K, H, NH, O]");
+  FscMlpDims d{};
+  d.K = (int32_t)dims[0];
+  d.H = (int32_t)dims[1];
+  d.NH = (int32_t)dims[2];
+  d.O = (int32_t)dims[3];
+  TORCH_CHECK(d.NH >= 1 && d.NH <= 4 && (int64_t)eps.size() == d.NH + 1,
+              "readout mlp: 1 to 4 hidden layers and one LayerNorm eps per LayerNorm");
+  d.eps0 = (float)eps[0];
+  for (int l = 0; l < d.NH; ++l) d.eps[l] = (float)eps[l + 1];
+  return d;
+}
+
+int64_t mlp_weights_floats(const FscMlpDims& d) {
+  int64_t n = 0;
+  check(fsc_readout_mlp_weights_floats(&d, &n), "fsc_readout_mlp_weights_floats");
+  return n;
+}
+
+Tensor readout_mlp_prepare(at::TensorList params, at::IntArrayRef dims, at::ArrayRef<double> eps) {
+  const FscMlpDims d = mlp_dims(dims, eps);
+  TORCH_CHECK((int64_t)params.size() == 2 + 4 * d.NH + 3, "readout mlp: expected ", 2 + 4 * d.NH + 3, " parameters");
+  std::vector<Tensor> P;
+  std::vector<const float*> ptrs;
+  for (size_t i = 0; i < params.size(); ++i) {
+    require_gpu({params[i]});
+    P.push_back(f32c(params[i]));
+  }
+  // expected element counts: input LN, per layer (W, b, ln g, ln b), output (W, b), weighted-sum weights
+  std::vector<int64_t> want = {d.K, d.K};
+  for (int l = 0; l < d.NH; ++l) {
+    want.push_back((int64_t)d.H * (l == 0 ? d.K : d.H));
+    want.push_back(d.H);
+    want.push_back(d.H);
+    want.push_back(d.H);
+  }
+  want.push_back((int64_t)d.O * d.H);
+  want.push_back(d.O);
+  want.push_back(d.O);
+  for (size_t i = 0; i < P.size(); ++i) {
+    TORCH_CHECK(P[i].numel() == want[i], "readout mlp parameter ", i, " has ", P[i].numel(), " entries, expected ",
+                want[i]);
+    ptrs.push_back(cf(P[i]));
+  }
+  Tensor w = at::empty({mlp_weights_floats(d)}, fopts(P[0]));
+  check(fsc_readout_mlp_prepare(&d, ptrs.data(), mf(w), stream_of(P[0])), "fsc_readout_mlp_prepare");
+  return w;
+}
+
+Tensor readout_mlp_prepare_meta(at::TensorList params, at::IntArrayRef dims, at::ArrayRef<double> eps) {
+  return at::empty({mlp_weights_floats(mlp_dims(dims, eps))}, fopts(params[0]));
+}
+
+Tensor readout_mlp(const Tensor& x_, const Tensor& w, at::IntArrayRef dims, at::ArrayRef<double> eps) {
+  require_gpu({x_, w});
+  const FscMlpDims d = mlp_dims(dims, eps);
+  TORCH_CHECK(x_.dim() == 2 && x_.size(1) == d.K, "x must be (N, ", d.K, ")");
+  TORCH_CHECK(w.scalar_type() == at::kFloat && w.is_contiguous() && w.numel() == mlp_weights_floats(d),
+              "readout mlp weights do not match the dims (readout_mlp_prepare's output expected)");
+  Tensor x = f32c(x_);
+  const int64_t N = x.size(0);
+  Tensor e = at::empty({N, 1}, fopts(x));
+  check(fsc_readout_mlp_forward(&d, N, cf(x), cf(w), mf(e), stream_of(x)), "fsc_readout_mlp_forward");
+  return e;
+}
+
+Tensor readout_mlp_meta(const Tensor& x, const Tensor&, at::IntArrayRef, at::ArrayRef<double>) {
+  return at::empty({x.size(0), 1}, fopts(x));
+}
+
+Tensor readout_mlp_backward(const Tensor& grad_, const Tensor& x_, const Tensor& w, at::IntArrayRef dims,
+                            at::ArrayRef<double> eps) {
+  require_gpu({grad_, x_, w});
+  const FscMlpDims d = mlp_dims(dims, eps);
+  TORCH_CHECK(x_.dim() == 2 && x_.size(1) == d.K, "x must be (N, ", d.K, ")");
+  TORCH_CHECK(grad_.numel() == x_.size(0), "grad must hold one value per row of x");
+  TORCH_CHECK(w.scalar_type() == at::kFloat && w.is_contiguous() && w.numel() == mlp_weights_floats(d),
+              "readout mlp weights do not match the dims (readout_mlp_prepare's output expected)");
+  Tensor x = f32c(x_), g = f32c(grad_);
+  const int64_t N = x.size(0);
+  Tensor dx = at::empty({N, d.K}, fopts(x));
+  check(fsc_readout_mlp_backward(&d, N, cf(x), cf(w), cf(g), mf(dx), stream_of(x)), "fsc_readout_mlp_backward");
+  return dx;
+}
+
+Tensor readout_mlp_backward_meta(const Tensor&, const Tensor& x, const Tensor&, at::IntArrayRef,
+                                 at::ArrayRef<double>) {
+  return at::empty(x.sizes(), fopts(x));
+}
+
 // -------------------------------------------------------------- readout feature assembly
 
 // The layers as float32 contiguous [N][M][C] tensors (kept alive by the caller).
@@ -1361,6 +1455,37 @@ Tensor gram_bilinear_autograd(const Tensor& t, const Tensor& Wf, const Tensor& W
   return GramFn::apply(t, Wf, Wb, scale)[0];
 }
 
+// Energy head: input gradient only (the forward is recomputed by the backward kernel, nothing saved but x).
+struct ReadoutMlpFn : public torch::autograd::Function<ReadoutMlpFn> {
+  static variable_list forward(AutogradContext* ctx, Tensor x, Tensor w, std::vector<int64_t> dims,
+                               std::vector<double> eps) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, at::IntArrayRef, at::ArrayRef<double>)>(
+        "fsctep::readout_mlp");
+    Tensor e = op.call(x, w, dims, eps);
+    ctx->save_for_backward({x, w});
+    ctx->saved_data["dims"] = dims;
+    ctx->saved_data["eps"] = eps;
+    return {e};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    variable_list res(4);
+    if (!grads[0].defined()) return res;
+    refuse_param_grad(ctx, {1}, "the readout MLP (folded weights)");
+    auto s = ctx->get_saved_variables();
+    static auto op = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, at::IntArrayRef,
+                                      at::ArrayRef<double>)>("fsctep::readout_mlp_backward");
+    const std::vector<int64_t> dims = ctx->saved_data["dims"].toIntVector();
+    const std::vector<double> eps = ctx->saved_data["eps"].toDoubleVector();
+    res[0] = op.call(grads[0], s[0], s[1], dims, eps);
+    return res;
+  }
+};
+
+Tensor readout_mlp_autograd(const Tensor& x, const Tensor& w, at::IntArrayRef dims, at::ArrayRef<double> eps) {
+  return ReadoutMlpFn::apply(x, w, dims.vec(), eps.vec())[0];
+}
+
 // Readout features: the gradient w.r.t. the layers is one scatter kernel fed by the per-key Gram
 // backward and the squared-norm gradient (no per-slice zero fills or accumulations).
 struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
@@ -1601,6 +1726,9 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
   m.def("gram_bilinear(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
   m.def("gram_bilinear_backward(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
+  m.def("readout_mlp_prepare(Tensor[] params, int[] dims, float[] eps) -> Tensor");
+  m.def("readout_mlp(Tensor x, Tensor weights, int[] dims, float[] eps) -> Tensor");
+  m.def("readout_mlp_backward(Tensor grad, Tensor x, Tensor weights, int[] dims, float[] eps) -> Tensor");
   m.def("edge_geometry(Tensor pos, Tensor shift, Tensor edge_src, Tensor edge_dst, Tensor dst_ptr, Tensor src_ptr, "
         "Tensor src_perm) -> (Tensor, Tensor)");
   m.def("edge_geometry_backward(Tensor? grad_n, Tensor? grad_r, Tensor n, Tensor r, Tensor dst_ptr, Tensor src_ptr, "
@@ -1640,6 +1768,9 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("gram_prepare_weights", gram_prepare_weights);
   m.impl("gram_bilinear", gram_bilinear);
   m.impl("gram_bilinear_backward", gram_bilinear_backward);
+  m.impl("readout_mlp_prepare", readout_mlp_prepare);
+  m.impl("readout_mlp", readout_mlp);
+  m.impl("readout_mlp_backward", readout_mlp_backward);
   m.impl("edge_geometry", edge_geometry);
   m.impl("edge_geometry_backward", edge_geometry_backward);
   m.impl("radial_mlp", radial_mlp);
@@ -1674,6 +1805,9 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("gram_prepare_weights", gram_prepare_weights_meta);
   m.impl("gram_bilinear", gram_bilinear_meta);
   m.impl("gram_bilinear_backward", gram_bilinear_backward_meta);
+  m.impl("readout_mlp_prepare", readout_mlp_prepare_meta);
+  m.impl("readout_mlp", readout_mlp_meta);
+  m.impl("readout_mlp_backward", readout_mlp_backward_meta);
   m.impl("edge_geometry", edge_geometry_meta);
   m.impl("edge_geometry_backward", edge_geometry_backward_meta);
   m.impl("radial_mlp", radial_mlp_meta);
@@ -1695,6 +1829,7 @@ TORCH_LIBRARY_IMPL(fsctep, Autograd, m) {
   m.impl("ictd_conv", ictd_conv_autograd);
   m.impl("ictd_conv1", ictd_conv1_autograd);
   m.impl("gram_bilinear", gram_bilinear_autograd);
+  m.impl("readout_mlp", readout_mlp_autograd);
   m.impl("edge_geometry", edge_geometry_autograd);
   m.impl("radial_mlp", radial_mlp_autograd);
   m.impl("edge_harmonics", edge_harmonics_autograd);
@@ -1707,7 +1842,8 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "sparse_conv1", "sparse_conv1_backward", "sparse_conv_direction", "sparse_conv_direction_backward",
                            "ictd_prepare_weights", "ictd_conv",
                            "ictd_conv_backward", "ictd_project", "ictd_conv1", "ictd_conv1_backward", "gram_prepare_weights",
-                           "gram_bilinear", "gram_bilinear_backward", "edge_geometry", "edge_geometry_backward",
+                           "gram_bilinear", "gram_bilinear_backward", "readout_mlp_prepare", "readout_mlp",
+                           "readout_mlp_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                            "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
                            "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "neighbor_list"})

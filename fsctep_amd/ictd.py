@@ -24,7 +24,7 @@ from . import ictd_ops
 from .readout_ops import ReadoutMaps, prepare_gram, readout_features
 from .graph import Graph, poison_invalid, prepare_species_graph, species_rows
 from .ictd_basis import canonical, coupling, layout_full, layout_o3
-from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp
+from .sparse import MainNet, RobustScalarWeightedSum, _radial_mlp, readout_energy
 
 LMAX_KERNELS = 3     # (lmax + 1)^2 <= 16 harmonic components in the projection and conv1 kernels
 
@@ -306,7 +306,8 @@ class _ICTDTrunk(nn.Module):
             if k == (0, 1):
                 sq = torch.cat([sq, scalars * scalars], dim=-1)
             outs.append(sq * factors[i])
-        e = self.weighted_sum(self.proj_total(torch.cat(outs, dim=-1)))
+        f = torch.cat(outs, dim=-1)
+        e = self.weighted_sum(self.proj_total(f)) if train else readout_energy(self.proj_total, self.weighted_sum, f)
         dip = None
         if self._dipole and with_dipole:
             # the (1, -1) Gram input, (N, d, n*C), by the same column map (differentiable gather)

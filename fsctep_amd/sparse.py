@@ -73,6 +73,31 @@ class RobustScalarWeightedSum(nn.Module):
         return (x * self.weights).sum(dim=-1, keepdim=True)
 
 
+def readout_energy(net: MainNet, weighted_sum: RobustScalarWeightedSum, x: torch.Tensor) -> torch.Tensor:
+    """weighted_sum(net(x)), (N, 1), by the fused readout-head kernels (``torch.ops.fsctep.readout_mlp``:
+    one launch forward, one for the input gradient; no parameter gradients) where the head has their shape:
+    fp32 GPU input with K % 4 == 0, 1 to 4 hidden layers all 64, 128 or 256 wide, affine LayerNorms and
+    Linear biases.  Other heads run as the torch modules (reference models/mlp.py:8-66, :117-133)."""
+    hid = [lin.out_features for lin in net.layers]
+    norms = [net.input_norm, *net.layer_norms]
+    K = x.shape[-1] if x.dim() == 2 else -1
+    if not (x.is_cuda and x.dtype == torch.float32 and K % 4 == 0 and K >= 4 and 1 <= len(hid) <= 4
+            and hid[0] in (64, 128, 256) and all(h == hid[0] for h in hid)
+            and all(ln.weight is not None and ln.bias is not None and ln.weight.dim() == 1 for ln in norms)
+            and all(lin.bias is not None for lin in (*net.layers, net.output))
+            and weighted_sum.weights.numel() == net.output.out_features):
+        return weighted_sum(net(x))
+    dims = [K, hid[0], len(hid), net.output.out_features]
+    eps = [float(ln.eps) for ln in norms]
+    params = [net.input_norm.weight, net.input_norm.bias]
+    for lin, ln in zip(net.layers, net.layer_norms):
+        params += [lin.weight, lin.bias, ln.weight, ln.bias]
+    params += [net.output.weight, net.output.bias, weighted_sum.weights]
+    with torch.no_grad():
+        w = torch.ops.fsctep.readout_mlp_prepare([p.detach() for p in params], dims, eps)
+    return torch.ops.fsctep.readout_mlp(x, w, dims, eps)
+
+
 def _radial_mlp(hidden_out: int, nb: int) -> nn.Sequential:
     return nn.Sequential(nn.Linear(nb, 64), nn.SiLU(), nn.Linear(64, 64), nn.SiLU(), nn.Linear(64, hidden_out))
 
@@ -318,7 +343,9 @@ class PureCartesianSparseTransformerLayer(nn.Module):
         # invariants in the reference order: layer-major, then rank L
         invs = (sq.view(-1, len(_COMPS), nL, self.channels) * self._readout_cache[skey]).transpose(1, 2)
         f5 = torch.cat([invs.flatten(1), f3 * f3], dim=-1)
-        return self.weighted_sum(self.proj_total(f5))
+        if train:
+            return self.weighted_sum(self.proj_total(f5))
+        return readout_energy(self.proj_total, self.weighted_sum, f5)
 
 
 def energy_and_forces(model: PureCartesianSparseTransformerLayer, pos, batch, cell, graph: Graph):

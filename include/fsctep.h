@@ -465,6 +465,37 @@ int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const flo
                         const float* grad_sq, const float* const* layers, const int32_t* gmap,
                         float* const* grad_layers, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Readout head of the energy, per atom: input LayerNorm, NH hidden layers of Linear -> LayerNorm ->
+ * SiLU (all H wide), the output Linear to O values and their weighted sum:
+ *   e[n] = w . (Wout a_NH(x[n]) + bout).
+ * Replaces MainNet.forward (models/mlp.py:8-66) followed by RobustScalarWeightedSum.forward
+ * (models/mlp.py:117-133), the energy head of every trunk (e.g.
+ * models/pure_cartesian_sparse_layers.py:831-833: weighted_sum(proj_total(f))), and their input
+ * gradient.  x [N][K] (K a multiple of 4), H 64, 128 or 256, 1 <= NH <= 4; fp32 products.
+ * fsc_readout_mlp_prepare folds the module parameters into one buffer of
+ * fsc_readout_mlp_weights_floats floats (opaque to the caller; x, that buffer and grad_x 16-byte
+ * aligned).  params is a host array of 2 + 4 NH + 3 device pointers:
+ *   input LayerNorm weight [K], bias [K];
+ *   per hidden layer l: Linear weight [H][K or H], bias [H], LayerNorm weight [H], bias [H];
+ *   output Linear weight [O][H], bias [O]; the weighted sum's weights [O].
+ * eps0 / eps[l]: the LayerNorms' eps.  The backward writes grad_x[n] = grad_energy[n] de[n]/dx[n]
+ * (the forward recomputed; no parameter gradients).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct FscMlpDims {
+  int32_t K, H, NH, O;
+  float eps0;
+  float eps[4];
+} FscMlpDims;
+int fsc_readout_mlp_weights_floats(const FscMlpDims* dims, int64_t* floats);
+int fsc_readout_mlp_prepare(const FscMlpDims* dims, const float* const* params, float* weights, hipStream_t stream);
+/* energy [N] */
+int fsc_readout_mlp_forward(const FscMlpDims* dims, int64_t n_atoms, const float* x, const float* weights,
+                            float* energy, hipStream_t stream);
+/* grad_energy [N] in, grad_x [N][K] out */
+int fsc_readout_mlp_backward(const FscMlpDims* dims, int64_t n_atoms, const float* x, const float* weights,
+                             const float* grad_energy, float* grad_x, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,3 +96,37 @@ def test_gram_sizes_and_fake_kernels():
         assert Wf.shape == Wb.shape == (78 * 256 * 64 * 2 + 512,)
         out = torch.ops.fsctep.gram_bilinear(torch.empty(7, 9, 192), Wf, Wb, 1.0)
         assert out.shape == (7, 64)
+
+
+def test_readout_mlp_sizes_errors_and_fake_kernels():
+    """Folded-weight buffer of the readout head: W1 diag(g0) and its transpose (2 H K), c1 and u1 (2 H), the
+    hidden LayerNorms (2 H each), the H x H layers and their transposes with biases, v (H) and e0 (4)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from fsctep_amd import ops  # noqa: F401
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("K", ctypes.c_int32), ("H", ctypes.c_int32), ("NH", ctypes.c_int32), ("O", ctypes.c_int32),
+                    ("eps0", ctypes.c_float), ("eps", ctypes.c_float * 4)]
+
+    lib = _lib.load()
+    n = ctypes.c_int64()
+    d = Dims(1600, 128, 3, 17, 1e-5, (ctypes.c_float * 4)(1e-5, 1e-5, 1e-5, 0.0))
+    assert lib.fsc_readout_mlp_weights_floats(ctypes.byref(d), ctypes.byref(n)) == 0
+    H, K = 128, 1600
+    assert n.value == 2 * H * K + 2 * H + 3 * 2 * H + 2 * (2 * H * H + H) + H + 4
+    for bad, msg in ((Dims(1602, 128, 3, 17, 1e-5), b"multiple of 4"), (Dims(640, 96, 3, 17, 1e-5), b"hidden width"),
+                     (Dims(640, 128, 5, 17, 1e-5), b"hidden layers")):
+        bad.eps = (ctypes.c_float * 4)(1e-5, 1e-5, 1e-5, 1e-5)
+        assert lib.fsc_readout_mlp_weights_floats(ctypes.byref(bad), ctypes.byref(n)) == 1
+        assert msg in lib.fsc_last_error()
+    with FakeTensorMode():
+        K, H = 640, 64
+        ps = [torch.empty(K), torch.empty(K), torch.empty(H, K), torch.empty(H), torch.empty(H), torch.empty(H),
+              torch.empty(H, H), torch.empty(H), torch.empty(H), torch.empty(H), torch.empty(17, H), torch.empty(17),
+              torch.empty(17)]
+        w = torch.ops.fsctep.readout_mlp_prepare(ps, [K, H, 2, 17], [1e-5] * 3)
+        assert w.shape == (2 * H * K + 2 * H + 2 * 2 * H + (2 * H * H + H) + H + 4,)
+        e = torch.ops.fsctep.readout_mlp(torch.empty(9, K), w, [K, H, 2, 17], [1e-5] * 3)
+        assert e.shape == (9, 1)
+        dx = torch.ops.fsctep.readout_mlp_backward(torch.empty(9, 1), torch.empty(9, K), w, [K, H, 2, 17], [1e-5] * 3)
+        assert dx.shape == (9, K)

@@ -19,7 +19,7 @@ OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_
        "edge_geometry_backward", "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
        "readout_gather", "readout_scatter", "readout_features", "graph_prepare", "edge_vec_geometry",
        "edge_vec_geometry_backward", "spatial_order", "ictd_project", "sparse_conv_direction",
-       "sparse_conv_direction_backward",
+       "sparse_conv_direction_backward", "readout_mlp_prepare", "readout_mlp", "readout_mlp_backward",
        # the per-edge (bucketed) ICTD ops under the reference extension's names (csrc/ictd_tp.cpp:498-521)
        "project_bucket_forward", "project_bucket_transpose_a", "project_bucket_transpose_b",
        "project_bucket_transpose_u", "mix_bucket_forward", "mix_bucket_transpose_y", "mix_bucket_transpose_w",
@@ -43,7 +43,7 @@ def test_schemas_registered_in_cpp():
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "CUDA")
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"fsctep::{name}", "Meta")
     for name in ("sparse_conv", "sparse_conv1", "ictd_conv", "ictd_conv1", "gram_bilinear", "readout_features",
-                 "edge_geometry", "edge_vec_geometry", "radial_mlp", "edge_harmonics"):
+                 "edge_geometry", "edge_vec_geometry", "radial_mlp", "edge_harmonics", "readout_mlp"):
         assert torch._C._dispatch_has_computed_kernel_for_dispatch_key(f"fsctep::{name}", "AutogradCUDA")
 
 
