@@ -276,10 +276,17 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
 // weight planes ([jl][il/8][o][il%8]: the 32 lanes of a K half read 512 contiguous bytes) are staged
 // in LDS and shared by the 8 waves; the next pair's planes are loaded a quarter at a time after each
 // group's t loads, so waiting for those never waits for the weights (one in-order load counter).
+// DL (D >= 5): the next pair's planes go straight from global memory into a second LDS buffer
+// (direct-to-LDS loads, a quarter after each group's t loads) instead of through 32 registers, which the
+// larger D need for their t operands (at D 9 the register copy spilled); the 128 KB of LDS leave one
+// workgroup per CU, the occupancy those D have anyway (D 9: 0.274 -> 0.264 ms, D 7 0.704 -> 0.689 ms at
+// 10k nodes; at D 3 it measured no faster).
 constexpr int NODES_BF = 256;
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(1))) void gram_global_void;
+typedef __attribute__((address_space(3))) void gram_lds_void;
 
-template <int D, int S, int TSB>
+template <int D, int S, int TSB, bool DL = false>
 __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, float scale,
                                                           const float* __restrict__ t,
                                                           const _Float16* __restrict__ Wf2,
@@ -291,7 +298,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   constexpr int PW = 2 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
   constexpr int PWQ = (PW + 3) / 4;
   static_assert((2 * PSZ / 8) % 512 == 0, "staging");
-  __shared__ __align__(16) _Float16 wl[2 * PSZ];
+  __shared__ __align__(16) _Float16 wlb[DL ? 2 : 1][2 * PSZ];
   const int nb = nC / 16, np = n_pairs(nb);
   const int ntiles = (int)((N + NN - 1) / NN);
   const int logical = xcd_logical(nchunks * ntiles);
@@ -315,13 +322,21 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
     for (int v = 0; v < 16; ++v) acc[ct][v] = 0.f;
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
   const int64_t plane = (int64_t)np * PSZ;
-  f4 pw[PW];
+  f4 pw[DL ? 1 : PW];
+  int buf = 0;
   auto fetch_part = [&](int p, int k) {
 #pragma unroll
     for (int i = k * PWQ; i < min(PW, (k + 1) * PWQ); ++i) {
       const int idx = threadIdx.x + 512 * i;
       const int pl = idx / (PSZ / 8), rem = idx - pl * (PSZ / 8);
-      pw[i] = *reinterpret_cast<const f4*>(Wf2 + pl * plane + (int64_t)p * PSZ + 8 * rem);
+      const _Float16* src = Wf2 + pl * plane + (int64_t)p * PSZ + 8 * rem;
+      if constexpr (DL) {
+        // lane l of the wave lands at the wave's base + 16 l: piece idx at 16 idx bytes, as below
+        __builtin_amdgcn_global_load_lds((gram_global_void*)src,
+                                         (gram_lds_void*)(&wlb[buf ^ 1][8 * (512 * i + 64 * wave)]), 16, 0, 0);
+      } else {
+        pw[i] = *reinterpret_cast<const f4*>(src);
+      }
     }
   };
   // t[n][m][I0 + 8q + j] times the node's power of two (exact), so the Gram values come out scaled
@@ -342,14 +357,22 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   };
   load_tc(I);
   load_ts(0, J, 0);
+  buf = 1;   // DL: the first pair goes to buffer 0
 #pragma unroll
   for (int k = 0; k < 4; ++k) fetch_part(p0, k);
-  const _Float16* wp = wl + q * S * 8 + r * 8;
+  buf = 0;
   for (int p = p0; p < p1; ++p) {
-    __syncthreads();
+    if constexpr (DL) {
+      __builtin_amdgcn_s_waitcnt(0);   // this pair's planes (direct-to-LDS loads are not tracked otherwise)
+      __syncthreads();
+    } else {
+      __syncthreads();
 #pragma unroll
-    for (int i = 0; i < PW; ++i) reinterpret_cast<f4*>(wl)[threadIdx.x + 512 * i] = pw[i];
-    __syncthreads();
+      for (int i = 0; i < PW; ++i) reinterpret_cast<f4*>(wlb[0])[threadIdx.x + 512 * i] = pw[i];
+      __syncthreads();
+    }
+    const _Float16* wl = wlb[DL ? buf : 0];
+    const _Float16* wp = wl + q * S * 8 + r * 8;
     const bool more = p + 1 < p1;
     int In = I, Jn = J + 1;
     if (Jn == nb) { ++In; Jn = In; }
@@ -398,6 +421,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
     if (more && In != I) load_tc(In);
     I = In;
     J = Jn;
+    if constexpr (DL) buf ^= 1;
   }
   // result register v of lane (r, q) is node 8 (v / 4) + 4 q + v % 4 of the wave, output column r
   const float f = scale * winv[0];
@@ -645,7 +669,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
     LaunchTimer tm("gram_forward", st);
 #define FSC_GF(DD)                                                                                 \
   if (bf)                                                                                          \
-    forward_h16_kernel<DD, S, 1><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, part, tg); \
+    forward_h16_kernel<DD, S, 1, (DD >= 5)><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, part, tg); \
   else                                                                                             \
     forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part, pchunk)
     switch (D) {
