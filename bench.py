@@ -81,7 +81,7 @@ WORKLOADS = {
 # operand, six of the nine part products on bf16 MFMA (the dropped ones are below 2^-23 |ab|).
 PRODUCTS = {
     "sparse": {"node_expand": "split-fp16", "node_expand_grad": "split-fp16", "edge_message": "split-bf16",
-               "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "fp32 MFMA",
+               "edge_message_grad": "split-fp16", "conv1 pair GEMMs": "split-fp16 (forward), fp32 MFMA (gradient)",
                "radial_mlp": "fp32 MFMA (first layer), split-fp16 (64-wide layers)",
                "receiver_sum, edge geometry, readout assembly": "fp32 VALU",
                "gram_forward, gram_backward": "split-fp16",

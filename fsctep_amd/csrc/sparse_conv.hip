@@ -1534,6 +1534,28 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4) hb[u][t4] = ld4(h + (int64_t)eld * KH + 16 * t4 + 4 * q);
   }
+  // Split-fp16 products (16x16x32 f16, K = 64 in two steps; K step ks takes the lane's k = 16 t4 + 4q + j
+  // for t4 = 2 ks, 2 ks + 1, the same set in both operands): each edge's h row scaled by a power of two
+  // from its own max (the four lanes of a row reduce it), each table row likewise, both undone on the result.
+  h8 bh[C1_TPW][2], bl[C1_TPW][2];
+  float se[C1_TPW];
+#pragma unroll
+  for (int u = 0; u < C1_TPW; ++u) {
+    float mx = 0.f;
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(hb[u][t4].x), fabsf(hb[u][t4].y)), fmaxf(fabsf(hb[u][t4].z), fabsf(hb[u][t4].w))));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float sc = pow2_scale(mx);
+    se[u] = 1.f / sc;   // a power of two: exact
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const f4 x0 = hb[u][2 * ks], x1 = hb[u][2 * ks + 1];
+      const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      split2h(v, sc, bh[u][ks], bl[u][ks]);
+    }
+  }
   auto tile_rows = [&](int pair, int u0, int u1) {   // tiles u0..u1-1 against the table of `pair`
     const float* mp = mb + (int64_t)pair * 3 * C * MB_STRIDE;
     const float* fp = mf + (int64_t)pair * 3 * 65 * C;
@@ -1544,13 +1566,30 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
       for (int t4 = 0; t4 < 4; ++t4) a[t4] = ld4(mp + (int64_t)(16 * rt + r) * MB_STRIDE + 16 * t4 + 4 * q);
       const int row = 16 * rt + 4 * q;   // first of the lane's four (p, c) outputs
       const f4 bias = ld4(fp + (row / C) * 65 * C + 64 * C + row % C);
+      float mx = 0.f;
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a[t4].x), fabsf(a[t4].y)), fmaxf(fabsf(a[t4].z), fabsf(a[t4].w))));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float sr = pow2_scale(mx);   // table row 16 rt + r
+      h8 ah[2], al[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const f4 x0 = a[2 * ks], x1 = a[2 * ks + 1];
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        split2h(v, sr, ah[ks], al[ks]);
+      }
+      f4 rinv;   // 1 / scale of the lane's output rows 4q + j
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rinv[j] = 1.f / __shfl(sr, 4 * q + j, 64);
 #pragma unroll
       for (int u = 0; u < C1_TPW; ++u) {
         if (u < u0 || u >= u1) continue;
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) acc = mfma_k16(a[t4], hb[u][t4], acc);
-        if (e[u] >= 0) st4(Q + (int64_t)e[u] * 3 * C + row, acc + bias);
+        for (int ks = 0; ks < 2; ++ks) acc = mfma_x3(ah[ks], al[ks], bh[u][ks], bl[u][ks], acc);
+        if (e[u] >= 0) st4(Q + (int64_t)e[u] * 3 * C + row, acc * rinv * se[u] + bias);
       }
     }
   };
