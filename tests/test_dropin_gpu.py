@@ -99,3 +99,28 @@ def test_ictd_precomputed_edge_vec(name):
     (gpos,) = torch.autograd.grad(e.sum(), pos)
     assert rel_inf(e.detach().squeeze(-1), g["energy_f64"]) < TOL
     assert rel_inf(-gpos, g["forces_f64"]) < TOL
+
+
+@pytest.mark.parametrize("name", ["sparse_open32_c32_l2", "ictd_pbc64_c128_l3"])
+def test_float64_inputs(name):
+    """Inputs in float64 (the reference's default dtype, utils/config.py:16): the energies are those of the
+    float32 inputs (the trunk computes in fp32) and the forces come back in float64."""
+    g = load_golden(name)
+    m = _ictd_model(g) if name.startswith("ictd") else seeded_hip_model(
+        int(g["channels"]), int(g["layers"]), int(g["param_seed"])).to(DEV)
+    n = g["pos"].shape[0]
+    A = torch.tensor(g["species"], device=DEV)
+    batch = torch.zeros(n, dtype=torch.long, device=DEV)
+    src, dst = torch.tensor(g["edge_src"], device=DEV), torch.tensor(g["edge_dst"], device=DEV)
+    out = {}
+    for dt in (torch.float32, torch.float64):
+        pos = torch.tensor(g["pos"], dtype=dt, device=DEV).requires_grad_(True)
+        sh = torch.tensor(g["edge_shifts"], dtype=dt, device=DEV)
+        cell = torch.tensor(g["cell"], dtype=dt, device=DEV).reshape(-1, 3, 3)
+        e = m(pos, A, batch, src, dst, sh, cell)
+        (f,) = torch.autograd.grad(e.sum(), pos)
+        out[dt] = (e.detach(), -f)
+    e32, f32 = out[torch.float32]
+    e64, f64 = out[torch.float64]
+    assert e64.dtype == torch.float32 and f64.dtype == torch.float64
+    assert rel_inf(e64, e32) < 1e-6 and rel_inf(f64, f32) < 1e-5
