@@ -1504,8 +1504,11 @@ __global__ __launch_bounds__(256) void conv1_pair_table_kernel(const float* __re
 // pair) each table row block is loaded once for all of them (the table is 48 KB per pair at C 64, which
 // one-tile waves re-read from L2 for every 16 edges).
 constexpr int C1_TPW = 4;
+// Below this many tiles a wave takes one tile (more, shorter waves: at 1,000 atoms there are about 3,300
+// tiles, 820 waves of four).
+constexpr int64_t C1_SMALL_TILES = 16384;
 
-template <int C>
+template <int C, int TPW>
 __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __restrict__ h,
                                                               const float* __restrict__ mf,
                                                               const float* __restrict__ mb,
@@ -1514,16 +1517,16 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   constexpr int NRT = 3 * C / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
+  const int t0 = (blockIdx.x * 4 + wave) * TPW;
   if (t0 >= n_tiles || pair_tiles[16 * (int64_t)t0] < 0) return;   // whole wave (unused tiles are at the end)
-  const int nt = min(C1_TPW, n_tiles - t0);
+  const int nt = min(TPW, n_tiles - t0);
   const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
-  int32_t e[C1_TPW];
-  bool used[C1_TPW];
-  f4 hb[C1_TPW][4];
+  int32_t e[TPW];
+  bool used[TPW];
+  f4 hb[TPW][4];
   bool same = true;
 #pragma unroll
-  for (int u = 0; u < C1_TPW; ++u) {
+  for (int u = 0; u < TPW; ++u) {
     const int t = t0 + min(u, nt - 1);
     const int32_t first = pair_tiles[16 * t];
     used[u] = u < nt && first >= 0;
@@ -1537,10 +1540,10 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
   // Split-fp16 products (16x16x32 f16, K = 64 in two steps; K step ks takes the lane's k = 16 t4 + 4q + j
   // for t4 = 2 ks, 2 ks + 1, the same set in both operands): each edge's h row scaled by a power of two
   // from its own max (the four lanes of a row reduce it), each table row likewise, both undone on the result.
-  h8 bh[C1_TPW][2], bl[C1_TPW][2];
-  float se[C1_TPW];
+  h8 bh[TPW][2], bl[TPW][2];
+  float se[TPW];
 #pragma unroll
-  for (int u = 0; u < C1_TPW; ++u) {
+  for (int u = 0; u < TPW; ++u) {
     float mx = 0.f;
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4)
@@ -1584,7 +1587,7 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
 #pragma unroll
       for (int j = 0; j < 4; ++j) rinv[j] = 1.f / __shfl(sr, 4 * q + j, 64);
 #pragma unroll
-      for (int u = 0; u < C1_TPW; ++u) {
+      for (int u = 0; u < TPW; ++u) {
         if (u < u0 || u >= u1) continue;
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1594,10 +1597,10 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_kernel(const float* __res
     }
   };
   if (same) {   // wave-uniform
-    tile_rows(tpair[t0], 0, C1_TPW);
+    tile_rows(tpair[t0], 0, TPW);
   } else {
 #pragma unroll
-    for (int u = 0; u < C1_TPW; ++u)
+    for (int u = 0; u < TPW; ++u)
       if (used[u]) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
@@ -1709,23 +1712,23 @@ __global__ __launch_bounds__(256) void conv1_receiver_grad_kernel(const float* _
 // dh[e][k] = sum_{p,c} dQ[e][p][c] mf[pair][p][k][c] for C1_TPW consecutive 16-edge tiles per wave
 // (one table load for all of them when they share a pair, as in the forward); transposed product
 // (table rows k are the A operand), lane (r, q) ends with four consecutive k of edge r per k tile.
-template <int C>
+template <int C, int TPW>
 __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* __restrict__ dQ,
                                                                    const float* __restrict__ mf,
                                                                    const int32_t* __restrict__ pair_tiles,
                                                                    int n_tiles, float* __restrict__ dh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int t0 = (blockIdx.x * 4 + wave) * C1_TPW;
+  const int t0 = (blockIdx.x * 4 + wave) * TPW;
   if (t0 >= n_tiles || pair_tiles[16 * (int64_t)t0] < 0) return;   // whole wave (unused tiles are at the end)
-  const int nt = min(C1_TPW, n_tiles - t0);
+  const int nt = min(TPW, n_tiles - t0);
   const int32_t* tpair = pair_tiles + 16 * (int64_t)n_tiles;
-  int32_t e[C1_TPW];
-  bool used[C1_TPW];
-  const float* dq[C1_TPW];
+  int32_t e[TPW];
+  bool used[TPW];
+  const float* dq[TPW];
   bool same = true;
 #pragma unroll
-  for (int u = 0; u < C1_TPW; ++u) {
+  for (int u = 0; u < TPW; ++u) {
     const int t = t0 + min(u, nt - 1);
     const int32_t first = pair_tiles[16 * t];
     used[u] = u < nt && first >= 0;
@@ -1737,9 +1740,9 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
   }
   auto tile_rows = [&](int pair, int u0, int u1) {   // tiles u0..u1-1 against the table of `pair`
     const float* fp = mf + (int64_t)pair * 3 * 65 * C;
-    f4 acc[C1_TPW][4];
+    f4 acc[TPW][4];
 #pragma unroll
-    for (int u = 0; u < C1_TPW; ++u)
+    for (int u = 0; u < TPW; ++u)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) acc[u][kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
@@ -1749,7 +1752,7 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) a[kt] = ld4(fp + (int64_t)(p * 65 + 16 * kt + r) * C + c0 + 4 * q);
 #pragma unroll
-      for (int u = 0; u < C1_TPW; ++u) {
+      for (int u = 0; u < TPW; ++u) {
         if (u < u0 || u >= u1) continue;
         const f4 b = ld4(dq[u] + p * C + c0);
 #pragma unroll
@@ -1757,17 +1760,17 @@ __global__ __launch_bounds__(256) void conv1_pair_gemm_grad_kernel(const float* 
       }
     }
 #pragma unroll
-    for (int u = 0; u < C1_TPW; ++u) {
+    for (int u = 0; u < TPW; ++u) {
       if (u < u0 || u >= u1 || e[u] < 0) continue;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) st4(dh + (int64_t)e[u] * KH + 16 * kt + 4 * q, acc[u][kt]);
     }
   };
   if (same) {   // wave-uniform
-    tile_rows(tpair[t0], 0, C1_TPW);
+    tile_rows(tpair[t0], 0, TPW);
   } else {
 #pragma unroll
-    for (int u = 0; u < C1_TPW; ++u)
+    for (int u = 0; u < TPW; ++u)
       if (used[u]) tile_rows(tpair[t0 + u], u, u + 1);
   }
 }
@@ -2025,17 +2028,24 @@ int fsc_sparse_conv1_forward(int64_t n_nodes, int64_t n_edges, int32_t channels,
   FSC_CHECK_ARG(n_edges == 0 || (pair_tiles && h && n && q_ws), "fsc_sparse_conv1_forward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_forward", stream);
-  const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
+  const int tpw = n_tiles >= C1_SMALL_TILES ? C1_TPW : 1;
+  const unsigned tgrid = (unsigned)((n_tiles + 4 * tpw - 1) / (4 * tpw)), ngrid = (unsigned)((n_nodes + 3) / 4);
+#define FSC_C1F(CC)                                                                                       \
+  if (n_tiles) {                                                                                          \
+    if (tpw == 1)                                                                                         \
+      conv1_pair_gemm_kernel<CC, 1><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws); \
+    else                                                                                                  \
+      conv1_pair_gemm_kernel<CC, C1_TPW><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws); \
+  }                                                                                                       \
+  conv1_receiver_kernel<CC><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
   if (channels == 128) {
-    if (n_tiles) conv1_pair_gemm_kernel<128><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
-    conv1_receiver_kernel<128><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
+    FSC_C1F(128)
   } else if (channels == 64) {
-    if (n_tiles) conv1_pair_gemm_kernel<64><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
-    conv1_receiver_kernel<64><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
+    FSC_C1F(64)
   } else {
-    if (n_tiles) conv1_pair_gemm_kernel<32><<<tgrid, 256, 0, stream>>>(h, mf, mb, pair_tiles, (int)n_tiles, q_ws);
-    conv1_receiver_kernel<32><<<ngrid, 256, 0, stream>>>(q_ws, n, dst_ptr, out, n_nodes);
+    FSC_C1F(32)
   }
+#undef FSC_C1F
   return check_launch("sparse conv1_forward") ? 2 : 0;
 }
 
@@ -2053,17 +2063,24 @@ int fsc_sparse_conv1_backward(int64_t n_nodes, int64_t n_edges, int32_t channels
                 "fsc_sparse_conv1_backward: null edge pointer");
   if (n_nodes == 0) return 0;
   LaunchTimer tm("conv1_backward", stream);
-  const unsigned tgrid = (unsigned)((n_tiles + 4 * C1_TPW - 1) / (4 * C1_TPW)), ngrid = (unsigned)((n_nodes + 3) / 4);
-  if (channels == 128) {
-    conv1_receiver_grad_kernel<128><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
-    if (n_tiles) conv1_pair_gemm_grad_kernel<128><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
-  } else if (channels == 64) {
-    conv1_receiver_grad_kernel<64><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
-    if (n_tiles) conv1_pair_gemm_grad_kernel<64><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
-  } else {
-    conv1_receiver_grad_kernel<32><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes);
-    if (n_tiles) conv1_pair_gemm_grad_kernel<32><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h);
+  const int tpw = n_tiles >= C1_SMALL_TILES ? C1_TPW : 1;
+  const unsigned tgrid = (unsigned)((n_tiles + 4 * tpw - 1) / (4 * tpw)), ngrid = (unsigned)((n_nodes + 3) / 4);
+#define FSC_C1B(CC)                                                                                          \
+  conv1_receiver_grad_kernel<CC><<<ngrid, 256, 0, stream>>>(grad_out, n, q_ws, dst_ptr, dq_ws, grad_n, n_nodes); \
+  if (n_tiles) {                                                                                             \
+    if (tpw == 1)                                                                                            \
+      conv1_pair_gemm_grad_kernel<CC, 1><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h); \
+    else                                                                                                     \
+      conv1_pair_gemm_grad_kernel<CC, C1_TPW><<<tgrid, 256, 0, stream>>>(dq_ws, mf, pair_tiles, (int)n_tiles, grad_h); \
   }
+  if (channels == 128) {
+    FSC_C1B(128)
+  } else if (channels == 64) {
+    FSC_C1B(64)
+  } else {
+    FSC_C1B(32)
+  }
+#undef FSC_C1B
   return check_launch("sparse conv1_backward") ? 2 : 0;
 }
 
