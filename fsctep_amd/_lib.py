@@ -42,11 +42,14 @@ SIGNATURES = {
     "fsc_gram_prepare_weights": [_p, _i32, _i32, _p, _p, _p],
     "fsc_gram_forward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
     "fsc_gram_backward": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
+    "fsc_gram_forward_blocked": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
+    "fsc_gram_backward_blocked": [_i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
     "fsc_edge_geometry_forward": [_i64, _p, _p, _p, _p, _p, _p, _p],
     "fsc_edge_geometry_backward": [_i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "fsc_edge_harmonics_forward": [_p, _i64, _p, _p, _p],
     "fsc_edge_harmonics_backward": [_p, _i64, _p, _p, _p, _p],
     "fsc_readout_gather": [_p, _i64, _p, _p, _p, _p, _p],
+    "fsc_readout_gather_blocked": [_p, _i64, _p, _p, _p, _p, _p],
     "fsc_readout_scatter": [_p, _i64, _p, _p, _p, _p, _p, _p],
     "fsc_readout_mlp_weights_floats": [_p, _pi64],
     "fsc_readout_mlp_prepare": [_p, _p, _p, _p],

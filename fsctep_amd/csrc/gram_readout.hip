@@ -18,7 +18,11 @@
 //   dt[n][m][i] = scale * sum_j A_n[i][j] t[n][m][j],   A_n = sum_o g[n][o] (W[o] + W[o]^T),
 // computed per (node tile, row block I) over all J with A formed by MFMA (K = o) and contracted
 // with t on the VALU; (W + W^T) is stored for I <= J (Wb[IJ][a][b][o]) and read transposed below
-// the diagonal.  Layouts: t [N][D][nC], W [S][nC][nC], out/grad_out [N][S].
+// the diagonal.  Layouts: t [N][D][nC] or, in the blocked entry points, quad-major [nC/4][D][N][4] (the four
+// channels 4c..4c+3 of component m of node n at ((c D + m) N + n) 4: the lanes of a wave, which are
+// consecutive nodes, read consecutive 16-byte pieces instead of one piece from each node's row, which left
+// the vector memory pipe the bound: the readout gather writes this order directly); W [S][nC][nC],
+// out/grad_out [N][S]; grad_t is always [N][D][nC].
 
 #include "common.h"
 #include "fsctep.h"
@@ -30,6 +34,14 @@ constexpr int NODES = 128;   // nodes per workgroup (8 waves x 16 MFMA rows)
 constexpr int PCHUNK = 8;    // block pairs per forward workgroup
 
 __host__ __device__ inline int n_pairs(int nb) { return nb * (nb + 1) / 2; }
+
+// The four channels i..i+3 (i % 4 == 0) of component m of node n.
+template <bool BLK>
+__device__ __forceinline__ const float* tq4(const float* __restrict__ t, int64_t N, int D, int nC, int64_t n, int m,
+                                            int i) {
+  if constexpr (BLK) return t + (((int64_t)(i >> 2) * D + m) * N + n) * 4;
+  else return t + (n * D + m) * nC + i;
+}
 __host__ __device__ inline int pair_index(int I, int J, int nb) { return I * nb - (I * (I - 1)) / 2 + (J - I); }
 
 // Workgroup w runs on XCD w % 8; give each XCD a contiguous range of logical tiles so tiles that
@@ -164,13 +176,12 @@ __global__ __launch_bounds__(256) void node_scale_kernel(int64_t N, int D, int n
   float mx = 0.f;
   if ((nC & 3) == 0 && D <= 9 && (reinterpret_cast<uintptr_t>(t) & 15) == 0) {
     // four columns per lane, all D rows requested before the sums (same sums, same order per column)
-    const f4* t4 = reinterpret_cast<const f4*>(tn);
     const int nq = nC >> 2;
     for (int c = lane; c < nq; c += 64) {
       f4 v[9];
 #pragma unroll
       for (int m = 0; m < 9; ++m)
-        if (m < D) v[m] = t4[m * nq + c];
+        if (m < D) v[m] = ld4(tq4<false>(t, N, D, nC, n, m, 4 * c));
       f4 s = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 9; ++m)
@@ -191,10 +202,41 @@ __global__ __launch_bounds__(256) void node_scale_kernel(int64_t N, int D, int n
   if (lane == 0) nsc[n] = pow2_scale(mx);
 }
 
+// The same scales from the blocked order: a lane per node (64 consecutive nodes per workgroup, each
+// (quad, component) read is one contiguous 1 KB piece per wave), the 8 waves take every 8th quad and
+// combine their maxima in LDS.
+__global__ __launch_bounds__(512) void node_scale_blocked_kernel(int64_t N, int D, int nC,
+                                                                 const float* __restrict__ t,
+                                                                 float* __restrict__ nsc) {
+  __shared__ float red[8][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t nl = n < N ? n : N - 1;   // lanes past N repeat the last node (not stored)
+  float mx = 0.f;
+  for (int c = wave; c < (nC >> 2); c += 8) {
+    f4 v[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m)
+      if (m < D) v[m] = ld4(tq4<true>(t, N, D, nC, nl, m, 4 * c));
+    f4 s = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 9; ++m)
+      if (m < D) s += v[m] * v[m];
+    mx = fmaxf(mx, fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  }
+  red[wave][lane] = mx;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < 8; ++w) mx = fmaxf(mx, red[w][lane]);
+    if (n < N) nsc[n] = pow2_scale(mx);
+  }
+}
+
 // Forward partial sums over pchunk block pairs: part[chunk][n][o].  A workgroup is 128 nodes (8 waves x
 // 16 MFMA rows) x one chunk; each pair's Wf block [il][o][jl] (256*S floats) is staged in LDS and shared
 // by the 8 waves, the next pair's block is loaded into registers while the current one is multiplied.
-template <int D, int S>
+template <int D, int S, bool BLK>
 __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float scale, const float* __restrict__ t,
                                            const float* __restrict__ Wf, int nchunks, float* __restrict__ part,
                                            int pchunk) {
@@ -211,7 +253,7 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
   const int r = lane & 15, q = lane >> 4;
   const int64_t n = (int64_t)tile * NN + wave * 16 + r;
   const bool valid = n < N;
-  const float* tn = t + (valid ? n : 0) * D * nC;
+  const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
   const int p0 = chunk * pchunk, p1 = min(p0 + pchunk, np);
   int I = 0, rowstart = 0;
   while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
@@ -235,13 +277,13 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
     if (p + 1 < p1) fetch(p + 1);
     f4 tj[D];
 #pragma unroll
-    for (int m = 0; m < D; ++m) tj[m] = valid ? ld4(tn + m * nC + J * 16 + 4 * q) : zero;
+    for (int m = 0; m < D; ++m) tj[m] = valid ? ld4(tq4<BLK>(t, N, D, nC, nl, m, J * 16 + 4 * q)) : zero;
     const float* wp = reinterpret_cast<const float*>(wl) + r * 16 + 4 * q;
 #pragma unroll 1
     for (int ig = 0; ig < 4; ++ig) {
       f4 ti[D];
 #pragma unroll
-      for (int m = 0; m < D; ++m) ti[m] = valid ? ld4(tn + m * nC + I * 16 + 4 * ig) : zero;
+      for (int m = 0; m < D; ++m) ti[m] = valid ? ld4(tq4<BLK>(t, N, D, nC, nl, m, I * 16 + 4 * ig)) : zero;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int il = 4 * ig + ii;
@@ -286,7 +328,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(1))) void gram_global_void;
 typedef __attribute__((address_space(3))) void gram_lds_void;
 
-template <int D, int S, int TSB, bool DL = false>
+template <int D, int S, int TSB, bool DL, bool BLK>
 __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, float scale,
                                                           const float* __restrict__ t,
                                                           const _Float16* __restrict__ Wf2,
@@ -309,7 +351,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   const int r = lane & 31, q = lane >> 5;
   const int64_t n = (int64_t)tile * NN + wave * 32 + r;
   const bool valid = n < N;
-  const float* tn = t + (valid ? n : 0) * D * nC;   // rows past N read node 0; their results are not stored
+  const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
   const float sn = valid ? nsc[n] : 1.f;
   const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
   int I = 0, rowstart = 0;
@@ -344,8 +386,8 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   auto load_tc = [&](int Ib) {
 #pragma unroll
     for (int m = 0; m < D; ++m) {
-      const f4 a = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q) : zero;
-      const f4 b = valid ? ld4(tn + m * nC + Ib * 16 + 8 * q + 4) : zero;
+      const f4 a = valid ? ld4(tq4<BLK>(t, N, D, nC, nl, m, Ib * 16 + 8 * q)) : zero;
+      const f4 b = valid ? ld4(tq4<BLK>(t, N, D, nC, nl, m, Ib * 16 + 8 * q + 4)) : zero;
       tc[m][0] = a.x * sn; tc[m][1] = a.y * sn; tc[m][2] = a.z * sn; tc[m][3] = a.w * sn;
       tc[m][4] = b.x * sn; tc[m][5] = b.y * sn; tc[m][6] = b.z * sn; tc[m][7] = b.w * sn;
     }
@@ -353,7 +395,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   f4 ts[TSB][D];
   auto load_ts = [&](int b, int Jb, int sg) {
 #pragma unroll
-    for (int m = 0; m < D; ++m) ts[b][m] = valid ? ld4(tn + m * nC + Jb * 16 + 4 * sg) : zero;
+    for (int m = 0; m < D; ++m) ts[b][m] = valid ? ld4(tq4<BLK>(t, N, D, nC, nl, m, Jb * 16 + 4 * sg)) : zero;
   };
   load_tc(I);
   load_ts(0, J, 0);
@@ -469,7 +511,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(int64_t NS, int nchunks, co
 // contracts it on the VALU with its own t[n][m][J0+4q..J0+4q+3]; the partial sums over q are reduced
 // once, after the J loop, with a butterfly that leaves lane q the rows il of its quarter, and both
 // scales are undone on the result.
-template <int D, int S, int ILW, bool PIPE>
+template <int D, int S, int ILW, bool PIPE, bool BLK>
 __global__ __launch_bounds__(512, D == 1 ? 4 : 2) void backward_h16_kernel(int64_t N, int nC, float scale,
                                                            const float* __restrict__ g, const float* __restrict__ t,
                                                            const _Float16* __restrict__ Wb2,
@@ -527,7 +569,7 @@ __global__ __launch_bounds__(512, D == 1 ? 4 : 2) void backward_h16_kernel(int64
       pw[i] = *reinterpret_cast<const f4*>(Wb2 + pl * plane + (int64_t)pr * 256 * S + 8 * rem);
     }
 #pragma unroll
-    for (int m = 0; m < D; ++m) tq[m] = ld4(t + (nl * D + m) * nC + J * 16 + 4 * q);
+    for (int m = 0; m < D; ++m) tq[m] = ld4(tq4<BLK>(t, N, D, nC, nl, m, J * 16 + 4 * q));
   };
   fetch(0);
   for (int J = 0; J < nb; ++J) {
@@ -645,7 +687,7 @@ FwdPlan fwd_plan(int64_t N, int nC) {
   return pl;
 }
 
-template <int S>
+template <int S, bool BLK>
 int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float* Wf, float* part, float* out,
               hipStream_t st) {
   const int np = n_pairs(nC / 16);
@@ -658,7 +700,10 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
   const float* winv = Wf + (int64_t)np * 512 * S;
   float* nsc = part + (int64_t)nchunks * N * S;
   if (bf) {
-    node_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, D, nC, t, nsc);
+    if (BLK)
+      node_scale_blocked_kernel<<<(unsigned)((N + 63) / 64), 512, 0, st>>>(N, D, nC, t, nsc);
+    else
+      node_scale_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(N, D, nC, t, nsc);
     if (check_launch("gram node scales")) return 2;
   }
   // tiles per group: as many as keep the group's t rows within about half an XCD's 4 MB L2 (at D 7,
@@ -669,9 +714,10 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
     LaunchTimer tm("gram_forward", st);
 #define FSC_GF(DD)                                                                                 \
   if (bf)                                                                                          \
-    forward_h16_kernel<DD, S, 1, (DD >= 5)><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, part, tg); \
+    forward_h16_kernel<DD, S, 1, (DD >= 5), BLK><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, \
+                                                                      part, tg);                                \
   else                                                                                             \
-    forward_kernel<DD, S><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part, pchunk)
+    forward_kernel<DD, S, BLK><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part, pchunk)
     switch (D) {
       case 1: FSC_GF(1); break;
       case 3: FSC_GF(3); break;
@@ -690,7 +736,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
 // largest D whose backward has the registers for the operand pipeline (at D 9 it spills)
 constexpr int GB_PIPE_DMAX = 7;
 
-template <int S>
+template <int S, bool BLK>
 int backward_s(int64_t N, int D, int nC, float scale, const float* g, const float* t, const float* Wb, float* dt,
                hipStream_t st) {
   // 16 rows il per wave while the accumulators (16 x D) fit the registers, else 8.
@@ -701,7 +747,7 @@ int backward_s(int64_t N, int D, int nC, float scale, const float* g, const floa
   const float* winv = Wb + (int64_t)n_pairs(nC / 16) * 512 * S;
   LaunchTimer tm("gram_backward", st);
 #define FSC_GBB(DD) \
-  backward_h16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD > 1 && DD <= GB_PIPE_DMAX)><<<grid, 512, 0, st>>>(N, nC, scale, \
+  backward_h16_kernel<DD, S, (DD <= 5 ? 16 : 8), (DD > 1 && DD <= GB_PIPE_DMAX), BLK><<<grid, 512, 0, st>>>(N, nC, scale, \
                                                                                                     g, t, Wb2, \
                                                                                             winv, dt)
   switch (D) {
@@ -747,22 +793,56 @@ int fsc_gram_prepare_weights(const float* W, int32_t S, int32_t nC, float* Wf, f
   return check_launch("gram prepare") ? 2 : 0;
 }
 
+static int gram_forward_any(bool blk, int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale,
+                            const float* t, const float* Wf, float* part_ws, float* out, hipStream_t stream,
+                            const char* who) {
+  if (check_dims(n_nodes, D, nC, S, who)) return 1;
+  FSC_CHECK_ARG(Wf && (n_nodes == 0 || (t && part_ws && out)), std::string(who) + ": null pointer");
+  FSC_CHECK_ARG(!blk || (reinterpret_cast<uintptr_t>(t) & 15) == 0, std::string(who) + ": t must be 16-byte aligned");
+  if (n_nodes == 0) return 0;
+  if (blk) {
+    if (S == 64) return forward_s<64, true>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+    return forward_s<32, true>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+  }
+  if (S == 64) return forward_s<64, false>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+  return forward_s<32, false>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+}
+
+static int gram_backward_any(bool blk, int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale,
+                             const float* grad_out, const float* t, const float* Wb, float* grad_t,
+                             hipStream_t stream, const char* who) {
+  if (check_dims(n_nodes, D, nC, S, who)) return 1;
+  FSC_CHECK_ARG(Wb && (n_nodes == 0 || (grad_out && t && grad_t)), std::string(who) + ": null pointer");
+  FSC_CHECK_ARG(!blk || (reinterpret_cast<uintptr_t>(t) & 15) == 0, std::string(who) + ": t must be 16-byte aligned");
+  if (n_nodes == 0) return 0;
+  if (blk) {
+    if (S == 64) return backward_s<64, true>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+    return backward_s<32, true>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+  }
+  if (S == 64) return backward_s<64, false>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+  return backward_s<32, false>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+}
+
 int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
                      const float* Wf, float* part_ws, float* out, hipStream_t stream) {
-  if (check_dims(n_nodes, D, nC, S, "fsc_gram_forward")) return 1;
-  FSC_CHECK_ARG(Wf && (n_nodes == 0 || (t && part_ws && out)), "fsc_gram_forward: null pointer");
-  if (n_nodes == 0) return 0;
-  if (S == 64) return forward_s<64>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
-  return forward_s<32>(n_nodes, D, nC, scale, t, Wf, part_ws, out, stream);
+  return gram_forward_any(false, n_nodes, D, nC, S, scale, t, Wf, part_ws, out, stream, "fsc_gram_forward");
 }
 
 int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* grad_out,
                       const float* t, const float* Wb, float* grad_t, hipStream_t stream) {
-  if (check_dims(n_nodes, D, nC, S, "fsc_gram_backward")) return 1;
-  FSC_CHECK_ARG(Wb && (n_nodes == 0 || (grad_out && t && grad_t)), "fsc_gram_backward: null pointer");
-  if (n_nodes == 0) return 0;
-  if (S == 64) return backward_s<64>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
-  return backward_s<32>(n_nodes, D, nC, scale, grad_out, t, Wb, grad_t, stream);
+  return gram_backward_any(false, n_nodes, D, nC, S, scale, grad_out, t, Wb, grad_t, stream, "fsc_gram_backward");
+}
+
+int fsc_gram_forward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
+                             const float* Wf, float* part_ws, float* out, hipStream_t stream) {
+  return gram_forward_any(true, n_nodes, D, nC, S, scale, t, Wf, part_ws, out, stream, "fsc_gram_forward_blocked");
+}
+
+int fsc_gram_backward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale,
+                              const float* grad_out, const float* t, const float* Wb, float* grad_t,
+                              hipStream_t stream) {
+  return gram_backward_any(true, n_nodes, D, nC, S, scale, grad_out, t, Wb, grad_t, stream,
+                           "fsc_gram_backward_blocked");
 }
 
 }  // extern "C"

@@ -483,7 +483,9 @@ int64_t gram_width(const Tensor& Wf, int64_t nC) {
   return 0;
 }
 
-Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale) {
+// blocked: t holds the (N, D, nC) values in the quad-major order of the blocked gather (the sizes still
+// name N, D and nC)
+Tensor gram_forward_impl(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, double scale, bool blocked) {
   require_gpu({t_, Wf, Wb});
   TORCH_CHECK(t_.dim() == 3, "t must be (N, D, nC)");
   const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = gram_width(Wf, nC);
@@ -492,17 +494,26 @@ Tensor gram_bilinear(const Tensor& t_, const Tensor& Wf, const Tensor& Wb, doubl
   check(fsc_gram_sizes(N, (int32_t)nC, (int32_t)S, &wfn, &wbn, &wsn), "fsc_gram_sizes");
   TORCH_CHECK(Wf.numel() == wfn && Wb.numel() == wbn, "prepared Gram weights do not match nC = ", nC);
   Tensor ws = at::empty({std::max<int64_t>(wsn, 1)}, fopts(t)), out = at::empty({N, S}, fopts(t));
-  check(fsc_gram_forward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(t), cf(Wf), mf(ws), mf(out),
-                         stream_of(t)),
-        "fsc_gram_forward");
+  if (blocked)
+    check(fsc_gram_forward_blocked(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(t), cf(Wf), mf(ws),
+                                   mf(out), stream_of(t)),
+          "fsc_gram_forward_blocked");
+  else
+    check(fsc_gram_forward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(t), cf(Wf), mf(ws), mf(out),
+                           stream_of(t)),
+          "fsc_gram_forward");
   return out;
+}
+
+Tensor gram_bilinear(const Tensor& t, const Tensor& Wf, const Tensor& Wb, double scale) {
+  return gram_forward_impl(t, Wf, Wb, scale, false);
 }
 
 Tensor gram_bilinear_meta(const Tensor& t, const Tensor& Wf, const Tensor&, double) {
   return at::empty({t.size(0), gram_width(Wf, t.size(2))}, fopts(t));
 }
 
-Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t_, const Tensor& Wb, double scale) {
+Tensor gram_backward_impl(const Tensor& grad_out, const Tensor& t_, const Tensor& Wb, double scale, bool blocked) {
   require_gpu({grad_out, t_, Wb});
   TORCH_CHECK(grad_out.dim() == 2 && t_.dim() == 3, "grad_out must be (N, S) and t (N, D, nC)");
   const int64_t N = t_.size(0), D = t_.size(1), nC = t_.size(2), S = grad_out.size(1);
@@ -511,10 +522,19 @@ Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t_, const Te
   TORCH_CHECK(Wb.numel() == wbn, "prepared Gram weights do not match nC = ", nC);
   Tensor g = f32c(grad_out), t = f32c(t_);
   Tensor dt = at::empty({N, D, nC}, fopts(t));
-  check(fsc_gram_backward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(g), cf(t), cf(Wb), mf(dt),
-                          stream_of(t)),
-        "fsc_gram_backward");
+  if (blocked)
+    check(fsc_gram_backward_blocked(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(g), cf(t), cf(Wb),
+                                    mf(dt), stream_of(t)),
+          "fsc_gram_backward_blocked");
+  else
+    check(fsc_gram_backward(N, (int32_t)D, (int32_t)nC, (int32_t)S, (float)scale, cf(g), cf(t), cf(Wb), mf(dt),
+                            stream_of(t)),
+          "fsc_gram_backward");
   return dt;
+}
+
+Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t, const Tensor& Wb, double scale) {
+  return gram_backward_impl(grad_out, t, Wb, scale, false);
 }
 
 Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&, double) {
@@ -714,23 +734,51 @@ Tensor gram_input(const Tensor& t_all, const FscReadoutTable* T, int64_t N, int 
   return t_all.narrow(0, N * col0, N * T->key_dim[k] * nC).view({N, T->key_dim[k], nC});
 }
 
-// scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.
-std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
-                                            at::ArrayRef<double> scales, const Tensor& srcmap, const Tensor& gmap,
-                                            at::IntArrayRef table) {
-  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
-  const FscReadoutTable* T = &Tv;
+bool aligned16(const Tensor& t) { return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0; }
+
+// The fused readout's forward: one gather, then the Gram bilinear of every key.  The Gram inputs only live
+// between the two (and in the backward), so where the vectorised gather applies (C a multiple of 4, a
+// node's n_layers*M*C <= 8192 entries in LDS, 16-byte aligned arrays) they are written in the
+// blocked quad-major order that the blocked Gram kernels read.
+struct ReadoutForward {
+  Tensor scalars, sq, t_all;
+  bool blocked;
+};
+ReadoutForward readout_forward_native(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
+                                      at::ArrayRef<double> scales, const Tensor& srcmap, const FscReadoutTable* T) {
   TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
                   (int64_t)scales.size() == T->n_keys,
               "one prepared Gram weight pair and scale per key");
-  auto [t_all, sq] = readout_gather(layers, srcmap, table);
-  const int64_t N = layers[0].size(0);
-  Tensor scalars;
+  std::vector<Tensor> X = readout_layers(layers, T);
+  Tensor sm = readout_map(srcmap, T, "srcmap");
+  const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C, P = nC * T->M;
+  bool blocked = T->C % 4 == 0 && P <= 8192 && aligned16(sm);   // the quad gather's limits
+  for (const Tensor& x : X) blocked = blocked && aligned16(x);
+  ReadoutForward r;
+  r.blocked = blocked;
+  r.t_all = at::empty({N * T->M * nC}, fopts(X[0]));
+  r.sq = at::empty({N, T->n_keys, nC}, fopts(X[0]));
+  std::vector<const float*> xp;
+  for (const Tensor& x : X) xp.push_back(cf(x));
+  if (blocked)
+    check(fsc_readout_gather_blocked(T, N, xp.data(), ci(sm), mf(r.t_all), mf(r.sq), stream_of(X[0])),
+          "fsc_readout_gather_blocked");
+  else
+    check(fsc_readout_gather(T, N, xp.data(), ci(sm), mf(r.t_all), mf(r.sq), stream_of(X[0])), "fsc_readout_gather");
   for (int k = 0; k < T->n_keys; ++k) {
-    Tensor o = gram_bilinear(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
-    scalars = scalars.defined() ? scalars.add_(o) : o;
+    Tensor o = gram_forward_impl(gram_input(r.t_all, T, N, k), Wf[k], Wb[k], scales[k], blocked);
+    r.scalars = r.scalars.defined() ? r.scalars.add_(o) : o;
   }
-  return {scalars, sq};
+  return r;
+}
+
+// scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.
+std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
+                                            at::ArrayRef<double> scales, const Tensor& srcmap, const Tensor&,
+                                            at::IntArrayRef table) {
+  const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
+  ReadoutForward r = readout_forward_native(layers, Wf, Wb, scales, srcmap, &Tv);
+  return {r.scalars, r.sq};
 }
 
 std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList Wf, at::TensorList,
@@ -1500,12 +1548,21 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
     TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
                     (int64_t)scales.size() == T->n_keys,
                 "one prepared Gram weight pair and scale per key");
-    auto [t_all, sq] = gather.call(layers, srcmap, table);
-    const int64_t N = layers[0].size(0);
-    Tensor scalars;
-    for (int k = 0; k < T->n_keys; ++k) {
-      Tensor o = gram.call(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
-      scalars = scalars.defined() ? scalars.add_(o) : o;
+    Tensor scalars, sq, t_all;
+    bool blocked = false;
+    if (!layers.empty() && layers[0].is_cuda()) {   // the native kernels directly (blocked Gram inputs)
+      ReadoutForward r = readout_forward_native(layers, Wf, Wb, scales, srcmap, T);
+      scalars = r.scalars;
+      sq = r.sq;
+      t_all = r.t_all;
+      blocked = r.blocked;
+    } else {   // other devices (meta, fake tensors) through the per-op kernels of the dispatcher
+      std::tie(t_all, sq) = gather.call(layers, srcmap, table);
+      const int64_t N = layers[0].size(0);
+      for (int k = 0; k < T->n_keys; ++k) {
+        Tensor o = gram.call(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
+        scalars = scalars.defined() ? scalars.add_(o) : o;
+      }
     }
     variable_list keep(layers.begin(), layers.end());
     keep.push_back(t_all);
@@ -1514,6 +1571,7 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
     ctx->save_for_backward(keep);
     ctx->saved_data["table"] = table;
     ctx->saved_data["n_layers"] = (int64_t)layers.size();
+    ctx->saved_data["blocked"] = blocked;
     ctx->saved_data["scales"] = c10::IValue(c10::ArrayRef<double>(scales));
     ctx->set_materialize_grads(false);   // an unused output skips its part of the backward
     return {scalars, sq};
@@ -1540,12 +1598,15 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
     const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
   const FscReadoutTable* T = &Tv;
     const int64_t N = layers[0].size(0);
+    const bool blocked = ctx->saved_data["blocked"].toBool();
     c10::List<std::optional<Tensor>> dt;
     for (int k = 0; k < nK; ++k) {
-      if (grads[0].defined())
-        dt.push_back(gram_bwd.call(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k]));
-      else
+      if (!grads[0].defined())
         dt.push_back(std::nullopt);
+      else if (blocked)
+        dt.push_back(gram_backward_impl(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k], true));
+      else
+        dt.push_back(gram_bwd.call(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k]));
     }
     std::optional<Tensor> dsq;
     if (grads[1].defined()) dsq = grads[1];

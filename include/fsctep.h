@@ -435,6 +435,17 @@ int fsc_gram_forward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float sc
 int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* grad_out,
                       const float* t, const float* Wb, float* grad_t, hipStream_t stream);
 
+/* The same two products for t in the quad-major order [nC/4][D][N][4] that fsc_readout_gather_blocked
+ * writes (channels 4c..4c+3 of component m of node n at ((c D + m) N + n) 4; t 16-byte aligned);
+ * out, grad_out and grad_t keep the layouts above.  A wave's lanes are consecutive nodes, and in this
+ * order their operand reads are contiguous.  Used by the fused readout (fsctep::readout_features),
+ * in place of fsc_readout_gather + fsc_gram_forward/backward on the same PyTorch reference lines. */
+int fsc_gram_forward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
+                             const float* Wf, float* part_ws, float* out, hipStream_t stream);
+int fsc_gram_backward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale,
+                              const float* grad_out, const float* t, const float* Wb, float* grad_t,
+                              hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Readout feature assembly.  From the per-layer node features X_l [N][M][C] (n_layers <= 4) it
  * builds the Gram inputs t_k [N][d_k][nC] of every key k (nC = n_layers * C; key k = components
@@ -461,6 +472,11 @@ typedef struct FscReadoutTable {
 } FscReadoutTable;
 int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
                        const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream);
+/* The gather with each t_k in the quad-major order [nC/4][d_k][N][4] of fsc_gram_forward_blocked (same
+ * offsets N * sum_{k'<k} key_dim[k'] * nC; sq unchanged).  Needs C a multiple of 4, n_layers*M*C <= 12288
+ * and 16-byte aligned arrays (status 1 otherwise). */
+int fsc_readout_gather_blocked(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
+                               const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream);
 int fsc_readout_scatter(const FscReadoutTable* table, int64_t n_nodes, const float* const* grad_t,
                         const float* grad_sq, const float* const* layers, const int32_t* gmap,
                         float* const* grad_layers, hipStream_t stream);
