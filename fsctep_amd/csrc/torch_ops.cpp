@@ -509,6 +509,11 @@ Tensor gram_bilinear(const Tensor& t, const Tensor& Wf, const Tensor& Wb, double
   return gram_forward_impl(t, Wf, Wb, scale, false);
 }
 
+// t: (N, D, nC) sizes over values in the blocked order of readout_gather_blocked.
+Tensor gram_bilinear_blocked(const Tensor& t, const Tensor& Wf, const Tensor& Wb, double scale) {
+  return gram_forward_impl(t, Wf, Wb, scale, true);
+}
+
 Tensor gram_bilinear_meta(const Tensor& t, const Tensor& Wf, const Tensor&, double) {
   return at::empty({t.size(0), gram_width(Wf, t.size(2))}, fopts(t));
 }
@@ -535,6 +540,10 @@ Tensor gram_backward_impl(const Tensor& grad_out, const Tensor& t_, const Tensor
 
 Tensor gram_bilinear_backward(const Tensor& grad_out, const Tensor& t, const Tensor& Wb, double scale) {
   return gram_backward_impl(grad_out, t, Wb, scale, false);
+}
+
+Tensor gram_bilinear_backward_blocked(const Tensor& grad_out, const Tensor& t, const Tensor& Wb, double scale) {
+  return gram_backward_impl(grad_out, t, Wb, scale, true);
 }
 
 Tensor gram_bilinear_backward_meta(const Tensor&, const Tensor& t, const Tensor&, double) {
@@ -657,18 +666,47 @@ Tensor readout_map(const Tensor& map, const FscReadoutTable* T, const char* what
   return i32c(map, what);
 }
 
-std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& srcmap, at::IntArrayRef table) {
+bool aligned16(const Tensor& t) { return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0; }
+
+// Whether the blocked gather takes this table: C a multiple of 4 and a node's n_layers*M*C <= 8192 entries
+// in LDS (decided from the table alone, so that every device, tracing ones included, takes the same path).
+bool readout_blocked(const FscReadoutTable* T) {
+  return T->C % 4 == 0 && (int64_t)T->n_layers * T->M * T->C <= 8192;
+}
+
+std::tuple<Tensor, Tensor> readout_gather_impl(at::TensorList layers, const Tensor& srcmap, at::IntArrayRef table,
+                                               bool blocked) {
   const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
   const FscReadoutTable* T = &Tv;
   std::vector<Tensor> X = readout_layers(layers, T);
   Tensor sm = readout_map(srcmap, T, "srcmap");
+  if (blocked) {   // the quad kernels need 16-byte aligned rows: a view at an odd offset is copied
+    TORCH_CHECK(readout_blocked(T), "readout_gather_blocked: needs C a multiple of 4 and n_layers*M*C <= 8192");
+    for (Tensor& x : X)
+      if (!aligned16(x)) x = x.clone();
+    if (!aligned16(sm)) sm = sm.clone();
+  }
   const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C;
   Tensor t_all = at::empty({N * T->M * nC}, fopts(X[0]));
   Tensor sq = at::empty({N, T->n_keys, nC}, fopts(X[0]));
   std::vector<const float*> xp;
   for (const Tensor& x : X) xp.push_back(cf(x));
-  check(fsc_readout_gather(T, N, xp.data(), ci(sm), mf(t_all), mf(sq), stream_of(X[0])), "fsc_readout_gather");
+  if (blocked)
+    check(fsc_readout_gather_blocked(T, N, xp.data(), ci(sm), mf(t_all), mf(sq), stream_of(X[0])),
+          "fsc_readout_gather_blocked");
+  else
+    check(fsc_readout_gather(T, N, xp.data(), ci(sm), mf(t_all), mf(sq), stream_of(X[0])), "fsc_readout_gather");
   return {t_all, sq};
+}
+
+std::tuple<Tensor, Tensor> readout_gather(at::TensorList layers, const Tensor& srcmap, at::IntArrayRef table) {
+  return readout_gather_impl(layers, srcmap, table, false);
+}
+
+// t_all with each key's Gram input in the quad-major order [nC/4][d_k][N][4] (fsc_readout_gather_blocked).
+std::tuple<Tensor, Tensor> readout_gather_blocked(at::TensorList layers, const Tensor& srcmap,
+                                                  at::IntArrayRef table) {
+  return readout_gather_impl(layers, srcmap, table, true);
 }
 
 std::tuple<Tensor, Tensor> readout_gather_meta(at::TensorList layers, const Tensor&, at::IntArrayRef table) {
@@ -734,51 +772,26 @@ Tensor gram_input(const Tensor& t_all, const FscReadoutTable* T, int64_t N, int 
   return t_all.narrow(0, N * col0, N * T->key_dim[k] * nC).view({N, T->key_dim[k], nC});
 }
 
-bool aligned16(const Tensor& t) { return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0; }
-
-// The fused readout's forward: one gather, then the Gram bilinear of every key.  The Gram inputs only live
-// between the two (and in the backward), so where the vectorised gather applies (C a multiple of 4, a
-// node's n_layers*M*C <= 8192 entries in LDS, 16-byte aligned arrays) they are written in the
-// blocked quad-major order that the blocked Gram kernels read.
-struct ReadoutForward {
-  Tensor scalars, sq, t_all;
-  bool blocked;
-};
-ReadoutForward readout_forward_native(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
-                                      at::ArrayRef<double> scales, const Tensor& srcmap, const FscReadoutTable* T) {
-  TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
-                  (int64_t)scales.size() == T->n_keys,
-              "one prepared Gram weight pair and scale per key");
-  std::vector<Tensor> X = readout_layers(layers, T);
-  Tensor sm = readout_map(srcmap, T, "srcmap");
-  const int64_t N = X[0].size(0), nC = (int64_t)T->n_layers * T->C, P = nC * T->M;
-  bool blocked = T->C % 4 == 0 && P <= 8192 && aligned16(sm);   // the quad gather's limits
-  for (const Tensor& x : X) blocked = blocked && aligned16(x);
-  ReadoutForward r;
-  r.blocked = blocked;
-  r.t_all = at::empty({N * T->M * nC}, fopts(X[0]));
-  r.sq = at::empty({N, T->n_keys, nC}, fopts(X[0]));
-  std::vector<const float*> xp;
-  for (const Tensor& x : X) xp.push_back(cf(x));
-  if (blocked)
-    check(fsc_readout_gather_blocked(T, N, xp.data(), ci(sm), mf(r.t_all), mf(r.sq), stream_of(X[0])),
-          "fsc_readout_gather_blocked");
-  else
-    check(fsc_readout_gather(T, N, xp.data(), ci(sm), mf(r.t_all), mf(r.sq), stream_of(X[0])), "fsc_readout_gather");
-  for (int k = 0; k < T->n_keys; ++k) {
-    Tensor o = gram_forward_impl(gram_input(r.t_all, T, N, k), Wf[k], Wb[k], scales[k], blocked);
-    r.scalars = r.scalars.defined() ? r.scalars.add_(o) : o;
-  }
-  return r;
-}
-
-// scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.
+// scalars = sum_k gram_bilinear(t_k, Wf[k], Wb[k], scales[k]) and the squared norms.  The Gram inputs only
+// live between the gather and the Gram kernels, so where the blocked gather applies they are written in the
+// quad-major order that the blocked Gram kernels read.
 std::tuple<Tensor, Tensor> readout_features(at::TensorList layers, at::TensorList Wf, at::TensorList Wb,
                                             at::ArrayRef<double> scales, const Tensor& srcmap, const Tensor&,
                                             at::IntArrayRef table) {
   const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
-  ReadoutForward r = readout_forward_native(layers, Wf, Wb, scales, srcmap, &Tv);
-  return {r.scalars, r.sq};
+  const FscReadoutTable* T = &Tv;
+  TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
+                  (int64_t)scales.size() == T->n_keys,
+              "one prepared Gram weight pair and scale per key");
+  const bool blocked = readout_blocked(T);
+  auto [t_all, sq] = readout_gather_impl(layers, srcmap, table, blocked);
+  const int64_t N = layers[0].size(0);
+  Tensor scalars;
+  for (int k = 0; k < T->n_keys; ++k) {
+    Tensor o = gram_forward_impl(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k], blocked);
+    scalars = scalars.defined() ? scalars.add_(o) : o;
+  }
+  return {scalars, sq};
 }
 
 std::tuple<Tensor, Tensor> readout_features_meta(at::TensorList layers, at::TensorList Wf, at::TensorList,
@@ -1543,26 +1556,24 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
     static auto gather =
         op_handle<std::tuple<Tensor, Tensor>(at::TensorList, const Tensor&, at::IntArrayRef)>("fsctep::readout_gather");
     static auto gram = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear");
+    static auto gather_blk = op_handle<std::tuple<Tensor, Tensor>(at::TensorList, const Tensor&, at::IntArrayRef)>(
+        "fsctep::readout_gather_blocked");
+    static auto gram_blk =
+        op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear_blocked");
     const FscReadoutTable Tv = unpack_table<FscReadoutTable>(table, "readout table");
   const FscReadoutTable* T = &Tv;
     TORCH_CHECK((int64_t)Wf.size() == T->n_keys && (int64_t)Wb.size() == T->n_keys &&
                     (int64_t)scales.size() == T->n_keys,
                 "one prepared Gram weight pair and scale per key");
+    // through the dispatcher, so that tracers (make_fx, TorchScript) record the calls
+    const bool blocked = readout_blocked(T);
     Tensor scalars, sq, t_all;
-    bool blocked = false;
-    if (!layers.empty() && layers[0].is_cuda()) {   // the native kernels directly (blocked Gram inputs)
-      ReadoutForward r = readout_forward_native(layers, Wf, Wb, scales, srcmap, T);
-      scalars = r.scalars;
-      sq = r.sq;
-      t_all = r.t_all;
-      blocked = r.blocked;
-    } else {   // other devices (meta, fake tensors) through the per-op kernels of the dispatcher
-      std::tie(t_all, sq) = gather.call(layers, srcmap, table);
-      const int64_t N = layers[0].size(0);
-      for (int k = 0; k < T->n_keys; ++k) {
-        Tensor o = gram.call(gram_input(t_all, T, N, k), Wf[k], Wb[k], scales[k]);
-        scalars = scalars.defined() ? scalars.add_(o) : o;
-      }
+    std::tie(t_all, sq) = blocked ? gather_blk.call(layers, srcmap, table) : gather.call(layers, srcmap, table);
+    const int64_t N = layers[0].size(0);
+    for (int k = 0; k < T->n_keys; ++k) {
+      const Tensor tk = gram_input(t_all, T, N, k);
+      Tensor o = blocked ? gram_blk.call(tk, Wf[k], Wb[k], scales[k]) : gram.call(tk, Wf[k], Wb[k], scales[k]);
+      scalars = scalars.defined() ? scalars.add_(o) : o;
     }
     variable_list keep(layers.begin(), layers.end());
     keep.push_back(t_all);
@@ -1588,6 +1599,8 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
                                              "(energy/force inference only)");
     static auto gram_bwd =
         op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>("fsctep::gram_bilinear_backward");
+    static auto gram_bwd_blk = op_handle<Tensor(const Tensor&, const Tensor&, const Tensor&, double)>(
+        "fsctep::gram_bilinear_backward_blocked");
     static auto scatter = op_handle<std::vector<Tensor>(const c10::List<std::optional<Tensor>>&,
                                                         const std::optional<Tensor>&, at::TensorList, const Tensor&,
                                                         at::IntArrayRef)>("fsctep::readout_scatter");
@@ -1604,7 +1617,7 @@ struct ReadoutFn : public torch::autograd::Function<ReadoutFn> {
       if (!grads[0].defined())
         dt.push_back(std::nullopt);
       else if (blocked)
-        dt.push_back(gram_backward_impl(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k], true));
+        dt.push_back(gram_bwd_blk.call(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k]));
       else
         dt.push_back(gram_bwd.call(grads[0], gram_input(t_all, T, N, k), s[nL + 1 + k], scales[k]));
     }
@@ -1787,6 +1800,8 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("gram_prepare_weights(Tensor W) -> (Tensor, Tensor)");
   m.def("gram_bilinear(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
   m.def("gram_bilinear_backward(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
+  m.def("gram_bilinear_blocked(Tensor t, Tensor Wf, Tensor Wb, float scale) -> Tensor");
+  m.def("gram_bilinear_backward_blocked(Tensor grad_out, Tensor t, Tensor Wb, float scale) -> Tensor");
   m.def("readout_mlp_prepare(Tensor[] params, int[] dims, float[] eps) -> Tensor");
   m.def("readout_mlp(Tensor x, Tensor weights, int[] dims, float[] eps) -> Tensor");
   m.def("readout_mlp_backward(Tensor grad, Tensor x, Tensor weights, int[] dims, float[] eps) -> Tensor");
@@ -1801,6 +1816,7 @@ TORCH_LIBRARY(fsctep, m) {
   m.def("radial_mlp_backward(Tensor grad_out, Tensor r, Tensor w0, Tensor b0, Tensor w2, Tensor b2, Tensor? w4, "
         "float r_cut, int basis) -> Tensor");
   m.def("readout_gather(Tensor[] layers, Tensor srcmap, int[] table) -> (Tensor, Tensor)");
+  m.def("readout_gather_blocked(Tensor[] layers, Tensor srcmap, int[] table) -> (Tensor, Tensor)");
   m.def("readout_scatter(Tensor?[] grad_t, Tensor? grad_sq, Tensor[] layers, Tensor gmap, int[] table) -> Tensor[]");
   m.def("readout_features(Tensor[] layers, Tensor[] Wf, Tensor[] Wb, float[] scales, Tensor srcmap, Tensor gmap, "
         "int[] table) -> (Tensor, Tensor)");
@@ -1828,6 +1844,8 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("ictd_conv1_backward", ictd_conv1_backward);
   m.impl("gram_prepare_weights", gram_prepare_weights);
   m.impl("gram_bilinear", gram_bilinear);
+  m.impl("gram_bilinear_blocked", gram_bilinear_blocked);
+  m.impl("gram_bilinear_backward_blocked", gram_bilinear_backward_blocked);
   m.impl("gram_bilinear_backward", gram_bilinear_backward);
   m.impl("readout_mlp_prepare", readout_mlp_prepare);
   m.impl("readout_mlp", readout_mlp);
@@ -1839,6 +1857,7 @@ TORCH_LIBRARY_IMPL(fsctep, CUDA, m) {
   m.impl("edge_harmonics", edge_harmonics);
   m.impl("edge_harmonics_backward", edge_harmonics_backward);
   m.impl("readout_gather", readout_gather);
+  m.impl("readout_gather_blocked", readout_gather_blocked);
   m.impl("readout_scatter", readout_scatter);
   m.impl("readout_features", readout_features);
   m.impl("graph_prepare", graph_prepare);
@@ -1865,6 +1884,8 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("ictd_conv1_backward", ictd_conv1_backward_meta);
   m.impl("gram_prepare_weights", gram_prepare_weights_meta);
   m.impl("gram_bilinear", gram_bilinear_meta);
+  m.impl("gram_bilinear_blocked", gram_bilinear_meta);
+  m.impl("gram_bilinear_backward_blocked", gram_bilinear_backward_meta);
   m.impl("gram_bilinear_backward", gram_bilinear_backward_meta);
   m.impl("readout_mlp_prepare", readout_mlp_prepare_meta);
   m.impl("readout_mlp", readout_mlp_meta);
@@ -1876,6 +1897,7 @@ TORCH_LIBRARY_IMPL(fsctep, Meta, m) {
   m.impl("edge_harmonics", edge_harmonics_meta);
   m.impl("edge_harmonics_backward", edge_harmonics_backward_meta);
   m.impl("readout_gather", readout_gather_meta);
+  m.impl("readout_gather_blocked", readout_gather_meta);
   m.impl("readout_scatter", readout_scatter_meta);
   m.impl("readout_features", readout_features_meta);
   m.impl("graph_prepare", graph_prepare_meta);
@@ -1907,6 +1929,7 @@ TORCH_LIBRARY_IMPL(fsctep, CPU, m) {
                            "readout_mlp_backward", "edge_geometry", "edge_geometry_backward",
                            "radial_mlp", "radial_mlp_backward", "edge_harmonics", "edge_harmonics_backward",
                            "readout_gather", "readout_scatter", "readout_features", "graph_prepare",
-                           "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "neighbor_list"})
+                           "edge_vec_geometry", "edge_vec_geometry_backward", "spatial_order", "neighbor_list",
+                           "gram_bilinear_blocked", "gram_bilinear_backward_blocked", "readout_gather_blocked"})
     m.impl(name, torch::CppFunction::makeFromBoxedFunction<&refuse_cpu>());
 }

@@ -20,6 +20,7 @@ OPS = ["sparse_prepare_weights", "sparse_conv", "sparse_conv_backward", "sparse_
        "readout_gather", "readout_scatter", "readout_features", "graph_prepare", "edge_vec_geometry",
        "edge_vec_geometry_backward", "spatial_order", "ictd_project", "sparse_conv_direction",
        "sparse_conv_direction_backward", "readout_mlp_prepare", "readout_mlp", "readout_mlp_backward",
+       "gram_bilinear_blocked", "gram_bilinear_backward_blocked", "readout_gather_blocked",
        # the per-edge (bucketed) ICTD ops under the reference extension's names (csrc/ictd_tp.cpp:498-521)
        "project_bucket_forward", "project_bucket_transpose_a", "project_bucket_transpose_b",
        "project_bucket_transpose_u", "mix_bucket_forward", "mix_bucket_transpose_y", "mix_bucket_transpose_w",
