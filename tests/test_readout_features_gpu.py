@@ -78,3 +78,38 @@ def _sq_grad_expand(gq, dims, layer, C):
     for k, d in enumerate(dims):
         parts.append(gq[:, k:k + 1, layer * C:(layer + 1) * C].expand(-1, d, -1))
     return torch.cat(parts, dim=1)
+
+
+def test_readout_features_misaligned_views():
+    """Feature layers that are views at an odd float offset (not 16-byte aligned) take the blocked
+    gather after a copy and give the same scalars, norms and gradients as aligned tensors, bit for bit;
+    with autograd off (the op's own device kernel) too."""
+    dims, C, nL, S, N = [1, 3, 9], 64, 3, 64, 300
+    M, nC = sum(dims), nL * C
+    g = torch.Generator(device=DEV).manual_seed(11)
+    feats = [torch.randn(N, M, C, device=DEV, generator=g) for _ in range(nL)]
+    grams = [torch.ops.fsctep.gram_prepare_weights(torch.randn(S, nC, nC, device=DEV, generator=g) * 0.05)
+             for _ in dims]
+    scales = [1.0 / math.sqrt(d) for d in dims]
+    maps = ReadoutMaps(nL, C, dims, resplit=False)
+    views = []
+    for f in feats:
+        buf = torch.empty(f.numel() + 1, device=DEV)
+        v = buf[1:].view(N, M, C)
+        v.copy_(f)
+        assert v.data_ptr() % 16 != 0
+        views.append(v)
+    gs = torch.randn(N, S, device=DEV, generator=g)
+    outs = []
+    for src in (feats, views):
+        x = [t.detach().requires_grad_(True) for t in src]
+        scal, sq = readout_features(x, grams, scales, maps)
+        d = torch.autograd.grad((scal * gs).sum() + sq.sum(), x)
+        with torch.inference_mode():   # autograd keys excluded: the op's device kernel itself
+            scal0, sq0 = readout_features([t.detach() for t in src], grams, scales, maps)
+        outs.append((scal, sq, d, scal0, sq0))
+    (a_s, a_q, a_d, a_s0, a_q0), (b_s, b_q, b_d, b_s0, b_q0) = outs
+    assert torch.equal(a_s, b_s) and torch.equal(a_q, b_q)
+    assert torch.equal(a_s0, a_s) and torch.equal(b_s0, b_s) and torch.equal(b_q0, b_q)
+    for u, w in zip(a_d, b_d):
+        assert torch.equal(u, w)
