@@ -31,7 +31,7 @@ namespace fsc {
 namespace gram {
 
 constexpr int NODES = 128;   // nodes per workgroup (8 waves x 16 MFMA rows)
-constexpr int PCHUNK = 8;    // block pairs per forward workgroup
+constexpr int PCHUNK = 8;    // block pairs per forward workgroup, or twice as many (fwd_plan)
 
 __host__ __device__ inline int n_pairs(int nb) { return nb * (nb + 1) / 2; }
 
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(512) void forward_kernel(int64_t N, int nC, float s
 
 // Forward with split-fp16 products on v_mfma_f32_32x32x16_f16 (32 nodes x 32 outputs per MFMA; the
 // Gram values of node n are scaled by nsc[n], the weights by sw, both undone on the result).  A
-// workgroup is 256 nodes (8 waves x 32) x one chunk of PCHUNK pairs; lane (r, q) of a wave is node r
+// workgroup is 256 nodes (8 waves x 32) x one chunk of pchunk pairs; lane (r, q) of a wave is node r
 // and K half q.  Step s (0..15) of a pair contracts K = 8q + j <-> (il = 8q + j, jl = s), so a lane
 // keeps t[n][m][I0 + 8q + j] (unchanged along a row of pairs) and streams t[n][m][J0 + s] four steps at
 // a time: the next group's loads are issued once the group's last G values are formed (TSB = 1, in
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
                                                           const _Float16* __restrict__ Wf2,
                                                           const float* __restrict__ winv,
                                                           const float* __restrict__ nsc, int nchunks,
-                                                          float* __restrict__ part, int tgroup) {
+                                                          int pchunk, float* __restrict__ part, int tgroup) {
   constexpr int NN = NODES_BF, CT = S / 32;
   constexpr int PSZ = 256 * S;            // fp16 per plane of a pair
   constexpr int PW = 2 * PSZ / 8 / 512;   // 16-byte pieces of a pair per thread
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(512) void forward_h16_kernel(int64_t N, int nC, flo
   const bool valid = n < N;
   const int64_t nl = valid ? n : 0;   // rows past N read node 0; their results are not stored
   const float sn = valid ? nsc[n] : 1.f;
-  const int p0 = chunk * PCHUNK, p1 = min(p0 + PCHUNK, np);
+  const int p0 = chunk * pchunk, p1 = min(p0 + pchunk, np);
   int I = 0, rowstart = 0;
   while (rowstart + (nb - I) <= p0) { rowstart += nb - I; ++I; }
   int J = I + (p0 - rowstart);
@@ -669,7 +669,7 @@ int check_dims(int64_t N, int32_t D, int32_t nC, int32_t S, const char* who) {
 // several times the fp32 kernel's rate per node; with at most 128 of its workgroups (one partial round
 // on 256 CUs) the fp32 kernel's twice as many smaller workgroups finish first.  The fp32 kernel (few
 // nodes) takes fewer pairs per workgroup, down to one, until there are about two workgroups per CU:
-// at 1,000 nodes and nC 192 that is 624 workgroups of one pair instead of 80 of eight.
+// at 1,000 nodes and nC 192 that is 624 workgroups of one pair instead of 40 of sixteen.
 struct FwdPlan {
   bool bf;
   int pchunk, nchunks;
@@ -677,8 +677,12 @@ struct FwdPlan {
 FwdPlan fwd_plan(int64_t N, int nC) {
   const int np = n_pairs(nC / 16);
   FwdPlan pl;
-  pl.bf = (int64_t)((np + PCHUNK - 1) / PCHUNK) * ((N + NODES_BF - 1) / NODES_BF) > 128;
+  const int64_t ntb = (N + NODES_BF - 1) / NODES_BF;
+  pl.bf = (int64_t)((np + PCHUNK - 1) / PCHUNK) * ntb > 128;
   pl.pchunk = PCHUNK;
+  // the split-fp16 kernel takes 16 pairs per workgroup while that still leaves more than 128 workgroups:
+  // 6 % faster at nC 384 (10,000 nodes, 760 workgroups), 5 % at nC 192 (10,000 nodes, 200 workgroups)
+  if (pl.bf && (int64_t)((np + 2 * PCHUNK - 1) / (2 * PCHUNK)) * ntb > 128) pl.pchunk = 2 * PCHUNK;
   if (!pl.bf) {
     const int64_t ntiles = (N + NODES - 1) / NODES;
     while (pl.pchunk > 1 && (int64_t)((np + pl.pchunk - 1) / pl.pchunk) * ntiles < 512) pl.pchunk /= 2;
@@ -715,7 +719,7 @@ int forward_s(int64_t N, int D, int nC, float scale, const float* t, const float
 #define FSC_GF(DD)                                                                                 \
   if (bf)                                                                                          \
     forward_h16_kernel<DD, S, 1, (DD >= 5), BLK><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf2, winv, nsc, nchunks, \
-                                                                      part, tg);                                \
+                                                                      pchunk, part, tg);                        \
   else                                                                                             \
     forward_kernel<DD, S, BLK><<<grid, 512, 0, st>>>(N, nC, scale, t, Wf, nchunks, part, pchunk)
     switch (D) {

@@ -85,8 +85,12 @@ def test_fake_kernels_trace_shapes():
 def test_gram_sizes_and_fake_kernels():
     from torch._subclasses.fake_tensor import FakeTensorMode
     from fsctep_amd import readout_ops
+    # 24 blocks -> 300 pairs; 1,000 nodes: 38 chunks of 8 x 4 tiles of 256 nodes (16-pair chunks would leave
+    # 76 <= 128 workgroups); 10,000 nodes: 19 chunks of 16 x 40 tiles; node scales
     wf, wb, ws = readout_ops.gram_sizes(1000, 384, 64)
-    assert ws == 38 * 1000 * 64 + 1000                       # 24 blocks -> 300 pairs -> 38 chunks of 8; node scales
+    assert ws == 38 * 1000 * 64 + 1000
+    _, _, ws = readout_ops.gram_sizes(10000, 384, 64)
+    assert ws == 19 * 10000 * 64 + 10000
     assert wf == wb == 300 * 256 * 64 * 2 + 512              # fp32 pairs + two fp16 planes + scale/maxima tail
     with pytest.raises(RuntimeError, match="multiple of 16"):
         readout_ops.gram_sizes(10, 40, 64)

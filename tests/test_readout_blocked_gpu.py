@@ -79,9 +79,10 @@ def test_blocked_gather_refuses_long_rows():
 
 
 # (N, D, nC, S): few nodes (the first four: fp32 forward kernel), many nodes (the rest: split-fp16
-# forward), partial tiles, D 1..9, nC 16 (one block), the 10k-atom channel widths
+# forward, 3500 nodes with chunks of 8 block pairs, the others of 16), partial tiles, D 1..9, nC 16 (one
+# block), the 10k-atom channel widths
 GRAM = [(70, 1, 64, 32), (130, 9, 192, 64), (1, 3, 16, 64), (1100, 5, 128, 32), (3500, 3, 192, 64),
-        (2500, 7, 384, 64), (1200, 5, 384, 32), (4000, 9, 192, 64), (4100, 1, 192, 64)]
+        (2500, 7, 384, 64), (2000, 5, 384, 32), (6700, 9, 192, 64), (7100, 1, 192, 64)]
 
 
 @pytest.mark.parametrize("N,D,nC,S", GRAM)
