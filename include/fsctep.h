@@ -438,8 +438,10 @@ int fsc_gram_backward(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float s
 /* The same two products for t in the quad-major order [nC/4][D][N][4] that fsc_readout_gather_blocked
  * writes (channels 4c..4c+3 of component m of node n at ((c D + m) N + n) 4; t 16-byte aligned);
  * out, grad_out and grad_t keep the layouts above.  A wave's lanes are consecutive nodes, and in this
- * order their operand reads are contiguous.  Used by the fused readout (fsctep::readout_features),
- * in place of fsc_readout_gather + fsc_gram_forward/backward on the same PyTorch reference lines. */
+ * order their operand reads are contiguous.  They replace the same reference code as fsc_gram_forward /
+ * fsc_gram_backward (models/pure_cartesian_sparse_layers.py:424-456,
+ * models/pure_cartesian_ictd_layers_full.py:999-1000, models/pure_cartesian_ictd_layers_o3.py:1017-1018);
+ * the fused readout (fsctep::readout_features) calls them after fsc_readout_gather_blocked. */
 int fsc_gram_forward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale, const float* t,
                              const float* Wf, float* part_ws, float* out, hipStream_t stream);
 int fsc_gram_backward_blocked(int64_t n_nodes, int32_t D, int32_t nC, int32_t S, float scale,
@@ -473,7 +475,9 @@ typedef struct FscReadoutTable {
 int fsc_readout_gather(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
                        const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream);
 /* The gather with each t_k in the quad-major order [nC/4][d_k][N][4] of fsc_gram_forward_blocked (same
- * offsets N * sum_{k'<k} key_dim[k'] * nC; sq unchanged).  Needs C a multiple of 4, n_layers*M*C <= 12288
+ * offsets N * sum_{k'<k} key_dim[k'] * nC; sq unchanged); replaces the same readout assembly as
+ * fsc_readout_gather (models/pure_cartesian_sparse_layers.py:769-833,
+ * models/pure_cartesian_ictd_layers_full.py:977-1024, models/pure_cartesian_ictd_layers_o3.py:987-1030).  Needs C a multiple of 4, n_layers*M*C <= 12288
  * and 16-byte aligned arrays (status 1 otherwise). */
 int fsc_readout_gather_blocked(const FscReadoutTable* table, int64_t n_nodes, const float* const* layers,
                                const int32_t* srcmap, float* t_all, float* sq, hipStream_t stream);
